@@ -1,0 +1,751 @@
+"""CPU oracle for the SparsePR sparse-attention hot path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product package (sparsepr_amd/) imports,
+links or calls this module; only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it, as the checker.
+
+This is a numpy restatement of the reference's semantics (the reference itself
+is never imported).  Every function cites the reference file:line it follows.
+Order-sensitive pieces (top-p map, exact-FP32 role step, budget selector) live
+in the C part, oracle/c/spr_oracle.c, loaded through ctypes below.
+
+Precision conventions (shared with the HIP kernels, see the project design notes):
+  * bf16 values are carried as float32 arrays whose values are bf16-representable
+    (round-to-nearest-even, `to_bf16`).
+  * k-means cross terms are evaluated in float64 (the bf16 products are exact);
+    the GPU's fp32 accumulation may flip labels only between near-tied centroids.
+  * centroid sums are accumulated in float64 (exact for bf16 inputs), then
+    mean32 = float32(sum / count), then (for bf16 centroids) rounded to bf16.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_C_LIB: ctypes.CDLL | None = None
+
+
+def c_lib() -> ctypes.CDLL:
+    """Load oracle/liboracle_c.so (built by oracle/Makefile)."""
+    global _C_LIB
+    if _C_LIB is None:
+        path = _HERE / "liboracle_c.so"
+        if not path.exists():
+            raise RuntimeError(f"oracle C library missing: {path} (run `make -C oracle`)")
+        lib = ctypes.CDLL(str(path))
+        f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+        i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+        u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+        i64 = ctypes.c_int64
+        i32 = ctypes.c_int32
+        lib.spr_oracle_expf.restype = ctypes.c_float
+        lib.spr_oracle_expf.argtypes = [ctypes.c_float]
+        lib.spr_oracle_expf_array.restype = None
+        lib.spr_oracle_expf_array.argtypes = [f32p, f32p, i64]
+        lib.oracle_topp_map.restype = None
+        lib.oracle_topp_map.argtypes = [
+            f32p, f32p, i32p, i64, i32, i32, i32, ctypes.c_float, ctypes.c_float, i32,
+            u8p, ctypes.c_void_p, ctypes.c_void_p,
+        ]
+        lib.oracle_select_budget.restype = None
+        lib.oracle_select_budget.argtypes = [f32p, i32p, i32p, i64, i32, i32, i32, u8p]
+        lib.oracle_role_step64.restype = None
+        lib.oracle_role_step64.argtypes = [
+            f32p, f32p, i64, i64, i32, i32p, f32p, i32p, ctypes.c_void_p,
+        ]
+        _C_LIB = lib
+    return _C_LIB
+
+
+# ----------------------------------------------------------------------------
+# dtype helpers
+# ----------------------------------------------------------------------------
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bfloat16 (nearest-even); result kept as float32."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    rounding = ((u >> 16) & 1) + 0x7FFF
+    r = ((u + rounding) & 0xFFFF0000).astype(np.uint32)
+    nan = np.isnan(a)
+    out = r.view(np.float32).copy()
+    out[nan] = np.float32("nan")
+    return out
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """uint16 bit patterns of bf16-representable float32 values."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    return (a.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def from_bf16_bits(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint32) << 16).view(np.float32)
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """Canonical fp32 exp shared with the GPU kernels (oracle/c/spr_oracle.c)."""
+    a = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty_like(a)
+    c_lib().spr_oracle_expf_array(a, out, a.size)
+    return out.reshape(np.shape(x))
+
+
+# ----------------------------------------------------------------------------
+# k-means (flash_kmeans + kmeans_utils)
+# ----------------------------------------------------------------------------
+
+def x_sq_for(x: np.ndarray, mode: str) -> np.ndarray:
+    """Per-point squared norm as the reference feeds it to the assign kernel.
+
+    mode "bf16": flash_kmeans computes ``(x ** 2).sum(-1)`` into an ``x.dtype``
+      buffer (kmeans_triton_impl.py:84-87): bf16(x_i^2) summed, rounded to bf16.
+    mode "fp32": the inline-x_sq kernel sums fp32 squares of the bf16 tile
+      (kmeans_utils.py:812-814).
+    Sums here are float64 (exact), then rounded once.
+    """
+    x64 = x.astype(np.float64)
+    if mode == "bf16":
+        sq = to_bf16((x64 * x64).astype(np.float32)).astype(np.float64)
+        return to_bf16(sq.sum(-1).astype(np.float32))
+    if mode == "fp32":
+        return (x64 * x64).sum(-1).astype(np.float32)
+    raise ValueError(mode)
+
+
+def kmeans_assign(x: np.ndarray, c: np.ndarray, x_sq: np.ndarray):
+    """Nearest centroid, lowest index among exact minima.
+
+    Follows assign_euclid_triton.py:803-917 (_euclid_assign_kernel):
+    dist = x_sq + c_sq - 2 x.c, clamped at 0; c_sq in fp32 from the centroids
+    (assign_euclid_triton.py:1282-1283); running argmin with strict `<` across
+    tiles and first index within a tile == lowest index overall.
+    Returns (labels int32 [B,N], dist float64 [B,N,K]).
+    """
+    x64 = x.astype(np.float64)
+    c64 = c.astype(np.float64)
+    c_sq = (c64 * c64).sum(-1).astype(np.float32).astype(np.float64)
+    cross = np.einsum("bnd,bkd->bnk", x64, c64)
+    dist = x_sq.astype(np.float64)[:, :, None] + c_sq[:, None, :] - 2.0 * cross
+    dist = np.maximum(dist, 0.0)
+    labels = np.argmin(dist, axis=-1).astype(np.int32)  # numpy returns the first minimum
+    return labels, dist
+
+
+def label_mismatches_are_ties(labels_gpu, labels_ref, dist, x_sq, c, rel_tol):
+    """True if every label disagreement is between centroids whose exact
+    distances differ by at most rel_tol * (x_sq + c_sq) (the scale at which the
+    fp32 distance is formed)."""
+    bad = labels_gpu != labels_ref
+    if not bad.any():
+        return True, 0
+    b_idx, n_idx = np.nonzero(bad)
+    c64 = c.astype(np.float64)
+    c_sq = (c64 * c64).sum(-1)
+    dg = dist[b_idx, n_idx, labels_gpu[b_idx, n_idx]]
+    dr = dist[b_idx, n_idx, labels_ref[b_idx, n_idx]]
+    scale = x_sq[b_idx, n_idx].astype(np.float64) + np.maximum(
+        c_sq[b_idx, labels_gpu[b_idx, n_idx]], c_sq[b_idx, labels_ref[b_idx, n_idx]]
+    )
+    ok = np.abs(dg - dr) <= rel_tol * np.maximum(scale, 1e-30)
+    return bool(ok.all()), int(bad.sum())
+
+
+def centroid_update(x: np.ndarray, labels: np.ndarray, old: np.ndarray, out_bf16: bool):
+    """Cluster means; empty clusters keep the old centroid.
+
+    Follows centroid_update_triton.py:316-386 (sums/max(cnt,1), where(cnt==0, old),
+    cast to x.dtype) and torch_fallback.py:72-108.  Sums in float64.
+    Returns (centroids [B,K,D] float32 (bf16-rounded if out_bf16), mean32, counts int32).
+    """
+    B, N, D = x.shape
+    K = old.shape[1]
+    sums = np.zeros((B, K, D), np.float64)
+    counts = np.zeros((B, K), np.int64)
+    for b in range(B):
+        np.add.at(sums[b], labels[b].astype(np.int64), x[b].astype(np.float64))
+        counts[b] = np.bincount(labels[b], minlength=K)
+    mean32 = (sums / np.maximum(counts, 1)[:, :, None]).astype(np.float32)
+    mean32 = np.where(counts[:, :, None] == 0, old.astype(np.float32), mean32)
+    cent = to_bf16(mean32) if out_bf16 else mean32
+    return cent, mean32, counts.astype(np.int32)
+
+
+def loop_centroid_update(x, labels, old):
+    """Double-loop restatement (torch_fallback.py:54-70) used to pin
+    centroid_update: per cluster, mean of member rows in float64."""
+    B, N, D = x.shape
+    K = old.shape[1]
+    out = np.zeros((B, K, D), np.float64)
+    for b in range(B):
+        for k in range(K):
+            mask = labels[b] == k
+            if mask.any():
+                out[b, k] = x[b][mask].astype(np.float64).mean(axis=0)
+            else:
+                out[b, k] = old[b, k]
+    return out
+
+
+def batch_kmeans_euclid(x, n_clusters, max_iters, tol=0.0, init_centroids=None,
+                        x_sq_mode="bf16", out_bf16=True):
+    """Lloyd loop with the reference's return convention.
+
+    kmeans_triton_impl.py:102-115: each iteration assigns with the current
+    centroids, updates, computes shift = max ||new - old||; breaks *before*
+    adopting the update when shift < tol.  Returns labels of the last
+    assignment, the adopted centroids, the sizes of the last assignment
+    (kmeans_utils.py:1312-1369 also returns sizes) and the iteration count.
+    """
+    if init_centroids is None:
+        raise ValueError("oracle needs explicit initial centroids")
+    cent = init_centroids.astype(np.float32)
+    x_sq = x_sq_for(x, x_sq_mode)
+    labels = counts = None
+    it = -1
+    for it in range(max_iters):
+        labels, _ = kmeans_assign(x, cent, x_sq)
+        new, _, counts = centroid_update(x, labels, cent, out_bf16)
+        shift = np.sqrt(((new.astype(np.float64) - cent.astype(np.float64)) ** 2).sum(-1)).max()
+        if shift < tol:
+            break
+        cent = new
+    return labels, cent, counts, it + 1
+
+
+def first_k_init(x: np.ndarray, k: int, seed: int) -> np.ndarray:
+    """Seeded first-k init used by the synthetic configs: the first k entries of
+    a seeded permutation of the N tokens, per batch (same permutation)."""
+    rng = np.random.default_rng(seed)
+    idx = rng.permutation(x.shape[1])[:k]
+    return x[:, idx, :].copy()
+
+
+def role_step64(features: np.ndarray, centroids: np.ndarray):
+    """One exact FP32 D=64 Lloyd step (n8_ops.cu:198-269, role_cluster_step_q64)."""
+    f = np.ascontiguousarray(features, np.float32)
+    c = np.ascontiguousarray(centroids, np.float32)
+    bh, n, d = f.shape
+    assert d == 64
+    k = c.shape[1]
+    labels = np.empty((bh, n), np.int32)
+    out = np.empty_like(c)
+    sizes = np.empty((bh, k), np.int32)
+    best = np.empty((bh, n), np.float32)
+    c_lib().oracle_role_step64(f, c, bh, n, k, labels, out, sizes, best.ctypes.data)
+    return labels, out, sizes, best
+
+
+# ----------------------------------------------------------------------------
+# permutation
+# ----------------------------------------------------------------------------
+
+def argsort_labels(labels: np.ndarray) -> np.ndarray:
+    """Stable ascending argsort per row (kmeans_utils.py:1674-1684 uses
+    torch.argsort; the within-cluster order is fixed here to ascending token)."""
+    return np.argsort(labels, axis=-1, kind="stable").astype(np.int32)
+
+
+def permute_rows(x: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """Y[bh,s] = X[bh, idx[bh,s]] (permute.py:12-43, kmeans_utils.py:1674-1684)."""
+    return np.take_along_axis(x, idx[..., None].astype(np.int64), axis=-2)
+
+
+def inverse_permute_rows(y: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """X[bh, idx[bh,s]] = Y[bh,s] (permute.py:90-119, kmeans_utils.py:1687-1695)."""
+    out = np.empty_like(y)
+    bh = y.shape[0]
+    for h in range(bh):
+        out[h, idx[h].astype(np.int64)] = y[h]
+    return out
+
+
+def permute_concat_rows(prefix, suffix, idx):
+    """permute(cat(prefix, suffix)) (permute.py:46-87)."""
+    return permute_rows(np.concatenate([prefix, suffix], axis=-2), idx)
+
+
+# ----------------------------------------------------------------------------
+# block selection
+# ----------------------------------------------------------------------------
+
+def identify_dynamic_map(qc, kc, k_sizes, p, min_kc_ratio=0.0, return_cum=False):
+    """Top-p cluster-pair map (kmeans_utils.py:1710-1742), canonical fp32 order.
+
+    qc [BH,Qc,D], kc [BH,Kc,D] float32; k_sizes [BH,Kc] -> bool [BH,Qc,Kc].
+    """
+    qc = np.ascontiguousarray(qc, np.float32)
+    kc = np.ascontiguousarray(kc, np.float32)
+    ks = np.ascontiguousarray(k_sizes, np.int32)
+    bh, qn, d = qc.shape
+    kn = kc.shape[1]
+    out = np.zeros((bh, qn, kn), np.uint8)
+    preserve = int(min_kc_ratio * kn) if min_kc_ratio > 0 else 0
+    cum = np.zeros((bh, qn, kn), np.float32) if return_cum else None
+    order = np.zeros((bh, qn, kn), np.int32) if return_cum else None
+    c_lib().oracle_topp_map(
+        qc, kc, ks, bh, qn, kn, d, np.float32(math.sqrt(d)), np.float32(p), preserve, out,
+        cum.ctypes.data if cum is not None else None,
+        order.ctypes.data if order is not None else None,
+    )
+    if return_cum:
+        return out.astype(bool), cum, order
+    return out.astype(bool)
+
+
+def identify_dynamic_map_f64(qc, kc, k_sizes, p, min_kc_ratio=0.0):
+    """The same selection evaluated in float64 with numpy's own ops; used to
+    pin the canonical fp32 version away from the threshold."""
+    bh, qn, d = qc.shape
+    kn = kc.shape[1]
+    s = np.einsum("bqd,bkd->bqk", qc.astype(np.float64), kc.astype(np.float64)) / math.sqrt(d)
+    s = s - s.max(-1, keepdims=True)
+    we = k_sizes.astype(np.float64)[:, None, :] * np.exp(s)
+    prob = we / np.maximum(we.sum(-1, keepdims=True), 1e-12)
+    order = np.argsort(-prob, axis=-1, kind="stable")
+    sp = np.take_along_axis(prob, order, -1)
+    cum = np.cumsum(sp, -1)
+    remove = np.zeros_like(cum, dtype=bool)
+    remove[..., 1:] = cum[..., :-1] > p
+    if min_kc_ratio > 0:
+        remove[..., : int(min_kc_ratio * kn)] = False
+    out = np.zeros((bh, qn, kn), bool)
+    np.put_along_axis(out, order, ~remove, -1)
+    return out, cum, order
+
+
+def svg_top_p_key_budgets(qc, kc, k_sizes, top_p):
+    """Per-q-cluster key budgets (n8_v6.py:181-230), float64 evaluation."""
+    d = qc.shape[2]
+    logits = np.einsum("bqd,bkd->bqk", qc.astype(np.float64), kc.astype(np.float64)) / math.sqrt(d)
+    logits -= logits.max(2, keepdims=True)
+    we = np.exp(logits) * k_sizes.astype(np.float64)[:, None, :]
+    prob = we / np.maximum(we.sum(2, keepdims=True), 1e-12)
+    order = np.argsort(-prob, axis=2, kind="stable")
+    cum = np.cumsum(np.take_along_axis(prob, order, 2), 2)
+    keep = cum <= top_p
+    keep = np.concatenate([np.ones_like(keep[:, :, :1]), keep[:, :, :-1]], axis=2)
+    sizes_sorted = np.take_along_axis(
+        np.broadcast_to(k_sizes.astype(np.int64)[:, None, :], prob.shape), order, 2)
+    return (sizes_sorted * keep).sum(2)
+
+
+def select_budget(scores, sizes, budgets, mode=0):
+    """Budget selector; mode 0 = n8_ops.cu:271-322, mode 1 = selector_budget.py:10-54.
+    Returns bool [BH, Qc+1, Kc+1] with the reference's header row/column."""
+    s = np.ascontiguousarray(scores, np.float32)
+    bh, qn, kn = s.shape
+    out = np.zeros((bh, qn + 1, kn + 1), np.uint8)
+    c_lib().oracle_select_budget(
+        s, np.ascontiguousarray(sizes, np.int32), np.ascontiguousarray(budgets, np.int32),
+        bh, qn, kn, int(mode), out)
+    return out.astype(bool)
+
+
+def compact_selected_clusters(mask):
+    """Ascending kept ids per row + counts (n8_ops.cu:324-355)."""
+    m = np.asarray(mask, bool)
+    kn = m.shape[-1]
+    flat = m.reshape(-1, kn)
+    ids = np.zeros(flat.shape, np.int32)
+    counts = np.zeros(flat.shape[0], np.int32)
+    for r in range(flat.shape[0]):
+        sel = np.nonzero(flat[r])[0]
+        ids[r, : sel.size] = sel
+        counts[r] = sel.size
+    return ids.reshape(m.shape), counts.reshape(m.shape[:-1])
+
+
+def density(dynamic_map, q_sizes, k_sizes):
+    """Kept pairs / all pairs per (cfg, head) (kmeans_utils.py:285-303)."""
+    block = q_sizes[..., :, None].astype(np.float64) * k_sizes[..., None, :].astype(np.float64)
+    return (block * dynamic_map).sum((-2, -1)) / block.sum((-2, -1))
+
+
+# ----------------------------------------------------------------------------
+# attention
+# ----------------------------------------------------------------------------
+
+def _cum(sizes):
+    return np.concatenate([np.zeros(sizes.shape[:-1] + (1,), np.int64),
+                           np.cumsum(sizes.astype(np.int64), -1)], -1)
+
+
+def block_sparse_attention_loop(q, k, v, dynamic_map, q_sizes, k_sizes):
+    """Loop-faithful restatement of dynamic_block_sparse_fwd_torch
+    (kmeans_utils.py:1748-1841): per q-block online softmax over kept k-blocks,
+    float32 arithmetic, acc / max(l, 1e-12).  q,k,v [B,H,S,D]."""
+    B, H, S, D = q.shape
+    qn = q_sizes.shape[-1]
+    kn = k_sizes.shape[-1]
+    qcum, kcum = _cum(q_sizes), _cum(k_sizes)
+    out = np.zeros_like(q, dtype=np.float32)
+    scale = np.float32(D ** -0.5)
+    for b in range(B):
+        for h in range(H):
+            for i in range(qn):
+                q0, q1 = qcum[b, h, i], qcum[b, h, i + 1]
+                if q1 == q0:
+                    continue
+                qb = q[b, h, q0:q1].astype(np.float32)
+                m = np.full((q1 - q0, 1), -np.inf, np.float32)
+                l = np.zeros((q1 - q0, 1), np.float32)
+                acc = np.zeros((q1 - q0, D), np.float32)
+                for j in range(kn):
+                    if not dynamic_map[b, h, i, j]:
+                        continue
+                    k0, k1 = kcum[b, h, j], kcum[b, h, j + 1]
+                    if k1 == k0:
+                        continue
+                    kb = k[b, h, k0:k1].astype(np.float32)
+                    vb = v[b, h, k0:k1].astype(np.float32)
+                    s = (qb @ kb.T) * scale
+                    mn = np.maximum(m, s.max(-1, keepdims=True))
+                    pij = np.exp(s - mn)
+                    a = np.exp(m - mn)
+                    l = l * a + pij.sum(-1, keepdims=True)
+                    acc = acc * a + pij @ vb
+                    m = mn
+                out[b, h, q0:q1] = acc / np.maximum(l, 1e-12)
+    return out
+
+
+def block_sparse_attention_dense(q, k, v, dynamic_map, q_sizes, k_sizes, return_lse=False):
+    """Closed form in float64: softmax over the kept keys of each query row.
+    Row i of q-cluster a attends key j of k-cluster c iff map[a, c].
+    Rows with no kept key get 0 (and lse = -inf)."""
+    B, H, S, D = q.shape
+    out = np.zeros((B, H, S, D), np.float64)
+    lse = np.full((B, H, S), -np.inf, np.float64)
+    for b in range(B):
+        for h in range(H):
+            ql = np.repeat(np.arange(q_sizes.shape[-1]), q_sizes[b, h].astype(np.int64))
+            kl = np.repeat(np.arange(k_sizes.shape[-1]), k_sizes[b, h].astype(np.int64))
+            mask = dynamic_map[b, h][ql][:, kl]
+            s = (q[b, h].astype(np.float64) @ k[b, h].astype(np.float64).T) / math.sqrt(D)
+            s = np.where(mask, s, -np.inf)
+            mx = s.max(-1, keepdims=True)
+            has = np.isfinite(mx[:, 0])
+            e = np.exp(s - np.where(np.isfinite(mx), mx, 0.0))
+            e = np.where(mask, e, 0.0)
+            l = e.sum(-1, keepdims=True)
+            o = (e @ v[b, h].astype(np.float64)) / np.maximum(l, 1e-300)
+            out[b, h] = np.where(has[:, None], o, 0.0)
+            lse[b, h] = np.where(has, mx[:, 0] + np.log(np.maximum(l[:, 0], 1e-300)), -np.inf)
+    if return_lse:
+        return out, lse
+    return out
+
+
+def dense_attention(q, k, v):
+    """softmax(q k^T / sqrt(D)) v in float64 (F.scaled_dot_product_attention,
+    n8_v6.py:1236-1243).  q [BH,M,D], k/v [BH,S,D]."""
+    d = q.shape[-1]
+    s = np.einsum("bmd,bsd->bms", q.astype(np.float64), k.astype(np.float64)) / math.sqrt(d)
+    s -= s.max(-1, keepdims=True)
+    e = np.exp(s)
+    return np.einsum("bms,bsd->bmd", e, v.astype(np.float64)) / e.sum(-1, keepdims=True)
+
+
+# ----------------------------------------------------------------------------
+# probes and reduced-rank residual repair (models/cosmos3/residual_repair.py)
+# ----------------------------------------------------------------------------
+
+def _probe_distances(features, labels, num_clusters):
+    """Per-token squared distance to its fp32 cluster center.
+
+    Centers: float64 sums (exact for bf16-valued features) / size, rounded to
+    fp32 (residual_repair.py:162-180 builds fp32 centers with scatter_add).
+    Distance: sequential over d, separate fp32 multiply and add (canonical)."""
+    bh, n, r = features.shape
+    f = features.astype(np.float32)
+    sizes = np.zeros((bh, num_clusters), np.int64)
+    centers = np.zeros((bh, num_clusters, r), np.float32)
+    for h in range(bh):
+        sizes[h] = np.bincount(labels[h], minlength=num_clusters)
+        s = np.zeros((num_clusters, r), np.float64)
+        np.add.at(s, labels[h].astype(np.int64), f[h].astype(np.float64))
+        centers[h] = (s / np.maximum(sizes[h], 1)[:, None]).astype(np.float32)
+    dist = np.zeros((bh, n), np.float32)
+    gathered = np.take_along_axis(centers, labels[..., None].astype(np.int64), 1)
+    diff = (f - gathered).astype(np.float32)
+    for t in range(r):
+        col = diff[:, :, t]
+        dist = (dist + (col * col).astype(np.float32)).astype(np.float32)
+    return sizes, dist
+
+
+def _weights_for(selected, labels, sizes, num_clusters):
+    bh = selected.shape[0]
+    w = np.zeros(selected.shape, np.float32)
+    for h in range(bh):
+        sl = labels[h][selected[h]]
+        sampled = np.bincount(sl, minlength=num_clusters)
+        gw = sizes[h].astype(np.float32) / np.maximum(sampled, 1).astype(np.float32)
+        wh = gw[sl]
+        w[h] = wh / max(np.float32(wh.mean(dtype=np.float64)), np.float32(1e-20))
+    return w
+
+
+def select_role_equal_probes_vectorized(features, labels, num_clusters, rows):
+    """residual_repair.py:118-208.  One representative per group (nearest token
+    to the group center, lowest token id on exact ties), groups ordered by size
+    descending (stable), first `rows`; empty-group slots fall back to token j.
+    Requires rows <= num_clusters."""
+    bh, n, _ = features.shape
+    count = min(max(1, int(rows)), int(n))
+    if count > num_clusters:
+        raise RuntimeError("vectorized probes require rows <= num_clusters")
+    sizes, dist = _probe_distances(features, labels, num_clusters)
+    selected = np.zeros((bh, count), np.int64)
+    for h in range(bh):
+        best_d = np.full(num_clusters, np.inf, np.float32)
+        np.minimum.at(best_d, labels[h], dist[h])
+        cand = np.where(dist[h] == best_d[labels[h]], np.arange(n), n)
+        best_i = np.full(num_clusters, n, np.int64)
+        np.minimum.at(best_i, labels[h], cand)
+        order = np.argsort(-sizes[h], kind="stable")
+        sel = best_i[order][:count]
+        sel = np.where(sel < n, sel, np.arange(count))
+        selected[h] = sel
+    weights = _weights_for(selected, labels, sizes, num_clusters)
+    return selected, weights
+
+
+def select_role_equal_probes(features, labels, num_clusters, rows):
+    """residual_repair.py:36-115.  Representative rounds: each round takes the
+    nearest remaining token of every non-exhausted group in size order, until
+    `rows` probes are chosen.  Works for rows > num_clusters."""
+    bh, n, _ = features.shape
+    count = min(max(1, int(rows)), int(n))
+    sizes, dist = _probe_distances(features, labels, num_clusters)
+    selected = np.zeros((bh, count), np.int64)
+    for h in range(bh):
+        remaining = dist[h].copy()
+        order = np.argsort(-sizes[h], kind="stable")
+        chosen = []
+        while len(chosen) < count:
+            best_d = np.full(num_clusters, np.inf, np.float32)
+            np.minimum.at(best_d, labels[h], remaining)
+            cand = np.where(remaining == best_d[labels[h]], np.arange(n), n)
+            best_i = np.full(num_clusters, n, np.int64)
+            np.minimum.at(best_i, labels[h], cand)
+            c = best_i[order]
+            c = c[c < n]
+            if c.size == 0:
+                break
+            take = c[: count - len(chosen)]
+            chosen.extend(take.tolist())
+            remaining[take] = np.inf
+        if len(chosen) != count:
+            raise RuntimeError("probe selection under-filled")
+        selected[h] = np.array(chosen, np.int64)
+    weights = _weights_for(selected, labels, sizes, num_clusters)
+    return selected, weights
+
+
+def select_first_token_largest_groups(labels, num_clusters, rows):
+    """residual_repair.py:211-260: first token of each of the largest groups;
+    weight = group size normalized to mean 1."""
+    bh, n = labels.shape
+    count = min(max(1, int(rows)), int(n))
+    if count > num_clusters:
+        raise RuntimeError("first-token probes require rows <= num_clusters")
+    selected = np.zeros((bh, count), np.int64)
+    weights = np.zeros((bh, count), np.float32)
+    for h in range(bh):
+        sizes = np.bincount(labels[h], minlength=num_clusters)
+        first = np.full(num_clusters, n, np.int64)
+        np.minimum.at(first, labels[h], np.arange(n))
+        order = np.argsort(-sizes, kind="stable")
+        sel = first[order][:count]
+        sel = np.where(sel < n, sel, np.arange(count))
+        selected[h] = sel
+        ss = sizes[labels[h][sel]].astype(np.float32)
+        weights[h] = ss / max(np.float32(ss.mean(dtype=np.float64)), np.float32(1e-20))
+    return selected, weights
+
+
+def fit_reduced_rank_residual(x_fit, y_fit, rank, ridge, weights=None,
+                              basis_source="raw_residual", dtype=np.float64):
+    """Weighted ridge reduced-rank regression (residual_repair.py:263-465).
+
+    Standardize X with weighted mean/std (scale clamped at 1e-5), center Y.
+    M < P: dual solve (Xw Xw^T + ridge I) dual = Yw; weight = Xw^T dual.
+    M >= P: primal solve (Xw^T Xw + ridge I) W = Xw^T Yw.
+    Basis: top-`rank` eigenvectors of the weighted output gram of the raw
+    (centered) residual ("raw_residual") or of the fitted values.
+    left = W basis.  Returns (x_mean[BH,1,P], x_scale, y_mean[BH,1,D], left[BH,P,r], basis[BH,D,r]).
+    """
+    x = x_fit.astype(dtype)
+    y = y_fit.astype(dtype)
+    bh, m, p = x.shape
+    if weights is None:
+        w = np.ones((bh, m, 1), dtype)
+        x_mean = x.mean(1, keepdims=True)
+        x_scale = np.maximum(x.std(1, ddof=1, keepdims=True), 1e-5)
+        y_mean = y.mean(1, keepdims=True)
+    else:
+        w = weights.astype(dtype)[:, :, None]
+        w_sum = np.maximum(w.sum(1, keepdims=True), 1e-20)
+        x_mean = (w * x).sum(1, keepdims=True) / w_sum
+        x_var = (w * (x - x_mean) ** 2).sum(1, keepdims=True) / w_sum
+        x_scale = np.maximum(np.sqrt(x_var), 1e-5)
+        y_mean = (w * y).sum(1, keepdims=True) / w_sum
+    xn = (x - x_mean) / x_scale
+    yc = y - y_mean
+    sw = np.sqrt(w)
+    xw = xn * sw
+    yw = yc * sw
+    eye_p = np.eye(p, dtype=dtype)
+    if m < p:
+        gram = xw @ np.swapaxes(xw, 1, 2) + ridge * np.eye(m, dtype=dtype)
+        dual = np.linalg.solve(gram, yw)
+        weight = np.swapaxes(xw, 1, 2) @ dual
+    else:
+        gram = np.swapaxes(xw, 1, 2) @ xw + ridge * eye_p
+        rhs = np.swapaxes(xw, 1, 2) @ yw
+        weight = np.linalg.solve(gram, rhs)
+    fitted = xn @ weight
+    values = yc if basis_source == "raw_residual" else fitted
+    out_gram = np.swapaxes(values, 1, 2) @ (values * w)
+    _evals, evecs = np.linalg.eigh(out_gram)
+    basis = evecs[:, :, -rank:]
+    left = weight @ basis
+    return x_mean, x_scale, y_mean, left, basis
+
+
+def recover_nonfinite_rrr_state(state, previous):
+    """Per-head fallback (residual_repair.py:509-587): a head whose state holds
+    a non-finite value takes the previous state, or a zero correction
+    (mean 0, scale 1, y_mean 0, left 0, basis 0) when there is none."""
+    bh = state[0].shape[0]
+    rec = np.zeros(bh, bool)
+    for t in state:
+        rec |= ~np.isfinite(t.reshape(bh, -1)).all(1)
+    if previous is None:
+        fb = (np.zeros_like(state[0]), np.ones_like(state[1]), np.zeros_like(state[2]),
+              np.zeros_like(state[3]), np.zeros_like(state[4]))
+    else:
+        fb = previous
+    sel = tuple(np.where(rec.reshape((bh,) + (1,) * (c.ndim - 1)), o, c) for c, o in zip(state, fb))
+    return sel, rec
+
+
+def repair_apply(base, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap):
+    """out = base + alpha * (((base - mu)/sigma) left basis^T + y_mean), optional
+    norm cap (residual_repair.py:95-155 kernel, :620-646 torch).  float64."""
+    b = base.astype(np.float64)
+    z = (b - x_mean) / x_scale
+    corr = (z @ left) @ np.swapaxes(basis, 1, 2) + y_mean
+    if norm_cap > 0.0:
+        bn = np.linalg.norm(b, axis=2, keepdims=True)
+        cn = np.maximum(np.linalg.norm(corr, axis=2, keepdims=True), 1e-20)
+        corr = corr * np.minimum(norm_cap * bn / cn, 1.0)
+    return b + alpha * corr
+
+
+def exact_probe_scatter(out, rows, dense_probes):
+    """out[bh, rows[bh,m]] = dense[bh,m] (residual_repair.py:257-282)."""
+    o = out.copy()
+    for h in range(out.shape[0]):
+        o[h, rows[h].astype(np.int64)] = dense_probes[h]
+    return o
+
+
+# ----------------------------------------------------------------------------
+# the whole layer (SAP top-p route + block-sparse attention + N8 repair)
+# ----------------------------------------------------------------------------
+
+@dataclass
+class LayerConfig:
+    q_clusters: int
+    k_clusters: int
+    kmeans_iters: int
+    top_p: float
+    probes: int
+    min_kc_ratio: float = 0.0
+    repair_rank: int = 16
+    repair_ridge: float = 0.1
+    repair_alpha: float = 1.0
+    repair_norm_cap: float = 0.0
+    init_seed: int = 0
+    x_sq_mode: str = "bf16"
+
+
+def sparsepr_layer(q, k, v, cfg: LayerConfig, timings: dict | None = None, bf16=True):
+    """One SparsePR attention layer on the CPU, float path of the oracle.
+
+    Composition (wan22.py:2221-2276 for the route and attention, n8_v6.py:1174-1444
+    for the repair, hunyuanvideo.py:160-239 for the ordering):
+      1. k-means of Q and K (Lloyd, fixed iterations, first-k init);
+      2. top-p cluster-pair map from the centroids;
+      3. permute Q/K/V into cluster order, block-sparse attention, inverse permute;
+      4. probes = role-equal representatives of the Q clusters (features = Q),
+         dense probe attention, RRR fit, apply, exact probe scatter.
+    q, k, v [BH, N, D] float32 (bf16-valued when bf16=True).
+    """
+    import time
+
+    def mark(name, t0):
+        if timings is not None:
+            timings[name] = timings.get(name, 0.0) + (time.perf_counter() - t0) * 1e3
+        return time.perf_counter()
+
+    t = time.perf_counter()
+    bh, n, d = q.shape
+    qi = first_k_init(q, cfg.q_clusters, cfg.init_seed)
+    ki = first_k_init(k, cfg.k_clusters, cfg.init_seed + 1)
+    q_labels, q_cent, q_sizes, _ = batch_kmeans_euclid(
+        q, cfg.q_clusters, cfg.kmeans_iters, 0.0, qi, cfg.x_sq_mode, bf16)
+    k_labels, k_cent, k_sizes, _ = batch_kmeans_euclid(
+        k, cfg.k_clusters, cfg.kmeans_iters, 0.0, ki, cfg.x_sq_mode, bf16)
+    t = mark("kmeans", t)
+    dmap = identify_dynamic_map(q_cent, k_cent, k_sizes, cfg.top_p, cfg.min_kc_ratio)
+    t = mark("select", t)
+    q_idx = argsort_labels(q_labels)
+    k_idx = argsort_labels(k_labels)
+    qp, kp, vp = permute_rows(q, q_idx), permute_rows(k, k_idx), permute_rows(v, k_idx)
+    t = mark("permute", t)
+    o = block_sparse_attention_loop(qp[None], kp[None], vp[None], dmap[None],
+                                    q_sizes[None], k_sizes[None])[0]
+    if bf16:
+        o = to_bf16(o)
+    t = mark("attention", t)
+    base = inverse_permute_rows(o, q_idx)
+    t = mark("permute", t)
+    rows_sel = min(cfg.probes, n)
+    if rows_sel <= cfg.q_clusters:
+        rows, weights = select_role_equal_probes_vectorized(q, q_labels, cfg.q_clusters, rows_sel)
+    else:
+        rows, weights = select_role_equal_probes(q, q_labels, cfg.q_clusters, rows_sel)
+    qprobe = np.take_along_axis(q, rows[..., None], 1)
+    dense = dense_attention(qprobe, k, v).astype(np.float32)
+    xfit = np.take_along_axis(base, rows[..., None], 1).astype(np.float32)
+    yfit = dense - xfit
+    state = fit_reduced_rank_residual(xfit, yfit, min(cfg.repair_rank, rows.shape[1], d),
+                                      cfg.repair_ridge, weights, dtype=np.float32)
+    state, _ = recover_nonfinite_rrr_state(state, None)
+    corrected = repair_apply(base, *state, cfg.repair_alpha, cfg.repair_norm_cap)
+    corrected = corrected.astype(np.float32)
+    if bf16:
+        corrected = to_bf16(corrected)
+        dense_out = to_bf16(dense)
+    else:
+        dense_out = dense
+    out = exact_probe_scatter(corrected, rows, dense_out)
+    mark("repair", t)
+    return {
+        "out": out, "base": base, "q_labels": q_labels, "k_labels": k_labels,
+        "q_centroids": q_cent, "k_centroids": k_cent, "q_sizes": q_sizes,
+        "k_sizes": k_sizes, "map": dmap, "rows": rows, "weights": weights,
+        "dense": dense, "density": density(dmap, q_sizes, k_sizes),
+    }
+
+

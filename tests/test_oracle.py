@@ -1,0 +1,478 @@
+"""Pins the CPU oracle against the reference's known-answer test, closed forms,
+brute force on tiny inputs and invariants.  CPU only."""
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _ulp_diff(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+# --------------------------------------------------------------------------- exp
+
+def test_expf_within_two_ulp_of_float64_exp(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.uniform(-87.0, 0.0, 200000), rng.uniform(-1.0, 1.0, 50000),
+        rng.uniform(0.0, 88.0, 20000), np.array([0.0, -0.0, -1e-30, -86.99, -87.0, 1.0])
+    ]).astype(np.float32)
+    got = oracle.expf(x)
+    ref = np.exp(x.astype(np.float64)).astype(np.float32)
+    assert _ulp_diff(got, ref).max() <= 2
+    assert oracle.expf(np.array([-87.5, -200.0], np.float32)).tolist() == [0.0, 0.0]
+    assert np.isinf(oracle.expf(np.array([89.0], np.float32))[0])
+
+
+def test_bf16_rounding_nearest_even(oracle):
+    # 1 + 2^-8 is exactly half way between bf16(1) and bf16(1 + 2^-7): ties to even (1.0)
+    vals = np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -2.5, 3.0e38], np.float32)
+    got = oracle.to_bf16(vals)
+    assert got[0] == 1.0
+    assert got[1] == np.float32(1.0 + 2 ** -6)
+    assert got[2] == -2.5
+    assert np.isinf(oracle.to_bf16(np.array([3.4e38], np.float32))[0])
+
+
+# --------------------------------------------------------------------------- selector KAT
+
+def test_selector_known_answer(oracle):
+    kat = json.loads((GOLDEN / "selector_kat.json").read_text())
+    scores = np.array(kat["scores"], np.float32)
+    sizes = np.array(kat["sizes"], np.int32)
+    budgets = np.array(kat["budgets"], np.int32)
+    for mode in (0, 1):
+        out = oracle.select_budget(scores, sizes, budgets, mode=mode)
+        assert out[0, 1:, 1:].tolist() == kat["expected_mask"]
+        assert out[0, 0, 0] == kat["expected_header_00"]
+        assert bool(out[0, 1:, 0].all()) == kat["expected_column0"]
+    ids, counts = oracle.compact_selected_clusters(np.array(kat["expected_mask"]))
+    assert counts.tolist() == kat["expected_counts"][0]
+    assert ids[0, :3].tolist() == kat["expected_ids"][0][0]
+    assert ids[1, :2].tolist() == kat["expected_ids"][0][1]
+
+
+def test_selector_modes_differ_only_on_zero_cost_before_crossing(oracle):
+    # sorted costs [5, 0, 3], budget 6: mode 0 adds the first positive crossing (c2);
+    # mode 1 adds sorted position `count`=1, the zero-cost cluster c1.
+    scores = np.array([[[3.0, 2.0, 1.0]]], np.float32)
+    sizes = np.array([[5, 0, 3]], np.int32)
+    budgets = np.array([[6]], np.int32)
+    m0 = oracle.select_budget(scores, sizes, budgets, 0)[0, 1, 1:]
+    m1 = oracle.select_budget(scores, sizes, budgets, 1)[0, 1, 1:]
+    assert m0.tolist() == [True, False, True]
+    assert m1.tolist() == [True, True, False]
+
+
+def _select_budget_brute(scores, sizes, budgets):
+    """Python restatement of the per-row walk (mode 0) for random cases."""
+    bh, qn, kn = scores.shape
+    out = np.zeros((bh, qn, kn), bool)
+    for h in range(bh):
+        for i in range(qn):
+            order = sorted(range(kn), key=lambda j: (-float(scores[h, i, j]), j))
+            sel, cross = 0, None
+            for j in order:
+                c = int(sizes[h, j])
+                if c <= 0:
+                    continue
+                if cross is None and sel + c <= budgets[h, i]:
+                    out[h, i, j] = True
+                    sel += c
+                elif cross is None:
+                    cross = j
+            if budgets[h, i] > 0 and sel < budgets[h, i] and cross is not None:
+                out[h, i, cross] = True
+    return out
+
+
+def test_selector_random_vs_walk(oracle):
+    rng = np.random.default_rng(3)
+    scores = rng.integers(0, 6, (2, 5, 9)).astype(np.float32)  # many ties
+    sizes = rng.integers(0, 7, (2, 9)).astype(np.int32)
+    budgets = rng.integers(0, 25, (2, 5)).astype(np.int32)
+    got = oracle.select_budget(scores, sizes, budgets, 0)[:, 1:, 1:]
+    assert (got == _select_budget_brute(scores, sizes, budgets)).all()
+
+
+# --------------------------------------------------------------------------- k-means
+
+def _bf16_data(oracle, rng, shape, scale=1.0):
+    return oracle.to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def test_assign_matches_brute_force_with_planted_ties(oracle):
+    rng = np.random.default_rng(1)
+    x = _bf16_data(oracle, rng, (2, 40, 8))
+    c = _bf16_data(oracle, rng, (2, 6, 8))
+    c[:, 4] = c[:, 1]  # duplicate centroid: every tie must resolve to index 1
+    x[:, 0] = c[:, 1]  # a point exactly on a centroid
+    x_sq = oracle.x_sq_for(x, "fp32")
+    labels, _ = oracle.kmeans_assign(x, c, x_sq)
+    for b in range(2):
+        for n in range(40):
+            best, bi = None, None
+            for k in range(6):
+                dot = sum(float(x[b, n, t]) * float(c[b, k, t]) for t in range(8))
+                csq = float(np.float32(sum(float(c[b, k, t]) ** 2 for t in range(8))))
+                d = max(float(x_sq[b, n]) + csq - 2.0 * dot, 0.0)
+                if best is None or d < best:
+                    best, bi = d, k
+            assert labels[b, n] == bi
+    assert (labels != 4).all()
+
+
+def test_x_sq_modes(oracle):
+    rng = np.random.default_rng(2)
+    x = _bf16_data(oracle, rng, (1, 16, 128))
+    f32 = oracle.x_sq_for(x, "fp32")
+    b16 = oracle.x_sq_for(x, "bf16")
+    ref = (x.astype(np.float64) ** 2).sum(-1)
+    assert np.allclose(f32, ref, rtol=1e-6)
+    assert np.allclose(b16, ref, rtol=2 ** -7)
+    assert (oracle.to_bf16(b16) == b16).all()
+
+
+def test_centroid_update_matches_double_loop(oracle):
+    rng = np.random.default_rng(4)
+    x = _bf16_data(oracle, rng, (2, 64, 16))
+    labels = rng.integers(0, 7, (2, 64)).astype(np.int32)
+    labels[labels == 5] = 6  # cluster 5 empty
+    old = _bf16_data(oracle, rng, (2, 7, 16))
+    cent, mean32, counts = oracle.centroid_update(x, labels, old, out_bf16=True)
+    loop = oracle.loop_centroid_update(x, labels, old)
+    assert (mean32 == loop.astype(np.float32)).all()
+    assert (cent == oracle.to_bf16(loop.astype(np.float32))).all()
+    assert (cent[:, 5] == old[:, 5]).all()
+    assert counts.sum(1).tolist() == [64, 64]
+
+
+def test_lloyd_return_convention(oracle):
+    rng = np.random.default_rng(5)
+    x = _bf16_data(oracle, rng, (1, 200, 8))
+    init = oracle.first_k_init(x, 5, seed=0)
+    # tol larger than any shift: break in the first iteration, return the init
+    labels, cent, counts, iters = oracle.batch_kmeans_euclid(x, 5, 7, tol=1e9, init_centroids=init)
+    assert iters == 1
+    assert (cent == init).all()
+    l0, _ = oracle.kmeans_assign(x, init, oracle.x_sq_for(x, "bf16"))
+    assert (labels == l0).all()
+    # tol = 0 never breaks: labels come from the last assignment, centroids from the last update
+    labels, cent, counts, iters = oracle.batch_kmeans_euclid(x, 5, 3, tol=0.0, init_centroids=init)
+    assert iters == 3
+    c = init
+    for _ in range(3):
+        lab, _ = oracle.kmeans_assign(x, c, oracle.x_sq_for(x, "bf16"))
+        c, _, cnt = oracle.centroid_update(x, lab, c, True)
+    assert (lab == labels).all() and (c == cent).all() and (cnt == counts).all()
+
+
+def test_lloyd_objective_non_increasing(oracle):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((1, 500, 4)).astype(np.float32)
+    c = oracle.first_k_init(x, 8, seed=1)
+    prev = None
+    for _ in range(6):
+        lab, dist = oracle.kmeans_assign(x, c, oracle.x_sq_for(x, "fp32"))
+        obj = np.take_along_axis(dist, lab[..., None].astype(np.int64), -1).sum()
+        if prev is not None:
+            assert obj <= prev * (1 + 1e-6)
+        prev = obj
+        c, _, _ = oracle.centroid_update(x, lab, c, out_bf16=False)
+
+
+def test_role_step64_vs_float64(oracle):
+    rng = np.random.default_rng(7)
+    f = rng.standard_normal((2, 300, 64)).astype(np.float32)
+    c = rng.standard_normal((2, 20, 64)).astype(np.float32)
+    c[:, 11] = c[:, 3]  # exact tie: lower index wins
+    labels, out, sizes, best = oracle.role_step64(f, c)
+    d64 = ((f[:, :, None, :].astype(np.float64) - c[:, None, :, :]) ** 2).sum(-1)
+    ref = d64.argmin(-1)
+    srt = np.sort(d64, -1)
+    clear = (srt[..., 1] - srt[..., 0]) > 1e-4 * srt[..., 0]
+    assert (labels[clear] == ref[clear]).all()
+    assert (labels != 11).all()
+    assert np.allclose(best, np.take_along_axis(d64, labels[..., None].astype(np.int64), -1)[..., 0], rtol=1e-5)
+    assert sizes.sum(1).tolist() == [300, 300]
+    for h in range(2):
+        for k in range(20):
+            m = labels[h] == k
+            exp = f[h][m].astype(np.float64).mean(0).astype(np.float32) if m.any() else c[h, k]
+            assert (out[h, k] == exp).all()
+
+
+# --------------------------------------------------------------------------- permutation
+
+def test_permutation_invariants(oracle):
+    rng = np.random.default_rng(8)
+    labels = rng.integers(0, 9, (3, 257)).astype(np.int32)
+    idx = oracle.argsort_labels(labels)
+    sorted_labels = np.take_along_axis(labels, idx.astype(np.int64), -1)
+    assert (np.diff(sorted_labels, axis=-1) >= 0).all()
+    for h in range(3):
+        assert sorted(idx[h].tolist()) == list(range(257))
+        for a, b in zip(idx[h][:-1], idx[h][1:]):
+            if labels[h, a] == labels[h, b]:
+                assert a < b  # stable
+    x = rng.standard_normal((3, 257, 5)).astype(np.float32)
+    y = oracle.permute_rows(x, idx)
+    assert (y[1, 7] == x[1, idx[1, 7]]).all()
+    assert (oracle.inverse_permute_rows(y, idx) == x).all()
+    pre, suf = x[:, :200], x[:, 200:]
+    idx2 = oracle.argsort_labels(labels)
+    assert (oracle.permute_concat_rows(pre, suf, idx2) == oracle.permute_rows(x, idx2)).all()
+
+
+# --------------------------------------------------------------------------- top-p map
+
+def _map_inputs(rng, bh=2, qn=6, kn=11, d=16, empty=(3,)):
+    qc = rng.standard_normal((bh, qn, d)).astype(np.float32)
+    kc = rng.standard_normal((bh, kn, d)).astype(np.float32)
+    ks = rng.integers(1, 50, (bh, kn)).astype(np.int32)
+    for e in empty:
+        ks[:, e] = 0
+    return qc, kc, ks
+
+
+def test_topp_map_matches_float64_away_from_threshold(oracle):
+    rng = np.random.default_rng(9)
+    for p in (0.5, 0.8, 0.9, 0.95):
+        qc, kc, ks = _map_inputs(rng)
+        got, cum32, _ = oracle.identify_dynamic_map(qc, kc, ks, p, return_cum=True)
+        ref, cum64, _ = oracle.identify_dynamic_map_f64(qc, kc, ks, p)
+        near = (np.abs(cum64 - p) < 1e-5).any(-1)
+        assert (got[~near] == ref[~near]).all()
+        assert np.allclose(cum32, cum64, atol=1e-6)
+
+
+def test_topp_map_invariants_and_brute_force(oracle):
+    rng = np.random.default_rng(10)
+    qc, kc, ks = _map_inputs(rng, bh=1, qn=4, kn=7, d=8, empty=(2,))
+    p = 0.7
+    got = oracle.identify_dynamic_map(qc, kc, ks, p)
+    for i in range(4):
+        s = [sum(float(qc[0, i, t]) * float(kc[0, j, t]) for t in range(8)) / math.sqrt(8) for j in range(7)]
+        mx = max(s)
+        w = [ks[0, j] * math.exp(s[j] - mx) for j in range(7)]
+        tot = sum(w)
+        probs = [wj / tot for wj in w]
+        order = sorted(range(7), key=lambda j: (-probs[j], j))
+        keep, cum = set(), 0.0
+        for r, j in enumerate(order):
+            if r == 0 or cum <= p:
+                keep.add(j)
+            cum += probs[j]
+        assert {j for j in range(7) if got[0, i, j]} == keep
+        assert got[0, i].sum() >= 1
+        assert not got[0, i, 2] or len(keep) == 7  # empty cluster only kept when everything is
+        assert sum(probs[j] for j in keep) >= p - 1e-6
+    many = oracle.identify_dynamic_map(qc, kc, ks, 0.01, min_kc_ratio=0.5)
+    assert (many.sum(-1) >= 3).all()
+
+
+# --------------------------------------------------------------------------- attention
+
+def _block_problem(oracle, rng, qn=5, kn=7, d=16, zero_q=2, zero_k=4, empty_row=1):
+    qs = rng.integers(1, 9, (1, 2, qn))
+    ks = rng.integers(1, 9, (1, 2, kn))
+    qs[..., zero_q] = 0
+    ks[..., zero_k] = 0
+    S = int(max(qs.sum(-1).max(), ks.sum(-1).max()))
+    qs[..., -1] += S - qs.sum(-1)
+    ks[..., -1] += S - ks.sum(-1)
+    q = rng.standard_normal((1, 2, S, d)).astype(np.float32)
+    k = rng.standard_normal((1, 2, S, d)).astype(np.float32)
+    v = rng.standard_normal((1, 2, S, d)).astype(np.float32)
+    m = rng.random((1, 2, qn, kn)) < 0.5
+    m[..., empty_row, :] = False
+    return q, k, v, m, qs, ks
+
+
+def test_block_sparse_loop_equals_dense_closed_form(oracle):
+    rng = np.random.default_rng(11)
+    for _ in range(3):
+        q, k, v, m, qs, ks = _block_problem(oracle, rng)
+        loop = oracle.block_sparse_attention_loop(q, k, v, m, qs, ks)
+        dense, lse = oracle.block_sparse_attention_dense(q, k, v, m, qs, ks, return_lse=True)
+        assert np.allclose(loop, dense, atol=2e-5, rtol=1e-4)
+        # rows of the all-dropped q-cluster are zero with lse = -inf
+        r0 = int(qs[0, 0, :1].sum())
+        r1 = r0 + int(qs[0, 0, 1])
+        assert (dense[0, 0, r0:r1] == 0).all() and np.isneginf(lse[0, 0, r0:r1]).all()
+
+
+def test_block_sparse_full_map_is_dense_attention(oracle):
+    rng = np.random.default_rng(12)
+    q, k, v, m, qs, ks = _block_problem(oracle, rng, empty_row=0, zero_q=0, zero_k=0)
+    m[:] = True
+    full = oracle.block_sparse_attention_dense(q, k, v, m, qs, ks)
+    d = oracle.dense_attention(q[0], k[0], v[0])
+    assert np.allclose(full[0], d, atol=1e-12)
+    # per-row closed form for one row
+    s = q[0, 1, 3].astype(np.float64) @ k[0, 1].T.astype(np.float64) / math.sqrt(q.shape[-1])
+    e = np.exp(s - s.max())
+    assert np.allclose(d[1, 3], (e / e.sum()) @ v[0, 1].astype(np.float64))
+
+
+def test_density(oracle):
+    m = np.array([[[[True, False], [False, True]]]])
+    qs = np.array([[[1, 3]]])
+    ks = np.array([[[2, 2]]])
+    # kept pairs = 1*2 + 3*2 = 8 of 16
+    assert oracle.density(m, qs, ks)[0, 0] == 0.5
+
+
+# --------------------------------------------------------------------------- probes
+
+def _probe_data(oracle, rng, bh=2, n=120, r=6, c=9):
+    f = oracle.to_bf16(rng.standard_normal((bh, n, r)).astype(np.float32))
+    labels = rng.integers(0, c, (bh, n)).astype(np.int32)
+    labels[:, :3] = 0
+    labels[labels == 4] = 5  # group 4 empty
+    return f, labels
+
+
+def test_probe_selection_brute_force(oracle):
+    rng = np.random.default_rng(13)
+    f, labels = _probe_data(oracle, rng)
+    f[0, 10] = f[0, 20]
+    labels[0, 10] = labels[0, 20]  # duplicate token: lower id wins
+    rows, weights = oracle.select_role_equal_probes_vectorized(f, labels, 9, 6)
+    for h in range(2):
+        sizes = [int((labels[h] == g).sum()) for g in range(9)]
+        order = sorted(range(9), key=lambda g: (-sizes[g], g))
+        expect = []
+        for g in order[:6]:
+            mem = [t for t in range(120) if labels[h, t] == g]
+            if not mem:
+                expect.append(None)
+                continue
+            cen = [sum(float(f[h, t, j]) for t in mem) / len(mem) for j in range(6)]
+            dist = [sum((float(f[h, t, j]) - cen[j]) ** 2 for j in range(6)) for t in mem]
+            best = min(dist)
+            expect.append(min(t for t, dd in zip(mem, dist) if dd <= best * (1 + 1e-6) + 1e-12))
+        for pos, e in enumerate(expect):
+            assert rows[h, pos] == (pos if e is None else e)
+        assert abs(weights[h].mean() - 1.0) < 1e-6
+        sl = labels[h][rows[h]]
+        raw = np.array([sizes[g] / max(1, int((sl == g).sum())) for g in sl])
+        assert np.allclose(weights[h], raw / raw.mean(), rtol=1e-6)
+    assert rows[0].tolist().count(20) == 0 or 10 not in rows[0].tolist()
+
+
+def test_probe_loop_equals_vectorized_when_rows_fit(oracle):
+    rng = np.random.default_rng(14)
+    f, labels = _probe_data(oracle, rng)
+    a = oracle.select_role_equal_probes_vectorized(f, labels, 9, 7)
+    b = oracle.select_role_equal_probes(f, labels, 9, 7)
+    assert (a[0] == b[0]).all() and np.allclose(a[1], b[1])
+    # more probes than groups: rounds; every row distinct and valid
+    rows, w = oracle.select_role_equal_probes(f, labels, 9, 30)
+    for h in range(2):
+        assert len(set(rows[h].tolist())) == 30
+    first, wf = oracle.select_first_token_largest_groups(labels, 9, 5)
+    for h in range(2):
+        sizes = [int((labels[h] == g).sum()) for g in range(9)]
+        order = sorted(range(9), key=lambda g: (-sizes[g], g))[:5]
+        assert first[h].tolist() == [int(np.nonzero(labels[h] == g)[0][0]) for g in order]
+        raw = np.array([sizes[g] for g in order], np.float64)
+        assert np.allclose(wf[h], raw / raw.mean(), rtol=1e-6)
+
+
+# --------------------------------------------------------------------------- RRR
+
+def _rrr_inputs(rng, bh=3, m=40, p=12, d=10, weighted=True):
+    x = rng.standard_normal((bh, m, p)).astype(np.float32)
+    y = (x @ rng.standard_normal((bh, p, d)).astype(np.float32) * 0.3
+         + 0.05 * rng.standard_normal((bh, m, d)).astype(np.float32))
+    w = rng.uniform(0.5, 2.0, (bh, m)).astype(np.float32) if weighted else None
+    return x, y, w
+
+
+@pytest.mark.parametrize("m,p", [(40, 12), (8, 12)])
+def test_rrr_normal_equations_and_basis(oracle, m, p):
+    rng = np.random.default_rng(15)
+    x, y, w = _rrr_inputs(rng, m=m, p=p)
+    rank, ridge = 4, 0.1
+    x_mean, x_scale, y_mean, left, basis = oracle.fit_reduced_rank_residual(x, y, rank, ridge, w)
+    wt = w.astype(np.float64)[:, :, None]
+    assert np.allclose((wt * x).sum(1, keepdims=True) / wt.sum(1, keepdims=True), x_mean)
+    xn = (x - x_mean) / x_scale
+    assert np.allclose((wt * xn).sum(1), 0, atol=1e-9)
+    assert np.allclose((wt * xn ** 2).sum(1) / wt.sum(1), 1, atol=1e-9)
+    xw, yw = xn * np.sqrt(wt), (y - y_mean) * np.sqrt(wt)
+    # unrestricted ridge solution from the SVD of Xw (a different algorithm)
+    u, s, vt = np.linalg.svd(xw, full_matrices=False)
+    w_svd = np.swapaxes(vt, 1, 2) @ ((s / (s ** 2 + ridge))[:, :, None] * (np.swapaxes(u, 1, 2) @ yw))
+    assert np.allclose(left, w_svd @ basis, atol=1e-8)
+    # basis: orthonormal, invariant subspace of the output gram with the top eigenvalues
+    g = np.swapaxes(y - y_mean, 1, 2) @ ((y - y_mean) * wt)
+    assert np.allclose(np.swapaxes(basis, 1, 2) @ basis, np.eye(rank), atol=1e-9)
+    proj = basis @ np.swapaxes(basis, 1, 2)
+    assert np.allclose(proj @ g @ basis, g @ basis, atol=1e-8)
+    ev = np.linalg.eigvalsh(g)
+    assert np.allclose(np.trace(np.swapaxes(basis, 1, 2) @ g @ basis, axis1=1, axis2=2), ev[:, -rank:].sum(1))
+
+
+def test_rrr_zero_residual_gives_zero_correction(oracle):
+    rng = np.random.default_rng(16)
+    x, _, w = _rrr_inputs(rng, p=12, d=12)
+    y = np.zeros((3, 40, 12), np.float32)
+    state = oracle.fit_reduced_rank_residual(x, y, 4, 0.1, w)
+    base = rng.standard_normal((3, 50, 12))
+    out = oracle.repair_apply(base, *state, 1.0, 0.0)
+    assert np.allclose(out, base, atol=1e-12)
+
+
+def test_recover_nonfinite_rrr_state(oracle):
+    rng = np.random.default_rng(17)
+    x, y, w = _rrr_inputs(rng)
+    state = oracle.fit_reduced_rank_residual(x, y, 4, 0.1, w)
+    bad = tuple(t.copy() for t in state)
+    bad[3][1, 0, 0] = np.nan
+    sel, rec = oracle.recover_nonfinite_rrr_state(bad, None)
+    assert rec.tolist() == [False, True, False]
+    assert (sel[3][1] == 0).all() and (sel[1][1] == 1).all()
+    assert (sel[3][0] == state[3][0]).all()
+    sel2, rec2 = oracle.recover_nonfinite_rrr_state(bad, state)
+    assert (sel2[3][1] == state[3][1]).all()
+
+
+def test_repair_norm_cap_and_scatter(oracle):
+    rng = np.random.default_rng(18)
+    x, y, w = _rrr_inputs(rng, p=12, d=12)
+    state = oracle.fit_reduced_rank_residual(x, y, 4, 0.1, w)
+    base = rng.standard_normal((3, 30, 12))
+    capped = oracle.repair_apply(base, *state, 1.0, 0.05)
+    corr = capped - base
+    assert (np.linalg.norm(corr, axis=2) <= 0.05 * np.linalg.norm(base, axis=2) + 1e-9).all()
+    rows = np.array([[0, 5], [1, 2], [29, 3]])
+    dense = rng.standard_normal((3, 2, 12))
+    out = oracle.exact_probe_scatter(capped, rows, dense)
+    assert (out[2, 29] == dense[2, 0]).all() and (out[0, 1] == capped[0, 1]).all()
+
+
+# --------------------------------------------------------------------------- whole layer
+
+def test_layer_runs_and_probe_rows_are_exact(oracle):
+    rng = np.random.default_rng(19)
+    bh, n, d = 2, 256, 16
+    q = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    k = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    v = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    cfg = oracle.LayerConfig(q_clusters=8, k_clusters=16, kmeans_iters=3, top_p=0.9, probes=8)
+    res = oracle.sparsepr_layer(q, k, v, cfg)
+    out = res["out"]
+    assert out.shape == (bh, n, d) and np.isfinite(out).all()
+    for h in range(bh):
+        assert (out[h, res["rows"][h]] == oracle.to_bf16(res["dense"][h])).all()
+    assert ((res["density"] > 0) & (res["density"] <= 1)).all()
