@@ -1,0 +1,107 @@
+// Shared helpers for the SparsePR HIP kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+// Status codes returned by every extern "C" entry point.
+enum {
+  SPR_OK = 0,
+  SPR_EINVAL = 1,      // bad argument (shape, size, null pointer, unsupported config)
+  SPR_ELAUNCH = 2,     // HIP launch / runtime error
+  SPR_EWORKSPACE = 3,  // workspace too small
+};
+
+void spr_set_error(const char* fmt, ...);
+
+#define SPR_REQUIRE(cond, ...)         \
+  do {                                 \
+    if (!(cond)) {                     \
+      spr_set_error(__VA_ARGS__);      \
+      return SPR_EINVAL;               \
+    }                                  \
+  } while (0)
+
+#define SPR_LAUNCHED(name)                                                   \
+  do {                                                                       \
+    hipError_t e_ = hipGetLastError();                                       \
+    if (e_ != hipSuccess) {                                                  \
+      spr_set_error("%s: launch failed: %s", name, hipGetErrorString(e_));   \
+      return SPR_ELAUNCH;                                                    \
+    }                                                                        \
+  } while (0)
+
+namespace spr {
+
+// ---------------------------------------------------------------- vector types
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+struct alignas(16) u32x4 {
+  uint32_t x, y, z, w;
+};
+
+// ---------------------------------------------------------------- bf16 <-> f32
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round to nearest even; NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ---------------------------------------------------------------- fp16 <-> f32
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// ---------------------------------------------------------------- exp
+// e^x in fp32 with a fixed evaluation order, used where results must be
+// reproducible bit for bit on the CPU (top-p block selection).  Cody-Waite
+// range reduction with a two-part ln2, degree-7 Taylor polynomial (Horner,
+// fused multiply-adds), exact scaling by 2^n.  x < -87 -> 0, x > 88.5 -> inf.
+__device__ __forceinline__ float canonical_expf(float x) {
+  if (x != x) return x;
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.5f) return __builtin_huge_valf();
+  const float log2e = 1.44269504088896341f;
+  const float ln2_hi = 0.693145751953125f;
+  const float ln2_lo = 1.428606765330187045e-06f;
+  float n = __builtin_rintf(__fmul_rn(x, log2e));
+  float r = __builtin_fmaf(-n, ln2_hi, x);
+  r = __builtin_fmaf(-n, ln2_lo, r);
+  float p = 1.98412698412698413e-04f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-03f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-02f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = static_cast<int>(n);
+  float scale = __uint_as_float(static_cast<uint32_t>(ni + 127) << 23);
+  return __fmul_rn(p, scale);
+}
+
+// ---------------------------------------------------------------- misc
+__host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace spr

@@ -1,0 +1,474 @@
+// Batched Euclidean k-means building blocks (one Lloyd iteration = assign ->
+// counting-sort argsort -> segmented mean).
+//
+// Replaces, for the SparsePR path:
+//   euclid_assign_triton / _euclid_assign_kernel   (flash_kmeans/assign_euclid_triton.py:803-917, :1238-1412)
+//   euclid_assign_inline_xsq_triton               (sparsepr/kmeans_utils.py:775-893)
+//   triton_centroid_update_sorted_euclid          (flash_kmeans/centroid_update_triton.py:316-386)
+//   original_centroids(_triton)                   (kernels/triton/centroid_reduction.py:138-196)
+//   role_cluster_step_q64 / k64                   (kernels/n8_ext/csrc/n8_ops.cu:198-269, :499-539)
+//
+// assign (bf16): crossT[c, x] = C . X^T on v_mfma_f32_32x32x16_bf16.  A = 32
+//   centroids x 16 dims read from an LDS tile, B = 32 points x 16 dims kept in
+//   registers for the whole kernel.  In the 32x32 accumulator a lane owns one
+//   point (column l % 32) and 16 centroids, so the argmin is lane-local plus one
+//   exchange with lane l ^ 32.  dist = max((x_sq + c_sq) - 2 cross, 0); the
+//   lowest index wins among exact minima, as in the reference.
+// mean: one workgroup per (batch, cluster) reads the cluster's rows in sorted
+//   order and accumulates in fp64 (exact for bf16 inputs, so the result does
+//   not depend on summation order); mean32 = float(sum / count); empty
+//   clusters keep the previous centroid.
+// role assign (fp32): exact FP32 distance, sequential fmaf over dims, lowest
+//   index on ties (n8_ops.cu:189-196 better_pair).
+#include "spr_common.h"
+
+namespace {
+
+using spr::u32x4;
+
+constexpr int ASSIGN_THREADS = 256;
+constexpr int ASSIGN_POINTS_PER_WAVE = 64;  // two 32-point MFMA column fragments
+constexpr int ASSIGN_POINTS = 4 * ASSIGN_POINTS_PER_WAVE;
+constexpr int CCHUNK = 64;  // centroids per LDS tile
+
+// x_sq_mode: 0 = fp32 sum of fp32 squares (inline-x_sq kernel),
+//            1 = bf16-rounded squares summed in fp32, result rounded to bf16
+//                (flash_kmeans x_sq buffer of x.dtype).
+template <int D>
+__global__ __launch_bounds__(ASSIGN_THREADS) void kmeans_assign_bf16_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ c, const float* __restrict__ c_sq,
+    const float* __restrict__ x_sq_in, int x_sq_mode, int64_t n, int32_t k, int32_t* __restrict__ labels) {
+  static_assert(D % 32 == 0 && D <= 256, "D must be a multiple of 32, at most 256");
+  constexpr int KSTEPS = D / 16;
+  constexpr int ROW_BYTES = D * 2 + 16;  // padded LDS row: conflict-free 16-byte reads
+  constexpr int PIECES = CCHUNK * D / 8; // 16-byte pieces per centroid tile
+  constexpr int PIECES_PER_THREAD = PIECES / ASSIGN_THREADS;
+  static_assert(PIECES % ASSIGN_THREADS == 0, "tile pieces must divide evenly");
+
+  __shared__ __attribute__((aligned(16))) uint8_t tile[2][CCHUNK * ROW_BYTES];
+  __shared__ float tile_csq[2][CCHUNK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const int64_t b = blockIdx.y;
+  const uint16_t* xb = x + b * n * D;
+  const uint16_t* cb = c + static_cast<int64_t>(b) * k * D;
+  const float* csqb = c_sq + static_cast<int64_t>(b) * k;
+
+  // ---- points of this lane: two fragments of 32 points
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * ASSIGN_POINTS + wave * ASSIGN_POINTS_PER_WAVE + col;
+  u32x4 xf[2][KSTEPS];
+  float xsq[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int64_t p = p0 + 32 * f;
+    const bool live = p < n;
+    float part = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      u32x4 v = live ? *reinterpret_cast<const u32x4*>(xb + p * D + s * 16 + half * 8) : u32x4{0, 0, 0, 0};
+      xf[f][s] = v;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = spr::bf16_lo(w[e]);
+        const float hi = spr::bf16_hi(w[e]);
+        if (x_sq_mode == 1) {
+          part += spr::bf16_to_f32(spr::f32_to_bf16(lo * lo));
+          part += spr::bf16_to_f32(spr::f32_to_bf16(hi * hi));
+        } else {
+          part = __builtin_fmaf(lo, lo, part);
+          part = __builtin_fmaf(hi, hi, part);
+        }
+      }
+    }
+    const float other = __shfl_xor(part, 32, 64);
+    float total = part + other;
+    if (x_sq_mode == 1) total = spr::bf16_to_f32(spr::f32_to_bf16(total));
+    if (x_sq_in != nullptr) total = live ? x_sq_in[b * n + p] : 0.0f;
+    xsq[f] = total;
+  }
+
+  float best[2] = {3.4e38f, 3.4e38f};
+  int32_t best_idx[2] = {0, 0};
+
+  const int nchunks = static_cast<int>((k + CCHUNK - 1) / CCHUNK);
+  u32x4 pre[PIECES_PER_THREAD];
+  float pre_csq = 0.0f;
+
+  auto fetch = [&](int chunk) {
+#pragma unroll
+    for (int i = 0; i < PIECES_PER_THREAD; ++i) {
+      const int piece = tid + i * ASSIGN_THREADS;
+      const int row = piece / (D / 8);
+      const int vec = piece % (D / 8);
+      const int64_t cidx = static_cast<int64_t>(chunk) * CCHUNK + row;
+      pre[i] = cidx < k ? *reinterpret_cast<const u32x4*>(cb + cidx * D + vec * 8) : u32x4{0, 0, 0, 0};
+    }
+    if (tid < CCHUNK) {
+      const int64_t cidx = static_cast<int64_t>(chunk) * CCHUNK + tid;
+      pre_csq = cidx < k ? csqb[cidx] : 0.0f;
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PIECES_PER_THREAD; ++i) {
+      const int piece = tid + i * ASSIGN_THREADS;
+      const int row = piece / (D / 8);
+      const int vec = piece % (D / 8);
+      *reinterpret_cast<u32x4*>(&tile[buf][row * ROW_BYTES + vec * 16]) = pre[i];
+    }
+    if (tid < CCHUNK) tile_csq[buf][tid] = pre_csq;
+  };
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+
+  for (int chunk = 0; chunk < nchunks; ++chunk) {
+    const int buf = chunk & 1;
+    if (chunk + 1 < nchunks) fetch(chunk + 1);
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      spr::f32x16 acc0 = {}, acc1 = {};
+      const uint8_t* arow = &tile[buf][(blk * 32 + col) * ROW_BYTES + half * 16];
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[0][s]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[1][s]), acc1, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int local = blk * 32 + 8 * i + 4 * half + j;
+          const int32_t cidx = chunk * CCHUNK + local;
+          const float csq = tile_csq[buf][local];
+          float d0 = __fsub_rn(__fadd_rn(xsq[0], csq), __fmul_rn(2.0f, acc0[4 * i + j]));
+          float d1 = __fsub_rn(__fadd_rn(xsq[1], csq), __fmul_rn(2.0f, acc1[4 * i + j]));
+          d0 = fmaxf(d0, 0.0f);
+          d1 = fmaxf(d1, 0.0f);
+          const bool valid = cidx < k;
+          if (valid && d0 < best[0]) {
+            best[0] = d0;
+            best_idx[0] = cidx;
+          }
+          if (valid && d1 < best[1]) {
+            best[1] = d1;
+            best_idx[1] = cidx;
+          }
+        }
+      }
+    }
+    if (chunk + 1 < nchunks) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const float od = __shfl_xor(best[f], 32, 64);
+    const int32_t oi = __shfl_xor(best_idx[f], 32, 64);
+    if (od < best[f] || (od == best[f] && oi < best_idx[f])) {
+      best[f] = od;
+      best_idx[f] = oi;
+    }
+    const int64_t p = p0 + 32 * f;
+    if (half == 0 && p < n) labels[b * n + p] = best_idx[f];
+  }
+}
+
+// c_sq[b, k] = sum_d float(c)^2 in fp32, sequential over d.
+template <typename T>
+__global__ void centroid_sq_kernel(const T* __restrict__ c, int64_t rows, int32_t d, float* __restrict__ out) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float s = 0.0f;
+  for (int t = 0; t < d; ++t) {
+    float v;
+    if constexpr (sizeof(T) == 2) {
+      v = spr::bf16_to_f32(c[r * d + t]);
+    } else {
+      v = c[r * d + t];
+    }
+    s = __builtin_fmaf(v, v, s);
+  }
+  out[r] = s;
+}
+
+// ---------------------------------------------------------------- segmented mean
+// T: uint16_t (bf16) or float.  One workgroup per (cluster, batch).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void centroid_mean_kernel(
+    const T* __restrict__ x, const int32_t* __restrict__ sorted_idx, const int32_t* __restrict__ offsets,
+    const T* __restrict__ old, int64_t n, int32_t k, float* __restrict__ mean32, T* __restrict__ out,
+    float* __restrict__ shift_max, float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum) {
+  constexpr int E = 16 / sizeof(T);  // elements per 16-byte vector
+  constexpr int VPR = D / E;         // vectors per row
+  static_assert(D % E == 0 && VPR <= 256, "unsupported D");
+  constexpr int R = 256 / VPR;       // rows in flight per step (threads past R * VPR idle)
+  __shared__ double red[R][D + 1];
+  __shared__ float sq[D];
+
+  const int tid = threadIdx.x;
+  const int v = tid % VPR;
+  const int rg = tid / VPR;
+  const int64_t b = blockIdx.y;
+  const int32_t cl = blockIdx.x;
+  const int32_t* off = offsets + b * (k + 1);
+  // offsets come from spr_argsort_labels; clamp anyway so a bad table cannot
+  // index outside [0, n).
+  const int32_t n32 = static_cast<int32_t>(n);
+  const int32_t start = min(max(off[cl], 0), n32);
+  const int32_t end = min(max(off[cl + 1], start), n32);
+  const int32_t* idx = sorted_idx + b * n;
+  const T* xb = x + b * n * D;
+
+  double acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.0;
+
+  auto add_vec = [&](const u32x4& w) {
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += static_cast<double>(spr::bf16_lo(ws[e]));
+        acc[2 * e + 1] += static_cast<double>(spr::bf16_hi(ws[e]));
+      }
+    } else {
+      acc[0] += static_cast<double>(__uint_as_float(w.x));
+      acc[1] += static_cast<double>(__uint_as_float(w.y));
+      acc[2] += static_cast<double>(__uint_as_float(w.z));
+      acc[3] += static_cast<double>(__uint_as_float(w.w));
+    }
+  };
+
+  const bool worker = rg < R;
+  int32_t r = worker ? start + rg : end;
+  for (; r + R < end; r += 2 * R) {
+    const uint32_t t0 = static_cast<uint32_t>(idx[r]);
+    const uint32_t t1 = static_cast<uint32_t>(idx[r + R]);
+    const u32x4 w0 = t0 < n ? reinterpret_cast<const u32x4*>(xb + static_cast<int64_t>(t0) * D)[v] : u32x4{0, 0, 0, 0};
+    const u32x4 w1 = t1 < n ? reinterpret_cast<const u32x4*>(xb + static_cast<int64_t>(t1) * D)[v] : u32x4{0, 0, 0, 0};
+    add_vec(w0);
+    add_vec(w1);
+  }
+  for (; r < end; r += R) {
+    const uint32_t t0 = static_cast<uint32_t>(idx[r]);
+    const u32x4 w0 = t0 < n ? reinterpret_cast<const u32x4*>(xb + static_cast<int64_t>(t0) * D)[v] : u32x4{0, 0, 0, 0};
+    add_vec(w0);
+  }
+  if (worker) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) red[rg][v * E + e] = acc[e];
+  }
+  __syncthreads();
+
+  const int32_t count = end - start;
+  const int64_t o = (b * k + cl) * D;
+  if (tid < D) {
+    double s = 0.0;
+    for (int g = 0; g < R; ++g) s += red[g][tid];
+    float m;
+    float prev;
+    if constexpr (sizeof(T) == 2) {
+      prev = spr::bf16_to_f32(old[o + tid]);
+    } else {
+      prev = old[o + tid];
+    }
+    m = count > 0 ? static_cast<float>(s / static_cast<double>(count)) : prev;
+    if (mean32 != nullptr) mean32[o + tid] = m;
+    float outv = m;
+    if (out != nullptr) {
+      if constexpr (sizeof(T) == 2) {
+        const uint16_t bits = spr::f32_to_bf16(m);
+        out[o + tid] = bits;
+        outv = spr::bf16_to_f32(bits);
+      } else {
+        out[o + tid] = m;
+      }
+    }
+    if (sums_accum != nullptr) sums_accum[o + tid] += static_cast<float>(s);
+    const float diff = outv - prev;
+    sq[tid] = diff * diff;
+  }
+  if (counts_accum != nullptr && tid == 0) counts_accum[b * k + cl] += count;
+  if (shift_max != nullptr) {
+    __syncthreads();
+    if (tid == 0) {
+      float s = 0.0f;
+      for (int t = 0; t < D; ++t) s += sq[t];
+      const float norm = sqrtf(s);
+      atomicMax(reinterpret_cast<unsigned int*>(shift_max), __float_as_uint(norm));
+    }
+  }
+}
+
+// ---------------------------------------------------------------- exact fp32 assign
+template <int D>
+__global__ __launch_bounds__(256) void role_assign_fp32_kernel(const float* __restrict__ f,
+                                                               const float* __restrict__ c, int64_t n,
+                                                               int32_t k, int32_t* __restrict__ labels,
+                                                               float* __restrict__ best_dist) {
+  constexpr int TILE = 64;
+  __shared__ __attribute__((aligned(16))) float tile[TILE * D];
+  const int64_t b = blockIdx.y;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool live = p < n;
+  float pt[D];
+#pragma unroll
+  for (int r = 0; r < D; r += 4) {
+    u32x4 w = live ? *reinterpret_cast<const u32x4*>(f + (b * n + p) * D + r) : u32x4{0, 0, 0, 0};
+    pt[r] = __uint_as_float(w.x);
+    pt[r + 1] = __uint_as_float(w.y);
+    pt[r + 2] = __uint_as_float(w.z);
+    pt[r + 3] = __uint_as_float(w.w);
+  }
+  float bd = 3.402823466e38f;
+  int32_t bi = 0x7fffffff;
+  const float* cb = c + b * static_cast<int64_t>(k) * D;
+  for (int32_t c0 = 0; c0 < k; c0 += TILE) {
+    const int rows = (k - c0) < TILE ? (k - c0) : TILE;
+    __syncthreads();
+    for (int i = threadIdx.x; i < rows * D / 4; i += blockDim.x) {
+      reinterpret_cast<u32x4*>(tile)[i] = reinterpret_cast<const u32x4*>(cb + static_cast<int64_t>(c0) * D)[i];
+    }
+    __syncthreads();
+    for (int j = 0; j < rows; ++j) {
+      const float* q = tile + j * D;
+      float dist = 0.0f;
+#pragma unroll
+      for (int r = 0; r < D; ++r) {
+        const float delta = __fsub_rn(pt[r], q[r]);
+        dist = __builtin_fmaf(delta, delta, dist);
+      }
+      const int32_t idx = c0 + j;
+      if (dist < bd || (dist == bd && idx < bi)) {
+        bd = dist;
+        bi = idx;
+      }
+    }
+  }
+  if (live) {
+    labels[b * n + p] = bi;
+    if (best_dist != nullptr) best_dist[b * n + p] = bd;
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ C ABI
+
+// c_sq[rows] = sum_d c[rows, d]^2 (fp32); dtype 0 = bf16, 2 = fp32.
+extern "C" int spr_centroid_sq(const void* c, int32_t dtype, int64_t rows, int32_t d, float* c_sq,
+                               hipStream_t stream) {
+  SPR_REQUIRE(rows >= 0 && d > 0, "spr_centroid_sq: bad size");
+  if (rows == 0) return SPR_OK;
+  SPR_REQUIRE(c && c_sq, "spr_centroid_sq: null pointer");
+  const int blocks = static_cast<int>(spr::ceil_div(rows, 256));
+  if (dtype == 0) {
+    centroid_sq_kernel<uint16_t><<<blocks, 256, 0, stream>>>(static_cast<const uint16_t*>(c), rows, d, c_sq);
+  } else if (dtype == 2) {
+    centroid_sq_kernel<float><<<blocks, 256, 0, stream>>>(static_cast<const float*>(c), rows, d, c_sq);
+  } else {
+    SPR_REQUIRE(false, "spr_centroid_sq: unsupported dtype %d", dtype);
+  }
+  SPR_LAUNCHED("centroid_sq_kernel");
+  return SPR_OK;
+}
+
+// labels[b, i] = argmin_k max((x_sq + c_sq) - 2 x.c, 0) for bf16 x [b, n, d],
+// bf16 centroids [b, k, d], fp32 c_sq [b, k].  x_sq: fp32 [b, n] or null
+// (computed inline with x_sq_mode 0 = fp32, 1 = bf16 buffer semantics).
+extern "C" int spr_kmeans_assign_bf16(const void* x, const void* centroids, const float* c_sq, const float* x_sq,
+                                      int32_t x_sq_mode, int64_t batch, int64_t n, int32_t k, int32_t d,
+                                      int32_t* labels, hipStream_t stream) {
+  SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_kmeans_assign_bf16: bad size");
+  SPR_REQUIRE(batch <= 65535, "spr_kmeans_assign_bf16: batch %lld exceeds 65535", (long long)batch);
+  SPR_REQUIRE(x_sq_mode == 0 || x_sq_mode == 1, "spr_kmeans_assign_bf16: x_sq_mode must be 0 or 1");
+  if (batch == 0 || n == 0) return SPR_OK;
+  SPR_REQUIRE(x && centroids && c_sq && labels, "spr_kmeans_assign_bf16: null pointer");
+  SPR_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(centroids) % 16 == 0,
+              "spr_kmeans_assign_bf16: x and centroids must be 16-byte aligned");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, ASSIGN_POINTS)), static_cast<uint32_t>(batch));
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* cp = static_cast<const uint16_t*>(centroids);
+  switch (d) {
+    case 64:
+      kmeans_assign_bf16_kernel<64><<<grid, ASSIGN_THREADS, 0, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode, n, k, labels);
+      break;
+    case 128:
+      kmeans_assign_bf16_kernel<128><<<grid, ASSIGN_THREADS, 0, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode, n, k, labels);
+      break;
+    default:
+      SPR_REQUIRE(false, "spr_kmeans_assign_bf16: head dim %d not supported (64, 128)", d);
+  }
+  SPR_LAUNCHED("kmeans_assign_bf16_kernel");
+  return SPR_OK;
+}
+
+// Segmented cluster means from a stable label sort (sorted_idx, offsets from
+// spr_argsort_labels).  dtype 0 = bf16 rows / bf16 centroids, 2 = fp32.
+// Outputs (each nullable): mean32 fp32 [b,k,d]; out (dtype) [b,k,d];
+// shift_max (fp32 scalar, must start at 0; receives max_k ||out - old||);
+// sums_accum fp32 [b,k,d] += sums; counts_accum int32 [b,k] += counts.
+extern "C" int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, const int32_t* offsets,
+                                 const void* old, int64_t batch, int64_t n, int32_t k, int32_t d, float* mean32,
+                                 void* out, float* shift_max, float* sums_accum, int32_t* counts_accum,
+                                 hipStream_t stream) {
+  SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_centroid_mean: bad size");
+  SPR_REQUIRE(batch <= 65535, "spr_centroid_mean: batch %lld exceeds 65535", (long long)batch);
+  if (batch == 0) return SPR_OK;
+  SPR_REQUIRE(sorted_idx && offsets && old, "spr_centroid_mean: null pointer");
+  SPR_REQUIRE(n == 0 || x, "spr_centroid_mean: null x");
+  dim3 grid(static_cast<uint32_t>(k), static_cast<uint32_t>(batch));
+#define SPR_MEAN_CASE(T, DD)                                                                            \
+  centroid_mean_kernel<T, DD><<<grid, 256, 0, stream>>>(                                                \
+      static_cast<const T*>(x), sorted_idx, offsets, static_cast<const T*>(old), n, k, mean32,        \
+      static_cast<T*>(out), shift_max, sums_accum, counts_accum)
+  if (dtype == 0) {
+    switch (d) {
+      case 64: SPR_MEAN_CASE(uint16_t, 64); break;
+      case 128: SPR_MEAN_CASE(uint16_t, 128); break;
+      default: SPR_REQUIRE(false, "spr_centroid_mean: bf16 head dim %d not supported (64, 128)", d);
+    }
+  } else if (dtype == 2) {
+    switch (d) {
+      case 16: SPR_MEAN_CASE(float, 16); break;
+      case 32: SPR_MEAN_CASE(float, 32); break;
+      case 48: SPR_MEAN_CASE(float, 48); break;
+      case 64: SPR_MEAN_CASE(float, 64); break;
+      case 128: SPR_MEAN_CASE(float, 128); break;
+      default: SPR_REQUIRE(false, "spr_centroid_mean: fp32 dim %d not supported (16, 32, 48, 64, 128)", d);
+    }
+  } else {
+    SPR_REQUIRE(false, "spr_centroid_mean: unsupported dtype %d", dtype);
+  }
+#undef SPR_MEAN_CASE
+  SPR_LAUNCHED("centroid_mean_kernel");
+  return SPR_OK;
+}
+
+// Exact-FP32 nearest centroid for fp32 features [b, n, d], centroids [b, k, d].
+extern "C" int spr_role_assign_fp32(const float* features, const float* centroids, int64_t batch, int64_t n,
+                                    int32_t k, int32_t d, int32_t* labels, float* best_dist,
+                                    hipStream_t stream) {
+  SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_role_assign_fp32: bad size");
+  SPR_REQUIRE(batch <= 65535, "spr_role_assign_fp32: batch exceeds 65535");
+  if (batch == 0 || n == 0) return SPR_OK;
+  SPR_REQUIRE(features && centroids && labels, "spr_role_assign_fp32: null pointer");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(batch));
+  switch (d) {
+    case 16: role_assign_fp32_kernel<16><<<grid, 256, 0, stream>>>(features, centroids, n, k, labels, best_dist); break;
+    case 32: role_assign_fp32_kernel<32><<<grid, 256, 0, stream>>>(features, centroids, n, k, labels, best_dist); break;
+    case 48: role_assign_fp32_kernel<48><<<grid, 256, 0, stream>>>(features, centroids, n, k, labels, best_dist); break;
+    case 64: role_assign_fp32_kernel<64><<<grid, 256, 0, stream>>>(features, centroids, n, k, labels, best_dist); break;
+    default: SPR_REQUIRE(false, "spr_role_assign_fp32: dim %d not supported (16, 32, 48, 64)", d);
+  }
+  SPR_LAUNCHED("role_assign_fp32_kernel");
+  return SPR_OK;
+}

@@ -1,0 +1,87 @@
+"""Native N8 kernels (drop-in for the reference's src/sparsepr/kernels/n8_extension.py).
+
+The reference loads a pybind module `n8_kernels` built from n8_ops.cu.  Here the
+same entry points are served by libsparsepr_hip.so through its C ABI.
+`load_n8_kernels()` returns a module-like object exposing the reference's export
+names (n8_ops.cu:642-664) so `hasattr` capability probes keep working; the
+model-specific QKV norm/RoPE fusions are not part of this library.
+"""
+
+from __future__ import annotations
+
+import types
+
+import torch
+
+from .. import _lib
+
+_MODULE: types.SimpleNamespace | None = None
+_LOAD_ERROR: Exception | None = None
+
+
+def _check_role_inputs(features, centroids, max_clusters):
+    _lib.require_gpu(features, centroids, what="role clustering")
+    if features.dtype != torch.float32 or centroids.dtype != torch.float32:
+        raise RuntimeError("Role clustering requires FP32 features and centroids")
+    if not (features.is_contiguous() and centroids.is_contiguous()):
+        raise RuntimeError("Role clustering inputs must be contiguous")
+    if (features.dim() != 3 or centroids.dim() != 3 or features.shape[0] != centroids.shape[0]
+            or features.shape[2] != 64 or centroids.shape[2] != 64):
+        raise RuntimeError("Role clustering expects features [BH,N,64], centroids [BH,C,64]")
+    clusters = centroids.shape[1]
+    if not 0 < clusters <= max_clusters:
+        raise RuntimeError("Unsupported role cluster count")
+
+
+def _role_step(features: torch.Tensor, centroids: torch.Tensor, max_clusters: int):
+    """One exact FP32 Lloyd step: assign, sizes, means (n8_ops.cu:499-529)."""
+    _check_role_inputs(features, centroids, max_clusters)
+    from ..flash_kmeans.kmeans_impl import centroid_update_sorted, euclid_assign
+    from .permute import argsort_labels
+
+    bh, n, d = features.shape
+    c = centroids.shape[1]
+    labels = euclid_assign(features, centroids)
+    idx, sizes, offsets = argsort_labels(labels, c)
+    res = centroid_update_sorted(features, labels, centroids, sorted_idx=idx, sizes=sizes, offsets=offsets)
+    return [labels, res.centroids, sizes]
+
+
+def role_cluster_step_q64(features: torch.Tensor, centroids: torch.Tensor):
+    """[labels int32, centroids fp32, sizes int32] for at most 512 clusters."""
+    return tuple(_role_step(features, centroids, 512))
+
+
+def role_cluster_step_k64(features: torch.Tensor, centroids: torch.Tensor):
+    """[labels int32, centroids fp32, sizes int32] for at most 1024 clusters."""
+    return tuple(_role_step(features, centroids, 1024))
+
+
+def _exports() -> dict:
+    return {
+        "role_cluster_step_q64": lambda f, c: _role_step(f, c, 512),
+        "role_cluster_step_k64": lambda f, c: _role_step(f, c, 1024),
+    }
+
+
+def load_n8_kernels(*, required: bool = False):
+    """Module-like view of the native kernels, or None when the library cannot
+    be loaded and `required` is False (reference n8_extension.py:24-42)."""
+    global _MODULE, _LOAD_ERROR
+    if _MODULE is not None:
+        return _MODULE
+    if _LOAD_ERROR is not None and not required:
+        return None
+    try:
+        _lib.load()
+    except Exception as exc:  # missing or stale library
+        _LOAD_ERROR = exc
+        if required:
+            raise RuntimeError(f"Could not load {_lib.LIB_PATH.name}: {exc}") from exc
+        return None
+    _MODULE = types.SimpleNamespace(**_exports())
+    return _MODULE
+
+
+def n8_cuda_extension_available() -> bool:
+    return load_n8_kernels(required=False) is not None

@@ -32,3 +32,18 @@ def oracle():
     from oracle import sparsepr_oracle
 
     return sparsepr_oracle
+
+
+@pytest.fixture(scope="session")
+def dev():
+    """A GPU device with the HIP library loaded.  Skips only when there is no
+    GPU at all; a missing library on a GPU box is a failure, not a skip."""
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from sparsepr_amd import _lib
+
+    _lib.load()
+    return torch.device("cuda:0")
+

@@ -1,0 +1,197 @@
+"""GPU parity: k-means assign (bf16 MFMA), segmented centroid mean, Lloyd loop,
+exact-FP32 role step.  Labels: identical except ties within 1e-6 of the fp32
+distance scale; centroids: bit-exact given identical labels (fp64 sums)."""
+
+import numpy as np
+import pytest
+import torch
+
+from tests._helpers import to_dev
+
+pytestmark = pytest.mark.gpu
+
+TIE_REL = 1e-6
+
+
+def _gmm(oracle, rng, b, n, d, comps, std=0.25):
+    means = rng.standard_normal((b, comps, d)).astype(np.float32)
+    which = rng.integers(0, comps, (b, n))
+    x = np.take_along_axis(means, which[..., None], 1) + std * rng.standard_normal((b, n, d)).astype(np.float32)
+    return oracle.to_bf16(x.astype(np.float32))
+
+
+@pytest.mark.parametrize("b,n,k,d", [(2, 3000, 256, 128), (3, 1001, 100, 128), (1, 4096, 64, 64),
+                                     (2, 500, 512, 128), (1, 37, 5, 64)])
+@pytest.mark.parametrize("mode", ["bf16", "fp32"])
+def test_assign_matches_oracle_up_to_ties(dev, oracle, b, n, k, d, mode):
+    from sparsepr_amd.flash_kmeans.kmeans_impl import X_SQ_BF16, X_SQ_FP32, euclid_assign
+
+    rng = np.random.default_rng(n + k + d)
+    x = _gmm(oracle, rng, b, n, d, max(k // 2, 2))
+    c = oracle.first_k_init(x, k, seed=1)
+    labels = euclid_assign(to_dev(x, dev, torch.bfloat16), to_dev(c, dev, torch.bfloat16),
+                           x_sq_mode=X_SQ_BF16 if mode == "bf16" else X_SQ_FP32).cpu().numpy()
+    x_sq = oracle.x_sq_for(x, mode)
+    ref, dist = oracle.kmeans_assign(x, c, x_sq)
+    ok, nbad = oracle.label_mismatches_are_ties(labels, ref, dist, x_sq, c, TIE_REL)
+    assert ok, f"{nbad} label mismatches beyond tie tolerance"
+    assert nbad <= max(2, labels.size // 1000)
+
+
+def test_assign_planted_exact_ties_pick_lowest_index(dev, oracle):
+    from sparsepr_amd.flash_kmeans.kmeans_impl import euclid_assign
+
+    rng = np.random.default_rng(3)
+    c = oracle.to_bf16(rng.standard_normal((1, 200, 128)).astype(np.float32))
+    c[0, 150] = c[0, 7]   # duplicate across LDS tiles
+    c[0, 40] = c[0, 33]   # duplicate within a tile
+    x = np.repeat(c[:, [7, 33, 150, 40]], 70, axis=1)  # points exactly on the centroids
+    labels = euclid_assign(to_dev(x, dev, torch.bfloat16), to_dev(c, dev, torch.bfloat16)).cpu().numpy()
+    assert (labels[0, :70] == 7).all() and (labels[0, 70:140] == 33).all()
+    assert (labels[0, 140:210] == 7).all() and (labels[0, 210:] == 33).all()
+
+
+def test_assign_with_given_x_sq(dev, oracle):
+    from sparsepr_amd.flash_kmeans import euclid_assign_triton
+
+    rng = np.random.default_rng(4)
+    x = _gmm(oracle, rng, 2, 2000, 128, 40)
+    c = oracle.first_k_init(x, 64, seed=2)
+    xt = to_dev(x, dev, torch.bfloat16)
+    x_sq = (xt.float() ** 2).sum(-1)
+    labels = euclid_assign_triton(xt, to_dev(c, dev, torch.bfloat16), x_sq).cpu().numpy()
+    xs = oracle.x_sq_for(x, "fp32")
+    ref, dist = oracle.kmeans_assign(x, c, xs)
+    ok, _ = oracle.label_mismatches_are_ties(labels, ref, dist, xs, c, TIE_REL)
+    assert ok
+
+
+@pytest.mark.parametrize("k,d", [(256, 128), (7, 64), (512, 128)])
+def test_centroid_mean_bit_exact(dev, oracle, k, d):
+    from sparsepr_amd.flash_kmeans.kmeans_impl import centroid_update_sorted
+
+    rng = np.random.default_rng(k)
+    n = 5000
+    x = _gmm(oracle, rng, 2, n, d, 30)
+    labels = rng.integers(0, k, (2, n)).astype(np.int32)
+    labels[labels == 3] = 4  # cluster 3 empty
+    old = oracle.to_bf16(rng.standard_normal((2, k, d)).astype(np.float32))
+    res = centroid_update_sorted(to_dev(x, dev, torch.bfloat16), to_dev(labels, dev),
+                                 to_dev(old, dev, torch.bfloat16), want_mean32=True, want_shift=True)
+    cent, mean32, counts = oracle.centroid_update(x, labels, old, out_bf16=True)
+    assert (res.mean32.cpu().numpy() == mean32).all()
+    assert (res.centroids.float().cpu().numpy() == cent).all()
+    assert (res.sizes.cpu().numpy() == counts).all()
+    shift = np.sqrt(((cent.astype(np.float64) - old) ** 2).sum(-1)).max()
+    assert abs(float(res.shift.item()) - shift) <= 1e-5 * max(shift, 1.0)
+
+
+def test_centroid_update_accumulates_into_buffers(dev, oracle):
+    from sparsepr_amd.flash_kmeans import triton_centroid_update_sorted_euclid
+
+    rng = np.random.default_rng(9)
+    x = _gmm(oracle, rng, 1, 800, 128, 10)
+    labels = rng.integers(0, 16, (1, 800)).astype(np.int32)
+    old = oracle.to_bf16(rng.standard_normal((1, 16, 128)).astype(np.float32))
+    sums = torch.ones((1, 16, 128), dtype=torch.float32, device=dev)
+    cnts = torch.full((1, 16), 2, dtype=torch.int32, device=dev)
+    out = triton_centroid_update_sorted_euclid(to_dev(x, dev, torch.bfloat16), to_dev(labels, dev),
+                                               to_dev(old, dev, torch.bfloat16), centroid_sums=sums,
+                                               centroid_cnts=cnts, calculate_new=False)
+    assert out is None
+    ref_sums = np.zeros((16, 128))
+    np.add.at(ref_sums, labels[0], x[0].astype(np.float64))
+    assert np.allclose(sums[0].cpu().numpy(), 1.0 + ref_sums, rtol=1e-6, atol=1e-5)
+    assert (cnts[0].cpu().numpy() == 2 + np.bincount(labels[0], minlength=16)).all()
+
+
+def test_lloyd_stepwise_parity(dev, oracle):
+    """Each iteration: GPU labels == oracle labels up to ties; given the GPU's
+    labels, the GPU centroids equal the oracle's bit for bit."""
+    from sparsepr_amd.flash_kmeans.kmeans_impl import X_SQ_BF16, centroid_update_sorted, euclid_assign
+
+    rng = np.random.default_rng(11)
+    x = _gmm(oracle, rng, 3, 6000, 128, 100)
+    xt = to_dev(x, dev, torch.bfloat16)
+    cent = oracle.first_k_init(x, 128, seed=3)
+    x_sq = oracle.x_sq_for(x, "bf16")
+    for _ in range(5):
+        ct = to_dev(cent, dev, torch.bfloat16)
+        lab = euclid_assign(xt, ct, x_sq_mode=X_SQ_BF16).cpu().numpy()
+        ref, dist = oracle.kmeans_assign(x, cent, x_sq)
+        ok, _ = oracle.label_mismatches_are_ties(lab, ref, dist, x_sq, cent, TIE_REL)
+        assert ok
+        res = centroid_update_sorted(xt, to_dev(lab, dev), ct)
+        new, _, counts = oracle.centroid_update(x, lab, cent, out_bf16=True)
+        assert (res.centroids.float().cpu().numpy() == new).all()
+        assert (res.sizes.cpu().numpy() == counts).all()
+        cent = new
+
+
+def test_batch_kmeans_euclid_whole_loop(dev, oracle):
+    from sparsepr_amd.flash_kmeans import batch_kmeans_Euclid
+
+    rng = np.random.default_rng(12)
+    x = _gmm(oracle, rng, 2, 4000, 128, 60)
+    init = oracle.first_k_init(x, 64, seed=4)
+    labels, cent, iters = batch_kmeans_Euclid(to_dev(x, dev, torch.bfloat16), 64, max_iters=5,
+                                              init_centroids=to_dev(init, dev, torch.bfloat16))
+    rl, rc, rs, ri = oracle.batch_kmeans_euclid(x, 64, 5, 0.0, init, "bf16", True)
+    assert iters == ri == 5
+    agree = (labels.cpu().numpy() == rl).mean()
+    assert agree > 0.999
+    if agree == 1.0:
+        assert (cent.float().cpu().numpy() == rc).all()
+    # tol larger than any shift: stops after one iteration and returns the init
+    labels, cent, iters = batch_kmeans_Euclid(to_dev(x, dev, torch.bfloat16), 64, max_iters=5, tol=1e9,
+                                              init_centroids=to_dev(init, dev, torch.bfloat16))
+    assert iters == 1 and (cent.float().cpu().numpy() == init).all()
+
+
+def test_kmeans_full_size_properties(dev):
+    """BASELINE config 2 shape (24 x 118,800 x 128, K=256, 5 iterations):
+    sizes sum to N, the objective does not increase, labels are the argmin."""
+    from sparsepr_amd.flash_kmeans.kmeans_impl import X_SQ_BF16, euclid_assign, lloyd
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    b, n, d, k = 24, 118800, 128, 256
+    means = torch.randn(b, k, d, device=dev, generator=g)
+    which = torch.randint(0, k, (b, n), device=dev, generator=g)
+    x = (torch.gather(means, 1, which[..., None].expand(-1, -1, d))
+         + 0.25 * torch.randn(b, n, d, device=dev, generator=g)).to(torch.bfloat16)
+    init = x[:, torch.randperm(n, device=dev, generator=g)[:k]]
+    res = lloyd(x, k, 5, 0.0, init, x_sq_mode=X_SQ_BF16)
+    assert bool((res.sizes.sum(1) == n).all())
+    xf = x.float()
+
+    def objective(c):
+        lab = euclid_assign(x, c, x_sq_mode=X_SQ_BF16).long()
+        return ((xf - torch.gather(c.float(), 1, lab[..., None].expand(-1, -1, d))) ** 2).sum().item()
+
+    assert objective(res.centroids) <= objective(init) * 1.0001
+    # spot-check argmin on a slice against a float64 evaluation
+    lab = euclid_assign(x, res.centroids, x_sq_mode=X_SQ_BF16)[:2, :2000].long()
+    dd = torch.cdist(xf[:2, :2000].double(), res.centroids[:2].double())
+    best = dd.gather(2, lab[..., None])[..., 0]
+    assert bool(((best - dd.min(2).values) <= 1e-3 * dd.min(2).values + 1e-3).all())
+
+
+def test_role_step64_exact(dev, oracle):
+    from sparsepr_amd.kernels.n8_extension import role_cluster_step_k64, role_cluster_step_q64
+
+    rng = np.random.default_rng(13)
+    f = rng.standard_normal((2, 3000, 64)).astype(np.float32)
+    c = rng.standard_normal((2, 300, 64)).astype(np.float32)
+    c[:, 250] = c[:, 17]
+    labels, cent, sizes = role_cluster_step_q64(to_dev(f, dev), to_dev(c, dev))
+    rl, rc, rs, _ = oracle.role_step64(f, c)
+    assert (labels.cpu().numpy() == rl).all()
+    assert (sizes.cpu().numpy() == rs).all()
+    assert np.allclose(cent.cpu().numpy(), rc, rtol=1e-5, atol=1e-6)
+    c2 = rng.standard_normal((2, 1000, 64)).astype(np.float32)
+    labels, cent, sizes = role_cluster_step_k64(to_dev(f, dev), to_dev(c2, dev))
+    rl, rc, rs, _ = oracle.role_step64(f, c2)
+    assert (labels.cpu().numpy() == rl).all()
+    with pytest.raises(RuntimeError):
+        role_cluster_step_q64(to_dev(f, dev), to_dev(c2, dev))  # 1000 > 512 clusters
