@@ -55,6 +55,17 @@ void spr_oracle_expf_array(const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = spr_oracle_expf(x[i]);
 }
 
+/* Round fp32 to bfloat16 (nearest even), returned as fp32. */
+static float bf16r(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof(u));
+  if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&f, &u, sizeof(f));
+  return f;
+}
+
 typedef struct {
   float value;
   int32_t index;
@@ -73,13 +84,18 @@ static int cmp_desc_then_index(const void* a, const void* b) {
  * with weighted_softmax :1698-1707), canonical fp32 order.
  *   qc [bh, qn, d], kc [bh, kn, d] fp32; k_sizes [bh, kn] int32
  *   map [bh, qn, kn] uint8 (0/1)
- *   probs_sorted/cum (optional, [bh, qn, kn]) expose the sorted probabilities and
- *   the running sum for near-threshold analysis.
+ *   cum_out/order_out (optional, [bh, qn, kn]) expose the running sum and the
+ *   sorted order for near-threshold analysis.
+ *   bf16 != 0 reproduces torch's bfloat16 dtype flow for bf16 centroids: the
+ *   matmul output and the scaled scores are bf16, weighted_softmax returns
+ *   bf16 probabilities (.to(input_dtype)), cumsum writes bf16 partial sums of
+ *   an fp32 accumulator, and `cumsum > p` compares in bf16 (p rounded to bf16).
  */
 void oracle_topp_map(const float* qc, const float* kc, const int32_t* k_sizes,
                      int64_t bh, int32_t qn, int32_t kn, int32_t d,
-                     float sqrt_d, float p, int32_t preserve_len,
+                     float sqrt_d, float p, int32_t preserve_len, int32_t bf16,
                      uint8_t* map, float* cum_out, int32_t* order_out) {
+  const float thr = bf16 ? bf16r(p) : p;
   float* s = (float*)malloc(sizeof(float) * kn);
   float* we = (float*)malloc(sizeof(float) * kn);
   keyed_t* keyed = (keyed_t*)malloc(sizeof(keyed_t) * kn);
@@ -91,7 +107,7 @@ void oracle_topp_map(const float* qc, const float* kc, const int32_t* k_sizes,
         const float* k = kc + (h * kn + j) * (int64_t)d;
         float acc = 0.0f;
         for (int32_t t = 0; t < d; ++t) acc = fmaf(q[t], k[t], acc);
-        s[j] = acc / sqrt_d;
+        s[j] = bf16 ? bf16r(bf16r(acc) / sqrt_d) : acc / sqrt_d;
         if (s[j] > m) m = s[j];
       }
       float sum = 0.0f;
@@ -102,7 +118,8 @@ void oracle_topp_map(const float* qc, const float* kc, const int32_t* k_sizes,
       }
       float denom = sum > 1e-12f ? sum : 1e-12f;
       for (int32_t j = 0; j < kn; ++j) {
-        keyed[j].value = we[j] / denom;
+        float prob = we[j] / denom;
+        keyed[j].value = bf16 ? bf16r(prob) : prob;
         keyed[j].index = j;
       }
       qsort(keyed, kn, sizeof(keyed_t), cmp_desc_then_index);
@@ -112,12 +129,13 @@ void oracle_topp_map(const float* qc, const float* kc, const int32_t* k_sizes,
       float prev = 0.0f;
       for (int32_t r = 0; r < kn; ++r) {
         cum = cum + keyed[r].value;
-        int remove = (r > 0) && (prev > p);
+        float shown = bf16 ? bf16r(cum) : cum;
+        int remove = (r > 0) && (prev > thr);
         if (r < preserve_len) remove = 0;
         row[keyed[r].index] = remove ? 0 : 1;
-        if (cum_out) cum_out[(h * qn + i) * (int64_t)kn + r] = cum;
+        if (cum_out) cum_out[(h * qn + i) * (int64_t)kn + r] = shown;
         if (order_out) order_out[(h * qn + i) * (int64_t)kn + r] = keyed[r].index;
-        prev = cum;
+        prev = shown;
       }
     }
   }

@@ -50,7 +50,7 @@ def c_lib() -> ctypes.CDLL:
         lib.spr_oracle_expf_array.argtypes = [f32p, f32p, i64]
         lib.oracle_topp_map.restype = None
         lib.oracle_topp_map.argtypes = [
-            f32p, f32p, i32p, i64, i32, i32, i32, ctypes.c_float, ctypes.c_float, i32,
+            f32p, f32p, i32p, i64, i32, i32, i32, ctypes.c_float, ctypes.c_float, i32, i32,
             u8p, ctypes.c_void_p, ctypes.c_void_p,
         ]
         lib.oracle_select_budget.restype = None
@@ -275,10 +275,12 @@ def permute_concat_rows(prefix, suffix, idx):
 # block selection
 # ----------------------------------------------------------------------------
 
-def identify_dynamic_map(qc, kc, k_sizes, p, min_kc_ratio=0.0, return_cum=False):
+def identify_dynamic_map(qc, kc, k_sizes, p, min_kc_ratio=0.0, return_cum=False, bf16=False):
     """Top-p cluster-pair map (kmeans_utils.py:1710-1742), canonical fp32 order.
 
     qc [BH,Qc,D], kc [BH,Kc,D] float32; k_sizes [BH,Kc] -> bool [BH,Qc,Kc].
+    bf16=True follows torch's dtype flow for bfloat16 centroids (bf16 scores,
+    bf16 probabilities, bf16 cumsum outputs, threshold compared in bf16).
     """
     qc = np.ascontiguousarray(qc, np.float32)
     kc = np.ascontiguousarray(kc, np.float32)
@@ -290,7 +292,7 @@ def identify_dynamic_map(qc, kc, k_sizes, p, min_kc_ratio=0.0, return_cum=False)
     cum = np.zeros((bh, qn, kn), np.float32) if return_cum else None
     order = np.zeros((bh, qn, kn), np.int32) if return_cum else None
     c_lib().oracle_topp_map(
-        qc, kc, ks, bh, qn, kn, d, np.float32(math.sqrt(d)), np.float32(p), preserve, out,
+        qc, kc, ks, bh, qn, kn, d, np.float32(math.sqrt(d)), np.float32(p), preserve, int(bool(bf16)), out,
         cum.ctypes.data if cum is not None else None,
         order.ctypes.data if order is not None else None,
     )
@@ -707,7 +709,7 @@ def sparsepr_layer(q, k, v, cfg: LayerConfig, timings: dict | None = None, bf16=
     k_labels, k_cent, k_sizes, _ = batch_kmeans_euclid(
         k, cfg.k_clusters, cfg.kmeans_iters, 0.0, ki, cfg.x_sq_mode, bf16)
     t = mark("kmeans", t)
-    dmap = identify_dynamic_map(q_cent, k_cent, k_sizes, cfg.top_p, cfg.min_kc_ratio)
+    dmap = identify_dynamic_map(q_cent, k_cent, k_sizes, cfg.top_p, cfg.min_kc_ratio, bf16=bf16)
     t = mark("select", t)
     q_idx = argsort_labels(q_labels)
     k_idx = argsort_labels(k_labels)

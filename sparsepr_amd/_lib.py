@@ -40,6 +40,21 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_kmeans_assign_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp]),
     "spr_centroid_mean": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "spr_role_assign_fp32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
+    # select.hip
+    "spr_topp_map": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _f32, _i32, _i32, _vp, _vp]),
+    "spr_select_budget": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "spr_compact_selected": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _vp]),
+    "spr_density": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),
+    # attention.hip
+    "spr_block_sparse_attention_workspace": (_sz, [_i64, _i32, _i32]),
+    "spr_block_sparse_attention_plan": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _sz, _vp]),
+    "spr_block_sparse_attention_run": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32, _f32,
+                                                      _vp, _vp, _vp]),
+    "spr_block_sparse_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,
+                                                  _f32, _vp, _vp, _vp, _sz, _vp]),
+    "spr_dense_attention_workspace": (_sz, [_i64, _i64, _i32, _i32]),
+    "spr_dense_attention": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _vp, _i32, _vp,
+                                           _vp, _sz, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -1,0 +1,613 @@
+// Block-sparse attention over cluster-pair blocks, and split-key dense attention
+// for probe queries (v_mfma_f32_32x32x16_bf16, fp32 online softmax).
+//
+// Replaces:
+//   dynamic_block_sparse_fwd_flashinfer -> FlashInfer VariableBlockSparseAttentionWrapper
+//       (src/sparsepr/kmeans_utils.py:2164-2350); semantics of dynamic_block_sparse_fwd_torch
+//       (kmeans_utils.py:1748-1841)
+//   dense probe attention F.scaled_dot_product_attention (src/sparsepr/models/common/n8_v6.py:1236-1243)
+//
+// Layout: Q [BHq, S, D], K/V [BHkv, S, D] bf16 rows, cluster-contiguous (the
+// permuted layout).  A query row of q-cluster a attends every key of every
+// k-cluster c with map[a, c]; empty rows output 0 (lse -inf).
+//
+// Plan (one workgroup per kv head): cluster offsets, 128-row tiles per
+// q-cluster, and for every q-cluster the ascending list of kept non-empty
+// k-cluster key ranges ("segments").  The attention kernel walks a q-cluster's
+// segments as one virtual key sequence in 64-key chunks, so cluster tails cost
+// no MFMA work.
+//
+// Per workgroup: 128 query rows of one q-cluster, 4 waves x 32 rows.
+//   S^T[key, q] = K Q^T : A = 32 keys x 16 dims from the K tile in LDS, B = the
+//                         wave's 32 query rows (registers, loaded once).
+//   O^T[d, q]  += V^T P^T: A = 32 dims x 16 keys from the transposed V tile, B = P
+//                         straight from the S^T accumulator (bf16), so a lane owns
+//                         one query row for S, P and O: the row max/sum needs one
+//                         exchange with lane l ^ 32 and nothing else.
+// The key order inside a 16-key MFMA step is permuted consistently in P and V
+// (key(t, h, e) = 16t + 8(e/4) + 4h + e%4), which makes P a plain slice of the
+// accumulator.  K/V tiles are double-buffered in LDS; the next chunk's rows are
+// fetched into registers while the current chunk computes.
+#include "spr_common.h"
+
+namespace {
+
+using spr::u32x4;
+
+constexpr int BM = 128;       // query rows per workgroup
+constexpr int BN = 64;        // keys per chunk
+constexpr int THREADS = 256;  // 4 waves
+
+struct Seg {
+  int32_t start;
+  int32_t len;
+};
+
+template <int D>
+struct Tile {
+  static constexpr int KSTEPS = D / 16;
+  static constexpr int DBLK = D / 32;
+  static constexpr int K_ROW = D * 2 + 16;   // bytes per key row of the K tile (+16 pad)
+  static constexpr int V_ROW = BN * 2 + 16;  // bytes per dim row of the V^T tile (+16 pad)
+  static constexpr int K_BYTES = BN * K_ROW;
+  static constexpr int V_BYTES = D * V_ROW;
+  static constexpr int K_PIECES = BN * D / 8 / THREADS;       // 16-byte K pieces per thread
+  static constexpr int V_PAIRS = (BN / 2) * (D / 8) / THREADS;  // (2 rows x 16 bytes) per thread
+  static_assert(K_PIECES >= 1 && V_PAIRS >= 1, "unsupported head dim");
+};
+
+// ---------------------------------------------------------------------------- plan
+
+// Workspace layout per kv head (int32 units), see plan_words().
+struct PlanView {
+  int32_t* q_off;     // [Qc + 1]
+  int32_t* tile_off;  // [Qc + 1]
+  int32_t* nseg;      // [Qc]
+  int32_t* total;     // [Qc]
+  Seg* segs;          // [Qc][Kc]
+};
+
+__host__ __device__ inline int64_t plan_words(int32_t qn, int32_t kn) {
+  return 2 * (int64_t)(qn + 1) + 2 * (int64_t)qn + 2 * (int64_t)qn * kn;
+}
+
+__host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn, int32_t kn) {
+  int32_t* p = base + h * plan_words(qn, kn);
+  PlanView v;
+  v.q_off = p;
+  v.tile_off = p + (qn + 1);
+  v.nseg = p + 2 * (qn + 1);
+  v.total = v.nseg + qn;
+  v.segs = reinterpret_cast<Seg*>(v.total + qn);
+  return v;
+}
+
+__global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __restrict__ map,
+                                                            const int32_t* __restrict__ q_sizes,
+                                                            const int32_t* __restrict__ k_sizes, int32_t qn,
+                                                            int32_t kn, int32_t s_rows, int32_t* __restrict__ plan) {
+  extern __shared__ int32_t k_off[];  // [kn + 1]
+  const int64_t h = blockIdx.x;
+  PlanView pv = plan_at(plan, h, qn, kn);
+  const int32_t* qs = q_sizes + h * qn;
+  const int32_t* ks = k_sizes + h * kn;
+  if (threadIdx.x == 0) {
+    int32_t run = 0;
+    for (int j = 0; j < kn; ++j) {
+      k_off[j] = run;
+      run = min(run + max(ks[j], 0), s_rows);
+    }
+    k_off[kn] = run;
+    int32_t qrun = 0, trun = 0;
+    for (int i = 0; i < qn; ++i) {
+      pv.q_off[i] = qrun;
+      pv.tile_off[i] = trun;
+      const int32_t next = min(qrun + max(qs[i], 0), s_rows);
+      trun += (next - qrun + BM - 1) / BM;
+      qrun = next;
+    }
+    pv.q_off[qn] = qrun;
+    pv.tile_off[qn] = trun;
+  }
+  __syncthreads();
+  // one wave per q-cluster row: ascending compaction of kept, non-empty k-clusters
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  for (int i = wave; i < qn; i += THREADS / 64) {
+    const uint8_t* mrow = map + (h * qn + i) * static_cast<int64_t>(kn);
+    Seg* out = pv.segs + static_cast<int64_t>(i) * kn;
+    int32_t count = 0;
+    int32_t total = 0;
+    for (int c0 = 0; c0 < kn; c0 += 64) {
+      const int c = c0 + lane;
+      int32_t len = 0, start = 0;
+      if (c < kn) {
+        start = k_off[c];
+        len = k_off[c + 1] - start;
+      }
+      const bool keep = c < kn && mrow[c] != 0 && len > 0;
+      const uint64_t bits = __ballot(keep);
+      const int pos = __popcll(bits & ((1ull << lane) - 1ull));
+      if (keep) out[count + pos] = Seg{start, len};
+      int32_t part = keep ? len : 0;
+      for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      total += part;
+      count += __popcll(bits);
+    }
+    if (lane == 0) {
+      pv.nseg[i] = count;
+      pv.total[i] = total;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------- main kernel
+
+// Position `vpos` of the virtual key sequence formed by segments [s, nseg),
+// where segment s starts at virtual position `base`.  -1 past the end.
+__device__ __forceinline__ int32_t key_at(int32_t vpos, int32_t s, int32_t base, const Seg* segs, int32_t nseg) {
+  while (s < nseg) {
+    const Seg g = segs[s];
+    if (vpos < base + g.len) return g.start + (vpos - base);
+    base += g.len;
+    ++s;
+  }
+  return -1;
+}
+
+__device__ __forceinline__ void advance(int32_t& s, int32_t& base, int32_t target, const Seg* segs, int32_t nseg) {
+  while (s < nseg) {
+    const int32_t len = segs[s].len;
+    if (target < base + len) return;
+    base += len;
+    ++s;
+  }
+}
+
+// MODE 0: block-sparse (plan), output normalised bf16 + optional lse.
+// MODE 1: dense split-key for probe rows: q rows [0, m) of a [BHq, m, D] tensor,
+//         keys [split * split_len, ...) of K/V; output unnormalised fp32 partials.
+template <int D, int MODE>
+__global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
+    float scale_log2, uint16_t* __restrict__ out, float* __restrict__ lse,
+    int32_t split_len, float* __restrict__ part_o, float* __restrict__ part_ml) {
+  using T = Tile<D>;
+  __shared__ __attribute__((aligned(16))) uint8_t k_tile[2][T::K_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t v_tile[2][T::V_BYTES];
+  __shared__ int32_t key_rows[3][BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const int64_t bhq = blockIdx.z;
+  const int64_t bhkv = bhq / group;
+
+  // ---- work item
+  int32_t row0, row1;        // query rows of this tile: [row0, row1)
+  const Seg* segs = nullptr;
+  int32_t nseg = 0;
+  int32_t total;
+  int32_t dense_k0 = 0;
+  if constexpr (MODE == 0) {
+    PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
+    const int32_t t = blockIdx.x;
+    if (t >= pv.tile_off[qn]) return;
+    int lo = 0, hi = qn;  // largest i with tile_off[i] <= t
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pv.tile_off[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int qc = lo;
+    row0 = pv.q_off[qc] + (t - pv.tile_off[qc]) * BM;
+    row1 = min(row0 + BM, pv.q_off[qc + 1]);
+    segs = pv.segs + static_cast<int64_t>(qc) * kn;
+    nseg = pv.nseg[qc];
+    total = pv.total[qc];
+  } else {
+    row0 = blockIdx.y * BM;
+    row1 = min(row0 + BM, s_q);
+    dense_k0 = blockIdx.x * split_len;
+    const int32_t k1 = min(dense_k0 + split_len, s_kv);
+    total = max(k1 - dense_k0, 0);
+  }
+
+  const uint16_t* qb = q + bhq * static_cast<int64_t>(s_q) * D;
+  const uint16_t* kb = k + bhkv * static_cast<int64_t>(s_kv) * D;
+  const uint16_t* vb = v + bhkv * static_cast<int64_t>(s_kv) * D;
+
+  // ---- this lane's query row, as MFMA B fragments over the head dim
+  const int32_t my_row = row0 + wave * 32 + col;
+  const bool row_live = my_row < row1;
+  u32x4 qf[T::KSTEPS];
+#pragma unroll
+  for (int s = 0; s < T::KSTEPS; ++s) {
+    qf[s] = row_live ? *reinterpret_cast<const u32x4*>(qb + static_cast<int64_t>(my_row) * D + s * 16 + half * 8)
+                     : u32x4{0, 0, 0, 0};
+  }
+
+  spr::f32x16 o_acc[T::DBLK];
+#pragma unroll
+  for (int b = 0; b < T::DBLK; ++b) o_acc[b] = spr::f32x16{};
+  float m_run = -__builtin_huge_valf();
+  float l_run = 0.0f;
+
+  const int nch = (total + BN - 1) / BN;
+
+  // wave 0 owns the segment cursor and writes the key row of every chunk position
+  int32_t cur_s = 0, cur_base = 0;
+  auto plan_chunk = [&](int c) {
+    if (wave == 0) {
+      const int32_t vpos = c * BN + lane;
+      if constexpr (MODE == 0) {
+        key_rows[c % 3][lane] = (vpos < total) ? key_at(vpos, cur_s, cur_base, segs, nseg) : -1;
+        advance(cur_s, cur_base, (c + 1) * BN, segs, nseg);
+      } else {
+        key_rows[c % 3][lane] = (vpos < total) ? dense_k0 + vpos : -1;
+      }
+    }
+  };
+
+  u32x4 kreg[T::K_PIECES];
+  u32x4 vreg[T::V_PAIRS][2];
+  auto fetch = [&](int c) {
+    const int32_t* kr = key_rows[c % 3];
+#pragma unroll
+    for (int i = 0; i < T::K_PIECES; ++i) {
+      const int g = tid + i * THREADS;
+      const int r = g / (D / 8);
+      const int pc = g % (D / 8);
+      const int32_t key = kr[r];
+      kreg[i] = key >= 0 ? *reinterpret_cast<const u32x4*>(kb + static_cast<int64_t>(key) * D + pc * 8)
+                         : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < T::V_PAIRS; ++i) {
+      const int g = tid + i * THREADS;
+      const int rp = g % (BN / 2);
+      const int pc = g / (BN / 2);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int32_t key = kr[2 * rp + e];
+        vreg[i][e] = key >= 0 ? *reinterpret_cast<const u32x4*>(vb + static_cast<int64_t>(key) * D + pc * 8)
+                              : u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < T::K_PIECES; ++i) {
+      const int g = tid + i * THREADS;
+      const int r = g / (D / 8);
+      const int pc = g % (D / 8);
+      *reinterpret_cast<u32x4*>(&k_tile[buf][r * T::K_ROW + pc * 16]) = kreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < T::V_PAIRS; ++i) {
+      const int g = tid + i * THREADS;
+      const int rp = g % (BN / 2);
+      const int pc = g / (BN / 2);
+      const uint32_t a[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
+      const uint32_t b[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // dims pc*8 + 2w (low halves) and pc*8 + 2w + 1 (high halves)
+        const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
+        const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
+        *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w) * T::V_ROW + rp * 4]) = lo;
+        *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w + 1) * T::V_ROW + rp * 4]) = hi;
+      }
+    }
+  };
+
+  if (nch > 0) {
+    plan_chunk(0);
+    if (nch > 1) plan_chunk(1);
+    __syncthreads();
+    fetch(0);
+    stash(0);
+    __syncthreads();
+  }
+
+  for (int c = 0; c < nch; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < nch) fetch(c + 1);
+    if (c + 2 < nch) plan_chunk(c + 2);
+
+    // ---- S^T = K Q^T for two 32-key blocks
+    spr::f32x16 s_acc[2];
+#pragma unroll
+    for (int kbk = 0; kbk < 2; ++kbk) {
+      s_acc[kbk] = spr::f32x16{};
+      const uint8_t* arow = &k_tile[buf][(kbk * 32 + col) * T::K_ROW + half * 16];
+#pragma unroll
+      for (int s = 0; s < T::KSTEPS; ++s) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
+        s_acc[kbk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[s]), s_acc[kbk],
+                                                             0, 0, 0);
+      }
+    }
+
+    // ---- online softmax (log2 domain); a lane owns one query row
+    const int32_t left = total - c * BN;  // keys of this chunk that exist
+    float mloc = -__builtin_huge_valf();
+#pragma unroll
+    for (int kbk = 0; kbk < 2; ++kbk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = kbk * 32 + 8 * i + 4 * half + j;
+          float sv = s_acc[kbk][4 * i + j] * scale_log2;
+          if (key >= left) sv = -__builtin_huge_valf();
+          s_acc[kbk][4 * i + j] = sv;
+          mloc = fmaxf(mloc, sv);
+        }
+      }
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const float m_use = (m_new == -__builtin_huge_valf()) ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float lsum = 0.0f;
+    uint32_t pf[4][4];  // P as bf16 pairs: [k-step][dword]
+#pragma unroll
+    for (int kbk = 0; kbk < 2; ++kbk) {
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(s_acc[kbk][e] - m_use);
+        const float p1 = __builtin_amdgcn_exp2f(s_acc[kbk][e + 1] - m_use);
+        lsum += p0 + p1;
+        const int t = kbk * 2 + e / 8;
+        pf[t][(e % 8) / 2] = spr::pack_bf16x2(p0, p1);
+      }
+    }
+    l_run = l_run * alpha + lsum;
+#pragma unroll
+    for (int b = 0; b < T::DBLK; ++b) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
+    }
+
+    // ---- O^T += V^T P^T
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4 bfrag = u32x4{pf[t][0], pf[t][1], pf[t][2], pf[t][3]};
+#pragma unroll
+      for (int b = 0; b < T::DBLK; ++b) {
+        const uint8_t* vrow = &v_tile[buf][(b * 32 + col) * T::V_ROW];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + (16 * t + 4 * half) * 2);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (16 * t + 8 + 4 * half) * 2);
+        const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+        o_acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag), o_acc[b], 0, 0,
+                                                           0);
+      }
+    }
+
+    if (c + 1 < nch) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if constexpr (MODE == 0) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (row_live) {
+      uint16_t* orow = out + (bhq * static_cast<int64_t>(s_q) + my_row) * D;
+#pragma unroll
+      for (int b = 0; b < T::DBLK; ++b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = b * 32 + 8 * i + 4 * half;
+          uint2 w;
+          w.x = spr::pack_bf16x2(o_acc[b][4 * i] * inv, o_acc[b][4 * i + 1] * inv);
+          w.y = spr::pack_bf16x2(o_acc[b][4 * i + 2] * inv, o_acc[b][4 * i + 3] * inv);
+          *reinterpret_cast<uint2*>(orow + d0) = w;
+        }
+      }
+      if (lse != nullptr && half == 0) {
+        lse[bhq * static_cast<int64_t>(s_q) + my_row] =
+            l_tot > 0.0f ? (m_run + __builtin_amdgcn_logf(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
+      }
+    }
+  } else {
+    // partials: part_o [BHq, nsplit, s_q, D] fp32, part_ml [BHq, nsplit, s_q, 2]
+    if (row_live) {
+      const int64_t slot = (bhq * gridDim.x + blockIdx.x) * static_cast<int64_t>(s_q) + my_row;
+      float* po = part_o + slot * D;
+#pragma unroll
+      for (int b = 0; b < T::DBLK; ++b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = b * 32 + 8 * i + 4 * half;
+          *reinterpret_cast<spr::f32x4*>(po + d0) =
+              spr::f32x4{o_acc[b][4 * i], o_acc[b][4 * i + 1], o_acc[b][4 * i + 2], o_acc[b][4 * i + 3]};
+        }
+      }
+      if (half == 0) {
+        part_ml[slot * 2] = m_run;
+        part_ml[slot * 2 + 1] = l_tot;
+      }
+    }
+  }
+}
+
+// Merge split-key partials: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+// One thread per (bhq, row, 4 dims).  out_dtype 0 = bf16, 2 = fp32.
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part_o,
+                                                           const float* __restrict__ part_ml, int64_t rows_total,
+                                                           int32_t s_q, int32_t nsplit, int32_t out_dtype,
+                                                           void* __restrict__ out, float* __restrict__ lse) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t r = g / (D / 4);
+  const int d0 = static_cast<int>(g % (D / 4)) * 4;
+  if (r >= rows_total) return;
+  const int64_t bhq = r / s_q;
+  const int64_t row = r - bhq * s_q;
+  float mx = -__builtin_huge_valf();
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, part_ml[((bhq * nsplit + s) * s_q + row) * 2]);
+  const float mu = (mx == -__builtin_huge_valf()) ? 0.0f : mx;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  float l = 0.0f;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t slot = (bhq * nsplit + s) * s_q + row;
+    const float w = __builtin_amdgcn_exp2f(part_ml[slot * 2] - mu);
+    l += w * part_ml[slot * 2 + 1];
+    const spr::f32x4 o = *reinterpret_cast<const spr::f32x4*>(part_o + slot * D + d0);
+    acc[0] += w * o[0];
+    acc[1] += w * o[1];
+    acc[2] += w * o[2];
+    acc[3] += w * o[3];
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if (out_dtype == 0) {
+    uint2 w;
+    w.x = spr::pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    w.y = spr::pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + r * D + d0) = w;
+  } else {
+    *reinterpret_cast<spr::f32x4*>(static_cast<float*>(out) + r * D + d0) =
+        spr::f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+  }
+  if (lse != nullptr && d0 == 0) {
+    lse[r] = l > 0.0f ? (mu + __builtin_amdgcn_logf(l)) * 0.69314718055994531f : -__builtin_huge_valf();
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------ C ABI
+
+extern "C" size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn, int32_t kn) {
+  return static_cast<size_t>(bh_kv * plan_words(qn, kn) * 4);
+}
+
+// Plan for spr_block_sparse_attention_run: map uint8 [bh_kv, qn, kn], q_sizes
+// [bh_kv, qn], k_sizes [bh_kv, kn] int32 (sizes are clamped to the s rows).
+extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes,
+                                               int64_t bh_kv, int64_t s, int32_t qn, int32_t kn, void* plan,
+                                               size_t plan_bytes, hipStream_t stream) {
+  SPR_REQUIRE(bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_plan: bad size");
+  SPR_REQUIRE(kn <= 16384, "spr_block_sparse_attention_plan: kn exceeds 16384");
+  SPR_REQUIRE(s < (int64_t(1) << 31), "spr_block_sparse_attention_plan: sequence too long");
+  SPR_REQUIRE(bh_kv <= 65535, "spr_block_sparse_attention_plan: bh_kv exceeds 65535");
+  SPR_REQUIRE(map && q_sizes && k_sizes && plan, "spr_block_sparse_attention_plan: null pointer");
+  const size_t need = spr_block_sparse_attention_workspace(bh_kv, qn, kn);
+  if (plan_bytes < need) {
+    spr_set_error("spr_block_sparse_attention_plan: plan buffer %zu < %zu bytes", plan_bytes, need);
+    return SPR_EWORKSPACE;
+  }
+  attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv)), THREADS, (kn + 1) * sizeof(int32_t), stream>>>(
+      map, q_sizes, k_sizes, qn, kn, static_cast<int32_t>(s), static_cast<int32_t*>(plan));
+  SPR_LAUNCHED("attn_plan_kernel");
+  return SPR_OK;
+}
+
+// q [bh_q, s, d], k/v [bh_kv, s, d] bf16 (cluster-contiguous), plan from
+// spr_block_sparse_attention_plan; out bf16 [bh_q, s, d]; lse fp32 [bh_q, s]
+// (nullable, natural log).  bh_q must be a multiple of bh_kv (GQA groups).
+extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan,
+                                              int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d, int32_t qn,
+                                              int32_t kn, float scale, void* out, float* lse, hipStream_t stream) {
+  SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_run: bad size");
+  SPR_REQUIRE(bh_q % bh_kv == 0, "spr_block_sparse_attention_run: bh_q=%lld not a multiple of bh_kv=%lld",
+              (long long)bh_q, (long long)bh_kv);
+  SPR_REQUIRE(d == 64 || d == 128, "spr_block_sparse_attention_run: head dim %d not supported (64, 128)", d);
+  SPR_REQUIRE(s < (int64_t(1) << 31), "spr_block_sparse_attention_run: sequence too long");
+  SPR_REQUIRE(bh_q <= 65535, "spr_block_sparse_attention_run: bh_q exceeds 65535");
+  if (bh_q == 0 || s == 0) return SPR_OK;
+  SPR_REQUIRE(q && k && v && plan && out, "spr_block_sparse_attention_run: null pointer");
+  SPR_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+              "spr_block_sparse_attention_run: q/k/v/out must be 16-byte aligned");
+  const int64_t max_tiles = spr::ceil_div(s, BM) + qn;
+  dim3 grid(static_cast<uint32_t>(max_tiles), 1, static_cast<uint32_t>(bh_q));
+  const int32_t group = static_cast<int32_t>(bh_q / bh_kv);
+  const float scale_log2 = scale * 1.4426950408889634f;
+#define SPR_ATTN(DD)                                                                                          \
+  attn_fwd_kernel<DD, 0><<<grid, THREADS, 0, stream>>>(                                                      \
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
+      static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
+      scale_log2, static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr)
+  if (d == 128) {
+    SPR_ATTN(128);
+  } else {
+    SPR_ATTN(64);
+  }
+#undef SPR_ATTN
+  SPR_LAUNCHED("attn_fwd_kernel");
+  return SPR_OK;
+}
+
+// Plan + run in one call (workspace = plan buffer).
+extern "C" int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,
+                                          const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q,
+                                          int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
+                                          void* out, float* lse, void* workspace, size_t workspace_bytes,
+                                          hipStream_t stream) {
+  if (bh_q == 0 || s == 0) return SPR_OK;
+  int st = spr_block_sparse_attention_plan(map, q_sizes, k_sizes, bh_kv, s, qn, kn, workspace, workspace_bytes,
+                                           stream);
+  if (st != SPR_OK) return st;
+  return spr_block_sparse_attention_run(q, k, v, workspace, bh_q, bh_kv, s, d, qn, kn, scale, out, lse, stream);
+}
+
+extern "C" size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t d, int32_t nsplit) {
+  return static_cast<size_t>(bh_q * nsplit * m * (static_cast<int64_t>(d) + 2) * 4);
+}
+
+// Dense softmax(q k^T * scale) v for a few query rows per head (probe rows):
+// q [bh_q, m, d] bf16, k/v [bh_kv, s_kv, d] bf16, keys split into nsplit ranges
+// processed in parallel and merged.  out [bh_q, m, d] (out_dtype 0 = bf16, 2 = fp32),
+// lse fp32 [bh_q, m] nullable.
+extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv,
+                                   int64_t m, int64_t s_kv, int32_t d, float scale, int32_t nsplit, void* out,
+                                   int32_t out_dtype, float* lse, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+  SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && m >= 0 && s_kv >= 0 && nsplit >= 1, "spr_dense_attention: bad size");
+  SPR_REQUIRE(bh_q % bh_kv == 0, "spr_dense_attention: bh_q not a multiple of bh_kv");
+  SPR_REQUIRE(d == 64 || d == 128, "spr_dense_attention: head dim %d not supported (64, 128)", d);
+  SPR_REQUIRE(out_dtype == 0 || out_dtype == 2, "spr_dense_attention: out_dtype must be 0 or 2");
+  SPR_REQUIRE(s_kv < (int64_t(1) << 31) && m < (int64_t(1) << 31), "spr_dense_attention: too long");
+  SPR_REQUIRE(bh_q <= 65535 && nsplit <= 65535, "spr_dense_attention: grid too large");
+  if (bh_q == 0 || m == 0) return SPR_OK;
+  SPR_REQUIRE(q && k && v && out && workspace, "spr_dense_attention: null pointer");
+  const size_t need = spr_dense_attention_workspace(bh_q, m, d, nsplit);
+  if (workspace_bytes < need) {
+    spr_set_error("spr_dense_attention: workspace %zu < %zu bytes", workspace_bytes, need);
+    return SPR_EWORKSPACE;
+  }
+  const int32_t split_len = static_cast<int32_t>(spr::ceil_div(s_kv, nsplit));
+  float* part_o = static_cast<float*>(workspace);
+  float* part_ml = part_o + bh_q * nsplit * m * d;
+  dim3 grid(static_cast<uint32_t>(nsplit), static_cast<uint32_t>(spr::ceil_div(m, BM)),
+            static_cast<uint32_t>(bh_q));
+  const int32_t group = static_cast<int32_t>(bh_q / bh_kv);
+  const float scale_log2 = scale * 1.4426950408889634f;
+  const int64_t rows_total = bh_q * m;
+  const uint32_t cblocks = static_cast<uint32_t>(spr::ceil_div(rows_total * (d / 4), 256));
+  if (d == 128) {
+    attn_fwd_kernel<128, 1><<<grid, THREADS, 0, stream>>>(
+        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+        static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, scale_log2, nullptr, nullptr,
+        split_len, part_o, part_ml);
+    SPR_LAUNCHED("attn_fwd_kernel(dense)");
+    attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
+                                                          nsplit, out_dtype, out, lse);
+  } else {
+    attn_fwd_kernel<64, 1><<<grid, THREADS, 0, stream>>>(
+        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
+        static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, scale_log2, nullptr, nullptr,
+        split_len, part_o, part_ml);
+    SPR_LAUNCHED("attn_fwd_kernel(dense)");
+    attn_combine_kernel<64><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
+                                                         nsplit, out_dtype, out, lse);
+  }
+  SPR_LAUNCHED("attn_combine_kernel");
+  return SPR_OK;
+}

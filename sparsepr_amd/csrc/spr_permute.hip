@@ -74,11 +74,14 @@ int launch_permute(const void* src, const void* suffix, const int32_t* idx, void
   if (bh == 0 || walk_rows == 0 || row_bytes == 0) return SPR_OK;
   SPR_REQUIRE(src && idx && dst, "%s: null pointer", name);
   SPR_REQUIRE(bh <= 65535, "%s: bh=%lld exceeds 65535", name, (long long)bh);
-  SPR_REQUIRE(row_bytes % 4 == 0, "%s: row bytes %lld not a multiple of 4", name, (long long)row_bytes);
-  const bool wide = (row_bytes % 16 == 0) && (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
-                    (reinterpret_cast<uintptr_t>(dst) % 16 == 0) &&
-                    (suffix == nullptr || reinterpret_cast<uintptr_t>(suffix) % 16 == 0);
-  const int64_t vec = wide ? 16 : 4;
+  SPR_REQUIRE(row_bytes % 2 == 0, "%s: row bytes %lld not a multiple of 2", name, (long long)row_bytes);
+  auto aligned = [&](uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(src) % a == 0) && (reinterpret_cast<uintptr_t>(dst) % a == 0) &&
+           (suffix == nullptr || reinterpret_cast<uintptr_t>(suffix) % a == 0);
+  };
+  const bool wide = (row_bytes % 16 == 0) && aligned(16);
+  const bool word = !wide && (row_bytes % 4 == 0) && aligned(4);
+  const int64_t vec = wide ? 16 : (word ? 4 : 2);
   const int64_t vpr = row_bytes / vec;
   const int64_t biggest = src_rows > dst_rows ? src_rows : dst_rows;
   SPR_REQUIRE(biggest * vpr < (int64_t(1) << 31), "%s: %lld rows of %lld bytes exceed the per-head limit",
@@ -91,10 +94,15 @@ int launch_permute(const void* src, const void* suffix, const int32_t* idx, void
         static_cast<const spr::u32x4*>(src), static_cast<const spr::u32x4*>(suffix), idx,
         static_cast<spr::u32x4*>(dst), static_cast<uint32_t>(src_rows), static_cast<uint32_t>(dst_rows),
         static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr));
-  } else {
+  } else if (word) {
     permute_rows_kernel<uint32_t, UNROLL, MODE><<<grid, 256, 0, stream>>>(
         static_cast<const uint32_t*>(src), static_cast<const uint32_t*>(suffix), idx,
         static_cast<uint32_t*>(dst), static_cast<uint32_t>(src_rows), static_cast<uint32_t>(dst_rows),
+        static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr));
+  } else {
+    permute_rows_kernel<uint16_t, UNROLL, MODE><<<grid, 256, 0, stream>>>(
+        static_cast<const uint16_t*>(src), static_cast<const uint16_t*>(suffix), idx,
+        static_cast<uint16_t*>(dst), static_cast<uint32_t>(src_rows), static_cast<uint32_t>(dst_rows),
         static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr));
   }
   SPR_LAUNCHED(name);

@@ -1,0 +1,332 @@
+// Block selection: top-p cluster-pair map, exact budget selector, mask
+// compaction into a kept-cluster schedule, kept-pair density.
+//
+// Replaces:
+//   identify_dynamic_map + weighted_softmax   (src/sparsepr/kmeans_utils.py:1710-1742, :1698-1707)
+//   svg_ear_select_budget(_schedule)          (kernels/n8_ext/csrc/n8_ops.cu:271-322, :541-638)
+//   exact_budget_dynamic_map_triton           (kernels/triton/selector_budget.py:10-54, :131-171)
+//   compact_selected_clusters                 (n8_ops.cu:324-355, :617-638)
+//   density_calculation                       (kmeans_utils.py:285-303)
+//
+// The top-p map must be reproducible bit for bit on the CPU (the decision
+// `cumsum > p` flips with the last ulp near the threshold), so every step has a
+// fixed fp32 evaluation order, with contraction disabled:
+//   score = (sequential fmaf over d of qc*kc) / sqrt(D)
+//   w_j e_j = size_j * canonical_expf(score_j - max)      (spr_common.h)
+//   denom  = max(sum_j in index order, 1e-12)
+//   prob_j = w_j e_j / denom
+//   order  = descending prob, ties by ascending index
+//   keep rank r iff r == 0 or cumsum(prob[order[0..r-1]]) <= p (r < preserve kept too).
+// With bf16 centroids (score_bf16 = 1) the reference's tensors are bf16 along the
+// way and the kernel rounds at the same points: matmul output and scaled score,
+// the softmax output (weighted_softmax returns input_dtype), each cumsum output,
+// and the threshold (a python float compared against a bf16 tensor is cast to bf16).
+#pragma clang fp contract(off)
+
+#include "spr_common.h"
+
+namespace {
+
+constexpr int SEL_THREADS = 256;
+constexpr int MAX_KC = 4096;
+
+__device__ __forceinline__ float bf16r(float f) { return spr::bf16_to_f32(spr::f32_to_bf16(f)); }
+
+__device__ __forceinline__ bool ranks_before(float pa, int ia, float pb, int ib) {
+  return pa > pb || (pa == pb && ia < ib);
+}
+
+__device__ float block_max(float v, float* scratch) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+  __syncthreads();
+  float m = scratch[0];
+  for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) m = fmaxf(m, scratch[w]);
+  __syncthreads();
+  return m;
+}
+
+// One workgroup per (bh, q-cluster) row.
+__global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __restrict__ qc,
+                                                               const float* __restrict__ kc,
+                                                               const int32_t* __restrict__ k_sizes,
+                                                               int32_t qn, int32_t kn, int32_t d, float sqrt_d,
+                                                               float p, int32_t preserve, int32_t score_bf16,
+                                                               uint8_t* __restrict__ map) {
+  __shared__ float q_row[512];
+  __shared__ float val[MAX_KC];
+  __shared__ float sorted_val[MAX_KC];
+  __shared__ int32_t sorted_idx[MAX_KC];
+  __shared__ uint8_t keep[MAX_KC];
+  __shared__ float scratch[SEL_THREADS / 64];
+  __shared__ float denom_s;
+
+  const int64_t row = blockIdx.x;  // bh * qn + q
+  const int64_t bh = row / qn;
+  const float* qrow = qc + row * d;
+  const float* kb = kc + bh * kn * static_cast<int64_t>(d);
+  const int32_t* sz = k_sizes + bh * kn;
+  for (int t = threadIdx.x; t < d; t += blockDim.x) q_row[t] = qrow[t];
+  __syncthreads();
+
+  float local_max = -__builtin_huge_valf();
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
+    const float* kr = kb + static_cast<int64_t>(j) * d;
+    float acc = 0.0f;
+    for (int t = 0; t < d; ++t) acc = __builtin_fmaf(q_row[t], kr[t], acc);
+    const float s = score_bf16 ? bf16r(__fdiv_rn(bf16r(acc), sqrt_d)) : __fdiv_rn(acc, sqrt_d);
+    val[j] = s;
+    local_max = fmaxf(local_max, s);
+  }
+  const float m = block_max(local_max, scratch);
+
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
+    const float w = static_cast<float>(sz[j]);
+    val[j] = __fmul_rn(w, spr::canonical_expf(__fsub_rn(val[j], m)));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sum = 0.0f;
+    for (int j = 0; j < kn; ++j) sum = __fadd_rn(sum, val[j]);
+    denom_s = sum > 1e-12f ? sum : 1e-12f;
+  }
+  __syncthreads();
+  const float denom = denom_s;
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
+    const float prob = __fdiv_rn(val[j], denom);
+    val[j] = score_bf16 ? bf16r(prob) : prob;
+  }
+  __syncthreads();
+
+  // rank sort: descending probability, ties by ascending index
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
+    const float pj = val[j];
+    int rank = 0;
+    for (int i = 0; i < kn; ++i) rank += ranks_before(val[i], i, pj, j) ? 1 : 0;
+    sorted_val[rank] = pj;
+    sorted_idx[rank] = j;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float thr = score_bf16 ? bf16r(p) : p;
+    float cum = 0.0f;
+    float prev = 0.0f;
+    for (int r = 0; r < kn; ++r) {
+      cum = __fadd_rn(cum, sorted_val[r]);
+      const float shown = score_bf16 ? bf16r(cum) : cum;
+      bool remove = (r > 0) && (prev > thr);
+      if (r < preserve) remove = false;
+      keep[sorted_idx[r]] = remove ? 0 : 1;
+      prev = shown;
+    }
+  }
+  __syncthreads();
+  uint8_t* out = map + row * kn;
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) out[j] = keep[j];
+}
+
+// One workgroup per (bh, q) row of scores [bh, qn, kn].
+// mode 0: n8_ops.cu semantics, mode 1: selector_budget.py / CPU-fallback semantics.
+__global__ __launch_bounds__(SEL_THREADS) void select_budget_kernel(
+    const float* __restrict__ scores, const int32_t* __restrict__ sizes, const int32_t* __restrict__ budgets,
+    int32_t qn, int32_t kn, int32_t mode, uint8_t* __restrict__ out, int32_t* __restrict__ ids,
+    int32_t* __restrict__ counts) {
+  __shared__ float val[MAX_KC];
+  __shared__ int32_t order[MAX_KC];
+  __shared__ uint8_t keep[MAX_KC];
+  const int64_t row = blockIdx.x;
+  const int64_t bh = row / qn;
+  const int32_t q = static_cast<int32_t>(row - bh * qn);
+  const float* srow = scores + row * kn;
+  const int32_t* sz = sizes + bh * kn;
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
+    val[j] = srow[j];
+    keep[j] = 0;
+  }
+  __syncthreads();
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
+    const float v = val[j];
+    int rank = 0;
+    for (int i = 0; i < kn; ++i) rank += ranks_before(val[i], i, v, j) ? 1 : 0;
+    order[rank] = j;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int32_t budget = budgets[row];
+    if (mode == 0) {
+      int64_t selected = 0;
+      int32_t crossing = -1;
+      for (int r = 0; r < kn; ++r) {
+        const int32_t c = order[r];
+        const int32_t cost = sz[c];
+        if (cost <= 0) continue;
+        if (crossing < 0 && selected + cost <= budget) {
+          keep[c] = 1;
+          selected += cost;
+        } else if (crossing < 0) {
+          crossing = c;
+        }
+      }
+      if (budget > 0 && selected < budget && crossing >= 0) keep[crossing] = 1;
+    } else {
+      int64_t cum = 0, selected = 0;
+      int32_t count = 0, valid = 0;
+      for (int r = 0; r < kn; ++r) {
+        const int32_t c = order[r];
+        const int32_t cost = sz[c];
+        if (cost > 0) {
+          ++valid;
+          cum += cost;
+          if (cum <= budget) {
+            keep[c] = 1;
+            selected += cost;
+            ++count;
+          }
+        }
+      }
+      if (budget > 0 && selected < budget && count < valid && count < kn) keep[order[count]] = 1;
+    }
+  }
+  __syncthreads();
+  const int64_t stride = static_cast<int64_t>(kn) + 1;
+  uint8_t* orow = out + (bh * (qn + 1) + q + 1) * stride;
+  for (int j = threadIdx.x; j <= kn; j += blockDim.x) orow[j] = (j == 0) ? 1 : keep[j - 1];
+  if (q == 0) {
+    uint8_t* head = out + bh * (qn + 1) * stride;
+    for (int j = threadIdx.x; j <= kn; j += blockDim.x) head[j] = (j == 0) ? 1 : 0;
+  }
+  if (ids != nullptr && counts != nullptr && threadIdx.x < 64) {
+    // ascending compaction of the kept flags by wave 0
+    const int lane = threadIdx.x;
+    int32_t* irow = ids + row * kn;
+    int32_t base = 0;
+    for (int c0 = 0; c0 < kn; c0 += 64) {
+      const int c = c0 + lane;
+      const bool k = c < kn && keep[c];
+      const uint64_t bits = __ballot(k);
+      const int pos = __popcll(bits & ((1ull << lane) - 1ull));
+      if (k) irow[base + pos] = c;
+      base += __popcll(bits);
+    }
+    if (lane == 0) counts[row] = base;
+  }
+}
+
+// One wave per row of a bool mask [rows, kn]: ascending kept ids + count.
+__global__ __launch_bounds__(64) void compact_kernel(const uint8_t* __restrict__ mask, int64_t rows, int32_t kn,
+                                                     int32_t* __restrict__ ids, int32_t* __restrict__ counts) {
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  const int lane = threadIdx.x;
+  const uint8_t* m = mask + row * kn;
+  int32_t* irow = ids + row * kn;
+  int32_t base = 0;
+  for (int c0 = 0; c0 < kn; c0 += 64) {
+    const int c = c0 + lane;
+    const bool k = c < kn && m[c] != 0;
+    const uint64_t bits = __ballot(k);
+    const int pos = __popcll(bits & ((1ull << lane) - 1ull));
+    if (k) irow[base + pos] = c;
+    base += __popcll(bits);
+  }
+  if (lane == 0) counts[row] = base;
+}
+
+// One workgroup per (cfg, head): kept pairs / all pairs, exact int64 sums.
+__global__ __launch_bounds__(256) void density_kernel(const uint8_t* __restrict__ map,
+                                                      const int32_t* __restrict__ q_sizes,
+                                                      const int32_t* __restrict__ k_sizes, int32_t qn,
+                                                      int32_t kn, float* __restrict__ out) {
+  __shared__ long long part[256];
+  __shared__ long long qtot[256];
+  __shared__ long long ktot[256];
+  const int64_t h = blockIdx.x;
+  const uint8_t* m = map + h * qn * static_cast<int64_t>(kn);
+  const int32_t* qs = q_sizes + h * qn;
+  const int32_t* ks = k_sizes + h * kn;
+  long long kept = 0, qsum = 0, ksum = 0;
+  for (int i = threadIdx.x; i < qn; i += blockDim.x) qsum += qs[i];
+  for (int j = threadIdx.x; j < kn; j += blockDim.x) ksum += ks[j];
+  for (int64_t e = threadIdx.x; e < static_cast<int64_t>(qn) * kn; e += blockDim.x) {
+    if (m[e]) {
+      const int i = static_cast<int>(e / kn);
+      const int j = static_cast<int>(e - static_cast<int64_t>(i) * kn);
+      kept += static_cast<long long>(qs[i]) * ks[j];
+    }
+  }
+  part[threadIdx.x] = kept;
+  qtot[threadIdx.x] = qsum;
+  ktot[threadIdx.x] = ksum;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    long long a = 0, b = 0, c = 0;
+    for (int t = 0; t < static_cast<int>(blockDim.x); ++t) {
+      a += part[t];
+      b += qtot[t];
+      c += ktot[t];
+    }
+    const double all = static_cast<double>(b) * static_cast<double>(c);
+    out[h] = all > 0.0 ? static_cast<float>(static_cast<double>(a) / all) : 0.0f;
+  }
+}
+
+}  // namespace
+
+// map uint8 [bh, qn, kn] from centroids qc [bh, qn, d], kc [bh, kn, d] (fp32
+// values; bf16 centroids are passed widened to fp32 with score_bf16 = 1) and
+// int32 key-cluster sizes [bh, kn].  sqrt_d is the divisor (float(sqrt(d))).
+extern "C" int spr_topp_map(const float* qc, const float* kc, const int32_t* k_sizes, int64_t bh, int32_t qn,
+                            int32_t kn, int32_t d, float sqrt_d, float p, int32_t preserve, int32_t score_bf16,
+                            uint8_t* map, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && qn >= 0 && kn >= 1, "spr_topp_map: bad size");
+  SPR_REQUIRE(kn <= MAX_KC, "spr_topp_map: %d key clusters exceed %d", kn, MAX_KC);
+  SPR_REQUIRE(d >= 1 && d <= 512, "spr_topp_map: head dim %d outside [1, 512]", d);
+  if (bh == 0 || qn == 0) return SPR_OK;
+  SPR_REQUIRE(qc && kc && k_sizes && map, "spr_topp_map: null pointer");
+  topp_map_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, 0, stream>>>(qc, kc, k_sizes, qn, kn, d,
+                                                                                     sqrt_d, p, preserve, score_bf16,
+                                                                                     map);
+  SPR_LAUNCHED("topp_map_kernel");
+  return SPR_OK;
+}
+
+// out uint8 [bh, qn + 1, kn + 1] (header row/column as the reference);
+// ids int32 [bh, qn, kn] and counts int32 [bh, qn] optional (both or neither).
+extern "C" int spr_select_budget(const float* scores, const int32_t* sizes, const int32_t* budgets, int64_t bh,
+                                 int32_t qn, int32_t kn, int32_t mode, uint8_t* out, int32_t* ids,
+                                 int32_t* counts, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && qn >= 0 && kn >= 1, "spr_select_budget: bad size");
+  SPR_REQUIRE(kn <= MAX_KC, "spr_select_budget: %d key clusters exceed %d", kn, MAX_KC);
+  SPR_REQUIRE(mode == 0 || mode == 1, "spr_select_budget: mode must be 0 or 1");
+  SPR_REQUIRE((ids == nullptr) == (counts == nullptr), "spr_select_budget: ids and counts go together");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(scores && sizes && budgets && out, "spr_select_budget: null pointer");
+  if (qn == 0) return SPR_OK;
+  select_budget_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, 0, stream>>>(
+      scores, sizes, budgets, qn, kn, mode, out, ids, counts);
+  SPR_LAUNCHED("select_budget_kernel");
+  return SPR_OK;
+}
+
+extern "C" int spr_compact_selected(const uint8_t* mask, int64_t rows, int32_t kn, int32_t* ids, int32_t* counts,
+                                    hipStream_t stream) {
+  SPR_REQUIRE(rows >= 0 && kn >= 1, "spr_compact_selected: bad size");
+  if (rows == 0) return SPR_OK;
+  SPR_REQUIRE(mask && ids && counts, "spr_compact_selected: null pointer");
+  SPR_REQUIRE(rows < (int64_t(1) << 31), "spr_compact_selected: too many rows");
+  compact_kernel<<<dim3(static_cast<uint32_t>(rows)), 64, 0, stream>>>(mask, rows, kn, ids, counts);
+  SPR_LAUNCHED("compact_kernel");
+  return SPR_OK;
+}
+
+// density[h] = sum_ij map[h,i,j] qs[h,i] ks[h,j] / (sum qs[h] * sum ks[h]) for h < heads.
+extern "C" int spr_density(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, int64_t heads,
+                           int32_t qn, int32_t kn, float* out, hipStream_t stream) {
+  SPR_REQUIRE(heads >= 0 && qn >= 1 && kn >= 1, "spr_density: bad size");
+  if (heads == 0) return SPR_OK;
+  SPR_REQUIRE(map && q_sizes && k_sizes && out, "spr_density: null pointer");
+  density_kernel<<<dim3(static_cast<uint32_t>(heads)), 256, 0, stream>>>(map, q_sizes, k_sizes, qn, kn, out);
+  SPR_LAUNCHED("density_kernel");
+  return SPR_OK;
+}

@@ -1,0 +1,101 @@
+"""Block-sparse attention over cluster-pair blocks and split-key dense probe
+attention on the HIP kernels of csrc/spr_attention.hip."""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+_PLAN_CACHE: dict = {}
+
+
+def _check_qkv(q, k, v, what):
+    dev = _lib.require_gpu(q, k, v, what=what)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise RuntimeError(f"{what}: bfloat16 Q/K/V required, got {q.dtype}/{k.dtype}/{v.dtype}")
+    return dev
+
+
+def plan_block_sparse(block_mask_map: torch.Tensor, block_row_sz: torch.Tensor, block_col_sz: torch.Tensor,
+                      seq_len: int) -> torch.Tensor:
+    """Kept-segment plan for [BHkv, Qc, Kc] maps (one small kernel)."""
+    dev = _lib.require_gpu(block_mask_map, what="block-sparse plan")
+    bh_kv, qn, kn = block_mask_map.shape
+    m = block_mask_map.to(torch.bool).contiguous()
+    qs = block_row_sz.to(device=dev, dtype=torch.int32).reshape(bh_kv, qn).contiguous()
+    ks = block_col_sz.to(device=dev, dtype=torch.int32).reshape(bh_kv, kn).contiguous()
+    nbytes = _lib.query("spr_block_sparse_attention_workspace", bh_kv, qn, kn)
+    plan = _lib.workspace(nbytes, dev)
+    _lib.call("spr_block_sparse_attention_plan", _lib.ptr(m), _lib.ptr(qs), _lib.ptr(ks), bh_kv, seq_len, qn, kn,
+              _lib.ptr(plan), plan.numel(), _lib.stream(dev))
+    return plan
+
+
+def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_mask_map: torch.Tensor,
+                           block_row_sz: torch.Tensor, block_col_sz: torch.Tensor, *, return_lse: bool = False,
+                           plan: torch.Tensor | None = None, scale: float | None = None):
+    """q [BHq, S, D], k/v [BHkv, S, D] bf16 cluster-contiguous; map [BHkv, Qc, Kc];
+    sizes [BHkv, Qc] / [BHkv, Kc].  Returns out [BHq, S, D] (and lse [BHq, S])."""
+    dev = _check_qkv(q, k, v, "block-sparse attention")
+    bh_q, s, d = q.shape
+    bh_kv = k.shape[0]
+    if k.shape != (bh_kv, s, d) or v.shape != k.shape:
+        raise RuntimeError(f"K/V shape {tuple(k.shape)} / {tuple(v.shape)} does not match Q {tuple(q.shape)}")
+    if bh_q % bh_kv != 0:
+        raise RuntimeError(f"Q heads ({bh_q}) must be divisible by KV heads ({bh_kv})")
+    _, qn, kn = block_mask_map.shape
+    if plan is None:
+        plan = plan_block_sparse(block_mask_map.to(dev), block_row_sz, block_col_sz, s)
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    out = torch.empty_like(qc)
+    lse = torch.empty((bh_q, s), dtype=torch.float32, device=dev) if return_lse else None
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(d)
+    _lib.call("spr_block_sparse_attention_run", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(plan), bh_q,
+              bh_kv, s, d, qn, kn, sc, _lib.ptr(out), _lib.ptr(lse), _lib.stream(dev))
+    return (out, lse) if return_lse else out
+
+
+def cached_plan(key, token, block_mask_map, block_row_sz, block_col_sz, seq_len):
+    """Plan cache keyed by an owner key; a matching token reuses the plan
+    (kmeans_utils.py:2229-2267 semantics)."""
+    entry = _PLAN_CACHE.get(key)
+    shape = (tuple(block_mask_map.shape), int(seq_len))
+    if entry is not None and entry[0] == token and entry[1] == shape:
+        return entry[2]
+    plan = plan_block_sparse(block_mask_map, block_row_sz, block_col_sz, seq_len)
+    _PLAN_CACHE[key] = (token, shape, plan)
+    return plan
+
+
+def clear_plan_cache():
+    _PLAN_CACHE.clear()
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float | None = None,
+                    out_dtype: torch.dtype = torch.float32, return_lse: bool = False, nsplit: int | None = None):
+    """softmax(q k^T * scale) v for few query rows: q [BHq, M, D], k/v [BHkv, S, D]
+    bf16 -> [BHq, M, D] in out_dtype (fp32 or bf16)."""
+    dev = _check_qkv(q, k, v, "dense attention")
+    bh_q, m, d = q.shape
+    bh_kv, s_kv, _ = k.shape
+    if v.shape != k.shape or k.shape[2] != d:
+        raise RuntimeError("dense attention: K/V shape mismatch")
+    if bh_q % bh_kv != 0:
+        raise RuntimeError("dense attention: Q heads must be a multiple of KV heads")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError("dense attention: out_dtype must be float32 or bfloat16")
+    if nsplit is None:
+        mtiles = max(1, (m + 127) // 128)
+        nsplit = max(1, min((1024 + bh_q * mtiles - 1) // (bh_q * mtiles), max(1, s_kv // 512)))
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    out = torch.empty((bh_q, m, d), dtype=out_dtype, device=dev)
+    lse = torch.empty((bh_q, m), dtype=torch.float32, device=dev) if return_lse else None
+    ws = _lib.workspace(_lib.query("spr_dense_attention_workspace", bh_q, m, d, nsplit), dev)
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(d)
+    _lib.call("spr_dense_attention", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), bh_q, bh_kv, m, s_kv, d, sc, nsplit,
+              _lib.ptr(out), 0 if out_dtype == torch.bfloat16 else 2, _lib.ptr(lse), _lib.ptr(ws), ws.numel(),
+              _lib.stream(dev))
+    return (out, lse) if return_lse else out

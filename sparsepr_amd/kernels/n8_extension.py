@@ -57,10 +57,39 @@ def role_cluster_step_k64(features: torch.Tensor, centroids: torch.Tensor):
     return tuple(_role_step(features, centroids, 1024))
 
 
+def svg_ear_select_budget(scores: torch.Tensor, cluster_sizes: torch.Tensor,
+                          budgets: torch.Tensor) -> torch.Tensor:
+    """Exact descending selector budget and bool-mask scatter (n8_ops.cu:541-571)."""
+    from .selection import MODE_N8_NATIVE, select_budget
+
+    _lib.require_gpu(scores, cluster_sizes, budgets, what="Selector inputs")
+    return select_budget(scores.contiguous(), cluster_sizes, budgets, MODE_N8_NATIVE)
+
+
+def svg_ear_select_budget_schedule(scores: torch.Tensor, cluster_sizes: torch.Tensor,
+                                   budgets: torch.Tensor):
+    """Selector plus ascending fixed-stride selected-cluster ids and counts (n8_ops.cu:573-615)."""
+    from .selection import MODE_N8_NATIVE, select_budget
+
+    _lib.require_gpu(scores, cluster_sizes, budgets, what="Selector inputs")
+    return tuple(select_budget(scores.contiguous(), cluster_sizes, budgets, MODE_N8_NATIVE,
+                               with_schedule=True))
+
+
+def compact_selected_clusters(selected_mask: torch.Tensor):
+    """Ascending fixed-stride cluster ids and a count for every row (n8_ops.cu:617-638)."""
+    from .selection import compact
+
+    return tuple(compact(selected_mask))
+
+
 def _exports() -> dict:
     return {
         "role_cluster_step_q64": lambda f, c: _role_step(f, c, 512),
         "role_cluster_step_k64": lambda f, c: _role_step(f, c, 1024),
+        "svg_ear_select_budget": svg_ear_select_budget,
+        "svg_ear_select_budget_schedule": lambda s, z, b: list(svg_ear_select_budget_schedule(s, z, b)),
+        "compact_selected_clusters": lambda m: list(compact_selected_clusters(m)),
     }
 
 

@@ -1,0 +1,186 @@
+"""GPU parity: block-sparse attention over cluster-pair blocks and the dense
+probe attention.  Tolerance (bf16 in/out, fp32 softmax): max-abs <= 2e-2 and
+cosine >= 0.999 against the float64 closed form; all-dropped rows exactly 0."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests._helpers import to_dev
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-2
+COS = 0.999
+
+
+def _cos(a, b):
+    a = a.reshape(-1).astype(np.float64)
+    b = b.reshape(-1).astype(np.float64)
+    return float(a @ b / max(np.linalg.norm(a) * np.linalg.norm(b), 1e-30))
+
+
+def _sizes(rng, n, total, empty_every=0):
+    w = rng.random(n) + 0.05
+    if empty_every:
+        w[::empty_every] = 0.0
+    s = np.floor(w / w.sum() * total).astype(np.int64)
+    s[np.argmax(w)] += total - s.sum()
+    return s
+
+
+def _problem(oracle, rng, B, Hq, Hkv, S, D, qn, kn, density=0.3, empty_row=True, scale=1.0):
+    q = oracle.to_bf16((scale * rng.standard_normal((B, Hq, S, D))).astype(np.float32))
+    k = oracle.to_bf16((scale * rng.standard_normal((B, Hkv, S, D))).astype(np.float32))
+    v = oracle.to_bf16(rng.standard_normal((B, Hkv, S, D)).astype(np.float32))
+    qs = np.stack([[_sizes(rng, qn, S, 5) for _ in range(Hkv)] for _ in range(B)])
+    ks = np.stack([[_sizes(rng, kn, S, 7) for _ in range(Hkv)] for _ in range(B)])
+    m = rng.random((B, Hkv, qn, kn)) < density
+    if empty_row:
+        m[..., 1, :] = False
+    return q, k, v, m, qs, ks
+
+
+def _reference(oracle, q, k, v, m, qs, ks):
+    B, Hq, S, D = q.shape
+    Hkv = k.shape[1]
+    g = Hq // Hkv
+    rep = lambda a: np.repeat(a, g, axis=1)
+    return oracle.block_sparse_attention_dense(q, rep(k), rep(v), rep(m), rep(qs), rep(ks), return_lse=True)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,D,qn,kn", [
+    (1, 2, 2, 700, 128, 6, 11),
+    (1, 3, 3, 1000, 64, 9, 40),
+    (2, 2, 2, 513, 128, 3, 17),     # q-clusters of > 128 rows: several tiles per cluster
+    (1, 4, 2, 600, 128, 5, 9),      # GQA group 2
+    (1, 1, 1, 64, 128, 1, 1),
+])
+def test_block_sparse_matches_closed_form(dev, oracle, B, Hq, Hkv, S, D, qn, kn):
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
+
+    rng = np.random.default_rng(S + D + qn)
+    q, k, v, m, qs, ks = _problem(oracle, rng, B, Hq, Hkv, S, D, qn, kn)
+    out, lse = dynamic_block_sparse_fwd_flashinfer(
+        to_dev(q, dev, torch.bfloat16), to_dev(k, dev, torch.bfloat16), to_dev(v, dev, torch.bfloat16),
+        torch.from_numpy(m), torch.from_numpy(qs).int(), torch.from_numpy(ks).int(), is_cpu=True,
+        num_kv_heads=Hkv if Hkv != Hq else None, return_lse=True)
+    ref, ref_lse = _reference(oracle, q, k, v, m, qs, ks)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - ref).max() <= ATOL
+    assert _cos(got, ref) >= COS
+    g = lse.cpu().numpy()
+    fin = np.isfinite(ref_lse)
+    assert np.allclose(g[fin], ref_lse[fin], atol=1e-3, rtol=1e-4)
+    assert np.isneginf(g[~fin]).all()
+    # rows of q-cluster 1 (all blocks dropped) are exactly zero
+    if qn > 1:
+        for b in range(B):
+            for h in range(Hq):
+                r0 = int(qs[b, h // (Hq // Hkv), :1].sum())
+                r1 = r0 + int(qs[b, h // (Hq // Hkv), 1])
+                assert (got[b, h, r0:r1] == 0).all()
+
+
+def test_block_sparse_matches_reference_loop(dev, oracle):
+    """Against the loop-faithful restatement of dynamic_block_sparse_fwd_torch."""
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_triton
+
+    rng = np.random.default_rng(7)
+    q, k, v, m, qs, ks = _problem(oracle, rng, 1, 2, 2, 400, 64, 4, 8)
+    loop = oracle.block_sparse_attention_loop(q, k, v, m, qs, ks)
+    out = dynamic_block_sparse_fwd_triton(to_dev(q, dev, torch.bfloat16), to_dev(k, dev, torch.bfloat16),
+                                          to_dev(v, dev, torch.bfloat16), to_dev(m, dev), to_dev(qs, dev),
+                                          to_dev(ks, dev))
+    got = out.float().cpu().numpy()
+    assert np.abs(got - loop).max() <= ATOL and _cos(got, loop) >= COS
+
+
+def test_block_sparse_full_map_equals_dense(dev, oracle):
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
+
+    rng = np.random.default_rng(8)
+    q, k, v, m, qs, ks = _problem(oracle, rng, 1, 2, 2, 333, 128, 4, 6, empty_row=False)
+    m[:] = True
+    out = dynamic_block_sparse_fwd_flashinfer(to_dev(q, dev, torch.bfloat16), to_dev(k, dev, torch.bfloat16),
+                                              to_dev(v, dev, torch.bfloat16), to_dev(m, dev), to_dev(qs, dev),
+                                              to_dev(ks, dev), is_cpu=False)
+    ref = oracle.dense_attention(q[0], k[0], v[0])
+    got = out[0].float().cpu().numpy()
+    assert np.abs(got - ref).max() <= ATOL and _cos(got, ref) >= COS
+
+
+def test_plan_cache_reuse(dev, oracle):
+    from sparsepr_amd.kernels.attention import clear_plan_cache
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
+
+    rng = np.random.default_rng(9)
+    q, k, v, m, qs, ks = _problem(oracle, rng, 1, 2, 2, 300, 128, 3, 5)
+    args = [to_dev(q, dev, torch.bfloat16), to_dev(k, dev, torch.bfloat16), to_dev(v, dev, torch.bfloat16)]
+    o1 = dynamic_block_sparse_fwd_flashinfer(*args, to_dev(m, dev), to_dev(qs, dev), to_dev(ks, dev), is_cpu=False,
+                                             plan_cache_key="layer0", plan_cache_token=1)
+    o2 = dynamic_block_sparse_fwd_flashinfer(*args, to_dev(m, dev), to_dev(qs, dev), to_dev(ks, dev), is_cpu=False,
+                                             plan_cache_key="layer0", plan_cache_token=1)
+    assert torch.equal(o1, o2)
+    with pytest.raises(ValueError):
+        dynamic_block_sparse_fwd_flashinfer(*args, to_dev(m, dev), to_dev(qs, dev), to_dev(ks, dev), is_cpu=False,
+                                            plan_cache_key="layer0")
+    clear_plan_cache()
+
+
+@pytest.mark.parametrize("M,S,D,nsplit", [(128, 5000, 128, None), (64, 4096, 64, 3), (200, 1000, 128, 1),
+                                          (17, 777, 128, 5)])
+def test_dense_probe_attention(dev, oracle, M, S, D, nsplit):
+    from sparsepr_amd.kernels.attention import dense_attention
+
+    rng = np.random.default_rng(M + S)
+    q = oracle.to_bf16(rng.standard_normal((3, M, D)).astype(np.float32))
+    k = oracle.to_bf16(rng.standard_normal((3, S, D)).astype(np.float32))
+    v = oracle.to_bf16(rng.standard_normal((3, S, D)).astype(np.float32))
+    out, lse = dense_attention(to_dev(q, dev, torch.bfloat16), to_dev(k, dev, torch.bfloat16),
+                               to_dev(v, dev, torch.bfloat16), nsplit=nsplit, return_lse=True)
+    ref = oracle.dense_attention(q, k, v)
+    got = out.cpu().numpy()
+    assert np.abs(got - ref).max() <= 5e-3 and _cos(got, ref) >= 0.9999
+    s = np.einsum("bmd,bsd->bms", q.astype(np.float64), k.astype(np.float64)) / math.sqrt(D)
+    ref_lse = np.log(np.exp(s - s.max(-1, keepdims=True)).sum(-1)) + s.max(-1)
+    assert np.allclose(lse.cpu().numpy(), ref_lse, atol=2e-3)
+
+
+def test_block_sparse_full_size_sampled_rows(dev, oracle):
+    """HunyuanVideo shape (24 heads x 118,800 x 128): a random map over 128 x 512
+    cluster pairs; 192 sampled rows checked against float64 on the CPU."""
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
+
+    H, S, D, qn, kn = 24, 118800, 128, 128, 512
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    q = torch.randn(1, H, S, D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, H, S, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, H, S, D, device=dev, generator=g).to(torch.bfloat16)
+    rng = np.random.default_rng(4)
+    qs = np.stack([_sizes(rng, qn, S, 0) for _ in range(H)])[None]
+    ks = np.stack([_sizes(rng, kn, S, 50) for _ in range(H)])[None]
+    m = rng.random((1, H, qn, kn)) < 0.12
+    out = dynamic_block_sparse_fwd_flashinfer(q, k, v, to_dev(m, dev), to_dev(qs, dev), to_dev(ks, dev),
+                                              is_cpu=False)
+    qoff = np.concatenate([np.zeros((1, H, 1), np.int64), np.cumsum(qs, -1)], -1)
+    koff = np.concatenate([np.zeros((1, H, 1), np.int64), np.cumsum(ks, -1)], -1)
+    for _ in range(192):
+        h = int(rng.integers(0, H))
+        r = int(rng.integers(0, S))
+        a = int(np.searchsorted(qoff[0, h], r, side="right") - 1)
+        keys = np.concatenate([np.arange(koff[0, h, c], koff[0, h, c + 1]) for c in np.nonzero(m[0, h, a])[0]]
+                              + [np.zeros(0, np.int64)])
+        got = out[0, h, r].float().cpu().numpy()
+        if keys.size == 0:
+            assert (got == 0).all()
+            continue
+        kk = k[0, h, torch.from_numpy(keys).to(dev)].double().cpu().numpy()
+        vv = v[0, h, torch.from_numpy(keys).to(dev)].double().cpu().numpy()
+        s = kk @ q[0, h, r].double().cpu().numpy() / math.sqrt(D)
+        e = np.exp(s - s.max())
+        ref = (e / e.sum()) @ vv
+        assert np.abs(got - ref).max() <= ATOL

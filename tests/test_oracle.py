@@ -476,3 +476,52 @@ def test_layer_runs_and_probe_rows_are_exact(oracle):
     for h in range(bh):
         assert (out[h, res["rows"][h]] == oracle.to_bf16(res["dense"][h])).all()
     assert ((res["density"] > 0) & (res["density"] <= 1)).all()
+
+
+def _torch_identify_dynamic_map(qc, kc, k_sizes, p, min_kc_ratio=0.0):
+    """The reference's op sequence (kmeans_utils.py:1698-1742) run with torch on
+    the CPU in the centroids' own dtype: an independent implementation of the
+    dtype flow (torch's matmul, rounding, sort and cumsum)."""
+    import torch
+
+    D = qc.shape[-1]
+    kc_num = kc.shape[-2]
+    s = torch.matmul(qc, kc.transpose(-2, -1)) / (D ** 0.5)
+    w = k_sizes.unsqueeze(-2).float()
+    input_dtype = s.dtype
+    sf = s.float()
+    e = torch.exp(sf - sf.max(-1, keepdim=True)[0])
+    we = w * e
+    probs = (we / we.sum(-1, keepdim=True).clamp(min=1e-12)).to(input_dtype)
+    sp, si = torch.sort(probs, dim=-1, descending=True, stable=True)
+    cum = torch.cumsum(sp, dim=-1)
+    rem = cum > p
+    rem[..., 1:] = rem[..., :-1].clone()
+    rem[..., 0] = False
+    if min_kc_ratio > 0:
+        rem[..., : int(min_kc_ratio * kc_num)] = False
+    out = torch.zeros(probs.shape, dtype=torch.bool)
+    out.scatter_(-1, si, ~rem)
+    return out, cum.float()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_topp_map_matches_torch_dtype_flow(oracle, bf16):
+    import torch
+
+    rng = np.random.default_rng(21 + bf16)
+    for p in (0.8, 0.9):
+        qc = (0.4 * rng.standard_normal((3, 16, 64))).astype(np.float32)
+        kc = (0.4 * rng.standard_normal((3, 40, 64))).astype(np.float32)
+        ks = rng.integers(0, 300, (3, 40)).astype(np.int32)
+        if bf16:
+            qc, kc = oracle.to_bf16(qc), oracle.to_bf16(kc)
+        dt = torch.bfloat16 if bf16 else torch.float32
+        ref, cum = _torch_identify_dynamic_map(torch.from_numpy(qc).to(dt), torch.from_numpy(kc).to(dt),
+                                               torch.from_numpy(ks), p)
+        got, gcum, _ = oracle.identify_dynamic_map(qc, kc, ks, p, bf16=bf16, return_cum=True)
+        # rows whose cumulative mass comes within one bf16 ulp (or 1e-5) of p are ties
+        tol = 2 ** -8 if bf16 else 1e-5
+        near = (np.abs(cum.numpy() - p) <= tol).any(-1)
+        assert (got[~near] == ref.numpy()[~near]).all()
+        assert (~near).mean() > 0.5
