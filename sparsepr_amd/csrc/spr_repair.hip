@@ -1,0 +1,434 @@
+// Probe-fitted reduced-rank residual repair: probe selection, fit preparation,
+// low-rank apply, exact-probe scatter.
+//
+// Replaces:
+//   select_role_equal_probes(_vectorized), select_first_token_largest_groups
+//       (src/sparsepr/models/cosmos3/residual_repair.py:36-260)
+//   n8_prepare_output_repair_fit_triton    (kernels/triton/residual_repair.py:798-857, kernel :330-363)
+//   n8_repair_apply_output_triton          (kernels/triton/residual_repair.py:478-562, kernel :95-155)
+//   n8_exact_probe_scatter_triton          (kernels/triton/residual_repair.py:656-700, kernel :257-282)
+//
+// Probe selection runs in two launches.  (1) distance: each token's squared
+// distance to its cluster center, summed over dims in index order with separate
+// fp32 multiply and add (a fixed order, so exact ties are reproducible).
+// (2) select, one workgroup per head: groups ordered by size (descending,
+// stable); in round r every group offers its r-th nearest token (ties by lower
+// token id) via an LDS atomicMin over 64-bit (distance bits, token) keys.
+#pragma clang fp contract(off)
+
+#include "spr_common.h"
+
+namespace {
+
+using spr::u32x4;
+
+constexpr int MAX_GROUPS = 2048;
+
+template <typename T>
+__device__ __forceinline__ float load_elem(const T* p, int64_t i) {
+  if constexpr (sizeof(T) == 2) {
+    return spr::bf16_to_f32(p[i]);
+  } else {
+    return p[i];
+  }
+}
+
+// dist[bh, t] = sum_d (f[t, d] - center[label[t], d])^2, d ascending.
+// 64 tokens per workgroup: 256 threads compute rounded squares into LDS, then
+// one thread per token adds its row in order.
+template <typename T, int R>
+__global__ __launch_bounds__(256) void probe_distance_kernel(const T* __restrict__ f,
+                                                             const int32_t* __restrict__ labels,
+                                                             const float* __restrict__ centers, int64_t n,
+                                                             int32_t groups, float* __restrict__ dist) {
+  __shared__ float sq[64][R + 1];
+  const int64_t bh = blockIdx.y;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
+  for (int e = threadIdx.x; e < 64 * R; e += blockDim.x) {
+    const int row = e / R;
+    const int d = e % R;
+    const int64_t t = t0 + row;
+    float v = 0.0f;
+    if (t < n) {
+      const int32_t lab = labels[bh * n + t];
+      const float c = (lab >= 0 && lab < groups) ? centers[(bh * groups + lab) * R + d] : 0.0f;
+      const float diff = __fsub_rn(load_elem(f, (bh * n + t) * R + d), c);
+      v = __fmul_rn(diff, diff);
+    }
+    sq[row][d] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int64_t t = t0 + threadIdx.x;
+    if (t < n) {
+      float acc = 0.0f;
+      for (int d = 0; d < R; ++d) acc = __fadd_rn(acc, sq[threadIdx.x][d]);
+      dist[bh * n + t] = acc;
+    }
+  }
+}
+
+// mode 0: vectorized role-equal (one representative per group, first `count`
+//         groups in size order; empty-group slots fall back to token j);
+// mode 1: representative rounds until `count` probes (an exhausted group offers
+//         its lowest token again, as the reference does);
+// mode 2: first token of each of the largest groups, weight = group size.
+__global__ __launch_bounds__(256) void probe_select_kernel(const float* __restrict__ dist,
+                                                           const int32_t* __restrict__ labels,
+                                                           const int32_t* __restrict__ sizes, int64_t n,
+                                                           int32_t groups, int32_t count, int32_t mode,
+                                                           int32_t* __restrict__ rows, float* __restrict__ weights,
+                                                           int32_t* __restrict__ status) {
+  __shared__ int32_t sz[MAX_GROUPS];
+  __shared__ int32_t order[MAX_GROUPS];
+  __shared__ unsigned long long best[MAX_GROUPS];
+  __shared__ unsigned long long prev[MAX_GROUPS];
+  __shared__ int32_t sampled[MAX_GROUPS];
+  __shared__ int32_t first_tok[MAX_GROUPS];
+  __shared__ int32_t chosen_count;
+  __shared__ double wsum;
+  const int64_t bh = blockIdx.x;
+  const int32_t* lab = labels + bh * n;
+  const float* dd = dist + bh * n;
+  int32_t* out_rows = rows + bh * count;
+  float* out_w = weights + bh * count;
+
+  for (int c = threadIdx.x; c < groups; c += blockDim.x) {
+    sz[c] = sizes[bh * groups + c];
+    prev[c] = 0ull;
+    sampled[c] = 0;
+  }
+  if (threadIdx.x == 0) chosen_count = 0;
+  __syncthreads();
+  // stable descending order of group sizes
+  for (int c = threadIdx.x; c < groups; c += blockDim.x) {
+    const int32_t s = sz[c];
+    int rank = 0;
+    for (int o = 0; o < groups; ++o) {
+      const int32_t so = sz[o];
+      rank += (so > s || (so == s && o < c)) ? 1 : 0;
+    }
+    order[rank] = c;
+  }
+  __syncthreads();
+
+  // Round r: every non-empty group offers its r-th smallest (distance, token)
+  // key.  A group whose members are all taken offers its lowest token id again,
+  // as the reference's all-infinite remaining distances do (residual_repair.py:70-98).
+  const unsigned long long none = ~0ull;
+  for (int c = threadIdx.x; c < groups; c += blockDim.x) first_tok[c] = 0x7fffffff;
+  for (int round = 0; round <= count; ++round) {
+    for (int c = threadIdx.x; c < groups; c += blockDim.x) best[c] = none;
+    __syncthreads();
+    for (int64_t t = threadIdx.x; t < n; t += blockDim.x) {
+      const int32_t c = lab[t];
+      if (c < 0 || c >= groups) continue;
+      const float dv = (mode == 2) ? 0.0f : dd[t];
+      const unsigned long long key =
+          (static_cast<unsigned long long>(__float_as_uint(dv)) << 32) | static_cast<uint32_t>(t);
+      if (round == 0) {
+        atomicMin(&best[c], key);
+        atomicMin(&first_tok[c], static_cast<int32_t>(t));
+      } else if (key > prev[c]) {
+        atomicMin(&best[c], key);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int32_t have = chosen_count;
+      for (int j = 0; j < groups && have < count; ++j) {
+        const int32_t c = order[j];
+        const unsigned long long key = best[c];
+        if (sz[c] <= 0) {
+          if (mode != 1) {
+            out_rows[have] = have;  // empty group: fallback token id = slot
+            ++have;
+          }
+        } else if (key != none) {
+          out_rows[have++] = static_cast<int32_t>(key & 0xffffffffull);
+        } else {
+          out_rows[have++] = first_tok[c];  // exhausted group
+        }
+      }
+      chosen_count = have;
+    }
+    for (int c = threadIdx.x; c < groups; c += blockDim.x) {
+      if (best[c] != none) prev[c] = best[c];
+    }
+    __syncthreads();
+    if (mode != 1 || chosen_count >= count || chosen_count == 0) break;
+  }
+  if (threadIdx.x == 0 && status != nullptr) status[bh] = chosen_count;
+  __syncthreads();
+
+  // weights: group size / probes sampled from the group, normalised to mean 1
+  const int32_t have = chosen_count;
+  for (int j = threadIdx.x; j < have; j += blockDim.x) {
+    const int32_t t = out_rows[j];
+    const int32_t c = (t >= 0 && t < n) ? lab[t] : -1;
+    if (c >= 0 && c < groups) atomicAdd(&sampled[c], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    for (int j = 0; j < have; ++j) {
+      const int32_t t = out_rows[j];
+      const int32_t c = (t >= 0 && t < n) ? lab[t] : -1;
+      float w = 0.0f;
+      if (c >= 0 && c < groups) {
+        const float size = static_cast<float>(sz[c]);
+        w = (mode == 2) ? size : __fdiv_rn(size, static_cast<float>(max(sampled[c], 1)));
+      }
+      out_w[j] = w;
+      s += static_cast<double>(w);
+    }
+    wsum = have > 0 ? s / static_cast<double>(have) : 0.0;
+  }
+  __syncthreads();
+  const float mean = fmaxf(static_cast<float>(wsum), 1e-20f);
+  for (int j = threadIdx.x; j < have; j += blockDim.x) out_w[j] = __fdiv_rn(out_w[j], mean);
+}
+
+// x_fit = float(base[rows]), dense_f = float(dense), y_fit = dense_f - x_fit.
+template <typename TB, typename TD>
+__global__ void fit_prep_kernel(const TB* __restrict__ base, const TD* __restrict__ dense,
+                                const int32_t* __restrict__ rows, int64_t n, int32_t m, int32_t d,
+                                float* __restrict__ x_fit, float* __restrict__ dense_f, float* __restrict__ y_fit) {
+  const int64_t bh = blockIdx.y;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < m * d; e += gridDim.x * blockDim.x) {
+    const int j = e / d;
+    const int c = e - j * d;
+    const int32_t r = rows[bh * m + j];
+    const float b = (r >= 0 && r < n) ? load_elem(base, (bh * n + r) * d + c) : 0.0f;
+    const float y = load_elem(dense, (bh * m + j) * static_cast<int64_t>(d) + c);
+    const int64_t o = (bh * m + j) * static_cast<int64_t>(d) + c;
+    x_fit[o] = b;
+    dense_f[o] = y;
+    y_fit[o] = __fsub_rn(y, b);
+  }
+}
+
+// out = base + alpha * (((base - mu) / sigma) L B^T + mu_y), optional norm cap.
+// One lane per token row (64 rows per wave); L and B are read from LDS as
+// wave-uniform broadcasts.  Loops over the head dim are fully unrolled so the
+// row stays in registers.
+template <int D, int RK>
+__global__ __launch_bounds__(256) void repair_apply_kernel(const uint16_t* __restrict__ base,
+                                                           const float* __restrict__ x_mean,
+                                                           const float* __restrict__ x_scale,
+                                                           const float* __restrict__ y_mean,
+                                                           const float* __restrict__ left,
+                                                           const float* __restrict__ basis, int64_t n, float alpha,
+                                                           float norm_cap, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float Ls[D][RK];
+  __shared__ __attribute__((aligned(16))) float Bs[D][RK];
+  __shared__ float mu[D], inv_sd[D], my[D];
+  const int64_t bh = blockIdx.y;
+  for (int e = threadIdx.x; e < D * RK; e += blockDim.x) {
+    Ls[e / RK][e % RK] = left[bh * D * RK + e];
+    Bs[e / RK][e % RK] = basis[bh * D * RK + e];
+  }
+  for (int e = threadIdx.x; e < D; e += blockDim.x) {
+    mu[e] = x_mean[bh * D + e];
+    inv_sd[e] = 1.0f / x_scale[bh * D + e];
+    my[e] = y_mean[bh * D + e];
+  }
+  __syncthreads();
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const u32x4* brow = reinterpret_cast<const u32x4*>(base + (bh * n + t) * D);
+  uint32_t packed[D / 2];
+#pragma unroll
+  for (int i = 0; i < D / 8; ++i) {
+    const u32x4 w = brow[i];
+    packed[4 * i] = w.x;
+    packed[4 * i + 1] = w.y;
+    packed[4 * i + 2] = w.z;
+    packed[4 * i + 3] = w.w;
+  }
+  float coords[RK];
+#pragma unroll
+  for (int r = 0; r < RK; ++r) coords[r] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < D / 2; ++i) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int dd = 2 * i + e;
+      const float b = e ? spr::bf16_hi(packed[i]) : spr::bf16_lo(packed[i]);
+      const float z = (b - mu[dd]) * inv_sd[dd];
+#pragma unroll
+      for (int r = 0; r < RK; ++r) coords[r] = __builtin_fmaf(z, Ls[dd][r], coords[r]);
+    }
+  }
+  float scale = alpha;
+  if (norm_cap > 0.0f) {
+    float bn = 0.0f, cn = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D / 2; ++i) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int dd = 2 * i + e;
+        const float b = e ? spr::bf16_hi(packed[i]) : spr::bf16_lo(packed[i]);
+        float corr = my[dd];
+#pragma unroll
+        for (int r = 0; r < RK; ++r) corr = __builtin_fmaf(coords[r], Bs[dd][r], corr);
+        bn = __builtin_fmaf(b, b, bn);
+        cn = __builtin_fmaf(corr, corr, cn);
+      }
+    }
+    scale = alpha * fminf(1.0f, norm_cap * sqrtf(bn) / fmaxf(sqrtf(cn), 1e-20f));
+  }
+  u32x4* orow = reinterpret_cast<u32x4*>(out + (bh * n + t) * D);
+#pragma unroll
+  for (int i = 0; i < D / 8; ++i) {
+    uint32_t o[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const uint32_t w = packed[4 * i + h];
+      float res[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int dd = 8 * i + 2 * h + e;
+        const float b = e ? spr::bf16_hi(w) : spr::bf16_lo(w);
+        float corr = my[dd];
+#pragma unroll
+        for (int r = 0; r < RK; ++r) corr = __builtin_fmaf(coords[r], Bs[dd][r], corr);
+        res[e] = __builtin_fmaf(scale, corr, b);
+      }
+      o[h] = spr::pack_bf16x2(res[0], res[1]);
+    }
+    orow[i] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// out[bh, rows[j]] = dense[bh, j] cast to the output dtype (bf16 out, fp32 or bf16 in).
+template <typename TD>
+__global__ void probe_scatter_kernel(const TD* __restrict__ dense, const int32_t* __restrict__ rows, int64_t n,
+                                     int32_t m, int32_t d, uint16_t* __restrict__ out) {
+  const int64_t bh = blockIdx.y;
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < m * d; e += gridDim.x * blockDim.x) {
+    const int j = e / d;
+    const int c = e - j * d;
+    const int32_t r = rows[bh * m + j];
+    if (r < 0 || r >= n) continue;
+    const float v = load_elem(dense, (bh * m + j) * static_cast<int64_t>(d) + c);
+    out[(bh * n + r) * d + c] = spr::f32_to_bf16(v);
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------ C ABI
+
+// dist fp32 [bh, n] for features [bh, n, r] (dtype 0 bf16 / 2 fp32), labels int32
+// [bh, n], centers fp32 [bh, groups, r].  r in {64, 128}.
+extern "C" int spr_probe_distances(const void* features, int32_t dtype, const int32_t* labels, const float* centers,
+                                   int64_t bh, int64_t n, int32_t groups, int32_t r, float* dist, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0 && groups >= 1, "spr_probe_distances: bad size");
+  SPR_REQUIRE(bh <= 65535, "spr_probe_distances: bh exceeds 65535");
+  if (bh == 0 || n == 0) return SPR_OK;
+  SPR_REQUIRE(features && labels && centers && dist, "spr_probe_distances: null pointer");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 64)), static_cast<uint32_t>(bh));
+#define SPR_PD(T, RR)                                                                                          \
+  probe_distance_kernel<T, RR><<<grid, 256, 0, stream>>>(static_cast<const T*>(features), labels, centers, n, \
+                                                          groups, dist)
+  if (dtype == 0 && r == 128) SPR_PD(uint16_t, 128);
+  else if (dtype == 0 && r == 64) SPR_PD(uint16_t, 64);
+  else if (dtype == 2 && r == 128) SPR_PD(float, 128);
+  else if (dtype == 2 && r == 64) SPR_PD(float, 64);
+  else SPR_REQUIRE(false, "spr_probe_distances: dtype %d / dim %d not supported", dtype, r);
+#undef SPR_PD
+  SPR_LAUNCHED("probe_distance_kernel");
+  return SPR_OK;
+}
+
+// rows int32 [bh, count], weights fp32 [bh, count]; filled int32 [bh] (nullable)
+// receives the number of rows found (count unless mode 1 ran out of tokens).
+// dist may be null for mode 2.
+extern "C" int spr_probe_select(const float* dist, const int32_t* labels, const int32_t* sizes, int64_t bh, int64_t n,
+                                int32_t groups, int32_t count, int32_t mode, int32_t* rows, float* weights,
+                                int32_t* filled, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0 && groups >= 1 && count >= 0, "spr_probe_select: bad size");
+  SPR_REQUIRE(groups <= MAX_GROUPS, "spr_probe_select: %d groups exceed %d", groups, MAX_GROUPS);
+  SPR_REQUIRE(mode >= 0 && mode <= 2, "spr_probe_select: mode must be 0, 1 or 2");
+  SPR_REQUIRE(mode == 1 || count <= groups, "spr_probe_select: rows=%d > groups=%d needs mode 1", count, groups);
+  SPR_REQUIRE(n < (int64_t(1) << 31), "spr_probe_select: n too large");
+  SPR_REQUIRE(count <= n, "spr_probe_select: more probes than tokens");
+  if (bh == 0 || count == 0) return SPR_OK;
+  SPR_REQUIRE(labels && sizes && rows && weights && (dist || mode == 2), "spr_probe_select: null pointer");
+  probe_select_kernel<<<dim3(static_cast<uint32_t>(bh)), 256, 0, stream>>>(dist, labels, sizes, n, groups, count,
+                                                                           mode, rows, weights, filled);
+  SPR_LAUNCHED("probe_select_kernel");
+  return SPR_OK;
+}
+
+// base [bh, n, d] (dtype 0 bf16 / 2 fp32), dense [bh, m, d] (dense_dtype 0/2), rows
+// int32 [bh, m] -> x_fit, dense_f, y_fit fp32 [bh, m, d].
+extern "C" int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense, int32_t dense_dtype,
+                                   const int32_t* rows, int64_t bh, int64_t n, int32_t m, int32_t d, float* x_fit,
+                                   float* dense_f, float* y_fit, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0 && m >= 0 && d >= 1, "spr_repair_fit_prep: bad size");
+  SPR_REQUIRE(bh <= 65535, "spr_repair_fit_prep: bh exceeds 65535");
+  if (bh == 0 || m == 0) return SPR_OK;
+  SPR_REQUIRE(base && dense && rows && x_fit && dense_f && y_fit, "spr_repair_fit_prep: null pointer");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(static_cast<int64_t>(m) * d, 256)), static_cast<uint32_t>(bh));
+#define SPR_FP(TB, TD)                                                                                          \
+  fit_prep_kernel<TB, TD><<<grid, 256, 0, stream>>>(static_cast<const TB*>(base), static_cast<const TD*>(dense), \
+                                                    rows, n, m, d, x_fit, dense_f, y_fit)
+  if (base_dtype == 0 && dense_dtype == 0) SPR_FP(uint16_t, uint16_t);
+  else if (base_dtype == 0 && dense_dtype == 2) SPR_FP(uint16_t, float);
+  else if (base_dtype == 2 && dense_dtype == 0) SPR_FP(float, uint16_t);
+  else if (base_dtype == 2 && dense_dtype == 2) SPR_FP(float, float);
+  else SPR_REQUIRE(false, "spr_repair_fit_prep: unsupported dtypes");
+#undef SPR_FP
+  SPR_LAUNCHED("fit_prep_kernel");
+  return SPR_OK;
+}
+
+// bf16 base/out [bh, n, d]; x_mean, x_scale, y_mean fp32 [bh, d]; left,
+// basis fp32 [bh, d, rank]; d in {64, 128}, rank 16.
+extern "C" int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
+                                const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
+                                float alpha, float norm_cap, void* out, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0, "spr_repair_apply: bad size");
+  SPR_REQUIRE((d == 128 || d == 64) && rank == 16, "spr_repair_apply: requires D in {64, 128}, rank=16 (got %d, %d)",
+              d, rank);
+  SPR_REQUIRE(bh <= 65535, "spr_repair_apply: bh exceeds 65535");
+  if (bh == 0 || n == 0) return SPR_OK;
+  SPR_REQUIRE(base && x_mean && x_scale && y_mean && left && basis && out, "spr_repair_apply: null pointer");
+  SPR_REQUIRE(reinterpret_cast<uintptr_t>(base) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
+              "spr_repair_apply: base/out must be 16-byte aligned");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
+  if (d == 128) {
+    repair_apply_kernel<128, 16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
+                                                           y_mean, left, basis, n, alpha, norm_cap,
+                                                           static_cast<uint16_t*>(out));
+  } else {
+    repair_apply_kernel<64, 16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
+                                                          y_mean, left, basis, n, alpha, norm_cap,
+                                                          static_cast<uint16_t*>(out));
+  }
+  SPR_LAUNCHED("repair_apply_kernel");
+  return SPR_OK;
+}
+
+// out bf16 [bh, n, d]; out[b, rows[b, j]] = dense[b, j] (dense_dtype 0 bf16 / 2 fp32).
+extern "C" int spr_probe_scatter(const void* dense, int32_t dense_dtype, const int32_t* rows, int64_t bh, int64_t n,
+                                 int32_t m, int32_t d, void* out, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0 && m >= 0 && d >= 1, "spr_probe_scatter: bad size");
+  SPR_REQUIRE(bh <= 65535, "spr_probe_scatter: bh exceeds 65535");
+  if (bh == 0 || m == 0) return SPR_OK;
+  SPR_REQUIRE(dense && rows && out, "spr_probe_scatter: null pointer");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(static_cast<int64_t>(m) * d, 256)), static_cast<uint32_t>(bh));
+  if (dense_dtype == 0) {
+    probe_scatter_kernel<uint16_t><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(dense), rows, n, m, d,
+                                                             static_cast<uint16_t*>(out));
+  } else if (dense_dtype == 2) {
+    probe_scatter_kernel<float><<<grid, 256, 0, stream>>>(static_cast<const float*>(dense), rows, n, m, d,
+                                                          static_cast<uint16_t*>(out));
+  } else {
+    SPR_REQUIRE(false, "spr_probe_scatter: unsupported dense dtype %d", dense_dtype);
+  }
+  SPR_LAUNCHED("probe_scatter_kernel");
+  return SPR_OK;
+}

@@ -1,0 +1,165 @@
+"""One SparsePR attention layer on the MI355X kernels: the hot path end to end.
+
+Composition (reference call sites):
+  route   : flash k-means of Q and of K (Lloyd, fixed iterations), top-p
+            cluster-pair map, K/V permutation  -- wan22.py:2221-2258 (SAP route),
+            n8_v6.py:905-925 (K/V permute)
+  attend  : Q permutation, block-sparse attention over the kept cluster pairs,
+            inverse permutation                -- hunyuanvideo.py:189-231
+  repair  : N8 probe repair of the dropped blocks -- n8_v6.py:1174-1444
+            (probes are role-equal representatives of the Q clusters; with the
+            top-p route the role features are the queries themselves)
+
+Every stage is a HIP kernel of libsparsepr_hip.so; the only non-HIP compute is
+the small fp32 RRR fit (torch.linalg on the GPU).  Nothing here synchronises
+the host.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from .flash_kmeans.kmeans_impl import X_SQ_BF16, gather_rows, lloyd
+from .kernels.attention import block_sparse_attention, plan_block_sparse
+from .kernels.selection import density, topp_map
+from .n8_v6 import N8V6Config, N8V6Core, N8V6Route
+from .synthetic import first_k_indices
+
+
+@dataclass(frozen=True)
+class SparsePRConfig:
+    num_q_centroids: int = 128
+    num_k_centroids: int = 512
+    kmeans_iters: int = 5
+    top_p: float = 0.9
+    min_kc_ratio: float = 0.0
+    probe_rows: int = 128
+    repair: bool = True
+    repair_rank: int = 16
+    repair_ridge: float = 0.1
+    repair_alpha: float = 1.0
+    repair_norm_cap: float = 0.0
+    init_seed: int = 0
+    x_sq_mode: int = X_SQ_BF16
+
+
+@dataclass
+class LayerTimings:
+    """Optional per-stage HIP events (recorded on the current stream)."""
+    events: dict = field(default_factory=dict)
+
+    def mark(self, name: str):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.events[name] = ev
+
+    def ms(self, a: str, b: str) -> float:
+        return self.events[a].elapsed_time(self.events[b])
+
+
+class SparsePRAttention:
+    """Stateless across calls except the repair core's last finite RRR state."""
+
+    def __init__(self, config: SparsePRConfig = SparsePRConfig()):
+        self.config = config
+        n8cfg = N8V6Config(num_q_centroids=config.num_q_centroids, num_k_centroids=config.num_k_centroids,
+                           probe_rows=config.probe_rows, repair_rank=config.repair_rank,
+                           repair_ridge=config.repair_ridge, repair_alpha=config.repair_alpha,
+                           repair_norm_cap=config.repair_norm_cap)
+        self.n8 = N8V6Core(n8cfg, validate=False)
+        self._init_idx: dict = {}
+
+    def _init_centroids(self, x: torch.Tensor, k: int, seed: int) -> torch.Tensor:
+        bh, n, _ = x.shape
+        key = (n, k, seed, x.device)
+        idx = self._init_idx.get(key)
+        if idx is None:
+            idx = first_k_indices(n, k, seed).to(torch.int32).to(x.device)
+            self._init_idx[key] = idx
+        return gather_rows(x, idx.unsqueeze(0).expand(bh, -1))
+
+    def route(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, timings: LayerTimings | None = None):
+        """q, k, v [B, H, N, D] bf16 -> (N8V6Route, q sorted indices)."""
+        cfg = self.config
+        _lib.require_gpu(q, k, v, what="SparsePRAttention")
+        B, H, N, D = q.shape
+        bh = B * H
+        qf = q.reshape(bh, N, D).contiguous()
+        kf = k.reshape(bh, N, D).contiguous()
+        vf = v.reshape(bh, N, D).contiguous()
+        qres = lloyd(qf, cfg.num_q_centroids, cfg.kmeans_iters, 0.0,
+                     self._init_centroids(qf, cfg.num_q_centroids, cfg.init_seed),
+                     x_sq_mode=cfg.x_sq_mode, want_mean32=True)
+        kres = lloyd(kf, cfg.num_k_centroids, cfg.kmeans_iters, 0.0,
+                     self._init_centroids(kf, cfg.num_k_centroids, cfg.init_seed + 1), x_sq_mode=cfg.x_sq_mode)
+        if timings is not None:
+            timings.mark("kmeans")
+        self.last_centroids = (qres.centroids, kres.centroids)
+        dmap = topp_map(qres.centroids, kres.centroids, kres.sizes, cfg.top_p, cfg.min_kc_ratio)
+        if timings is not None:
+            timings.mark("select")
+        from .kernels.permute import permute_tensor_by_labels_triton
+
+        k_perm, _ = permute_tensor_by_labels_triton(k, None, 2, sorted_indices=kres.sorted_idx)
+        v_perm, _ = permute_tensor_by_labels_triton(v, None, 2, sorted_indices=kres.sorted_idx)
+        dens = density(dmap, qres.sizes, kres.sizes)
+        route = N8V6Route(
+            q_labels=qres.labels, k_labels=kres.labels, q_cluster_sizes=qres.sizes, k_cluster_sizes=kres.sizes,
+            video_dynamic_map=dmap, q_role_features=qf, k_permuted=k_perm, v_permuted=v_perm,
+            k_sorted_indices=kres.sorted_idx, base_video_density=dens, q_kmeans_iters=qres.iters,
+            k_kmeans_iters=kres.iters, q_role_centers=qres.mean32)
+        return route, qres.sorted_idx
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, timings: LayerTimings | None = None):
+        """Sparse attention output [B, H, N, D] bf16 (with repair unless disabled)."""
+        cfg = self.config
+        B, H, N, D = q.shape
+        bh = B * H
+        if timings is not None:
+            timings.mark("start")
+        route, q_idx = self.route(q, k, v, timings)
+        from .kernels.permute import apply_inverse_permutation_triton, permute_tensor_by_labels_triton
+
+        q_perm, _ = permute_tensor_by_labels_triton(q, None, 2, sorted_indices=q_idx)
+        if timings is not None:
+            timings.mark("permute")
+        plan = plan_block_sparse(route.video_dynamic_map, route.q_cluster_sizes, route.k_cluster_sizes, N)
+        if timings is not None:
+            timings.mark("plan")
+        o_perm = block_sparse_attention(q_perm.reshape(bh, N, D), route.k_permuted.reshape(bh, N, D),
+                                        route.v_permuted.reshape(bh, N, D), route.video_dynamic_map,
+                                        route.q_cluster_sizes, route.k_cluster_sizes, plan=plan)
+        if timings is not None:
+            timings.mark("attention")
+        base = apply_inverse_permutation_triton(o_perm.view(B, H, N, D), q_idx, 2)
+        if timings is not None:
+            timings.mark("unpermute")
+        self.last_route = route
+        if not cfg.repair:
+            return base
+        out, info = self.n8.repair(base, q, k, v, route)
+        self.last_repair_info = info
+        if timings is not None:
+            timings.mark("repair")
+        return out
+
+    __call__ = forward
+
+
+def kept_pair_flops(route: N8V6Route, head_dim: int) -> torch.Tensor:
+    """Executed attention flops: 4 * D * sum over kept (a, c) of |Q_a| |K_c| (device scalar)."""
+    qs = route.q_cluster_sizes.to(torch.float64)
+    ks = route.k_cluster_sizes.to(torch.float64)
+    m = route.video_dynamic_map.to(torch.float64)
+    pairs = torch.einsum("hq,hqk,hk->", qs, m, ks)
+    return 4.0 * head_dim * pairs
+
+
+def dense_flops(heads: int, tokens: int, head_dim: int) -> float:
+    return 4.0 * heads * tokens * tokens * head_dim
+
+
+__all__ = ["SparsePRAttention", "SparsePRConfig", "LayerTimings", "kept_pair_flops", "dense_flops"]

@@ -24,7 +24,7 @@ def _cos(a, b):
 
 def _sizes(rng, n, total, empty_every=0):
     w = rng.random(n) + 0.05
-    if empty_every:
+    if empty_every and n > empty_every:
         w[::empty_every] = 0.0
     s = np.floor(w / w.sum() * total).astype(np.int64)
     s[np.argmax(w)] += total - s.sum()
@@ -38,7 +38,7 @@ def _problem(oracle, rng, B, Hq, Hkv, S, D, qn, kn, density=0.3, empty_row=True,
     qs = np.stack([[_sizes(rng, qn, S, 5) for _ in range(Hkv)] for _ in range(B)])
     ks = np.stack([[_sizes(rng, kn, S, 7) for _ in range(Hkv)] for _ in range(B)])
     m = rng.random((B, Hkv, qn, kn)) < density
-    if empty_row:
+    if empty_row and qn > 1:
         m[..., 1, :] = False
     return q, k, v, m, qs, ks
 

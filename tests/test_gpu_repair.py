@@ -1,0 +1,116 @@
+"""GPU parity: probe selection (bit-exact rows, weights), fit preparation,
+repair apply (vs float64 closed form), exact probe scatter, RRR fit vs the
+float64 oracle, non-finite recovery, N8V6Core.repair end to end."""
+
+import numpy as np
+import pytest
+import torch
+
+from tests._helpers import to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _probe_data(oracle, rng, bh=3, n=4000, r=128, c=40, empty=(5,)):
+    f = oracle.to_bf16(rng.standard_normal((bh, n, r)).astype(np.float32))
+    labels = rng.integers(0, c, (bh, n)).astype(np.int32)
+    for e in empty:
+        labels[labels == e] = (e + 1) % c
+    return f, labels
+
+
+@pytest.mark.parametrize("r", [64, 128])
+def test_vectorized_probes_bit_exact(dev, oracle, r):
+    from sparsepr_amd.residual_repair import select_role_equal_probes_vectorized
+
+    rng = np.random.default_rng(r)
+    f, labels = _probe_data(oracle, rng, r=r)
+    f[0, 100] = f[0, 7]
+    labels[0, 100] = labels[0, 7]  # exact distance tie: lower token wins
+    for count in (16, 39, 40):  # 40 > non-empty groups (39): fallback slots
+        rows, w = select_role_equal_probes_vectorized(to_dev(f, dev, torch.bfloat16), to_dev(labels, dev),
+                                                      num_clusters=40, rows=count)
+        rr, rw = oracle.select_role_equal_probes_vectorized(f, labels, 40, count)
+        assert rows.dtype == torch.int64 and (rows.cpu().numpy() == rr).all()
+        assert np.allclose(w.cpu().numpy(), rw, rtol=1e-6)
+
+
+def test_round_probes_and_first_token(dev, oracle):
+    from sparsepr_amd.residual_repair import select_first_token_largest_groups, select_role_equal_probes
+
+    rng = np.random.default_rng(3)
+    f, labels = _probe_data(oracle, rng, n=600, c=12, empty=(2,))
+    labels[1, :] = np.where(labels[1] == 3, 4, labels[1])
+    labels[1, 50] = 3  # a single-member group: exhausted after the first round
+    rows, w = select_role_equal_probes(to_dev(f, dev, torch.bfloat16), to_dev(labels, dev), num_clusters=12, rows=40)
+    rr, rw = oracle.select_role_equal_probes(f, labels, 12, 40)
+    assert (rows.cpu().numpy() == rr).all()
+    assert np.allclose(w.cpu().numpy(), rw, rtol=1e-6)
+    rows, w = select_first_token_largest_groups(to_dev(f, dev, torch.bfloat16), to_dev(labels, dev),
+                                                num_clusters=12, rows=8)
+    rr, rw = oracle.select_first_token_largest_groups(labels, 12, 8)
+    assert (rows.cpu().numpy() == rr).all() and np.allclose(w.cpu().numpy(), rw, rtol=1e-6)
+
+
+def test_fit_prep_apply_scatter(dev, oracle):
+    from sparsepr_amd.kernels.residual_repair import (n8_exact_probe_scatter_triton,
+                                                      n8_prepare_output_repair_fit_triton,
+                                                      n8_repair_apply_output_triton)
+
+    rng = np.random.default_rng(5)
+    bh, n, d, m = 3, 3000, 128, 64
+    base = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    dense = oracle.to_bf16(rng.standard_normal((bh, m, d)).astype(np.float32))
+    rows = np.stack([rng.choice(n, m, replace=False) for _ in range(bh)])
+    bt = to_dev(base, dev, torch.bfloat16)
+    bufs = [torch.empty((bh, m, d), device=dev) for _ in range(3)]
+    xf, df, yf = n8_prepare_output_repair_fit_triton(bt, to_dev(dense, dev, torch.bfloat16), to_dev(rows, dev), *bufs)
+    ref_x = np.take_along_axis(base, rows[..., None], 1)
+    assert (xf.cpu().numpy() == ref_x).all() and (df.cpu().numpy() == dense).all()
+    assert (yf.cpu().numpy() == (dense - ref_x)).all()
+    w = rng.uniform(0.5, 2, (bh, m)).astype(np.float32)
+    state = oracle.fit_reduced_rank_residual(ref_x, dense - ref_x, 16, 0.1, w, dtype=np.float64)
+    st = [to_dev(s.astype(np.float32), dev) for s in state]
+    for cap in (0.0, 0.05):
+        out = n8_repair_apply_output_triton(bt, *st, 0.7, cap)
+        ref = oracle.repair_apply(base, *[s.astype(np.float32) for s in state], 0.7, cap)
+        assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
+    out = n8_repair_apply_output_triton(bt, *st, 1.0, 0.0)
+    n8_exact_probe_scatter_triton(out, to_dev(rows, dev), df)
+    o = out.float().cpu().numpy()
+    for h in range(bh):
+        assert (o[h, rows[h]] == dense[h]).all()
+
+
+@pytest.mark.parametrize("m,p", [(128, 128), (64, 128), (64, 64)])
+def test_rrr_fit_matches_float64(dev, oracle, m, p):
+    from sparsepr_amd.residual_repair import fit_reduced_rank_residual
+
+    rng = np.random.default_rng(m + p)
+    x = rng.standard_normal((4, m, p)).astype(np.float32)
+    y = (x @ rng.standard_normal((4, p, p)).astype(np.float32) * 0.05
+         + 0.02 * rng.standard_normal((4, m, p)).astype(np.float32))
+    w = rng.uniform(0.5, 2.0, (4, m)).astype(np.float32)
+    got = fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=16, ridge=0.1, weights=to_dev(w, dev),
+                                    output_basis_backend="skinny", fit_backend="dual_cholesky",
+                                    decomposition_backend="eigh", basis_source="raw_residual")
+    ref = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w)
+    for g, r in zip(got[:3], ref[:3]):
+        assert np.allclose(g.cpu().numpy(), r, rtol=1e-4, atol=1e-5)
+    # left basis^T is the basis-independent part of the fitted map
+    gl = (got[3] @ got[4].transpose(1, 2)).cpu().numpy()
+    rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
+    assert np.allclose(gl, rl, rtol=2e-3, atol=2e-4)
+
+
+def test_recover_nonfinite_state_gpu(dev):
+    from sparsepr_amd.residual_repair import recover_nonfinite_rrr_state
+
+    st = tuple(torch.randn(3, 4, 5, device=dev) for _ in range(5))
+    bad = tuple(t.clone() for t in st)
+    bad[2][1, 0, 0] = float("nan")
+    sel, mask, policy = recover_nonfinite_rrr_state(bad, None)
+    assert mask.cpu().tolist() == [False, True, False] and policy.startswith("zero")
+    assert (sel[1][1] == 1).all() and (sel[3][1] == 0).all() and torch.equal(sel[3][0], st[3][0])
+    sel, mask, policy = recover_nonfinite_rrr_state(bad, st)
+    assert torch.equal(sel[2][1], st[2][1]) and policy.startswith("reuse")
