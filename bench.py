@@ -1,0 +1,174 @@
+#!/usr/bin/env python3
+"""Benchmark: one SparsePR attention layer at the HunyuanVideo shape on one MI355X.
+
+Workload: batch 1, 24 heads, 118,800 tokens (33 x 45 x 80),
+head_dim 128, bf16; flash k-means with 128 Q-clusters and 512 K-clusters
+(5 Lloyd iterations, seeded first-k init), top-p 0.9 cluster-pair selection,
+block-sparse attention, N8 repair with 128 probes.  Synthetic frame-correlated
+Gaussian-mixture Q/K/V (400 components), generated on the device before timing.
+
+One step = one full layer call (route + attention + repair) on inputs resident
+in HBM.  Prints ONE JSON line.  `roofline` describes the dominant kernel (the
+block-sparse attention, MFMA-bound): algorithmic flops = 4 * D * sum of kept
+|Q_a| * |K_c| pairs, divided by the kernel's average duration measured with HIP
+events around its launch on the stream it runs on.  `cpu_baseline` times the
+CPU oracle (numpy, the reference algorithm restated) on a bounded sample
+(the first head of the same inputs), scaled to ms per layer.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "SparsePR attn ms/layer + % MFMA/HBM roofline at 118,800-token video shape"
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBS = 8000.0
+GEN = dict(seed=0, amp=2.3, qk_corr=0.1, step_std=0.1, noise_std=0.3)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--top-p", type=float, default=0.9)
+    ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
+    ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def traffic_from_profiles():
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary, if any."""
+    f = ROOT / "profiles" / "attention_c4_hbm_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return float(json.loads(f.read_text())["bytes_per_launch"])
+    except Exception:
+        return None
+
+
+def cpu_baseline(q, k, v, cfg, heads: int):
+    """Time the CPU oracle's layer on `heads` heads of the same inputs."""
+    import numpy as np
+
+    from oracle import sparsepr_oracle as orc
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    qn = q[0, :heads].float().cpu().numpy()
+    kn = k[0, :heads].float().cpu().numpy()
+    vn = v[0, :heads].float().cpu().numpy()
+    ocfg = orc.LayerConfig(q_clusters=cfg.num_q_centroids, k_clusters=cfg.num_k_centroids,
+                           kmeans_iters=cfg.kmeans_iters, top_p=cfg.top_p, probes=cfg.probe_rows,
+                           init_seed=cfg.init_seed)
+    stages: dict = {}
+    t0 = time.perf_counter()
+    orc.sparsepr_layer(qn, kn, vn, ocfg, timings=stages)
+    secs = time.perf_counter() - t0
+    total_heads = q.shape[1]
+    return {
+        "value": round(secs * 1e3 * total_heads / heads, 1),
+        "unit": "ms/layer",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"CPU oracle (numpy restatement: k-means, top-p map, loop-faithful block-sparse attention, "
+                   f"N8 repair) on {heads} of {total_heads} heads of the same inputs, {secs:.1f} s, scaled x"
+                   f"{total_heads / heads:g}; stage ms: " + ", ".join(f"{k}={v:.0f}" for k, v in stages.items())),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards by head with no "
+              "communication, see the design notes.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.layer import LayerTimings, SparsePRAttention, SparsePRConfig, dense_flops, kept_pair_flops
+
+    torch.cuda.set_device(0)
+    shape = synthetic.HUNYUAN
+    q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **GEN)
+    cfg = SparsePRConfig(num_q_centroids=128, num_k_centroids=512, kmeans_iters=5, top_p=args.top_p,
+                         probe_rows=128, repair=not args.no_repair)
+    layer = SparsePRAttention(cfg)
+    for _ in range(args.warmup):
+        layer(q, k, v)
+    torch.cuda.synchronize()
+
+    marks = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tm = LayerTimings()
+        layer(q, k, v, timings=tm)
+        marks.append(tm)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    names = list(marks[0].events)
+    stage_ms = {b: round(sum(m.ms(a, b) for m in marks) / len(marks), 3) for a, b in zip(names[:-1], names[1:])}
+    attn_ms = sum(m.ms("plan", "attention") for m in marks) / len(marks)
+    route = layer.last_route
+    kept = float(kept_pair_flops(route, shape.dim).item())
+    dens = float(route.base_video_density.item())
+    achieved = kept / (attn_ms * 1e-3) / 1e12
+    traffic = traffic_from_profiles()
+
+    result = {
+        "metric": METRIC,
+        "value": round(ms_per_step, 3),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (frame-correlated Gaussian mixture, seeded, generated on device)",
+        "config": {
+            "workload": "C4 HunyuanVideo-shaped SparsePR layer: 1x24x118800x128 bf16, Qc=128, Kc=512, "
+                        f"5 Lloyd iters, top-p {args.top_p}, " + ("no repair" if args.no_repair else "128 probes"),
+            "heads": shape.heads, "tokens": shape.tokens, "head_dim": shape.dim,
+            "kept_pair_density": round(dens, 4),
+            "kept_attention_tflop": round(kept / 1e12, 3),
+            "dense_attention_tflop": round(dense_flops(shape.heads, shape.tokens, shape.dim) / 1e12, 1),
+            "generator": GEN,
+        },
+        "stages_ms": stage_ms,
+        "roofline": {
+            "kernel": "attn_fwd_kernel<128,0> (block-sparse attention)",
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel_ms": round(attn_ms, 3),
+        },
+    }
+    if not args.no_cpu_baseline and args.cpu_heads > 0:
+        result["cpu_baseline"] = cpu_baseline(q, k, v, cfg, args.cpu_heads)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

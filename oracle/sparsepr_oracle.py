@@ -131,7 +131,7 @@ def kmeans_assign(x: np.ndarray, c: np.ndarray, x_sq: np.ndarray):
     x64 = x.astype(np.float64)
     c64 = c.astype(np.float64)
     c_sq = (c64 * c64).sum(-1).astype(np.float32).astype(np.float64)
-    cross = np.einsum("bnd,bkd->bnk", x64, c64)
+    cross = np.matmul(x64, np.swapaxes(c64, 1, 2))
     dist = x_sq.astype(np.float64)[:, :, None] + c_sq[:, None, :] - 2.0 * cross
     dist = np.maximum(dist, 0.0)
     labels = np.argmin(dist, axis=-1).astype(np.int32)  # numpy returns the first minimum
@@ -157,6 +157,13 @@ def label_mismatches_are_ties(labels_gpu, labels_ref, dist, x_sq, c, rel_tol):
     return bool(ok.all()), int(bad.sum())
 
 
+def _group_sums(x2: np.ndarray, labels1: np.ndarray, k: int) -> np.ndarray:
+    """Per-group float64 column sums of x2 [N, D] (exact for bf16-valued data)."""
+    lab = labels1.astype(np.int64)
+    x64 = x2.astype(np.float64)
+    return np.stack([np.bincount(lab, weights=x64[:, d], minlength=k) for d in range(x64.shape[1])], axis=1)
+
+
 def centroid_update(x: np.ndarray, labels: np.ndarray, old: np.ndarray, out_bf16: bool):
     """Cluster means; empty clusters keep the old centroid.
 
@@ -169,7 +176,7 @@ def centroid_update(x: np.ndarray, labels: np.ndarray, old: np.ndarray, out_bf16
     sums = np.zeros((B, K, D), np.float64)
     counts = np.zeros((B, K), np.int64)
     for b in range(B):
-        np.add.at(sums[b], labels[b].astype(np.int64), x[b].astype(np.float64))
+        sums[b] = _group_sums(x[b], labels[b], K)
         counts[b] = np.bincount(labels[b], minlength=K)
     mean32 = (sums / np.maximum(counts, 1)[:, :, None]).astype(np.float32)
     mean32 = np.where(counts[:, :, None] == 0, old.astype(np.float32), mean32)
@@ -471,8 +478,7 @@ def _probe_distances(features, labels, num_clusters):
     centers = np.zeros((bh, num_clusters, r), np.float32)
     for h in range(bh):
         sizes[h] = np.bincount(labels[h], minlength=num_clusters)
-        s = np.zeros((num_clusters, r), np.float64)
-        np.add.at(s, labels[h].astype(np.int64), f[h].astype(np.float64))
+        s = _group_sums(f[h], labels[h], num_clusters)
         centers[h] = (s / np.maximum(sizes[h], 1)[:, None]).astype(np.float32)
     dist = np.zeros((bh, n), np.float32)
     gathered = np.take_along_axis(centers, labels[..., None].astype(np.int64), 1)

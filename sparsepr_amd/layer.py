@@ -105,7 +105,7 @@ class SparsePRAttention:
 
         k_perm, _ = permute_tensor_by_labels_triton(k, None, 2, sorted_indices=kres.sorted_idx)
         v_perm, _ = permute_tensor_by_labels_triton(v, None, 2, sorted_indices=kres.sorted_idx)
-        dens = density(dmap, qres.sizes, kres.sizes)
+        dens = density(dmap, qres.sizes, kres.sizes).mean()  # device scalar: no host sync
         route = N8V6Route(
             q_labels=qres.labels, k_labels=kres.labels, q_cluster_sizes=qres.sizes, k_cluster_sizes=kres.sizes,
             video_dynamic_map=dmap, q_role_features=qf, k_permuted=k_perm, v_permuted=v_perm,

@@ -53,6 +53,13 @@ def _svg_top_p_key_budgets(q_centroids, k_centroids, k_cluster_sizes, top_p):
     return (sorted_sizes * keep.long()).sum(dim=2)
 
 
+def _effective_density(base_density, count: int, tokens: int):
+    """min(1, base + M / N); a device-tensor density stays on the device (no sync)."""
+    if torch.is_tensor(base_density):
+        return (base_density + count / float(tokens)).clamp(max=1.0)
+    return min(1.0, base_density + count / float(tokens))
+
+
 @dataclass(frozen=True)
 class N8V6Config:
     """Immutable N8-V6 configuration (field names and defaults of n8_v6.py:233-349)."""
@@ -249,6 +256,6 @@ class N8V6Core:
             "repair_basis_source": cfg.repair_basis_source,
             "repair_backend": "hip_mi355x",
             "repair_recovery_policy": policy,
-            "effective_video_density": min(1.0, route.base_video_density + count / float(tokens)),
+            "effective_video_density": _effective_density(route.base_video_density, count, tokens),
         }
         return corrected.view_as(base_video), info

@@ -3,10 +3,15 @@
 Tokens are laid out frame by frame.  Each head draws `components` mixture means
 ~N(0, amp^2 I); the means drift along the frame axis as a random walk with step
 std `step_std` per frame (frame-correlated video content).  Each token picks a
-component uniformly, and Q and K share the component means (so query and key
-clusters align, as they do for real video attention), while V uses its own
-means.  Token = mean + noise_std * N(0, I).  Everything is generated on the
-device from a seeded torch generator and stored as bf16.
+component uniformly.  Key means are correlated with the query means of the same
+component (correlation `qk_corr`), value means are independent.  Token = mean +
+noise_std * N(0, I).  Everything is generated on the device from a seeded torch
+generator and stored as bf16.
+
+amp sets the spread of cluster-level attention logits (about amp^2 in units of
+q.k/sqrt(D)) and qk_corr the extra logit of a key cluster of the query's own
+component (about qk_corr * amp^2 * sqrt(D)); together they set how much of the
+attention mass top-p has to keep.
 """
 
 from __future__ import annotations
@@ -38,19 +43,21 @@ CPU_SMALL = VideoShape(heads=2, frames=4, height=32, width=32, dim=64, component
 
 
 def frame_gmm_qkv(shape: VideoShape, *, seed: int = 0, amp: float = 0.3, step_std: float = 0.1,
-                  noise_std: float = 0.3, device="cuda", dtype=torch.bfloat16, heads: int | None = None):
+                  noise_std: float = 0.3, qk_corr: float = 1.0, device="cuda", dtype=torch.bfloat16,
+                  heads: int | None = None):
     """Returns q, k, v of shape [1, H, N, D] in `dtype` (H = `heads` or shape.heads)."""
     h = shape.heads if heads is None else heads
     n_frames, per_frame, d, c = shape.frames, shape.height * shape.width, shape.dim, shape.components
     g = torch.Generator(device=device)
     g.manual_seed(seed)
     outs = []
-    for which in range(2):  # 0: shared Q/K means, 1: V means
+    for which in range(3):  # Q means, independent part of K means, V means
         base = amp * torch.randn(h, 1, c, d, device=device, generator=g)
         steps = step_std * torch.randn(h, n_frames, c, d, device=device, generator=g)
         steps[:, 0] = 0.0
         outs.append(base + torch.cumsum(steps, dim=1))  # [H, F, C, D]
-    qk_means, v_means = outs
+    q_means, k_free, v_means = outs
+    k_means = qk_corr * q_means + (1.0 - qk_corr ** 2) ** 0.5 * k_free
     frame_of = torch.arange(n_frames, device=device).repeat_interleave(per_frame)  # [N]
 
     def draw(means):
@@ -59,8 +66,8 @@ def frame_gmm_qkv(shape: VideoShape, *, seed: int = 0, amp: float = 0.3, step_st
         mu = torch.gather(means.reshape(h, n_frames * c, d), 1, idx.unsqueeze(-1).expand(-1, -1, d))
         return (mu + noise_std * torch.randn(h, n_frames * per_frame, d, device=device, generator=g)).to(dtype)
 
-    q = draw(qk_means)
-    k = draw(qk_means)
+    q = draw(q_means)
+    k = draw(k_means)
     v = draw(v_means)
     return q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)
 

@@ -38,6 +38,7 @@ def _problem(oracle, rng, B, Hq, Hkv, S, D, qn, kn, density=0.3, empty_row=True,
     qs = np.stack([[_sizes(rng, qn, S, 5) for _ in range(Hkv)] for _ in range(B)])
     ks = np.stack([[_sizes(rng, kn, S, 7) for _ in range(Hkv)] for _ in range(B)])
     m = rng.random((B, Hkv, qn, kn)) < density
+    m[..., 0, 0] = True
     if empty_row and qn > 1:
         m[..., 1, :] = False
     return q, k, v, m, qs, ks
