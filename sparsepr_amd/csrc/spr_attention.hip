@@ -43,12 +43,25 @@ struct Seg {
   int32_t len;
 };
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Threshold (log2 units) by which a row maximum must grow before the running
+// output is rescaled; p = 2^(s - m) stays below 2^8 in between.
+constexpr float RESCALE_SLACK = 8.0f;
+
 template <int D>
 struct Tile {
   static constexpr int KSTEPS = D / 16;
   static constexpr int DBLK = D / 32;
   static constexpr int K_ROW = D * 2 + 16;   // bytes per key row of the K tile (+16 pad)
-  static constexpr int V_ROW = BN * 2 + 16;  // bytes per dim row of the V^T tile (+16 pad)
+  static constexpr int V_ROW = BN * 2 + 8;   // bytes per dim row of the V^T tile (+8 pad: 32 rows hit
+                                             // 32 distinct even banks, so 64-bit reads are conflict-free)
   static constexpr int K_BYTES = BN * K_ROW;
   static constexpr int V_BYTES = D * V_ROW;
   static constexpr int K_PIECES = BN * D / 8 / THREADS;       // 16-byte K pieces per thread
@@ -165,13 +178,16 @@ __device__ __forceinline__ void advance(int32_t& s, int32_t& base, int32_t targe
 }
 
 // MODE 0: block-sparse (plan), output normalised bf16 + optional lse.
+//         1-D grid; workgroup b runs on XCD b % 8 and takes logical tile
+//         (b % 8) * (gridDim.x / 8) + b / 8, so consecutive tiles (the tiles of
+//         one q-cluster, which read the same key blocks) share one XCD's L2.
 // MODE 1: dense split-key for probe rows: q rows [0, m) of a [BHq, m, D] tensor,
 //         keys [split * split_len, ...) of K/V; output unnormalised fp32 partials.
 template <int D, int MODE>
 __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
-    float scale_log2, uint16_t* __restrict__ out, float* __restrict__ lse,
+    int32_t bh_q, int32_t tiles_per_head, float scale_log2, uint16_t* __restrict__ out, float* __restrict__ lse,
     int32_t split_len, float* __restrict__ part_o, float* __restrict__ part_ml) {
   using T = Tile<D>;
   __shared__ __attribute__((aligned(16))) uint8_t k_tile[2][T::K_BYTES];
@@ -183,18 +199,21 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   const int wave = tid >> 6;
   const int col = lane & 31;
   const int half = lane >> 5;
-  const int64_t bhq = blockIdx.z;
-  const int64_t bhkv = bhq / group;
 
   // ---- work item
+  int64_t bhq;
   int32_t row0, row1;        // query rows of this tile: [row0, row1)
   const Seg* segs = nullptr;
   int32_t nseg = 0;
   int32_t total;
   int32_t dense_k0 = 0;
   if constexpr (MODE == 0) {
-    PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
-    const int32_t t = blockIdx.x;
+    const int64_t per_xcd = gridDim.x / 8;
+    const int64_t logical = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    bhq = logical / tiles_per_head;
+    const int32_t t = static_cast<int32_t>(logical - bhq * tiles_per_head);
+    if (bhq >= bh_q) return;
+    PlanView pv = plan_at(const_cast<int32_t*>(plan), bhq / group, qn, kn);
     if (t >= pv.tile_off[qn]) return;
     int lo = 0, hi = qn;  // largest i with tile_off[i] <= t
     while (hi - lo > 1) {
@@ -208,12 +227,14 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
     nseg = pv.nseg[qc];
     total = pv.total[qc];
   } else {
+    bhq = blockIdx.z;
     row0 = blockIdx.y * BM;
     row1 = min(row0 + BM, s_q);
     dense_k0 = blockIdx.x * split_len;
     const int32_t k1 = min(dense_k0 + split_len, s_kv);
     total = max(k1 - dense_k0, 0);
   }
+  const int64_t bhkv = bhq / group;
 
   const uint16_t* qb = q + bhq * static_cast<int64_t>(s_q) * D;
   const uint16_t* kb = k + bhkv * static_cast<int64_t>(s_kv) * D;
@@ -232,7 +253,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   spr::f32x16 o_acc[T::DBLK];
 #pragma unroll
   for (int b = 0; b < T::DBLK; ++b) o_acc[b] = spr::f32x16{};
-  float m_run = -__builtin_huge_valf();
+  float m_run = -__builtin_huge_valf();  // running max (log2 units, may lag the true max by < RESCALE_SLACK)
   float l_run = 0.0f;
 
   const int nch = (total + BN - 1) / BN;
@@ -294,9 +315,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
       const uint32_t b[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        // dims pc*8 + 2w (low halves) and pc*8 + 2w + 1 (high halves)
-        const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
-        const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
+        // dims pc*8 + 2w (low halves of a, b) and pc*8 + 2w + 1 (high halves)
+        const uint32_t lo = __builtin_amdgcn_perm(b[w], a[w], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(b[w], a[w], 0x07060302u);
         *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w) * T::V_ROW + rp * 4]) = lo;
         *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w + 1) * T::V_ROW + rp * 4]) = hi;
       }
@@ -317,7 +338,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
     if (c + 1 < nch) fetch(c + 1);
     if (c + 2 < nch) plan_chunk(c + 2);
 
-    // ---- S^T = K Q^T for two 32-key blocks
+    // ---- S^T = K Q^T for two 32-key blocks (raw, unscaled scores)
     spr::f32x16 s_acc[2];
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk) {
@@ -331,47 +352,53 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
       }
     }
 
+    // ---- keys past the end exist only in the last chunk
+    const int32_t left = total - c * BN;
+    if (left < BN) {
+#pragma unroll
+      for (int kbk = 0; kbk < 2; ++kbk) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kbk * 32 + 8 * (e / 4) + 4 * half + (e % 4);
+          if (key >= left) s_acc[kbk][e] = -__builtin_huge_valf();
+        }
+      }
+    }
+
     // ---- online softmax (log2 domain); a lane owns one query row
-    const int32_t left = total - c * BN;  // keys of this chunk that exist
     float mloc = -__builtin_huge_valf();
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = kbk * 32 + 8 * i + 4 * half + j;
-          float sv = s_acc[kbk][4 * i + j] * scale_log2;
-          if (key >= left) sv = -__builtin_huge_valf();
-          s_acc[kbk][4 * i + j] = sv;
-          mloc = fmaxf(mloc, sv);
-        }
-      }
+      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s_acc[kbk][e]);
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float m_new = fmaxf(m_run, mloc);
-    const float m_use = (m_new == -__builtin_huge_valf()) ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * scale_log2;
+    // Rescale lazily: only when some row's maximum grew by more than the slack.
+    if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
+      const float m_new = fmaxf(m_run, mloc);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < T::DBLK; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
+      }
+      m_run = m_new;
+    }
+    const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
     float lsum = 0.0f;
     uint32_t pf[4][4];  // P as bf16 pairs: [k-step][dword]
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk) {
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(s_acc[kbk][e] - m_use);
-        const float p1 = __builtin_amdgcn_exp2f(s_acc[kbk][e + 1] - m_use);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e], scale_log2, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e + 1], scale_log2, neg_m));
         lsum += p0 + p1;
-        const int t = kbk * 2 + e / 8;
-        pf[t][(e % 8) / 2] = spr::pack_bf16x2(p0, p1);
+        pf[kbk * 2 + e / 8][(e % 8) / 2] = pack2(p0, p1);
       }
     }
-    l_run = l_run * alpha + lsum;
-#pragma unroll
-    for (int b = 0; b < T::DBLK; ++b) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
-    }
+    l_run += lsum;
 
     // ---- O^T += V^T P^T
 #pragma unroll
@@ -404,8 +431,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
         for (int i = 0; i < 4; ++i) {
           const int d0 = b * 32 + 8 * i + 4 * half;
           uint2 w;
-          w.x = spr::pack_bf16x2(o_acc[b][4 * i] * inv, o_acc[b][4 * i + 1] * inv);
-          w.y = spr::pack_bf16x2(o_acc[b][4 * i + 2] * inv, o_acc[b][4 * i + 3] * inv);
+          w.x = pack2(o_acc[b][4 * i] * inv, o_acc[b][4 * i + 1] * inv);
+          w.y = pack2(o_acc[b][4 * i + 2] * inv, o_acc[b][4 * i + 3] * inv);
           *reinterpret_cast<uint2*>(orow + d0) = w;
         }
       }
@@ -467,8 +494,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   if (out_dtype == 0) {
     uint2 w;
-    w.x = spr::pack_bf16x2(acc[0] * inv, acc[1] * inv);
-    w.y = spr::pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    w.x = pack2(acc[0] * inv, acc[1] * inv);
+    w.y = pack2(acc[2] * inv, acc[3] * inv);
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + r * D + d0) = w;
   } else {
     *reinterpret_cast<spr::f32x4*>(static_cast<float*>(out) + r * D + d0) =
@@ -526,14 +553,17 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
                   reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
               "spr_block_sparse_attention_run: q/k/v/out must be 16-byte aligned");
   const int64_t max_tiles = spr::ceil_div(s, BM) + qn;
-  dim3 grid(static_cast<uint32_t>(max_tiles), 1, static_cast<uint32_t>(bh_q));
+  const int64_t blocks = spr::ceil_div(max_tiles * bh_q, 8) * 8;
+  SPR_REQUIRE(blocks < (int64_t(1) << 31), "spr_block_sparse_attention_run: too many tiles");
+  dim3 grid(static_cast<uint32_t>(blocks));
   const int32_t group = static_cast<int32_t>(bh_q / bh_kv);
   const float scale_log2 = scale * 1.4426950408889634f;
 #define SPR_ATTN(DD)                                                                                          \
   attn_fwd_kernel<DD, 0><<<grid, THREADS, 0, stream>>>(                                                      \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
-      scale_log2, static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr)
+      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, static_cast<uint16_t*>(out),  \
+      lse, 0, nullptr, nullptr)
   if (d == 128) {
     SPR_ATTN(128);
   } else {
@@ -594,16 +624,16 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
   if (d == 128) {
     attn_fwd_kernel<128, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-        static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, scale_log2, nullptr, nullptr,
-        split_len, part_o, part_ml);
+        static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
+        scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                           nsplit, out_dtype, out, lse);
   } else {
     attn_fwd_kernel<64, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-        static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, scale_log2, nullptr, nullptr,
-        split_len, part_o, part_ml);
+        static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
+        scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<64><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                          nsplit, out_dtype, out, lse);
