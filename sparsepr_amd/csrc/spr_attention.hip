@@ -38,10 +38,14 @@ constexpr int BM = 128;       // query rows per workgroup
 constexpr int BN = 64;        // keys per chunk
 constexpr int THREADS = 256;  // 4 waves
 
+// A kept key range as seen by the virtual key sequence of one q-cluster: virtual
+// positions [previous vend, vend) map to key rows delta + position.
 struct Seg {
-  int32_t start;
-  int32_t len;
+  int32_t delta;
+  int32_t vend;
 };
+
+constexpr int MAX_LDS_SEGS = 1024;  // segment lists up to this length are staged in LDS
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -141,10 +145,14 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
       const bool keep = c < kn && mrow[c] != 0 && len > 0;
       const uint64_t bits = __ballot(keep);
       const int pos = __popcll(bits & ((1ull << lane) - 1ull));
-      if (keep) out[count + pos] = Seg{start, len};
-      int32_t part = keep ? len : 0;
-      for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-      total += part;
+      int32_t incl = keep ? len : 0;  // inclusive scan of kept lengths over the wave
+      for (int o = 1; o < 64; o <<= 1) {
+        const int32_t up = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += up;
+      }
+      const int32_t vend = total + incl;
+      if (keep) out[count + pos] = Seg{start - (vend - len), vend};
+      total += __shfl(incl, 63, 64);
       count += __popcll(bits);
     }
     if (lane == 0) {
@@ -156,34 +164,13 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
 
 // ---------------------------------------------------------------------------- main kernel
 
-// Position `vpos` of the virtual key sequence formed by segments [s, nseg),
-// where segment s starts at virtual position `base`.  -1 past the end.
-__device__ __forceinline__ int32_t key_at(int32_t vpos, int32_t s, int32_t base, const Seg* segs, int32_t nseg) {
-  while (s < nseg) {
-    const Seg g = segs[s];
-    if (vpos < base + g.len) return g.start + (vpos - base);
-    base += g.len;
-    ++s;
-  }
-  return -1;
-}
-
-__device__ __forceinline__ void advance(int32_t& s, int32_t& base, int32_t target, const Seg* segs, int32_t nseg) {
-  while (s < nseg) {
-    const int32_t len = segs[s].len;
-    if (target < base + len) return;
-    base += len;
-    ++s;
-  }
-}
-
 // MODE 0: block-sparse (plan), output normalised bf16 + optional lse.
 //         1-D grid; workgroup b runs on XCD b % 8 and takes logical tile
 //         (b % 8) * (gridDim.x / 8) + b / 8, so consecutive tiles (the tiles of
 //         one q-cluster, which read the same key blocks) share one XCD's L2.
 // MODE 1: dense split-key for probe rows: q rows [0, m) of a [BHq, m, D] tensor,
 //         keys [split * split_len, ...) of K/V; output unnormalised fp32 partials.
-template <int D, int MODE>
+template <int D, int MODE, bool SEGL>
 __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
@@ -193,6 +180,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t k_tile[2][T::K_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t v_tile[2][T::V_BYTES];
   __shared__ int32_t key_rows[3][BN];
+  __shared__ Seg seg_lds[SEGL ? MAX_LDS_SEGS : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -203,7 +191,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   // ---- work item
   int64_t bhq;
   int32_t row0, row1;        // query rows of this tile: [row0, row1)
-  const Seg* segs = nullptr;
+  const Seg* segs = nullptr;  // global copy of the segment list (MODE 0)
   int32_t nseg = 0;
   int32_t total;
   int32_t dense_k0 = 0;
@@ -239,6 +227,15 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   const uint16_t* qb = q + bhq * static_cast<int64_t>(s_q) * D;
   const uint16_t* kb = k + bhkv * static_cast<int64_t>(s_kv) * D;
   const uint16_t* vb = v + bhkv * static_cast<int64_t>(s_kv) * D;
+  // raw buffer views of this head's K and V: 32-bit offsets, reads past the end return 0
+  const int32_t kv_bytes = s_kv * D * 2;
+  const __amdgpu_buffer_rsrc_t k_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kb), 0, kv_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vb), 0, kv_bytes, 0x00020000);
+  if constexpr (MODE == 0 && SEGL) {
+    for (int i = tid; i < nseg; i += THREADS) seg_lds[i] = segs[i];
+  }
 
   // ---- this lane's query row, as MFMA B fragments over the head dim
   const int32_t my_row = row0 + wave * 32 + col;
@@ -258,59 +255,68 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
 
   const int nch = (total + BN - 1) / BN;
 
-  // wave 0 owns the segment cursor and writes the key row of every chunk position
-  int32_t cur_s = 0, cur_base = 0;
+  // Wave 0 writes the key row of every position of a chunk, two chunks ahead.
+  // Positions past the end repeat the last key (their scores are masked), so
+  // every load below is unconditional.
+  int32_t cur_s = 0;  // segment holding the first position of the next chunk to plan
+  auto seg_of = [&](int32_t vpos) {
+    int32_t s = cur_s;
+    if constexpr (SEGL) {
+      while (s < nseg - 1 && vpos >= seg_lds[s].vend) ++s;
+    } else {
+      while (s < nseg - 1 && vpos >= segs[s].vend) ++s;
+    }
+    return s;
+  };
   auto plan_chunk = [&](int c) {
     if (wave == 0) {
-      const int32_t vpos = c * BN + lane;
+      const int32_t vpos = min(c * BN + lane, total - 1);
       if constexpr (MODE == 0) {
-        key_rows[c % 3][lane] = (vpos < total) ? key_at(vpos, cur_s, cur_base, segs, nseg) : -1;
-        advance(cur_s, cur_base, (c + 1) * BN, segs, nseg);
+        const int32_t s = seg_of(vpos);
+        int32_t delta;
+        if constexpr (SEGL) delta = seg_lds[s].delta; else delta = segs[s].delta;
+        key_rows[c % 3][lane] = delta + vpos;
+        cur_s = __builtin_amdgcn_readlane(s, 63);
       } else {
-        key_rows[c % 3][lane] = (vpos < total) ? dense_k0 + vpos : -1;
+        key_rows[c % 3][lane] = dense_k0 + vpos;
       }
     }
   };
 
   u32x4 kreg[T::K_PIECES];
   u32x4 vreg[T::V_PAIRS][2];
+  auto bload = [](__amdgpu_buffer_rsrc_t r, int32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  };
   auto fetch = [&](int c) {
     const int32_t* kr = key_rows[c % 3];
 #pragma unroll
     for (int i = 0; i < T::K_PIECES; ++i) {
-      const int g = tid + i * THREADS;
-      const int r = g / (D / 8);
-      const int pc = g % (D / 8);
-      const int32_t key = kr[r];
-      kreg[i] = key >= 0 ? *reinterpret_cast<const u32x4*>(kb + static_cast<int64_t>(key) * D + pc * 8)
-                         : u32x4{0, 0, 0, 0};
+      const int r = tid / (D / 8) + i * (THREADS / (D / 8));
+      const int pc = tid % (D / 8);
+      kreg[i] = bload(k_rsrc, kr[r] * (D * 2) + pc * 16);
     }
+    const int rp = tid % (BN / 2);
+    const int32_t key0 = kr[2 * rp] * (D * 2);
+    const int32_t key1 = kr[2 * rp + 1] * (D * 2);
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
-      const int g = tid + i * THREADS;
-      const int rp = g % (BN / 2);
-      const int pc = g / (BN / 2);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int32_t key = kr[2 * rp + e];
-        vreg[i][e] = key >= 0 ? *reinterpret_cast<const u32x4*>(vb + static_cast<int64_t>(key) * D + pc * 8)
-                              : u32x4{0, 0, 0, 0};
-      }
+      const int pc = tid / (BN / 2) + i * (THREADS / (BN / 2));
+      vreg[i][0] = bload(v_rsrc, key0 + pc * 16);
+      vreg[i][1] = bload(v_rsrc, key1 + pc * 16);
     }
   };
   auto stash = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < T::K_PIECES; ++i) {
-      const int g = tid + i * THREADS;
-      const int r = g / (D / 8);
-      const int pc = g % (D / 8);
+      const int r = tid / (D / 8) + i * (THREADS / (D / 8));
+      const int pc = tid % (D / 8);
       *reinterpret_cast<u32x4*>(&k_tile[buf][r * T::K_ROW + pc * 16]) = kreg[i];
     }
+    const int rp = tid % (BN / 2);
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
-      const int g = tid + i * THREADS;
-      const int rp = g % (BN / 2);
-      const int pc = g / (BN / 2);
+      const int pc = tid / (BN / 2) + i * (THREADS / (BN / 2));
       const uint32_t a[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
       const uint32_t b[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
 #pragma unroll
@@ -325,6 +331,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   };
 
   if (nch > 0) {
+    if constexpr (MODE == 0 && SEGL) __syncthreads();  // staged segment list visible to wave 0
     plan_chunk(0);
     if (nch > 1) plan_chunk(1);
     __syncthreads();
@@ -386,7 +393,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
       m_run = m_new;
     }
     const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
-    float lsum = 0.0f;
+    // The row sum adds the bf16-rounded probabilities that also weight V.
+    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    float lsum0 = 0.0f, lsum1 = 0.0f;
     uint32_t pf[4][4];  // P as bf16 pairs: [k-step][dword]
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk) {
@@ -394,11 +403,16 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
       for (int e = 0; e < 16; e += 2) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e], scale_log2, neg_m));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e + 1], scale_log2, neg_m));
-        lsum += p0 + p1;
-        pf[kbk * 2 + e / 8][(e % 8) / 2] = pack2(p0, p1);
+        const uint32_t pk = pack2(p0, p1);
+        pf[kbk * 2 + e / 8][(e % 8) / 2] = pk;
+        if (e % 4 == 0) {
+          lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+        } else {
+          lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+        }
       }
     }
-    l_run += lsum;
+    l_run += lsum0 + lsum1;
 
     // ---- O^T += V^T P^T
 #pragma unroll
@@ -545,7 +559,7 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_block_sparse_attention_run: bh_q=%lld not a multiple of bh_kv=%lld",
               (long long)bh_q, (long long)bh_kv);
   SPR_REQUIRE(d == 64 || d == 128, "spr_block_sparse_attention_run: head dim %d not supported (64, 128)", d);
-  SPR_REQUIRE(s < (int64_t(1) << 31), "spr_block_sparse_attention_run: sequence too long");
+  SPR_REQUIRE(s * d * 2 < (int64_t(1) << 31), "spr_block_sparse_attention_run: a head of K/V exceeds 2 GiB");
   SPR_REQUIRE(bh_q <= 65535, "spr_block_sparse_attention_run: bh_q exceeds 65535");
   if (bh_q == 0 || s == 0) return SPR_OK;
   SPR_REQUIRE(q && k && v && plan && out, "spr_block_sparse_attention_run: null pointer");
@@ -558,16 +572,17 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   dim3 grid(static_cast<uint32_t>(blocks));
   const int32_t group = static_cast<int32_t>(bh_q / bh_kv);
   const float scale_log2 = scale * 1.4426950408889634f;
-#define SPR_ATTN(DD)                                                                                          \
-  attn_fwd_kernel<DD, 0><<<grid, THREADS, 0, stream>>>(                                                      \
+#define SPR_ATTN(DD, SL)                                                                                      \
+  attn_fwd_kernel<DD, 0, SL><<<grid, THREADS, 0, stream>>>(                                                  \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
       static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, static_cast<uint16_t*>(out),  \
       lse, 0, nullptr, nullptr)
+  const bool seg_lds = kn <= MAX_LDS_SEGS;
   if (d == 128) {
-    SPR_ATTN(128);
+    if (seg_lds) SPR_ATTN(128, true); else SPR_ATTN(128, false);
   } else {
-    SPR_ATTN(64);
+    if (seg_lds) SPR_ATTN(64, true); else SPR_ATTN(64, false);
   }
 #undef SPR_ATTN
   SPR_LAUNCHED("attn_fwd_kernel");
@@ -603,7 +618,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_dense_attention: bh_q not a multiple of bh_kv");
   SPR_REQUIRE(d == 64 || d == 128, "spr_dense_attention: head dim %d not supported (64, 128)", d);
   SPR_REQUIRE(out_dtype == 0 || out_dtype == 2, "spr_dense_attention: out_dtype must be 0 or 2");
-  SPR_REQUIRE(s_kv < (int64_t(1) << 31) && m < (int64_t(1) << 31), "spr_dense_attention: too long");
+  SPR_REQUIRE(s_kv * d * 2 < (int64_t(1) << 31) && m < (int64_t(1) << 31), "spr_dense_attention: too long");
   SPR_REQUIRE(bh_q <= 65535 && nsplit <= 65535, "spr_dense_attention: grid too large");
   if (bh_q == 0 || m == 0) return SPR_OK;
   SPR_REQUIRE(q && k && v && out && workspace, "spr_dense_attention: null pointer");
@@ -622,7 +637,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
   const int64_t rows_total = bh_q * m;
   const uint32_t cblocks = static_cast<uint32_t>(spr::ceil_div(rows_total * (d / 4), 256));
   if (d == 128) {
-    attn_fwd_kernel<128, 1><<<grid, THREADS, 0, stream>>>(
+    attn_fwd_kernel<128, 1, false><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
         scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
@@ -630,7 +645,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                           nsplit, out_dtype, out, lse);
   } else {
-    attn_fwd_kernel<64, 1><<<grid, THREADS, 0, stream>>>(
+    attn_fwd_kernel<64, 1, false><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
         scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
