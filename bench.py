@@ -43,6 +43,10 @@ def parse():
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["attention", "copy"], default=None,
+                    help="profiling aids: 'attention' routes once, then times only the block-sparse attention "
+                         "kernel for --steps launches; 'copy' runs --steps plain 512 MiB device copies (the "
+                         "calibration kernel for the HBM traffic counters)")
     return ap.parse_args()
 
 
@@ -91,12 +95,73 @@ def cpu_baseline(q, k, v, cfg, heads: int):
     }
 
 
+def only_copy(args):
+    """--steps device copies of 512 MiB (read 512 MiB + write 512 MiB per launch)."""
+    import torch
+
+    n = 256 * 1024 * 1024
+    src = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(json.dumps({"copy_bytes_per_launch": n * 2, "ms_per_copy": round(ms, 4),
+                      "gbs_read_plus_write": round(2 * n * 2 / ms / 1e6, 1)}), flush=True)
+
+
+def only_attention(args):
+    """Route the C4 inputs once, then time --steps launches of the block-sparse attention alone."""
+    import torch
+
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.kernels.attention import block_sparse_attention, plan_block_sparse
+    from sparsepr_amd.kernels.permute import permute_tensor_by_labels_triton
+    from sparsepr_amd.layer import SparsePRAttention, SparsePRConfig, kept_pair_flops
+
+    shape = synthetic.HUNYUAN
+    q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **GEN)
+    layer = SparsePRAttention(SparsePRConfig(top_p=args.top_p, repair=False))
+    route, q_idx = layer.route(q, k, v)
+    B, H, N, D = q.shape
+    qp, _ = permute_tensor_by_labels_triton(q, None, 2, sorted_indices=q_idx)
+    qp = qp.reshape(B * H, N, D)
+    kp = route.k_permuted.reshape(B * H, N, D)
+    vp = route.v_permuted.reshape(B * H, N, D)
+    plan = plan_block_sparse(route.video_dynamic_map, route.q_cluster_sizes, route.k_cluster_sizes, N)
+
+    def run():
+        return block_sparse_attention(qp, kp, vp, route.video_dynamic_map, route.q_cluster_sizes,
+                                      route.k_cluster_sizes, plan=plan)
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    flops = float(kept_pair_flops(route, D).item())
+    print(json.dumps({"kernel": "attn_fwd_kernel<128,0>", "ms_per_launch": round(ms, 3),
+                      "tflops": round(flops / ms / 1e9, 1), "frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+                      "density": round(float(route.base_video_density.item()), 4)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards by head with no "
               "communication, see the design notes.", file=sys.stderr)
         sys.exit(2)
+    if args.only == "copy":
+        return only_copy(args)
+    if args.only == "attention":
+        return only_attention(args)
     import torch
 
     from sparsepr_amd import synthetic

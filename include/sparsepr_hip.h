@@ -88,6 +88,102 @@ int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, c
 int spr_role_assign_fp32(const float* features, const float* centroids, int64_t batch, int64_t n, int32_t k,
                          int32_t d, int32_t* labels, float* best_dist, hipStream_t stream);
 
+/* ---------------------------------------------------------------- cluster-pair selection
+ * kmeans_utils.py:1710-1742 identify_dynamic_map (+ weighted_softmax :1698-1707),
+ * n8_v6.py:181-230 _svg_top_p_key_budgets.  One workgroup per (head, q-cluster) row:
+ *   s = fl(qc . kc) / sqrt_d (sequential fp32 dot), p = k_size * exp(s - max) / sum,
+ *   descending sort (index tie-break), sequential cumsum, keep ranks whose preceding
+ *   cumsum <= p (rank 0 always), then the min_kc_ratio floor (`preserve` ranks).
+ *   qc fp32 [bh, qn, d], kc fp32 [bh, kn, d], k_sizes int32 [bh, kn] -> map uint8
+ *   [bh, qn, kn].  score_bf16 = 1 rounds every intermediate the way bf16 tensors do in
+ *   torch (matmul output, scaled score, probabilities, cumsum); kn <= 4096. */
+int spr_topp_map(const float* qc, const float* kc, const int32_t* k_sizes, int64_t bh, int32_t qn, int32_t kn,
+                 int32_t d, float sqrt_d, float p, int32_t preserve, int32_t score_bf16, uint8_t* map,
+                 hipStream_t stream);
+/* n8_ops.cu:271-322,541-571 svg_ear_select_budget (mode 0) and the Triton / CPU selectors
+ * selector_budget.py:131-171, n8_v6.py:1088-1111 (mode 1: crossing at sorted position
+ * `count`); n8_ops.cu:573-638 svg_ear_select_budget_schedule when ids/counts are given.
+ *   scores fp32 [bh, qn, kn], sizes int32 [bh, kn], budgets int32 [bh, qn] ->
+ *   out uint8 [bh, qn + 1, kn + 1] (header row/column set as the reference);
+ *   ids int32 [bh, qn, kn] + counts int32 [bh, qn] (both or neither). */
+int spr_select_budget(const float* scores, const int32_t* sizes, const int32_t* budgets, int64_t bh, int32_t qn,
+                      int32_t kn, int32_t mode, uint8_t* out, int32_t* ids, int32_t* counts, hipStream_t stream);
+/* n8_ops.cu:324-355,609-638 compact_selected_clusters: ascending kept ids per mask row;
+ * entries past counts[row] are left unwritten (the reference returns them uninitialised).
+ *   mask uint8 [rows, kn] -> ids int32 [rows, kn], counts int32 [rows]. */
+int spr_compact_selected(const uint8_t* mask, int64_t rows, int32_t kn, int32_t* ids, int32_t* counts,
+                         hipStream_t stream);
+/* kmeans_utils.py:285-303 density_calculation:
+ *   out[h] = sum_ij map[h,i,j] qs[h,i] ks[h,j] / (sum_i qs[h,i] * sum_j ks[h,j]). */
+int spr_density(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, int64_t heads, int32_t qn,
+                int32_t kn, float* out, hipStream_t stream);
+
+/* ---------------------------------------------------------------- block-sparse attention
+ * kmeans_utils.py:2164-2350 dynamic_block_sparse_fwd_flashinfer (FlashInfer
+ * VariableBlockSparseAttentionWrapper.plan / .run), semantics of
+ * dynamic_block_sparse_fwd_torch kmeans_utils.py:1748-1841.
+ * Plan: per kv head, cluster offsets, 128-row query tiles and, per q-cluster, the kept
+ * non-empty key ranges.  map uint8 [bh_kv, qn, kn], q_sizes int32 [bh_kv, qn],
+ * k_sizes int32 [bh_kv, kn]; sizes are clamped to the s rows. */
+size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn, int32_t kn);
+int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_kv,
+                                    int64_t s, int32_t qn, int32_t kn, void* plan, size_t plan_bytes,
+                                    hipStream_t stream);
+/* q bf16 [bh_q, s, d], k/v bf16 [bh_kv, s, d] in cluster-contiguous order; bh_q a
+ * multiple of bh_kv (query head h uses kv head h / (bh_q / bh_kv)); d in {64, 128}.
+ * out bf16 [bh_q, s, d]: softmax over the kept keys of the row's q-cluster (scale
+ * applied to q.k); rows of empty q-clusters are 0.  lse fp32 [bh_q, s] (nullable,
+ * natural log of the scaled sum, -inf for an empty row). */
+int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan, int64_t bh_q,
+                                   int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
+                                   void* out, float* lse, hipStream_t stream);
+/* Plan + run in one call; workspace = plan buffer of spr_block_sparse_attention_workspace bytes. */
+int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,
+                               const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q, int64_t bh_kv, int64_t s,
+                               int32_t d, int32_t qn, int32_t kn, float scale, void* out, float* lse, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+/* n8_v6.py:1236-1243 dense probe attention (F.scaled_dot_product_attention of the probe
+ * rows against every key).  q bf16 [bh_q, m, d], k/v bf16 [bh_kv, s_kv, d]; keys split
+ * into nsplit ranges computed in parallel and merged; out [bh_q, m, d] (out_dtype 0 =
+ * bf16, 2 = fp32); lse fp32 [bh_q, m] nullable. */
+size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t d, int32_t nsplit);
+int spr_dense_attention(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv, int64_t m,
+                        int64_t s_kv, int32_t d, float scale, int32_t nsplit, void* out, int32_t out_dtype,
+                        float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------- N8 residual repair
+ * residual_repair.py:36-118 select_role_equal_probes(_vectorized), group distances:
+ *   dist[b, i] = sum_r (features[b, i, r] - centers[b, labels[b, i], r])^2 in fp32,
+ *   evaluated in index order (sub, mul, add).  features dtype 0 bf16 / 2 fp32, r in
+ *   {64, 128}; centers fp32 [bh, groups, r]; dist fp32 [bh, n]. */
+int spr_probe_distances(const void* features, int32_t dtype, const int32_t* labels, const float* centers, int64_t bh,
+                        int64_t n, int32_t groups, int32_t r, float* dist, hipStream_t stream);
+/* residual_repair.py:121-260 probe choice.  mode 0 = vectorized (one nearest token per
+ * group, largest groups first), 1 = rounds (select_role_equal_probes, more rows than
+ * groups), 2 = select_first_token_largest_groups.  rows int32 [bh, count], weights fp32
+ * [bh, count] (size / sampled, normalised to mean 1), filled int32 [bh] nullable.
+ * groups <= 2048. */
+int spr_probe_select(const float* dist, const int32_t* labels, const int32_t* sizes, int64_t bh, int64_t n,
+                     int32_t groups, int32_t count, int32_t mode, int32_t* rows, float* weights, int32_t* filled,
+                     hipStream_t stream);
+/* residual_repair.py:798-857 n8_prepare_output_repair_fit_triton:
+ *   x_fit = base[rows], dense_f = float(dense), y_fit = dense_f - x_fit (fp32 [bh, m, d]). */
+int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense, int32_t dense_dtype,
+                        const int32_t* rows, int64_t bh, int64_t n, int32_t m, int32_t d, float* x_fit,
+                        float* dense_f, float* y_fit, hipStream_t stream);
+/* residual_repair.py:478-562 n8_repair_apply_output_triton:
+ *   out = base + alpha * (((base - x_mean) / x_scale) . left . basis^T + y_mean), the
+ *   correction's row norm capped at norm_cap when norm_cap > 0.  base/out bf16
+ *   [bh, n, d]; x_mean, x_scale, y_mean fp32 [bh, d]; left, basis fp32 [bh, d, rank];
+ *   d in {64, 128}, rank 16. */
+int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
+                     const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
+                     float alpha, float norm_cap, void* out, hipStream_t stream);
+/* residual_repair.py:656-700 n8_exact_probe_scatter_triton: out[b, rows[b, j]] =
+ * dense[b, j] (rounded to bf16); dense dtype 0 bf16 / 2 fp32; rows outside [0, n) skipped. */
+int spr_probe_scatter(const void* dense, int32_t dense_dtype, const int32_t* rows, int64_t bh, int64_t n, int32_t m,
+                      int32_t d, void* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
