@@ -179,7 +179,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   using T = Tile<D>;
   __shared__ __attribute__((aligned(16))) uint8_t k_tile[2][T::K_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t v_tile[2][T::V_BYTES];
-  __shared__ int32_t key_rows[3][BN];
+  __shared__ int32_t key_rows[4][BN];
   __shared__ Seg seg_lds[SEGL ? MAX_LDS_SEGS : 1];
 
   const int tid = threadIdx.x;
@@ -255,9 +255,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
 
   const int nch = (total + BN - 1) / BN;
 
-  // Wave 0 writes the key row of every position of a chunk, two chunks ahead.
-  // Positions past the end repeat the last key (their scores are masked), so
-  // every load below is unconditional.
+  // Wave 0 writes the key row of every position of a chunk three chunks ahead
+  // (ring of 4); every thread reads the rows it loads one chunk before it loads
+  // them, so global loads issue without waiting on LDS.  Positions past the end
+  // repeat the last key (their scores are masked), so every load is unconditional.
   int32_t cur_s = 0;  // segment holding the first position of the next chunk to plan
   auto seg_of = [&](int32_t vpos) {
     int32_t s = cur_s;
@@ -275,10 +276,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
         const int32_t s = seg_of(vpos);
         int32_t delta;
         if constexpr (SEGL) delta = seg_lds[s].delta; else delta = segs[s].delta;
-        key_rows[c % 3][lane] = delta + vpos;
+        key_rows[c % 4][lane] = delta + vpos;
         cur_s = __builtin_amdgcn_readlane(s, 63);
       } else {
-        key_rows[c % 3][lane] = dense_k0 + vpos;
+        key_rows[c % 4][lane] = dense_k0 + vpos;
       }
     }
   };
@@ -288,22 +289,24 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   auto bload = [](__amdgpu_buffer_rsrc_t r, int32_t off) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   };
-  auto fetch = [&](int c) {
-    const int32_t* kr = key_rows[c % 3];
+  int32_t krow[T::K_PIECES];  // key rows of this thread's K pieces in the next chunk to fetch
+  int32_t vrow[2];              // key rows of this thread's two V rows
+  auto load_rows = [&](int c) {  // plain copies, so nothing waits on these reads until fetch()
+    const int32_t* kr = key_rows[c % 4];
 #pragma unroll
-    for (int i = 0; i < T::K_PIECES; ++i) {
-      const int r = tid / (D / 8) + i * (THREADS / (D / 8));
-      const int pc = tid % (D / 8);
-      kreg[i] = bload(k_rsrc, kr[r] * (D * 2) + pc * 16);
-    }
+    for (int i = 0; i < T::K_PIECES; ++i) krow[i] = kr[tid / (D / 8) + i * (THREADS / (D / 8))];
     const int rp = tid % (BN / 2);
-    const int32_t key0 = kr[2 * rp] * (D * 2);
-    const int32_t key1 = kr[2 * rp + 1] * (D * 2);
+    vrow[0] = kr[2 * rp];
+    vrow[1] = kr[2 * rp + 1];
+  };
+  auto fetch = [&]() {
+#pragma unroll
+    for (int i = 0; i < T::K_PIECES; ++i) kreg[i] = bload(k_rsrc, krow[i] * (D * 2) + (tid % (D / 8)) * 16);
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
       const int pc = tid / (BN / 2) + i * (THREADS / (BN / 2));
-      vreg[i][0] = bload(v_rsrc, key0 + pc * 16);
-      vreg[i][1] = bload(v_rsrc, key1 + pc * 16);
+      vreg[i][0] = bload(v_rsrc, vrow[0] * (D * 2) + pc * 16);
+      vreg[i][1] = bload(v_rsrc, vrow[1] * (D * 2) + pc * 16);
     }
   };
   auto stash = [&](int buf) {
@@ -334,16 +337,19 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
     if constexpr (MODE == 0 && SEGL) __syncthreads();  // staged segment list visible to wave 0
     plan_chunk(0);
     if (nch > 1) plan_chunk(1);
+    if (nch > 2) plan_chunk(2);
     __syncthreads();
-    fetch(0);
+    load_rows(0);
+    fetch();
+    if (nch > 1) load_rows(1);
     stash(0);
     __syncthreads();
   }
 
   for (int c = 0; c < nch; ++c) {
     const int buf = c & 1;
-    if (c + 1 < nch) fetch(c + 1);
-    if (c + 2 < nch) plan_chunk(c + 2);
+    if (c + 1 < nch) fetch();            // rows of chunk c + 1, read during chunk c - 1
+    if (c + 2 < nch) load_rows(c + 2);
 
     // ---- S^T = K Q^T for two 32-key blocks (raw, unscaled scores)
     spr::f32x16 s_acc[2];
@@ -359,6 +365,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
       }
     }
 
+    if (c + 3 < nch) plan_chunk(c + 3);
+
     // ---- keys past the end exist only in the last chunk
     const int32_t left = total - c * BN;
     if (left < BN) {
@@ -372,60 +380,58 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
       }
     }
 
-    // ---- online softmax (log2 domain); a lane owns one query row
-    float mloc = -__builtin_huge_valf();
+    // ---- online softmax (log2 domain) and O^T += V^T P^T, one 32-key half at a
+    // time: a lane owns one query row, and the softmax of one half overlaps the
+    // MFMAs of the other.
+    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk) {
+      float mloc = -__builtin_huge_valf();
 #pragma unroll
       for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s_acc[kbk][e]);
-    }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * scale_log2;
-    // Rescale lazily: only when some row's maximum grew by more than the slack.
-    if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
-      const float m_new = fmaxf(m_run, mloc);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * scale_log2;
+      // Rescale lazily: only when some row's maximum grew by more than the slack.
+      if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
 #pragma unroll
-      for (int b = 0; b < T::DBLK; ++b) {
+        for (int b = 0; b < T::DBLK; ++b) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
+          for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
+        }
+        m_run = m_new;
       }
-      m_run = m_new;
-    }
-    const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
-    // The row sum adds the bf16-rounded probabilities that also weight V.
-    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-    float lsum0 = 0.0f, lsum1 = 0.0f;
-    uint32_t pf[4][4];  // P as bf16 pairs: [k-step][dword]
-#pragma unroll
-    for (int kbk = 0; kbk < 2; ++kbk) {
+      const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
+      // The row sum adds the bf16-rounded probabilities that also weight V.
+      float lsum0 = 0.0f, lsum1 = 0.0f;
+      uint32_t pf[2][4];  // P of this half as bf16 pairs: [k-step][dword]
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e], scale_log2, neg_m));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e + 1], scale_log2, neg_m));
         const uint32_t pk = pack2(p0, p1);
-        pf[kbk * 2 + e / 8][(e % 8) / 2] = pk;
+        pf[e / 8][(e % 8) / 2] = pk;
         if (e % 4 == 0) {
           lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
         } else {
           lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
         }
       }
-    }
-    l_run += lsum0 + lsum1;
-
-    // ---- O^T += V^T P^T
+      l_run += lsum0 + lsum1;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const u32x4 bfrag = u32x4{pf[t][0], pf[t][1], pf[t][2], pf[t][3]};
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = kbk * 2 + tt;
+        const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
 #pragma unroll
-      for (int b = 0; b < T::DBLK; ++b) {
-        const uint8_t* vrow = &v_tile[buf][(b * 32 + col) * T::V_ROW];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + (16 * t + 4 * half) * 2);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (16 * t + 8 + 4 * half) * 2);
-        const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
-        o_acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag), o_acc[b], 0, 0,
-                                                           0);
+        for (int b = 0; b < T::DBLK; ++b) {
+          const uint8_t* vrow = &v_tile[buf][(b * 32 + col) * T::V_ROW];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + (16 * t + 4 * half) * 2);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (16 * t + 8 + 4 * half) * 2);
+          const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+          o_acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag), o_acc[b], 0,
+                                                             0, 0);
+        }
       }
     }
 
