@@ -35,7 +35,7 @@ constexpr int CCHUNK = 64;  // centroids per LDS tile
 //            1 = bf16-rounded squares summed in fp32, result rounded to bf16
 //                (flash_kmeans x_sq buffer of x.dtype).
 template <int D>
-__global__ __launch_bounds__(ASSIGN_THREADS) void kmeans_assign_bf16_kernel(
+__global__ __launch_bounds__(ASSIGN_THREADS, 2) void kmeans_assign_bf16_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ c, const float* __restrict__ c_sq,
     const float* __restrict__ x_sq_in, int x_sq_mode, int64_t n, int32_t k, int32_t* __restrict__ labels) {
   static_assert(D % 32 == 0 && D <= 256, "D must be a multiple of 32, at most 256");
@@ -77,8 +77,10 @@ __global__ __launch_bounds__(ASSIGN_THREADS) void kmeans_assign_bf16_kernel(
         const float lo = spr::bf16_lo(w[e]);
         const float hi = spr::bf16_hi(w[e]);
         if (x_sq_mode == 1) {
-          part += spr::bf16_to_f32(spr::f32_to_bf16(lo * lo));
-          part += spr::bf16_to_f32(spr::f32_to_bf16(hi * hi));
+          // squares rounded to bf16 (v_cvt_pk_bf16_f32, round to nearest even), summed in order
+          const uint32_t sq2 = spr::pack_bf16x2_rne(lo * lo, hi * hi);
+          part += spr::bf16_lo(sq2);
+          part += spr::bf16_hi(sq2);
         } else {
           part = __builtin_fmaf(lo, lo, part);
           part = __builtin_fmaf(hi, hi, part);
@@ -87,7 +89,7 @@ __global__ __launch_bounds__(ASSIGN_THREADS) void kmeans_assign_bf16_kernel(
     }
     const float other = __shfl_xor(part, 32, 64);
     float total = part + other;
-    if (x_sq_mode == 1) total = spr::bf16_to_f32(spr::f32_to_bf16(total));
+    if (x_sq_mode == 1) total = spr::bf16_lo(spr::pack_bf16x2_rne(total, 0.0f));
     if (x_sq_in != nullptr) total = live ? x_sq_in[b * n + p] : 0.0f;
     xsq[f] = total;
   }
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(ASSIGN_THREADS) void kmeans_assign_bf16_kernel(
     }
     if (tid < CCHUNK) {
       const int64_t cidx = static_cast<int64_t>(chunk) * CCHUNK + tid;
-      pre_csq = cidx < k ? csqb[cidx] : 0.0f;
+      pre_csq = cidx < k ? csqb[cidx] : __builtin_huge_valf();  // padding centroids never win
     }
   };
   auto stash = [&](int buf) {
@@ -148,19 +150,16 @@ __global__ __launch_bounds__(ASSIGN_THREADS) void kmeans_assign_bf16_kernel(
           const int local = blk * 32 + 8 * i + 4 * half + j;
           const int32_t cidx = chunk * CCHUNK + local;
           const float csq = tile_csq[buf][local];
-          float d0 = __fsub_rn(__fadd_rn(xsq[0], csq), __fmul_rn(2.0f, acc0[4 * i + j]));
-          float d1 = __fsub_rn(__fadd_rn(xsq[1], csq), __fmul_rn(2.0f, acc1[4 * i + j]));
-          d0 = fmaxf(d0, 0.0f);
-          d1 = fmaxf(d1, 0.0f);
-          const bool valid = cidx < k;
-          if (valid && d0 < best[0]) {
-            best[0] = d0;
-            best_idx[0] = cidx;
-          }
-          if (valid && d1 < best[1]) {
-            best[1] = d1;
-            best_idx[1] = cidx;
-          }
+          // (x_sq + c_sq) - 2 cross with one rounding per step: 2 * cross is exact, so
+          // fma(-2, cross, x_sq + c_sq) rounds exactly like the reference's subtraction.
+          const float d0 = fmaxf(__builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq)), 0.0f);
+          const float d1 = fmaxf(__builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq)), 0.0f);
+          const bool t0 = d0 < best[0];
+          const bool t1 = d1 < best[1];
+          best[0] = t0 ? d0 : best[0];
+          best_idx[0] = t0 ? cidx : best_idx[0];
+          best[1] = t1 ? d1 : best[1];
+          best_idx[1] = t1 ? cidx : best_idx[1];
         }
       }
     }
@@ -209,7 +208,8 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
   constexpr int E = 16 / sizeof(T);  // elements per 16-byte vector
   constexpr int VPR = D / E;         // vectors per row
   static_assert(D % E == 0 && VPR <= 256, "unsupported D");
-  constexpr int R = 256 / VPR;       // rows in flight per step (threads past R * VPR idle)
+  constexpr int R = 256 / VPR;       // row groups (threads past R * VPR idle)
+  constexpr int RPT = 16;            // rows per thread per pass
   __shared__ double red[R][D + 1];
   __shared__ float sq[D];
 
@@ -247,20 +247,31 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
     }
   };
 
+  // Passes of R * RPT rows: each thread issues the loads of its RPT rows before
+  // adding any of them, and the next pass's row indices are in flight while
+  // the current rows are added.
   const bool worker = rg < R;
-  int32_t r = worker ? start + rg : end;
-  for (; r + R < end; r += 2 * R) {
-    const uint32_t t0 = static_cast<uint32_t>(idx[r]);
-    const uint32_t t1 = static_cast<uint32_t>(idx[r + R]);
-    const u32x4 w0 = t0 < n ? reinterpret_cast<const u32x4*>(xb + static_cast<int64_t>(t0) * D)[v] : u32x4{0, 0, 0, 0};
-    const u32x4 w1 = t1 < n ? reinterpret_cast<const u32x4*>(xb + static_cast<int64_t>(t1) * D)[v] : u32x4{0, 0, 0, 0};
-    add_vec(w0);
-    add_vec(w1);
-  }
-  for (; r < end; r += R) {
-    const uint32_t t0 = static_cast<uint32_t>(idx[r]);
-    const u32x4 w0 = t0 < n ? reinterpret_cast<const u32x4*>(xb + static_cast<int64_t>(t0) * D)[v] : u32x4{0, 0, 0, 0};
-    add_vec(w0);
+  constexpr int STEP = R * RPT;
+  int32_t ix[RPT];
+  auto load_ix = [&](int32_t base) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int32_t r = base + rg + R * i;
+      ix[i] = (worker && r < end) ? idx[r] : -1;
+    }
+  };
+  load_ix(start);
+  for (int32_t base = start; base < end; base += STEP) {
+    u32x4 w[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const uint32_t t = static_cast<uint32_t>(ix[i]);
+      w[i] = t < static_cast<uint32_t>(n32) ? reinterpret_cast<const u32x4*>(xb + static_cast<int64_t>(t) * D)[v]
+                                            : u32x4{0, 0, 0, 0};
+    }
+    if (base + STEP < end) load_ix(base + STEP);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) add_vec(w[i]);
   }
   if (worker) {
 #pragma unroll
