@@ -68,10 +68,13 @@ int spr_centroid_sq(const void* c, int32_t dtype, int64_t rows, int32_t d, float
 /* assign_euclid_triton.py:1238-1412 euclid_assign_triton / kmeans_utils.py:775-893 inline-x_sq variant.
  *   bf16 x [batch, n, d], bf16 centroids [batch, k, d], fp32 c_sq [batch, k];
  *   x_sq fp32 [batch, n] or NULL (computed inline: x_sq_mode 0 = fp32, 1 = bf16 buffer);
+ *   x_sq_out fp32 [batch, n] nullable: receives the inline x_sq (when x_sq is NULL) so
+ *   later iterations over the same points can pass it back (kmeans_triton_impl.py:84-87
+ *   computes it once per Lloyd loop);
  *   labels int32 [batch, n]; d in {64, 128}. */
 int spr_kmeans_assign_bf16(const void* x, const void* centroids, const float* c_sq, const float* x_sq,
-                           int32_t x_sq_mode, int64_t batch, int64_t n, int32_t k, int32_t d, int32_t* labels,
-                           hipStream_t stream);
+                           int32_t x_sq_mode, float* x_sq_out, int64_t batch, int64_t n, int32_t k, int32_t d,
+                           int32_t* labels, hipStream_t stream);
 /* centroid_update_triton.py:316-386 triton_centroid_update_sorted_euclid,
  * centroid_reduction.py:138-196 original_centroids_triton, n8_ops.cu:255-269 finalize.
  *   Means of the rows of each cluster (sorted_idx/offsets from spr_argsort_labels), fp64

@@ -37,7 +37,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_argsort_labels": (ctypes.c_int, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _sz, _vp]),
     # kmeans.hip
     "spr_centroid_sq": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp]),
-    "spr_kmeans_assign_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32, _vp, _vp]),
+    "spr_kmeans_assign_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "spr_centroid_mean": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "spr_role_assign_fp32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     # select.hip

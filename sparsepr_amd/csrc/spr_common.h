@@ -93,7 +93,7 @@ __device__ __forceinline__ float canonical_expf(float x) {
   const float log2e = 1.44269504088896341f;
   const float ln2_hi = 0.693145751953125f;
   const float ln2_lo = 1.428606765330187045e-06f;
-  float n = __builtin_rintf(__fmul_rn(x, log2e));
+  float n = __builtin_rintf(x * log2e);
   float r = __builtin_fmaf(-n, ln2_hi, x);
   r = __builtin_fmaf(-n, ln2_lo, r);
   float p = 1.98412698412698413e-04f;
@@ -106,7 +106,7 @@ __device__ __forceinline__ float canonical_expf(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   int ni = static_cast<int>(n);
   float scale = __uint_as_float(static_cast<uint32_t>(ni + 127) << 23);
-  return __fmul_rn(p, scale);
+  return p * scale;  // power-of-two scaling (rounds only for a subnormal result)
 }
 
 // ---------------------------------------------------------------- misc

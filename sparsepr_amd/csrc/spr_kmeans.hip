@@ -37,7 +37,8 @@ constexpr int CCHUNK = 64;  // centroids per LDS tile
 template <int D>
 __global__ __launch_bounds__(ASSIGN_THREADS, 2) void kmeans_assign_bf16_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ c, const float* __restrict__ c_sq,
-    const float* __restrict__ x_sq_in, int x_sq_mode, int64_t n, int32_t k, int32_t* __restrict__ labels) {
+    const float* __restrict__ x_sq_in, int x_sq_mode, float* __restrict__ x_sq_out, int64_t n, int32_t k,
+    int32_t* __restrict__ labels) {
   static_assert(D % 32 == 0 && D <= 256, "D must be a multiple of 32, at most 256");
   constexpr int KSTEPS = D / 16;
   constexpr int ROW_BYTES = D * 2 + 16;  // padded LDS row: conflict-free 16-byte reads
@@ -90,7 +91,11 @@ __global__ __launch_bounds__(ASSIGN_THREADS, 2) void kmeans_assign_bf16_kernel(
     const float other = __shfl_xor(part, 32, 64);
     float total = part + other;
     if (x_sq_mode == 1) total = spr::bf16_lo(spr::pack_bf16x2_rne(total, 0.0f));
-    if (x_sq_in != nullptr) total = live ? x_sq_in[b * n + p] : 0.0f;
+    if (x_sq_in != nullptr) {
+      total = live ? x_sq_in[b * n + p] : 0.0f;
+    } else if (x_sq_out != nullptr && live && half == 0) {
+      x_sq_out[b * n + p] = total;  // reused by later iterations over the same points
+    }
     xsq[f] = total;
   }
 
@@ -396,7 +401,7 @@ extern "C" int spr_centroid_sq(const void* c, int32_t dtype, int64_t rows, int32
 // bf16 centroids [b, k, d], fp32 c_sq [b, k].  x_sq: fp32 [b, n] or null
 // (computed inline with x_sq_mode 0 = fp32, 1 = bf16 buffer semantics).
 extern "C" int spr_kmeans_assign_bf16(const void* x, const void* centroids, const float* c_sq, const float* x_sq,
-                                      int32_t x_sq_mode, int64_t batch, int64_t n, int32_t k, int32_t d,
+                                      int32_t x_sq_mode, float* x_sq_out, int64_t batch, int64_t n, int32_t k, int32_t d,
                                       int32_t* labels, hipStream_t stream) {
   SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_kmeans_assign_bf16: bad size");
   SPR_REQUIRE(batch <= 65535, "spr_kmeans_assign_bf16: batch %lld exceeds 65535", (long long)batch);
@@ -410,10 +415,12 @@ extern "C" int spr_kmeans_assign_bf16(const void* x, const void* centroids, cons
   const uint16_t* cp = static_cast<const uint16_t*>(centroids);
   switch (d) {
     case 64:
-      kmeans_assign_bf16_kernel<64><<<grid, ASSIGN_THREADS, 0, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode, n, k, labels);
+      kmeans_assign_bf16_kernel<64><<<grid, ASSIGN_THREADS, 0, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode, x_sq_out, n, k,
+                                                                        labels);
       break;
     case 128:
-      kmeans_assign_bf16_kernel<128><<<grid, ASSIGN_THREADS, 0, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode, n, k, labels);
+      kmeans_assign_bf16_kernel<128><<<grid, ASSIGN_THREADS, 0, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode, x_sq_out, n,
+                                                                         k, labels);
       break;
     default:
       SPR_REQUIRE(false, "spr_kmeans_assign_bf16: head dim %d not supported (64, 128)", d);

@@ -33,39 +33,54 @@ __device__ __forceinline__ float load_elem(const T* p, int64_t i) {
   }
 }
 
-// dist[bh, t] = sum_d (f[t, d] - center[label[t], d])^2, d ascending.
-// 64 tokens per workgroup: 256 threads compute rounded squares into LDS, then
-// one thread per token adds its row in order.
+// dist[bh, t] = sum_d (f[t, d] - center[label[t], d])^2, d ascending, each term
+// rounded (sub, mul, add; no contraction).  One thread per token: the row and its
+// centre row are read with 16-byte loads.
 template <typename T, int R>
 __global__ __launch_bounds__(256) void probe_distance_kernel(const T* __restrict__ f,
                                                              const int32_t* __restrict__ labels,
                                                              const float* __restrict__ centers, int64_t n,
                                                              int32_t groups, float* __restrict__ dist) {
-  __shared__ float sq[64][R + 1];
+  constexpr int E = 16 / sizeof(T);  // feature elements per 16-byte load
   const int64_t bh = blockIdx.y;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 64;
-  for (int e = threadIdx.x; e < 64 * R; e += blockDim.x) {
-    const int row = e / R;
-    const int d = e % R;
-    const int64_t t = t0 + row;
-    float v = 0.0f;
-    if (t < n) {
-      const int32_t lab = labels[bh * n + t];
-      const float c = (lab >= 0 && lab < groups) ? centers[(bh * groups + lab) * R + d] : 0.0f;
-      const float diff = __fsub_rn(load_elem(f, (bh * n + t) * R + d), c);
-      v = __fmul_rn(diff, diff);
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const int32_t lab = labels[bh * n + t];
+  const bool ok = lab >= 0 && lab < groups;
+  const spr::f32x4* crow = reinterpret_cast<const spr::f32x4*>(centers + (bh * groups + (ok ? lab : 0)) * R);
+  const u32x4* frow = reinterpret_cast<const u32x4*>(f + (bh * n + t) * R);
+  float acc = 0.0f;
+#pragma unroll 4
+  for (int q = 0; q < R / E; ++q) {
+    const u32x4 w = frow[q];
+    float fv[E];
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        fv[2 * e] = spr::bf16_lo(ws[e]);
+        fv[2 * e + 1] = spr::bf16_hi(ws[e]);
+      }
+    } else {
+      fv[0] = __uint_as_float(w.x);
+      fv[1] = __uint_as_float(w.y);
+      fv[2] = __uint_as_float(w.z);
+      fv[3] = __uint_as_float(w.w);
     }
-    sq[row][d] = v;
-  }
-  __syncthreads();
-  if (threadIdx.x < 64) {
-    const int64_t t = t0 + threadIdx.x;
-    if (t < n) {
-      float acc = 0.0f;
-      for (int d = 0; d < R; ++d) acc = __fadd_rn(acc, sq[threadIdx.x][d]);
-      dist[bh * n + t] = acc;
+#pragma unroll
+    for (int g = 0; g < E / 4; ++g) {
+      const spr::f32x4 c = ok ? crow[q * (E / 4) + g] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // plain operators: the file-level contract(off) keeps mul and add apart
+        // (the library's __f*_rn helpers carry their own contraction flags)
+        const float diff = fv[4 * g + e] - c[e];
+        const float sq = diff * diff;
+        acc = acc + sq;
+      }
     }
   }
+  dist[bh * n + t] = acc;
 }
 
 // mode 0: vectorized role-equal (one representative per group, first `count`

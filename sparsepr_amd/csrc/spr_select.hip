@@ -75,7 +75,7 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
     const float* kr = kb + static_cast<int64_t>(j) * d;
     float acc = 0.0f;
     for (int t = 0; t < d; ++t) acc = __builtin_fmaf(q_row[t], kr[t], acc);
-    const float s = score_bf16 ? bf16r(__fdiv_rn(bf16r(acc), sqrt_d)) : __fdiv_rn(acc, sqrt_d);
+    const float s = score_bf16 ? bf16r(bf16r(acc) / sqrt_d) : acc / sqrt_d;
     val[j] = s;
     local_max = fmaxf(local_max, s);
   }
@@ -83,18 +83,18 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
 
   for (int j = threadIdx.x; j < kn; j += blockDim.x) {
     const float w = static_cast<float>(sz[j]);
-    val[j] = __fmul_rn(w, spr::canonical_expf(__fsub_rn(val[j], m)));
+    val[j] = w * spr::canonical_expf(val[j] - m);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     float sum = 0.0f;
-    for (int j = 0; j < kn; ++j) sum = __fadd_rn(sum, val[j]);
+    for (int j = 0; j < kn; ++j) sum = sum + val[j];
     denom_s = sum > 1e-12f ? sum : 1e-12f;
   }
   __syncthreads();
   const float denom = denom_s;
   for (int j = threadIdx.x; j < kn; j += blockDim.x) {
-    const float prob = __fdiv_rn(val[j], denom);
+    const float prob = val[j] / denom;
     val[j] = score_bf16 ? bf16r(prob) : prob;
   }
   __syncthreads();
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
     float cum = 0.0f;
     float prev = 0.0f;
     for (int r = 0; r < kn; ++r) {
-      cum = __fadd_rn(cum, sorted_val[r]);
+      cum = cum + sorted_val[r];
       const float shown = score_bf16 ? bf16r(cum) : cum;
       bool remove = (r > 0) && (prev > thr);
       if (r < preserve) remove = false;

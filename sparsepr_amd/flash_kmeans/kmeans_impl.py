@@ -58,8 +58,11 @@ def centroid_sq(c: torch.Tensor) -> torch.Tensor:
 
 def euclid_assign(x: torch.Tensor, centroids: torch.Tensor, x_sq: torch.Tensor | None = None,
                   *, x_sq_mode: int = X_SQ_BF16, c_sq: torch.Tensor | None = None,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """Nearest-centroid ids int32 [B, N] (lowest index among exact minima)."""
+                  out: torch.Tensor | None = None, x_sq_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Nearest-centroid ids int32 [B, N] (lowest index among exact minima).
+
+    With x_sq None the squared norms are computed inline (per x_sq_mode); a float32
+    [B, N] `x_sq_out` then receives them for reuse by later calls on the same x."""
     dev = _check_x(x, "euclid_assign")
     _lib.require_gpu(centroids, what="euclid_assign")
     B, N, D = x.shape
@@ -76,8 +79,12 @@ def euclid_assign(x: torch.Tensor, centroids: torch.Tensor, x_sq: torch.Tensor |
         if c_sq is None:
             c_sq = centroid_sq(cc)
         xs = None if x_sq is None else x_sq.to(torch.float32).contiguous()
+        if x_sq_out is not None and (x_sq_out.shape != (B, N) or x_sq_out.dtype != torch.float32
+                                     or not x_sq_out.is_contiguous()):
+            raise RuntimeError("x_sq_out must be a contiguous float32 [B, N] tensor")
         _lib.call("spr_kmeans_assign_bf16", _lib.ptr(xc), _lib.ptr(cc), _lib.ptr(c_sq.contiguous()),
-                  _lib.ptr(xs), int(x_sq_mode), B, N, K, D, _lib.ptr(out), _lib.stream(dev))
+                  _lib.ptr(xs), int(x_sq_mode), _lib.ptr(x_sq_out if xs is None else None), B, N, K, D,
+                  _lib.ptr(out), _lib.stream(dev))
     elif x.dtype == torch.float32:
         _lib.call("spr_role_assign_fp32", _lib.ptr(xc), _lib.ptr(cc), B, N, K, D, _lib.ptr(out), None,
                   _lib.stream(dev))
@@ -160,10 +167,17 @@ def lloyd(x: torch.Tensor, n_clusters: int, max_iters: int, tol: float = 0.0,
     from ..kernels.permute import argsort_labels
 
     labels = torch.empty((B, N), dtype=torch.int32, device=dev)
+    # squared point norms: computed by the first assignment, reused afterwards
+    cached_sq = None
+    if x_sq is None and x.dtype == torch.bfloat16 and max_iters > 1:
+        cached_sq = torch.empty((B, N), dtype=torch.float32, device=dev)
     res = None
     it = -1
     for it in range(max_iters):
-        euclid_assign(x, cent, x_sq, x_sq_mode=x_sq_mode, out=labels)
+        if x_sq is None and cached_sq is not None and it > 0:
+            euclid_assign(x, cent, cached_sq, x_sq_mode=x_sq_mode, out=labels)
+        else:
+            euclid_assign(x, cent, x_sq, x_sq_mode=x_sq_mode, out=labels, x_sq_out=cached_sq)
         sorted_idx, sizes, offsets = argsort_labels(labels, K)
         res = centroid_update_sorted(x, labels, cent, want_mean32=want_mean32, want_shift=tol > 0 or verbose,
                                      sorted_idx=sorted_idx, sizes=sizes, offsets=offsets)

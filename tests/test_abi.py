@@ -44,7 +44,7 @@ def test_entry_points_validate_arguments_without_a_gpu():
     st = lib.spr_argsort_labels(None, 1, 10, 0, None, None, None, None, 0, None)
     assert st == 1 and b"k=0" in lib.spr_last_error()
     # unsupported head dim for the bf16 assign
-    st = lib.spr_kmeans_assign_bf16(16, 16, 16, None, 0, 1, 10, 4, 96, 16, None)
+    st = lib.spr_kmeans_assign_bf16(16, 16, 16, None, 0, None, 1, 10, 4, 96, 16, None)
     assert st == 1 and b"head dim 96" in lib.spr_last_error()
     # empty problems are no-ops
     assert lib.spr_permute_rows(None, None, None, 0, 5, 256, None) == 0
