@@ -60,7 +60,8 @@ def build(verbose: bool = False) -> Path:
     with ThreadPoolExecutor(workers) as pool:
         objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    # --no-undefined: a kernel whose host stub was not emitted fails here, not at load time
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -46,6 +46,10 @@ struct Seg {
 };
 
 constexpr int MAX_LDS_SEGS = 1024;  // segment lists up to this length are staged in LDS
+#ifndef ATTN_NW
+#define ATTN_NW 4  // block-sparse kernel: waves per workgroup
+#define ATTN_QB 1  //                      32-row query blocks per wave
+#endif
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -59,7 +63,7 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 // output is rescaled; p = 2^(s - m) stays below 2^8 in between.
 constexpr float RESCALE_SLACK = 8.0f;
 
-template <int D>
+template <int D, int NTHREADS>
 struct Tile {
   static constexpr int KSTEPS = D / 16;
   static constexpr int DBLK = D / 32;
@@ -68,8 +72,8 @@ struct Tile {
                                              // 32 distinct even banks, so 64-bit reads are conflict-free)
   static constexpr int K_BYTES = BN * K_ROW;
   static constexpr int V_BYTES = D * V_ROW;
-  static constexpr int K_PIECES = BN * D / 8 / THREADS;       // 16-byte K pieces per thread
-  static constexpr int V_PAIRS = (BN / 2) * (D / 8) / THREADS;  // (2 rows x 16 bytes) per thread
+  static constexpr int K_PIECES = BN * D / 8 / NTHREADS;       // 16-byte K pieces per thread
+  static constexpr int V_PAIRS = (BN / 2) * (D / 8) / NTHREADS;  // (2 rows x 16 bytes) per thread
   static_assert(K_PIECES >= 1 && V_PAIRS >= 1, "unsupported head dim");
 };
 
@@ -170,13 +174,19 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
 //         one q-cluster, which read the same key blocks) share one XCD's L2.
 // MODE 1: dense split-key for probe rows: q rows [0, m) of a [BHq, m, D] tensor,
 //         keys [split * split_len, ...) of K/V; output unnormalised fp32 partials.
-template <int D, int MODE, bool SEGL>
-__global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
+// NW waves per workgroup, QB 32-row query blocks per wave (NW * QB * 32 = BM).
+// QB = 2 runs one wave per SIMD with the output accumulators in AGPRs: every K
+// and V fragment read from LDS then feeds two MFMAs, and each wave carries twice
+// as many independent MFMA chains.
+template <int D, int MODE, bool SEGL, int NW, int QB>
+__global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
     int32_t bh_q, int32_t tiles_per_head, float scale_log2, uint16_t* __restrict__ out, float* __restrict__ lse,
     int32_t split_len, float* __restrict__ part_o, float* __restrict__ part_ml) {
-  using T = Tile<D>;
+  constexpr int NT = NW * 64;
+  static_assert(NW * QB * 32 == BM, "tile shape");
+  using T = Tile<D, NT>;
   __shared__ __attribute__((aligned(16))) uint8_t k_tile[2][T::K_BYTES];
   __shared__ __attribute__((aligned(16))) uint8_t v_tile[2][T::V_BYTES];
   __shared__ int32_t key_rows[4][BN];
@@ -234,24 +244,34 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   const __amdgpu_buffer_rsrc_t v_rsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vb), 0, kv_bytes, 0x00020000);
   if constexpr (MODE == 0 && SEGL) {
-    for (int i = tid; i < nseg; i += THREADS) seg_lds[i] = segs[i];
+    for (int i = tid; i < nseg; i += NT) seg_lds[i] = segs[i];
   }
 
-  // ---- this lane's query row, as MFMA B fragments over the head dim
-  const int32_t my_row = row0 + wave * 32 + col;
-  const bool row_live = my_row < row1;
-  u32x4 qf[T::KSTEPS];
+  // ---- this lane's query rows (one per block), as MFMA B fragments over the head dim
+  int32_t my_row[QB];
+  bool row_live[QB];
+  u32x4 qf[QB][T::KSTEPS];
 #pragma unroll
-  for (int s = 0; s < T::KSTEPS; ++s) {
-    qf[s] = row_live ? *reinterpret_cast<const u32x4*>(qb + static_cast<int64_t>(my_row) * D + s * 16 + half * 8)
+  for (int j = 0; j < QB; ++j) {
+    my_row[j] = row0 + (wave * QB + j) * 32 + col;
+    row_live[j] = my_row[j] < row1;
+#pragma unroll
+    for (int s = 0; s < T::KSTEPS; ++s) {
+      qf[j][s] = row_live[j]
+                     ? *reinterpret_cast<const u32x4*>(qb + static_cast<int64_t>(my_row[j]) * D + s * 16 + half * 8)
                      : u32x4{0, 0, 0, 0};
+    }
   }
 
-  spr::f32x16 o_acc[T::DBLK];
+  spr::f32x16 o_acc[QB][T::DBLK];
+  float m_run[QB], l_run[QB];  // running max (log2 units, may lag the true max by < RESCALE_SLACK), sum
 #pragma unroll
-  for (int b = 0; b < T::DBLK; ++b) o_acc[b] = spr::f32x16{};
-  float m_run = -__builtin_huge_valf();  // running max (log2 units, may lag the true max by < RESCALE_SLACK)
-  float l_run = 0.0f;
+  for (int j = 0; j < QB; ++j) {
+#pragma unroll
+    for (int b = 0; b < T::DBLK; ++b) o_acc[j][b] = spr::f32x16{};
+    m_run[j] = -__builtin_huge_valf();
+    l_run[j] = 0.0f;
+  }
 
   const int nch = (total + BN - 1) / BN;
 
@@ -294,32 +314,36 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
   auto load_rows = [&](int c) {  // plain copies, so nothing waits on these reads until fetch()
     const int32_t* kr = key_rows[c % 4];
 #pragma unroll
-    for (int i = 0; i < T::K_PIECES; ++i) krow[i] = kr[tid / (D / 8) + i * (THREADS / (D / 8))];
+    for (int i = 0; i < T::K_PIECES; ++i) krow[i] = kr[tid / (D / 8) + i * (NT / (D / 8))];
     const int rp = tid % (BN / 2);
     vrow[0] = kr[2 * rp];
     vrow[1] = kr[2 * rp + 1];
   };
-  auto fetch = [&]() {
+  auto fetch_k = [&]() {
 #pragma unroll
     for (int i = 0; i < T::K_PIECES; ++i) kreg[i] = bload(k_rsrc, krow[i] * (D * 2) + (tid % (D / 8)) * 16);
+  };
+  auto fetch_v = [&]() {
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
-      const int pc = tid / (BN / 2) + i * (THREADS / (BN / 2));
+      const int pc = tid / (BN / 2) + i * (NT / (BN / 2));
       vreg[i][0] = bload(v_rsrc, vrow[0] * (D * 2) + pc * 16);
       vreg[i][1] = bload(v_rsrc, vrow[1] * (D * 2) + pc * 16);
     }
   };
-  auto stash = [&](int buf) {
+  auto stash_k = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < T::K_PIECES; ++i) {
-      const int r = tid / (D / 8) + i * (THREADS / (D / 8));
+      const int r = tid / (D / 8) + i * (NT / (D / 8));
       const int pc = tid % (D / 8);
       *reinterpret_cast<u32x4*>(&k_tile[buf][r * T::K_ROW + pc * 16]) = kreg[i];
     }
+  };
+  auto stash_v = [&](int buf) {
     const int rp = tid % (BN / 2);
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
-      const int pc = tid / (BN / 2) + i * (THREADS / (BN / 2));
+      const int pc = tid / (BN / 2) + i * (NT / (BN / 2));
       const uint32_t a[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
       const uint32_t b[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
 #pragma unroll
@@ -340,144 +364,170 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_kernel(
     if (nch > 2) plan_chunk(2);
     __syncthreads();
     load_rows(0);
-    fetch();
+    fetch_k();
+    fetch_v();
     if (nch > 1) load_rows(1);
-    stash(0);
+    stash_k(0);
+    stash_v(0);
     __syncthreads();
   }
 
+  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  // Per chunk: K of chunk c + 1 is fetched at the top and stashed after the
+  // first 32-key half (its LDS buffer is free since the last barrier), then V of
+  // chunk c + 1 is fetched and stashed at the end, so the two staging sets are
+  // never live together.  Each half: S^T = K Q^T (each K fragment feeds the QB
+  // query blocks of the wave), online softmax (log2 domain; a lane owns one
+  // query row per block), O^T += V^T P^T.
   for (int c = 0; c < nch; ++c) {
     const int buf = c & 1;
-    if (c + 1 < nch) fetch();            // rows of chunk c + 1, read during chunk c - 1
-    if (c + 2 < nch) load_rows(c + 2);
-
-    // ---- S^T = K Q^T for two 32-key blocks (raw, unscaled scores)
-    spr::f32x16 s_acc[2];
+    const bool more = c + 1 < nch;
+    if (more) fetch_k();  // rows of chunk c + 1, read during chunk c - 1
+    const int32_t left = total - c * BN;  // keys past the end exist only in the last chunk
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk) {
-      s_acc[kbk] = spr::f32x16{};
-      const uint8_t* arow = &k_tile[buf][(kbk * 32 + col) * T::K_ROW + half * 16];
+      spr::f32x16 s_acc[QB];
 #pragma unroll
-      for (int s = 0; s < T::KSTEPS; ++s) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
-        s_acc[kbk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[s]), s_acc[kbk],
-                                                             0, 0, 0);
-      }
-    }
-
-    if (c + 3 < nch) plan_chunk(c + 3);
-
-    // ---- keys past the end exist only in the last chunk
-    const int32_t left = total - c * BN;
-    if (left < BN) {
+      for (int j = 0; j < QB; ++j) s_acc[j] = spr::f32x16{};
+      {
+        const uint8_t* arow = &k_tile[buf][(kbk * 32 + col) * T::K_ROW + half * 16];
 #pragma unroll
-      for (int kbk = 0; kbk < 2; ++kbk) {
+        for (int s = 0; s < T::KSTEPS; ++s) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kbk * 32 + 8 * (e / 4) + 4 * half + (e % 4);
-          if (key >= left) s_acc[kbk][e] = -__builtin_huge_valf();
+          for (int j = 0; j < QB; ++j) {
+            s_acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[j][s]), s_acc[j],
+                                                               0, 0, 0);
+          }
         }
       }
-    }
+      if (kbk == 0 && c + 3 < nch) plan_chunk(c + 3);
+      if (left < BN) {
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int key = kbk * 32 + 8 * (e / 4) + 4 * half + (e % 4);
+            if (key >= left) s_acc[j][e] = -__builtin_huge_valf();
+          }
+        }
+      }
 
-    // ---- online softmax (log2 domain) and O^T += V^T P^T, one 32-key half at a
-    // time: a lane owns one query row, and the softmax of one half overlaps the
-    // MFMAs of the other.
-    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+      float mloc[QB];
+      bool grow = false;
 #pragma unroll
-    for (int kbk = 0; kbk < 2; ++kbk) {
-      float mloc = -__builtin_huge_valf();
+      for (int j = 0; j < QB; ++j) {
+        float mx = -__builtin_huge_valf();
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s_acc[kbk][e]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64)) * scale_log2;
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_acc[j][e]);
+        mloc[j] = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+        grow = grow || (mloc[j] > m_run[j] + RESCALE_SLACK);
+      }
       // Rescale lazily: only when some row's maximum grew by more than the slack.
-      if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
+      if (__ballot(grow) != 0ull) {
 #pragma unroll
-        for (int b = 0; b < T::DBLK; ++b) {
+        for (int j = 0; j < QB; ++j) {
+          const float m_new = fmaxf(m_run[j], mloc[j]);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+          l_run[j] *= alpha;
 #pragma unroll
-          for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
-        }
-        m_run = m_new;
-      }
-      const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
-      // The row sum adds the bf16-rounded probabilities that also weight V.
-      float lsum0 = 0.0f, lsum1 = 0.0f;
-      uint32_t pf[2][4];  // P of this half as bf16 pairs: [k-step][dword]
+          for (int b = 0; b < T::DBLK; ++b) {
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e], scale_log2, neg_m));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[kbk][e + 1], scale_log2, neg_m));
-        const uint32_t pk = pack2(p0, p1);
-        pf[e / 8][(e % 8) / 2] = pk;
-        if (e % 4 == 0) {
-          lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
-        } else {
-          lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+            for (int e = 0; e < 16; ++e) o_acc[j][b][e] *= alpha;
+          }
+          m_run[j] = m_new;
         }
       }
-      l_run += lsum0 + lsum1;
+      uint32_t pf[QB][2][4];  // P of this half as bf16 pairs: [block][k-step][dword]
+#pragma unroll
+      for (int j = 0; j < QB; ++j) {
+        const float neg_m = (m_run[j] == -__builtin_huge_valf()) ? 0.0f : -m_run[j];
+        // The row sum adds the bf16-rounded probabilities that also weight V.
+        float lsum0 = 0.0f, lsum1 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[j][e], scale_log2, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[j][e + 1], scale_log2, neg_m));
+          const uint32_t pk = pack2(p0, p1);
+          pf[j][e / 8][(e % 8) / 2] = pk;
+          if (e % 4 == 0) {
+            lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+          } else {
+            lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+          }
+        }
+        l_run[j] += lsum0 + lsum1;
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         const int t = kbk * 2 + tt;
-        const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
 #pragma unroll
         for (int b = 0; b < T::DBLK; ++b) {
-          const uint8_t* vrow = &v_tile[buf][(b * 32 + col) * T::V_ROW];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + (16 * t + 4 * half) * 2);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (16 * t + 8 + 4 * half) * 2);
+          const uint8_t* vrow_p = &v_tile[buf][(b * 32 + col) * T::V_ROW];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow_p + (16 * t + 4 * half) * 2);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow_p + (16 * t + 8 + 4 * half) * 2);
           const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
-          o_acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag), o_acc[b], 0,
-                                                             0, 0);
+#pragma unroll
+          for (int j = 0; j < QB; ++j) {
+            const u32x4 bfrag = u32x4{pf[j][tt][0], pf[j][tt][1], pf[j][tt][2], pf[j][tt][3]};
+            o_acc[j][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag),
+                                                                  o_acc[j][b], 0, 0, 0);
+          }
         }
       }
+      if (kbk == 0 && more) {
+        stash_k(buf ^ 1);
+        fetch_v();
+        if (c + 2 < nch) load_rows(c + 2);
+      }
     }
-
-    if (c + 1 < nch) stash(buf ^ 1);
+    if (more) stash_v(buf ^ 1);
     __syncthreads();
   }
 
   // ---- epilogue
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  if constexpr (MODE == 0) {
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (row_live) {
-      uint16_t* orow = out + (bhq * static_cast<int64_t>(s_q) + my_row) * D;
 #pragma unroll
-      for (int b = 0; b < T::DBLK; ++b) {
+  for (int j = 0; j < QB; ++j) {
+    const float l_tot = l_run[j] + __shfl_xor(l_run[j], 32, 64);
+    if constexpr (MODE == 0) {
+      const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+      if (row_live[j]) {
+        uint16_t* orow = out + (bhq * static_cast<int64_t>(s_q) + my_row[j]) * D;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d0 = b * 32 + 8 * i + 4 * half;
-          uint2 w;
-          w.x = pack2(o_acc[b][4 * i] * inv, o_acc[b][4 * i + 1] * inv);
-          w.y = pack2(o_acc[b][4 * i + 2] * inv, o_acc[b][4 * i + 3] * inv);
-          *reinterpret_cast<uint2*>(orow + d0) = w;
+        for (int b = 0; b < T::DBLK; ++b) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int d0 = b * 32 + 8 * i + 4 * half;
+            uint2 w;
+            w.x = pack2(o_acc[j][b][4 * i] * inv, o_acc[j][b][4 * i + 1] * inv);
+            w.y = pack2(o_acc[j][b][4 * i + 2] * inv, o_acc[j][b][4 * i + 3] * inv);
+            *reinterpret_cast<uint2*>(orow + d0) = w;
+          }
+        }
+        if (lse != nullptr && half == 0) {
+          lse[bhq * static_cast<int64_t>(s_q) + my_row[j]] =
+              l_tot > 0.0f ? (m_run[j] + __builtin_amdgcn_logf(l_tot)) * 0.69314718055994531f
+                           : -__builtin_huge_valf();
         }
       }
-      if (lse != nullptr && half == 0) {
-        lse[bhq * static_cast<int64_t>(s_q) + my_row] =
-            l_tot > 0.0f ? (m_run + __builtin_amdgcn_logf(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
-      }
-    }
-  } else {
-    // partials: part_o [BHq, nsplit, s_q, D] fp32, part_ml [BHq, nsplit, s_q, 2]
-    if (row_live) {
-      const int64_t slot = (bhq * gridDim.x + blockIdx.x) * static_cast<int64_t>(s_q) + my_row;
-      float* po = part_o + slot * D;
+    } else {
+      // partials: part_o [BHq, nsplit, s_q, D] fp32, part_ml [BHq, nsplit, s_q, 2]
+      if (row_live[j]) {
+        const int64_t slot = (bhq * gridDim.x + blockIdx.x) * static_cast<int64_t>(s_q) + my_row[j];
+        float* po = part_o + slot * D;
 #pragma unroll
-      for (int b = 0; b < T::DBLK; ++b) {
+        for (int b = 0; b < T::DBLK; ++b) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d0 = b * 32 + 8 * i + 4 * half;
-          *reinterpret_cast<spr::f32x4*>(po + d0) =
-              spr::f32x4{o_acc[b][4 * i], o_acc[b][4 * i + 1], o_acc[b][4 * i + 2], o_acc[b][4 * i + 3]};
+          for (int i = 0; i < 4; ++i) {
+            const int d0 = b * 32 + 8 * i + 4 * half;
+            *reinterpret_cast<spr::f32x4*>(po + d0) =
+                spr::f32x4{o_acc[j][b][4 * i], o_acc[j][b][4 * i + 1], o_acc[j][b][4 * i + 2], o_acc[j][b][4 * i + 3]};
+          }
         }
-      }
-      if (half == 0) {
-        part_ml[slot * 2] = m_run;
-        part_ml[slot * 2 + 1] = l_tot;
+        if (half == 0) {
+          part_ml[slot * 2] = m_run[j];
+          part_ml[slot * 2 + 1] = l_tot;
+        }
       }
     }
   }
@@ -579,7 +629,7 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   const int32_t group = static_cast<int32_t>(bh_q / bh_kv);
   const float scale_log2 = scale * 1.4426950408889634f;
 #define SPR_ATTN(DD, SL)                                                                                      \
-  attn_fwd_kernel<DD, 0, SL><<<grid, THREADS, 0, stream>>>(                                                  \
+  attn_fwd_kernel<DD, 0, SL, ATTN_NW, ATTN_QB><<<grid, ATTN_NW * 64, 0, stream>>>(                          \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
       static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, static_cast<uint16_t*>(out),  \
@@ -643,7 +693,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
   const int64_t rows_total = bh_q * m;
   const uint32_t cblocks = static_cast<uint32_t>(spr::ceil_div(rows_total * (d / 4), 256));
   if (d == 128) {
-    attn_fwd_kernel<128, 1, false><<<grid, THREADS, 0, stream>>>(
+    attn_fwd_kernel<128, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
         scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
@@ -651,7 +701,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                           nsplit, out_dtype, out, lse);
   } else {
-    attn_fwd_kernel<64, 1, false><<<grid, THREADS, 0, stream>>>(
+    attn_fwd_kernel<64, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
         scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
