@@ -20,6 +20,8 @@
 //   clusters keep the previous centroid.
 // role assign (fp32): exact FP32 distance, sequential fmaf over dims, lowest
 //   index on ties (n8_ops.cu:189-196 better_pair).
+#include <algorithm>
+
 #include "spr_common.h"
 
 namespace {
@@ -204,12 +206,62 @@ __global__ void centroid_sq_kernel(const T* __restrict__ c, int64_t rows, int32_
 }
 
 // ---------------------------------------------------------------- segmented mean
-// T: uint16_t (bf16) or float.  One workgroup per (cluster, batch).
+// Mean of one cluster from its fp64 sum: mean32 = float(sum / count) (empty ->
+// previous centroid), out = mean32 in the centroid dtype, optional running
+// sums/counts and max centroid shift.  Called by every thread of the workgroup;
+// threads below D own one dim (`s` valid there).
+template <typename T, int D>
+__device__ void finalize_mean(double s, int32_t count, int64_t b, int32_t cl, int32_t k, const T* __restrict__ old,
+                              float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max,
+                              float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum, float* sq) {
+  const int tid = threadIdx.x;
+  const int64_t o = (b * k + cl) * D;
+  if (tid < D) {
+    float prev;
+    if constexpr (sizeof(T) == 2) {
+      prev = spr::bf16_to_f32(old[o + tid]);
+    } else {
+      prev = old[o + tid];
+    }
+    const float m = count > 0 ? static_cast<float>(s / static_cast<double>(count)) : prev;
+    if (mean32 != nullptr) mean32[o + tid] = m;
+    float outv = m;
+    if (out != nullptr) {
+      if constexpr (sizeof(T) == 2) {
+        const uint16_t bits = spr::f32_to_bf16(m);
+        out[o + tid] = bits;
+        outv = spr::bf16_to_f32(bits);
+      } else {
+        out[o + tid] = m;
+      }
+    }
+    if (sums_accum != nullptr) sums_accum[o + tid] += static_cast<float>(s);
+    const float diff = outv - prev;
+    sq[tid] = diff * diff;
+  }
+  if (counts_accum != nullptr && tid == 0) counts_accum[b * k + cl] += count;
+  if (shift_max != nullptr) {
+    __syncthreads();
+    if (tid == 0) {
+      float acc = 0.0f;
+      for (int t = 0; t < D; ++t) acc += sq[t];
+      const float norm = sqrtf(acc);
+      atomicMax(reinterpret_cast<unsigned int*>(shift_max), __float_as_uint(norm));
+    }
+  }
+}
+
+// T: uint16_t (bf16) or float.  Workgroup (cl * nsplit + sp, b) sums slice sp of
+// the `nsplit` equal slices of cluster cl's rows (sorted order) in fp64.  With
+// nsplit == 1 it also finalizes; otherwise it writes the slice sums to
+// partial[b][cl][sp][D] for centroid_mean_finalize_kernel, which adds the
+// slices in order (the result does not depend on the split).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void centroid_mean_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ sorted_idx, const int32_t* __restrict__ offsets,
-    const T* __restrict__ old, int64_t n, int32_t k, float* __restrict__ mean32, T* __restrict__ out,
-    float* __restrict__ shift_max, float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum) {
+    const T* __restrict__ old, int64_t n, int32_t k, int32_t nsplit, double* __restrict__ partial,
+    float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max, float* __restrict__ sums_accum,
+    int32_t* __restrict__ counts_accum) {
   constexpr int E = 16 / sizeof(T);  // elements per 16-byte vector
   constexpr int VPR = D / E;         // vectors per row
   static_assert(D % E == 0 && VPR <= 256, "unsupported D");
@@ -222,13 +274,17 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
   const int v = tid % VPR;
   const int rg = tid / VPR;
   const int64_t b = blockIdx.y;
-  const int32_t cl = blockIdx.x;
+  const int32_t cl = blockIdx.x / nsplit;
+  const int32_t sp = blockIdx.x - cl * nsplit;
   const int32_t* off = offsets + b * (k + 1);
   // offsets come from spr_argsort_labels; clamp anyway so a bad table cannot
   // index outside [0, n).
   const int32_t n32 = static_cast<int32_t>(n);
-  const int32_t start = min(max(off[cl], 0), n32);
-  const int32_t end = min(max(off[cl + 1], start), n32);
+  const int32_t c_start = min(max(off[cl], 0), n32);
+  const int32_t c_end = min(max(off[cl + 1], c_start), n32);
+  const int32_t slice = (c_end - c_start + nsplit - 1) / nsplit;
+  const int32_t start = min(c_start + sp * slice, c_end);
+  const int32_t end = min(start + slice, c_end);
   const int32_t* idx = sorted_idx + b * n;
   const T* xb = x + b * n * D;
 
@@ -284,44 +340,35 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
   }
   __syncthreads();
 
-  const int32_t count = end - start;
-  const int64_t o = (b * k + cl) * D;
+  double s = 0.0;
   if (tid < D) {
-    double s = 0.0;
     for (int g = 0; g < R; ++g) s += red[g][tid];
-    float m;
-    float prev;
-    if constexpr (sizeof(T) == 2) {
-      prev = spr::bf16_to_f32(old[o + tid]);
-    } else {
-      prev = old[o + tid];
-    }
-    m = count > 0 ? static_cast<float>(s / static_cast<double>(count)) : prev;
-    if (mean32 != nullptr) mean32[o + tid] = m;
-    float outv = m;
-    if (out != nullptr) {
-      if constexpr (sizeof(T) == 2) {
-        const uint16_t bits = spr::f32_to_bf16(m);
-        out[o + tid] = bits;
-        outv = spr::bf16_to_f32(bits);
-      } else {
-        out[o + tid] = m;
-      }
-    }
-    if (sums_accum != nullptr) sums_accum[o + tid] += static_cast<float>(s);
-    const float diff = outv - prev;
-    sq[tid] = diff * diff;
   }
-  if (counts_accum != nullptr && tid == 0) counts_accum[b * k + cl] += count;
-  if (shift_max != nullptr) {
-    __syncthreads();
-    if (tid == 0) {
-      float s = 0.0f;
-      for (int t = 0; t < D; ++t) s += sq[t];
-      const float norm = sqrtf(s);
-      atomicMax(reinterpret_cast<unsigned int*>(shift_max), __float_as_uint(norm));
-    }
+  if (nsplit > 1) {
+    if (tid < D) partial[((b * k + cl) * nsplit + sp) * D + tid] = s;
+    return;
   }
+  finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, sq);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void centroid_mean_finalize_kernel(
+    const double* __restrict__ partial, const int32_t* __restrict__ offsets, const T* __restrict__ old, int64_t n,
+    int32_t k, int32_t nsplit, float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max,
+    float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum) {
+  __shared__ float sq[D];
+  const int64_t b = blockIdx.y;
+  const int32_t cl = blockIdx.x;
+  const int32_t* off = offsets + b * (k + 1);
+  const int32_t n32 = static_cast<int32_t>(n);
+  const int32_t c_start = min(max(off[cl], 0), n32);
+  const int32_t c_end = min(max(off[cl + 1], c_start), n32);
+  double s = 0.0;
+  if (threadIdx.x < D) {
+    const double* p = partial + (b * k + cl) * nsplit * D + threadIdx.x;
+    for (int sp = 0; sp < nsplit; ++sp) s += p[sp * D];
+  }
+  finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, sq);
 }
 
 // ---------------------------------------------------------------- exact fp32 assign
@@ -434,20 +481,46 @@ extern "C" int spr_kmeans_assign_bf16(const void* x, const void* centroids, cons
 // Outputs (each nullable): mean32 fp32 [b,k,d]; out (dtype) [b,k,d];
 // shift_max (fp32 scalar, must start at 0; receives max_k ||out - old||);
 // sums_accum fp32 [b,k,d] += sums; counts_accum int32 [b,k] += counts.
+// Slices per cluster: about 256 rows each on average, at most 16.
+static int32_t mean_splits(int64_t n, int32_t k) {
+  const int64_t avg = n / (k > 0 ? k : 1);
+  return static_cast<int32_t>(std::min<int64_t>(16, std::max<int64_t>(1, (avg + 255) / 256)));
+}
+
+extern "C" size_t spr_centroid_mean_workspace(int64_t batch, int64_t n, int32_t k, int32_t d) {
+  const int32_t ns = mean_splits(n, k);
+  return ns > 1 ? static_cast<size_t>(batch * k * ns * static_cast<int64_t>(d) * sizeof(double)) : 0;
+}
+
 extern "C" int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, const int32_t* offsets,
                                  const void* old, int64_t batch, int64_t n, int32_t k, int32_t d, float* mean32,
                                  void* out, float* shift_max, float* sums_accum, int32_t* counts_accum,
-                                 hipStream_t stream) {
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
   SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_centroid_mean: bad size");
   SPR_REQUIRE(batch <= 65535, "spr_centroid_mean: batch %lld exceeds 65535", (long long)batch);
   if (batch == 0) return SPR_OK;
   SPR_REQUIRE(sorted_idx && offsets && old, "spr_centroid_mean: null pointer");
   SPR_REQUIRE(n == 0 || x, "spr_centroid_mean: null x");
-  dim3 grid(static_cast<uint32_t>(k), static_cast<uint32_t>(batch));
-#define SPR_MEAN_CASE(T, DD)                                                                            \
-  centroid_mean_kernel<T, DD><<<grid, 256, 0, stream>>>(                                                \
-      static_cast<const T*>(x), sorted_idx, offsets, static_cast<const T*>(old), n, k, mean32,        \
-      static_cast<T*>(out), shift_max, sums_accum, counts_accum)
+  const int32_t ns = mean_splits(n, k);
+  const size_t need = spr_centroid_mean_workspace(batch, n, k, d);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+    spr_set_error("spr_centroid_mean: workspace %zu < %zu bytes", workspace_bytes, need);
+    return SPR_EWORKSPACE;
+  }
+  SPR_REQUIRE(static_cast<int64_t>(k) * ns < (int64_t(1) << 31), "spr_centroid_mean: too many clusters");
+  double* partial = static_cast<double*>(workspace);
+  dim3 grid(static_cast<uint32_t>(k * ns), static_cast<uint32_t>(batch));
+  dim3 fgrid(static_cast<uint32_t>(k), static_cast<uint32_t>(batch));
+#define SPR_MEAN_CASE(T, DD)                                                                                 \
+  do {                                                                                                       \
+    centroid_mean_kernel<T, DD><<<grid, 256, 0, stream>>>(                                                   \
+        static_cast<const T*>(x), sorted_idx, offsets, static_cast<const T*>(old), n, k, ns, partial, mean32, \
+        static_cast<T*>(out), shift_max, sums_accum, counts_accum);                                          \
+    if (ns > 1)                                                                                              \
+      centroid_mean_finalize_kernel<T, DD><<<fgrid, 256, 0, stream>>>(                                       \
+          partial, offsets, static_cast<const T*>(old), n, k, ns, mean32, static_cast<T*>(out), shift_max,   \
+          sums_accum, counts_accum);                                                                         \
+  } while (0)
   if (dtype == 0) {
     switch (d) {
       case 64: SPR_MEAN_CASE(uint16_t, 64); break;

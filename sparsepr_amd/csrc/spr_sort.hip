@@ -26,7 +26,7 @@ __device__ __forceinline__ uint32_t bin_of(int32_t label, int32_t k) {
 __global__ __launch_bounds__(256) void label_hist_kernel(const int32_t* __restrict__ labels, int64_t n,
                                                          int32_t k, int32_t nchunks,
                                                          int32_t* __restrict__ hist) {
-  __shared__ int32_t h[MAX_BINS];
+  extern __shared__ int32_t h[];  // [k + 1]
   const int32_t bins = k + 1;
   const int64_t row = blockIdx.y;
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CHUNK;
@@ -119,19 +119,30 @@ __global__ __launch_bounds__(64) void label_scatter_kernel(const int32_t* __rest
                                                            int32_t k, int32_t nchunks,
                                                            const int32_t* __restrict__ bases,
                                                            int32_t* __restrict__ sorted_idx) {
-  __shared__ int32_t cnt[MAX_BINS];
+  extern __shared__ int32_t cnt[];  // [k + 1]
   const int32_t bins = k + 1;
   const int64_t row = blockIdx.y;
   const int lane = threadIdx.x;
   const int32_t* b = bases + (row * nchunks + blockIdx.x) * bins;
   for (int j = lane; j < bins; j += 64) cnt[j] = b[j];
-  __syncthreads();
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CHUNK;
   const int64_t c1 = c0 + CHUNK < n ? c0 + CHUNK : n;
-  for (int64_t g = c0; g < c1; g += 64) {
+  // all of the chunk's labels are loaded before the first ranking step
+  constexpr int GROUPS = CHUNK / 64;
+  int32_t bins_of[GROUPS];
+#pragma unroll
+  for (int i = 0; i < GROUPS; ++i) {
+    const int64_t t = c0 + i * 64 + lane;
+    bins_of[i] = t < c1 ? static_cast<int32_t>(bin_of(labels[row * n + t], k)) : -1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < GROUPS; ++i) {
+    const int64_t g = c0 + i * 64;
+    if (g >= c1) break;
     const int64_t t = g + lane;
     const bool live = t < c1;
-    const int32_t bin = live ? static_cast<int32_t>(bin_of(labels[row * n + t], k)) : -1;
+    const int32_t bin = bins_of[i];
     int rank = 0;
     int count = 0;
 #pragma unroll 16
@@ -190,11 +201,12 @@ extern "C" int spr_argsort_labels(const int32_t* labels, int64_t rows, int64_t n
   }
   const int32_t nchunks = static_cast<int32_t>(spr::ceil_div(n, CHUNK));
   int32_t* hist = static_cast<int32_t*>(workspace);
-  label_hist_kernel<<<dim3(nchunks, rows), 256, 0, stream>>>(labels, n, k, nchunks, hist);
+  const size_t bin_bytes = static_cast<size_t>(k + 1) * sizeof(int32_t);
+  label_hist_kernel<<<dim3(nchunks, rows), 256, bin_bytes, stream>>>(labels, n, k, nchunks, hist);
   SPR_LAUNCHED("label_hist_kernel");
   label_scan_kernel<<<dim3(rows), 1024, 0, stream>>>(hist, k, nchunks, sizes, offsets);
   SPR_LAUNCHED("label_scan_kernel");
-  label_scatter_kernel<<<dim3(nchunks, rows), 64, 0, stream>>>(labels, n, k, nchunks, hist, sorted_idx);
+  label_scatter_kernel<<<dim3(nchunks, rows), 64, bin_bytes, stream>>>(labels, n, k, nchunks, hist, sorted_idx);
   SPR_LAUNCHED("label_scatter_kernel");
   return SPR_OK;
 }

@@ -126,9 +126,13 @@ def centroid_update_sorted(x: torch.Tensor, labels: torch.Tensor, old: torch.Ten
     new = torch.empty_like(oc) if out is None else out
     mean32 = torch.empty((B, K, D), dtype=torch.float32, device=dev) if want_mean32 else None
     shift = torch.zeros(1, dtype=torch.float32, device=dev) if want_shift else None
+    lib = _lib.load()
+    ws_bytes = int(lib.spr_centroid_mean_workspace(B, N, K, D))
+    ws = _lib.workspace(ws_bytes, dev) if ws_bytes > 0 else None
     _lib.call("spr_centroid_mean", _lib.ptr(xc), _lib.DTYPE_CODE[x.dtype], _lib.ptr(sorted_idx),
               _lib.ptr(offsets), _lib.ptr(oc), B, N, K, D, _lib.ptr(mean32), _lib.ptr(new),
-              _lib.ptr(shift), _lib.ptr(sums_accum), _lib.ptr(counts_accum), _lib.stream(dev))
+              _lib.ptr(shift), _lib.ptr(sums_accum), _lib.ptr(counts_accum), _lib.ptr(ws), ws_bytes,
+              _lib.stream(dev))
     return UpdateResult(new, sizes, sorted_idx, offsets, mean32, shift)
 
 

@@ -66,7 +66,7 @@ def test_assign_with_given_x_sq(dev, oracle):
     assert ok
 
 
-@pytest.mark.parametrize("k,d", [(256, 128), (7, 64), (512, 128)])
+@pytest.mark.parametrize("k,d", [(256, 128), (7, 64), (512, 128), (2, 128), (5, 128)])  # k <= 7: split clusters
 def test_centroid_mean_bit_exact(dev, oracle, k, d):
     from sparsepr_amd.flash_kmeans.kmeans_impl import centroid_update_sorted
 
