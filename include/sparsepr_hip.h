@@ -140,15 +140,18 @@ int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, 
  * multiple of bh_kv (query head h uses kv head h / (bh_q / bh_kv)); d in {64, 128}.
  * out bf16 [bh_q, s, d]: softmax over the kept keys of the row's q-cluster (scale
  * applied to q.k); rows of empty q-clusters are 0.  lse fp32 [bh_q, s] (nullable,
- * natural log of the scaled sum, -inf for an empty row). */
+ * natural log of the scaled sum, -inf for an empty row).  q_index int32 [bh_q, s] (nullable):
+ * q, out and lse stay in token order and cluster-sorted row r is token q_index[r], which fuses
+ * permute_tensor_by_labels_triton of Q and apply_inverse_permutation_triton of the output
+ * (hunyuanvideo.py:189-231) into the attention. */
 int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan, int64_t bh_q,
                                    int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
-                                   void* out, float* lse, hipStream_t stream);
+                                   const int32_t* q_index, void* out, float* lse, hipStream_t stream);
 /* Plan + run in one call; workspace = plan buffer of spr_block_sparse_attention_workspace bytes. */
 int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,
                                const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q, int64_t bh_kv, int64_t s,
-                               int32_t d, int32_t qn, int32_t kn, float scale, void* out, float* lse, void* workspace,
-                               size_t workspace_bytes, hipStream_t stream);
+                               int32_t d, int32_t qn, int32_t kn, float scale, const int32_t* q_index, void* out,
+                               float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* n8_v6.py:1236-1243 dense probe attention (F.scaled_dot_product_attention of the probe
  * rows against every key).  q bf16 [bh_q, m, d], k/v bf16 [bh_kv, s_kv, d]; keys split
  * into nsplit ranges computed in parallel and merged; out [bh_q, m, d] (out_dtype 0 =

@@ -182,8 +182,9 @@ template <int D, int MODE, bool SEGL, int NW, int QB>
 __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
-    int32_t bh_q, int32_t tiles_per_head, float scale_log2, uint16_t* __restrict__ out, float* __restrict__ lse,
-    int32_t split_len, float* __restrict__ part_o, float* __restrict__ part_ml) {
+    int32_t bh_q, int32_t tiles_per_head, float scale_log2, const int32_t* __restrict__ q_index,
+    uint16_t* __restrict__ out, float* __restrict__ lse, int32_t split_len, float* __restrict__ part_o,
+    float* __restrict__ part_ml) {
   constexpr int NT = NW * 64;
   static_assert(NW * QB * 32 == BM, "tile shape");
   using T = Tile<D, NT>;
@@ -247,7 +248,9 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     for (int i = tid; i < nseg; i += NT) seg_lds[i] = segs[i];
   }
 
-  // ---- this lane's query rows (one per block), as MFMA B fragments over the head dim
+  // ---- this lane's query rows (one per block), as MFMA B fragments over the head dim.
+  // With q_index, tile row r is the query stored at row q_index[r] (the layout of
+  // q, out and lse); rows outside [0, s_q) are treated as absent.
   int32_t my_row[QB];
   bool row_live[QB];
   u32x4 qf[QB][T::KSTEPS];
@@ -255,6 +258,10 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   for (int j = 0; j < QB; ++j) {
     my_row[j] = row0 + (wave * QB + j) * 32 + col;
     row_live[j] = my_row[j] < row1;
+    if (q_index != nullptr && row_live[j]) {
+      my_row[j] = q_index[bhq * static_cast<int64_t>(s_q) + my_row[j]];
+      row_live[j] = my_row[j] >= 0 && my_row[j] < s_q;
+    }
 #pragma unroll
     for (int s = 0; s < T::KSTEPS; ++s) {
       qf[j][s] = row_live[j]
@@ -608,9 +615,13 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
 // q [bh_q, s, d], k/v [bh_kv, s, d] bf16 (cluster-contiguous), plan from
 // spr_block_sparse_attention_plan; out bf16 [bh_q, s, d]; lse fp32 [bh_q, s]
 // (nullable, natural log).  bh_q must be a multiple of bh_kv (GQA groups).
+// q_index int32 [bh_q, s] (nullable): q, out and lse stay in token order and
+// cluster-sorted row r is token q_index[r] (the Q permutation and its inverse
+// fused into the attention).
 extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan,
                                               int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d, int32_t qn,
-                                              int32_t kn, float scale, void* out, float* lse, hipStream_t stream) {
+                                              int32_t kn, float scale, const int32_t* q_index, void* out, float* lse,
+                                              hipStream_t stream) {
   SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_run: bad size");
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_block_sparse_attention_run: bh_q=%lld not a multiple of bh_kv=%lld",
               (long long)bh_q, (long long)bh_kv);
@@ -632,8 +643,8 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   attn_fwd_kernel<DD, 0, SL, ATTN_NW, ATTN_QB><<<grid, ATTN_NW * 64, 0, stream>>>(                          \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
-      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, static_cast<uint16_t*>(out),  \
-      lse, 0, nullptr, nullptr)
+      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index,                     \
+      static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr)
   const bool seg_lds = kn <= MAX_LDS_SEGS;
   if (d == 128) {
     if (seg_lds) SPR_ATTN(128, true); else SPR_ATTN(128, false);
@@ -649,13 +660,14 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
 extern "C" int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,
                                           const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q,
                                           int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
-                                          void* out, float* lse, void* workspace, size_t workspace_bytes,
-                                          hipStream_t stream) {
+                                          const int32_t* q_index, void* out, float* lse, void* workspace,
+                                          size_t workspace_bytes, hipStream_t stream) {
   if (bh_q == 0 || s == 0) return SPR_OK;
   int st = spr_block_sparse_attention_plan(map, q_sizes, k_sizes, bh_kv, s, qn, kn, workspace, workspace_bytes,
                                            stream);
   if (st != SPR_OK) return st;
-  return spr_block_sparse_attention_run(q, k, v, workspace, bh_q, bh_kv, s, d, qn, kn, scale, out, lse, stream);
+  return spr_block_sparse_attention_run(q, k, v, workspace, bh_q, bh_kv, s, d, qn, kn, scale, q_index, out, lse,
+                                        stream);
 }
 
 extern "C" size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t d, int32_t nsplit) {
@@ -696,7 +708,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_fwd_kernel<128, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
-        scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
+        scale_log2, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                           nsplit, out_dtype, out, lse);
@@ -704,7 +716,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_fwd_kernel<64, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
-        scale_log2, nullptr, nullptr, split_len, part_o, part_ml);
+        scale_log2, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<64><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                          nsplit, out_dtype, out, lse);

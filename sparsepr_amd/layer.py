@@ -4,8 +4,9 @@ Composition (reference call sites):
   route   : flash k-means of Q and of K (Lloyd, fixed iterations), top-p
             cluster-pair map, K/V permutation  -- wan22.py:2221-2258 (SAP route),
             n8_v6.py:905-925 (K/V permute)
-  attend  : Q permutation, block-sparse attention over the kept cluster pairs,
-            inverse permutation                -- hunyuanvideo.py:189-231
+  attend  : block-sparse attention over the kept cluster pairs, reading Q and
+            writing the output through the query sort index (the Q permutation
+            and its inverse fused in)          -- hunyuanvideo.py:189-231
   repair  : N8 probe repair of the dropped blocks -- n8_v6.py:1174-1444
             (probes are role-equal representatives of the Q clusters; with the
             top-p route the role features are the queries themselves)
@@ -121,22 +122,17 @@ class SparsePRAttention:
         if timings is not None:
             timings.mark("start")
         route, q_idx = self.route(q, k, v, timings)
-        from .kernels.permute import apply_inverse_permutation_triton, permute_tensor_by_labels_triton
-
-        q_perm, _ = permute_tensor_by_labels_triton(q, None, 2, sorted_indices=q_idx)
-        if timings is not None:
-            timings.mark("permute")
         plan = plan_block_sparse(route.video_dynamic_map, route.q_cluster_sizes, route.k_cluster_sizes, N)
         if timings is not None:
             timings.mark("plan")
-        o_perm = block_sparse_attention(q_perm.reshape(bh, N, D), route.k_permuted.reshape(bh, N, D),
-                                        route.v_permuted.reshape(bh, N, D), route.video_dynamic_map,
-                                        route.q_cluster_sizes, route.k_cluster_sizes, plan=plan)
+        # The Q permutation and the output's inverse permutation (hunyuanvideo.py:189-231)
+        # are fused into the attention through q_index: q and base stay in token order.
+        base = block_sparse_attention(q.reshape(bh, N, D), route.k_permuted.reshape(bh, N, D),
+                                      route.v_permuted.reshape(bh, N, D), route.video_dynamic_map,
+                                      route.q_cluster_sizes, route.k_cluster_sizes, plan=plan,
+                                      q_index=q_idx).view(B, H, N, D)
         if timings is not None:
             timings.mark("attention")
-        base = apply_inverse_permutation_triton(o_perm.view(B, H, N, D), q_idx, 2)
-        if timings is not None:
-            timings.mark("unpermute")
         self.last_route = route
         if not cfg.repair:
             return base

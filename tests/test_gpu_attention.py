@@ -185,3 +185,32 @@ def test_block_sparse_full_size_sampled_rows(dev, oracle):
         e = np.exp(s - s.max())
         ref = (e / e.sum()) @ vv
         assert np.abs(got - ref).max() <= ATOL
+
+
+def test_q_index_fuses_the_query_permutation(dev, oracle):
+    """Reading Q and writing O through the query sort index equals permute ->
+    attention -> inverse permute exactly (same rows, same arithmetic)."""
+    from sparsepr_amd.kernels.attention import block_sparse_attention
+    from sparsepr_amd.kernels.permute import apply_inverse_permutation_triton, permute_tensor_by_labels_triton
+
+    rng = np.random.default_rng(21)
+    q, k, v, m, qs, ks = _problem(oracle, rng, 1, 4, 2, 900, 128, 7, 13)
+    q, k, v, m, ks = q[0], k[0], v[0], m[0], ks[0]
+    bh_q, s, d = q.shape
+    labels = np.repeat(np.arange(7), qs[0][0])[None, :].repeat(bh_q, 0)
+    for h in range(bh_q):  # tokens of each q-cluster scattered over the sequence
+        labels[h] = labels[h][rng.permutation(s)]
+    labels_t = to_dev(labels.astype(np.int32), dev)
+    qd = to_dev(q, dev, torch.bfloat16)
+    q_perm, idx = permute_tensor_by_labels_triton(qd.unsqueeze(0), labels_t.unsqueeze(0), 2)
+    sizes = torch.from_numpy(np.stack([np.bincount(labels[h], minlength=7) for h in range(bh_q)]).astype(np.int32))
+    args = (to_dev(k, dev, torch.bfloat16), to_dev(v, dev, torch.bfloat16), to_dev(m, dev), sizes[::2].to(dev),
+            to_dev(ks, dev))
+    ref_sorted, ref_lse = block_sparse_attention(q_perm[0], *args, return_lse=True)
+    ref = apply_inverse_permutation_triton(ref_sorted.unsqueeze(0), idx, 2)[0]
+    qi = idx.reshape(bh_q, s)
+    got, lse = block_sparse_attention(qd, *args, return_lse=True, q_index=qi)
+    assert torch.equal(got, ref)
+    inv = torch.empty_like(qi)
+    inv.scatter_(1, qi.long(), torch.arange(s, device=dev, dtype=torch.int32).expand(bh_q, -1).contiguous())
+    assert torch.equal(lse, torch.gather(ref_lse, 1, inv.long()))
