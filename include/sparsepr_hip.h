@@ -81,14 +81,15 @@ int spr_kmeans_assign_bf16(const void* x, const void* centroids, const float* c_
  *   accumulation, empty clusters keep `old`.  dtype 0 (bf16, d in {64,128}) or 2 (fp32,
  *   d in {16,32,48,64,128}).  Nullable outputs: mean32 fp32 [batch,k,d], out dtype [batch,k,d],
  *   shift_max fp32 scalar (pre-zeroed; max_k ||out-old||), sums_accum fp32 += sums,
- *   counts_accum int32 += counts.  Large clusters are split into row slices whose fp64 partial
+ *   counts_accum int32 += counts, c_sq_out fp32 [batch,k] = squared norms of `out` (as
+ *   spr_centroid_sq computes them, for the next assignment).  Large clusters are split into row slices whose fp64 partial
  *   sums go to the workspace (spr_centroid_mean_workspace bytes, 0 when no split is needed)
  *   and are added in slice order. */
 size_t spr_centroid_mean_workspace(int64_t batch, int64_t n, int32_t k, int32_t d);
 int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, const int32_t* offsets,
                       const void* old, int64_t batch, int64_t n, int32_t k, int32_t d, float* mean32, void* out,
-                      float* shift_max, float* sums_accum, int32_t* counts_accum, void* workspace,
-                      size_t workspace_bytes, hipStream_t stream);
+                      float* shift_max, float* sums_accum, int32_t* counts_accum, float* c_sq_out,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* n8_ops.cu:198-253 role_cluster_assign_accumulate_q64_kernel (assignment part):
  *   exact FP32 distance (sequential fmaf), lowest index on ties; d in {16,32,48,64}.
  *   best_dist nullable. */

@@ -40,7 +40,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_kmeans_assign_bf16": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "spr_centroid_mean_workspace": (_sz, [_i64, _i64, _i32, _i32]),
     "spr_centroid_mean": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
-                                         _vp, _sz, _vp]),
+                                         _vp, _vp, _sz, _vp]),
     "spr_role_assign_fp32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     # select.hip
     "spr_topp_map": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _f32, _i32, _i32, _vp, _vp]),

@@ -213,7 +213,8 @@ __global__ void centroid_sq_kernel(const T* __restrict__ c, int64_t rows, int32_
 template <typename T, int D>
 __device__ void finalize_mean(double s, int32_t count, int64_t b, int32_t cl, int32_t k, const T* __restrict__ old,
                               float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max,
-                              float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum, float* sq) {
+                              float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum,
+                              float* __restrict__ c_sq_out, float* sq, float* cv) {
   const int tid = threadIdx.x;
   const int64_t o = (b * k + cl) * D;
   if (tid < D) {
@@ -238,15 +239,23 @@ __device__ void finalize_mean(double s, int32_t count, int64_t b, int32_t cl, in
     if (sums_accum != nullptr) sums_accum[o + tid] += static_cast<float>(s);
     const float diff = outv - prev;
     sq[tid] = diff * diff;
+    cv[tid] = outv;
   }
   if (counts_accum != nullptr && tid == 0) counts_accum[b * k + cl] += count;
-  if (shift_max != nullptr) {
+  if (shift_max != nullptr || c_sq_out != nullptr) {
     __syncthreads();
-    if (tid == 0) {
+    if (shift_max != nullptr && tid == 0) {
       float acc = 0.0f;
       for (int t = 0; t < D; ++t) acc += sq[t];
       const float norm = sqrtf(acc);
       atomicMax(reinterpret_cast<unsigned int*>(shift_max), __float_as_uint(norm));
+    }
+    // squared norm of the new centroid for the next assignment, in the order of
+    // centroid_sq_kernel (sequential fma over d)
+    if (c_sq_out != nullptr && tid == 64 % blockDim.x) {
+      float acc = 0.0f;
+      for (int t = 0; t < D; ++t) acc = __builtin_fmaf(cv[t], cv[t], acc);
+      c_sq_out[b * k + cl] = acc;
     }
   }
 }
@@ -261,14 +270,14 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
     const T* __restrict__ x, const int32_t* __restrict__ sorted_idx, const int32_t* __restrict__ offsets,
     const T* __restrict__ old, int64_t n, int32_t k, int32_t nsplit, double* __restrict__ partial,
     float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max, float* __restrict__ sums_accum,
-    int32_t* __restrict__ counts_accum) {
+    int32_t* __restrict__ counts_accum, float* __restrict__ c_sq_out) {
   constexpr int E = 16 / sizeof(T);  // elements per 16-byte vector
   constexpr int VPR = D / E;         // vectors per row
   static_assert(D % E == 0 && VPR <= 256, "unsupported D");
   constexpr int R = 256 / VPR;       // row groups (threads past R * VPR idle)
   constexpr int RPT = 16;            // rows per thread per pass
   __shared__ double red[R][D + 1];
-  __shared__ float sq[D];
+  __shared__ float sq[D], cv[D];
 
   const int tid = threadIdx.x;
   const int v = tid % VPR;
@@ -348,15 +357,16 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
     if (tid < D) partial[((b * k + cl) * nsplit + sp) * D + tid] = s;
     return;
   }
-  finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, sq);
+  finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, c_sq_out,
+                      sq, cv);
 }
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void centroid_mean_finalize_kernel(
     const double* __restrict__ partial, const int32_t* __restrict__ offsets, const T* __restrict__ old, int64_t n,
     int32_t k, int32_t nsplit, float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max,
-    float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum) {
-  __shared__ float sq[D];
+    float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum, float* __restrict__ c_sq_out) {
+  __shared__ float sq[D], cv[D];
   const int64_t b = blockIdx.y;
   const int32_t cl = blockIdx.x;
   const int32_t* off = offsets + b * (k + 1);
@@ -368,7 +378,8 @@ __global__ __launch_bounds__(256) void centroid_mean_finalize_kernel(
     const double* p = partial + (b * k + cl) * nsplit * D + threadIdx.x;
     for (int sp = 0; sp < nsplit; ++sp) s += p[sp * D];
   }
-  finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, sq);
+  finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, c_sq_out,
+                      sq, cv);
 }
 
 // ---------------------------------------------------------------- exact fp32 assign
@@ -495,7 +506,7 @@ extern "C" size_t spr_centroid_mean_workspace(int64_t batch, int64_t n, int32_t 
 extern "C" int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, const int32_t* offsets,
                                  const void* old, int64_t batch, int64_t n, int32_t k, int32_t d, float* mean32,
                                  void* out, float* shift_max, float* sums_accum, int32_t* counts_accum,
-                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                 float* c_sq_out, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_centroid_mean: bad size");
   SPR_REQUIRE(batch <= 65535, "spr_centroid_mean: batch %lld exceeds 65535", (long long)batch);
   if (batch == 0) return SPR_OK;
@@ -515,11 +526,11 @@ extern "C" int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* so
   do {                                                                                                       \
     centroid_mean_kernel<T, DD><<<grid, 256, 0, stream>>>(                                                   \
         static_cast<const T*>(x), sorted_idx, offsets, static_cast<const T*>(old), n, k, ns, partial, mean32, \
-        static_cast<T*>(out), shift_max, sums_accum, counts_accum);                                          \
+        static_cast<T*>(out), shift_max, sums_accum, counts_accum, c_sq_out);                                \
     if (ns > 1)                                                                                              \
       centroid_mean_finalize_kernel<T, DD><<<fgrid, 256, 0, stream>>>(                                       \
           partial, offsets, static_cast<const T*>(old), n, k, ns, mean32, static_cast<T*>(out), shift_max,   \
-          sums_accum, counts_accum);                                                                         \
+          sums_accum, counts_accum, c_sq_out);                                                               \
   } while (0)
   if (dtype == 0) {
     switch (d) {

@@ -46,41 +46,46 @@ __global__ __launch_bounds__(1024) void label_scan_kernel(int32_t* __restrict__ 
                                                           int32_t nchunks, int32_t* __restrict__ sizes,
                                                           int32_t* __restrict__ offsets) {
   __shared__ int32_t tot[MAX_BINS];
-  __shared__ int32_t part[1024];
+  __shared__ int32_t wsum[16];
+  constexpr int U = 8;  // chunk rows in flight per thread
   const int32_t bins = k + 1;
   const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   int32_t* hrow = hist + row * static_cast<int64_t>(nchunks) * bins;
-  for (int j = threadIdx.x; j < bins; j += blockDim.x) {
+  for (int j = tid; j < bins; j += blockDim.x) {
     int32_t s = 0;
     int c = 0;
-    for (; c + 4 <= nchunks; c += 4) {
-      int32_t a = hrow[(c + 0) * bins + j], b = hrow[(c + 1) * bins + j];
-      int32_t d = hrow[(c + 2) * bins + j], e = hrow[(c + 3) * bins + j];
-      s += a + b + d + e;
+    for (; c + U <= nchunks; c += U) {
+      int32_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = hrow[(c + u) * bins + j];
+#pragma unroll
+      for (int u = 0; u < U; ++u) s += v[u];
     }
     for (; c < nchunks; ++c) s += hrow[c * bins + j];
     tot[j] = s;
   }
   __syncthreads();
-  // exclusive scan of tot[0..bins): contiguous segment per thread
+  // exclusive scan of tot[0..bins): a contiguous segment per thread, segment sums
+  // scanned across the block with wave shuffles
   const int per = (bins + blockDim.x - 1) / blockDim.x;
-  const int lo = threadIdx.x * per;
+  const int lo = tid * per;
   const int hi = lo + per < bins ? lo + per : bins;
   int32_t seg = 0;
   for (int j = lo; j < hi; ++j) seg += tot[j];
-  part[threadIdx.x] = seg;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t run = 0;
-    for (int i = 0; i < static_cast<int>(blockDim.x); ++i) {
-      int32_t v = part[i];
-      part[i] = run;
-      run += v;
-    }
+  int32_t incl = seg;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t up = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += up;
   }
+  if (lane == 63) wsum[wave] = incl;
   __syncthreads();
+  int32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += wsum[w];
   {
-    int32_t run = part[threadIdx.x];
+    int32_t run = before + incl - seg;
     for (int j = lo; j < hi; ++j) {
       int32_t v = tot[j];
       if (sizes != nullptr && j < k) sizes[row * k + j] = v;
@@ -89,21 +94,19 @@ __global__ __launch_bounds__(1024) void label_scan_kernel(int32_t* __restrict__ 
     }
   }
   __syncthreads();
-  for (int j = threadIdx.x; j < bins; j += blockDim.x) {
+  for (int j = tid; j < bins; j += blockDim.x) {
     if (offsets != nullptr) offsets[row * (k + 1) + j] = tot[j];
     int32_t run = tot[j];
     int c = 0;
-    for (; c + 4 <= nchunks; c += 4) {
-      int32_t a = hrow[(c + 0) * bins + j], b = hrow[(c + 1) * bins + j];
-      int32_t d = hrow[(c + 2) * bins + j], e = hrow[(c + 3) * bins + j];
-      hrow[(c + 0) * bins + j] = run;
-      run += a;
-      hrow[(c + 1) * bins + j] = run;
-      run += b;
-      hrow[(c + 2) * bins + j] = run;
-      run += d;
-      hrow[(c + 3) * bins + j] = run;
-      run += e;
+    for (; c + U <= nchunks; c += U) {
+      int32_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = hrow[(c + u) * bins + j];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        hrow[(c + u) * bins + j] = run;
+        run += v[u];
+      }
     }
     for (; c < nchunks; ++c) {
       int32_t a = hrow[c * bins + j];

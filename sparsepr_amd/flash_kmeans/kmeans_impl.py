@@ -107,8 +107,8 @@ def centroid_update_sorted(x: torch.Tensor, labels: torch.Tensor, old: torch.Ten
                            want_mean32: bool = False, want_shift: bool = False,
                            sums_accum: torch.Tensor | None = None,
                            counts_accum: torch.Tensor | None = None,
-                           sorted_idx=None, sizes=None, offsets=None, out: torch.Tensor | None = None
-                           ) -> UpdateResult:
+                           sorted_idx=None, sizes=None, offsets=None, out: torch.Tensor | None = None,
+                           c_sq_out: torch.Tensor | None = None) -> UpdateResult:
     """Cluster means of x under labels; empty clusters keep `old`."""
     dev = _check_x(x, "centroid_update")
     B, N, D = x.shape
@@ -131,8 +131,8 @@ def centroid_update_sorted(x: torch.Tensor, labels: torch.Tensor, old: torch.Ten
     ws = _lib.workspace(ws_bytes, dev) if ws_bytes > 0 else None
     _lib.call("spr_centroid_mean", _lib.ptr(xc), _lib.DTYPE_CODE[x.dtype], _lib.ptr(sorted_idx),
               _lib.ptr(offsets), _lib.ptr(oc), B, N, K, D, _lib.ptr(mean32), _lib.ptr(new),
-              _lib.ptr(shift), _lib.ptr(sums_accum), _lib.ptr(counts_accum), _lib.ptr(ws), ws_bytes,
-              _lib.stream(dev))
+              _lib.ptr(shift), _lib.ptr(sums_accum), _lib.ptr(counts_accum), _lib.ptr(c_sq_out), _lib.ptr(ws),
+              ws_bytes, _lib.stream(dev))
     return UpdateResult(new, sizes, sorted_idx, offsets, mean32, shift)
 
 
@@ -177,14 +177,18 @@ def lloyd(x: torch.Tensor, n_clusters: int, max_iters: int, tol: float = 0.0,
         cached_sq = torch.empty((B, N), dtype=torch.float32, device=dev)
     res = None
     it = -1
+    # centroid norms: computed once, then produced by each update for the next assignment
+    c_sq = centroid_sq(cent) if x.dtype == torch.bfloat16 else None
     for it in range(max_iters):
         if x_sq is None and cached_sq is not None and it > 0:
-            euclid_assign(x, cent, cached_sq, x_sq_mode=x_sq_mode, out=labels)
+            euclid_assign(x, cent, cached_sq, x_sq_mode=x_sq_mode, c_sq=c_sq, out=labels)
         else:
-            euclid_assign(x, cent, x_sq, x_sq_mode=x_sq_mode, out=labels, x_sq_out=cached_sq)
+            euclid_assign(x, cent, x_sq, x_sq_mode=x_sq_mode, c_sq=c_sq, out=labels, x_sq_out=cached_sq)
         sorted_idx, sizes, offsets = argsort_labels(labels, K)
+        next_sq = torch.empty((B, K), dtype=torch.float32, device=dev) if c_sq is not None else None
         res = centroid_update_sorted(x, labels, cent, want_mean32=want_mean32, want_shift=tol > 0 or verbose,
-                                     sorted_idx=sorted_idx, sizes=sizes, offsets=offsets)
+                                     sorted_idx=sorted_idx, sizes=sizes, offsets=offsets, c_sq_out=next_sq)
+        c_sq = next_sq
         if verbose:
             print(f"Iter {it}, center shift: {float(res.shift.item()):.6f}")
         if tol > 0 and float(res.shift.item()) < tol:
