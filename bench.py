@@ -118,7 +118,6 @@ def only_attention(args):
 
     from sparsepr_amd import synthetic
     from sparsepr_amd.kernels.attention import block_sparse_attention, plan_block_sparse
-    from sparsepr_amd.kernels.permute import permute_tensor_by_labels_triton
     from sparsepr_amd.layer import SparsePRAttention, SparsePRConfig, kept_pair_flops
 
     shape = synthetic.HUNYUAN
@@ -126,15 +125,12 @@ def only_attention(args):
     layer = SparsePRAttention(SparsePRConfig(top_p=args.top_p, repair=False))
     route, q_idx = layer.route(q, k, v)
     B, H, N, D = q.shape
-    qp, _ = permute_tensor_by_labels_triton(q, None, 2, sorted_indices=q_idx)
-    qp = qp.reshape(B * H, N, D)
-    kp = route.k_permuted.reshape(B * H, N, D)
-    vp = route.v_permuted.reshape(B * H, N, D)
     plan = plan_block_sparse(route.video_dynamic_map, route.q_cluster_sizes, route.k_cluster_sizes, N)
 
-    def run():
-        return block_sparse_attention(qp, kp, vp, route.video_dynamic_map, route.q_cluster_sizes,
-                                      route.k_cluster_sizes, plan=plan)
+    def run():  # the layer's call: token-order q read through its sort index, cluster-sorted K/V
+        return block_sparse_attention(q.reshape(B * H, N, D), route.k_permuted.reshape(B * H, N, D),
+                                      route.v_permuted.reshape(B * H, N, D), route.video_dynamic_map,
+                                      route.q_cluster_sizes, route.k_cluster_sizes, plan=plan, q_index=q_idx)
 
     for _ in range(args.warmup):
         run()

@@ -144,15 +144,19 @@ int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, 
  * natural log of the scaled sum, -inf for an empty row).  q_index int32 [bh_q, s] (nullable):
  * q, out and lse stay in token order and cluster-sorted row r is token q_index[r], which fuses
  * permute_tensor_by_labels_triton of Q and apply_inverse_permutation_triton of the output
- * (hunyuanvideo.py:189-231) into the attention. */
+ * (hunyuanvideo.py:189-231) into the attention.  k_index int32 [bh_kv, s] (nullable): k and v stay
+ * in token order and cluster-sorted key position p is token k_index[p] (the K/V permutation of
+ * n8_v6.py:905-925 fused into the key gather). */
 int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan, int64_t bh_q,
                                    int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
-                                   const int32_t* q_index, void* out, float* lse, hipStream_t stream);
+                                   const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
+                                   hipStream_t stream);
 /* Plan + run in one call; workspace = plan buffer of spr_block_sparse_attention_workspace bytes. */
 int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,
                                const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q, int64_t bh_kv, int64_t s,
-                               int32_t d, int32_t qn, int32_t kn, float scale, const int32_t* q_index, void* out,
-                               float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                               int32_t d, int32_t qn, int32_t kn, float scale, const int32_t* q_index,
+                               const int32_t* k_index, void* out, float* lse, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
 /* n8_v6.py:1236-1243 dense probe attention (F.scaled_dot_product_attention of the probe
  * rows against every key).  q bf16 [bh_q, m, d], k/v bf16 [bh_kv, s_kv, d]; keys split
  * into nsplit ranges computed in parallel and merged; out [bh_q, m, d] (out_dtype 0 =

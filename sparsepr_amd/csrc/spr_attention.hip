@@ -183,7 +183,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
     int32_t bh_q, int32_t tiles_per_head, float scale_log2, const int32_t* __restrict__ q_index,
-    uint16_t* __restrict__ out, float* __restrict__ lse, int32_t split_len, float* __restrict__ part_o,
+    const int32_t* __restrict__ k_index, uint16_t* __restrict__ out, float* __restrict__ lse, int32_t split_len, float* __restrict__ part_o,
     float* __restrict__ part_ml) {
   constexpr int NT = NW * 64;
   static_assert(NW * QB * 32 == BM, "tile shape");
@@ -303,7 +303,10 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         const int32_t s = seg_of(vpos);
         int32_t delta;
         if constexpr (SEGL) delta = seg_lds[s].delta; else delta = segs[s].delta;
-        key_rows[c % 4][lane] = delta + vpos;
+        // with k_index, cluster-sorted key position p is stored at row k_index[p]
+        // (a bad index only reads zeros: the K/V loads are range-checked)
+        key_rows[c % 4][lane] = k_index != nullptr ? k_index[bhkv * static_cast<int64_t>(s_kv) + delta + vpos]
+                                                   : delta + vpos;
         cur_s = __builtin_amdgcn_readlane(s, 63);
       } else {
         key_rows[c % 4][lane] = dense_k0 + vpos;
@@ -617,11 +620,13 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
 // (nullable, natural log).  bh_q must be a multiple of bh_kv (GQA groups).
 // q_index int32 [bh_q, s] (nullable): q, out and lse stay in token order and
 // cluster-sorted row r is token q_index[r] (the Q permutation and its inverse
-// fused into the attention).
+// fused into the attention).  k_index int32 [bh_kv, s] (nullable): k and v stay
+// in token order and cluster-sorted key position p is token k_index[p] (the K/V
+// permutation fused into the key gather).
 extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan,
                                               int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d, int32_t qn,
-                                              int32_t kn, float scale, const int32_t* q_index, void* out, float* lse,
-                                              hipStream_t stream) {
+                                              int32_t kn, float scale, const int32_t* q_index,
+                                              const int32_t* k_index, void* out, float* lse, hipStream_t stream) {
   SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_run: bad size");
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_block_sparse_attention_run: bh_q=%lld not a multiple of bh_kv=%lld",
               (long long)bh_q, (long long)bh_kv);
@@ -643,7 +648,7 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   attn_fwd_kernel<DD, 0, SL, ATTN_NW, ATTN_QB><<<grid, ATTN_NW * 64, 0, stream>>>(                          \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
-      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index,                     \
+      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index, k_index,            \
       static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr)
   const bool seg_lds = kn <= MAX_LDS_SEGS;
   if (d == 128) {
@@ -660,14 +665,14 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
 extern "C" int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,
                                           const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q,
                                           int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
-                                          const int32_t* q_index, void* out, float* lse, void* workspace,
-                                          size_t workspace_bytes, hipStream_t stream) {
+                                          const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
+                                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (bh_q == 0 || s == 0) return SPR_OK;
   int st = spr_block_sparse_attention_plan(map, q_sizes, k_sizes, bh_kv, s, qn, kn, workspace, workspace_bytes,
                                            stream);
   if (st != SPR_OK) return st;
-  return spr_block_sparse_attention_run(q, k, v, workspace, bh_q, bh_kv, s, d, qn, kn, scale, q_index, out, lse,
-                                        stream);
+  return spr_block_sparse_attention_run(q, k, v, workspace, bh_q, bh_kv, s, d, qn, kn, scale, q_index, k_index,
+                                        out, lse, stream);
 }
 
 extern "C" size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t d, int32_t nsplit) {
@@ -708,7 +713,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_fwd_kernel<128, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
-        scale_log2, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
+        scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                           nsplit, out_dtype, out, lse);
@@ -716,7 +721,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_fwd_kernel<64, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
-        scale_log2, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
+        scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<64><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                          nsplit, out_dtype, out, lse);

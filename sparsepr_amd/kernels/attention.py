@@ -37,12 +37,14 @@ def plan_block_sparse(block_mask_map: torch.Tensor, block_row_sz: torch.Tensor, 
 def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_mask_map: torch.Tensor,
                            block_row_sz: torch.Tensor, block_col_sz: torch.Tensor, *, return_lse: bool = False,
                            plan: torch.Tensor | None = None, scale: float | None = None,
-                           q_index: torch.Tensor | None = None):
+                           q_index: torch.Tensor | None = None, k_index: torch.Tensor | None = None):
     """q [BHq, S, D], k/v [BHkv, S, D] bf16 cluster-contiguous; map [BHkv, Qc, Kc];
     sizes [BHkv, Qc] / [BHkv, Kc].  Returns out [BHq, S, D] (and lse [BHq, S]).
 
     With q_index int32 [BHq, S] (the stable argsort of the query labels), q and
-    the outputs stay in token order: cluster-sorted row r is token q_index[r]."""
+    the outputs stay in token order: cluster-sorted row r is token q_index[r].
+    With k_index int32 [BHkv, S] (the stable argsort of the key labels), k and v
+    stay in token order: cluster-sorted key position p is token k_index[p]."""
     dev = _check_qkv(q, k, v, "block-sparse attention")
     bh_q, s, d = q.shape
     bh_kv = k.shape[0]
@@ -59,11 +61,16 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
         if tuple(q_index.shape) != (bh_q, s):
             raise RuntimeError(f"q_index must have shape {(bh_q, s)}, got {tuple(q_index.shape)}")
         qi = q_index.to(device=dev, dtype=torch.int32).contiguous()
+    ki = None
+    if k_index is not None:
+        if tuple(k_index.shape) != (bh_kv, s):
+            raise RuntimeError(f"k_index must have shape {(bh_kv, s)}, got {tuple(k_index.shape)}")
+        ki = k_index.to(device=dev, dtype=torch.int32).contiguous()
     out = torch.empty_like(qc)
     lse = torch.empty((bh_q, s), dtype=torch.float32, device=dev) if return_lse else None
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(d)
     _lib.call("spr_block_sparse_attention_run", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(plan), bh_q,
-              bh_kv, s, d, qn, kn, sc, _lib.ptr(qi), _lib.ptr(out), _lib.ptr(lse), _lib.stream(dev))
+              bh_kv, s, d, qn, kn, sc, _lib.ptr(qi), _lib.ptr(ki), _lib.ptr(out), _lib.ptr(lse), _lib.stream(dev))
     return (out, lse) if return_lse else out
 
 

@@ -82,8 +82,13 @@ class SparsePRAttention:
             self._init_idx[key] = idx
         return gather_rows(x, idx.unsqueeze(0).expand(bh, -1))
 
-    def route(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, timings: LayerTimings | None = None):
-        """q, k, v [B, H, N, D] bf16 -> (N8V6Route, q sorted indices)."""
+    def route(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, timings: LayerTimings | None = None,
+              *, materialize_kv: bool = True):
+        """q, k, v [B, H, N, D] bf16 -> (N8V6Route, q sorted indices).
+
+        With materialize_kv False the route carries no permuted K/V copies
+        (k_permuted / v_permuted are None): forward() reads K and V through the
+        key sort index instead."""
         cfg = self.config
         _lib.require_gpu(q, k, v, what="SparsePRAttention")
         B, H, N, D = q.shape
@@ -102,10 +107,12 @@ class SparsePRAttention:
         dmap = topp_map(qres.centroids, kres.centroids, kres.sizes, cfg.top_p, cfg.min_kc_ratio)
         if timings is not None:
             timings.mark("select")
-        from .kernels.permute import permute_tensor_by_labels_triton
+        k_perm = v_perm = None
+        if materialize_kv:
+            from .kernels.permute import permute_tensor_by_labels_triton
 
-        k_perm, _ = permute_tensor_by_labels_triton(k, None, 2, sorted_indices=kres.sorted_idx)
-        v_perm, _ = permute_tensor_by_labels_triton(v, None, 2, sorted_indices=kres.sorted_idx)
+            k_perm, _ = permute_tensor_by_labels_triton(k, None, 2, sorted_indices=kres.sorted_idx)
+            v_perm, _ = permute_tensor_by_labels_triton(v, None, 2, sorted_indices=kres.sorted_idx)
         dens = density(dmap, qres.sizes, kres.sizes).mean()  # device scalar: no host sync
         route = N8V6Route(
             q_labels=qres.labels, k_labels=kres.labels, q_cluster_sizes=qres.sizes, k_cluster_sizes=kres.sizes,
@@ -127,6 +134,9 @@ class SparsePRAttention:
             timings.mark("plan")
         # The Q permutation and the output's inverse permutation (hunyuanvideo.py:189-231)
         # are fused into the attention through q_index: q and base stay in token order.
+        # K and V are read from their cluster-sorted copies: contiguous key ranges
+        # keep the key stream's cache locality (gathering them through
+        # k_sorted_indices instead costs more attention time than the copies).
         base = block_sparse_attention(q.reshape(bh, N, D), route.k_permuted.reshape(bh, N, D),
                                       route.v_permuted.reshape(bh, N, D), route.video_dynamic_map,
                                       route.q_cluster_sizes, route.k_cluster_sizes, plan=plan,

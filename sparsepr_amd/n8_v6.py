@@ -158,8 +158,8 @@ class N8V6Route:
     k_cluster_sizes: torch.Tensor
     video_dynamic_map: torch.Tensor
     q_role_features: torch.Tensor
-    k_permuted: torch.Tensor
-    v_permuted: torch.Tensor
+    k_permuted: torch.Tensor | None  # None when the consumer gathers through k_sorted_indices
+    v_permuted: torch.Tensor | None
     k_sorted_indices: torch.Tensor
     base_video_density: float
     q_kmeans_iters: int

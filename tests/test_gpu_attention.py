@@ -214,3 +214,14 @@ def test_q_index_fuses_the_query_permutation(dev, oracle):
     inv = torch.empty_like(qi)
     inv.scatter_(1, qi.long(), torch.arange(s, device=dev, dtype=torch.int32).expand(bh_q, -1).contiguous())
     assert torch.equal(lse, torch.gather(ref_lse, 1, inv.long()))
+    # keys in token order, read through the key sort index
+    bh_kv = k.shape[0]
+    kperm = np.stack([rng.permutation(s) for _ in range(bh_kv)]).astype(np.int32)  # sorted position -> token
+    k_tok = np.empty_like(k)
+    v_tok = np.empty_like(v)
+    for h in range(bh_kv):
+        k_tok[h, kperm[h]] = k[h]
+        v_tok[h, kperm[h]] = v[h]
+    got2 = block_sparse_attention(qd, to_dev(k_tok, dev, torch.bfloat16), to_dev(v_tok, dev, torch.bfloat16),
+                                  *args[2:], q_index=qi, k_index=to_dev(kperm, dev))
+    assert torch.equal(got2, ref)
