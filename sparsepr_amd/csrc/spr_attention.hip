@@ -59,6 +59,18 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// max / sum of x over lanes l and l ^ 32 (v_permlane32_swap exchanges the upper
+// half-wave of one operand with the lower half of the other, so the two results
+// hold x[l] and x[l ^ 32] in some order; max and + are symmetric in them).
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Threshold (log2 units) by which a row maximum must grow before the running
 // output is rescaled; p = 2^(s - m) stays below 2^8 in between.
 constexpr float RESCALE_SLACK = 8.0f;
@@ -175,10 +187,12 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
 // MODE 1: dense split-key for probe rows: q rows [0, m) of a [BHq, m, D] tensor,
 //         keys [split * split_len, ...) of K/V; output unnormalised fp32 partials.
 // NW waves per workgroup, QB 32-row query blocks per wave (NW * QB * 32 = BM).
+// KIDX: keys are gathered through k_index (a compile-time switch, so the plain
+// path carries no global load, and no wait on one, in its chunk planning).
 // QB = 2 runs one wave per SIMD with the output accumulators in AGPRs: every K
 // and V fragment read from LDS then feeds two MFMAs, and each wave carries twice
 // as many independent MFMA chains.
-template <int D, int MODE, bool SEGL, int NW, int QB>
+template <int D, int MODE, bool SEGL, int NW, int QB, bool KIDX>
 __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
@@ -305,8 +319,11 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         if constexpr (SEGL) delta = seg_lds[s].delta; else delta = segs[s].delta;
         // with k_index, cluster-sorted key position p is stored at row k_index[p]
         // (a bad index only reads zeros: the K/V loads are range-checked)
-        key_rows[c % 4][lane] = k_index != nullptr ? k_index[bhkv * static_cast<int64_t>(s_kv) + delta + vpos]
-                                                   : delta + vpos;
+        if constexpr (KIDX) {
+          key_rows[c % 4][lane] = k_index[bhkv * static_cast<int64_t>(s_kv) + delta + vpos];
+        } else {
+          key_rows[c % 4][lane] = delta + vpos;
+        }
         cur_s = __builtin_amdgcn_readlane(s, 63);
       } else {
         key_rows[c % 4][lane] = dense_k0 + vpos;
@@ -382,6 +399,14 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     __syncthreads();
   }
 
+  // Complete the query loads here, on every path into the loop, so that no wait
+  // for them is left to the loop body (where it would also drain the loads of
+  // the next chunk, which share the in-order counter).
+#pragma unroll
+  for (int j = 0; j < QB; ++j) {
+#pragma unroll
+    for (int s = 0; s < T::KSTEPS; ++s) asm volatile("" ::"v"(qf[j][s].x), "v"(qf[j][s].y), "v"(qf[j][s].z), "v"(qf[j][s].w));
+  }
   const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
   // Per chunk: K of chunk c + 1 is fetched at the top and stashed after the
   // first 32-key half (its LDS buffer is free since the last barrier), then V of
@@ -430,7 +455,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         float mx = -__builtin_huge_valf();
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_acc[j][e]);
-        mloc[j] = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+        mloc[j] = max_xor32(mx) * scale_log2;
         grow = grow || (mloc[j] > m_run[j] + RESCALE_SLACK);
       }
       // Rescale lazily: only when some row's maximum grew by more than the slack.
@@ -498,7 +523,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   // ---- epilogue
 #pragma unroll
   for (int j = 0; j < QB; ++j) {
-    const float l_tot = l_run[j] + __shfl_xor(l_run[j], 32, 64);
+    const float l_tot = sum_xor32(l_run[j]);
     if constexpr (MODE == 0) {
       const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
       if (row_live[j]) {
@@ -644,12 +669,20 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   dim3 grid(static_cast<uint32_t>(blocks));
   const int32_t group = static_cast<int32_t>(bh_q / bh_kv);
   const float scale_log2 = scale * 1.4426950408889634f;
-#define SPR_ATTN(DD, SL)                                                                                      \
-  attn_fwd_kernel<DD, 0, SL, ATTN_NW, ATTN_QB><<<grid, ATTN_NW * 64, 0, stream>>>(                          \
+#define SPR_ATTN2(DD, SL, KX)                                                                                 \
+  attn_fwd_kernel<DD, 0, SL, ATTN_NW, ATTN_QB, KX><<<grid, ATTN_NW * 64, 0, stream>>>(                      \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
       static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index, k_index,            \
       static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr)
+#define SPR_ATTN(DD, SL)               \
+  do {                                 \
+    if (k_index != nullptr) {          \
+      SPR_ATTN2(DD, SL, true);         \
+    } else {                           \
+      SPR_ATTN2(DD, SL, false);        \
+    }                                  \
+  } while (0)
   const bool seg_lds = kn <= MAX_LDS_SEGS;
   if (d == 128) {
     if (seg_lds) SPR_ATTN(128, true); else SPR_ATTN(128, false);
@@ -657,6 +690,7 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
     if (seg_lds) SPR_ATTN(64, true); else SPR_ATTN(64, false);
   }
 #undef SPR_ATTN
+#undef SPR_ATTN2
   SPR_LAUNCHED("attn_fwd_kernel");
   return SPR_OK;
 }
@@ -710,7 +744,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
   const int64_t rows_total = bh_q * m;
   const uint32_t cblocks = static_cast<uint32_t>(spr::ceil_div(rows_total * (d / 4), 256));
   if (d == 128) {
-    attn_fwd_kernel<128, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
+    attn_fwd_kernel<128, 1, false, 4, 1, false><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
         scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
@@ -718,7 +752,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                           nsplit, out_dtype, out, lse);
   } else {
-    attn_fwd_kernel<64, 1, false, 4, 1><<<grid, THREADS, 0, stream>>>(
+    attn_fwd_kernel<64, 1, false, 4, 1, false><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
         scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml);

@@ -238,33 +238,39 @@ __global__ __launch_bounds__(256) void density_kernel(const uint8_t* __restrict_
                                                       const int32_t* __restrict__ q_sizes,
                                                       const int32_t* __restrict__ k_sizes, int32_t qn,
                                                       int32_t kn, float* __restrict__ out) {
-  __shared__ long long part[256];
-  __shared__ long long qtot[256];
-  __shared__ long long ktot[256];
+  __shared__ long long red[3][4];
   const int64_t h = blockIdx.x;
+  const int tid = threadIdx.x;
   const uint8_t* m = map + h * qn * static_cast<int64_t>(kn);
   const int32_t* qs = q_sizes + h * qn;
   const int32_t* ks = k_sizes + h * kn;
   long long kept = 0, qsum = 0, ksum = 0;
-  for (int i = threadIdx.x; i < qn; i += blockDim.x) qsum += qs[i];
-  for (int j = threadIdx.x; j < kn; j += blockDim.x) ksum += ks[j];
-  for (int64_t e = threadIdx.x; e < static_cast<int64_t>(qn) * kn; e += blockDim.x) {
-    if (m[e]) {
-      const int i = static_cast<int>(e / kn);
-      const int j = static_cast<int>(e - static_cast<int64_t>(i) * kn);
-      kept += static_cast<long long>(qs[i]) * ks[j];
-    }
+  for (int i = tid; i < qn; i += blockDim.x) qsum += qs[i];
+  for (int j = tid; j < kn; j += blockDim.x) ksum += ks[j];
+  // thread t owns columns t, t + 256, ...: per row, the kept key mass times the row's size
+  for (int i = 0; i < qn; ++i) {
+    const uint8_t* row = m + static_cast<int64_t>(i) * kn;
+    long long rs = 0;
+    for (int j = tid; j < kn; j += blockDim.x) rs += row[j] ? ks[j] : 0;
+    kept += rs * qs[i];
   }
-  part[threadIdx.x] = kept;
-  qtot[threadIdx.x] = qsum;
-  ktot[threadIdx.x] = ksum;
+  for (int o = 32; o > 0; o >>= 1) {
+    kept += __shfl_xor(kept, o, 64);
+    qsum += __shfl_xor(qsum, o, 64);
+    ksum += __shfl_xor(ksum, o, 64);
+  }
+  if ((tid & 63) == 0) {
+    red[0][tid >> 6] = kept;
+    red[1][tid >> 6] = qsum;
+    red[2][tid >> 6] = ksum;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     long long a = 0, b = 0, c = 0;
-    for (int t = 0; t < static_cast<int>(blockDim.x); ++t) {
-      a += part[t];
-      b += qtot[t];
-      c += ktot[t];
+    for (int w = 0; w < static_cast<int>(blockDim.x) / 64; ++w) {
+      a += red[0][w];
+      b += red[1][w];
+      c += red[2][w];
     }
     const double all = static_cast<double>(b) * static_cast<double>(c);
     out[h] = all > 0.0 ? static_cast<float>(static_cast<double>(a) / all) : 0.0f;
