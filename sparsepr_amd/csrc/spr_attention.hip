@@ -45,7 +45,7 @@ struct Seg {
   int32_t vend;
 };
 
-constexpr int MAX_LDS_SEGS = 1024;  // segment lists up to this length are staged in LDS
+constexpr int MAX_LDS_SEGS = 768;  // segment lists up to this length are staged in LDS
 #ifndef ATTN_NW
 #define ATTN_NW 4  // block-sparse kernel: waves per workgroup
 #define ATTN_QB 1  //                      32-row query blocks per wave
@@ -71,6 +71,11 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Column of chunk key p in a V^T row: bits 2 and 3 of p swapped, so the keys
+// 16t + 4h + {0..3} and 16t + 8 + 4h + {0..3} of one MFMA A fragment (lane half
+// h, k-step t) sit in the 8 consecutive columns 16t + 8h + {0..7}.
+__device__ __forceinline__ int v_col(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
+
 // Threshold (log2 units) by which a row maximum must grow before the running
 // output is rescaled; p = 2^(s - m) stays below 2^8 in between.
 constexpr float RESCALE_SLACK = 8.0f;
@@ -80,8 +85,8 @@ struct Tile {
   static constexpr int KSTEPS = D / 16;
   static constexpr int DBLK = D / 32;
   static constexpr int K_ROW = D * 2 + 16;   // bytes per key row of the K tile (+16 pad)
-  static constexpr int V_ROW = BN * 2 + 8;   // bytes per dim row of the V^T tile (+8 pad: 32 rows hit
-                                             // 32 distinct even banks, so 64-bit reads are conflict-free)
+  static constexpr int V_ROW = BN * 2 + 16;  // bytes per dim row of the V^T tile (+16 pad: 8 consecutive
+                                             // rows cover all 32 banks, so 128-bit reads are conflict-free)
   static constexpr int K_BYTES = BN * K_ROW;
   static constexpr int V_BYTES = D * V_ROW;
   static constexpr int K_PIECES = BN * D / 8 / NTHREADS;       // 16-byte K pieces per thread
@@ -368,6 +373,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   };
   auto stash_v = [&](int buf) {
     const int rp = tid % (BN / 2);
+    const int vc = v_col(2 * rp);  // keys 2rp, 2rp + 1 land in columns vc, vc + 1
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
       const int pc = tid / (BN / 2) + i * (NT / (BN / 2));
@@ -378,8 +384,8 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         // dims pc*8 + 2w (low halves of a, b) and pc*8 + 2w + 1 (high halves)
         const uint32_t lo = __builtin_amdgcn_perm(b[w], a[w], 0x05040100u);
         const uint32_t hi = __builtin_amdgcn_perm(b[w], a[w], 0x07060302u);
-        *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w) * T::V_ROW + rp * 4]) = lo;
-        *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w + 1) * T::V_ROW + rp * 4]) = hi;
+        *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w) * T::V_ROW + vc * 2]) = lo;
+        *reinterpret_cast<uint32_t*>(&v_tile[buf][(pc * 8 + 2 * w + 1) * T::V_ROW + vc * 2]) = hi;
       }
     }
   };
@@ -498,10 +504,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         const int t = kbk * 2 + tt;
 #pragma unroll
         for (int b = 0; b < T::DBLK; ++b) {
-          const uint8_t* vrow_p = &v_tile[buf][(b * 32 + col) * T::V_ROW];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow_p + (16 * t + 4 * half) * 2);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow_p + (16 * t + 8 + 4 * half) * 2);
-          const u32x4 a = u32x4{lo.x, lo.y, hi.x, hi.y};
+          const u32x4 a = *reinterpret_cast<const u32x4*>(&v_tile[buf][(b * 32 + col) * T::V_ROW + (16 * t + 8 * half) * 2]);
 #pragma unroll
           for (int j = 0; j < QB; ++j) {
             const u32x4 bfrag = u32x4{pf[j][tt][0], pf[j][tt][1], pf[j][tt][2], pf[j][tt][3]};
