@@ -571,6 +571,287 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------- block-sparse, D = 128, LDS DMA
+// The same work items, plan walk and online softmax as attn_fwd_kernel MODE 0,
+// with K and V chunks copied from HBM straight into LDS (buffer_load ... lds,
+// 16 bytes a lane, 1 KB per wave instruction) a whole chunk ahead: no staging
+// registers, no staging work in the wave's instruction stream.
+//
+// Tiles hold 64 key rows of 256 bytes, row-major; the sixteen 16-byte pieces of
+// row r are XOR-swizzled: piece j sits at slot j ^ (r & 7) in the K tile (the
+// S^T A fragments, 128-bit reads of 8 consecutive rows, hit 32 distinct banks)
+// and at slot j ^ 2(r & 3) in the V tile.  V^T fragments come from the
+// transposing read ds_read_b64_tr_b16: in each group of 16 lanes, output lane
+// 4A + B receives element B of the 8-byte reads of lanes A, A + 4, A + 8 and
+// A + 12.  Lane s of group g (A = s % 4, i = s / 4 within the group) therefore
+// reads row 16t + 8r + 4h + i, dims 32b + 16(g & 1) + 4A, and output lane
+// (dim d, half h) receives keys 16t + 8r + 4h + {0..3} of dim d: read r = 0, 1
+// give the two 4-key halves of the A fragment in the key order the S^T
+// accumulator produces (key(t, h, e) = 16t + 8(e/4) + 4h + e%4).  The 4 rows x
+// 2 pieces each 16-lane group reads map to 8 distinct bank groups.
+constexpr int DROW = 256;         // bytes per key row (D = 128)
+constexpr int DTILE = BN * DROW;  // bytes per K or V chunk tile
+
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+#endif
+}
+
+struct alignas(8) u32x2 {
+  uint32_t x, y;
+};
+
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint8_t* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(p)));
+#else
+  return u32x2{0, 0};
+#endif
+}
+
+template <bool SEGL, bool KIDX>
+__global__ __launch_bounds__(THREADS, 2) void attn_dma_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int32_t s_q,
+    int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan, int32_t bh_q,
+    int32_t tiles_per_head, float scale_log2, const int32_t* __restrict__ q_index,
+    const int32_t* __restrict__ k_index, uint16_t* __restrict__ out, float* __restrict__ lse) {
+  constexpr int D = 128;
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBLK = D / 32;
+  __shared__ __attribute__((aligned(1024))) uint8_t k_tile0[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_tile1[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_tile0[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_tile1[DTILE];
+  __shared__ int32_t key_rows[4][BN];
+  __shared__ Seg seg_lds[SEGL ? MAX_LDS_SEGS : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  // ---- work item: XCD-grouped tile order, as in attn_fwd_kernel MODE 0
+  const int64_t per_xcd = gridDim.x / 8;
+  const int64_t logical = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int64_t bhq = logical / tiles_per_head;
+  const int32_t tile = static_cast<int32_t>(logical - bhq * tiles_per_head);
+  if (bhq >= bh_q) return;
+  const int64_t bhkv = bhq / group;
+  PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
+  if (tile >= pv.tile_off[qn]) return;
+  int lo = 0, hi = qn;  // largest i with tile_off[i] <= tile
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (pv.tile_off[mid] <= tile) lo = mid; else hi = mid;
+  }
+  const int qc = lo;
+  const int32_t row0 = pv.q_off[qc] + (tile - pv.tile_off[qc]) * BM;
+  const int32_t row1 = min(row0 + BM, pv.q_off[qc + 1]);
+  const Seg* segs = pv.segs + static_cast<int64_t>(qc) * kn;
+  const int32_t nseg = pv.nseg[qc];
+  const int32_t total = pv.total[qc];
+
+  const uint16_t* qb = q + bhq * static_cast<int64_t>(s_q) * D;
+  const int32_t kv_bytes = s_kv * D * 2;
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(k + bhkv * static_cast<int64_t>(s_kv) * D), 0, kv_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(v + bhkv * static_cast<int64_t>(s_kv) * D), 0, kv_bytes, 0x00020000);
+  if constexpr (SEGL) {
+    for (int i = tid; i < nseg; i += THREADS) seg_lds[i] = segs[i];
+  }
+
+  // ---- this lane's query row as MFMA B fragments over the head dim
+  int32_t my_row = row0 + wave * 32 + col;
+  bool row_live = my_row < row1;
+  if (q_index != nullptr && row_live) {
+    my_row = q_index[bhq * static_cast<int64_t>(s_q) + my_row];
+    row_live = my_row >= 0 && my_row < s_q;
+  }
+  u32x4 qf[KSTEPS];
+#pragma unroll
+  for (int s = 0; s < KSTEPS; ++s) {
+    qf[s] = row_live ? *reinterpret_cast<const u32x4*>(qb + static_cast<int64_t>(my_row) * D + s * 16 + half * 8)
+                     : u32x4{0, 0, 0, 0};
+  }
+  spr::f32x16 o_acc[DBLK];
+#pragma unroll
+  for (int b = 0; b < DBLK; ++b) o_acc[b] = spr::f32x16{};
+  float m_run = -__builtin_huge_valf();
+  float l_run = 0.0f;
+
+  const int nch = (total + BN - 1) / BN;
+
+  // Key rows of each chunk, planned three chunks ahead by wave 0 (ring of 4), as
+  // in attn_fwd_kernel; positions past the end repeat the last key (masked).
+  int32_t cur_s = 0;
+  auto plan_chunk = [&](int c) {
+    if (wave == 0) {
+      const int32_t vpos = min(c * BN + lane, total - 1);
+      int32_t s = cur_s;
+      if constexpr (SEGL) {
+        while (s < nseg - 1 && vpos >= seg_lds[s].vend) ++s;
+      } else {
+        while (s < nseg - 1 && vpos >= segs[s].vend) ++s;
+      }
+      int32_t delta;
+      if constexpr (SEGL) delta = seg_lds[s].delta; else delta = segs[s].delta;
+      if constexpr (KIDX) {
+        key_rows[c % 4][lane] = k_index[bhkv * static_cast<int64_t>(s_kv) + delta + vpos];
+      } else {
+        key_rows[c % 4][lane] = delta + vpos;
+      }
+      cur_s = __builtin_amdgcn_readlane(s, 63);
+    }
+  };
+
+  // DMA of one chunk: wave w, instruction i fills tile rows 4w + 16i .. + 3.
+  int32_t krow[4];
+  auto load_rows = [&](int c) {
+    const int32_t* kr = key_rows[c % 4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) krow[i] = kr[4 * wave + 16 * i + (lane >> 4)];
+  };
+  auto dma = [&](uint8_t* kt, uint8_t* vt) {
+    const int slot = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r0 = 4 * wave + 16 * i;
+      const int row = r0 + (lane >> 4);
+      const int32_t off = krow[i] * DROW;
+      lds_dma16(k_rsrc, kt + r0 * DROW, off + ((slot ^ (row & 7)) << 4));
+      lds_dma16(v_rsrc, vt + r0 * DROW, off + ((slot ^ ((row & 3) << 1)) << 4));
+    }
+  };
+
+  // lane-constant parts of the fragment addresses
+  const int k_x = half ^ (col & 7);  // K: piece 2s + half of row 32kbk + col sits at slot 2s ^ k_x
+  const int tr_a = lane & 3, tr_i = (lane >> 2) & 3, tr_g = (lane >> 4) & 1;
+  const int v_lane = (4 * half + tr_i) * DROW + (tr_a & 1) * 8;  // row 4h + i, byte within piece
+  const int v_piece = 2 * tr_g + (tr_a >> 1);                    // piece of block b: 4b + v_piece
+  const int v_x = 2 * tr_i;                                        // slot = piece ^ v_x
+
+  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  auto chunk = [&](int c, const uint8_t* kt, const uint8_t* vt, uint8_t* kt_next, uint8_t* vt_next) {
+    if (c + 1 < nch) dma(kt_next, vt_next);  // rows of chunk c + 1, read during chunk c - 1
+    if (c + 2 < nch) load_rows(c + 2);
+    const int32_t left = total - c * BN;  // keys past the end exist only in the last chunk
+#pragma unroll
+    for (int kbk = 0; kbk < 2; ++kbk) {
+      spr::f32x16 s_acc = spr::f32x16{};
+      {
+        const uint8_t* arow = kt + (kbk * 32 + col) * DROW;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(arow + (((2 * s) ^ k_x) << 4));
+          s_acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[s]), s_acc, 0, 0, 0);
+        }
+      }
+      if (kbk == 0 && c + 3 < nch) plan_chunk(c + 3);
+      if (left < BN) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kbk * 32 + 8 * (e / 4) + 4 * half + (e % 4);
+          if (key >= left) s_acc[e] = -__builtin_huge_valf();
+        }
+      }
+      float mx = -__builtin_huge_valf();
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_acc[e]);
+      const float mloc = max_xor32(mx) * scale_log2;
+      // Rescale lazily: only when some row's maximum grew by more than the slack.
+      if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
+        }
+        m_run = m_new;
+      }
+      uint32_t pf[2][4];  // P of this half as bf16 pairs: [k-step][dword]
+      {
+        const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
+        // The row sum adds the bf16-rounded probabilities that also weight V.
+        float lsum0 = 0.0f, lsum1 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[e], scale_log2, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[e + 1], scale_log2, neg_m));
+          const uint32_t pk = pack2(p0, p1);
+          pf[e / 8][(e % 8) / 2] = pk;
+          if (e % 4 == 0) {
+            lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+          } else {
+            lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+          }
+        }
+        l_run += lsum0 + lsum1;
+      }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int t = kbk * 2 + tt;
+        const uint8_t* vrow = vt + 16 * t * DROW + v_lane;
+        const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b) {
+          const int slot = ((4 * b + v_piece) ^ v_x) << 4;
+          const u32x2 r0 = lds_read_tr16(vrow + slot);
+          const u32x2 r1 = lds_read_tr16(vrow + 8 * DROW + slot);
+          const u32x4 a = u32x4{r0.x, r0.y, r1.x, r1.y};
+          o_acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag), o_acc[b], 0, 0,
+                                                             0);
+        }
+      }
+    }
+    __syncthreads();  // waits for this wave's DMA of chunk c + 1, and frees the tiles of chunk c
+  };
+
+  if (nch > 0) {
+    if constexpr (SEGL) __syncthreads();  // staged segment list visible to wave 0
+    plan_chunk(0);
+    if (nch > 1) plan_chunk(1);
+    if (nch > 2) plan_chunk(2);
+    __syncthreads();
+    load_rows(0);
+    dma(k_tile0, v_tile0);
+    if (nch > 1) load_rows(1);
+    __syncthreads();
+  }
+  for (int c = 0; c < nch; c += 2) {
+    chunk(c, k_tile0, v_tile0, k_tile1, v_tile1);
+    if (c + 1 < nch) chunk(c + 1, k_tile1, v_tile1, k_tile0, v_tile0);
+  }
+
+  // ---- epilogue
+  const float l_tot = sum_xor32(l_run);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (row_live) {
+    uint16_t* orow = out + (bhq * static_cast<int64_t>(s_q) + my_row) * D;
+#pragma unroll
+    for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = b * 32 + 8 * i + 4 * half;
+        uint2 w;
+        w.x = pack2(o_acc[b][4 * i] * inv, o_acc[b][4 * i + 1] * inv);
+        w.y = pack2(o_acc[b][4 * i + 2] * inv, o_acc[b][4 * i + 3] * inv);
+        *reinterpret_cast<uint2*>(orow + d0) = w;
+      }
+    }
+    if (lse != nullptr && half == 0) {
+      lse[bhq * static_cast<int64_t>(s_q) + my_row] =
+          l_tot > 0.0f ? (m_run + __builtin_amdgcn_logf(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
+    }
+  }
+}
+
 // Merge split-key partials: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
 // One thread per (bhq, row, 4 dims).  out_dtype 0 = bf16, 2 = fp32.
 template <int D>
@@ -687,13 +968,24 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
     }                                  \
   } while (0)
   const bool seg_lds = kn <= MAX_LDS_SEGS;
+#define SPR_DMA(SL, KX)                                                                                       \
+  attn_dma_kernel<SL, KX><<<grid, THREADS, 0, stream>>>(                                                        \
+      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
+      static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
+      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index, k_index,            \
+      static_cast<uint16_t*>(out), lse)
   if (d == 128) {
-    if (seg_lds) SPR_ATTN(128, true); else SPR_ATTN(128, false);
+    if (k_index != nullptr) {
+      if (seg_lds) SPR_DMA(true, true); else SPR_DMA(false, true);
+    } else {
+      if (seg_lds) SPR_DMA(true, false); else SPR_DMA(false, false);
+    }
   } else {
     if (seg_lds) SPR_ATTN(64, true); else SPR_ATTN(64, false);
   }
 #undef SPR_ATTN
 #undef SPR_ATTN2
+#undef SPR_DMA
   SPR_LAUNCHED("attn_fwd_kernel");
   return SPR_OK;
 }
