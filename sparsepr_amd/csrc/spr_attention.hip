@@ -98,15 +98,16 @@ struct Tile {
 
 // Workspace layout per kv head (int32 units), see plan_words().
 struct PlanView {
-  int32_t* q_off;     // [Qc + 1]
-  int32_t* tile_off;  // [Qc + 1]
-  int32_t* nseg;      // [Qc]
+  int32_t* q_off;      // [Qc + 1]
+  int32_t* tile_off;   // [Qc + 1] first BM-row tile of each q-cluster
+  int32_t* tile2_off;  // [Qc + 1] first 2*BM-row tile of each q-cluster
+  int32_t* nseg;       // [Qc]
   int32_t* total;     // [Qc]
   Seg* segs;          // [Qc][Kc]
 };
 
 __host__ __device__ inline int64_t plan_words(int32_t qn, int32_t kn) {
-  return 2 * (int64_t)(qn + 1) + 2 * (int64_t)qn + 2 * (int64_t)qn * kn;
+  return 3 * (int64_t)(qn + 1) + 2 * (int64_t)qn + 2 * (int64_t)qn * kn;
 }
 
 __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn, int32_t kn) {
@@ -114,7 +115,8 @@ __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn
   PlanView v;
   v.q_off = p;
   v.tile_off = p + (qn + 1);
-  v.nseg = p + 2 * (qn + 1);
+  v.tile2_off = p + 2 * (qn + 1);
+  v.nseg = p + 3 * (qn + 1);
   v.total = v.nseg + qn;
   v.segs = reinterpret_cast<Seg*>(v.total + qn);
   return v;
@@ -136,16 +138,19 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
       run = min(run + max(ks[j], 0), s_rows);
     }
     k_off[kn] = run;
-    int32_t qrun = 0, trun = 0;
+    int32_t qrun = 0, trun = 0, trun2 = 0;
     for (int i = 0; i < qn; ++i) {
       pv.q_off[i] = qrun;
       pv.tile_off[i] = trun;
+      pv.tile2_off[i] = trun2;
       const int32_t next = min(qrun + max(qs[i], 0), s_rows);
       trun += (next - qrun + BM - 1) / BM;
+      trun2 += (next - qrun + 2 * BM - 1) / (2 * BM);
       qrun = next;
     }
     pv.q_off[qn] = qrun;
     pv.tile_off[qn] = trun;
+    pv.tile2_off[qn] = trun2;
   }
   __syncthreads();
   // one wave per q-cluster row: ascending compaction of kept, non-empty k-clusters
@@ -612,8 +617,12 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint8_t* p) {
 #endif
 }
 
-template <bool SEGL, bool KIDX>
-__global__ __launch_bounds__(THREADS, 2) void attn_dma_kernel(
+// NW = 4: 128 query rows per workgroup, two workgroups per CU; NW = 8: 256 rows,
+// one workgroup per CU whose eight waves share each K/V chunk (half the HBM/L2
+// traffic and DMA issue per query row).  Waves whose 32 rows all lie past the
+// tile's end keep the chunk's DMA and barriers and skip its compute.
+template <int NW, bool SEGL, bool KIDX>
+__global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int32_t s_q,
     int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan, int32_t bh_q,
     int32_t tiles_per_head, float scale_log2, const int32_t* __restrict__ q_index,
@@ -621,6 +630,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_dma_kernel(
   constexpr int D = 128;
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
+  constexpr int NT = NW * 64;
+  constexpr int TBM = NW * 32;              // query rows per workgroup
+  constexpr int DMA_PER_WAVE = 16 / NW;     // 1 KB (4-row) DMA instructions per wave per tile
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   __shared__ __attribute__((aligned(1024))) uint8_t k_tile0[DTILE];
   __shared__ __attribute__((aligned(1024))) uint8_t k_tile1[DTILE];
   __shared__ __attribute__((aligned(1024))) uint8_t v_tile0[DTILE];
@@ -642,15 +655,17 @@ __global__ __launch_bounds__(THREADS, 2) void attn_dma_kernel(
   if (bhq >= bh_q) return;
   const int64_t bhkv = bhq / group;
   PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
-  if (tile >= pv.tile_off[qn]) return;
-  int lo = 0, hi = qn;  // largest i with tile_off[i] <= tile
+  const int32_t* toff = NW == 8 ? pv.tile2_off : pv.tile_off;
+  if (tile >= toff[qn]) return;
+  int lo = 0, hi = qn;  // largest i with toff[i] <= tile
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
-    if (pv.tile_off[mid] <= tile) lo = mid; else hi = mid;
+    if (toff[mid] <= tile) lo = mid; else hi = mid;
   }
   const int qc = lo;
-  const int32_t row0 = pv.q_off[qc] + (tile - pv.tile_off[qc]) * BM;
-  const int32_t row1 = min(row0 + BM, pv.q_off[qc + 1]);
+  const int32_t row0 = pv.q_off[qc] + (tile - toff[qc]) * TBM;
+  const int32_t row1 = min(row0 + TBM, pv.q_off[qc + 1]);
+  const bool wave_live = row0 + 32 * wave < row1;
   const Seg* segs = pv.segs + static_cast<int64_t>(qc) * kn;
   const int32_t nseg = pv.nseg[qc];
   const int32_t total = pv.total[qc];
@@ -662,7 +677,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_dma_kernel(
   const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(v + bhkv * static_cast<int64_t>(s_kv) * D), 0, kv_bytes, 0x00020000);
   if constexpr (SEGL) {
-    for (int i = tid; i < nseg; i += THREADS) seg_lds[i] = segs[i];
+    for (int i = tid; i < nseg; i += NT) seg_lds[i] = segs[i];
   }
 
   // ---- this lane's query row as MFMA B fragments over the head dim
@@ -709,18 +724,18 @@ __global__ __launch_bounds__(THREADS, 2) void attn_dma_kernel(
     }
   };
 
-  // DMA of one chunk: wave w, instruction i fills tile rows 4w + 16i .. + 3.
-  int32_t krow[4];
+  // DMA of one chunk: wave w, instruction i fills tile rows 4w + 4 NW i .. + 3.
+  int32_t krow[DMA_PER_WAVE];
   auto load_rows = [&](int c) {
     const int32_t* kr = key_rows[c % 4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) krow[i] = kr[4 * wave + 16 * i + (lane >> 4)];
+    for (int i = 0; i < DMA_PER_WAVE; ++i) krow[i] = kr[4 * wave + 4 * NW * i + (lane >> 4)];
   };
   auto dma = [&](uint8_t* kt, uint8_t* vt) {
     const int slot = lane & 15;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r0 = 4 * wave + 16 * i;
+    for (int i = 0; i < DMA_PER_WAVE; ++i) {
+      const int r0 = 4 * wave + 4 * NW * i;
       const int row = r0 + (lane >> 4);
       const int32_t off = krow[i] * DROW;
       lds_dma16(k_rsrc, kt + r0 * DROW, off + ((slot ^ (row & 7)) << 4));
@@ -740,6 +755,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_dma_kernel(
     if (c + 1 < nch) dma(kt_next, vt_next);  // rows of chunk c + 1, read during chunk c - 1
     if (c + 2 < nch) load_rows(c + 2);
     const int32_t left = total - c * BN;  // keys past the end exist only in the last chunk
+    if (!wave_live) {  // (never wave 0, which plans the chunks)
+      __syncthreads();
+      return;
+    }
 #pragma unroll
     for (int kbk = 0; kbk < 2; ++kbk) {
       spr::f32x16 s_acc = spr::f32x16{};
@@ -968,11 +987,16 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
     }                                  \
   } while (0)
   const bool seg_lds = kn <= MAX_LDS_SEGS;
+#ifndef ATTN_DMA_NW
+#define ATTN_DMA_NW 8
+#endif
+  const int64_t max_tiles_dma = spr::ceil_div(s, ATTN_DMA_NW * 32) + qn;
+  dim3 grid_dma(static_cast<uint32_t>(spr::ceil_div(max_tiles_dma * bh_q, 8) * 8));
 #define SPR_DMA(SL, KX)                                                                                       \
-  attn_dma_kernel<SL, KX><<<grid, THREADS, 0, stream>>>(                                                        \
+  attn_dma_kernel<ATTN_DMA_NW, SL, KX><<<grid_dma, ATTN_DMA_NW * 64, 0, stream>>>(                            \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
-      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index, k_index,            \
+      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles_dma), scale_log2, q_index, k_index,        \
       static_cast<uint16_t*>(out), lse)
   if (d == 128) {
     if (k_index != nullptr) {
