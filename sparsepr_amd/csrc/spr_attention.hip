@@ -11,23 +11,28 @@
 // permuted layout).  A query row of q-cluster a attends every key of every
 // k-cluster c with map[a, c]; empty rows output 0 (lse -inf).
 //
-// Plan (one workgroup per kv head): cluster offsets, 128-row tiles per
+// Plan (one workgroup per kv head): cluster offsets, 128- and 256-row tiles per
 // q-cluster, and for every q-cluster the ascending list of kept non-empty
-// k-cluster key ranges ("segments").  The attention kernel walks a q-cluster's
+// k-cluster key ranges ("segments").  The attention kernels walk a q-cluster's
 // segments as one virtual key sequence in 64-key chunks, so cluster tails cost
 // no MFMA work.
 //
-// Per workgroup: 128 query rows of one q-cluster, 4 waves x 32 rows.
+// Every wave owns 32 query rows of one q-cluster:
 //   S^T[key, q] = K Q^T : A = 32 keys x 16 dims from the K tile in LDS, B = the
 //                         wave's 32 query rows (registers, loaded once).
-//   O^T[d, q]  += V^T P^T: A = 32 dims x 16 keys from the transposed V tile, B = P
-//                         straight from the S^T accumulator (bf16), so a lane owns
-//                         one query row for S, P and O: the row max/sum needs one
+//   O^T[d, q]  += V^T P^T: A = 32 dims x 16 keys of V^T from LDS, B = P straight
+//                         from the S^T accumulator (bf16), so a lane owns one
+//                         query row for S, P and O: the row max/sum needs one
 //                         exchange with lane l ^ 32 and nothing else.
 // The key order inside a 16-key MFMA step is permuted consistently in P and V
 // (key(t, h, e) = 16t + 8(e/4) + 4h + e%4), which makes P a plain slice of the
-// accumulator.  K/V tiles are double-buffered in LDS; the next chunk's rows are
-// fetched into registers while the current chunk computes.
+// accumulator.
+//
+// Kernels: attn_pipe_kernel (D = 128 block-sparse: 256-row tiles, K/V DMA'd
+// into swizzled LDS tiles, next-S/softmax pipelining) and attn_fwd_kernel
+// (D = 64 block-sparse and the dense probe attention: 128-row tiles, K/V
+// staged through registers into a padded K tile and a transposed V tile,
+// double-buffered, the next chunk fetched while the current one computes).
 #include "spr_common.h"
 
 namespace {
@@ -576,16 +581,16 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------- block-sparse, D = 128, LDS DMA
-// The same work items, plan walk and online softmax as attn_fwd_kernel MODE 0,
-// with K and V chunks copied from HBM straight into LDS (buffer_load ... lds,
-// 16 bytes a lane, 1 KB per wave instruction) a whole chunk ahead: no staging
-// registers, no staging work in the wave's instruction stream.
+// ---------------------------------------------------------------------------- block-sparse, D = 128: LDS layout
+// K and V chunks are copied from HBM straight into LDS (buffer_load ... lds, 16
+// bytes a lane, 1 KB per wave instruction): no staging registers and no staging
+// work in the waves' instruction streams.
 //
 // Tiles hold 64 key rows of 256 bytes, row-major; the sixteen 16-byte pieces of
-// row r are XOR-swizzled: piece j sits at slot j ^ (r & 7) in the K tile (the
-// S^T A fragments, 128-bit reads of 8 consecutive rows, hit 32 distinct banks)
-// and at slot j ^ 2(r & 3) in the V tile.  V^T fragments come from the
+// row r are XOR-swizzled for the 64 four-byte LDS banks: piece j sits at slot
+// j ^ (r & 15) in the K tile (the S^T A fragments, 128-bit reads of 16
+// consecutive rows per cycle, cover all 64 banks) and at slot j ^ 4(r & 3) in
+// the V tile.  V^T fragments come from the
 // transposing read ds_read_b64_tr_b16: in each group of 16 lanes, output lane
 // 4A + B receives element B of the 8-byte reads of lanes A, A + 4, A + 8 and
 // A + 12.  Lane s of group g (A = s % 4, i = s / 4 within the group) therefore
@@ -593,7 +598,8 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
 // (dim d, half h) receives keys 16t + 8r + 4h + {0..3} of dim d: read r = 0, 1
 // give the two 4-key halves of the A fragment in the key order the S^T
 // accumulator produces (key(t, h, e) = 16t + 8(e/4) + 4h + e%4).  The 4 rows x
-// 2 pieces each 16-lane group reads map to 8 distinct bank groups.
+// 4 pieces each half-wave reads (pieces 4b .. 4b + 3) land in 16 distinct
+// slots, all 64 banks.
 constexpr int DROW = 256;         // bytes per key row (D = 128)
 constexpr int DTILE = BN * DROW;  // bytes per K or V chunk tile
 
@@ -617,27 +623,42 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint8_t* p) {
 #endif
 }
 
-// NW = 4: 128 query rows per workgroup, two workgroups per CU; NW = 8: 256 rows,
-// one workgroup per CU whose eight waves share each K/V chunk (half the HBM/L2
-// traffic and DMA issue per query row).  Waves whose 32 rows all lie past the
-// tile's end keep the chunk's DMA and barriers and skip its compute.
-template <int NW, bool SEGL, bool KIDX>
-__global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
+// ---------------------------------------------------------------------------- block-sparse, D = 128, pipelined
+// The work items, plan walk and online softmax of attn_fwd_kernel MODE 0 over
+// 256-row query tiles: eight waves of 32 rows (two per SIMD, one workgroup per
+// CU) share each K/V chunk, which halves the HBM/L2 traffic and DMA issue per
+// query row against 128-row tiles.  S^T of the next 32-key half is computed
+// while the current half's probabilities are formed: after the row max and
+// lazy rescale of half h, one straight-line block issues the MFMAs of S(h + 1),
+// the exponentials of half h and the MFMAs of O += P(h) V, so the matrix unit
+// works through the softmax.  Waves whose rows all lie past the tile's end keep
+// the DMA and barriers and skip the compute.  S(h + 1) of a chunk's second half
+// reads the next chunk's K tile, so the chunk barrier sits before that block
+// and four LDS buffers rotate: chunk x is DMA'd right after the barrier of
+// chunk x - 3 (its buffer's previous chunk, x - 4, was last read before it)
+// and waited for before the barrier of chunk x - 1, two chunks later; key rows
+// are planned four chunks ahead.
+template <bool SEGL, bool KIDX>
+__global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int32_t s_q,
     int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan, int32_t bh_q,
     int32_t tiles_per_head, float scale_log2, const int32_t* __restrict__ q_index,
     const int32_t* __restrict__ k_index, uint16_t* __restrict__ out, float* __restrict__ lse) {
+  constexpr int NW = 8;
   constexpr int D = 128;
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
   constexpr int NT = NW * 64;
-  constexpr int TBM = NW * 32;              // query rows per workgroup
-  constexpr int DMA_PER_WAVE = 16 / NW;     // 1 KB (4-row) DMA instructions per wave per tile
-  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  constexpr int TBM = NW * 32;
+  constexpr int DMA_PER_WAVE = 16 / NW;
   __shared__ __attribute__((aligned(1024))) uint8_t k_tile0[DTILE];
   __shared__ __attribute__((aligned(1024))) uint8_t k_tile1[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_tile2[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_tile3[DTILE];
   __shared__ __attribute__((aligned(1024))) uint8_t v_tile0[DTILE];
   __shared__ __attribute__((aligned(1024))) uint8_t v_tile1[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_tile2[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_tile3[DTILE];
   __shared__ int32_t key_rows[4][BN];
   __shared__ Seg seg_lds[SEGL ? MAX_LDS_SEGS : 1];
 
@@ -647,7 +668,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  // ---- work item: XCD-grouped tile order, as in attn_fwd_kernel MODE 0
+  // ---- work item: XCD-grouped order over 256-row tiles
   const int64_t per_xcd = gridDim.x / 8;
   const int64_t logical = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   const int64_t bhq = logical / tiles_per_head;
@@ -655,15 +676,14 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
   if (bhq >= bh_q) return;
   const int64_t bhkv = bhq / group;
   PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
-  const int32_t* toff = NW == 8 ? pv.tile2_off : pv.tile_off;
-  if (tile >= toff[qn]) return;
-  int lo = 0, hi = qn;  // largest i with toff[i] <= tile
+  if (tile >= pv.tile2_off[qn]) return;
+  int lo = 0, hi = qn;  // largest i with tile2_off[i] <= tile
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
-    if (toff[mid] <= tile) lo = mid; else hi = mid;
+    if (pv.tile2_off[mid] <= tile) lo = mid; else hi = mid;
   }
   const int qc = lo;
-  const int32_t row0 = pv.q_off[qc] + (tile - toff[qc]) * TBM;
+  const int32_t row0 = pv.q_off[qc] + (tile - pv.tile2_off[qc]) * TBM;
   const int32_t row1 = min(row0 + TBM, pv.q_off[qc + 1]);
   const bool wave_live = row0 + 32 * wave < row1;
   const Seg* segs = pv.segs + static_cast<int64_t>(qc) * kn;
@@ -680,7 +700,6 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
     for (int i = tid; i < nseg; i += NT) seg_lds[i] = segs[i];
   }
 
-  // ---- this lane's query row as MFMA B fragments over the head dim
   int32_t my_row = row0 + wave * 32 + col;
   bool row_live = my_row < row1;
   if (q_index != nullptr && row_live) {
@@ -701,8 +720,6 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
 
   const int nch = (total + BN - 1) / BN;
 
-  // Key rows of each chunk, planned three chunks ahead by wave 0 (ring of 4), as
-  // in attn_fwd_kernel; positions past the end repeat the last key (masked).
   int32_t cur_s = 0;
   auto plan_chunk = [&](int c) {
     if (wave == 0) {
@@ -723,8 +740,6 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
       cur_s = __builtin_amdgcn_readlane(s, 63);
     }
   };
-
-  // DMA of one chunk: wave w, instruction i fills tile rows 4w + 4 NW i .. + 3.
   int32_t krow[DMA_PER_WAVE];
   auto load_rows = [&](int c) {
     const int32_t* kr = key_rows[c % 4];
@@ -738,114 +753,155 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void attn_dma_kernel(
       const int r0 = 4 * wave + 4 * NW * i;
       const int row = r0 + (lane >> 4);
       const int32_t off = krow[i] * DROW;
-      lds_dma16(k_rsrc, kt + r0 * DROW, off + ((slot ^ (row & 7)) << 4));
-      lds_dma16(v_rsrc, vt + r0 * DROW, off + ((slot ^ ((row & 3) << 1)) << 4));
+      lds_dma16(k_rsrc, kt + r0 * DROW, off + ((slot ^ (row & 15)) << 4));
+      lds_dma16(v_rsrc, vt + r0 * DROW, off + ((slot ^ ((row & 3) << 2)) << 4));
     }
   };
 
-  // lane-constant parts of the fragment addresses
-  const int k_x = half ^ (col & 7);  // K: piece 2s + half of row 32kbk + col sits at slot 2s ^ k_x
+  const int k_x = half ^ (col & 15);
   const int tr_a = lane & 3, tr_i = (lane >> 2) & 3, tr_g = (lane >> 4) & 1;
-  const int v_lane = (4 * half + tr_i) * DROW + (tr_a & 1) * 8;  // row 4h + i, byte within piece
-  const int v_piece = 2 * tr_g + (tr_a >> 1);                    // piece of block b: 4b + v_piece
-  const int v_x = 2 * tr_i;                                        // slot = piece ^ v_x
-
+  const int v_lane = (4 * half + tr_i) * DROW + (tr_a & 1) * 8;
+  const int v_piece = 2 * tr_g + (tr_a >> 1);
+  const int v_x = 4 * tr_i;
   const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-  auto chunk = [&](int c, const uint8_t* kt, const uint8_t* vt, uint8_t* kt_next, uint8_t* vt_next) {
-    if (c + 1 < nch) dma(kt_next, vt_next);  // rows of chunk c + 1, read during chunk c - 1
-    if (c + 2 < nch) load_rows(c + 2);
-    const int32_t left = total - c * BN;  // keys past the end exist only in the last chunk
-    if (!wave_live) {  // (never wave 0, which plans the chunks)
-      __syncthreads();
-      return;
+
+  auto s_mma = [&](spr::f32x16& acc, const uint8_t* kt, int kbk) {
+    acc = spr::f32x16{};
+    const uint8_t* arow = kt + (kbk * 32 + col) * DROW;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(arow + (((2 * s) ^ k_x) << 4));
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[s]), acc, 0, 0, 0);
     }
+  };
+  // Row max of half kbk (masked past the end) and lazy rescale; returns -m.
+  auto row_max = [&](spr::f32x16& acc, int kbk, int32_t left) {
+    if (left < BN) {
 #pragma unroll
-    for (int kbk = 0; kbk < 2; ++kbk) {
-      spr::f32x16 s_acc = spr::f32x16{};
-      {
-        const uint8_t* arow = kt + (kbk * 32 + col) * DROW;
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(arow + (((2 * s) ^ k_x) << 4));
-          s_acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[s]), s_acc, 0, 0, 0);
-        }
-      }
-      if (kbk == 0 && c + 3 < nch) plan_chunk(c + 3);
-      if (left < BN) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = kbk * 32 + 8 * (e / 4) + 4 * half + (e % 4);
-          if (key >= left) s_acc[e] = -__builtin_huge_valf();
-        }
-      }
-      float mx = -__builtin_huge_valf();
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_acc[e]);
-      const float mloc = max_xor32(mx) * scale_log2;
-      // Rescale lazily: only when some row's maximum grew by more than the slack.
-      if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int b = 0; b < DBLK; ++b) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
-        }
-        m_run = m_new;
-      }
-      uint32_t pf[2][4];  // P of this half as bf16 pairs: [k-step][dword]
-      {
-        const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
-        // The row sum adds the bf16-rounded probabilities that also weight V.
-        float lsum0 = 0.0f, lsum1 = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[e], scale_log2, neg_m));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[e + 1], scale_log2, neg_m));
-          const uint32_t pk = pack2(p0, p1);
-          pf[e / 8][(e % 8) / 2] = pk;
-          if (e % 4 == 0) {
-            lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
-          } else {
-            lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
-          }
-        }
-        l_run += lsum0 + lsum1;
-      }
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int t = kbk * 2 + tt;
-        const uint8_t* vrow = vt + 16 * t * DROW + v_lane;
-        const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
-#pragma unroll
-        for (int b = 0; b < DBLK; ++b) {
-          const int slot = ((4 * b + v_piece) ^ v_x) << 4;
-          const u32x2 r0 = lds_read_tr16(vrow + slot);
-          const u32x2 r1 = lds_read_tr16(vrow + 8 * DROW + slot);
-          const u32x4 a = u32x4{r0.x, r0.y, r1.x, r1.y};
-          o_acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag), o_acc[b], 0, 0,
-                                                             0);
-        }
+      for (int e = 0; e < 16; ++e) {
+        const int key = kbk * 32 + 8 * (e / 4) + 4 * half + (e % 4);
+        if (key >= left) acc[e] = -__builtin_huge_valf();
       }
     }
-    __syncthreads();  // waits for this wave's DMA of chunk c + 1, and frees the tiles of chunk c
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, acc[e]);
+    const float mloc = max_xor32(mx) * scale_log2;
+    if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
+      const float m_new = fmaxf(m_run, mloc);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
+      }
+      m_run = m_new;
+    }
+  };
+  // One straight-line block: S^T of the next half into acc_next (K tile kt_n,
+  // half kbk_n), interleaved step by step with P = 2^(s - m) of the current half
+  // (acc) and its row sum, then O^T += V^T P^T over the current half's keys
+  // (V tile vt, half kbk).  Fragments are read two steps ahead; the MFMAs of
+  // S(h + 1) do not depend on the exponentials of half h, so the matrix unit and
+  // the VALU work side by side.
+  auto step = [&](spr::f32x16& acc_next, const uint8_t* kt_n, int kbk_n, const spr::f32x16& acc, const uint8_t* vt,
+                  int kbk) {
+    const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
+    uint32_t pf[2][4];
+    float lsum0 = 0.0f, lsum1 = 0.0f;
+    acc_next = spr::f32x16{};
+    const uint8_t* arow = kt_n + (kbk_n * 32 + col) * DROW;
+    auto kfrag = [&](int st) { return *reinterpret_cast<const u32x4*>(arow + (((2 * st) ^ k_x) << 4)); };
+    u32x4 ka[3];
+    ka[0] = kfrag(0);
+    ka[1] = kfrag(1);
+#pragma unroll
+    for (int st = 0; st < KSTEPS; ++st) {
+      if (st + 2 < KSTEPS) ka[(st + 2) % 3] = kfrag(st + 2);
+      acc_next = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ka[st % 3]), spr::as_bf16x8(qf[st]), acc_next,
+                                                         0, 0, 0);
+      const int e = 2 * st;
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e], scale_log2, neg_m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e + 1], scale_log2, neg_m));
+      const uint32_t pk = pack2(p0, p1);
+      pf[e / 8][(e % 8) / 2] = pk;
+      if (e % 4 == 0) {
+        lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+      } else {
+        lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+      }
+    }
+    l_run += lsum0 + lsum1;
+    auto vfrag = [&](int f) {  // f = 4 tt + b
+      const uint8_t* vrow = vt + 16 * (kbk * 2 + f / DBLK) * DROW + v_lane + (((4 * (f % DBLK) + v_piece) ^ v_x) << 4);
+      const u32x2 r0 = lds_read_tr16(vrow);
+      const u32x2 r1 = lds_read_tr16(vrow + 8 * DROW);
+      return u32x4{r0.x, r0.y, r1.x, r1.y};
+    };
+    u32x4 va[3];
+    va[0] = vfrag(0);
+    va[1] = vfrag(1);
+#pragma unroll
+    for (int f = 0; f < 2 * DBLK; ++f) {
+      if (f + 2 < 2 * DBLK) va[(f + 2) % 3] = vfrag(f + 2);
+      const int tt = f / DBLK;
+      const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
+      o_acc[f % DBLK] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(va[f % 3]), spr::as_bf16x8(bfrag),
+                                                                o_acc[f % DBLK], 0, 0, 0);
+    }
+  };
+
+  spr::f32x16 s_a, s_b;  // S^T of the current half / of the next half
+  // Chunk x in tiles kt/vt; kt1 = K tile of chunk x + 1; kt3/vt3 (the tiles of
+  // chunk x - 1) receive chunk x + 3.  The last chunk's second half still
+  // computes a next S (from a stale buffer, unused) so that every block is the
+  // same straight-line code.
+  auto chunk = [&](int x, const uint8_t* kt, const uint8_t* vt, const uint8_t* kt1, uint8_t* kt3, uint8_t* vt3) {
+    const int32_t left = total - x * BN;
+    // ---- first half (S in s_a); S of the second half goes to s_b
+    if (wave_live) {
+      row_max(s_a, 0, left);
+      step(s_b, kt, 1, s_a, vt, 0);
+    }
+    if (x + 4 < nch) plan_chunk(x + 4);
+    if (x + 3 < nch) load_rows(x + 3);
+    // ---- second half (S in s_b); S of the next chunk's first half goes to s_a
+    if (wave_live) row_max(s_b, 1, left);
+    // this wave's DMA of chunk x + 1 landed (that of chunk x + 2, issued later, may not have)
+    if (x + 2 < nch) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_WAVE) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();  // ... every wave's; and no wave reads chunk x - 1 any more
+    if (x + 3 < nch) dma(kt3, vt3);
+    if (wave_live) step(s_a, kt1, 0, s_b, vt, 1);
   };
 
   if (nch > 0) {
     if constexpr (SEGL) __syncthreads();  // staged segment list visible to wave 0
-    plan_chunk(0);
-    if (nch > 1) plan_chunk(1);
-    if (nch > 2) plan_chunk(2);
+    for (int c = 0; c < 4 && c < nch; ++c) plan_chunk(c);
     __syncthreads();
     load_rows(0);
     dma(k_tile0, v_tile0);
-    if (nch > 1) load_rows(1);
-    __syncthreads();
-  }
-  for (int c = 0; c < nch; c += 2) {
-    chunk(c, k_tile0, v_tile0, k_tile1, v_tile1);
-    if (c + 1 < nch) chunk(c + 1, k_tile1, v_tile1, k_tile0, v_tile0);
+    if (nch > 1) {
+      load_rows(1);
+      dma(k_tile1, v_tile1);
+    }
+    if (nch > 2) {
+      load_rows(2);
+      dma(k_tile2, v_tile2);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // chunks 0 .. 2 landed
+    if (wave_live) s_mma(s_a, k_tile0, 0);
+    for (int x = 0; x < nch; x += 4) {
+      chunk(x, k_tile0, v_tile0, k_tile1, k_tile3, v_tile3);
+      if (x + 1 < nch) chunk(x + 1, k_tile1, v_tile1, k_tile2, k_tile0, v_tile0);
+      if (x + 2 < nch) chunk(x + 2, k_tile2, v_tile2, k_tile3, k_tile1, v_tile1);
+      if (x + 3 < nch) chunk(x + 3, k_tile3, v_tile3, k_tile0, k_tile2, v_tile2);
+    }
   }
 
   // ---- epilogue
@@ -987,29 +1043,26 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
     }                                  \
   } while (0)
   const bool seg_lds = kn <= MAX_LDS_SEGS;
-#ifndef ATTN_DMA_NW
-#define ATTN_DMA_NW 8
-#endif
-  const int64_t max_tiles_dma = spr::ceil_div(s, ATTN_DMA_NW * 32) + qn;
-  dim3 grid_dma(static_cast<uint32_t>(spr::ceil_div(max_tiles_dma * bh_q, 8) * 8));
-#define SPR_DMA(SL, KX)                                                                                       \
-  attn_dma_kernel<ATTN_DMA_NW, SL, KX><<<grid_dma, ATTN_DMA_NW * 64, 0, stream>>>(                            \
+  const int64_t max_tiles_pipe = spr::ceil_div(s, 2 * BM) + qn;
+  dim3 grid_pipe(static_cast<uint32_t>(spr::ceil_div(max_tiles_pipe * bh_q, 8) * 8));
+#define SPR_PIPE(SL, KX)                                                                                      \
+  attn_pipe_kernel<SL, KX><<<grid_pipe, 512, 0, stream>>>(                                                      \
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
-      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles_dma), scale_log2, q_index, k_index,        \
+      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles_pipe), scale_log2, q_index, k_index,       \
       static_cast<uint16_t*>(out), lse)
   if (d == 128) {
     if (k_index != nullptr) {
-      if (seg_lds) SPR_DMA(true, true); else SPR_DMA(false, true);
+      if (seg_lds) SPR_PIPE(true, true); else SPR_PIPE(false, true);
     } else {
-      if (seg_lds) SPR_DMA(true, false); else SPR_DMA(false, false);
+      if (seg_lds) SPR_PIPE(true, false); else SPR_PIPE(false, false);
     }
   } else {
     if (seg_lds) SPR_ATTN(64, true); else SPR_ATTN(64, false);
   }
 #undef SPR_ATTN
 #undef SPR_ATTN2
-#undef SPR_DMA
+#undef SPR_PIPE
   SPR_LAUNCHED("attn_fwd_kernel");
   return SPR_OK;
 }
