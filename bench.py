@@ -143,7 +143,7 @@ def only_attention(args):
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     flops = float(kept_pair_flops(route, D).item())
-    print(json.dumps({"kernel": "attn_fwd_kernel<128,0>", "ms_per_launch": round(ms, 3),
+    print(json.dumps({"kernel": "attn_pipe_kernel", "ms_per_launch": round(ms, 3),
                       "tflops": round(flops / ms / 1e9, 1), "frac": round(flops / ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
                       "density": round(float(route.base_video_density.item()), 4)}), flush=True)
 
@@ -216,7 +216,7 @@ def main():
         },
         "stages_ms": stage_ms,
         "roofline": {
-            "kernel": "attn_fwd_kernel<128,0> (block-sparse attention)",
+            "kernel": "attn_pipe_kernel (D=128 block-sparse attention)",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": MFMA_BF16_PEAK_TFLOPS,
