@@ -471,7 +471,12 @@ def _probe_distances(features, labels, num_clusters):
 
     Centers: float64 sums (exact for bf16-valued features) / size, rounded to
     fp32 (residual_repair.py:162-180 builds fp32 centers with scatter_add).
-    Distance: sequential over d, separate fp32 multiply and add (canonical)."""
+    Distance: the reference sums the squared differences with torch's reduction
+    (residual_repair.py:65, :160-164), whose fp32 order is unspecified; the
+    canonical order here is a sequential fp32 sum (separate multiply and add)
+    within each group of 8 consecutive dims, then a balanced pairwise tree over
+    the groups in index order (dims and groups zero-padded to 8 x a power of
+    two; the padding adds exact zeros, so r <= 8 is the plain sequential sum)."""
     bh, n, r = features.shape
     f = features.astype(np.float32)
     sizes = np.zeros((bh, num_clusters), np.int64)
@@ -480,12 +485,20 @@ def _probe_distances(features, labels, num_clusters):
         sizes[h] = np.bincount(labels[h], minlength=num_clusters)
         s = _group_sums(f[h], labels[h], num_clusters)
         centers[h] = (s / np.maximum(sizes[h], 1)[:, None]).astype(np.float32)
-    dist = np.zeros((bh, n), np.float32)
     gathered = np.take_along_axis(centers, labels[..., None].astype(np.int64), 1)
     diff = (f - gathered).astype(np.float32)
-    for t in range(r):
-        col = diff[:, :, t]
-        dist = (dist + (col * col).astype(np.float32)).astype(np.float32)
+    groups = -(-r // 8)
+    span = 1 << (groups - 1).bit_length()  # tree width: groups rounded up to a power of two
+    padded = np.zeros((bh, n, span * 8), np.float32)  # zero terms add exactly 0.0
+    padded[..., :r] = diff
+    d = padded.reshape(bh, n, span, 8)
+    part = np.zeros((bh, n, span), np.float32)
+    for e in range(8):
+        col = d[..., e]
+        part = (part + (col * col).astype(np.float32)).astype(np.float32)
+    while part.shape[-1] > 1:
+        part = (part[..., 0::2] + part[..., 1::2]).astype(np.float32)
+    dist = part[..., 0]
     return sizes, dist
 
 

@@ -16,11 +16,19 @@
 // token id) via an LDS atomicMin over 64-bit (distance bits, token) keys.
 #pragma clang fp contract(off)
 
+#include <algorithm>
+
 #include "spr_common.h"
 
 namespace {
 
 using spr::u32x4;
+
+// x[l] + x[l ^ 32] (v_permlane32_swap returns both halves; + is symmetric in them).
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 constexpr int MAX_GROUPS = 2048;
 
@@ -33,54 +41,65 @@ __device__ __forceinline__ float load_elem(const T* p, int64_t i) {
   }
 }
 
-// dist[bh, t] = sum_d (f[t, d] - center[label[t], d])^2, d ascending, each term
-// rounded (sub, mul, add; no contraction).  One thread per token: the row and its
-// centre row are read with 16-byte loads.
+// dist[bh, t] = sum_d (f[t, d] - center[label[t], d])^2 in fp32, each term rounded
+// (sub, mul, add; no contraction): sequential within each group of 8 consecutive
+// dims, then a balanced pairwise tree over the groups in index order (the
+// reference's torch .sum() fixes no order; this is the canonical one).
 template <typename T, int R>
 __global__ __launch_bounds__(256) void probe_distance_kernel(const T* __restrict__ f,
                                                              const int32_t* __restrict__ labels,
                                                              const float* __restrict__ centers, int64_t n,
                                                              int32_t groups, float* __restrict__ dist) {
-  constexpr int E = 16 / sizeof(T);  // feature elements per 16-byte load
+  // R / 8 lanes share a row (coalesced 16- or 32-byte loads); lane k sums dims
+  // 8k .. 8k + 7 sequentially (separate fp32 multiply and add), then a butterfly
+  // over the row's lanes adds the partials as a balanced pairwise tree in index
+  // order (x + y == y + x, so both lanes of every pair hold the same sum).  A
+  // workgroup covers 256 rows, 64 per wave.
+  constexpr int L = R / 8;
+  constexpr int RPS = 64 / L;  // rows per wave step
   const int64_t bh = blockIdx.y;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= n) return;
-  const int32_t lab = labels[bh * n + t];
-  const bool ok = lab >= 0 && lab < groups;
-  const spr::f32x4* crow = reinterpret_cast<const spr::f32x4*>(centers + (bh * groups + (ok ? lab : 0)) * R);
-  const u32x4* frow = reinterpret_cast<const u32x4*>(f + (bh * n + t) * R);
-  float acc = 0.0f;
+  const int lane = threadIdx.x & 63;
+  const int k = lane % L;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x >> 6) * 64 + lane / L;
 #pragma unroll 4
-  for (int q = 0; q < R / E; ++q) {
-    const u32x4 w = frow[q];
-    float fv[E];
-    if constexpr (sizeof(T) == 2) {
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  for (int st = 0; st < 64 / RPS; ++st) {
+    const int64_t t = row0 + st * RPS;
+    float acc = 0.0f;
+    if (t < n) {
+      const int32_t lab = labels[bh * n + t];
+      const bool ok = lab >= 0 && lab < groups;
+      const spr::f32x4* crow =
+          reinterpret_cast<const spr::f32x4*>(centers + (bh * groups + (ok ? lab : 0)) * R + 8 * k);
+      const spr::f32x4 c0 = ok ? crow[0] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const spr::f32x4 c1 = ok ? crow[1] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+      float fv[8];
+      if constexpr (sizeof(T) == 2) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(f + (bh * n + t) * R + 8 * k);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        fv[2 * e] = spr::bf16_lo(ws[e]);
-        fv[2 * e + 1] = spr::bf16_hi(ws[e]);
+        for (int e = 0; e < 4; ++e) {
+          fv[2 * e] = spr::bf16_lo(ws[e]);
+          fv[2 * e + 1] = spr::bf16_hi(ws[e]);
+        }
+      } else {
+        const spr::f32x4* fr = reinterpret_cast<const spr::f32x4*>(f + (bh * n + t) * R + 8 * k);
+        const spr::f32x4 a = fr[0], b = fr[1];
+        fv[0] = a[0]; fv[1] = a[1]; fv[2] = a[2]; fv[3] = a[3];
+        fv[4] = b[0]; fv[5] = b[1]; fv[6] = b[2]; fv[7] = b[3];
       }
-    } else {
-      fv[0] = __uint_as_float(w.x);
-      fv[1] = __uint_as_float(w.y);
-      fv[2] = __uint_as_float(w.z);
-      fv[3] = __uint_as_float(w.w);
-    }
 #pragma unroll
-    for (int g = 0; g < E / 4; ++g) {
-      const spr::f32x4 c = ok ? crow[q * (E / 4) + g] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 8; ++e) {
         // plain operators: the file-level contract(off) keeps mul and add apart
-        // (the library's __f*_rn helpers carry their own contraction flags)
-        const float diff = fv[4 * g + e] - c[e];
+        const float diff = fv[e] - cv[e];
         const float sq = diff * diff;
         acc = acc + sq;
       }
     }
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) acc = acc + __shfl_xor(acc, o, 64);
+    if (t < n && k == 0) dist[bh * n + t] = acc;
   }
-  dist[bh * n + t] = acc;
 }
 
 // mode 0: vectorized role-equal (one representative per group, first `count`
@@ -317,6 +336,202 @@ __global__ __launch_bounds__(256) void repair_apply_kernel(const uint16_t* __res
 }
 
 // out[bh, rows[j]] = dense[bh, j] cast to the output dtype (bf16 out, fp32 or bf16 in).
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): eight fp32 values as two
+// packed bf16 fragments (about 16 mantissa bits between them).
+__device__ __forceinline__ void split_bf16x8(const float (&v)[8], u32x4& hi, u32x4& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = spr::pack_bf16x2_rne(v[2 * i], v[2 * i + 1]);
+    l[i] = spr::pack_bf16x2_rne(v[2 * i] - spr::bf16_lo(h[i]), v[2 * i + 1] - spr::bf16_hi(h[i]));
+  }
+  hi = u32x4{h[0], h[1], h[2], h[3]};
+  lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+
+// Rank-16 correction on v_mfma_f32_32x32x16_bf16, D = 128: one wave per 32 rows.
+// fp32 operands enter as bf16 hi + lo pairs and each product is
+// hi*hi + lo*hi + hi*lo (about 16 mantissa bits; the reference's tl.dot runs in
+// TF32 by default).
+//   coords^T[rank, row] = L^T z^T: A = L^T (32 ranks, 16..31 zero) x 16 dims; B =
+//     z^T, where lane (row l % 32, k-half h) holds dims 16s + 8h .. + 7 of its
+//     row.  The accumulator gives that lane ranks 8i + 4h + j (i = 0, 1;
+//     registers 0..7).
+//   corr^T[dim, row] = B coords^T with the rank (k) index of this product in the
+//     order rho(h, m) = 8(m / 4) + 4h + m % 4, so registers 0..7 of the coords
+//     accumulator are the B operand as they stand; A = basis in the same rank
+//     order.  Row a of N-tile nt is dim 32 nt + pi(a), pi swapping bits 2 and 3
+//     of a, so lane (row, h) receives exactly the 64 dims it read: register
+//     8q + e of tile nt is dim 16(2 nt + q) + 8h + e, and out = b + scale corr
+//     needs no exchange.
+// Rows stream through LDS: every wave DMAs its own 32-row batches (1 KB, four
+// rows, per instruction; buffer range checks return zeros past the end) into a
+// private double buffer one batch ahead, so only vmcnt waits order them.  The
+// 16-byte pieces of row r sit at slot j ^ (r & 15): the fragment reads of 16
+// consecutive rows hit all 64 banks.  Each workgroup (8 waves, one per CU)
+// stages the head's factors once and walks 256-row batches.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+#endif
+}
+
+template <bool CAP>
+__global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* __restrict__ base,
+                                                                const float* __restrict__ x_mean,
+                                                                const float* __restrict__ x_scale,
+                                                                const float* __restrict__ y_mean,
+                                                                const float* __restrict__ left,
+                                                                const float* __restrict__ basis, int64_t n,
+                                                                float alpha, float norm_cap,
+                                                                uint16_t* __restrict__ out) {
+  constexpr int D = 128;
+  constexpr int RK = 16;
+  constexpr int ROWB = D * 2;        // bytes per row
+  constexpr int TILE = 32 * ROWB;    // one wave's batch
+  __shared__ u32x4 lfrag[8][2][RK][2];   // [k-step s][k-half h][rank] (hi, lo): L[16s + 8h + e][rank]
+  __shared__ u32x4 bfrag[4][32][2][2];   // [N-tile][row a][k-half h] (hi, lo): basis[32 nt + pi(a)][rho(h, m)]
+  __shared__ float mu[D], inv_sd[D], my[D];
+  __shared__ __attribute__((aligned(1024))) uint8_t rows_lds[8][2][TILE];  // [wave][buffer]
+  const int64_t bh = blockIdx.y;
+  const float* lm = left + bh * D * RK;
+  const float* bm = basis + bh * D * RK;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int col = lane & 31;
+  const int h = lane >> 5;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + bh * n * D), 0, static_cast<int32_t>(n * ROWB),
+                                        0x00020000);
+  // batch starting at wave row w0 into buffer tile: instruction i moves rows 4i .. 4i + 3
+  auto dma = [&](int64_t w0, uint8_t* tile) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + (lane >> 4);
+      const int64_t row = w0 + r;
+      const int32_t off = row < n ? static_cast<int32_t>(row * ROWB) + (((lane & 15) ^ (r & 15)) << 4)
+                                  : static_cast<int32_t>(n * ROWB);  // past the range: reads zeros
+      lds_dma16(rsrc, tile + i * 1024, off);
+    }
+  };
+  int64_t w0 = static_cast<int64_t>(blockIdx.x) * 256 + wave * 32;
+  if (w0 < n) dma(w0, rows_lds[wave][0]);
+
+  for (int f = tid; f < 8 * 2 * RK; f += blockDim.x) {
+    const int st = f / (2 * RK), hh = (f / RK) % 2, rk = f % RK;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = lm[(16 * st + 8 * hh + e) * RK + rk];
+    split_bf16x8(v, lfrag[st][hh][rk][0], lfrag[st][hh][rk][1]);
+  }
+  for (int f = tid; f < 4 * 32 * 2; f += blockDim.x) {
+    const int nt = f / 64, a = (f / 2) % 32, hh = f % 2;
+    const int dim = 32 * nt + ((a & ~12) | ((a & 4) << 1) | ((a & 8) >> 1));
+    float v[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) v[m] = bm[dim * RK + 8 * (m / 4) + 4 * hh + m % 4];
+    split_bf16x8(v, bfrag[nt][a][hh][0], bfrag[nt][a][hh][1]);
+  }
+  for (int e = tid; e < D; e += blockDim.x) {
+    mu[e] = x_mean[bh * D + e];
+    inv_sd[e] = 1.0f / x_scale[bh * D + e];
+    my[e] = y_mean[bh * D + e];
+  }
+  __syncthreads();
+
+  const u32x4 zero = {0, 0, 0, 0};
+  for (int buf = 0; w0 < n; w0 += stride, buf ^= 1) {
+    const bool more = w0 + stride < n;
+    if (more) dma(w0 + stride, rows_lds[wave][buf ^ 1]);
+    if (more) {
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this batch landed; the next may not have
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const uint8_t* tile = rows_lds[wave][buf];
+    u32x4 bv[8];  // dims 16s + 8h .. + 7 of row col
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      bv[st] = *reinterpret_cast<const u32x4*>(tile + col * ROWB + (((2 * st + h) ^ (col & 15)) << 4));
+    }
+    spr::f32x16 cacc = spr::f32x16{};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const uint32_t w[4] = {bv[st].x, bv[st].y, bv[st].z, bv[st].w};
+      float z[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int dd = 16 * st + 8 * h + e;
+        const float b = (e & 1) ? spr::bf16_hi(w[e / 2]) : spr::bf16_lo(w[e / 2]);
+        z[e] = (b - mu[dd]) * inv_sd[dd];
+      }
+      u32x4 zh, zl;
+      split_bf16x8(z, zh, zl);
+      const u32x4 ah = col < RK ? lfrag[st][h][col][0] : zero;
+      const u32x4 al = col < RK ? lfrag[st][h][col][1] : zero;
+      cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zh), cacc, 0, 0, 0);
+      cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(al), spr::as_bf16x8(zh), cacc, 0, 0, 0);
+      cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zl), cacc, 0, 0, 0);
+    }
+    u32x4 ch, cl;
+    {
+      float c[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) c[m] = cacc[m];
+      split_bf16x8(c, ch, cl);
+    }
+    spr::f32x16 acc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const u32x4 ah = bfrag[nt][col][h][0];
+      const u32x4 al = bfrag[nt][col][h][1];
+      acc[nt] = spr::f32x16{};
+      acc[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(ch), acc[nt], 0, 0, 0);
+      acc[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(al), spr::as_bf16x8(ch), acc[nt], 0, 0, 0);
+      acc[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(cl), acc[nt], 0, 0, 0);
+    }
+    // corr = acc + y_mean; with CAP, norms over the row's 128 dims (this lane's 64 and lane l ^ 32's)
+    float bn = 0.0f, cn = 0.0f;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int st = 2 * nt + r / 8, e = r % 8;
+        acc[nt][r] += my[16 * st + 8 * h + e];
+        if constexpr (CAP) {
+          const uint32_t w = (e / 2 == 0) ? bv[st].x : (e / 2 == 1) ? bv[st].y : (e / 2 == 2) ? bv[st].z : bv[st].w;
+          const float b = (e & 1) ? spr::bf16_hi(w) : spr::bf16_lo(w);
+          bn = __builtin_fmaf(b, b, bn);
+          cn = __builtin_fmaf(acc[nt][r], acc[nt][r], cn);
+        }
+      }
+    }
+    float scale = alpha;
+    if constexpr (CAP) {
+      bn = sum_xor32(bn);
+      cn = sum_xor32(cn);
+      scale = alpha * fminf(1.0f, norm_cap * sqrtf(bn) / fmaxf(sqrtf(cn), 1e-20f));
+    }
+    const int64_t row = w0 + col;
+    if (row < n) {
+      uint16_t* orow = out + (bh * n + row) * D;
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        const uint32_t w[4] = {bv[st].x, bv[st].y, bv[st].z, bv[st].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o[i] = spr::pack_bf16x2(__builtin_fmaf(scale, acc[st / 2][8 * (st % 2) + 2 * i], spr::bf16_lo(w[i])),
+                                  __builtin_fmaf(scale, acc[st / 2][8 * (st % 2) + 2 * i + 1], spr::bf16_hi(w[i])));
+        }
+        *reinterpret_cast<u32x4*>(orow + 16 * st + 8 * h) = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+  }
+}
+
 template <typename TD>
 __global__ void probe_scatter_kernel(const TD* __restrict__ dense, const int32_t* __restrict__ rows, int64_t n,
                                      int32_t m, int32_t d, uint16_t* __restrict__ out) {
@@ -343,7 +558,7 @@ extern "C" int spr_probe_distances(const void* features, int32_t dtype, const in
   SPR_REQUIRE(bh <= 65535, "spr_probe_distances: bh exceeds 65535");
   if (bh == 0 || n == 0) return SPR_OK;
   SPR_REQUIRE(features && labels && centers && dist, "spr_probe_distances: null pointer");
-  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 64)), static_cast<uint32_t>(bh));
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
 #define SPR_PD(T, RR)                                                                                          \
   probe_distance_kernel<T, RR><<<grid, 256, 0, stream>>>(static_cast<const T*>(features), labels, centers, n, \
                                                           groups, dist)
@@ -413,12 +628,22 @@ extern "C" int spr_repair_apply(const void* base, const float* x_mean, const flo
   SPR_REQUIRE(base && x_mean && x_scale && y_mean && left && basis && out, "spr_repair_apply: null pointer");
   SPR_REQUIRE(reinterpret_cast<uintptr_t>(base) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
               "spr_repair_apply: base/out must be 16-byte aligned");
-  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
   if (d == 128) {
-    repair_apply_kernel<128, 16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
-                                                           y_mean, left, basis, n, alpha, norm_cap,
-                                                           static_cast<uint16_t*>(out));
+    SPR_REQUIRE(n * 256 < (int64_t(1) << 31), "spr_repair_apply: a head's rows exceed 2 GiB");
+    // one resident workgroup per CU (256 CUs), each walking 256-row batches of one head
+    const int64_t per_head = std::max<int64_t>(1, std::min<int64_t>(spr::ceil_div(n, 256), 256 / bh));
+    dim3 grid(static_cast<uint32_t>(per_head), static_cast<uint32_t>(bh));
+    if (norm_cap > 0.0f) {
+      repair_apply_mfma_kernel<true><<<grid, 512, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
+                                                               y_mean, left, basis, n, alpha, norm_cap,
+                                                               static_cast<uint16_t*>(out));
+    } else {
+      repair_apply_mfma_kernel<false><<<grid, 512, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
+                                                                y_mean, left, basis, n, alpha, norm_cap,
+                                                                static_cast<uint16_t*>(out));
+    }
   } else {
+    dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
     repair_apply_kernel<64, 16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
                                                           y_mean, left, basis, n, alpha, norm_cap,
                                                           static_cast<uint16_t*>(out));
