@@ -205,6 +205,131 @@ __global__ void centroid_sq_kernel(const T* __restrict__ c, int64_t rows, int32_
   out[r] = s;
 }
 
+// Same assignment with the batch's centroids resident in LDS: a 768-thread
+// workgroup (three waves per SIMD) stages all k centroids (padded rows; zeros and c_sq = +inf past k)
+// once, then each wave walks 64-point blocks of the batch against them with no
+// further barriers, centroid reloads or staging work.  Used while the padded
+// centroids fit in LDS (k <= ASSIGN_RESIDENT_K at D = 128).
+constexpr int ASSIGN_RESIDENT_K = 512;
+
+constexpr int ASSIGN_RESIDENT_THREADS = 768;
+
+template <int D>
+__global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resident_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ c, const float* __restrict__ c_sq,
+    const float* __restrict__ x_sq_in, int x_sq_mode, float* __restrict__ x_sq_out, int64_t n, int32_t k,
+    int32_t* __restrict__ labels) {
+  constexpr int KSTEPS = D / 16;
+  constexpr int ROW_BYTES = D * 2 + 16;  // padded LDS row: conflict-free 16-byte reads
+  extern __shared__ __attribute__((aligned(16))) uint8_t assign_smem[];
+  const int kpad = (k + CCHUNK - 1) / CCHUNK * CCHUNK;
+  uint8_t* cent = assign_smem;
+  float* csq_l = reinterpret_cast<float*>(assign_smem + static_cast<int64_t>(kpad) * ROW_BYTES);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const int64_t b = blockIdx.y;
+  const uint16_t* xb = x + b * n * D;
+  const uint16_t* cb = c + static_cast<int64_t>(b) * k * D;
+  const float* csqb = c_sq + static_cast<int64_t>(b) * k;
+
+  for (int piece = tid; piece < kpad * (D / 8); piece += blockDim.x) {
+    const int row = piece / (D / 8);
+    const int vec = piece % (D / 8);
+    const u32x4 v = row < k ? *reinterpret_cast<const u32x4*>(cb + static_cast<int64_t>(row) * D + vec * 8)
+                            : u32x4{0, 0, 0, 0};
+    *reinterpret_cast<u32x4*>(cent + row * ROW_BYTES + vec * 16) = v;
+  }
+  for (int r = tid; r < kpad; r += blockDim.x) csq_l[r] = r < k ? csqb[r] : __builtin_huge_valf();
+  __syncthreads();
+
+  const int64_t blocks = (n + ASSIGN_POINTS_PER_WAVE - 1) / ASSIGN_POINTS_PER_WAVE;
+  for (int64_t blk = static_cast<int64_t>(blockIdx.x) * (blockDim.x / 64) + wave; blk < blocks;
+       blk += static_cast<int64_t>(gridDim.x) * (blockDim.x / 64)) {
+    const int64_t p0 = blk * ASSIGN_POINTS_PER_WAVE + col;
+    u32x4 xf[2][KSTEPS];
+    float xsq[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const int64_t p = p0 + 32 * f;
+      const bool live = p < n;
+      float part = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        u32x4 v = live ? *reinterpret_cast<const u32x4*>(xb + p * D + s * 16 + half * 8) : u32x4{0, 0, 0, 0};
+        xf[f][s] = v;
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = spr::bf16_lo(w[e]);
+          const float hi = spr::bf16_hi(w[e]);
+          if (x_sq_mode == 1) {
+            const uint32_t sq2 = spr::pack_bf16x2_rne(lo * lo, hi * hi);
+            part += spr::bf16_lo(sq2);
+            part += spr::bf16_hi(sq2);
+          } else {
+            part = __builtin_fmaf(lo, lo, part);
+            part = __builtin_fmaf(hi, hi, part);
+          }
+        }
+      }
+      const float other = __shfl_xor(part, 32, 64);
+      float total = part + other;
+      if (x_sq_mode == 1) total = spr::bf16_lo(spr::pack_bf16x2_rne(total, 0.0f));
+      if (x_sq_in != nullptr) {
+        total = live ? x_sq_in[b * n + p] : 0.0f;
+      } else if (x_sq_out != nullptr && live && half == 0) {
+        x_sq_out[b * n + p] = total;
+      }
+      xsq[f] = total;
+    }
+
+    float best[2] = {3.4e38f, 3.4e38f};
+    int32_t best_idx[2] = {0, 0};
+    for (int c0 = 0; c0 < kpad; c0 += 32) {
+      spr::f32x16 acc0 = {}, acc1 = {};
+      const uint8_t* arow = cent + (c0 + col) * ROW_BYTES + half * 16;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[0][s]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[1][s]), acc1, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int32_t cidx = c0 + 8 * i + 4 * half + j;
+          const float csq = csq_l[cidx];
+          // (x_sq + c_sq) - 2 cross, one rounding per step (2 * cross is exact)
+          const float d0 = fmaxf(__builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq)), 0.0f);
+          const float d1 = fmaxf(__builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq)), 0.0f);
+          const bool t0 = d0 < best[0];
+          const bool t1 = d1 < best[1];
+          best[0] = t0 ? d0 : best[0];
+          best_idx[0] = t0 ? cidx : best_idx[0];
+          best[1] = t1 ? d1 : best[1];
+          best_idx[1] = t1 ? cidx : best_idx[1];
+        }
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+      const float od = __shfl_xor(best[f], 32, 64);
+      const int32_t oi = __shfl_xor(best_idx[f], 32, 64);
+      if (od < best[f] || (od == best[f] && oi < best_idx[f])) {
+        best[f] = od;
+        best_idx[f] = oi;
+      }
+      const int64_t p = p0 + 32 * f;
+      if (half == 0 && p < n) labels[b * n + p] = best_idx[f];
+    }
+  }
+}
+
 // ---------------------------------------------------------------- segmented mean
 // Mean of one cluster from its fp64 sum: mean32 = float(sum / count) (empty ->
 // previous centroid), out = mean32 in the centroid dtype, optional running
@@ -471,6 +596,30 @@ extern "C" int spr_kmeans_assign_bf16(const void* x, const void* centroids, cons
   dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, ASSIGN_POINTS)), static_cast<uint32_t>(batch));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* cp = static_cast<const uint16_t*>(centroids);
+  if (d == 128 && k <= ASSIGN_RESIDENT_K) {
+    // one resident workgroup per CU (256 CUs), sharing the batch's point blocks
+    const int64_t kpad = spr::ceil_div(k, CCHUNK) * CCHUNK;
+    const size_t lds = static_cast<size_t>(kpad) * (128 * 2 + 16) + static_cast<size_t>(kpad) * 4;
+    constexpr int waves = ASSIGN_RESIDENT_THREADS / 64;
+    const int64_t per_batch =
+        std::max<int64_t>(1, std::min<int64_t>(spr::ceil_div(n, waves * ASSIGN_POINTS_PER_WAVE), 256 / batch));
+    static bool lds_raised = false;  // dynamic LDS beyond 64 KB must be allowed once per process
+    if (!lds_raised) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&kmeans_assign_resident_kernel<128>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               ASSIGN_RESIDENT_K * (128 * 2 + 16) + ASSIGN_RESIDENT_K * 4);
+      if (e != hipSuccess) {
+        spr_set_error("spr_kmeans_assign_bf16: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+        return SPR_ELAUNCH;
+      }
+      lds_raised = true;
+    }
+    kmeans_assign_resident_kernel<128><<<dim3(static_cast<uint32_t>(per_batch), static_cast<uint32_t>(batch)),
+                                         ASSIGN_RESIDENT_THREADS, lds, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode,
+                                                                                  x_sq_out, n, k, labels);
+    SPR_LAUNCHED("kmeans_assign_resident_kernel");
+    return SPR_OK;
+  }
   switch (d) {
     case 64:
       kmeans_assign_bf16_kernel<64><<<grid, ASSIGN_THREADS, 0, stream>>>(xp, cp, c_sq, x_sq, x_sq_mode, x_sq_out, n, k,
