@@ -287,6 +287,13 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
       xsq[f] = total;
     }
 
+    // Per 32-centroid step each lane scans its 16 candidates (index c0 + 4 half +
+    // 8i + j, ascending in (i, j)) for the step's smallest unclamped distance
+    // r = (x_sq + c_sq) - 2 cross (one rounding per step; 2 cross is exact),
+    // strict <, so the lowest index wins among equal minima; the step's result
+    // then meets the running best once.  The clamp max(r, 0) changes the answer
+    // only when some r <= 0: all such candidates tie at 0 and the lowest index
+    // among them wins, which a (rare, wave-uniform) rescan of the step restores.
     float best[2] = {3.4e38f, 3.4e38f};
     int32_t best_idx[2] = {0, 0};
     for (int c0 = 0; c0 < kpad; c0 += 32) {
@@ -298,23 +305,61 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
         acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[0][s]), acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[1][s]), acc1, 0, 0, 0);
       }
+      const float* csq_step = csq_l + c0 + 4 * half;
+      float lb0 = 0.0f, lb1 = 0.0f;
+      int32_t lo0 = 0, lo1 = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int32_t cidx = c0 + 8 * i + 4 * half + j;
-          const float csq = csq_l[cidx];
-          // (x_sq + c_sq) - 2 cross, one rounding per step (2 * cross is exact)
-          const float d0 = fmaxf(__builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq)), 0.0f);
-          const float d1 = fmaxf(__builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq)), 0.0f);
-          const bool t0 = d0 < best[0];
-          const bool t1 = d1 < best[1];
-          best[0] = t0 ? d0 : best[0];
-          best_idx[0] = t0 ? cidx : best_idx[0];
-          best[1] = t1 ? d1 : best[1];
-          best_idx[1] = t1 ? cidx : best_idx[1];
+          const int off = 8 * i + j;
+          const float csq = csq_step[off];
+          const float r0 = __builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq));
+          const float r1 = __builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq));
+          if (off == 0) {
+            lb0 = r0;
+            lb1 = r1;
+          } else {
+            const bool t0 = r0 < lb0;
+            const bool t1 = r1 < lb1;
+            lb0 = t0 ? r0 : lb0;
+            lo0 = t0 ? off : lo0;
+            lb1 = t1 ? r1 : lb1;
+            lo1 = t1 ? off : lo1;
+          }
         }
       }
+      if (__ballot(lb0 <= 0.0f || lb1 <= 0.0f) != 0ull) {
+        // first candidate with r <= 0, in index order, at distance 0
+        bool found0 = false, found1 = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int off = 8 * i + j;
+            const float csq = csq_step[off];
+            const float r0 = __builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq));
+            const float r1 = __builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq));
+            if (lb0 <= 0.0f && !found0 && r0 <= 0.0f) {
+              lo0 = off;
+              found0 = true;
+            }
+            if (lb1 <= 0.0f && !found1 && r1 <= 0.0f) {
+              lo1 = off;
+              found1 = true;
+            }
+          }
+        }
+        lb0 = fmaxf(lb0, 0.0f);
+        lb1 = fmaxf(lb1, 0.0f);
+      }
+      const int32_t base = c0 + 4 * half;
+      const bool t0 = lb0 < best[0];
+      const bool t1 = lb1 < best[1];
+      best[0] = t0 ? lb0 : best[0];
+      best_idx[0] = t0 ? base + lo0 : best_idx[0];
+      best[1] = t1 ? lb1 : best[1];
+      best_idx[1] = t1 ? base + lo1 : best_idx[1];
     }
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
