@@ -205,14 +205,15 @@ __global__ void centroid_sq_kernel(const T* __restrict__ c, int64_t rows, int32_
   out[r] = s;
 }
 
-// Same assignment with the batch's centroids resident in LDS: a 768-thread
-// workgroup (three waves per SIMD) stages all k centroids (padded rows; zeros and c_sq = +inf past k)
-// once, then each wave walks 64-point blocks of the batch against them with no
-// further barriers, centroid reloads or staging work.  Used while the padded
-// centroids fit in LDS (k <= ASSIGN_RESIDENT_K at D = 128).
+// Same assignment with the batch's centroids resident in LDS: a 1024-thread
+// workgroup (four waves per SIMD) stages all k centroids once (padded rows;
+// zeros and c_sq = +inf past k), then each wave walks 64-point blocks of the
+// batch against them with no further barriers, centroid reloads or staging
+// work.  Used while the padded centroids fit in LDS (k <= ASSIGN_RESIDENT_K at
+// D = 128).
 constexpr int ASSIGN_RESIDENT_K = 512;
 
-constexpr int ASSIGN_RESIDENT_THREADS = 768;
+constexpr int ASSIGN_RESIDENT_THREADS = 1024;
 
 template <int D>
 __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resident_kernel(
