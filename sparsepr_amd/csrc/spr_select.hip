@@ -47,20 +47,56 @@ __device__ float block_max(float v, float* scratch) {
   return m;
 }
 
+// score(q, k) = sum_t q[t] k[t], sequential fused multiply-adds in t.  The key
+// centroid's row is read with 16-byte loads, 32 floats issued ahead of their
+// multiply-adds (16-byte aligned rows), so the chain does not wait on one load
+// per step.
+__device__ __forceinline__ float row_dot(const float* q_row, const float* kr, int d) {
+  float acc = 0.0f;
+  if ((d & 3) == 0 && (reinterpret_cast<uintptr_t>(kr) & 15) == 0) {
+    const spr::f32x4* k4 = reinterpret_cast<const spr::f32x4*>(kr);
+    const spr::f32x4* q4 = reinterpret_cast<const spr::f32x4*>(q_row);
+    const int n4 = d >> 2;
+    for (int t = 0; t < n4; t += 8) {
+      spr::f32x4 kv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) kv[u] = t + u < n4 ? k4[t + u] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (t + u < n4) {
+          const spr::f32x4 qv = q4[t + u];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = __builtin_fmaf(qv[e], kv[u][e], acc);
+        }
+      }
+    }
+  } else {
+    for (int t = 0; t < d; ++t) acc = __builtin_fmaf(q_row[t], kr[t], acc);
+  }
+  return acc;
+}
+
 // One workgroup per (bh, q-cluster) row.
+//   scores, max, weighted exp, sum (one thread, index order), probabilities;
+//   sort by (probability desc, index asc) with a bitonic network (the order is
+//   total, so the result equals a rank sort's);
+//   the shown cumsum of the sorted probabilities never decreases (terms >= 0,
+//   bf16 rounding monotone), so "remove rank r when r > 0 and the cumsum through
+//   r - 1 exceeds p" keeps exactly the ranks below cut = max(first such r,
+//   preserve): one thread walks the chain up to the crossing only.
 __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __restrict__ qc,
                                                                const float* __restrict__ kc,
                                                                const int32_t* __restrict__ k_sizes,
                                                                int32_t qn, int32_t kn, int32_t d, float sqrt_d,
                                                                float p, int32_t preserve, int32_t score_bf16,
                                                                uint8_t* __restrict__ map) {
-  __shared__ float q_row[512];
-  __shared__ float val[MAX_KC];
+  __shared__ __attribute__((aligned(16))) float q_row[512];
+  __shared__ __attribute__((aligned(16))) float val[MAX_KC];
   __shared__ float sorted_val[MAX_KC];
   __shared__ int32_t sorted_idx[MAX_KC];
-  __shared__ uint8_t keep[MAX_KC];
   __shared__ float scratch[SEL_THREADS / 64];
   __shared__ float denom_s;
+  __shared__ int32_t cut_s;
 
   const int64_t row = blockIdx.x;  // bh * qn + q
   const int64_t bh = row / qn;
@@ -72,12 +108,10 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
 
   float local_max = -__builtin_huge_valf();
   for (int j = threadIdx.x; j < kn; j += blockDim.x) {
-    const float* kr = kb + static_cast<int64_t>(j) * d;
-    float acc = 0.0f;
-    for (int t = 0; t < d; ++t) acc = __builtin_fmaf(q_row[t], kr[t], acc);
-    const float s = score_bf16 ? bf16r(bf16r(acc) / sqrt_d) : acc / sqrt_d;
-    val[j] = s;
-    local_max = fmaxf(local_max, s);
+    const float acc = row_dot(q_row, kb + static_cast<int64_t>(j) * d, d);
+    const float sc = score_bf16 ? bf16r(bf16r(acc) / sqrt_d) : acc / sqrt_d;
+    val[j] = sc;
+    local_max = fmaxf(local_max, sc);
   }
   const float m = block_max(local_max, scratch);
 
@@ -88,42 +122,73 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
   __syncthreads();
   if (threadIdx.x == 0) {
     float sum = 0.0f;
-    for (int j = 0; j < kn; ++j) sum = sum + val[j];
+    int j = 0;
+    for (; j + 4 <= kn; j += 4) {
+      const spr::f32x4 v = *reinterpret_cast<const spr::f32x4*>(&val[j]);
+      sum = sum + v[0];
+      sum = sum + v[1];
+      sum = sum + v[2];
+      sum = sum + v[3];
+    }
+    for (; j < kn; ++j) sum = sum + val[j];
     denom_s = sum > 1e-12f ? sum : 1e-12f;
   }
   __syncthreads();
   const float denom = denom_s;
-  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
-    const float prob = val[j] / denom;
-    val[j] = score_bf16 ? bf16r(prob) : prob;
+  int n2 = 1;
+  while (n2 < kn) n2 <<= 1;
+  for (int j = threadIdx.x; j < n2; j += blockDim.x) {
+    if (j < kn) {
+      const float prob = val[j] / denom;
+      sorted_val[j] = score_bf16 ? bf16r(prob) : prob;
+    } else {
+      sorted_val[j] = -__builtin_huge_valf();  // padding sorts last
+    }
+    sorted_idx[j] = j;
   }
   __syncthreads();
 
-  // rank sort: descending probability, ties by ascending index
-  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
-    const float pj = val[j];
-    int rank = 0;
-    for (int i = 0; i < kn; ++i) rank += ranks_before(val[i], i, pj, j) ? 1 : 0;
-    sorted_val[rank] = pj;
-    sorted_idx[rank] = j;
+  // bitonic sort: ranks_before(a, b) first
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < n2; i += blockDim.x) {
+        const int l = i ^ stride;
+        if (l > i) {
+          const float vi = sorted_val[i], vl = sorted_val[l];
+          const int32_t ii = sorted_idx[i], il = sorted_idx[l];
+          const bool first = (i & size) == 0;  // this run ends up in ranks_before order
+          const bool swap = first ? ranks_before(vl, il, vi, ii) : ranks_before(vi, ii, vl, il);
+          if (swap) {
+            sorted_val[i] = vl;
+            sorted_val[l] = vi;
+            sorted_idx[i] = il;
+            sorted_idx[l] = ii;
+          }
+        }
+      }
+      __syncthreads();
+    }
   }
-  __syncthreads();
+
   if (threadIdx.x == 0) {
     const float thr = score_bf16 ? bf16r(p) : p;
     float cum = 0.0f;
-    float prev = 0.0f;
+    float prev = 0.0f;  // shown cumsum through rank r - 1
+    int cut = kn;
     for (int r = 0; r < kn; ++r) {
+      if (r > 0 && prev > thr) {
+        cut = r > preserve ? r : preserve;
+        break;
+      }
       cum = cum + sorted_val[r];
-      const float shown = score_bf16 ? bf16r(cum) : cum;
-      bool remove = (r > 0) && (prev > thr);
-      if (r < preserve) remove = false;
-      keep[sorted_idx[r]] = remove ? 0 : 1;
-      prev = shown;
+      prev = score_bf16 ? bf16r(cum) : cum;
     }
+    cut_s = cut < kn ? cut : kn;
   }
   __syncthreads();
+  const int cut = cut_s;
   uint8_t* out = map + row * kn;
-  for (int j = threadIdx.x; j < kn; j += blockDim.x) out[j] = keep[j];
+  for (int r = threadIdx.x; r < kn; r += blockDim.x) out[sorted_idx[r]] = r < cut ? 1 : 0;
 }
 
 // One workgroup per (bh, q) row of scores [bh, qn, kn].
