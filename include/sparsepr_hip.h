@@ -194,6 +194,19 @@ int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense,
 int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
                      const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
                      float alpha, float norm_cap, void* out, hipStream_t stream);
+/* residual_repair.py:317-465 _fit_reduced_rank_residual_fp32, for weights given, m >= p,
+ * the full output basis of the raw residual and decomposition "eigh" (the N8 layer's
+ * configuration): weighted standardisation (:364-384), primal ridge solve (:424-434),
+ * top-rank eigenvectors of y_w^T y_w (:449-456; Householder tridiagonalisation,
+ * multisection and inverse iteration) and left = weight . basis (:463-464).
+ * x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
+ * [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (basis columns in
+ * ascending eigenvalue order).  Requires m >= p, m, p, d <= 128, 1 <= rank <= min(16, d).
+ * workspace: spr_rrr_fit_workspace(bh) bytes of device memory. */
+size_t spr_rrr_fit_workspace(int64_t bh);
+int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p, int32_t d,
+                int32_t rank, float ridge, float* x_mean, float* x_scale, float* y_mean, float* left, float* basis,
+                void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* residual_repair.py:656-700 n8_exact_probe_scatter_triton: out[b, rows[b, j]] =
  * dense[b, j] (rounded to bf16); dense dtype 0 bf16 / 2 fp32; rows outside [0, n) skipped. */
 int spr_probe_scatter(const void* dense, int32_t dense_dtype, const int32_t* rows, int64_t bh, int64_t n, int32_t m,

@@ -63,6 +63,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_repair_fit_prep": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "spr_repair_apply": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _f32, _f32, _vp, _vp]),
     "spr_probe_scatter": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
+    # rrr.hip
+    "spr_rrr_fit_workspace": (_sz, [_i64]),
+    "spr_rrr_fit": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp,
+                                   _vp, _sz, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

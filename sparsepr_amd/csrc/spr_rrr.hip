@@ -1,0 +1,846 @@
+// Weighted ridge reduced-rank residual fit.
+//
+// Replaces, for the configuration the N8 layer runs (weights given, M >= P,
+// full output basis of the raw residual, eigh):
+//   _fit_reduced_rank_residual_fp32 (src/sparsepr/models/cosmos3/residual_repair.py:317-465):
+//   weighted mean / variance standardisation (:364-384), the primal ridge solve
+//   (:424-434), the top-r eigenvectors of the weighted output gram y_w^T y_w
+//   (:449-456) and left = weight basis (:463-464).
+//
+// Per head, in fp32:
+//   w_sum = max(sum w, 1e-20); x_mean = sum w x / w_sum; x_scale = max(sqrt(sum w
+//   (x - x_mean)^2 / w_sum), 1e-5); y_mean = sum w y / w_sum;
+//   x_w = (x - x_mean) / x_scale * sqrt(w); y_w = (y - y_mean) * sqrt(w);
+//   G = x_w^T x_w + ridge I, B = y_w^T y_w;
+//   basis = top-`rank` eigenvectors of B, ascending eigenvalue order (as eigh);
+//   left = G^-1 x_w^T y_w basis = G^-1 x_w^T Z with Z = y_w basis.
+//
+// Four launches, stream ordered:
+//   rrr_stats_kernel   one workgroup per head: the weighted statistics.
+//   rrr_gram_kernel    20 workgroups per head: one 32 x 32 lower tile of G or B
+//                      each, mirrored, into the workspace.
+//   rrr_factor_kernel  two workgroups per head, side by side:
+//     y = 0: eigenvectors of B.  B is held in registers (thread t owns row t / 8,
+//            columns t % 8 + 8 q) and reduced to tridiagonal form by Householder
+//            reflections (two barriers per column); the top eigenvalues come from
+//            64-way multisection on Sturm counts (one wave per eigenvalue), their
+//            vectors from inverse iteration on the tridiagonal matrix (pivoted LU,
+//            three steps, members of a cluster orthogonalised against each other
+//            as they are computed), the reflections are applied back, and a
+//            Cholesky-QR pass makes the basis orthonormal to rounding.
+//     y = 1: Cholesky factor of G, register resident, one barrier per column,
+//            written over G in the workspace.
+//   rrr_solve_kernel   one workgroup per head: Z = y_w basis, x_w^T Z (one wave per
+//                      basis column), forward and back substitution in registers.
+#include "spr_common.h"
+
+namespace {
+
+constexpr int RRR_MAX = 128;  // M, P, D at most
+constexpr int RRR_MAX_RANK = 16;
+constexpr int RRR_THREADS = 1024;
+constexpr int RRR_MAT = RRR_MAX * RRR_MAX;  // one workspace matrix (floats)
+constexpr int RRR_LS = RRR_MAX + 1;         // padded LDS row: rows i and i + 1 start one bank apart
+
+// ---- lane reductions (DPP within rows of 16 lanes, readlane across rows)
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_read(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// Sum over the 8 lanes 8g .. 8g + 7 (every lane of the group gets the same value).
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  return v;
+}
+// Sum over the wave, uniform result.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x124>(v);  // row_ror 4
+  v += dpp_mov<0x128>(v);  // row_ror 8
+  return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x124>(v));
+  v = fmaxf(v, dpp_mov<0x128>(v));
+  return fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
+}
+// LDS written by some lanes of a wave, then read by others of the same wave.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+// a[q] for a runtime q as an OR of masked bit patterns: a select chain over the
+// array gets folded into one load from a selected address, which keeps the array
+// on the stack.
+__device__ __forceinline__ float pick16(const float (&a)[16], int q) {
+  int v = 0;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) v |= __float_as_int(a[u]) & -static_cast<int>(q == u);
+  return __int_as_float(v);
+}
+
+// ---- statistics: one workgroup of 256 threads per head
+__global__ __launch_bounds__(256) void rrr_stats_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                                                        const float* __restrict__ w, int32_t m, int32_t p, int32_t d,
+                                                        float* __restrict__ x_mean, float* __restrict__ x_scale,
+                                                        float* __restrict__ y_mean) {
+  const int t = threadIdx.x;
+  const int64_t h = blockIdx.x;
+  const float* xh = x + h * m * p;
+  const float* yh = y + h * m * d;
+  const float* wh = w + h * m;
+  float ws = 0.0f;
+  for (int r = 0; r < m; ++r) ws += wh[r];
+  ws = fmaxf(ws, 1e-20f);
+  if (t < p) {
+    float s = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < m; ++r) s += wh[r] * xh[r * p + t];
+    const float mean = s / ws;
+    float v = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < m; ++r) {
+      const float dv = xh[r * p + t] - mean;
+      v += wh[r] * (dv * dv);
+    }
+    x_mean[h * p + t] = mean;
+    x_scale[h * p + t] = fmaxf(sqrtf(v / ws), 1e-5f);
+  } else if (t >= RRR_MAX && t - RRR_MAX < d) {
+    const int c = t - RRR_MAX;
+    float s = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < m; ++r) s += wh[r] * yh[r * d + c];
+    y_mean[h * d + c] = s / ws;
+  }
+}
+
+// ---- G and B, 32 x 32 lower tiles (10 per matrix), mirrored; zero outside p x p / d x d
+__global__ __launch_bounds__(256) void rrr_gram_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                                                       const float* __restrict__ w, int32_t m, int32_t p, int32_t d,
+                                                       float ridge, const float* __restrict__ x_mean,
+                                                       const float* __restrict__ x_scale,
+                                                       const float* __restrict__ y_mean, float* __restrict__ ws) {
+  __shared__ float pa[RRR_MAX][33];
+  __shared__ float pb[RRR_MAX][33];
+  const int t = threadIdx.x;
+  const int64_t h = blockIdx.x;
+  const int which = blockIdx.y / 10;  // 0: G from x, 1: B from y
+  const int lt = blockIdx.y % 10;
+  const int ti = lt >= 6 ? 3 : (lt >= 3 ? 2 : (lt >= 1 ? 1 : 0));
+  const int tj = lt - ti * (ti + 1) / 2;
+  const int cols = which == 0 ? p : d;
+  const float* src = which == 0 ? x + h * m * p : y + h * m * d;
+  const float* mu = which == 0 ? x_mean + h * p : y_mean + h * d;
+  const float* wh = w + h * m;
+  for (int e = t; e < RRR_MAX * 32; e += 256) {
+    const int r = e >> 5, cc = e & 31;
+    const int ci = 32 * ti + cc, cj = 32 * tj + cc;
+    float vi = 0.0f, vj = 0.0f;
+    if (r < m) {
+      const float sw = sqrtf(wh[r]);
+      if (ci < cols) {
+        const float c0 = src[r * cols + ci] - mu[ci];
+        vi = (which == 0 ? c0 / x_scale[h * p + ci] : c0) * sw;
+      }
+      if (cj < cols) {
+        const float c0 = src[r * cols + cj] - mu[cj];
+        vj = (which == 0 ? c0 / x_scale[h * p + cj] : c0) * sw;
+      }
+    }
+    pa[r][cc] = vi;
+    pb[r][cc] = vj;
+  }
+  __syncthreads();
+  const int a = t >> 4, b = t & 15;
+  float s00 = 0.0f, s01 = 0.0f, s10 = 0.0f, s11 = 0.0f;
+  for (int r = 0; r < m; ++r) {
+    const float u0 = pa[r][2 * a], u1 = pa[r][2 * a + 1];
+    const float v0 = pb[r][2 * b], v1 = pb[r][2 * b + 1];
+    s00 += u0 * v0;
+    s01 += u0 * v1;
+    s10 += u1 * v0;
+    s11 += u1 * v1;
+  }
+  float* out = ws + (h * 2 + which) * RRR_MAT;
+  const float acc[2][2] = {{s00, s01}, {s10, s11}};
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int gi = 32 * ti + 2 * a + u, gj = 32 * tj + 2 * b + v;
+      const float val = acc[u][v] + ((which == 0 && gi == gj && gi < cols) ? ridge : 0.0f);
+      out[gi * RRR_MAX + gj] = val;
+      if (ti != tj) out[gj * RRR_MAX + gi] = val;
+    }
+  }
+}
+
+// ---- eigen path LDS layout (floats).  Householder columns and the p vectors are
+// stored permuted, j -> (j % 8) * 17 + j / 8, so that lane c's sixteen values
+// (j = c + 8 q) are consecutive and the eight lane groups start in distinct banks.
+constexpr int HV_STRIDE = 136;
+__device__ __forceinline__ int hv_perm(int j) { return (j & 7) * 17 + (j >> 3); }
+constexpr int EIG_HV = 0;                            // [128][136] Householder columns (raw, permuted)
+constexpr int EIG_DD = EIG_HV + RRR_MAX * HV_STRIDE;  // tridiagonal diagonal
+constexpr int EIG_EE = EIG_DD + RRR_MAX;             // off-diagonal
+constexpr int EIG_TAU = EIG_EE + RRR_MAX;            // reflector tau
+constexpr int EIG_SCL = EIG_TAU + RRR_MAX;           // reflector scale: v_j = raw_j * scl (j > k + 1)
+constexpr int EIG_PB = EIG_SCL + RRR_MAX;            // [2][136] p = tau A v (permuted)
+constexpr int EIG_PART = EIG_PB + 2 * HV_STRIDE;     // [2][16] per-wave p . v
+constexpr int EIG_LAM = EIG_PART + 32;               // [16] eigenvalues, descending
+constexpr int EIG_LU = EIG_LAM + RRR_MAX_RANK;       // [6][128][16] LU of T - lambda_s I, then X = vectors of T
+constexpr int EIG_VB = EIG_LU + 6 * RRR_MAX * 16;    // [16][128] eigenvectors of B
+constexpr int EIG_S = EIG_VB + 16 * RRR_MAX;         // [16][16] Gram of the vectors, then R
+constexpr int EIG_X = EIG_S + 256;                   // [16][16] R^-1
+constexpr int EIG_FLOATS = EIG_X + 256;
+
+__device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int n, int rank, float* __restrict__ basis) {
+  const int t = threadIdx.x, i = t >> 3, c = t & 7, lane = t & 63, wv = t >> 6;
+  float* hv = sm + EIG_HV;
+  float* dd = sm + EIG_DD;
+  float* ee = sm + EIG_EE;
+  float* tau = sm + EIG_TAU;
+  float* scl = sm + EIG_SCL;
+
+  float a[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) a[q] = bmat[i * RRR_MAX + c + 8 * q];
+  for (int e = t; e < EIG_PART + 32; e += RRR_THREADS) sm[e] = 0.0f;  // columns, p buffers, partials
+  __syncthreads();
+
+  // ---- Householder tridiagonalisation (lower), A <- H A H column by column.
+  // Columns go in blocks of eight: during block kb, a[q] holds column c + 8 (q + kb),
+  // so the column being reduced is a[0] of the lanes with c = k % 8 (the array shifts
+  // down one register per block).  Columns <= k read zeros from the column and p
+  // buffers, so their updates are no-ops without masks; groups of four registers that
+  // are past the end are skipped, and so are waves whose rows are all <= k.
+  int kb = 0;
+  for (; 8 * kb + 2 < n; ++kb) {
+    if (kb > 0) {
+#pragma unroll
+      for (int q = 0; q < 15; ++q) a[q] = a[q + 1];
+      a[15] = 0.0f;
+    }
+    const int nq = 16 - kb;  // registers still in the matrix
+    for (int kc = 0; kc < 8; ++kc) {
+      const int k = 8 * kb + kc;
+      if (k + 2 >= n) break;
+      if (c == kc) {
+        hv[k * HV_STRIDE + hv_perm(i)] = i > k ? a[0] : 0.0f;  // zero on and above the diagonal
+        if (i == k) dd[k] = a[0];
+      }
+      __syncthreads();
+      const float* col = hv + k * HV_STRIDE;
+      const float c0 = col[hv_perm(lane)], c1 = col[hv_perm(lane + 64)];
+      const float x0 = lane > k + 1 ? c0 : 0.0f;
+      const float x1 = lane + 64 > k + 1 ? c1 : 0.0f;
+      const float sigma = wave_sum(x0 * x0 + x1 * x1);
+      const float alpha = col[hv_perm(k + 1)];
+      float tk = 0.0f, sk = 0.0f, beta = alpha;
+      if (sigma != 0.0f) {
+        const float nrm = __builtin_amdgcn_sqrtf(alpha * alpha + sigma);
+        beta = alpha >= 0.0f ? -nrm : nrm;
+        tk = (beta - alpha) * __builtin_amdgcn_rcpf(beta);
+        sk = __builtin_amdgcn_rcpf(alpha - beta);
+      }
+      if (t == 0) {
+        ee[k] = beta;
+        tau[k] = tk;
+        scl[k] = sk;
+      }
+      const bool live = 8 * wv + 7 > k;  // this wave holds rows below k
+      float* pb = sm + EIG_PB + (k & 1) * HV_STRIDE;
+      float* pt = sm + EIG_PART + (k & 1) * 16;
+      float v[16];
+      float pr = 0.0f, vi = 0.0f;
+      if (live) {
+        const float* cq = col + c * 17 + kb;
+        float cv[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) cv[q] = cq[q];
+        // v_{k+1} = 1 sits in register 0 of lane kc + 1, or register 1 of lane 0 (kc = 7)
+        const bool one0 = c == kc + 1, one1 = kc == 7 && c == 0;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          if (4 * g4 < nq) {
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int q = 4 * g4 + u;
+              const float vq = cv[q] * sk;
+              v[q] = q == 0 ? (one0 ? 1.0f : vq) : (q == 1 ? (one1 ? 1.0f : vq) : vq);
+              pr = fmaf(a[q], v[q], pr);
+            }
+          }
+        }
+        pr = sum8(pr) * tk;
+        vi = i == k + 1 ? 1.0f : col[hv_perm(i)] * sk;
+        const float kp = wave_sum((c == 0 && i > k) ? pr * vi : 0.0f);
+        if (c == 0) pb[hv_perm(i)] = i > k ? pr : 0.0f;
+        if (lane == 0) pt[wv] = kp;
+      } else {
+        if (c == 0) pb[hv_perm(i)] = 0.0f;
+        if (lane == 0) pt[wv] = 0.0f;
+      }
+      __syncthreads();
+      if (live) {
+        const float4* p4 = reinterpret_cast<const float4*>(pt);
+        const float4 s0 = p4[0], s1 = p4[1], s2 = p4[2], s3 = p4[3];
+        const float ks = ((s0.x + s0.y) + (s0.z + s0.w)) + ((s1.x + s1.y) + (s1.z + s1.w)) +
+                         (((s2.x + s2.y) + (s2.z + s2.w)) + ((s3.x + s3.y) + (s3.z + s3.w)));
+        const float kk = 0.5f * tk * ks;
+        const float wi = i > k ? pr - kk * vi : 0.0f;
+        const float* pq = pb + c * 17 + kb;
+        float pv[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) pv[q] = pq[q];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          if (4 * g4 < nq) {
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int q = 4 * g4 + u;
+              const float wj = fmaf(-kk, v[q], pv[q]);
+              a[q] = fmaf(-vi, wj, fmaf(-wi, v[q], a[q]));
+            }
+          }
+        }
+      }
+    }
+  }
+  // trailing 2 x 2 (or 1 x 1) block: column j sits in register j / 8 - (kb - 1)
+  {
+    const int sh = kb > 0 ? kb - 1 : 0;
+    if (n >= 2) {
+      if (i == n - 2 && c == ((n - 2) & 7)) dd[n - 2] = pick16(a, ((n - 2) >> 3) - sh);
+      if (i == n - 1 && c == ((n - 1) & 7)) dd[n - 1] = pick16(a, ((n - 1) >> 3) - sh);
+      if (i == n - 1 && c == ((n - 2) & 7)) ee[n - 2] = pick16(a, ((n - 2) >> 3) - sh);
+    } else if (t == 0) {
+      dd[0] = a[0];
+    }
+  }
+  __syncthreads();
+
+  // ---- bounds of the spectrum (every wave, lanes over the rows, same values everywhere)
+  float lo, hi, tnorm, e2max;
+  {
+    float lo_l = 3.4e38f, hi_l = -3.4e38f, tn_l = 0.0f, e2_l = 0.0f;
+    for (int j = lane; j < n; j += 64) {
+      const float el = j > 0 ? fabsf(ee[j - 1]) : 0.0f;
+      const float er = j + 1 < n ? fabsf(ee[j]) : 0.0f;
+      lo_l = fminf(lo_l, dd[j] - (el + er));
+      hi_l = fmaxf(hi_l, dd[j] + (el + er));
+      tn_l = fmaxf(tn_l, fabsf(dd[j]) + el + er);
+      e2_l = fmaxf(e2_l, er * er);
+    }
+    lo = -wave_max(-lo_l);
+    hi = wave_max(hi_l);
+    tnorm = wave_max(tn_l);
+    e2max = wave_max(e2_l);
+  }
+  const float pivmin = 1.17549435e-38f * fmaxf(1.0f, e2max);
+  const float slack = 2.0f * 1.1920929e-7f * tnorm + pivmin;
+  lo -= slack;
+  hi += slack;
+
+  // ---- top eigenvalues by multisection on Sturm counts: the 16 lanes of group g of
+  // wave w evaluate 16 points inside the bracket of the (4 w + g + 1)-th largest
+  // eigenvalue, which shrinks 17-fold per round; five rounds leave it about
+  // 1.4e-6 (hi - lo) wide, which inverse iteration does not need to be narrower.
+  float* lam = sm + EIG_LAM;
+  if (4 * wv < rank) {
+    const int grp = lane >> 4, gl = lane & 15;
+    const int sv = 4 * wv + grp;
+    const int idx = n - 1 - min(sv, rank - 1);  // ascending index
+    float l = lo, u = hi;
+    for (int round = 0; round < 5; ++round) {
+      const float step = (u - l) * (1.0f / 17.0f);
+      const float xq = l + step * static_cast<float>(gl + 1);
+      // Sturm count: eigenvalues below xq
+      float q = dd[0] - xq;
+      if (fabsf(q) < pivmin) q = -pivmin;
+      int cnt = q < 0.0f;
+#pragma unroll 4
+      for (int j = 1; j < n; ++j) {
+        const float e = ee[j - 1];
+        q = (dd[j] - xq) - (e * e) * __builtin_amdgcn_rcpf(q);
+        if (fabsf(q) < pivmin) q = -pivmin;
+        cnt += q < 0.0f;
+      }
+      const uint64_t mask = __ballot(cnt <= idx);
+      const int below = __popcll((mask >> (16 * grp)) & 0xFFFFull);  // points at or below the eigenvalue
+      const float nl = below > 0 ? l + step * static_cast<float>(below) : l;
+      const float nu = below < 16 ? l + step * static_cast<float>(below + 1) : u;
+      l = nl;
+      u = nu;
+    }
+    if (gl == 0 && sv < rank) lam[sv] = 0.5f * (l + u);
+  }
+  __syncthreads();
+
+  // ---- eigenvectors of T by inverse iteration: lane s of wave 0 computes vector s
+  // (column s of X), with the pivoted LU of T - lambda_s I in its own columns of the
+  // U / L arrays.  Members of a cluster (eigenvalue gaps below 1e-3 ||T||) run in
+  // successive rounds and are orthogonalised against the members before them.
+  float* X = sm + EIG_LU + 5 * RRR_MAX * 16;  // [128][16]
+  if (wv == 0) {
+    const float ortol = 1e-3f * tnorm;
+    const float ptol = fmaxf(1.1920929e-7f * tnorm, 1e-30f);  // smallest pivot magnitude
+    const int s = lane;
+    const bool act = s < rank;
+    int mypos = 0, maxpos = 0;
+    {
+      int pos = 0;
+      for (int u = 1; u < rank; ++u) {
+        pos = (lam[u - 1] - lam[u] < ortol) ? pos + 1 : 0;
+        if (u == s) mypos = pos;
+        maxpos = max(maxpos, pos);
+      }
+    }
+    float* RU0 = sm + EIG_LU;  // [128][16] 1 / pivot
+    float* U1 = RU0 + RRR_MAX * 16;
+    float* U2 = U1 + RRR_MAX * 16;
+    float* LM = U2 + RRR_MAX * 16;
+    float* PV = LM + RRR_MAX * 16;
+    const float lm = act ? lam[s] : 0.0f;
+    // the tridiagonal in registers (lane l holds entries l and l + 64), read by readlane
+    const float d0 = dd[lane], d1 = dd[lane + 64], e0 = ee[lane], e1 = ee[lane + 64];
+    // (readlane of registers every lane wrote before the divergent part below)
+    auto dget = [&](int j) {
+      const float r0 = lane_read(d0, j & 63), r1 = lane_read(d1, j & 63);
+      return j < 64 ? r0 : r1;
+    };
+    auto eget = [&](int j) {
+      const float r0 = lane_read(e0, j & 63), r1 = lane_read(e1, j & 63);
+      return j < 64 ? r0 : r1;
+    };
+    for (int rho = 0; rho <= maxpos; ++rho) {
+      if (act && mypos == rho) {
+        float cd = dget(0) - lm;
+        float cs = n > 1 ? eget(0) : 0.0f;
+        for (int j = 0; j + 1 < n; ++j) {
+          const float sub = eget(j);
+          const float nd = dget(j + 1) - lm;
+          const float ns = j + 2 < n ? eget(j + 1) : 0.0f;
+          const bool sw = fabsf(cd) < fabsf(sub);
+          const float piv = sw ? sub : cd;
+          const float oth = sw ? cd : sub;
+          const float l = oth == 0.0f ? 0.0f : oth * __builtin_amdgcn_rcpf(piv);
+          const float pv = fabsf(piv) < ptol ? copysignf(ptol, piv) : piv;
+          RU0[j * 16 + s] = __builtin_amdgcn_rcpf(pv);
+          U1[j * 16 + s] = sw ? nd : cs;
+          U2[j * 16 + s] = sw ? ns : 0.0f;
+          LM[j * 16 + s] = l;
+          PV[j * 16 + s] = sw ? 1.0f : 0.0f;
+          const float ncd = sw ? cs - l * nd : nd - l * cs;
+          cs = sw ? -l * ns : ns;
+          cd = ncd;
+        }
+        const float pv = fabsf(cd) < ptol ? copysignf(ptol, cd) : cd;
+        RU0[(n - 1) * 16 + s] = __builtin_amdgcn_rcpf(pv);
+        // start vector: deterministic, distinct per eigenvalue
+        for (int j = 0; j < n; ++j) {
+          const uint32_t hsh = (static_cast<uint32_t>(j) * 2654435761u) ^ (static_cast<uint32_t>(s + 1) * 0x9E3779B9u);
+          const uint32_t mix = (hsh ^ (hsh >> 15)) * 0x2C1B3C6Du;
+          X[j * 16 + s] = static_cast<float>((mix >> 8) & 0xFFFF) * (2.0f / 65535.0f) - 1.0f;
+        }
+        // Three solves.  Between solves X is only rescaled (by 1 / max |x|, applied as
+        // the next forward pass loads it); cluster members are also orthogonalised
+        // against the members before them.  The norm is taken once, at the end.
+        float sc = 1.0f;
+        for (int it = 0; it < 3; ++it) {
+          // P, L: forward elimination of the right-hand side, 8 rows per batch of loads
+          float cur = X[s] * sc;
+          for (int j0 = 0; j0 + 1 < n; j0 += 8) {
+            float nx[8], lv[8], pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int j = min(j0 + u, RRR_MAX - 2);
+              nx[u] = X[(j + 1) * 16 + s];
+              lv[u] = LM[j * 16 + s];
+              pv[u] = PV[j * 16 + s];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int j = j0 + u;
+              if (j + 1 < n) {
+                const bool sw = pv[u] != 0.0f;
+                const float xn = nx[u] * sc;
+                X[j * 16 + s] = sw ? xn : cur;
+                cur = sw ? cur - lv[u] * xn : xn - lv[u] * cur;
+              }
+            }
+          }
+          // U: back substitution, tracking the largest magnitude
+          float x1 = cur * RU0[(n - 1) * 16 + s], x2 = 0.0f;
+          X[(n - 1) * 16 + s] = x1;
+          float mx = fabsf(x1);
+          for (int j0 = n - 2; j0 >= 0; j0 -= 8) {
+            float xi[8], u1[8], u2[8], ru[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int j = max(j0 - u, 0);
+              xi[u] = X[j * 16 + s];
+              u1[u] = U1[j * 16 + s];
+              u2[u] = U2[j * 16 + s];
+              ru[u] = RU0[j * 16 + s];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int j = j0 - u;
+              if (j >= 0) {
+                const float xv = (xi[u] - u1[u] * x1 - u2[u] * x2) * ru[u];
+                X[j * 16 + s] = xv;
+                mx = fmaxf(mx, fabsf(xv));
+                x2 = x1;
+                x1 = xv;
+              }
+            }
+          }
+          sc = mx > 0.0f ? 1.0f / mx : 1.0f;
+          if (mypos > 0) {
+            for (int j = 0; j < n; ++j) X[j * 16 + s] *= sc;
+            sc = 1.0f;
+            for (int o = s - mypos; o < s; ++o) {
+              float dt = 0.0f;
+              for (int j = 0; j < n; ++j) dt += X[j * 16 + s] * X[j * 16 + o];
+              for (int j = 0; j < n; ++j) X[j * 16 + s] -= dt * X[j * 16 + o];
+            }
+            float ss = 0.0f;
+            for (int j = 0; j < n; ++j) ss += X[j * 16 + s] * X[j * 16 + s];
+            const float nr = sqrtf(ss);
+            sc = nr > 0.0f ? 1.0f / nr : 0.0f;
+          }
+        }
+        float ss = 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) {
+          const float xv = X[j * 16 + s] * sc;
+          ss += xv * xv;
+        }
+        const float nr = sqrtf(ss);
+        const float f = nr > 0.0f ? sc / nr : 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) X[j * 16 + s] *= f;
+      }
+      wave_sync();
+    }
+  }
+  __syncthreads();
+
+  // ---- back to B's coordinates: y <- H_0 H_1 ... H_{n-3} y, four vectors per wave
+  float* vb = sm + EIG_VB;
+  if (4 * wv < rank) {
+    float y0[4], y1[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sv = 4 * wv + u;
+      y0[u] = (sv < rank && lane < n) ? X[lane * 16 + sv] : 0.0f;
+      y1[u] = (sv < rank && lane + 64 < n) ? X[(lane + 64) * 16 + sv] : 0.0f;
+    }
+    const int pl0 = hv_perm(lane), pl1 = hv_perm(lane + 64);
+    int k = n - 3;
+    float tk = 0.0f, sk = 0.0f, r0 = 0.0f, r1 = 0.0f;
+    if (k >= 0) {
+      tk = tau[k];
+      sk = scl[k];
+      r0 = hv[k * HV_STRIDE + pl0];
+      r1 = hv[k * HV_STRIDE + pl1];
+    }
+    for (; k >= 0; --k) {
+      // next reflector's data, loaded while this one is applied
+      const int kn = max(k - 1, 0);
+      const float tn = tau[kn], sn = scl[kn];
+      const float n0 = hv[kn * HV_STRIDE + pl0], n1 = hv[kn * HV_STRIDE + pl1];
+      if (tk != 0.0f) {
+        const float v0 = lane == k + 1 ? 1.0f : r0 * sk;
+        const float v1 = lane + 64 == k + 1 ? 1.0f : r1 * sk;
+        float dt[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dt[u] = tk * wave_sum(v0 * y0[u] + v1 * y1[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          y0[u] -= dt[u] * v0;
+          y1[u] -= dt[u] * v1;
+        }
+      }
+      tk = tn;
+      sk = sn;
+      r0 = n0;
+      r1 = n1;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int sv = 4 * wv + u;
+      if (sv < rank) {
+        vb[sv * RRR_MAX + lane] = y0[u];
+        vb[sv * RRR_MAX + lane + 64] = y1[u];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- Cholesky-QR: S = V^T V = R^T R, basis = V R^-1.  The 16 x 16 factor and
+  // inverse run in wave 0, lane j holding column j, with static register indices.
+  float* S = sm + EIG_S;
+  float* XR = sm + EIG_X;
+  if (wv < rank) {
+    const float y0 = vb[wv * RRR_MAX + lane], y1 = vb[wv * RRR_MAX + lane + 64];
+    for (int s2 = 0; s2 <= wv; ++s2) {
+      const float dt = wave_sum(y0 * vb[s2 * RRR_MAX + lane] + y1 * vb[s2 * RRR_MAX + lane + 64]);
+      if (lane == 0) {
+        S[s2 * 16 + wv] = dt;
+        S[wv * 16 + s2] = dt;
+      }
+    }
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const int j = lane;
+    const bool on = j < rank;
+    float col[16];  // col[r] = S[r][j], then R[r][j]
+#pragma unroll
+    for (int r = 0; r < 16; ++r) col[r] = (on && r < rank) ? S[r * 16 + j] : (r == j ? 1.0f : 0.0f);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float rkk = sqrtf(lane_read(col[k], k));
+      // row k of R: R[k][j] = S[k][j] / R[k][k] for j > k, R[k][k] itself for j = k
+      if (j > k) col[k] = col[k] / rkk;
+      else if (j == k) col[k] = rkk;
+      // trailing update: S[r][j] -= R[k][r] R[k][j] for k < r <= j
+#pragma unroll
+      for (int r = k + 1; r < 16; ++r) {
+        const float rkr = lane_read(col[k], r);
+        if (r <= j) col[r] -= rkr * col[k];
+      }
+    }
+    // X = R^-1 column j: X[r][j] for r = j .. 0, X[r][j] = 0 above j
+    float xr[16];
+#pragma unroll
+    for (int r = 15; r >= 0; --r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int u = r + 1; u < 16; ++u) acc += lane_read(col[r], u) * xr[u];  // R[r][u]: register r of lane u
+      const float rrr = lane_read(col[r], r);
+      xr[r] = r > j ? 0.0f : (r == j ? 1.0f / rrr : -acc / rrr);
+    }
+    if (on) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) XR[r * 16 + j] = xr[r];
+    }
+  }
+  __syncthreads();
+  if (wv < rank) {
+    float q0 = 0.0f, q1 = 0.0f;
+    for (int s = 0; s <= wv; ++s) {
+      const float f = XR[s * 16 + wv];
+      q0 += vb[s * RRR_MAX + lane] * f;
+      q1 += vb[s * RRR_MAX + lane + 64] * f;
+    }
+    // eigenvalue rank wv (0 = largest) goes to column rank - 1 - wv: ascending order
+    const int col = rank - 1 - wv;
+    if (lane < n) basis[lane * rank + col] = q0;
+    if (lane + 64 < n) basis[(lane + 64) * rank + col] = q1;
+  }
+}
+
+// Cholesky of G (p x p, register resident), L written over G (lower triangle).  The
+// whole trailing block is updated (it stays symmetric), so a lane needs no per-column
+// test.  Columns go in blocks of eight as in the tridiagonalisation (g[0] of lanes
+// c = k % 8 is the pivot column, the array shifts down one register per block);
+// groups of four registers past the end are skipped, and so are waves whose rows
+// are all finished.
+__device__ void rrr_cholesky(float* sm, float* __restrict__ gmat, int p) {
+  const int t = threadIdx.x, i = t >> 3, c = t & 7, wv = t >> 6;
+  float g[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) g[q] = gmat[i * RRR_MAX + c + 8 * q];
+  if (t < 2 * HV_STRIDE) sm[t] = 0.0f;
+  __syncthreads();  // G read before L is written over it; column buffers cleared
+  for (int kb = 0; 8 * kb < p; ++kb) {
+    if (kb > 0) {
+#pragma unroll
+      for (int q = 0; q < 15; ++q) g[q] = g[q + 1];
+      g[15] = 0.0f;
+    }
+    const int nq = 16 - kb;
+    for (int kc = 0; kc < 8; ++kc) {
+      const int k = 8 * kb + kc;
+      if (k >= p) break;
+      float* buf = sm + (k & 1) * HV_STRIDE;
+      if (c == kc) buf[hv_perm(i)] = i >= k ? g[0] : 0.0f;
+      __syncthreads();
+      const float dk = buf[hv_perm(k)];
+      if (c == kc && i >= k && i < p) gmat[i * RRR_MAX + k] = g[0] / sqrtf(dk);
+      if (8 * wv + 7 > k) {
+        const float f = i > k ? buf[hv_perm(i)] * __builtin_amdgcn_rcpf(dk) : 0.0f;
+        const float* bq = buf + c * 17 + kb;
+        float bv[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) bv[q] = bq[q];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          if (4 * g4 < nq) {
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < 4; ++u) g[4 * g4 + u] = fmaf(-f, bv[4 * g4 + u], g[4 * g4 + u]);
+          }
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(RRR_THREADS, 1) void rrr_factor_kernel(float* __restrict__ ws, int32_t p, int32_t d,
+                                                                    int32_t rank, float* __restrict__ basis) {
+  __shared__ float sm[EIG_FLOATS];
+  const int64_t h = blockIdx.x;
+  if (blockIdx.y == 1) {
+    rrr_cholesky(sm, ws + (h * 2) * RRR_MAT, p);
+  } else {
+    rrr_eigen(sm, ws + (h * 2 + 1) * RRR_MAT, d, rank, basis + h * d * rank);
+  }
+}
+
+// Z = y_w basis, rb = x_w^T Z, left = L^-T L^-1 rb.
+__global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* __restrict__ x,
+                                                                   const float* __restrict__ y,
+                                                                   const float* __restrict__ w, int32_t m, int32_t p,
+                                                                   int32_t d, int32_t rank,
+                                                                   const float* __restrict__ x_mean,
+                                                                   const float* __restrict__ x_scale,
+                                                                   const float* __restrict__ y_mean,
+                                                                   const float* __restrict__ ws,
+                                                                   const float* __restrict__ basis,
+                                                                   float* __restrict__ left) {
+  __shared__ float ls[RRR_MAX * RRR_LS];  // L (lower)
+  __shared__ float xt[RRR_MAX * RRR_LS];  // x_w^T
+  __shared__ __align__(16) float zs[RRR_MAX][RRR_MAX_RANK];
+  __shared__ __align__(16) float bs[RRR_MAX][RRR_MAX_RANK];
+  const int t = threadIdx.x, i = t >> 3, c = t & 7, lane = t & 63, wv = t >> 6;
+  const int64_t h = blockIdx.x;
+  const float* xh = x + h * m * p;
+  const float* yh = y + h * m * d;
+  const float* lg = ws + (h * 2) * RRR_MAT;
+  for (int e = t; e < RRR_MAX * RRR_MAX_RANK; e += RRR_THREADS) {
+    const int r = e / RRR_MAX_RANK, j = e % RRR_MAX_RANK;
+    bs[r][j] = (r < d && j < rank) ? basis[(h * d + r) * rank + j] : 0.0f;
+  }
+  for (int e = t; e < RRR_MAT; e += RRR_THREADS) {
+    const int r = e >> 7, cc = e & 127;
+    ls[r * RRR_LS + cc] = (r < p && cc <= r) ? lg[e] : 0.0f;
+  }
+  // thread (row i, columns c + 8 q): x_w to LDS transposed, y_w in registers
+  const float sw = i < m ? sqrtf(w[h * m + i]) : 0.0f;
+  float yw[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int j = c + 8 * q;
+    xt[j * RRR_LS + i] = (i < m && j < p) ? (xh[i * p + j] - x_mean[h * p + j]) / x_scale[h * p + j] * sw : 0.0f;
+    yw[q] = (i < m && j < d) ? (yh[i * d + j] - y_mean[h * d + j]) * sw : 0.0f;
+  }
+  __syncthreads();
+  // Z[i][*] = sum_k y_w[i][k] basis[k][*], reduced over the 8 lanes of the row
+  {
+    float z[RRR_MAX_RANK];
+#pragma unroll
+    for (int j = 0; j < RRR_MAX_RANK; ++j) z[j] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const float4* br = reinterpret_cast<const float4*>(&bs[c + 8 * q][0]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float4 bv = br[u];
+        z[4 * u + 0] += yw[q] * bv.x;
+        z[4 * u + 1] += yw[q] * bv.y;
+        z[4 * u + 2] += yw[q] * bv.z;
+        z[4 * u + 3] += yw[q] * bv.w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RRR_MAX_RANK; ++j) z[j] = sum8(z[j]);
+    zs[i][c] = pick16(z, c);
+    zs[i][c + 8] = pick16(z, c + 8);
+  }
+  __syncthreads();
+  if (wv >= rank) return;
+  // rb[row][wv] for rows lane and lane + 64
+  const int j = wv;
+  float b0 = 0.0f, b1 = 0.0f;
+  for (int r = 0; r < m; ++r) {
+    const float zr = zs[r][j];
+    b0 += xt[lane * RRR_LS + r] * zr;
+    b1 += xt[(lane + 64) * RRR_LS + r] * zr;
+  }
+  // forward: L y = rb
+  for (int k = 0; k < p; ++k) {
+    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
+    const float yk = bk / ls[k * RRR_LS + k];
+    if (lane == (k & 63)) {
+      if (k < 64) b0 = yk;
+      else b1 = yk;
+    }
+    if (lane > k && lane < p) b0 -= ls[lane * RRR_LS + k] * yk;
+    if (lane + 64 > k && lane + 64 < p) b1 -= ls[(lane + 64) * RRR_LS + k] * yk;
+  }
+  // backward: L^T x = y
+  for (int k = p - 1; k >= 0; --k) {
+    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
+    const float xk = bk / ls[k * RRR_LS + k];
+    if (lane == (k & 63)) {
+      if (k < 64) b0 = xk;
+      else b1 = xk;
+    }
+    if (lane < k) b0 -= ls[k * RRR_LS + lane] * xk;
+    if (lane + 64 < k) b1 -= ls[k * RRR_LS + lane + 64] * xk;
+  }
+  if (lane < p) left[(h * p + lane) * rank + j] = b0;
+  if (lane + 64 < p) left[(h * p + lane + 64) * rank + j] = b1;
+}
+
+}  // namespace
+
+extern "C" size_t spr_rrr_fit_workspace(int64_t bh) {
+  return bh <= 0 ? 0 : static_cast<size_t>(bh) * 2 * RRR_MAT * sizeof(float);
+}
+
+// x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
+// [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (fp32).
+// Requires m >= p, m, p, d <= 128, 1 <= rank <= min(16, d).
+extern "C" int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
+                           int32_t d, int32_t rank, float ridge, float* x_mean, float* x_scale, float* y_mean,
+                           float* left, float* basis, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && m >= 1 && p >= 1 && d >= 1, "spr_rrr_fit: bad size");
+  SPR_REQUIRE(m >= p, "spr_rrr_fit: needs m >= p (got m=%d, p=%d)", m, p);
+  SPR_REQUIRE(m <= RRR_MAX && p <= RRR_MAX && d <= RRR_MAX, "spr_rrr_fit: m, p, d must be at most %d", RRR_MAX);
+  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d, "spr_rrr_fit: rank %d outside [1, min(16, d)]", rank);
+  SPR_REQUIRE(ridge >= 0.0f, "spr_rrr_fit: ridge must be non-negative");
+  SPR_REQUIRE(bh <= 65535, "spr_rrr_fit: too many heads");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(x && y && weights && x_mean && x_scale && y_mean && left && basis && workspace,
+              "spr_rrr_fit: null pointer");
+  SPR_REQUIRE(workspace_bytes >= spr_rrr_fit_workspace(bh), "spr_rrr_fit: workspace too small (%zu < %zu)",
+              workspace_bytes, spr_rrr_fit_workspace(bh));
+  float* ws = static_cast<float*>(workspace);
+  const uint32_t nb = static_cast<uint32_t>(bh);
+  rrr_stats_kernel<<<dim3(nb), 256, 0, stream>>>(x, y, weights, m, p, d, x_mean, x_scale, y_mean);
+  SPR_LAUNCHED("rrr_stats_kernel");
+  rrr_gram_kernel<<<dim3(nb, 20), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, ws);
+  SPR_LAUNCHED("rrr_gram_kernel");
+  rrr_factor_kernel<<<dim3(nb, 2), RRR_THREADS, 0, stream>>>(ws, p, d, rank, basis);
+  SPR_LAUNCHED("rrr_factor_kernel");
+  rrr_solve_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, x_mean, x_scale, y_mean, ws,
+                                                         basis, left);
+  SPR_LAUNCHED("rrr_solve_kernel");
+  return SPR_OK;
+}

@@ -151,6 +151,8 @@ def _fit_fp32(x_fit, y_fit, *, rank, ridge, weights, output_basis_backend, cache
         raise RuntimeError(f"RRR basis_source must be 'fitted_residual' or 'raw_residual', got {basis_source!r}.")
     x = x_fit.float()
     y = y_fit.float()
+    if _rrr_fit_fused(x, y, weights, rank, output_basis_backend, basis_source):
+        return _rrr_fit_hip(x, y, weights, int(rank), float(ridge))
     if weights is None:
         w = torch.ones((*x.shape[:2], 1), device=x.device, dtype=torch.float32)
         x_mean = x.mean(dim=1, keepdim=True)
@@ -217,6 +219,45 @@ def _fit_fp32(x_fit, y_fit, *, rank, ridge, weights, output_basis_backend, cache
         left = torch.bmm(xw.transpose(1, 2), torch.bmm(dual, basis)).contiguous()
     else:
         left = torch.bmm(weight, basis).contiguous()
+    return x_mean, x_scale, y_mean, left, basis
+
+
+def _rrr_fit_fused(x, y, weights, rank, output_basis_backend, basis_source):
+    """Whether the fit is the one spr_rrr_fit computes in one kernel: weights given,
+    M >= P (primal ridge solve), the eigen basis of the raw weighted residual, every
+    dimension at most 128 and rank at most 16, on the GPU."""
+    bh, m, p = (int(v) for v in x.shape)
+    d = int(y.shape[2])
+    if not (x.is_cuda and weights is not None and basis_source == "raw_residual"):
+        return False
+    if output_basis_backend == "skinny" and m < d:
+        return False
+    return bh > 0 and p <= m <= 128 and d <= 128 and int(rank) <= 16
+
+
+def _rrr_fit_hip(x, y, weights, rank, ridge):
+    """Weighted standardisation, primal ridge solve and the top-rank eigenvectors of
+    y_w^T y_w in four launches (reference :364-384, :424-434, :449-456, :463-464).
+    Eigenvector signs (as eigh's) are arbitrary; left . basis^T does not depend on them."""
+    dev = _lib.require_gpu(x, y, weights, what="reduced-rank residual fit")
+    if weights.shape != x.shape[:2]:
+        raise RuntimeError(f"RRR weights must have shape {tuple(x.shape[:2])}, got {tuple(weights.shape)}.")
+    bh, m, p = (int(v) for v in x.shape)
+    d = int(y.shape[2])
+    x = x.contiguous()
+    y = y.contiguous()
+    w = weights.to(device=dev, dtype=torch.float32).contiguous()
+    f32 = dict(device=dev, dtype=torch.float32)
+    x_mean = torch.empty((bh, 1, p), **f32)
+    x_scale = torch.empty((bh, 1, p), **f32)
+    y_mean = torch.empty((bh, 1, d), **f32)
+    left = torch.empty((bh, p, rank), **f32)
+    basis = torch.empty((bh, d, rank), **f32)
+    ws_bytes = int(_lib.query("spr_rrr_fit_workspace", bh))
+    ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
+    _lib.call("spr_rrr_fit", _lib.ptr(x), _lib.ptr(y), _lib.ptr(w), bh, m, p, d, rank, ridge, _lib.ptr(x_mean),
+              _lib.ptr(x_scale), _lib.ptr(y_mean), _lib.ptr(left), _lib.ptr(basis), _lib.ptr(ws), ws_bytes,
+              _lib.stream(dev))
     return x_mean, x_scale, y_mean, left, basis
 
 

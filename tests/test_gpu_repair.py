@@ -103,6 +103,70 @@ def test_rrr_fit_matches_float64(dev, oracle, m, p):
     assert np.allclose(gl, rl, rtol=2e-3, atol=2e-4)
 
 
+@pytest.mark.parametrize("m,p,d,rank", [(128, 128, 128, 16), (128, 64, 128, 16), (96, 96, 33, 5), (17, 9, 7, 1)])
+def test_rrr_fused_fit_kernel(dev, oracle, m, p, d, rank):
+    """spr_rrr_fit (one-sided Jacobi basis, Cholesky ridge solve) against the float64 fit:
+    statistics, the basis-independent map left . basis^T, an orthonormal basis and
+    basis^T (y_w^T y_w) basis equal to the top eigenvalues in ascending order."""
+    from sparsepr_amd import residual_repair as rr
+
+    rng = np.random.default_rng(1000 * m + 10 * d + rank)
+    bh = 3
+    x = (rng.standard_normal((bh, m, p)) * rng.uniform(0.5, 3.0, (1, 1, p)) + 0.3).astype(np.float32)
+    y = (x @ rng.standard_normal((bh, p, d)).astype(np.float32) * 0.05
+         + 0.02 * rng.standard_normal((bh, m, d)).astype(np.float32))
+    w = rng.uniform(0.5, 2.0, (bh, m)).astype(np.float32)
+    w[0, : m // 4] = 0.0  # rows outside the fit
+    xt, yt, wt = to_dev(x, dev), to_dev(y, dev), to_dev(w, dev)
+    assert rr._rrr_fit_fused(xt, yt, wt, rank, "skinny", "raw_residual")
+    got = [t.cpu().numpy().astype(np.float64) for t in rr._rrr_fit_hip(xt, yt, wt, rank, 0.1)]
+    ref = oracle.fit_reduced_rank_residual(x, y, rank, 0.1, w)
+    for g, r in zip(got[:3], ref[:3]):
+        assert np.allclose(g, r, rtol=1e-4, atol=1e-5)
+    gl = got[3] @ np.swapaxes(got[4], 1, 2)
+    rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
+    assert np.abs(gl - rl).max() <= 2e-3 * np.abs(rl).max()
+    basis = got[4]
+    assert np.abs(np.swapaxes(basis, 1, 2) @ basis - np.eye(rank)).max() <= 1e-5
+    yw = (y.astype(np.float64) - ref[2]) * np.sqrt(w.astype(np.float64))[:, :, None]
+    gram = np.swapaxes(yw, 1, 2) @ yw
+    top = np.linalg.eigvalsh(gram)[:, -rank:]
+    proj = np.swapaxes(basis, 1, 2) @ gram @ basis
+    for h in range(bh):
+        assert np.allclose(np.diag(proj[h]), top[h], rtol=1e-4, atol=1e-6 * top[h, -1])
+
+
+def test_rrr_fused_fit_degenerate_spectra(dev, oracle):
+    """Clusters of equal eigenvalues inside the top 16 (orthogonalised within the cluster)
+    and a zero residual (one cluster of 16 at zero): the basis stays orthonormal and the
+    fitted map matches the float64 fit, which is unique when no cluster straddles the
+    16 / 17 boundary."""
+    from sparsepr_amd import residual_repair as rr
+
+    rng = np.random.default_rng(7)
+    m = p = d = 128
+    x = rng.standard_normal((2, m, p)).astype(np.float32)
+    w = np.ones((2, m), np.float32)
+    # head 0: y_w = U diag(s) V^T with U orthogonal to the constant vector (zero mean),
+    # s repeating 5, 5, 5, 4, 4, 3 x 4, 2 x 7 in the top 16 and 0.5 x 16 below
+    q, _ = np.linalg.qr(np.concatenate([np.ones((m, 1)), rng.standard_normal((m, m - 1))], axis=1))
+    u = q[:, 1:33]
+    v, _ = np.linalg.qr(rng.standard_normal((d, 32)))
+    sv = np.array([5, 5, 5, 4, 4, 3, 3, 3, 3] + [2] * 7 + [0.5] * 16, np.float64)
+    y0 = (u * sv) @ v.T
+    y = np.stack([y0, np.full((m, d), 0.25)]).astype(np.float32)  # head 1: constant rows
+    xt, yt, wt = to_dev(x, dev), to_dev(y, dev), to_dev(w, dev)
+    got = [t.cpu().numpy().astype(np.float64) for t in rr._rrr_fit_hip(xt, yt, wt, 16, 0.1)]
+    assert all(np.isfinite(g).all() for g in got)
+    basis = got[4]
+    assert np.abs(np.swapaxes(basis, 1, 2) @ basis - np.eye(16)).max() <= 1e-5
+    ref = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w)
+    gl = got[3] @ np.swapaxes(got[4], 1, 2)
+    rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
+    assert np.abs(gl[0] - rl[0]).max() <= 2e-3 * np.abs(rl[0]).max()
+    assert np.abs(gl[1]).max() <= 1e-6  # zero residual: zero correction
+
+
 def test_recover_nonfinite_state_gpu(dev):
     from sparsepr_amd.residual_repair import recover_nonfinite_rrr_state
 
