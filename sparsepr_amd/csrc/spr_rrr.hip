@@ -829,8 +829,10 @@ extern "C" int spr_rrr_fit(const float* x, const float* y, const float* weights,
   if (bh == 0) return SPR_OK;
   SPR_REQUIRE(x && y && weights && x_mean && x_scale && y_mean && left && basis && workspace,
               "spr_rrr_fit: null pointer");
-  SPR_REQUIRE(workspace_bytes >= spr_rrr_fit_workspace(bh), "spr_rrr_fit: workspace too small (%zu < %zu)",
-              workspace_bytes, spr_rrr_fit_workspace(bh));
+  if (workspace_bytes < spr_rrr_fit_workspace(bh)) {
+    spr_set_error("spr_rrr_fit: workspace too small (%zu < %zu)", workspace_bytes, spr_rrr_fit_workspace(bh));
+    return SPR_EWORKSPACE;
+  }
   float* ws = static_cast<float*>(workspace);
   const uint32_t nb = static_cast<uint32_t>(bh);
   rrr_stats_kernel<<<dim3(nb), 256, 0, stream>>>(x, y, weights, m, p, d, x_mean, x_scale, y_mean);

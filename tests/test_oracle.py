@@ -369,6 +369,41 @@ def test_probe_selection_brute_force(oracle):
     assert rows[0].tolist().count(20) == 0 or 10 not in rows[0].tolist()
 
 
+@pytest.mark.parametrize("r", [6, 20, 128])
+def test_probe_distance_canonical_order(oracle, r):
+    """The distance order the kernel reproduces: per token, fp32 sums of squared
+    differences over groups of 8 dims in sequence, then a pairwise tree over the groups
+    (padded to a power of two).  Checked bit for bit against a scalar float32 loop in that
+    order, and against float64 distances to 1e-6 relative."""
+    rng = np.random.default_rng(100 + r)
+    bh, n, c = 1, 24, 3
+    f = oracle.to_bf16(rng.standard_normal((bh, n, r)).astype(np.float32))
+    labels = rng.integers(0, c, (bh, n)).astype(np.int32)
+    _sizes, got = oracle._probe_distances(f, labels, c)
+    f32 = np.float32
+    for t in range(n):
+        mem = f[0, labels[0] == labels[0, t]].astype(np.float64)
+        cen = (mem.sum(0) / len(mem)).astype(np.float32)
+        diff = [f32(f32(f[0, t, j]) - cen[j]) for j in range(r)]
+        groups = -(-r // 8)
+        span = 1
+        while span < groups:
+            span *= 2
+        parts = []
+        for g in range(span):
+            acc = f32(0.0)
+            for e in range(8):
+                j = 8 * g + e
+                dj = diff[j] if j < r else f32(0.0)
+                acc = f32(acc + f32(dj * dj))
+            parts.append(acc)
+        while len(parts) > 1:
+            parts = [f32(parts[2 * u] + parts[2 * u + 1]) for u in range(len(parts) // 2)]
+        assert got[0, t] == parts[0]
+        exact = float(((f[0, t].astype(np.float64) - mem.mean(0)) ** 2).sum())
+        assert abs(float(got[0, t]) - exact) <= 1e-6 * max(exact, 1e-12) + 1e-6 * float(cen.astype(np.float64) @ cen)
+
+
 def test_probe_loop_equals_vectorized_when_rows_fit(oracle):
     rng = np.random.default_rng(14)
     f, labels = _probe_data(oracle, rng)
