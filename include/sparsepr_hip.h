@@ -177,10 +177,12 @@ int spr_probe_distances(const void* features, int32_t dtype, const int32_t* labe
  * group, largest groups first), 1 = rounds (select_role_equal_probes, more rows than
  * groups), 2 = select_first_token_largest_groups.  rows int32 [bh, count], weights fp32
  * [bh, count] (size / sampled, normalised to mean 1), filled int32 [bh] nullable.
- * groups <= 2048. */
+ * groups <= 2048.  workspace (spr_probe_select_workspace bytes, nullable) splits the pass
+ * over the tokens across many workgroups per head in modes 0 and 2. */
+size_t spr_probe_select_workspace(int64_t bh, int32_t groups);
 int spr_probe_select(const float* dist, const int32_t* labels, const int32_t* sizes, int64_t bh, int64_t n,
                      int32_t groups, int32_t count, int32_t mode, int32_t* rows, float* weights, int32_t* filled,
-                     hipStream_t stream);
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* residual_repair.py:798-857 n8_prepare_output_repair_fit_triton:
  *   x_fit = base[rows], dense_f = float(dense), y_fit = dense_f - x_fit (fp32 [bh, m, d]). */
 int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense, int32_t dense_dtype,

@@ -59,7 +59,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            _vp, _sz, _vp]),
     # repair.hip
     "spr_probe_distances": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
-    "spr_probe_select": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "spr_probe_select_workspace": (_sz, [_i64, _i32]),
+    "spr_probe_select": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _sz,
+                                        _vp]),
     "spr_repair_fit_prep": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "spr_repair_apply": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _f32, _f32, _vp, _vp]),
     "spr_probe_scatter": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),

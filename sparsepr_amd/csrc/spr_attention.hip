@@ -136,32 +136,58 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
   PlanView pv = plan_at(plan, h, qn, kn);
   const int32_t* qs = q_sizes + h * qn;
   const int32_t* ks = k_sizes + h * kn;
-  if (threadIdx.x == 0) {
-    int32_t run = 0;
-    for (int j = 0; j < kn; ++j) {
-      k_off[j] = run;
-      run = min(run + max(ks[j], 0), s_rows);
+  // Offsets are running sums clamped at s_rows; the sizes are clamped at zero, so the
+  // clamped running sum equals min(prefix sum, s_rows) and wave scans compute it.
+  const int wv = threadIdx.x >> 6;
+  const int ln = threadIdx.x & 63;
+  auto scan64 = [&](int64_t v) {  // inclusive scan over the wave
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t up = __shfl_up(v, o, 64);
+      if (ln >= o) v += up;
     }
-    k_off[kn] = run;
-    int32_t qrun = 0, trun = 0, trun2 = 0;
-    for (int i = 0; i < qn; ++i) {
-      pv.q_off[i] = qrun;
-      pv.tile_off[i] = trun;
-      pv.tile2_off[i] = trun2;
-      const int32_t next = min(qrun + max(qs[i], 0), s_rows);
-      trun += (next - qrun + BM - 1) / BM;
-      trun2 += (next - qrun + 2 * BM - 1) / (2 * BM);
-      qrun = next;
+    return v;
+  };
+  if (wv == 0) {  // k-cluster offsets (every workgroup of the head, for its rows)
+    int64_t carry = 0;
+    for (int c0 = 0; c0 < kn; c0 += 64) {
+      const int c = c0 + ln;
+      const int64_t own = c < kn ? max(ks[c], 0) : 0;
+      const int64_t incl = scan64(own);
+      if (c < kn) k_off[c] = static_cast<int32_t>(min(carry + incl - own, static_cast<int64_t>(s_rows)));
+      carry += __shfl(incl, 63, 64);
     }
-    pv.q_off[qn] = qrun;
-    pv.tile_off[qn] = trun;
-    pv.tile2_off[qn] = trun2;
+    if (ln == 0) k_off[kn] = static_cast<int32_t>(min(carry, static_cast<int64_t>(s_rows)));
+  } else if (wv == 1 && blockIdx.y == 0) {  // q-cluster offsets and tile counts
+    int64_t carry = 0, tcarry = 0, t2carry = 0;
+    for (int i0 = 0; i0 < qn; i0 += 64) {
+      const int i = i0 + ln;
+      const int64_t own = i < qn ? max(qs[i], 0) : 0;
+      const int64_t incl = scan64(own);
+      const int64_t qrun = min(carry + incl - own, static_cast<int64_t>(s_rows));
+      const int64_t next = min(carry + incl, static_cast<int64_t>(s_rows));
+      const int64_t tl = i < qn ? (next - qrun + BM - 1) / BM : 0;
+      const int64_t tl2 = i < qn ? (next - qrun + 2 * BM - 1) / (2 * BM) : 0;
+      const int64_t ti = scan64(tl), ti2 = scan64(tl2);
+      if (i < qn) {
+        pv.q_off[i] = static_cast<int32_t>(qrun);
+        pv.tile_off[i] = static_cast<int32_t>(tcarry + ti - tl);
+        pv.tile2_off[i] = static_cast<int32_t>(t2carry + ti2 - tl2);
+      }
+      carry += __shfl(incl, 63, 64);
+      tcarry += __shfl(ti, 63, 64);
+      t2carry += __shfl(ti2, 63, 64);
+    }
+    if (ln == 0) {
+      pv.q_off[qn] = static_cast<int32_t>(min(carry, static_cast<int64_t>(s_rows)));
+      pv.tile_off[qn] = static_cast<int32_t>(tcarry);
+      pv.tile2_off[qn] = static_cast<int32_t>(t2carry);
+    }
   }
   __syncthreads();
   // one wave per q-cluster row: ascending compaction of kept, non-empty k-clusters
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  for (int i = wave; i < qn; i += THREADS / 64) {
+  for (int i = blockIdx.y * (THREADS / 64) + wave; i < qn; i += gridDim.y * (THREADS / 64)) {
     const uint8_t* mrow = map + (h * qn + i) * static_cast<int64_t>(kn);
     Seg* out = pv.segs + static_cast<int64_t>(i) * kn;
     int32_t count = 0;
@@ -993,7 +1019,9 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
     spr_set_error("spr_block_sparse_attention_plan: plan buffer %zu < %zu bytes", plan_bytes, need);
     return SPR_EWORKSPACE;
   }
-  attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv)), THREADS, (kn + 1) * sizeof(int32_t), stream>>>(
+  // one wave per q-cluster row: the rows of a head spread over several workgroups
+  const uint32_t row_groups = static_cast<uint32_t>(spr::ceil_div(qn, THREADS / 64));
+  attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv), row_groups), THREADS, (kn + 1) * sizeof(int32_t), stream>>>(
       map, q_sizes, k_sizes, qn, kn, static_cast<int32_t>(s), static_cast<int32_t*>(plan));
   SPR_LAUNCHED("attn_plan_kernel");
   return SPR_OK;

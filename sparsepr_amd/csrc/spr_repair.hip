@@ -102,6 +102,42 @@ __global__ __launch_bounds__(256) void probe_distance_kernel(const T* __restrict
   }
 }
 
+// First pass of probe selection for modes 0 and 2, split over many workgroups per head:
+// each workgroup reduces its slice of tokens to the smallest (distance bits, token) key
+// per group in LDS, then merges those keys into the head's keys in `best` with 64-bit
+// global atomicMin.  The minimum over all tokens does not depend on the order.
+constexpr int PROBE_SLICE = 2048;  // tokens per workgroup
+
+__global__ void probe_best_init_kernel(unsigned long long* __restrict__ best, int64_t total) {
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    best[e] = ~0ull;
+}
+
+__global__ __launch_bounds__(256) void probe_best_kernel(const float* __restrict__ dist,
+                                                         const int32_t* __restrict__ labels, int64_t n,
+                                                         int32_t groups, int32_t mode,
+                                                         unsigned long long* __restrict__ best) {
+  __shared__ unsigned long long lb[MAX_GROUPS];
+  const int64_t bh = blockIdx.y;
+  for (int c = threadIdx.x; c < groups; c += blockDim.x) lb[c] = ~0ull;
+  __syncthreads();
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * PROBE_SLICE;
+  const int64_t t1 = min(n, t0 + PROBE_SLICE);
+  const int32_t* lab = labels + bh * n;
+  const float* dd = dist + bh * n;
+  for (int64_t t = t0 + threadIdx.x; t < t1; t += blockDim.x) {
+    const int32_t c = lab[t];
+    if (c < 0 || c >= groups) continue;
+    const float dv = (mode == 2) ? 0.0f : dd[t];
+    atomicMin(&lb[c], (static_cast<unsigned long long>(__float_as_uint(dv)) << 32) | static_cast<uint32_t>(t));
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < groups; c += blockDim.x) {
+    if (lb[c] != ~0ull) atomicMin(&best[bh * groups + c], lb[c]);
+  }
+}
+
 // mode 0: vectorized role-equal (one representative per group, first `count`
 //         groups in size order; empty-group slots fall back to token j);
 // mode 1: representative rounds until `count` probes (an exhausted group offers
@@ -112,7 +148,8 @@ __global__ __launch_bounds__(256) void probe_select_kernel(const float* __restri
                                                            const int32_t* __restrict__ sizes, int64_t n,
                                                            int32_t groups, int32_t count, int32_t mode,
                                                            int32_t* __restrict__ rows, float* __restrict__ weights,
-                                                           int32_t* __restrict__ status) {
+                                                           int32_t* __restrict__ status,
+                                                           const unsigned long long* __restrict__ gbest) {
   __shared__ int32_t sz[MAX_GROUPS];
   __shared__ int32_t order[MAX_GROUPS];
   __shared__ unsigned long long best[MAX_GROUPS];
@@ -152,19 +189,23 @@ __global__ __launch_bounds__(256) void probe_select_kernel(const float* __restri
   const unsigned long long none = ~0ull;
   for (int c = threadIdx.x; c < groups; c += blockDim.x) first_tok[c] = 0x7fffffff;
   for (int round = 0; round <= count; ++round) {
-    for (int c = threadIdx.x; c < groups; c += blockDim.x) best[c] = none;
-    __syncthreads();
-    for (int64_t t = threadIdx.x; t < n; t += blockDim.x) {
-      const int32_t c = lab[t];
-      if (c < 0 || c >= groups) continue;
-      const float dv = (mode == 2) ? 0.0f : dd[t];
-      const unsigned long long key =
-          (static_cast<unsigned long long>(__float_as_uint(dv)) << 32) | static_cast<uint32_t>(t);
-      if (round == 0) {
-        atomicMin(&best[c], key);
-        atomicMin(&first_tok[c], static_cast<int32_t>(t));
-      } else if (key > prev[c]) {
-        atomicMin(&best[c], key);
+    if (gbest != nullptr) {  // modes 0 and 2: the keys of the split first pass
+      for (int c = threadIdx.x; c < groups; c += blockDim.x) best[c] = gbest[bh * groups + c];
+    } else {
+      for (int c = threadIdx.x; c < groups; c += blockDim.x) best[c] = none;
+      __syncthreads();
+      for (int64_t t = threadIdx.x; t < n; t += blockDim.x) {
+        const int32_t c = lab[t];
+        if (c < 0 || c >= groups) continue;
+        const float dv = (mode == 2) ? 0.0f : dd[t];
+        const unsigned long long key =
+            (static_cast<unsigned long long>(__float_as_uint(dv)) << 32) | static_cast<uint32_t>(t);
+        if (round == 0) {
+          atomicMin(&best[c], key);
+          atomicMin(&first_tok[c], static_cast<int32_t>(t));
+        } else if (key > prev[c]) {
+          atomicMin(&best[c], key);
+        }
       }
     }
     __syncthreads();
@@ -203,19 +244,20 @@ __global__ __launch_bounds__(256) void probe_select_kernel(const float* __restri
     if (c >= 0 && c < groups) atomicAdd(&sampled[c], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double s = 0.0;
-    for (int j = 0; j < have; ++j) {
-      const int32_t t = out_rows[j];
-      const int32_t c = (t >= 0 && t < n) ? lab[t] : -1;
-      float w = 0.0f;
-      if (c >= 0 && c < groups) {
-        const float size = static_cast<float>(sz[c]);
-        w = (mode == 2) ? size : __fdiv_rn(size, static_cast<float>(max(sampled[c], 1)));
-      }
-      out_w[j] = w;
-      s += static_cast<double>(w);
+  for (int j = threadIdx.x; j < have; j += blockDim.x) {
+    const int32_t t = out_rows[j];
+    const int32_t c = (t >= 0 && t < n) ? lab[t] : -1;
+    float w = 0.0f;
+    if (c >= 0 && c < groups) {
+      const float size = static_cast<float>(sz[c]);
+      w = (mode == 2) ? size : __fdiv_rn(size, static_cast<float>(max(sampled[c], 1)));
     }
+    out_w[j] = w;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // the mean in a fixed (sequential) order
+    double s = 0.0;
+    for (int j = 0; j < have; ++j) s += static_cast<double>(out_w[j]);
     wsum = have > 0 ? s / static_cast<double>(have) : 0.0;
   }
   __syncthreads();
@@ -572,12 +614,17 @@ extern "C" int spr_probe_distances(const void* features, int32_t dtype, const in
   return SPR_OK;
 }
 
+extern "C" size_t spr_probe_select_workspace(int64_t bh, int32_t groups) {
+  return (bh <= 0 || groups <= 0) ? 0 : static_cast<size_t>(bh) * groups * sizeof(unsigned long long);
+}
+
 // rows int32 [bh, count], weights fp32 [bh, count]; filled int32 [bh] (nullable)
 // receives the number of rows found (count unless mode 1 ran out of tokens).
-// dist may be null for mode 2.
+// dist may be null for mode 2.  workspace (spr_probe_select_workspace bytes, nullable)
+// lets modes 0 and 2 split the pass over the tokens across many workgroups per head.
 extern "C" int spr_probe_select(const float* dist, const int32_t* labels, const int32_t* sizes, int64_t bh, int64_t n,
                                 int32_t groups, int32_t count, int32_t mode, int32_t* rows, float* weights,
-                                int32_t* filled, hipStream_t stream) {
+                                int32_t* filled, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && n >= 0 && groups >= 1 && count >= 0, "spr_probe_select: bad size");
   SPR_REQUIRE(groups <= MAX_GROUPS, "spr_probe_select: %d groups exceed %d", groups, MAX_GROUPS);
   SPR_REQUIRE(mode >= 0 && mode <= 2, "spr_probe_select: mode must be 0, 1 or 2");
@@ -586,8 +633,26 @@ extern "C" int spr_probe_select(const float* dist, const int32_t* labels, const 
   SPR_REQUIRE(count <= n, "spr_probe_select: more probes than tokens");
   if (bh == 0 || count == 0) return SPR_OK;
   SPR_REQUIRE(labels && sizes && rows && weights && (dist || mode == 2), "spr_probe_select: null pointer");
+  SPR_REQUIRE(bh <= 65535, "spr_probe_select: too many heads");
+  unsigned long long* gbest = nullptr;
+  if (workspace != nullptr && mode != 1) {
+    if (workspace_bytes < spr_probe_select_workspace(bh, groups)) {
+      spr_set_error("spr_probe_select: workspace too small (%zu < %zu)", workspace_bytes,
+                    spr_probe_select_workspace(bh, groups));
+      return SPR_EWORKSPACE;
+    }
+    gbest = static_cast<unsigned long long*>(workspace);
+    const int64_t total = bh * groups;
+    probe_best_init_kernel<<<dim3(static_cast<uint32_t>(spr::ceil_div(total, 256))), 256, 0, stream>>>(gbest, total);
+    SPR_LAUNCHED("probe_best_init_kernel");
+    if (n > 0) {
+      const dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, PROBE_SLICE)), static_cast<uint32_t>(bh));
+      probe_best_kernel<<<grid, 256, 0, stream>>>(dist, labels, n, groups, mode, gbest);
+      SPR_LAUNCHED("probe_best_kernel");
+    }
+  }
   probe_select_kernel<<<dim3(static_cast<uint32_t>(bh)), 256, 0, stream>>>(dist, labels, sizes, n, groups, count,
-                                                                           mode, rows, weights, filled);
+                                                                           mode, rows, weights, filled, gbest);
   SPR_LAUNCHED("probe_select_kernel");
   return SPR_OK;
 }

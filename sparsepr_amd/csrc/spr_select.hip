@@ -304,20 +304,46 @@ __global__ __launch_bounds__(256) void density_kernel(const uint8_t* __restrict_
                                                       const int32_t* __restrict__ k_sizes, int32_t qn,
                                                       int32_t kn, float* __restrict__ out) {
   __shared__ long long red[3][4];
+  extern __shared__ int32_t qk_sizes[];  // [qn] then [kn]
   const int64_t h = blockIdx.x;
   const int tid = threadIdx.x;
   const uint8_t* m = map + h * qn * static_cast<int64_t>(kn);
   const int32_t* qs = q_sizes + h * qn;
   const int32_t* ks = k_sizes + h * kn;
+  int32_t* sq = qk_sizes;
+  int32_t* sk = qk_sizes + qn;
   long long kept = 0, qsum = 0, ksum = 0;
-  for (int i = tid; i < qn; i += blockDim.x) qsum += qs[i];
-  for (int j = tid; j < kn; j += blockDim.x) ksum += ks[j];
-  // thread t owns columns t, t + 256, ...: per row, the kept key mass times the row's size
-  for (int i = 0; i < qn; ++i) {
-    const uint8_t* row = m + static_cast<int64_t>(i) * kn;
-    long long rs = 0;
-    for (int j = tid; j < kn; j += blockDim.x) rs += row[j] ? ks[j] : 0;
-    kept += rs * qs[i];
+  for (int i = tid; i < qn; i += blockDim.x) {
+    sq[i] = qs[i];
+    qsum += qs[i];
+  }
+  for (int j = tid; j < kn; j += blockDim.x) {
+    sk[j] = ks[j];
+    ksum += ks[j];
+  }
+  __syncthreads();
+  // sum over (i, j) of map[i][j] ? qs[i] * ks[j] : 0, walked as 16-byte vectors of the
+  // map when rows are whole vectors (every load independent), else byte by byte
+  if ((kn & 15) == 0 && (reinterpret_cast<uintptr_t>(m) & 15) == 0) {
+    const int vpr = kn >> 4;
+    const int total = qn * vpr;
+    const uint4* mv = reinterpret_cast<const uint4*>(m);
+    for (int v = tid; v < total; v += blockDim.x) {
+      const int i = v / vpr;
+      const int j0 = (v - i * vpr) << 4;
+      const uint4 w = mv[v];
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+      long long rs = 0;
+#pragma unroll
+      for (int b = 0; b < 16; ++b) rs += ((ws[b >> 2] >> (8 * (b & 3))) & 0xFFu) ? sk[j0 + b] : 0;
+      kept += rs * sq[i];
+    }
+  } else {
+    for (int e = tid; e < qn * kn; e += blockDim.x) {
+      const int i = e / kn;
+      const int j = e - i * kn;
+      kept += m[e] ? static_cast<long long>(sk[j]) * sq[i] : 0;
+    }
   }
   for (int o = 32; o > 0; o >>= 1) {
     kept += __shfl_xor(kept, o, 64);
@@ -397,7 +423,9 @@ extern "C" int spr_density(const uint8_t* map, const int32_t* q_sizes, const int
   SPR_REQUIRE(heads >= 0 && qn >= 1 && kn >= 1, "spr_density: bad size");
   if (heads == 0) return SPR_OK;
   SPR_REQUIRE(map && q_sizes && k_sizes && out, "spr_density: null pointer");
-  density_kernel<<<dim3(static_cast<uint32_t>(heads)), 256, 0, stream>>>(map, q_sizes, k_sizes, qn, kn, out);
+  SPR_REQUIRE(static_cast<int64_t>(qn) * kn < (int64_t(1) << 31) && qn + kn <= 16384, "spr_density: map too large");
+  density_kernel<<<dim3(static_cast<uint32_t>(heads)), 256, (qn + kn) * sizeof(int32_t), stream>>>(map, q_sizes, k_sizes,
+                                                                                                   qn, kn, out);
   SPR_LAUNCHED("density_kernel");
   return SPR_OK;
 }

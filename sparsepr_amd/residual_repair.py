@@ -77,8 +77,11 @@ def select_probes(features: torch.Tensor, labels: torch.Tensor, num_clusters: in
         sizes = argsort_labels(lab, num_clusters)[1]
     out_rows = torch.empty((bh, count), dtype=torch.int32, device=dev)
     weights = torch.empty((bh, count), dtype=torch.float32, device=dev)
+    ws_bytes = int(_lib.query("spr_probe_select_workspace", bh, num_clusters))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     _lib.call("spr_probe_select", _lib.ptr(dist), _lib.ptr(lab), _lib.ptr(sizes.to(torch.int32).contiguous()), bh,
-              n, num_clusters, count, mode, _lib.ptr(out_rows), _lib.ptr(weights), None, _lib.stream(dev))
+              n, num_clusters, count, mode, _lib.ptr(out_rows), _lib.ptr(weights), None, _lib.ptr(ws), ws_bytes,
+              _lib.stream(dev))
     return out_rows.long(), weights
 
 

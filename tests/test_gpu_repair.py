@@ -35,6 +35,39 @@ def test_vectorized_probes_bit_exact(dev, oracle, r):
         assert np.allclose(w.cpu().numpy(), rw, rtol=1e-6)
 
 
+@pytest.mark.parametrize("mode", [0, 2])
+def test_probe_select_split_pass_matches_single(dev, oracle, mode):
+    """Modes 0 and 2 with a workspace split the pass over the tokens across workgroups
+    (global 64-bit atomicMin merge); without one a single workgroup per head walks all
+    tokens.  Both give the oracle's rows and weights, including an exact distance tie
+    between tokens in different slices (the lower token wins)."""
+    from sparsepr_amd import _lib
+
+    rng = np.random.default_rng(31 + mode)
+    bh, n, c, count = 2, 20000, 64, 48
+    f, labels = _probe_data(oracle, rng, bh=bh, n=n, r=64, c=c, empty=(9,))
+    f[1, 15000] = f[1, 300]
+    labels[1, 15000] = labels[1, 300]
+    _sizes, dist = oracle._probe_distances(f, labels, c)
+    sizes = np.stack([np.bincount(labels[h], minlength=c) for h in range(bh)]).astype(np.int32)
+    d_dist, d_lab, d_sz = to_dev(dist.astype(np.float32), dev), to_dev(labels, dev), to_dev(sizes, dev)
+    outs = []
+    for use_ws in (True, False):
+        rows = torch.empty((bh, count), dtype=torch.int32, device=dev)
+        w = torch.empty((bh, count), dtype=torch.float32, device=dev)
+        nb = int(_lib.query("spr_probe_select_workspace", bh, c)) if use_ws else 0
+        ws = torch.empty((max(nb, 1),), dtype=torch.uint8, device=dev)
+        _lib.call("spr_probe_select", _lib.ptr(d_dist), _lib.ptr(d_lab), _lib.ptr(d_sz), bh, n, c, count, mode,
+                  _lib.ptr(rows), _lib.ptr(w), None, _lib.ptr(ws) if use_ws else None, nb, _lib.stream(dev))
+        outs.append((rows.cpu().numpy(), w.cpu().numpy()))
+    assert (outs[0][0] == outs[1][0]).all() and (outs[0][1] == outs[1][1]).all()
+    if mode == 0:
+        rr, rw = oracle.select_role_equal_probes_vectorized(f, labels, c, count)
+    else:
+        rr, rw = oracle.select_first_token_largest_groups(labels, c, count)
+    assert (outs[0][0] == rr).all() and np.allclose(outs[0][1], rw, rtol=1e-6)
+
+
 def test_round_probes_and_first_token(dev, oracle):
     from sparsepr_amd.residual_repair import select_first_token_largest_groups, select_role_equal_probes
 

@@ -73,6 +73,21 @@ def test_topp_map_full_size_invariants(dev, oracle):
     assert np.allclose(dens.cpu().numpy(), ref_d, rtol=1e-6)
 
 
+@pytest.mark.parametrize("qn,kn", [(7, 37), (5, 48)])
+def test_density_byte_and_vector_paths(dev, oracle, qn, kn):
+    """density_calculation on maps whose rows are not (37) and are (48) whole 16-byte
+    vectors, against the oracle's closed form."""
+    from sparsepr_amd.kmeans_utils import density_calculation
+
+    rng = np.random.default_rng(qn * kn)
+    m = rng.random((3, qn, kn)) < 0.3
+    qs = rng.integers(0, 900, (3, qn)).astype(np.int32)
+    ks = rng.integers(0, 400, (3, kn)).astype(np.int32)
+    got = density_calculation(to_dev(m, dev)[None], to_dev(qs, dev)[None], to_dev(ks, dev)[None])
+    ref = oracle.density(m[None], qs[None], ks[None])
+    assert np.allclose(got.cpu().numpy(), ref, rtol=1e-6)
+
+
 def test_selector_known_answer_gpu(dev):
     from sparsepr_amd.kernels.n8_extension import (compact_selected_clusters, load_n8_kernels,
                                                    svg_ear_select_budget_schedule)
