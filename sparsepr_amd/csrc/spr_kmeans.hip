@@ -257,12 +257,17 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
     for (int f = 0; f < 2; ++f) {
       const int64_t p = p0 + 32 * f;
       const bool live = p < n;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s)
+        xf[f][s] = live ? *reinterpret_cast<const u32x4*>(xb + p * D + s * 16 + half * 8) : u32x4{0, 0, 0, 0};
+      if (x_sq_in != nullptr) {  // later Lloyd iterations: the norms of the first
+        xsq[f] = live ? x_sq_in[b * n + p] : 0.0f;
+        continue;
+      }
       float part = 0.0f;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
-        u32x4 v = live ? *reinterpret_cast<const u32x4*>(xb + p * D + s * 16 + half * 8) : u32x4{0, 0, 0, 0};
-        xf[f][s] = v;
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t w[4] = {xf[f][s].x, xf[f][s].y, xf[f][s].z, xf[f][s].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float lo = spr::bf16_lo(w[e]);
@@ -280,11 +285,7 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
       const float other = __shfl_xor(part, 32, 64);
       float total = part + other;
       if (x_sq_mode == 1) total = spr::bf16_lo(spr::pack_bf16x2_rne(total, 0.0f));
-      if (x_sq_in != nullptr) {
-        total = live ? x_sq_in[b * n + p] : 0.0f;
-      } else if (x_sq_out != nullptr && live && half == 0) {
-        x_sq_out[b * n + p] = total;
-      }
+      if (x_sq_out != nullptr && live && half == 0) x_sq_out[b * n + p] = total;
       xsq[f] = total;
     }
 
