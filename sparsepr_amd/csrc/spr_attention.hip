@@ -901,8 +901,11 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();  // ... every wave's; and no wave reads chunk x - 1 any more
-    if (x + 3 < nch) dma(kt3, vt3);
     if (wave_live) step(s_a, kt1, 0, s_b, vt, 1);
+    // chunk x + 3 into chunk x - 1's tiles, issued after this chunk's compute rather than
+    // at the barrier, where every wave starts reading the next K tile (same-box timing:
+    // about 2 % faster)
+    if (x + 3 < nch) dma(kt3, vt3);
   };
 
   if (nch > 0) {
