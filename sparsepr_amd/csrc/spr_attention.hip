@@ -803,10 +803,12 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   // Row max of half kbk (masked past the end) and lazy rescale; returns -m.
   auto row_max = [&](spr::f32x16& acc, int kbk, int32_t left) {
     if (left < BN) {
+      // element e holds key kbk * 32 + 8 (e / 4) + 4 half + e % 4; compared as an
+      // immediate against one per-lane limit, so no per-element key registers
+      const int lim = left - kbk * 32 - 4 * half;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int key = kbk * 32 + 8 * (e / 4) + 4 * half + (e % 4);
-        if (key >= left) acc[e] = -__builtin_huge_valf();
+        if (8 * (e / 4) + (e % 4) >= lim) acc[e] = -__builtin_huge_valf();
       }
     }
     float mx = -__builtin_huge_valf();
