@@ -43,10 +43,11 @@ def parse():
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["attention", "copy"], default=None,
+    ap.add_argument("--only", choices=["attention", "copy", "svg_ear"], default=None,
                     help="profiling aids: 'attention' routes once, then times only the block-sparse attention "
                          "kernel for --steps launches; 'copy' runs --steps plain 512 MiB device copies (the "
-                         "calibration kernel for the HBM traffic counters)")
+                         "calibration kernel for the HBM traffic counters); 'svg_ear' routes once, then times "
+                         "the N8 value-error routing scores (N8's default selector) on the routed clusters")
     return ap.parse_args()
 
 
@@ -148,6 +149,61 @@ def only_attention(args):
                       "density": round(float(route.base_video_density.item()), 4)}), flush=True)
 
 
+def only_svg_ear(args):
+    """Route the C4 inputs once, then time --steps launches of the SVG-EAR value-error routing
+    scores (all 24 heads x 128 query centroids x 512 key clusters over the cluster-sorted K/V).
+    Algorithmic HBM bytes per launch: K and V read once (2 * BH * N * D * 2) plus the
+    centroids and the score matrix; algorithmic flops: 2 * BH * Qc * N * D (token logits)."""
+    import torch
+
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.kernels.svg_ear import svg_ear_value_error_scores_triton
+    from sparsepr_amd.layer import SparsePRAttention, SparsePRConfig
+
+    shape = synthetic.HUNYUAN
+    q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **GEN)
+    layer = SparsePRAttention(SparsePRConfig(top_p=args.top_p, repair=False))
+    route, _ = layer.route(q, k, v)
+    B, H, N, D = q.shape
+    bh = B * H
+    qc = layer.last_centroids[0].float().reshape(bh, -1, D).contiguous()
+    kc = layer.last_centroids[1].float().reshape(bh, -1, D).contiguous()
+    sizes = route.k_cluster_sizes.reshape(bh, -1).to(torch.int32).contiguous()
+    ks, vs = route.k_permuted.reshape(bh, N, D), route.v_permuted.reshape(bh, N, D)
+    # value centroids: per-cluster means of the sorted V (prefix sums over the runs)
+    ends = sizes.long().cumsum(1)
+    csum = torch.nn.functional.pad(vs.float().cumsum(1), (0, 0, 1, 0))
+    vc = ((csum.gather(1, ends[..., None].expand(-1, -1, D))
+           - csum.gather(1, (ends - sizes.long())[..., None].expand(-1, -1, D)))
+          / sizes.clamp_min(1)[..., None].float()).contiguous()
+    del csum
+
+    def run():
+        return svg_ear_value_error_scores_triton(qcentroids=qc, k_sorted=ks, v_sorted=vs, kcentroids=kc,
+                                                 vcentroids=vc, kcluster_sizes=sizes, gqa_group=1)
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        scores = run()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    qn, kn = qc.shape[1], kc.shape[1]
+    nbytes = 2 * bh * N * D * 2 + (qc.numel() + kc.numel() + vc.numel() + scores.numel()) * 4
+    flops = 2.0 * bh * qn * N * D
+    gbs = nbytes / ms / 1e6
+    print(json.dumps({"kernel": "svg_ear_score_kernel<value>", "ms_per_launch": round(ms, 4),
+                      "config": {"bh": bh, "tokens": N, "q_clusters": qn, "k_clusters": kn},
+                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes},
+                      "tflops": round(flops / ms / 1e9, 1),
+                      "finite_scores": round(float(torch.isfinite(scores).float().mean().item()), 4)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -158,6 +214,8 @@ def main():
         return only_copy(args)
     if args.only == "attention":
         return only_attention(args)
+    if args.only == "svg_ear":
+        return only_svg_ear(args)
     import torch
 
     from sparsepr_amd import synthetic

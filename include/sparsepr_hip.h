@@ -214,6 +214,26 @@ int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh
 int spr_probe_scatter(const void* dense, int32_t dense_dtype, const int32_t* rows, int64_t bh, int64_t n, int32_t m,
                       int32_t d, void* out, hipStream_t stream);
 
+/* ---------------------------------------------------------------- SVG-EAR routing scores
+ * svg_ear.py:95-192,453-531 svg_ear_value_error_scores_triton (mode 0; Jensen term when
+ * jensen_var_cap > 0, var_k_diag [kv_heads, kn, d] fp32), svg_ear.py:195-286,534-600 the
+ * grouped variant (same scores), svg_ear.py:7-92,372-450 attention_mass_scores_triton
+ * (mode 1; v_sorted, k_centroids, v_centroids, var_k_diag unused).
+ *   q_centroids fp32 [q_heads, qn, d]; k_sorted, v_sorted bf16 [kv_heads, t_stored, d]
+ *   (tokens in cluster order); k_centroids, v_centroids fp32 [kv_heads, kn, d];
+ *   k_sizes int32 [kv_heads, kn] (the clusters' consecutive token runs from token 0;
+ *   negative sizes count as 0, runs are clamped to t_stored) -> scores fp32
+ *   [q_heads, qn, kn], -inf for an empty cluster.  q_heads = kv_heads * group, d = 128.
+ *   Token logits use q rounded to TF32 (nearest, ties away), as tl.dot(input_precision
+ *   "tf32") does; the centroid logit uses q in fp32.
+ * spr_svg_ear_scores_flops: algorithmic flops of the token logits, 2 q_heads qn tokens d. */
+size_t spr_svg_ear_scores_flops(int64_t q_heads, int32_t qn, int64_t tokens);
+int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_sorted, const uint16_t* v_sorted,
+                       const float* k_centroids, const float* v_centroids, const float* var_k_diag,
+                       float jensen_var_cap, const int32_t* k_sizes, int64_t q_heads, int32_t qn, int32_t kn,
+                       int64_t kv_heads, int64_t t_stored, int32_t d, int32_t group, int32_t mode, float* scores,
+                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -681,6 +681,97 @@ def exact_probe_scatter(out, rows, dense_probes):
 
 
 # ----------------------------------------------------------------------------
+# SVG-EAR routing scores (src/sparsepr/kernels/triton/svg_ear.py)
+# ----------------------------------------------------------------------------
+
+def tf32_rna(x: np.ndarray) -> np.ndarray:
+    """float32 -> TF32 (10 stored mantissa bits), nearest with ties away from zero: the
+    input rounding of the reference's tl.dot(..., input_precision="tf32")
+    (svg_ear.py:63,157).  Returned as float32."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    b = ((b + 0x1000) & 0xFFFFE000).astype(np.uint32)
+    return b.view(np.float32)
+
+
+def _cluster_runs(sizes_row: np.ndarray, tokens: int):
+    """Consecutive token runs of the clusters from token 0 (the reference's offsets =
+    [0, cumsum(sizes)], svg_ear.py:416-426), clamped to the stored tokens."""
+    s = np.maximum(sizes_row.astype(np.int64), 0)
+    ends = np.minimum(np.cumsum(s), tokens)
+    starts = np.minimum(np.concatenate(([0], np.cumsum(s)[:-1])), tokens)
+    return starts, ends
+
+
+def svg_ear_value_error_scores(qc, k_sorted, v_sorted, kc, vc, sizes, group, var_k_diag=None,
+                               jensen_var_cap=0.0):
+    """Log value-error routing scores (svg_ear.py:95-192 kernel, :453-531 wrapper).
+
+    For query centroid q (fp32) and the tokens t of key cluster c:
+      l_c = (q . kc) / sqrt(D) [+ 0.5 min(sum_d q_d^2 var_d / D, cap)]      (:133-140)
+      l_t = (tf32(q) . k_t) / sqrt(D)                                         (:157)
+      m = max(l_c, max_t l_t); w_c = e^(l_c - m); w_t = e^(l_t - m)
+      E = sum_t max(w_c^2 |vc|^2 + w_t^2 |v_t|^2 - 2 w_t w_c (v_t . vc), 0)   (:175-182)
+      score = log(max(E / n_c, 1e-30)) + 2 m, -inf for an empty cluster      (:186-188)
+    The reference keeps m as a running max over BLOCK_N-token chunks and rescales E by
+    alpha^2 and w_c by alpha; that is the same quantity in exact arithmetic, so this
+    restatement uses the final max directly, in float64.  Query head h reads kv head
+    h // group.  Shapes: qc [QH, Qc, D]; k_sorted, v_sorted [KVH, T, D]; kc, vc, var_k_diag
+    [KVH, Kc, D]; sizes [KVH, Kc] -> [QH, Qc, Kc] float32."""
+    qh_n, qn, d = qc.shape
+    kn = kc.shape[1]
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    out = np.full((qh_n, qn, kn), -np.inf, dtype=np.float64)
+    for h in range(qh_n):
+        kh = h // group
+        q64 = qc[h].astype(np.float64)
+        qt = tf32_rna(qc[h]).astype(np.float64)
+        starts, ends = _cluster_runs(sizes[kh], k_sorted.shape[1])
+        for c in range(kn):
+            n = int(ends[c] - starts[c])
+            if n <= 0:
+                continue
+            kcv = kc[kh, c].astype(np.float64)
+            vcv = vc[kh, c].astype(np.float64)
+            lc = (q64 @ kcv) * scale
+            if jensen_var_cap > 0.0:
+                s2 = ((q64 * q64) @ var_k_diag[kh, c].astype(np.float64)) / d
+                lc = lc + 0.5 * np.minimum(s2, jensen_var_cap)
+            kt = k_sorted[kh, starts[c]:ends[c]].astype(np.float64)
+            vt = v_sorted[kh, starts[c]:ends[c]].astype(np.float64)
+            lt = (qt @ kt.T) * scale
+            m = np.maximum(lc, lt.max(axis=1))
+            cw = np.exp(lc - m)[:, None]
+            tw = np.exp(lt - m[:, None])
+            err = cw * cw * (vcv @ vcv) + tw * tw * (vt * vt).sum(axis=1)[None, :] \
+                - 2.0 * tw * cw * (vt @ vcv)[None, :]
+            e = np.maximum(err, 0.0).sum(axis=1)
+            out[h, :, c] = np.log(np.maximum(e / n, 1e-30)) + 2.0 * m
+    return out.astype(np.float32)
+
+
+def attention_mass_scores(qc, k_sorted, sizes, group):
+    """Log attention mass of each key cluster at each query centroid (svg_ear.py:7-92
+    kernel, :372-450 wrapper): score = log(max(sum_t e^(l_t - m), 1e-30)) + m with
+    l_t = (tf32(q) . k_t) / sqrt(D), m = max_t l_t; -inf for an empty cluster.  float64,
+    final max in place of the running one (same value in exact arithmetic)."""
+    qh_n, qn, d = qc.shape
+    kn = sizes.shape[1]
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    out = np.full((qh_n, qn, kn), -np.inf, dtype=np.float64)
+    for h in range(qh_n):
+        kh = h // group
+        qt = tf32_rna(qc[h]).astype(np.float64)
+        starts, ends = _cluster_runs(sizes[kh], k_sorted.shape[1])
+        for c in range(kn):
+            if ends[c] <= starts[c]:
+                continue
+            lt = (qt @ k_sorted[kh, starts[c]:ends[c]].astype(np.float64).T) * scale
+            m = lt.max(axis=1)
+            out[h, :, c] = np.log(np.maximum(np.exp(lt - m[:, None]).sum(axis=1), 1e-30)) + m
+    return out.astype(np.float32)
+
+
+# ----------------------------------------------------------------------------
 # the whole layer (SAP top-p route + block-sparse attention + N8 repair)
 # ----------------------------------------------------------------------------
 

@@ -1,0 +1,465 @@
+// SVG-EAR routing scores: per (query head, query centroid, key cluster) the log
+// value-error score of N8's default selector and the log attention mass.
+//
+// Replaces:
+//   _svg_ear_value_error_kernel + svg_ear_value_error_scores_triton
+//       (src/sparsepr/kernels/triton/svg_ear.py:95-192, :453-531)
+//   _svg_ear_grouped_value_error_kernel + svg_ear_grouped_value_error_scores_triton
+//       (svg_ear.py:195-286, :534-600): the same scores, one K/V walk per GQA group
+//   _attention_mass_score_kernel + attention_mass_scores_triton (svg_ear.py:7-92, :372-450)
+//
+// Scores, for query centroid q and the tokens t of key cluster c (k, v bf16):
+//   l_t = (q~ . k_t) / sqrt(D), q~ = q rounded to TF32 (the reference's tl.dot
+//         input_precision="tf32"), l_c = (q . kc) / sqrt(D) (+ Jensen term)
+//   value error: m = max(l_c, max_t l_t), w_c = e^(l_c - m), w_t = e^(l_t - m),
+//       E = sum_t max(w_c^2 |vc|^2 + w_t^2 |v_t|^2 - 2 w_t w_c (v_t . vc), 0)
+//       score = log(max(E / n_c, 1e-30)) + 2 m;  -inf for an empty cluster
+//   attention mass: score = log(max(sum_t e^(l_t - m), 1e-30)) + m, m = max_t l_t
+// The running max is kept per 32-token chunk with the reference's rescaling
+// (E *= alpha^2, w_c *= alpha; the mass sum *= alpha).
+//
+// Layout.  A first kernel writes the centroid logits l_c [query head, centroid,
+// cluster] (fp32 dot products over d, sequential, 64 clusters per workgroup)
+// into the score buffer; the score kernel overwrites each entry with its score.
+// The score kernel runs one workgroup of four waves per (query head, 8
+// consecutive key clusters); wave w scores query rows 32 w .. 32 w + 31 of each
+// group of 128 (a loop covers more centroids).  The clusters' tokens are one
+// contiguous run, walked in 32-token chunks (a chunk never spans two clusters).
+// Per chunk: every thread holds 32 bytes of K and of V (token tid / 8, dims
+// 16 (tid % 8) .. + 15), prefetched during the previous chunk; it stores the K
+// bytes into a swizzled LDS tile (16-byte piece p of token row t at slot
+// p ^ (t % 16): the MFMA fragment reads hit 16 distinct slots per 16 lanes) and
+// reduces |v_t|^2 and v_t . vc over the token's 8 threads (DPP) into LDS.  After one
+// barrier S^T = K Q~^T comes from 16 bf16 MFMAs per wave: q~ is split into bf16
+// hi + lo with hi + lo == q~ exactly (q~ has 11 significant bits, hi the top 8,
+// lo the next 3), so every product is the reference's TF32 product exactly and
+// only the fp32 summation order differs.  Two LDS buffers alternate by chunk.
+// The token runs come from a block prefix sum of the sizes and are clamped to
+// the stored tokens, so no size vector can make the kernel read outside K or V.
+#include <type_traits>
+
+#include "spr_common.h"
+
+namespace {
+
+using spr::f32x16;
+using spr::u32x4;
+
+constexpr int SE_D = 128;
+constexpr int SE_THREADS = 256;
+constexpr int SE_WAVES = SE_THREADS / 64;
+constexpr int SE_CHUNK = 32;  // tokens per chunk: one 32-row MFMA block
+constexpr int SE_KSTEPS = SE_D / 16;
+constexpr float SE_LOG2E = 1.4426950408889634f;
+
+// Round to TF32 (10 stored mantissa bits), to nearest with ties away from zero.
+__device__ __forceinline__ float tf32_rna(float x) {
+  return __uint_as_float((__float_as_uint(x) + 0x1000u) & 0xffffe000u);
+}
+
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * SE_LOG2E); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// sum over lanes 8 i .. 8 i + 7 (quad_perm [1, 0, 3, 2], [2, 3, 0, 1], then row_half_mirror)
+__device__ __forceinline__ float oct_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  return v + dpp_mov<0x141>(v);
+}
+
+// max / sum over lanes l and l ^ 32: v_permlane32_swap of x with itself gives the
+// lower half-wave's value in the first result and the upper half's in the second on
+// every lane, so both lanes of a pair combine the same two operands in the same order.
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+constexpr int SE_ROW = SE_D * 2;  // bytes per bf16 token row
+constexpr int SE_CPW = 8;         // key clusters per workgroup
+constexpr int CL_CLUSTERS = 64;   // clusters per centroid-logit workgroup
+
+// l_c = (q . kc) / sqrt(D) (+ 0.5 min(sum_d q_d^2 var_d / D, cap)) for 128 query rows x
+// 64 clusters per workgroup: thread -> query row tid / 2, clusters 32 (tid % 2) .. + 31;
+// fp32 fma chains over d in order.  Written to out [qh, qn, kn].
+__global__ __launch_bounds__(SE_THREADS) void svg_ear_centroid_logit_kernel(
+    const float* __restrict__ qc, const float* __restrict__ kcent, const float* __restrict__ var_k, float cap,
+    int32_t qn, int32_t kn, int32_t group, float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float kc_l[CL_CLUSTERS][SE_D];
+  __shared__ __attribute__((aligned(16))) float var_l[CL_CLUSTERS][SE_D];
+  const int64_t qh = blockIdx.y;
+  const int64_t kh = qh / group;
+  const int cb = blockIdx.x * CL_CLUSTERS;
+  const int ncl = min(CL_CLUSTERS, kn - cb);
+  const int tid = threadIdx.x;
+  const float scale = 1.0f / 11.313708498984761f;
+  for (int i = tid; i < CL_CLUSTERS * SE_D; i += SE_THREADS) {
+    const int c = i / SE_D, d = i % SE_D;
+    const bool live = c < ncl;
+    kc_l[c][d] = live ? kcent[(kh * kn + cb + c) * SE_D + d] : 0.0f;
+    var_l[c][d] = (live && var_k != nullptr) ? var_k[(kh * kn + cb + c) * SE_D + d] : 0.0f;
+  }
+  __syncthreads();
+  const int h = tid & 1;
+  for (int r = tid >> 1; r < qn; r += SE_THREADS / 2) {
+    const float* qrow = qc + (qh * qn + r) * SE_D;
+    float dot[32], s2[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) dot[j] = s2[j] = 0.0f;
+    for (int d0 = 0; d0 < SE_D; d0 += 4) {
+      const float4 qv = *reinterpret_cast<const float4*>(qrow + d0);
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const float4 kv = *reinterpret_cast<const float4*>(&kc_l[32 * h + j][d0]);
+        dot[j] = __builtin_fmaf(qv.x, kv.x, dot[j]);
+        dot[j] = __builtin_fmaf(qv.y, kv.y, dot[j]);
+        dot[j] = __builtin_fmaf(qv.z, kv.z, dot[j]);
+        dot[j] = __builtin_fmaf(qv.w, kv.w, dot[j]);
+        if (var_k != nullptr) {
+          const float4 vv = *reinterpret_cast<const float4*>(&var_l[32 * h + j][d0]);
+          s2[j] = __builtin_fmaf(qv.x * qv.x, vv.x, s2[j]);
+          s2[j] = __builtin_fmaf(qv.y * qv.y, vv.y, s2[j]);
+          s2[j] = __builtin_fmaf(qv.z * qv.z, vv.z, s2[j]);
+          s2[j] = __builtin_fmaf(qv.w * qv.w, vv.w, s2[j]);
+        }
+      }
+    }
+    float* orow = out + (qh * qn + r) * kn + cb + 32 * h;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      if (32 * h + j < ncl) {
+        float l = dot[j] * scale;
+        if (var_k != nullptr) l += 0.5f * fminf(s2[j] / static_cast<float>(SE_D), cap);
+        orow[j] = l;
+      }
+    }
+  }
+}
+
+template <int MODE>  // 0: value error (scores holds l_c on entry), 1: attention mass
+__global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
+    const float* __restrict__ qc, const uint16_t* __restrict__ ks, const uint16_t* __restrict__ vs,
+    const float* __restrict__ vcent, const int32_t* __restrict__ k_sizes, int32_t qn, int32_t kn, int64_t t_stored,
+    int32_t group, float* __restrict__ scores) {
+  __shared__ __attribute__((aligned(16))) uint8_t k_l[2][SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(16))) float vn2_l[2][SE_CHUNK];
+  __shared__ __attribute__((aligned(16))) float cdv_l[2][SE_CHUNK];
+  __shared__ float vc_l[SE_CPW][SE_D];
+  __shared__ float vc2_l[SE_CPW];
+  __shared__ float cl_l[SE_CPW][32 * SE_WAVES];
+  __shared__ int64_t run_l[SE_CPW + 1];
+  __shared__ int64_t red_l[SE_WAVES];
+
+  const int c_begin = blockIdx.x * SE_CPW;
+  const int ncl = min(SE_CPW, kn - c_begin);
+  const int64_t qh = blockIdx.y;
+  const int64_t kh = qh / group;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const float scale = 1.0f / 11.313708498984761f;  // 1 / sqrt(128), as the fp32 quotient
+
+  // ---- token runs of clusters c_begin .. c_begin + ncl - 1 (negative sizes count as 0)
+  const int32_t* sz = k_sizes + kh * kn;
+  int64_t part = 0;
+  for (int j = tid; j < c_begin; j += SE_THREADS) part += max(sz[j], 0);
+  for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+  if (lane == 0) red_l[wave] = part;
+  if (MODE == 0) {
+    for (int i = tid; i < SE_CPW * SE_D; i += SE_THREADS) {
+      const int j = i / SE_D;
+      vc_l[j][i % SE_D] = j < ncl ? vcent[(kh * kn + c_begin + j) * SE_D + i % SE_D] : 0.0f;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int64_t cum = 0;
+    for (int w = 0; w < SE_WAVES; ++w) cum += red_l[w];
+    run_l[0] = min(cum, t_stored);
+    for (int j = 0; j < SE_CPW; ++j) {
+      if (j < ncl) cum += max(sz[c_begin + j], 0);
+      run_l[j + 1] = min(cum, t_stored);
+    }
+  }
+  if (MODE == 0) {
+    for (int j = wave; j < SE_CPW; j += SE_WAVES) {
+      const float a = vc_l[j][2 * lane], b = vc_l[j][2 * lane + 1];
+      const float s = wave_sum(__builtin_fmaf(a, a, b * b));
+      if (lane == 0) vc2_l[j] = s;
+    }
+  }
+  __syncthreads();
+  auto cl_len = [&](int j) { return static_cast<int32_t>(run_l[j + 1] - run_l[j]); };
+  // empty clusters score -inf
+  for (int j = 0; j < ncl; ++j) {
+    if (cl_len(j) <= 0) {
+      for (int q = tid; q < qn; q += SE_THREADS) scores[(qh * qn + q) * kn + c_begin + j] = -__builtin_huge_valf();
+    }
+  }
+  int j_first = 0;
+  while (j_first < ncl && cl_len(j_first) <= 0) ++j_first;
+  if (j_first >= ncl) return;
+
+  // ---- prefetch registers: token pt = tid / 8 of the chunk, pieces 2 (tid % 8) and + 1
+  constexpr int PIECES = SE_CHUNK * (SE_ROW / 16) / SE_THREADS;
+  const int pt = tid >> 3;
+  const int pp = PIECES * (tid & 7);
+  u32x4 kreg[PIECES], vreg[PIECES];
+  auto fetch = [&](int j, int c0) {
+    const bool live = c0 + pt < cl_len(j);
+    const int64_t row = kh * t_stored + run_l[j] + c0 + (live ? pt : 0);
+    const uint16_t* kr = ks + row * SE_D + 8 * pp;
+#pragma unroll
+    for (int i = 0; i < PIECES; ++i) kreg[i] = live ? *reinterpret_cast<const u32x4*>(kr + 8 * i) : u32x4{0, 0, 0, 0};
+    if (MODE == 0) {
+      const uint16_t* vr = vs + row * SE_D + 8 * pp;
+#pragma unroll
+      for (int i = 0; i < PIECES; ++i) vreg[i] = live ? *reinterpret_cast<const u32x4*>(vr + 8 * i) : u32x4{0, 0, 0, 0};
+    }
+  };
+  // next (cluster, chunk) of the walk; j = ncl when done
+  auto advance = [&](int& j, int& c0) {
+    c0 += SE_CHUNK;
+    if (c0 >= cl_len(j)) {
+      c0 = 0;
+      ++j;
+      while (j < ncl && cl_len(j) <= 0) ++j;
+    }
+  };
+
+  int si = 0;  // chunk counter over the whole kernel: buffer si & 1
+  for (int q0 = 0; q0 < qn; q0 += 32 * SE_WAVES) {
+    const int q = q0 + 32 * wave + col;
+    const bool q_live = q < qn;
+    const bool wave_live = q0 + 32 * wave < qn;
+    const float* qrow = qc + (qh * qn + (q_live ? q : 0)) * SE_D;
+
+    // B fragments: q~ dims 16 s + 8 half + 0..7 as bf16 hi and lo
+    u32x4 qhi[SE_KSTEPS], qlo[SE_KSTEPS];
+#pragma unroll
+    for (int s = 0; s < SE_KSTEPS; ++s) {
+      float v[8];
+      if (q_live) {
+        const float4 a = *reinterpret_cast<const float4*>(qrow + 16 * s + 8 * half);
+        const float4 b = *reinterpret_cast<const float4*>(qrow + 16 * s + 8 * half + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+      }
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float t0 = tf32_rna(v[2 * i]), t1 = tf32_rna(v[2 * i + 1]);
+        const float h0 = __uint_as_float(__float_as_uint(t0) & 0xffff0000u);
+        const float h1 = __uint_as_float(__float_as_uint(t1) & 0xffff0000u);
+        h[i] = (__float_as_uint(h0) >> 16) | (__float_as_uint(h1) & 0xffff0000u);
+        // t - h has at most 3 significant bits: exact in fp32 and in bf16
+        l[i] = (__float_as_uint(t0 - h0) >> 16) | (__float_as_uint(t1 - h1) & 0xffff0000u);
+      }
+      qhi[s] = u32x4{h[0], h[1], h[2], h[3]};
+      qlo[s] = u32x4{l[0], l[1], l[2], l[3]};
+    }
+    if (MODE == 0) {
+      // centroid logits of this query group (written by svg_ear_centroid_logit_kernel); the
+      // barrier first: a wave may still read the previous group's cl_l
+      __syncthreads();
+      for (int i = tid; i < SE_CPW * 32 * SE_WAVES; i += SE_THREADS) {
+        const int j = i / (32 * SE_WAVES), r = q0 + i % (32 * SE_WAVES);
+        cl_l[j][i % (32 * SE_WAVES)] = (j < ncl && r < qn) ? scores[(qh * qn + r) * kn + c_begin + j] : 0.0f;
+      }
+      __syncthreads();  // every wave has read l_c before any score of the group is written
+    }
+
+    float m = 0.0f, cw = 1.0f, esum = 0.0f;
+    int j = j_first, c0 = 0;
+    fetch(j, c0);
+    while (j < ncl) {
+      const int buf = si & 1;
+      const int cn = min(SE_CHUNK, cl_len(j) - c0);
+      uint8_t* kt = k_l[buf];
+      // K bytes into the swizzled tile; |v|^2 and v . vc of token pt
+#pragma unroll
+      for (int i = 0; i < PIECES; ++i)
+        *reinterpret_cast<u32x4*>(kt + pt * SE_ROW + (((pp + i) ^ (pt & 15)) << 4)) = kreg[i];
+      if (MODE == 0) {
+        const float* cc = vc_l[j] + 8 * pp;
+        float pn = 0.0f, pc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PIECES; ++i) {
+          const uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = spr::bf16_lo(w[e]), hi = spr::bf16_hi(w[e]);
+            pn = __builtin_fmaf(lo, lo, pn);
+            pn = __builtin_fmaf(hi, hi, pn);
+            pc = __builtin_fmaf(lo, cc[8 * i + 2 * e], pc);
+            pc = __builtin_fmaf(hi, cc[8 * i + 2 * e + 1], pc);
+          }
+        }
+        pn = oct_sum(pn);
+        pc = oct_sum(pc);
+        if ((tid & 7) == 0) {
+          vn2_l[buf][pt] = pn;
+          cdv_l[buf][pt] = pc;
+        }
+      }
+      const int jc = j;
+      const bool first = c0 == 0;
+      const bool last = c0 + SE_CHUNK >= cl_len(j);
+      advance(j, c0);
+      if (j < ncl) fetch(j, c0);  // next chunk's K/V in flight during this chunk's compute
+      __syncthreads();            // this chunk's K tile, |v|^2 and v . vc are in LDS
+      ++si;
+      if (wave_live) {
+        if (first) {
+          m = MODE == 0 ? cl_l[jc][32 * wave + col] : -__builtin_huge_valf();
+          cw = 1.0f;
+          esum = 0.0f;
+        }
+        f32x16 acc[1] = {};
+        constexpr int NB = SE_CHUNK / 32;
+#pragma unroll
+        for (int s = 0; s < SE_KSTEPS; ++s) {
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const int row = 32 * b + col;
+            const u32x4 a = *reinterpret_cast<const u32x4*>(kt + row * SE_ROW + (((2 * s + half) ^ (row & 15)) << 4));
+            acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qhi[s]), acc[b], 0, 0, 0);
+            acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qlo[s]), acc[b], 0, 0, 0);
+          }
+        }
+        // element e of block b is token 32 b + 8 (e / 4) + 4 half + e % 4 of the chunk
+        // The chunk's 16 elements per lane, straight-line.  A full chunk (the common case)
+        // needs no mask; in a partial one a token past the end gets exponent -inf (weight
+        // 0) and its error term is multiplied by 0 (its K and V rows are zero, so every
+        // term stays finite).
+        auto update = [&](auto masked) {
+          constexpr bool MASKED = decltype(masked)::value;
+          auto live = [&](int b, int e) { return 32 * b + 8 * (e / 4) + 4 * half + (e % 4) < cn; };
+          float cmax = -__builtin_huge_valf();
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              acc[b][e] *= scale;
+              cmax = fmaxf(cmax, (!MASKED || live(b, e)) ? acc[b][e] : -__builtin_huge_valf());
+            }
+          }
+          cmax = max_xor32(cmax);
+          const float m_new = fmaxf(m, cmax);
+          const float alpha = exp_fast(m - m_new);
+          float add = 0.0f;
+          if (MODE == 0) {
+            cw *= alpha;
+            esum *= alpha * alpha;
+            const float base = cw * cw * vc2_l[jc];
+            const float two_cw = 2.0f * cw;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int t0 = 32 * b + 8 * i + 4 * half;
+                const float4 vn = *reinterpret_cast<const float4*>(&vn2_l[buf][t0]);
+                const float4 cd = *reinterpret_cast<const float4*>(&cdv_l[buf][t0]);
+                const float vna[4] = {vn.x, vn.y, vn.z, vn.w};
+                const float cda[4] = {cd.x, cd.y, cd.z, cd.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const bool lv = !MASKED || live(b, 4 * i + r);
+                  const float tw = exp_fast(lv ? acc[b][4 * i + r] - m_new : -__builtin_huge_valf());
+                  const float err = fmaxf(base + tw * tw * vna[r] - tw * two_cw * cda[r], 0.0f);
+                  add += MASKED ? err * static_cast<float>(lv) : err;
+                }
+              }
+            }
+          } else {
+            esum *= alpha;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+              for (int e = 0; e < 16; ++e) {
+                const bool lv = !MASKED || live(b, e);
+                add += exp_fast(lv ? acc[b][e] - m_new : -__builtin_huge_valf());
+              }
+            }
+          }
+          esum += add;
+          m = m_new;
+        };
+        if (cn == SE_CHUNK) {
+          update(std::false_type{});
+        } else {
+          update(std::true_type{});
+        }
+        if (last) {
+          const float total = sum_xor32(esum);
+          if (q_live && half == 0) {
+            const float score = MODE == 0
+                                    ? logf(fmaxf(total / static_cast<float>(cl_len(jc)), 1.0e-30f)) + 2.0f * m
+                                    : logf(fmaxf(total, 1.0e-30f)) + m;
+            scores[(qh * qn + q) * kn + c_begin + jc] = score;
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" size_t spr_svg_ear_scores_flops(int64_t q_heads, int32_t qn, int64_t tokens) {
+  return static_cast<size_t>(2) * q_heads * qn * tokens * SE_D;
+}
+
+extern "C" int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_sorted, const uint16_t* v_sorted,
+                                  const float* k_centroids, const float* v_centroids, const float* var_k_diag,
+                                  float jensen_var_cap, const int32_t* k_sizes, int64_t q_heads, int32_t qn,
+                                  int32_t kn, int64_t kv_heads, int64_t t_stored, int32_t d, int32_t group,
+                                  int32_t mode, float* scores, hipStream_t stream) {
+  SPR_REQUIRE(mode == 0 || mode == 1, "spr_svg_ear_scores: mode must be 0 (value error) or 1 (attention mass)");
+  SPR_REQUIRE(d == SE_D, "spr_svg_ear_scores: head dim must be 128 (got %d)", d);
+  SPR_REQUIRE(qn >= 1 && kn >= 1 && kv_heads >= 1 && group >= 1 && t_stored >= 1,
+              "spr_svg_ear_scores: bad size");
+  SPR_REQUIRE(q_heads == kv_heads * group, "spr_svg_ear_scores: q_heads %lld != kv_heads %lld * group %d",
+              static_cast<long long>(q_heads), static_cast<long long>(kv_heads), group);
+  SPR_REQUIRE(q_heads <= 65535 && kn <= (1 << 30), "spr_svg_ear_scores: grid too large");
+  SPR_REQUIRE(q_centroids && k_sorted && k_sizes && scores, "spr_svg_ear_scores: null pointer");
+  if (mode == 0) {
+    SPR_REQUIRE(v_sorted && k_centroids && v_centroids, "spr_svg_ear_scores: value error needs V and centroids");
+    SPR_REQUIRE(!(jensen_var_cap > 0.0f) || var_k_diag != nullptr,
+                "spr_svg_ear_scores: Jensen-aware routing requires var_k_diag");
+  }
+  const dim3 grid(static_cast<uint32_t>((kn + SE_CPW - 1) / SE_CPW), static_cast<uint32_t>(q_heads));
+  if (mode == 0) {
+    const bool jensen = jensen_var_cap > 0.0f;
+    svg_ear_centroid_logit_kernel<<<dim3(static_cast<uint32_t>((kn + CL_CLUSTERS - 1) / CL_CLUSTERS),
+                                         static_cast<uint32_t>(q_heads)),
+                                    SE_THREADS, 0, stream>>>(q_centroids, k_centroids, jensen ? var_k_diag : nullptr,
+                                                             jensen ? jensen_var_cap : 0.0f, qn, kn, group, scores);
+    SPR_LAUNCHED("svg_ear_centroid_logit_kernel");
+    svg_ear_score_kernel<0><<<grid, SE_THREADS, 0, stream>>>(q_centroids, k_sorted, v_sorted, v_centroids, k_sizes,
+                                                             qn, kn, t_stored, group, scores);
+    SPR_LAUNCHED("svg_ear_score_kernel<value>");
+  } else {
+    svg_ear_score_kernel<1><<<grid, SE_THREADS, 0, stream>>>(q_centroids, k_sorted, nullptr, nullptr, k_sizes, qn,
+                                                             kn, t_stored, group, scores);
+    SPR_LAUNCHED("svg_ear_score_kernel<mass>");
+  }
+  return SPR_OK;
+}

@@ -560,3 +560,108 @@ def test_topp_map_matches_torch_dtype_flow(oracle, bf16):
         near = (np.abs(cum.numpy() - p) <= tol).any(-1)
         assert (got[~near] == ref.numpy()[~near]).all()
         assert (~near).mean() > 0.5
+
+
+# --------------------------------------------------------------------------- SVG-EAR routing scores
+
+def test_tf32_rounding_ties_away_from_zero(oracle):
+    # 1 + 2^-11 lies half way between TF32 neighbours 1 and 1 + 2^-10: ties away from zero
+    # (round-to-nearest-even would give 1)
+    vals = np.array([1 + 2 ** -11, 1 + 2 ** -12, -(1 + 2 ** -11), 1 + 3 * 2 ** -12, 1 + 2 ** -10, 3.0],
+                    np.float32)
+    got = oracle.tf32_rna(vals)
+    assert got.tolist() == [1 + 2 ** -10, 1.0, -(1 + 2 ** -10), 1 + 2 ** -10, 1 + 2 ** -10, 3.0]
+    x = np.random.default_rng(1).standard_normal(100000).astype(np.float32)
+    t = oracle.tf32_rna(x)
+    assert (t.view(np.uint32) & 0x1FFF == 0).all()
+    # within half a TF32 ulp
+    ulp = np.ldexp(1.0, np.frexp(np.abs(x).astype(np.float64))[1] - 11)
+    assert (np.abs(t.astype(np.float64) - x) <= ulp / 2).all()
+
+
+def _svg_case(rng, qh, group, qn, sizes, d=128, scale=0.3, extra=3):
+    kvh = qh // group
+    kn = sizes.shape[1]
+    t = int(sizes.sum(axis=1).max()) + extra
+    qc = (rng.standard_normal((qh, qn, d)) * scale).astype(np.float32)
+    k = rng.standard_normal((kvh, t, d)).astype(np.float32)
+    v = rng.standard_normal((kvh, t, d)).astype(np.float32)
+    kc = (rng.standard_normal((kvh, kn, d)) * 0.5).astype(np.float32)
+    vc = (rng.standard_normal((kvh, kn, d)) * 0.5).astype(np.float32)
+    return qc, k, v, kc, vc
+
+
+def _brute_value_error(qc, k, v, kc, vc, sizes, group, var=None, cap=0.0):
+    """exp(score) = (1/n) sum_t || e^{l_c} vc - e^{l_t} v_t ||^2 by direct vector norms: no
+    expansion into |vc|^2, |v|^2, v.vc and no max shift (small logits keep e^l finite)."""
+    qh, qn, d = qc.shape
+    kn = sizes.shape[1]
+    sc = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    out = np.full((qh, qn, kn), -np.inf)
+    for h in range(qh):
+        kh = h // group
+        off = 0
+        for c in range(kn):
+            n = int(sizes[kh, c])
+            if n == 0:
+                continue
+            for i in range(qn):
+                q = qc[h, i].astype(np.float64)
+                lc = float(q @ kc[kh, c]) * sc
+                if cap > 0.0:
+                    lc += 0.5 * min(float((q * q) @ var[kh, c]) / d, cap)
+                qt = (q.astype(np.float32).view(np.uint32).astype(np.uint64) + 0x1000) & 0xFFFFE000
+                qt = qt.astype(np.uint32).view(np.float32).astype(np.float64)
+                tot = 0.0
+                for t in range(off, off + n):
+                    lt = float(qt @ k[kh, t].astype(np.float64)) * sc
+                    diff = math.exp(lc) * vc[kh, c].astype(np.float64) - math.exp(lt) * v[kh, t].astype(np.float64)
+                    tot += float(diff @ diff)
+                out[h, i, c] = math.log(tot / n)
+            off += n
+    return out
+
+
+@pytest.mark.parametrize("group", [1, 2])
+def test_svg_ear_value_error_closed_form(oracle, group):
+    rng = np.random.default_rng(7 + group)
+    sizes = np.array([[3, 0, 5, 1], [2, 4, 0, 6]], np.int32)[: 2 // group]
+    qc, k, v, kc, vc = _svg_case(rng, 2, group, 3, sizes)
+    got = oracle.svg_ear_value_error_scores(qc, k, v, kc, vc, sizes, group).astype(np.float64)
+    ref = _brute_value_error(qc, k, v, kc, vc, sizes, group)
+    assert (np.isinf(got) == np.isinf(ref)).all()
+    fin = np.isfinite(ref)
+    assert np.abs(got[fin] - ref[fin]).max() < 1e-5
+
+
+def test_svg_ear_jensen_term(oracle):
+    rng = np.random.default_rng(11)
+    sizes = np.array([[4, 2, 3]], np.int32)
+    qc, k, v, kc, vc = _svg_case(rng, 1, 1, 4, sizes)
+    var = rng.uniform(0.0, 2.0, kc.shape).astype(np.float32)
+    base = oracle.svg_ear_value_error_scores(qc, k, v, kc, vc, sizes, 1)
+    zero = oracle.svg_ear_value_error_scores(qc, k, v, kc, vc, sizes, 1, np.zeros_like(var), 0.5)
+    assert np.array_equal(base, zero)
+    for cap in (0.01, 10.0):  # the cap binding and not binding
+        got = oracle.svg_ear_value_error_scores(qc, k, v, kc, vc, sizes, 1, var, cap).astype(np.float64)
+        ref = _brute_value_error(qc, k, v, kc, vc, sizes, 1, var, cap)
+        assert np.abs(got - ref).max() < 1e-5
+
+
+def test_attention_mass_is_cluster_logsumexp(oracle):
+    from scipy.special import logsumexp
+
+    rng = np.random.default_rng(3)
+    sizes = np.array([[5, 0, 9, 1, 30]], np.int32)
+    qc, k, _, _, _ = _svg_case(rng, 2, 2, 6, sizes, scale=2.0)
+    got = oracle.attention_mass_scores(qc, k, sizes, 2).astype(np.float64)
+    sc = float(np.float32(1.0) / np.sqrt(np.float32(128)))
+    qt = oracle.tf32_rna(qc).astype(np.float64)
+    off = np.concatenate(([0], np.cumsum(sizes[0])))
+    for h in range(2):
+        for c in range(5):
+            if sizes[0, c] == 0:
+                assert np.isinf(got[h, :, c]).all() and (got[h, :, c] < 0).all()
+                continue
+            lt = (qt[h] @ k[0, off[c]:off[c + 1]].astype(np.float64).T) * sc
+            assert np.abs(got[h, :, c] - logsumexp(lt, axis=1)).max() < 1e-5
