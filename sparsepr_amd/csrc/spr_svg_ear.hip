@@ -64,6 +64,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, int32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+#endif
+}
+
+// Workgroup barrier after this wave's LDS accesses completed, with no wait on the
+// vector memory counter: LDS DMA of later chunks stays in flight across it (its
+// landing is waited for explicitly).  The memory clobber keeps the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
@@ -154,13 +166,25 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
     const float* __restrict__ qc, const uint16_t* __restrict__ ks, const uint16_t* __restrict__ vs,
     const float* __restrict__ vcent, const int32_t* __restrict__ k_sizes, int32_t qn, int32_t kn, int64_t t_stored,
     int32_t group, float* __restrict__ scores) {
-  __shared__ __attribute__((aligned(16))) uint8_t k_l[2][SE_CHUNK * SE_ROW];
+  // four K and four V tiles as separate arrays: the chunk loop is unrolled by four so that
+  // every LDS read names a tile the compiler can tell apart from the ones being DMA'd
+  // (otherwise it waits for all DMA in flight before each read)
+  __shared__ __attribute__((aligned(1024))) uint8_t k_l0[SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_l1[SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_l2[SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_l3[SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_l0[SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_l1[SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_l2[SE_CHUNK * SE_ROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_l3[SE_CHUNK * SE_ROW];
   __shared__ __attribute__((aligned(16))) float vn2_l[2][SE_CHUNK];
   __shared__ __attribute__((aligned(16))) float cdv_l[2][SE_CHUNK];
   __shared__ float vc_l[SE_CPW][SE_D];
   __shared__ float vc2_l[SE_CPW];
   __shared__ float cl_l[SE_CPW][32 * SE_WAVES];
-  __shared__ int64_t run_l[SE_CPW + 1];
+  __shared__ int32_t start_l[SE_CPW];  // first stored token of each cluster's run (clamped)
+  __shared__ int32_t len_l[SE_CPW];    // tokens in each run (clamped)
+  __shared__ int32_t nxt_l[SE_CPW];    // next cluster with tokens (ncl if none)
   __shared__ int64_t red_l[SE_WAVES];
 
   const int c_begin = blockIdx.x * SE_CPW;
@@ -190,10 +214,16 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
   if (tid == 0) {
     int64_t cum = 0;
     for (int w = 0; w < SE_WAVES; ++w) cum += red_l[w];
-    run_l[0] = min(cum, t_stored);
     for (int j = 0; j < SE_CPW; ++j) {
+      const int64_t a = min(cum, t_stored);
       if (j < ncl) cum += max(sz[c_begin + j], 0);
-      run_l[j + 1] = min(cum, t_stored);
+      start_l[j] = static_cast<int32_t>(a);
+      len_l[j] = static_cast<int32_t>(min(cum, t_stored) - a);
+    }
+    int next = ncl;
+    for (int j = SE_CPW - 1; j >= 0; --j) {
+      nxt_l[j] = next;
+      if (j < ncl && len_l[j] > 0) next = j;
     }
   }
   if (MODE == 0) {
@@ -204,32 +234,63 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
     }
   }
   __syncthreads();
-  auto cl_len = [&](int j) { return static_cast<int32_t>(run_l[j + 1] - run_l[j]); };
+  auto cl_len = [&](int j) { return len_l[j]; };
   // empty clusters score -inf
   for (int j = 0; j < ncl; ++j) {
     if (cl_len(j) <= 0) {
       for (int q = tid; q < qn; q += SE_THREADS) scores[(qh * qn + q) * kn + c_begin + j] = -__builtin_huge_valf();
     }
   }
-  int j_first = 0;
-  while (j_first < ncl && cl_len(j_first) <= 0) ++j_first;
+  const int j_first = cl_len(0) > 0 ? 0 : nxt_l[0];
   if (j_first >= ncl) return;
 
-  // ---- prefetch registers: token pt = tid / 8 of the chunk, pieces 2 (tid % 8) and + 1
-  constexpr int PIECES = SE_CHUNK * (SE_ROW / 16) / SE_THREADS;
-  const int pt = tid >> 3;
-  const int pp = PIECES * (tid & 7);
-  u32x4 kreg[PIECES], vreg[PIECES];
-  auto fetch = [&](int j, int c0) {
-    const bool live = c0 + pt < cl_len(j);
-    const int64_t row = kh * t_stored + run_l[j] + c0 + (live ? pt : 0);
-    const uint16_t* kr = ks + row * SE_D + 8 * pp;
+  // ---- K/V chunks land in LDS by DMA: 32 token rows of 256 bytes per tile; wave w moves rows
+  // 4 w .. 4 w + 3 and 16 + 4 w .. + 3 (1 KB per instruction).  In the K tile the lane that
+  // fills slot p of row t fetches piece p ^ (t % 16) (the swizzle of the MFMA reads); V is
+  // stored as is.  Rows past the cluster's run hold the next cluster's tokens (masked in the
+  // scores); rows past the stored tokens read as zero (buffer bounds).
+  const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(ks + kh * t_stored * SE_D), 0, static_cast<int32_t>(t_stored * SE_ROW), 0x00020000);
+  const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(MODE == 0 ? vs + kh * t_stored * SE_D : ks), 0, static_cast<int32_t>(t_stored * SE_ROW),
+      0x00020000);
+  auto dma = [&](int j, int c0, uint8_t* kd, uint8_t* vd) {
+    const int slot = lane & 15;
 #pragma unroll
-    for (int i = 0; i < PIECES; ++i) kreg[i] = live ? *reinterpret_cast<const u32x4*>(kr + 8 * i) : u32x4{0, 0, 0, 0};
-    if (MODE == 0) {
-      const uint16_t* vr = vs + row * SE_D + 8 * pp;
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = 4 * wave + 16 * i;
+      const int row = r0 + (lane >> 4);
+      const int32_t off = (start_l[j] + c0 + row) * SE_ROW;
+      lds_dma16(k_rsrc, kd + r0 * SE_ROW, off + ((slot ^ (row & 15)) << 4));
+      if (MODE == 0) lds_dma16(v_rsrc, vd + r0 * SE_ROW, off + (slot << 4));
+    }
+  };
+  constexpr int DMA_PER_CHUNK = MODE == 0 ? 4 : 2;  // per wave
+  // |v_t|^2 and v_t . vc of chunk (j, c0) from V tile b into vn2_l / cdv_l[p]: token tid / 8,
+  // dims 16 (tid % 8) .. + 15, reduced over the token's 8 lanes
+  auto vstats = [&](int j, const uint8_t* vt, int p) {
+    const int pt = tid >> 3, pp = 2 * (tid & 7);
+    const uint8_t* vr = vt + pt * SE_ROW + pp * 16;
+    const float* cc = vc_l[j] + 8 * pp;
+    float pn = 0.0f, pc = 0.0f;
 #pragma unroll
-      for (int i = 0; i < PIECES; ++i) vreg[i] = live ? *reinterpret_cast<const u32x4*>(vr + 8 * i) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < 2; ++i) {
+      const u32x4 v4 = *reinterpret_cast<const u32x4*>(vr + 16 * i);
+      const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = spr::bf16_lo(w[e]), hi = spr::bf16_hi(w[e]);
+        pn = __builtin_fmaf(lo, lo, pn);
+        pn = __builtin_fmaf(hi, hi, pn);
+        pc = __builtin_fmaf(lo, cc[8 * i + 2 * e], pc);
+        pc = __builtin_fmaf(hi, cc[8 * i + 2 * e + 1], pc);
+      }
+    }
+    pn = oct_sum(pn);
+    pc = oct_sum(pc);
+    if ((tid & 7) == 0) {
+      vn2_l[p][pt] = pn;
+      cdv_l[p][pt] = pc;
     }
   };
   // next (cluster, chunk) of the walk; j = ncl when done
@@ -237,12 +298,10 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
     c0 += SE_CHUNK;
     if (c0 >= cl_len(j)) {
       c0 = 0;
-      ++j;
-      while (j < ncl && cl_len(j) <= 0) ++j;
+      j = nxt_l[j];
     }
   };
 
-  int si = 0;  // chunk counter over the whole kernel: buffer si & 1
   for (int q0 = 0; q0 < qn; q0 += 32 * SE_WAVES) {
     const int q = q0 + 32 * wave + col;
     const bool q_live = q < qn;
@@ -275,10 +334,10 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
       qhi[s] = u32x4{h[0], h[1], h[2], h[3]};
       qlo[s] = u32x4{l[0], l[1], l[2], l[3]};
     }
+    // every wave is done with the previous query group (its tiles, statistics and cl_l)
+    __syncthreads();
     if (MODE == 0) {
-      // centroid logits of this query group (written by svg_ear_centroid_logit_kernel); the
-      // barrier first: a wave may still read the previous group's cl_l
-      __syncthreads();
+      // centroid logits of this query group (written by svg_ear_centroid_logit_kernel)
       for (int i = tid; i < SE_CPW * 32 * SE_WAVES; i += SE_THREADS) {
         const int j = i / (32 * SE_WAVES), r = q0 + i % (32 * SE_WAVES);
         cl_l[j][i % (32 * SE_WAVES)] = (j < ncl && r < qn) ? scores[(qh * qn + r) * kn + c_begin + j] : 0.0f;
@@ -287,83 +346,107 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
     }
 
     float m = 0.0f, cw = 1.0f, esum = 0.0f;
-    int j = j_first, c0 = 0;
-    fetch(j, c0);
-    while (j < ncl) {
-      const int buf = si & 1;
-      const int cn = min(SE_CHUNK, cl_len(j) - c0);
-      uint8_t* kt = k_l[buf];
-      // K bytes into the swizzled tile; |v|^2 and v . vc of token pt
-#pragma unroll
-      for (int i = 0; i < PIECES; ++i)
-        *reinterpret_cast<u32x4*>(kt + pt * SE_ROW + (((pp + i) ^ (pt & 15)) << 4)) = kreg[i];
-      if (MODE == 0) {
-        const float* cc = vc_l[j] + 8 * pp;
-        float pn = 0.0f, pc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < PIECES; ++i) {
-          const uint32_t w[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float lo = spr::bf16_lo(w[e]), hi = spr::bf16_hi(w[e]);
-            pn = __builtin_fmaf(lo, lo, pn);
-            pn = __builtin_fmaf(hi, hi, pn);
-            pc = __builtin_fmaf(lo, cc[8 * i + 2 * e], pc);
-            pc = __builtin_fmaf(hi, cc[8 * i + 2 * e + 1], pc);
-          }
-        }
-        pn = oct_sum(pn);
-        pc = oct_sum(pc);
-        if ((tid & 7) == 0) {
-          vn2_l[buf][pt] = pn;
-          cdv_l[buf][pt] = pc;
-        }
+    int j = j_first, c0 = 0;       // chunk computed
+    int jv = j_first, cv = 0;      // chunk whose V statistics come next
+    int jd = j_first, cd = 0;      // next chunk to DMA
+    int issued = 0, step = 0;      // chunks DMA'd / computed in this query group
+    // chunks 0 .. 2 into tiles 0 .. 2 (named arrays, as in the loop)
+    auto prologue_dma = [&](uint8_t* kd, uint8_t* vd) {
+      if (jd < ncl) {
+        dma(jd, cd, kd, vd);
+        ++issued;
+        advance(jd, cd);
       }
+    };
+    prologue_dma(k_l0, v_l0);
+    prologue_dma(k_l1, v_l1);
+    prologue_dma(k_l2, v_l2);
+    // chunk 0 landed (this wave's DMA), then every wave's; its V statistics
+    if (issued == 3) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_CHUNK) : "memory");
+    } else if (issued == 2) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PER_CHUNK) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    lds_barrier();
+    if (MODE == 0) vstats(jv, v_l0, 0);
+    advance(jv, cv);
+    // S^T of the chunk in tile kt: 16 MFMAs (hi and lo halves of q~ per 16-dim step)
+    auto smma = [&](f32x16& acc, const uint8_t* kt) {
+      acc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < SE_KSTEPS; ++s) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(kt + col * SE_ROW + (((2 * s + half) ^ (col & 15)) << 4));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qhi[s]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qlo[s]), acc, 0, 0, 0);
+      }
+    };
+    f32x16 acc_a, acc_b;
+    if (wave_live) smma(acc_a, k_l0);
+    // One chunk step s: DMAs chunk s + 3 into kd / vd, takes the V statistics of chunk
+    // s + 1 from vt1 into buf ^ 1, issues the MFMAs of chunk s + 1 (tile kt1) into
+    // acc_next and folds chunk s (acc_cur, statistics buf) into the running state: the
+    // matrix unit works on s + 1 while the VALU works on s.  Returns false when the walk
+    // is done.
+    auto chunk_step = [&](const uint8_t* kt1, const uint8_t* vt1, uint8_t* kd, uint8_t* vd, const int buf,
+                          f32x16& acc_cur, f32x16& acc_next) {
+      if (j >= ncl) return false;
+      const int cn = min(SE_CHUNK, cl_len(j) - c0);
       const int jc = j;
       const bool first = c0 == 0;
       const bool last = c0 + SE_CHUNK >= cl_len(j);
+      // chunk step + 1 landed (this wave's DMA; the one of step + 2 may still be in flight),
+      // then every wave's; every wave is past step - 1, so its tiles and statistics are free
+      if (issued > step + 2) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA_PER_CHUNK) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      lds_barrier();
+      if (jd < ncl) {
+        dma(jd, cd, kd, vd);
+        ++issued;
+        advance(jd, cd);
+      }
+      const bool has_next = jv < ncl;
+      if (has_next) {
+        if (MODE == 0) vstats(jv, vt1, buf ^ 1);
+        advance(jv, cv);
+      }
       advance(j, c0);
-      if (j < ncl) fetch(j, c0);  // next chunk's K/V in flight during this chunk's compute
-      __syncthreads();            // this chunk's K tile, |v|^2 and v . vc are in LDS
-      ++si;
+      ++step;
       if (wave_live) {
+        if (has_next) smma(acc_next, kt1);
         if (first) {
           m = MODE == 0 ? cl_l[jc][32 * wave + col] : -__builtin_huge_valf();
           cw = 1.0f;
           esum = 0.0f;
         }
-        f32x16 acc[1] = {};
-        constexpr int NB = SE_CHUNK / 32;
-#pragma unroll
-        for (int s = 0; s < SE_KSTEPS; ++s) {
-#pragma unroll
-          for (int b = 0; b < NB; ++b) {
-            const int row = 32 * b + col;
-            const u32x4 a = *reinterpret_cast<const u32x4*>(kt + row * SE_ROW + (((2 * s + half) ^ (row & 15)) << 4));
-            acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qhi[s]), acc[b], 0, 0, 0);
-            acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qlo[s]), acc[b], 0, 0, 0);
-          }
-        }
+        f32x16* acc = &acc_cur;
+        constexpr int NB = 1;
         // element e of block b is token 32 b + 8 (e / 4) + 4 half + e % 4 of the chunk
         // The chunk's 16 elements per lane, straight-line.  A full chunk (the common case)
-        // needs no mask; in a partial one a token past the end gets exponent -inf (weight
-        // 0) and its error term is multiplied by 0 (its K and V rows are zero, so every
-        // term stays finite).
+        // needs no mask; in a partial one a token past the end (its rows hold the next
+        // cluster's tokens or zeros) gets exponent -inf (weight 0) and its error term is
+        // cleared bitwise, so no value of those rows reaches the sums.
         auto update = [&](auto masked) {
           constexpr bool MASKED = decltype(masked)::value;
           auto live = [&](int b, int e) { return 32 * b + 8 * (e / 4) + 4 * half + (e % 4) < cn; };
+          // max over the raw dot products, scaled once: fl(a s) is monotone in a for s > 0,
+          // so this is the max of the scaled logits
           float cmax = -__builtin_huge_valf();
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              acc[b][e] *= scale;
-              cmax = fmaxf(cmax, (!MASKED || live(b, e)) ? acc[b][e] : -__builtin_huge_valf());
-            }
+            for (int e = 0; e < 16; ++e) cmax = fmaxf(cmax, (!MASKED || live(b, e)) ? acc[b][e] : -__builtin_huge_valf());
           }
-          cmax = max_xor32(cmax);
+          cmax = max_xor32(cmax) * scale;
           const float m_new = fmaxf(m, cmax);
           const float alpha = exp_fast(m - m_new);
+          // e^(l - m_new) = 2^(dot * scale * log2 e - m_new * log2 e), one fma per element
+          const float c1 = scale * SE_LOG2E;
+          const float negm = -m_new * SE_LOG2E;
           float add = 0.0f;
           if (MODE == 0) {
             cw *= alpha;
@@ -382,9 +465,12 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                   const bool lv = !MASKED || live(b, 4 * i + r);
-                  const float tw = exp_fast(lv ? acc[b][4 * i + r] - m_new : -__builtin_huge_valf());
-                  const float err = fmaxf(base + tw * tw * vna[r] - tw * two_cw * cda[r], 0.0f);
-                  add += MASKED ? err * static_cast<float>(lv) : err;
+                  const float x = __builtin_fmaf(acc[b][4 * i + r], c1, negm);
+                  const float tw = __builtin_amdgcn_exp2f(lv ? x : -__builtin_huge_valf());
+                  // w_c^2 |vc|^2 + w_t (w_t |v|^2 - 2 w_c v.vc)
+                  const float err =
+                      fmaxf(__builtin_fmaf(tw, __builtin_fmaf(tw, vna[r], -two_cw * cda[r]), base), 0.0f);
+                  add += MASKED ? __int_as_float(__float_as_int(err) & -static_cast<int>(lv)) : err;
                 }
               }
             }
@@ -395,7 +481,7 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
 #pragma unroll
               for (int e = 0; e < 16; ++e) {
                 const bool lv = !MASKED || live(b, e);
-                add += exp_fast(lv ? acc[b][e] - m_new : -__builtin_huge_valf());
+                add += __builtin_amdgcn_exp2f(lv ? __builtin_fmaf(acc[b][e], c1, negm) : -__builtin_huge_valf());
               }
             }
           }
@@ -417,6 +503,10 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
           }
         }
       }
+      return true;
+    };
+    while (chunk_step(k_l1, v_l1, k_l3, v_l3, 0, acc_a, acc_b) && chunk_step(k_l2, v_l2, k_l0, v_l0, 1, acc_b, acc_a) &&
+           chunk_step(k_l3, v_l3, k_l1, v_l1, 0, acc_a, acc_b) && chunk_step(k_l0, v_l0, k_l2, v_l2, 1, acc_b, acc_a)) {
     }
   }
 }
@@ -439,6 +529,9 @@ extern "C" int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_so
   SPR_REQUIRE(q_heads == kv_heads * group, "spr_svg_ear_scores: q_heads %lld != kv_heads %lld * group %d",
               static_cast<long long>(q_heads), static_cast<long long>(kv_heads), group);
   SPR_REQUIRE(q_heads <= 65535 && kn <= (1 << 30), "spr_svg_ear_scores: grid too large");
+  SPR_REQUIRE(t_stored < (int64_t(1) << 31) / (2 * SE_D) - SE_CHUNK,
+              "spr_svg_ear_scores: at most %lld stored tokens per head",
+              static_cast<long long>((int64_t(1) << 31) / (2 * SE_D) - SE_CHUNK - 1));
   SPR_REQUIRE(q_centroids && k_sorted && k_sizes && scores, "spr_svg_ear_scores: null pointer");
   if (mode == 0) {
     SPR_REQUIRE(v_sorted && k_centroids && v_centroids, "spr_svg_ear_scores: value error needs V and centroids");
