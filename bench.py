@@ -43,11 +43,12 @@ def parse():
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["attention", "copy", "svg_ear"], default=None,
+    ap.add_argument("--only", choices=["attention", "copy", "svg_ear", "role_proj"], default=None,
                     help="profiling aids: 'attention' routes once, then times only the block-sparse attention "
                          "kernel for --steps launches; 'copy' runs --steps plain 512 MiB device copies (the "
                          "calibration kernel for the HBM traffic counters); 'svg_ear' routes once, then times "
-                         "the N8 value-error routing scores (N8's default selector) on the routed clusters")
+                         "the N8 value-error routing scores (N8's default selector) on the routed clusters; "
+                         "'role_proj' times N8's Q role projection (rank 64) over the C4 Q")
     return ap.parse_args()
 
 
@@ -204,6 +205,40 @@ def only_svg_ear(args):
                       "finite_scores": round(float(torch.isfinite(scores).float().mean().item()), 4)}), flush=True)
 
 
+def only_role_proj(args):
+    """--steps launches of the Q role projection + row RMS normalisation at the C4 shape
+    (24 heads x 118,800 tokens, D = 128, rank 64).  Algorithmic HBM bytes per launch: Q read
+    once (bf16) + the fp32 features written once (+ the factors)."""
+    import torch
+
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.kernels.role_projection import role_projection_rms_triton
+
+    shape = synthetic.HUNYUAN
+    q, _, _ = synthetic.frame_gmm_qkv(shape, device="cuda", **GEN)
+    B, H, N, D = q.shape
+    x = q.reshape(B * H, N, D)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    factor = torch.randn((B * H, D, 64), device="cuda", generator=g) / D ** 0.5
+    out = torch.empty((B * H, N, 64), device="cuda")
+    for _ in range(args.warmup):
+        role_projection_rms_triton(x, factor, out=out)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        role_projection_rms_triton(x, factor, out=out)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    nbytes = x.numel() * 2 + out.numel() * 4 + factor.numel() * 4
+    gbs = nbytes / ms / 1e6
+    print(json.dumps({"kernel": "role_projection_kernel<128, 2>", "ms_per_launch": round(ms, 4),
+                      "config": {"bh": B * H, "tokens": N, "head_dim": D, "rank": 64},
+                      "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                   "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes}}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -216,6 +251,8 @@ def main():
         return only_attention(args)
     if args.only == "svg_ear":
         return only_svg_ear(args)
+    if args.only == "role_proj":
+        return only_role_proj(args)
     import torch
 
     from sparsepr_amd import synthetic

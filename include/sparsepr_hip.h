@@ -214,6 +214,14 @@ int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh
 int spr_probe_scatter(const void* dense, int32_t dense_dtype, const int32_t* rows, int64_t bh, int64_t n, int32_t m,
                       int32_t d, void* out, hipStream_t stream);
 
+/* ---------------------------------------------------------------- role projection
+ * role_projection.py:16-103 role_projection_rms_triton: out = p / sqrt(max(mean_r p_r^2,
+ * 1e-12)), p = x . F~ with F~ the factor rounded to TF32 (nearest, ties away).
+ *   x bf16 [bh, n, d], d in {64, 128}; factor fp32 [bh, d, rank], 1 <= rank <= 128 ->
+ *   out fp32 [bh, n, rank]. */
+int spr_role_projection_rms(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d, int32_t rank,
+                            float* out, hipStream_t stream);
+
 /* ---------------------------------------------------------------- SVG-EAR routing scores
  * svg_ear.py:95-192,453-531 svg_ear_value_error_scores_triton (mode 0; Jensen term when
  * jensen_var_cap > 0, var_k_diag [kv_heads, kn, d] fp32), svg_ear.py:195-286,534-600 the

@@ -749,6 +749,16 @@ def svg_ear_value_error_scores(qc, k_sorted, v_sorted, kc, vc, sizes, group, var
     return out.astype(np.float32)
 
 
+def role_projection_rms(x, factor):
+    """Role-coordinate projection with row RMS normalisation (role_projection.py:16-55
+    kernel, :58-103 wrapper): p = x . tf32(F) (x bf16-representable, so exact in TF32),
+    out = p / sqrt(max(mean_r p_r^2, 1e-12)).  x [BH, N, D], factor [BH, D, R] -> float32
+    [BH, N, R]; float64 inside."""
+    p = np.einsum("bnd,bdr->bnr", x.astype(np.float64), tf32_rna(factor).astype(np.float64))
+    ms = np.maximum((p * p).mean(axis=2, keepdims=True), 1e-12)
+    return (p / np.sqrt(ms)).astype(np.float32)
+
+
 def attention_mass_scores(qc, k_sorted, sizes, group):
     """Log attention mass of each key cluster at each query centroid (svg_ear.py:7-92
     kernel, :372-450 wrapper): score = log(max(sum_t e^(l_t - m), 1e-30)) + m with

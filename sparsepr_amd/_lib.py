@@ -69,6 +69,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_rrr_fit_workspace": (_sz, [_i64]),
     "spr_rrr_fit": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _sz, _vp]),
+    # role_proj.hip
+    "spr_role_projection_rms": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     # svg_ear.hip
     "spr_svg_ear_scores_flops": (_sz, [_i64, _i32, _i64]),
     "spr_svg_ear_scores": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _i32, _i32, _i64, _i64,

@@ -1,0 +1,168 @@
+// Role-coordinate projection with row RMS normalisation (N8's Q role features).
+//
+// Replaces:
+//   _role_projection_rms_kernel + role_projection_rms_triton
+//       (src/sparsepr/kernels/triton/role_projection.py:16-55, :58-103)
+//
+//   p = x . F~, out = p / sqrt(max(sum_r p_r^2 / R, 1e-12))
+// for x bf16 [bh, n, d] and the factor F fp32 [bh, d, R]; F~ is F rounded to TF32
+// (nearest, ties away), as the reference's tl.dot(..., input_precision="tf32") rounds
+// its fp32 operand (a bf16 x is exact in TF32).  F~ is split into bf16 hi + lo with
+// hi + lo == F~ exactly, so each product is exact and only the fp32 summation order
+// differs.
+//
+// Layout: one workgroup of four waves per (head, 2048 tokens); F~^T hi / lo of the head
+// sit in LDS (R rows padded to a multiple of 32, d columns, 16-byte pieces swizzled
+// by row).  A wave computes P^T = F~^T X^T for 32 tokens per step: A = F~^T fragments
+// from LDS, B = X^T fragments straight from HBM (lane = token, 16 contiguous bytes per
+// 16-dim step, the next block's prefetched), so each lane ends up with R / 2 values of
+// one token and the row's sum of squares needs one exchange between the two half-waves.
+#include "spr_common.h"
+
+namespace {
+
+using spr::f32x16;
+using spr::u32x4;
+
+constexpr int RP_THREADS = 256;
+constexpr int RP_WAVES = RP_THREADS / 64;
+constexpr int RP_TOKENS = 2048;  // tokens per workgroup
+constexpr int RP_MAX_R = 128;
+
+__device__ __forceinline__ float tf32_rna(float x) {
+  return __uint_as_float((__float_as_uint(x) + 0x1000u) & 0xffffe000u);
+}
+
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// D = head dim (D / 8 sixteen-byte pieces per F~^T row); RB = rank padded to 32, in 32-row blocks.
+template <int D, int RB>
+__global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint16_t* __restrict__ x,
+                                                                     const float* __restrict__ factor, int64_t n,
+                                                                     int32_t rank, float* __restrict__ out) {
+  constexpr int KSTEPS = D / 16;
+  constexpr int ROWB = D * 2;  // bytes per F~^T row (bf16)
+  constexpr int RP = RB * 32;
+  __shared__ __attribute__((aligned(16))) uint8_t fhi[RP * ROWB];
+  __shared__ __attribute__((aligned(16))) uint8_t flo[RP * ROWB];
+  const int64_t b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  // F~^T into LDS: element (r, k) of row r at piece (k / 8) ^ (r % (D / 8)), slot k % 8
+  const float* fb = factor + b * D * rank;
+  for (int i = tid; i < RP * D / 2; i += RP_THREADS) {
+    const int r = i / (D / 2), k = 2 * (i % (D / 2));
+    const float v0 = r < rank ? tf32_rna(fb[static_cast<int64_t>(k) * rank + r]) : 0.0f;
+    const float v1 = r < rank ? tf32_rna(fb[static_cast<int64_t>(k + 1) * rank + r]) : 0.0f;
+    const uint32_t h0 = __float_as_uint(v0) & 0xffff0000u, h1 = __float_as_uint(v1) & 0xffff0000u;
+    const uint32_t hw = (h0 >> 16) | h1;
+    // v - hi has at most 3 significant bits: exact in fp32 and in bf16
+    const uint32_t lw = (__float_as_uint(v0 - __uint_as_float(h0)) >> 16) |
+                        (__float_as_uint(v1 - __uint_as_float(h1)) & 0xffff0000u);
+    const int off = r * ROWB + ((((k >> 3) ^ (r % (D / 8))) << 4) | ((k & 7) << 1));
+    *reinterpret_cast<uint32_t*>(fhi + off) = hw;
+    *reinterpret_cast<uint32_t*>(flo + off) = lw;
+  }
+  __syncthreads();
+
+  const uint16_t* xb = x + b * n * D;
+  float* ob = out + b * n * rank;
+  const int64_t t_begin = static_cast<int64_t>(blockIdx.x) * RP_TOKENS;
+  const int64_t t_end = min(t_begin + RP_TOKENS, n);
+  // X^T fragments of a 32-token block: lane = token, 16 bytes per 16-dim step (zero past the end)
+  auto load_x = [&](u32x4 (&xf)[KSTEPS], int64_t t0) {
+    const int64_t t = t0 + col;
+    const bool live = t < t_end;
+    const uint16_t* xr = xb + (live ? t : t0) * D + 8 * half;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      xf[s] = *reinterpret_cast<const u32x4*>(xr + 16 * s);
+      if (!live) xf[s] = u32x4{0, 0, 0, 0};
+    }
+  };
+  u32x4 xn[KSTEPS];
+  if (t_begin + 32 * wave < t_end) load_x(xn, t_begin + 32 * wave);
+  for (int64_t t0 = t_begin + 32 * wave; t0 < t_end; t0 += 32 * RP_WAVES) {
+    const int64_t t = t0 + col;
+    const bool live = t < t_end;
+    u32x4 xf[KSTEPS];
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) xf[s] = xn[s];
+    // the next block's loads are in flight during this block's MFMAs and stores
+    if (t0 + 32 * RP_WAVES < t_end) load_x(xn, t0 + 32 * RP_WAVES);
+    f32x16 acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      acc[rb] = f32x16{};
+      const int r = 32 * rb + col;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const int off = r * ROWB + (((2 * s + half) ^ (r % (D / 8))) << 4);
+        const u32x4 ah = *reinterpret_cast<const u32x4*>(fhi + off);
+        const u32x4 al = *reinterpret_cast<const u32x4*>(flo + off);
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(xf[s]), acc[rb], 0, 0, 0);
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(al), spr::as_bf16x8(xf[s]), acc[rb], 0, 0, 0);
+      }
+    }
+    // lane (token col, half) holds p_r for r = 32 rb + 8 (e / 4) + 4 half + e % 4 (zero past rank)
+    float ss = 0.0f;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ss = __builtin_fmaf(acc[rb][e], acc[rb][e], ss);
+    }
+    ss = sum_xor32(ss);
+    const float inv = 1.0f / sqrtf(fmaxf(ss / static_cast<float>(rank), 1.0e-12f));
+    if (live) {
+      float* orow = ob + t * rank;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r0 = 32 * rb + 8 * g + 4 * half;
+          if (r0 + 3 < rank && (rank & 3) == 0) {
+            *reinterpret_cast<float4*>(orow + r0) = make_float4(acc[rb][4 * g] * inv, acc[rb][4 * g + 1] * inv,
+                                                                acc[rb][4 * g + 2] * inv, acc[rb][4 * g + 3] * inv);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (r0 + i < rank) orow[r0 + i] = acc[rb][4 * g + i] * inv;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int spr_role_projection_rms(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d,
+                                       int32_t rank, float* out, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0, "spr_role_projection_rms: bad size");
+  SPR_REQUIRE(d == 64 || d == 128, "spr_role_projection_rms: head dim must be 64 or 128 (got %d)", d);
+  SPR_REQUIRE(rank >= 1 && rank <= RP_MAX_R, "spr_role_projection_rms: rank must be in [1, %d] (got %d)", RP_MAX_R,
+              rank);
+  if (bh == 0 || n == 0) return SPR_OK;
+  SPR_REQUIRE(x && factor && out, "spr_role_projection_rms: null pointer");
+  SPR_REQUIRE(bh <= 65535, "spr_role_projection_rms: too many heads");
+  const dim3 grid(static_cast<uint32_t>((n + RP_TOKENS - 1) / RP_TOKENS), static_cast<uint32_t>(bh));
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const int rb = (rank + 31) / 32;
+#define SPR_RP(DD, RBB) role_projection_kernel<DD, RBB><<<grid, RP_THREADS, 0, stream>>>(xp, factor, n, rank, out)
+  if (d == 128) {
+    if (rb == 1) SPR_RP(128, 1); else if (rb == 2) SPR_RP(128, 2); else if (rb == 3) SPR_RP(128, 3); else SPR_RP(128, 4);
+  } else {
+    if (rb == 1) SPR_RP(64, 1); else if (rb == 2) SPR_RP(64, 2); else if (rb == 3) SPR_RP(64, 3); else SPR_RP(64, 4);
+  }
+#undef SPR_RP
+  SPR_LAUNCHED("role_projection_kernel");
+  return SPR_OK;
+}

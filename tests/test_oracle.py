@@ -665,3 +665,22 @@ def test_attention_mass_is_cluster_logsumexp(oracle):
                 continue
             lt = (qt[h] @ k[0, off[c]:off[c + 1]].astype(np.float64).T) * sc
             assert np.abs(got[h, :, c] - logsumexp(lt, axis=1)).max() < 1e-5
+
+
+def test_role_projection_rms_closed_form(oracle):
+    rng = np.random.default_rng(5)
+    x = oracle.to_bf16(rng.standard_normal((2, 9, 64)).astype(np.float32))
+    f = rng.standard_normal((2, 64, 48)).astype(np.float32)
+    x[1, 3] = 0.0  # a zero row: p = 0, the 1e-12 floor keeps it at 0
+    got = oracle.role_projection_rms(x, f).astype(np.float64)
+    ft = oracle.tf32_rna(f).astype(np.float64)
+    for b in range(2):
+        for n in range(9):
+            p = np.array([sum(float(x[b, n, d]) * ft[b, d, r] for d in range(64)) for r in range(48)])
+            nrm = np.linalg.norm(p)
+            want = p * math.sqrt(48) / nrm if nrm > 0 else np.zeros(48)
+            assert np.abs(got[b, n] - want).max() < 1e-5
+    # rows are unit RMS (except the zero row), and the projection uses the TF32 factor
+    rms = np.sqrt((got ** 2).mean(axis=2))
+    assert np.abs(np.delete(rms.reshape(-1), 1 * 9 + 3) - 1.0).max() < 1e-6
+    assert not np.allclose(oracle.role_projection_rms(x, f), oracle.role_projection_rms(x, f + 2 ** -14 * f), atol=0)
