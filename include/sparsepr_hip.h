@@ -221,6 +221,15 @@ int spr_probe_scatter(const void* dense, int32_t dense_dtype, const int32_t* row
  *   out fp32 [bh, n, rank]. */
 int spr_role_projection_rms(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d, int32_t rank,
                             float* out, hipStream_t stream);
+/* n8_v6.py:141-149 _role_k_projection_normalize_fp32 (torch.compile'd): p = x . F~ as
+ * above, key_scale[h] = max(sqrt(mean over tokens and rank of p^2), 1e-8), out = p / key_scale.
+ *   x bf16 [bh, n, d], d in {64, 128}; factor fp32 [bh, d, rank], rank <= 128 -> out fp32
+ *   [bh, n, rank], key_scale fp32 [bh].  The per-head sum of p^2 is formed deterministically
+ *   (fp64 per-workgroup partials in the workspace, summed in order);
+ *   workspace: spr_role_k_projection_workspace(bh, n) bytes. */
+size_t spr_role_k_projection_workspace(int64_t bh, int64_t n);
+int spr_role_k_projection(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d, int32_t rank,
+                          float* out, float* key_scale, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- SVG-EAR routing scores
  * svg_ear.py:95-192,453-531 svg_ear_value_error_scores_triton (mode 0; Jensen term when

@@ -759,6 +759,16 @@ def role_projection_rms(x, factor):
     return (p / np.sqrt(ms)).astype(np.float32)
 
 
+def role_k_projection_normalize(k, factor):
+    """_role_k_projection_normalize_fp32 (n8_v6.py:141-149): key = k . tf32(F) (the fp32
+    bmm under the reference's TF32 contract), key_scale = max(sqrt(mean over tokens and rank
+    of key^2), 1e-8) per head, returns (key / key_scale float32, key_scale float32 [BH, 1, 1]).
+    float64 inside."""
+    p = np.einsum("bnd,bdr->bnr", k.astype(np.float64), tf32_rna(factor).astype(np.float64))
+    scale = np.maximum(np.sqrt((p * p).mean(axis=(1, 2), keepdims=True)), 1e-8)
+    return (p / scale).astype(np.float32), scale.astype(np.float32)
+
+
 def attention_mass_scores(qc, k_sorted, sizes, group):
     """Log attention mass of each key cluster at each query centroid (svg_ear.py:7-92
     kernel, :372-450 wrapper): score = log(max(sum_t e^(l_t - m), 1e-30)) + m with

@@ -39,10 +39,15 @@ __device__ __forceinline__ float sum_xor32(float x) {
 }
 
 // D = head dim (D / 8 sixteen-byte pieces per F~^T row); RB = rank padded to 32, in 32-row blocks.
-template <int D, int RB>
+// MODE 0: rows normalised by their RMS.  MODE 1: no output; the workgroup's sum of p^2 goes to
+// partial[head][block] (fp64).  MODE 2: p divided by the head's scale sqrt(max(mean p^2, ...))
+// formed from the partials in block order (the same on every workgroup); block 0 stores it.
+template <int D, int RB, int MODE>
 __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint16_t* __restrict__ x,
                                                                      const float* __restrict__ factor, int64_t n,
-                                                                     int32_t rank, float* __restrict__ out) {
+                                                                     int32_t rank, float* __restrict__ out,
+                                                                     double* __restrict__ partial,
+                                                                     float* __restrict__ head_scale) {
   constexpr int KSTEPS = D / 16;
   constexpr int ROWB = D * 2;  // bytes per F~^T row (bf16)
   constexpr int RP = RB * 32;
@@ -74,6 +79,17 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
 
   const uint16_t* xb = x + b * n * D;
   float* ob = out + b * n * rank;
+  __shared__ double red_l[RP_WAVES];
+  float div = 1.0f;
+  if (MODE == 2) {
+    // the head's scale: fp64 sum of the partials in block order, then as the reference
+    // rounds it: fp32 mean, sqrt, clamp at 1e-8
+    double tot = 0.0;
+    for (uint32_t i = 0; i < gridDim.x; ++i) tot += partial[b * gridDim.x + i];
+    div = fmaxf(sqrtf(static_cast<float>(tot / (static_cast<double>(n) * rank))), 1.0e-8f);
+    if (blockIdx.x == 0 && tid == 0) head_scale[b] = div;
+  }
+  double wsum = 0.0;  // MODE 1: this lane's sum of p^2
   const int64_t t_begin = static_cast<int64_t>(blockIdx.x) * RP_TOKENS;
   const int64_t t_end = min(t_begin + RP_TOKENS, n);
   // X^T fragments of a 32-token block: lane = token, 16 bytes per 16-dim step (zero past the end)
@@ -118,8 +134,13 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
 #pragma unroll
       for (int e = 0; e < 16; ++e) ss = __builtin_fmaf(acc[rb][e], acc[rb][e], ss);
     }
+    if (MODE == 1) {
+      wsum += live ? static_cast<double>(ss) : 0.0;
+      continue;
+    }
     ss = sum_xor32(ss);
     const float inv = 1.0f / sqrtf(fmaxf(ss / static_cast<float>(rank), 1.0e-12f));
+    auto nrm = [&](float v) { return MODE == 0 ? v * inv : v / div; };
     if (live) {
       float* orow = ob + t * rank;
 #pragma unroll
@@ -128,21 +149,47 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
         for (int g = 0; g < 4; ++g) {
           const int r0 = 32 * rb + 8 * g + 4 * half;
           if (r0 + 3 < rank && (rank & 3) == 0) {
-            *reinterpret_cast<float4*>(orow + r0) = make_float4(acc[rb][4 * g] * inv, acc[rb][4 * g + 1] * inv,
-                                                                acc[rb][4 * g + 2] * inv, acc[rb][4 * g + 3] * inv);
+            *reinterpret_cast<float4*>(orow + r0) = make_float4(nrm(acc[rb][4 * g]), nrm(acc[rb][4 * g + 1]),
+                                                                nrm(acc[rb][4 * g + 2]), nrm(acc[rb][4 * g + 3]));
           } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              if (r0 + i < rank) orow[r0 + i] = acc[rb][4 * g + i] * inv;
+              if (r0 + i < rank) orow[r0 + i] = nrm(acc[rb][4 * g + i]);
             }
           }
         }
       }
     }
   }
+  if (MODE == 1) {
+    // lanes in order, then waves in order: the same fp64 sum on every run
+    for (int o = 1; o < 64; o <<= 1) wsum += __shfl_xor(wsum, o, 64);
+    if (lane == 0) red_l[wave] = wsum;
+    __syncthreads();
+    if (tid == 0) {
+      double t = 0.0;
+      for (int w = 0; w < RP_WAVES; ++w) t += red_l[w];
+      partial[b * gridDim.x + blockIdx.x] = t;
+    }
+  }
 }
 
 }  // namespace
+
+template <int MODE>
+static void launch_role_projection(dim3 grid, hipStream_t stream, const uint16_t* xp, const float* factor, int64_t n,
+                                   int32_t d, int32_t rank, float* out, double* partial, float* head_scale) {
+  const int rb = (rank + 31) / 32;
+#define SPR_RP(DD, RBB)                                                                                       \
+  role_projection_kernel<DD, RBB, MODE><<<grid, RP_THREADS, 0, stream>>>(xp, factor, n, rank, out, partial, \
+                                                                          head_scale)
+  if (d == 128) {
+    if (rb == 1) SPR_RP(128, 1); else if (rb == 2) SPR_RP(128, 2); else if (rb == 3) SPR_RP(128, 3); else SPR_RP(128, 4);
+  } else {
+    if (rb == 1) SPR_RP(64, 1); else if (rb == 2) SPR_RP(64, 2); else if (rb == 3) SPR_RP(64, 3); else SPR_RP(64, 4);
+  }
+#undef SPR_RP
+}
 
 extern "C" int spr_role_projection_rms(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d,
                                        int32_t rank, float* out, hipStream_t stream) {
@@ -154,15 +201,36 @@ extern "C" int spr_role_projection_rms(const void* x, const float* factor, int64
   SPR_REQUIRE(x && factor && out, "spr_role_projection_rms: null pointer");
   SPR_REQUIRE(bh <= 65535, "spr_role_projection_rms: too many heads");
   const dim3 grid(static_cast<uint32_t>((n + RP_TOKENS - 1) / RP_TOKENS), static_cast<uint32_t>(bh));
-  const uint16_t* xp = static_cast<const uint16_t*>(x);
-  const int rb = (rank + 31) / 32;
-#define SPR_RP(DD, RBB) role_projection_kernel<DD, RBB><<<grid, RP_THREADS, 0, stream>>>(xp, factor, n, rank, out)
-  if (d == 128) {
-    if (rb == 1) SPR_RP(128, 1); else if (rb == 2) SPR_RP(128, 2); else if (rb == 3) SPR_RP(128, 3); else SPR_RP(128, 4);
-  } else {
-    if (rb == 1) SPR_RP(64, 1); else if (rb == 2) SPR_RP(64, 2); else if (rb == 3) SPR_RP(64, 3); else SPR_RP(64, 4);
-  }
-#undef SPR_RP
+  launch_role_projection<0>(grid, stream, static_cast<const uint16_t*>(x), factor, n, d, rank, out, nullptr, nullptr);
   SPR_LAUNCHED("role_projection_kernel");
+  return SPR_OK;
+}
+
+extern "C" size_t spr_role_k_projection_workspace(int64_t bh, int64_t n) {
+  return static_cast<size_t>(bh) * static_cast<size_t>((n + RP_TOKENS - 1) / RP_TOKENS) * sizeof(double);
+}
+
+extern "C" int spr_role_k_projection(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d,
+                                     int32_t rank, float* out, float* key_scale, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0, "spr_role_k_projection: bad size");
+  SPR_REQUIRE(d == 64 || d == 128, "spr_role_k_projection: head dim must be 64 or 128 (got %d)", d);
+  SPR_REQUIRE(rank >= 1 && rank <= RP_MAX_R, "spr_role_k_projection: rank must be in [1, %d] (got %d)", RP_MAX_R,
+              rank);
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(n >= 1, "spr_role_k_projection: no tokens");
+  SPR_REQUIRE(x && factor && out && key_scale, "spr_role_k_projection: null pointer");
+  SPR_REQUIRE(bh <= 65535, "spr_role_k_projection: too many heads");
+  if (workspace == nullptr || workspace_bytes < spr_role_k_projection_workspace(bh, n)) {
+    spr_set_error("spr_role_k_projection: workspace of %zu bytes needed", spr_role_k_projection_workspace(bh, n));
+    return SPR_EWORKSPACE;
+  }
+  const dim3 grid(static_cast<uint32_t>((n + RP_TOKENS - 1) / RP_TOKENS), static_cast<uint32_t>(bh));
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  double* part = static_cast<double*>(workspace);
+  launch_role_projection<1>(grid, stream, xp, factor, n, d, rank, nullptr, part, nullptr);
+  SPR_LAUNCHED("role_projection_kernel<sum of squares>");
+  launch_role_projection<2>(grid, stream, xp, factor, n, d, rank, out, part, key_scale);
+  SPR_LAUNCHED("role_projection_kernel<head scale>");
   return SPR_OK;
 }

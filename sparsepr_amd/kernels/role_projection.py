@@ -57,3 +57,31 @@ def role_projection_rms_triton(
     _lib.call("spr_role_projection_rms", _lib.ptr(x), _lib.ptr(factor), bh, tokens, dim, rank, _lib.ptr(out),
               _lib.stream(dev))
     return out
+
+
+def role_k_projection_normalize(k: torch.Tensor, k_factor: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Project K through its factor and divide by the head's RMS over (tokens, rank).
+
+    The torch.compile'd ``_role_k_projection_normalize_fp32`` of n8_v6.py:141-149:
+    key = bmm(k, k_factor) (TF32 factor, as the reference's fp32 matmul under its TF32
+    contract), key_scale = sqrt(mean(key^2 over tokens and rank)).clamp_min(1e-8) per head,
+    returns (key / key_scale, key_scale [BH, 1, 1]).  Two launches of the projection kernel
+    (the first only sums p^2 per workgroup, deterministically, the second divides) so the
+    fp32 key is written once.  bf16 K with D in {64, 128}, rank <= 128."""
+    if k.ndim != 3 or k_factor.ndim != 3 or k_factor.shape[:2] != (k.shape[0], k.shape[2]):
+        raise RuntimeError(f"Expected K[BH,N,D], F[BH,D,R], got {tuple(k.shape)}, {tuple(k_factor.shape)}.")
+    if k.dtype != torch.bfloat16 or k.shape[2] not in (64, 128) or k_factor.shape[2] > 128:
+        raise RuntimeError(f"The HIP K projection takes bf16 K with D in {{64, 128}} and R <= 128 "
+                           f"(got {k.dtype}, D={k.shape[2]}, R={k_factor.shape[2]}).")
+    dev = _lib.require_gpu(k, k_factor, what="role K projection")
+    bh, n, d = k.shape
+    rank = int(k_factor.shape[2])
+    kc = k.contiguous()
+    f = k_factor.float().contiguous()
+    out = torch.empty((bh, n, rank), device=dev, dtype=torch.float32)
+    scale = torch.empty((bh, 1, 1), device=dev, dtype=torch.float32)
+    ws_bytes = int(_lib.query("spr_role_k_projection_workspace", bh, n))
+    ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
+    _lib.call("spr_role_k_projection", _lib.ptr(kc), _lib.ptr(f), bh, n, d, rank, _lib.ptr(out), _lib.ptr(scale),
+              _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+    return out, scale

@@ -684,3 +684,21 @@ def test_role_projection_rms_closed_form(oracle):
     rms = np.sqrt((got ** 2).mean(axis=2))
     assert np.abs(np.delete(rms.reshape(-1), 1 * 9 + 3) - 1.0).max() < 1e-6
     assert not np.allclose(oracle.role_projection_rms(x, f), oracle.role_projection_rms(x, f + 2 ** -14 * f), atol=0)
+
+
+def test_role_k_projection_head_scale(oracle):
+    rng = np.random.default_rng(8)
+    k = oracle.to_bf16(rng.standard_normal((3, 40, 64)).astype(np.float32))
+    f = rng.standard_normal((3, 64, 32)).astype(np.float32)
+    k[2] = 0.0  # an all-zero head: scale clamps at 1e-8 and the key stays 0
+    key, scale = oracle.role_k_projection_normalize(k, f)
+    ft = oracle.tf32_rna(f).astype(np.float64)
+    for b in range(2):
+        p = k[b].astype(np.float64) @ ft[b]
+        s = np.linalg.norm(p) / math.sqrt(p.size)  # Frobenius norm: another route to the RMS
+        assert abs(scale[b, 0, 0] - s) <= 1e-6 * s
+        assert np.abs(key[b] - p / s).max() < 1e-5
+    assert scale[2, 0, 0] == np.float32(1e-8) and not key[2].any()
+    # scaling K by c scales the key by 1 (the head RMS normalises it away) and the scale by c
+    key2, scale2 = oracle.role_k_projection_normalize(k * 4.0, f)
+    assert np.abs(key2[:2] - key[:2]).max() < 1e-6 and np.abs(scale2[:2] / scale[:2] - 4.0).max() < 1e-6
