@@ -191,8 +191,10 @@ class N8V6Core:
 
     def route(self, *args, **kwargs):
         raise NotImplementedError(
-            "The N8 role-space router (role metrics/factors and SVG-EAR scores) is not provided by "
-            "sparsepr_amd; use sparsepr_amd.layer.SparsePRAttention.route (top-p cluster routing)."
+            "The N8 role-space router is not provided by sparsepr_amd: its metric covariance/factor "
+            "step and route orchestration are not built (its SVG-EAR scores and role projections are: "
+            "sparsepr_amd.kernels.svg_ear, sparsepr_amd.kernels.role_projection); use "
+            "sparsepr_amd.layer.SparsePRAttention.route (top-p cluster routing)."
         )
 
     def repair(self, base_video, q_video, k_full, v_full, route: N8V6Route):
