@@ -3,9 +3,11 @@
 
 `N8V6Core.repair` runs entirely on the HIP kernels (probe selection, dense probe
 attention, fit preparation, apply, exact scatter) plus the small fp32 RRR fit
-on the GPU.  The N8 role-space router (`route`: role metrics and factors,
-SVG-EAR selector scores) is not part of this library; the top-p router of
-`sparsepr_amd.layer` produces an `N8V6Route` that `repair` consumes.
+on the GPU.  The N8 role-space router (`route`) is not part of this library:
+its SVG-EAR selector scores and role projections are (sparsepr_amd.kernels.svg_ear,
+sparsepr_amd.kernels.role_projection), its role-metric factors and orchestration
+are not.  The top-p router of `sparsepr_amd.layer` produces an `N8V6Route` that
+`repair` consumes.
 """
 
 from __future__ import annotations
