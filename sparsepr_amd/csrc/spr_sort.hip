@@ -124,6 +124,7 @@ __global__ __launch_bounds__(64) void label_scatter_kernel(const int32_t* __rest
                                                            int32_t* __restrict__ sorted_idx) {
   extern __shared__ int32_t cnt[];  // [k + 1]
   const int32_t bins = k + 1;
+  const int nbits = 32 - __builtin_clz(static_cast<uint32_t>(bins));  // 2^nbits > k + 1 > every bin
   const int64_t row = blockIdx.y;
   const int lane = threadIdx.x;
   const int32_t* b = bases + (row * nchunks + blockIdx.x) * bins;
@@ -146,15 +147,17 @@ __global__ __launch_bounds__(64) void label_scatter_kernel(const int32_t* __rest
     const int64_t t = g + lane;
     const bool live = t < c1;
     const int32_t bin = bins_of[i];
-    int rank = 0;
-    int count = 0;
-#pragma unroll 16
-    for (int j = 0; j < 64; ++j) {
-      const int32_t other = __builtin_amdgcn_readlane(bin, j);
-      const bool same = other == bin;
-      count += same ? 1 : 0;
-      rank += (same && j < lane) ? 1 : 0;
+    // lanes holding the same bin, one ballot per bin bit (nbits bits hold every bin and
+    // keep the pattern of -1, past the chunk, apart from all of them); the rank is the
+    // number of such lanes below this one, which keeps the sort stable
+    uint64_t same = ~0ull;
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool set = (bin >> bit) & 1;
+      const uint64_t m = __ballot(set);
+      same &= set ? m : ~m;
     }
+    const int rank = __popcll(same & ((1ull << lane) - 1ull));
+    const int count = __popcll(same);
     int32_t pos = 0;
     if (live) pos = cnt[bin] + rank;
     __builtin_amdgcn_wave_barrier();
