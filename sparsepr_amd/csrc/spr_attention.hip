@@ -115,6 +115,12 @@ __host__ __device__ inline int64_t plan_words(int32_t qn, int32_t kn) {
   return 3 * (int64_t)(qn + 1) + 2 * (int64_t)qn + 2 * (int64_t)qn * kn;
 }
 
+// After the bh_kv per-head plans: head_order[bh_kv], the kv head processed in each kv-head
+// slot of the 256-row tile grid (see attn_head_order_kernel).
+__host__ __device__ inline int32_t* head_order_at(int32_t* base, int64_t bh_kv, int32_t qn, int32_t kn) {
+  return base + bh_kv * plan_words(qn, kn);
+}
+
 __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn, int32_t kn) {
   int32_t* p = base + h * plan_words(qn, kn);
   PlanView v;
@@ -694,13 +700,15 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  // ---- work item: XCD-grouped order over 256-row tiles
+  // ---- work item: XCD-grouped order over 256-row tiles; head slot -> head through the
+  // plan's work-balanced head order
   const int64_t per_xcd = gridDim.x / 8;
   const int64_t logical = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  const int64_t bhq = logical / tiles_per_head;
-  const int32_t tile = static_cast<int32_t>(logical - bhq * tiles_per_head);
-  if (bhq >= bh_q) return;
-  const int64_t bhkv = bhq / group;
+  const int64_t slot = logical / tiles_per_head;
+  const int32_t tile = static_cast<int32_t>(logical - slot * tiles_per_head);
+  if (slot >= bh_q) return;
+  const int64_t bhkv = head_order_at(const_cast<int32_t*>(plan), bh_q / group, qn, kn)[slot / group];
+  const int64_t bhq = bhkv * group + slot % group;
   PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
   if (tile >= pv.tile2_off[qn]) return;
   int lo = 0, hi = qn;  // largest i with tile2_off[i] <= tile
@@ -1005,8 +1013,43 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 
 // ------------------------------------------------------------------------------ C ABI
 
+// Order of the kv heads over the tile grid of attn_pipe_kernel.  The hardware hands
+// workgroup i to XCD i % 8 and the kernel gives each XCD a contiguous run of heads
+// (bh_kv / 8 kv heads), so an XCD whose heads keep more key pairs finishes last.  The
+// work of a head is sum over q-clusters of 256-row tiles x 64-key chunks; heads are
+// ranked by it (ties by index) and dealt to the XCDs in snake order (0..7, 7..0, ...),
+// which evens the per-XCD sums.  Identity when bh_kv is not a multiple of 8 or above
+// HO_MAX heads.  One workgroup.
+constexpr int HO_MAX = 1024;
+__global__ __launch_bounds__(256) void attn_head_order_kernel(int32_t* __restrict__ plan, int32_t bh_kv, int32_t qn,
+                                                              int32_t kn) {
+  __shared__ int64_t work[HO_MAX];
+  int32_t* order = head_order_at(plan, bh_kv, qn, kn);
+  const int tid = threadIdx.x;
+  if (bh_kv % 8 != 0 || bh_kv > HO_MAX) {
+    for (int h = tid; h < bh_kv; h += blockDim.x) order[h] = h;
+    return;
+  }
+  for (int h = tid; h < bh_kv; h += blockDim.x) {
+    const PlanView pv = plan_at(plan, h, qn, kn);
+    int64_t w = 0;
+    for (int qc = 0; qc < qn; ++qc)
+      w += static_cast<int64_t>(pv.tile2_off[qc + 1] - pv.tile2_off[qc]) * ((pv.total[qc] + BN - 1) / BN);
+    work[h] = w;
+  }
+  __syncthreads();
+  const int hpx = bh_kv / 8;
+  for (int h = tid; h < bh_kv; h += blockDim.x) {
+    int rank = 0;
+    for (int o = 0; o < bh_kv; ++o) rank += (work[o] > work[h] || (work[o] == work[h] && o < h)) ? 1 : 0;
+    const int r = rank / 8, i = rank % 8;
+    const int x = (r & 1) ? 7 - i : i;
+    order[x * hpx + r] = h;
+  }
+}
+
 extern "C" size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn, int32_t kn) {
-  return static_cast<size_t>(bh_kv * plan_words(qn, kn) * 4);
+  return static_cast<size_t>((bh_kv * plan_words(qn, kn) + bh_kv) * 4);
 }
 
 // Plan for spr_block_sparse_attention_run: map uint8 [bh_kv, qn, kn], q_sizes
@@ -1029,6 +1072,8 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
   attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv), row_groups), THREADS, (kn + 1) * sizeof(int32_t), stream>>>(
       map, q_sizes, k_sizes, qn, kn, static_cast<int32_t>(s), static_cast<int32_t*>(plan));
   SPR_LAUNCHED("attn_plan_kernel");
+  attn_head_order_kernel<<<1, 256, 0, stream>>>(static_cast<int32_t*>(plan), static_cast<int32_t>(bh_kv), qn, kn);
+  SPR_LAUNCHED("attn_head_order_kernel");
   return SPR_OK;
 }
 
