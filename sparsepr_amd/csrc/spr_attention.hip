@@ -1016,14 +1016,15 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // Order of the kv heads over the tile grid of attn_pipe_kernel.  The hardware hands
 // workgroup i to XCD i % 8 and the kernel gives each XCD a contiguous run of heads
 // (bh_kv / 8 kv heads), so an XCD whose heads keep more key pairs finishes last.  The
-// work of a head is sum over q-clusters of 256-row tiles x 64-key chunks; heads are
-// ranked by it (ties by index) and dealt to the XCDs in snake order (0..7, 7..0, ...),
-// which evens the per-XCD sums.  Identity when bh_kv is not a multiple of 8 or above
-// HO_MAX heads.  One workgroup.
+// work of a head is sum over q-clusters of 256-row tiles x 64-key chunks; in descending
+// order of work (ties by index) each head goes to the XCD with the least work so far
+// among those with a free slot (longest-processing-time first, bh_kv / 8 heads each).
+// Identity when bh_kv is not a multiple of 8 or above HO_MAX heads.  One workgroup.
 constexpr int HO_MAX = 1024;
 __global__ __launch_bounds__(256) void attn_head_order_kernel(int32_t* __restrict__ plan, int32_t bh_kv, int32_t qn,
                                                               int32_t kn) {
   __shared__ int64_t work[HO_MAX];
+  __shared__ int16_t by_rank[HO_MAX];
   int32_t* order = head_order_at(plan, bh_kv, qn, kn);
   const int tid = threadIdx.x;
   if (bh_kv % 8 != 0 || bh_kv > HO_MAX) {
@@ -1038,13 +1039,26 @@ __global__ __launch_bounds__(256) void attn_head_order_kernel(int32_t* __restric
     work[h] = w;
   }
   __syncthreads();
-  const int hpx = bh_kv / 8;
   for (int h = tid; h < bh_kv; h += blockDim.x) {
     int rank = 0;
     for (int o = 0; o < bh_kv; ++o) rank += (work[o] > work[h] || (work[o] == work[h] && o < h)) ? 1 : 0;
-    const int r = rank / 8, i = rank % 8;
-    const int x = (r & 1) ? 7 - i : i;
-    order[x * hpx + r] = h;
+    by_rank[rank] = static_cast<int16_t>(h);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const int hpx = bh_kv / 8;
+    int64_t load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int used[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int rank = 0; rank < bh_kv; ++rank) {
+      const int h = by_rank[rank];
+      int best = -1;
+      for (int x = 0; x < 8; ++x) {
+        if (used[x] < hpx && (best < 0 || load[x] < load[best])) best = x;
+      }
+      order[best * hpx + used[best]] = h;
+      ++used[best];
+      load[best] += work[h];
+    }
   }
 }
 
