@@ -1031,12 +1031,15 @@ __global__ __launch_bounds__(256) void attn_head_order_kernel(int32_t* __restric
     for (int h = tid; h < bh_kv; h += blockDim.x) order[h] = h;
     return;
   }
-  for (int h = tid; h < bh_kv; h += blockDim.x) {
+  for (int h = tid; h < bh_kv; h += blockDim.x) work[h] = 0;
+  __syncthreads();
+  // (head, q-cluster) terms spread over the workgroup, summed with LDS atomics (integers:
+  // the order does not matter)
+  for (int64_t i = tid; i < static_cast<int64_t>(bh_kv) * qn; i += blockDim.x) {
+    const int h = static_cast<int>(i / qn), qc = static_cast<int>(i % qn);
     const PlanView pv = plan_at(plan, h, qn, kn);
-    int64_t w = 0;
-    for (int qc = 0; qc < qn; ++qc)
-      w += static_cast<int64_t>(pv.tile2_off[qc + 1] - pv.tile2_off[qc]) * ((pv.total[qc] + BN - 1) / BN);
-    work[h] = w;
+    const int64_t w = static_cast<int64_t>(pv.tile2_off[qc + 1] - pv.tile2_off[qc]) * ((pv.total[qc] + BN - 1) / BN);
+    if (w != 0) atomicAdd(reinterpret_cast<unsigned long long*>(&work[h]), static_cast<unsigned long long>(w));
   }
   __syncthreads();
   for (int h = tid; h < bh_kv; h += blockDim.x) {
