@@ -109,10 +109,14 @@ struct PlanView {
   int32_t* nseg;       // [Qc]
   int32_t* total;     // [Qc]
   Seg* segs;          // [Qc][Kc]
+  int32_t* qc_by_len;     // [Qc] q-clusters by decreasing key count (ties by index)
+  int32_t* tile2_sorted;  // [Qc + 1] first 2*BM-row tile of each in that order
 };
 
 __host__ __device__ inline int64_t plan_words(int32_t qn, int32_t kn) {
-  return 3 * (int64_t)(qn + 1) + 2 * (int64_t)qn + 2 * (int64_t)qn * kn;
+  // (+ 2 qn + 2: qc_by_len, tile2_sorted and one pad word, keeping every head's segment
+  // list 8-byte aligned)
+  return 3 * (int64_t)(qn + 1) + 2 * (int64_t)qn + 2 * (int64_t)qn * kn + 2 * (int64_t)qn + 2;
 }
 
 // After the bh_kv per-head plans: head_order[bh_kv], the kv head processed in each kv-head
@@ -130,6 +134,8 @@ __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn
   v.nseg = p + 3 * (qn + 1);
   v.total = v.nseg + qn;
   v.segs = reinterpret_cast<Seg*>(v.total + qn);
+  v.qc_by_len = v.total + qn + 2 * (int64_t)qn * kn;
+  v.tile2_sorted = v.qc_by_len + qn;
   return v;
 }
 
@@ -710,14 +716,15 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int64_t bhkv = head_order_at(const_cast<int32_t*>(plan), bh_q / group, qn, kn)[slot / group];
   const int64_t bhq = bhkv * group + slot % group;
   PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
-  if (tile >= pv.tile2_off[qn]) return;
-  int lo = 0, hi = qn;  // largest i with tile2_off[i] <= tile
+  // tiles of a head in decreasing q-cluster key count (the plan's tile2_sorted order)
+  if (tile >= pv.tile2_sorted[qn]) return;
+  int lo = 0, hi = qn;  // largest i with tile2_sorted[i] <= tile
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
-    if (pv.tile2_off[mid] <= tile) lo = mid; else hi = mid;
+    if (pv.tile2_sorted[mid] <= tile) lo = mid; else hi = mid;
   }
-  const int qc = lo;
-  const int32_t row0 = pv.q_off[qc] + (tile - pv.tile2_off[qc]) * TBM;
+  const int qc = pv.qc_by_len[lo];
+  const int32_t row0 = pv.q_off[qc] + (tile - pv.tile2_sorted[lo]) * TBM;
   const int32_t row1 = min(row0 + TBM, pv.q_off[qc + 1]);
   const bool wave_live = row0 + 32 * wave < row1;
   const Seg* segs = pv.segs + static_cast<int64_t>(qc) * kn;
@@ -1027,6 +1034,30 @@ __global__ __launch_bounds__(256) void attn_head_order_kernel(int32_t* __restric
   __shared__ int16_t by_rank[HO_MAX];
   int32_t* order = head_order_at(plan, bh_kv, qn, kn);
   const int tid = threadIdx.x;
+  // inside each head, the q-clusters by decreasing key count, so that every XCD ends on
+  // its shortest tiles, and the tile offsets in that order
+  for (int64_t i = tid; i < static_cast<int64_t>(bh_kv) * qn; i += blockDim.x) {
+    const int h = static_cast<int>(i / qn), qc = static_cast<int>(i % qn);
+    const PlanView pv = plan_at(plan, h, qn, kn);
+    const int32_t t = pv.total[qc];
+    int rank = 0;
+    for (int o = 0; o < qn; ++o) {
+      const int32_t u = pv.total[o];
+      rank += (u > t || (u == t && o < qc)) ? 1 : 0;
+    }
+    pv.qc_by_len[rank] = qc;
+  }
+  __syncthreads();
+  for (int h = tid; h < bh_kv; h += blockDim.x) {
+    const PlanView pv = plan_at(plan, h, qn, kn);
+    int32_t run = 0;
+    for (int r = 0; r < qn; ++r) {
+      pv.tile2_sorted[r] = run;
+      const int qc = pv.qc_by_len[r];
+      run += pv.tile2_off[qc + 1] - pv.tile2_off[qc];
+    }
+    pv.tile2_sorted[qn] = run;
+  }
   if (bh_kv % 8 != 0 || bh_kv > HO_MAX) {
     for (int h = tid; h < bh_kv; h += blockDim.x) order[h] = h;
     return;
