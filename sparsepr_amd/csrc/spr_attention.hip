@@ -1028,36 +1028,46 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // among those with a free slot (longest-processing-time first, bh_kv / 8 heads each).
 // Identity when bh_kv is not a multiple of 8 or above HO_MAX heads.  One workgroup.
 constexpr int HO_MAX = 1024;
+constexpr int TO_MAX_QN = 4096;  // q-clusters per head the tile order handles in LDS
+
+// Inside each head, the q-clusters by decreasing key count (ties by index), so that every
+// XCD ends on its shortest tiles, and the first tile of each in that order.  One
+// workgroup per kv head; key counts, tile counts and the order staged in LDS.
+__global__ __launch_bounds__(256) void attn_tile_order_kernel(int32_t* __restrict__ plan, int32_t qn, int32_t kn) {
+  extern __shared__ int32_t to_lds[];  // total[qn], tiles[qn], by_len[qn]
+  int32_t* tl = to_lds;
+  int32_t* tc = to_lds + qn;
+  int32_t* by_len = to_lds + 2 * qn;
+  const PlanView pv = plan_at(plan, blockIdx.x, qn, kn);
+  const int tid = threadIdx.x;
+  for (int qc = tid; qc < qn; qc += blockDim.x) {
+    tl[qc] = pv.total[qc];
+    tc[qc] = pv.tile2_off[qc + 1] - pv.tile2_off[qc];
+  }
+  __syncthreads();
+  for (int qc = tid; qc < qn; qc += blockDim.x) {
+    const int32_t t = tl[qc];
+    int rank = 0;
+    for (int o = 0; o < qn; ++o) rank += (tl[o] > t || (tl[o] == t && o < qc)) ? 1 : 0;
+    by_len[rank] = qc;
+    pv.qc_by_len[rank] = qc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t run = 0;
+    for (int r = 0; r < qn; ++r) {
+      pv.tile2_sorted[r] = run;
+      run += tc[by_len[r]];
+    }
+    pv.tile2_sorted[qn] = run;
+  }
+}
 __global__ __launch_bounds__(256) void attn_head_order_kernel(int32_t* __restrict__ plan, int32_t bh_kv, int32_t qn,
                                                               int32_t kn) {
   __shared__ int64_t work[HO_MAX];
   __shared__ int16_t by_rank[HO_MAX];
   int32_t* order = head_order_at(plan, bh_kv, qn, kn);
   const int tid = threadIdx.x;
-  // inside each head, the q-clusters by decreasing key count, so that every XCD ends on
-  // its shortest tiles, and the tile offsets in that order
-  for (int64_t i = tid; i < static_cast<int64_t>(bh_kv) * qn; i += blockDim.x) {
-    const int h = static_cast<int>(i / qn), qc = static_cast<int>(i % qn);
-    const PlanView pv = plan_at(plan, h, qn, kn);
-    const int32_t t = pv.total[qc];
-    int rank = 0;
-    for (int o = 0; o < qn; ++o) {
-      const int32_t u = pv.total[o];
-      rank += (u > t || (u == t && o < qc)) ? 1 : 0;
-    }
-    pv.qc_by_len[rank] = qc;
-  }
-  __syncthreads();
-  for (int h = tid; h < bh_kv; h += blockDim.x) {
-    const PlanView pv = plan_at(plan, h, qn, kn);
-    int32_t run = 0;
-    for (int r = 0; r < qn; ++r) {
-      pv.tile2_sorted[r] = run;
-      const int qc = pv.qc_by_len[r];
-      run += pv.tile2_off[qc + 1] - pv.tile2_off[qc];
-    }
-    pv.tile2_sorted[qn] = run;
-  }
   if (bh_kv % 8 != 0 || bh_kv > HO_MAX) {
     for (int h = tid; h < bh_kv; h += blockDim.x) order[h] = h;
     return;
@@ -1107,6 +1117,7 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
                                                size_t plan_bytes, hipStream_t stream) {
   SPR_REQUIRE(bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_plan: bad size");
   SPR_REQUIRE(kn <= 16384, "spr_block_sparse_attention_plan: kn exceeds 16384");
+  SPR_REQUIRE(qn <= TO_MAX_QN, "spr_block_sparse_attention_plan: qn exceeds %d", TO_MAX_QN);
   SPR_REQUIRE(s < (int64_t(1) << 31), "spr_block_sparse_attention_plan: sequence too long");
   SPR_REQUIRE(bh_kv <= 65535, "spr_block_sparse_attention_plan: bh_kv exceeds 65535");
   SPR_REQUIRE(map && q_sizes && k_sizes && plan, "spr_block_sparse_attention_plan: null pointer");
@@ -1120,6 +1131,9 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
   attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv), row_groups), THREADS, (kn + 1) * sizeof(int32_t), stream>>>(
       map, q_sizes, k_sizes, qn, kn, static_cast<int32_t>(s), static_cast<int32_t*>(plan));
   SPR_LAUNCHED("attn_plan_kernel");
+  attn_tile_order_kernel<<<dim3(static_cast<uint32_t>(bh_kv)), 256, 3 * qn * sizeof(int32_t), stream>>>(
+      static_cast<int32_t*>(plan), qn, kn);
+  SPR_LAUNCHED("attn_tile_order_kernel");
   attn_head_order_kernel<<<1, 256, 0, stream>>>(static_cast<int32_t*>(plan), static_cast<int32_t>(bh_kv), qn, kn);
   SPR_LAUNCHED("attn_head_order_kernel");
   return SPR_OK;
