@@ -130,9 +130,11 @@ int spr_density(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_siz
  * kmeans_utils.py:2164-2350 dynamic_block_sparse_fwd_flashinfer (FlashInfer
  * VariableBlockSparseAttentionWrapper.plan / .run), semantics of
  * dynamic_block_sparse_fwd_torch kmeans_utils.py:1748-1841.
- * Plan: per kv head, cluster offsets, 128-row query tiles and, per q-cluster, the kept
- * non-empty key ranges.  map uint8 [bh_kv, qn, kn], q_sizes int32 [bh_kv, qn],
- * k_sizes int32 [bh_kv, kn]; sizes are clamped to the s rows. */
+ * Plan: per kv head, cluster offsets, 128- and 256-row query tiles and, per q-cluster,
+ * the kept non-empty key ranges; the 256-row tiles of a head in decreasing q-cluster key
+ * count; after the heads, the order in which the kv heads fill the tile grid (balanced
+ * over the 8 XCDs by work).  map uint8 [bh_kv, qn, kn], q_sizes int32 [bh_kv, qn],
+ * k_sizes int32 [bh_kv, kn]; sizes are clamped to the s rows; qn <= 4096, kn <= 16384. */
 size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn, int32_t kn);
 int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_kv,
                                     int64_t s, int32_t qn, int32_t kn, void* plan, size_t plan_bytes,
