@@ -134,7 +134,10 @@ int spr_density(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_siz
  * the kept non-empty key ranges; the 256-row tiles of a head in decreasing q-cluster key
  * count; after the heads, the order in which the kv heads fill the tile grid (balanced
  * over the 8 XCDs by work).  map uint8 [bh_kv, qn, kn], q_sizes int32 [bh_kv, qn],
- * k_sizes int32 [bh_kv, kn]; sizes are clamped to the s rows; qn <= 4096, kn <= 16384. */
+ * k_sizes int32 [bh_kv, kn]; sizes are clamped to the s rows; qn <= 4096, kn <= 16384.
+ * The plan ends with a header (bh_kv, qn, kn, s) written after the rest of the plan; the
+ * run checks plan_bytes on the host, and its kernels compare the header with their own
+ * sizes and leave `out` unwritten when it does not match (a plan built for other sizes). */
 size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn, int32_t kn);
 int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_kv,
                                     int64_t s, int32_t qn, int32_t kn, void* plan, size_t plan_bytes,
@@ -149,9 +152,9 @@ int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, 
  * (hunyuanvideo.py:189-231) into the attention.  k_index int32 [bh_kv, s] (nullable): k and v stay
  * in token order and cluster-sorted key position p is token k_index[p] (the K/V permutation of
  * n8_v6.py:905-925 fused into the key gather). */
-int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan, int64_t bh_q,
-                                   int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
-                                   const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
+int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan, size_t plan_bytes,
+                                   int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn,
+                                   float scale, const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
                                    hipStream_t stream);
 /* Plan + run in one call; workspace = plan buffer of spr_block_sparse_attention_workspace bytes. */
 int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,

@@ -23,12 +23,14 @@
 #include <string.h>
 #include <float.h>
 
-/* e^x in fp32.  x <= -87 returns 0 (keeps every nonzero result normal, so
- * the final scaling by 2^n is exact); x >= 88.5 returns +inf. */
+/* e^x in fp32.  x < -87 returns 0 (keeps every nonzero result normal, so
+ * the final scaling by 2^n is exact); x > 89 returns +inf.  The scaling is
+ * applied as 2^(n - n/2) * 2^(n/2) so that n = 128 (x up to ln(FLT_MAX))
+ * stays finite. */
 float spr_oracle_expf(float x) {
   if (x != x) return x;
   if (x < -87.0f) return 0.0f;
-  if (x > 88.5f) return INFINITY;
+  if (x > 89.0f) return INFINITY;
   const float log2e = 1.44269504088896341f;
   const float ln2_hi = 0.693145751953125f;        /* 12 significant bits: n*ln2_hi exact */
   const float ln2_lo = 1.428606765330187045e-06f; /* ln2 - ln2_hi */
@@ -45,10 +47,12 @@ float spr_oracle_expf(float x) {
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
   int ni = (int)n;
-  uint32_t bits = (uint32_t)(ni + 127) << 23;
-  float scale;
-  memcpy(&scale, &bits, sizeof(scale));
-  return p * scale;
+  int nb = ni >> 1, na = ni - nb;
+  uint32_t bits_a = (uint32_t)(na + 127) << 23, bits_b = (uint32_t)(nb + 127) << 23;
+  float sa, sb;
+  memcpy(&sa, &bits_a, sizeof(sa));
+  memcpy(&sb, &bits_b, sizeof(sb));
+  return (p * sa) * sb;
 }
 
 void spr_oracle_expf_array(const float* x, float* y, int64_t n) {

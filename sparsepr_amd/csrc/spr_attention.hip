@@ -113,16 +113,34 @@ struct PlanView {
   int32_t* tile2_sorted;  // [Qc + 1] first 2*BM-row tile of each in that order
 };
 
+// Word offset of a head's segment list, rounded up to even so that (with an even
+// plan_words) every head's Seg array is 8-byte aligned.
+__host__ __device__ inline int64_t plan_seg_offset(int32_t qn) { return (5 * (int64_t)qn + 3 + 1) & ~int64_t(1); }
+
 __host__ __device__ inline int64_t plan_words(int32_t qn, int32_t kn) {
-  // (+ 2 qn + 2: qc_by_len, tile2_sorted and one pad word, keeping every head's segment
-  // list 8-byte aligned)
-  return 3 * (int64_t)(qn + 1) + 2 * (int64_t)qn + 2 * (int64_t)qn * kn + 2 * (int64_t)qn + 2;
+  // q_off, tile_off, tile2_off [qn + 1] each, nseg, total [qn] each, (pad), segs [qn][kn]
+  // pairs, qc_by_len [qn], tile2_sorted [qn + 1], then a pad word: an even count
+  return plan_seg_offset(qn) + 2 * (int64_t)qn * kn + 2 * (int64_t)qn + 2;
 }
 
 // After the bh_kv per-head plans: head_order[bh_kv], the kv head processed in each kv-head
-// slot of the 256-row tile grid (see attn_head_order_kernel).
+// slot of the 256-row tile grid (see attn_head_order_kernel), then the plan header.
 __host__ __device__ inline int32_t* head_order_at(int32_t* base, int64_t bh_kv, int32_t qn, int32_t kn) {
   return base + bh_kv * plan_words(qn, kn);
+}
+
+// Plan header (5 words after head_order): magic, bh_kv, qn, kn, s.  The plan kernels
+// write it last; the attention kernels compare it with their own arguments and do
+// nothing when it does not match, so a plan built for other sizes (or never built)
+// cannot send them past the ends of the plan, Q or K/V.
+constexpr int32_t PLAN_MAGIC = 0x50525053;  // "SPRP"
+constexpr int PLAN_HEADER_WORDS = 5;
+__host__ __device__ inline const int32_t* plan_header_at(const int32_t* base, int64_t bh_kv, int32_t qn, int32_t kn) {
+  return base + bh_kv * plan_words(qn, kn) + bh_kv;
+}
+__device__ inline bool plan_matches(const int32_t* base, int64_t bh_kv, int32_t qn, int32_t kn, int32_t s) {
+  const int32_t* hd = plan_header_at(base, bh_kv, qn, kn);
+  return hd[0] == PLAN_MAGIC && hd[1] == static_cast<int32_t>(bh_kv) && hd[2] == qn && hd[3] == kn && hd[4] == s;
 }
 
 __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn, int32_t kn) {
@@ -133,8 +151,8 @@ __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn
   v.tile2_off = p + 2 * (qn + 1);
   v.nseg = p + 3 * (qn + 1);
   v.total = v.nseg + qn;
-  v.segs = reinterpret_cast<Seg*>(v.total + qn);
-  v.qc_by_len = v.total + qn + 2 * (int64_t)qn * kn;
+  v.segs = reinterpret_cast<Seg*>(p + plan_seg_offset(qn));
+  v.qc_by_len = p + plan_seg_offset(qn) + 2 * (int64_t)qn * kn;
   v.tile2_sorted = v.qc_by_len + qn;
   return v;
 }
@@ -279,6 +297,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     bhq = logical / tiles_per_head;
     const int32_t t = static_cast<int32_t>(logical - bhq * tiles_per_head);
     if (bhq >= bh_q) return;
+    if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) return;
     PlanView pv = plan_at(const_cast<int32_t*>(plan), bhq / group, qn, kn);
     if (t >= pv.tile_off[qn]) return;
     int lo = 0, hi = qn;  // largest i with tile_off[i] <= t
@@ -713,6 +732,7 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int64_t slot = logical / tiles_per_head;
   const int32_t tile = static_cast<int32_t>(logical - slot * tiles_per_head);
   if (slot >= bh_q) return;
+  if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) return;
   const int64_t bhkv = head_order_at(const_cast<int32_t*>(plan), bh_q / group, qn, kn)[slot / group];
   const int64_t bhq = bhkv * group + slot % group;
   PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);
@@ -1106,8 +1126,22 @@ __global__ __launch_bounds__(256) void attn_head_order_kernel(int32_t* __restric
   }
 }
 
+// Written after the rest of the plan (stream order), so a run that sees a matching
+// header sees the finished plan.
+__global__ void attn_plan_header_kernel(int32_t* __restrict__ plan, int32_t bh_kv, int32_t qn, int32_t kn,
+                                        int32_t s) {
+  int32_t* hd = head_order_at(plan, bh_kv, qn, kn) + bh_kv;
+  if (threadIdx.x == 0) {
+    hd[0] = PLAN_MAGIC;
+    hd[1] = bh_kv;
+    hd[2] = qn;
+    hd[3] = kn;
+    hd[4] = s;
+  }
+}
+
 extern "C" size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn, int32_t kn) {
-  return static_cast<size_t>((bh_kv * plan_words(qn, kn) + bh_kv) * 4);
+  return static_cast<size_t>((bh_kv * plan_words(qn, kn) + bh_kv + PLAN_HEADER_WORDS) * 4);
 }
 
 // Plan for spr_block_sparse_attention_run: map uint8 [bh_kv, qn, kn], q_sizes
@@ -1128,7 +1162,20 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
   }
   // one wave per q-cluster row: the rows of a head spread over several workgroups
   const uint32_t row_groups = static_cast<uint32_t>(spr::ceil_div(qn, THREADS / 64));
-  attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv), row_groups), THREADS, (kn + 1) * sizeof(int32_t), stream>>>(
+  const size_t koff_bytes = (kn + 1) * sizeof(int32_t);  // up to 65540 bytes at kn = 16384
+  if (koff_bytes > 65536) {
+    static bool raised = false;  // the attribute is per kernel, per process
+    if (!raised) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_plan_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 16384 * 4 + 4);
+      if (e != hipSuccess) {
+        spr_set_error("spr_block_sparse_attention_plan: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+        return SPR_ELAUNCH;
+      }
+      raised = true;
+    }
+  }
+  attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv), row_groups), THREADS, koff_bytes, stream>>>(
       map, q_sizes, k_sizes, qn, kn, static_cast<int32_t>(s), static_cast<int32_t*>(plan));
   SPR_LAUNCHED("attn_plan_kernel");
   attn_tile_order_kernel<<<dim3(static_cast<uint32_t>(bh_kv)), 256, 3 * qn * sizeof(int32_t), stream>>>(
@@ -1136,6 +1183,9 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
   SPR_LAUNCHED("attn_tile_order_kernel");
   attn_head_order_kernel<<<1, 256, 0, stream>>>(static_cast<int32_t*>(plan), static_cast<int32_t>(bh_kv), qn, kn);
   SPR_LAUNCHED("attn_head_order_kernel");
+  attn_plan_header_kernel<<<1, 64, 0, stream>>>(static_cast<int32_t*>(plan), static_cast<int32_t>(bh_kv), qn, kn,
+                                                static_cast<int32_t>(s));
+  SPR_LAUNCHED("attn_plan_header_kernel");
   return SPR_OK;
 }
 
@@ -1148,8 +1198,8 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
 // in token order and cluster-sorted key position p is token k_index[p] (the K/V
 // permutation fused into the key gather).
 extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan,
-                                              int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d, int32_t qn,
-                                              int32_t kn, float scale, const int32_t* q_index,
+                                              size_t plan_bytes, int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d,
+                                              int32_t qn, int32_t kn, float scale, const int32_t* q_index,
                                               const int32_t* k_index, void* out, float* lse, hipStream_t stream) {
   SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_run: bad size");
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_block_sparse_attention_run: bh_q=%lld not a multiple of bh_kv=%lld",
@@ -1159,6 +1209,15 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   SPR_REQUIRE(bh_q <= 65535, "spr_block_sparse_attention_run: bh_q exceeds 65535");
   if (bh_q == 0 || s == 0) return SPR_OK;
   SPR_REQUIRE(q && k && v && plan && out, "spr_block_sparse_attention_run: null pointer");
+  SPR_REQUIRE(kn <= 16384 && qn <= TO_MAX_QN && bh_kv <= 65535, "spr_block_sparse_attention_run: bad plan size");
+  {
+    const size_t need = spr_block_sparse_attention_workspace(bh_kv, qn, kn);
+    if (plan_bytes < need) {
+      spr_set_error("spr_block_sparse_attention_run: plan buffer %zu < %zu bytes for bh_kv=%lld qn=%d kn=%d",
+                    plan_bytes, need, (long long)bh_kv, qn, kn);
+      return SPR_EWORKSPACE;
+    }
+  }
   SPR_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
               "spr_block_sparse_attention_run: q/k/v/out must be 16-byte aligned");
@@ -1217,8 +1276,8 @@ extern "C" int spr_block_sparse_attention(const void* q, const void* k, const vo
   int st = spr_block_sparse_attention_plan(map, q_sizes, k_sizes, bh_kv, s, qn, kn, workspace, workspace_bytes,
                                            stream);
   if (st != SPR_OK) return st;
-  return spr_block_sparse_attention_run(q, k, v, workspace, bh_q, bh_kv, s, d, qn, kn, scale, q_index, k_index,
-                                        out, lse, stream);
+  return spr_block_sparse_attention_run(q, k, v, workspace, workspace_bytes, bh_q, bh_kv, s, d, qn, kn, scale,
+                                        q_index, k_index, out, lse, stream);
 }
 
 extern "C" size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t d, int32_t nsplit) {
@@ -1275,3 +1334,4 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
   SPR_LAUNCHED("attn_combine_kernel");
   return SPR_OK;
 }
+

@@ -85,11 +85,14 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
 // e^x in fp32 with a fixed evaluation order, used where results must be
 // reproducible bit for bit on the CPU (top-p block selection).  Cody-Waite
 // range reduction with a two-part ln2, degree-7 Taylor polynomial (Horner,
-// fused multiply-adds), exact scaling by 2^n.  x < -87 -> 0, x > 88.5 -> inf.
+// fused multiply-adds), exact scaling by 2^n applied as 2^(n - n/2) * 2^(n/2) so
+// that n = 128 (x up to ln(FLT_MAX) ~ 88.72) stays finite.  x < -87 -> 0 (every
+// nonzero result is normal, so the scaling never rounds); x > 89 -> inf, and
+// x in (ln(FLT_MAX), 89] overflows to inf in the scaling.
 __device__ __forceinline__ float canonical_expf(float x) {
   if (x != x) return x;
   if (x < -87.0f) return 0.0f;
-  if (x > 88.5f) return __builtin_huge_valf();
+  if (x > 89.0f) return __builtin_huge_valf();
   const float log2e = 1.44269504088896341f;
   const float ln2_hi = 0.693145751953125f;
   const float ln2_lo = 1.428606765330187045e-06f;
@@ -104,9 +107,11 @@ __device__ __forceinline__ float canonical_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int ni = static_cast<int>(n);
-  float scale = __uint_as_float(static_cast<uint32_t>(ni + 127) << 23);
-  return p * scale;  // power-of-two scaling (rounds only for a subnormal result)
+  const int ni = static_cast<int>(n);
+  const int nb = ni >> 1, na = ni - nb;  // both in [-63, 64]
+  const float sa = __uint_as_float(static_cast<uint32_t>(na + 127) << 23);
+  const float sb = __uint_as_float(static_cast<uint32_t>(nb + 127) << 23);
+  return (p * sa) * sb;  // exact power-of-two scaling
 }
 
 // ---------------------------------------------------------------- misc

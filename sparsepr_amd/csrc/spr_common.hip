@@ -15,4 +15,4 @@ void spr_set_error(const char* fmt, ...) {
 
 extern "C" const char* spr_last_error(void) { return g_last_error; }
 
-extern "C" int spr_abi_version(void) { return 1; }
+extern "C" int spr_abi_version(void) { return 2; }

@@ -55,6 +55,10 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
     _, qn, kn = block_mask_map.shape
     if plan is None:
         plan = plan_block_sparse(block_mask_map.to(dev), block_row_sz, block_col_sz, s)
+    need = int(_lib.query("spr_block_sparse_attention_workspace", bh_kv, qn, kn))
+    if plan.numel() < need or plan.device != dev:
+        raise RuntimeError(f"block-sparse attention: the plan ({plan.numel()} bytes on {plan.device}) was not built "
+                           f"for bh_kv={bh_kv}, qn={qn}, kn={kn} ({need} bytes on {dev})")
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
     qi = None
     if q_index is not None:
@@ -69,8 +73,9 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
     out = torch.empty_like(qc)
     lse = torch.empty((bh_q, s), dtype=torch.float32, device=dev) if return_lse else None
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(d)
-    _lib.call("spr_block_sparse_attention_run", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(plan), bh_q,
-              bh_kv, s, d, qn, kn, sc, _lib.ptr(qi), _lib.ptr(ki), _lib.ptr(out), _lib.ptr(lse), _lib.stream(dev))
+    _lib.call("spr_block_sparse_attention_run", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(plan),
+              plan.numel(), bh_q, bh_kv, s, d, qn, kn, sc, _lib.ptr(qi), _lib.ptr(ki), _lib.ptr(out), _lib.ptr(lse),
+              _lib.stream(dev))
     return (out, lse) if return_lse else out
 
 

@@ -12,7 +12,6 @@ are not.  The top-p router of `sparsepr_amd.layer` produces an `N8V6Route` that
 
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass
 
 import torch
@@ -28,31 +27,6 @@ from .residual_repair import (
     recover_nonfinite_rrr_state,
     select_probes,
 )
-
-
-def _svg_top_p_key_budgets(q_centroids, k_centroids, k_cluster_sizes, top_p):
-    """SVG2 adaptive key-token budgets per query cluster (reference n8_v6.py:181-230)."""
-    if q_centroids.ndim != 3 or k_centroids.ndim != 3:
-        raise ValueError("TopP budget centroids must be [BH,C,D].")
-    if q_centroids.shape[0] != k_centroids.shape[0]:
-        raise ValueError("TopP Q/K centroids must have the same head count.")
-    if q_centroids.shape[2] != k_centroids.shape[2]:
-        raise ValueError("TopP Q/K centroids must have the same head dimension.")
-    if tuple(k_cluster_sizes.shape) != tuple(k_centroids.shape[:2]):
-        raise ValueError("TopP K-cluster sizes must match K centroids.")
-    if not 0.0 < float(top_p) <= 1.0:
-        raise ValueError(f"svg_ear_top_p must be in (0,1], got {top_p}.")
-    dim = int(q_centroids.shape[2])
-    logits = torch.bmm(q_centroids.float(), k_centroids.float().transpose(1, 2)) / math.sqrt(dim)
-    weights = k_cluster_sizes.float().unsqueeze(1)
-    logits = logits - logits.amax(dim=2, keepdim=True)
-    weighted_exp = logits.exp() * weights
-    probabilities = weighted_exp / weighted_exp.sum(dim=2, keepdim=True).clamp_min(1.0e-12)
-    sorted_probabilities, order = torch.sort(probabilities, dim=2, descending=True)
-    keep = sorted_probabilities.cumsum(dim=2) <= float(top_p)
-    keep = torch.nn.functional.pad(keep[:, :, :-1], (1, 0), value=True)
-    sorted_sizes = torch.gather(k_cluster_sizes.long().unsqueeze(1).expand(-1, q_centroids.shape[1], -1), 2, order)
-    return (sorted_sizes * keep.long()).sum(dim=2)
 
 
 def _effective_density(base_density, count: int, tokens: int):
@@ -128,6 +102,13 @@ class N8V6Config:
             raise ValueError("repair_norm_cap must be non-negative.")
         if self.repair_features not in {"output", "output_role"}:
             raise ValueError(f"repair_features must be output or output_role; got {self.repair_features!r}.")
+        if self.repair_features == "output_role":
+            # residual_repair.py:388-475,737-797 (role features appended to the fit's
+            # features) has no HIP kernels here; refuse it instead of running the
+            # output-only repair under the other name.
+            raise NotImplementedError(
+                "repair_features='output_role' is not supported by the MI355X build: the role-feature fit "
+                "preparation and apply kernels are not built; use repair_features='output'.")
         if self.repair_basis_source not in {"raw_residual", "fitted_residual"}:
             raise ValueError(f"repair_basis_source must be raw_residual or fitted_residual; got "
                              f"{self.repair_basis_source!r}.")
@@ -207,6 +188,9 @@ class N8V6Core:
         batch, heads, tokens, dim = base_video.shape
         bh = batch * heads
         cfg = self.config
+        if cfg.repair_features != "output":
+            raise NotImplementedError(f"repair_features={cfg.repair_features!r} is not supported by the MI355X "
+                                      "build; only the output-feature repair is built.")
         base = base_video.contiguous().view(bh, tokens, dim)
         if route.probe_rows is not None and route.probe_weights is not None:
             rows, weights = route.probe_rows, route.probe_weights

@@ -314,12 +314,6 @@ def recover_nonfinite_rrr_state(state, previous):
     return selected, recovered, policy
 
 
-def predict_reduced_rank_residual(x, state):
-    x_mean, x_scale, y_mean, left, basis = state
-    normalized = (x.float() - x_mean) / x_scale
-    return torch.bmm(torch.bmm(normalized, left), basis.transpose(1, 2)) + y_mean
-
-
 def apply_reduced_rank_residual(base, role, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap):
     """base + alpha * correction (optional norm cap), cast to base.dtype (reference :620-646).
     Output-only bf16 rank-16 states with D in {64, 128} use the HIP apply kernel;

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_symbols():
         assert hasattr(lib, name), f"{name} missing from {_lib.LIB_PATH.name}"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.spr_abi_version() == 1
+    assert lib.spr_abi_version() == 2
     assert isinstance(lib.spr_last_error(), bytes)
 
 

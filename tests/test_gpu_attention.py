@@ -58,6 +58,8 @@ def _reference(oracle, q, k, v, m, qs, ks):
     (2, 2, 2, 513, 128, 3, 17),     # q-clusters of > 128 rows: several tiles per cluster
     (1, 4, 2, 600, 128, 5, 9),      # GQA group 2
     (1, 1, 1, 64, 128, 1, 1),
+    (1, 2, 2, 3000, 128, 6, 1024),  # kn > 768: segment lists read from the plan, not LDS
+    (1, 1, 1, 2000, 64, 4, 900),    # the same for the D = 64 kernel
 ])
 def test_block_sparse_matches_closed_form(dev, oracle, B, Hq, Hkv, S, D, qn, kn):
     from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
@@ -225,3 +227,39 @@ def test_q_index_fuses_the_query_permutation(dev, oracle):
     got2 = block_sparse_attention(qd, to_dev(k_tok, dev, torch.bfloat16), to_dev(v_tok, dev, torch.bfloat16),
                                   *args[2:], q_index=qi, k_index=to_dev(kperm, dev))
     assert torch.equal(got2, ref)
+
+
+def test_run_rejects_a_plan_for_other_sizes(dev, oracle):
+    """A plan buffer too small for the run's sizes is refused on the host (status 3); a
+    plan built for another sequence length is seen by the kernels' header check, which
+    leaves the output unwritten."""
+    from sparsepr_amd import _lib
+    from sparsepr_amd.kernels.attention import plan_block_sparse
+
+    rng = np.random.default_rng(11)
+    q, k, v, m, qs, ks = _problem(oracle, rng, 1, 2, 2, 500, 128, 4, 8, empty_row=False)
+    qd, kd, vd = (to_dev(a[0], dev, torch.bfloat16) for a in (q, k, v))
+    plan = plan_block_sparse(to_dev(m[0], dev), to_dev(qs[0], dev), to_dev(ks[0], dev), 500)
+    lib = _lib.load()
+    stream = _lib.stream(dev)
+    out = torch.full_like(qd, 7.0)
+    # too small for qn=4, kn=16: refused before any launch
+    st = lib.spr_block_sparse_attention_run(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), plan.data_ptr(),
+                                            plan.numel(), 2, 2, 500, 128, 4, 16, 0.1, None, None, out.data_ptr(),
+                                            None, stream)
+    assert st == 3 and b"plan buffer" in lib.spr_last_error()
+    # built for s = 500, run over the first 400 rows: the header does not match
+    q4, k4, v4 = (t[:, :400].contiguous() for t in (qd, kd, vd))
+    out4 = torch.full_like(q4, 7.0)
+    st = lib.spr_block_sparse_attention_run(q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), plan.data_ptr(),
+                                            plan.numel(), 2, 2, 400, 128, 4, 8, 0.1, None, None, out4.data_ptr(),
+                                            None, stream)
+    torch.cuda.synchronize()
+    assert st == 0
+    assert bool((out4 == 7.0).all())
+    # the matching run writes every row
+    st = lib.spr_block_sparse_attention_run(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), plan.data_ptr(),
+                                            plan.numel(), 2, 2, 500, 128, 4, 8, 0.1, None, None, out.data_ptr(),
+                                            None, stream)
+    torch.cuda.synchronize()
+    assert st == 0 and not bool((out == 7.0).all(dim=-1).any())

@@ -21,7 +21,8 @@ def _gmm(oracle, rng, b, n, d, comps, std=0.25):
 
 
 @pytest.mark.parametrize("b,n,k,d", [(2, 3000, 256, 128), (3, 1001, 100, 128), (1, 4096, 64, 64),
-                                     (2, 500, 512, 128), (1, 37, 5, 64)])
+                                     (2, 500, 512, 128), (1, 37, 5, 64),
+                                     (1, 3000, 1000, 128)])  # k > 512: the streamed (non-resident) kernel
 @pytest.mark.parametrize("mode", ["bf16", "fp32"])
 def test_assign_matches_oracle_up_to_ties(dev, oracle, b, n, k, d, mode):
     from sparsepr_amd.flash_kmeans.kmeans_impl import X_SQ_BF16, X_SQ_FP32, euclid_assign

@@ -30,6 +30,13 @@ def test_expf_within_two_ulp_of_float64_exp(oracle):
     assert _ulp_diff(got, ref).max() <= 2
     assert oracle.expf(np.array([-87.5, -200.0], np.float32)).tolist() == [0.0, 0.0]
     assert np.isinf(oracle.expf(np.array([89.0], np.float32))[0])
+    # the top of the range, where round(x log2 e) = 128: finite up to ln(FLT_MAX)
+    top = np.linspace(88.0, 88.7228, 4001).astype(np.float32)
+    got = oracle.expf(top)
+    assert np.isfinite(got).all()
+    assert _ulp_diff(got, np.exp(top.astype(np.float64)).astype(np.float32)).max() <= 2
+    over = np.array([88.7230, 88.8, 88.99], np.float32)  # e^x > FLT_MAX
+    assert np.isinf(oracle.expf(over)).all()
 
 
 def test_bf16_rounding_nearest_even(oracle):
