@@ -162,6 +162,19 @@ int spr_block_sparse_attention(const void* q, const void* k, const void* v, cons
                                int32_t d, int32_t qn, int32_t kn, float scale, const int32_t* q_index,
                                const int32_t* k_index, void* out, float* lse, void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
+/* No counterpart in the reference: spr_block_sparse_attention for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  Same arguments and results, with the plan kept in a fixed 64 MiB device
+ * array of the library (one per device, held until the process ends) instead of a
+ * workspace; calls no hipMalloc/hipFree.  Returns 3 when the plan for (bh_kv, qn, kn)
+ * needs more than 64 MiB (spr_block_sparse_attention_workspace bytes).  Calls that
+ * overlap on one device share the array and race; the calling thread's current device
+ * must be the stream's device. */
+int spr_block_sparse_attention_noalloc(const void* q, const void* k, const void* v, const uint8_t* map,
+                                       const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q, int64_t bh_kv,
+                                       int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
+                                       const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
+                                       hipStream_t stream);
 /* n8_v6.py:1236-1243 dense probe attention (F.scaled_dot_product_attention of the probe
  * rows against every key).  q bf16 [bh_q, m, d], k/v bf16 [bh_kv, s_kv, d]; keys split
  * into nsplit ranges computed in parallel and merged; out [bh_q, m, d] (out_dtype 0 =

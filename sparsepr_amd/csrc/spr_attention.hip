@@ -34,6 +34,7 @@
 // staged through registers into a padded K tile and a transposed V tile,
 // double-buffered, the next chunk fetched while the current one computes).
 #include "spr_common.h"
+#include <mutex>
 
 namespace {
 
@@ -1335,3 +1336,72 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
   return SPR_OK;
 }
 
+// ---------------------------------------------------------------- allocation-free variant
+// spr_block_sparse_attention with its plan in a fixed device array instead of a caller
+// workspace, for callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops that forbid hipMalloc).  `scratch` holds one plan of at most
+// NOALLOC_PLAN_BYTES: every BASELINE shape fits (C3 15.4 MiB, C4 12.1 MiB, C5 20.1 MiB,
+// the N8 defaults of 300 x 1000 clusters at 24 heads 55.1 MiB).  Each device the library
+// runs on holds its own copy until the process ends.  The host never names the array in
+// a launch or copy: its device address is looked up once per device with
+// hipGetSymbolAddress, with that device current, and kept in g_scratch_addr.
+// The plan kernels write every word the run reads (the header last), so nothing has to
+// start at zero; calls that overlap on one device (two streams, two threads) share the
+// array and race.
+constexpr size_t NOALLOC_PLAN_BYTES = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_PLAN_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[NOALLOC_MAX_DEVICES] = {};
+
+// Device address of this device's `scratch` (looked up on the first call per device).
+int noalloc_scratch_addr(void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    spr_set_error("spr_block_sparse_attention_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return SPR_ELAUNCH;
+  }
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) {
+    spr_set_error("spr_block_sparse_attention_noalloc: device %d outside [0, %d)", dev, NOALLOC_MAX_DEVICES);
+    return SPR_EINVAL;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      spr_set_error("spr_block_sparse_attention_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                    dev, hipGetErrorString(e));
+      return SPR_ELAUNCH;
+    }
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return SPR_OK;
+}
+}  // namespace
+
+extern "C" int spr_block_sparse_attention_noalloc(const void* q, const void* k, const void* v, const uint8_t* map,
+                                                  const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q,
+                                                  int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn,
+                                                  float scale, const int32_t* q_index, const int32_t* k_index,
+                                                  void* out, float* lse, hipStream_t stream) {
+  SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_noalloc: bad size");
+  if (bh_q == 0 || s == 0) return SPR_OK;
+  SPR_REQUIRE(kn <= 16384 && qn <= TO_MAX_QN && bh_kv <= 65535, "spr_block_sparse_attention_noalloc: bad plan size");
+  const size_t need = spr_block_sparse_attention_workspace(bh_kv, qn, kn);
+  if (need > NOALLOC_PLAN_BYTES) {
+    spr_set_error("spr_block_sparse_attention_noalloc: the plan for bh_kv=%lld qn=%d kn=%d needs %zu bytes, more "
+                  "than the %zu-byte fixed plan array; use spr_block_sparse_attention with a workspace",
+                  (long long)bh_kv, qn, kn, need, NOALLOC_PLAN_BYTES);
+    return SPR_EWORKSPACE;
+  }
+  void* plan = nullptr;
+  const int st = noalloc_scratch_addr(&plan);
+  if (st != SPR_OK) return st;
+  return spr_block_sparse_attention(q, k, v, map, q_sizes, k_sizes, bh_q, bh_kv, s, d, qn, kn, scale, q_index,
+                                    k_index, out, lse, plan, need, stream);
+}
