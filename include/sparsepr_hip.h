@@ -103,11 +103,14 @@ int spr_role_assign_fp32(const float* features, const float* centroids, int64_t 
  *   descending sort (index tie-break), sequential cumsum, keep ranks whose preceding
  *   cumsum <= p (rank 0 always), then the min_kc_ratio floor (`preserve` ranks).
  *   qc fp32 [bh, qn, d], kc fp32 [bh, kn, d], k_sizes int32 [bh, kn] -> map uint8
- *   [bh, qn, kn].  score_bf16 = 1 rounds every intermediate the way bf16 tensors do in
- *   torch (matmul output, scaled score, probabilities, cumsum); kn <= 4096. */
+ *   [bh, qn, kn] (nullable) and budgets int32 [bh, qn] (nullable; the sum of the kept
+ *   clusters' sizes, the key-token budgets of n8_v6.py:181-230, whose keep rule is the
+ *   same); at least one of the two.  score_bf16 = 1 rounds every intermediate the way
+ *   bf16 tensors do in torch (matmul output, scaled score, probabilities, cumsum);
+ *   kn <= 4096. */
 int spr_topp_map(const float* qc, const float* kc, const int32_t* k_sizes, int64_t bh, int32_t qn, int32_t kn,
                  int32_t d, float sqrt_d, float p, int32_t preserve, int32_t score_bf16, uint8_t* map,
-                 hipStream_t stream);
+                 int32_t* budgets, hipStream_t stream);
 /* n8_ops.cu:271-322,541-571 svg_ear_select_budget (mode 0) and the Triton / CPU selectors
  * selector_budget.py:131-171, n8_v6.py:1088-1111 (mode 1: crossing at sorted position
  * `count`); n8_ops.cu:573-638 svg_ear_select_budget_schedule when ids/counts are given.

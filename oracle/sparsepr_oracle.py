@@ -330,19 +330,14 @@ def identify_dynamic_map_f64(qc, kc, k_sizes, p, min_kc_ratio=0.0):
 
 
 def svg_top_p_key_budgets(qc, kc, k_sizes, top_p):
-    """Per-q-cluster key budgets (n8_v6.py:181-230), float64 evaluation."""
-    d = qc.shape[2]
-    logits = np.einsum("bqd,bkd->bqk", qc.astype(np.float64), kc.astype(np.float64)) / math.sqrt(d)
-    logits -= logits.max(2, keepdims=True)
-    we = np.exp(logits) * k_sizes.astype(np.float64)[:, None, :]
-    prob = we / np.maximum(we.sum(2, keepdims=True), 1e-12)
-    order = np.argsort(-prob, axis=2, kind="stable")
-    cum = np.cumsum(np.take_along_axis(prob, order, 2), 2)
-    keep = cum <= top_p
-    keep = np.concatenate([np.ones_like(keep[:, :, :1]), keep[:, :, :-1]], axis=2)
-    sizes_sorted = np.take_along_axis(
-        np.broadcast_to(k_sizes.astype(np.int64)[:, None, :], prob.shape), order, 2)
-    return (sizes_sorted * keep).sum(2)
+    """Per-q-cluster key-token budgets (n8_v6.py:181-230): the sizes of the key clusters
+    kept by the top-p rule, summed.  The reference's chain (fp32 bmm / sqrt(d), max
+    shift, exp times sizes, divide by the clamped sum, descending sort, cumsum, keep
+    rank 0 and every rank whose preceding cumsum <= top_p) is identify_dynamic_map's
+    fp32 chain (kmeans_utils.py:1698-1742) with the same keep rule, so it is evaluated
+    by that canonical fp32 restatement.  Returns int64 [BH, Qc]."""
+    keep = identify_dynamic_map(np.asarray(qc, np.float32), np.asarray(kc, np.float32), k_sizes, top_p)
+    return (keep.astype(np.int64) * np.asarray(k_sizes, np.int64)[:, None, :]).sum(2)
 
 
 def select_budget(scores, sizes, budgets, mode=0):

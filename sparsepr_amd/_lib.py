@@ -43,7 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                          _vp, _vp, _sz, _vp]),
     "spr_role_assign_fp32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     # select.hip
-    "spr_topp_map": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _f32, _i32, _i32, _vp, _vp]),
+    "spr_topp_map": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _f32, _i32, _i32, _vp, _vp, _vp]),
     "spr_select_budget": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "spr_compact_selected": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp, _vp]),
     "spr_density": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _vp, _vp]),

@@ -89,7 +89,8 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
                                                                const int32_t* __restrict__ k_sizes,
                                                                int32_t qn, int32_t kn, int32_t d, float sqrt_d,
                                                                float p, int32_t preserve, int32_t score_bf16,
-                                                               uint8_t* __restrict__ map) {
+                                                               uint8_t* __restrict__ map,
+                                                               int32_t* __restrict__ budgets) {
   __shared__ __attribute__((aligned(16))) float q_row[512];
   __shared__ __attribute__((aligned(16))) float val[MAX_KC];
   __shared__ float sorted_val[MAX_KC];
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
   __shared__ float scratch[SEL_THREADS / 64];
   __shared__ float denom_s;
   __shared__ int32_t cut_s;
+  __shared__ unsigned long long budget_s;
 
   const int64_t row = blockIdx.x;  // bh * qn + q
   const int64_t bh = row / qn;
@@ -184,11 +186,23 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
       prev = score_bf16 ? bf16r(cum) : cum;
     }
     cut_s = cut < kn ? cut : kn;
+    budget_s = 0;
   }
   __syncthreads();
   const int cut = cut_s;
-  uint8_t* out = map + row * kn;
-  for (int r = threadIdx.x; r < kn; r += blockDim.x) out[sorted_idx[r]] = r < cut ? 1 : 0;
+  if (map != nullptr) {
+    uint8_t* out = map + row * kn;
+    for (int r = threadIdx.x; r < kn; r += blockDim.x) out[sorted_idx[r]] = r < cut ? 1 : 0;
+  }
+  if (budgets != nullptr) {
+    // key-token budget of the kept clusters (n8_v6.py:226-230): sum of their sizes;
+    // integers, so the summation order does not matter
+    unsigned long long part = 0;
+    for (int r = threadIdx.x; r < cut; r += blockDim.x) part += static_cast<unsigned long long>(max(sz[sorted_idx[r]], 0));
+    if (part != 0) atomicAdd(&budget_s, part);
+    __syncthreads();
+    if (threadIdx.x == 0) budgets[row] = static_cast<int32_t>(min(budget_s, 0x7FFFFFFFull));
+  }
 }
 
 // One workgroup per (bh, q) row of scores [bh, qn, kn].
@@ -375,15 +389,15 @@ __global__ __launch_bounds__(256) void density_kernel(const uint8_t* __restrict_
 // int32 key-cluster sizes [bh, kn].  sqrt_d is the divisor (float(sqrt(d))).
 extern "C" int spr_topp_map(const float* qc, const float* kc, const int32_t* k_sizes, int64_t bh, int32_t qn,
                             int32_t kn, int32_t d, float sqrt_d, float p, int32_t preserve, int32_t score_bf16,
-                            uint8_t* map, hipStream_t stream) {
+                            uint8_t* map, int32_t* budgets, hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && qn >= 0 && kn >= 1, "spr_topp_map: bad size");
   SPR_REQUIRE(kn <= MAX_KC, "spr_topp_map: %d key clusters exceed %d", kn, MAX_KC);
   SPR_REQUIRE(d >= 1 && d <= 512, "spr_topp_map: head dim %d outside [1, 512]", d);
   if (bh == 0 || qn == 0) return SPR_OK;
-  SPR_REQUIRE(qc && kc && k_sizes && map, "spr_topp_map: null pointer");
+  SPR_REQUIRE(qc && kc && k_sizes && (map || budgets), "spr_topp_map: null pointer");
   topp_map_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, 0, stream>>>(qc, kc, k_sizes, qn, kn, d,
                                                                                      sqrt_d, p, preserve, score_bf16,
-                                                                                     map);
+                                                                                     map, budgets);
   SPR_LAUNCHED("topp_map_kernel");
   return SPR_OK;
 }

@@ -29,8 +29,38 @@ def topp_map(qc: torch.Tensor, kc: torch.Tensor, k_sizes: torch.Tensor, p: float
     preserve = int(min_kc_ratio * kn) if min_kc_ratio > 0 else 0
     out = torch.empty((r, qn, kn), dtype=torch.bool, device=dev)
     _lib.call("spr_topp_map", _lib.ptr(q32), _lib.ptr(k32), _lib.ptr(ks), r, qn, kn, d,
-              float(math.sqrt(d)), float(p), preserve, score_bf16, _lib.ptr(out), _lib.stream(dev))
+              float(math.sqrt(d)), float(p), preserve, score_bf16, _lib.ptr(out), None, _lib.stream(dev))
     return out
+
+
+def top_p_key_budgets(q_centroids: torch.Tensor, k_centroids: torch.Tensor, k_cluster_sizes: torch.Tensor,
+                      top_p: float) -> torch.Tensor:
+    """SVG2 key-token budget of each query cluster (n8_v6.py:181-230): the summed sizes
+    of the key clusters that the fp32 top-p rule keeps (rank 0 always, then every rank
+    whose preceding cumulative mass is <= top_p).  [BH, Qc, D] x [BH, Kc, D] -> int64
+    [BH, Qc].  The fp32 chain is the top-p map's (the same kernel, map not written)."""
+    if q_centroids.ndim != 3 or k_centroids.ndim != 3:
+        raise ValueError("TopP budget centroids must be [BH,C,D].")
+    if q_centroids.shape[0] != k_centroids.shape[0]:
+        raise ValueError("TopP Q/K centroids must have the same head count.")
+    if q_centroids.shape[2] != k_centroids.shape[2]:
+        raise ValueError("TopP Q/K centroids must have the same head dimension.")
+    if tuple(k_cluster_sizes.shape) != tuple(k_centroids.shape[:2]):
+        raise ValueError(
+            "TopP K-cluster sizes must match K centroids, got "
+            f"sizes={tuple(k_cluster_sizes.shape)} centroids={tuple(k_centroids.shape)}.")
+    if not 0.0 < float(top_p) <= 1.0:
+        raise ValueError(f"svg_ear_top_p must be in (0,1], got {top_p}.")
+    dev = _lib.require_gpu(q_centroids, k_centroids, k_cluster_sizes, what="top-p key budgets")
+    r, qn, d = q_centroids.shape
+    kn = k_centroids.shape[1]
+    q32 = q_centroids.float().contiguous()
+    k32 = k_centroids.float().contiguous()
+    ks = k_cluster_sizes.to(torch.int32).contiguous()
+    budgets = torch.empty((r, qn), dtype=torch.int32, device=dev)
+    _lib.call("spr_topp_map", _lib.ptr(q32), _lib.ptr(k32), _lib.ptr(ks), r, qn, kn, d, float(math.sqrt(d)),
+              float(top_p), 0, 0, None, _lib.ptr(budgets), _lib.stream(dev))
+    return budgets.long()
 
 
 def select_budget(scores: torch.Tensor, sizes: torch.Tensor, budgets: torch.Tensor, mode: int,

@@ -149,6 +149,81 @@ def test_batch_kmeans_euclid_whole_loop(dev, oracle):
     assert iters == 1 and (cent.float().cpu().numpy() == init).all()
 
 
+@pytest.mark.parametrize("backend,x_sq_mode,labels_dtype,sizes_dtype", [
+    ("cuvs", "bf16", torch.int64, torch.int32),   # in-file loop: x.dtype x_sq buffer (kmeans_utils.py:1550-1580)
+    ("flash", "fp32", torch.int32, torch.int64),  # warm start: inline fp32 x_sq (kmeans_utils.py:1396-1411)
+])
+def test_kmeans_utils_dispatcher_warm_start(dev, oracle, backend, x_sq_mode, labels_dtype, sizes_dtype):
+    """kmeans_utils.batch_kmeans_Euclid (:1504-1580) at its default tol = 1e-4, warm
+    started, against the oracle's loop with that backend's x_sq precision."""
+    from sparsepr_amd.kmeans_utils import batch_kmeans_Euclid
+
+    rng = np.random.default_rng(17)
+    x = _gmm(oracle, rng, 2, 4000, 128, 60)
+    init = oracle.first_k_init(x, 64, seed=5)
+    labels, cent, sizes, iters = batch_kmeans_Euclid(to_dev(x, dev, torch.bfloat16), 64, max_iters=4,
+                                                     init_centroids=to_dev(init, dev, torch.bfloat16),
+                                                     backend=backend)
+    rl, rc, rs, ri = oracle.batch_kmeans_euclid(x, 64, 4, 1e-4, init, x_sq_mode, True)
+    assert labels.dtype == labels_dtype and sizes.dtype == sizes_dtype
+    assert iters == ri
+    agree = (labels.cpu().numpy() == rl).mean()
+    assert agree > 0.999
+    if agree == 1.0:
+        assert (cent.float().cpu().numpy() == rc).all()
+        assert (sizes.cpu().numpy() == rs).all()
+    # points sitting exactly on the initial centroids converge at once: shift 0 < tol
+    x0 = np.repeat(init, 10, axis=1)
+    labels, cent, sizes, iters = batch_kmeans_Euclid(to_dev(x0, dev, torch.bfloat16), 64, max_iters=4,
+                                                     init_centroids=to_dev(init, dev, torch.bfloat16),
+                                                     backend=backend)
+    assert iters == 1 and (cent.float().cpu().numpy() == init).all()
+    assert (sizes.cpu().numpy() == 10).all()
+
+
+@pytest.mark.parametrize("backend", ["cuvs", "flash"])
+def test_kmeans_utils_assign_only(dev, oracle, backend):
+    """max_iters = 0 (kmeans_utils.py:1212-1278): one assignment to the given centroids
+    with the fp32 x_sq, int64 labels and sizes, 0 iterations, centroids unchanged."""
+    from sparsepr_amd.kmeans_utils import batch_kmeans_Euclid
+
+    rng = np.random.default_rng(18)
+    x = _gmm(oracle, rng, 2, 3000, 128, 40)
+    c = oracle.first_k_init(x, 100, seed=6)
+    ct = to_dev(c, dev, torch.bfloat16)
+    labels, cent, sizes, iters = batch_kmeans_Euclid(to_dev(x, dev, torch.bfloat16), 100, max_iters=0,
+                                                     init_centroids=ct, backend=backend)
+    assert iters == 0 and labels.dtype == torch.int64 and sizes.dtype == torch.int64
+    assert torch.equal(cent, ct)
+    xs = oracle.x_sq_for(x, "fp32")
+    ref, dist = oracle.kmeans_assign(x, c, xs)
+    got = labels.cpu().numpy()
+    ok, _ = oracle.label_mismatches_are_ties(got, ref, dist, xs, c, TIE_REL)
+    assert ok
+    assert (sizes.cpu().numpy() == np.stack([np.bincount(r, minlength=100) for r in got])).all()
+    with pytest.raises(RuntimeError, match="requires init_centroids"):
+        batch_kmeans_Euclid(to_dev(x, dev, torch.bfloat16), 100, max_iters=0, backend=backend)
+
+
+def test_kmeans_utils_n8_backend_and_errors(dev, oracle):
+    """backend n8_cuda_ext (:1468-1501): fixed exact-FP32 D = 64 steps from given centroids."""
+    from sparsepr_amd.kmeans_utils import batch_kmeans_Euclid
+
+    rng = np.random.default_rng(19)
+    f = rng.standard_normal((2, 2000, 64)).astype(np.float32)
+    c = f[:, :40].copy()
+    labels, cent, sizes, iters = batch_kmeans_Euclid(to_dev(f, dev), 40, max_iters=2, init_centroids=to_dev(c, dev),
+                                                     backend="n8_cuda_ext")
+    l1, c1, _, _ = oracle.role_step64(f, c)
+    l2, c2, s2, _ = oracle.role_step64(f, c1)
+    assert iters == 2 and sizes.dtype == torch.int64
+    assert (labels.cpu().numpy() == l2).mean() > 0.999
+    with pytest.raises(RuntimeError, match="Unknown Euclidean k-means backend"):
+        batch_kmeans_Euclid(to_dev(f, dev), 40, backend="bogus")
+    with pytest.raises(RuntimeError, match="requires initialized centroids"):
+        batch_kmeans_Euclid(to_dev(f, dev), 40, max_iters=2, backend="n8_cuda_ext")
+
+
 def test_kmeans_full_size_properties(dev):
     """BASELINE config 2 shape (24 x 118,800 x 128, K=256, 5 iterations):
     sizes sum to N, the objective does not increase, labels are the argmin."""

@@ -85,6 +85,24 @@ def test_round_probes_and_first_token(dev, oracle):
     assert (rows.cpu().numpy() == rr).all() and np.allclose(w.cpu().numpy(), rw, rtol=1e-6)
 
 
+def test_round_probes_hand_derived_sequence(dev):
+    """The hand-worked case of the oracle's test (three groups of 5, 2 and 1 tokens, eight
+    probes): exhausted groups re-offer their lowest token id.  Features padded with zero
+    dims to the kernel's 64 (the distances are unchanged)."""
+    from sparsepr_amd.residual_repair import select_role_equal_probes
+
+    f = np.zeros((1, 8, 64), np.float32)
+    for t, xy in {0: (0.0, 0.0), 2: (3.0, 0.0), 4: (-1.0, 0.0), 6: (0.5, 0.0), 7: (-2.5, 0.0),
+                  1: (10.0, 1.0), 5: (10.0, 4.0), 3: (-7.0, -7.0)}.items():
+        f[0, t, :2] = xy
+    labels = np.array([[0, 1, 0, 2, 0, 1, 0, 0]], np.int32)
+    rows, w = select_role_equal_probes(to_dev(f, dev), to_dev(labels, dev), num_clusters=3, rows=8)
+    assert rows.cpu().numpy()[0].tolist() == [0, 1, 3, 6, 5, 3, 4, 1]
+    per_group = {0: 5.0 / 3.0, 1: 2.0 / 3.0, 2: 0.5}
+    want = np.array([per_group[int(labels[0, r])] for r in [0, 1, 3, 6, 5, 3, 4, 1]])
+    assert np.allclose(w.cpu().numpy()[0], want, rtol=1e-6)
+
+
 def test_fit_prep_apply_scatter(dev, oracle):
     from sparsepr_amd.kernels.residual_repair import (n8_exact_probe_scatter_triton,
                                                       n8_prepare_output_repair_fit_triton,

@@ -42,6 +42,21 @@ def test_topp_map_bit_exact(dev, oracle, bh, qn, kn, d, bf16, p, ratio):
     assert (got[0].cpu().numpy() == ref).all()
 
 
+@pytest.mark.parametrize("bh,qn,kn,d", [(4, 32, 64, 64), (2, 128, 512, 128), (3, 100, 500, 128)])
+@pytest.mark.parametrize("p", [0.5, 0.85, 0.95])
+def test_top_p_key_budgets_exact(dev, oracle, bh, qn, kn, d, p):
+    """SVG2 key-token budgets (n8_v6.py:181-230): integers, equal to the oracle's."""
+    from sparsepr_amd.kernels.selection import top_p_key_budgets
+
+    rng = np.random.default_rng(bh * 7 + kn + int(100 * p))
+    qc, kc, ks = _centroids(rng, bh, qn, kn, d, scale=0.4)
+    got = top_p_key_budgets(to_dev(qc, dev), to_dev(kc, dev), to_dev(ks, dev), p)
+    assert got.dtype == torch.int64 and tuple(got.shape) == (bh, qn)
+    assert (got.cpu().numpy() == oracle.svg_top_p_key_budgets(qc, kc, ks, p)).all()
+    with pytest.raises(ValueError, match="svg_ear_top_p"):
+        top_p_key_budgets(to_dev(qc, dev), to_dev(kc, dev), to_dev(ks, dev), 1.5)
+
+
 def test_topp_map_all_empty_keeps_everything(dev, oracle):
     from sparsepr_amd.kmeans_utils import identify_dynamic_map
 
