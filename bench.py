@@ -1,19 +1,26 @@
 #!/usr/bin/env python3
-"""Benchmark: one SparsePR attention layer at the HunyuanVideo shape on one MI355X.
+"""Benchmark: one SparsePR attention layer at the BASELINE shapes on one MI355X.
 
-Workload: batch 1, 24 heads, 118,800 tokens (33 x 45 x 80),
-head_dim 128, bf16; flash k-means with 128 Q-clusters and 512 K-clusters
-(5 Lloyd iterations, seeded first-k init), top-p 0.9 cluster-pair selection,
-block-sparse attention, N8 repair with 128 probes.  Synthetic frame-correlated
-Gaussian-mixture Q/K/V (400 components), generated on the device before timing.
+Default workload (the headline): batch 1, 24 heads, 118,800 tokens
+(33 x 45 x 80), head_dim 128, bf16; flash k-means with 128 Q-clusters and 512 K-clusters
+(5 Lloyd iterations, seeded first-k init), top-p 0.9 cluster-pair selection, block-sparse
+attention, N8 repair with 128 probes.  Synthetic frame-correlated Gaussian-mixture Q/K/V
+(400 components), generated on the device before timing.
 
-One step = one full layer call (route + attention + repair) on inputs resident
-in HBM.  Prints ONE JSON line.  `roofline` describes the dominant kernel (the
-block-sparse attention, MFMA-bound): algorithmic flops = 4 * D * sum of kept
-|Q_a| * |K_c| pairs, divided by the kernel's average duration measured with HIP
-events around its launch on the stream it runs on.  `cpu_baseline` times the
-CPU oracle (numpy, the reference algorithm restated) on a bounded sample
-(the first head of the same inputs), scaled to ms per layer.
+--config selects another BASELINE configuration:
+  c1  the CPU-runnable case (2 x 4,096 x 64, Qc 32, Kc 64, 10 iterations, 64 probes);
+  c2  standalone batched k-means (24 x 118,800 x 128, K 256, 5 iterations);
+  c3  Wan2.2 (40 x 32,760 x 128, Qc 100, Kc 500, 128 probes);
+  c4  HunyuanVideo (the default);
+  c5  Cosmos2.5 (40 x 84,480 x 128, Qc 128, Kc 512): one line per top-p in
+      {0.7, 0.8, 0.9, 0.95} x repair on/off (or the --top-p / --no-repair point).
+
+One step = one full layer call (route + attention + repair) on inputs resident in HBM
+(c2: one Lloyd loop).  Each line carries `roofline` for the dominant kernel, measured
+with HIP events around its launches on the stream it runs on.  `cpu_baseline` is the
+CPU oracle (numpy, the reference algorithm restated) at BASELINE config 1, median of 5
+runs after 1 warm-up with the per-stage split, in the same process as the GPU run;
+`cpu_baseline_same_workload` times one head of the measured workload itself.
 """
 
 from __future__ import annotations
@@ -39,7 +46,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--top-p", type=float, default=0.9)
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c4",
+                    help="BASELINE configuration (c4, the HunyuanVideo layer, is the headline)")
+    ap.add_argument("--amp", type=float, default=None,
+                    help="component-mean amplitude of the generator (default 2.3; 1.0 is the literal "
+                         "means ~N(0, 1) of the BASELINE description)")
+    ap.add_argument("--top-p", type=float, default=None)
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -63,34 +75,99 @@ def traffic_from_profiles():
         return None
 
 
-def cpu_baseline(q, k, v, cfg, heads: int):
-    """Time the CPU oracle's layer on `heads` heads of the same inputs."""
-    import numpy as np
-
-    from oracle import sparsepr_oracle as orc
-
+def _cpu_threads() -> int:
     try:
         from threadpoolctl import threadpool_info
 
-        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+        return int(max([p.get("num_threads", 1) for p in threadpool_info()] or [1]))
     except Exception:
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def _oracle_cfg(cfg):
+    from oracle import sparsepr_oracle as orc
+
+    return orc.LayerConfig(q_clusters=cfg.num_q_centroids, k_clusters=cfg.num_k_centroids,
+                           kmeans_iters=cfg.kmeans_iters, top_p=cfg.top_p, probes=cfg.probe_rows,
+                           init_seed=cfg.init_seed)
+
+
+def cpu_baseline_c1(runs: int = 5):
+    """BASELINE config 1 on the CPU oracle, as the CPU baseline plan specifies: fp32, median of
+    `runs` runs after one warm-up, per-stage split; the block-sparse attention both as the
+    loop-faithful restatement of dynamic_block_sparse_fwd_torch and as the vectorized
+    masked-dense variant.  Also times the GPU layer on the same inputs (bf16) in this process."""
+    import numpy as np
+    import torch
+
+    from oracle import sparsepr_oracle as orc
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.layer import SparsePRAttention
+
+    c1 = _layer_configs()["c1"]
+    shape, gen, cfg = c1["shape"], c1["gen"], c1["cfg"]
+    q, k, v = synthetic.frame_gmm_qkv(shape, device="cpu", dtype=torch.float32, **gen)
+    qn, kn, vn = (t[0].numpy() for t in (q, k, v))
+    ocfg = _oracle_cfg(cfg)
+    torch.set_num_threads(os.cpu_count() or 1)
+    res = {}
+    for attention in ("loop", "dense"):
+        totals, stages = [], []
+        for i in range(runs + 1):
+            st: dict = {}
+            t0 = time.perf_counter()
+            orc.sparsepr_layer(qn, kn, vn, ocfg, timings=st, bf16=False, attention=attention)
+            if i > 0:  # the first run is the warm-up
+                totals.append((time.perf_counter() - t0) * 1e3)
+                stages.append(st)
+        med = int(np.argsort(totals)[len(totals) // 2])
+        res[attention] = (float(np.median(totals)), {k: round(v, 2) for k, v in stages[med].items()})
+    # the GPU layer on the same inputs (bf16: the kernels' input type)
+    qg, kg, vg = (t.to("cuda", torch.bfloat16) for t in (q, k, v))
+    layer = SparsePRAttention(cfg)
+    for _ in range(3):
+        layer(qg, kg, vg)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        layer(qg, kg, vg)
+    torch.cuda.synchronize()
+    gpu_ms = (time.perf_counter() - t0) * 1e3 / 20
+    loop_ms, loop_st = res["loop"]
+    dense_ms, dense_st = res["dense"]
+    return {
+        "value": round(loop_ms, 2),
+        "unit": "ms/layer at BASELINE config 1",
+        "cores": _cpu_threads(),
+        "kind": "port",
+        "sample": ("BASELINE config 1 (1 x 2 x 4,096 x 64 fp32, Qc 32, Kc 64, 10 Lloyd iterations, top-p 0.9, "
+                   f"64 probes) on the CPU oracle, median of {runs} runs after 1 warm-up, loop-faithful "
+                   "block-sparse attention"),
+        "stages_ms": loop_st,
+        "vectorized_attention_variant": {"value": round(dense_ms, 2), "stages_ms": dense_st},
+        "gpu_ms_same_inputs_bf16": round(gpu_ms, 3),
+    }
+
+
+def cpu_baseline_slice(q, k, v, cfg, heads: int):
+    """The CPU oracle's layer on `heads` heads of the measured inputs (the heads are
+    independent, so the layer's CPU time is this slice's times H / heads, reported as such)."""
+    from oracle import sparsepr_oracle as orc
+
     qn = q[0, :heads].float().cpu().numpy()
     kn = k[0, :heads].float().cpu().numpy()
     vn = v[0, :heads].float().cpu().numpy()
-    ocfg = orc.LayerConfig(q_clusters=cfg.num_q_centroids, k_clusters=cfg.num_k_centroids,
-                           kmeans_iters=cfg.kmeans_iters, top_p=cfg.top_p, probes=cfg.probe_rows,
-                           init_seed=cfg.init_seed)
     stages: dict = {}
     t0 = time.perf_counter()
-    orc.sparsepr_layer(qn, kn, vn, ocfg, timings=stages)
+    orc.sparsepr_layer(qn, kn, vn, _oracle_cfg(cfg), timings=stages)
     secs = time.perf_counter() - t0
     total_heads = q.shape[1]
     return {
         "value": round(secs * 1e3 * total_heads / heads, 1),
         "unit": "ms/layer",
-        "cores": int(threads),
+        "cores": _cpu_threads(),
         "kind": "port",
+        "slice_ms": round(secs * 1e3, 1),
         "sample": (f"CPU oracle (numpy restatement: k-means, top-p map, loop-faithful block-sparse attention, "
                    f"N8 repair) on {heads} of {total_heads} heads of the same inputs, {secs:.1f} s, scaled x"
                    f"{total_heads / heads:g}; stage ms: " + ", ".join(f"{k}={v:.0f}" for k, v in stages.items())),
@@ -124,7 +201,7 @@ def only_attention(args):
 
     shape = synthetic.HUNYUAN
     q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **GEN)
-    layer = SparsePRAttention(SparsePRConfig(top_p=args.top_p, repair=False))
+    layer = SparsePRAttention(SparsePRConfig(top_p=args.top_p or 0.9, repair=False))
     route, q_idx = layer.route(q, k, v)
     B, H, N, D = q.shape
     plan = plan_block_sparse(route.video_dynamic_map, route.q_cluster_sizes, route.k_cluster_sizes, N)
@@ -163,7 +240,7 @@ def only_svg_ear(args):
 
     shape = synthetic.HUNYUAN
     q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **GEN)
-    layer = SparsePRAttention(SparsePRConfig(top_p=args.top_p, repair=False))
+    layer = SparsePRAttention(SparsePRConfig(top_p=args.top_p or 0.9, repair=False))
     route, _ = layer.route(q, k, v)
     B, H, N, D = q.shape
     bh = B * H
@@ -239,6 +316,198 @@ def only_role_proj(args):
                                    "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes}}), flush=True)
 
 
+def _layer_configs():
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.layer import SparsePRConfig
+
+    c1_gen = dict(seed=0, amp=1.0, step_std=0.0, noise_std=0.3, qk_corr=1.0)
+    return {
+        "c1": dict(shape=synthetic.CPU_SMALL, gen=c1_gen,
+                   cfg=SparsePRConfig(num_q_centroids=32, num_k_centroids=64, kmeans_iters=10, top_p=0.9,
+                                      probe_rows=64),
+                   workload="C1 CPU-runnable SparsePR layer: 1x2x4096x64 (4 x 32 x 32), Qc=32, Kc=64, "
+                            "10 Lloyd iters, top-p 0.9, 64 probes"),
+        "c3": dict(shape=synthetic.WAN, gen=GEN,
+                   cfg=SparsePRConfig(num_q_centroids=100, num_k_centroids=500, kmeans_iters=5, top_p=0.9,
+                                      probe_rows=128),
+                   workload="C3 Wan2.2-shaped SparsePR layer: 1x40x32760x128 bf16, Qc=100, Kc=500, "
+                            "5 Lloyd iters, top-p 0.9, 128 probes"),
+        "c4": dict(shape=synthetic.HUNYUAN, gen=GEN,
+                   cfg=SparsePRConfig(num_q_centroids=128, num_k_centroids=512, kmeans_iters=5, top_p=0.9,
+                                      probe_rows=128),
+                   workload="C4 HunyuanVideo-shaped SparsePR layer: 1x24x118800x128 bf16, Qc=128, Kc=512, "
+                            "5 Lloyd iters, top-p 0.9, 128 probes"),
+        "c5": dict(shape=synthetic.COSMOS, gen=GEN,
+                   cfg=SparsePRConfig(num_q_centroids=128, num_k_centroids=512, kmeans_iters=5, top_p=0.9,
+                                      probe_rows=128),
+                   workload="C5 Cosmos-Predict2.5-shaped SparsePR layer: 1x40x84480x128 bf16, Qc=128, Kc=512, "
+                            "5 Lloyd iters"),
+    }
+
+
+def bench_layer(args, name, top_p=None, repair=True, amp=None, with_cpu=False):
+    """Time `args.steps` layer calls after `args.warmup`; returns the JSON result dict."""
+    import dataclasses
+
+    import torch
+
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.layer import LayerTimings, SparsePRAttention, dense_flops, kept_pair_flops
+
+    spec = _layer_configs()[name]
+    shape = spec["shape"]
+    gen = dict(spec["gen"])
+    if amp is not None:
+        gen["amp"] = amp
+    cfg = spec["cfg"]
+    if top_p is not None:
+        cfg = dataclasses.replace(cfg, top_p=top_p)
+    cfg = dataclasses.replace(cfg, repair=repair)
+    q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **gen)
+    layer = SparsePRAttention(cfg)
+    for _ in range(args.warmup):
+        layer(q, k, v)
+    torch.cuda.synchronize()
+    marks = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tm = LayerTimings()
+        layer(q, k, v, timings=tm)
+        marks.append(tm)
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    names = list(marks[0].events)
+    stage_ms = {b: round(sum(m.ms(a, b) for m in marks) / len(marks), 3) for a, b in zip(names[:-1], names[1:])}
+    attn_ms = sum(m.ms("plan", "attention") for m in marks) / len(marks)
+    route = layer.last_route
+    kept = float(kept_pair_flops(route, shape.dim).item())
+    dens = float(route.base_video_density.item())
+    achieved = kept / (attn_ms * 1e-3) / 1e12
+    heads, tokens, d = shape.heads, shape.tokens, shape.dim
+    # algorithmic bytes of the attention: Q, K, V read once and O written once (bf16)
+    attn_bytes = 4 * heads * tokens * d * 2
+    workload = spec["workload"]
+    if name == "c5":
+        workload += f", top-p {cfg.top_p}, " + ("128 probes" if repair else "no repair")
+    result = {
+        "metric": METRIC,
+        "value": round(ms_per_step, 3),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (frame-correlated Gaussian mixture, seeded, generated on device)",
+        "config": {
+            "workload": workload, "heads": heads, "tokens": tokens, "head_dim": d, "top_p": cfg.top_p,
+            "repair": repair, "kept_pair_density": round(dens, 4),
+            "kept_attention_tflop": round(kept / 1e12, 3),
+            "dense_attention_tflop": round(dense_flops(heads, tokens, d) / 1e12, 2),
+            "generator": gen,
+        },
+        "stages_ms": stage_ms,
+        "roofline": {
+            "kernel": "attn_pipe_kernel (D=128 block-sparse attention)" if d == 128
+            else "attn_fwd_kernel<64> (D=64 block-sparse attention)",
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": traffic_from_profiles() if name == "c4" and amp is None and cfg.top_p == 0.9 else None,
+            "kernel_ms": round(attn_ms, 3),
+            # the same launch against the HBM roof: its floor is the larger of the two times
+            "hbm_floor_ms": round(attn_bytes / HBM_PEAK_GBS / 1e6, 3),
+            "mfma_floor_ms": round(kept / MFMA_BF16_PEAK_TFLOPS / 1e9, 3),
+        },
+    }
+    if with_cpu and not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_c1()
+        if args.cpu_heads > 0 and name != "c1":
+            result["cpu_baseline_same_workload"] = cpu_baseline_slice(q, k, v, cfg, args.cpu_heads)
+    return result
+
+
+def bench_kmeans_c2(args):
+    """batched flash k-means, 24 x 118,800 x 128 bf16, K = 256, 5 Lloyd
+    iterations from a seeded first-k init.  value = ms per Lloyd loop.  The rooflines time the
+    assign (MFMA / HBM) and the centroid update (sort + mean, HBM) separately with HIP events."""
+    import torch
+
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.flash_kmeans.kmeans_impl import X_SQ_BF16, centroid_update_sorted, euclid_assign, lloyd
+    from sparsepr_amd.kernels.permute import argsort_labels
+
+    B, N, D, K, iters = 24, 118800, 128, 256, 5
+    x = synthetic.gmm_points(B, N, D, 256, seed=0, std=0.25, device="cuda")
+    idx = synthetic.first_k_indices(N, K, 0).to("cuda")
+    init = x[:, idx].contiguous()
+
+    def run():
+        return lloyd(x, K, iters, 0.0, init, x_sq_mode=X_SQ_BF16)
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        res = run()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # the assign alone (later iterations: cached squared norms) and the update alone
+    x_sq = torch.empty((B, N), device="cuda")
+    labels = euclid_assign(x, res.centroids, None, x_sq_mode=X_SQ_BF16, x_sq_out=x_sq)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record()
+    for _ in range(args.steps):
+        euclid_assign(x, res.centroids, x_sq, x_sq_mode=X_SQ_BF16, out=labels)
+    ev[1].record()
+    ev[2].record()
+    for _ in range(args.steps):
+        si, sz, off = argsort_labels(labels, K)
+        centroid_update_sorted(x, labels, res.centroids, sorted_idx=si, sizes=sz, offsets=off)
+    ev[3].record()
+    torch.cuda.synchronize()
+    assign_ms = ev[0].elapsed_time(ev[1]) / args.steps
+    update_ms = ev[2].elapsed_time(ev[3]) / args.steps
+    a_flops = 2.0 * B * N * K * D
+    a_bytes = B * N * D * 2 + B * N * 4 + B * K * D * 2
+    u_bytes = B * N * D * 2 + B * N * 4 + B * K * D * 4
+    return {
+        "metric": "flash_kmeans batched Lloyd ms (5 iterations) + % MFMA/HBM roofline",
+        "value": round(ms, 3),
+        "unit": "ms/loop",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (256-component Gaussian mixture, std 0.25, Dirichlet(1) weights, seeded, on device)",
+        "config": {"workload": "C2 standalone batched k-means: 24 x 118800 x 128 bf16, K=256, 5 Lloyd iters, "
+                               "first-k init", "batch": B, "points": N, "dim": D, "clusters": K,
+                   "iters": int(res.iters)},
+        # K = 256: 256 flop per byte, below the ~312 flop/B ridge, so the HBM floor is the higher one
+        "roofline": {"kernel": "kmeans_assign_resident_kernel<128> (K=256)", "bound": "hbm",
+                     "achieved": round(a_bytes / assign_ms / 1e6, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(a_bytes / assign_ms / 1e6 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel_ms": round(assign_ms, 4),
+                     "mfma_tflops": round(a_flops / assign_ms / 1e9, 1),
+                     "mfma_frac": round(a_flops / assign_ms / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "roofline_update": {"kernel": "label sort + centroid_mean_kernel (K=256)", "bound": "hbm",
+                            "achieved": round(u_bytes / update_ms / 1e6, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(u_bytes / update_ms / 1e6 / HBM_PEAK_GBS, 4),
+                            "kernel_ms": round(update_ms, 4)},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -255,75 +524,18 @@ def main():
         return only_role_proj(args)
     import torch
 
-    from sparsepr_amd import synthetic
-    from sparsepr_amd.layer import LayerTimings, SparsePRAttention, SparsePRConfig, dense_flops, kept_pair_flops
-
     torch.cuda.set_device(0)
-    shape = synthetic.HUNYUAN
-    q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **GEN)
-    cfg = SparsePRConfig(num_q_centroids=128, num_k_centroids=512, kmeans_iters=5, top_p=args.top_p,
-                         probe_rows=128, repair=not args.no_repair)
-    layer = SparsePRAttention(cfg)
-    for _ in range(args.warmup):
-        layer(q, k, v)
-    torch.cuda.synchronize()
-
-    marks = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        tm = LayerTimings()
-        layer(q, k, v, timings=tm)
-        marks.append(tm)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
-
-    names = list(marks[0].events)
-    stage_ms = {b: round(sum(m.ms(a, b) for m in marks) / len(marks), 3) for a, b in zip(names[:-1], names[1:])}
-    attn_ms = sum(m.ms("plan", "attention") for m in marks) / len(marks)
-    route = layer.last_route
-    kept = float(kept_pair_flops(route, shape.dim).item())
-    dens = float(route.base_video_density.item())
-    achieved = kept / (attn_ms * 1e-3) / 1e12
-    traffic = traffic_from_profiles()
-
-    result = {
-        "metric": METRIC,
-        "value": round(ms_per_step, 3),
-        "unit": "ms/layer",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 3),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (frame-correlated Gaussian mixture, seeded, generated on device)",
-        "config": {
-            "workload": "C4 HunyuanVideo-shaped SparsePR layer: 1x24x118800x128 bf16, Qc=128, Kc=512, "
-                        f"5 Lloyd iters, top-p {args.top_p}, " + ("no repair" if args.no_repair else "128 probes"),
-            "heads": shape.heads, "tokens": shape.tokens, "head_dim": shape.dim,
-            "kept_pair_density": round(dens, 4),
-            "kept_attention_tflop": round(kept / 1e12, 3),
-            "dense_attention_tflop": round(dense_flops(shape.heads, shape.tokens, shape.dim) / 1e12, 1),
-            "generator": GEN,
-        },
-        "stages_ms": stage_ms,
-        "roofline": {
-            "kernel": "attn_pipe_kernel (D=128 block-sparse attention)",
-            "bound": "mfma",
-            "achieved": round(achieved, 1),
-            "peak": MFMA_BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-            "traffic": traffic,
-            "kernel_ms": round(attn_ms, 3),
-        },
-    }
-    if not args.no_cpu_baseline and args.cpu_heads > 0:
-        result["cpu_baseline"] = cpu_baseline(q, k, v, cfg, args.cpu_heads)
-    print(json.dumps(result), flush=True)
+    if args.config == "c2":
+        print(json.dumps(bench_kmeans_c2(args)), flush=True)
+        return
+    if args.config == "c5" and args.top_p is None and not args.no_repair:
+        for repair in (True, False):
+            for top_p in (0.7, 0.8, 0.9, 0.95):
+                print(json.dumps(bench_layer(args, "c5", top_p=top_p, repair=repair, amp=args.amp)), flush=True)
+        return
+    res = bench_layer(args, args.config, top_p=args.top_p, repair=not args.no_repair, amp=args.amp,
+                      with_cpu=args.config in ("c1", "c4"))
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":

@@ -806,7 +806,7 @@ class LayerConfig:
     x_sq_mode: str = "bf16"
 
 
-def sparsepr_layer(q, k, v, cfg: LayerConfig, timings: dict | None = None, bf16=True):
+def sparsepr_layer(q, k, v, cfg: LayerConfig, timings: dict | None = None, bf16=True, attention="loop"):
     """One SparsePR attention layer on the CPU, float path of the oracle.
 
     Composition (wan22.py:2221-2276 for the route and attention, n8_v6.py:1174-1444
@@ -840,8 +840,12 @@ def sparsepr_layer(q, k, v, cfg: LayerConfig, timings: dict | None = None, bf16=
     k_idx = argsort_labels(k_labels)
     qp, kp, vp = permute_rows(q, q_idx), permute_rows(k, k_idx), permute_rows(v, k_idx)
     t = mark("permute", t)
-    o = block_sparse_attention_loop(qp[None], kp[None], vp[None], dmap[None],
-                                    q_sizes[None], k_sizes[None])[0]
+    if attention == "loop":  # dynamic_block_sparse_fwd_torch's block loop
+        o = block_sparse_attention_loop(qp[None], kp[None], vp[None], dmap[None],
+                                        q_sizes[None], k_sizes[None])[0]
+    else:  # the vectorized masked-dense variant of the same result
+        o = block_sparse_attention_dense(qp[None], kp[None], vp[None], dmap[None],
+                                         q_sizes[None], k_sizes[None])[0].astype(np.float32)
     if bf16:
         o = to_bf16(o)
     t = mark("attention", t)
