@@ -75,6 +75,16 @@ int spr_centroid_sq(const void* c, int32_t dtype, int64_t rows, int32_t d, float
 int spr_kmeans_assign_bf16(const void* x, const void* centroids, const float* c_sq, const float* x_sq,
                            int32_t x_sq_mode, float* x_sq_out, int64_t batch, int64_t n, int32_t k, int32_t d,
                            int32_t* labels, hipStream_t stream);
+/* assign_euclid_triton.py:803-1030 / kmeans_utils.py:775-893 on fp32 inputs, where
+ * tl.dot rounds both operands to TF32 (nearest, ties away): the role-space k-means of
+ * N8V6Core.route (n8_v6.py:719,790).  dist = max((x_sq + c_sq) - 2 tf32(x).tf32(c), 0)
+ *   with exact TF32 products summed in fp32, lowest index among exact minima.
+ *   x fp32 [batch, n, d], centroids fp32 [batch, k, d], c_sq fp32 [batch, k];
+ *   x_sq fp32 [batch, n] or NULL (inline: fp32 sum of the fp32 squares of x);
+ *   x_sq_out nullable as for spr_kmeans_assign_bf16; d in {16, 32, 48, 64, 128}. */
+int spr_kmeans_assign_tf32(const float* x, const float* centroids, const float* c_sq, const float* x_sq,
+                           float* x_sq_out, int64_t batch, int64_t n, int32_t k, int32_t d, int32_t* labels,
+                           hipStream_t stream);
 /* centroid_update_triton.py:316-386 triton_centroid_update_sorted_euclid,
  * centroid_reduction.py:138-196 original_centroids_triton, n8_ops.cu:255-269 finalize.
  *   Means of the rows of each cluster (sorted_idx/offsets from spr_argsort_labels), fp64

@@ -138,6 +138,24 @@ def kmeans_assign(x: np.ndarray, c: np.ndarray, x_sq: np.ndarray):
     return labels, dist
 
 
+def kmeans_assign_tf32(x: np.ndarray, c: np.ndarray, x_sq: np.ndarray | None = None):
+    """The flash-kmeans assign on fp32 inputs (assign_euclid_triton.py:863-917,
+    kmeans_utils.py:806-834): tl.dot rounds both fp32 operands to TF32 (nearest, ties
+    away), so cross = tf32(x) . tf32(c) with exact products (float64 sum here);
+    x_sq = fp32 sum of the fp32 squares of x (inline, kmeans_utils.py:812-814) unless
+    given; c_sq = fp32 sum of the fp32 squares of c ((centroids.float() ** 2).sum(-1));
+    dist = max(x_sq + c_sq - 2 cross, 0), lowest index among exact minima.
+    Returns (labels int32 [B, N], dist float64 [B, N, K], x_sq float32 [B, N])."""
+    x32 = np.ascontiguousarray(x, np.float32)
+    c32 = np.ascontiguousarray(c, np.float32)
+    if x_sq is None:
+        x_sq = (x32 * x32).astype(np.float64).sum(-1).astype(np.float32)
+    c_sq = (c32 * c32).astype(np.float64).sum(-1).astype(np.float32)
+    cross = np.matmul(tf32_rna(x32).astype(np.float64), np.swapaxes(tf32_rna(c32).astype(np.float64), 1, 2))
+    dist = np.maximum(x_sq.astype(np.float64)[:, :, None] + c_sq.astype(np.float64)[:, None, :] - 2.0 * cross, 0.0)
+    return np.argmin(dist, axis=-1).astype(np.int32), dist, x_sq
+
+
 def label_mismatches_are_ties(labels_gpu, labels_ref, dist, x_sq, c, rel_tol):
     """True if every label disagreement is between centroids whose exact
     distances differ by at most rel_tol * (x_sq + c_sq) (the scale at which the

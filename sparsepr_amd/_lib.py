@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_centroid_mean": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                          _vp, _vp, _sz, _vp]),
     "spr_role_assign_fp32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
+    "spr_kmeans_assign_tf32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     # select.hip
     "spr_topp_map": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _f32, _i32, _i32, _vp, _vp, _vp]),
     "spr_select_budget": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),

@@ -187,6 +187,186 @@ __global__ __launch_bounds__(ASSIGN_THREADS, 2) void kmeans_assign_bf16_kernel(
   }
 }
 
+// fp32 x -> TF32 (10 stored mantissa bits), nearest with ties away from zero: the
+// operand rounding of tl.dot on fp32 inputs (input_precision "tf32", Triton's default).
+__device__ __forceinline__ uint32_t tf32_rna_bits(float v) { return (__float_as_uint(v) + 0x1000u) & 0xFFFFE000u; }
+
+// A TF32 value t as two bf16 halves with hi + lo = t exactly: hi keeps the sign,
+// exponent and top 7 mantissa bits (t's upper 16 bits), lo = t - hi has at most 3
+// significant bits, so it is a bf16 value too.  Products of halves are exact in fp32,
+// and hi*hi + hi*lo + lo*hi + lo*lo is the exact product of two TF32 values.
+__device__ __forceinline__ void tf32_split(float v, uint32_t& hi16, uint32_t& lo16) {
+  const uint32_t t = tf32_rna_bits(v);
+  const float hi = __uint_as_float(t & 0xFFFF0000u);
+  const float lo = __uint_as_float(t) - hi;  // exact
+  hi16 = t >> 16;
+  lo16 = __float_as_uint(lo) >> 16;  // exact: lo has <= 3 significant bits
+}
+
+// labels = argmin_k max((x_sq + c_sq) - 2 x.c, 0) for fp32 x and centroids, with the
+// dot product of their TF32 roundings (exact products, fp32 accumulation): the
+// flash-kmeans assign on fp32 inputs (assign_euclid_triton.py:897, kmeans_utils.py:829).
+// x_sq (when not given) is the fp32 sum of the fp32 squares of x itself
+// (kmeans_utils.py:812-814).  The layout follows kmeans_assign_bf16_kernel: 256 points
+// per workgroup, 64-centroid LDS tiles (hi and lo halves), v_mfma_f32_32x32x16_bf16,
+// four products per 16-dim step.
+template <int D>
+__global__ __launch_bounds__(ASSIGN_THREADS, D > 64 ? 1 : 2) void kmeans_assign_tf32_kernel(
+    const float* __restrict__ x, const float* __restrict__ c, const float* __restrict__ c_sq,
+    const float* __restrict__ x_sq_in, float* __restrict__ x_sq_out, int64_t n, int32_t k,
+    int32_t* __restrict__ labels) {
+  static_assert(D % 16 == 0 && D <= 128, "D must be a multiple of 16, at most 128");
+  constexpr int KSTEPS = D / 16;
+  constexpr int ROW_BYTES = D * 2 + 16;     // padded bf16 LDS row
+  constexpr int QUADS = CCHUNK * D / 4;     // 4-float pieces per centroid tile
+  constexpr int QUADS_PER_THREAD = QUADS / ASSIGN_THREADS;
+  static_assert(QUADS % ASSIGN_THREADS == 0, "tile pieces must divide evenly");
+
+  __shared__ __attribute__((aligned(16))) uint8_t tile_hi[2][CCHUNK * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t tile_lo[2][CCHUNK * ROW_BYTES];
+  __shared__ float tile_csq[2][CCHUNK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const int64_t b = blockIdx.y;
+  const float* xb = x + b * n * D;
+  const float* cb = c + static_cast<int64_t>(b) * k * D;
+  const float* csqb = c_sq + static_cast<int64_t>(b) * k;
+
+  // ---- points of this lane: two fragments of 32 points, 8 dims per k-step
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * ASSIGN_POINTS + wave * ASSIGN_POINTS_PER_WAVE + col;
+  u32x4 xh[2][KSTEPS], xl[2][KSTEPS];
+  float xsq[2];
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const int64_t p = p0 + 32 * f;
+    const bool live = p < n;
+    float part = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      const spr::f32x4* src = reinterpret_cast<const spr::f32x4*>(xb + p * D + s * 16 + half * 8);
+      const spr::f32x4 v0 = live ? src[0] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const spr::f32x4 v1 = live ? src[1] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const float e[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      uint32_t h[8], l[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        tf32_split(e[u], h[u], l[u]);
+        part = __fadd_rn(part, __fmul_rn(e[u], e[u]));
+      }
+      xh[f][s] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      xl[f][s] = u32x4{l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16)};
+    }
+    const float other = __shfl_xor(part, 32, 64);
+    float total = part + other;
+    if (x_sq_in != nullptr) {
+      total = live ? x_sq_in[b * n + p] : 0.0f;
+    } else if (x_sq_out != nullptr && live && half == 0) {
+      x_sq_out[b * n + p] = total;
+    }
+    xsq[f] = total;
+  }
+
+  float best[2] = {3.4e38f, 3.4e38f};
+  int32_t best_idx[2] = {0, 0};
+  const int nchunks = static_cast<int>((k + CCHUNK - 1) / CCHUNK);
+  spr::f32x4 pre[QUADS_PER_THREAD];
+  float pre_csq = 0.0f;
+
+  auto fetch = [&](int chunk) {
+#pragma unroll
+    for (int i = 0; i < QUADS_PER_THREAD; ++i) {
+      const int quad = tid + i * ASSIGN_THREADS;
+      const int row = quad / (D / 4);
+      const int vec = quad % (D / 4);
+      const int64_t cidx = static_cast<int64_t>(chunk) * CCHUNK + row;
+      pre[i] = cidx < k ? *reinterpret_cast<const spr::f32x4*>(cb + cidx * D + vec * 4)
+                        : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    if (tid < CCHUNK) {
+      const int64_t cidx = static_cast<int64_t>(chunk) * CCHUNK + tid;
+      pre_csq = cidx < k ? csqb[cidx] : __builtin_huge_valf();  // padding centroids never win
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < QUADS_PER_THREAD; ++i) {
+      const int quad = tid + i * ASSIGN_THREADS;
+      const int row = quad / (D / 4);
+      const int vec = quad % (D / 4);
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) tf32_split(pre[i][u], h[u], l[u]);
+      *reinterpret_cast<uint2*>(&tile_hi[buf][row * ROW_BYTES + vec * 8]) = uint2{h[0] | (h[1] << 16),
+                                                                                  h[2] | (h[3] << 16)};
+      *reinterpret_cast<uint2*>(&tile_lo[buf][row * ROW_BYTES + vec * 8]) = uint2{l[0] | (l[1] << 16),
+                                                                                  l[2] | (l[3] << 16)};
+    }
+    if (tid < CCHUNK) tile_csq[buf][tid] = pre_csq;
+  };
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+
+  for (int chunk = 0; chunk < nchunks; ++chunk) {
+    const int buf = chunk & 1;
+    if (chunk + 1 < nchunks) fetch(chunk + 1);
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      spr::f32x16 acc0 = {}, acc1 = {};
+      const int roff = (blk * 32 + col) * ROW_BYTES + half * 16;
+#pragma unroll
+      for (int s = 0; s < KSTEPS; ++s) {
+        const spr::bf16x8 ah = spr::as_bf16x8(*reinterpret_cast<const u32x4*>(&tile_hi[buf][roff + s * 32]));
+        const spr::bf16x8 al = spr::as_bf16x8(*reinterpret_cast<const u32x4*>(&tile_lo[buf][roff + s * 32]));
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xh[0][s]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xh[1][s]), acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xl[0][s]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xl[1][s]), acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xh[0][s]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xh[1][s]), acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xl[0][s]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xl[1][s]), acc1, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int local = blk * 32 + 8 * i + 4 * half + j;
+          const int32_t cidx = chunk * CCHUNK + local;
+          const float csq = tile_csq[buf][local];
+          const float d0 = fmaxf(__builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq)), 0.0f);
+          const float d1 = fmaxf(__builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq)), 0.0f);
+          const bool t0 = d0 < best[0];
+          const bool t1 = d1 < best[1];
+          best[0] = t0 ? d0 : best[0];
+          best_idx[0] = t0 ? cidx : best_idx[0];
+          best[1] = t1 ? d1 : best[1];
+          best_idx[1] = t1 ? cidx : best_idx[1];
+        }
+      }
+    }
+    if (chunk + 1 < nchunks) stash(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int f = 0; f < 2; ++f) {
+    const float od = __shfl_xor(best[f], 32, 64);
+    const int32_t oi = __shfl_xor(best_idx[f], 32, 64);
+    if (od < best[f] || (od == best[f] && oi < best_idx[f])) {
+      best[f] = od;
+      best_idx[f] = oi;
+    }
+    const int64_t p = p0 + 32 * f;
+    if (half == 0 && p < n) labels[b * n + p] = best_idx[f];
+  }
+}
+
 // c_sq[b, k] = sum_d float(c)^2 in fp32, sequential over d.
 template <typename T>
 __global__ void centroid_sq_kernel(const T* __restrict__ c, int64_t rows, int32_t d, float* __restrict__ out) {
@@ -680,6 +860,35 @@ extern "C" int spr_kmeans_assign_bf16(const void* x, const void* centroids, cons
       SPR_REQUIRE(false, "spr_kmeans_assign_bf16: head dim %d not supported (64, 128)", d);
   }
   SPR_LAUNCHED("kmeans_assign_bf16_kernel");
+  return SPR_OK;
+}
+
+// labels[b, i] = argmin_k max((x_sq + c_sq) - 2 tf32(x).tf32(c), 0) for fp32 x [b, n, d]
+// and centroids [b, k, d], fp32 c_sq [b, k]; x_sq fp32 [b, n] or null (inline fp32).
+extern "C" int spr_kmeans_assign_tf32(const float* x, const float* centroids, const float* c_sq, const float* x_sq,
+                                      float* x_sq_out, int64_t batch, int64_t n, int32_t k, int32_t d,
+                                      int32_t* labels, hipStream_t stream) {
+  SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_kmeans_assign_tf32: bad size");
+  SPR_REQUIRE(batch <= 65535, "spr_kmeans_assign_tf32: batch %lld exceeds 65535", (long long)batch);
+  if (batch == 0 || n == 0) return SPR_OK;
+  SPR_REQUIRE(x && centroids && c_sq && labels, "spr_kmeans_assign_tf32: null pointer");
+  SPR_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(centroids) % 16 == 0,
+              "spr_kmeans_assign_tf32: x and centroids must be 16-byte aligned");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, ASSIGN_POINTS)), static_cast<uint32_t>(batch));
+#define SPR_TF32_ASSIGN(DD)                                                                                    \
+  kmeans_assign_tf32_kernel<DD><<<grid, ASSIGN_THREADS, 0, stream>>>(x, centroids, c_sq, x_sq, x_sq_out, n, k, \
+                                                                     labels)
+  switch (d) {
+    case 16: SPR_TF32_ASSIGN(16); break;
+    case 32: SPR_TF32_ASSIGN(32); break;
+    case 48: SPR_TF32_ASSIGN(48); break;
+    case 64: SPR_TF32_ASSIGN(64); break;
+    case 128: SPR_TF32_ASSIGN(128); break;
+    default:
+      SPR_REQUIRE(false, "spr_kmeans_assign_tf32: feature dim %d not supported (16, 32, 48, 64, 128)", d);
+  }
+#undef SPR_TF32_ASSIGN
+  SPR_LAUNCHED("kmeans_assign_tf32_kernel");
   return SPR_OK;
 }
 

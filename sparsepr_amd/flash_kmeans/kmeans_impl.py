@@ -3,7 +3,8 @@
 One iteration is four launches and no host synchronisation (unless tol > 0):
   1. c_sq = ||c||^2 (fp32)                       spr_centroid_sq
   2. labels = argmin distance (bf16 MFMA)         spr_kmeans_assign_bf16
-     or the exact-FP32 assign for fp32 inputs    spr_role_assign_fp32
+     or, for fp32 inputs, with the TF32 dot      spr_kmeans_assign_tf32
+     products the reference's tl.dot forms
   3. stable counting sort of the labels           spr_argsort_labels
   4. segmented fp64 mean -> new centroids         spr_centroid_mean
 The sort of step 3 in the last iteration is exactly argsort(final labels), so
@@ -86,8 +87,13 @@ def euclid_assign(x: torch.Tensor, centroids: torch.Tensor, x_sq: torch.Tensor |
                   _lib.ptr(xs), int(x_sq_mode), _lib.ptr(x_sq_out if xs is None else None), B, N, K, D,
                   _lib.ptr(out), _lib.stream(dev))
     elif x.dtype == torch.float32:
-        _lib.call("spr_role_assign_fp32", _lib.ptr(xc), _lib.ptr(cc), B, N, K, D, _lib.ptr(out), None,
-                  _lib.stream(dev))
+        # tl.dot on fp32 operands rounds them to TF32 (assign_euclid_triton.py:897,
+        # kmeans_utils.py:829); the products and the fp32 sums are otherwise exact
+        if c_sq is None:
+            c_sq = centroid_sq(cc)
+        xs = None if x_sq is None else x_sq.to(torch.float32).contiguous()
+        _lib.call("spr_kmeans_assign_tf32", _lib.ptr(xc), _lib.ptr(cc), _lib.ptr(c_sq.contiguous()), _lib.ptr(xs),
+                  _lib.ptr(x_sq_out if xs is None else None), B, N, K, D, _lib.ptr(out), _lib.stream(dev))
     else:
         raise RuntimeError(f"euclid_assign: unsupported dtype {x.dtype} (bfloat16 or float32)")
     return out
@@ -173,12 +179,12 @@ def lloyd(x: torch.Tensor, n_clusters: int, max_iters: int, tol: float = 0.0,
     labels = torch.empty((B, N), dtype=torch.int32, device=dev)
     # squared point norms: computed by the first assignment, reused afterwards
     cached_sq = None
-    if x_sq is None and x.dtype == torch.bfloat16 and max_iters > 1:
+    if x_sq is None and max_iters > 1:
         cached_sq = torch.empty((B, N), dtype=torch.float32, device=dev)
     res = None
     it = -1
     # centroid norms: computed once, then produced by each update for the next assignment
-    c_sq = centroid_sq(cent) if x.dtype == torch.bfloat16 else None
+    c_sq = centroid_sq(cent)
     for it in range(max_iters):
         if x_sq is None and cached_sq is not None and it > 0:
             euclid_assign(x, cent, cached_sq, x_sq_mode=x_sq_mode, c_sq=c_sq, out=labels)

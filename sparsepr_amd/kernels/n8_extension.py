@@ -36,12 +36,15 @@ def _check_role_inputs(features, centroids, max_clusters):
 def _role_step(features: torch.Tensor, centroids: torch.Tensor, max_clusters: int):
     """One exact FP32 Lloyd step: assign, sizes, means (n8_ops.cu:499-529)."""
     _check_role_inputs(features, centroids, max_clusters)
-    from ..flash_kmeans.kmeans_impl import centroid_update_sorted, euclid_assign
+    from ..flash_kmeans.kmeans_impl import centroid_update_sorted
     from .permute import argsort_labels
 
     bh, n, d = features.shape
     c = centroids.shape[1]
-    labels = euclid_assign(features, centroids)
+    labels = torch.empty((bh, n), dtype=torch.int32, device=features.device)
+    # exact FP32 distances, sequential fmaf over the dims (n8_ops.cu:189-253), not TF32
+    _lib.call("spr_role_assign_fp32", _lib.ptr(features), _lib.ptr(centroids), bh, n, c, d, _lib.ptr(labels), None,
+              _lib.stream(features.device))
     idx, sizes, offsets = argsort_labels(labels, c)
     res = centroid_update_sorted(features, labels, centroids, sorted_idx=idx, sizes=sizes, offsets=offsets)
     return [labels, res.centroids, sizes]

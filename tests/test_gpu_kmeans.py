@@ -253,6 +253,52 @@ def test_kmeans_full_size_properties(dev):
     assert bool(((best - dd.min(2).values) <= 1e-3 * dd.min(2).values + 1e-3).all())
 
 
+@pytest.mark.parametrize("b,n,k,d", [(2, 3000, 300, 64), (2, 2500, 1000, 48), (1, 777, 37, 16), (1, 1000, 64, 32),
+                                     (1, 600, 70, 128)])
+def test_assign_tf32_matches_oracle_up_to_ties(dev, oracle, b, n, k, d):
+    """fp32 role-space features (the N8 route's shapes: rank 64 / 300 Q clusters, rank 48 /
+    1000 K clusters): TF32 products, fp32 norms, lowest index on ties."""
+    from sparsepr_amd.flash_kmeans.kmeans_impl import euclid_assign
+
+    rng = np.random.default_rng(n + k + d)
+    means = rng.standard_normal((b, max(k // 3, 2), d)).astype(np.float32)
+    x = (means[:, rng.integers(0, means.shape[1], n)] + 0.3 * rng.standard_normal((b, n, d))).astype(np.float32)
+    c = x[:, rng.permutation(n)[:k]].copy()
+    c[:, k // 2] = c[:, 1]  # an exact duplicate: the lower index wins
+    x_sq_out = torch.empty((b, n), device=dev)
+    labels = euclid_assign(to_dev(x, dev), to_dev(c, dev), x_sq_out=x_sq_out).cpu().numpy()
+    ref, dist, x_sq = oracle.kmeans_assign_tf32(x, c)
+    ok, nbad = oracle.label_mismatches_are_ties(labels, ref, dist, x_sq, c, TIE_REL)
+    assert ok, f"{nbad} label mismatches beyond tie tolerance"
+    assert nbad <= max(2, labels.size // 1000)
+    assert (labels != k // 2).all()
+    assert np.allclose(x_sq_out.cpu().numpy(), x_sq, rtol=1e-6)
+
+
+def test_lloyd_fp32_features_tf32(dev, oracle):
+    """The flash Lloyd loop on fp32 features, one iteration at a time: each iteration's labels
+    against the oracle's TF32 assignment from the same centroids, centroids the means."""
+    from sparsepr_amd.flash_kmeans.kmeans_impl import lloyd
+
+    rng = np.random.default_rng(23)
+    b, n, d, k = 2, 4000, 48, 200
+    means = rng.standard_normal((b, 60, d)).astype(np.float32)
+    x = (means[:, rng.integers(0, 60, n)] + 0.3 * rng.standard_normal((b, n, d))).astype(np.float32)
+    c = x[:, :k].copy()
+    xt = to_dev(x, dev)
+    cent = to_dev(c, dev)
+    for it in range(3):
+        res = lloyd(xt, k, 1, 0.0, cent)
+        ref, dist, x_sq = oracle.kmeans_assign_tf32(x, cent.cpu().numpy())
+        got = res.labels.cpu().numpy()
+        ok, nbad = oracle.label_mismatches_are_ties(got, ref, dist, x_sq, cent.cpu().numpy(), TIE_REL)
+        assert ok and nbad <= 2
+        new, mean32, _ = oracle.centroid_update(x, got, cent.cpu().numpy(), out_bf16=False)
+        # fp64 sums of fp32 rows: equal up to the last fp64 bit, so up to rare fp32 double rounding
+        assert np.allclose(res.centroids.cpu().numpy(), new, rtol=1e-6, atol=1e-7)
+        cent = res.centroids
+
+
 def test_role_step64_exact(dev, oracle):
     from sparsepr_amd.kernels.n8_extension import role_cluster_step_k64, role_cluster_step_q64
 

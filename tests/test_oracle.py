@@ -137,6 +137,38 @@ def test_assign_matches_brute_force_with_planted_ties(oracle):
     assert (labels != 4).all()
 
 
+def test_assign_tf32_brute_force_and_rounding_matters(oracle):
+    """kmeans_assign_tf32 against a loop with explicitly TF32-rounded operands, and a planted
+    point whose nearest centroid differs between TF32 and exact fp32 products (a dropped
+    rounding step fails the second check)."""
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((2, 30, 16)).astype(np.float32)
+    c = rng.standard_normal((2, 7, 16)).astype(np.float32)
+    labels, dist, x_sq = oracle.kmeans_assign_tf32(x, c)
+    for b in range(2):
+        for n in range(30):
+            xs = float(np.float32(sum(float(np.float32(v * v)) for v in x[b, n])))
+            best = None
+            for k in range(7):
+                xt, ct = oracle.tf32_rna(x[b, n]), oracle.tf32_rna(c[b, k])
+                cross = sum(float(a) * float(bb) for a, bb in zip(xt, ct))
+                cs = float(np.float32(sum(float(np.float32(v * v)) for v in c[b, k])))
+                d = max(xs + cs - 2.0 * cross, 0.0)
+                if best is None or d < best[0]:
+                    best = (d, k)
+            assert labels[b, n] == best[1]
+    # 1-D case: x = 1 + 1.25 * 2^-10 rounds to 1 + 2^-10 in TF32; centroids 1 and 1 + 2^-9.
+    # Exact products put x nearer 1 + 2^-9; with the TF32 cross term both distances equal
+    # x_sq - 1 - 2^-9, and the lower index, 0, wins.
+    xv = np.zeros((1, 1, 16), np.float32)
+    cv = np.zeros((1, 2, 16), np.float32)
+    xv[0, 0, 0] = 1 + 1.25 * 2 ** -10
+    cv[0, 0, 0], cv[0, 1, 0] = 1.0, 1 + 2 ** -9
+    tl, td, _ = oracle.kmeans_assign_tf32(xv, cv)
+    exact = ((xv[0, 0, 0].astype(np.float64) - cv[0, :, 0].astype(np.float64)) ** 2)
+    assert int(np.argmin(exact)) == 1 and tl[0, 0] == 0
+
+
 def test_x_sq_modes(oracle):
     rng = np.random.default_rng(2)
     x = _bf16_data(oracle, rng, (1, 16, 128))
