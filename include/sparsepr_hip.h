@@ -100,6 +100,18 @@ int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, c
                       const void* old, int64_t batch, int64_t n, int32_t k, int32_t d, float* mean32, void* out,
                       float* shift_max, float* sums_accum, int32_t* counts_accum, float* c_sq_out,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* operator_kmeans.py:609-679 original_centroids / joint_original_centroids, centroid_reduction.py:
+ * 138-196 original_centroids_triton / joint_original_centroids_triton: fp32 means of the rows of
+ * x (and of y, nullable, in the same traversal of the sorted index) per cluster, fp64 sums;
+ * an empty cluster takes its fp32 fallback row (x_fallback / y_fallback nullable: zeros).
+ *   x, y dtype 0 bf16 (d in {64, 128}) or 2 fp32 (d in {16, 32, 48, 64, 128}) [batch, n, d];
+ *   sorted_idx / offsets from spr_argsort_labels; x_out, y_out fp32 [batch, k, d];
+ *   workspace spr_original_centroids_workspace bytes (0 when no cluster is split). */
+size_t spr_original_centroids_workspace(int64_t batch, int64_t n, int32_t k, int32_t d);
+int spr_original_centroids(const void* x, const void* y, int32_t dtype, const int32_t* sorted_idx,
+                           const int32_t* offsets, int64_t batch, int64_t n, int32_t k, int32_t d,
+                           const float* x_fallback, const float* y_fallback, float* x_out, float* y_out,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* n8_ops.cu:198-253 role_cluster_assign_accumulate_q64_kernel (assignment part):
  *   exact FP32 distance (sequential fmaf), lowest index on ties; d in {16,32,48,64}.
  *   best_dist nullable. */
@@ -281,6 +293,47 @@ int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_sorted, const
                        float jensen_var_cap, const int32_t* k_sizes, int64_t q_heads, int32_t qn, int32_t kn,
                        int64_t kv_heads, int64_t t_stored, int32_t d, int32_t group, int32_t mode, float* scores,
                        hipStream_t stream);
+
+/* ---------------------------------------------------------------- N8 role metrics and factors
+ * operator_kmeans.py:62-92,491-498 covariance / key_metric_from_queries /
+ * value_metric_from_values (rows = deterministic_token_sample positions, :52-59) and
+ * :517-531 query_metric_from_key_centroids (sizes = cluster sizes, post_scale = 1 / d):
+ *   out fp32 [bh, d, d] = post_scale / max(used, 1) * sum over the used rows (x - mean)(x - mean)^T;
+ *   x dtype 0 bf16 / 2 fp32 [bh, n, d], d <= 128; rows int32 [count] shared by the heads
+ *   (nullable: all n rows); sizes int32 [bh, n] (nullable, only without rows): a row is used
+ *   only when its size is > 0; center = 1 subtracts the used rows' mean. */
+int spr_role_metric(const void* x, int32_t dtype, int64_t bh, int64_t n, int32_t d, const int32_t* rows,
+                    int32_t count, const int32_t* sizes, int32_t center, float post_scale, float* out,
+                    hipStream_t stream);
+/* torch.linalg.eigh for the top eigenpairs (operator_kmeans.py:115-118, residual_repair.py:468-506):
+ *   mats fp32 [bh, n, n] symmetric (symmetrize = 1: 0.5 (A + A^T)); vecs fp32 [bh, n, rank] the
+ *   eigenvectors of the rank largest eigenvalues in ascending order; vals fp32 [bh, rank]
+ *   (nullable) their Rayleigh quotients, ascending.  n <= 128, rank <= min(64, n).
+ *   Householder tridiagonalisation, multisection on Sturm counts, inverse iteration, Cholesky-QR. */
+int spr_sym_top_eig(const float* mats, int64_t bh, int32_t n, int32_t rank, int32_t symmetrize, float* vecs,
+                    float* vals, hipStream_t stream);
+/* operator_kmeans.py:95-151 metric_factor: factor fp32 [bh, n, rank] = top-rank eigenvectors of
+ * 0.5 (M + M^T), column c scaled by sqrt(max(lambda_c, 0) / max(mean max(lambda, 0), 1e-12));
+ * workspace spr_metric_factor_workspace(bh, rank) bytes (the eigenvalues). */
+size_t spr_metric_factor_workspace(int64_t bh, int32_t rank);
+int spr_metric_factor(const float* metric, int64_t bh, int32_t n, int32_t rank, float* factor, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+/* operator_kmeans.py:219-477 warm_subspace_metric_factor (+ n8_v6.py:478-519 _updated_factor's
+ * per-head recovery when prev_factor is given): metric fp32 [bh, n, n], prev_state fp32
+ * [bh, n, rank] (the previous basis), prev_factor fp32 [bh, n, rank] (nullable) -> factor,
+ * state fp32 [bh, n, rank], recovered uint8 [bh] (nullable).  ortho 0 each_cholesky_qr,
+ * 1 each_cholesky_qr2, 2 cholesky_qr; ritz 0 rayleigh_cholesky, 1 diagonal, 2 previous_scale.
+ * n <= 128, rank <= 64. */
+int spr_warm_metric_factor(const float* metric, const float* prev_state, const float* prev_factor, int64_t bh,
+                           int32_t n, int32_t rank, int32_t power_iters, int32_t ortho, int32_t ritz,
+                           float rayleigh_ridge, float cqr_ridge, float* factor, float* state, uint8_t* recovered,
+                           hipStream_t stream);
+/* operator_kmeans.py:534-555 project_tokens (+ normalize_rows_rms with row_rms = 1, eps 1e-6) and
+ * n8_v6.py:152-178 the compiled K-centroid projection (tf32 = 1, div = the key scale):
+ *   out fp32 [bh, m, r] = (x fp32 [bh, m, d] . factor fp32 [bh, d, r]) / div[h] (div nullable);
+ *   d <= 128, r <= 64. */
+int spr_project_rows(const float* x, const float* factor, const float* div, int64_t bh, int64_t m, int32_t d,
+                     int32_t r, int32_t tf32, int32_t row_rms, float eps, float* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -715,6 +715,131 @@ def _cluster_runs(sizes_row: np.ndarray, tokens: int):
     return starts, ends
 
 
+# ----------------------------------------------------------------------------
+# N8 role metrics and factors (models/cosmos3/operator_kmeans.py)
+# ----------------------------------------------------------------------------
+
+def role_metric(x, rows=None, sizes=None, center=False, post_scale=1.0):
+    """covariance / key_metric_from_queries / value_metric_from_values (operator_kmeans.py:62-92,
+    :491-498) on the sampled rows, and query_metric_from_key_centroids (:517-531) with
+    sizes (rows with size <= 0 are left out of the mean and the count) and post_scale 1/d.
+    out [BH, D, D] = post_scale / max(count, 1) * sum (x - mean)(x - mean)^T, float64."""
+    x = np.asarray(x, np.float64)
+    bh, n, d = x.shape
+    out = np.zeros((bh, d, d), np.float64)
+    for h in range(bh):
+        xs = x[h] if rows is None else x[h, np.asarray(rows, np.int64)]
+        if sizes is not None:
+            xs = xs[np.asarray(sizes[h]) > 0]
+        cnt = max(xs.shape[0], 1)
+        if center and xs.shape[0] > 0:
+            xs = xs - xs.sum(0) / cnt
+        out[h] = xs.T @ xs / cnt * post_scale
+    return out
+
+
+def metric_factor(metric, rank):
+    """operator_kmeans.py:95-151: eigh of 0.5 (M + M^T), the top `rank` eigenpairs (ascending),
+    eigenvalues clamped at 0, factor = V sqrt(lambda / max(mean lambda, 1e-12)).  float64."""
+    m = np.asarray(metric, np.float64)
+    m = 0.5 * (m + np.swapaxes(m, 1, 2))
+    w, v = np.linalg.eigh(m)
+    w = np.maximum(w[:, -rank:], 0.0)
+    v = v[:, :, -rank:]
+    norm = np.maximum(w.mean(1, keepdims=True), 1e-12)
+    return v * np.sqrt(w / norm)[:, None, :]
+
+
+def _cholesky_or_none(a):
+    try:
+        return np.linalg.cholesky(a)
+    except np.linalg.LinAlgError:
+        return None
+
+
+def _cholesky_qr(x, ridge):
+    """operator_kmeans.py:326-358 for one head: normalise the columns (norm clamped at 1e-12),
+    Gram + max(mean diag, 1e-12) * ridge I, lower Cholesky (identity on failure),
+    x L^-T.  Returns (basis, failed)."""
+    xn = x / np.maximum(np.linalg.norm(x, axis=0, keepdims=True), 1e-12)
+    g = xn.T @ xn
+    g = 0.5 * (g + g.T)
+    g = g + np.eye(g.shape[0]) * max(float(np.diag(g).mean()), 1e-12) * ridge
+    l = _cholesky_or_none(g)
+    if l is None:
+        return xn, True
+    return np.linalg.solve(l, xn.T).T, False
+
+
+def warm_subspace_metric_factor(metric, previous, rank, power_iters=2, orthogonalization="each_cholesky_qr2",
+                                ritz_mode="rayleigh_cholesky", rayleigh_ridge=1e-4, cholesky_qr_ridge=1e-5):
+    """operator_kmeans.py:219-477 restated in float64 for the Cholesky-QR orthogonalisations
+    and the rayleigh_cholesky / diagonal / previous_scale finishes.  previous [BH, D, r] is
+    the previous basis.  Returns (factor, basis, recovered bool [BH])."""
+    m_all = np.asarray(metric, np.float64)
+    prev_all = np.asarray(previous, np.float64)
+    bh = m_all.shape[0]
+    factors, bases, rec = [], [], np.zeros(bh, bool)
+    for h in range(bh):
+        m, prev = m_all[h], prev_all[h]
+        prev_scales = np.maximum(np.linalg.norm(prev, axis=0), 1e-12)
+        basis = prev / prev_scales
+        diag = None
+        failed = False
+        for it in range(power_iters):
+            applied = m @ basis
+            if ritz_mode == "diagonal" and it == power_iters - 1:
+                diag = (basis * applied).sum(0)
+            if orthogonalization == "cholesky_qr":
+                basis = applied / np.maximum(np.linalg.norm(applied, axis=0), 1e-12)
+                continue
+            basis, f = _cholesky_qr(applied, cholesky_qr_ridge)
+            failed |= f
+            if orthogonalization == "each_cholesky_qr2" and it == power_iters - 1:
+                basis, f = _cholesky_qr(basis, max(cholesky_qr_ridge, 1e-5))
+                failed |= f
+        if orthogonalization == "cholesky_qr":
+            basis, f = _cholesky_qr(basis, 1e-6)
+            failed |= f
+        if ritz_mode == "previous_scale":
+            factor = basis * prev_scales
+        elif ritz_mode == "diagonal":
+            ev = np.maximum(diag, 0.0)
+            factor = basis * np.sqrt(ev / max(ev.mean(), 1e-12))
+        else:
+            ray = basis.T @ (m @ basis)
+            ray = 0.5 * (ray + ray.T)
+            norm = max(float(np.diag(ray).mean()), 1e-12)
+            l = _cholesky_or_none(ray + np.eye(rank) * norm * rayleigh_ridge)
+            if l is None:
+                l = _cholesky_or_none(ray + np.eye(rank) * norm * max(1e-2, rayleigh_ridge))
+            if l is None:
+                l = np.eye(rank)
+                failed = True
+            factor = basis @ l / np.sqrt(norm)
+        failed |= not (np.isfinite(factor).all() and np.isfinite(basis).all())
+        factors.append(factor)
+        bases.append(basis)
+        rec[h] = failed
+    return np.stack(factors), np.stack(bases), rec
+
+
+def project_rows(x, factor, div=None, tf32=False, row_rms=False, eps=1e-6):
+    """project_tokens (operator_kmeans.py:534-538), optionally / a per-head divisor (the
+    compiled K-centroid projection, n8_v6.py:152-178, whose "high" precision rounds both fp32
+    operands to TF32) and normalize_rows_rms (:548-555).  float64 products."""
+    x = np.asarray(x, np.float32)
+    f = np.asarray(factor, np.float32)
+    if tf32:
+        x, f = tf32_rna(x), tf32_rna(f)
+    p = np.matmul(x.astype(np.float64), f.astype(np.float64))
+    if div is not None:
+        p = p / np.asarray(div, np.float64).reshape(-1, 1, 1)
+    if row_rms:
+        p = p / np.maximum(np.sqrt((p * p).mean(-1, keepdims=True)), eps)
+    return p
+
+
 def svg_ear_value_error_scores(qc, k_sorted, v_sorted, kc, vc, sizes, group, var_k_diag=None,
                                jensen_var_cap=0.0):
     """Log value-error routing scores (svg_ear.py:95-192 kernel, :453-531 wrapper).

@@ -41,6 +41,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_centroid_mean_workspace": (_sz, [_i64, _i64, _i32, _i32]),
     "spr_centroid_mean": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                          _vp, _vp, _sz, _vp]),
+    "spr_original_centroids_workspace": (_sz, [_i64, _i64, _i32, _i32]),
+    "spr_original_centroids": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp,
+                                              _vp, _sz, _vp]),
     "spr_role_assign_fp32": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp]),
     "spr_kmeans_assign_tf32": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     # select.hip
@@ -72,6 +75,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_rrr_fit_workspace": (_sz, [_i64]),
     "spr_rrr_fit": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _sz, _vp]),
+    "spr_sym_top_eig": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]),
+    # metric.hip
+    "spr_role_metric": (ctypes.c_int, [_vp, _i32, _i64, _i64, _i32, _vp, _i32, _vp, _i32, _f32, _vp, _vp]),
+    "spr_metric_factor_workspace": (_sz, [_i64, _i32]),
+    "spr_metric_factor": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _vp, _sz, _vp]),
+    "spr_warm_metric_factor": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _vp,
+                                              _vp, _vp, _vp]),
+    "spr_project_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
     # role_proj.hip
     "spr_role_projection_rms": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "spr_role_k_projection_workspace": (_sz, [_i64, _i64]),

@@ -863,6 +863,140 @@ extern "C" int spr_kmeans_assign_bf16(const void* x, const void* centroids, cons
   return SPR_OK;
 }
 
+namespace {
+
+// Original-space means of one or two tensors (x and, with JOINT, y) under one label
+// traversal: workgroup (cl * nsplit + sp, b) sums slice sp of cluster cl's rows (sorted
+// order) of x and y in fp64.  With nsplit == 1 it writes the fp32 means directly;
+// otherwise partial[b][cl][sp][2][D] holds the slice sums and original_mean_finalize_kernel
+// adds them in slice order.  Empty clusters take the fp32 fallback row, or 0 without one.
+template <typename T, int D, bool JOINT>
+__global__ __launch_bounds__(256) void original_mean_kernel(
+    const T* __restrict__ x, const T* __restrict__ y, const int32_t* __restrict__ sorted_idx,
+    const int32_t* __restrict__ offsets, int64_t n, int32_t k, int32_t nsplit, double* __restrict__ partial,
+    const float* __restrict__ x_fb, const float* __restrict__ y_fb, float* __restrict__ x_out,
+    float* __restrict__ y_out) {
+  constexpr int E = 16 / sizeof(T);
+  constexpr int VPR = D / E;
+  static_assert(D % E == 0 && VPR <= 256, "unsupported D");
+  constexpr int R = 256 / VPR;
+  constexpr int RPT = JOINT ? 8 : 16;
+  constexpr int NT = JOINT ? 2 : 1;
+  __shared__ double red[NT][R][D + 1];
+  const int tid = threadIdx.x;
+  const int v = tid % VPR;
+  const int rg = tid / VPR;
+  const int64_t b = blockIdx.y;
+  const int32_t cl = blockIdx.x / nsplit;
+  const int32_t sp = blockIdx.x - cl * nsplit;
+  const int32_t* off = offsets + b * (k + 1);
+  const int32_t n32 = static_cast<int32_t>(n);
+  const int32_t c_start = min(max(off[cl], 0), n32);
+  const int32_t c_end = min(max(off[cl + 1], c_start), n32);
+  const int32_t slice = (c_end - c_start + nsplit - 1) / nsplit;
+  const int32_t start = min(c_start + sp * slice, c_end);
+  const int32_t end = min(start + slice, c_end);
+  const int32_t* idx = sorted_idx + b * n;
+  const T* src[2] = {x + b * n * D, JOINT ? y + b * n * D : nullptr};
+
+  double acc[NT][E];
+#pragma unroll
+  for (int q = 0; q < NT; ++q)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[q][e] = 0.0;
+  auto add_vec = [&](int q, const u32x4& w) {
+    if constexpr (sizeof(T) == 2) {
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[q][2 * e] += static_cast<double>(spr::bf16_lo(ws[e]));
+        acc[q][2 * e + 1] += static_cast<double>(spr::bf16_hi(ws[e]));
+      }
+    } else {
+      acc[q][0] += static_cast<double>(__uint_as_float(w.x));
+      acc[q][1] += static_cast<double>(__uint_as_float(w.y));
+      acc[q][2] += static_cast<double>(__uint_as_float(w.z));
+      acc[q][3] += static_cast<double>(__uint_as_float(w.w));
+    }
+  };
+  const bool worker = rg < R;
+  constexpr int STEP = R * RPT;
+  int32_t ix[RPT];
+  auto load_ix = [&](int32_t base) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int32_t r = base + rg + R * i;
+      ix[i] = (worker && r < end) ? idx[r] : -1;
+    }
+  };
+  load_ix(start);
+  for (int32_t base = start; base < end; base += STEP) {
+    u32x4 w[NT][RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const uint32_t t = static_cast<uint32_t>(ix[i]);
+#pragma unroll
+      for (int q = 0; q < NT; ++q)
+        w[q][i] = t < static_cast<uint32_t>(n32)
+                      ? reinterpret_cast<const u32x4*>(src[q] + static_cast<int64_t>(t) * D)[v]
+                      : u32x4{0, 0, 0, 0};
+    }
+    if (base + STEP < end) load_ix(base + STEP);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+#pragma unroll
+      for (int q = 0; q < NT; ++q) add_vec(q, w[q][i]);
+  }
+  if (worker) {
+#pragma unroll
+    for (int q = 0; q < NT; ++q)
+#pragma unroll
+      for (int e = 0; e < E; ++e) red[q][rg][v * E + e] = acc[q][e];
+  }
+  __syncthreads();
+  if (tid < D) {
+    const int32_t count = c_end - c_start;
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+      double s = 0.0;
+      for (int g = 0; g < R; ++g) s += red[q][g][tid];
+      if (nsplit > 1) {
+        partial[(((b * k + cl) * nsplit + sp) * 2 + q) * D + tid] = s;
+      } else {
+        const float* fb = q == 0 ? x_fb : y_fb;
+        float* o = q == 0 ? x_out : y_out;
+        const int64_t at = (b * k + cl) * D + tid;
+        o[at] = count > 0 ? static_cast<float>(s / static_cast<double>(count)) : (fb != nullptr ? fb[at] : 0.0f);
+      }
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void original_mean_finalize_kernel(
+    const double* __restrict__ partial, const int32_t* __restrict__ offsets, int64_t n, int32_t k, int32_t nsplit,
+    int32_t ntensors, const float* __restrict__ x_fb, const float* __restrict__ y_fb, float* __restrict__ x_out,
+    float* __restrict__ y_out) {
+  const int64_t b = blockIdx.y;
+  const int32_t cl = blockIdx.x;
+  const int32_t* off = offsets + b * (k + 1);
+  const int32_t n32 = static_cast<int32_t>(n);
+  const int32_t c_start = min(max(off[cl], 0), n32);
+  const int32_t c_end = min(max(off[cl + 1], c_start), n32);
+  const int32_t count = c_end - c_start;
+  for (int e = threadIdx.x; e < ntensors * D; e += blockDim.x) {
+    const int q = e / D, c = e - q * D;
+    double s = 0.0;
+    for (int sp = 0; sp < nsplit; ++sp) s += partial[(((b * k + cl) * nsplit + sp) * 2 + q) * D + c];
+    const float* fb = q == 0 ? x_fb : y_fb;
+    float* o = q == 0 ? x_out : y_out;
+    const int64_t at = (b * k + cl) * D + c;
+    o[at] = count > 0 ? static_cast<float>(s / static_cast<double>(count)) : (fb != nullptr ? fb[at] : 0.0f);
+  }
+}
+
+}  // namespace
+
 // labels[b, i] = argmin_k max((x_sq + c_sq) - 2 tf32(x).tf32(c), 0) for fp32 x [b, n, d]
 // and centroids [b, k, d], fp32 c_sq [b, k]; x_sq fp32 [b, n] or null (inline fp32).
 extern "C" int spr_kmeans_assign_tf32(const float* x, const float* centroids, const float* c_sq, const float* x_sq,
@@ -889,6 +1023,74 @@ extern "C" int spr_kmeans_assign_tf32(const float* x, const float* centroids, co
   }
 #undef SPR_TF32_ASSIGN
   SPR_LAUNCHED("kmeans_assign_tf32_kernel");
+  return SPR_OK;
+}
+
+static int32_t mean_splits(int64_t n, int32_t k);
+
+extern "C" size_t spr_original_centroids_workspace(int64_t batch, int64_t n, int32_t k, int32_t d) {
+  const int32_t ns = mean_splits(n, k);
+  return ns > 1 ? static_cast<size_t>(batch * k * ns * 2 * static_cast<int64_t>(d) * sizeof(double)) : 0;
+}
+
+// fp32 means of x (and y, nullable) rows per cluster from a stable label sort (sorted_idx,
+// offsets of spr_argsort_labels); empty clusters take the fp32 fallback rows (nullable: 0).
+// dtype 0 bf16 (d in {64, 128}) or 2 fp32 (d in {16, 32, 48, 64, 128}); y has x's dtype.
+extern "C" int spr_original_centroids(const void* x, const void* y, int32_t dtype, const int32_t* sorted_idx,
+                                      const int32_t* offsets, int64_t batch, int64_t n, int32_t k, int32_t d,
+                                      const float* x_fallback, const float* y_fallback, float* x_out, float* y_out,
+                                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  SPR_REQUIRE(batch >= 0 && n >= 0 && k >= 1, "spr_original_centroids: bad size");
+  SPR_REQUIRE(batch <= 65535, "spr_original_centroids: batch %lld exceeds 65535", (long long)batch);
+  SPR_REQUIRE((y == nullptr) == (y_out == nullptr), "spr_original_centroids: y and y_out go together");
+  if (batch == 0) return SPR_OK;
+  SPR_REQUIRE(sorted_idx && offsets && x_out, "spr_original_centroids: null pointer");
+  SPR_REQUIRE(n == 0 || x, "spr_original_centroids: null x");
+  const int32_t ns = mean_splits(n, k);
+  const size_t need = spr_original_centroids_workspace(batch, n, k, d);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+    spr_set_error("spr_original_centroids: workspace %zu < %zu bytes", workspace_bytes, need);
+    return SPR_EWORKSPACE;
+  }
+  SPR_REQUIRE(static_cast<int64_t>(k) * ns < (int64_t(1) << 31), "spr_original_centroids: too many clusters");
+  double* partial = static_cast<double*>(workspace);
+  dim3 grid(static_cast<uint32_t>(k * ns), static_cast<uint32_t>(batch));
+  dim3 fgrid(static_cast<uint32_t>(k), static_cast<uint32_t>(batch));
+  const int ntensors = y != nullptr ? 2 : 1;
+#define SPR_ORIG_CASE(T, DD)                                                                                      \
+  do {                                                                                                            \
+    if (y != nullptr)                                                                                             \
+      original_mean_kernel<T, DD, true><<<grid, 256, 0, stream>>>(                                                \
+          static_cast<const T*>(x), static_cast<const T*>(y), sorted_idx, offsets, n, k, ns, partial, x_fallback, \
+          y_fallback, x_out, y_out);                                                                              \
+    else                                                                                                          \
+      original_mean_kernel<T, DD, false><<<grid, 256, 0, stream>>>(static_cast<const T*>(x), nullptr, sorted_idx, \
+                                                                   offsets, n, k, ns, partial, x_fallback,       \
+                                                                   nullptr, x_out, nullptr);                     \
+    if (ns > 1)                                                                                                   \
+      original_mean_finalize_kernel<DD><<<fgrid, 256, 0, stream>>>(partial, offsets, n, k, ns, ntensors,          \
+                                                                   x_fallback, y_fallback, x_out, y_out);         \
+  } while (0)
+  if (dtype == 0) {
+    switch (d) {
+      case 64: SPR_ORIG_CASE(uint16_t, 64); break;
+      case 128: SPR_ORIG_CASE(uint16_t, 128); break;
+      default: SPR_REQUIRE(false, "spr_original_centroids: bf16 dim %d not supported (64, 128)", d);
+    }
+  } else if (dtype == 2) {
+    switch (d) {
+      case 16: SPR_ORIG_CASE(float, 16); break;
+      case 32: SPR_ORIG_CASE(float, 32); break;
+      case 48: SPR_ORIG_CASE(float, 48); break;
+      case 64: SPR_ORIG_CASE(float, 64); break;
+      case 128: SPR_ORIG_CASE(float, 128); break;
+      default: SPR_REQUIRE(false, "spr_original_centroids: fp32 dim %d not supported (16, 32, 48, 64, 128)", d);
+    }
+  } else {
+    SPR_REQUIRE(false, "spr_original_centroids: unsupported dtype %d", dtype);
+  }
+#undef SPR_ORIG_CASE
+  SPR_LAUNCHED("original_mean_kernel");
   return SPR_OK;
 }
 

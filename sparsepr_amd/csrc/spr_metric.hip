@@ -1,0 +1,592 @@
+// Role metrics and their factors for the N8 router (N8V6Core.route).
+//
+// Replaces (src/sparsepr/models/cosmos3/operator_kmeans.py):
+//   covariance / key_metric_from_queries / value_metric_from_values (:62-92, :491-498)
+//   query_metric_from_key_centroids (:517-531)
+//   metric_factor (:95-151)
+//   warm_subspace_metric_factor with each_cholesky_qr(2) / cholesky_qr and the
+//     rayleigh_cholesky, diagonal and previous_scale finishes (:219-477),
+//     cholesky_with_device_fallback (:154-216)
+//   project_tokens / normalize_rows_rms and the compiled K-centroid projection
+//     (:534-555; src/sparsepr/models/common/n8_v6.py:141-178)
+// and the per-head recovery of N8V6Core._updated_factor (n8_v6.py:478-519).
+//
+// role_metric_kernel   out = post_scale / count * sum over the used rows of (x - mean)(x - mean)^T,
+//                      one 32 x 32 output tile per workgroup, rows staged in LDS, fp32.
+// warm_factor_kernel   one 1024-thread workgroup per head with the metric (128 x 128), the basis
+//                      and its image in LDS: metric . basis products, column normalisation,
+//                      Gram, Cholesky (one wave), triangular solves, Rayleigh matrix, fallback
+//                      Cholesky, all fp32.
+// factor_scale_kernel  eigenvectors x sqrt(max(lambda, 0) / max(mean lambda, 1e-12)).
+// project_rows_kernel  one wave per row: p = x . F (fp32, or both operands rounded to TF32 as
+//                      a "high"-precision fp32 matmul does), / a per-head divisor, optional
+//                      row-RMS normalisation.
+#include "spr_common.h"
+
+extern "C" int spr_sym_top_eig(const float* mats, int64_t bh, int32_t n, int32_t rank, int32_t symmetrize,
+                               float* vecs, float* vals, hipStream_t stream);
+
+namespace {
+
+constexpr int MET_MAX_D = 128;
+constexpr int MET_MAX_R = 64;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_read(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// Sum over the wave, uniform result.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x124>(v);  // row_ror 4
+  v += dpp_mov<0x128>(v);  // row_ror 8
+  return (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
+}
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+__device__ __forceinline__ float tf32_rna(float v) {
+  return __uint_as_float((__float_as_uint(v) + 0x1000u) & 0xFFFFE000u);
+}
+
+template <typename T>
+__device__ __forceinline__ float load_f32(const T* p);
+template <>
+__device__ __forceinline__ float load_f32<uint16_t>(const uint16_t* p) {
+  return __uint_as_float(static_cast<uint32_t>(*p) << 16);
+}
+template <>
+__device__ __forceinline__ float load_f32<float>(const float* p) {
+  return *p;
+}
+
+// ---------------------------------------------------------------- covariance
+// grid (bh, tiles^2): tile (ti, tj) of the d x d output; rows used: rows[0 .. count) when
+// rows is given (the same positions for every head), else all n rows, each only when
+// sizes[h, r] > 0 (sizes nullable).
+template <typename T>
+__global__ __launch_bounds__(256) void role_metric_kernel(const T* __restrict__ x, int64_t n, int32_t d,
+                                                          const int32_t* __restrict__ rows, int32_t count,
+                                                          const int32_t* __restrict__ sizes, int32_t center,
+                                                          float post_scale, float* __restrict__ out) {
+  constexpr int RB = 64;  // rows per LDS stage
+  __shared__ float ta[RB][33];
+  __shared__ float tb[RB][33];
+  __shared__ float mean_a[32], mean_b[32];
+  __shared__ int32_t used_s;
+  const int t = threadIdx.x;
+  const int64_t h = blockIdx.x;
+  const int tiles = (d + 31) / 32;
+  const int ti = blockIdx.y / tiles, tj = blockIdx.y % tiles;
+  const T* xh = x + h * n * d;
+  const int32_t* sz = sizes != nullptr ? sizes + h * n : nullptr;
+  const int64_t total = rows != nullptr ? count : n;
+  auto row_of = [&](int64_t r) -> int64_t { return rows != nullptr ? rows[r] : r; };
+  auto valid = [&](int64_t r) -> bool { return sz == nullptr || sz[r] > 0; };
+
+  // column means over the used rows (sequential per column), and the used-row count
+  if (!center && sz == nullptr) {
+    if (t < 32) {
+      mean_a[t] = 0.0f;
+      mean_b[t] = 0.0f;
+    }
+    if (t == 0) used_s = static_cast<int32_t>(total);
+  } else if (t < 64) {
+    const int cc = t & 31;
+    const int col = (t < 32 ? 32 * ti : 32 * tj) + cc;
+    float s = 0.0f;
+    int32_t used = 0;
+    for (int64_t r = 0; r < total; ++r) {
+      const int64_t row = row_of(r);
+      if (!valid(row)) continue;
+      ++used;
+      if (center && col < d) s += load_f32(xh + row * d + col);
+    }
+    const float cnt = static_cast<float>(used > 0 ? used : 1);
+    const float m = center && col < d ? s / cnt : 0.0f;
+    if (t < 32) mean_a[cc] = m; else mean_b[cc] = m;
+    if (t == 0) used_s = used;
+  }
+  __syncthreads();
+  const int a = t >> 4, b = t & 15;  // outputs (2a, 2a + 1) x (2b, 2b + 1) of the tile
+  float s00 = 0.0f, s01 = 0.0f, s10 = 0.0f, s11 = 0.0f;
+  for (int64_t r0 = 0; r0 < total; r0 += RB) {
+    for (int e = t; e < RB * 32; e += 256) {
+      const int rr = e >> 5, cc = e & 31;
+      const int64_t r = r0 + rr;
+      float va = 0.0f, vb = 0.0f;
+      if (r < total) {
+        const int64_t row = row_of(r);
+        if (valid(row)) {
+          const int ca = 32 * ti + cc, cb = 32 * tj + cc;
+          if (ca < d) va = load_f32(xh + row * d + ca) - mean_a[cc];
+          if (cb < d) vb = load_f32(xh + row * d + cb) - mean_b[cc];
+        }
+      }
+      ta[rr][cc] = va;
+      tb[rr][cc] = vb;
+    }
+    __syncthreads();
+    const int rows_here = static_cast<int>(total - r0 < RB ? total - r0 : RB);
+    for (int rr = 0; rr < rows_here; ++rr) {
+      const float u0 = ta[rr][2 * a], u1 = ta[rr][2 * a + 1];
+      const float v0 = tb[rr][2 * b], v1 = tb[rr][2 * b + 1];
+      s00 = __builtin_fmaf(u0, v0, s00);
+      s01 = __builtin_fmaf(u0, v1, s01);
+      s10 = __builtin_fmaf(u1, v0, s10);
+      s11 = __builtin_fmaf(u1, v1, s11);
+    }
+    __syncthreads();
+  }
+  const float cnt = static_cast<float>(used_s > 0 ? used_s : 1);
+  const float acc[2][2] = {{s00, s01}, {s10, s11}};
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int gi = 32 * ti + 2 * a + u, gj = 32 * tj + 2 * b + v;
+      if (gi < d && gj < d) out[(h * d + gi) * d + gj] = acc[u][v] / cnt * post_scale;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- cold factor scaling
+// factor [n][r] holds the eigenvectors (ascending); vals [r] the eigenvalues (ascending):
+// factor *= sqrt(max(lambda, 0) / max(mean_r max(lambda, 0), 1e-12)).
+__global__ __launch_bounds__(256) void factor_scale_kernel(float* __restrict__ factor, const float* __restrict__ vals,
+                                                           int32_t n, int32_t r) {
+  __shared__ float scale_s[MET_MAX_R];
+  const int64_t h = blockIdx.x;
+  const float* lv = vals + h * r;
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int c = 0; c < r; ++c) s += fmaxf(lv[c], 0.0f);
+    const float norm = fmaxf(s / static_cast<float>(r), 1e-12f);
+    for (int c = 0; c < r; ++c) scale_s[c] = sqrtf(fmaxf(lv[c], 0.0f) / norm);
+  }
+  __syncthreads();
+  float* f = factor + h * n * r;
+  for (int e = threadIdx.x; e < n * r; e += blockDim.x) f[e] *= scale_s[e % r];
+}
+
+// ---------------------------------------------------------------- warm subspace update
+constexpr int WF_THREADS = 1024;
+constexpr int LDM = MET_MAX_D + 1;  // padded metric row
+constexpr int LDB = MET_MAX_R + 1;  // padded basis row
+
+enum WarmOrtho { ORTHO_EACH_CQR = 0, ORTHO_EACH_CQR2 = 1, ORTHO_FINAL_CQR = 2 };
+enum WarmRitz { RITZ_RAYLEIGH_CHOLESKY = 0, RITZ_DIAGONAL = 1, RITZ_PREVIOUS_SCALE = 2 };
+
+struct WarmSmem {
+  float m[MET_MAX_D * LDM];   // metric
+  float b[MET_MAX_D * LDB];   // basis
+  float w[MET_MAX_D * LDB];   // metric . basis, scratch
+  float g[MET_MAX_R * LDB];   // Gram / Rayleigh matrix, its Cholesky factor (lower)
+  float colv[MET_MAX_R];      // per-column values (norms, diagonal Ritz values, scales)
+  float scal[4];
+  int32_t fail;
+};
+
+// w = m . b (n x n times n x r); thread (row i, column group cb), columns cb + 8 u
+__device__ void wf_apply(WarmSmem& s, int n, int r) {
+  const int t = threadIdx.x, i = t >> 3, cb = t & 7;
+  if (i < n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int j = 0; j < n; ++j) {
+      const float mij = s.m[i * LDM + j];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] = __builtin_fmaf(mij, s.b[j * LDB + cb + 8 * u], acc[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (cb + 8 * u < r) s.w[i * LDB + cb + 8 * u] = acc[u];
+    }
+  }
+  __syncthreads();
+}
+
+// column norms of src (n x r) into colv, clamped at 1e-12
+__device__ void wf_colnorms(WarmSmem& s, const float* src, int n, int r) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int col = wv; col < r; col += WF_THREADS / 64) {
+    const float v0 = lane < n ? src[lane * LDB + col] : 0.0f;
+    const float v1 = lane + 64 < n ? src[(lane + 64) * LDB + col] : 0.0f;
+    const float ss = wave_sum(v0 * v0 + v1 * v1);
+    if (lane == 0) s.colv[col] = fmaxf(sqrtf(ss), 1e-12f);
+  }
+  __syncthreads();
+}
+
+// g = a^T c (r x r), computed for p <= q and mirrored (exactly symmetric)
+__device__ void wf_gram(WarmSmem& s, const float* a, const float* c, int n, int r, bool symmetrize) {
+  for (int e = threadIdx.x; e < r * r; e += WF_THREADS) {
+    const int p = e / r, q = e - p * r;
+    if (q < p) continue;
+    float acc = 0.0f, acc2 = 0.0f;
+    for (int i = 0; i < n; ++i) {
+      acc = __builtin_fmaf(a[i * LDB + p], c[i * LDB + q], acc);
+      if (symmetrize) acc2 = __builtin_fmaf(a[i * LDB + q], c[i * LDB + p], acc2);
+    }
+    const float v = symmetrize ? 0.5f * (acc + acc2) : acc;
+    s.g[p * LDB + q] = v;
+    s.g[q * LDB + p] = v;
+  }
+  __syncthreads();
+}
+
+// In-place lower Cholesky of g[0..r) + shift I, by wave 0 (lane = row).  Returns (to every
+// thread) whether it succeeded: every pivot finite and positive.  g keeps the shifted
+// matrix's original entries above the diagonal; on failure the factor is undefined.
+__device__ bool wf_cholesky(WarmSmem& s, const float* src, int r, float shift) {
+  const int t = threadIdx.x, lane = t & 63;
+  if (t < 64) {
+    // copy the lower triangle of src (+ shift on the diagonal) into g
+    for (int j = 0; j < r; ++j) {
+      if (lane < r && j <= lane) s.g[lane * LDB + j] = src[lane * LDB + j] + (j == lane ? shift : 0.0f);
+    }
+    wave_sync();
+    bool ok = true;
+    for (int k = 0; k < r; ++k) {
+      const float piv = s.g[k * LDB + k];
+      ok = ok && (piv > 0.0f) && (piv < __builtin_huge_valf());
+      const float lkk = sqrtf(fmaxf(piv, 1e-30f));
+      float lik = 0.0f;
+      if (lane > k && lane < r) {
+        lik = s.g[lane * LDB + k] / lkk;
+        s.g[lane * LDB + k] = lik;
+      }
+      wave_sync();
+      if (lane == k) s.g[k * LDB + k] = lkk;
+      if (lane > k && lane < r) {
+        for (int j = k + 1; j <= lane; ++j) s.g[lane * LDB + j] -= lik * s.g[j * LDB + k];
+      }
+      wave_sync();
+    }
+    if (lane == 0) s.fail = ok ? 0 : 1;
+  }
+  __syncthreads();
+  return s.fail == 0;
+}
+
+// Cholesky-QR of src (n x r) into s.b (operator_kmeans.py:326-358): columns normalised
+// (norm clamped at 1e-12), Gram, jitter = max(mean diag, 1e-12) * ridge on the diagonal,
+// Cholesky (identity on failure), b = normalised . L^-T.  Returns whether it failed.
+__device__ bool wf_cholesky_qr(WarmSmem& s, const float* src, int n, int r, float ridge) {
+  wf_colnorms(s, src, n, r);
+  // normalised columns into w (src may be w itself: each element read then written by one thread)
+  for (int e = threadIdx.x; e < n * r; e += WF_THREADS) {
+    const int i = e / r, c = e - i * r;
+    s.w[i * LDB + c] = src[i * LDB + c] / s.colv[c];
+  }
+  __syncthreads();
+  wf_gram(s, s.w, s.w, n, r, true);
+  if (threadIdx.x == 0) {
+    float tr = 0.0f;
+    for (int c = 0; c < r; ++c) tr += s.g[c * LDB + c];
+    s.scal[0] = fmaxf(tr / static_cast<float>(r), 1e-12f) * ridge;
+  }
+  __syncthreads();
+  const bool ok = wf_cholesky(s, s.g, r, s.scal[0]);  // in place
+  // b = w L^-T: row i solves L y = w_i (forward substitution), identity L on failure
+  if (threadIdx.x < n) {
+    const int i = threadIdx.x;
+    for (int c = 0; c < r; ++c) {
+      float acc = s.w[i * LDB + c];
+      if (ok) {
+        for (int k = 0; k < c; ++k) acc -= s.g[c * LDB + k] * s.b[i * LDB + k];
+        acc /= s.g[c * LDB + c];
+      }
+      s.b[i * LDB + c] = acc;
+    }
+  }
+  __syncthreads();
+  return !ok;
+}
+
+// One head per workgroup.  metric [n][n]; prev_state [n][r] (the previous basis, or the cold
+// factor); prev_factor [n][r] (nullable: the previous factor); outputs factor, state [n][r]
+// and recovered[h] (1 = a Cholesky failed or a result is not finite; then, when prev_factor
+// is given, factor and state are the previous ones).
+__global__ __launch_bounds__(WF_THREADS, 1) void warm_factor_kernel(
+    const float* __restrict__ metric, const float* __restrict__ prev_state, const float* __restrict__ prev_factor,
+    int32_t n, int32_t r, int32_t power_iters, int32_t ortho, int32_t ritz, float rayleigh_ridge, float cqr_ridge,
+    float* __restrict__ factor, float* __restrict__ state, uint8_t* __restrict__ recovered) {
+  __shared__ WarmSmem s;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int64_t h = blockIdx.x;
+  const float* mh = metric + h * n * n;
+  const float* ps = prev_state + h * n * r;
+  const float* pf = prev_factor != nullptr ? prev_factor + h * n * r : nullptr;
+  for (int e = t; e < n * n; e += WF_THREADS) s.m[(e / n) * LDM + (e % n)] = mh[e];
+  for (int e = t; e < n * r; e += WF_THREADS) s.b[(e / r) * LDB + (e % r)] = ps[e];
+  __syncthreads();
+  bool failed = false;
+  // previous column scales (only the previous_scale finish uses them), then the
+  // column-normalised previous basis
+  wf_colnorms(s, s.b, n, r);
+  __shared__ float prev_scale[MET_MAX_R];
+  if (t < r) prev_scale[t] = s.colv[t];
+  for (int e = t; e < n * r; e += WF_THREADS) {
+    const int i = e / r, c = e - i * r;
+    s.b[i * LDB + c] /= s.colv[c];
+  }
+  __syncthreads();
+  __shared__ float diag_vals[MET_MAX_R];
+  for (int it = 0; it < power_iters; ++it) {
+    wf_apply(s, n, r);  // w = m b
+    if (ritz == RITZ_DIAGONAL && it == power_iters - 1) {
+      for (int col = wv; col < r; col += WF_THREADS / 64) {
+        float acc = 0.0f;
+        if (lane < n) acc += s.b[lane * LDB + col] * s.w[lane * LDB + col];
+        if (lane + 64 < n) acc += s.b[(lane + 64) * LDB + col] * s.w[(lane + 64) * LDB + col];
+        const float dsum = wave_sum(acc);
+        if (lane == 0) diag_vals[col] = dsum;
+      }
+      __syncthreads();
+    }
+    if (ortho == ORTHO_FINAL_CQR) {
+      // unorthogonalised power step: columns rescaled to unit norm
+      wf_colnorms(s, s.w, n, r);
+      for (int e = t; e < n * r; e += WF_THREADS) {
+        const int i = e / r, c = e - i * r;
+        s.b[i * LDB + c] = s.w[i * LDB + c] / s.colv[c];
+      }
+      __syncthreads();
+    } else {
+      failed |= wf_cholesky_qr(s, s.w, n, r, cqr_ridge);
+      if (ortho == ORTHO_EACH_CQR2 && it == power_iters - 1) {
+        // the corrective pass: same calibrated ridge floor (operator_kmeans.py:380-392)
+        for (int e = t; e < n * r; e += WF_THREADS) {
+          const int i = e / r, c = e - i * r;
+          s.w[i * LDB + c] = s.b[i * LDB + c];
+        }
+        __syncthreads();
+        failed |= wf_cholesky_qr(s, s.w, n, r, fmaxf(cqr_ridge, 1e-5f));
+      }
+    }
+  }
+  if (ortho == ORTHO_FINAL_CQR) {
+    for (int e = t; e < n * r; e += WF_THREADS) {
+      const int i = e / r, c = e - i * r;
+      s.w[i * LDB + c] = s.b[i * LDB + c];
+    }
+    __syncthreads();
+    failed |= wf_cholesky_qr(s, s.w, n, r, 1e-6f);
+  }
+  // finish: the factor goes to w, the basis stays in b
+  if (ritz == RITZ_PREVIOUS_SCALE || ritz == RITZ_DIAGONAL) {
+    if (t == 0) {
+      if (ritz == RITZ_DIAGONAL) {
+        float sum = 0.0f;
+        for (int c = 0; c < r; ++c) sum += fmaxf(diag_vals[c], 0.0f);
+        const float norm = fmaxf(sum / static_cast<float>(r), 1e-12f);
+        for (int c = 0; c < r; ++c) s.colv[c] = sqrtf(fmaxf(diag_vals[c], 0.0f) / norm);
+      } else {
+        for (int c = 0; c < r; ++c) s.colv[c] = prev_scale[c];
+      }
+    }
+    __syncthreads();
+    for (int e = t; e < n * r; e += WF_THREADS) {
+      const int i = e / r, c = e - i * r;
+      s.w[i * LDB + c] = s.b[i * LDB + c] * s.colv[c];
+    }
+    __syncthreads();
+  } else {
+    // Rayleigh matrix R = b^T (m b), symmetrised; normalizer = max(mean diag R, 1e-12);
+    // L = chol(R + normalizer ridge I), else chol(R + normalizer max(1e-2, ridge) I), else I
+    // with the head marked failed (operator_kmeans.py:154-216, :442-458)
+    wf_apply(s, n, r);
+    wf_gram(s, s.b, s.w, n, r, true);
+    if (t == 0) {
+      float tr = 0.0f;
+      for (int c = 0; c < r; ++c) tr += s.g[c * LDB + c];
+      s.scal[1] = fmaxf(tr / static_cast<float>(r), 1e-12f);
+    }
+    __syncthreads();
+    // R is kept in w (m b is dead) for the fallback factorisation; the chosen factor goes
+    // to the metric region, which is no longer needed
+    for (int e = t; e < r * r; e += WF_THREADS) {
+      const int p = e / r, q = e - p * r;
+      s.w[p * LDB + q] = s.g[p * LDB + q];
+    }
+    __syncthreads();
+    const float normalizer = s.scal[1];
+    bool ok = true;
+    float* l_primary = s.m;  // [r][r]
+    {
+      ok = wf_cholesky(s, s.w, r, normalizer * rayleigh_ridge);
+      for (int e = t; e < r * r; e += WF_THREADS) l_primary[e] = s.g[(e / r) * LDB + (e % r)];
+      __syncthreads();
+    }
+    if (!ok) {
+      ok = wf_cholesky(s, s.w, r, normalizer * fmaxf(1e-2f, rayleigh_ridge));
+      if (ok) {
+        for (int e = t; e < r * r; e += WF_THREADS) l_primary[e] = s.g[(e / r) * LDB + (e % r)];
+      } else {
+        for (int e = t; e < r * r; e += WF_THREADS) l_primary[e] = (e / r == e % r) ? 1.0f : 0.0f;
+        failed = true;
+      }
+      __syncthreads();
+    }
+    // factor = b L / sqrt(normalizer), L lower (entries above the diagonal are zero)
+    const float inv = 1.0f / sqrtf(normalizer);
+    for (int e = t; e < n * r; e += WF_THREADS) {
+      const int i = e / r, c = e - i * r;
+      float acc = 0.0f;
+      for (int k = c; k < r; ++k) acc = __builtin_fmaf(s.b[i * LDB + k], l_primary[k * r + c], acc);
+      s.w[i * LDB + c] = acc * inv;
+    }
+    __syncthreads();
+  }
+  // recovery: a failed factorisation or a non-finite factor or basis keeps the previous ones
+  __shared__ int32_t nonfinite;
+  if (t == 0) nonfinite = 0;
+  __syncthreads();
+  for (int e = t; e < n * r; e += WF_THREADS) {
+    const int i = e / r, c = e - i * r;
+    const float fv = s.w[i * LDB + c], bv = s.b[i * LDB + c];
+    if (!(fabsf(fv) < __builtin_huge_valf()) || !(fabsf(bv) < __builtin_huge_valf())) nonfinite = 1;
+  }
+  __syncthreads();
+  const bool rec = failed || nonfinite != 0;
+  const bool keep_prev = rec && pf != nullptr;
+  float* fo = factor + h * n * r;
+  float* so = state + h * n * r;
+  for (int e = t; e < n * r; e += WF_THREADS) {
+    const int i = e / r, c = e - i * r;
+    fo[e] = keep_prev ? pf[e] : s.w[i * LDB + c];
+    so[e] = keep_prev ? ps[e] : s.b[i * LDB + c];
+  }
+  if (t == 0 && recovered != nullptr) recovered[h] = rec ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- row projections
+// one wave per (head, row): lane c < r computes sum_j x[row][j] F[j][c] in index order
+// (fmaf), then divides by div[h] (nullable) and, with row_rms, by
+// max(sqrt(mean_c p_c^2), eps).
+__global__ __launch_bounds__(256) void project_rows_kernel(const float* __restrict__ x, const float* __restrict__ f,
+                                                           const float* __restrict__ div, int64_t m, int32_t d,
+                                                           int32_t r, int32_t tf32, int32_t row_rms, float eps,
+                                                           float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t h = blockIdx.y;
+  if (row >= m) return;
+  const float* xr = x + (h * m + row) * d;
+  const float* fh = f + h * d * r;
+  float acc = 0.0f;
+  if (lane < r) {
+    for (int j = 0; j < d; ++j) {
+      float xv = xr[j], fv = fh[j * r + lane];
+      if (tf32) {
+        xv = tf32_rna(xv);
+        fv = tf32_rna(fv);
+      }
+      acc = __builtin_fmaf(xv, fv, acc);
+    }
+    if (div != nullptr) acc = acc / div[h];
+  }
+  if (row_rms) {
+    const float ms = wave_sum(lane < r ? acc * acc : 0.0f) / static_cast<float>(r);
+    acc = acc / fmaxf(sqrtf(ms), eps);
+  }
+  if (lane < r) out[(h * m + row) * r + lane] = acc;
+}
+
+}  // namespace
+
+// x (dtype 0 bf16 / 2 fp32) [bh, n, d], d <= 128; rows int32 [count] (nullable: all n rows);
+// sizes int32 [bh, n] (nullable; only with rows == NULL: rows with size <= 0 are skipped and
+// not counted); center: subtract the used rows' mean; out fp32 [bh, d, d] =
+// post_scale / max(used, 1) * sum (x - mean)(x - mean)^T.
+extern "C" int spr_role_metric(const void* x, int32_t dtype, int64_t bh, int64_t n, int32_t d, const int32_t* rows,
+                               int32_t count, const int32_t* sizes, int32_t center, float post_scale, float* out,
+                               hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0 && d >= 1 && d <= MET_MAX_D, "spr_role_metric: bad size (d=%d)", d);
+  SPR_REQUIRE(dtype == 0 || dtype == 2, "spr_role_metric: dtype must be 0 (bf16) or 2 (fp32)");
+  SPR_REQUIRE(rows == nullptr || sizes == nullptr, "spr_role_metric: rows and sizes are exclusive");
+  SPR_REQUIRE(rows == nullptr || count >= 0, "spr_role_metric: negative count");
+  SPR_REQUIRE(bh <= 65535, "spr_role_metric: too many heads");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(x && out, "spr_role_metric: null pointer");
+  const int tiles = (d + 31) / 32;
+  dim3 grid(static_cast<uint32_t>(bh), static_cast<uint32_t>(tiles * tiles));
+  if (dtype == 0) {
+    role_metric_kernel<uint16_t><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(x), n, d, rows, count, sizes,
+                                                            center, post_scale, out);
+  } else {
+    role_metric_kernel<float><<<grid, 256, 0, stream>>>(static_cast<const float*>(x), n, d, rows, count, sizes, center,
+                                                         post_scale, out);
+  }
+  SPR_LAUNCHED("role_metric_kernel");
+  return SPR_OK;
+}
+
+extern "C" size_t spr_metric_factor_workspace(int64_t bh, int32_t rank) {
+  return static_cast<size_t>(bh > 0 ? bh : 0) * static_cast<size_t>(rank > 0 ? rank : 0) * sizeof(float);
+}
+
+// metric fp32 [bh, n, n] -> factor fp32 [bh, n, rank]: the top-rank eigenvectors of
+// 0.5 (M + M^T) (ascending eigenvalue order), column c scaled by
+// sqrt(max(lambda_c, 0) / max(mean max(lambda, 0), 1e-12)); workspace: the eigenvalues.
+extern "C" int spr_metric_factor(const float* metric, int64_t bh, int32_t n, int32_t rank, float* factor,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  SPR_REQUIRE(rank >= 1 && rank <= MET_MAX_R && rank <= n, "spr_metric_factor: rank %d outside [1, min(64, n)]",
+              rank);
+  if (bh <= 0) return SPR_OK;
+  if (workspace_bytes < spr_metric_factor_workspace(bh, rank)) {
+    spr_set_error("spr_metric_factor: workspace %zu < %zu bytes", workspace_bytes,
+                  spr_metric_factor_workspace(bh, rank));
+    return SPR_EWORKSPACE;
+  }
+  float* vals = static_cast<float*>(workspace);
+  const int st = spr_sym_top_eig(metric, bh, n, rank, 1, factor, vals, stream);
+  if (st != SPR_OK) return st;
+  factor_scale_kernel<<<dim3(static_cast<uint32_t>(bh)), 256, 0, stream>>>(factor, vals, n, rank);
+  SPR_LAUNCHED("factor_scale_kernel");
+  return SPR_OK;
+}
+
+// warm_subspace_metric_factor + the per-head recovery of N8V6Core._updated_factor.
+// ortho: 0 each_cholesky_qr, 1 each_cholesky_qr2, 2 cholesky_qr (once, after the
+// normalised power steps); ritz: 0 rayleigh_cholesky, 1 diagonal, 2 previous_scale.
+extern "C" int spr_warm_metric_factor(const float* metric, const float* prev_state, const float* prev_factor,
+                                      int64_t bh, int32_t n, int32_t rank, int32_t power_iters, int32_t ortho,
+                                      int32_t ritz, float rayleigh_ridge, float cqr_ridge, float* factor, float* state,
+                                      uint8_t* recovered, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 1 && n <= MET_MAX_D, "spr_warm_metric_factor: n=%d outside [1, %d]", n, MET_MAX_D);
+  SPR_REQUIRE(rank >= 1 && rank <= MET_MAX_R && rank <= n, "spr_warm_metric_factor: rank %d outside [1, 64]", rank);
+  SPR_REQUIRE(power_iters >= 1, "spr_warm_metric_factor: power_iters must be positive");
+  SPR_REQUIRE(ortho >= 0 && ortho <= 2 && ritz >= 0 && ritz <= 2, "spr_warm_metric_factor: bad mode");
+  SPR_REQUIRE(rayleigh_ridge > 0.0f && cqr_ridge > 0.0f, "spr_warm_metric_factor: ridges must be positive");
+  SPR_REQUIRE(bh <= 65535, "spr_warm_metric_factor: too many heads");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(metric && prev_state && factor && state, "spr_warm_metric_factor: null pointer");
+  warm_factor_kernel<<<dim3(static_cast<uint32_t>(bh)), WF_THREADS, 0, stream>>>(
+      metric, prev_state, prev_factor, n, rank, power_iters, ortho, ritz, rayleigh_ridge, cqr_ridge, factor, state,
+      recovered);
+  SPR_LAUNCHED("warm_factor_kernel");
+  return SPR_OK;
+}
+
+// out fp32 [bh, m, r] = (x [bh, m, d] . factor [bh, d, r]) / div[h] (div nullable), with
+// tf32 = 1 both operands rounded to TF32 first; row_rms = 1 divides each row by
+// max(sqrt(mean p^2), eps).  d <= 128, r <= 64.
+extern "C" int spr_project_rows(const float* x, const float* factor, const float* div, int64_t bh, int64_t m,
+                                int32_t d, int32_t r, int32_t tf32, int32_t row_rms, float eps, float* out,
+                                hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && m >= 0 && d >= 1 && d <= MET_MAX_D && r >= 1 && r <= 64, "spr_project_rows: bad size");
+  SPR_REQUIRE(bh <= 65535, "spr_project_rows: too many heads");
+  if (bh == 0 || m == 0) return SPR_OK;
+  SPR_REQUIRE(x && factor && out, "spr_project_rows: null pointer");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(m, 4)), static_cast<uint32_t>(bh));
+  project_rows_kernel<<<grid, 256, 0, stream>>>(x, factor, div, m, d, r, tf32, row_rms, eps, out);
+  SPR_LAUNCHED("project_rows_kernel");
+  return SPR_OK;
+}

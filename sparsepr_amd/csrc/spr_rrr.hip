@@ -189,34 +189,58 @@ __global__ __launch_bounds__(256) void rrr_gram_kernel(const float* __restrict__
 // (j = c + 8 q) are consecutive and the eight lane groups start in distinct banks.
 constexpr int HV_STRIDE = 136;
 __device__ __forceinline__ int hv_perm(int j) { return (j & 7) * 17 + (j >> 3); }
-constexpr int EIG_HV = 0;                            // [128][136] Householder columns (raw, permuted)
-constexpr int EIG_DD = EIG_HV + RRR_MAX * HV_STRIDE;  // tridiagonal diagonal
-constexpr int EIG_EE = EIG_DD + RRR_MAX;             // off-diagonal
-constexpr int EIG_TAU = EIG_EE + RRR_MAX;            // reflector tau
-constexpr int EIG_SCL = EIG_TAU + RRR_MAX;           // reflector scale: v_j = raw_j * scl (j > k + 1)
-constexpr int EIG_PB = EIG_SCL + RRR_MAX;            // [2][136] p = tau A v (permuted)
-constexpr int EIG_PART = EIG_PB + 2 * HV_STRIDE;     // [2][16] per-wave p . v
-constexpr int EIG_LAM = EIG_PART + 32;               // [16] eigenvalues, descending
-constexpr int EIG_LU = EIG_LAM + RRR_MAX_RANK;       // [6][128][16] LU of T - lambda_s I, then X = vectors of T
-constexpr int EIG_VB = EIG_LU + 6 * RRR_MAX * 16;    // [16][128] eigenvectors of B
-constexpr int EIG_S = EIG_VB + 16 * RRR_MAX;         // [16][16] Gram of the vectors, then R
-constexpr int EIG_X = EIG_S + 256;                   // [16][16] R^-1
-constexpr int EIG_FLOATS = EIG_X + 256;
+// LDS layout (floats) of the eigen solver for at most MAXR vectors.  Regions that are
+// dead after a phase are reused by a later one: the LU factors hold the back-transformed
+// vectors, the tridiagonal eigenvectors the Gram matrix and its factor, the Householder
+// columns the final basis.
+template <int MAXR>
+struct EigLayout {
+  static_assert(MAXR >= 16 && MAXR <= 64 && MAXR % 16 == 0, "MAXR in {16, 32, 48, 64}");
+  static constexpr int HV = 0;                        // [128][136] Householder columns (raw, permuted)
+  static constexpr int DD = HV + RRR_MAX * HV_STRIDE;  // tridiagonal diagonal
+  static constexpr int EE = DD + RRR_MAX;             // off-diagonal
+  static constexpr int TAU = EE + RRR_MAX;            // reflector tau
+  static constexpr int SCL = TAU + RRR_MAX;           // reflector scale: v_j = raw_j * scl (j > k + 1)
+  static constexpr int PB = SCL + RRR_MAX;            // [2][136] p = tau A v (permuted)
+  static constexpr int PART = PB + 2 * HV_STRIDE;     // [2][16] per-wave p . v
+  static constexpr int LAM = PART + 32;               // [MAXR] eigenvalues, descending
+  static constexpr int LU = LAM + MAXR;               // [5][128][16] LU of T - lambda_s I, 16 vectors at a time
+  static constexpr int X = LU + 5 * RRR_MAX * 16;     // [128][MAXR] eigenvectors of T
+  static constexpr int FLOATS = X + RRR_MAX * MAXR;
+  static constexpr int VB = LU;                       // [MAXR][128] eigenvectors of B (after inverse iteration)
+  static constexpr int S = X;                         // [MAXR][MAXR] Gram, then R (after back-transformation)
+  static constexpr int Q = HV;                        // [128][MAXR] orthonormal basis
+  static_assert(MAXR * RRR_MAX <= 5 * RRR_MAX * 16, "VB must fit in the LU region");
+};
 
-__device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int n, int rank, float* __restrict__ basis) {
+// Top-`rank` eigenpairs of the symmetric n x n matrix bmat (row stride ld; entries
+// outside n x n are treated as zero).  symmetrize: use 0.5 (A + A^T).  basis [n][rank]
+// gets the eigenvectors in ascending eigenvalue order (as torch.linalg.eigh's last
+// `rank` columns); vals [rank] (nullable) their Rayleigh quotients, ascending.
+template <int MAXR>
+__device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int n, int rank, bool symmetrize,
+                          float* __restrict__ basis, float* __restrict__ vals) {
+  using L = EigLayout<MAXR>;
   const int t = threadIdx.x, i = t >> 3, c = t & 7, lane = t & 63, wv = t >> 6;
-  float* hv = sm + EIG_HV;
-  float* dd = sm + EIG_DD;
-  float* ee = sm + EIG_EE;
-  float* tau = sm + EIG_TAU;
-  float* scl = sm + EIG_SCL;
+  float* hv = sm + L::HV;
+  float* dd = sm + L::DD;
+  float* ee = sm + L::EE;
+  float* tau = sm + L::TAU;
+  float* scl = sm + L::SCL;
 
   float a[16];
 #pragma unroll
-  for (int q = 0; q < 16; ++q) a[q] = bmat[i * RRR_MAX + c + 8 * q];
-  for (int e = t; e < EIG_PART + 32; e += RRR_THREADS) sm[e] = 0.0f;  // columns, p buffers, partials
+  for (int q = 0; q < 16; ++q) {
+    const int j = c + 8 * q;
+    float v = 0.0f;
+    if (i < n && j < n) {
+      v = bmat[i * ld + j];
+      if (symmetrize) v = 0.5f * (v + bmat[j * ld + i]);
+    }
+    a[q] = v;
+  }
+  for (int e = t; e < L::PART + 32; e += RRR_THREADS) sm[e] = 0.0f;  // columns, p buffers, partials
   __syncthreads();
-
   // ---- Householder tridiagonalisation (lower), A <- H A H column by column.
   // Columns go in blocks of eight: during block kb, a[q] holds column c + 8 (q + kb),
   // so the column being reduced is a[0] of the lanes with c = k % 8 (the array shifts
@@ -258,8 +282,8 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int n, int 
         scl[k] = sk;
       }
       const bool live = 8 * wv + 7 > k;  // this wave holds rows below k
-      float* pb = sm + EIG_PB + (k & 1) * HV_STRIDE;
-      float* pt = sm + EIG_PART + (k & 1) * 16;
+      float* pb = sm + L::PB + (k & 1) * HV_STRIDE;
+      float* pt = sm + L::PART + (k & 1) * 16;
       float v[16];
       float pr = 0.0f, vi = 0.0f;
       if (live) {
@@ -357,7 +381,7 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int n, int 
   // wave w evaluate 16 points inside the bracket of the (4 w + g + 1)-th largest
   // eigenvalue, which shrinks 17-fold per round; five rounds leave it about
   // 1.4e-6 (hi - lo) wide, which inverse iteration does not need to be narrower.
-  float* lam = sm + EIG_LAM;
+  float* lam = sm + L::LAM;
   if (4 * wv < rank) {
     const int grp = lane >> 4, gl = lane & 15;
     const int sv = 4 * wv + grp;
@@ -388,34 +412,22 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int n, int 
   }
   __syncthreads();
 
-  // ---- eigenvectors of T by inverse iteration: lane s of wave 0 computes vector s
-  // (column s of X), with the pivoted LU of T - lambda_s I in its own columns of the
-  // U / L arrays.  Members of a cluster (eigenvalue gaps below 1e-3 ||T||) run in
-  // successive rounds and are orthogonalised against the members before them.
-  float* X = sm + EIG_LU + 5 * RRR_MAX * 16;  // [128][16]
+  // ---- eigenvectors of T by inverse iteration, 16 at a time: lane s of wave 0 computes
+  // vector 16 bt + s (column of X), with the pivoted LU of T - lambda I in its own
+  // columns of the U / L arrays.  Members of a cluster (eigenvalue gaps below
+  // 1e-3 ||T||) run in successive rounds and are orthogonalised against the members
+  // before them (earlier batches are complete).
+  float* X = sm + L::X;  // [128][MAXR]
   if (wv == 0) {
     const float ortol = 1e-3f * tnorm;
     const float ptol = fmaxf(1.1920929e-7f * tnorm, 1e-30f);  // smallest pivot magnitude
-    const int s = lane;
-    const bool act = s < rank;
-    int mypos = 0, maxpos = 0;
-    {
-      int pos = 0;
-      for (int u = 1; u < rank; ++u) {
-        pos = (lam[u - 1] - lam[u] < ortol) ? pos + 1 : 0;
-        if (u == s) mypos = pos;
-        maxpos = max(maxpos, pos);
-      }
-    }
-    float* RU0 = sm + EIG_LU;  // [128][16] 1 / pivot
+    float* RU0 = sm + L::LU;  // [128][16] 1 / pivot
     float* U1 = RU0 + RRR_MAX * 16;
     float* U2 = U1 + RRR_MAX * 16;
     float* LM = U2 + RRR_MAX * 16;
     float* PV = LM + RRR_MAX * 16;
-    const float lm = act ? lam[s] : 0.0f;
     // the tridiagonal in registers (lane l holds entries l and l + 64), read by readlane
     const float d0 = dd[lane], d1 = dd[lane + 64], e0 = ee[lane], e1 = ee[lane + 64];
-    // (readlane of registers every lane wrote before the divergent part below)
     auto dget = [&](int j) {
       const float r0 = lane_read(d0, j & 63), r1 = lane_read(d1, j & 63);
       return j < 64 ? r0 : r1;
@@ -424,233 +436,243 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int n, int 
       const float r0 = lane_read(e0, j & 63), r1 = lane_read(e1, j & 63);
       return j < 64 ? r0 : r1;
     };
-    for (int rho = 0; rho <= maxpos; ++rho) {
-      if (act && mypos == rho) {
-        float cd = dget(0) - lm;
-        float cs = n > 1 ? eget(0) : 0.0f;
-        for (int j = 0; j + 1 < n; ++j) {
-          const float sub = eget(j);
-          const float nd = dget(j + 1) - lm;
-          const float ns = j + 2 < n ? eget(j + 1) : 0.0f;
-          const bool sw = fabsf(cd) < fabsf(sub);
-          const float piv = sw ? sub : cd;
-          const float oth = sw ? cd : sub;
-          const float l = oth == 0.0f ? 0.0f : oth * __builtin_amdgcn_rcpf(piv);
-          const float pv = fabsf(piv) < ptol ? copysignf(ptol, piv) : piv;
-          RU0[j * 16 + s] = __builtin_amdgcn_rcpf(pv);
-          U1[j * 16 + s] = sw ? nd : cs;
-          U2[j * 16 + s] = sw ? ns : 0.0f;
-          LM[j * 16 + s] = l;
-          PV[j * 16 + s] = sw ? 1.0f : 0.0f;
-          const float ncd = sw ? cs - l * nd : nd - l * cs;
-          cs = sw ? -l * ns : ns;
-          cd = ncd;
-        }
-        const float pv = fabsf(cd) < ptol ? copysignf(ptol, cd) : cd;
-        RU0[(n - 1) * 16 + s] = __builtin_amdgcn_rcpf(pv);
-        // start vector: deterministic, distinct per eigenvalue
-        for (int j = 0; j < n; ++j) {
-          const uint32_t hsh = (static_cast<uint32_t>(j) * 2654435761u) ^ (static_cast<uint32_t>(s + 1) * 0x9E3779B9u);
-          const uint32_t mix = (hsh ^ (hsh >> 15)) * 0x2C1B3C6Du;
-          X[j * 16 + s] = static_cast<float>((mix >> 8) & 0xFFFF) * (2.0f / 65535.0f) - 1.0f;
-        }
-        // Three solves.  Between solves X is only rescaled (by 1 / max |x|, applied as
-        // the next forward pass loads it); cluster members are also orthogonalised
-        // against the members before them.  The norm is taken once, at the end.
-        float sc = 1.0f;
-        for (int it = 0; it < 3; ++it) {
-          // P, L: forward elimination of the right-hand side, 8 rows per batch of loads
-          float cur = X[s] * sc;
-          for (int j0 = 0; j0 + 1 < n; j0 += 8) {
-            float nx[8], lv[8], pv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int j = min(j0 + u, RRR_MAX - 2);
-              nx[u] = X[(j + 1) * 16 + s];
-              lv[u] = LM[j * 16 + s];
-              pv[u] = PV[j * 16 + s];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int j = j0 + u;
-              if (j + 1 < n) {
-                const bool sw = pv[u] != 0.0f;
-                const float xn = nx[u] * sc;
-                X[j * 16 + s] = sw ? xn : cur;
-                cur = sw ? cur - lv[u] * xn : xn - lv[u] * cur;
-              }
-            }
-          }
-          // U: back substitution, tracking the largest magnitude
-          float x1 = cur * RU0[(n - 1) * 16 + s], x2 = 0.0f;
-          X[(n - 1) * 16 + s] = x1;
-          float mx = fabsf(x1);
-          for (int j0 = n - 2; j0 >= 0; j0 -= 8) {
-            float xi[8], u1[8], u2[8], ru[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int j = max(j0 - u, 0);
-              xi[u] = X[j * 16 + s];
-              u1[u] = U1[j * 16 + s];
-              u2[u] = U2[j * 16 + s];
-              ru[u] = RU0[j * 16 + s];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-              const int j = j0 - u;
-              if (j >= 0) {
-                const float xv = (xi[u] - u1[u] * x1 - u2[u] * x2) * ru[u];
-                X[j * 16 + s] = xv;
-                mx = fmaxf(mx, fabsf(xv));
-                x2 = x1;
-                x1 = xv;
-              }
-            }
-          }
-          sc = mx > 0.0f ? 1.0f / mx : 1.0f;
-          if (mypos > 0) {
-            for (int j = 0; j < n; ++j) X[j * 16 + s] *= sc;
-            sc = 1.0f;
-            for (int o = s - mypos; o < s; ++o) {
-              float dt = 0.0f;
-              for (int j = 0; j < n; ++j) dt += X[j * 16 + s] * X[j * 16 + o];
-              for (int j = 0; j < n; ++j) X[j * 16 + s] -= dt * X[j * 16 + o];
-            }
-            float ss = 0.0f;
-            for (int j = 0; j < n; ++j) ss += X[j * 16 + s] * X[j * 16 + s];
-            const float nr = sqrtf(ss);
-            sc = nr > 0.0f ? 1.0f / nr : 0.0f;
-          }
-        }
-        float ss = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < n; ++j) {
-          const float xv = X[j * 16 + s] * sc;
-          ss += xv * xv;
-        }
-        const float nr = sqrtf(ss);
-        const float f = nr > 0.0f ? sc / nr : 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < n; ++j) X[j * 16 + s] *= f;
-      }
-      wave_sync();
-    }
-  }
-  __syncthreads();
-
-  // ---- back to B's coordinates: y <- H_0 H_1 ... H_{n-3} y, four vectors per wave
-  float* vb = sm + EIG_VB;
-  if (4 * wv < rank) {
-    float y0[4], y1[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int sv = 4 * wv + u;
-      y0[u] = (sv < rank && lane < n) ? X[lane * 16 + sv] : 0.0f;
-      y1[u] = (sv < rank && lane + 64 < n) ? X[(lane + 64) * 16 + sv] : 0.0f;
-    }
-    const int pl0 = hv_perm(lane), pl1 = hv_perm(lane + 64);
-    int k = n - 3;
-    float tk = 0.0f, sk = 0.0f, r0 = 0.0f, r1 = 0.0f;
-    if (k >= 0) {
-      tk = tau[k];
-      sk = scl[k];
-      r0 = hv[k * HV_STRIDE + pl0];
-      r1 = hv[k * HV_STRIDE + pl1];
-    }
-    for (; k >= 0; --k) {
-      // next reflector's data, loaded while this one is applied
-      const int kn = max(k - 1, 0);
-      const float tn = tau[kn], sn = scl[kn];
-      const float n0 = hv[kn * HV_STRIDE + pl0], n1 = hv[kn * HV_STRIDE + pl1];
-      if (tk != 0.0f) {
-        const float v0 = lane == k + 1 ? 1.0f : r0 * sk;
-        const float v1 = lane + 64 == k + 1 ? 1.0f : r1 * sk;
-        float dt[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) dt[u] = tk * wave_sum(v0 * y0[u] + v1 * y1[u]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          y0[u] -= dt[u] * v0;
-          y1[u] -= dt[u] * v1;
+    for (int bt = 0; 16 * bt < rank; ++bt) {
+      const int sl = lane;  // column of the LU arrays
+      const int s = 16 * bt + lane;
+      const bool act = lane < 16 && s < rank;
+      int mypos = 0, maxpos = 0;
+      {
+        int pos = 0;
+        for (int u = 1; u < min(rank, 16 * bt + 16); ++u) {
+          pos = (lam[u - 1] - lam[u] < ortol) ? pos + 1 : 0;
+          if (u == s) mypos = pos;
+          if (u >= 16 * bt) maxpos = max(maxpos, pos);
         }
       }
-      tk = tn;
-      sk = sn;
-      r0 = n0;
-      r1 = n1;
-    }
+      const float lm = act ? lam[s] : 0.0f;
+      for (int rho = 0; rho <= maxpos; ++rho) {
+        if (act && mypos == rho) {
+          float cd = dget(0) - lm;
+          float cs = n > 1 ? eget(0) : 0.0f;
+          for (int j = 0; j + 1 < n; ++j) {
+            const float sub = eget(j);
+            const float nd = dget(j + 1) - lm;
+            const float ns = j + 2 < n ? eget(j + 1) : 0.0f;
+            const bool sw = fabsf(cd) < fabsf(sub);
+            const float piv = sw ? sub : cd;
+            const float oth = sw ? cd : sub;
+            const float l = oth == 0.0f ? 0.0f : oth * __builtin_amdgcn_rcpf(piv);
+            const float pv = fabsf(piv) < ptol ? copysignf(ptol, piv) : piv;
+            RU0[j * 16 + sl] = __builtin_amdgcn_rcpf(pv);
+            U1[j * 16 + sl] = sw ? nd : cs;
+            U2[j * 16 + sl] = sw ? ns : 0.0f;
+            LM[j * 16 + sl] = l;
+            PV[j * 16 + sl] = sw ? 1.0f : 0.0f;
+            const float ncd = sw ? cs - l * nd : nd - l * cs;
+            cs = sw ? -l * ns : ns;
+            cd = ncd;
+          }
+          const float pv = fabsf(cd) < ptol ? copysignf(ptol, cd) : cd;
+          RU0[(n - 1) * 16 + sl] = __builtin_amdgcn_rcpf(pv);
+          // start vector: deterministic, distinct per eigenvalue
+          for (int j = 0; j < n; ++j) {
+            const uint32_t hsh =
+                (static_cast<uint32_t>(j) * 2654435761u) ^ (static_cast<uint32_t>(s + 1) * 0x9E3779B9u);
+            const uint32_t mix = (hsh ^ (hsh >> 15)) * 0x2C1B3C6Du;
+            X[j * MAXR + s] = static_cast<float>((mix >> 8) & 0xFFFF) * (2.0f / 65535.0f) - 1.0f;
+          }
+          // Three solves.  Between solves X is only rescaled (by 1 / max |x|, applied as
+          // the next forward pass loads it); cluster members are also orthogonalised
+          // against the members before them.  The norm is taken once, at the end.
+          float sc = 1.0f;
+          for (int it = 0; it < 3; ++it) {
+            // P, L: forward elimination of the right-hand side, 8 rows per batch of loads
+            float cur = X[s] * sc;
+            for (int j0 = 0; j0 + 1 < n; j0 += 8) {
+              float nx[8], lv[8], pv[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int sv = 4 * wv + u;
-      if (sv < rank) {
-        vb[sv * RRR_MAX + lane] = y0[u];
-        vb[sv * RRR_MAX + lane + 64] = y1[u];
+              for (int u = 0; u < 8; ++u) {
+                const int j = min(j0 + u, RRR_MAX - 2);
+                nx[u] = X[(j + 1) * MAXR + s];
+                lv[u] = LM[j * 16 + sl];
+                pv[u] = PV[j * 16 + sl];
+              }
+#pragma unroll
+              for (int u = 0; u < 8; ++u) {
+                const int j = j0 + u;
+                if (j + 1 < n) {
+                  const bool sw = pv[u] != 0.0f;
+                  const float xn = nx[u] * sc;
+                  X[j * MAXR + s] = sw ? xn : cur;
+                  cur = sw ? cur - lv[u] * xn : xn - lv[u] * cur;
+                }
+              }
+            }
+            // U: back substitution, tracking the largest magnitude
+            float x1 = cur * RU0[(n - 1) * 16 + sl], x2 = 0.0f;
+            X[(n - 1) * MAXR + s] = x1;
+            float mx = fabsf(x1);
+            for (int j0 = n - 2; j0 >= 0; j0 -= 8) {
+              float xi[8], u1[8], u2[8], ru[8];
+#pragma unroll
+              for (int u = 0; u < 8; ++u) {
+                const int j = max(j0 - u, 0);
+                xi[u] = X[j * MAXR + s];
+                u1[u] = U1[j * 16 + sl];
+                u2[u] = U2[j * 16 + sl];
+                ru[u] = RU0[j * 16 + sl];
+              }
+#pragma unroll
+              for (int u = 0; u < 8; ++u) {
+                const int j = j0 - u;
+                if (j >= 0) {
+                  const float xv = (xi[u] - u1[u] * x1 - u2[u] * x2) * ru[u];
+                  X[j * MAXR + s] = xv;
+                  mx = fmaxf(mx, fabsf(xv));
+                  x2 = x1;
+                  x1 = xv;
+                }
+              }
+            }
+            sc = mx > 0.0f ? 1.0f / mx : 1.0f;
+            if (mypos > 0) {
+              for (int j = 0; j < n; ++j) X[j * MAXR + s] *= sc;
+              sc = 1.0f;
+              for (int o = s - mypos; o < s; ++o) {
+                float dt = 0.0f;
+                for (int j = 0; j < n; ++j) dt += X[j * MAXR + s] * X[j * MAXR + o];
+                for (int j = 0; j < n; ++j) X[j * MAXR + s] -= dt * X[j * MAXR + o];
+              }
+              float ss = 0.0f;
+              for (int j = 0; j < n; ++j) ss += X[j * MAXR + s] * X[j * MAXR + s];
+              const float nr = sqrtf(ss);
+              sc = nr > 0.0f ? 1.0f / nr : 0.0f;
+            }
+          }
+          float ss = 0.0f;
+#pragma unroll 8
+          for (int j = 0; j < n; ++j) {
+            const float xv = X[j * MAXR + s] * sc;
+            ss += xv * xv;
+          }
+          const float nr = sqrtf(ss);
+          const float f = nr > 0.0f ? sc / nr : 0.0f;
+#pragma unroll 8
+          for (int j = 0; j < n; ++j) X[j * MAXR + s] *= f;
+        }
+        wave_sync();
       }
     }
   }
   __syncthreads();
 
-  // ---- Cholesky-QR: S = V^T V = R^T R, basis = V R^-1.  The 16 x 16 factor and
-  // inverse run in wave 0, lane j holding column j, with static register indices.
-  float* S = sm + EIG_S;
-  float* XR = sm + EIG_X;
-  if (wv < rank) {
-    const float y0 = vb[wv * RRR_MAX + lane], y1 = vb[wv * RRR_MAX + lane + 64];
-    for (int s2 = 0; s2 <= wv; ++s2) {
+  // ---- back to B's coordinates: y <- H_0 H_1 ... H_{n-3} y, four vectors per wave per pass
+  float* vb = sm + L::VB;  // (the LU arrays are dead)
+  for (int base = 0; base < rank; base += 64) {
+    if (base + 4 * wv < rank) {
+      float y0[4], y1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int sv = base + 4 * wv + u;
+        y0[u] = (sv < rank && lane < n) ? X[lane * MAXR + sv] : 0.0f;
+        y1[u] = (sv < rank && lane + 64 < n) ? X[(lane + 64) * MAXR + sv] : 0.0f;
+      }
+      const int pl0 = hv_perm(lane), pl1 = hv_perm(lane + 64);
+      int k = n - 3;
+      float tk = 0.0f, sk = 0.0f, r0 = 0.0f, r1 = 0.0f;
+      if (k >= 0) {
+        tk = tau[k];
+        sk = scl[k];
+        r0 = hv[k * HV_STRIDE + pl0];
+        r1 = hv[k * HV_STRIDE + pl1];
+      }
+      for (; k >= 0; --k) {
+        // next reflector's data, loaded while this one is applied
+        const int kn = max(k - 1, 0);
+        const float tn = tau[kn], sn = scl[kn];
+        const float n0 = hv[kn * HV_STRIDE + pl0], n1 = hv[kn * HV_STRIDE + pl1];
+        if (tk != 0.0f) {
+          const float v0 = lane == k + 1 ? 1.0f : r0 * sk;
+          const float v1 = lane + 64 == k + 1 ? 1.0f : r1 * sk;
+          float dt[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) dt[u] = tk * wave_sum(v0 * y0[u] + v1 * y1[u]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            y0[u] -= dt[u] * v0;
+            y1[u] -= dt[u] * v1;
+          }
+        }
+        tk = tn;
+        sk = sn;
+        r0 = n0;
+        r1 = n1;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int sv = base + 4 * wv + u;
+        if (sv < rank) {
+          vb[sv * RRR_MAX + lane] = y0[u];
+          vb[sv * RRR_MAX + lane + 64] = y1[u];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- Cholesky-QR: S = V^T V = R^T R (R upper, in place), then Q R = V by forward
+  // substitution over the columns; Q is orthonormal to rounding.
+  float* S = sm + L::S;  // (the tridiagonal eigenvectors are dead)
+  for (int col = wv; col < rank; col += RRR_THREADS / 64) {
+    const float y0 = vb[col * RRR_MAX + lane], y1 = vb[col * RRR_MAX + lane + 64];
+    for (int s2 = 0; s2 <= col; ++s2) {
       const float dt = wave_sum(y0 * vb[s2 * RRR_MAX + lane] + y1 * vb[s2 * RRR_MAX + lane + 64]);
       if (lane == 0) {
-        S[s2 * 16 + wv] = dt;
-        S[wv * 16 + s2] = dt;
+        S[s2 * MAXR + col] = dt;
+        S[col * MAXR + s2] = dt;
       }
     }
   }
   __syncthreads();
-  if (wv == 0) {
-    const int j = lane;
-    const bool on = j < rank;
-    float col[16];  // col[r] = S[r][j], then R[r][j]
-#pragma unroll
-    for (int r = 0; r < 16; ++r) col[r] = (on && r < rank) ? S[r * 16 + j] : (r == j ? 1.0f : 0.0f);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float rkk = sqrtf(lane_read(col[k], k));
-      // row k of R: R[k][j] = S[k][j] / R[k][k] for j > k, R[k][k] itself for j = k
-      if (j > k) col[k] = col[k] / rkk;
-      else if (j == k) col[k] = rkk;
-      // trailing update: S[r][j] -= R[k][r] R[k][j] for k < r <= j
-#pragma unroll
-      for (int r = k + 1; r < 16; ++r) {
-        const float rkr = lane_read(col[k], r);
-        if (r <= j) col[r] -= rkr * col[k];
-      }
+  for (int k = 0; k < rank; ++k) {
+    const float rkk = sqrtf(S[k * MAXR + k]);
+    __syncthreads();
+    if (t >= k && t < rank) S[k * MAXR + t] = t == k ? rkk : S[k * MAXR + t] / rkk;
+    __syncthreads();
+    for (int e = t; e < rank * rank; e += RRR_THREADS) {
+      const int r = e / rank, q = e - r * rank;
+      if (r > k && q >= r) S[r * MAXR + q] -= S[k * MAXR + r] * S[k * MAXR + q];
     }
-    // X = R^-1 column j: X[r][j] for r = j .. 0, X[r][j] = 0 above j
-    float xr[16];
-#pragma unroll
-    for (int r = 15; r >= 0; --r) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int u = r + 1; u < 16; ++u) acc += lane_read(col[r], u) * xr[u];  // R[r][u]: register r of lane u
-      const float rrr = lane_read(col[r], r);
-      xr[r] = r > j ? 0.0f : (r == j ? 1.0f / rrr : -acc / rrr);
-    }
-    if (on) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) XR[r * 16 + j] = xr[r];
+    __syncthreads();
+  }
+  float* Qm = sm + L::Q;  // [128][MAXR] (the Householder columns are dead)
+  if (t < n) {
+    for (int col = 0; col < rank; ++col) {
+      float acc = vb[col * RRR_MAX + t];
+      for (int s2 = 0; s2 < col; ++s2) acc -= Qm[t * MAXR + s2] * S[s2 * MAXR + col];
+      Qm[t * MAXR + col] = acc / S[col * MAXR + col];
     }
   }
   __syncthreads();
-  if (wv < rank) {
-    float q0 = 0.0f, q1 = 0.0f;
-    for (int s = 0; s <= wv; ++s) {
-      const float f = XR[s * 16 + wv];
-      q0 += vb[s * RRR_MAX + lane] * f;
-      q1 += vb[s * RRR_MAX + lane + 64] * f;
+  // eigenvalue rank col (0 = largest) goes to column rank - 1 - col: ascending order
+  for (int e = t; e < n * rank; e += RRR_THREADS) {
+    const int r = e / rank, col = e - r * rank;
+    basis[r * rank + (rank - 1 - col)] = Qm[r * MAXR + col];
+  }
+  if (vals != nullptr) {
+    // Rayleigh quotients q^T A q (the symmetric part of A gives the same value)
+    for (int col = wv; col < rank; col += RRR_THREADS / 64) {
+      const float q0 = lane < n ? Qm[lane * MAXR + col] : 0.0f;
+      const float q1 = lane + 64 < n ? Qm[(lane + 64) * MAXR + col] : 0.0f;
+      float a0 = 0.0f, a1 = 0.0f;
+      for (int j = 0; j < n; ++j) {
+        const float qj = Qm[j * MAXR + col];
+        if (lane < n) a0 += bmat[j * ld + lane] * qj;
+        if (lane + 64 < n) a1 += bmat[j * ld + lane + 64] * qj;
+      }
+      const float lam_c = wave_sum(q0 * a0 + q1 * a1);
+      if (lane == 0) vals[rank - 1 - col] = lam_c;
     }
-    // eigenvalue rank wv (0 = largest) goes to column rank - 1 - wv: ascending order
-    const int col = rank - 1 - wv;
-    if (lane < n) basis[lane * rank + col] = q0;
-    if (lane + 64 < n) basis[(lane + 64) * rank + col] = q1;
   }
 }
 
@@ -703,13 +725,26 @@ __device__ void rrr_cholesky(float* sm, float* __restrict__ gmat, int p) {
 
 __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_factor_kernel(float* __restrict__ ws, int32_t p, int32_t d,
                                                                     int32_t rank, float* __restrict__ basis) {
-  __shared__ float sm[EIG_FLOATS];
+  __shared__ float sm[EigLayout<RRR_MAX_RANK>::FLOATS];
   const int64_t h = blockIdx.x;
   if (blockIdx.y == 1) {
     rrr_cholesky(sm, ws + (h * 2) * RRR_MAT, p);
   } else {
-    rrr_eigen(sm, ws + (h * 2 + 1) * RRR_MAT, d, rank, basis + h * d * rank);
+    rrr_eigen<RRR_MAX_RANK>(sm, ws + (h * 2 + 1) * RRR_MAT, RRR_MAX, d, rank, false, basis + h * d * rank,
+                            nullptr);
   }
+}
+
+// Top-rank eigenpairs of a batch of symmetric matrices, one workgroup per matrix.
+template <int MAXR>
+__global__ __launch_bounds__(RRR_THREADS, 1) void sym_top_eig_kernel(const float* __restrict__ mats, int32_t n,
+                                                                     int32_t rank, int32_t symmetrize,
+                                                                     float* __restrict__ vecs,
+                                                                     float* __restrict__ vals) {
+  __shared__ float sm[EigLayout<MAXR>::FLOATS];
+  const int64_t h = blockIdx.x;
+  rrr_eigen<MAXR>(sm, mats + h * n * n, n, n, rank, symmetrize != 0, vecs + h * n * rank,
+                  vals != nullptr ? vals + h * rank : nullptr);
 }
 
 // Z = y_w basis, rb = x_w^T Z, left = L^-T L^-1 rb.
@@ -844,5 +879,26 @@ extern "C" int spr_rrr_fit(const float* x, const float* y, const float* weights,
   rrr_solve_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, x_mean, x_scale, y_mean, ws,
                                                          basis, left);
   SPR_LAUNCHED("rrr_solve_kernel");
+  return SPR_OK;
+}
+
+// mats fp32 [bh, n, n] symmetric (symmetrize = 1: use 0.5 (A + A^T)); vecs fp32 [bh, n, rank]:
+// the eigenvectors of the `rank` largest eigenvalues in ascending order; vals fp32 [bh, rank]
+// (nullable): their Rayleigh quotients, ascending.  1 <= n <= 128, 1 <= rank <= min(64, n).
+extern "C" int spr_sym_top_eig(const float* mats, int64_t bh, int32_t n, int32_t rank, int32_t symmetrize,
+                               float* vecs, float* vals, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 1 && n <= RRR_MAX, "spr_sym_top_eig: n=%d outside [1, %d]", n, RRR_MAX);
+  SPR_REQUIRE(rank >= 1 && rank <= 64 && rank <= n, "spr_sym_top_eig: rank %d outside [1, min(64, n)]", rank);
+  SPR_REQUIRE(bh <= 65535, "spr_sym_top_eig: too many matrices");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(mats && vecs, "spr_sym_top_eig: null pointer");
+  if (rank <= RRR_MAX_RANK) {
+    sym_top_eig_kernel<RRR_MAX_RANK><<<dim3(static_cast<uint32_t>(bh)), RRR_THREADS, 0, stream>>>(
+        mats, n, rank, symmetrize, vecs, vals);
+  } else {
+    sym_top_eig_kernel<64><<<dim3(static_cast<uint32_t>(bh)), RRR_THREADS, 0, stream>>>(mats, n, rank, symmetrize,
+                                                                                       vecs, vals);
+  }
+  SPR_LAUNCHED("sym_top_eig_kernel");
   return SPR_OK;
 }

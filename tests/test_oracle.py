@@ -822,3 +822,89 @@ def test_rounds_probe_sequence_hand_derived(oracle):
     # fewer rows than groups stops inside round 1; the count is capped at the tokens
     assert oracle.select_role_equal_probes(f, labels, 3, 2)[0][0].tolist() == [0, 1]
     assert oracle.select_role_equal_probes(f, labels, 3, 20)[0].shape == (1, 8)
+
+
+# --------------------------------------------------------------------------- N8 role metrics and factors
+
+def test_role_metric_against_numpy_cov(oracle):
+    """Centred metric = np.cov(bias=True) of the used rows; uncentred = centred + mean mean^T
+    (two routes to the same matrix); the size mask drops rows from the mean and the count."""
+    rng = np.random.default_rng(51)
+    x = (rng.standard_normal((2, 300, 8)) + 0.5).astype(np.float32)
+    rows = np.array([0, 7, 19, 150, 151, 299])
+    cen = oracle.role_metric(x, rows=rows, center=True)
+    unc = oracle.role_metric(x, rows=rows, center=False)
+    for h in range(2):
+        xs = x[h, rows].astype(np.float64)
+        assert np.allclose(cen[h], np.cov(xs.T, bias=True), rtol=1e-12, atol=1e-12)
+        mu = xs.mean(0)
+        assert np.allclose(unc[h], cen[h] + np.outer(mu, mu), rtol=1e-10, atol=1e-12)
+    sizes = rng.integers(-1, 3, (2, 300))
+    q = oracle.role_metric(x, sizes=sizes, center=True, post_scale=1.0 / 8)
+    for h in range(2):
+        xs = x[h, sizes[h] > 0].astype(np.float64)
+        assert np.allclose(q[h], np.cov(xs.T, bias=True) / 8, rtol=1e-12, atol=1e-12)
+
+
+def _spectrum_matrix(rng, bh, d, eig):
+    qm = np.linalg.qr(rng.standard_normal((bh, d, d)))[0]
+    return np.einsum("bij,j,bkj->bik", qm, eig, qm), qm
+
+
+def test_metric_factor_constructed_spectrum(oracle):
+    """M = Q diag(lambda) Q^T with known lambda: F F^T = sum over the top r of
+    lambda_i / mean(top r, clamped) q_i q_i^T; a negative eigenvalue inside the top r gives a
+    zero column; an asymmetric perturbation is removed by the symmetrisation."""
+    rng = np.random.default_rng(52)
+    d, r = 12, 5
+    eig = np.array([-3.0, -1, 0.1, 0.2, 0.3, 0.5, 0.8, 1.3, 2.1, 3.4, 5.5, 8.9])
+    m, qm = _spectrum_matrix(rng, 2, d, eig)
+    skew = rng.standard_normal((2, d, d)) * 1e-3
+    f = oracle.metric_factor(m + skew - np.swapaxes(skew, 1, 2), r)
+    top = eig[-r:]
+    want = np.einsum("bij,j,bkj->bik", qm[:, :, -r:], top / top.mean(), qm[:, :, -r:])
+    assert np.allclose(np.einsum("bir,bjr->bij", f, f), want, atol=1e-9)
+    neg = np.array([-5.0, -4, -3, -2, -1, 0.5, 0.7])
+    m2, _ = _spectrum_matrix(rng, 1, 7, neg)
+    f2 = oracle.metric_factor(m2, 3)  # top 3: -1, 0.5, 0.7 -> the -1 column is zero
+    assert np.allclose(f2[0, :, 0], 0.0) and np.abs(f2[0, :, 1:]).max() > 0.1
+
+
+def test_warm_subspace_factor_fixed_point(oracle):
+    """Started from the exact top-r eigenvectors, subspace iteration stays on that subspace:
+    F F^T = P M P / mean(diag of the Rayleigh matrix), up to the 1e-4 Rayleigh ridge; the
+    Cholesky-QR basis is orthonormal; every finish gives the same subspace; a NaN metric
+    marks the head recovered."""
+    rng = np.random.default_rng(53)
+    d, r = 16, 6
+    eig = np.linspace(0.1, 1.0, d) ** 3
+    eig[-r:] = [2.0, 2.5, 3.0, 4.0, 5.0, 7.0]
+    m, qm = _spectrum_matrix(rng, 2, d, eig)
+    prev = qm[:, :, -r:] * rng.uniform(0.5, 2.0, (2, 1, r))  # columns with arbitrary scales
+    f, b, rec = oracle.warm_subspace_metric_factor(m, prev, r)
+    assert not rec.any()
+    proj = np.einsum("bir,bjr->bij", qm[:, :, -r:], qm[:, :, -r:])
+    pmp = proj @ m @ proj
+    norm = eig[-r:].mean()
+    assert np.allclose(np.einsum("bir,bjr->bij", f, f), pmp / norm, atol=2e-3 * np.abs(pmp / norm).max())
+    assert np.allclose(np.einsum("bir,bis->brs", b, b), np.eye(r), atol=1e-4)
+    for ortho, ritz in [("each_cholesky_qr", "diagonal"), ("cholesky_qr", "previous_scale")]:
+        f2, b2, _ = oracle.warm_subspace_metric_factor(m, prev, r, orthogonalization=ortho, ritz_mode=ritz)
+        assert np.allclose(np.einsum("bir,bjr->bij", b2, b2), proj, atol=1e-3)
+    bad = m.copy()
+    bad[1, 0, 0] = np.nan
+    _, _, rec = oracle.warm_subspace_metric_factor(bad, prev, r)
+    assert rec.tolist() == [False, True]
+
+
+def test_project_rows_loop(oracle):
+    rng = np.random.default_rng(54)
+    x = rng.standard_normal((1, 5, 8)).astype(np.float32)
+    f = rng.standard_normal((1, 8, 3)).astype(np.float32)
+    got = oracle.project_rows(x, f, div=np.array([2.0]), tf32=True)
+    for i in range(5):
+        for c in range(3):
+            want = sum(float(a) * float(b) for a, b in zip(oracle.tf32_rna(x[0, i]), oracle.tf32_rna(f[0, :, c])))
+            assert abs(got[0, i, c] - want / 2.0) < 1e-12
+    rms = oracle.project_rows(x, f, row_rms=True)
+    assert np.allclose(np.sqrt((rms ** 2).mean(-1)), 1.0)
