@@ -69,6 +69,28 @@ def _batch_kmeans_n8_native(x, n_clusters, max_iters, init_centroids):
     return labels, centroids, sizes.long(), int(max_iters)
 
 
+def _lloyd_result(x, n_clusters, max_iters=100, tol=1e-4, init_centroids=None, backend="cuvs"):
+    """batch_kmeans_Euclid's loop returning the LloydResult, whose sorted_idx / offsets (the
+    stable sort of the final labels) the N8 route reuses for its centroids and permutation."""
+    from .flash_kmeans.kmeans_impl import LloydResult
+
+    if backend == "n8_cuda_ext":
+        labels, cent, _sizes, iters = _batch_kmeans_n8_native(x, n_clusters, max_iters, init_centroids)
+        idx, sizes, offsets = argsort_labels(labels, n_clusters)
+        return LloydResult(labels, cent, sizes, iters, idx, offsets)
+    if backend not in ("flash", "cuvs"):
+        raise RuntimeError(
+            f"Unknown Euclidean k-means backend {backend!r}. "
+            "Expected 'cuvs', 'flash', or 'n8_cuda_ext'."
+        )
+    if max_iters <= 0:
+        raise RuntimeError("the route's k-means needs at least one iteration")
+    if not x.is_cuda:
+        raise RuntimeError("Flash-KMeans backend requires a CUDA input tensor.")
+    mode = X_SQ_FP32 if (backend == "flash" and init_centroids is not None) else X_SQ_BF16
+    return lloyd(x.contiguous(), n_clusters, max_iters, tol, init_centroids, x_sq_mode=mode)
+
+
 def batch_kmeans_Euclid(x, n_clusters, max_iters=100, tol=1e-4, init_centroids=None, verbose=False,
                         backend="cuvs"):
     """Batched Euclidean k-means (kmeans_utils.py:1504-1580).

@@ -1,22 +1,35 @@
-"""N8-V6 method core: route carrier types and the current-step probe repair
-(drop-in for src/sparsepr/models/common/n8_v6.py on the sparse-attention path).
+"""N8-V6 method core: role routing and the current-step probe repair (drop-in for
+src/sparsepr/models/common/n8_v6.py on the sparse-attention path).
 
-`N8V6Core.repair` runs entirely on the HIP kernels (probe selection, dense probe
-attention, fit preparation, apply, exact scatter) plus the small fp32 RRR fit
-on the GPU.  The N8 role-space router (`route`) is not part of this library:
-its SVG-EAR selector scores and role projections are (sparsepr_amd.kernels.svg_ear,
-sparsepr_amd.kernels.role_projection), its role-metric factors and orchestration
-are not.  The top-p router of `sparsepr_amd.layer` produces an `N8V6Route` that
-`repair` consumes.
+`N8V6Core.route` computes the video-token cluster map: role metrics and factors (cold
+eigen factor, then warm subspace updates), TF32 role projections, role-space k-means of K
+and Q, original-space centroids, the K/V permutation, SVG-EAR / attention-mass selector
+scores, fixed-density or top-p key budgets and the exact budget selector.
+`N8V6Core.repair` runs the probe selection, dense probe attention, fit preparation, the
+reduced-rank fit, the apply and the exact scatter.  Every compute step is a HIP kernel of
+libsparsepr_hip.so.  Configurations whose kernels are not built (joint K/V role features,
+Householder-QR factor updates, other projection precisions, output_role repair) raise
+NotImplementedError.
 """
 
 from __future__ import annotations
 
+import math
+import os
+import time
 from dataclasses import dataclass
 
 import torch
 
+from . import _lib, kmeans_utils
+from . import operator_kmeans as _ok
+from .kernels import role_metric as _rm
 from .kernels.attention import dense_attention
+from .kernels.permute import argsort_labels, permute_tensor_by_labels_triton
+from .kernels.role_projection import role_k_projection_normalize, role_projection_rms_triton
+from .kernels.selection import MODE_N8_NATIVE, MODE_TRITON, select_budget, top_p_key_budgets
+from .kernels.svg_ear import (attention_mass_scores_triton, svg_ear_grouped_value_error_scores_triton,
+                              svg_ear_value_error_scores_triton)
 from .kernels.residual_repair import n8_exact_probe_scatter_triton, n8_prepare_output_repair_fit_triton
 from .residual_repair import (
     MODE_FIRST_TOKEN,
@@ -153,32 +166,336 @@ class N8V6Route:
     q_role_centers: torch.Tensor | None = None
 
 
+_ENV_OFF = {"", "0", "false", "no", "off"}
+
+
+def _env_flag(name: str) -> bool:
+    return os.environ.get(name, "0").lower() not in _ENV_OFF
+
+
 class N8V6Core:
-    """Per-attention-layer N8-V6 state: the last finite repair state (carried
-    across denoising steps for non-finite recovery) and the fit buffers."""
+    """Per-attention-layer N8-V6 state (n8_v6.py:371-406): role factors and their subspace
+    states, the previous centroids (warm starts and empty-cluster fallbacks), the last finite
+    repair state, and the fit buffers.  Single-threaded and stream ordered."""
 
     def __init__(self, config: N8V6Config, *, validate: bool = True):
         if validate:
             config.validate()
         self.config = config
+        self.q_centroids = None
+        self.k_centroids = None
+        self.v_centroids = None
+        self.q_factor_state = None
+        self.k_factor_state = None
+        self.v_factor_state = None
+        self.q_factor_current = None
+        self.k_factor_current = None
+        self.v_factor_current = None
+        self.q_factor_recovery_mask = None
+        self.k_factor_recovery_mask = None
+        self.v_factor_recovery_mask = None
         self.repair_state_current = None
         self.repair_recovery_mask = None
         self.route_call_index = 0
         self._fit_feature_buffer = None
         self._dense_probe_buffer = None
         self._fit_target_buffer = None
+        self._full_k_order = None
+        self.last_route_profile: dict = {}
         self.last_repair_profile: dict = {}
+        self.diagnostic_callback = None
+
+    @property
+    def initialized(self) -> bool:
+        return self.q_centroids is not None
 
     def reset(self) -> None:
         self.__init__(self.config, validate=False)
 
-    def route(self, *args, **kwargs):
-        raise NotImplementedError(
-            "The N8 role-space router is not provided by sparsepr_amd: its metric covariance/factor "
-            "step and route orchestration are not built (its SVG-EAR scores and role projections are: "
-            "sparsepr_amd.kernels.svg_ear, sparsepr_amd.kernels.role_projection); use "
-            "sparsepr_amd.layer.SparsePRAttention.route (top-p cluster routing)."
-        )
+    def _emit_diagnostic(self, stage: str, *, tensors: dict, scalars: dict) -> None:
+        callback = self.diagnostic_callback
+        if callback is not None:
+            callback(stage, tensors, {"core_route_call": int(self.route_call_index), **scalars})
+
+    def _full_key_order(self, video_order: torch.Tensor, video_tokens: int, total_tokens: int) -> torch.Tensor:
+        """The video key order followed by the identity over the suffix (n8_v6.py:407-432)."""
+        bh = int(video_order.shape[0])
+        expected = (bh, total_tokens)
+        if (self._full_k_order is None or tuple(self._full_k_order.shape) != expected
+                or self._full_k_order.device != video_order.device):
+            self._full_k_order = torch.empty(expected, device=video_order.device, dtype=torch.int32)
+            suffix = torch.arange(video_tokens, total_tokens, device=video_order.device, dtype=torch.int32)
+            self._full_k_order[:, video_tokens:].copy_(suffix.unsqueeze(0))
+        self._full_k_order[:, :video_tokens].copy_(video_order)
+        return self._full_k_order
+
+    def _check_route_config(self, dim: int) -> None:
+        cfg = self.config
+        if cfg.role_v_weight > 0.0:
+            raise NotImplementedError("N8 routing with role_v_weight > 0 (joint K/V role features) is not built "
+                                      "for the MI355X kernels.")
+        if cfg.factor_orthogonalization not in _rm.ORTHO or cfg.factor_ritz_mode not in _rm.RITZ:
+            raise NotImplementedError(
+                f"factor_orthogonalization={cfg.factor_orthogonalization!r} / factor_ritz_mode="
+                f"{cfg.factor_ritz_mode!r} are not built for the MI355X kernels (Cholesky-QR variants and the "
+                "rayleigh_cholesky, diagonal and previous_scale finishes are).")
+        if not cfg.compile_role_kv_projection or cfg.role_kv_matmul_precision != "high":
+            raise NotImplementedError(
+                "The MI355X K role projection computes the compiled projection at role_kv_matmul_precision "
+                "'high' (TF32 factor); other projection precisions are not built.")
+        if max(cfg.role_q_rank, cfg.role_k_rank) > 64 or dim not in (64, 128):
+            raise NotImplementedError("N8 routing on the MI355X kernels needs head_dim 64 or 128 and ranks <= 64.")
+
+    def _updated_factor(self, metric, previous, current, rank):
+        """n8_v6.py:478-519: the cold eigen factor on the first call, then one warm subspace
+        update per call with per-head reuse of the previous factor when it fails."""
+        cfg = self.config
+        if previous is None:
+            factor = _ok.metric_factor(metric, rank)
+            recovered = torch.zeros(metric.shape[0], device=metric.device, dtype=torch.bool)
+            return factor, factor, recovered
+        if current is None:
+            raise RuntimeError("Warm role-factor state is missing its current factor.")
+        return _rm.warm_metric_factor(
+            metric, previous, rank, prev_factor=current, power_iters=cfg.factor_power_iters,
+            orthogonalization=cfg.factor_orthogonalization, ritz_mode=cfg.factor_ritz_mode,
+            rayleigh_ridge=cfg.factor_rayleigh_ridge, cholesky_qr_ridge=cfg.factor_cholesky_qr_ridge)
+
+    def route(self, q_video, k_video, v_video, *, gqa_group_size: int = 1, always_attended_keys: int = 0,
+              total_key_tokens: int | None = None, k_full_source=None, v_full_source=None) -> N8V6Route:
+        """The N8-V6 video-token map (n8_v6.py:521-1172): role metrics and factors, role-space
+        k-means of K then Q, original-space centroids, the K/V permutation, the selector
+        scores, the budgets and the exact budget selector, all on the HIP kernels."""
+        if q_video.shape != k_video.shape or q_video.shape != v_video.shape or q_video.ndim != 4:
+            raise RuntimeError(
+                "N8-V6 expects matching [B,H,N,D] video Q/K/V; got "
+                f"Q={tuple(q_video.shape)}, K={tuple(k_video.shape)}, V={tuple(v_video.shape)}."
+            )
+        batch, heads, tokens, dim = q_video.shape
+        self.config.validate(dim)
+        self._check_route_config(dim)
+        _lib.require_gpu(q_video, k_video, v_video, what="N8V6Core.route")
+        bh = batch * heads
+        cfg = self.config
+        q = q_video.contiguous().view(bh, tokens, dim)
+        profile_breakdown = bool(cfg.profile_breakdown or getattr(self, "profile_breakdown_active", False))
+        group = int(gqa_group_size)
+        if group <= 0 or heads % group != 0:
+            raise ValueError(f"gqa_group_size must divide the query-head count; got H={heads}, G={group}.")
+        kv_heads = heads // group
+        if group > 1:
+            k = k_video[:, ::group].contiguous().view(batch * kv_heads, tokens, dim)
+            v = v_video[:, ::group].contiguous().view(batch * kv_heads, tokens, dim)
+            _, q_metric_source = _ok.gqa_metric_sources(q_video, k_video, q_cluster_heads=heads,
+                                                        k_cluster_heads=kv_heads, gqa_group_size=group)
+            metric_sample_tokens = cfg.metric_sample_tokens * group
+        else:
+            k = k_video.contiguous().view(bh, tokens, dim)
+            v = v_video.contiguous().view(bh, tokens, dim)
+            q_metric_source = q
+            metric_sample_tokens = cfg.metric_sample_tokens
+        self.last_route_profile = {
+            "n8_profile_enabled": profile_breakdown, "n8_gqa_key_sharing": bool(group > 1),
+            "n8_gqa_group_size": group, "n8_q_cluster_heads": heads, "n8_k_cluster_heads": kv_heads,
+            "n8_k_runtime_heads": heads, "n8_selector_budget_mode": cfg.selector_budget_mode,
+            "n8_svg_ear_top_p": float(cfg.svg_ear_top_p),
+            "n8_adaptive_budget_min_density": float(cfg.adaptive_budget_min_density),
+            "n8_adaptive_budget_max_density": float(cfg.adaptive_budget_max_density),
+            "n8_backend": "hip_mi355x",
+        }
+        started = [time.perf_counter()]
+
+        def profile_mark(name: str) -> None:
+            if not profile_breakdown:
+                return
+            torch.cuda.synchronize(q_video.device)
+            now = time.perf_counter()
+            self.last_route_profile[f"n8_route_{name}_ms"] = (now - started[0]) * 1000.0
+            started[0] = now
+
+        if profile_breakdown:
+            torch.cuda.synchronize(q_video.device)
+            started[0] = time.perf_counter()
+
+        # ---- K role factor (n8_v6.py:611-657)
+        refresh = (self.q_factor_current is None or self.k_factor_current is None
+                   or self.route_call_index % cfg.factor_refresh_every == 0)
+        if refresh:
+            k_metric = _ok.key_metric_from_queries(q_metric_source, metric_sample_tokens)
+            if self.diagnostic_callback is not None:
+                self._emit_diagnostic("clustering", tensors={"k_role_metric": k_metric},
+                                      scalars={"phase": "kv_metrics_before_factorization"})
+            k_factor, self.k_factor_state, self.k_factor_recovery_mask = self._updated_factor(
+                k_metric, self.k_factor_state, self.k_factor_current, cfg.role_k_rank)
+            self.k_factor_current = k_factor
+            self.v_factor_recovery_mask = torch.zeros(k_factor.shape[0], device=k_factor.device, dtype=torch.bool)
+        else:
+            k_factor = self.k_factor_current
+        profile_mark("kv_metric_factor")
+        # ---- K role features and the warm start (n8_v6.py:658-704): TF32 projection,
+        # one RMS scale per head
+        k_features, k_scale = role_k_projection_normalize(k, k_factor)
+        k_init = None
+        if self.k_centroids is not None:
+            k_init = _rm.project_rows(self.k_centroids, k_factor, divisor=k_scale, tf32=True)
+        profile_mark("kv_projection_init")
+        k_iters = cfg.kmeans_iter_step if self.initialized else cfg.kmeans_iter_init
+        k_backend = cfg.kmeans_backend
+        if k_backend == "n8_cuda_ext" and k_init is None:
+            k_backend = "flash"
+        k_res = kmeans_utils._lloyd_result(k_features, cfg.num_k_centroids, max_iters=k_iters,
+                                           init_centroids=k_init, backend=k_backend)
+        k_labels, k_sizes, k_iter = k_res.labels, k_res.sizes.long(), k_res.iters
+        profile_mark("kmeans_k")
+        # ---- original-space K and V centroids, one label traversal (n8_v6.py:719-726)
+        self.k_centroids, self.v_centroids = _ok.joint_original_centroids(
+            k, v, k_labels, k_sizes, x_empty_fallback=self.k_centroids, y_empty_fallback=self.v_centroids,
+            sorted_labels=(k_res.sorted_idx, k_res.offsets))
+        profile_mark("kv_centroids")
+        # ---- Q role factor from the key centroids (n8_v6.py:728-755)
+        if refresh:
+            q_metric = _ok.query_metric_from_key_centroids(self.k_centroids, k_sizes)
+            if self.diagnostic_callback is not None:
+                self._emit_diagnostic("clustering", tensors={"q_role_metric": q_metric},
+                                      scalars={"phase": "q_metric_before_factorization"})
+            q_factor, self.q_factor_state, self.q_factor_recovery_mask = self._updated_factor(
+                q_metric, self.q_factor_state, self.q_factor_current, cfg.role_q_rank)
+            self.q_factor_current = q_factor
+        else:
+            q_factor = self.q_factor_current
+        if group > 1:
+            q_factor_runtime = q_factor.view(batch, kv_heads, dim, cfg.role_q_rank).repeat_interleave(
+                group, dim=1).contiguous().view(bh, dim, cfg.role_q_rank)
+        else:
+            q_factor_runtime = q_factor
+        profile_mark("q_metric_factor")
+        # ---- Q role features, warm start, k-means, original-space Q centroids (n8_v6.py:756-804)
+        q_features = role_projection_rms_triton(q, q_factor_runtime)
+        q_init = None
+        if self.q_centroids is not None:
+            q_init = _rm.project_rows(self.q_centroids, q_factor_runtime, row_rms=True, eps=1e-6)
+        profile_mark("q_projection_init")
+        q_backend = cfg.kmeans_backend
+        if q_backend == "n8_cuda_ext" and q_init is None:
+            q_backend = "flash"
+        q_res = kmeans_utils._lloyd_result(q_features, cfg.num_q_centroids, max_iters=k_iters,
+                                           init_centroids=q_init, backend=q_backend)
+        q_labels, q_sizes, q_iter = q_res.labels, q_res.sizes.long(), q_res.iters
+        profile_mark("kmeans_q")
+        self.q_centroids = _ok.original_centroids(q, q_labels, q_sizes, empty_fallback=self.q_centroids,
+                                                  sorted_labels=(q_res.sorted_idx, q_res.offsets))
+        profile_mark("q_centroids")
+        # ---- GQA: K clusters shared by the query heads of a group (n8_v6.py:806-839)
+        if group > 1:
+            def per_q_head(t, *tail):
+                return t.view(batch, kv_heads, *tail).repeat_interleave(group, dim=1).contiguous().view(
+                    bh, *tail)
+
+            k_labels_runtime = per_q_head(k_labels, tokens)
+            k_sizes_runtime = per_q_head(k_sizes, cfg.num_k_centroids)
+            k_centroids_runtime = per_q_head(self.k_centroids, cfg.num_k_centroids, dim)
+            v_centroids_runtime = per_q_head(self.v_centroids, cfg.num_k_centroids, dim)
+            k_order = argsort_labels(k_labels_runtime, cfg.num_k_centroids)[0]
+        else:
+            k_labels_runtime, k_sizes_runtime = k_labels, k_sizes
+            k_centroids_runtime, v_centroids_runtime = self.k_centroids, self.v_centroids
+            k_order = k_res.sorted_idx  # the stable argsort of the final labels
+        if self.diagnostic_callback is not None:
+            self._emit_diagnostic("clustering", tensors={
+                "q_factor": q_factor, "k_factor": k_factor, "q_centroids": self.q_centroids,
+                "k_centroids": self.k_centroids, "v_centroids": self.v_centroids, "q_cluster_sizes": q_sizes,
+                "k_cluster_sizes": k_sizes, "q_factor_recovery_mask": self.q_factor_recovery_mask,
+                "k_factor_recovery_mask": self.k_factor_recovery_mask},
+                scalars={"phase": "cluster_result", "factor_refresh": bool(refresh), "q_kmeans_iters": int(q_iter),
+                         "k_kmeans_iters": int(k_iter), "factor_recovery_policy": "reuse_previous_finite_factor"})
+        # ---- K/V permuted once into cluster order (n8_v6.py:900-933)
+        use_full_layout = k_full_source is not None or v_full_source is not None
+        if use_full_layout:
+            if k_full_source is None or v_full_source is None:
+                raise ValueError("k_full_source and v_full_source must be provided together.")
+            if k_full_source.shape != v_full_source.shape or k_full_source.ndim != 4:
+                raise ValueError("Full K/V sources must have matching [B,H,N,D] shapes.")
+            if tuple(k_full_source.shape[:2]) != (batch, heads) or k_full_source.shape[-1] != dim:
+                raise ValueError("Full K/V sources do not match the video tensor head layout.")
+            total_layout_tokens = int(k_full_source.shape[2])
+            if total_layout_tokens < tokens:
+                raise ValueError("Full K/V source is shorter than the video prefix.")
+            full_order = self._full_key_order(k_order, tokens, total_layout_tokens)
+            k_permuted, _ = permute_tensor_by_labels_triton(k_full_source, None, dim=2, sorted_indices=full_order)
+            v_permuted, _ = permute_tensor_by_labels_triton(v_full_source, None, dim=2, sorted_indices=full_order)
+            selector_k = k_permuted.reshape(bh, total_layout_tokens, dim)
+            selector_v = v_permuted.reshape(bh, total_layout_tokens, dim)
+        else:
+            k_permuted, _ = permute_tensor_by_labels_triton(k_video, None, dim=2, sorted_indices=k_order)
+            v_permuted, _ = permute_tensor_by_labels_triton(v_video, None, dim=2, sorted_indices=k_order)
+            selector_k = k_permuted.reshape(bh, tokens, dim)
+            selector_v = v_permuted.reshape(bh, tokens, dim)
+        profile_mark("kv_permute")
+        # ---- selector scores (n8_v6.py:934-990)
+        use_grouped = bool(cfg.grouped_svg_ear_router and cfg.selector_policy == "svg_ear_value" and group > 1)
+        if use_grouped:
+            stored = int(selector_k.shape[1])
+            k_native = selector_k.view(batch, heads, stored, dim)[:, ::group].contiguous().view(
+                batch * kv_heads, stored, dim)
+            v_native = selector_v.view(batch, heads, stored, dim)[:, ::group].contiguous().view(
+                batch * kv_heads, stored, dim)
+            scores = svg_ear_grouped_value_error_scores_triton(
+                qcentroids=self.q_centroids, k_sorted=k_native, v_sorted=v_native, kcentroids=self.k_centroids,
+                vcentroids=self.v_centroids, kcluster_sizes=k_sizes, gqa_group=group,
+                block_q=min(cfg.selector_block_q, 16), block_n=cfg.selector_block_n,
+                num_warps=max(4, cfg.selector_num_warps))
+        elif cfg.selector_policy == "attention_mass":
+            scores = attention_mass_scores_triton(
+                qcentroids=self.q_centroids, k_sorted=selector_k, kcluster_sizes=k_sizes_runtime, gqa_group=1,
+                block_q=cfg.selector_block_q, block_n=cfg.selector_block_n, num_warps=cfg.selector_num_warps,
+                logical_tokens=tokens)
+        else:
+            scores = svg_ear_value_error_scores_triton(
+                qcentroids=self.q_centroids, k_sorted=selector_k, v_sorted=selector_v,
+                kcentroids=k_centroids_runtime, vcentroids=v_centroids_runtime, kcluster_sizes=k_sizes_runtime,
+                gqa_group=1, var_k_diag=None, jensen_var_cap=0.0, block_q=cfg.selector_block_q,
+                block_n=cfg.selector_block_n, num_warps=cfg.selector_num_warps, logical_tokens=tokens)
+        profile_mark("selector_scores")
+        if self.diagnostic_callback is not None:
+            self._emit_diagnostic("svg_ear_selection", tensors={"svg_ear_scores": scores},
+                                  scalars={"phase": "scores_before_budget_selection",
+                                           "selector_policy": cfg.selector_policy,
+                                           "grouped_svg_ear_router": use_grouped})
+        # ---- key budgets (n8_v6.py:1004-1061)
+        total_keys = int(total_key_tokens) if total_key_tokens is not None else tokens
+        if total_keys < tokens or always_attended_keys < 0 or always_attended_keys > total_keys:
+            raise ValueError(f"Invalid key accounting: video={tokens}, total={total_keys}, "
+                             f"always={always_attended_keys}.")
+        if cfg.selector_budget_mode == "fixed_density":
+            base_total_density = max(0.0, cfg.target_density - cfg.probe_rows / float(tokens))
+            target_keys = int(math.ceil(base_total_density * total_keys))
+            budget = max(0, target_keys - int(always_attended_keys))
+            budgets = torch.full((bh, cfg.num_q_centroids), budget, device=q_video.device, dtype=torch.int32)
+            base_density = budget / float(tokens)
+        else:
+            budgets = top_p_key_budgets(self.q_centroids, k_centroids_runtime, k_sizes_runtime, cfg.svg_ear_top_p)
+            budgets = budgets.clamp(min=int(math.ceil(cfg.adaptive_budget_min_density * tokens)),
+                                    max=int(math.floor(cfg.adaptive_budget_max_density * tokens)))
+            pair_density = (budgets * q_sizes).sum(dim=1).float() / float(tokens * tokens)
+            base_density = float(pair_density.mean().item())
+        # ---- exact budget selector (n8_v6.py:1062-1112): the n8_kernels semantics when
+        # SPARSEPR_N8_CUDA_EXT_SELECTOR is set, else the Triton selector's
+        mode = MODE_N8_NATIVE if _env_flag("SPARSEPR_N8_CUDA_EXT_SELECTOR") else MODE_TRITON
+        routed = select_budget(scores, k_sizes_runtime, budgets, mode)
+        video_map = routed[:, 1:, 1:]
+        profile_mark("selector_budget")
+        if self.diagnostic_callback is not None:
+            self._emit_diagnostic("svg_ear_selection", tensors={"routed_map": routed, "requested_key_budget": budgets},
+                                  scalars={"phase": "budget_selection_result",
+                                           "selector_budget_mode": cfg.selector_budget_mode,
+                                           "base_video_density": float(base_density)})
+        result = N8V6Route(
+            q_labels=q_labels, k_labels=k_labels_runtime, q_cluster_sizes=q_sizes, k_cluster_sizes=k_sizes_runtime,
+            video_dynamic_map=video_map, q_role_features=q_features, k_permuted=k_permuted, v_permuted=v_permuted,
+            k_sorted_indices=k_order, base_video_density=base_density, q_kmeans_iters=int(q_iter),
+            k_kmeans_iters=int(k_iter), permuted_includes_suffix=use_full_layout)
+        self.route_call_index += 1
+        return result
 
     def repair(self, base_video, q_video, k_full, v_full, route: N8V6Route):
         """Current-step M-probe / rank-r repair of video rows (reference n8_v6.py:1174-1444).
