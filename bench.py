@@ -55,12 +55,13 @@ def parse():
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["attention", "copy", "svg_ear", "role_proj"], default=None,
+    ap.add_argument("--only", choices=["attention", "copy", "svg_ear", "role_proj", "n8_route"], default=None,
                     help="profiling aids: 'attention' routes once, then times only the block-sparse attention "
                          "kernel for --steps launches; 'copy' runs --steps plain 512 MiB device copies (the "
                          "calibration kernel for the HBM traffic counters); 'svg_ear' routes once, then times "
                          "the N8 value-error routing scores (N8's default selector) on the routed clusters; "
-                         "'role_proj' times N8's Q role projection (rank 64) over the C4 Q")
+                         "'role_proj' times N8's Q role projection (rank 64) over the C4 Q; 'n8_route' times the "
+                         "HunyuanVideo adapter's N8 step (route, attention, repair) at the C4 shape")
     return ap.parse_args()
 
 
@@ -316,6 +317,116 @@ def only_role_proj(args):
                                    "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": nbytes}}), flush=True)
 
 
+def only_n8_route(args):
+    """The HunyuanVideo adapter's N8 step at the C4 shape (hunyuanvideo.py:160-239) with the
+    default N8V6Config (300 Q / 1000 K clusters, ranks 64 / 48, fixed density 0.22, 64 probes):
+    route (role metrics, warm factors, role-space k-means, centroids, K/V permute, SVG-EAR
+    scores, exact budget selector), query permute, padded block-sparse attention over the
+    118,800 video + 256 text tokens (77 prompt), inverse permute, repair.  Warm-up includes the
+    cold call (25 Lloyd iterations); the timed steps are the warm calls of a denoising loop
+    (2 iterations from the previous centroids).  Stage times come from one extra call with
+    the route's synchronising profile marks; the attention is timed with HIP events on the
+    stream it is launched on, inside the timed steps."""
+    import torch
+    import torch.nn.functional as F
+
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.kernels.permute import apply_inverse_permutation_triton, permute_tensor_by_labels_triton
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
+    from sparsepr_amd.n8_v6 import N8V6Config, N8V6Core
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    shape = synthetic.HUNYUAN
+    text, prompt = 256, 77
+    qv, kv, vv = synthetic.frame_gmm_qkv(shape, device=dev, **GEN)
+    B, H, Nv, D = qv.shape
+    g = torch.Generator(device=dev).manual_seed(5)
+    query, key, value = (torch.cat((a, (0.8 * torch.randn((B, H, text, D), device=dev, generator=g)).to(a.dtype)), 2)
+                         for a in (qv, kv, vv))
+    cfg = N8V6Config()
+    core = N8V6Core(cfg)
+    text_idx = torch.arange(Nv, Nv + text, device=dev, dtype=torch.int32).expand(B * H, -1)
+    sizes_tail = torch.tensor([prompt, text - prompt], device=dev, dtype=torch.long)
+    attn_events = []
+
+    def step(ev=None):
+        route = core.route(qv, kv, vv, always_attended_keys=prompt, total_key_tokens=Nv + prompt,
+                           k_full_source=key, v_full_source=value)
+        q_order = torch.argsort(route.q_labels, dim=-1, stable=True).to(torch.int32)
+        q_perm, _ = permute_tensor_by_labels_triton(query, None, dim=2,
+                                                    sorted_indices=torch.cat((q_order, text_idx), 1).contiguous())
+        qc, kc = route.video_dynamic_map.shape[-2:]
+        block_map = F.pad(route.video_dynamic_map.view(B, H, qc, kc), (0, 2, 0, 2), value=False)
+        block_map[:, :, :-1, -2] = True
+        block_map[:, :, -2, :-1] = True
+        block_map[:, :, -1, -1] = True
+        qs = torch.cat((route.q_cluster_sizes.view(B, H, qc), sizes_tail.expand(B, H, 2)), 2)
+        ks = torch.cat((route.k_cluster_sizes.view(B, H, kc), sizes_tail.expand(B, H, 2)), 2)
+        if ev is not None:
+            ev[0].record()
+        out_perm = dynamic_block_sparse_fwd_flashinfer(q_perm, route.k_permuted, route.v_permuted, block_map, qs, ks,
+                                                       is_cpu=False)
+        if ev is not None:
+            ev[1].record()
+        base_video = apply_inverse_permutation_triton(out_perm[:, :, :Nv], q_order, dim=2)
+        repaired, info = core.repair(base_video, qv, key[:, :, :Nv + prompt], value[:, :, :Nv + prompt], route)
+        return route, block_map, qs, ks, info
+
+    for _ in range(max(args.warmup, 1)):  # the first call is the cold one
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        attn_events.append(ev)
+        route, block_map, qs, ks, info = step(ev)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    attn_ms = sum(a.elapsed_time(b) for a, b in attn_events) / len(attn_events)
+    kept = float((block_map.float() * qs[..., :, None].float() * ks[..., None, :].float()).sum().item()) * 4 * D
+    # one extra call with the route's stage marks (synchronising, so not in the timed steps)
+    core.profile_breakdown_active = True
+    t1 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    profiled_ms = (time.perf_counter() - t1) * 1e3
+    core.profile_breakdown_active = False
+    stages = {k[len("n8_route_"):-3]: round(v, 3) for k, v in core.last_route_profile.items()
+              if k.startswith("n8_route_") and k.endswith("_ms")}
+    bh, tot = B * H, Nv + text
+    # algorithmic HBM bytes of the streaming stages (bf16 Q/K/V rows, fp32 role features)
+    stage_bytes = {
+        "kv_projection_init": bh * Nv * (D * 2 + cfg.role_k_rank * 4),
+        "kv_centroids": bh * Nv * (2 * D * 2 + 4),
+        "q_projection_init": bh * Nv * (D * 2 + cfg.role_q_rank * 4),
+        "q_centroids": bh * Nv * (D * 2 + 4),
+        "kv_permute": bh * tot * (4 * D * 2 + 4),
+        "selector_scores": bh * tot * 2 * D * 2,
+    }
+    stage_roofline = {name: {"ms": stages[name], "gbs": round(b / stages[name] / 1e6, 1),
+                             "hbm_frac": round(b / stages[name] / 1e6 / HBM_PEAK_GBS, 4)}
+                      for name, b in stage_bytes.items() if stages.get(name)}
+    achieved = kept / (attn_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "N8 (HunyuanVideo adapter) layer ms: route + padded block-sparse attention + repair",
+        "value": round(ms, 3), "unit": "ms/layer", "n_gpus": 1, "steps": args.steps, "warmup": max(args.warmup, 1),
+        "ms_per_step": round(ms, 3), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (frame-correlated Gaussian mixture video + Gaussian text, seeded, on device)",
+        "config": {"workload": "C4-shaped HunyuanVideo N8 step: 1x24x(118800 video + 256 text, 77 prompt)x128 bf16, "
+                               "default N8V6Config (Qc 300, Kc 1000, ranks 64/48, density 0.22, 64 probes), warm calls",
+                   "q_kmeans_iters": int(route.q_kmeans_iters), "k_kmeans_iters": int(route.k_kmeans_iters),
+                   "base_video_density": round(float(route.base_video_density), 4),
+                   "effective_video_density": round(float(info["effective_video_density"]), 4),
+                   "kept_attention_tflop": round(kept / 1e12, 3), "generator": GEN},
+        "stages_ms": {"route_profiled_call_ms": round(profiled_ms, 3), **stages},
+        "stage_roofline": stage_roofline,
+        "roofline": {"kernel": "attn_pipe_kernel (padded N8 map)", "bound": "mfma", "achieved": round(achieved, 1),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel_ms": round(attn_ms, 3)},
+    }), flush=True)
+
+
 def _layer_configs():
     from sparsepr_amd import synthetic
     from sparsepr_amd.layer import SparsePRConfig
@@ -522,6 +633,8 @@ def main():
         return only_svg_ear(args)
     if args.only == "role_proj":
         return only_role_proj(args)
+    if args.only == "n8_route":
+        return only_n8_route(args)
     import torch
 
     torch.cuda.set_device(0)
