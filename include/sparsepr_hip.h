@@ -239,15 +239,18 @@ int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense,
 int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
                      const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
                      float alpha, float norm_cap, void* out, hipStream_t stream);
-/* residual_repair.py:317-465 _fit_reduced_rank_residual_fp32, for weights given, m >= p,
- * the full output basis of the raw residual and decomposition "eigh" (the N8 layer's
- * configuration): weighted standardisation (:364-384), primal ridge solve (:424-434),
- * top-rank eigenvectors of y_w^T y_w (:449-456; Householder tridiagonalisation,
- * multisection and inverse iteration) and left = weight . basis (:463-464).
- * x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
- * [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (basis columns in
- * ascending eigenvalue order).  Requires m >= p, m, p, d <= 128, 1 <= rank <= min(16, d).
- * workspace: spr_rrr_fit_workspace(bh) bytes of device memory. */
+/* residual_repair.py:263-465 fit_reduced_rank_residual / _fit_reduced_rank_residual_fp32 for
+ * every configuration it accepts with m, p, d <= 128 and rank <= 16:
+ *   weighted standardisation (:364-384; weights == NULL: plain mean and unbiased std);
+ *   primal ridge solve for m >= p (:424-434), dual for m < p (:386-423, both fit_backend
+ *   forms); the top-rank eigenvectors of the weighted output gram of the raw residual
+ *   (basis_source 0) or of the fitted values (1) (:435-462; the "full" and "skinny" /
+ *   eigh / SVD routes span this subspace); left = weight . basis or x_w^T dual basis (:463-464).
+ *   x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
+ *   [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (basis columns in
+ *   ascending eigenvalue order).  1 <= rank <= min(16, d, m).
+ *   workspace: spr_rrr_fit_workspace(bh) bytes of device memory.
+ * spr_rrr_fit is spr_rrr_fit_ex with basis_source 0. */
 size_t spr_rrr_fit_workspace(int64_t bh);
 int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p, int32_t d,
                 int32_t rank, float ridge, float* x_mean, float* x_scale, float* y_mean, float* left, float* basis,
@@ -310,6 +313,23 @@ int spr_role_metric(const void* x, int32_t dtype, int64_t bh, int64_t n, int32_t
  *   eigenvectors of the rank largest eigenvalues in ascending order; vals fp32 [bh, rank]
  *   (nullable) their Rayleigh quotients, ascending.  n <= 128, rank <= min(64, n).
  *   Householder tridiagonalisation, multisection on Sturm counts, inverse iteration, Cholesky-QR. */
+int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p, int32_t d,
+                   int32_t rank, float ridge, int32_t basis_source, float* x_mean, float* x_scale, float* y_mean,
+                   float* left, float* basis, void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* residual_repair.py:468-506 reduced_rank_output_basis: the top-rank right singular basis of
+ * a [bh, m, d] fp32 as the eigenvectors of a^T a (ascending), m, d <= 128, rank <= min(16, d).
+ * workspace: spr_rrr_fit_workspace(bh) bytes. */
+int spr_rrr_output_basis(const float* a, int64_t bh, int32_t m, int32_t d, int32_t rank, float* basis,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* residual_repair.py:509-587 recover_nonfinite_rrr_state: per head, a non-finite value in any
+ * of the five state tensors selects the previous state (prev_* all given) or the zero
+ * correction (x_mean 0, x_scale 1, y_mean 0, left 0, basis 0; prev_* all NULL).  out_* may
+ * alias the current state; recovered u8 [bh] (nullable). */
+int spr_rrr_recover(const float* x_mean, const float* x_scale, const float* y_mean, const float* left,
+                    const float* basis, const float* prev_x_mean, const float* prev_x_scale, const float* prev_y_mean,
+                    const float* prev_left, const float* prev_basis, int64_t bh, int32_t p, int32_t d, int32_t rank,
+                    float* out_x_mean, float* out_x_scale, float* out_y_mean, float* out_left, float* out_basis,
+                    uint8_t* recovered, hipStream_t stream);
 int spr_sym_top_eig(const float* mats, int64_t bh, int32_t n, int32_t rank, int32_t symmetrize, float* vecs,
                     float* vals, hipStream_t stream);
 /* operator_kmeans.py:95-151 metric_factor: factor fp32 [bh, n, rank] = top-rank eigenvectors of

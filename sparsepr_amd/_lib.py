@@ -75,6 +75,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_rrr_fit_workspace": (_sz, [_i64]),
     "spr_rrr_fit": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _sz, _vp]),
+    "spr_rrr_fit_ex": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp,
+                                      _vp, _vp, _sz, _vp]),
+    "spr_rrr_output_basis": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
+    "spr_rrr_recover": (ctypes.c_int, [_vp] * 10 + [_i64, _i32, _i32, _i32] + [_vp] * 7),
     "spr_sym_top_eig": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]),
     # metric.hip
     "spr_role_metric": (ctypes.c_int, [_vp, _i32, _i64, _i64, _i32, _vp, _i32, _vp, _i32, _f32, _vp, _vp]),

@@ -1,37 +1,43 @@
 // Weighted ridge reduced-rank residual fit.
 //
-// Replaces, for the configuration the N8 layer runs (weights given, M >= P,
-// full output basis of the raw residual, eigh):
-//   _fit_reduced_rank_residual_fp32 (src/sparsepr/models/cosmos3/residual_repair.py:317-465):
-//   weighted mean / variance standardisation (:364-384), the primal ridge solve
-//   (:424-434), the top-r eigenvectors of the weighted output gram y_w^T y_w
-//   (:449-456) and left = weight basis (:463-464).
+// Replaces _fit_reduced_rank_residual_fp32 (src/sparsepr/models/cosmos3/residual_repair.py:317-465)
+// for every configuration it accepts with M, P, D <= 128 and rank <= 16:
+//   weighted (or, without weights, plain mean and unbiased std) standardisation (:364-384);
+//   the ridge solve in primal form for M >= P (:424-434) and in dual form for M < P (:386-423);
+//   the output basis of the raw residual or of the fitted values (:435-462): the
+//   top-r eigenvectors of the weighted output gram, which span the same subspace as the
+//   "skinny" row-gram / SVD routes (:468-506);
+//   left = weight basis (primal) or x_w^T dual basis (dual) (:463-464).
+// recover_nonfinite_rrr_state (:509-587) is rrr_recover_kernel: a per-head finite test of the
+// five state tensors and a select against the previous state (or a zero correction).
 //
 // Per head, in fp32:
 //   w_sum = max(sum w, 1e-20); x_mean = sum w x / w_sum; x_scale = max(sqrt(sum w
-//   (x - x_mean)^2 / w_sum), 1e-5); y_mean = sum w y / w_sum;
-//   x_w = (x - x_mean) / x_scale * sqrt(w); y_w = (y - y_mean) * sqrt(w);
-//   G = x_w^T x_w + ridge I, B = y_w^T y_w;
-//   basis = top-`rank` eigenvectors of B, ascending eigenvalue order (as eigh);
-//   left = G^-1 x_w^T y_w basis = G^-1 x_w^T Z with Z = y_w basis.
+//   (x - x_mean)^2 / w_sum), 1e-5) (no weights: w = 1, variance over m - 1);
+//   y_mean = sum w y / w_sum; x_w = (x - x_mean) / x_scale * sqrt(w); y_w = (y - y_mean) * sqrt(w);
+//   primal: G = x_w^T x_w + ridge I (p x p); dual: G = x_w x_w^T + ridge I (m x m);
+//   raw basis: top-`rank` eigenvectors of B = y_w^T y_w (ascending eigenvalue order, as eigh);
+//   fitted basis: of B = F^T F with F = x_w G^-1 x_w^T y_w (primal) or y_w - ridge G^-1 y_w (dual);
+//   Z = y_w basis; left = G^-1 x_w^T Z (primal) or x_w^T G^-1 Z (dual).
 //
-// Four launches, stream ordered:
+// Launches, stream ordered (raw basis: four; fitted basis: seven):
 //   rrr_stats_kernel   one workgroup per head: the weighted statistics.
-//   rrr_gram_kernel    20 workgroups per head: one 32 x 32 lower tile of G or B
+//   rrr_gram_kernel    10 workgroups per matrix per head: one 32 x 32 lower tile of G or B
 //                      each, mirrored, into the workspace.
-//   rrr_factor_kernel  two workgroups per head, side by side:
-//     y = 0: eigenvectors of B.  B is held in registers (thread t owns row t / 8,
-//            columns t % 8 + 8 q) and reduced to tridiagonal form by Householder
-//            reflections (two barriers per column); the top eigenvalues come from
-//            64-way multisection on Sturm counts (one wave per eigenvalue), their
-//            vectors from inverse iteration on the tridiagonal matrix (pivoted LU,
-//            three steps, members of a cluster orthogonalised against each other
-//            as they are computed), the reflections are applied back, and a
-//            Cholesky-QR pass makes the basis orthonormal to rounding.
-//     y = 1: Cholesky factor of G, register resident, one barrier per column,
-//            written over G in the workspace.
-//   rrr_solve_kernel   one workgroup per head: Z = y_w basis, x_w^T Z (one wave per
-//                      basis column), forward and back substitution in registers.
+//   rrr_factor_kernel  one or two workgroups per head:
+//     eigen:   B is held in registers (thread t owns row t / 8, columns t % 8 + 8 q) and
+//              reduced to tridiagonal form by Householder reflections (two barriers per
+//              column); the top eigenvalues come from 64-way multisection on Sturm counts
+//              (one wave per eigenvalue), their vectors from inverse iteration on the
+//              tridiagonal matrix (pivoted LU, three steps, members of a cluster
+//              orthogonalised against each other as they are computed), the reflections are
+//              applied back, and a Cholesky-QR pass makes the basis orthonormal to rounding.
+//     Cholesky: factor of G, register resident, one barrier per column, written over G.
+//   rrr_fitted_kernel  (fitted basis) F into the workspace, then rrr_gram_kernel for B and
+//                      the eigen part of rrr_factor_kernel.
+//   rrr_solve_kernel   one workgroup per head: Z = y_w basis, then the substitutions
+//                      (one wave per basis column, refined twice against fp64 residuals)
+//                      and the x_w products of the form in use.
 #include "spr_common.h"
 
 namespace {
@@ -88,7 +94,10 @@ __device__ __forceinline__ float pick16(const float (&a)[16], int q) {
   return __int_as_float(v);
 }
 
-// ---- statistics: one workgroup of 256 threads per head
+// ---- statistics: one workgroup of 256 threads per head.  w == nullptr: unit weights,
+// the variance over m - 1 (torch.std), NaN at m = 1 as there.
+__device__ __forceinline__ float clamp_min_nan(float v, float lo) { return v != v ? v : fmaxf(v, lo); }
+
 __global__ __launch_bounds__(256) void rrr_stats_kernel(const float* __restrict__ x, const float* __restrict__ y,
                                                         const float* __restrict__ w, int32_t m, int32_t p, int32_t d,
                                                         float* __restrict__ x_mean, float* __restrict__ x_scale,
@@ -97,87 +106,114 @@ __global__ __launch_bounds__(256) void rrr_stats_kernel(const float* __restrict_
   const int64_t h = blockIdx.x;
   const float* xh = x + h * m * p;
   const float* yh = y + h * m * d;
-  const float* wh = w + h * m;
-  float ws = 0.0f;
-  for (int r = 0; r < m; ++r) ws += wh[r];
-  ws = fmaxf(ws, 1e-20f);
+  const float* wh = w != nullptr ? w + h * m : nullptr;
+  float ws = static_cast<float>(m), var_div = static_cast<float>(m - 1);
+  if (wh != nullptr) {
+    ws = 0.0f;
+    for (int r = 0; r < m; ++r) ws += wh[r];
+    ws = fmaxf(ws, 1e-20f);
+    var_div = ws;
+  }
   if (t < p) {
     float s = 0.0f;
 #pragma unroll 8
-    for (int r = 0; r < m; ++r) s += wh[r] * xh[r * p + t];
+    for (int r = 0; r < m; ++r) s += (wh != nullptr ? wh[r] : 1.0f) * xh[r * p + t];
     const float mean = s / ws;
     float v = 0.0f;
 #pragma unroll 8
     for (int r = 0; r < m; ++r) {
       const float dv = xh[r * p + t] - mean;
-      v += wh[r] * (dv * dv);
+      v += (wh != nullptr ? wh[r] : 1.0f) * (dv * dv);
     }
     x_mean[h * p + t] = mean;
-    x_scale[h * p + t] = fmaxf(sqrtf(v / ws), 1e-5f);
+    x_scale[h * p + t] = clamp_min_nan(sqrtf(v / var_div), 1e-5f);
   } else if (t >= RRR_MAX && t - RRR_MAX < d) {
     const int c = t - RRR_MAX;
     float s = 0.0f;
 #pragma unroll 8
-    for (int r = 0; r < m; ++r) s += wh[r] * yh[r * d + c];
+    for (int r = 0; r < m; ++r) s += (wh != nullptr ? wh[r] : 1.0f) * yh[r * d + c];
     y_mean[h * d + c] = s / ws;
   }
 }
 
-// ---- G and B, 32 x 32 lower tiles (10 per matrix), mirrored; zero outside p x p / d x d
+// Workspace per head: three 128 x 128 fp32 matrices.  Slot 0: G, then its Cholesky
+// factor; slot 1: B; slot 2: F (fitted basis only).
+constexpr int RRR_SLOTS = 3;
+__device__ __forceinline__ float* ws_slot(float* ws, int64_t h, int slot) {
+  return ws + (h * RRR_SLOTS + slot) * RRR_MAT;
+}
+
+// ---- Gram matrices, 32 x 32 lower tiles (10 per 128 x 128 matrix), mirrored; zero outside
+// the matrix.  The element (r, c) of the matrix whose Gram is summed over r:
+//   GRAM_PRIMAL   x_w[r][c]   (r < m, c < p)  -> G = x_w^T x_w + ridge I, slot 0
+//   GRAM_DUAL     x_w[c][r]   (r < p, c < m)  -> G = x_w x_w^T + ridge I, slot 0
+//   GRAM_RESIDUAL y_w[r][c]   (r < m, c < d)  -> B = y_w^T y_w, slot 1
+//   GRAM_PLAIN    a[r][c]     (r < m, c < d)  -> B = a^T a, slot 1 (row stride a_ld, head stride a_hs)
+// blockIdx.y / 10 picks kind0 or kind1, blockIdx.y % 10 the tile.
+enum GramKind : int32_t { GRAM_PRIMAL = 0, GRAM_DUAL = 1, GRAM_RESIDUAL = 2, GRAM_PLAIN = 3 };
+
 __global__ __launch_bounds__(256) void rrr_gram_kernel(const float* __restrict__ x, const float* __restrict__ y,
                                                        const float* __restrict__ w, int32_t m, int32_t p, int32_t d,
                                                        float ridge, const float* __restrict__ x_mean,
                                                        const float* __restrict__ x_scale,
-                                                       const float* __restrict__ y_mean, float* __restrict__ ws) {
+                                                       const float* __restrict__ y_mean, const float* __restrict__ a,
+                                                       int64_t a_hs, int32_t a_ld, int32_t kind0, int32_t kind1,
+                                                       float* __restrict__ ws) {
   __shared__ float pa[RRR_MAX][33];
   __shared__ float pb[RRR_MAX][33];
   const int t = threadIdx.x;
   const int64_t h = blockIdx.x;
-  const int which = blockIdx.y / 10;  // 0: G from x, 1: B from y
+  const int kind = blockIdx.y < 10 ? kind0 : kind1;
   const int lt = blockIdx.y % 10;
   const int ti = lt >= 6 ? 3 : (lt >= 3 ? 2 : (lt >= 1 ? 1 : 0));
   const int tj = lt - ti * (ti + 1) / 2;
-  const int cols = which == 0 ? p : d;
-  const float* src = which == 0 ? x + h * m * p : y + h * m * d;
-  const float* mu = which == 0 ? x_mean + h * p : y_mean + h * d;
-  const float* wh = w + h * m;
+  const int rows = kind == GRAM_DUAL ? p : m;
+  const int cols = kind == GRAM_PRIMAL ? p : (kind == GRAM_DUAL ? m : d);
+  const float* xh = x + h * m * p;
+  const float* yh = y + h * m * d;
+  const float* wh = w != nullptr ? w + h * m : nullptr;
+  const float* xm = x_mean + h * p;
+  const float* xs = x_scale + h * p;
+  const float* ym = y_mean + h * d;
+  const float* ah = a != nullptr ? a + h * a_hs : nullptr;
+  auto elem = [&](int r, int cc) -> float {
+    switch (kind) {
+      case GRAM_PRIMAL:
+        return (xh[r * p + cc] - xm[cc]) / xs[cc] * (wh != nullptr ? sqrtf(wh[r]) : 1.0f);
+      case GRAM_DUAL:
+        return (xh[cc * p + r] - xm[r]) / xs[r] * (wh != nullptr ? sqrtf(wh[cc]) : 1.0f);
+      case GRAM_RESIDUAL:
+        return (yh[r * d + cc] - ym[cc]) * (wh != nullptr ? sqrtf(wh[r]) : 1.0f);
+      default:
+        return ah[static_cast<int64_t>(r) * a_ld + cc];
+    }
+  };
   for (int e = t; e < RRR_MAX * 32; e += 256) {
     const int r = e >> 5, cc = e & 31;
     const int ci = 32 * ti + cc, cj = 32 * tj + cc;
-    float vi = 0.0f, vj = 0.0f;
-    if (r < m) {
-      const float sw = sqrtf(wh[r]);
-      if (ci < cols) {
-        const float c0 = src[r * cols + ci] - mu[ci];
-        vi = (which == 0 ? c0 / x_scale[h * p + ci] : c0) * sw;
-      }
-      if (cj < cols) {
-        const float c0 = src[r * cols + cj] - mu[cj];
-        vj = (which == 0 ? c0 / x_scale[h * p + cj] : c0) * sw;
-      }
-    }
-    pa[r][cc] = vi;
-    pb[r][cc] = vj;
+    pa[r][cc] = (r < rows && ci < cols) ? elem(r, ci) : 0.0f;
+    pb[r][cc] = (r < rows && cj < cols) ? elem(r, cj) : 0.0f;
   }
   __syncthreads();
-  const int a = t >> 4, b = t & 15;
+  const int ta = t >> 4, tb = t & 15;
   float s00 = 0.0f, s01 = 0.0f, s10 = 0.0f, s11 = 0.0f;
-  for (int r = 0; r < m; ++r) {
-    const float u0 = pa[r][2 * a], u1 = pa[r][2 * a + 1];
-    const float v0 = pb[r][2 * b], v1 = pb[r][2 * b + 1];
+  for (int r = 0; r < rows; ++r) {
+    const float u0 = pa[r][2 * ta], u1 = pa[r][2 * ta + 1];
+    const float v0 = pb[r][2 * tb], v1 = pb[r][2 * tb + 1];
     s00 += u0 * v0;
     s01 += u0 * v1;
     s10 += u1 * v0;
     s11 += u1 * v1;
   }
-  float* out = ws + (h * 2 + which) * RRR_MAT;
+  const bool is_g = kind == GRAM_PRIMAL || kind == GRAM_DUAL;
+  float* out = ws_slot(ws, h, is_g ? 0 : 1);
   const float acc[2][2] = {{s00, s01}, {s10, s11}};
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
-      const int gi = 32 * ti + 2 * a + u, gj = 32 * tj + 2 * b + v;
-      const float val = acc[u][v] + ((which == 0 && gi == gj && gi < cols) ? ridge : 0.0f);
+      const int gi = 32 * ti + 2 * ta + u, gj = 32 * tj + 2 * tb + v;
+      const float val = acc[u][v] + ((is_g && gi == gj && gi < cols) ? ridge : 0.0f);
       out[gi * RRR_MAX + gj] = val;
       if (ti != tj) out[gj * RRR_MAX + gi] = val;
     }
@@ -723,15 +759,17 @@ __device__ void rrr_cholesky(float* sm, float* __restrict__ gmat, int p) {
   }
 }
 
-__global__ __launch_bounds__(RRR_THREADS, 1) void rrr_factor_kernel(float* __restrict__ ws, int32_t p, int32_t d,
-                                                                    int32_t rank, float* __restrict__ basis) {
+// role = blockIdx.y + role0: 0 the eigenvectors of B (slot 1), 1 the Cholesky factor of the
+// ng x ng matrix G (slot 0).
+__global__ __launch_bounds__(RRR_THREADS, 1) void rrr_factor_kernel(float* __restrict__ ws, int32_t ng, int32_t d,
+                                                                    int32_t rank, int32_t role0,
+                                                                    float* __restrict__ basis) {
   __shared__ float sm[EigLayout<RRR_MAX_RANK>::FLOATS];
   const int64_t h = blockIdx.x;
-  if (blockIdx.y == 1) {
-    rrr_cholesky(sm, ws + (h * 2) * RRR_MAT, p);
+  if (blockIdx.y + role0 == 1) {
+    rrr_cholesky(sm, ws_slot(ws, h, 0), ng);
   } else {
-    rrr_eigen<RRR_MAX_RANK>(sm, ws + (h * 2 + 1) * RRR_MAT, RRR_MAX, d, rank, false, basis + h * d * rank,
-                            nullptr);
+    rrr_eigen<RRR_MAX_RANK>(sm, ws_slot(ws, h, 1), RRR_MAX, d, rank, false, basis + h * d * rank, nullptr);
   }
 }
 
@@ -747,15 +785,181 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void sym_top_eig_kernel(const float
                   vals != nullptr ? vals + h * rank : nullptr);
 }
 
-// Z = y_w basis, rb = x_w^T Z, left = L^-T L^-1 rb.
+// L (ng x ng lower, slot 0) into LDS and x_w^T into LDS ([p][m], zero padded).
+__device__ __forceinline__ void load_factor_and_xt(const float* __restrict__ lg, int ng, const float* __restrict__ xh,
+                                                   const float* __restrict__ wh, const float* __restrict__ xm,
+                                                   const float* __restrict__ xs, int m, int p, float* ls,
+                                                   float* xt) {
+  const int t = threadIdx.x, i = t >> 3, c = t & 7;
+  for (int e = t; e < RRR_MAT; e += RRR_THREADS) {
+    const int r = e >> 7, cc = e & 127;
+    ls[r * RRR_LS + cc] = (r < ng && cc <= r) ? lg[e] : 0.0f;
+  }
+  const float sw = i < m ? (wh != nullptr ? sqrtf(wh[i]) : 1.0f) : 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int j = c + 8 * q;
+    xt[j * RRR_LS + i] = (i < m && j < p) ? (xh[i * p + j] - xm[j]) / xs[j] * sw : 0.0f;
+  }
+}
+
+// L L^T u = b for one right-hand side held by a wave: entry k in lane k % 64 of b0 (k < 64)
+// or b1 (k >= 64).  Entries at or beyond n stay as they are.
+__device__ __forceinline__ void chol_solve_wave(const float* ls, int n, int lane, float& b0, float& b1) {
+  for (int k = 0; k < n; ++k) {  // L y = b
+    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
+    const float yk = bk / ls[k * RRR_LS + k];
+    if (lane == (k & 63)) {
+      if (k < 64) b0 = yk;
+      else b1 = yk;
+    }
+    if (lane > k && lane < n) b0 -= ls[lane * RRR_LS + k] * yk;
+    if (lane + 64 > k && lane + 64 < n) b1 -= ls[(lane + 64) * RRR_LS + k] * yk;
+  }
+  for (int k = n - 1; k >= 0; --k) {  // L^T u = y
+    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
+    const float xk = bk / ls[k * RRR_LS + k];
+    if (lane == (k & 63)) {
+      if (k < 64) b0 = xk;
+      else b1 = xk;
+    }
+    if (lane < k) b0 -= ls[k * RRR_LS + lane] * xk;
+    if (lane + 64 < k) b1 -= ls[k * RRR_LS + lane + 64] * xk;
+  }
+}
+
+// v = x_w^T u for u over the m rows (held as in chol_solve_wave): entry a (< p) in lane a % 64.
+__device__ __forceinline__ void xt_times(const float* xt, int m, int lane, float& b0, float& b1) {
+  float l0 = 0.0f, l1 = 0.0f;
+  for (int r = 0; r < m; ++r) {
+    const float u = lane_read(r < 64 ? b0 : b1, r & 63);
+    l0 += xt[lane * RRR_LS + r] * u;
+    l1 += xt[(lane + 64) * RRR_LS + r] * u;
+  }
+  b0 = l0;
+  b1 = l1;
+}
+
+__device__ __forceinline__ double lane_read_d(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(b), lane);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+
+// G u for the ridge system, in fp64 from x_w (exact fp32 values in xt) rather than from the
+// rounded G: dual (u over the m rows): x_w x_w^T u + ridge u; primal (u over the p
+// features): x_w^T x_w u + ridge u.  u and the result are held as in chol_solve_wave.
+__device__ __forceinline__ void ridge_apply_f64(const float* xt, bool dual, int m, int p, float ridge, int lane,
+                                                float u0, float u1, double& g0, double& g1) {
+  const int n_in = dual ? m : p, n_mid = dual ? p : m;
+  double v0 = 0.0, v1 = 0.0;  // the middle vector: x_w^T u (dual) or x_w u (primal)
+  for (int k = 0; k < n_in; ++k) {
+    const double uk = static_cast<double>(lane_read(k < 64 ? u0 : u1, k & 63));
+    // dual: v[a] = sum_r x_w[r][a] u[r] = xt[a][r]; primal: v[r] = sum_a x_w[r][a] u[a] = xt[a][r]
+    const float e0 = dual ? xt[lane * RRR_LS + k] : xt[k * RRR_LS + lane];
+    const float e1 = dual ? xt[(lane + 64) * RRR_LS + k] : xt[k * RRR_LS + lane + 64];
+    v0 = fma(static_cast<double>(e0), uk, v0);
+    v1 = fma(static_cast<double>(e1), uk, v1);
+  }
+  double w0 = 0.0, w1 = 0.0;  // x_w v (dual) or x_w^T v (primal)
+  for (int k = 0; k < n_mid; ++k) {
+    const double vk = lane_read_d(k < 64 ? v0 : v1, k & 63);
+    const float e0 = dual ? xt[k * RRR_LS + lane] : xt[lane * RRR_LS + k];
+    const float e1 = dual ? xt[k * RRR_LS + lane + 64] : xt[(lane + 64) * RRR_LS + k];
+    w0 = fma(static_cast<double>(e0), vk, w0);
+    w1 = fma(static_cast<double>(e1), vk, w1);
+  }
+  g0 = w0 + static_cast<double>(ridge) * u0;
+  g1 = w1 + static_cast<double>(ridge) * u1;
+}
+
+// Solve G u = b (b held as in chol_solve_wave, entries at or beyond ng zero) with the fp32
+// Cholesky factor and two steps of iterative refinement whose residuals b - G u are
+// accumulated in fp64 from x_w.  The condition number of G is about the largest eigenvalue
+// of the weighted gram over the ridge (1e5 and more for token-count weights), so the plain
+// fp32 solve keeps only a few digits; each refinement step multiplies its error by about
+// cond * 2^-24.
+__device__ __forceinline__ void ridge_solve_refined(const float* ls, const float* xt, bool dual, int m, int p,
+                                                    float ridge, int lane, float& b0, float& b1) {
+  const int ng = dual ? m : p;
+  const float r0 = b0, r1 = b1;
+  chol_solve_wave(ls, ng, lane, b0, b1);
+  for (int it = 0; it < 2; ++it) {
+    double g0, g1;
+    ridge_apply_f64(xt, dual, m, p, ridge, lane, b0, b1, g0, g1);
+    float d0 = lane < ng ? static_cast<float>(static_cast<double>(r0) - g0) : 0.0f;
+    float d1 = lane + 64 < ng ? static_cast<float>(static_cast<double>(r1) - g1) : 0.0f;
+    chol_solve_wave(ls, ng, lane, d0, d1);
+    b0 += d0;
+    b1 += d1;
+  }
+}
+
+// The weighted fitted values F [m][d] into slot 2 (row stride 128): one wave per column.
+//   dual:   F = y_w - ridge G^-1 y_w;  primal: F = x_w G^-1 x_w^T y_w.
+__global__ __launch_bounds__(RRR_THREADS, 1) void rrr_fitted_kernel(const float* __restrict__ x,
+                                                                    const float* __restrict__ y,
+                                                                    const float* __restrict__ w, int32_t m, int32_t p,
+                                                                    int32_t d, float ridge,
+                                                                    const float* __restrict__ x_mean,
+                                                                    const float* __restrict__ x_scale,
+                                                                    const float* __restrict__ y_mean,
+                                                                    float* __restrict__ ws) {
+  __shared__ float ls[RRR_MAX * RRR_LS];
+  __shared__ float xt[RRR_MAX * RRR_LS];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int64_t h = blockIdx.x;
+  const bool dual = m < p;
+  const int ng = dual ? m : p;
+  const float* wh = w != nullptr ? w + h * m : nullptr;
+  const float* yh = y + h * m * d;
+  const float* ym = y_mean + h * d;
+  load_factor_and_xt(ws_slot(ws, h, 0), ng, x + h * m * p, wh, x_mean + h * p, x_scale + h * p, m, p, ls, xt);
+  __syncthreads();
+  float* f = ws_slot(ws, h, 2);
+  const float sw0 = lane < m ? (wh != nullptr ? sqrtf(wh[lane]) : 1.0f) : 0.0f;
+  const float sw1 = lane + 64 < m ? (wh != nullptr ? sqrtf(wh[lane + 64]) : 1.0f) : 0.0f;
+  for (int col = wv; col < d; col += RRR_THREADS / 64) {
+    const float y0 = lane < m ? (yh[lane * d + col] - ym[col]) * sw0 : 0.0f;
+    const float y1 = lane + 64 < m ? (yh[(lane + 64) * d + col] - ym[col]) * sw1 : 0.0f;
+    float b0, b1;
+    if (dual) {
+      b0 = y0;
+      b1 = y1;
+      ridge_solve_refined(ls, xt, true, m, p, ridge, lane, b0, b1);
+      b0 = y0 - ridge * b0;
+      b1 = y1 - ridge * b1;
+    } else {
+      b0 = y0;
+      b1 = y1;
+      xt_times(xt, m, lane, b0, b1);  // x_w^T y_w[:, col]
+      ridge_solve_refined(ls, xt, false, m, p, ridge, lane, b0, b1);
+      float f0 = 0.0f, f1 = 0.0f;  // F[r] = sum_a x_w[r][a] W[a]
+      for (int r = 0; r < m; ++r) {
+        const float v = wave_sum(xt[lane * RRR_LS + r] * b0 + xt[(lane + 64) * RRR_LS + r] * b1);
+        if (lane == (r & 63)) {
+          if (r < 64) f0 = v;
+          else f1 = v;
+        }
+      }
+      b0 = f0;
+      b1 = f1;
+    }
+    if (lane < m) f[lane * RRR_MAX + col] = b0;
+    if (lane + 64 < m) f[(lane + 64) * RRR_MAX + col] = b1;
+  }
+}
+
+// Z = y_w basis, then left = G^-1 x_w^T Z (primal) or x_w^T G^-1 Z (dual).
 __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* __restrict__ x,
                                                                    const float* __restrict__ y,
                                                                    const float* __restrict__ w, int32_t m, int32_t p,
-                                                                   int32_t d, int32_t rank,
+                                                                   int32_t d, int32_t rank, float ridge,
                                                                    const float* __restrict__ x_mean,
                                                                    const float* __restrict__ x_scale,
                                                                    const float* __restrict__ y_mean,
-                                                                   const float* __restrict__ ws,
+                                                                   float* __restrict__ ws,
                                                                    const float* __restrict__ basis,
                                                                    float* __restrict__ left) {
   __shared__ float ls[RRR_MAX * RRR_LS];  // L (lower)
@@ -764,24 +968,21 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* 
   __shared__ __align__(16) float bs[RRR_MAX][RRR_MAX_RANK];
   const int t = threadIdx.x, i = t >> 3, c = t & 7, lane = t & 63, wv = t >> 6;
   const int64_t h = blockIdx.x;
-  const float* xh = x + h * m * p;
+  const bool dual = m < p;
+  const int ng = dual ? m : p;
   const float* yh = y + h * m * d;
-  const float* lg = ws + (h * 2) * RRR_MAT;
+  const float* wh = w != nullptr ? w + h * m : nullptr;
   for (int e = t; e < RRR_MAX * RRR_MAX_RANK; e += RRR_THREADS) {
     const int r = e / RRR_MAX_RANK, j = e % RRR_MAX_RANK;
     bs[r][j] = (r < d && j < rank) ? basis[(h * d + r) * rank + j] : 0.0f;
   }
-  for (int e = t; e < RRR_MAT; e += RRR_THREADS) {
-    const int r = e >> 7, cc = e & 127;
-    ls[r * RRR_LS + cc] = (r < p && cc <= r) ? lg[e] : 0.0f;
-  }
-  // thread (row i, columns c + 8 q): x_w to LDS transposed, y_w in registers
-  const float sw = i < m ? sqrtf(w[h * m + i]) : 0.0f;
+  load_factor_and_xt(ws_slot(ws, h, 0), ng, x + h * m * p, wh, x_mean + h * p, x_scale + h * p, m, p, ls, xt);
+  // thread (row i, columns c + 8 q): y_w in registers
+  const float sw = i < m ? (wh != nullptr ? sqrtf(wh[i]) : 1.0f) : 0.0f;
   float yw[16];
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int j = c + 8 * q;
-    xt[j * RRR_LS + i] = (i < m && j < p) ? (xh[i * p + j] - x_mean[h * p + j]) / x_scale[h * p + j] * sw : 0.0f;
     yw[q] = (i < m && j < d) ? (yh[i * d + j] - y_mean[h * d + j]) * sw : 0.0f;
   }
   __syncthreads();
@@ -809,76 +1010,172 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* 
   }
   __syncthreads();
   if (wv >= rank) return;
-  // rb[row][wv] for rows lane and lane + 64
   const int j = wv;
-  float b0 = 0.0f, b1 = 0.0f;
-  for (int r = 0; r < m; ++r) {
-    const float zr = zs[r][j];
-    b0 += xt[lane * RRR_LS + r] * zr;
-    b1 += xt[(lane + 64) * RRR_LS + r] * zr;
-  }
-  // forward: L y = rb
-  for (int k = 0; k < p; ++k) {
-    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
-    const float yk = bk / ls[k * RRR_LS + k];
-    if (lane == (k & 63)) {
-      if (k < 64) b0 = yk;
-      else b1 = yk;
-    }
-    if (lane > k && lane < p) b0 -= ls[lane * RRR_LS + k] * yk;
-    if (lane + 64 > k && lane + 64 < p) b1 -= ls[(lane + 64) * RRR_LS + k] * yk;
-  }
-  // backward: L^T x = y
-  for (int k = p - 1; k >= 0; --k) {
-    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
-    const float xk = bk / ls[k * RRR_LS + k];
-    if (lane == (k & 63)) {
-      if (k < 64) b0 = xk;
-      else b1 = xk;
-    }
-    if (lane < k) b0 -= ls[k * RRR_LS + lane] * xk;
-    if (lane + 64 < k) b1 -= ls[k * RRR_LS + lane + 64] * xk;
+  float b0 = zs[lane][j], b1 = zs[lane + 64][j];  // zero at rows >= m
+  if (dual) {
+    ridge_solve_refined(ls, xt, true, m, p, ridge, lane, b0, b1);
+    xt_times(xt, m, lane, b0, b1);
+  } else {
+    xt_times(xt, m, lane, b0, b1);
+    ridge_solve_refined(ls, xt, false, m, p, ridge, lane, b0, b1);
   }
   if (lane < p) left[(h * p + lane) * rank + j] = b0;
   if (lane + 64 < p) left[(h * p + lane + 64) * rank + j] = b1;
 }
 
+// Per head: recovered = any non-finite value in the five state tensors; the output takes the
+// previous state's values (prev non-null) or the zero correction (x_mean 0, x_scale 1,
+// y_mean 0, left 0, basis 0) where recovered, the current ones elsewhere.  out may alias cur.
+struct RrrState {
+  const float* t[5];
+};
+struct RrrStateOut {
+  float* t[5];
+};
+__global__ __launch_bounds__(256) void rrr_recover_kernel(RrrState cur, RrrState prev, RrrStateOut out, int32_t p,
+                                                          int32_t d, int32_t rank, uint8_t* __restrict__ recovered) {
+  const int64_t h = blockIdx.x;
+  const int64_t n[5] = {p, p, d, static_cast<int64_t>(p) * rank, static_cast<int64_t>(d) * rank};
+  int bad = 0;
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    for (int64_t e = threadIdx.x; e < n[k]; e += blockDim.x) {
+      const float v = cur.t[k][h * n[k] + e];
+      bad |= !(fabsf(v) <= 3.402823466e38f);
+    }
+  }
+  bad = __syncthreads_or(bad);
+#pragma unroll
+  for (int k = 0; k < 5; ++k) {
+    for (int64_t e = threadIdx.x; e < n[k]; e += blockDim.x) {
+      const int64_t o = h * n[k] + e;
+      float v = cur.t[k][o];
+      if (bad) v = prev.t[0] != nullptr ? prev.t[k][o] : (k == 1 ? 1.0f : 0.0f);
+      out.t[k][o] = v;
+    }
+  }
+  if (threadIdx.x == 0 && recovered != nullptr) recovered[h] = static_cast<uint8_t>(bad);
+}
+
 }  // namespace
 
 extern "C" size_t spr_rrr_fit_workspace(int64_t bh) {
-  return bh <= 0 ? 0 : static_cast<size_t>(bh) * 2 * RRR_MAT * sizeof(float);
+  return bh <= 0 ? 0 : static_cast<size_t>(bh) * RRR_SLOTS * RRR_MAT * sizeof(float);
 }
 
-// x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
-// [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (fp32).
-// Requires m >= p, m, p, d <= 128, 1 <= rank <= min(16, d).
-extern "C" int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
-                           int32_t d, int32_t rank, float ridge, float* x_mean, float* x_scale, float* y_mean,
-                           float* left, float* basis, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+// x [bh, m, p], y [bh, m, d], weights [bh, m] fp32 (nullable: unit weights, unbiased std);
+// outputs x_mean [bh, p], x_scale [bh, p], y_mean [bh, d], left [bh, p, rank], basis
+// [bh, d, rank] (fp32).  basis_source 0: raw residual, 1: fitted values.  m, p, d <= 128,
+// 1 <= rank <= min(16, d, m).
+extern "C" int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
+                              int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean,
+                              float* x_scale, float* y_mean, float* left, float* basis, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && m >= 1 && p >= 1 && d >= 1, "spr_rrr_fit: bad size");
-  SPR_REQUIRE(m >= p, "spr_rrr_fit: needs m >= p (got m=%d, p=%d)", m, p);
   SPR_REQUIRE(m <= RRR_MAX && p <= RRR_MAX && d <= RRR_MAX, "spr_rrr_fit: m, p, d must be at most %d", RRR_MAX);
-  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d, "spr_rrr_fit: rank %d outside [1, min(16, d)]", rank);
+  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d && rank <= m,
+              "spr_rrr_fit: rank %d outside [1, min(16, d, m)]", rank);
   SPR_REQUIRE(ridge >= 0.0f, "spr_rrr_fit: ridge must be non-negative");
+  SPR_REQUIRE(basis_source == 0 || basis_source == 1, "spr_rrr_fit: basis_source must be 0 (raw) or 1 (fitted)");
   SPR_REQUIRE(bh <= 65535, "spr_rrr_fit: too many heads");
   if (bh == 0) return SPR_OK;
-  SPR_REQUIRE(x && y && weights && x_mean && x_scale && y_mean && left && basis && workspace,
-              "spr_rrr_fit: null pointer");
+  SPR_REQUIRE(x && y && x_mean && x_scale && y_mean && left && basis && workspace, "spr_rrr_fit: null pointer");
   if (workspace_bytes < spr_rrr_fit_workspace(bh)) {
     spr_set_error("spr_rrr_fit: workspace too small (%zu < %zu)", workspace_bytes, spr_rrr_fit_workspace(bh));
     return SPR_EWORKSPACE;
   }
   float* ws = static_cast<float*>(workspace);
   const uint32_t nb = static_cast<uint32_t>(bh);
+  const bool dual = m < p;
+  const int32_t ng = dual ? m : p;
+  const int32_t gkind = dual ? GRAM_DUAL : GRAM_PRIMAL;
   rrr_stats_kernel<<<dim3(nb), 256, 0, stream>>>(x, y, weights, m, p, d, x_mean, x_scale, y_mean);
   SPR_LAUNCHED("rrr_stats_kernel");
-  rrr_gram_kernel<<<dim3(nb, 20), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, ws);
-  SPR_LAUNCHED("rrr_gram_kernel");
-  rrr_factor_kernel<<<dim3(nb, 2), RRR_THREADS, 0, stream>>>(ws, p, d, rank, basis);
-  SPR_LAUNCHED("rrr_factor_kernel");
-  rrr_solve_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, x_mean, x_scale, y_mean, ws,
-                                                         basis, left);
+  if (basis_source == 0) {
+    rrr_gram_kernel<<<dim3(nb, 20), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, nullptr,
+                                                      0, 0, gkind, GRAM_RESIDUAL, ws);
+    SPR_LAUNCHED("rrr_gram_kernel");
+    rrr_factor_kernel<<<dim3(nb, 2), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 0, basis);
+    SPR_LAUNCHED("rrr_factor_kernel");
+  } else {
+    rrr_gram_kernel<<<dim3(nb, 10), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, nullptr,
+                                                      0, 0, gkind, gkind, ws);
+    SPR_LAUNCHED("rrr_gram_kernel");
+    rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 1, basis);
+    SPR_LAUNCHED("rrr_factor_kernel");
+    rrr_fitted_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean,
+                                                            ws);
+    SPR_LAUNCHED("rrr_fitted_kernel");
+    rrr_gram_kernel<<<dim3(nb, 10), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean,
+                                                      ws + 2 * RRR_MAT, int64_t(RRR_SLOTS) * RRR_MAT, RRR_MAX,
+                                                      GRAM_PLAIN, GRAM_PLAIN, ws);
+    SPR_LAUNCHED("rrr_gram_kernel");
+    rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 0, basis);
+    SPR_LAUNCHED("rrr_factor_kernel");
+  }
+  rrr_solve_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, ridge, x_mean, x_scale,
+                                                         y_mean, ws, basis, left);
   SPR_LAUNCHED("rrr_solve_kernel");
+  return SPR_OK;
+}
+
+// The raw-residual fit (basis_source 0).
+extern "C" int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
+                           int32_t d, int32_t rank, float ridge, float* x_mean, float* x_scale, float* y_mean,
+                           float* left, float* basis, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return spr_rrr_fit_ex(x, y, weights, bh, m, p, d, rank, ridge, 0, x_mean, x_scale, y_mean, left, basis, workspace,
+                        workspace_bytes, stream);
+}
+
+// Top-`rank` right singular basis of a [bh, m, d] (fp32): the eigenvectors of a^T a,
+// ascending eigenvalue order.  m, d <= 128, 1 <= rank <= min(16, d).
+extern "C" int spr_rrr_output_basis(const float* a, int64_t bh, int32_t m, int32_t d, int32_t rank, float* basis,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && m >= 1 && d >= 1 && m <= RRR_MAX && d <= RRR_MAX,
+              "spr_rrr_output_basis: m, d must be in [1, %d]", RRR_MAX);
+  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d, "spr_rrr_output_basis: rank %d outside [1, min(16, d)]",
+              rank);
+  SPR_REQUIRE(bh <= 65535, "spr_rrr_output_basis: too many heads");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(a && basis && workspace, "spr_rrr_output_basis: null pointer");
+  if (workspace_bytes < spr_rrr_fit_workspace(bh)) {
+    spr_set_error("spr_rrr_output_basis: workspace too small (%zu < %zu)", workspace_bytes,
+                  spr_rrr_fit_workspace(bh));
+    return SPR_EWORKSPACE;
+  }
+  float* ws = static_cast<float*>(workspace);
+  const uint32_t nb = static_cast<uint32_t>(bh);
+  rrr_gram_kernel<<<dim3(nb, 10), 256, 0, stream>>>(nullptr, nullptr, nullptr, m, 1, d, 0.0f, nullptr, nullptr,
+                                                    nullptr, a, int64_t(m) * d, d, GRAM_PLAIN, GRAM_PLAIN, ws);
+  SPR_LAUNCHED("rrr_gram_kernel");
+  rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, 1, d, rank, 0, basis);
+  SPR_LAUNCHED("rrr_factor_kernel");
+  return SPR_OK;
+}
+
+// State tensors x_mean [bh, p], x_scale [bh, p], y_mean [bh, d], left [bh, p, rank],
+// basis [bh, d, rank] (fp32); prev_* all null (zero correction) or all given; out_* may
+// alias the current state; recovered [bh] u8 (nullable).
+extern "C" int spr_rrr_recover(const float* x_mean, const float* x_scale, const float* y_mean, const float* left,
+                               const float* basis, const float* prev_x_mean, const float* prev_x_scale,
+                               const float* prev_y_mean, const float* prev_left, const float* prev_basis, int64_t bh,
+                               int32_t p, int32_t d, int32_t rank, float* out_x_mean, float* out_x_scale,
+                               float* out_y_mean, float* out_left, float* out_basis, uint8_t* recovered,
+                               hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && p >= 1 && d >= 1 && rank >= 1, "spr_rrr_recover: bad size");
+  SPR_REQUIRE(bh <= 2147483647, "spr_rrr_recover: too many heads");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(x_mean && x_scale && y_mean && left && basis && out_x_mean && out_x_scale && out_y_mean && out_left &&
+                  out_basis,
+              "spr_rrr_recover: null pointer");
+  const int given = (prev_x_mean != nullptr) + (prev_x_scale != nullptr) + (prev_y_mean != nullptr) +
+                    (prev_left != nullptr) + (prev_basis != nullptr);
+  SPR_REQUIRE(given == 0 || given == 5, "spr_rrr_recover: give all five previous tensors or none");
+  const RrrState cur{{x_mean, x_scale, y_mean, left, basis}};
+  const RrrState prev{{prev_x_mean, prev_x_scale, prev_y_mean, prev_left, prev_basis}};
+  const RrrStateOut out{{out_x_mean, out_x_scale, out_y_mean, out_left, out_basis}};
+  rrr_recover_kernel<<<dim3(static_cast<uint32_t>(bh)), 256, 0, stream>>>(cur, prev, out, p, d, rank, recovered);
+  SPR_LAUNCHED("rrr_recover_kernel");
   return SPR_OK;
 }
 

@@ -544,7 +544,7 @@ class N8V6Core:
         state = fit_reduced_rank_residual(
             x_fit, y_fit, rank=min(cfg.repair_rank, count, dim), ridge=cfg.repair_ridge, weights=weights,
             output_basis_backend="skinny", cache_identity=True, fit_backend="dual_cholesky",
-            decomposition_backend="eigh", basis_source=cfg.repair_basis_source)
+            decomposition_backend="triton_top16", basis_source=cfg.repair_basis_source)
         state, self.repair_recovery_mask, policy = recover_nonfinite_rrr_state(state, self.repair_state_current)
         self.repair_state_current = state
         x_mean, x_scale, y_mean, left, basis = state

@@ -1,11 +1,11 @@
 """Current-step reduced-rank residual repair (drop-in for the reference's
 src/sparsepr/models/cosmos3/residual_repair.py).
 
-Probe selection, the fit-input gathers, the low-rank apply and the exact probe
-scatter are HIP kernels.  The fit itself is small batched linear algebra
-([BH, M, P] with M, P <= 128) and runs on the GPU through torch.linalg in fp32,
-with the reference's branch structure (dual Cholesky for M < P, primal solve
-otherwise; eigen basis of the weighted residual).
+Probe selection, the fit-input gathers, the reduced-rank fit (csrc/spr_rrr.hip: primal
+or dual ridge solve, raw or fitted output basis, with or without weights), the
+non-finite state recovery, the low-rank apply and the exact probe scatter are HIP
+kernels.  Configurations outside the kernels' limits (M, P, D > 128, rank > 16, role
+features in the apply) raise instead of falling back to another implementation.
 """
 
 from __future__ import annotations
@@ -118,20 +118,16 @@ def select_first_token_largest_groups(role_features, role_labels, *, num_cluster
 def fit_reduced_rank_residual(x_fit, y_fit, *, rank, ridge, weights=None, output_basis_backend="full",
                               cache_identity=False, fit_backend="standard", decomposition_backend="eigh",
                               basis_source="fitted_residual"):
-    """Weighted batched ridge reduced-rank regression in fp32 (reference :263-465).
+    """Weighted batched ridge reduced-rank regression in fp32 (reference :263-465), on
+    spr_rrr_fit_ex.  Returns (x_mean [BH,1,P], x_scale [BH,1,P], y_mean [BH,1,D],
+    left [BH,P,r], basis [BH,D,r]).
 
-    Returns (x_mean [BH,1,P], x_scale [BH,1,P], y_mean [BH,1,D], left [BH,P,r], basis [BH,D,r]).
-    decomposition_backend "triton_top16" (the reference's approximate top-16 power
-    iteration) is served by the exact eigen decomposition."""
-    with torch.autocast(device_type=x_fit.device.type, enabled=False):
-        return _fit_fp32(x_fit, y_fit, rank=rank, ridge=ridge, weights=weights,
-                         output_basis_backend=output_basis_backend, cache_identity=cache_identity,
-                         fit_backend=fit_backend, decomposition_backend=decomposition_backend,
-                         basis_source=basis_source)
-
-
-def _fit_fp32(x_fit, y_fit, *, rank, ridge, weights, output_basis_backend, cache_identity, fit_backend,
-              decomposition_backend, basis_source):
+    M < P solves in dual form, M >= P in primal form (both fit_backend values: they
+    differ in the factorisation the reference calls, not in the solution).  The basis is
+    the top-r eigenvectors of the weighted output gram of the raw residual or of the
+    fitted values; the "skinny" row-gram route and every decomposition_backend compute
+    the same subspace (the reference's "triton_top16" approximates it by power
+    iteration), so they share this exact solver.  cache_identity has no effect here."""
     if x_fit.ndim != 3 or y_fit.ndim != 3 or x_fit.shape[:2] != y_fit.shape[:2]:
         raise RuntimeError(
             "RRR expects X=[BH,M,P] and Y=[BH,M,D] with matching BH/M, got "
@@ -152,104 +148,29 @@ def _fit_fp32(x_fit, y_fit, *, rank, ridge, weights, output_basis_backend, cache
         )
     if basis_source not in {"fitted_residual", "raw_residual"}:
         raise RuntimeError(f"RRR basis_source must be 'fitted_residual' or 'raw_residual', got {basis_source!r}.")
-    x = x_fit.float()
-    y = y_fit.float()
-    if _rrr_fit_fused(x, y, weights, rank, output_basis_backend, basis_source):
-        return _rrr_fit_hip(x, y, weights, int(rank), float(ridge))
-    if weights is None:
-        w = torch.ones((*x.shape[:2], 1), device=x.device, dtype=torch.float32)
-        x_mean = x.mean(dim=1, keepdim=True)
-        x_scale = x.std(dim=1, keepdim=True).clamp_min(1e-5)
-        y_mean = y.mean(dim=1, keepdim=True)
-    else:
-        if weights.shape != x.shape[:2]:
-            raise RuntimeError(f"RRR weights must have shape {tuple(x.shape[:2])}, got {tuple(weights.shape)}.")
-        w = weights.to(device=x.device, dtype=torch.float32).unsqueeze(2)
-        w_sum = w.sum(dim=1, keepdim=True).clamp_min(1e-20)
-        x_mean = (w * x).sum(dim=1, keepdim=True) / w_sum
-        x_var = (w * (x - x_mean).square()).sum(dim=1, keepdim=True) / w_sum
-        x_scale = x_var.sqrt().clamp_min(1e-5)
-        y_mean = (w * y).sum(dim=1, keepdim=True) / w_sum
-    xn = (x - x_mean) / x_scale
-    yc = y - y_mean
-    sw = w.sqrt()
-    xw = xn * sw
-    yw = yc * sw
-    p = int(x.shape[2])
-    m = int(x.shape[1])
-    dual = None
-    weight = None
-    fitted = None
-    weighted_fitted = None
-
-    def eye(size):
-        base = cached_identity(size, device=x.device, dtype=torch.float32) if cache_identity else \
-            torch.eye(size, device=x.device, dtype=torch.float32)
-        return base.expand(x.shape[0], -1, -1)
-
-    if m < p:
-        gram = torch.bmm(xw, xw.transpose(1, 2))
-        if fit_backend == "dual_cholesky":
-            gram.diagonal(dim1=1, dim2=2).add_(float(ridge))
-            factor, _info = torch.linalg.cholesky_ex(gram, check_errors=False)
-            dual = torch.cholesky_solve(yw, factor)
-            weighted_fitted = torch.add(yw, dual, alpha=-float(ridge))
-        else:
-            dual = torch.linalg.solve_ex(gram + float(ridge) * eye(m), yw)[0]
-            weight = torch.bmm(xw.transpose(1, 2), dual)
-            fitted = torch.bmm(xn, weight)
-    else:
-        gram = torch.bmm(xw.transpose(1, 2), xw)
-        rhs = torch.bmm(xw.transpose(1, 2), yw)
-        weight = torch.linalg.solve_ex(gram + float(ridge) * eye(p), rhs)[0]
-        fitted = torch.bmm(xn, weight)
-    if output_basis_backend == "skinny" and m < int(y.shape[2]):
-        if basis_source == "raw_residual":
-            basis_input = yw
-        else:
-            if weighted_fitted is None:
-                weighted_fitted = fitted * sw
-            basis_input = weighted_fitted
-        basis = reduced_rank_output_basis(basis_input, rank=int(rank), backend=decomposition_backend)
-    else:
-        values = yc if basis_source == "raw_residual" else fitted
-        if values is None:  # dual Cholesky with the full basis: materialise the fit
-            values = torch.bmm(xn, torch.bmm(xw.transpose(1, 2), dual))
-        output_gram = torch.bmm(values.transpose(1, 2), values * w)
-        _evals, evecs = torch.linalg.eigh(output_gram)
-        basis = evecs[:, :, -int(rank):].contiguous()
-    if dual is not None and weight is None:
-        left = torch.bmm(xw.transpose(1, 2), torch.bmm(dual, basis)).contiguous()
-    else:
-        left = torch.bmm(weight, basis).contiguous()
-    return x_mean, x_scale, y_mean, left, basis
+    if (decomposition_backend == "triton_top16" and output_basis_backend == "skinny"
+            and x_fit.shape[1] < y_fit.shape[2] and rank != 16):
+        raise RuntimeError(f"triton_top16 requires rank=16, got {rank}.")
+    return _rrr_fit_hip(x_fit, y_fit, weights, int(rank), float(ridge),
+                        1 if basis_source == "fitted_residual" else 0)
 
 
-def _rrr_fit_fused(x, y, weights, rank, output_basis_backend, basis_source):
-    """Whether the fit is the one spr_rrr_fit computes in one kernel: weights given,
-    M >= P (primal ridge solve), the eigen basis of the raw weighted residual, every
-    dimension at most 128 and rank at most 16, on the GPU."""
-    bh, m, p = (int(v) for v in x.shape)
-    d = int(y.shape[2])
-    if not (x.is_cuda and weights is not None and basis_source == "raw_residual"):
-        return False
-    if output_basis_backend == "skinny" and m < d:
-        return False
-    return bh > 0 and p <= m <= 128 and d <= 128 and int(rank) <= 16
-
-
-def _rrr_fit_hip(x, y, weights, rank, ridge):
-    """Weighted standardisation, primal ridge solve and the top-rank eigenvectors of
-    y_w^T y_w in four launches (reference :364-384, :424-434, :449-456, :463-464).
-    Eigenvector signs (as eigh's) are arbitrary; left . basis^T does not depend on them."""
+def _rrr_fit_hip(x, y, weights, rank, ridge, basis_source=0):
+    """The fit in 4 launches (raw residual basis) or 7 (fitted values), fp32 whatever
+    the input dtype.  Eigenvector signs (as eigh's) are arbitrary; left . basis^T does
+    not depend on them."""
     dev = _lib.require_gpu(x, y, weights, what="reduced-rank residual fit")
-    if weights.shape != x.shape[:2]:
-        raise RuntimeError(f"RRR weights must have shape {tuple(x.shape[:2])}, got {tuple(weights.shape)}.")
     bh, m, p = (int(v) for v in x.shape)
     d = int(y.shape[2])
-    x = x.contiguous()
-    y = y.contiguous()
-    w = weights.to(device=dev, dtype=torch.float32).contiguous()
+    if max(m, p, d) > 128 or rank > 16:
+        raise NotImplementedError(
+            f"The MI355X reduced-rank fit handles M, P, D <= 128 and rank <= 16; got M={m}, P={p}, D={d}, "
+            f"rank={rank}.")
+    if weights is not None and tuple(weights.shape) != (bh, m):
+        raise RuntimeError(f"RRR weights must have shape {(bh, m)}, got {tuple(weights.shape)}.")
+    x = x.float().contiguous()
+    y = y.float().contiguous()
+    w = None if weights is None else weights.to(device=dev, dtype=torch.float32).contiguous()
     f32 = dict(device=dev, dtype=torch.float32)
     x_mean = torch.empty((bh, 1, p), **f32)
     x_scale = torch.empty((bh, 1, p), **f32)
@@ -257,47 +178,50 @@ def _rrr_fit_hip(x, y, weights, rank, ridge):
     left = torch.empty((bh, p, rank), **f32)
     basis = torch.empty((bh, d, rank), **f32)
     ws_bytes = int(_lib.query("spr_rrr_fit_workspace", bh))
-    ws = torch.empty((ws_bytes,), device=dev, dtype=torch.uint8)
-    _lib.call("spr_rrr_fit", _lib.ptr(x), _lib.ptr(y), _lib.ptr(w), bh, m, p, d, rank, ridge, _lib.ptr(x_mean),
-              _lib.ptr(x_scale), _lib.ptr(y_mean), _lib.ptr(left), _lib.ptr(basis), _lib.ptr(ws), ws_bytes,
-              _lib.stream(dev))
+    ws = _lib.workspace(ws_bytes, dev)
+    _lib.call("spr_rrr_fit_ex", _lib.ptr(x), _lib.ptr(y), _lib.ptr(w), bh, m, p, d, rank, ridge, int(basis_source),
+              _lib.ptr(x_mean), _lib.ptr(x_scale), _lib.ptr(y_mean), _lib.ptr(left), _lib.ptr(basis), _lib.ptr(ws),
+              ws_bytes, _lib.stream(dev))
     return x_mean, x_scale, y_mean, left, basis
 
 
 def reduced_rank_output_basis(weighted_fitted, *, rank, backend):
-    """Top-r right singular basis of [BH, M, D] via the M x M row gram (reference :468-506)."""
+    """Top-r right singular basis of [BH, M, D] (reference :468-506) on spr_rrr_output_basis:
+    the eigenvectors of A^T A, orthonormal, ascending.  Every backend names this subspace."""
     if weighted_fitted.ndim != 3:
         raise RuntimeError(f"weighted_fitted must have shape [BH,M,D], got {tuple(weighted_fitted.shape)}.")
     if rank <= 0 or rank > min(weighted_fitted.shape[1:]):
         raise RuntimeError(f"Invalid rank={rank} for weighted_fitted={tuple(weighted_fitted.shape)}.")
-    if backend in {"eigh", "triton_top16"}:
-        row_gram = torch.bmm(weighted_fitted, weighted_fitted.transpose(1, 2))
-        eigenvalues, left_vectors = torch.linalg.eigh(row_gram)
-        left_vectors = left_vectors[:, :, -rank:]
-        scales = eigenvalues[:, -rank:].clamp_min(1e-20).rsqrt().unsqueeze(1)
-        return (torch.bmm(weighted_fitted.transpose(1, 2), left_vectors) * scales).contiguous()
-    if backend not in {"svd_gesvdj", "svd_gesvd"}:
+    if backend == "triton_top16" and rank != 16:
+        raise RuntimeError(f"triton_top16 requires rank=16, got {rank}.")
+    if backend not in {"eigh", "triton_top16", "svd_gesvdj", "svd_gesvd"}:
         raise RuntimeError(f"Unknown exact decomposition backend {backend!r}.")
-    _u, _s, vh = torch.linalg.svd(weighted_fitted, full_matrices=False)
-    return vh[:, :rank, :].transpose(1, 2).contiguous()
+    dev = _lib.require_gpu(weighted_fitted, what="reduced-rank output basis")
+    bh, m, d = (int(v) for v in weighted_fitted.shape)
+    if max(m, d) > 128 or rank > 16:
+        raise NotImplementedError(f"The MI355X output basis handles M, D <= 128 and rank <= 16; got M={m}, D={d}, "
+                                  f"rank={rank}.")
+    a = weighted_fitted.float().contiguous()
+    basis = torch.empty((bh, d, int(rank)), device=dev, dtype=torch.float32)
+    ws_bytes = int(_lib.query("spr_rrr_fit_workspace", bh))
+    ws = _lib.workspace(ws_bytes, dev)
+    _lib.call("spr_rrr_output_basis", _lib.ptr(a), bh, m, d, int(rank), _lib.ptr(basis), _lib.ptr(ws), ws_bytes,
+              _lib.stream(dev))
+    return basis
 
 
 def recover_nonfinite_rrr_state(state, previous):
-    """Per-head containment of a non-finite fit (reference :509-587): reuse the
-    head's previous state, or a zero correction when there is none."""
+    """Per-head containment of a non-finite fit (reference :509-587) on spr_rrr_recover:
+    a head with any non-finite state value takes its previous state, or a zero
+    correction when there is none.  Returns (state, recovered [BH] bool, policy)."""
     if len(state) != 5:
         raise RuntimeError(f"RRR state must contain five tensors, got {len(state)}.")
     batch_heads = int(state[0].shape[0])
     if any(int(t.shape[0]) != batch_heads for t in state):
         raise RuntimeError("RRR state tensors must share their batch-head dimension.")
-    recovered = torch.zeros(batch_heads, device=state[0].device, dtype=torch.bool)
-    for t in state:
-        if not torch.is_floating_point(t):
-            raise RuntimeError("RRR state tensors must be floating point.")
-        recovered |= ~torch.isfinite(t).reshape(batch_heads, -1).all(dim=1)
+    if any(not torch.is_floating_point(t) for t in state):
+        raise RuntimeError("RRR state tensors must be floating point.")
     if previous is None:
-        fallback = (torch.zeros_like(state[0]), torch.ones_like(state[1]), torch.zeros_like(state[2]),
-                    torch.zeros_like(state[3]), torch.zeros_like(state[4]))
         policy = "zero_repair_without_previous_state"
     else:
         if len(previous) != len(state) or any(
@@ -305,33 +229,41 @@ def recover_nonfinite_rrr_state(state, previous):
             for old, new in zip(previous, state, strict=True)
         ):
             raise RuntimeError("Previous RRR state does not match the current fit.")
-        fallback = previous
         policy = "reuse_previous_finite_repair_state"
-    selected = tuple(
-        torch.where(recovered.reshape(batch_heads, *((1,) * (cur.ndim - 1))), old, cur)
-        for cur, old in zip(state, fallback, strict=True)
-    )
-    return selected, recovered, policy
+    dev = _lib.require_gpu(*state, what="RRR state recovery")
+    x_mean, x_scale, y_mean, left, basis = state
+    p, d, rank = int(left.shape[1]), int(basis.shape[1]), int(left.shape[2])
+    shapes = [(batch_heads, 1, p), (batch_heads, 1, p), (batch_heads, 1, d), (batch_heads, p, rank),
+              (batch_heads, d, rank)]
+    if [tuple(t.shape) for t in state] != shapes:
+        raise RuntimeError(f"RRR state shapes {[tuple(t.shape) for t in state]} do not match {shapes}.")
+    cur = [t.float().contiguous() for t in state]
+    prev = [None] * 5 if previous is None else [t.float().contiguous() for t in previous]
+    out = [torch.empty_like(t) for t in cur]
+    recovered = torch.empty((batch_heads,), device=dev, dtype=torch.uint8)
+    _lib.call("spr_rrr_recover", *[_lib.ptr(t) for t in cur], *[_lib.ptr(t) for t in prev], batch_heads, p, d, rank,
+              *[_lib.ptr(t) for t in out], _lib.ptr(recovered), _lib.stream(dev))
+    selected = tuple(o if o.dtype == t.dtype else o.to(t.dtype) for o, t in zip(out, state))
+    return selected, recovered.bool(), policy
 
 
 def apply_reduced_rank_residual(base, role, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap):
-    """base + alpha * correction (optional norm cap), cast to base.dtype (reference :620-646).
-    Output-only bf16 rank-16 states with D in {64, 128} use the HIP apply kernel;
-    other shapes (role features, other ranks) use torch ops on the GPU."""
-    if (role is None and base.is_cuda and base.dtype == torch.bfloat16 and base.shape[2] in (64, 128)
-            and left.shape[2] == 16 and left.shape[1] == base.shape[2]):
-        from .kernels.residual_repair import repair_apply_output
-
-        return repair_apply_output(base.contiguous(), x_mean.contiguous(), x_scale.contiguous(),
-                                   y_mean.contiguous(), left.contiguous(), basis.contiguous(), alpha, norm_cap)
-    base_dim = int(base.shape[2])
-    coords = torch.bmm((base.float() - x_mean[:, :, :base_dim]) / x_scale[:, :, :base_dim], left[:, :base_dim])
+    """base + alpha * correction (optional norm cap), in base's dtype (reference :600-646), on
+    the HIP apply kernel: output-only states (role None), bf16 base, D in {64, 128},
+    rank <= 16 (a smaller rank is padded with zero columns, which add nothing)."""
     if role is not None:
-        coords = coords + torch.bmm((role.float() - x_mean[:, :, base_dim:]) / x_scale[:, :, base_dim:],
-                                    left[:, base_dim:])
-    correction = torch.bmm(coords, basis.transpose(1, 2)) + y_mean
-    if norm_cap > 0.0:
-        cn = torch.linalg.vector_norm(correction, dim=2, keepdim=True).clamp_min(1e-20)
-        bn = torch.linalg.vector_norm(base.float(), dim=2, keepdim=True)
-        correction = correction * (float(norm_cap) * bn / cn).clamp_max(1.0)
-    return (base.float() + float(alpha) * correction).to(base.dtype)
+        raise NotImplementedError("The MI355X repair apply takes output features only; role features "
+                                  "(repair_features='output_role') are not built.")
+    bh, tokens, dim = (int(v) for v in base.shape)
+    rank = int(left.shape[2])
+    if base.dtype != torch.bfloat16 or dim not in (64, 128) or rank > 16 or int(left.shape[1]) != dim:
+        raise NotImplementedError(
+            f"The MI355X repair apply needs a bf16 base with D in (64, 128) and rank <= 16; got {base.dtype}, "
+            f"D={dim}, rank={rank}, left={tuple(left.shape)}.")
+    from .kernels.residual_repair import repair_apply_output
+
+    if rank < 16:
+        left = torch.nn.functional.pad(left.float(), (0, 16 - rank))
+        basis = torch.nn.functional.pad(basis.float(), (0, 16 - rank))
+    return repair_apply_output(base.contiguous(), x_mean.contiguous(), x_scale.contiguous(), y_mean.contiguous(),
+                               left.contiguous(), basis.contiguous(), alpha, norm_cap)

@@ -275,13 +275,25 @@ def test_n8_hunyuan_composition_default_config(dev, oracle):
         er, ew = oracle.select_role_equal_probes_vectorized(feats, ql[h:h + 1], cfg.num_q_centroids, cfg.probe_rows)
         assert (rr == er[0]).all() and np.allclose(rw, ew[0], rtol=1e-6)
         bh_np = base_video[0, h].float().cpu().numpy()
-        dense = oracle.to_bf16(oracle.dense_attention(qh[rr][None], kh[None], vh[None]).astype(np.float32))
+        gr = repaired[0, h].float().cpu().numpy()
+        # the probe rows of the output are the GPU's dense probe attention (bf16 operands and
+        # probabilities): within the attention bound of the float64 attention
+        dense_ref = oracle.dense_attention(qh[rr][None], kh[None], vh[None])[0]
+        dense = gr[rr][None]
+        assert np.abs(dense[0] - dense_ref).max() <= 2e-2
+        # the repair of the GPU base fitted to those probes by the float64 oracle (the fit's
+        # raw-residual basis turns with one-ulp changes of the targets when its eigengap at
+        # the rank cut is small, so both fits see the same targets)
         xfit = bh_np[rr][None]
         state = oracle.fit_reduced_rank_residual(xfit, dense - xfit, cfg.repair_rank, cfg.repair_ridge, rw[None])
         ref_out = oracle.repair_apply(bh_np[None], *state, cfg.repair_alpha, 0.0)[0]
         ref_out[rr] = dense[0]
-        gr = repaired[0, h].float().cpu().numpy()
-        assert np.abs(gr - ref_out).max() <= 2e-2
+        # bf16 output: one ulp of the value (a rounding flip between the fp32 and float64
+        # corrections) plus 1e-2 for the fp32 fit
+        err = np.abs(gr - ref_out)
+        bound = 1e-2 + 2.0 ** -8 * np.abs(ref_out)
+        worst = np.unravel_index(np.argmax(err - bound), err.shape)
+        assert (err <= bound).all(), (h, worst, float(err[worst]), float(ref_out[worst]), float(err.max()))
     # text rows (hunyuanvideo.py:203-207): the prompt queries see every video key and the
     # prompt keys; the padding queries see only the padding keys
     tq = query[0, :, Nv:].float().cpu().numpy()

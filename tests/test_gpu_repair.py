@@ -133,30 +133,86 @@ def test_fit_prep_apply_scatter(dev, oracle):
         assert (o[h, rows[h]] == dense[h]).all()
 
 
-@pytest.mark.parametrize("m,p", [(128, 128), (64, 128), (64, 64)])
-def test_rrr_fit_matches_float64(dev, oracle, m, p):
+@pytest.mark.parametrize("m,p", [(128, 128), (64, 128), (64, 64), (40, 96)])
+@pytest.mark.parametrize("basis_source", ["raw_residual", "fitted_residual"])
+@pytest.mark.parametrize("weighted", [True, False])
+def test_rrr_fit_matches_float64(dev, oracle, m, p, basis_source, weighted):
+    """fit_reduced_rank_residual in primal (M >= P) and dual (M < P) form, with and without
+    weights (unit weights, unbiased std), raw-residual and fitted-value bases, against the
+    float64 fit: statistics to 1e-4, the basis-independent map left . basis^T to 2e-3."""
     from sparsepr_amd.residual_repair import fit_reduced_rank_residual
 
     rng = np.random.default_rng(m + p)
     x = rng.standard_normal((4, m, p)).astype(np.float32)
     y = (x @ rng.standard_normal((4, p, p)).astype(np.float32) * 0.05
          + 0.02 * rng.standard_normal((4, m, p)).astype(np.float32))
-    w = rng.uniform(0.5, 2.0, (4, m)).astype(np.float32)
-    got = fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=16, ridge=0.1, weights=to_dev(w, dev),
+    w = rng.uniform(0.5, 2.0, (4, m)).astype(np.float32) if weighted else None
+    got = fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=16, ridge=0.1,
+                                    weights=None if w is None else to_dev(w, dev),
                                     output_basis_backend="skinny", fit_backend="dual_cholesky",
-                                    decomposition_backend="eigh", basis_source="raw_residual")
-    ref = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w)
+                                    decomposition_backend="triton_top16", basis_source=basis_source)
+    ref = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=basis_source)
     for g, r in zip(got[:3], ref[:3]):
         assert np.allclose(g.cpu().numpy(), r, rtol=1e-4, atol=1e-5)
     # left basis^T is the basis-independent part of the fitted map
     gl = (got[3] @ got[4].transpose(1, 2)).cpu().numpy()
     rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
-    assert np.allclose(gl, rl, rtol=2e-3, atol=2e-4)
+    assert np.abs(gl - rl).max() <= 2e-3 * np.abs(rl).max()
 
 
-@pytest.mark.parametrize("m,p,d,rank", [(128, 128, 128, 16), (128, 64, 128, 16), (96, 96, 33, 5), (17, 9, 7, 1)])
+def test_rrr_fit_unweighted_single_row_is_recovered(dev):
+    """M = 1 without weights: the unbiased std is NaN (as torch.std), the state is non-finite
+    and the recovery selects the zero correction."""
+    from sparsepr_amd.residual_repair import fit_reduced_rank_residual, recover_nonfinite_rrr_state
+
+    x = torch.randn((2, 1, 8), device=dev)
+    y = torch.randn((2, 1, 8), device=dev)
+    st = fit_reduced_rank_residual(x, y, rank=1, ridge=0.1, basis_source="raw_residual")
+    assert torch.isnan(st[1]).all()
+    sel, rec, _ = recover_nonfinite_rrr_state(st, None)
+    assert rec.all() and (sel[1] == 1).all() and (sel[3] == 0).all() and (sel[4] == 0).all()
+
+
+@pytest.mark.parametrize("m,d,rank", [(64, 128, 16), (128, 128, 16), (30, 17, 5)])
+def test_reduced_rank_output_basis(dev, m, d, rank):
+    """The top right singular subspace of [BH, M, D] against numpy's SVD: orthonormal basis,
+    equal projector (a gap at the cut)."""
+    from sparsepr_amd.residual_repair import reduced_rank_output_basis
+
+    rng = np.random.default_rng(m * d + rank)
+    k = min(m, d)
+    sv = np.concatenate([np.linspace(10.0, 5.0, rank), np.linspace(1.0, 0.1, k - rank)])
+    a = np.stack([np.linalg.qr(rng.standard_normal((m, k)))[0] * sv @ np.linalg.qr(rng.standard_normal((d, k)))[0].T
+                  for _ in range(3)]).astype(np.float32)
+    b = reduced_rank_output_basis(to_dev(a, dev), rank=rank, backend="eigh").cpu().numpy().astype(np.float64)
+    assert np.abs(np.swapaxes(b, 1, 2) @ b - np.eye(rank)).max() <= 1e-5
+    vt = np.linalg.svd(a.astype(np.float64), full_matrices=False)[2][:, :rank]
+    assert np.abs(b @ np.swapaxes(b, 1, 2) - np.swapaxes(vt, 1, 2) @ vt).max() <= 1e-4
+
+
+def test_apply_pads_small_rank(dev, oracle):
+    """apply_reduced_rank_residual at rank 5 (zero-padded to the kernel's 16) against float64."""
+    from sparsepr_amd.residual_repair import apply_reduced_rank_residual
+
+    rng = np.random.default_rng(9)
+    bh, n, d, r = 2, 700, 128, 5
+    base = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    st = [rng.standard_normal((bh, 1, d)).astype(np.float32) * 0.1, rng.uniform(0.5, 2, (bh, 1, d)).astype(np.float32),
+          rng.standard_normal((bh, 1, d)).astype(np.float32) * 0.1,
+          rng.standard_normal((bh, d, r)).astype(np.float32) * 0.05, rng.standard_normal((bh, d, r)).astype(np.float32)]
+    out = apply_reduced_rank_residual(to_dev(base, dev, torch.bfloat16), None, *[to_dev(t, dev) for t in st], 0.8, 0.0)
+    ref = oracle.repair_apply(base, *st, 0.8, 0.0)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
+    with pytest.raises(NotImplementedError, match="output features only"):
+        apply_reduced_rank_residual(to_dev(base, dev, torch.bfloat16), torch.zeros(1, device=dev),
+                                    *[to_dev(t, dev) for t in st], 0.8, 0.0)
+
+
+@pytest.mark.parametrize("m,p,d,rank", [(128, 128, 128, 16), (128, 64, 128, 16), (96, 96, 33, 5), (17, 9, 7, 1),
+                                        (64, 128, 128, 16), (17, 40, 7, 1)])
 def test_rrr_fused_fit_kernel(dev, oracle, m, p, d, rank):
-    """spr_rrr_fit (one-sided Jacobi basis, Cholesky ridge solve) against the float64 fit:
+    """spr_rrr_fit (Householder + multisection eigen basis, Cholesky ridge solve in primal or
+    dual form) against the float64 fit:
     statistics, the basis-independent map left . basis^T, an orthonormal basis and
     basis^T (y_w^T y_w) basis equal to the top eigenvalues in ascending order."""
     from sparsepr_amd import residual_repair as rr
@@ -169,7 +225,6 @@ def test_rrr_fused_fit_kernel(dev, oracle, m, p, d, rank):
     w = rng.uniform(0.5, 2.0, (bh, m)).astype(np.float32)
     w[0, : m // 4] = 0.0  # rows outside the fit
     xt, yt, wt = to_dev(x, dev), to_dev(y, dev), to_dev(w, dev)
-    assert rr._rrr_fit_fused(xt, yt, wt, rank, "skinny", "raw_residual")
     got = [t.cpu().numpy().astype(np.float64) for t in rr._rrr_fit_hip(xt, yt, wt, rank, 0.1)]
     ref = oracle.fit_reduced_rank_residual(x, y, rank, 0.1, w)
     for g, r in zip(got[:3], ref[:3]):
@@ -218,14 +273,27 @@ def test_rrr_fused_fit_degenerate_spectra(dev, oracle):
     assert np.abs(gl[1]).max() <= 1e-6  # zero residual: zero correction
 
 
-def test_recover_nonfinite_state_gpu(dev):
+def test_recover_nonfinite_state_gpu(dev, oracle):
+    """spr_rrr_recover against the oracle's per-head select: NaN and inf heads, no previous
+    state (zero correction) and a previous state."""
     from sparsepr_amd.residual_repair import recover_nonfinite_rrr_state
 
-    st = tuple(torch.randn(3, 4, 5, device=dev) for _ in range(5))
-    bad = tuple(t.clone() for t in st)
-    bad[2][1, 0, 0] = float("nan")
-    sel, mask, policy = recover_nonfinite_rrr_state(bad, None)
-    assert mask.cpu().tolist() == [False, True, False] and policy.startswith("zero")
-    assert (sel[1][1] == 1).all() and (sel[3][1] == 0).all() and torch.equal(sel[3][0], st[3][0])
-    sel, mask, policy = recover_nonfinite_rrr_state(bad, st)
-    assert torch.equal(sel[2][1], st[2][1]) and policy.startswith("reuse")
+    rng = np.random.default_rng(4)
+    bh, p, d, r = 4, 128, 96, 16
+    shapes = [(bh, 1, p), (bh, 1, p), (bh, 1, d), (bh, p, r), (bh, d, r)]
+    st = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    prev = [rng.standard_normal(sh).astype(np.float32) for sh in shapes]
+    st[2][1, 0, 7] = np.nan
+    st[4][3, 95, 15] = np.inf
+    st[3][3, 0, 0] = -np.inf
+    cur = tuple(to_dev(t, dev) for t in st)
+    for previous in (None, prev):
+        sel, mask, policy = recover_nonfinite_rrr_state(cur, None if previous is None else
+                                                        tuple(to_dev(t, dev) for t in previous))
+        ref_sel, ref_rec = oracle.recover_nonfinite_rrr_state(st, previous)
+        assert mask.cpu().numpy().tolist() == ref_rec.tolist() == [False, True, False, True]
+        assert policy.startswith("zero" if previous is None else "reuse")
+        for g, want in zip(sel, ref_sel):
+            assert np.array_equal(g.cpu().numpy(), want)
+    with pytest.raises(RuntimeError, match="five tensors"):
+        recover_nonfinite_rrr_state(cur[:4], None)
