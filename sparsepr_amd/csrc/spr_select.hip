@@ -76,14 +76,48 @@ __device__ __forceinline__ float row_dot(const float* q_row, const float* kr, in
   return acc;
 }
 
+// Sorts n2 (a power of two) (value, index) pairs in LDS so that ranks_before holds along
+// the array (a bitonic network; the order is total, so the result equals a rank sort's).
+// Every thread of the block calls it.
+__device__ void bitonic_rank_sort(float* v, int32_t* idx, int n2) {
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < n2; i += blockDim.x) {
+        const int l = i ^ stride;
+        if (l > i) {
+          const float vi = v[i], vl = v[l];
+          const int32_t ii = idx[i], il = idx[l];
+          const bool first = (i & size) == 0;  // this run ends up in ranks_before order
+          const bool swap = first ? ranks_before(vl, il, vi, ii) : ranks_before(vi, ii, vl, il);
+          if (swap) {
+            v[i] = vl;
+            v[l] = vi;
+            idx[i] = il;
+            idx[l] = ii;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ int pow2_at_least(int n) {
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  return n2;
+}
+
 // One workgroup per (bh, q-cluster) row.
-//   scores, max, weighted exp, sum (one thread, index order), probabilities;
+//   scores, max, weighted exp, sum (index order, one wave reading 64 values per step
+//   into registers), probabilities;
 //   sort by (probability desc, index asc) with a bitonic network (the order is
 //   total, so the result equals a rank sort's);
 //   the shown cumsum of the sorted probabilities never decreases (terms >= 0,
 //   bf16 rounding monotone), so "remove rank r when r > 0 and the cumsum through
 //   r - 1 exceeds p" keeps exactly the ranks below cut = max(first such r,
-//   preserve): one thread walks the chain up to the crossing only.
+//   preserve): one wave walks the chain up to the crossing only, 64 values at a time.
+// Dynamic LDS: 2 x n2 floats/ints (n2 = kn rounded up to a power of two).
 __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __restrict__ qc,
                                                                const float* __restrict__ kc,
                                                                const int32_t* __restrict__ k_sizes,
@@ -92,14 +126,17 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
                                                                uint8_t* __restrict__ map,
                                                                int32_t* __restrict__ budgets) {
   __shared__ __attribute__((aligned(16))) float q_row[512];
-  __shared__ __attribute__((aligned(16))) float val[MAX_KC];
-  __shared__ float sorted_val[MAX_KC];
-  __shared__ int32_t sorted_idx[MAX_KC];
+  extern __shared__ __attribute__((aligned(16))) uint8_t sel_dyn[];
   __shared__ float scratch[SEL_THREADS / 64];
   __shared__ float denom_s;
   __shared__ int32_t cut_s;
   __shared__ unsigned long long budget_s;
 
+  const int n2 = pow2_at_least(kn);
+  float* sorted_val = reinterpret_cast<float*>(sel_dyn);         // [n2]: weighted exps, then probabilities
+  int32_t* sorted_idx = reinterpret_cast<int32_t*>(sorted_val + n2);  // [n2]
+  const int lane = threadIdx.x & 63;
+  const bool wave0 = threadIdx.x < 64;
   const int64_t row = blockIdx.x;  // bh * qn + q
   const int64_t bh = row / qn;
   const float* qrow = qc + row * d;
@@ -112,36 +149,30 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
   for (int j = threadIdx.x; j < kn; j += blockDim.x) {
     const float acc = row_dot(q_row, kb + static_cast<int64_t>(j) * d, d);
     const float sc = score_bf16 ? bf16r(bf16r(acc) / sqrt_d) : acc / sqrt_d;
-    val[j] = sc;
+    sorted_val[j] = sc;
     local_max = fmaxf(local_max, sc);
   }
   const float m = block_max(local_max, scratch);
 
   for (int j = threadIdx.x; j < kn; j += blockDim.x) {
     const float w = static_cast<float>(sz[j]);
-    val[j] = w * spr::canonical_expf(val[j] - m);
+    sorted_val[j] = w * spr::canonical_expf(sorted_val[j] - m);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (wave0) {  // sum in index order
     float sum = 0.0f;
-    int j = 0;
-    for (; j + 4 <= kn; j += 4) {
-      const spr::f32x4 v = *reinterpret_cast<const spr::f32x4*>(&val[j]);
-      sum = sum + v[0];
-      sum = sum + v[1];
-      sum = sum + v[2];
-      sum = sum + v[3];
+    for (int base = 0; base < kn; base += 64) {
+      const float x = base + lane < kn ? sorted_val[base + lane] : 0.0f;
+      const int n = min(64, kn - base);
+      for (int u = 0; u < n; ++u) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), u));
     }
-    for (; j < kn; ++j) sum = sum + val[j];
-    denom_s = sum > 1e-12f ? sum : 1e-12f;
+    if (lane == 0) denom_s = sum > 1e-12f ? sum : 1e-12f;
   }
   __syncthreads();
   const float denom = denom_s;
-  int n2 = 1;
-  while (n2 < kn) n2 <<= 1;
   for (int j = threadIdx.x; j < n2; j += blockDim.x) {
     if (j < kn) {
-      const float prob = val[j] / denom;
+      const float prob = sorted_val[j] / denom;
       sorted_val[j] = score_bf16 ? bf16r(prob) : prob;
     } else {
       sorted_val[j] = -__builtin_huge_valf();  // padding sorts last
@@ -149,44 +180,32 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
     sorted_idx[j] = j;
   }
   __syncthreads();
+  bitonic_rank_sort(sorted_val, sorted_idx, n2);
 
-  // bitonic sort: ranks_before(a, b) first
-  for (int size = 2; size <= n2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < n2; i += blockDim.x) {
-        const int l = i ^ stride;
-        if (l > i) {
-          const float vi = sorted_val[i], vl = sorted_val[l];
-          const int32_t ii = sorted_idx[i], il = sorted_idx[l];
-          const bool first = (i & size) == 0;  // this run ends up in ranks_before order
-          const bool swap = first ? ranks_before(vl, il, vi, ii) : ranks_before(vi, ii, vl, il);
-          if (swap) {
-            sorted_val[i] = vl;
-            sorted_val[l] = vi;
-            sorted_idx[i] = il;
-            sorted_idx[l] = ii;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-
-  if (threadIdx.x == 0) {
+  if (wave0) {
     const float thr = score_bf16 ? bf16r(p) : p;
     float cum = 0.0f;
     float prev = 0.0f;  // shown cumsum through rank r - 1
     int cut = kn;
-    for (int r = 0; r < kn; ++r) {
-      if (r > 0 && prev > thr) {
-        cut = r > preserve ? r : preserve;
-        break;
+    bool done = false;
+    for (int base = 0; base < kn && !done; base += 64) {
+      const float x = base + lane < kn ? sorted_val[base + lane] : 0.0f;
+      const int n = min(64, kn - base);
+      for (int u = 0; u < n; ++u) {
+        const int r = base + u;
+        if (r > 0 && prev > thr) {
+          cut = r > preserve ? r : preserve;
+          done = true;
+          break;
+        }
+        cum = cum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), u));
+        prev = score_bf16 ? bf16r(cum) : cum;
       }
-      cum = cum + sorted_val[r];
-      prev = score_bf16 ? bf16r(cum) : cum;
     }
-    cut_s = cut < kn ? cut : kn;
-    budget_s = 0;
+    if (lane == 0) {
+      cut_s = cut < kn ? cut : kn;
+      budget_s = 0;
+    }
   }
   __syncthreads();
   const int cut = cut_s;
@@ -207,64 +226,101 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
 
 // One workgroup per (bh, q) row of scores [bh, qn, kn].
 // mode 0: n8_ops.cu semantics, mode 1: selector_budget.py / CPU-fallback semantics.
+// Both walk the clusters in (score desc, index asc) order, skip empty ones, and keep a
+// cluster while the running cost of the non-empty clusters so far stays within the
+// budget; the running cost only grows, so that is the set {non-empty r : cum_r <= budget}
+// with cum the inclusive prefix sum of the non-empty costs in sorted order.  They differ
+// in the one extra cluster taken when the budget is not met: mode 0 the first non-empty
+// cluster past it (the crossing), mode 1 the cluster at sorted position `count`.
+// Dynamic LDS: n2 floats + n2 ints + kn bytes (n2 = kn rounded up to a power of two).
 __global__ __launch_bounds__(SEL_THREADS) void select_budget_kernel(
     const float* __restrict__ scores, const int32_t* __restrict__ sizes, const int32_t* __restrict__ budgets,
     int32_t qn, int32_t kn, int32_t mode, uint8_t* __restrict__ out, int32_t* __restrict__ ids,
     int32_t* __restrict__ counts) {
-  __shared__ float val[MAX_KC];
-  __shared__ int32_t order[MAX_KC];
-  __shared__ uint8_t keep[MAX_KC];
+  extern __shared__ __attribute__((aligned(16))) uint8_t sel_dyn[];
+  __shared__ long long wave_tot[SEL_THREADS / 64];
+  __shared__ long long red_sel[SEL_THREADS / 64];
+  __shared__ int32_t red_cnt[SEL_THREADS / 64], red_valid[SEL_THREADS / 64], red_cross[SEL_THREADS / 64];
+  const int n2 = pow2_at_least(kn);
+  float* val = reinterpret_cast<float*>(sel_dyn);
+  int32_t* order = reinterpret_cast<int32_t*>(val + n2);
+  uint8_t* keep = reinterpret_cast<uint8_t*>(order + n2);
   const int64_t row = blockIdx.x;
   const int64_t bh = row / qn;
   const int32_t q = static_cast<int32_t>(row - bh * qn);
   const float* srow = scores + row * kn;
   const int32_t* sz = sizes + bh * kn;
-  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
-    val[j] = srow[j];
-    keep[j] = 0;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int32_t budget = budgets[row];
+  for (int j = t; j < n2; j += blockDim.x) {
+    val[j] = j < kn ? srow[j] : -__builtin_huge_valf();  // padding sorts last
+    order[j] = j;
+    if (j < kn) keep[j] = 0;
   }
   __syncthreads();
-  for (int j = threadIdx.x; j < kn; j += blockDim.x) {
-    const float v = val[j];
-    int rank = 0;
-    for (int i = 0; i < kn; ++i) rank += ranks_before(val[i], i, v, j) ? 1 : 0;
-    order[rank] = j;
+  bitonic_rank_sort(val, order, n2);
+  // inclusive prefix sum of the non-empty costs in sorted order: thread t owns ranks
+  // [t E, t E + E)
+  const int per = (n2 + SEL_THREADS - 1) / SEL_THREADS;
+  const int r0 = t * per;
+  long long local = 0;
+  for (int u = 0; u < per; ++u) {
+    const int r = r0 + u;
+    if (r < kn) local += max(sz[order[r]], 0);
   }
+  long long incl = local;  // wave inclusive scan of the thread totals
+  for (int o = 1; o < 64; o <<= 1) {
+    const long long up = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += up;
+  }
+  if (lane == 63) wave_tot[wv] = incl;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int32_t budget = budgets[row];
-    if (mode == 0) {
-      int64_t selected = 0;
-      int32_t crossing = -1;
-      for (int r = 0; r < kn; ++r) {
-        const int32_t c = order[r];
-        const int32_t cost = sz[c];
-        if (cost <= 0) continue;
-        if (crossing < 0 && selected + cost <= budget) {
-          keep[c] = 1;
-          selected += cost;
-        } else if (crossing < 0) {
-          crossing = c;
-        }
-      }
-      if (budget > 0 && selected < budget && crossing >= 0) keep[crossing] = 1;
+  long long cum = incl - local;
+  for (int w = 0; w < wv; ++w) cum += wave_tot[w];
+  long long sel = 0;
+  int32_t cnt = 0, valid = 0, cross = 0x7FFFFFFF;
+  for (int u = 0; u < per; ++u) {
+    const int r = r0 + u;
+    if (r >= kn) break;
+    const int32_t c = order[r];
+    const int32_t cost = sz[c];
+    if (cost <= 0) continue;
+    cum += cost;
+    ++valid;
+    if (cum <= budget) {
+      keep[c] = 1;
+      sel += cost;
+      ++cnt;
     } else {
-      int64_t cum = 0, selected = 0;
-      int32_t count = 0, valid = 0;
-      for (int r = 0; r < kn; ++r) {
-        const int32_t c = order[r];
-        const int32_t cost = sz[c];
-        if (cost > 0) {
-          ++valid;
-          cum += cost;
-          if (cum <= budget) {
-            keep[c] = 1;
-            selected += cost;
-            ++count;
-          }
-        }
-      }
-      if (budget > 0 && selected < budget && count < valid && count < kn) keep[order[count]] = 1;
+      cross = min(cross, r);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    sel += __shfl_xor(sel, o, 64);
+    cnt += __shfl_xor(cnt, o, 64);
+    valid += __shfl_xor(valid, o, 64);
+    cross = min(cross, __shfl_xor(cross, o, 64));
+  }
+  if (lane == 0) {
+    red_sel[wv] = sel;
+    red_cnt[wv] = cnt;
+    red_valid[wv] = valid;
+    red_cross[wv] = cross;
+  }
+  __syncthreads();
+  if (t == 0) {
+    long long selected = 0;
+    int32_t count = 0, n_valid = 0, crossing = 0x7FFFFFFF;
+    for (int w = 0; w < SEL_THREADS / 64; ++w) {
+      selected += red_sel[w];
+      count += red_cnt[w];
+      n_valid += red_valid[w];
+      crossing = min(crossing, red_cross[w]);
+    }
+    if (mode == 0) {
+      if (budget > 0 && selected < budget && crossing != 0x7FFFFFFF) keep[order[crossing]] = 1;
+    } else {
+      if (budget > 0 && selected < budget && count < n_valid && count < kn) keep[order[count]] = 1;
     }
   }
   __syncthreads();
@@ -395,9 +451,11 @@ extern "C" int spr_topp_map(const float* qc, const float* kc, const int32_t* k_s
   SPR_REQUIRE(d >= 1 && d <= 512, "spr_topp_map: head dim %d outside [1, 512]", d);
   if (bh == 0 || qn == 0) return SPR_OK;
   SPR_REQUIRE(qc && kc && k_sizes && (map || budgets), "spr_topp_map: null pointer");
-  topp_map_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, 0, stream>>>(qc, kc, k_sizes, qn, kn, d,
-                                                                                     sqrt_d, p, preserve, score_bf16,
-                                                                                     map, budgets);
+  int n2 = 1;
+  while (n2 < kn) n2 <<= 1;
+  const size_t lds = static_cast<size_t>(n2) * 8;  // at most 32 KB (kn <= 4096)
+  topp_map_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, lds, stream>>>(
+      qc, kc, k_sizes, qn, kn, d, sqrt_d, p, preserve, score_bf16, map, budgets);
   SPR_LAUNCHED("topp_map_kernel");
   return SPR_OK;
 }
@@ -414,7 +472,10 @@ extern "C" int spr_select_budget(const float* scores, const int32_t* sizes, cons
   if (bh == 0) return SPR_OK;
   SPR_REQUIRE(scores && sizes && budgets && out, "spr_select_budget: null pointer");
   if (qn == 0) return SPR_OK;
-  select_budget_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, 0, stream>>>(
+  int n2 = 1;
+  while (n2 < kn) n2 <<= 1;
+  const size_t lds = static_cast<size_t>(n2) * 8 + ((static_cast<size_t>(kn) + 15) & ~size_t(15));  // <= 36 KB
+  select_budget_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, lds, stream>>>(
       scores, sizes, budgets, qn, kn, mode, out, ids, counts);
   SPR_LAUNCHED("select_budget_kernel");
   return SPR_OK;
