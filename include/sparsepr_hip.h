@@ -167,6 +167,15 @@ size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn, int32_t k
 int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_kv,
                                     int64_t s, int32_t qn, int32_t kn, void* plan, size_t plan_bytes,
                                     hipStream_t stream);
+/* n8_ops.cu:573-638 svg_ear_select_budget_schedule / compact_selected_clusters as the
+ * attention's work list: the same plan built from a selector schedule instead of the map.
+ * ids int32 [bh_kv, qn, kn]: row r's first counts[r] entries are its kept k-clusters in
+ * strictly ascending order (as spr_select_budget and spr_compact_selected write them);
+ * counts int32 [bh_kv, qn].  An entry outside [0, kn) or not above every earlier entry
+ * of its row is ignored, so the plan never lists a key range twice. */
+int spr_block_sparse_attention_plan_schedule(const int32_t* ids, const int32_t* counts, const int32_t* q_sizes,
+                                             const int32_t* k_sizes, int64_t bh_kv, int64_t s, int32_t qn,
+                                             int32_t kn, void* plan, size_t plan_bytes, hipStream_t stream);
 /* q bf16 [bh_q, s, d], k/v bf16 [bh_kv, s, d] in cluster-contiguous order; bh_q a
  * multiple of bh_kv (query head h uses kv head h / (bh_q / bh_kv)); d in {64, 128}.
  * out bf16 [bh_q, s, d]: softmax over the kept keys of the row's q-cluster (scale

@@ -54,6 +54,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     # attention.hip
     "spr_block_sparse_attention_workspace": (_sz, [_i64, _i32, _i32]),
     "spr_block_sparse_attention_plan": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _sz, _vp]),
+    "spr_block_sparse_attention_plan_schedule": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _sz,
+                                                                _vp]),
     "spr_block_sparse_attention_run": (ctypes.c_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i32, _i32, _i32,
                                                       _f32, _vp, _vp, _vp, _vp, _vp]),
     "spr_block_sparse_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,

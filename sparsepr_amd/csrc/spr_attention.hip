@@ -158,7 +158,15 @@ __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn
   return v;
 }
 
+// The kept k-clusters of a q-cluster row come from the map (map != nullptr) or from a
+// selector schedule: ids [bh, qn, kn] int32 with counts [bh, qn] (the ascending kept ids
+// svg_ear_select_budget_schedule / compact_selected_clusters emit, n8_ops.cu:573-638).  A
+// schedule entry outside [0, kn) or not above the entry before it is ignored, so every
+// key range enters a row's segment list at most once, in ascending order: the plan is
+// the same as from the equivalent map.
 __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __restrict__ map,
+                                                            const int32_t* __restrict__ ids,
+                                                            const int32_t* __restrict__ counts,
                                                             const int32_t* __restrict__ q_sizes,
                                                             const int32_t* __restrict__ k_sizes, int32_t qn,
                                                             int32_t kn, int32_t s_rows, int32_t* __restrict__ plan) {
@@ -219,18 +227,38 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   for (int i = blockIdx.y * (THREADS / 64) + wave; i < qn; i += gridDim.y * (THREADS / 64)) {
-    const uint8_t* mrow = map + (h * qn + i) * static_cast<int64_t>(kn);
+    const int64_t row = h * qn + i;
     Seg* out = pv.segs + static_cast<int64_t>(i) * kn;
     int32_t count = 0;
     int32_t total = 0;
-    for (int c0 = 0; c0 < kn; c0 += 64) {
-      const int c = c0 + lane;
+    // map: walk the kn flags; schedule: walk the row's min(count, kn) ids
+    const int32_t n_in = map != nullptr ? kn : min(max(counts[row], 0), kn);
+    int32_t last = -1;  // schedule: the last id taken so far
+    for (int c0 = 0; c0 < n_in; c0 += 64) {
+      int c;
+      bool listed;
+      if (map != nullptr) {
+        c = c0 + lane;
+        listed = c < kn && map[row * kn + c] != 0;
+      } else {
+        // taken iff in range and above every earlier id of the row (a max-scan)
+        c = c0 + lane < n_in ? ids[row * kn + c0 + lane] : -1;
+        int run = c;
+        for (int o = 1; o < 64; o <<= 1) {
+          const int up = __shfl_up(run, o, 64);
+          if (lane >= o) run = max(run, up);
+        }
+        int before = __shfl_up(run, 1, 64);
+        before = max(lane == 0 ? -1 : before, last);
+        listed = c0 + lane < n_in && c >= 0 && c < kn && c > before;
+        last = max(last, __shfl(run, 63, 64));
+      }
       int32_t len = 0, start = 0;
-      if (c < kn) {
+      if (listed) {
         start = k_off[c];
         len = k_off[c + 1] - start;
       }
-      const bool keep = c < kn && mrow[c] != 0 && len > 0;
+      const bool keep = listed && len > 0;
       const uint64_t bits = __ballot(keep);
       const int pos = __popcll(bits & ((1ull << lane) - 1ull));
       int32_t incl = keep ? len : 0;  // inclusive scan of kept lengths over the wave
@@ -1147,15 +1175,17 @@ extern "C" size_t spr_block_sparse_attention_workspace(int64_t bh_kv, int32_t qn
 
 // Plan for spr_block_sparse_attention_run: map uint8 [bh_kv, qn, kn], q_sizes
 // [bh_kv, qn], k_sizes [bh_kv, kn] int32 (sizes are clamped to the s rows).
-extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes,
-                                               int64_t bh_kv, int64_t s, int32_t qn, int32_t kn, void* plan,
-                                               size_t plan_bytes, hipStream_t stream) {
+static int block_sparse_plan(const uint8_t* map, const int32_t* ids, const int32_t* counts, const int32_t* q_sizes,
+                             const int32_t* k_sizes, int64_t bh_kv, int64_t s, int32_t qn, int32_t kn, void* plan,
+                             size_t plan_bytes, hipStream_t stream) {
   SPR_REQUIRE(bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_plan: bad size");
   SPR_REQUIRE(kn <= 16384, "spr_block_sparse_attention_plan: kn exceeds 16384");
   SPR_REQUIRE(qn <= TO_MAX_QN, "spr_block_sparse_attention_plan: qn exceeds %d", TO_MAX_QN);
   SPR_REQUIRE(s < (int64_t(1) << 31), "spr_block_sparse_attention_plan: sequence too long");
   SPR_REQUIRE(bh_kv <= 65535, "spr_block_sparse_attention_plan: bh_kv exceeds 65535");
-  SPR_REQUIRE(map && q_sizes && k_sizes && plan, "spr_block_sparse_attention_plan: null pointer");
+  SPR_REQUIRE((map != nullptr) != (ids != nullptr && counts != nullptr),
+              "spr_block_sparse_attention_plan: give a map or a schedule (ids and counts)");
+  SPR_REQUIRE(q_sizes && k_sizes && plan, "spr_block_sparse_attention_plan: null pointer");
   const size_t need = spr_block_sparse_attention_workspace(bh_kv, qn, kn);
   if (plan_bytes < need) {
     spr_set_error("spr_block_sparse_attention_plan: plan buffer %zu < %zu bytes", plan_bytes, need);
@@ -1177,7 +1207,7 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
     }
   }
   attn_plan_kernel<<<dim3(static_cast<uint32_t>(bh_kv), row_groups), THREADS, koff_bytes, stream>>>(
-      map, q_sizes, k_sizes, qn, kn, static_cast<int32_t>(s), static_cast<int32_t*>(plan));
+      map, ids, counts, q_sizes, k_sizes, qn, kn, static_cast<int32_t>(s), static_cast<int32_t*>(plan));
   SPR_LAUNCHED("attn_plan_kernel");
   attn_tile_order_kernel<<<dim3(static_cast<uint32_t>(bh_kv)), 256, 3 * qn * sizeof(int32_t), stream>>>(
       static_cast<int32_t*>(plan), qn, kn);
@@ -1188,6 +1218,23 @@ extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t
                                                 static_cast<int32_t>(s));
   SPR_LAUNCHED("attn_plan_header_kernel");
   return SPR_OK;
+}
+
+extern "C" int spr_block_sparse_attention_plan(const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes,
+                                               int64_t bh_kv, int64_t s, int32_t qn, int32_t kn, void* plan,
+                                               size_t plan_bytes, hipStream_t stream) {
+  SPR_REQUIRE(map != nullptr, "spr_block_sparse_attention_plan: null map");
+  return block_sparse_plan(map, nullptr, nullptr, q_sizes, k_sizes, bh_kv, s, qn, kn, plan, plan_bytes, stream);
+}
+
+// The plan from a selector schedule: ids int32 [bh_kv, qn, kn] (row r's first counts[r]
+// entries are its kept k-clusters, strictly ascending), counts int32 [bh_kv, qn].
+extern "C" int spr_block_sparse_attention_plan_schedule(const int32_t* ids, const int32_t* counts,
+                                                        const int32_t* q_sizes, const int32_t* k_sizes,
+                                                        int64_t bh_kv, int64_t s, int32_t qn, int32_t kn, void* plan,
+                                                        size_t plan_bytes, hipStream_t stream) {
+  SPR_REQUIRE(ids != nullptr && counts != nullptr, "spr_block_sparse_attention_plan_schedule: null schedule");
+  return block_sparse_plan(nullptr, ids, counts, q_sizes, k_sizes, bh_kv, s, qn, kn, plan, plan_bytes, stream);
 }
 
 // q [bh_q, s, d], k/v [bh_kv, s, d] bf16 (cluster-contiguous), plan from

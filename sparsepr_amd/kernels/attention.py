@@ -34,6 +34,30 @@ def plan_block_sparse(block_mask_map: torch.Tensor, block_row_sz: torch.Tensor, 
     return plan
 
 
+def plan_block_sparse_from_schedule(selected_ids: torch.Tensor, selected_counts: torch.Tensor,
+                                    block_row_sz: torch.Tensor, block_col_sz: torch.Tensor,
+                                    seq_len: int) -> torch.Tensor:
+    """The kept-segment plan from a selector schedule (svg_ear_select_budget_schedule /
+    compact_selected_clusters, n8_ops.cu:573-638): ids int32 [BHkv, Qc, Kc] whose first
+    counts[r] entries per row are the kept k-clusters, ascending; counts [BHkv, Qc].  The
+    plan equals plan_block_sparse of the equivalent map."""
+    dev = _lib.require_gpu(selected_ids, selected_counts, what="block-sparse plan from a schedule")
+    if selected_ids.ndim != 3:
+        raise RuntimeError(f"selected_ids must be [BHkv, Qc, Kc], got {tuple(selected_ids.shape)}")
+    bh_kv, qn, kn = selected_ids.shape
+    if tuple(selected_counts.shape) != (bh_kv, qn):
+        raise RuntimeError(f"selected_counts must be {(bh_kv, qn)}, got {tuple(selected_counts.shape)}")
+    ids = selected_ids.to(torch.int32).contiguous()
+    counts = selected_counts.to(torch.int32).contiguous()
+    qs = block_row_sz.to(device=dev, dtype=torch.int32).reshape(bh_kv, qn).contiguous()
+    ks = block_col_sz.to(device=dev, dtype=torch.int32).reshape(bh_kv, kn).contiguous()
+    nbytes = _lib.query("spr_block_sparse_attention_workspace", bh_kv, qn, kn)
+    plan = _lib.workspace(nbytes, dev)
+    _lib.call("spr_block_sparse_attention_plan_schedule", _lib.ptr(ids), _lib.ptr(counts), _lib.ptr(qs), _lib.ptr(ks),
+              bh_kv, seq_len, qn, kn, _lib.ptr(plan), plan.numel(), _lib.stream(dev))
+    return plan
+
+
 def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_mask_map: torch.Tensor,
                            block_row_sz: torch.Tensor, block_col_sz: torch.Tensor, *, return_lse: bool = False,
                            plan: torch.Tensor | None = None, scale: float | None = None,

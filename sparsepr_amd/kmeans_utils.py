@@ -155,14 +155,17 @@ def density_calculation(dynamic_map, q_cluster_sizes, k_cluster_sizes):
 
 def dynamic_block_sparse_fwd_flashinfer(q, k, v, block_mask_map, block_row_sz, block_col_sz, is_cpu=True,
                                         num_kv_heads=None, return_lse=False, plan_cache_key=None,
-                                        plan_cache_token=None):
+                                        plan_cache_token=None, selected_schedule=None):
     """Variable-block-sparse attention (kmeans_utils.py:2164-2350), HIP kernel.
 
     q [B, H_q, S, D], k/v [B, H_kv, S, D] bf16 in cluster order; block_mask_map
     [B, H_kv, Qc, Kc] bool; block_row_sz [B, H_kv, Qc], block_col_sz [B, H_kv, Kc].
     num_kv_heads enables GQA (query head h uses kv head h // (H_q / H_kv)).
     return_lse adds the natural-log LSE [B, H_q, S] (fp32).  plan_cache_key /
-    plan_cache_token reuse the kept-segment plan while the token is unchanged."""
+    plan_cache_token reuse the kept-segment plan while the token is unchanged.
+    selected_schedule = (ids [B, H_kv, Qc, Kc], counts [B, H_kv, Qc]), the selector's
+    ascending kept-cluster schedule (svg_ear_select_budget_schedule), builds the plan
+    from the schedule instead of scanning the map (the same plan when both agree)."""
     from .kernels.attention import block_sparse_attention, cached_plan
 
     B, H_q, S, D = q.shape
@@ -186,7 +189,15 @@ def dynamic_block_sparse_fwd_flashinfer(q, k, v, block_mask_map, block_row_sz, b
     rows = block_row_sz.reshape(B * H_kv, qc_num).to(dev)
     cols = block_col_sz.reshape(B * H_kv, kc_num).to(dev)
     plan = None
-    if plan_cache_key is not None:
+    if selected_schedule is not None:
+        if plan_cache_key is not None:
+            raise ValueError("selected_schedule and plan_cache_key are exclusive.")
+        from .kernels.attention import plan_block_sparse_from_schedule
+
+        ids, counts = selected_schedule
+        plan = plan_block_sparse_from_schedule(ids.reshape(B * H_kv, qc_num, kc_num),
+                                               counts.reshape(B * H_kv, qc_num), rows, cols, S)
+    elif plan_cache_key is not None:
         if plan_cache_token is None:
             raise ValueError("plan_cache_token is required when plan_cache_key is set.")
         plan = cached_plan(plan_cache_key, plan_cache_token, bmap, rows, cols, S)

@@ -263,3 +263,61 @@ def test_run_rejects_a_plan_for_other_sizes(dev, oracle):
                                             None, stream)
     torch.cuda.synchronize()
     assert st == 0 and not bool((out == 7.0).all(dim=-1).any())
+
+
+@pytest.mark.parametrize("kn", [40, 900])  # 900: the segment list stays in global memory
+def test_plan_from_schedule_matches_map(dev, oracle, kn):
+    """The selector schedule as the attention's work list: the plan from compacted ids and
+    counts gives bit-identical output to the plan from the map; a schedule with unsorted,
+    duplicate and out-of-range entries acts as the map of the entries above every earlier
+    entry of their row (checked against the float64 closed form too)."""
+    from sparsepr_amd.kernels.attention import (block_sparse_attention, plan_block_sparse,
+                                                plan_block_sparse_from_schedule)
+    from sparsepr_amd.kernels.n8_extension import compact_selected_clusters
+
+    rng = np.random.default_rng(kn)
+    B, H, S, D, qn = 1, 3, 4000, 128, 12
+    q, k, v, m, qs, ks = _problem(oracle, rng, B, H, H, S, D, qn, kn, density=0.25)
+    qt, kt, vt = (to_dev(t[0], dev, torch.bfloat16) for t in (q, k, v))
+    mt, qst, kst = to_dev(m[0], dev), to_dev(qs[0], dev), to_dev(ks[0], dev)
+    ids, counts = compact_selected_clusters(mt)
+    plan_m = plan_block_sparse(mt, qst, kst, S)
+    plan_s = plan_block_sparse_from_schedule(ids, counts, qst, kst, S)
+    o_m = block_sparse_attention(qt, kt, vt, mt, qst, kst, plan=plan_m)
+    o_s = block_sparse_attention(qt, kt, vt, mt, qst, kst, plan=plan_s)
+    assert torch.equal(o_m, o_s)
+    # through the selector and the drop-in attention call
+    from sparsepr_amd.kernels.n8_extension import svg_ear_select_budget_schedule
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
+
+    scores = torch.randn((H, qn, kn), device=dev)
+    budgets = torch.full((H, qn), S // 5, device=dev, dtype=torch.int32)
+    sel_mask, sel_ids, sel_counts = svg_ear_select_budget_schedule(scores, kst, budgets)
+    vmap = sel_mask[:, 1:, 1:].contiguous()
+    args = (qt[None], kt[None], vt[None], vmap[None], qst[None], kst[None])
+    assert torch.equal(dynamic_block_sparse_fwd_flashinfer(*args, is_cpu=False),
+                       dynamic_block_sparse_fwd_flashinfer(*args, is_cpu=False,
+                                                           selected_schedule=(sel_ids[None], sel_counts[None])))
+    # a malformed schedule: shuffled rows with duplicates, -1 and kn entries
+    ids_np = np.full((H, qn, kn), -7, np.int32)
+    cnt_np = np.zeros((H, qn), np.int32)
+    taken = np.zeros((H, qn, kn), bool)
+    for h in range(H):
+        for i in range(qn):
+            row = list(rng.choice(kn, size=rng.integers(0, min(kn, 30) + 1), replace=False))
+            row += [-1, kn] + (row[:3] if row else [])
+            rng.shuffle(row)
+            row = row[:kn]
+            ids_np[h, i, :len(row)] = row
+            cnt_np[h, i] = len(row) + (2 if i == 0 else 0)  # counts past the listed entries read the -7s
+            best = -1
+            for c in list(row) + ([-7, -7] if i == 0 else []):
+                if 0 <= c < kn and c > best:
+                    taken[h, i, c] = True
+                best = max(best, c)
+    plan_x = plan_block_sparse_from_schedule(to_dev(ids_np, dev), to_dev(cnt_np, dev), qst, kst, S)
+    o_x = block_sparse_attention(qt, kt, vt, to_dev(taken, dev), qst, kst, plan=plan_x)
+    o_t = block_sparse_attention(qt, kt, vt, to_dev(taken, dev), qst, kst)
+    assert torch.equal(o_x, o_t)
+    ref, _ = _reference(oracle, q, k, v, taken[None], qs, ks)
+    assert np.abs(o_x.float().cpu().numpy() - ref[0]).max() <= 2e-2
