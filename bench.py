@@ -55,13 +55,14 @@ def parse():
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["attention", "copy", "svg_ear", "role_proj", "n8_route"], default=None,
+    ap.add_argument("--only", choices=["attention", "copy", "svg_ear", "role_proj", "n8_route", "qkv"], default=None,
                     help="profiling aids: 'attention' routes once, then times only the block-sparse attention "
                          "kernel for --steps launches; 'copy' runs --steps plain 512 MiB device copies (the "
                          "calibration kernel for the HBM traffic counters); 'svg_ear' routes once, then times "
                          "the N8 value-error routing scores (N8's default selector) on the routed clusters; "
                          "'role_proj' times N8's Q role projection (rank 64) over the C4 Q; 'n8_route' times the "
-                         "HunyuanVideo adapter's N8 step (route, attention, repair) at the C4 shape")
+                         "HunyuanVideo adapter's N8 step (route, attention, repair) at the C4 shape; 'qkv' times "
+                         "the Wan and Cosmos2.5 QKV norm + RoPE fusions at the C3 / C5 shapes")
     return ap.parse_args()
 
 
@@ -427,6 +428,63 @@ def only_n8_route(args):
     }), flush=True)
 
 
+def only_qkv(args):
+    """The model-edge fusions at their models' shapes: Wan's Q/K RMSNorm + complex RoPE + BHLD
+    layout at the C3 shape (1 x 32,760 x 40 heads x 128) and Cosmos2.5's per-head RMSNorm +
+    rotate-half RoPE at the C5 shape (1 x 84,480 x 40 x 128), bf16.  One line per fusion,
+    HBM roofline over the algorithmic bytes (Q, K, V read and written once, plus the RoPE
+    table), timed with HIP events on the stream the kernel runs on."""
+    import torch
+
+    from sparsepr_amd.kernels.n8_extension import cosmos25_qkv_norm_rope_bshd, wan_qkv_norm_rope_layout
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    heads, d = 40, 128
+    c = heads * d
+    bf = torch.bfloat16
+    cases = []
+    tok = 32760
+    qkv = [torch.randn((1, tok, c), device=dev, generator=g).to(bf) for _ in range(3)]
+    w = [(1 + 0.1 * torch.randn(c, device=dev, generator=g)).to(bf) for _ in range(2)]
+    ang = torch.rand((tok, d // 2), device=dev, generator=g) * 6.0
+    fr, fi = torch.cos(ang).contiguous(), torch.sin(ang).contiguous()
+    cases.append(("wan_qkv_kernel (Wan QKV RMSNorm + RoPE + BHLD layout)",
+                  "C3 Wan2.2 shape: 1 x 32760 tokens x 40 heads x 128 bf16",
+                  lambda: wan_qkv_norm_rope_layout(*qkv, *w, fr, fi, heads=heads, epsilon=1e-6),
+                  6 * tok * c * 2 + tok * d * 4 + 2 * c * 2))
+    tok2 = 84480
+    qkv2 = [torch.randn((1, tok2, c), device=dev, generator=g).to(bf) for _ in range(3)]
+    w2 = [1 + 0.1 * torch.randn(d, device=dev, generator=g) for _ in range(2)]
+    ang2 = (torch.rand((tok2, 1, 1, d), device=dev, generator=g) * 40.0).contiguous()
+    cases.append(("cosmos_qkv_kernel<bf16, 128> (Cosmos2.5 QKV RMSNorm + rotate-half RoPE)",
+                  "C5 Cosmos-Predict2.5 shape: 1 x 84480 tokens x 40 heads x 128 bf16",
+                  lambda: cosmos25_qkv_norm_rope_bshd(*qkv2, *w2, ang2, heads=heads, epsilon=1e-6),
+                  6 * tok2 * c * 2 + tok2 * d * 4 + 2 * d * 4))
+    for kernel, workload, run, nbytes in cases:
+        for _ in range(max(args.warmup, 1)):
+            run()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            run()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / args.steps
+        gbs = nbytes / ms / 1e6
+        print(json.dumps({
+            "metric": "QKV norm + RoPE fusion ms per call + % HBM roofline", "value": round(ms, 4), "unit": "ms/call",
+            "n_gpus": 1, "steps": args.steps, "warmup": max(args.warmup, 1), "ms_per_step": round(ms, 4),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (Gaussian Q/K/V, seeded, on device)", "config": {"workload": workload},
+            "roofline": {"kernel": kernel, "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "algorithmic_bytes": nbytes, "kernel_ms": round(ms, 4)},
+        }), flush=True)
+
+
 def _layer_configs():
     from sparsepr_amd import synthetic
     from sparsepr_amd.layer import SparsePRConfig
@@ -635,6 +693,8 @@ def main():
         return only_role_proj(args)
     if args.only == "n8_route":
         return only_n8_route(args)
+    if args.only == "qkv":
+        return only_qkv(args)
     import torch
 
     torch.cuda.set_device(0)

@@ -248,6 +248,25 @@ int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense,
 int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
                      const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
                      float alpha, float norm_cap, void* out, hipStream_t stream);
+/* ---- model-edge fusions (spr_qkv.hip) */
+/* n8_ops.cu:16-105 wan_qkv_norm_rope_layout_kernel (host :356-413): q, k, v [batch, tokens,
+ * channels = heads * head_dim] of dtype (0 bf16, 1 fp16, 2 fp32); RMSNorm over all channels of
+ * a token with weights [channels] of the same dtype, rounded to the dtype, then complex-pair
+ * RoPE by freq_real / freq_imag fp32 [tokens, head_dim / 2]; outputs [batch, heads, tokens,
+ * head_dim] (V relaid out).  head_dim even; 16-byte aligned device pointers. */
+int spr_wan_qkv_norm_rope_layout(const void* q, const void* k, const void* v, const void* q_weight,
+                                 const void* k_weight, const float* freq_real, const float* freq_imag, int32_t dtype,
+                                 int64_t batch, int64_t tokens, int32_t channels, int32_t heads, float epsilon,
+                                 void* q_out, void* k_out, void* v_out, hipStream_t stream);
+/* n8_ops.cu:107-187 cosmos25_qkv_norm_rope_bshd_kernel (host :415-497): q, k, v [batch, tokens,
+ * heads * head_dim] of dtype; RMSNorm over each head's head_dim values with fp32 weights
+ * [head_dim], rounded to the dtype, then rotate-half RoPE by fp32 angles [tokens, head_dim]
+ * (sincosf); outputs [batch, tokens, heads, head_dim].  head_dim even, epsilon > 0. */
+int spr_cosmos25_qkv_norm_rope_bshd(const void* q, const void* k, const void* v, const float* q_weight,
+                                    const float* k_weight, const float* rope_angles, int32_t dtype, int64_t batch,
+                                    int64_t tokens, int32_t heads, int32_t head_dim, float epsilon, void* q_out,
+                                    void* k_out, void* v_out, hipStream_t stream);
+
 /* residual_repair.py:263-465 fit_reduced_rank_residual / _fit_reduced_rank_residual_fp32 for
  * every configuration it accepts with m, p, d <= 128 and rank <= 16:
  *   weighted standardisation (:364-384; weights == NULL: plain mean and unbiased std);

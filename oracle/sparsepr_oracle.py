@@ -930,6 +930,72 @@ def attention_mass_scores(qc, k_sorted, sizes, group):
 
 
 # ----------------------------------------------------------------------------
+# model-edge fusions: Q/K RMSNorm + RoPE + layout (n8_ops.cu:16-187)
+# ----------------------------------------------------------------------------
+
+def round_to(x, dtype):
+    """Round float64 values to the model dtype ('bf16', 'fp16', 'fp32'; 'fp64' keeps
+    them), returned as float64."""
+    x = np.asarray(x, np.float64)
+    if dtype == "bf16":
+        return to_bf16(x.astype(np.float32)).astype(np.float64)
+    if dtype == "fp16":
+        return x.astype(np.float16).astype(np.float64)
+    if dtype == "fp32":
+        return x.astype(np.float32).astype(np.float64)
+    return x
+
+
+def _rms_normalize(x, w, eps, dtype):
+    """x / sqrt(mean(x^2) + eps) * w over the last axis, rounded to the model dtype
+    (the rounding boundary the reference keeps before RoPE, n8_ops.cu:78-90,158-170)."""
+    x = np.asarray(x, np.float64)
+    inv = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return round_to(x * inv * np.asarray(w, np.float64), dtype)
+
+
+def wan_qkv_norm_rope_layout(q, k, v, q_weight, k_weight, freq_real, freq_imag, heads, eps, dtype="bf16"):
+    """wan_qkv_norm_rope_layout_kernel (n8_ops.cu:16-105): q, k, v [B, L, C]; RMSNorm over
+    the C channels of a token, rounded; channels (2i, 2i + 1) of each head rotated as
+    (x0 fr - x1 fi, x0 fi + x1 fr) with freq_real / freq_imag [L, D / 2]; outputs
+    [B, H, L, D].  float64 arithmetic, rounded to dtype at the norm and at the output."""
+    b, l, c = q.shape
+    d = c // heads
+    fr = np.asarray(freq_real, np.float64)[None, :, None, :]
+    fi = np.asarray(freq_imag, np.float64)[None, :, None, :]
+
+    def rope(x):
+        x = x.reshape(b, l, heads, d // 2, 2)
+        x0, x1 = x[..., 0], x[..., 1]
+        out = np.stack((x0 * fr - x1 * fi, x0 * fi + x1 * fr), axis=-1).reshape(b, l, heads, d)
+        return round_to(out, dtype).transpose(0, 2, 1, 3)
+
+    qo = rope(_rms_normalize(q, q_weight, eps, dtype))
+    ko = rope(_rms_normalize(k, k_weight, eps, dtype))
+    vo = np.asarray(v, np.float64).reshape(b, l, heads, d).transpose(0, 2, 1, 3)
+    return qo, ko, vo
+
+
+def cosmos25_qkv_norm_rope_bshd(q, k, v, q_weight, k_weight, rope_angles, heads, eps, dtype="bf16"):
+    """cosmos25_qkv_norm_rope_bshd_kernel (n8_ops.cu:107-187): q, k, v [B, S, H * D]; RMSNorm
+    over each head's D values with fp32 weights [D], rounded; out[d] = x[d] cos(a[s, d]) -
+    x[d + D/2] sin(a[s, d]) for d < D/2 and x[d] cos + x[d - D/2] sin above (the rotate-half
+    convention); outputs [B, S, H, D].  float64 arithmetic, rounded to dtype twice."""
+    b, s_len, c = q.shape
+    d = c // heads
+    half = d // 2
+    ang = np.asarray(rope_angles, np.float64).reshape(s_len, d)[None, :, None, :]
+    cos, sin = np.cos(ang), np.sin(ang)
+
+    def rope(x, w):
+        r = _rms_normalize(np.asarray(x, np.float64).reshape(b, s_len, heads, d), w, eps, dtype)
+        partner = np.concatenate((-r[..., half:], r[..., :half]), axis=-1)
+        return round_to(r * cos + partner * sin, dtype)
+
+    return rope(q, q_weight), rope(k, k_weight), np.asarray(v, np.float64).reshape(b, s_len, heads, d)
+
+
+# ----------------------------------------------------------------------------
 # the whole layer (SAP top-p route + block-sparse attention + N8 repair)
 # ----------------------------------------------------------------------------
 

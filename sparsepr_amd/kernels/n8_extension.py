@@ -3,8 +3,7 @@
 The reference loads a pybind module `n8_kernels` built from n8_ops.cu.  Here the
 same entry points are served by libsparsepr_hip.so through its C ABI.
 `load_n8_kernels()` returns a module-like object exposing the reference's export
-names (n8_ops.cu:642-664) so `hasattr` capability probes keep working; the
-model-specific QKV norm/RoPE fusions are not part of this library.
+names (n8_ops.cu:642-664) so `hasattr` capability probes keep working.
 """
 
 from __future__ import annotations
@@ -50,6 +49,88 @@ def _role_step(features: torch.Tensor, centroids: torch.Tensor, max_clusters: in
     return [labels, res.centroids, sizes]
 
 
+def _qkv_common(q, k, v, what):
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError(f"{what} QKV inputs must be CUDA tensors")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise RuntimeError(f"{what} QKV inputs must be contiguous")
+    if q.shape != k.shape or q.shape != v.shape or q.dim() != 3:
+        raise RuntimeError(f"{what} QKV inputs must have matching [B,{'L' if what == 'Wan' else 'S'},C] shapes")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise RuntimeError(f"{what} QKV dtypes must match")
+    if q.dtype not in _lib.DTYPE_CODE:
+        raise RuntimeError(f"{what} QKV dtype {q.dtype} is not bf16, fp16 or fp32")
+
+
+def wan_qkv_norm_rope_layout(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: torch.Tensor,
+                             k_weight: torch.Tensor, freq_real: torch.Tensor, freq_imag: torch.Tensor, *,
+                             heads: int, epsilon: float):
+    """Native-Wan Q/K RMSNorm over all C channels, complex-pair RoPE and the BHLD layout
+    (n8_ops.cu:16-105, host :356-413): q, k, v [B, L, C] -> three [B, H, L, D] tensors."""
+    _qkv_common(q, k, v, "Wan")
+    if not (q_weight.is_cuda and k_weight.is_cuda and q_weight.is_contiguous() and k_weight.is_contiguous()):
+        raise RuntimeError("Wan norm weights must be contiguous CUDA tensors")
+    if q_weight.dtype != q.dtype or k_weight.dtype != q.dtype:
+        raise RuntimeError("Wan norm weights must match the QKV dtype")
+    if not (freq_real.is_cuda and freq_imag.is_cuda and freq_real.dtype == torch.float32
+            and freq_imag.dtype == torch.float32 and freq_real.is_contiguous() and freq_imag.is_contiguous()):
+        raise RuntimeError("Wan RoPE frequency tensors must be contiguous CUDA FP32")
+    batch, tokens, channels = (int(x) for x in q.shape)
+    heads = int(heads)
+    if heads <= 0 or channels % heads != 0:
+        raise RuntimeError("Wan channels must divide num_heads")
+    head_dim = channels // heads
+    if head_dim % 2 != 0:
+        raise RuntimeError("Wan head_dim must be even")
+    if q_weight.numel() != channels or k_weight.numel() != channels:
+        raise RuntimeError("Wan norm weights must contain C elements")
+    if (freq_real.shape != freq_imag.shape or freq_real.dim() != 2 or freq_real.shape[0] != tokens
+            or freq_real.shape[1] != head_dim // 2):
+        raise RuntimeError("Wan RoPE frequencies must have shape [L,D/2]")
+    dev = _lib.require_gpu(q, k, v, q_weight, k_weight, freq_real, freq_imag, what="Wan QKV")
+    out = [torch.empty((batch, heads, tokens, head_dim), dtype=q.dtype, device=dev) for _ in range(3)]
+    _lib.call("spr_wan_qkv_norm_rope_layout", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(q_weight),
+              _lib.ptr(k_weight), _lib.ptr(freq_real), _lib.ptr(freq_imag), _lib.DTYPE_CODE[q.dtype], batch, tokens,
+              channels, heads, float(epsilon), *[_lib.ptr(t) for t in out], _lib.stream(dev))
+    return tuple(out)
+
+
+def cosmos25_qkv_norm_rope_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_weight: torch.Tensor,
+                                k_weight: torch.Tensor, rope_angles: torch.Tensor, *, heads: int, epsilon: float):
+    """Cosmos2.5 per-head Q/K RMSNorm (fp32 weights) and Transformer-Engine rotate-half RoPE
+    (n8_ops.cu:107-187, host :415-497): q, k, v [B, S, H*D] -> three [B, S, H, D] tensors."""
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    _qkv_common(q, k, v, "Cosmos2.5")
+    q_weight = q_weight.float().contiguous()
+    k_weight = k_weight.float().contiguous()
+    rope_angles = rope_angles.float().contiguous()
+    if not (q_weight.is_cuda and k_weight.is_cuda):
+        raise RuntimeError("Cosmos2.5 norm weights must be contiguous CUDA FP32 tensors")
+    if not rope_angles.is_cuda:
+        raise RuntimeError("Cosmos2.5 RoPE angles must be contiguous CUDA FP32")
+    if len({t.device for t in (q, k, v, q_weight, k_weight, rope_angles)}) != 1:
+        raise RuntimeError("Cosmos2.5 QKV, weights, and RoPE angles must share one CUDA device")
+    batch, tokens, channels = (int(x) for x in q.shape)
+    heads = int(heads)
+    if heads <= 0 or channels % heads != 0:
+        raise RuntimeError("Cosmos2.5 channels must divide num_heads")
+    head_dim = channels // heads
+    if head_dim <= 0 or head_dim % 2 != 0:
+        raise RuntimeError("Cosmos2.5 head_dim must be positive and even")
+    if q_weight.numel() != head_dim or k_weight.numel() != head_dim:
+        raise RuntimeError("Cosmos2.5 norm weights must contain head_dim elements")
+    if tuple(rope_angles.shape) != (tokens, 1, 1, head_dim):
+        raise RuntimeError("Cosmos2.5 RoPE angles must have shape [S,1,1,D]")
+    if not epsilon > 0.0:
+        raise RuntimeError("Cosmos2.5 RMSNorm epsilon must be positive")
+    dev = q.device
+    out = [torch.empty((batch, tokens, heads, head_dim), dtype=q.dtype, device=dev) for _ in range(3)]
+    _lib.call("spr_cosmos25_qkv_norm_rope_bshd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(q_weight),
+              _lib.ptr(k_weight), _lib.ptr(rope_angles), _lib.DTYPE_CODE[q.dtype], batch, tokens, heads, head_dim,
+              float(epsilon), *[_lib.ptr(t) for t in out], _lib.stream(dev))
+    return tuple(out)
+
+
 def role_cluster_step_q64(features: torch.Tensor, centroids: torch.Tensor):
     """[labels int32, centroids fp32, sizes int32] for at most 512 clusters."""
     return tuple(_role_step(features, centroids, 512))
@@ -88,6 +169,10 @@ def compact_selected_clusters(selected_mask: torch.Tensor):
 
 def _exports() -> dict:
     return {
+        "wan_qkv_norm_rope_layout": lambda q, k, v, qw, kw, fr, fi, heads, eps: list(
+            wan_qkv_norm_rope_layout(q, k, v, qw, kw, fr, fi, heads=heads, epsilon=eps)),
+        "cosmos25_qkv_norm_rope_bshd": lambda q, k, v, qw, kw, ang, heads, eps: list(
+            cosmos25_qkv_norm_rope_bshd(q, k, v, qw, kw, ang, heads=heads, epsilon=eps)),
         "role_cluster_step_q64": lambda f, c: _role_step(f, c, 512),
         "role_cluster_step_k64": lambda f, c: _role_step(f, c, 1024),
         "svg_ear_select_budget": svg_ear_select_budget,

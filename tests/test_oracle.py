@@ -908,3 +908,70 @@ def test_project_rows_loop(oracle):
             assert abs(got[0, i, c] - want / 2.0) < 1e-12
     rms = oracle.project_rows(x, f, row_rms=True)
     assert np.allclose(np.sqrt((rms ** 2).mean(-1)), 1.0)
+
+
+# ---------------------------------------------------------------- QKV norm + RoPE fusions
+
+def test_wan_qkv_oracle_pins(oracle):
+    """Wan's RoPE as complex multiplication of adjacent channel pairs (an independent
+    numpy-complex formulation), the RMSNorm's unit RMS and scale invariance, the identity
+    at angle 0 and the exact quarter turn, and the BHLD layout of V."""
+    rng = np.random.default_rng(71)
+    b, l, h, d = 2, 7, 3, 8
+    c = h * d
+    q = rng.standard_normal((b, l, c)) * 3.0
+    k = rng.standard_normal((b, l, c))
+    v = rng.standard_normal((b, l, c))
+    w = rng.uniform(0.5, 1.5, c)
+    ang = rng.uniform(-3, 3, (l, d // 2))
+    qo, ko, vo = oracle.wan_qkv_norm_rope_layout(q, k, v, w, w, np.cos(ang), np.sin(ang), h, 1e-6, dtype="fp64")
+    rms = np.sqrt((q * q).mean(-1, keepdims=True) + 1e-6)
+    z = ((q / rms * w).reshape(b, l, h, d // 2, 2) @ np.array([1.0, 1j])) * np.exp(1j * ang)[None, :, None, :]
+    want = np.stack((z.real, z.imag), -1).reshape(b, l, h, d).transpose(0, 2, 1, 3)
+    assert np.allclose(qo, want, rtol=1e-12, atol=1e-12)
+    assert np.array_equal(vo, v.reshape(b, l, h, d).transpose(0, 2, 1, 3))
+    ones = np.ones(c)
+    q1, _, _ = oracle.wan_qkv_norm_rope_layout(q, k, v, ones, ones, np.ones((l, d // 2)), np.zeros((l, d // 2)),
+                                               h, 0.0, dtype="fp64")
+    assert np.allclose((q1 ** 2).transpose(0, 2, 1, 3).reshape(b, l, c).mean(-1), 1.0)  # unit RMS per token
+    q2, _, _ = oracle.wan_qkv_norm_rope_layout(5.0 * q, k, v, ones, ones, np.ones((l, d // 2)),
+                                               np.zeros((l, d // 2)), h, 0.0, dtype="fp64")
+    assert np.allclose(q1, q2)
+    # quarter turn: (x0, x1) -> (-x1, x0), exact in bf16
+    qb, _, _ = oracle.wan_qkv_norm_rope_layout(q, k, v, w, w, np.zeros((l, d // 2)), np.ones((l, d // 2)), h, 1e-6)
+    qn, _, _ = oracle.wan_qkv_norm_rope_layout(q, k, v, w, w, np.ones((l, d // 2)), np.zeros((l, d // 2)), h, 1e-6)
+    assert np.array_equal(qb[..., 0::2], -qn[..., 1::2]) and np.array_equal(qb[..., 1::2], qn[..., 0::2])
+
+
+def test_cosmos_qkv_oracle_pins(oracle):
+    """Cosmos's rotate-half RoPE equals complex multiplication of the pairs (d, d + D/2) when
+    the angle table repeats its halves (Transformer Engine's layout); a rotation keeps each
+    pair's norm and the inverse angle undoes it; per-head unit RMS; the quarter turn."""
+    rng = np.random.default_rng(72)
+    b, s_len, h, d = 2, 5, 3, 16
+    half = d // 2
+    q = rng.standard_normal((b, s_len, h * d)) * 2.0
+    k = rng.standard_normal((b, s_len, h * d))
+    v = rng.standard_normal((b, s_len, h * d))
+    w = rng.uniform(0.5, 1.5, d)
+    freqs = rng.uniform(-3, 3, (s_len, half))
+    ang = np.concatenate((freqs, freqs), -1).reshape(s_len, 1, 1, d)
+    qo, _, vo = oracle.cosmos25_qkv_norm_rope_bshd(q, k, v, w, w, ang, h, 1e-6, dtype="fp64")
+    x = q.reshape(b, s_len, h, d)
+    r = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * w
+    z = (r[..., :half] + 1j * r[..., half:]) * np.exp(1j * freqs)[None, :, None, :]
+    assert np.allclose(qo, np.concatenate((z.real, z.imag), -1), rtol=1e-12, atol=1e-12)
+    assert np.array_equal(vo, v.reshape(b, s_len, h, d))
+    assert np.allclose(np.hypot(qo[..., :half], qo[..., half:]), np.hypot(r[..., :half], r[..., half:]))
+    back, _, _ = oracle.cosmos25_qkv_norm_rope_bshd(qo.reshape(b, s_len, h * d), k, v, np.ones(d), np.ones(d),
+                                                    -ang, h, 0.0, dtype="fp64")
+    rn = r / np.sqrt((r * r).mean(-1, keepdims=True))
+    assert np.allclose(back, rn)
+    ones = np.ones(d)
+    q1, _, _ = oracle.cosmos25_qkv_norm_rope_bshd(q, k, v, ones, ones, np.zeros((s_len, 1, 1, d)), h, 0.0,
+                                                  dtype="fp64")
+    assert np.allclose((q1 ** 2).mean(-1), 1.0)
+    qt, _, _ = oracle.cosmos25_qkv_norm_rope_bshd(q, k, v, w, w, np.full((s_len, 1, 1, d), np.pi / 2), h, 1e-6)
+    qz, _, _ = oracle.cosmos25_qkv_norm_rope_bshd(q, k, v, w, w, np.zeros((s_len, 1, 1, d)), h, 1e-6)
+    # cos(pi/2) is 6e-17, below half an ulp of any of these values
+    assert np.array_equal(qt[..., :half], -qz[..., half:]) and np.array_equal(qt[..., half:], qz[..., :half])
