@@ -487,7 +487,9 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
       }
       const float lm = act ? lam[s] : 0.0f;
       for (int rho = 0; rho <= maxpos; ++rho) {
-        if (act && mypos == rho) {
+        const bool mine = act && mypos == rho;
+        float sc = 1.0f;
+        if (mine) {
           float cd = dget(0) - lm;
           float cs = n > 1 ? eget(0) : 0.0f;
           for (int j = 0; j + 1 < n; ++j) {
@@ -517,11 +519,13 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
             const uint32_t mix = (hsh ^ (hsh >> 15)) * 0x2C1B3C6Du;
             X[j * MAXR + s] = static_cast<float>((mix >> 8) & 0xFFFF) * (2.0f / 65535.0f) - 1.0f;
           }
-          // Three solves.  Between solves X is only rescaled (by 1 / max |x|, applied as
-          // the next forward pass loads it); cluster members are also orthogonalised
-          // against the members before them.  The norm is taken once, at the end.
-          float sc = 1.0f;
-          for (int it = 0; it < 3; ++it) {
+        }
+        // Three solves.  Between solves X is only rescaled (by 1 / max |x|, applied as the
+        // next forward pass loads it); cluster members are also normalised and
+        // orthogonalised against the members before them, by the whole wave, one member
+        // at a time.  The norm is taken once, at the end.
+        for (int it = 0; it < 3; ++it) {
+          if (mine) {
             // P, L: forward elimination of the right-hand side, 8 rows per batch of loads
             float cur = X[s] * sc;
             for (int j0 = 0; j0 + 1 < n; j0 += 8) {
@@ -571,20 +575,33 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
               }
             }
             sc = mx > 0.0f ? 1.0f / mx : 1.0f;
-            if (mypos > 0) {
-              for (int j = 0; j < n; ++j) X[j * MAXR + s] *= sc;
-              sc = 1.0f;
-              for (int o = s - mypos; o < s; ++o) {
-                float dt = 0.0f;
-                for (int j = 0; j < n; ++j) dt += X[j * MAXR + s] * X[j * MAXR + o];
-                for (int j = 0; j < n; ++j) X[j * MAXR + s] -= dt * X[j * MAXR + o];
-              }
-              float ss = 0.0f;
-              for (int j = 0; j < n; ++j) ss += X[j * MAXR + s] * X[j * MAXR + s];
-              const float nr = sqrtf(ss);
-              sc = nr > 0.0f ? 1.0f / nr : 0.0f;
-            }
           }
+          wave_sync();
+          uint64_t todo = __ballot(mine && mypos > 0);
+          while (todo != 0ull) {
+            const int ls = __builtin_ctzll(todo);
+            todo &= todo - 1ull;
+            const int sv = 16 * bt + ls;
+            const int mp = __builtin_amdgcn_readlane(mypos, ls);
+            const float scv = lane_read(sc, ls);
+            float x0 = lane < n ? X[lane * MAXR + sv] * scv : 0.0f;
+            float x1 = lane + 64 < n ? X[(lane + 64) * MAXR + sv] * scv : 0.0f;
+            for (int o = sv - mp; o < sv; ++o) {
+              const float p0 = lane < n ? X[lane * MAXR + o] : 0.0f;
+              const float p1 = lane + 64 < n ? X[(lane + 64) * MAXR + o] : 0.0f;
+              const float dt = wave_sum(x0 * p0 + x1 * p1);
+              x0 -= dt * p0;
+              x1 -= dt * p1;
+            }
+            const float nr = sqrtf(wave_sum(x0 * x0 + x1 * x1));
+            const float f = nr > 0.0f ? 1.0f / nr : 0.0f;
+            if (lane < n) X[lane * MAXR + sv] = x0 * f;
+            if (lane + 64 < n) X[(lane + 64) * MAXR + sv] = x1 * f;
+            if (lane == ls) sc = 1.0f;
+            wave_sync();
+          }
+        }
+        if (mine) {
           float ss = 0.0f;
 #pragma unroll 8
           for (int j = 0; j < n; ++j) {
