@@ -36,7 +36,7 @@
 //   rrr_fitted_kernel  (fitted basis) F into the workspace, then rrr_gram_kernel for B and
 //                      the eigen part of rrr_factor_kernel.
 //   rrr_solve_kernel   one workgroup per head: Z = y_w basis, then the substitutions
-//                      (one wave per basis column, refined twice against fp64 residuals)
+//                      (one wave per basis column, refined once against an fp64 residual)
 //                      and the x_w products of the form in use.
 #include "spr_common.h"
 
@@ -241,8 +241,9 @@ struct EigLayout {
   static constexpr int PART = PB + 2 * HV_STRIDE;     // [2][16] per-wave p . v
   static constexpr int LAM = PART + 32;               // [MAXR] eigenvalues, descending
   static constexpr int LU = LAM + MAXR;               // [5][128][16] LU of T - lambda_s I, 16 vectors at a time
-  static constexpr int X = LU + 5 * RRR_MAX * 16;     // [128][MAXR] eigenvectors of T
-  static constexpr int FLOATS = X + RRR_MAX * MAXR;
+  static constexpr int X = LU + 5 * RRR_MAX * 16;     // [128][XS] eigenvectors of T
+  static constexpr int XS = MAXR + 1;                 // X row stride: column reads hit distinct banks
+  static constexpr int FLOATS = X + RRR_MAX * XS;
   static constexpr int VB = LU;                       // [MAXR][128] eigenvectors of B (after inverse iteration)
   static constexpr int S = X;                         // [MAXR][MAXR] Gram, then R (after back-transformation)
   static constexpr int Q = HV;                        // [128][MAXR] orthonormal basis
@@ -453,7 +454,8 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
   // columns of the U / L arrays.  Members of a cluster (eigenvalue gaps below
   // 1e-3 ||T||) run in successive rounds and are orthogonalised against the members
   // before them (earlier batches are complete).
-  float* X = sm + L::X;  // [128][MAXR]
+  float* X = sm + L::X;  // [128][XS]
+  constexpr int XS = L::XS;
   if (wv == 0) {
     const float ortol = 1e-3f * tnorm;
     const float ptol = fmaxf(1.1920929e-7f * tnorm, 1e-30f);  // smallest pivot magnitude
@@ -517,7 +519,7 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
             const uint32_t hsh =
                 (static_cast<uint32_t>(j) * 2654435761u) ^ (static_cast<uint32_t>(s + 1) * 0x9E3779B9u);
             const uint32_t mix = (hsh ^ (hsh >> 15)) * 0x2C1B3C6Du;
-            X[j * MAXR + s] = static_cast<float>((mix >> 8) & 0xFFFF) * (2.0f / 65535.0f) - 1.0f;
+            X[j * XS + s] = static_cast<float>((mix >> 8) & 0xFFFF) * (2.0f / 65535.0f) - 1.0f;
           }
         }
         // Three solves.  Between solves X is only rescaled (by 1 / max |x|, applied as the
@@ -533,7 +535,7 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
 #pragma unroll
               for (int u = 0; u < 8; ++u) {
                 const int j = min(j0 + u, RRR_MAX - 2);
-                nx[u] = X[(j + 1) * MAXR + s];
+                nx[u] = X[(j + 1) * XS + s];
                 lv[u] = LM[j * 16 + sl];
                 pv[u] = PV[j * 16 + sl];
               }
@@ -543,21 +545,21 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
                 if (j + 1 < n) {
                   const bool sw = pv[u] != 0.0f;
                   const float xn = nx[u] * sc;
-                  X[j * MAXR + s] = sw ? xn : cur;
+                  X[j * XS + s] = sw ? xn : cur;
                   cur = sw ? cur - lv[u] * xn : xn - lv[u] * cur;
                 }
               }
             }
             // U: back substitution, tracking the largest magnitude
             float x1 = cur * RU0[(n - 1) * 16 + sl], x2 = 0.0f;
-            X[(n - 1) * MAXR + s] = x1;
+            X[(n - 1) * XS + s] = x1;
             float mx = fabsf(x1);
             for (int j0 = n - 2; j0 >= 0; j0 -= 8) {
               float xi[8], u1[8], u2[8], ru[8];
 #pragma unroll
               for (int u = 0; u < 8; ++u) {
                 const int j = max(j0 - u, 0);
-                xi[u] = X[j * MAXR + s];
+                xi[u] = X[j * XS + s];
                 u1[u] = U1[j * 16 + sl];
                 u2[u] = U2[j * 16 + sl];
                 ru[u] = RU0[j * 16 + sl];
@@ -567,7 +569,7 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
                 const int j = j0 - u;
                 if (j >= 0) {
                   const float xv = (xi[u] - u1[u] * x1 - u2[u] * x2) * ru[u];
-                  X[j * MAXR + s] = xv;
+                  X[j * XS + s] = xv;
                   mx = fmaxf(mx, fabsf(xv));
                   x2 = x1;
                   x1 = xv;
@@ -584,19 +586,19 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
             const int sv = 16 * bt + ls;
             const int mp = __builtin_amdgcn_readlane(mypos, ls);
             const float scv = lane_read(sc, ls);
-            float x0 = lane < n ? X[lane * MAXR + sv] * scv : 0.0f;
-            float x1 = lane + 64 < n ? X[(lane + 64) * MAXR + sv] * scv : 0.0f;
+            float x0 = lane < n ? X[lane * XS + sv] * scv : 0.0f;
+            float x1 = lane + 64 < n ? X[(lane + 64) * XS + sv] * scv : 0.0f;
             for (int o = sv - mp; o < sv; ++o) {
-              const float p0 = lane < n ? X[lane * MAXR + o] : 0.0f;
-              const float p1 = lane + 64 < n ? X[(lane + 64) * MAXR + o] : 0.0f;
+              const float p0 = lane < n ? X[lane * XS + o] : 0.0f;
+              const float p1 = lane + 64 < n ? X[(lane + 64) * XS + o] : 0.0f;
               const float dt = wave_sum(x0 * p0 + x1 * p1);
               x0 -= dt * p0;
               x1 -= dt * p1;
             }
             const float nr = sqrtf(wave_sum(x0 * x0 + x1 * x1));
             const float f = nr > 0.0f ? 1.0f / nr : 0.0f;
-            if (lane < n) X[lane * MAXR + sv] = x0 * f;
-            if (lane + 64 < n) X[(lane + 64) * MAXR + sv] = x1 * f;
+            if (lane < n) X[lane * XS + sv] = x0 * f;
+            if (lane + 64 < n) X[(lane + 64) * XS + sv] = x1 * f;
             if (lane == ls) sc = 1.0f;
             wave_sync();
           }
@@ -605,13 +607,13 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
           float ss = 0.0f;
 #pragma unroll 8
           for (int j = 0; j < n; ++j) {
-            const float xv = X[j * MAXR + s] * sc;
+            const float xv = X[j * XS + s] * sc;
             ss += xv * xv;
           }
           const float nr = sqrtf(ss);
           const float f = nr > 0.0f ? sc / nr : 0.0f;
 #pragma unroll 8
-          for (int j = 0; j < n; ++j) X[j * MAXR + s] *= f;
+          for (int j = 0; j < n; ++j) X[j * XS + s] *= f;
         }
         wave_sync();
       }
@@ -627,8 +629,8 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int sv = base + 4 * wv + u;
-        y0[u] = (sv < rank && lane < n) ? X[lane * MAXR + sv] : 0.0f;
-        y1[u] = (sv < rank && lane + 64 < n) ? X[(lane + 64) * MAXR + sv] : 0.0f;
+        y0[u] = (sv < rank && lane < n) ? X[lane * XS + sv] : 0.0f;
+        y1[u] = (sv < rank && lane + 64 < n) ? X[(lane + 64) * XS + sv] : 0.0f;
       }
       const int pl0 = hv_perm(lane), pl1 = hv_perm(lane + 64);
       int k = n - 3;
@@ -892,17 +894,17 @@ __device__ __forceinline__ void ridge_apply_f64(const float* xt, bool dual, int 
 }
 
 // Solve G u = b (b held as in chol_solve_wave, entries at or beyond ng zero) with the fp32
-// Cholesky factor and two steps of iterative refinement whose residuals b - G u are
+// Cholesky factor and one step of iterative refinement whose residual b - G u is
 // accumulated in fp64 from x_w.  The condition number of G is about the largest eigenvalue
 // of the weighted gram over the ridge (1e5 and more for token-count weights), so the plain
-// fp32 solve keeps only a few digits; each refinement step multiplies its error by about
+// fp32 solve keeps only a few digits; the refinement step multiplies its error by about
 // cond * 2^-24.
 __device__ __forceinline__ void ridge_solve_refined(const float* ls, const float* xt, bool dual, int m, int p,
                                                     float ridge, int lane, float& b0, float& b1) {
   const int ng = dual ? m : p;
   const float r0 = b0, r1 = b1;
   chol_solve_wave(ls, ng, lane, b0, b1);
-  for (int it = 0; it < 2; ++it) {
+  {
     double g0, g1;
     ridge_apply_f64(xt, dual, m, p, ridge, lane, b0, b1, g0, g1);
     float d0 = lane < ng ? static_cast<float>(static_cast<double>(r0) - g0) : 0.0f;
