@@ -9,8 +9,9 @@
 //   n8_exact_probe_scatter_triton          (kernels/triton/residual_repair.py:656-700, kernel :257-282)
 //
 // Probe selection runs in two launches.  (1) distance: each token's squared
-// distance to its cluster center, summed over dims in index order with separate
-// fp32 multiply and add (a fixed order, so exact ties are reproducible).
+// distance to its cluster center in fp32 with separate multiply and add, summed
+// sequentially within each group of 8 consecutive dims and then by a balanced
+// pairwise tree over the groups (a fixed order, so exact ties are reproducible).
 // (2) select, one workgroup per head: groups ordered by size (descending,
 // stable); in round r every group offers its r-th nearest token (ties by lower
 // token id) via an LDS atomicMin over 64-bit (distance bits, token) keys.

@@ -11,9 +11,8 @@ Composition (reference call sites):
             (probes are role-equal representatives of the Q clusters; with the
             top-p route the role features are the queries themselves)
 
-Every stage is a HIP kernel of libsparsepr_hip.so; the only non-HIP compute is
-the small fp32 RRR fit (torch.linalg on the GPU).  Nothing here synchronises
-the host.
+Every stage is a HIP kernel of libsparsepr_hip.so, the reduced-rank fit
+included.  Nothing here synchronises the host.
 """
 
 from __future__ import annotations
