@@ -627,7 +627,7 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
   constexpr int VPR = D / E;         // vectors per row
   static_assert(D % E == 0 && VPR <= 256, "unsupported D");
   constexpr int R = 256 / VPR;       // row groups (threads past R * VPR idle)
-  constexpr int RPT = 16;            // rows per thread per pass
+  constexpr int RPT = 8;             // rows per thread per pass
   __shared__ double red[R][D + 1];
   __shared__ float sq[D], cv[D];
 
