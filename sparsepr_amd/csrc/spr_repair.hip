@@ -42,6 +42,50 @@ __device__ __forceinline__ float load_elem(const T* p, int64_t i) {
   }
 }
 
+// Eight consecutive feature values as fp32 (bf16: one 16-byte load; fp32: two).
+template <typename T>
+struct Feat8 {
+  u32x4 w[sizeof(T) == 2 ? 1 : 2];
+};
+
+template <typename T>
+__device__ __forceinline__ Feat8<T> load_feat8(const T* __restrict__ p) {
+  Feat8<T> r;
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  r.w[0] = q[0];
+  if constexpr (sizeof(T) == 4) r.w[1] = q[1];
+  return r;
+}
+
+// The sequential fp32 sum over the eight dims of (f - c)^2, each term rounded (sub,
+// mul, add; no contraction).
+template <typename T>
+__device__ __forceinline__ float part8(const Feat8<T>& x, spr::f32x4 c0, spr::f32x4 c1) {
+  const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+  float fv[8];
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t ws[4] = {x.w[0].x, x.w[0].y, x.w[0].z, x.w[0].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      fv[2 * e] = spr::bf16_lo(ws[e]);
+      fv[2 * e + 1] = spr::bf16_hi(ws[e]);
+    }
+  } else {
+    const uint32_t ws[8] = {x.w[0].x, x.w[0].y, x.w[0].z, x.w[0].w, x.w[1].x, x.w[1].y, x.w[1].z, x.w[1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) fv[e] = __uint_as_float(ws[e]);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // plain operators: the file-level contract(off) keeps mul and add apart
+    const float diff = fv[e] - cv[e];
+    const float sq = diff * diff;
+    acc = acc + sq;
+  }
+  return acc;
+}
+
 // dist[bh, t] = sum_d (f[t, d] - center[label[t], d])^2 in fp32, each term rounded
 // (sub, mul, add; no contraction): sequential within each group of 8 consecutive
 // dims, then a balanced pairwise tree over the groups in index order (the
@@ -52,54 +96,131 @@ __global__ __launch_bounds__(256) void probe_distance_kernel(const T* __restrict
                                                              const float* __restrict__ centers, int64_t n,
                                                              int32_t groups, float* __restrict__ dist) {
   // R / 8 lanes share a row (coalesced 16- or 32-byte loads); lane k sums dims
-  // 8k .. 8k + 7 sequentially (separate fp32 multiply and add), then a butterfly
-  // over the row's lanes adds the partials as a balanced pairwise tree in index
-  // order (x + y == y + x, so both lanes of every pair hold the same sum).  A
-  // workgroup covers 256 rows, 64 per wave.
+  // 8k .. 8k + 7 sequentially, then a butterfly over the row's lanes adds the
+  // partials as a balanced pairwise tree in index order (x + y == y + x, so both
+  // lanes of every pair hold the same sum).  A wave covers 64 rows in steps of
+  // 64 / L rows; it loads its 64 labels once (one per lane) and issues the feature
+  // and center loads of U steps before using any of them.  Rows past n load row
+  // n - 1 and store nothing; an out-of-range label loads center 0 and uses zeros.
   constexpr int L = R / 8;
-  constexpr int RPS = 64 / L;  // rows per wave step
+  constexpr int RPS = 64 / L;   // rows per wave step
+  constexpr int STEPS = 64 / RPS;
+  constexpr int U = STEPS < 8 ? STEPS : 8;
   const int64_t bh = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int k = lane % L;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x >> 6) * 64 + lane / L;
-#pragma unroll 4
-  for (int st = 0; st < 64 / RPS; ++st) {
-    const int64_t t = row0 + st * RPS;
-    float acc = 0.0f;
-    if (t < n) {
-      const int32_t lab = labels[bh * n + t];
-      const bool ok = lab >= 0 && lab < groups;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 + (threadIdx.x >> 6) * 64;
+  if (base >= n) return;
+  const int32_t my_lab = labels[bh * n + std::min<int64_t>(base + lane, n - 1)];
+  const spr::f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s0 = 0; s0 < STEPS; s0 += U) {
+    Feat8<T> fx[U];
+    spr::f32x4 c0[U], c1[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = std::min<int64_t>(base + (s0 + u) * RPS + lane / L, n - 1);
+      fx[u] = load_feat8(f + (bh * n + t) * R + 8 * k);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the feature loads ahead of the label wait
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int32_t lab = __shfl(my_lab, (s0 + u) * RPS + lane / L, 64);
+      ok[u] = lab >= 0 && lab < groups;
       const spr::f32x4* crow =
-          reinterpret_cast<const spr::f32x4*>(centers + (bh * groups + (ok ? lab : 0)) * R + 8 * k);
-      const spr::f32x4 c0 = ok ? crow[0] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      const spr::f32x4 c1 = ok ? crow[1] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
-      float fv[8];
-      if constexpr (sizeof(T) == 2) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(f + (bh * n + t) * R + 8 * k);
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+          reinterpret_cast<const spr::f32x4*>(centers + (bh * groups + (ok[u] ? lab : 0)) * R + 8 * k);
+      c0[u] = crow[0];
+      c1[u] = crow[1];
+    }
+    float acc[U];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          fv[2 * e] = spr::bf16_lo(ws[e]);
-          fv[2 * e + 1] = spr::bf16_hi(ws[e]);
-        }
-      } else {
-        const spr::f32x4* fr = reinterpret_cast<const spr::f32x4*>(f + (bh * n + t) * R + 8 * k);
-        const spr::f32x4 a = fr[0], b = fr[1];
-        fv[0] = a[0]; fv[1] = a[1]; fv[2] = a[2]; fv[3] = a[3];
-        fv[4] = b[0]; fv[5] = b[1]; fv[6] = b[2]; fv[7] = b[3];
-      }
+    for (int u = 0; u < U; ++u) acc[u] = part8(fx[u], ok[u] ? c0[u] : zero, ok[u] ? c1[u] : zero);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // plain operators: the file-level contract(off) keeps mul and add apart
-        const float diff = fv[e] - cv[e];
-        const float sq = diff * diff;
-        acc = acc + sq;
-      }
+    for (int o = 1; o < L; o <<= 1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc[u] = acc[u] + __shfl_xor(acc[u], o, 64);
     }
 #pragma unroll
-    for (int o = 1; o < L; o <<= 1) acc = acc + __shfl_xor(acc, o, 64);
-    if (t < n && k == 0) dist[bh * n + t] = acc;
+    for (int u = 0; u < U; ++u) {
+      const int64_t t = base + (s0 + u) * RPS + lane / L;
+      if (t < n && k == 0) dist[bh * n + t] = acc[u];
+    }
+  }
+}
+
+// The same distances with the head's centers staged in LDS (groups * R * 4 bytes, at
+// most PD_LDS_BYTES).  Read from memory, the centers cost the vector-memory path twice
+// the feature bytes; from LDS they cost nothing there.  A 512-thread workgroup stages
+// one head's centers once and then walks a slice of that head's rows in 64-row tiles,
+// one tile per wave at a time, with the next tile's labels loaded during the current
+// one.  Within a center row the 16-byte pieces are stored as [half][lane] (piece 2k + h
+// at h * L + k), so the R / 8 lanes of a row read consecutive pieces (no bank
+// conflicts).  Results are identical to probe_distance_kernel's (same arithmetic).
+constexpr int PD_LDS_BYTES = 65536;
+constexpr int PD_LDS_THREADS = 512;
+
+template <typename T, int R>
+// four waves per SIMD: two workgroups per CU (at most 128 VGPRs)
+__global__ __launch_bounds__(PD_LDS_THREADS) __attribute__((amdgpu_waves_per_eu(4))) void probe_distance_lds_kernel(
+    const T* __restrict__ f, const int32_t* __restrict__ labels, const float* __restrict__ centers, int64_t n,
+    int32_t groups, int64_t rows_per_block, float* __restrict__ dist) {
+  extern __shared__ __align__(16) spr::f32x4 pd_cs[];
+  constexpr int L = R / 8;
+  constexpr int RPS = 64 / L;
+  constexpr int STEPS = 64 / RPS;
+  constexpr int U = STEPS < 4 ? STEPS : 4;  // more would spill at 128 VGPRs
+  constexpr int WAVES = PD_LDS_THREADS / 64;
+  const int64_t bh = blockIdx.y;
+  {
+    const spr::f32x4* src = reinterpret_cast<const spr::f32x4*>(centers + bh * groups * R);
+    for (int i = threadIdx.x; i < groups * (R / 4); i += PD_LDS_THREADS) {
+      const int g = i / (R / 4), j = i % (R / 4);  // piece j = 2k + h of center g
+      pd_cs[g * (R / 4) + (j & 1) * L + (j >> 1)] = src[i];
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int k = lane % L;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_block;
+  const int64_t r1 = std::min<int64_t>(n, r0 + rows_per_block);
+  const int32_t* lab_h = labels + bh * n;
+  const spr::f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  int64_t base = r0 + (threadIdx.x >> 6) * 64;
+  int32_t my_lab = base < r1 ? lab_h[std::min<int64_t>(base + lane, r1 - 1)] : 0;
+  for (; base < r1; base += WAVES * 64) {
+    const int64_t next = base + WAVES * 64;
+#pragma unroll
+    for (int s0 = 0; s0 < STEPS; s0 += U) {
+      Feat8<T> fx[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t t = std::min<int64_t>(base + (s0 + u) * RPS + lane / L, r1 - 1);
+        fx[u] = load_feat8(f + (bh * n + t) * R + 8 * k);
+      }
+      int32_t next_lab = 0;
+      if (s0 + U >= STEPS && next < r1) next_lab = lab_h[std::min<int64_t>(next + lane, r1 - 1)];
+      __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the first use
+      float acc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int32_t lab = __shfl(my_lab, (s0 + u) * RPS + lane / L, 64);
+        const bool ok = lab >= 0 && lab < groups;
+        const spr::f32x4* crow = pd_cs + (ok ? lab : 0) * (R / 4) + k;
+        acc[u] = part8(fx[u], ok ? crow[0] : zero, ok ? crow[L] : zero);
+      }
+#pragma unroll
+      for (int o = 1; o < L; o <<= 1) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u] = acc[u] + __shfl_xor(acc[u], o, 64);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t t = base + (s0 + u) * RPS + lane / L;
+        if (t < r1 && k == 0) dist[bh * n + t] = acc[u];
+      }
+      if (s0 + U >= STEPS) my_lab = next_lab;
+    }
   }
 }
 
@@ -601,10 +722,22 @@ extern "C" int spr_probe_distances(const void* features, int32_t dtype, const in
   SPR_REQUIRE(bh <= 65535, "spr_probe_distances: bh exceeds 65535");
   if (bh == 0 || n == 0) return SPR_OK;
   SPR_REQUIRE(features && labels && centers && dist, "spr_probe_distances: null pointer");
-  dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
-#define SPR_PD(T, RR)                                                                                          \
-  probe_distance_kernel<T, RR><<<grid, 256, 0, stream>>>(static_cast<const T*>(features), labels, centers, n, \
-                                                          groups, dist)
+  const size_t lds = static_cast<size_t>(groups) * r * sizeof(float);
+  const bool staged = lds <= PD_LDS_BYTES;
+  // staged: one round of two workgroups per CU over the chip's 256 CUs, slices whole tiles
+  const int64_t slices = std::max<int64_t>(1, std::min<int64_t>(spr::ceil_div(n, 64 * 8), 512 / bh));
+  const int64_t per_slice = spr::ceil_div(spr::ceil_div(n, slices), 64) * 64;
+  const dim3 sgrid(static_cast<uint32_t>(spr::ceil_div(n, per_slice)), static_cast<uint32_t>(bh));
+  const dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
+#define SPR_PD(T, RR)                                                                                               \
+  do {                                                                                                               \
+    if (staged)                                                                                                      \
+      probe_distance_lds_kernel<T, RR><<<sgrid, PD_LDS_THREADS, lds, stream>>>(                                      \
+          static_cast<const T*>(features), labels, centers, n, groups, per_slice, dist);                             \
+    else                                                                                                             \
+      probe_distance_kernel<T, RR><<<grid, 256, 0, stream>>>(static_cast<const T*>(features), labels, centers, n,   \
+                                                              groups, dist);                                         \
+  } while (0)
   if (dtype == 0 && r == 128) SPR_PD(uint16_t, 128);
   else if (dtype == 0 && r == 64) SPR_PD(uint16_t, 64);
   else if (dtype == 2 && r == 128) SPR_PD(float, 128);

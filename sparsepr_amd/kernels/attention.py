@@ -134,7 +134,9 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale:
         raise RuntimeError("dense attention: out_dtype must be float32 or bfloat16")
     if nsplit is None:
         mtiles = max(1, (m + 127) // 128)
-        nsplit = max(1, min((1024 + bh_q * mtiles - 1) // (bh_q * mtiles), max(1, s_kv // 512)))
+        # at most 1024 workgroups (two per CU): one more than a multiple of the chip's
+        # slots leaves a nearly empty last round
+        nsplit = max(1, min(1024 // (bh_q * mtiles), s_kv // 512))
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
     out = torch.empty((bh_q, m, d), dtype=out_dtype, device=dev)
     lse = torch.empty((bh_q, m), dtype=torch.float32, device=dev) if return_lse else None

@@ -35,6 +35,29 @@ def test_vectorized_probes_bit_exact(dev, oracle, r):
         assert np.allclose(w.cpu().numpy(), rw, rtol=1e-6)
 
 
+@pytest.mark.parametrize("r,c,fp32", [(128, 40, False), (128, 128, False), (128, 300, False), (64, 256, False),
+                                       (64, 257, False), (128, 40, True)])
+def test_probe_distances_bit_exact(dev, oracle, r, c, fp32):
+    """Distances bit-exact against the oracle's canonical order, with the head's centers
+    staged in LDS (c * r * 4 <= 64 KB) and read from memory (larger), in bf16 and fp32
+    (bf16-valued) features, over a token count that is not a multiple of the slice."""
+    from sparsepr_amd import _lib
+    from sparsepr_amd.residual_repair import group_centers
+
+    rng = np.random.default_rng(r * 1000 + c)
+    bh, n = 3, 5001
+    f, labels = _probe_data(oracle, rng, bh=bh, n=n, r=r, c=c, empty=(3,))
+    dtype = torch.float32 if fp32 else torch.bfloat16
+    d_f, d_lab = to_dev(f, dev, dtype), to_dev(labels, dev)
+    centers, _ = group_centers(d_f, d_lab, c)
+    dist = torch.empty((bh, n), dtype=torch.float32, device=dev)
+    _lib.call("spr_probe_distances", _lib.ptr(d_f), _lib.DTYPE_CODE[dtype], _lib.ptr(d_lab),
+              _lib.ptr(centers.float().contiguous()), bh, n, c, r, _lib.ptr(dist), _lib.stream(dev))
+    _sizes, ref = oracle._probe_distances(f, labels, c)
+    got = dist.cpu().numpy()
+    assert np.array_equal(got, ref.astype(np.float32)), np.abs(got - ref).max()
+
+
 @pytest.mark.parametrize("mode", [0, 2])
 def test_probe_select_split_pass_matches_single(dev, oracle, mode):
     """Modes 0 and 2 with a workspace split the pass over the tokens across workgroups
