@@ -133,10 +133,11 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale:
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise RuntimeError("dense attention: out_dtype must be float32 or bfloat16")
     if nsplit is None:
+        # one round of workgroups, two per CU over the chip's 256 CUs (measured at the
+        # C4 shape: 21 splits 0.31 ms, 42 splits 0.32 ms, 43 splits 0.36 ms, since a
+        # workgroup past a whole round leaves a nearly empty last one)
         mtiles = max(1, (m + 127) // 128)
-        # at most 1024 workgroups (two per CU): one more than a multiple of the chip's
-        # slots leaves a nearly empty last round
-        nsplit = max(1, min(1024 // (bh_q * mtiles), s_kv // 512))
+        nsplit = max(1, min(512 // (bh_q * mtiles), s_kv // 512))
     qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
     out = torch.empty((bh_q, m, d), dtype=out_dtype, device=dev)
     lse = torch.empty((bh_q, m), dtype=torch.float32, device=dev) if return_lse else None

@@ -152,6 +152,28 @@ def test_dense_probe_attention(dev, oracle, M, S, D, nsplit):
     assert np.allclose(lse.cpu().numpy(), ref_lse, atol=2e-3)
 
 
+@pytest.mark.parametrize("M,S,nsplit", [(300, 3000, 4), (300, 10, 8)])
+def test_dense_probe_attention_gqa_tiles(dev, oracle, M, S, nsplit):
+    """D = 128 with query heads sharing key heads (6 on 2), more rows than one 256-row
+    tile, a key count that is not a multiple of the 64-key chunk, and (S = 10 over 8
+    splits) key splits with no keys at all."""
+    from sparsepr_amd.kernels.attention import dense_attention
+
+    rng = np.random.default_rng(M * S)
+    q = oracle.to_bf16(rng.standard_normal((6, M, 128)).astype(np.float32))
+    k = oracle.to_bf16(rng.standard_normal((2, S, 128)).astype(np.float32))
+    v = oracle.to_bf16(rng.standard_normal((2, S, 128)).astype(np.float32))
+    out, lse = dense_attention(to_dev(q, dev, torch.bfloat16), to_dev(k, dev, torch.bfloat16),
+                               to_dev(v, dev, torch.bfloat16), nsplit=nsplit, return_lse=True)
+    kk, vv = np.repeat(k, 3, 0), np.repeat(v, 3, 0)
+    ref = oracle.dense_attention(q, kk, vv)
+    got = out.cpu().numpy()
+    assert np.abs(got - ref).max() <= 5e-3 and _cos(got, ref) >= 0.9999
+    s = np.einsum("bmd,bsd->bms", q.astype(np.float64), kk.astype(np.float64)) / math.sqrt(128)
+    ref_lse = np.log(np.exp(s - s.max(-1, keepdims=True)).sum(-1)) + s.max(-1)
+    assert np.allclose(lse.cpu().numpy(), ref_lse, atol=2e-3)
+
+
 def test_block_sparse_full_size_sampled_rows(dev, oracle):
     """HunyuanVideo shape (24 heads x 118,800 x 128): a random map over 128 x 512
     cluster pairs; 192 sampled rows checked against float64 on the CPU."""
