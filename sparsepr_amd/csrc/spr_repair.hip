@@ -553,10 +553,16 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
   constexpr int RK = 16;
   constexpr int ROWB = D * 2;        // bytes per row
   constexpr int TILE = 32 * ROWB;    // one wave's batch
-  __shared__ u32x4 lfrag[8][2][RK][2];   // [k-step s][k-half h][rank] (hi, lo): L[16s + 8h + e][rank]
+  __shared__ u32x4 lfrag[8][2][32][2];   // [k-step s][k-half h][rank] (hi, lo): L[16s + 8h + e][rank], 0 past RK
   __shared__ u32x4 bfrag[4][32][2][2];   // [N-tile][row a][k-half h] (hi, lo): basis[32 nt + pi(a)][rho(h, m)]
-  __shared__ float mu[D], inv_sd[D], my[D];
+  __shared__ __attribute__((aligned(16))) float mu[D], inv_sd[D], my[D];
   __shared__ __attribute__((aligned(1024))) uint8_t rows_lds[8][2][TILE];  // [wave][buffer]
+  auto lds8 = [](const float* p, float (&x)[8]) {  // 8 consecutive floats, 32-byte aligned
+    const spr::f32x4 a = reinterpret_cast<const spr::f32x4*>(p)[0];
+    const spr::f32x4 b = reinterpret_cast<const spr::f32x4*>(p)[1];
+    x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+    x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+  };
   const int64_t bh = blockIdx.y;
   const float* lm = left + bh * D * RK;
   const float* bm = basis + bh * D * RK;
@@ -583,11 +589,11 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
   int64_t w0 = static_cast<int64_t>(blockIdx.x) * 256 + wave * 32;
   if (w0 < n) dma(w0, rows_lds[wave][0]);
 
-  for (int f = tid; f < 8 * 2 * RK; f += blockDim.x) {
-    const int st = f / (2 * RK), hh = (f / RK) % 2, rk = f % RK;
+  for (int f = tid; f < 8 * 2 * 32; f += blockDim.x) {
+    const int st = f / 64, hh = (f / 32) % 2, rk = f % 32;
     float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = lm[(16 * st + 8 * hh + e) * RK + rk];
+    for (int e = 0; e < 8; ++e) v[e] = rk < RK ? lm[(16 * st + 8 * hh + e) * RK + rk] : 0.0f;
     split_bf16x8(v, lfrag[st][hh][rk][0], lfrag[st][hh][rk][1]);
   }
   for (int f = tid; f < 4 * 32 * 2; f += blockDim.x) {
@@ -605,16 +611,25 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
   }
   __syncthreads();
 
-  const u32x4 zero = {0, 0, 0, 0};
-  for (int buf = 0; w0 < n; w0 += stride, buf ^= 1) {
+  // Batch it is DMA'd into buffer it % 2 one batch ahead.  Once its rows are in
+  // registers the buffer stages the batch's output: written in the input's swizzled
+  // layout, read back in row order, so each store instruction writes 1 KB of
+  // consecutive bytes (a store of 16-byte pieces from 32 rows at once runs about 20 %
+  // slower).  Vector-memory operations complete in issue order and every batch but a
+  // wave's last issues 8 DMAs and 8 stores, so batch it has landed once no more than
+  // [stores of it - 1] + [DMA of it + 1] are outstanding.
+  for (int it = 0; w0 < n; w0 += stride, ++it) {
+    const int buf = it & 1;
     const bool more = w0 + stride < n;
     if (more) dma(w0 + stride, rows_lds[wave][buf ^ 1]);
-    if (more) {
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");  // this batch landed; the next may not have
+    if (it >= 1 && more) {
+      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    } else if (it >= 1 || more) {
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    const uint8_t* tile = rows_lds[wave][buf];
+    uint8_t* tile = rows_lds[wave][buf];
     u32x4 bv[8];  // dims 16s + 8h .. + 7 of row col
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
@@ -624,17 +639,18 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const uint32_t w[4] = {bv[st].x, bv[st].y, bv[st].z, bv[st].w};
-      float z[8];
+      float z[8], m8[8], s8[8];
+      lds8(mu + 16 * st + 8 * h, m8);
+      lds8(inv_sd + 16 * st + 8 * h, s8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int dd = 16 * st + 8 * h + e;
         const float b = (e & 1) ? spr::bf16_hi(w[e / 2]) : spr::bf16_lo(w[e / 2]);
-        z[e] = (b - mu[dd]) * inv_sd[dd];
+        z[e] = (b - m8[e]) * s8[e];
       }
       u32x4 zh, zl;
       split_bf16x8(z, zh, zl);
-      const u32x4 ah = col < RK ? lfrag[st][h][col][0] : zero;
-      const u32x4 al = col < RK ? lfrag[st][h][col][1] : zero;
+      const u32x4 ah = lfrag[st][h][col][0];
+      const u32x4 al = lfrag[st][h][col][1];
       cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zh), cacc, 0, 0, 0);
       cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(al), spr::as_bf16x8(zh), cacc, 0, 0, 0);
       cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zl), cacc, 0, 0, 0);
@@ -660,10 +676,13 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
     float bn = 0.0f, cn = 0.0f;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
+      float y8[2][8];
+      lds8(my + 32 * nt + 8 * h, y8[0]);
+      lds8(my + 32 * nt + 16 + 8 * h, y8[1]);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int st = 2 * nt + r / 8, e = r % 8;
-        acc[nt][r] += my[16 * st + 8 * h + e];
+        acc[nt][r] += y8[r / 8][e];
         if constexpr (CAP) {
           const uint32_t w = (e / 2 == 0) ? bv[st].x : (e / 2 == 1) ? bv[st].y : (e / 2 == 2) ? bv[st].z : bv[st].w;
           const float b = (e & 1) ? spr::bf16_hi(w) : spr::bf16_lo(w);
@@ -678,20 +697,24 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
       cn = sum_xor32(cn);
       scale = alpha * fminf(1.0f, norm_cap * sqrtf(bn) / fmaxf(sqrtf(cn), 1e-20f));
     }
-    const int64_t row = w0 + col;
-    if (row < n) {
-      uint16_t* orow = out + (bh * n + row) * D;
+    // output rows into the batch's buffer (its input is in registers), then out in row order
 #pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        const uint32_t w[4] = {bv[st].x, bv[st].y, bv[st].z, bv[st].w};
-        uint32_t o[4];
+    for (int st = 0; st < 8; ++st) {
+      const uint32_t w[4] = {bv[st].x, bv[st].y, bv[st].z, bv[st].w};
+      uint32_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          o[i] = spr::pack_bf16x2(__builtin_fmaf(scale, acc[st / 2][8 * (st % 2) + 2 * i], spr::bf16_lo(w[i])),
-                                  __builtin_fmaf(scale, acc[st / 2][8 * (st % 2) + 2 * i + 1], spr::bf16_hi(w[i])));
-        }
-        *reinterpret_cast<u32x4*>(orow + 16 * st + 8 * h) = u32x4{o[0], o[1], o[2], o[3]};
+      for (int i = 0; i < 4; ++i) {
+        o[i] = spr::pack_bf16x2(__builtin_fmaf(scale, acc[st / 2][8 * (st % 2) + 2 * i], spr::bf16_lo(w[i])),
+                                __builtin_fmaf(scale, acc[st / 2][8 * (st % 2) + 2 * i + 1], spr::bf16_hi(w[i])));
       }
+      *reinterpret_cast<u32x4*>(tile + col * ROWB + (((2 * st + h) ^ (col & 15)) << 4)) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+    uint16_t* obase = out + (bh * n + w0) * D;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // instruction i: rows 4i .. 4i + 3, piece lane % 16 of each
+      const int r = 4 * i + (lane >> 4), j = lane & 15;
+      const u32x4 o = *reinterpret_cast<const u32x4*>(tile + r * ROWB + ((j ^ (r & 15)) << 4));
+      if (w0 + r < n) *reinterpret_cast<u32x4*>(obase + r * D + 8 * j) = o;
     }
   }
 }
