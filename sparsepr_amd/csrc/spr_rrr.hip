@@ -255,7 +255,7 @@ struct EigLayout {
 // gets the eigenvectors in ascending eigenvalue order (as torch.linalg.eigh's last
 // `rank` columns); vals [rank] (nullable) their Rayleigh quotients, ascending.
 template <int MAXR>
-__device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int n, int rank, bool symmetrize,
+__device__ __forceinline__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int n, int rank, bool symmetrize,
                           float* __restrict__ basis, float* __restrict__ vals) {
   using L = EigLayout<MAXR>;
   const int t = threadIdx.x, i = t >> 3, c = t & 7, lane = t & 63, wv = t >> 6;
@@ -452,8 +452,10 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
   // ---- eigenvectors of T by inverse iteration, 16 at a time: lane s of wave 0 computes
   // vector 16 bt + s (column of X), with the pivoted LU of T - lambda I in its own
   // columns of the U / L arrays.  Members of a cluster (eigenvalue gaps below
-  // 1e-3 ||T||) run in successive rounds and are orthogonalised against the members
-  // before them (earlier batches are complete).
+  // 1e-3 ||T||) are solved together, each with its own shift, and after every solve
+  // they are normalised and orthogonalised in order against the members before them
+  // (earlier batches are complete): block inverse iteration, which converges to the
+  // cluster's invariant subspace.
   float* X = sm + L::X;  // [128][XS]
   constexpr int XS = L::XS;
   if (wv == 0) {
@@ -478,18 +480,19 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
       const int sl = lane;  // column of the LU arrays
       const int s = 16 * bt + lane;
       const bool act = lane < 16 && s < rank;
-      int mypos = 0, maxpos = 0;
+      int mypos = 0;  // members of this vector's cluster before it
       {
         int pos = 0;
         for (int u = 1; u < min(rank, 16 * bt + 16); ++u) {
           pos = (lam[u - 1] - lam[u] < ortol) ? pos + 1 : 0;
           if (u == s) mypos = pos;
-          if (u >= 16 * bt) maxpos = max(maxpos, pos);
         }
       }
       const float lm = act ? lam[s] : 0.0f;
-      for (int rho = 0; rho <= maxpos; ++rho) {
-        const bool mine = act && mypos == rho;
+      // a member of a cluster with followers or predecessors
+      const bool clustered = act && (mypos > 0 || (s + 1 < rank && lam[s] - lam[s + 1] < ortol));
+      {
+        const bool mine = act;
         float sc = 1.0f;
         if (mine) {
           float cd = dget(0) - lm;
@@ -579,7 +582,9 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
             sc = mx > 0.0f ? 1.0f / mx : 1.0f;
           }
           wave_sync();
-          uint64_t todo = __ballot(mine && mypos > 0);
+          // cluster members in ascending order: normalised, and orthogonalised against the
+          // members before them (which this pass has already normalised)
+          uint64_t todo = __ballot(clustered);
           while (todo != 0ull) {
             const int ls = __builtin_ctzll(todo);
             todo &= todo - 1ull;
@@ -737,7 +742,7 @@ __device__ void rrr_eigen(float* sm, const float* __restrict__ bmat, int ld, int
 // c = k % 8 is the pivot column, the array shifts down one register per block);
 // groups of four registers past the end are skipped, and so are waves whose rows
 // are all finished.
-__device__ void rrr_cholesky(float* sm, float* __restrict__ gmat, int p) {
+__device__ __forceinline__ void rrr_cholesky(float* sm, float* __restrict__ gmat, int p) {
   const int t = threadIdx.x, i = t >> 3, c = t & 7, wv = t >> 6;
   float g[16];
 #pragma unroll
