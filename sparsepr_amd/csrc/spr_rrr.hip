@@ -828,37 +828,78 @@ __device__ __forceinline__ void load_factor_and_xt(const float* __restrict__ lg,
 }
 
 // L L^T u = b for one right-hand side held by a wave: entry k in lane k % 64 of b0 (k < 64)
-// or b1 (k >= 64).  Entries at or beyond n stay as they are.
+// or b1 (k >= 64).  Entries at or beyond n stay as they are.  Each substitution step is a
+// short dependent chain (scale by the reciprocal pivot, broadcast, one FMA per lane); the
+// factor entries it needs are read from LDS eight steps at a time ahead of the chain.
 __device__ __forceinline__ void chol_solve_wave(const float* ls, int n, int lane, float& b0, float& b1) {
-  for (int k = 0; k < n; ++k) {  // L y = b
-    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
-    const float yk = bk / ls[k * RRR_LS + k];
-    if (lane == (k & 63)) {
-      if (k < 64) b0 = yk;
-      else b1 = yk;
+  const float rd0 = lane < n ? 1.0f / ls[lane * RRR_LS + lane] : 0.0f;
+  const float rd1 = lane + 64 < n ? 1.0f / ls[(lane + 64) * RRR_LS + lane + 64] : 0.0f;
+  for (int k0 = 0; k0 < n; k0 += 8) {  // L y = b: column k of L, rows lane and lane + 64
+    float c0[8], c1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = min(k0 + u, RRR_MAX - 1);
+      c0[u] = lane > k ? ls[lane * RRR_LS + k] : 0.0f;
+      c1[u] = lane + 64 > k ? ls[(lane + 64) * RRR_LS + k] : 0.0f;
     }
-    if (lane > k && lane < n) b0 -= ls[lane * RRR_LS + k] * yk;
-    if (lane + 64 > k && lane + 64 < n) b1 -= ls[(lane + 64) * RRR_LS + k] * yk;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      if (k < n) {
+        const float yk = lane_read(k < 64 ? b0 * rd0 : b1 * rd1, k & 63);
+        if (lane == (k & 63)) {
+          if (k < 64) b0 = yk;
+          else b1 = yk;
+        }
+        b0 = fmaf(-c0[u], yk, b0);
+        b1 = fmaf(-c1[u], yk, b1);
+      }
+    }
   }
-  for (int k = n - 1; k >= 0; --k) {  // L^T u = y
-    const float bk = lane_read(k < 64 ? b0 : b1, k & 63);
-    const float xk = bk / ls[k * RRR_LS + k];
-    if (lane == (k & 63)) {
-      if (k < 64) b0 = xk;
-      else b1 = xk;
+  for (int k0 = n - 1; k0 >= 0; k0 -= 8) {  // L^T u = y: row k of L, columns lane and lane + 64
+    float c0[8], c1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = max(k0 - u, 0);
+      c0[u] = lane < k ? ls[k * RRR_LS + lane] : 0.0f;
+      c1[u] = lane + 64 < k ? ls[k * RRR_LS + lane + 64] : 0.0f;
     }
-    if (lane < k) b0 -= ls[k * RRR_LS + lane] * xk;
-    if (lane + 64 < k) b1 -= ls[k * RRR_LS + lane + 64] * xk;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 - u;
+      if (k >= 0) {
+        const float xk = lane_read(k < 64 ? b0 * rd0 : b1 * rd1, k & 63);
+        if (lane == (k & 63)) {
+          if (k < 64) b0 = xk;
+          else b1 = xk;
+        }
+        b0 = fmaf(-c0[u], xk, b0);
+        b1 = fmaf(-c1[u], xk, b1);
+      }
+    }
   }
 }
 
 // v = x_w^T u for u over the m rows (held as in chol_solve_wave): entry a (< p) in lane a % 64.
 __device__ __forceinline__ void xt_times(const float* xt, int m, int lane, float& b0, float& b1) {
   float l0 = 0.0f, l1 = 0.0f;
-  for (int r = 0; r < m; ++r) {
-    const float u = lane_read(r < 64 ? b0 : b1, r & 63);
-    l0 += xt[lane * RRR_LS + r] * u;
-    l1 += xt[(lane + 64) * RRR_LS + r] * u;
+  for (int r0 = 0; r0 < m; r0 += 8) {
+    float e0[8], e1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int r = min(r0 + u, RRR_MAX - 1);
+      e0[u] = xt[lane * RRR_LS + r];
+      e1[u] = xt[(lane + 64) * RRR_LS + r];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int r = r0 + u;
+      if (r < m) {
+        const float uu = lane_read(r < 64 ? b0 : b1, r & 63);
+        l0 += e0[u] * uu;
+        l1 += e1[u] * uu;
+      }
+    }
   }
   b0 = l0;
   b1 = l1;
@@ -878,21 +919,43 @@ __device__ __forceinline__ void ridge_apply_f64(const float* xt, bool dual, int 
                                                 float u0, float u1, double& g0, double& g1) {
   const int n_in = dual ? m : p, n_mid = dual ? p : m;
   double v0 = 0.0, v1 = 0.0;  // the middle vector: x_w^T u (dual) or x_w u (primal)
-  for (int k = 0; k < n_in; ++k) {
-    const double uk = static_cast<double>(lane_read(k < 64 ? u0 : u1, k & 63));
-    // dual: v[a] = sum_r x_w[r][a] u[r] = xt[a][r]; primal: v[r] = sum_a x_w[r][a] u[a] = xt[a][r]
-    const float e0 = dual ? xt[lane * RRR_LS + k] : xt[k * RRR_LS + lane];
-    const float e1 = dual ? xt[(lane + 64) * RRR_LS + k] : xt[k * RRR_LS + lane + 64];
-    v0 = fma(static_cast<double>(e0), uk, v0);
-    v1 = fma(static_cast<double>(e1), uk, v1);
+  for (int k0 = 0; k0 < n_in; k0 += 8) {
+    float e0[8], e1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = min(k0 + u, RRR_MAX - 1);
+      // dual: v[a] = sum_r x_w[r][a] u[r] = xt[a][r]; primal: v[r] = sum_a x_w[r][a] u[a] = xt[a][r]
+      e0[u] = dual ? xt[lane * RRR_LS + k] : xt[k * RRR_LS + lane];
+      e1[u] = dual ? xt[(lane + 64) * RRR_LS + k] : xt[k * RRR_LS + lane + 64];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      if (k < n_in) {
+        const double uk = static_cast<double>(lane_read(k < 64 ? u0 : u1, k & 63));
+        v0 = fma(static_cast<double>(e0[u]), uk, v0);
+        v1 = fma(static_cast<double>(e1[u]), uk, v1);
+      }
+    }
   }
   double w0 = 0.0, w1 = 0.0;  // x_w v (dual) or x_w^T v (primal)
-  for (int k = 0; k < n_mid; ++k) {
-    const double vk = lane_read_d(k < 64 ? v0 : v1, k & 63);
-    const float e0 = dual ? xt[k * RRR_LS + lane] : xt[lane * RRR_LS + k];
-    const float e1 = dual ? xt[k * RRR_LS + lane + 64] : xt[(lane + 64) * RRR_LS + k];
-    w0 = fma(static_cast<double>(e0), vk, w0);
-    w1 = fma(static_cast<double>(e1), vk, w1);
+  for (int k0 = 0; k0 < n_mid; k0 += 8) {
+    float e0[8], e1[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = min(k0 + u, RRR_MAX - 1);
+      e0[u] = dual ? xt[k * RRR_LS + lane] : xt[lane * RRR_LS + k];
+      e1[u] = dual ? xt[k * RRR_LS + lane + 64] : xt[(lane + 64) * RRR_LS + k];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      if (k < n_mid) {
+        const double vk = lane_read_d(k < 64 ? v0 : v1, k & 63);
+        w0 = fma(static_cast<double>(e0[u]), vk, w0);
+        w1 = fma(static_cast<double>(e1[u]), vk, w1);
+      }
+    }
   }
   g0 = w0 + static_cast<double>(ridge) * u0;
   g1 = w1 + static_cast<double>(ridge) * u1;
