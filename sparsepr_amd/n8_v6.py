@@ -502,13 +502,18 @@ class N8V6Core:
 
         base_video, q_video [B, H, N, D]; k_full, v_full [B, H, N', D] bf16.
         Returns (corrected [B, H, N, D], info dict)."""
-        batch, heads, tokens, dim = base_video.shape
+        return self.repair_finish(base_video, self.repair_probes(q_video, k_full, v_full, route), route)
+
+    def repair_probes(self, q_video, k_full, v_full, route: N8V6Route):
+        """The part of the repair that does not read the base output: probe rows and
+        weights (cached on the route) and the dense attention of the probe queries over
+        all keys.  It can run while the sparse attention computes the base."""
+        batch, heads, tokens, dim = q_video.shape
         bh = batch * heads
         cfg = self.config
         if cfg.repair_features != "output":
             raise NotImplementedError(f"repair_features={cfg.repair_features!r} is not supported by the MI355X "
                                       "build; only the output-feature repair is built.")
-        base = base_video.contiguous().view(bh, tokens, dim)
         if route.probe_rows is not None and route.probe_weights is not None:
             rows, weights = route.probe_rows, route.probe_weights
             cache_hit = True
@@ -525,7 +530,6 @@ class N8V6Core:
                                           cfg.probe_rows, mode, centers=route.q_role_centers, sizes=sizes)
             route.probe_rows = rows
             route.probe_weights = weights
-        count = int(rows.shape[1])
         q_flat = q_video.contiguous().view(bh, tokens, dim)
         from .flash_kmeans.kmeans_impl import gather_rows
 
@@ -534,6 +538,17 @@ class N8V6Core:
         vf = v_full.reshape(bh, -1, dim)
         dense_probe = dense_attention(q_probe, kf, vf, out_dtype=q_video.dtype if q_video.dtype == torch.bfloat16
                                       else torch.float32)
+        return rows, weights, dense_probe, cache_hit
+
+    def repair_finish(self, base_video, probes, route: N8V6Route):
+        """The rest of the repair given repair_probes' result: fit on the probe rows of
+        the base output, low-rank correction of every row, exact probe rows."""
+        batch, heads, tokens, dim = base_video.shape
+        bh = batch * heads
+        cfg = self.config
+        rows, weights, dense_probe, cache_hit = probes
+        base = base_video.contiguous().view(bh, tokens, dim)
+        count = int(rows.shape[1])
         shape = (bh, count, dim)
         if self._fit_feature_buffer is None or tuple(self._fit_feature_buffer.shape) != shape:
             self._fit_feature_buffer = torch.empty(shape, device=base.device, dtype=torch.float32)
