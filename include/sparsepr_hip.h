@@ -38,6 +38,11 @@ int spr_permute_rows(const void* src, const int32_t* idx, void* dst, int64_t bh,
  *   dst[b, idx[b, s], :] = src[b, s, :] */
 int spr_inverse_permute_rows(const void* src, const int32_t* idx, void* dst, int64_t bh, int64_t rows,
                              int64_t row_bytes, hipStream_t stream);
+/* The same (permute.py:235-274; the adapters pass the video part of the attention output,
+ * a slice of a longer tensor, hunyuanvideo.py:229-231) with head b's source rows starting
+ * src_head_bytes after head b - 1's (src_head_bytes >= rows * row_bytes): read in place. */
+int spr_inverse_permute_rows_strided(const void* src, int64_t src_head_bytes, const int32_t* idx, void* dst,
+                                     int64_t bh, int64_t rows, int64_t row_bytes, hipStream_t stream);
 /* permute.py:175-232 permute_concatenated_tensors_by_labels_triton
  *   dst[b, s, :] = cat(prefix[b], suffix[b])[idx[b, s], :] */
 int spr_permute_concat_rows(const void* prefix, const void* suffix, const int32_t* idx, void* dst, int64_t bh,
@@ -217,6 +222,13 @@ size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t d, int32_t
 int spr_dense_attention(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv, int64_t m,
                         int64_t s_kv, int32_t d, float scale, int32_t nsplit, void* out, int32_t out_dtype,
                         float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The same call site (n8_v6.py:1236-1243, whose keys are the video keys plus the prompt
+ * tokens, a slice of the full K/V): kv head h's s_kv rows start kv_head_stride elements
+ * after head h - 1's (kv_head_stride >= s_kv * d), so the slice is read in place. */
+int spr_dense_attention_strided(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv, int64_t m,
+                                int64_t s_kv, int64_t kv_head_stride, int32_t d, float scale, int32_t nsplit,
+                                void* out, int32_t out_dtype, float* lse, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream);
 
 /* ---------------------------------------------------------------- N8 residual repair
  * residual_repair.py:36-118 select_role_equal_probes(_vectorized), group distances:

@@ -29,6 +29,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     # permute.hip
     "spr_permute_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "spr_inverse_permute_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "spr_inverse_permute_rows_strided": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
     "spr_permute_concat_rows": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "spr_gather_rows": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
     "spr_scatter_rows": (ctypes.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
@@ -65,6 +66,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_dense_attention_workspace": (_sz, [_i64, _i64, _i32, _i32]),
     "spr_dense_attention": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _vp, _i32, _vp,
                                            _vp, _sz, _vp]),
+    "spr_dense_attention_strided": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _vp,
+                                                   _i32, _vp, _vp, _sz, _vp]),
     # repair.hip
     "spr_probe_distances": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "spr_probe_select_workspace": (_sz, [_i64, _i32]),

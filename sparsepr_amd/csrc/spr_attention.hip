@@ -298,7 +298,8 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
     int32_t bh_q, int32_t tiles_per_head, float scale_log2, const int32_t* __restrict__ q_index,
     const int32_t* __restrict__ k_index, uint16_t* __restrict__ out, float* __restrict__ lse, int32_t split_len, float* __restrict__ part_o,
-    float* __restrict__ part_ml) {
+    float* __restrict__ part_ml, int64_t kv_stride) {
+  // kv_stride: elements from one kv head's rows to the next (s_kv * D when packed)
   constexpr int NT = NW * 64;
   static_assert(NW * QB * 32 == BM, "tile shape");
   using T = Tile<D, NT>;
@@ -351,8 +352,8 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   const int64_t bhkv = bhq / group;
 
   const uint16_t* qb = q + bhq * static_cast<int64_t>(s_q) * D;
-  const uint16_t* kb = k + bhkv * static_cast<int64_t>(s_kv) * D;
-  const uint16_t* vb = v + bhkv * static_cast<int64_t>(s_kv) * D;
+  const uint16_t* kb = k + bhkv * kv_stride;
+  const uint16_t* vb = v + bhkv * kv_stride;
   // raw buffer views of this head's K and V: 32-bit offsets, reads past the end return 0
   const int32_t kv_bytes = s_kv * D * 2;
   const __amdgpu_buffer_rsrc_t k_rsrc =
@@ -1280,7 +1281,7 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
       static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
       static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
       static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index, k_index,            \
-      static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr)
+      static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr, s * DD)
 #define SPR_ATTN(DD, SL)               \
   do {                                 \
     if (k_index != nullptr) {          \
@@ -1336,11 +1337,29 @@ extern "C" size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t
 // q [bh_q, m, d] bf16, k/v [bh_kv, s_kv, d] bf16, keys split into nsplit ranges
 // processed in parallel and merged.  out [bh_q, m, d] (out_dtype 0 = bf16, 2 = fp32),
 // lse fp32 [bh_q, m] nullable.
+extern "C" int spr_dense_attention_strided(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv,
+                                           int64_t m, int64_t s_kv, int64_t kv_head_stride, int32_t d, float scale,
+                                           int32_t nsplit, void* out, int32_t out_dtype, float* lse, void* workspace,
+                                           size_t workspace_bytes, hipStream_t stream);
+
 extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv,
                                    int64_t m, int64_t s_kv, int32_t d, float scale, int32_t nsplit, void* out,
                                    int32_t out_dtype, float* lse, void* workspace, size_t workspace_bytes,
                                    hipStream_t stream) {
+  return spr_dense_attention_strided(q, k, v, bh_q, bh_kv, m, s_kv, s_kv * d, d, scale, nsplit, out, out_dtype, lse,
+                                     workspace, workspace_bytes, stream);
+}
+
+// The same with kv head h's rows starting kv_head_stride elements after head h - 1's
+// (rows of d contiguous elements, s_kv of them per head): a slice of the keys of a larger
+// packed tensor is read in place.
+extern "C" int spr_dense_attention_strided(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv,
+                                           int64_t m, int64_t s_kv, int64_t kv_head_stride, int32_t d, float scale,
+                                           int32_t nsplit, void* out, int32_t out_dtype, float* lse, void* workspace,
+                                           size_t workspace_bytes, hipStream_t stream) {
   SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && m >= 0 && s_kv >= 0 && nsplit >= 1, "spr_dense_attention: bad size");
+  SPR_REQUIRE(kv_head_stride >= s_kv * d, "spr_dense_attention: kv head stride %lld below s_kv * d",
+              static_cast<long long>(kv_head_stride));
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_dense_attention: bh_q not a multiple of bh_kv");
   SPR_REQUIRE(d == 64 || d == 128, "spr_dense_attention: head dim %d not supported (64, 128)", d);
   SPR_REQUIRE(out_dtype == 0 || out_dtype == 2, "spr_dense_attention: out_dtype must be 0 or 2");
@@ -1366,7 +1385,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_fwd_kernel<128, 1, false, 4, 1, false><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
-        scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
+        scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml, kv_head_stride);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                           nsplit, out_dtype, out, lse);
@@ -1374,7 +1393,7 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
     attn_fwd_kernel<64, 1, false, 4, 1, false><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
-        scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml);
+        scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml, kv_head_stride);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
     attn_combine_kernel<64><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
                                                          nsplit, out_dtype, out, lse);

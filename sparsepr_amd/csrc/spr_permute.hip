@@ -20,7 +20,8 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const V* __restrict__
                                                            const int32_t* __restrict__ idx,
                                                            V* __restrict__ dst, uint32_t src_rows,
                                                            uint32_t dst_rows, uint32_t prefix_rows,
-                                                           uint32_t vec_per_row) {
+                                                           uint32_t vec_per_row, uint64_t src_bh) {
+  // src_bh: vectors from one head's source rows to the next (MODE_GATHER / MODE_SCATTER)
   // MODE_GATHER / MODE_CONCAT walk the destination rows (idx has dst_rows
   // entries per bh); MODE_SCATTER walks the source rows (idx has src_rows).
   const uint32_t walk_rows = (MODE == MODE_SCATTER) ? src_rows : dst_rows;
@@ -41,9 +42,9 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const V* __restrict__
     if (MODE == MODE_GATHER) {
       const bool valid = live[u] && r < src_rows;
       dst_off[u] = bh * per_bh + g;
-      vals[u] = valid ? src[(bh * src_rows + r) * vec_per_row + v] : V{};
+      vals[u] = valid ? src[bh * src_bh + static_cast<uint64_t>(r) * vec_per_row + v] : V{};
     } else if (MODE == MODE_SCATTER) {
-      vals[u] = live[u] ? src[bh * per_bh + g] : V{};
+      vals[u] = live[u] ? src[bh * src_bh + g] : V{};
       dst_off[u] = (bh * dst_rows + r) * vec_per_row + v;
       live[u] = live[u] && r < dst_rows;
     } else {
@@ -68,16 +69,21 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const V* __restrict__
 template <int MODE>
 int launch_permute(const void* src, const void* suffix, const int32_t* idx, void* dst, int64_t bh,
                    int64_t src_rows, int64_t dst_rows, int64_t prefix_rows, int64_t row_bytes,
-                   hipStream_t stream, const char* name) {
+                   hipStream_t stream, const char* name, int64_t src_head_bytes = 0) {
+  // src_head_bytes: bytes from one head's source rows to the next (0: packed, src_rows rows)
   SPR_REQUIRE(bh >= 0 && src_rows >= 0 && dst_rows >= 0, "%s: negative size", name);
   const int64_t walk_rows = (MODE == MODE_SCATTER) ? src_rows : dst_rows;
   if (bh == 0 || walk_rows == 0 || row_bytes == 0) return SPR_OK;
   SPR_REQUIRE(src && idx && dst, "%s: null pointer", name);
   SPR_REQUIRE(bh <= 65535, "%s: bh=%lld exceeds 65535", name, (long long)bh);
   SPR_REQUIRE(row_bytes % 2 == 0, "%s: row bytes %lld not a multiple of 2", name, (long long)row_bytes);
+  if (src_head_bytes == 0) src_head_bytes = src_rows * row_bytes;
+  SPR_REQUIRE(src_head_bytes >= src_rows * row_bytes, "%s: source head stride %lld below %lld rows of %lld bytes",
+              name, (long long)src_head_bytes, (long long)src_rows, (long long)row_bytes);
   auto aligned = [&](uintptr_t a) {
     return (reinterpret_cast<uintptr_t>(src) % a == 0) && (reinterpret_cast<uintptr_t>(dst) % a == 0) &&
-           (suffix == nullptr || reinterpret_cast<uintptr_t>(suffix) % a == 0);
+           (suffix == nullptr || reinterpret_cast<uintptr_t>(suffix) % a == 0) &&
+           static_cast<uintptr_t>(src_head_bytes) % a == 0;
   };
   const bool wide = (row_bytes % 16 == 0) && aligned(16);
   const bool word = !wide && (row_bytes % 4 == 0) && aligned(4);
@@ -93,17 +99,17 @@ int launch_permute(const void* src, const void* suffix, const int32_t* idx, void
     permute_rows_kernel<spr::u32x4, UNROLL, MODE><<<grid, 256, 0, stream>>>(
         static_cast<const spr::u32x4*>(src), static_cast<const spr::u32x4*>(suffix), idx,
         static_cast<spr::u32x4*>(dst), static_cast<uint32_t>(src_rows), static_cast<uint32_t>(dst_rows),
-        static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr));
+        static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr), static_cast<uint64_t>(src_head_bytes / vec));
   } else if (word) {
     permute_rows_kernel<uint32_t, UNROLL, MODE><<<grid, 256, 0, stream>>>(
         static_cast<const uint32_t*>(src), static_cast<const uint32_t*>(suffix), idx,
         static_cast<uint32_t*>(dst), static_cast<uint32_t>(src_rows), static_cast<uint32_t>(dst_rows),
-        static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr));
+        static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr), static_cast<uint64_t>(src_head_bytes / vec));
   } else {
     permute_rows_kernel<uint16_t, UNROLL, MODE><<<grid, 256, 0, stream>>>(
         static_cast<const uint16_t*>(src), static_cast<const uint16_t*>(suffix), idx,
         static_cast<uint16_t*>(dst), static_cast<uint32_t>(src_rows), static_cast<uint32_t>(dst_rows),
-        static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr));
+        static_cast<uint32_t>(prefix_rows), static_cast<uint32_t>(vpr), static_cast<uint64_t>(src_head_bytes / vec));
   }
   SPR_LAUNCHED(name);
   return SPR_OK;
@@ -123,6 +129,14 @@ extern "C" int spr_inverse_permute_rows(const void* src, const int32_t* idx, voi
                                         int64_t rows, int64_t row_bytes, hipStream_t stream) {
   return launch_permute<MODE_SCATTER>(src, nullptr, idx, dst, bh, rows, rows, 0, row_bytes, stream,
                                       "spr_inverse_permute_rows");
+}
+
+// spr_inverse_permute_rows with head b's source rows starting src_head_bytes after head
+// b - 1's (a slice of the rows of a larger packed tensor, read in place).
+extern "C" int spr_inverse_permute_rows_strided(const void* src, int64_t src_head_bytes, const int32_t* idx, void* dst,
+                                                int64_t bh, int64_t rows, int64_t row_bytes, hipStream_t stream) {
+  return launch_permute<MODE_SCATTER>(src, nullptr, idx, dst, bh, rows, rows, 0, row_bytes, stream,
+                                      "spr_inverse_permute_rows_strided", src_head_bytes);
 }
 
 // dst[b, s, :] = cat(prefix[b], suffix[b])[idx[b, s], :]

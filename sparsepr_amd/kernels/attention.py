@@ -138,12 +138,17 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale:
         # workgroup past a whole round leaves a nearly empty last one)
         mtiles = max(1, (m + 127) // 128)
         nsplit = max(1, min(512 // (bh_q * mtiles), s_kv // 512))
-    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    qc = q.contiguous()
+    # K/V whose rows are packed within each head, with one head stride for both (a slice
+    # of the keys of a larger tensor), are read in place
+    in_place = (k.stride(2) == 1 and k.stride(1) == d and v.stride() == k.stride() and k.stride(0) >= s_kv * d
+                and k.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0)
+    kc, vc = (k, v) if in_place else (k.contiguous(), v.contiguous())
     out = torch.empty((bh_q, m, d), dtype=out_dtype, device=dev)
     lse = torch.empty((bh_q, m), dtype=torch.float32, device=dev) if return_lse else None
     ws = _lib.workspace(_lib.query("spr_dense_attention_workspace", bh_q, m, d, nsplit), dev)
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(d)
-    _lib.call("spr_dense_attention", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), bh_q, bh_kv, m, s_kv, d, sc, nsplit,
-              _lib.ptr(out), 0 if out_dtype == torch.bfloat16 else 2, _lib.ptr(lse), _lib.ptr(ws), ws.numel(),
-              _lib.stream(dev))
+    _lib.call("spr_dense_attention_strided", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), bh_q, bh_kv, m, s_kv,
+              kc.stride(0) if bh_kv > 1 else s_kv * d, d, sc, nsplit, _lib.ptr(out),
+              0 if out_dtype == torch.bfloat16 else 2, _lib.ptr(lse), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
     return (out, lse) if return_lse else out

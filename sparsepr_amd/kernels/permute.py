@@ -132,7 +132,16 @@ def apply_inverse_permutation_triton(
     B, H, S, D = permuted_tensor.shape
     bh = B * H
     si = sorted_indices.to(torch.int32).reshape(bh, S).contiguous()
-    inp = permuted_tensor.reshape(bh, S, D).contiguous()
+    t = permuted_tensor
+    # rows packed within each head and one stride between heads (a slice of the rows of a
+    # longer tensor, e.g. the video part of an attention output): read in place
+    if t.stride(3) == 1 and t.stride(2) == D and (H == 1 or t.stride(0) == H * t.stride(1)):
+        head = t.stride(1) if H > 1 else (t.stride(0) if B > 1 else S * D)
+        out = torch.empty((bh, S, D), dtype=t.dtype, device=dev)
+        _lib.call("spr_inverse_permute_rows_strided", _lib.ptr(t), head * t.element_size(), _lib.ptr(si),
+                  _lib.ptr(out), bh, S, D * t.element_size(), _lib.stream(dev))
+        return out.reshape(B, H, S, D)
+    inp = t.reshape(bh, S, D).contiguous()
     out = torch.empty_like(inp)
     _lib.call("spr_inverse_permute_rows", _lib.ptr(inp), _lib.ptr(si), _lib.ptr(out), bh, S,
               D * inp.element_size(), _lib.stream(dev))

@@ -174,6 +174,28 @@ def test_dense_probe_attention_gqa_tiles(dev, oracle, M, S, nsplit):
     assert np.allclose(lse.cpu().numpy(), ref_lse, atol=2e-3)
 
 
+def test_dense_probe_attention_reads_a_key_slice_in_place(dev, oracle):
+    """K/V given as the first S keys of a longer packed tensor (the probes attend the video
+    keys plus the prompt): read in place through the head stride, the output is the same
+    bits as from packed copies, and matches the float64 closed form."""
+    from sparsepr_amd.kernels.attention import dense_attention
+
+    rng = np.random.default_rng(77)
+    full = 1300
+    q = oracle.to_bf16(rng.standard_normal((4, 64, 128)).astype(np.float32))
+    kf = oracle.to_bf16(rng.standard_normal((4, full, 128)).astype(np.float32))
+    vf = oracle.to_bf16(rng.standard_normal((4, full, 128)).astype(np.float32))
+    dk, dv = to_dev(kf, dev, torch.bfloat16), to_dev(vf, dev, torch.bfloat16)
+    for s_kv in (1000, 1077):
+        ks, vs = dk[:, :s_kv], dv[:, :s_kv]
+        assert not ks.is_contiguous()
+        got = dense_attention(to_dev(q, dev, torch.bfloat16), ks, vs)
+        packed = dense_attention(to_dev(q, dev, torch.bfloat16), ks.contiguous(), vs.contiguous())
+        assert torch.equal(got, packed)
+        ref = oracle.dense_attention(q, kf[:, :s_kv], vf[:, :s_kv])
+        assert np.abs(got.cpu().numpy() - ref).max() <= 5e-3
+
+
 def test_block_sparse_full_size_sampled_rows(dev, oracle):
     """HunyuanVideo shape (24 heads x 118,800 x 128): a random map over 128 x 512
     cluster pairs; 192 sampled rows checked against float64 on the CPU."""

@@ -109,3 +109,21 @@ def test_permute_full_size_round_trip(dev):
     assert torch.equal(apply_inverse_permutation_triton(y, idx, dim=2), x)
     _, sizes, offsets = argsort_labels(lab, 512)
     assert torch.equal(sizes.sum(1), torch.full((24,), 118800, dtype=torch.int64, device=dev).to(sizes.dtype))
+
+
+def test_inverse_permutation_of_a_row_slice_in_place(dev):
+    """The video rows of a longer [B, H, S + T, D] tensor (a slice, not packed) are
+    un-permuted in place: the same bits as from a packed copy, and a round trip."""
+    from sparsepr_amd.kernels.permute import apply_inverse_permutation_triton, permute_tensor_by_labels_triton
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    B, H, S, T, D = 2, 3, 1000, 77, 128
+    full = torch.randn((B, H, S + T, D), device=dev, generator=g).to(torch.bfloat16)
+    idx = torch.argsort(torch.rand((B * H, S), device=dev, generator=g), dim=-1).to(torch.int32)
+    view = full[:, :, :S]
+    assert not view.is_contiguous()
+    got = apply_inverse_permutation_triton(view, idx, dim=2)
+    ref = apply_inverse_permutation_triton(view.contiguous(), idx, dim=2)
+    assert torch.equal(got, ref)
+    back, _ = permute_tensor_by_labels_triton(got, None, 2, sorted_indices=idx)
+    assert torch.equal(back, view)
