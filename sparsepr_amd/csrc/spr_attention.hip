@@ -738,14 +738,16 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   constexpr int NT = NW * 64;
   constexpr int TBM = NW * 32;
   constexpr int DMA_PER_WAVE = 16 / NW;
-  __shared__ __attribute__((aligned(1024))) uint8_t k_tile0[DTILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t k_tile1[DTILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t k_tile2[DTILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t k_tile3[DTILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_tile0[DTILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_tile1[DTILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_tile2[DTILE];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_tile3[DTILE];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_tiles[4][DTILE];
+  uint8_t* const k_tile0 = k_tiles[0];
+  uint8_t* const k_tile1 = k_tiles[1];
+  uint8_t* const k_tile2 = k_tiles[2];
+  uint8_t* const k_tile3 = k_tiles[3];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_tiles[4][DTILE];
+  uint8_t* const v_tile0 = v_tiles[0];
+  uint8_t* const v_tile1 = v_tiles[1];
+  uint8_t* const v_tile2 = v_tiles[2];
+  uint8_t* const v_tile3 = v_tiles[3];
   __shared__ int32_t key_rows[4][BN];
   __shared__ Seg seg_lds[SEGL ? MAX_LDS_SEGS : 1];
 
@@ -776,7 +778,15 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int qc = pv.qc_by_len[lo];
   const int32_t row0 = pv.q_off[qc] + (tile - pv.tile2_sorted[lo]) * TBM;
   const int32_t row1 = min(row0 + TBM, pv.q_off[qc + 1]);
-  const bool wave_live = row0 + 32 * wave < row1;
+  // A tile with at most four live 32-row blocks pairs its waves: wave w (< 4) takes the
+  // first 32-key half of every chunk for block w and wave w + 4 the second half, each with
+  // its own online softmax, merged at the end (split-key helpers).  Otherwise wave w owns
+  // block w and both halves.
+  const int nblk = (row1 - row0 + 31) / 32;
+  const bool split = nblk <= NW / 2;
+  const int blk = split ? (wave & (NW / 2 - 1)) : wave;
+  const int only = split ? (wave / (NW / 2)) : 0;  // the half a split wave processes
+  const bool wave_live = blk < nblk;
   const Seg* segs = pv.segs + static_cast<int64_t>(qc) * kn;
   const int32_t nseg = pv.nseg[qc];
   const int32_t total = pv.total[qc];
@@ -791,7 +801,7 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     for (int i = tid; i < nseg; i += NT) seg_lds[i] = segs[i];
   }
 
-  int32_t my_row = row0 + wave * 32 + col;
+  int32_t my_row = row0 + blk * 32 + col;
   bool row_live = my_row < row1;
   if (q_index != nullptr && row_live) {
     my_row = q_index[bhq * static_cast<int64_t>(s_q) + my_row];
@@ -991,16 +1001,80 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();  // chunks 0 .. 2 landed
-    if (wave_live) s_mma(s_a, k_tile0, 0);
-    for (int x = 0; x < nch; x += 4) {
-      chunk(x, k_tile0, v_tile0, k_tile1, k_tile3, v_tile3);
-      if (x + 1 < nch) chunk(x + 1, k_tile1, v_tile1, k_tile2, k_tile0, v_tile0);
-      if (x + 2 < nch) chunk(x + 2, k_tile2, v_tile2, k_tile3, k_tile1, v_tile1);
-      if (x + 3 < nch) chunk(x + 3, k_tile3, v_tile3, k_tile0, k_tile2, v_tile2);
+    if (wave_live) s_mma(s_a, k_tile0, only);
+    if (split) {
+      // One half per chunk: S of this wave's half of chunk x is in s_a; S of the same half
+      // of chunk x + 1 (the next K tile, so after the barrier) goes to s_b.  The barriers,
+      // DMAs and planning are those of the full path.
+      for (int x = 0; x < nch; ++x) {
+        const int32_t left = total - x * BN;
+        if (x + 4 < nch) plan_chunk(x + 4);
+        if (x + 3 < nch) load_rows(x + 3);
+        if (wave_live) row_max(s_a, only, left);
+        if (x + 2 < nch) {
+          asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DMA_PER_WAVE) : "memory");
+        } else {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        if (wave_live) {
+          step(s_b, k_tiles[(x + 1) & 3], only, s_a, v_tiles[x & 3], only);
+          s_a = s_b;
+        }
+        if (x + 3 < nch) dma(k_tiles[(x + 3) & 3], v_tiles[(x + 3) & 3]);
+      }
+    } else {
+      for (int x = 0; x < nch; x += 4) {
+        chunk(x, k_tile0, v_tile0, k_tile1, k_tile3, v_tile3);
+        if (x + 1 < nch) chunk(x + 1, k_tile1, v_tile1, k_tile2, k_tile0, v_tile0);
+        if (x + 2 < nch) chunk(x + 2, k_tile2, v_tile2, k_tile3, k_tile1, v_tile1);
+        if (x + 3 < nch) chunk(x + 3, k_tile3, v_tile3, k_tile0, k_tile2, v_tile2);
+      }
     }
   }
 
   // ---- epilogue
+  if (split) {
+    // wave w + 4 hands its (m, l, O) for the second halves to wave w through the K/V tiles
+    // (every wave is past its last chunk after the barrier)
+    __syncthreads();
+    uint8_t* const kt_m = k_tiles[blk];
+    float* ml = reinterpret_cast<float*>(v_tile0);
+    if (only == 1 && wave_live) {
+      float* po = reinterpret_cast<float*>(kt_m) + lane * (DBLK * 16);
+#pragma unroll
+      for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+          *reinterpret_cast<spr::f32x4*>(po + b * 16 + e) =
+              spr::f32x4{o_acc[b][e], o_acc[b][e + 1], o_acc[b][e + 2], o_acc[b][e + 3]};
+        }
+      }
+      ml[(blk * 64 + lane) * 2] = m_run;
+      ml[(blk * 64 + lane) * 2 + 1] = l_run;
+    }
+    __syncthreads();
+    if (only == 1) {
+      row_live = false;  // the first-half wave writes the block
+    } else if (wave_live) {
+      const float* po = reinterpret_cast<const float*>(kt_m) + lane * (DBLK * 16);
+      const float m1 = ml[(blk * 64 + lane) * 2], l1 = ml[(blk * 64 + lane) * 2 + 1];
+      const float mm = fmaxf(m_run, m1);
+      const float a0 = m_run == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(m_run - mm);
+      const float a1 = m1 == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+#pragma unroll
+      for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+          const spr::f32x4 o1 = *reinterpret_cast<const spr::f32x4*>(po + b * 16 + e);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o_acc[b][e + j] = o_acc[b][e + j] * a0 + o1[j] * a1;
+        }
+      }
+      l_run = l_run * a0 + l1 * a1;
+      m_run = mm;
+    }
+  }
   const float l_tot = sum_xor32(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (row_live) {
