@@ -53,6 +53,9 @@ def parse():
                          "means ~N(0, 1) of the BASELINE description)")
     ap.add_argument("--top-p", type=float, default=None)
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
+    ap.add_argument("--one-stream", action="store_true",
+                    help="run the whole layer on one stream (by default Q's k-means and the repair's probe "
+                         "part run on a second stream beside K's k-means)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU-oracle sample (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["attention", "copy", "svg_ear", "role_proj", "n8_route", "qkv"], default=None,
@@ -531,7 +534,7 @@ def bench_layer(args, name, top_p=None, repair=True, amp=None, with_cpu=False):
     cfg = spec["cfg"]
     if top_p is not None:
         cfg = dataclasses.replace(cfg, top_p=top_p)
-    cfg = dataclasses.replace(cfg, repair=repair)
+    cfg = dataclasses.replace(cfg, repair=repair, overlap_streams=not args.one_stream)
     q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **gen)
     layer = SparsePRAttention(cfg)
     for _ in range(args.warmup):

@@ -44,6 +44,9 @@ class SparsePRConfig:
     repair_norm_cap: float = 0.0
     init_seed: int = 0
     x_sq_mode: int = X_SQ_BF16
+    # Q's k-means and the repair's probe part (probe selection, dense probe attention)
+    # run on a second stream beside K's k-means; results are the same either way.
+    overlap_streams: bool = True
 
 
 @dataclass
@@ -71,6 +74,14 @@ class SparsePRAttention:
                            repair_norm_cap=config.repair_norm_cap)
         self.n8 = N8V6Core(n8cfg, validate=False)
         self._init_idx: dict = {}
+        self._side_streams: dict = {}
+
+    def _side_stream(self, device: torch.device) -> torch.cuda.Stream:
+        s = self._side_streams.get(device)
+        if s is None:
+            s = torch.cuda.Stream(device=device)  # default priority
+            self._side_streams[device] = s
+        return s
 
     def _init_centroids(self, x: torch.Tensor, k: int, seed: int) -> torch.Tensor:
         bh, n, _ = x.shape
@@ -88,6 +99,16 @@ class SparsePRAttention:
         With materialize_kv False the route carries no permuted K/V copies
         (k_permuted / v_permuted are None): forward() reads K and V through the
         key sort index instead."""
+        route, q_idx, _ = self._route(q, k, v, timings, materialize_kv=materialize_kv, with_probes=False)
+        return route, q_idx
+
+    def _route(self, q, k, v, timings, *, materialize_kv: bool, with_probes: bool):
+        """route() plus, with with_probes, the repair's base-independent part (probe rows
+        and the dense attention of the probe queries), which needs only Q's clusters.
+
+        With overlap_streams, Q's Lloyd loop and that probe part run on a side stream
+        while K's Lloyd loop runs on the caller's stream; the caller's stream waits for
+        the side stream before the top-p map, so every later stage sees both."""
         cfg = self.config
         _lib.require_gpu(q, k, v, what="SparsePRAttention")
         B, H, N, D = q.shape
@@ -95,30 +116,55 @@ class SparsePRAttention:
         qf = q.reshape(bh, N, D).contiguous()
         kf = k.reshape(bh, N, D).contiguous()
         vf = v.reshape(bh, N, D).contiguous()
-        qres = lloyd(qf, cfg.num_q_centroids, cfg.kmeans_iters, 0.0,
-                     self._init_centroids(qf, cfg.num_q_centroids, cfg.init_seed),
-                     x_sq_mode=cfg.x_sq_mode, want_mean32=True)
+        route = N8V6Route(
+            q_labels=None, k_labels=None, q_cluster_sizes=None, k_cluster_sizes=None, video_dynamic_map=None,
+            q_role_features=qf, k_permuted=None, v_permuted=None, k_sorted_indices=None, base_video_density=None,
+            q_kmeans_iters=0, k_kmeans_iters=0)
+
+        def q_side():
+            qres = lloyd(qf, cfg.num_q_centroids, cfg.kmeans_iters, 0.0,
+                         self._init_centroids(qf, cfg.num_q_centroids, cfg.init_seed),
+                         x_sq_mode=cfg.x_sq_mode, want_mean32=True)
+            route.q_labels, route.q_cluster_sizes = qres.labels, qres.sizes
+            route.q_role_centers, route.q_kmeans_iters = qres.mean32, qres.iters
+            probes = self.n8.repair_probes(q, k, v, route) if with_probes else None
+            return qres, probes
+
+        main = torch.cuda.current_stream(q.device)
+        side = self._side_stream(q.device) if cfg.overlap_streams else None
+        if side is not None:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                qres, probes = q_side()
+        else:
+            qres, probes = q_side()
         kres = lloyd(kf, cfg.num_k_centroids, cfg.kmeans_iters, 0.0,
                      self._init_centroids(kf, cfg.num_k_centroids, cfg.init_seed + 1), x_sq_mode=cfg.x_sq_mode)
+        if side is not None:
+            main.wait_stream(side)
+            # made on the side stream, read on this one: keep the allocator from handing
+            # their memory back to the side stream before this stream is done with them
+            shared = [qres.labels, qres.centroids, qres.sizes, qres.sorted_idx, qres.offsets, qres.mean32]
+            if probes is not None:
+                shared += [probes[0], probes[1], probes[2]]
+            for t in shared:
+                if t is not None:
+                    t.record_stream(main)
         if timings is not None:
             timings.mark("kmeans")
         self.last_centroids = (qres.centroids, kres.centroids)
         dmap = topp_map(qres.centroids, kres.centroids, kres.sizes, cfg.top_p, cfg.min_kc_ratio)
         if timings is not None:
             timings.mark("select")
-        k_perm = v_perm = None
         if materialize_kv:
             from .kernels.permute import permute_tensor_by_labels_triton
 
-            k_perm, _ = permute_tensor_by_labels_triton(k, None, 2, sorted_indices=kres.sorted_idx)
-            v_perm, _ = permute_tensor_by_labels_triton(v, None, 2, sorted_indices=kres.sorted_idx)
-        dens = density(dmap, qres.sizes, kres.sizes).mean()  # device scalar: no host sync
-        route = N8V6Route(
-            q_labels=qres.labels, k_labels=kres.labels, q_cluster_sizes=qres.sizes, k_cluster_sizes=kres.sizes,
-            video_dynamic_map=dmap, q_role_features=qf, k_permuted=k_perm, v_permuted=v_perm,
-            k_sorted_indices=kres.sorted_idx, base_video_density=dens, q_kmeans_iters=qres.iters,
-            k_kmeans_iters=kres.iters, q_role_centers=qres.mean32)
-        return route, qres.sorted_idx
+            route.k_permuted, _ = permute_tensor_by_labels_triton(k, None, 2, sorted_indices=kres.sorted_idx)
+            route.v_permuted, _ = permute_tensor_by_labels_triton(v, None, 2, sorted_indices=kres.sorted_idx)
+        route.k_labels, route.k_cluster_sizes, route.k_sorted_indices = kres.labels, kres.sizes, kres.sorted_idx
+        route.video_dynamic_map, route.k_kmeans_iters = dmap, kres.iters
+        route.base_video_density = density(dmap, qres.sizes, kres.sizes).mean()  # device scalar: no host sync
+        return route, qres.sorted_idx, probes
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, timings: LayerTimings | None = None):
         """Sparse attention output [B, H, N, D] bf16 (with repair unless disabled)."""
@@ -127,7 +173,7 @@ class SparsePRAttention:
         bh = B * H
         if timings is not None:
             timings.mark("start")
-        route, q_idx = self.route(q, k, v, timings)
+        route, q_idx, probes = self._route(q, k, v, timings, materialize_kv=True, with_probes=cfg.repair)
         plan = plan_block_sparse(route.video_dynamic_map, route.q_cluster_sizes, route.k_cluster_sizes, N)
         if timings is not None:
             timings.mark("plan")
@@ -145,7 +191,7 @@ class SparsePRAttention:
         self.last_route = route
         if not cfg.repair:
             return base
-        out, info = self.n8.repair(base, q, k, v, route)
+        out, info = self.n8.repair_finish(base, probes, route)
         self.last_repair_info = info
         if timings is not None:
             timings.mark("repair")

@@ -102,3 +102,24 @@ def test_layer_stagewise_parity(dev, oracle, name):
         assert np.abs(got[h, rr[h]] - dense[h]).max() <= 1e-2  # probe rows carry the dense output
     info = layer.last_repair_info
     assert 0.0 < float(info["effective_video_density"]) <= 1.0
+
+
+def test_side_stream_route_matches_one_stream(dev):
+    """Q's k-means and the repair's probe part on a side stream give the same bits as
+    the whole layer on one stream, on two calls in a row (the second reuses the side
+    stream and the allocator's blocks)."""
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.layer import SparsePRAttention, SparsePRConfig
+
+    shape = synthetic.VideoShape(heads=3, frames=2, height=48, width=64, dim=128, components=40)
+    q, k, v = synthetic.frame_gmm_qkv(shape, seed=4, device=dev, amp=1.5, qk_corr=0.3)
+    base = dict(num_q_centroids=48, num_k_centroids=96, kmeans_iters=4, top_p=0.85, probe_rows=48)
+    one = SparsePRAttention(SparsePRConfig(**base, overlap_streams=False))
+    two = SparsePRAttention(SparsePRConfig(**base, overlap_streams=True))
+    for call in range(2):
+        ref = one(q, k, v)
+        out = two(q, k, v)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"call {call}: outputs differ"
+        assert torch.equal(two.last_route.probe_rows, one.last_route.probe_rows)
+        assert torch.equal(two.last_route.video_dynamic_map, one.last_route.video_dynamic_map)
