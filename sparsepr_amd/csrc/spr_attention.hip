@@ -561,12 +561,14 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         mloc[j] = max_xor32(mx) * scale_log2;
         grow = grow || (mloc[j] > m_run[j] + RESCALE_SLACK);
       }
-      // Rescale lazily: only when some row's maximum grew by more than the slack.
+      // Rescale lazily: only a row whose maximum grew by more than the slack moves its
+      // running maximum, so a row's result does not depend on the other rows of its wave.
       if (__ballot(grow) != 0ull) {
 #pragma unroll
         for (int j = 0; j < QB; ++j) {
-          const float m_new = fmaxf(m_run[j], mloc[j]);
-          const float alpha = __builtin_amdgcn_exp2f(m_run[j] - m_new);
+          const bool up = mloc[j] > m_run[j] + RESCALE_SLACK;
+          const float m_new = up ? mloc[j] : m_run[j];
+          const float alpha = up ? __builtin_amdgcn_exp2f(m_run[j] - m_new) : 1.0f;
           l_run[j] *= alpha;
 #pragma unroll
           for (int b = 0; b < T::DBLK; ++b) {
@@ -890,9 +892,12 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, acc[e]);
     const float mloc = max_xor32(mx) * scale_log2;
-    if (__ballot(mloc > m_run + RESCALE_SLACK) != 0ull) {
-      const float m_new = fmaxf(m_run, mloc);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    const bool up = mloc > m_run + RESCALE_SLACK;
+    if (__ballot(up) != 0ull) {
+      // only the rows whose maximum grew move theirs: a row's result does not depend on
+      // the other rows of its wave
+      const float m_new = up ? mloc : m_run;
+      const float alpha = up ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
       l_run *= alpha;
 #pragma unroll
       for (int b = 0; b < DBLK; ++b) {

@@ -728,6 +728,11 @@ __global__ void probe_scatter_kernel(const TD* __restrict__ dense, const int32_t
     const int c = e - j * d;
     const int32_t r = rows[bh * m + j];
     if (r < 0 || r >= n) continue;
+    // A row listed more than once takes its last entry, as a sequential assignment would;
+    // the other entries' threads write nothing, so the result does not depend on timing.
+    bool later = false;
+    for (int jj = j + 1; jj < m && !later; ++jj) later = rows[bh * m + jj] == r;
+    if (later) continue;
     const float v = load_elem(dense, (bh * m + j) * static_cast<int64_t>(d) + c);
     out[(bh * n + r) * d + c] = spr::f32_to_bf16(v);
   }

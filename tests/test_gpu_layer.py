@@ -123,3 +123,35 @@ def test_side_stream_route_matches_one_stream(dev):
         assert torch.equal(out, ref), f"call {call}: outputs differ"
         assert torch.equal(two.last_route.probe_rows, one.last_route.probe_rows)
         assert torch.equal(two.last_route.video_dynamic_map, one.last_route.video_dynamic_map)
+
+
+def test_repeated_probe_token_gets_identical_dense_rows(dev):
+    """BASELINE config 1's route offers head 1's token 1498 twice as a probe (64 probes over
+    32 q-clusters take several representative rounds, and an exhausted group offers its
+    token again).  Both copies sit in different waves of the dense probe attention (8 key
+    splits of 512 keys).  A row's running maximum moves only on its own growth, so the two
+    copies get the same bits, the exact-probe scatter writes one value, and repeated layer
+    calls give the same output."""
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.layer import SparsePRAttention, SparsePRConfig
+
+    q, k, v = synthetic.frame_gmm_qkv(synthetic.CPU_SMALL, seed=0, amp=1.0, step_std=0.0, noise_std=0.3,
+                                      qk_corr=1.0, device=dev)
+    layer = SparsePRAttention(SparsePRConfig(num_q_centroids=32, num_k_centroids=64, kmeans_iters=10, top_p=0.9,
+                                             probe_rows=64))
+    route, _ = layer.route(q, k, v)
+    rows, _, dense, _ = layer.n8.repair_probes(q, k, v, route)
+    torch.cuda.synchronize()
+    repeated = 0
+    for h in range(rows.shape[0]):
+        pos: dict = {}
+        for j, t in enumerate(rows[h].tolist()):
+            pos.setdefault(t, []).append(j)
+        for t, js in pos.items():
+            for j in js[1:]:
+                repeated += 1
+                assert torch.equal(dense[h, j], dense[h, js[0]]), f"head {h} token {t}: probes {js} differ"
+    assert repeated > 0, "the configuration no longer repeats a probe token; pick another that does"
+    first = layer(q, k, v).clone()
+    for _ in range(4):
+        assert torch.equal(layer(q, k, v), first)

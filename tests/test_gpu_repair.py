@@ -320,3 +320,26 @@ def test_recover_nonfinite_state_gpu(dev, oracle):
             assert np.array_equal(g.cpu().numpy(), want)
     with pytest.raises(RuntimeError, match="five tensors"):
         recover_nonfinite_rrr_state(cur[:4], None)
+
+
+def test_probe_scatter_repeated_row_takes_its_last_entry(dev):
+    """A row listed twice (the representative rounds can offer a token again) is written
+    once, from its last entry, as a sequential assignment would; repeated calls agree."""
+    from sparsepr_amd.kernels.residual_repair import n8_exact_probe_scatter_triton
+
+    bh, n, m, d = 2, 300, 40, 64
+    g = torch.Generator(device="cpu").manual_seed(3)
+    rows = torch.randint(0, n, (bh, m), generator=g)
+    rows[0, 30] = rows[0, 5]
+    rows[1, 39] = rows[1, 0]
+    rows[1, 20] = rows[1, 0]
+    dense = torch.randn((bh, m, d), generator=g)
+    base = torch.randn((bh, n, d), generator=g).to(torch.bfloat16)
+    ref = base.clone()
+    for b in range(bh):
+        for j in range(m):
+            ref[b, rows[b, j]] = dense[b, j].to(torch.bfloat16)
+    for _ in range(5):
+        out = base.to(dev).clone()
+        n8_exact_probe_scatter_triton(out, rows.to(dev), dense.to(dev))
+        assert torch.equal(out.cpu(), ref)
