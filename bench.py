@@ -53,6 +53,9 @@ def parse():
                          "means ~N(0, 1) of the BASELINE description)")
     ap.add_argument("--top-p", type=float, default=None)
     ap.add_argument("--no-repair", action="store_true", help="route + attention only (sweep use)")
+    ap.add_argument("--graph", action="store_true",
+                    help="time the layer captured as a HIP graph (sparsepr_amd.layer.LayerGraph) over the same "
+                         "inputs: `value` is the replay time; stages and roofline come from the eager calls")
     ap.add_argument("--one-stream", action="store_true",
                     help="run the whole layer on one stream (by default Q's k-means and the repair's probe "
                          "part run on a second stream beside K's k-means)")
@@ -549,6 +552,18 @@ def bench_layer(args, name, top_p=None, repair=True, amp=None, with_cpu=False):
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    eager_ms = ms_per_step
+    if args.graph:
+        g = layer.graphed(q, k, v)
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            g.replay()
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
     names = list(marks[0].events)
     stage_ms = {b: round(sum(m.ms(a, b) for m in marks) / len(marks), 3) for a, b in zip(names[:-1], names[1:])}
     attn_ms = sum(m.ms("plan", "attention") for m in marks) / len(marks)
@@ -582,6 +597,8 @@ def bench_layer(args, name, top_p=None, repair=True, amp=None, with_cpu=False):
             "dense_attention_tflop": round(dense_flops(heads, tokens, d) / 1e12, 2),
             "generator": gen,
         },
+        "launch": "hip_graph_replay" if args.graph else "eager",
+        "eager_ms_per_step": round(eager_ms, 3),
         "stages_ms": stage_ms,
         "roofline": {
             "kernel": "attn_pipe_kernel (D=128 block-sparse attention)" if d == 128

@@ -199,6 +199,53 @@ class SparsePRAttention:
 
     __call__ = forward
 
+    def graphed(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, warmup: int = 2) -> "LayerGraph":
+        """This layer captured as a HIP graph for inputs of q's, k's and v's shapes."""
+        return LayerGraph(self, q, k, v, warmup)
+
+
+class LayerGraph:
+    """One SparsePR layer call captured as a HIP graph over input buffers of its own.
+
+    Every kernel of the layer (both streams' Lloyd loops, the map, the permutation, the
+    plan, the attention and the repair) is recorded once; a call copies new Q, K, V into
+    the captured buffers and replays the graph, so the host launches one graph instead of
+    about a hundred kernels.  The result is the same bits as an eager call on the same
+    inputs.  `out` is overwritten by the next replay: clone it to keep it.  Calls on one
+    layer (graphed or eager) stay stream ordered; the repair's last finite state carries
+    over between them as in eager calls."""
+
+    def __init__(self, layer: "SparsePRAttention", q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                 warmup: int = 2):
+        _lib.require_gpu(q, k, v, what="LayerGraph")
+        self.layer = layer
+        self.q, self.k, self.v = q.clone(), k.clone(), v.clone()
+        dev = q.device
+        cur = torch.cuda.current_stream(dev)
+        # warm-up calls make every lazily built buffer and cache before the capture
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                layer(self.q, self.k, self.v)
+        cur.wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = layer(self.q, self.k, self.v)
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.out
+
+    def __call__(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        if q.shape != self.q.shape or k.shape != self.k.shape or v.shape != self.v.shape:
+            raise RuntimeError(f"LayerGraph was captured for Q/K/V {tuple(self.q.shape)}; got {tuple(q.shape)}, "
+                               f"{tuple(k.shape)}, {tuple(v.shape)}")
+        self.q.copy_(q)
+        self.k.copy_(k)
+        self.v.copy_(v)
+        return self.replay()
+
 
 def kept_pair_flops(route: N8V6Route, head_dim: int) -> torch.Tensor:
     """Executed attention flops: 4 * D * sum over kept (a, c) of |Q_a| |K_c| (device scalar)."""

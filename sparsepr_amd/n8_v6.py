@@ -560,7 +560,14 @@ class N8V6Core:
             x_fit, y_fit, rank=min(cfg.repair_rank, count, dim), ridge=cfg.repair_ridge, weights=weights,
             output_basis_backend="skinny", cache_identity=True, fit_backend="dual_cholesky",
             decomposition_backend="triton_top16", basis_source=cfg.repair_basis_source)
-        state, self.repair_recovery_mask, policy = recover_nonfinite_rrr_state(state, self.repair_state_current)
+        previous = self.repair_state_current
+        state, self.repair_recovery_mask, policy = recover_nonfinite_rrr_state(state, previous)
+        # The last finite state lives in buffers of its own, written in place, so that a
+        # call captured in a HIP graph reads, on each replay, what the previous call wrote.
+        if previous is not None and all(a.shape == b.shape and a.dtype == b.dtype for a, b in zip(previous, state)):
+            for a, b in zip(previous, state):
+                a.copy_(b)
+            state = previous
         self.repair_state_current = state
         x_mean, x_scale, y_mean, left, basis = state
         corrected = apply_reduced_rank_residual(base, None, x_mean, x_scale, y_mean, left, basis, cfg.repair_alpha,

@@ -155,3 +155,36 @@ def test_repeated_probe_token_gets_identical_dense_rows(dev):
     first = layer(q, k, v).clone()
     for _ in range(4):
         assert torch.equal(layer(q, k, v), first)
+
+
+@pytest.mark.parametrize("name", ["c1", "d128"])
+def test_graph_replay_matches_eager(dev, name):
+    """The layer captured as a HIP graph gives, on every replay with new inputs, the bits
+    of an eager layer fed the same sequence of inputs; eager work and synchronisations run
+    between the replays, and the second half of the replays run after an eager call of
+    the graphed layer itself."""
+    from sparsepr_amd import synthetic
+    from sparsepr_amd.layer import SparsePRAttention, SparsePRConfig
+
+    if name == "c1":
+        shape = synthetic.CPU_SMALL
+        cfg = SparsePRConfig(num_q_centroids=32, num_k_centroids=64, kmeans_iters=10, top_p=0.9, probe_rows=64)
+        gen = dict(amp=1.0, step_std=0.0, noise_std=0.3, qk_corr=1.0)
+    else:
+        shape = synthetic.VideoShape(heads=3, frames=2, height=48, width=64, dim=128, components=40)
+        cfg = SparsePRConfig(num_q_centroids=48, num_k_centroids=96, kmeans_iters=4, top_p=0.85, probe_rows=48)
+        gen = dict(amp=1.5, qk_corr=0.3)
+    inputs = [synthetic.frame_gmm_qkv(shape, seed=s, device=dev, **gen) for s in range(6)]
+    graphed_layer = SparsePRAttention(cfg)
+    g = graphed_layer.graphed(*inputs[0])
+    eager = SparsePRAttention(cfg)
+    for _ in range(3):  # the graphed layer's warm-up and capture calls
+        eager(*inputs[0])
+    for i, (q, k, v) in enumerate(inputs[1:], start=1):
+        got = g(q, k, v).clone()
+        torch.cuda.synchronize()
+        ref = eager(q, k, v)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"replay {i} differs from the eager call"
+        if i == 3:  # an eager call of the graphed layer between replays
+            assert torch.equal(graphed_layer(q, k, v), eager(q, k, v))
