@@ -600,7 +600,12 @@ __device__ void finalize_mean(double s, int32_t count, int64_t b, int32_t cl, in
       float acc = 0.0f;
       for (int t = 0; t < D; ++t) acc += sq[t];
       const float norm = sqrtf(acc);
-      atomicMax(reinterpret_cast<unsigned int*>(shift_max), __float_as_uint(norm));
+      // The stored maximum only grows, so a shift not above a value read from it cannot be
+      // the maximum: those workgroups skip the atomic.  Every workgroup of a launch
+      // otherwise queued on the one address (about 24,000 at 1000 clusters x 24 heads).
+      unsigned int* const sm = reinterpret_cast<unsigned int*>(shift_max);
+      if (__float_as_uint(norm) > __hip_atomic_load(sm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        atomicMax(sm, __float_as_uint(norm));
     }
     // squared norm of the new centroid for the next assignment, in the order of
     // centroid_sq_kernel (sequential fma over d)
