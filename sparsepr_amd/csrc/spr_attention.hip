@@ -780,14 +780,18 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int qc = pv.qc_by_len[lo];
   const int32_t row0 = pv.q_off[qc] + (tile - pv.tile2_sorted[lo]) * TBM;
   const int32_t row1 = min(row0 + TBM, pv.q_off[qc + 1]);
-  // A tile with at most four live 32-row blocks pairs its waves: wave w (< 4) takes the
+  // A tile with three or four live 32-row blocks pairs its waves: wave w (< 4) takes the
   // first 32-key half of every chunk for block w and wave w + 4 the second half, each with
-  // its own online softmax, merged at the end (split-key helpers).  Otherwise wave w owns
-  // block w and both halves.
+  // its own online softmax, merged at the end (split-key helpers).  A tile with one or two
+  // live blocks ("duo") walks its chunks two at a time: wave w takes block w & 1, half
+  // (w >> 1) & 1 of chunk 2j + (w >> 2) in step j, so each block's keys are shared by four
+  // waves, merged at the end.  Otherwise wave w owns block w and both halves.
   const int nblk = (row1 - row0 + 31) / 32;
-  const bool split = nblk <= NW / 2;
-  const int blk = split ? (wave & (NW / 2 - 1)) : wave;
-  const int only = split ? (wave / (NW / 2)) : 0;  // the half a split wave processes
+  const bool duo = nblk <= 2;
+  const bool split = !duo && nblk <= NW / 2;
+  const int blk = duo ? (wave & 1) : split ? (wave & (NW / 2 - 1)) : wave;
+  const int only = duo ? ((wave >> 1) & 1) : split ? (wave / (NW / 2)) : 0;  // the half a wave processes
+  const int duo_part = wave >> 1;  // duo: 0 .. 3 = half + 2 (chunk parity); part 0 merges
   const bool wave_live = blk < nblk;
   const Seg* segs = pv.segs + static_cast<int64_t>(qc) * kn;
   const int32_t nseg = pv.nseg[qc];
@@ -960,6 +964,37 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     }
   };
 
+  // P = 2^(s - m) of half kbk (acc) and its row sum, then O^T += V^T P^T over that half's
+  // keys: a step with no next S to overlap (duo tiles).
+  auto pv_step = [&](const spr::f32x16& acc, const uint8_t* vt, int kbk) {
+    const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
+    uint32_t pf[2][4];
+    float lsum0 = 0.0f, lsum1 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e], scale_log2, neg_m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e + 1], scale_log2, neg_m));
+      const uint32_t pk = pack2(p0, p1);
+      pf[e / 8][(e % 8) / 2] = pk;
+      if (e % 4 == 0) {
+        lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+      } else {
+        lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+      }
+    }
+    l_run += lsum0 + lsum1;
+#pragma unroll
+    for (int f = 0; f < 2 * DBLK; ++f) {
+      const uint8_t* vrow = vt + 16 * (kbk * 2 + f / DBLK) * DROW + v_lane + (((4 * (f % DBLK) + v_piece) ^ v_x) << 4);
+      const u32x2 r0 = lds_read_tr16(vrow);
+      const u32x2 r1 = lds_read_tr16(vrow + 8 * DROW);
+      const int tt = f / DBLK;
+      const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
+      o_acc[f % DBLK] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(u32x4{r0.x, r0.y, r1.x, r1.y}),
+                                                                spr::as_bf16x8(bfrag), o_acc[f % DBLK], 0, 0, 0);
+    }
+  };
+
   spr::f32x16 s_a, s_b;  // S^T of the current half / of the next half
   // Chunk x in tiles kt/vt; kt1 = K tile of chunk x + 1; kt3/vt3 (the tiles of
   // chunk x - 1) receive chunk x + 3.  The last chunk's second half still
@@ -990,7 +1025,41 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     if (x + 3 < nch) dma(kt3, vt3);
   };
 
-  if (nch > 0) {
+  if (nch > 0 && duo) {
+    // Step j computes chunks 2j and 2j + 1 (buffers (2j) & 3, (2j + 1) & 3) while chunks
+    // 2j + 2 and 2j + 3 land in the other two buffers, whose chunks the step before
+    // finished; key rows are planned four chunks ahead.
+    if constexpr (SEGL) __syncthreads();  // staged segment list visible to wave 0
+    for (int c = 0; c < 4 && c < nch; ++c) plan_chunk(c);
+    __syncthreads();
+    load_rows(0);
+    dma(k_tile0, v_tile0);
+    if (nch > 1) {
+      load_rows(1);
+      dma(k_tile1, v_tile1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (int x = 0; x < nch; x += 2) {
+      __syncthreads();  // chunks x, x + 1 landed for every wave; chunks x - 2, x - 1 are done
+      if (x + 2 < nch) {
+        load_rows(x + 2);
+        dma(k_tiles[(x + 2) & 3], v_tiles[(x + 2) & 3]);
+      }
+      if (x + 3 < nch) {
+        load_rows(x + 3);
+        dma(k_tiles[(x + 3) & 3], v_tiles[(x + 3) & 3]);
+      }
+      const int c = x + (duo_part >> 1);
+      if (wave_live && c < nch) {
+        s_mma(s_a, k_tiles[c & 3], only);
+        row_max(s_a, only, total - c * BN);
+        pv_step(s_a, v_tiles[c & 3], only);
+      }
+      if (x + 4 < nch) plan_chunk(x + 4);
+      if (x + 5 < nch) plan_chunk(x + 5);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's chunks x + 2, x + 3 landed
+    }
+  } else if (nch > 0) {
     if constexpr (SEGL) __syncthreads();  // staged segment list visible to wave 0
     for (int c = 0; c < 4 && c < nch; ++c) plan_chunk(c);
     __syncthreads();
@@ -1039,6 +1108,63 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   }
 
   // ---- epilogue
+  if (duo) {
+    // parts 1 .. 3 of block b hand (m, l, O) to part 0 (wave b) through the K/V tiles:
+    // O of (b, part) in slot 3 b + part - 1 (16 KB each: k_tiles[0..3], v_tiles[0..1]),
+    // m and l in v_tiles[3]; part 0 adds them in part order
+    __syncthreads();  // every wave is past its last chunk
+    auto o_slot = [&](int b, int pt) {
+      const int sl = 3 * b + pt - 1;
+      return reinterpret_cast<float*>(sl < 4 ? k_tiles[sl] : v_tiles[sl - 4]);
+    };
+    float* ml = reinterpret_cast<float*>(v_tiles[3]);
+    if (duo_part != 0 && wave_live) {
+      float* po = o_slot(blk, duo_part) + lane * (DBLK * 16);
+#pragma unroll
+      for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; e += 4) {
+          *reinterpret_cast<spr::f32x4*>(po + b * 16 + e) =
+              spr::f32x4{o_acc[b][e], o_acc[b][e + 1], o_acc[b][e + 2], o_acc[b][e + 3]};
+        }
+      }
+      ml[((3 * blk + duo_part - 1) * 64 + lane) * 2] = m_run;
+      ml[((3 * blk + duo_part - 1) * 64 + lane) * 2 + 1] = l_run;
+    }
+    __syncthreads();
+    if (duo_part != 0) {
+      row_live = false;  // part 0 writes the block
+    } else if (wave_live) {
+      float mm = m_run;
+#pragma unroll
+      for (int pt = 1; pt < 4; ++pt) mm = fmaxf(mm, ml[((3 * blk + pt - 1) * 64 + lane) * 2]);
+      const float a0 = m_run == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(m_run - mm);
+      l_run *= a0;
+#pragma unroll
+      for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o_acc[b][e] *= a0;
+      }
+#pragma unroll
+      for (int pt = 1; pt < 4; ++pt) {
+        const float mi = ml[((3 * blk + pt - 1) * 64 + lane) * 2];
+        const float li = ml[((3 * blk + pt - 1) * 64 + lane) * 2 + 1];
+        const float ai = mi == -__builtin_huge_valf() ? 0.0f : __builtin_amdgcn_exp2f(mi - mm);
+        const float* po = o_slot(blk, pt) + lane * (DBLK * 16);
+#pragma unroll
+        for (int b = 0; b < DBLK; ++b) {
+#pragma unroll
+          for (int e = 0; e < 16; e += 4) {
+            const spr::f32x4 oi = *reinterpret_cast<const spr::f32x4*>(po + b * 16 + e);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o_acc[b][e + j] += oi[j] * ai;
+          }
+        }
+        l_run += li * ai;
+      }
+      m_run = mm;
+    }
+  }
   if (split) {
     // wave w + 4 hands its (m, l, O) for the second halves to wave w through the K/V tiles
     // (every wave is past its last chunk after the barrier)
