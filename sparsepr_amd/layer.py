@@ -107,8 +107,9 @@ class SparsePRAttention:
         and the dense attention of the probe queries), which needs only Q's clusters.
 
         With overlap_streams, Q's Lloyd loop and that probe part run on a side stream
-        while K's Lloyd loop runs on the caller's stream; the caller's stream waits for
-        the side stream before the top-p map, so every later stage sees both."""
+        while K's Lloyd loop runs on the caller's stream; then the top-p map runs on the
+        side stream beside the K/V permutation on the caller's, which waits for it before
+        returning, so every later stage sees both."""
         cfg = self.config
         _lib.require_gpu(q, k, v, what="SparsePRAttention")
         B, H, N, D = q.shape
@@ -153,17 +154,34 @@ class SparsePRAttention:
         if timings is not None:
             timings.mark("kmeans")
         self.last_centroids = (qres.centroids, kres.centroids)
-        dmap = topp_map(qres.centroids, kres.centroids, kres.sizes, cfg.top_p, cfg.min_kc_ratio)
-        if timings is not None:
-            timings.mark("select")
+
+        def select():
+            dmap = topp_map(qres.centroids, kres.centroids, kres.sizes, cfg.top_p, cfg.min_kc_ratio)
+            return dmap, density(dmap, qres.sizes, kres.sizes).mean()  # device scalar: no host sync
+
+        if side is not None:
+            # the map (latency-bound) on the side stream beside the K/V permutation (HBM-bound)
+            side.wait_stream(main)
+            for t in (kres.centroids, kres.sizes):
+                t.record_stream(side)
+            with torch.cuda.stream(side):
+                dmap, dens = select()
+        else:
+            dmap, dens = select()
         if materialize_kv:
             from .kernels.permute import permute_tensor_by_labels_triton
 
             route.k_permuted, _ = permute_tensor_by_labels_triton(k, None, 2, sorted_indices=kres.sorted_idx)
             route.v_permuted, _ = permute_tensor_by_labels_triton(v, None, 2, sorted_indices=kres.sorted_idx)
+        if side is not None:
+            main.wait_stream(side)
+            dmap.record_stream(main)
+            dens.record_stream(main)
+        if timings is not None:
+            timings.mark("select")
         route.k_labels, route.k_cluster_sizes, route.k_sorted_indices = kres.labels, kres.sizes, kres.sorted_idx
         route.video_dynamic_map, route.k_kmeans_iters = dmap, kres.iters
-        route.base_video_density = density(dmap, qres.sizes, kres.sizes).mean()  # device scalar: no host sync
+        route.base_video_density = dens
         return route, qres.sorted_idx, probes
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, timings: LayerTimings | None = None):
