@@ -537,7 +537,7 @@ def bench_layer(args, name, top_p=None, repair=True, amp=None, with_cpu=False):
     cfg = spec["cfg"]
     if top_p is not None:
         cfg = dataclasses.replace(cfg, top_p=top_p)
-    cfg = dataclasses.replace(cfg, repair=repair, overlap_streams=not args.one_stream)
+    cfg = dataclasses.replace(cfg, repair=repair, overlap_streams=False if args.one_stream else None)
     q, k, v = synthetic.frame_gmm_qkv(shape, device="cuda", **gen)
     layer = SparsePRAttention(cfg)
     for _ in range(args.warmup):
