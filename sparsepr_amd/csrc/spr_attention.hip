@@ -72,6 +72,12 @@ __device__ __forceinline__ float max_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// max_xor32(x) * s for s > 0, as max(r0 * s, r1 * s): the products are canonical floats,
+// so the max needs no canonicalising ops on the lane-swapped bits (one VALU op fewer).
+__device__ __forceinline__ float max_xor32_scaled(float x, float s) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]) * s, __uint_as_float(r[1]) * s);
+}
 __device__ __forceinline__ float sum_xor32(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -558,7 +564,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         float mx = -__builtin_huge_valf();
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_acc[j][e]);
-        mloc[j] = max_xor32(mx) * scale_log2;
+        mloc[j] = max_xor32_scaled(mx, scale_log2);
         grow = grow || (mloc[j] > m_run[j] + RESCALE_SLACK);
       }
       // Rescale lazily: only a row whose maximum grew by more than the slack moves its
@@ -824,6 +830,10 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   for (int b = 0; b < DBLK; ++b) o_acc[b] = spr::f32x16{};
   float m_run = -__builtin_huge_valf();
   float l_run = 0.0f;
+  // kept beside m_run and changed only when it moves: the exponent offset (0 while the
+  // row has seen no finite score) and the lazy-rescale threshold
+  float neg_m = 0.0f;
+  float m_thr = -__builtin_huge_valf();
 
   const int nch = (total + BN - 1) / BN;
 
@@ -895,8 +905,8 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     float mx = -__builtin_huge_valf();
 #pragma unroll
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, acc[e]);
-    const float mloc = max_xor32(mx) * scale_log2;
-    const bool up = mloc > m_run + RESCALE_SLACK;
+    const float mloc = max_xor32_scaled(mx, scale_log2);
+    const bool up = mloc > m_thr;
     if (__ballot(up) != 0ull) {
       // only the rows whose maximum grew move theirs: a row's result does not depend on
       // the other rows of its wave
@@ -909,6 +919,8 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
         for (int e = 0; e < 16; ++e) o_acc[b][e] *= alpha;
       }
       m_run = m_new;
+      m_thr = m_new + RESCALE_SLACK;
+      neg_m = (m_new == -__builtin_huge_valf()) ? 0.0f : -m_new;
     }
   };
   // One straight-line block: S^T of the next half into acc_next (K tile kt_n,
@@ -919,7 +931,6 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   // the VALU work side by side.
   auto step = [&](spr::f32x16& acc_next, const uint8_t* kt_n, int kbk_n, const spr::f32x16& acc, const uint8_t* vt,
                   int kbk) {
-    const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
     uint32_t pf[2][4];
     float lsum0 = 0.0f, lsum1 = 0.0f;
     acc_next = spr::f32x16{};
@@ -967,7 +978,6 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   // P = 2^(s - m) of half kbk (acc) and its row sum, then O^T += V^T P^T over that half's
   // keys: a step with no next S to overlap (duo tiles).
   auto pv_step = [&](const spr::f32x16& acc, const uint8_t* vt, int kbk) {
-    const float neg_m = (m_run == -__builtin_huge_valf()) ? 0.0f : -m_run;
     uint32_t pf[2][4];
     float lsum0 = 0.0f, lsum1 = 0.0f;
 #pragma unroll
@@ -1459,6 +1469,9 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_block_sparse_attention_run: bh_q=%lld not a multiple of bh_kv=%lld",
               (long long)bh_q, (long long)bh_kv);
   SPR_REQUIRE(d == 64 || d == 128, "spr_block_sparse_attention_run: head dim %d not supported (64, 128)", d);
+  // the row maximum is taken on unscaled scores and then scaled, which needs scale > 0
+  SPR_REQUIRE(scale > 0.0f && scale < __builtin_huge_valf(),
+              "spr_block_sparse_attention_run: scale must be positive and finite (got %g)", double(scale));
   SPR_REQUIRE(s * d * 2 < (int64_t(1) << 31), "spr_block_sparse_attention_run: a head of K/V exceeds 2 GiB");
   SPR_REQUIRE(bh_q <= 65535, "spr_block_sparse_attention_run: bh_q exceeds 65535");
   if (bh_q == 0 || s == 0) return SPR_OK;
@@ -1568,6 +1581,8 @@ extern "C" int spr_dense_attention_strided(const void* q, const void* k, const v
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_dense_attention: bh_q not a multiple of bh_kv");
   SPR_REQUIRE(d == 64 || d == 128, "spr_dense_attention: head dim %d not supported (64, 128)", d);
   SPR_REQUIRE(out_dtype == 0 || out_dtype == 2, "spr_dense_attention: out_dtype must be 0 or 2");
+  SPR_REQUIRE(scale > 0.0f && scale < __builtin_huge_valf(),
+              "spr_dense_attention: scale must be positive and finite (got %g)", double(scale));
   SPR_REQUIRE(s_kv * d * 2 < (int64_t(1) << 31) && m < (int64_t(1) << 31), "spr_dense_attention: too long");
   SPR_REQUIRE(bh_q <= 65535 && nsplit <= 65535, "spr_dense_attention: grid too large");
   if (bh_q == 0 || m == 0) return SPR_OK;

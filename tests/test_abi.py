@@ -48,3 +48,10 @@ def test_entry_points_validate_arguments_without_a_gpu():
     assert st == 1 and b"head dim 96" in lib.spr_last_error()
     # empty problems are no-ops
     assert lib.spr_permute_rows(None, None, None, 0, 5, 256, None) == 0
+    # the attention takes the row maximum before scaling, so the scale must be positive
+    for scale in (0.0, -0.125, float("inf")):
+        st = lib.spr_block_sparse_attention_run(None, None, None, None, 0, 0, 1, 0, 128, 1, 1, scale, None, None,
+                                                None, None, None)
+        assert st == 1 and b"scale must be positive" in lib.spr_last_error()
+        st = lib.spr_dense_attention(None, None, None, 0, 1, 1, 16, 128, scale, 1, None, 0, None, None, 0, None)
+        assert st == 1 and b"scale must be positive" in lib.spr_last_error()
