@@ -232,9 +232,11 @@ int spr_dense_attention_strided(const void* q, const void* k, const void* v, int
 
 /* ---------------------------------------------------------------- N8 residual repair
  * residual_repair.py:36-118 select_role_equal_probes(_vectorized), group distances:
- *   dist[b, i] = sum_r (features[b, i, r] - centers[b, labels[b, i], r])^2 in fp32,
- *   evaluated in index order (sub, mul, add).  features dtype 0 bf16 / 2 fp32, r in
- *   {64, 128}; centers fp32 [bh, groups, r]; dist fp32 [bh, n]. */
+ *   dist[b, i] = sum_r (features[b, i, r] - centers[b, labels[b, i], r])^2 in fp32, each
+ *   term a separate subtract, multiply and add; the terms are summed sequentially within
+ *   groups of 8 consecutive dimensions, then the group sums by a pairwise tree (zero
+ *   padded to a power of two), a fixed order, so exact ties reproduce.  features dtype
+ *   0 bf16 / 2 fp32; centers fp32 [bh, groups, r]; dist fp32 [bh, n]. */
 int spr_probe_distances(const void* features, int32_t dtype, const int32_t* labels, const float* centers, int64_t bh,
                         int64_t n, int32_t groups, int32_t r, float* dist, hipStream_t stream);
 /* residual_repair.py:121-260 probe choice.  mode 0 = vectorized (one nearest token per
@@ -279,18 +281,8 @@ int spr_cosmos25_qkv_norm_rope_bshd(const void* q, const void* k, const void* v,
                                     int64_t tokens, int32_t heads, int32_t head_dim, float epsilon, void* q_out,
                                     void* k_out, void* v_out, hipStream_t stream);
 
-/* residual_repair.py:263-465 fit_reduced_rank_residual / _fit_reduced_rank_residual_fp32 for
- * every configuration it accepts with m, p, d <= 128 and rank <= 16:
- *   weighted standardisation (:364-384; weights == NULL: plain mean and unbiased std);
- *   primal ridge solve for m >= p (:424-434), dual for m < p (:386-423, both fit_backend
- *   forms); the top-rank eigenvectors of the weighted output gram of the raw residual
- *   (basis_source 0) or of the fitted values (1) (:435-462; the "full" and "skinny" /
- *   eigh / SVD routes span this subspace); left = weight . basis or x_w^T dual basis (:463-464).
- *   x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
- *   [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (basis columns in
- *   ascending eigenvalue order).  1 <= rank <= min(16, d, m).
- *   workspace: spr_rrr_fit_workspace(bh) bytes of device memory.
- * spr_rrr_fit is spr_rrr_fit_ex with basis_source 0. */
+/* residual_repair.py:263-465 fit_reduced_rank_residual with basis_source "raw_residual":
+ * spr_rrr_fit_ex (below) with basis_source 0.  workspace: spr_rrr_fit_workspace(bh) bytes. */
 size_t spr_rrr_fit_workspace(int64_t bh);
 int spr_rrr_fit(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p, int32_t d,
                 int32_t rank, float ridge, float* x_mean, float* x_scale, float* y_mean, float* left, float* basis,
@@ -348,14 +340,38 @@ int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_sorted, const
 int spr_role_metric(const void* x, int32_t dtype, int64_t bh, int64_t n, int32_t d, const int32_t* rows,
                     int32_t count, const int32_t* sizes, int32_t center, float post_scale, float* out,
                     hipStream_t stream);
-/* torch.linalg.eigh for the top eigenpairs (operator_kmeans.py:115-118, residual_repair.py:468-506):
- *   mats fp32 [bh, n, n] symmetric (symmetrize = 1: 0.5 (A + A^T)); vecs fp32 [bh, n, rank] the
- *   eigenvectors of the rank largest eigenvalues in ascending order; vals fp32 [bh, rank]
- *   (nullable) their Rayleigh quotients, ascending.  n <= 128, rank <= min(64, n).
- *   Householder tridiagonalisation, multisection on Sturm counts, inverse iteration, Cholesky-QR. */
+/* residual_repair.py:263-465 fit_reduced_rank_residual / _fit_reduced_rank_residual_fp32 for
+ * every configuration it accepts with m, p, d <= 128 and rank <= 16:
+ *   weighted standardisation (:364-384; weights == NULL: plain mean and unbiased std);
+ *   primal ridge solve for m >= p (:424-434), dual for m < p (:386-423, both fit_backend
+ *   forms); the top-rank eigenvectors of the weighted output gram of the raw residual
+ *   (basis_source 0) or of the fitted values (1) (:435-462; the "full" and "skinny" with
+ *   eigh / SVD routes span this subspace); left = weight . basis or x_w^T dual basis
+ *   (:463-464).
+ *   x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
+ *   [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (basis columns in
+ *   ascending eigenvalue order).  1 <= rank <= min(16, d, m).
+ *   workspace: spr_rrr_fit_workspace(bh) bytes of device memory. */
 int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p, int32_t d,
                    int32_t rank, float ridge, int32_t basis_source, float* x_mean, float* x_scale, float* y_mean,
                    float* left, float* basis, void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The same fit with the "skinny" route and decomposition_backend "triton_top16"
+ * (residual_repair.py:435-451,497-503; the reference's GPU N8 repair, n8_v6.py:1310-1320):
+ * the basis is spr_rrr_top16_basis of the weighted raw residual (basis_source 0) or of the
+ * weighted fitted values (1).  m = 64, d = 128, rank = 16; p <= 128. */
+int spr_rrr_fit_top16(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
+                      int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean, float* x_scale,
+                      float* y_mean, float* left, float* basis, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+/* rrr_eigensolver.py:86-128 top16_right_basis_triton: values fp32 [bh, 64, 128] -> basis fp32
+ * [bh, 128, 16].  A = V V^T; from the QR factor Q0 of the cosine seed C[i][j] =
+ * cos((i + 1/2)(j + 1) pi / 64), power_iters steps Q = Y X / sqrt(s) with Y = A Q and (X, s)
+ * the inv_sqrt_iters-step Newton-Schulz inverse square root of Y^T Y (s its Frobenius norm);
+ * then V^T Q orthonormalised the same way.  An approximation of the top-16 right singular
+ * subspace, not the exact one.  The fit uses the reference's defaults, 8 and 6; both counts
+ * in [1, 4096]. */
+int spr_rrr_top16_basis(const float* values, int64_t bh, int32_t power_iters, int32_t inv_sqrt_iters, float* basis,
+                        hipStream_t stream);
 /* residual_repair.py:468-506 reduced_rank_output_basis: the top-rank right singular basis of
  * a [bh, m, d] fp32 as the eigenvectors of a^T a (ascending), m, d <= 128, rank <= min(16, d).
  * workspace: spr_rrr_fit_workspace(bh) bytes. */
@@ -370,6 +386,11 @@ int spr_rrr_recover(const float* x_mean, const float* x_scale, const float* y_me
                     const float* prev_left, const float* prev_basis, int64_t bh, int32_t p, int32_t d, int32_t rank,
                     float* out_x_mean, float* out_x_scale, float* out_y_mean, float* out_left, float* out_basis,
                     uint8_t* recovered, hipStream_t stream);
+/* torch.linalg.eigh for the top eigenpairs (operator_kmeans.py:115-118, residual_repair.py:468-506):
+ *   mats fp32 [bh, n, n] symmetric (symmetrize = 1: 0.5 (A + A^T)); vecs fp32 [bh, n, rank] the
+ *   eigenvectors of the rank largest eigenvalues in ascending order; vals fp32 [bh, rank]
+ *   (nullable) their Rayleigh quotients, ascending.  n <= 128, rank <= min(64, n).
+ *   Householder tridiagonalisation, multisection on Sturm counts, inverse iteration, Cholesky-QR. */
 int spr_sym_top_eig(const float* mats, int64_t bh, int32_t n, int32_t rank, int32_t symmetrize, float* vecs,
                     float* vals, hipStream_t stream);
 /* operator_kmeans.py:95-151 metric_factor: factor fp32 [bh, n, rank] = top-rank eigenvectors of

@@ -606,15 +606,65 @@ def select_first_token_largest_groups(labels, num_clusters, rows):
     return selected, weights
 
 
+def top16_seed() -> np.ndarray:
+    """The fixed start of the top-16 subspace iteration (rrr_eigensolver.py:71-81): the
+    reduced QR factor Q of C[i][j] = cos((i + 1/2)(j + 1) pi / 64), i < 64, j < 16, as
+    LAPACK's Householder QR (numpy's, torch's) returns it."""
+    rows = np.arange(64, dtype=np.float64)[:, None]
+    cols = np.arange(16, dtype=np.float64)[None, :]
+    q, _ = np.linalg.qr(np.cos((rows + 0.5) * (cols + 1.0) * (math.pi / 64.0)))
+    return q
+
+
+def newton_schulz_inv_sqrt(gram: np.ndarray, iters: int):
+    """The fixed-count Newton-Schulz inverse square root of rrr_eigensolver.py:31-40 and
+    :58-66 over a batch of symmetric matrices: scale = max(||G||_F, 1e-20), N = G / scale,
+    X0 = I, X <- X (3 I - N X X) / 2.  Returns (X, scale); X ~ N^(-1/2) where converged."""
+    r = gram.shape[-1]
+    eye = np.eye(r, dtype=gram.dtype)
+    scale = np.maximum(np.sqrt((gram * gram).sum(axis=(-2, -1), keepdims=True)), 1e-20)
+    normalized = gram / scale
+    inv_sqrt = np.broadcast_to(eye, gram.shape).copy()
+    for _ in range(iters):
+        squared = inv_sqrt @ inv_sqrt
+        inv_sqrt = 0.5 * (inv_sqrt @ (3.0 * eye - normalized @ squared))
+    return inv_sqrt, scale
+
+
+def top16_right_basis(values: np.ndarray, power_iters: int = 8, inv_sqrt_iters: int = 6) -> np.ndarray:
+    """top16_right_basis_triton (rrr_eigensolver.py:86-128) in float64: A = V V^T for
+    V [BH, 64, 128]; from Q0 (top16_seed), `power_iters` steps Y = A Q, Q = Y X / sqrt(s)
+    with (X, s) = newton_schulz_inv_sqrt(Y^T Y); then B = V^T Q and the basis
+    B X / sqrt(s) with (X, s) = newton_schulz_inv_sqrt(B^T B).  Not the exact eigenbasis:
+    its span is that of V^T A^power_iters Q0, and where a Gram is ill-conditioned the
+    six Newton-Schulz steps leave it short of orthonormal, as the reference's is."""
+    v = np.asarray(values, np.float64)
+    if v.shape[1:] != (64, 128):
+        raise RuntimeError(f"N8 top-16 kernel requires [BH,64,128], got {tuple(v.shape)}.")
+    a = v @ np.swapaxes(v, 1, 2)
+    q = np.broadcast_to(top16_seed(), (v.shape[0], 64, 16)).copy()
+    for _ in range(power_iters):
+        y = a @ q
+        inv_sqrt, scale = newton_schulz_inv_sqrt(np.swapaxes(y, 1, 2) @ y, inv_sqrt_iters)
+        q = (y @ inv_sqrt) / np.sqrt(scale)
+    raw = np.swapaxes(v, 1, 2) @ q
+    inv_sqrt, scale = newton_schulz_inv_sqrt(np.swapaxes(raw, 1, 2) @ raw, inv_sqrt_iters)
+    return (raw @ inv_sqrt) / np.sqrt(scale)
+
+
 def fit_reduced_rank_residual(x_fit, y_fit, rank, ridge, weights=None,
-                              basis_source="raw_residual", dtype=np.float64):
+                              basis_source="raw_residual", dtype=np.float64,
+                              output_basis_backend="full", decomposition_backend="eigh"):
     """Weighted ridge reduced-rank regression (residual_repair.py:263-465).
 
     Standardize X with weighted mean/std (scale clamped at 1e-5), center Y.
     M < P: dual solve (Xw Xw^T + ridge I) dual = Yw; weight = Xw^T dual.
     M >= P: primal solve (Xw^T Xw + ridge I) W = Xw^T Yw.
     Basis: top-`rank` eigenvectors of the weighted output gram of the raw
-    (centered) residual ("raw_residual") or of the fitted values.
+    (centered) residual ("raw_residual") or of the fitted values.  With the
+    "skinny" route, M < D and decomposition_backend "triton_top16"
+    (residual_repair.py:435-451,497-503) it is top16_right_basis of the weighted
+    values instead (the reference's GPU N8 repair, n8_v6.py:1310-1320).
     left = W basis.  Returns (x_mean[BH,1,P], x_scale, y_mean[BH,1,D], left[BH,P,r], basis[BH,D,r]).
     """
     x = x_fit.astype(dtype)
@@ -648,9 +698,14 @@ def fit_reduced_rank_residual(x_fit, y_fit, rank, ridge, weights=None,
         weight = np.linalg.solve(gram, rhs)
     fitted = xn @ weight
     values = yc if basis_source == "raw_residual" else fitted
-    out_gram = np.swapaxes(values, 1, 2) @ (values * w)
-    _evals, evecs = np.linalg.eigh(out_gram)
-    basis = evecs[:, :, -rank:]
+    if output_basis_backend == "skinny" and m < y.shape[2] and decomposition_backend == "triton_top16":
+        if rank != 16:
+            raise RuntimeError(f"triton_top16 requires rank=16, got {rank}.")
+        basis = top16_right_basis(values * sw)
+    else:
+        out_gram = np.swapaxes(values, 1, 2) @ (values * w)
+        _evals, evecs = np.linalg.eigh(out_gram)
+        basis = evecs[:, :, -rank:]
     left = weight @ basis
     return x_mean, x_scale, y_mean, left, basis
 

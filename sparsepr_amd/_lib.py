@@ -85,6 +85,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                    _vp, _sz, _vp]),
     "spr_rrr_fit_ex": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp, _vp,
                                       _vp, _vp, _sz, _vp]),
+    "spr_rrr_fit_top16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32, _vp, _vp, _vp,
+                                         _vp, _vp, _vp, _sz, _vp]),
+    "spr_rrr_top16_basis": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _vp]),
     "spr_rrr_output_basis": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _sz, _vp]),
     "spr_rrr_recover": (ctypes.c_int, [_vp] * 10 + [_i64, _i32, _i32, _i32] + [_vp] * 7),
     "spr_sym_top_eig": (ctypes.c_int, [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _vp]),

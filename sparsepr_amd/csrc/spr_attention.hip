@@ -150,6 +150,20 @@ __device__ inline bool plan_matches(const int32_t* base, int64_t bh_kv, int32_t 
   return hd[0] == PLAN_MAGIC && hd[1] == static_cast<int32_t>(bh_kv) && hd[2] == qn && hd[3] == kn && hd[4] == s;
 }
 
+// A plan built for other sizes: the whole (1-D) grid writes NaN over the output [bh_q, s, d]
+// bf16 and the LSE [bh_q, s] (when given), each workgroup a strided share, so the caller sees
+// the mismatch instead of stale memory.  d is 64 or 128, so the output is whole 16-byte pieces.
+__device__ inline void fill_nan_output(uint16_t* out, float* lse, int64_t bh_q, int32_t s, int32_t d) {
+  const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t pieces = bh_q * s * (d / 8);
+  const spr::u32x4 nan8 = {0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u};
+  for (int64_t i = first; i < pieces; i += step) reinterpret_cast<spr::u32x4*>(out)[i] = nan8;
+  if (lse != nullptr) {
+    for (int64_t i = first; i < bh_q * s; i += step) lse[i] = __builtin_nanf("");
+  }
+}
+
 __host__ __device__ inline PlanView plan_at(int32_t* base, int64_t h, int32_t qn, int32_t kn) {
   int32_t* p = base + h * plan_words(qn, kn);
   PlanView v;
@@ -332,8 +346,11 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     const int64_t logical = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     bhq = logical / tiles_per_head;
     const int32_t t = static_cast<int32_t>(logical - bhq * tiles_per_head);
+    if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) {
+      fill_nan_output(out, lse, bh_q, s_q, D);
+      return;
+    }
     if (bhq >= bh_q) return;
-    if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) return;
     PlanView pv = plan_at(const_cast<int32_t*>(plan), bhq / group, qn, kn);
     if (t >= pv.tile_off[qn]) return;
     int lo = 0, hi = qn;  // largest i with tile_off[i] <= t
@@ -771,8 +788,11 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int64_t logical = static_cast<int64_t>(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   const int64_t slot = logical / tiles_per_head;
   const int32_t tile = static_cast<int32_t>(logical - slot * tiles_per_head);
+  if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) {
+    fill_nan_output(out, lse, bh_q, s_q, D);
+    return;
+  }
   if (slot >= bh_q) return;
-  if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) return;
   const int64_t bhkv = head_order_at(const_cast<int32_t*>(plan), bh_q / group, qn, kn)[slot / group];
   const int64_t bhq = bhkv * group + slot % group;
   PlanView pv = plan_at(const_cast<int32_t*>(plan), bhkv, qn, kn);

@@ -69,15 +69,15 @@ __global__ __launch_bounds__(256) void permute_rows_kernel(const V* __restrict__
 template <int MODE>
 int launch_permute(const void* src, const void* suffix, const int32_t* idx, void* dst, int64_t bh,
                    int64_t src_rows, int64_t dst_rows, int64_t prefix_rows, int64_t row_bytes,
-                   hipStream_t stream, const char* name, int64_t src_head_bytes = 0) {
-  // src_head_bytes: bytes from one head's source rows to the next (0: packed, src_rows rows)
+                   hipStream_t stream, const char* name, int64_t src_head_bytes = -1) {
+  // src_head_bytes: bytes from one head's source rows to the next (-1: packed, src_rows rows)
   SPR_REQUIRE(bh >= 0 && src_rows >= 0 && dst_rows >= 0, "%s: negative size", name);
   const int64_t walk_rows = (MODE == MODE_SCATTER) ? src_rows : dst_rows;
   if (bh == 0 || walk_rows == 0 || row_bytes == 0) return SPR_OK;
   SPR_REQUIRE(src && idx && dst, "%s: null pointer", name);
   SPR_REQUIRE(bh <= 65535, "%s: bh=%lld exceeds 65535", name, (long long)bh);
   SPR_REQUIRE(row_bytes % 2 == 0, "%s: row bytes %lld not a multiple of 2", name, (long long)row_bytes);
-  if (src_head_bytes == 0) src_head_bytes = src_rows * row_bytes;
+  if (src_head_bytes == -1) src_head_bytes = src_rows * row_bytes;
   SPR_REQUIRE(src_head_bytes >= src_rows * row_bytes, "%s: source head stride %lld below %lld rows of %lld bytes",
               name, (long long)src_head_bytes, (long long)src_rows, (long long)row_bytes);
   auto aligned = [&](uintptr_t a) {
@@ -132,9 +132,13 @@ extern "C" int spr_inverse_permute_rows(const void* src, const int32_t* idx, voi
 }
 
 // spr_inverse_permute_rows with head b's source rows starting src_head_bytes after head
-// b - 1's (a slice of the rows of a larger packed tensor, read in place).
+// b - 1's (a slice of the rows of a larger packed tensor, read in place); the stride is
+// explicit, at least rows * row_bytes (no value stands for "packed").
 extern "C" int spr_inverse_permute_rows_strided(const void* src, int64_t src_head_bytes, const int32_t* idx, void* dst,
                                                 int64_t bh, int64_t rows, int64_t row_bytes, hipStream_t stream) {
+  SPR_REQUIRE(src_head_bytes >= 0 && src_head_bytes >= rows * row_bytes,
+              "spr_inverse_permute_rows_strided: source head stride %lld below %lld rows of %lld bytes",
+              (long long)src_head_bytes, (long long)rows, (long long)row_bytes);
   return launch_permute<MODE_SCATTER>(src, nullptr, idx, dst, bh, rows, rows, 0, row_bytes, stream,
                                       "spr_inverse_permute_rows_strided", src_head_bytes);
 }

@@ -1144,26 +1144,197 @@ __global__ __launch_bounds__(256) void rrr_recover_kernel(RrrState cur, RrrState
   if (threadIdx.x == 0 && recovered != nullptr) recovered[h] = static_cast<uint8_t>(bad);
 }
 
+// ---- the fixed-count top-16 subspace basis of the N8 repair (top16_right_basis_triton,
+// src/sparsepr/kernels/triton/rrr_eigensolver.py:14-128), for V [64][128] per head:
+//   A = V V^T; Q0 = the reduced QR factor of C[i][j] = cos((i + 1/2)(j + 1) pi / 64);
+//   8 times: Y = A Q, (X, s) = ns(Y^T Y), Q = Y X / sqrt(s);
+//   B = V^T Q, (X, s) = ns(B^T B), basis = B X / sqrt(s);
+// with ns(G): s = max(||G||_F, 1e-20), N = G / s, X0 = I, six times X <- X (3 I - N X X) / 2.
+// The columns of C are DCT-II vectors, orthogonal with norm sqrt(32), so Householder QR
+// (LAPACK's convention, which torch.linalg.qr follows) gives Q0 = C diag(sign) / sqrt(32) with
+// the signs of R's diagonal below.  The result is not the exact eigenbasis, and where a Gram
+// is ill-conditioned the six Newton-Schulz steps leave it short of orthonormal, as the
+// reference's is.  One 256-thread workgroup per head, everything in LDS, fp32 with sequential
+// sums.  V comes from the raw residual ((y - y_mean) sqrt(w)) when vals is null, else from
+// vals (row stride vals_ld, head stride vals_hs).
+constexpr int T16_M = 64, T16_D = 128, T16_R = 16;
+constexpr uint32_t T16_SEED_NEGATIVE = 0x8E1Fu;  // R[j][j] < 0 for j = 0-4, 9-11, 15
+constexpr int T16_POWER_ITERS = 8, T16_NS_ITERS = 6;  // the reference's defaults
+
+// Newton-Schulz on the 16 x 16 Gram G held one entry per thread (thread t: entry (t / 16,
+// t % 16)): leaves X ~ (G / s)^(-1/2) in x and returns sqrt(s).  x and tmp swap roles as
+// the iterations go (every thread swaps alike); nrm and ubuf are scratch [16][17].
+__device__ __forceinline__ float t16_newton_schulz(float g, int ns_iters, float (*nrm)[17], float (*&x)[17],
+                                                   float (*&tmp)[17], float (*ubuf)[17], float* red) {
+  const int t = threadIdx.x, a = t >> 4, b = t & 15, lane = t & 63, wv = t >> 6;
+  const float sq = wave_sum(g * g);
+  if (lane == 0) red[wv] = sq;
+  __syncthreads();
+  const float scale = fmaxf(sqrtf(((red[0] + red[1]) + red[2]) + red[3]), 1e-20f);
+  nrm[a][b] = g / scale;
+  x[a][b] = a == b ? 1.0f : 0.0f;
+  __syncthreads();
+  for (int it = 0; it < ns_iters; ++it) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < T16_R; ++k) s = fmaf(x[a][k], x[k][b], s);
+    tmp[a][b] = s;
+    __syncthreads();
+    float u = 0.0f;
+#pragma unroll
+    for (int k = 0; k < T16_R; ++k) u = fmaf(nrm[a][k], tmp[k][b], u);
+    ubuf[a][b] = (a == b ? 3.0f : 0.0f) - u;
+    __syncthreads();
+    float v = 0.0f;
+#pragma unroll
+    for (int k = 0; k < T16_R; ++k) v = fmaf(x[a][k], ubuf[k][b], v);
+    tmp[a][b] = 0.5f * v;
+    __syncthreads();
+    float(*swap)[17] = x;
+    x = tmp;
+    tmp = swap;
+  }
+  return sqrtf(scale);
+}
+
+__global__ __launch_bounds__(256) void rrr_top16_kernel(const float* __restrict__ y, const float* __restrict__ w,
+                                                        const float* __restrict__ y_mean,
+                                                        const float* __restrict__ vals, int64_t vals_hs,
+                                                        int32_t vals_ld, int32_t power_iters, int32_t ns_iters,
+                                                        float* __restrict__ basis) {
+  __shared__ float vs[T16_M][T16_D + 1];
+  __shared__ float as[T16_M * (T16_M + 1)];  // A [64][65]; after the iterations B [128][17]
+  __shared__ float qs[T16_M][T16_R + 1];
+  __shared__ float ys[T16_M][T16_R + 1];
+  __shared__ float sm[4][T16_R][T16_R + 1];
+  __shared__ float red[4];
+  const int t = threadIdx.x;
+  const int64_t h = blockIdx.x;
+  if (vals == nullptr) {
+    const float* yh = y + h * T16_M * T16_D;
+    const float* ym = y_mean + h * T16_D;
+    for (int e = t; e < T16_M * T16_D; e += 256) {
+      const int r = e >> 7, c = e & 127;
+      vs[r][c] = (yh[e] - ym[c]) * (w != nullptr ? sqrtf(w[h * T16_M + r]) : 1.0f);
+    }
+  } else {
+    const float* vh = vals + h * vals_hs;
+    for (int e = t; e < T16_M * T16_D; e += 256) {
+      const int r = e >> 7, c = e & 127;
+      vs[r][c] = vh[static_cast<int64_t>(r) * vals_ld + c];
+    }
+  }
+  {  // Q0
+    const int i = t >> 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = (t & 3) + 4 * u;
+      const double c = cos((i + 0.5) * (j + 1.0) * (3.14159265358979323846 / 64.0)) / sqrt(32.0);
+      qs[i][j] = static_cast<float>((T16_SEED_NEGATIVE >> j) & 1u ? -c : c);
+    }
+  }
+  __syncthreads();
+  {  // A = V V^T: thread t owns rows t / 16 + 16 u and columns t % 16 + 16 v
+    const int bi = t >> 4, bj = t & 15;
+    float acc[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[u][v] = 0.0f;
+    for (int c = 0; c < T16_D; ++c) {
+      float ri[4], rj[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        ri[u] = vs[bi + 16 * u][c];
+        rj[u] = vs[bj + 16 * u][c];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[u][v] = fmaf(ri[u], rj[v], acc[u][v]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) as[(bi + 16 * u) * (T16_M + 1) + bj + 16 * v] = acc[u][v];
+  }
+  __syncthreads();
+  float(*nrm)[17] = sm[0];
+  float(*xm)[17] = sm[1];
+  float(*tmp)[17] = sm[2];
+  float(*ubuf)[17] = sm[3];
+  const int a = t >> 4, b = t & 15;
+  const int ri = t >> 2, rc = t & 3;  // 64 x 16 products: row ri, columns rc + 4 u
+  for (int it = 0; it < power_iters; ++it) {
+    float yv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < T16_M; ++k) {
+      const float av = as[ri * (T16_M + 1) + k];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) yv[u] = fmaf(av, qs[k][rc + 4 * u], yv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ys[ri][rc + 4 * u] = yv[u];
+    __syncthreads();
+    float g = 0.0f;
+    for (int r = 0; r < T16_M; ++r) g = fmaf(ys[r][a], ys[r][b], g);
+    const float root = t16_newton_schulz(g, ns_iters, nrm, xm, tmp, ubuf, red);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float s = 0.0f;
+#pragma unroll
+      for (int k = 0; k < T16_R; ++k) s = fmaf(ys[ri][k], xm[k][rc + 4 * u], s);
+      qs[ri][rc + 4 * u] = s / root;
+    }
+    __syncthreads();
+  }
+  // B = V^T Q [128][16] into as (row stride 17): thread t owns row t / 2, columns 8 (t % 2) + v
+  const int bc = t >> 1, bo = 8 * (t & 1);
+  {
+    float bv[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) bv[v] = 0.0f;
+    for (int r = 0; r < T16_M; ++r) {
+      const float vv = vs[r][bc];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) bv[v] = fmaf(vv, qs[r][bo + v], bv[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < 8; ++v) as[bc * (T16_R + 1) + bo + v] = bv[v];
+  }
+  __syncthreads();
+  float g = 0.0f;
+  for (int r = 0; r < T16_D; ++r) g = fmaf(as[r * (T16_R + 1) + a], as[r * (T16_R + 1) + b], g);
+  const float root = t16_newton_schulz(g, ns_iters, nrm, xm, tmp, ubuf, red);
+  float* out = basis + h * T16_D * T16_R;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < T16_R; ++k) s = fmaf(as[bc * (T16_R + 1) + k], xm[k][bo + v], s);
+    out[bc * T16_R + bo + v] = s / root;
+  }
+}
+
 }  // namespace
 
 extern "C" size_t spr_rrr_fit_workspace(int64_t bh) {
   return bh <= 0 ? 0 : static_cast<size_t>(bh) * RRR_SLOTS * RRR_MAT * sizeof(float);
 }
 
-// x [bh, m, p], y [bh, m, d], weights [bh, m] fp32 (nullable: unit weights, unbiased std);
-// outputs x_mean [bh, p], x_scale [bh, p], y_mean [bh, d], left [bh, p, rank], basis
-// [bh, d, rank] (fp32).  basis_source 0: raw residual, 1: fitted values.  m, p, d <= 128,
-// 1 <= rank <= min(16, d, m).
-extern "C" int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
-                              int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean,
-                              float* x_scale, float* y_mean, float* left, float* basis, void* workspace,
-                              size_t workspace_bytes, hipStream_t stream) {
+namespace {
+// The fit's launches; top16: the basis from rrr_top16_kernel instead of the exact eigenvectors.
+int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p, int32_t d,
+                   int32_t rank, float ridge, int32_t basis_source, bool top16, float* x_mean, float* x_scale,
+                   float* y_mean, float* left, float* basis, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && m >= 1 && p >= 1 && d >= 1, "spr_rrr_fit: bad size");
   SPR_REQUIRE(m <= RRR_MAX && p <= RRR_MAX && d <= RRR_MAX, "spr_rrr_fit: m, p, d must be at most %d", RRR_MAX);
   SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d && rank <= m,
               "spr_rrr_fit: rank %d outside [1, min(16, d, m)]", rank);
   SPR_REQUIRE(ridge >= 0.0f, "spr_rrr_fit: ridge must be non-negative");
   SPR_REQUIRE(basis_source == 0 || basis_source == 1, "spr_rrr_fit: basis_source must be 0 (raw) or 1 (fitted)");
+  SPR_REQUIRE(!top16 || (m == T16_M && d == T16_D && rank == T16_R),
+              "spr_rrr_fit_top16: needs m = 64, d = 128 and rank 16 (got m=%d, d=%d, rank=%d)", m, d, rank);
   SPR_REQUIRE(bh <= 65535, "spr_rrr_fit: too many heads");
   if (bh == 0) return SPR_OK;
   SPR_REQUIRE(x && y && x_mean && x_scale && y_mean && left && basis && workspace, "spr_rrr_fit: null pointer");
@@ -1178,7 +1349,25 @@ extern "C" int spr_rrr_fit_ex(const float* x, const float* y, const float* weigh
   const int32_t gkind = dual ? GRAM_DUAL : GRAM_PRIMAL;
   rrr_stats_kernel<<<dim3(nb), 256, 0, stream>>>(x, y, weights, m, p, d, x_mean, x_scale, y_mean);
   SPR_LAUNCHED("rrr_stats_kernel");
-  if (basis_source == 0) {
+  if (top16) {
+    rrr_gram_kernel<<<dim3(nb, 10), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, nullptr,
+                                                      0, 0, gkind, gkind, ws);
+    SPR_LAUNCHED("rrr_gram_kernel");
+    rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 1, basis);
+    SPR_LAUNCHED("rrr_factor_kernel");
+    if (basis_source == 0) {
+      rrr_top16_kernel<<<dim3(nb), 256, 0, stream>>>(y, weights, y_mean, nullptr, 0, 0, T16_POWER_ITERS,
+                                                     T16_NS_ITERS, basis);
+    } else {
+      rrr_fitted_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean,
+                                                              ws);
+      SPR_LAUNCHED("rrr_fitted_kernel");
+      rrr_top16_kernel<<<dim3(nb), 256, 0, stream>>>(nullptr, nullptr, nullptr, ws + 2 * RRR_MAT,
+                                                     int64_t(RRR_SLOTS) * RRR_MAT, RRR_MAX, T16_POWER_ITERS,
+                                                     T16_NS_ITERS, basis);
+    }
+    SPR_LAUNCHED("rrr_top16_kernel");
+  } else if (basis_source == 0) {
     rrr_gram_kernel<<<dim3(nb, 20), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, nullptr,
                                                       0, 0, gkind, GRAM_RESIDUAL, ws);
     SPR_LAUNCHED("rrr_gram_kernel");
@@ -1203,6 +1392,44 @@ extern "C" int spr_rrr_fit_ex(const float* x, const float* y, const float* weigh
   rrr_solve_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, ridge, x_mean, x_scale,
                                                          y_mean, ws, basis, left);
   SPR_LAUNCHED("rrr_solve_kernel");
+  return SPR_OK;
+}
+}  // namespace
+
+// x [bh, m, p], y [bh, m, d], weights [bh, m] fp32 (nullable: unit weights, unbiased std);
+// outputs x_mean [bh, p], x_scale [bh, p], y_mean [bh, d], left [bh, p, rank], basis
+// [bh, d, rank] (fp32).  basis_source 0: raw residual, 1: fitted values.  m, p, d <= 128,
+// 1 <= rank <= min(16, d, m).
+extern "C" int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
+                              int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean,
+                              float* x_scale, float* y_mean, float* left, float* basis, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
+  return rrr_fit_launch(x, y, weights, bh, m, p, d, rank, ridge, basis_source, false, x_mean, x_scale, y_mean, left,
+                        basis, workspace, workspace_bytes, stream);
+}
+
+// spr_rrr_fit_ex with the N8 repair's top-16 subspace basis (rrr_top16_kernel) in place of
+// the exact eigenvectors: m = 64, d = 128, rank = 16.
+extern "C" int spr_rrr_fit_top16(const float* x, const float* y, const float* weights, int64_t bh, int32_t m,
+                                 int32_t p, int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean,
+                                 float* x_scale, float* y_mean, float* left, float* basis, void* workspace,
+                                 size_t workspace_bytes, hipStream_t stream) {
+  return rrr_fit_launch(x, y, weights, bh, m, p, d, rank, ridge, basis_source, true, x_mean, x_scale, y_mean, left,
+                        basis, workspace, workspace_bytes, stream);
+}
+
+// The top-16 subspace basis alone: values [bh, 64, 128] fp32 -> basis [bh, 128, 16] fp32.
+extern "C" int spr_rrr_top16_basis(const float* values, int64_t bh, int32_t power_iters, int32_t inv_sqrt_iters,
+                                   float* basis, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && bh <= 65535, "spr_rrr_top16_basis: bad head count");
+  SPR_REQUIRE(power_iters > 0 && inv_sqrt_iters > 0 && power_iters <= 4096 && inv_sqrt_iters <= 4096,
+              "spr_rrr_top16_basis: iteration counts must be in [1, 4096]");
+  if (bh == 0) return SPR_OK;
+  SPR_REQUIRE(values && basis, "spr_rrr_top16_basis: null pointer");
+  rrr_top16_kernel<<<dim3(static_cast<uint32_t>(bh)), 256, 0, stream>>>(nullptr, nullptr, nullptr, values,
+                                                                       int64_t(T16_M) * T16_D, T16_D, power_iters,
+                                                                       inv_sqrt_iters, basis);
+  SPR_LAUNCHED("rrr_top16_kernel");
   return SPR_OK;
 }
 

@@ -31,6 +31,7 @@ def plan_block_sparse(block_mask_map: torch.Tensor, block_row_sz: torch.Tensor, 
     plan = _lib.workspace(nbytes, dev)
     _lib.call("spr_block_sparse_attention_plan", _lib.ptr(m), _lib.ptr(qs), _lib.ptr(ks), bh_kv, seq_len, qn, kn,
               _lib.ptr(plan), plan.numel(), _lib.stream(dev))
+    plan.spr_plan_sizes = (int(bh_kv), int(qn), int(kn), int(seq_len))
     return plan
 
 
@@ -55,6 +56,7 @@ def plan_block_sparse_from_schedule(selected_ids: torch.Tensor, selected_counts:
     plan = _lib.workspace(nbytes, dev)
     _lib.call("spr_block_sparse_attention_plan_schedule", _lib.ptr(ids), _lib.ptr(counts), _lib.ptr(qs), _lib.ptr(ks),
               bh_kv, seq_len, qn, kn, _lib.ptr(plan), plan.numel(), _lib.stream(dev))
+    plan.spr_plan_sizes = (int(bh_kv), int(qn), int(kn), int(seq_len))
     return plan
 
 
@@ -79,6 +81,12 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
     _, qn, kn = block_mask_map.shape
     if plan is None:
         plan = plan_block_sparse(block_mask_map.to(dev), block_row_sz, block_col_sz, s)
+    # a plan from plan_block_sparse* carries the sizes it was built for (the kernels check
+    # them too, and write NaN over the output when they differ)
+    built = getattr(plan, "spr_plan_sizes", None)
+    if built is not None and built != (int(bh_kv), int(qn), int(kn), int(s)):
+        raise RuntimeError(f"block-sparse attention: the plan was built for (bh_kv, qn, kn, seq_len) = {built}, "
+                           f"not {(int(bh_kv), int(qn), int(kn), int(s))}")
     need = int(_lib.query("spr_block_sparse_attention_workspace", bh_kv, qn, kn))
     if plan.numel() < need or plan.device != dev:
         raise RuntimeError(f"block-sparse attention: the plan ({plan.numel()} bytes on {plan.device}) was not built "

@@ -133,10 +133,12 @@ def apply_inverse_permutation_triton(
     bh = B * H
     si = sorted_indices.to(torch.int32).reshape(bh, S).contiguous()
     t = permuted_tensor
-    # rows packed within each head and one stride between heads (a slice of the rows of a
-    # longer tensor, e.g. the video part of an attention output): read in place
-    if t.stride(3) == 1 and t.stride(2) == D and (H == 1 or t.stride(0) == H * t.stride(1)):
-        head = t.stride(1) if H > 1 else (t.stride(0) if B > 1 else S * D)
+    # rows packed within each head and one stride of at least S rows between heads (a slice
+    # of the rows of a longer tensor, e.g. the video part of an attention output): read in
+    # place.  Anything else (an expanded tensor's zero head stride included) is copied first.
+    head = t.stride(1) if H > 1 else (t.stride(0) if B > 1 else S * D)
+    if (t.stride(3) == 1 and t.stride(2) == D and (H == 1 or t.stride(0) == H * t.stride(1))
+            and head >= S * D):
         out = torch.empty((bh, S, D), dtype=t.dtype, device=dev)
         _lib.call("spr_inverse_permute_rows_strided", _lib.ptr(t), head * t.element_size(), _lib.ptr(si),
                   _lib.ptr(out), bh, S, D * t.element_size(), _lib.stream(dev))

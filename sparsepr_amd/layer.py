@@ -122,7 +122,6 @@ class SparsePRAttention:
         bh = B * H
         qf = q.reshape(bh, N, D).contiguous()
         kf = k.reshape(bh, N, D).contiguous()
-        vf = v.reshape(bh, N, D).contiguous()
         route = N8V6Route(
             q_labels=None, k_labels=None, q_cluster_sizes=None, k_cluster_sizes=None, video_dynamic_map=None,
             q_role_features=qf, k_permuted=None, v_permuted=None, k_sorted_indices=None, base_video_density=None,

@@ -556,10 +556,16 @@ class N8V6Core:
             self._fit_target_buffer = torch.empty(shape, device=base.device, dtype=torch.float32)
         x_fit, dense_probe_f, y_fit = n8_prepare_output_repair_fit_triton(
             base, dense_probe, rows, self._fit_feature_buffer, self._dense_probe_buffer, self._fit_target_buffer)
+        # The reference's GPU route (n8_v6.py:1310-1320): with fewer probes than D the basis is
+        # the top-16 subspace iteration, whose kernel takes exactly 64 probes at D = 128 (the
+        # N8 default) and rank 16.  Other counts below D, which the reference's kernel refuses,
+        # take the exact eigenbasis here.
+        rank = min(cfg.repair_rank, count, dim)
+        backend = "triton_top16" if (count, dim, rank) == (64, 128, 16) else "eigh"
         state = fit_reduced_rank_residual(
-            x_fit, y_fit, rank=min(cfg.repair_rank, count, dim), ridge=cfg.repair_ridge, weights=weights,
+            x_fit, y_fit, rank=rank, ridge=cfg.repair_ridge, weights=weights,
             output_basis_backend="skinny", cache_identity=True, fit_backend="dual_cholesky",
-            decomposition_backend="triton_top16", basis_source=cfg.repair_basis_source)
+            decomposition_backend=backend, basis_source=cfg.repair_basis_source)
         previous = self.repair_state_current
         state, self.repair_recovery_mask, policy = recover_nonfinite_rrr_state(state, previous)
         # The last finite state lives in buffers of its own, written in place, so that a

@@ -125,9 +125,11 @@ def fit_reduced_rank_residual(x_fit, y_fit, *, rank, ridge, weights=None, output
     M < P solves in dual form, M >= P in primal form (both fit_backend values: they
     differ in the factorisation the reference calls, not in the solution).  The basis is
     the top-r eigenvectors of the weighted output gram of the raw residual or of the
-    fitted values; the "skinny" row-gram route and every decomposition_backend compute
-    the same subspace (the reference's "triton_top16" approximates it by power
-    iteration), so they share this exact solver.  cache_identity has no effect here."""
+    fitted values; the "full" route and the "skinny" row-gram route with the eigh or SVD
+    backends compute that subspace.  The "skinny" route with M < D and "triton_top16"
+    (the reference's GPU N8 repair) takes the fixed-count subspace iteration of
+    top16_right_basis_triton instead, as the reference does (:435-451, :497-503): an
+    approximation that is not the exact eigenbasis.  cache_identity has no effect here."""
     if x_fit.ndim != 3 or y_fit.ndim != 3 or x_fit.shape[:2] != y_fit.shape[:2]:
         raise RuntimeError(
             "RRR expects X=[BH,M,P] and Y=[BH,M,D] with matching BH/M, got "
@@ -148,17 +150,22 @@ def fit_reduced_rank_residual(x_fit, y_fit, *, rank, ridge, weights=None, output
         )
     if basis_source not in {"fitted_residual", "raw_residual"}:
         raise RuntimeError(f"RRR basis_source must be 'fitted_residual' or 'raw_residual', got {basis_source!r}.")
-    if (decomposition_backend == "triton_top16" and output_basis_backend == "skinny"
-            and x_fit.shape[1] < y_fit.shape[2] and rank != 16):
-        raise RuntimeError(f"triton_top16 requires rank=16, got {rank}.")
+    top16 = (output_basis_backend == "skinny" and x_fit.shape[1] < y_fit.shape[2]
+             and decomposition_backend == "triton_top16")
+    if top16:
+        if rank != 16:
+            raise RuntimeError(f"triton_top16 requires rank=16, got {rank}.")
+        if (int(x_fit.shape[1]), int(y_fit.shape[2])) != (64, 128):
+            raise RuntimeError(
+                f"N8 top-16 kernel requires [BH,64,128], got {(int(x_fit.shape[0]), int(x_fit.shape[1]), int(y_fit.shape[2]))}.")
     return _rrr_fit_hip(x_fit, y_fit, weights, int(rank), float(ridge),
-                        1 if basis_source == "fitted_residual" else 0)
+                        1 if basis_source == "fitted_residual" else 0, top16)
 
 
-def _rrr_fit_hip(x, y, weights, rank, ridge, basis_source=0):
+def _rrr_fit_hip(x, y, weights, rank, ridge, basis_source=0, top16=False):
     """The fit in 4 launches (raw residual basis) or 7 (fitted values), fp32 whatever
-    the input dtype.  Eigenvector signs (as eigh's) are arbitrary; left . basis^T does
-    not depend on them."""
+    the input dtype; with top16 the basis comes from the top-16 subspace iteration.
+    Eigenvector signs (as eigh's) are arbitrary; left . basis^T does not depend on them."""
     dev = _lib.require_gpu(x, y, weights, what="reduced-rank residual fit")
     bh, m, p = (int(v) for v in x.shape)
     d = int(y.shape[2])
@@ -179,22 +186,28 @@ def _rrr_fit_hip(x, y, weights, rank, ridge, basis_source=0):
     basis = torch.empty((bh, d, rank), **f32)
     ws_bytes = int(_lib.query("spr_rrr_fit_workspace", bh))
     ws = _lib.workspace(ws_bytes, dev)
-    _lib.call("spr_rrr_fit_ex", _lib.ptr(x), _lib.ptr(y), _lib.ptr(w), bh, m, p, d, rank, ridge, int(basis_source),
+    _lib.call("spr_rrr_fit_top16" if top16 else "spr_rrr_fit_ex", _lib.ptr(x), _lib.ptr(y), _lib.ptr(w), bh, m, p, d,
+              rank, ridge, int(basis_source),
               _lib.ptr(x_mean), _lib.ptr(x_scale), _lib.ptr(y_mean), _lib.ptr(left), _lib.ptr(basis), _lib.ptr(ws),
               ws_bytes, _lib.stream(dev))
     return x_mean, x_scale, y_mean, left, basis
 
 
 def reduced_rank_output_basis(weighted_fitted, *, rank, backend):
-    """Top-r right singular basis of [BH, M, D] (reference :468-506) on spr_rrr_output_basis:
-    the eigenvectors of A^T A, orthonormal, ascending.  Every backend names this subspace."""
+    """Top-r right singular basis of [BH, M, D] (reference :468-506).  "eigh" and the SVD
+    backends: spr_rrr_output_basis, the eigenvectors of A^T A, orthonormal, ascending;
+    "triton_top16": top16_right_basis_triton (rank 16, [BH, 64, 128])."""
     if weighted_fitted.ndim != 3:
         raise RuntimeError(f"weighted_fitted must have shape [BH,M,D], got {tuple(weighted_fitted.shape)}.")
     if rank <= 0 or rank > min(weighted_fitted.shape[1:]):
         raise RuntimeError(f"Invalid rank={rank} for weighted_fitted={tuple(weighted_fitted.shape)}.")
-    if backend == "triton_top16" and rank != 16:
-        raise RuntimeError(f"triton_top16 requires rank=16, got {rank}.")
-    if backend not in {"eigh", "triton_top16", "svd_gesvdj", "svd_gesvd"}:
+    if backend == "triton_top16":
+        if rank != 16:
+            raise RuntimeError(f"triton_top16 requires rank=16, got {rank}.")
+        from .kernels.rrr_eigensolver import top16_right_basis_triton
+
+        return top16_right_basis_triton(weighted_fitted)
+    if backend not in {"eigh", "svd_gesvdj", "svd_gesvd"}:
         raise RuntimeError(f"Unknown exact decomposition backend {backend!r}.")
     dev = _lib.require_gpu(weighted_fitted, what="reduced-rank output basis")
     bh, m, d = (int(v) for v in weighted_fitted.shape)

@@ -276,7 +276,8 @@ def test_q_index_fuses_the_query_permutation(dev, oracle):
 def test_run_rejects_a_plan_for_other_sizes(dev, oracle):
     """A plan buffer too small for the run's sizes is refused on the host (status 3); a
     plan built for another sequence length is seen by the kernels' header check, which
-    leaves the output unwritten."""
+    writes NaN over the whole output and LSE (D = 128 and D = 64 kernels); the Python
+    wrapper refuses such a plan before any launch."""
     from sparsepr_amd import _lib
     from sparsepr_amd.kernels.attention import plan_block_sparse
 
@@ -295,12 +296,24 @@ def test_run_rejects_a_plan_for_other_sizes(dev, oracle):
     # built for s = 500, run over the first 400 rows: the header does not match
     q4, k4, v4 = (t[:, :400].contiguous() for t in (qd, kd, vd))
     out4 = torch.full_like(q4, 7.0)
+    lse4 = torch.zeros((2, 400), device=dev)
     st = lib.spr_block_sparse_attention_run(q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), plan.data_ptr(),
                                             plan.numel(), 2, 2, 400, 128, 4, 8, 0.1, None, None, out4.data_ptr(),
-                                            None, stream)
+                                            lse4.data_ptr(), stream)
     torch.cuda.synchronize()
     assert st == 0
-    assert bool((out4 == 7.0).all())
+    assert bool(torch.isnan(out4).all()) and bool(torch.isnan(lse4).all())
+    q64 = q4[:, :, :64].contiguous()
+    out64 = torch.full_like(q64, 7.0)
+    st = lib.spr_block_sparse_attention_run(q64.data_ptr(), q64.data_ptr(), q64.data_ptr(), plan.data_ptr(),
+                                            plan.numel(), 2, 2, 400, 64, 4, 8, 0.1, None, None, out64.data_ptr(),
+                                            None, stream)
+    torch.cuda.synchronize()
+    assert st == 0 and bool(torch.isnan(out64).all())
+    from sparsepr_amd.kernels.attention import block_sparse_attention
+
+    with pytest.raises(RuntimeError, match="plan was built for"):
+        block_sparse_attention(q4, k4, v4, to_dev(m[0], dev), to_dev(qs[0], dev), to_dev(ks[0], dev), plan=plan)
     # the matching run writes every row
     st = lib.spr_block_sparse_attention_run(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), plan.data_ptr(),
                                             plan.numel(), 2, 2, 500, 128, 4, 8, 0.1, None, None, out.data_ptr(),

@@ -281,13 +281,22 @@ def test_n8_hunyuan_composition_default_config(dev, oracle):
         dense_ref = oracle.dense_attention(qh[rr][None], kh[None], vh[None])[0]
         dense = gr[rr][None]
         assert np.abs(dense[0] - dense_ref).max() <= 2e-2
-        # the repair of the GPU base fitted to those probes by the float64 oracle (the fit's
-        # raw-residual basis turns with one-ulp changes of the targets when its eigengap at
-        # the rank cut is small, so both fits see the same targets)
+        # the repair of the GPU base fitted to those probes by the float64 oracle on the
+        # reference GPU's route (64 probes < D: the "skinny" top-16 subspace basis,
+        # n8_v6.py:1310-1320); both fits see the same targets
         xfit = bh_np[rr][None]
-        state = oracle.fit_reduced_rank_residual(xfit, dense - xfit, cfg.repair_rank, cfg.repair_ridge, rw[None])
+        state = oracle.fit_reduced_rank_residual(xfit, dense - xfit, cfg.repair_rank, cfg.repair_ridge, rw[None],
+                                                 output_basis_backend="skinny", decomposition_backend="triton_top16")
         ref_out = oracle.repair_apply(bh_np[None], *state, cfg.repair_alpha, 0.0)[0]
         ref_out[rr] = dense[0]
+        # how far the exact eigenbasis (the reference's CPU route) would put the output
+        exact = oracle.fit_reduced_rank_residual(xfit, dense - xfit, cfg.repair_rank, cfg.repair_ridge, rw[None])
+        exact_out = oracle.repair_apply(bh_np[None], *exact, cfg.repair_alpha, 0.0)[0]
+        exact_out[rr] = dense[0]
+        ce, ct = exact_out - bh_np, ref_out - bh_np
+        cos = (ce * ct).sum(1) / np.maximum(np.linalg.norm(ce, axis=1) * np.linalg.norm(ct, axis=1), 1e-30)
+        print(f"head {h}: top-16 vs exact basis: output max-abs {np.abs(exact_out - ref_out).max():.4g}, "
+              f"correction max-abs {np.abs(ct).max():.4g}, min row cosine of the corrections {cos.min():.4f}")
         # bf16 output: one ulp of the value (a rounding flip between the fp32 and float64
         # corrections) plus 1e-2 for the fp32 fit
         err = np.abs(gr - ref_out)

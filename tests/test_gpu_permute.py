@@ -127,3 +127,25 @@ def test_inverse_permutation_of_a_row_slice_in_place(dev):
     assert torch.equal(got, ref)
     back, _ = permute_tensor_by_labels_triton(got, None, 2, sorted_indices=idx)
     assert torch.equal(back, view)
+
+
+def test_inverse_permutation_of_an_expanded_tensor(dev):
+    """An expanded tensor (zero head strides: every head views one [S, D] block) takes the
+    copying path, not the in-place one: each head is un-permuted from the shared block.  The
+    strided entry point refuses a head stride below S rows."""
+    from sparsepr_amd import _lib
+    from sparsepr_amd.kernels.permute import apply_inverse_permutation_triton
+
+    g = torch.Generator(device=dev).manual_seed(12)
+    B, H, S, D = 2, 3, 500, 128
+    block = torch.randn((1, 1, S, D), device=dev, generator=g).to(torch.bfloat16)
+    view = block.expand(B, H, S, D)
+    assert view.stride(0) == 0 and view.stride(1) == 0
+    idx = torch.argsort(torch.rand((B * H, S), device=dev, generator=g), dim=-1).to(torch.int32)
+    got = apply_inverse_permutation_triton(view, idx, dim=2)
+    ref = apply_inverse_permutation_triton(view.contiguous(), idx, dim=2)
+    assert torch.equal(got, ref)
+    out = torch.empty((B * H, S, D), device=dev, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="head stride"):
+        _lib.call("spr_inverse_permute_rows_strided", _lib.ptr(block), 0, _lib.ptr(idx), _lib.ptr(out), B * H, S,
+                  D * 2, _lib.stream(dev))

@@ -173,7 +173,7 @@ def test_rrr_fit_matches_float64(dev, oracle, m, p, basis_source, weighted):
     got = fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=16, ridge=0.1,
                                     weights=None if w is None else to_dev(w, dev),
                                     output_basis_backend="skinny", fit_backend="dual_cholesky",
-                                    decomposition_backend="triton_top16", basis_source=basis_source)
+                                    decomposition_backend="eigh", basis_source=basis_source)
     ref = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=basis_source)
     for g, r in zip(got[:3], ref[:3]):
         assert np.allclose(g.cpu().numpy(), r, rtol=1e-4, atol=1e-5)
@@ -181,6 +181,73 @@ def test_rrr_fit_matches_float64(dev, oracle, m, p, basis_source, weighted):
     gl = (got[3] @ got[4].transpose(1, 2)).cpu().numpy()
     rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
     assert np.abs(gl - rl).max() <= 2e-3 * np.abs(rl).max()
+
+
+def _top16_values(rng, bh, decay):
+    """[bh, 64, 128] with singular values decaying as exp(-decay i): at decay 0.1-0.3 the
+    Grams of the subspace iteration are ill-conditioned and its basis is far from the
+    exact one (and from orthonormal)."""
+    u = rng.standard_normal((bh, 64, 64)) * np.exp(-decay * np.arange(64))
+    return (u @ rng.standard_normal((bh, 64, 128)) / 20).astype(np.float32)
+
+
+@pytest.mark.parametrize("decay", [0.0, 0.1, 0.3])
+def test_top16_basis_matches_oracle(dev, oracle, decay):
+    """top16_right_basis_triton (rrr_eigensolver.py:86-128) against the float64 restatement,
+    column for column (the same seed, signs included) within 1e-4, at the default iteration
+    counts and at 3 / 2; the Gram of the result (far from I at the larger decays) within
+    1e-4 too."""
+    from sparsepr_amd.kernels.rrr_eigensolver import top16_right_basis_triton
+
+    rng = np.random.default_rng(int(decay * 100) + 3)
+    v = _top16_values(rng, 6, decay)
+    for kw in ({}, {"power_iters": 3, "inv_sqrt_iters": 2}):
+        got = top16_right_basis_triton(to_dev(v, dev), **kw).cpu().numpy().astype(np.float64)
+        ref = oracle.top16_right_basis(v, **kw)
+        assert got.shape == (6, 128, 16)
+        assert np.abs(got - ref).max() <= 1e-4
+        assert np.abs(np.swapaxes(got, 1, 2) @ got - np.swapaxes(ref, 1, 2) @ ref).max() <= 1e-4
+    with pytest.raises(RuntimeError, match=r"requires \[BH,64,128\]"):
+        top16_right_basis_triton(torch.zeros((2, 32, 128), device=dev))
+
+
+@pytest.mark.parametrize("p", [128, 48])
+@pytest.mark.parametrize("basis_source", ["raw_residual", "fitted_residual"])
+@pytest.mark.parametrize("weighted", [True, False])
+def test_rrr_fit_top16_matches_oracle(dev, oracle, p, basis_source, weighted):
+    """The reference GPU N8 repair's fit (64 probes, D = 128, rank 16, "skinny",
+    "dual_cholesky", "triton_top16"; n8_v6.py:1310-1320) against the float64 oracle on the
+    same route, dual (P = 128) and primal (P = 48): statistics to 1e-4, the basis column for
+    column to 1e-3, left . basis^T to 2e-3 of its maximum.  The exact-eigh fit of the same
+    inputs differs by far more, so the route is what is being checked."""
+    from sparsepr_amd.residual_repair import fit_reduced_rank_residual
+
+    rng = np.random.default_rng(p + 2 * weighted + (basis_source == "raw_residual"))
+    x = rng.standard_normal((4, 64, p)).astype(np.float32)
+    y = (x @ rng.standard_normal((4, p, 128)).astype(np.float32) * 0.02
+         + _top16_values(rng, 4, 0.1)).astype(np.float32)
+    w = rng.uniform(0.5, 2.0, (4, 64)).astype(np.float32) if weighted else None
+    got = fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=16, ridge=0.1,
+                                    weights=None if w is None else to_dev(w, dev),
+                                    output_basis_backend="skinny", cache_identity=True, fit_backend="dual_cholesky",
+                                    decomposition_backend="triton_top16", basis_source=basis_source)
+    ref = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=basis_source,
+                                           output_basis_backend="skinny", decomposition_backend="triton_top16")
+    exact = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=basis_source)
+    for g, r in zip(got[:3], ref[:3]):
+        assert np.allclose(g.cpu().numpy(), r, rtol=1e-4, atol=1e-5)
+    assert np.abs(got[4].cpu().numpy() - ref[4]).max() <= 1e-3
+    gl = (got[3] @ got[4].transpose(1, 2)).cpu().numpy()
+    rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
+    el = exact[3] @ np.swapaxes(exact[4], 1, 2)
+    assert np.abs(gl - rl).max() <= 2e-3 * np.abs(rl).max()
+    assert np.abs(el - rl).max() > 5e-2 * np.abs(rl).max()
+    with pytest.raises(RuntimeError, match="rank=16"):
+        fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=8, ridge=0.1, output_basis_backend="skinny",
+                                  decomposition_backend="triton_top16")
+    with pytest.raises(RuntimeError, match=r"requires \[BH,64,128\]"):
+        fit_reduced_rank_residual(to_dev(x[:, :40], dev), to_dev(y[:, :40], dev), rank=16, ridge=0.1,
+                                  output_basis_backend="skinny", decomposition_backend="triton_top16")
 
 
 def test_rrr_fit_unweighted_single_row_is_recovered(dev):

@@ -535,6 +535,198 @@ def test_repair_norm_cap_and_scatter(oracle):
     assert (out[2, 29] == dense[2, 0]).all() and (out[0, 1] == capped[0, 1]).all()
 
 
+@pytest.mark.parametrize("ridge", [0.0, 0.3])
+def test_repair_apply_at_fit_rows_satisfies_normal_equations(oracle, ridge):
+    """A full-rank fit (rank = D, M > P = D) applied at its own fit rows: the residual
+    y - (apply(x) - x) satisfies the weighted ridge normal equations, sum w r = 0 and
+    sum w xn^T r = ridge W, with xn standardised here by numpy's weighted average and W the
+    map the state applies.  A wrong standardisation or a dropped y_mean in the apply fails."""
+    rng = np.random.default_rng(41)
+    bh, m, d = 2, 40, 6
+    x = (3.0 * rng.standard_normal((bh, m, d)) + rng.uniform(-2, 2, (bh, 1, d))).astype(np.float32)
+    y = (x @ rng.standard_normal((bh, d, d)) * 0.2 + 0.3 * rng.standard_normal((bh, m, d))
+         + np.array([1.5, -2.0, 0.5, 3.0, -1.0, 0.25])).astype(np.float32)
+    w = rng.uniform(0.5, 2.0, (bh, m)).astype(np.float32)
+    state = oracle.fit_reduced_rank_residual(x, y, d, ridge, w)
+    pred = oracle.repair_apply(x, *state, 1.0, 0.0) - x.astype(np.float64)
+    r = y.astype(np.float64) - pred
+    for h in range(bh):
+        wh = w[h].astype(np.float64)
+        mu = np.average(x[h].astype(np.float64), axis=0, weights=wh)
+        sd = np.sqrt(np.average((x[h] - mu) ** 2, axis=0, weights=wh))
+        xn = (x[h] - mu) / sd
+        assert np.abs(wh @ r[h]).max() <= 1e-9 * np.abs(y[h]).sum()
+        W = state[3][h] @ state[4][h].T
+        assert np.allclose((xn * wh[:, None]).T @ r[h], ridge * W, atol=1e-8)
+    # the apply at other rows uses the same affine map (a check of linearity in base)
+    b2 = rng.standard_normal((bh, 7, d))
+    a0 = oracle.repair_apply(np.zeros((bh, 1, d)), *state, 1.0, 0.0)
+    a1 = oracle.repair_apply(b2, *state, 1.0, 0.0)
+    assert np.allclose(a1 - b2 - a0, (b2 / state[1]) @ state[3] @ np.swapaxes(state[4], 1, 2), atol=1e-10)
+
+
+def test_repair_apply_hand_worked(oracle):
+    """Two tokens worked out by hand (dyadic numbers, exact), with x_scale != 1, y_mean != 0
+    and alpha != 1; then the norm cap on a token whose correction is (6, 8) against a base
+    of norm 5."""
+    base = np.array([[[1.0, 2.0], [3.0, 5.0]]])
+    x_mean = np.array([[[1.0, 1.0]]])
+    x_scale = np.array([[[2.0, 4.0]]])
+    y_mean = np.array([[[0.5, -1.0]]])
+    left = np.array([[[1.0], [2.0]]])
+    basis = np.array([[[3.0], [-1.0]]])
+    out = oracle.repair_apply(base, x_mean, x_scale, y_mean, left, basis, 0.5, 0.0)
+    # token 0: z = (0, 1/4), z.left = 1/2, corr = (3/2, -1/2) + (1/2, -1) = (2, -3/2)
+    # token 1: z = (1, 1),   z.left = 3,   corr = (9, -3) + (1/2, -1)   = (19/2, -4)
+    assert (out == np.array([[[2.0, 1.25], [7.75, 3.0]]])).all()
+    # base (3, 4): z = ((3-1)/2, (4-0)/4) = (1, 1); z.left = 3; corr = (6, 6) + (0, 2) = (6, 8);
+    # cap 0.25 * |base| / |corr| = 0.125 -> (0.75, 1); alpha 2 -> (4.5, 6)
+    capped = oracle.repair_apply(np.array([[[3.0, 4.0]]]), np.array([[[1.0, 0.0]]]), x_scale,
+                                 np.array([[[0.0, 2.0]]]), left, np.array([[[2.0], [2.0]]]), 2.0, 0.25)
+    assert np.allclose(capped, [[[4.5, 6.0]]], rtol=0, atol=1e-12)
+
+
+@pytest.mark.parametrize("m", [40, 8])
+def test_rrr_fitted_basis_by_lstsq(oracle, m):
+    """basis_source="fitted_residual": the fitted values from numpy's least squares on the
+    ridge-augmented system [x_w; sqrt(ridge) I] W = [y_w; 0] (not the oracle's solve); the
+    basis spans the top-rank right singular vectors of sqrt(w) * fitted (numpy SVD)."""
+    rng = np.random.default_rng(42)
+    x, y, w = _rrr_inputs(rng, m=m, p=12, d=10)
+    rank, ridge = 3, 0.2
+    x_mean, x_scale, y_mean, left, basis = oracle.fit_reduced_rank_residual(
+        x, y, rank, ridge, w, basis_source="fitted_residual")
+    raw = oracle.fit_reduced_rank_residual(x, y, rank, ridge, w, basis_source="raw_residual")[4]
+    for h in range(x.shape[0]):
+        wh = w[h].astype(np.float64)
+        mu = np.average(x[h].astype(np.float64), axis=0, weights=wh)
+        xn = (x[h] - mu) / np.sqrt(np.average((x[h] - mu) ** 2, axis=0, weights=wh))
+        ym = np.average(y[h].astype(np.float64), axis=0, weights=wh)
+        sw = np.sqrt(wh)[:, None]
+        a = np.vstack((xn * sw, math.sqrt(ridge) * np.eye(x.shape[2])))
+        rhs = np.vstack(((y[h] - ym) * sw, np.zeros((x.shape[2], y.shape[2]))))
+        W = np.linalg.lstsq(a, rhs, rcond=None)[0]
+        _, _, vt = np.linalg.svd(sw * (xn @ W))
+        want = vt[:rank].T @ vt[:rank]
+        assert np.allclose(basis[h] @ basis[h].T, want, atol=1e-8)
+        assert not np.allclose(raw[h] @ raw[h].T, want, atol=1e-3)  # the two sources differ here
+        assert np.allclose(left[h], W @ basis[h], atol=1e-8)
+
+
+def test_rrr_unweighted_uses_unbiased_std(oracle):
+    """Without weights the scale is the unbiased (ddof 1) standard deviation, clamped at
+    1e-5, and the means are plain means; at M = 3 ddof changes the scale by sqrt(3/2)."""
+    rng = np.random.default_rng(43)
+    x = rng.standard_normal((2, 3, 5)).astype(np.float32)
+    x[1, :, 4] = 7.0  # a constant feature: std 0 -> the clamp
+    y = rng.standard_normal((2, 3, 4)).astype(np.float32)
+    x_mean, x_scale, y_mean, _, _ = oracle.fit_reduced_rank_residual(x, y, 2, 0.1, None)
+    assert np.allclose(x_mean[:, 0], x.astype(np.float64).mean(1))
+    assert np.allclose(y_mean[:, 0], y.astype(np.float64).mean(1))
+    want = np.maximum(np.std(x.astype(np.float64), axis=1, ddof=1), 1e-5)
+    assert np.allclose(x_scale[:, 0], want, rtol=1e-12)
+    assert x_scale[1, 0, 4] == 1e-5
+
+
+# --------------------------------------------------------------------------- top-16 subspace
+
+TOP16_SEED_SIGNS = [-1, -1, -1, -1, -1, 1, 1, 1, 1, -1, -1, -1, 1, 1, 1, -1]
+
+
+def test_top16_seed_is_signed_dct(oracle):
+    """The seed's columns are DCT-II vectors (orthogonal, norm sqrt(32)), so LAPACK's
+    Householder QR returns them scaled by 1/sqrt(32) and the signs of R's diagonal; numpy
+    and torch (the reference calls torch.linalg.qr) agree on those signs."""
+    import torch
+
+    q = oracle.top16_seed()
+    i = np.arange(64)[:, None]
+    j = np.arange(16)[None, :]
+    c = np.cos((i + 0.5) * (j + 1) * math.pi / 64)
+    assert np.allclose(c.T @ c, 32 * np.eye(16), atol=1e-12)
+    assert np.allclose(q, c / math.sqrt(32) * np.array(TOP16_SEED_SIGNS), atol=1e-14)
+    ct = torch.cos((torch.arange(64.0)[:, None] + 0.5) * (torch.arange(16.0)[None, :] + 1.0) * (math.pi / 64.0))
+    _, r = torch.linalg.qr(ct, mode="reduced")
+    assert torch.sign(torch.diagonal(r)).tolist() == TOP16_SEED_SIGNS
+
+
+def test_newton_schulz_matches_spectral_route(oracle):
+    """The matrix Newton-Schulz iteration equals the scalar recurrence x <- x (3 - v x^2) / 2
+    (x0 = 1) applied to the eigenvalues v of G / ||G||_F (numpy eigh): a transposed product,
+    a wrong constant or a different normalisation fails; converged, X = (G / s)^(-1/2)."""
+    rng = np.random.default_rng(44)
+    a = rng.standard_normal((3, 30, 16)) * np.exp(-0.3 * np.arange(16))
+    g = np.swapaxes(a, 1, 2) @ a
+    for iters in (1, 2, 6):
+        x, s = oracle.newton_schulz_inv_sqrt(g, iters)
+        lam, e = np.linalg.eigh(g)
+        v = lam / np.linalg.norm(g, axis=(1, 2))[:, None]
+        f = np.ones_like(v)
+        for _ in range(iters):
+            f = 0.5 * f * (3.0 - v * f * f)
+        want = e @ (f[:, :, None] * np.swapaxes(e, 1, 2))
+        assert np.allclose(x, want, atol=1e-9 * np.abs(want).max())
+        assert np.allclose(s[:, 0, 0], np.sqrt((g ** 2).sum((1, 2))))
+    # a well-conditioned Gram converges in a dozen steps (the uncoupled iteration lets
+    # rounding errors grow again over many more steps once converged)
+    a = rng.standard_normal((3, 200, 16))
+    g = np.swapaxes(a, 1, 2) @ a
+    x, s = oracle.newton_schulz_inv_sqrt(g, 12)
+    assert np.allclose(x @ (g / s) @ x, np.eye(16), atol=1e-10)
+
+
+def test_top16_basis_span_and_convergence(oracle):
+    """The basis spans V^T (V V^T)^k Q0 (a QR of that product, another route), for k = 8 and
+    k = 3; with many iterations on a spectrum with a gap at 16 it converges to the exact top-16
+    right singular subspace (numpy SVD), orthonormal."""
+    rng = np.random.default_rng(45)
+    u, _ = np.linalg.qr(rng.standard_normal((2, 64, 64)))
+    vt, _ = np.linalg.qr(rng.standard_normal((2, 128, 64)))
+    s = np.concatenate((np.linspace(3.0, 2.0, 16), np.linspace(1.0, 0.1, 48)))
+    v = (u * s) @ np.swapaxes(vt, 1, 2)
+    q0 = oracle.top16_seed()
+    for k in (8, 3):
+        # the default is the reference's 8 power iterations
+        b = oracle.top16_right_basis(v) if k == 8 else oracle.top16_right_basis(v, power_iters=k)
+        a = v @ np.swapaxes(v, 1, 2)
+        direct = np.swapaxes(v, 1, 2) @ np.linalg.matrix_power(a, k) @ q0
+        qd, _ = np.linalg.qr(direct)
+        qb, _ = np.linalg.qr(b)
+        assert np.allclose(qb @ np.swapaxes(qb, 1, 2), qd @ np.swapaxes(qd, 1, 2), atol=1e-9)
+    b = oracle.top16_right_basis(v, power_iters=60, inv_sqrt_iters=12)
+    exact = vt[:, :, :16]
+    assert np.allclose(b @ np.swapaxes(b, 1, 2), exact @ np.swapaxes(exact, 1, 2), atol=1e-8)
+    assert np.allclose(np.swapaxes(b, 1, 2) @ b, np.eye(16), atol=1e-8)
+
+
+def test_top16_fit_is_the_skinny_triton_route(oracle):
+    """The fit with output_basis_backend "skinny", M < D and "triton_top16" uses the top-16
+    basis of the weighted values (raw residual or weighted fitted values), and left = W basis;
+    other routes keep the exact eigenbasis; rank other than 16 is refused as the reference does."""
+    rng = np.random.default_rng(46)
+    x = rng.standard_normal((2, 64, 128)).astype(np.float32)
+    y = (rng.standard_normal((2, 64, 64)) * np.exp(-0.1 * np.arange(64))) @ rng.standard_normal((2, 64, 128)) / 20
+    w = rng.uniform(0.5, 2.0, (2, 64)).astype(np.float32)
+    for source in ("raw_residual", "fitted_residual"):
+        st = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=source, output_basis_backend="skinny",
+                                              decomposition_backend="triton_top16")
+        ex = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=source, output_basis_backend="skinny")
+        sw = np.sqrt(w.astype(np.float64))[:, :, None]
+        yc = (y - st[2]) * sw
+        xw = (x - st[0]) / st[1] * sw
+        dual = np.linalg.solve(xw @ np.swapaxes(xw, 1, 2) + 0.1 * np.eye(64), yc)
+        vals = yc if source == "raw_residual" else yc - 0.1 * dual  # sqrt(w) fitted = y_w - ridge dual
+        assert np.allclose(st[4], oracle.top16_right_basis(vals), atol=1e-10)
+        assert np.allclose(st[3], np.swapaxes(xw, 1, 2) @ dual @ st[4], atol=1e-8)
+        assert not np.allclose(st[4] @ np.swapaxes(st[4], 1, 2), ex[4] @ np.swapaxes(ex[4], 1, 2), atol=1e-3)
+        full =oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=source,
+                                                decomposition_backend="triton_top16")
+        assert np.allclose(full[4] @ np.swapaxes(full[4], 1, 2), ex[4] @ np.swapaxes(ex[4], 1, 2), atol=1e-8)
+    with pytest.raises(RuntimeError, match="rank=16"):
+        oracle.fit_reduced_rank_residual(x, y, 8, 0.1, w, output_basis_backend="skinny",
+                                         decomposition_backend="triton_top16")
+
+
 # --------------------------------------------------------------------------- whole layer
 
 def test_layer_runs_and_probe_rows_are_exact(oracle):
