@@ -191,25 +191,32 @@ __global__ __launch_bounds__(ASSIGN_THREADS, 2) void kmeans_assign_bf16_kernel(
 // operand rounding of tl.dot on fp32 inputs (input_precision "tf32", Triton's default).
 __device__ __forceinline__ uint32_t tf32_rna_bits(float v) { return (__float_as_uint(v) + 0x1000u) & 0xFFFFE000u; }
 
-// A TF32 value t as two bf16 halves with hi + lo = t exactly: hi keeps the sign,
-// exponent and top 7 mantissa bits (t's upper 16 bits), lo = t - hi has at most 3
-// significant bits, so it is a bf16 value too.  Products of halves are exact in fp32,
-// and hi*hi + hi*lo + lo*hi + lo*lo is the exact product of two TF32 values.
-__device__ __forceinline__ void tf32_split(float v, uint32_t& hi16, uint32_t& lo16) {
-  const uint32_t t = tf32_rna_bits(v);
-  const float hi = __uint_as_float(t & 0xFFFF0000u);
-  const float lo = __uint_as_float(t) - hi;  // exact
-  hi16 = t >> 16;
-  lo16 = __float_as_uint(lo) >> 16;  // exact: lo has <= 3 significant bits
+// fp16 images of TF32 values.  v~ = tf32(v) has 11 significant bits, as many as fp16
+// carries, so v~ 2^e is exact in fp16 wherever it lies in fp16's normal range.  The scale
+// 2^e puts the largest magnitude of a point row (or of a centroid tile) in [2^14, 2^15);
+// entries below 2^-29 of it become fp16 subnormals and keep only their leading bits, a
+// change far below the fp32 rounding of the distance they enter.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ int tf32_scale_exp(float amax) {
+  int e = 0;
+  if (amax > 0.0f && amax < __builtin_huge_valf()) e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e
+  return 15 - e;
 }
+__device__ __forceinline__ uint32_t tf32_f16_bits(float v, int se) {
+  const float t = __builtin_ldexpf(__uint_as_float(tf32_rna_bits(v)), se);
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(t));
+}
+__device__ __forceinline__ float tf32_abs(float v) { return fabsf(__uint_as_float(tf32_rna_bits(v))); }
 
 // labels = argmin_k max((x_sq + c_sq) - 2 x.c, 0) for fp32 x and centroids, with the
 // dot product of their TF32 roundings (exact products, fp32 accumulation): the
 // flash-kmeans assign on fp32 inputs (assign_euclid_triton.py:897, kmeans_utils.py:829).
 // x_sq (when not given) is the fp32 sum of the fp32 squares of x itself
 // (kmeans_utils.py:812-814).  The layout follows kmeans_assign_bf16_kernel: 256 points
-// per workgroup, 64-centroid LDS tiles (hi and lo halves), v_mfma_f32_32x32x16_bf16,
-// four products per 16-dim step.
+// per workgroup, 64-centroid LDS tiles, v_mfma_f32_32x32x16_f16 on the scaled fp16 images
+// (one product per 16-dim step: every product of two TF32 values is exact in the fp32
+// accumulator), and the accumulated dot taken back by the two exact power-of-two scales
+// inside the distance's fused multiply-add.
 template <int D>
 __global__ __launch_bounds__(ASSIGN_THREADS, D > 64 ? 1 : 2) void kmeans_assign_tf32_kernel(
     const float* __restrict__ x, const float* __restrict__ c, const float* __restrict__ c_sq,
@@ -217,14 +224,15 @@ __global__ __launch_bounds__(ASSIGN_THREADS, D > 64 ? 1 : 2) void kmeans_assign_
     int32_t* __restrict__ labels) {
   static_assert(D % 16 == 0 && D <= 128, "D must be a multiple of 16, at most 128");
   constexpr int KSTEPS = D / 16;
-  constexpr int ROW_BYTES = D * 2 + 16;     // padded bf16 LDS row
+  constexpr int ROW_BYTES = D * 2 + 16;     // padded fp16 LDS row
   constexpr int QUADS = CCHUNK * D / 4;     // 4-float pieces per centroid tile
   constexpr int QUADS_PER_THREAD = QUADS / ASSIGN_THREADS;
   static_assert(QUADS % ASSIGN_THREADS == 0, "tile pieces must divide evenly");
 
-  __shared__ __attribute__((aligned(16))) uint8_t tile_hi[2][CCHUNK * ROW_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t tile_lo[2][CCHUNK * ROW_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t tile[2][CCHUNK * ROW_BYTES];
   __shared__ float tile_csq[2][CCHUNK];
+  __shared__ int tile_exp[2];
+  __shared__ float tile_max[ASSIGN_THREADS / 64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -236,29 +244,41 @@ __global__ __launch_bounds__(ASSIGN_THREADS, D > 64 ? 1 : 2) void kmeans_assign_
   const float* cb = c + static_cast<int64_t>(b) * k * D;
   const float* csqb = c_sq + static_cast<int64_t>(b) * k;
 
-  // ---- points of this lane: two fragments of 32 points, 8 dims per k-step
+  // ---- points of this lane: two fragments of 32 points, 8 dims per k-step; the row's
+  // largest TF32 magnitude (both lanes of the row) sets its scale
   const int64_t p0 = static_cast<int64_t>(blockIdx.x) * ASSIGN_POINTS + wave * ASSIGN_POINTS_PER_WAVE + col;
-  u32x4 xh[2][KSTEPS], xl[2][KSTEPS];
+  u32x4 xf[2][KSTEPS];
   float xsq[2];
+  int xexp[2];
 #pragma unroll
   for (int f = 0; f < 2; ++f) {
     const int64_t p = p0 + 32 * f;
     const bool live = p < n;
-    float part = 0.0f;
+    float part = 0.0f, amax = 0.0f;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
       const spr::f32x4* src = reinterpret_cast<const spr::f32x4*>(xb + p * D + s * 16 + half * 8);
       const spr::f32x4 v0 = live ? src[0] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       const spr::f32x4 v1 = live ? src[1] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       const float e[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-      uint32_t h[8], l[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        tf32_split(e[u], h[u], l[u]);
         part = __fadd_rn(part, __fmul_rn(e[u], e[u]));
+        amax = fmaxf(amax, tf32_abs(e[u]));
       }
-      xh[f][s] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-      xl[f][s] = u32x4{l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16)};
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    xexp[f] = tf32_scale_exp(amax);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {  // the row again (cached), now as scaled fp16
+      const spr::f32x4* src = reinterpret_cast<const spr::f32x4*>(xb + p * D + s * 16 + half * 8);
+      const spr::f32x4 v0 = live ? src[0] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const spr::f32x4 v1 = live ? src[1] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const float e[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      uint32_t h[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) h[u] = tf32_f16_bits(e[u], xexp[f]);
+      xf[f][s] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
     }
     const float other = __shfl_xor(part, 32, 64);
     float total = part + other;
@@ -291,21 +311,37 @@ __global__ __launch_bounds__(ASSIGN_THREADS, D > 64 ? 1 : 2) void kmeans_assign_
       pre_csq = cidx < k ? csqb[cidx] : __builtin_huge_valf();  // padding centroids never win
     }
   };
+  // Two barriers: the tile's largest magnitude (over every thread's pieces), then the
+  // scaled fp16 tile.  The tile being written was last read before the barrier that
+  // ended the previous chunk.
   auto stash = [&](int buf) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < QUADS_PER_THREAD; ++i) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) m = fmaxf(m, tf32_abs(pre[i][u]));
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) tile_max[wave] = m;
+    __syncthreads();
+    float tm = tile_max[0];
+#pragma unroll
+    for (int w = 1; w < ASSIGN_THREADS / 64; ++w) tm = fmaxf(tm, tile_max[w]);
+    const int et = tf32_scale_exp(tm);
 #pragma unroll
     for (int i = 0; i < QUADS_PER_THREAD; ++i) {
       const int quad = tid + i * ASSIGN_THREADS;
       const int row = quad / (D / 4);
       const int vec = quad % (D / 4);
-      uint32_t h[4], l[4];
+      uint32_t h[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) tf32_split(pre[i][u], h[u], l[u]);
-      *reinterpret_cast<uint2*>(&tile_hi[buf][row * ROW_BYTES + vec * 8]) = uint2{h[0] | (h[1] << 16),
-                                                                                  h[2] | (h[3] << 16)};
-      *reinterpret_cast<uint2*>(&tile_lo[buf][row * ROW_BYTES + vec * 8]) = uint2{l[0] | (l[1] << 16),
-                                                                                  l[2] | (l[3] << 16)};
+      for (int u = 0; u < 4; ++u) h[u] = tf32_f16_bits(pre[i][u], et);
+      *reinterpret_cast<uint2*>(&tile[buf][row * ROW_BYTES + vec * 8]) = uint2{h[0] | (h[1] << 16),
+                                                                              h[2] | (h[3] << 16)};
     }
     if (tid < CCHUNK) tile_csq[buf][tid] = pre_csq;
+    if (tid == 0) tile_exp[buf] = et;
   };
 
   fetch(0);
@@ -315,22 +351,19 @@ __global__ __launch_bounds__(ASSIGN_THREADS, D > 64 ? 1 : 2) void kmeans_assign_
   for (int chunk = 0; chunk < nchunks; ++chunk) {
     const int buf = chunk & 1;
     if (chunk + 1 < nchunks) fetch(chunk + 1);
+    // -2 x.c = acc * (-2 2^-(point exponent + tile exponent)), exact
+    const int et = tile_exp[buf];
+    const float k0 = __builtin_ldexpf(-2.0f, -(xexp[0] + et));
+    const float k1 = __builtin_ldexpf(-2.0f, -(xexp[1] + et));
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
       spr::f32x16 acc0 = {}, acc1 = {};
       const int roff = (blk * 32 + col) * ROW_BYTES + half * 16;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
-        const spr::bf16x8 ah = spr::as_bf16x8(*reinterpret_cast<const u32x4*>(&tile_hi[buf][roff + s * 32]));
-        const spr::bf16x8 al = spr::as_bf16x8(*reinterpret_cast<const u32x4*>(&tile_lo[buf][roff + s * 32]));
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xh[0][s]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xh[1][s]), acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xl[0][s]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, spr::as_bf16x8(xl[1][s]), acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xh[0][s]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xh[1][s]), acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xl[0][s]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, spr::as_bf16x8(xl[1][s]), acc1, 0, 0, 0);
+        const f16x8_t a = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const u32x4*>(&tile[buf][roff + s * 32]));
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(f16x8_t, xf[0][s]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, __builtin_bit_cast(f16x8_t, xf[1][s]), acc1, 0, 0, 0);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -339,8 +372,8 @@ __global__ __launch_bounds__(ASSIGN_THREADS, D > 64 ? 1 : 2) void kmeans_assign_
           const int local = blk * 32 + 8 * i + 4 * half + j;
           const int32_t cidx = chunk * CCHUNK + local;
           const float csq = tile_csq[buf][local];
-          const float d0 = fmaxf(__builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq)), 0.0f);
-          const float d1 = fmaxf(__builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq)), 0.0f);
+          const float d0 = fmaxf(__builtin_fmaf(k0, acc0[4 * i + j], __fadd_rn(xsq[0], csq)), 0.0f);
+          const float d1 = fmaxf(__builtin_fmaf(k1, acc1[4 * i + j], __fadd_rn(xsq[1], csq)), 0.0f);
           const bool t0 = d0 < best[0];
           const bool t1 = d1 < best[1];
           best[0] = t0 ? d0 : best[0];

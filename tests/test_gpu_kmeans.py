@@ -275,6 +275,29 @@ def test_assign_tf32_matches_oracle_up_to_ties(dev, oracle, b, n, k, d):
     assert np.allclose(x_sq_out.cpu().numpy(), x_sq, rtol=1e-6)
 
 
+@pytest.mark.parametrize("d", [48, 64])
+def test_assign_tf32_wide_range(dev, oracle, d):
+    """The TF32 products go through fp16 images scaled by a power of two per point row and per
+    64-centroid tile: rows and centroids spread over 10^-3 .. 10^5 (past fp16's 65504 and below
+    its normal range without the scale), with tiny entries inside rows, still match the oracle's
+    TF32 assignment up to ties."""
+    from sparsepr_amd.flash_kmeans.kmeans_impl import euclid_assign
+
+    rng = np.random.default_rng(d + 5)
+    b, n, k = 2, 2000, 300
+    cmag = 10.0 ** rng.uniform(-3, 5, (b, k, 1))
+    c = (rng.standard_normal((b, k, d)) * cmag).astype(np.float32)
+    pick = rng.integers(0, k, (b, n))
+    x = np.take_along_axis(c, pick[..., None], 1) * (1 + 0.05 * rng.standard_normal((b, n, d)))
+    x[:, ::7, 3] *= 1e-6  # entries far below their row's largest one
+    x = x.astype(np.float32)
+    labels = euclid_assign(to_dev(x, dev), to_dev(c, dev)).cpu().numpy()
+    ref, dist, x_sq = oracle.kmeans_assign_tf32(x, c)
+    ok, nbad = oracle.label_mismatches_are_ties(labels, ref, dist, x_sq, c, TIE_REL)
+    assert ok, f"{nbad} label mismatches beyond tie tolerance"
+    assert nbad <= max(2, labels.size // 1000)
+
+
 def test_lloyd_fp32_features_tf32(dev, oracle):
     """The flash Lloyd loop on fp32 features, one iteration at a time: each iteration's labels
     against the oracle's TF32 assignment from the same centroids, centroids the means."""
