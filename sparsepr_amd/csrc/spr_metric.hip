@@ -177,42 +177,65 @@ __global__ __launch_bounds__(256) void factor_scale_kernel(float* __restrict__ f
 
 // ---------------------------------------------------------------- warm subspace update
 constexpr int WF_THREADS = 1024;
-constexpr int LDM = MET_MAX_D + 1;  // padded metric row
-constexpr int LDB = MET_MAX_R + 1;  // padded basis row
+// Rows are 16-byte aligned for vector reads and 4 banks apart, so the eight rows one wave
+// reads at a time fall in distinct banks.
+constexpr int LDM = MET_MAX_D + 4;  // metric row
+constexpr int LDB = MET_MAX_R + 4;  // basis row
 
 enum WarmOrtho { ORTHO_EACH_CQR = 0, ORTHO_EACH_CQR2 = 1, ORTHO_FINAL_CQR = 2 };
 enum WarmRitz { RITZ_RAYLEIGH_CHOLESKY = 0, RITZ_DIAGONAL = 1, RITZ_PREVIOUS_SCALE = 2 };
 
 struct WarmSmem {
-  float m[MET_MAX_D * LDM];   // metric
-  float b[MET_MAX_D * LDB];   // basis
-  float w[MET_MAX_D * LDB];   // metric . basis, scratch
-  float g[MET_MAX_R * LDB];   // Gram / Rayleigh matrix, its Cholesky factor (lower)
+  __attribute__((aligned(16))) float m[MET_MAX_D * LDM];  // metric
+  __attribute__((aligned(16))) float b[MET_MAX_D * LDB];  // basis
+  __attribute__((aligned(16))) float w[MET_MAX_D * LDB];  // metric . basis, scratch
+  __attribute__((aligned(16))) float g[MET_MAX_R * LDB];  // Gram / Rayleigh matrix, its Cholesky factor (lower)
+  __attribute__((aligned(16))) float lcol[MET_MAX_R];     // the Cholesky column in flight
   float colv[MET_MAX_R];      // per-column values (norms, diagonal Ritz values, scales)
   float scal[4];
   int32_t fail;
 };
 
-// w = m . b (n x n times n x r); thread (row i, column group cb), columns cb + 8 u
-__device__ void wf_apply(WarmSmem& s, int n, int r) {
-  const int t = threadIdx.x, i = t >> 3, cb = t & 7;
-  if (i < n) {
+// Sum over the 8 lanes 8g .. 8g + 7 (every lane of the group gets the same value).
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  return v;
+}
+
+// w = m . b (n x n times n x r); thread t: row t / 8, columns 8 (t % 8) .. + 7, the sum over
+// j in index order; m read four entries at a time, b eight columns at a time
+__device__ __forceinline__ void wf_apply(WarmSmem& s, int n, int r) {
+  const int t = threadIdx.x, i = t >> 3, c0 = 8 * (t & 7);
+  if (i < n && c0 < r) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int j = 0; j < n; ++j) {
-      const float mij = s.m[i * LDM + j];
+    auto step = [&](float mij, int j) {
+      const spr::f32x4 b0 = *reinterpret_cast<const spr::f32x4*>(&s.b[j * LDB + c0]);
+      const spr::f32x4 b1 = *reinterpret_cast<const spr::f32x4*>(&s.b[j * LDB + c0 + 4]);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] = __builtin_fmaf(mij, s.b[j * LDB + cb + 8 * u], acc[u]);
+      for (int u = 0; u < 4; ++u) {
+        acc[u] = __builtin_fmaf(mij, b0[u], acc[u]);
+        acc[4 + u] = __builtin_fmaf(mij, b1[u], acc[4 + u]);
+      }
+    };
+    int j = 0;
+    for (; j + 4 <= n; j += 4) {
+      const spr::f32x4 mv = *reinterpret_cast<const spr::f32x4*>(&s.m[i * LDM + j]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) step(mv[u], j + u);
     }
+    for (; j < n; ++j) step(s.m[i * LDM + j], j);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      if (cb + 8 * u < r) s.w[i * LDB + cb + 8 * u] = acc[u];
+      if (c0 + u < r) s.w[i * LDB + c0 + u] = acc[u];
     }
   }
   __syncthreads();
 }
 
 // column norms of src (n x r) into colv, clamped at 1e-12
-__device__ void wf_colnorms(WarmSmem& s, const float* src, int n, int r) {
+__device__ __forceinline__ void wf_colnorms(WarmSmem& s, const float* src, int n, int r) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   for (int col = wv; col < r; col += WF_THREADS / 64) {
     const float v0 = lane < n ? src[lane * LDB + col] : 0.0f;
@@ -223,61 +246,130 @@ __device__ void wf_colnorms(WarmSmem& s, const float* src, int n, int r) {
   __syncthreads();
 }
 
-// g = a^T c (r x r), computed for p <= q and mirrored (exactly symmetric)
-__device__ void wf_gram(WarmSmem& s, const float* a, const float* c, int n, int r, bool symmetrize) {
-  for (int e = threadIdx.x; e < r * r; e += WF_THREADS) {
-    const int p = e / r, q = e - p * r;
-    if (q < p) continue;
-    float acc = 0.0f, acc2 = 0.0f;
+// g = a^T c (r x r), or 0.5 (a^T c + c^T a) when symmetrize; thread t owns the 2 x 2 tile
+// at (2 (t / 32), 2 (t % 32)), sums over the rows in index order; tiles on or above the
+// diagonal are computed and mirrored, so g is exactly symmetric
+__device__ __forceinline__ void wf_gram(WarmSmem& s, const float* a, const float* c, int n, int r, bool symmetrize) {
+  const int t = threadIdx.x, p0 = 2 * (t >> 5), q0 = 2 * (t & 31);
+  if (p0 < r && q0 < r && p0 <= q0) {
+    float acc[2][2] = {{0, 0}, {0, 0}}, acc2[2][2] = {{0, 0}, {0, 0}};
     for (int i = 0; i < n; ++i) {
-      acc = __builtin_fmaf(a[i * LDB + p], c[i * LDB + q], acc);
-      if (symmetrize) acc2 = __builtin_fmaf(a[i * LDB + q], c[i * LDB + p], acc2);
+      const float2 ap = *reinterpret_cast<const float2*>(&a[i * LDB + p0]);
+      const float2 cq = *reinterpret_cast<const float2*>(&c[i * LDB + q0]);
+      acc[0][0] = __builtin_fmaf(ap.x, cq.x, acc[0][0]);
+      acc[0][1] = __builtin_fmaf(ap.x, cq.y, acc[0][1]);
+      acc[1][0] = __builtin_fmaf(ap.y, cq.x, acc[1][0]);
+      acc[1][1] = __builtin_fmaf(ap.y, cq.y, acc[1][1]);
+      if (symmetrize) {
+        const float2 aq = *reinterpret_cast<const float2*>(&a[i * LDB + q0]);
+        const float2 cp = *reinterpret_cast<const float2*>(&c[i * LDB + p0]);
+        acc2[0][0] = __builtin_fmaf(aq.x, cp.x, acc2[0][0]);
+        acc2[0][1] = __builtin_fmaf(aq.y, cp.x, acc2[0][1]);
+        acc2[1][0] = __builtin_fmaf(aq.x, cp.y, acc2[1][0]);
+        acc2[1][1] = __builtin_fmaf(aq.y, cp.y, acc2[1][1]);
+      }
     }
-    const float v = symmetrize ? 0.5f * (acc + acc2) : acc;
-    s.g[p * LDB + q] = v;
-    s.g[q * LDB + p] = v;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const int p = p0 + u, q = q0 + v;
+        if (p < r && q < r && p <= q) {
+          const float val = symmetrize ? 0.5f * (acc[u][v] + acc2[u][v]) : acc[u][v];
+          s.g[p * LDB + q] = val;
+          s.g[q * LDB + p] = val;
+        }
+      }
+    }
   }
   __syncthreads();
 }
 
-// In-place lower Cholesky of g[0..r) + shift I, by wave 0 (lane = row).  Returns (to every
-// thread) whether it succeeded: every pivot finite and positive.  g keeps the shifted
-// matrix's original entries above the diagonal; on failure the factor is undefined.
-__device__ bool wf_cholesky(WarmSmem& s, const float* src, int r, float shift) {
-  const int t = threadIdx.x, lane = t & 63;
-  if (t < 64) {
-    // copy the lower triangle of src (+ shift on the diagonal) into g
-    for (int j = 0; j < r; ++j) {
-      if (lane < r && j <= lane) s.g[lane * LDB + j] = src[lane * LDB + j] + (j == lane ? shift : 0.0f);
-    }
-    wave_sync();
-    bool ok = true;
-    for (int k = 0; k < r; ++k) {
-      const float piv = s.g[k * LDB + k];
+// In-place lower Cholesky of src[0..r) + shift I into g, by wave 0: lane = row, the row in
+// registers; each column of L goes through LDS once and comes back as broadcast reads
+// (a readlane per entry instead measured twice as slow).  Sets *fail (0 = every pivot
+// finite and positive).  Only the lower triangle of g is written; on failure the factor is
+// undefined.  Kept out of line (it is called from several places and is fully unrolled);
+// its LDS pointers carry their address space, so the accesses stay LDS instructions.
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) int32_t lds_i32;
+__device__ __noinline__ void wf_cholesky_wave(const lds_f32* src, lds_f32* g, lds_f32* lcol, lds_i32* fail, int r,
+                                              float shift) {
+  const int lane = threadIdx.x & 63;
+  float row[MET_MAX_R];
+#pragma unroll
+  for (int j = 0; j < MET_MAX_R; ++j) {
+    row[j] = (lane < r && j <= lane && j < r) ? src[lane * LDB + j] + (j == lane ? shift : 0.0f) : 0.0f;
+  }
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < MET_MAX_R; ++k) {
+    if (k < r) {
+      const float piv = __shfl(row[k], k, 64);
       ok = ok && (piv > 0.0f) && (piv < __builtin_huge_valf());
       const float lkk = sqrtf(fmaxf(piv, 1e-30f));
-      float lik = 0.0f;
-      if (lane > k && lane < r) {
-        lik = s.g[lane * LDB + k] / lkk;
-        s.g[lane * LDB + k] = lik;
-      }
+      const float lik = lane > k ? row[k] / lkk : 0.0f;
+      row[k] = lane == k ? lkk : (lane > k ? lik : row[k]);
+      lcol[lane] = lik;
       wave_sync();
-      if (lane == k) s.g[k * LDB + k] = lkk;
-      if (lane > k && lane < r) {
-        for (int j = k + 1; j <= lane; ++j) s.g[lane * LDB + j] -= lik * s.g[j * LDB + k];
-      }
+#pragma unroll
+      for (int j = k + 1; j < MET_MAX_R; ++j) row[j] -= lik * lcol[j];  // entries past the lane are unused
       wave_sync();
     }
-    if (lane == 0) s.fail = ok ? 0 : 1;
+  }
+#pragma unroll
+  for (int j = 0; j < MET_MAX_R; ++j) {
+    if (lane < r && j <= lane) g[lane * LDB + j] = row[j];
+  }
+  if (lane == 0) *fail = ok ? 0 : 1;
+}
+__device__ __forceinline__ bool wf_cholesky(WarmSmem& s, const float* src, int r, float shift) {
+  if (threadIdx.x < 64) {
+    // generic to LDS address space (the pointers point into the workgroup's LDS)
+    wf_cholesky_wave((const lds_f32*)src, (lds_f32*)s.g, (lds_f32*)s.lcol, (lds_i32*)&s.fail, r, shift);
   }
   __syncthreads();
   return s.fail == 0;
 }
 
+// b = w L^-T: row i solves L y = w_i by forward substitution (identity L when ok is false).
+// Threads 8 i .. 8 i + 7 share the row; thread 8 i + u keeps y[c] for c = u mod 8 in
+// registers, and each step sums the eight partial dot products (DPP) before the division.
+// Out of line for the same reason as the Cholesky.
+__device__ __noinline__ void wf_solve_rows(const lds_f32* g, const lds_f32* w, lds_f32* b, int n, int r, bool ok) {
+  const int t = threadIdx.x, i = t >> 3, u = t & 7;
+  float y[MET_MAX_R / 8];
+#pragma unroll
+  for (int q = 0; q < MET_MAX_R / 8; ++q) y[q] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < MET_MAX_R; ++c) {
+    if (c < r) {
+      float part = 0.0f;
+#pragma unroll
+      for (int q = 0; q < MET_MAX_R / 8; ++q) {
+        if (8 * q < c) {
+          const int k = 8 * q + u;
+          part = k < c ? __builtin_fmaf(g[c * LDB + k], y[q], part) : part;
+        }
+      }
+      const float tot = sum8(part);
+      const float wic = i < n ? w[i * LDB + c] : 0.0f;
+      const float yc = ok ? (wic - tot) / g[c * LDB + c] : wic;
+      if (u == (c & 7)) y[c >> 3] = yc;
+    }
+  }
+  if (i < n) {
+#pragma unroll
+    for (int q = 0; q < MET_MAX_R / 8; ++q) {
+      if (8 * q + u < r) b[i * LDB + 8 * q + u] = y[q];
+    }
+  }
+}
+
 // Cholesky-QR of src (n x r) into s.b (operator_kmeans.py:326-358): columns normalised
 // (norm clamped at 1e-12), Gram, jitter = max(mean diag, 1e-12) * ridge on the diagonal,
 // Cholesky (identity on failure), b = normalised . L^-T.  Returns whether it failed.
-__device__ bool wf_cholesky_qr(WarmSmem& s, const float* src, int n, int r, float ridge) {
+__device__ __forceinline__ bool wf_cholesky_qr(WarmSmem& s, const float* src, int n, int r, float ridge) {
   wf_colnorms(s, src, n, r);
   // normalised columns into w (src may be w itself: each element read then written by one thread)
   for (int e = threadIdx.x; e < n * r; e += WF_THREADS) {
@@ -293,18 +385,7 @@ __device__ bool wf_cholesky_qr(WarmSmem& s, const float* src, int n, int r, floa
   }
   __syncthreads();
   const bool ok = wf_cholesky(s, s.g, r, s.scal[0]);  // in place
-  // b = w L^-T: row i solves L y = w_i (forward substitution), identity L on failure
-  if (threadIdx.x < n) {
-    const int i = threadIdx.x;
-    for (int c = 0; c < r; ++c) {
-      float acc = s.w[i * LDB + c];
-      if (ok) {
-        for (int k = 0; k < c; ++k) acc -= s.g[c * LDB + k] * s.b[i * LDB + k];
-        acc /= s.g[c * LDB + c];
-      }
-      s.b[i * LDB + c] = acc;
-    }
-  }
+  wf_solve_rows((const lds_f32*)s.g, (const lds_f32*)s.w, (lds_f32*)s.b, n, r, ok);
   __syncthreads();
   return !ok;
 }
