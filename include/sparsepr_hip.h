@@ -86,7 +86,7 @@ int spr_kmeans_assign_bf16(const void* x, const void* centroids, const float* c_
  *   with exact TF32 products summed in fp32, lowest index among exact minima.
  *   x fp32 [batch, n, d], centroids fp32 [batch, k, d], c_sq fp32 [batch, k];
  *   x_sq fp32 [batch, n] or NULL (inline: fp32 sum of the fp32 squares of x);
- *   x_sq_out nullable as for spr_kmeans_assign_bf16; d in {16, 32, 48, 64, 128}. */
+ *   x_sq_out nullable as for spr_kmeans_assign_bf16; d a multiple of 16 up to 128. */
 int spr_kmeans_assign_tf32(const float* x, const float* centroids, const float* c_sq, const float* x_sq,
                            float* x_sq_out, int64_t batch, int64_t n, int32_t k, int32_t d, int32_t* labels,
                            hipStream_t stream);
@@ -94,7 +94,7 @@ int spr_kmeans_assign_tf32(const float* x, const float* centroids, const float* 
  * centroid_reduction.py:138-196 original_centroids_triton, n8_ops.cu:255-269 finalize.
  *   Means of the rows of each cluster (sorted_idx/offsets from spr_argsort_labels), fp64
  *   accumulation, empty clusters keep `old`.  dtype 0 (bf16, d in {64,128}) or 2 (fp32,
- *   d in {16,32,48,64,128}).  Nullable outputs: mean32 fp32 [batch,k,d], out dtype [batch,k,d],
+ *   d a multiple of 16 up to 128).  Nullable outputs: mean32 fp32 [batch,k,d], out dtype [batch,k,d],
  *   shift_max fp32 scalar (pre-zeroed; max_k ||out-old||), sums_accum fp32 += sums,
  *   counts_accum int32 += counts, c_sq_out fp32 [batch,k] = squared norms of `out` (as
  *   spr_centroid_sq computes them, for the next assignment).  Large clusters are split into row slices whose fp64 partial
@@ -308,6 +308,15 @@ int spr_role_projection_rms(const void* x, const float* factor, int64_t bh, int6
 size_t spr_role_k_projection_workspace(int64_t bh, int64_t n);
 int spr_role_k_projection(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d, int32_t rank,
                           float* out, float* key_scale, void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The same under role_kv_matmul_precision (n8_v6.py:77-86,141-178): precision 0 "high" (TF32
+ * factor), 1 "highest" (fp32 factor, also compile_role_kv_projection=False's
+ * normalize_feature_scale(project_tokens(...)), operator_kmeans.py:540-550), 2 "medium" (bf16
+ * factor); out[t][out_col + c] (rows of out_ld floats) = (weight p) / key_scale, so the K and
+ * the weighted V features of _role_kv_projection_normalize_fp32 (n8_v6.py:91-103) fill one
+ * [bh, n, R_k + R_v] tensor side by side. */
+int spr_role_k_projection_ex(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d, int32_t rank,
+                             int32_t precision, float weight, float* out, int32_t out_ld, int32_t out_col,
+                             float* key_scale, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- SVG-EAR routing scores
  * svg_ear.py:95-192,453-531 svg_ear_value_error_scores_triton (mode 0; Jensen term when
@@ -415,6 +424,12 @@ int spr_warm_metric_factor(const float* metric, const float* prev_state, const f
  *   d <= 128, r <= 64. */
 int spr_project_rows(const float* x, const float* factor, const float* div, int64_t bh, int64_t m, int32_t d,
                      int32_t r, int32_t tf32, int32_t row_rms, float eps, float* out, hipStream_t stream);
+/* The same with precision 0 fp32 / 1 TF32 / 2 bf16 operands (role_kv_matmul_precision
+ * "highest" / "high" / "medium") and out[i][out_col + c] (rows of out_ld floats) = weight (p / div)
+ * (the K and weighted V centroid projections of _role_kv_init_projection_fp32, n8_v6.py:118-126). */
+int spr_project_rows_ex(const float* x, const float* factor, const float* div, int64_t bh, int64_t m, int32_t d,
+                        int32_t r, int32_t precision, int32_t row_rms, float eps, float weight, float* out,
+                        int32_t out_ld, int32_t out_col, hipStream_t stream);
 
 #ifdef __cplusplus
 }

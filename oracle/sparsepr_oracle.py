@@ -879,20 +879,22 @@ def warm_subspace_metric_factor(metric, previous, rank, power_iters=2, orthogona
     return np.stack(factors), np.stack(bases), rec
 
 
-def project_rows(x, factor, div=None, tf32=False, row_rms=False, eps=1e-6):
+def project_rows(x, factor, div=None, tf32=False, row_rms=False, eps=1e-6, precision=None, weight=1.0):
     """project_tokens (operator_kmeans.py:534-538), optionally / a per-head divisor (the
     compiled K-centroid projection, n8_v6.py:152-178, whose "high" precision rounds both fp32
-    operands to TF32) and normalize_rows_rms (:548-555).  float64 products."""
+    operands to TF32, "medium" to bf16) times weight (the V half of
+    _role_kv_init_projection_fp32, :118-126) and normalize_rows_rms (:548-555).  float64
+    products."""
     x = np.asarray(x, np.float32)
     f = np.asarray(factor, np.float32)
-    if tf32:
-        x, f = tf32_rna(x), tf32_rna(f)
+    prec = precision if precision is not None else ("high" if tf32 else "highest")
+    x, f = matmul_precision_operand(x, prec), matmul_precision_operand(f, prec)
     p = np.matmul(x.astype(np.float64), f.astype(np.float64))
     if div is not None:
         p = p / np.asarray(div, np.float64).reshape(-1, 1, 1)
     if row_rms:
         p = p / np.maximum(np.sqrt((p * p).mean(-1, keepdims=True)), eps)
-    return p
+    return weight * p
 
 
 def svg_ear_value_error_scores(qc, k_sorted, v_sorted, kc, vc, sizes, group, var_k_diag=None,
@@ -952,14 +954,39 @@ def role_projection_rms(x, factor):
     return (p / np.sqrt(ms)).astype(np.float32)
 
 
-def role_k_projection_normalize(k, factor):
-    """_role_k_projection_normalize_fp32 (n8_v6.py:141-149): key = k . tf32(F) (the fp32
-    bmm under the reference's TF32 contract), key_scale = max(sqrt(mean over tokens and rank
-    of key^2), 1e-8) per head, returns (key / key_scale float32, key_scale float32 [BH, 1, 1]).
-    float64 inside."""
-    p = np.einsum("bnd,bdr->bnr", k.astype(np.float64), tf32_rna(factor).astype(np.float64))
+def matmul_precision_operand(x, precision):
+    """An fp32 operand as torch's fp32 matmul under set_float32_matmul_precision sees it
+    (n8_v6.py:77-86): "highest" unchanged, "high" rounded to TF32, "medium" rounded to
+    bf16 (nearest even).  float32."""
+    x = np.asarray(x, np.float32)
+    if precision == "high":
+        return tf32_rna(x)
+    if precision == "medium":
+        return to_bf16(x)
+    if precision == "highest":
+        return x
+    raise ValueError(f"unknown precision {precision!r}")
+
+
+def role_k_projection_normalize(k, factor, precision="high", weight=1.0):
+    """_role_k_projection_normalize_fp32 (n8_v6.py:141-149) under role_kv_matmul_precision
+    (the V half of _role_kv_projection_normalize_fp32, :91-103, with weight): key = k . F~
+    with F~ the factor as the matmul sees it (k is bf16, unchanged by any of the roundings),
+    key_scale = max(sqrt(mean over tokens and rank of key^2), 1e-8) per head; returns
+    ((weight key) / key_scale float32, key_scale float32 [BH, 1, 1]).  float64 inside."""
+    f = matmul_precision_operand(factor, precision)
+    p = np.einsum("bnd,bdr->bnr", k.astype(np.float64), f.astype(np.float64))
     scale = np.maximum(np.sqrt((p * p).mean(axis=(1, 2), keepdims=True)), 1e-8)
-    return (p / scale).astype(np.float32), scale.astype(np.float32)
+    return ((weight * p) / scale).astype(np.float32), scale.astype(np.float32)
+
+
+def role_kv_projection_normalize(k, v, k_factor, v_factor, v_weight, precision="high"):
+    """_role_kv_projection_normalize_fp32 (n8_v6.py:91-103): cat(key / key_scale,
+    (v_weight value) / value_scale) along the feature axis.  Returns (features, key_scale,
+    value_scale)."""
+    kf, ks = role_k_projection_normalize(k, k_factor, precision)
+    vf, vs = role_k_projection_normalize(v, v_factor, precision, weight=v_weight)
+    return np.concatenate((kf, vf), axis=2), ks, vs
 
 
 def attention_mass_scores(qc, k_sorted, sizes, group):

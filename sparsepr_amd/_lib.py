@@ -98,10 +98,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_warm_metric_factor": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _vp,
                                               _vp, _vp, _vp]),
     "spr_project_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
+    "spr_project_rows_ex": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _f32, _vp, _i32,
+                                           _i32, _vp]),
     # role_proj.hip
     "spr_role_projection_rms": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "spr_role_k_projection_workspace": (_sz, [_i64, _i64]),
     "spr_role_k_projection": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "spr_role_k_projection_ex": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _f32, _vp, _i32, _i32, _vp,
+                                                _vp, _sz, _vp]),
     # svg_ear.hip
     "spr_svg_ear_scores_flops": (_sz, [_i64, _i32, _i64]),
     "spr_svg_ear_scores": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _i32, _i32, _i64, _i64,

@@ -1055,9 +1055,12 @@ extern "C" int spr_kmeans_assign_tf32(const float* x, const float* centroids, co
     case 32: SPR_TF32_ASSIGN(32); break;
     case 48: SPR_TF32_ASSIGN(48); break;
     case 64: SPR_TF32_ASSIGN(64); break;
+    case 80: SPR_TF32_ASSIGN(80); break;
+    case 96: SPR_TF32_ASSIGN(96); break;
+    case 112: SPR_TF32_ASSIGN(112); break;
     case 128: SPR_TF32_ASSIGN(128); break;
     default:
-      SPR_REQUIRE(false, "spr_kmeans_assign_tf32: feature dim %d not supported (16, 32, 48, 64, 128)", d);
+      SPR_REQUIRE(false, "spr_kmeans_assign_tf32: feature dim %d not supported (a multiple of 16 up to 128)", d);
   }
 #undef SPR_TF32_ASSIGN
   SPR_LAUNCHED("kmeans_assign_tf32_kernel");
@@ -1189,8 +1192,11 @@ extern "C" int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* so
       case 32: SPR_MEAN_CASE(float, 32); break;
       case 48: SPR_MEAN_CASE(float, 48); break;
       case 64: SPR_MEAN_CASE(float, 64); break;
+      case 80: SPR_MEAN_CASE(float, 80); break;
+      case 96: SPR_MEAN_CASE(float, 96); break;
+      case 112: SPR_MEAN_CASE(float, 112); break;
       case 128: SPR_MEAN_CASE(float, 128); break;
-      default: SPR_REQUIRE(false, "spr_centroid_mean: fp32 dim %d not supported (16, 32, 48, 64, 128)", d);
+      default: SPR_REQUIRE(false, "spr_centroid_mean: fp32 dim %d not supported (a multiple of 16 up to 128)", d);
     }
   } else {
     SPR_REQUIRE(false, "spr_centroid_mean: unsupported dtype %d", dtype);

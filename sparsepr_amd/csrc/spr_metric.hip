@@ -19,8 +19,9 @@
 //                      Cholesky, all fp32.
 // factor_scale_kernel  eigenvectors x sqrt(max(lambda, 0) / max(mean lambda, 1e-12)).
 // project_rows_kernel  one wave per row: p = x . F (fp32, or both operands rounded to TF32 as
-//                      a "high"-precision fp32 matmul does), / a per-head divisor, optional
-//                      row-RMS normalisation.
+//                      a "high"-precision fp32 matmul does, or to bf16 as a "medium" one
+//                      does), / a per-head divisor, optional row-RMS normalisation, times a
+//                      weight, into columns of a wider row.
 #include "spr_common.h"
 
 extern "C" int spr_sym_top_eig(const float* mats, int64_t bh, int32_t n, int32_t rank, int32_t symmetrize,
@@ -551,9 +552,12 @@ __global__ __launch_bounds__(WF_THREADS, 1) void warm_factor_kernel(
 // one wave per (head, row): lane c < r computes sum_j x[row][j] F[j][c] in index order
 // (fmaf), then divides by div[h] (nullable) and, with row_rms, by
 // max(sqrt(mean_c p_c^2), eps).
+// precision 0: fp32 operands; 1: both rounded to TF32; 2: both rounded to bf16 (nearest even).
+// out[row][out_col + c] (rows of out_ld floats) = weight * (p_c / div[h]).
 __global__ __launch_bounds__(256) void project_rows_kernel(const float* __restrict__ x, const float* __restrict__ f,
                                                            const float* __restrict__ div, int64_t m, int32_t d,
-                                                           int32_t r, int32_t tf32, int32_t row_rms, float eps,
+                                                           int32_t r, int32_t precision, int32_t row_rms, float eps,
+                                                           int32_t out_ld, int32_t out_col, float weight,
                                                            float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -565,9 +569,12 @@ __global__ __launch_bounds__(256) void project_rows_kernel(const float* __restri
   if (lane < r) {
     for (int j = 0; j < d; ++j) {
       float xv = xr[j], fv = fh[j * r + lane];
-      if (tf32) {
+      if (precision == 1) {
         xv = tf32_rna(xv);
         fv = tf32_rna(fv);
+      } else if (precision == 2) {
+        xv = spr::bf16_to_f32(spr::f32_to_bf16(xv));
+        fv = spr::bf16_to_f32(spr::f32_to_bf16(fv));
       }
       acc = __builtin_fmaf(xv, fv, acc);
     }
@@ -577,7 +584,7 @@ __global__ __launch_bounds__(256) void project_rows_kernel(const float* __restri
     const float ms = wave_sum(lane < r ? acc * acc : 0.0f) / static_cast<float>(r);
     acc = acc / fmaxf(sqrtf(ms), eps);
   }
-  if (lane < r) out[(h * m + row) * r + lane] = acc;
+  if (lane < r) out[(h * m + row) * out_ld + out_col + lane] = weight == 1.0f ? acc : weight * acc;
 }
 
 }  // namespace
@@ -659,15 +666,25 @@ extern "C" int spr_warm_metric_factor(const float* metric, const float* prev_sta
 // out fp32 [bh, m, r] = (x [bh, m, d] . factor [bh, d, r]) / div[h] (div nullable), with
 // tf32 = 1 both operands rounded to TF32 first; row_rms = 1 divides each row by
 // max(sqrt(mean p^2), eps).  d <= 128, r <= 64.
-extern "C" int spr_project_rows(const float* x, const float* factor, const float* div, int64_t bh, int64_t m,
-                                int32_t d, int32_t r, int32_t tf32, int32_t row_rms, float eps, float* out,
-                                hipStream_t stream) {
+extern "C" int spr_project_rows_ex(const float* x, const float* factor, const float* div, int64_t bh, int64_t m,
+                                   int32_t d, int32_t r, int32_t precision, int32_t row_rms, float eps, float weight,
+                                   float* out, int32_t out_ld, int32_t out_col, hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && m >= 0 && d >= 1 && d <= MET_MAX_D && r >= 1 && r <= 64, "spr_project_rows: bad size");
   SPR_REQUIRE(bh <= 65535, "spr_project_rows: too many heads");
+  SPR_REQUIRE(precision >= 0 && precision <= 2, "spr_project_rows: precision must be 0, 1 or 2 (got %d)", precision);
+  SPR_REQUIRE(out_col >= 0 && out_ld >= out_col + r, "spr_project_rows: columns %d + %d exceed rows of %d", out_col,
+              r, out_ld);
   if (bh == 0 || m == 0) return SPR_OK;
   SPR_REQUIRE(x && factor && out, "spr_project_rows: null pointer");
   dim3 grid(static_cast<uint32_t>(spr::ceil_div(m, 4)), static_cast<uint32_t>(bh));
-  project_rows_kernel<<<grid, 256, 0, stream>>>(x, factor, div, m, d, r, tf32, row_rms, eps, out);
+  project_rows_kernel<<<grid, 256, 0, stream>>>(x, factor, div, m, d, r, precision, row_rms, eps, out_ld, out_col,
+                                                weight, out);
   SPR_LAUNCHED("project_rows_kernel");
   return SPR_OK;
+}
+
+extern "C" int spr_project_rows(const float* x, const float* factor, const float* div, int64_t bh, int64_t m,
+                                int32_t d, int32_t r, int32_t tf32, int32_t row_rms, float eps, float* out,
+                                hipStream_t stream) {
+  return spr_project_rows_ex(x, factor, div, bh, m, d, r, tf32 ? 1 : 0, row_rms, eps, 1.0f, out, r, 0, stream);
 }

@@ -1,15 +1,22 @@
-// Role-coordinate projection with row RMS normalisation (N8's Q role features).
+// Role-coordinate projection with row RMS normalisation (N8's Q role features), and the
+// K (or V) role projection with one RMS scale per head.
 //
 // Replaces:
 //   _role_projection_rms_kernel + role_projection_rms_triton
 //       (src/sparsepr/kernels/triton/role_projection.py:16-55, :58-103)
+//   _role_k_projection_normalize_fp32 / _role_kv_projection_normalize_fp32, torch.compile'd
+//       under role_kv_matmul_precision (src/sparsepr/models/common/n8_v6.py:77-149), and
+//       normalize_feature_scale(project_tokens(...)) (operator_kmeans.py:540-550)
 //
 //   p = x . F~, out = p / sqrt(max(sum_r p_r^2 / R, 1e-12))
-// for x bf16 [bh, n, d] and the factor F fp32 [bh, d, R]; F~ is F rounded to TF32
-// (nearest, ties away), as the reference's tl.dot(..., input_precision="tf32") rounds
-// its fp32 operand (a bf16 x is exact in TF32).  F~ is split into bf16 hi + lo with
-// hi + lo == F~ exactly, so each product is exact and only the fp32 summation order
-// differs.
+// for x bf16 [bh, n, d] and the factor F fp32 [bh, d, R]; F~ is F as the fp32 matmul sees it:
+//   PREC 0 ("high", and tl.dot(..., input_precision="tf32")): rounded to TF32 (nearest, ties
+//          away; a bf16 x is exact in TF32), split into bf16 hi + lo with hi + lo == F~;
+//   PREC 1 ("highest", plain fp32): F itself, split into bf16 hi + mid + lo (8 significant
+//          bits each, 24 in all) with hi + mid + lo == F;
+//   PREC 2 ("medium", bf16 operands): F rounded to bf16 (nearest even).
+// Each product of a bf16 x with a bf16 piece is exact, so only the fp32 summation order
+// differs from the reference's.
 //
 // Layout: one workgroup of four waves per (head, 2048 tokens); F~^T hi / lo of the head
 // sit in LDS (R rows padded to a multiple of 32, d columns, 16-byte pieces swizzled
@@ -42,17 +49,20 @@ __device__ __forceinline__ float sum_xor32(float x) {
 // MODE 0: rows normalised by their RMS.  MODE 1: no output; the workgroup's sum of p^2 goes to
 // partial[head][block] (fp64).  MODE 2: p divided by the head's scale sqrt(max(mean p^2, ...))
 // formed from the partials in block order (the same on every workgroup); block 0 stores it.
-template <int D, int RB, int MODE>
+// MODE 2 writes (weight p) / scale into columns out_col .. out_col + R of rows out_ld floats long.
+// NP = bf16 pieces of F~ (PREC 0: 2, 1: 3, 2: 1).
+template <int D, int RB, int MODE, int PREC>
 __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint16_t* __restrict__ x,
                                                                      const float* __restrict__ factor, int64_t n,
                                                                      int32_t rank, float* __restrict__ out,
+                                                                     int32_t out_ld, int32_t out_col, float weight,
                                                                      double* __restrict__ partial,
                                                                      float* __restrict__ head_scale) {
   constexpr int KSTEPS = D / 16;
   constexpr int ROWB = D * 2;  // bytes per F~^T row (bf16)
   constexpr int RP = RB * 32;
-  __shared__ __attribute__((aligned(16))) uint8_t fhi[RP * ROWB];
-  __shared__ __attribute__((aligned(16))) uint8_t flo[RP * ROWB];
+  constexpr int NP = PREC == 0 ? 2 : (PREC == 1 ? 3 : 1);
+  __shared__ __attribute__((aligned(16))) uint8_t fpc[NP][RP * ROWB];
   const int64_t b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -60,25 +70,31 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
   const int col = lane & 31;
   const int half = lane >> 5;
 
-  // F~^T into LDS: element (r, k) of row r at piece (k / 8) ^ (r % (D / 8)), slot k % 8
+  // F~^T pieces into LDS: element (r, k) of row r at piece (k / 8) ^ (r % (D / 8)), slot k % 8.
+  // Each piece is the top 16 bits (a bf16) of what the earlier pieces leave, so the pieces
+  // sum to F~ exactly (the remainders are exact in fp32).
   const float* fb = factor + b * D * rank;
   for (int i = tid; i < RP * D / 2; i += RP_THREADS) {
     const int r = i / (D / 2), k = 2 * (i % (D / 2));
-    const float v0 = r < rank ? tf32_rna(fb[static_cast<int64_t>(k) * rank + r]) : 0.0f;
-    const float v1 = r < rank ? tf32_rna(fb[static_cast<int64_t>(k + 1) * rank + r]) : 0.0f;
-    const uint32_t h0 = __float_as_uint(v0) & 0xffff0000u, h1 = __float_as_uint(v1) & 0xffff0000u;
-    const uint32_t hw = (h0 >> 16) | h1;
-    // v - hi has at most 3 significant bits: exact in fp32 and in bf16
-    const uint32_t lw = (__float_as_uint(v0 - __uint_as_float(h0)) >> 16) |
-                        (__float_as_uint(v1 - __uint_as_float(h1)) & 0xffff0000u);
+    float v[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float f = r < rank ? fb[static_cast<int64_t>(k + u) * rank + r] : 0.0f;
+      v[u] = PREC == 0 ? tf32_rna(f) : (PREC == 2 ? spr::bf16_to_f32(spr::f32_to_bf16(f)) : f);
+    }
     const int off = r * ROWB + ((((k >> 3) ^ (r % (D / 8))) << 4) | ((k & 7) << 1));
-    *reinterpret_cast<uint32_t*>(fhi + off) = hw;
-    *reinterpret_cast<uint32_t*>(flo + off) = lw;
+#pragma unroll
+    for (int pc = 0; pc < NP; ++pc) {
+      const uint32_t h0 = __float_as_uint(v[0]) & 0xffff0000u, h1 = __float_as_uint(v[1]) & 0xffff0000u;
+      *reinterpret_cast<uint32_t*>(fpc[pc] + off) = (h0 >> 16) | h1;
+      v[0] -= __uint_as_float(h0);
+      v[1] -= __uint_as_float(h1);
+    }
   }
   __syncthreads();
 
   const uint16_t* xb = x + b * n * D;
-  float* ob = out + b * n * rank;
+  float* ob = out + b * n * (MODE == 2 ? out_ld : rank);
   __shared__ double red_l[RP_WAVES];
   float div = 1.0f;
   if (MODE == 2) {
@@ -121,10 +137,11 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
         const int off = r * ROWB + (((2 * s + half) ^ (r % (D / 8))) << 4);
-        const u32x4 ah = *reinterpret_cast<const u32x4*>(fhi + off);
-        const u32x4 al = *reinterpret_cast<const u32x4*>(flo + off);
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(xf[s]), acc[rb], 0, 0, 0);
-        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(al), spr::as_bf16x8(xf[s]), acc[rb], 0, 0, 0);
+#pragma unroll
+        for (int pc = 0; pc < NP; ++pc) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(fpc[pc] + off);
+          acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[s]), acc[rb], 0, 0, 0);
+        }
       }
     }
     // lane (token col, half) holds p_r for r = 32 rb + 8 (e / 4) + 4 half + e % 4 (zero past rank)
@@ -140,15 +157,15 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
     }
     ss = sum_xor32(ss);
     const float inv = 1.0f / sqrtf(fmaxf(ss / static_cast<float>(rank), 1.0e-12f));
-    auto nrm = [&](float v) { return MODE == 0 ? v * inv : v / div; };
+    auto nrm = [&](float v) { return MODE == 0 ? v * inv : (weight * v) / div; };
     if (live) {
-      float* orow = ob + t * rank;
+      float* orow = MODE == 2 ? ob + t * out_ld + out_col : ob + t * rank;
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int r0 = 32 * rb + 8 * g + 4 * half;
-          if (r0 + 3 < rank && (rank & 3) == 0) {
+          if (r0 + 3 < rank && (rank & 3) == 0 && (MODE != 2 || ((out_ld | out_col) & 3) == 0)) {
             *reinterpret_cast<float4*>(orow + r0) = make_float4(nrm(acc[rb][4 * g]), nrm(acc[rb][4 * g + 1]),
                                                                 nrm(acc[rb][4 * g + 2]), nrm(acc[rb][4 * g + 3]));
           } else {
@@ -176,13 +193,15 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
 
 }  // namespace
 
-template <int MODE>
+template <int MODE, int PREC>
 static void launch_role_projection(dim3 grid, hipStream_t stream, const uint16_t* xp, const float* factor, int64_t n,
-                                   int32_t d, int32_t rank, float* out, double* partial, float* head_scale) {
+                                   int32_t d, int32_t rank, float* out, int32_t out_ld, int32_t out_col, float weight,
+                                   double* partial, float* head_scale) {
   const int rb = (rank + 31) / 32;
-#define SPR_RP(DD, RBB)                                                                                       \
-  role_projection_kernel<DD, RBB, MODE><<<grid, RP_THREADS, 0, stream>>>(xp, factor, n, rank, out, partial, \
-                                                                          head_scale)
+#define SPR_RP(DD, RBB)                                                                                     \
+  role_projection_kernel<DD, RBB, MODE, PREC><<<grid, RP_THREADS, 0, stream>>>(xp, factor, n, rank, out,  \
+                                                                              out_ld, out_col, weight,    \
+                                                                              partial, head_scale)
   if (d == 128) {
     if (rb == 1) SPR_RP(128, 1); else if (rb == 2) SPR_RP(128, 2); else if (rb == 3) SPR_RP(128, 3); else SPR_RP(128, 4);
   } else {
@@ -201,7 +220,8 @@ extern "C" int spr_role_projection_rms(const void* x, const float* factor, int64
   SPR_REQUIRE(x && factor && out, "spr_role_projection_rms: null pointer");
   SPR_REQUIRE(bh <= 65535, "spr_role_projection_rms: too many heads");
   const dim3 grid(static_cast<uint32_t>((n + RP_TOKENS - 1) / RP_TOKENS), static_cast<uint32_t>(bh));
-  launch_role_projection<0>(grid, stream, static_cast<const uint16_t*>(x), factor, n, d, rank, out, nullptr, nullptr);
+  launch_role_projection<0, 0>(grid, stream, static_cast<const uint16_t*>(x), factor, n, d, rank, out, rank, 0, 1.0f,
+                               nullptr, nullptr);
   SPR_LAUNCHED("role_projection_kernel");
   return SPR_OK;
 }
@@ -210,13 +230,18 @@ extern "C" size_t spr_role_k_projection_workspace(int64_t bh, int64_t n) {
   return static_cast<size_t>(bh) * static_cast<size_t>((n + RP_TOKENS - 1) / RP_TOKENS) * sizeof(double);
 }
 
-extern "C" int spr_role_k_projection(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d,
-                                     int32_t rank, float* out, float* key_scale, void* workspace,
-                                     size_t workspace_bytes, hipStream_t stream) {
+extern "C" int spr_role_k_projection_ex(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d,
+                                        int32_t rank, int32_t precision, float weight, float* out, int32_t out_ld,
+                                        int32_t out_col, float* key_scale, void* workspace, size_t workspace_bytes,
+                                        hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && n >= 0, "spr_role_k_projection: bad size");
   SPR_REQUIRE(d == 64 || d == 128, "spr_role_k_projection: head dim must be 64 or 128 (got %d)", d);
   SPR_REQUIRE(rank >= 1 && rank <= RP_MAX_R, "spr_role_k_projection: rank must be in [1, %d] (got %d)", RP_MAX_R,
               rank);
+  SPR_REQUIRE(precision >= 0 && precision <= 2, "spr_role_k_projection: precision must be 0, 1 or 2 (got %d)",
+              precision);
+  SPR_REQUIRE(out_col >= 0 && out_ld >= out_col + rank, "spr_role_k_projection: columns %d + %d exceed rows of %d",
+              out_col, rank, out_ld);
   if (bh == 0) return SPR_OK;
   SPR_REQUIRE(n >= 1, "spr_role_k_projection: no tokens");
   SPR_REQUIRE(x && factor && out && key_scale, "spr_role_k_projection: null pointer");
@@ -228,9 +253,22 @@ extern "C" int spr_role_k_projection(const void* x, const float* factor, int64_t
   const dim3 grid(static_cast<uint32_t>((n + RP_TOKENS - 1) / RP_TOKENS), static_cast<uint32_t>(bh));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   double* part = static_cast<double*>(workspace);
-  launch_role_projection<1>(grid, stream, xp, factor, n, d, rank, nullptr, part, nullptr);
-  SPR_LAUNCHED("role_projection_kernel<sum of squares>");
-  launch_role_projection<2>(grid, stream, xp, factor, n, d, rank, out, part, key_scale);
-  SPR_LAUNCHED("role_projection_kernel<head scale>");
+#define SPR_KP(PP)                                                                                             \
+  do {                                                                                                         \
+    launch_role_projection<1, PP>(grid, stream, xp, factor, n, d, rank, nullptr, 0, 0, 1.0f, part, nullptr);   \
+    SPR_LAUNCHED("role_projection_kernel<sum of squares>");                                                    \
+    launch_role_projection<2, PP>(grid, stream, xp, factor, n, d, rank, out, out_ld, out_col, weight, part,     \
+                                  key_scale);                                                                  \
+    SPR_LAUNCHED("role_projection_kernel<head scale>");                                                        \
+  } while (0)
+  if (precision == 0) SPR_KP(0); else if (precision == 1) SPR_KP(1); else SPR_KP(2);
+#undef SPR_KP
   return SPR_OK;
+}
+
+extern "C" int spr_role_k_projection(const void* x, const float* factor, int64_t bh, int64_t n, int32_t d,
+                                     int32_t rank, float* out, float* key_scale, void* workspace,
+                                     size_t workspace_bytes, hipStream_t stream) {
+  return spr_role_k_projection_ex(x, factor, bh, n, d, rank, 0, 1.0f, out, rank, 0, key_scale, workspace,
+                                  workspace_bytes, stream);
 }

@@ -80,20 +80,30 @@ def warm_metric_factor(metric: torch.Tensor, prev_state: torch.Tensor, rank: int
 
 
 def project_rows(x: torch.Tensor, factor: torch.Tensor, *, divisor: torch.Tensor | None = None, tf32: bool = False,
-                 row_rms: bool = False, eps: float = 1e-6) -> torch.Tensor:
-    """(x [BH, M, D] . factor [BH, D, r]) / divisor[h], optionally TF32-rounded operands and
-    row-RMS normalisation; fp32 [BH, M, r]."""
-    dev = _lib.require_gpu(x, factor, divisor, what="row projection")
+                 row_rms: bool = False, eps: float = 1e-6, precision: str | None = None, weight: float = 1.0,
+                 out: torch.Tensor | None = None, out_col: int = 0) -> torch.Tensor:
+    """(x [BH, M, D] . factor [BH, D, r]) / divisor[h] times weight, optionally row-RMS
+    normalised; fp32 [BH, M, r], or columns out_col .. out_col + r of out [BH, M, C].  The
+    operands are fp32, or both rounded to TF32 (tf32, or precision "high") or to bf16
+    (precision "medium"); precision "highest" is fp32."""
+    dev = _lib.require_gpu(x, factor, divisor, out, what="row projection")
     if x.ndim != 3 or factor.ndim != 3 or x.shape[0] != factor.shape[0] or x.shape[2] != factor.shape[1]:
         raise RuntimeError(f"Projection shape mismatch: x={tuple(x.shape)}, factor={tuple(factor.shape)}.")
     bh, m, d = x.shape
     r = factor.shape[2]
+    prec = 1 if tf32 else 0
+    if precision is not None:
+        prec = {"highest": 0, "high": 1, "medium": 2}[precision]
     xc = x.float().contiguous()
     fc = factor.float().contiguous()
     dv = None if divisor is None else divisor.float().reshape(bh).contiguous()
-    out = torch.empty((bh, m, r), dtype=torch.float32, device=dev)
-    _lib.call("spr_project_rows", _lib.ptr(xc), _lib.ptr(fc), _lib.ptr(dv), bh, m, d, r, int(bool(tf32)),
-              int(bool(row_rms)), float(eps), _lib.ptr(out), _lib.stream(dev))
+    if out is None:
+        out = torch.empty((bh, m, r), dtype=torch.float32, device=dev)
+    elif (out.ndim != 3 or tuple(out.shape[:2]) != (bh, m) or out.dtype != torch.float32 or not out.is_contiguous()
+          or out_col < 0 or out_col + r > out.shape[2]):
+        raise RuntimeError(f"Projection output must be contiguous fp32 [{bh}, {m}, >= {out_col + r}].")
+    _lib.call("spr_project_rows_ex", _lib.ptr(xc), _lib.ptr(fc), _lib.ptr(dv), bh, m, d, r, prec, int(bool(row_rms)),
+              float(eps), float(weight), _lib.ptr(out), int(out.shape[2]), int(out_col), _lib.stream(dev))
     return out
 
 

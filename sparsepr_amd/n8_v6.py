@@ -7,9 +7,8 @@ and Q, original-space centroids, the K/V permutation, SVG-EAR / attention-mass s
 scores, fixed-density or top-p key budgets and the exact budget selector.
 `N8V6Core.repair` runs the probe selection, dense probe attention, fit preparation, the
 reduced-rank fit, the apply and the exact scatter.  Every compute step is a HIP kernel of
-libsparsepr_hip.so.  Configurations whose kernels are not built (joint K/V role features,
-Householder-QR factor updates, other projection precisions, output_role repair) raise
-NotImplementedError.
+libsparsepr_hip.so.  Configurations whose kernels are not built (Householder-QR factor
+updates, output_role repair) raise NotImplementedError.
 """
 
 from __future__ import annotations
@@ -26,7 +25,8 @@ from . import operator_kmeans as _ok
 from .kernels import role_metric as _rm
 from .kernels.attention import dense_attention
 from .kernels.permute import argsort_labels, permute_tensor_by_labels_triton
-from .kernels.role_projection import role_k_projection_normalize, role_projection_rms_triton
+from .kernels.role_projection import (role_k_projection_normalize, role_kv_projection_normalize,
+                                      role_projection_rms_triton)
 from .kernels.selection import MODE_N8_NATIVE, MODE_TRITON, select_budget, top_p_key_budgets
 from .kernels.svg_ear import (attention_mass_scores_triton, svg_ear_grouped_value_error_scores_triton,
                               svg_ear_value_error_scores_triton)
@@ -231,20 +231,23 @@ class N8V6Core:
 
     def _check_route_config(self, dim: int) -> None:
         cfg = self.config
-        if cfg.role_v_weight > 0.0:
-            raise NotImplementedError("N8 routing with role_v_weight > 0 (joint K/V role features) is not built "
-                                      "for the MI355X kernels.")
         if cfg.factor_orthogonalization not in _rm.ORTHO or cfg.factor_ritz_mode not in _rm.RITZ:
             raise NotImplementedError(
                 f"factor_orthogonalization={cfg.factor_orthogonalization!r} / factor_ritz_mode="
                 f"{cfg.factor_ritz_mode!r} are not built for the MI355X kernels (Cholesky-QR variants and the "
                 "rayleigh_cholesky, diagonal and previous_scale finishes are).")
-        if not cfg.compile_role_kv_projection or cfg.role_kv_matmul_precision != "high":
-            raise NotImplementedError(
-                "The MI355X K role projection computes the compiled projection at role_kv_matmul_precision "
-                "'high' (TF32 factor); other projection precisions are not built.")
-        if max(cfg.role_q_rank, cfg.role_k_rank) > 64 or dim not in (64, 128):
-            raise NotImplementedError("N8 routing on the MI355X kernels needs head_dim 64 or 128 and ranks <= 64.")
+        ranks = (cfg.role_q_rank, cfg.role_k_rank) + ((cfg.role_v_rank,) if cfg.role_v_weight > 0.0 else ())
+        k_feature_dim = cfg.role_k_rank + (cfg.role_v_rank if cfg.role_v_weight > 0.0 else 0)
+        if max(ranks) > 64 or dim not in (64, 128) or k_feature_dim > 128:
+            raise NotImplementedError("N8 routing on the MI355X kernels needs head_dim 64 or 128, ranks <= 64 and "
+                                      "K role features (role_k_rank, + role_v_rank when role_v_weight > 0) <= 128.")
+
+    def _kv_precision(self) -> str:
+        """The fp32 matmul precision of the K (and V) role projections (n8_v6.py:658-704): the
+        compiled projections run under role_kv_matmul_precision; the uncompiled ones are plain
+        fp32 bmm (project_tokens), which is "highest"."""
+        cfg = self.config
+        return cfg.role_kv_matmul_precision if cfg.compile_role_kv_projection else "highest"
 
     def _updated_factor(self, metric, previous, current, rank):
         """n8_v6.py:478-519: the cold eigen factor on the first call, then one warm subspace
@@ -317,27 +320,55 @@ class N8V6Core:
             torch.cuda.synchronize(q_video.device)
             started[0] = time.perf_counter()
 
-        # ---- K role factor (n8_v6.py:611-657)
+        # ---- K (and V) role factors (n8_v6.py:611-657)
+        joint_v = cfg.role_v_weight > 0.0
         refresh = (self.q_factor_current is None or self.k_factor_current is None
+                   or (joint_v and self.v_factor_current is None)
                    or self.route_call_index % cfg.factor_refresh_every == 0)
         if refresh:
             k_metric = _ok.key_metric_from_queries(q_metric_source, metric_sample_tokens)
+            v_metric = _ok.value_metric_from_values(v, cfg.metric_sample_tokens) if joint_v else None
             if self.diagnostic_callback is not None:
-                self._emit_diagnostic("clustering", tensors={"k_role_metric": k_metric},
+                metric_tensors = {"k_role_metric": k_metric}
+                if v_metric is not None:
+                    metric_tensors["v_role_metric"] = v_metric
+                self._emit_diagnostic("clustering", tensors=metric_tensors,
                                       scalars={"phase": "kv_metrics_before_factorization"})
             k_factor, self.k_factor_state, self.k_factor_recovery_mask = self._updated_factor(
                 k_metric, self.k_factor_state, self.k_factor_current, cfg.role_k_rank)
             self.k_factor_current = k_factor
-            self.v_factor_recovery_mask = torch.zeros(k_factor.shape[0], device=k_factor.device, dtype=torch.bool)
+            if v_metric is not None:
+                v_factor, self.v_factor_state, self.v_factor_recovery_mask = self._updated_factor(
+                    v_metric, self.v_factor_state, self.v_factor_current, cfg.role_v_rank)
+                self.v_factor_current = v_factor
+            else:
+                v_factor = None
+                self.v_factor_recovery_mask = torch.zeros(k_factor.shape[0], device=k_factor.device,
+                                                          dtype=torch.bool)
         else:
             k_factor = self.k_factor_current
+            v_factor = self.v_factor_current if joint_v else None
         profile_mark("kv_metric_factor")
-        # ---- K role features and the warm start (n8_v6.py:658-704): TF32 projection,
-        # one RMS scale per head
-        k_features, k_scale = role_k_projection_normalize(k, k_factor)
+        # ---- K role features and the warm start (n8_v6.py:658-704): the projection under the
+        # K/V matmul precision, one RMS scale per head (and the weighted V features beside the K
+        # ones when role_v_weight > 0)
+        precision = self._kv_precision()
+        if joint_v:
+            k_features, k_scale, v_scale = role_kv_projection_normalize(k, v, k_factor, v_factor, cfg.role_v_weight,
+                                                                        precision=precision)
+        else:
+            k_features, k_scale = role_k_projection_normalize(k, k_factor, precision=precision)
+            v_scale = None
         k_init = None
         if self.k_centroids is not None:
-            k_init = _rm.project_rows(self.k_centroids, k_factor, divisor=k_scale, tf32=True)
+            if joint_v:
+                k_init = torch.empty((self.k_centroids.shape[0], self.k_centroids.shape[1], k_features.shape[2]),
+                                     device=k_features.device, dtype=torch.float32)
+                _rm.project_rows(self.k_centroids, k_factor, divisor=k_scale, precision=precision, out=k_init)
+                _rm.project_rows(self.v_centroids, v_factor, divisor=v_scale, precision=precision,
+                                 weight=cfg.role_v_weight, out=k_init, out_col=cfg.role_k_rank)
+            else:
+                k_init = _rm.project_rows(self.k_centroids, k_factor, divisor=k_scale, precision=precision)
         profile_mark("kv_projection_init")
         k_iters = cfg.kmeans_iter_step if self.initialized else cfg.kmeans_iter_init
         k_backend = cfg.kmeans_backend

@@ -73,7 +73,7 @@ def _check_scores(scores, ref):
 def _check_call(oracle, core, q, k, v, cap, route, cfg, prev=None):
     """Stagewise checks of one route call.  prev: the state before the call (warm calls)."""
     from sparsepr_amd import operator_kmeans as ok
-    from sparsepr_amd.kernels.role_projection import role_k_projection_normalize
+    from sparsepr_amd.kernels.role_projection import role_k_projection_normalize, role_kv_projection_normalize
 
     B, H, N, D = q.shape
     qf = q.reshape(H, N, D)
@@ -95,10 +95,36 @@ def _check_call(oracle, core, q, k, v, cap, route, cfg, prev=None):
             cfg.factor_cholesky_qr_ridge)
         assert not rrec.any() and not core.k_factor_recovery_mask.any()
         assert np.abs(kfac - rf).max() <= 2e-3 * np.abs(rf).max()
-    # K role features (the projection has its own tests) and the K k-means: the final labels
-    # are the TF32 argmin of the centroids entering the last iteration, which a GPU Lloyd with
-    # one iteration fewer from the route's initialisation reproduces (warm calls)
-    kfeat, kscale = role_k_projection_normalize(kf, core.k_factor_current)
+    joint = cfg.role_v_weight > 0.0
+    precision = cfg.role_kv_matmul_precision if cfg.compile_role_kv_projection else "highest"
+    if joint:
+        # V metric: the centred covariance of the deterministic V sample, and the V factor
+        v_metric = cap.get("v_role_metric")
+        assert _rel(v_metric.cpu().numpy(), oracle.role_metric(vn, rows=pos, center=True)) <= 1e-5
+        vfac = core.v_factor_current.cpu().numpy()
+        if prev is None:
+            assert _rel(_gram(vfac), _gram(oracle.metric_factor(v_metric.cpu().numpy(), cfg.role_v_rank))) <= 1e-3
+        else:
+            rf, rb, rrec = oracle.warm_subspace_metric_factor(
+                v_metric.cpu().numpy(), prev["v_state"], cfg.role_v_rank, cfg.factor_power_iters,
+                cfg.factor_orthogonalization, cfg.factor_ritz_mode, cfg.factor_rayleigh_ridge,
+                cfg.factor_cholesky_qr_ridge)
+            assert not rrec.any() and not core.v_factor_recovery_mask.any()
+            assert np.abs(vfac - rf).max() <= 2e-3 * np.abs(rf).max()
+    # K role features under the K/V matmul precision (joint with the weighted V features) and
+    # the K k-means: the final labels are the TF32 argmin of the centroids entering the last
+    # iteration, which a GPU Lloyd with one iteration fewer from the route's initialisation
+    # reproduces (warm calls)
+    if joint:
+        kfeat, kscale, vscale = role_kv_projection_normalize(kf, vf, core.k_factor_current, core.v_factor_current,
+                                                             cfg.role_v_weight, precision=precision)
+        ref_feat = oracle.role_kv_projection_normalize(kn, vn, core.k_factor_current.cpu().numpy(),
+                                                       core.v_factor_current.cpu().numpy(), cfg.role_v_weight,
+                                                       precision)[0]
+    else:
+        kfeat, kscale = role_k_projection_normalize(kf, core.k_factor_current, precision=precision)
+        ref_feat = oracle.role_k_projection_normalize(kn, core.k_factor_current.cpu().numpy(), precision)[0]
+    assert np.abs(kfeat.cpu().numpy().astype(np.float64) - ref_feat).max() <= 2e-5 * max(np.abs(ref_feat).max(), 1)
     klab = route.k_labels.cpu().numpy()
     ksz = route.k_cluster_sizes.cpu().numpy()
     assert (ksz == np.stack([np.bincount(r, minlength=cfg.num_k_centroids) for r in klab])).all()
@@ -106,7 +132,10 @@ def _check_call(oracle, core, q, k, v, cap, route, cfg, prev=None):
         from sparsepr_amd.flash_kmeans.kmeans_impl import lloyd
         from sparsepr_amd.kernels.role_metric import project_rows
 
-        kinit = project_rows(prev["k_centroids"], core.k_factor_current, divisor=kscale, tf32=True)
+        kinit = project_rows(prev["k_centroids"], core.k_factor_current, divisor=kscale, precision=precision)
+        if joint:
+            kinit = torch.cat((kinit, project_rows(prev["v_centroids"], core.v_factor_current, divisor=vscale,
+                                                   precision=precision, weight=cfg.role_v_weight)), dim=2)
         iters = route.k_kmeans_iters
         start = kinit if iters == 1 else lloyd(kfeat, cfg.num_k_centroids, iters - 1, 0.0, kinit).centroids
         ref, dist, xsq = oracle.kmeans_assign_tf32(kfeat.cpu().numpy(), start.cpu().numpy())
@@ -175,6 +204,41 @@ def test_n8_route_stagewise_cold_and_warm(dev, oracle):
     route2 = core.route(q2, k2, v2)
     torch.cuda.synchronize()
     assert route2.k_kmeans_iters <= cfg.kmeans_iter_step and core.route_call_index == 2
+    _check_call(oracle, core, q2, k2, v2, cap2, route2, cfg, prev=prev)
+
+
+def _state_of(core):
+    return {"k_state": core.k_factor_state.cpu().numpy(), "k_centroids": core.k_centroids.clone(),
+            "v_state": None if core.v_factor_state is None else core.v_factor_state.cpu().numpy(),
+            "v_centroids": core.v_centroids.clone(), "k_centroids_np": core.k_centroids.cpu().numpy(),
+            "v_centroids_np": core.v_centroids.cpu().numpy(), "q_centroids_np": core.q_centroids.cpu().numpy()}
+
+
+@pytest.mark.parametrize("v_weight,precision,compiled", [(0.5, "high", True), (0.0, "highest", True),
+                                                         (0.0, "medium", True), (0.7, "medium", False),
+                                                         (0.0, "high", False)])
+def test_n8_route_joint_kv_features_and_precisions(dev, oracle, v_weight, precision, compiled):
+    """role_v_weight > 0 (the V metric and factor, joint K/V role features for the K k-means,
+    n8_v6.py:611-704) and the K/V projection precisions (role_kv_matmul_precision; uncompiled
+    projections are fp32), stage by stage on a cold and a warm call."""
+    from sparsepr_amd.n8_v6 import N8V6Config, N8V6Core
+
+    q, k, v = _inputs(dev, seed=13)
+    cfg = N8V6Config(num_q_centroids=48, num_k_centroids=160, kmeans_iter_init=5, kmeans_iter_step=2,
+                     probe_rows=32, target_density=0.25, role_v_weight=v_weight, role_v_rank=16,
+                     role_kv_matmul_precision=precision, compile_role_kv_projection=compiled)
+    core = N8V6Core(cfg)
+    cap = _Capture()
+    core.diagnostic_callback = cap
+    route = core.route(q, k, v)
+    torch.cuda.synchronize()
+    _check_call(oracle, core, q, k, v, cap, route, cfg)
+    prev = _state_of(core)
+    q2, k2, v2 = (t + (0.05 * torch.randn(t.shape, device=dev)).to(t.dtype) for t in (q, k, v))
+    cap2 = _Capture()
+    core.diagnostic_callback = cap2
+    route2 = core.route(q2, k2, v2)
+    torch.cuda.synchronize()
     _check_call(oracle, core, q2, k2, v2, cap2, route2, cfg, prev=prev)
 
 

@@ -99,3 +99,56 @@ def test_role_k_projection_full_size(dev, oracle):
     got = key[:, rows].cpu().numpy().astype(np.float64)
     got_rows = got / np.sqrt((got ** 2).mean(axis=2, keepdims=True))
     assert np.abs(got_rows - p).max() < 1e-4
+
+
+@pytest.mark.parametrize("precision", ["high", "highest", "medium"])
+def test_role_k_projection_precisions(dev, oracle, precision):
+    """The K projection under role_kv_matmul_precision (n8_v6.py:77-86): the factor as TF32
+    ("high"), fp32 ("highest", three exact bf16 pieces) or bf16 ("medium") against the float64
+    oracle on the same operand rounding; the three differ from one another by more than the
+    tolerance, so each rounding is what is checked."""
+    from sparsepr_amd.kernels.role_projection import role_k_projection_normalize
+
+    rng = np.random.default_rng(31)
+    bh, n, d, r = 2, 3000, 128, 48
+    k = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    f = (rng.standard_normal((bh, d, r)) / np.sqrt(d)).astype(np.float32)
+    key, scale = role_k_projection_normalize(to_dev(k, dev, torch.bfloat16), to_dev(f, dev), precision=precision)
+    torch.cuda.synchronize()
+    got = key.cpu().numpy().astype(np.float64)
+    refs = {p: oracle.role_k_projection_normalize(k, f, p)[0].astype(np.float64) for p in ("high", "highest", "medium")}
+    assert np.abs(got - refs[precision]).max() < ATOL
+    for other, ref in refs.items():
+        if other != precision:
+            assert np.abs(got - ref).max() > 4 * ATOL
+    assert np.abs(scale.cpu().numpy() - oracle.role_k_projection_normalize(k, f, precision)[1]).max() <= 1e-5
+
+
+@pytest.mark.parametrize("precision", ["high", "highest", "medium"])
+def test_role_kv_projection_and_init(dev, oracle, precision):
+    """Joint K/V role features (_role_kv_projection_normalize_fp32, n8_v6.py:91-103): K features
+    in the first R_k columns, (v_weight value) / value_scale in the next R_v; the warm start
+    (_role_kv_init_projection_fp32, :118-126) through the strided, weighted row projection."""
+    from sparsepr_amd.kernels.role_metric import project_rows
+    from sparsepr_amd.kernels.role_projection import role_kv_projection_normalize
+
+    rng = np.random.default_rng(32)
+    bh, n, d, rk, rv, w, c = 2, 2500, 128, 48, 16, 0.35, 70
+    k = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    v = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    kf = (rng.standard_normal((bh, d, rk)) / np.sqrt(d)).astype(np.float32)
+    vf = (rng.standard_normal((bh, d, rv)) / np.sqrt(d)).astype(np.float32)
+    feats, ks, vs = role_kv_projection_normalize(to_dev(k, dev, torch.bfloat16), to_dev(v, dev, torch.bfloat16),
+                                                 to_dev(kf, dev), to_dev(vf, dev), w, precision=precision)
+    rfeat, rks, rvs = oracle.role_kv_projection_normalize(k, v, kf, vf, w, precision)
+    assert feats.shape == (bh, n, rk + rv)
+    assert np.abs(feats.cpu().numpy().astype(np.float64) - rfeat).max() < ATOL
+    assert np.abs(ks.cpu().numpy() - rks).max() <= 1e-5 and np.abs(vs.cpu().numpy() - rvs).max() <= 1e-5
+    kc = rng.standard_normal((bh, c, d)).astype(np.float32)
+    vc = rng.standard_normal((bh, c, d)).astype(np.float32)
+    init = torch.full((bh, c, rk + rv), 7.0, device=dev)
+    project_rows(to_dev(kc, dev), to_dev(kf, dev), divisor=ks, precision=precision, out=init)
+    project_rows(to_dev(vc, dev), to_dev(vf, dev), divisor=vs, precision=precision, weight=w, out=init, out_col=rk)
+    ref_init = np.concatenate((oracle.project_rows(kc, kf, rks.reshape(-1), precision=precision),
+                               oracle.project_rows(vc, vf, rvs.reshape(-1), precision=precision, weight=w)), axis=2)
+    assert np.abs(init.cpu().numpy() - ref_init).max() <= 1e-4 * np.abs(ref_init).max()

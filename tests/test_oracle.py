@@ -1167,3 +1167,28 @@ def test_cosmos_qkv_oracle_pins(oracle):
     qz, _, _ = oracle.cosmos25_qkv_norm_rope_bshd(q, k, v, w, w, np.zeros((s_len, 1, 1, d)), h, 1e-6)
     # cos(pi/2) is 6e-17, below half an ulp of any of these values
     assert np.array_equal(qt[..., :half], -qz[..., half:]) and np.array_equal(qt[..., half:], qz[..., :half])
+
+
+def test_matmul_precision_operands_and_joint_features(oracle):
+    """The fp32 matmul precisions as operand roundings: "medium" rounds to bf16 as torch's
+    bfloat16 conversion does, "high" to TF32, "highest" not at all; the joint K/V features put
+    the K features first and give the V half an RMS of exactly v_weight over the head."""
+    import torch
+
+    rng = np.random.default_rng(47)
+    x = (rng.standard_normal((3, 40)) * 10.0 ** rng.uniform(-3, 3, (3, 40))).astype(np.float32)
+    assert (oracle.matmul_precision_operand(x, "medium") == torch.from_numpy(x).to(torch.bfloat16).float().numpy()).all()
+    assert (oracle.matmul_precision_operand(x, "highest") == x).all()
+    assert (oracle.matmul_precision_operand(x, "high") == oracle.tf32_rna(x)).all()
+    k = oracle.to_bf16(rng.standard_normal((2, 300, 32)).astype(np.float32))
+    v = oracle.to_bf16(rng.standard_normal((2, 300, 32)).astype(np.float32))
+    kf = rng.standard_normal((2, 32, 12)).astype(np.float32)
+    vf = rng.standard_normal((2, 32, 4)).astype(np.float32)
+    feats, ks, vs = oracle.role_kv_projection_normalize(k, v, kf, vf, 0.25, "highest")
+    assert feats.shape == (2, 300, 16)
+    assert np.allclose(feats[:, :, :12], oracle.role_k_projection_normalize(k, kf, "highest")[0])
+    rms_v = np.sqrt((feats[:, :, 12:].astype(np.float64) ** 2).mean(axis=(1, 2)))
+    assert np.allclose(rms_v, 0.25, rtol=1e-6)
+    # a direct loop for one entry: (w * sum_d k v_f) / vs
+    p = sum(float(v[1, 7, j]) * float(vf[1, j, 2]) for j in range(32))
+    assert abs(feats[1, 7, 14] - 0.25 * p / float(vs[1, 0, 0])) <= 1e-6 * max(abs(feats[1, 7, 14]), 1e-6)
