@@ -412,8 +412,17 @@ int spr_metric_factor(const float* metric, int64_t bh, int32_t n, int32_t rank, 
  * per-head recovery when prev_factor is given): metric fp32 [bh, n, n], prev_state fp32
  * [bh, n, rank] (the previous basis), prev_factor fp32 [bh, n, rank] (nullable) -> factor,
  * state fp32 [bh, n, rank], recovered uint8 [bh] (nullable).  ortho 0 each_cholesky_qr,
- * 1 each_cholesky_qr2, 2 cholesky_qr; ritz 0 rayleigh_cholesky, 1 diagonal, 2 previous_scale.
- * n <= 128, rank <= 64. */
+ * 1 each_cholesky_qr2, 2 cholesky_qr, 3 each_qr, 4 final_qr (Householder QR, LAPACK's sign
+ * convention as torch.linalg.qr); ritz 0 rayleigh_cholesky, 1 diagonal, 2 previous_scale,
+ * 3 full (eigh of the Rayleigh matrix; columns in ascending eigenvalue order, signs are the
+ * eigensolver's).  n <= 128, rank <= 64.  The full finish needs
+ * spr_warm_metric_factor_workspace(bh, n, rank, ritz) bytes of workspace (0 for the others);
+ * spr_warm_metric_factor is the workspace-free form (ritz 0..2). */
+size_t spr_warm_metric_factor_workspace(int64_t bh, int32_t n, int32_t rank, int32_t ritz);
+int spr_warm_metric_factor_ex(const float* metric, const float* prev_state, const float* prev_factor, int64_t bh,
+                              int32_t n, int32_t rank, int32_t power_iters, int32_t ortho, int32_t ritz,
+                              float rayleigh_ridge, float cqr_ridge, float* factor, float* state, uint8_t* recovered,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream);
 int spr_warm_metric_factor(const float* metric, const float* prev_state, const float* prev_factor, int64_t bh,
                            int32_t n, int32_t rank, int32_t power_iters, int32_t ortho, int32_t ritz,
                            float rayleigh_ridge, float cqr_ridge, float* factor, float* state, uint8_t* recovered,

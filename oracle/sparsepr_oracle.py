@@ -826,11 +826,22 @@ def _cholesky_qr(x, ridge):
     return np.linalg.solve(l, xn.T).T, False
 
 
+def householder_qr(x):
+    """torch.linalg.qr(x, mode="reduced") (operator_kmeans.py:366,371,419): LAPACK geqrf +
+    orgqr, i.e. Householder reflections H_k = I - tau_k v_k v_k^T with v_k[k] = 1 and the
+    diagonal of R equal to -sign(alpha_k) |x_k| (alpha_k the pivot entry; tau_k = 0 when the
+    column below the pivot is zero).  numpy's qr is the same LAPACK pair."""
+    q, _ = np.linalg.qr(np.asarray(x, np.float64), mode="reduced")
+    return q
+
+
 def warm_subspace_metric_factor(metric, previous, rank, power_iters=2, orthogonalization="each_cholesky_qr2",
                                 ritz_mode="rayleigh_cholesky", rayleigh_ridge=1e-4, cholesky_qr_ridge=1e-5):
-    """operator_kmeans.py:219-477 restated in float64 for the Cholesky-QR orthogonalisations
-    and the rayleigh_cholesky / diagonal / previous_scale finishes.  previous [BH, D, r] is
-    the previous basis.  Returns (factor, basis, recovered bool [BH])."""
+    """operator_kmeans.py:219-477 restated in float64: the Householder-QR (each_qr, final_qr)
+    and Cholesky-QR orthogonalisations, and the full / rayleigh_cholesky / diagonal /
+    previous_scale finishes.  previous [BH, D, r] is the previous basis.  Returns
+    (factor, basis, recovered bool [BH]).  The full finish's columns follow eigh's ascending
+    eigenvalue order; their signs are eigh's (arbitrary), so only F F^T is defined."""
     m_all = np.asarray(metric, np.float64)
     prev_all = np.asarray(previous, np.float64)
     bh = m_all.shape[0]
@@ -838,14 +849,17 @@ def warm_subspace_metric_factor(metric, previous, rank, power_iters=2, orthogona
     for h in range(bh):
         m, prev = m_all[h], prev_all[h]
         prev_scales = np.maximum(np.linalg.norm(prev, axis=0), 1e-12)
-        basis = prev / prev_scales
+        basis = householder_qr(prev) if orthogonalization == "each_qr" else prev / prev_scales
         diag = None
         failed = False
         for it in range(power_iters):
             applied = m @ basis
             if ritz_mode == "diagonal" and it == power_iters - 1:
                 diag = (basis * applied).sum(0)
-            if orthogonalization == "cholesky_qr":
+            if orthogonalization == "each_qr":
+                basis = householder_qr(applied)
+                continue
+            if orthogonalization in ("cholesky_qr", "final_qr"):
                 basis = applied / np.maximum(np.linalg.norm(applied, axis=0), 1e-12)
                 continue
             basis, f = _cholesky_qr(applied, cholesky_qr_ridge)
@@ -853,7 +867,9 @@ def warm_subspace_metric_factor(metric, previous, rank, power_iters=2, orthogona
             if orthogonalization == "each_cholesky_qr2" and it == power_iters - 1:
                 basis, f = _cholesky_qr(basis, max(cholesky_qr_ridge, 1e-5))
                 failed |= f
-        if orthogonalization == "cholesky_qr":
+        if orthogonalization == "final_qr":
+            basis = householder_qr(basis)
+        elif orthogonalization == "cholesky_qr":
             basis, f = _cholesky_qr(basis, 1e-6)
             failed |= f
         if ritz_mode == "previous_scale":
@@ -861,6 +877,12 @@ def warm_subspace_metric_factor(metric, previous, rank, power_iters=2, orthogona
         elif ritz_mode == "diagonal":
             ev = np.maximum(diag, 0.0)
             factor = basis * np.sqrt(ev / max(ev.mean(), 1e-12))
+        elif ritz_mode == "full":
+            ray = basis.T @ (m @ basis)
+            ray = 0.5 * (ray + ray.T)
+            ev, rot = np.linalg.eigh(ray)
+            ev = np.maximum(ev, 0.0)
+            factor = (basis @ rot) * np.sqrt(ev / max(ev.mean(), 1e-12))
         else:
             ray = basis.T @ (m @ basis)
             ray = 0.5 * (ray + ray.T)

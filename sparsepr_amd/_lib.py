@@ -97,6 +97,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "spr_metric_factor": (ctypes.c_int, [_vp, _i64, _i32, _i32, _vp, _vp, _sz, _vp]),
     "spr_warm_metric_factor": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _vp,
                                               _vp, _vp, _vp]),
+    "spr_warm_metric_factor_workspace": (_sz, [_i64, _i32, _i32, _i32]),
+    "spr_warm_metric_factor_ex": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _vp,
+                                                 _vp, _vp, _vp, _sz, _vp]),
     "spr_project_rows": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _vp, _vp]),
     "spr_project_rows_ex": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _f32, _vp, _i32,
                                            _i32, _vp]),

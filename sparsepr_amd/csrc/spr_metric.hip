@@ -4,9 +4,9 @@
 //   covariance / key_metric_from_queries / value_metric_from_values (:62-92, :491-498)
 //   query_metric_from_key_centroids (:517-531)
 //   metric_factor (:95-151)
-//   warm_subspace_metric_factor with each_cholesky_qr(2) / cholesky_qr and the
-//     rayleigh_cholesky, diagonal and previous_scale finishes (:219-477),
-//     cholesky_with_device_fallback (:154-216)
+//   warm_subspace_metric_factor with every orthogonalisation (each_qr, final_qr,
+//     each_cholesky_qr(2), cholesky_qr) and every finish (full, rayleigh_cholesky, diagonal,
+//     previous_scale) (:219-477), cholesky_with_device_fallback (:154-216)
 //   project_tokens / normalize_rows_rms and the compiled K-centroid projection
 //     (:534-555; src/sparsepr/models/common/n8_v6.py:141-178)
 // and the per-head recovery of N8V6Core._updated_factor (n8_v6.py:478-519).
@@ -15,8 +15,10 @@
 //                      one 32 x 32 output tile per workgroup, rows staged in LDS, fp32.
 // warm_factor_kernel   one 1024-thread workgroup per head with the metric (128 x 128), the basis
 //                      and its image in LDS: metric . basis products, column normalisation,
-//                      Gram, Cholesky (one wave), triangular solves, Rayleigh matrix, fallback
-//                      Cholesky, all fp32.
+//                      Gram, Cholesky (one wave), triangular solves, Householder QR (columns
+//                      register resident, one barrier per reflector), Rayleigh matrix,
+//                      fallback Cholesky, all fp32.  The full finish hands the Rayleigh
+//                      matrix to spr_sym_top_eig and warm_full_finish_kernel.
 // factor_scale_kernel  eigenvectors x sqrt(max(lambda, 0) / max(mean lambda, 1e-12)).
 // project_rows_kernel  one wave per row: p = x . F (fp32, or both operands rounded to TF32 as
 //                      a "high"-precision fp32 matmul does, or to bf16 as a "medium" one
@@ -183,8 +185,8 @@ constexpr int WF_THREADS = 1024;
 constexpr int LDM = MET_MAX_D + 4;  // metric row
 constexpr int LDB = MET_MAX_R + 4;  // basis row
 
-enum WarmOrtho { ORTHO_EACH_CQR = 0, ORTHO_EACH_CQR2 = 1, ORTHO_FINAL_CQR = 2 };
-enum WarmRitz { RITZ_RAYLEIGH_CHOLESKY = 0, RITZ_DIAGONAL = 1, RITZ_PREVIOUS_SCALE = 2 };
+enum WarmOrtho { ORTHO_EACH_CQR = 0, ORTHO_EACH_CQR2 = 1, ORTHO_FINAL_CQR = 2, ORTHO_EACH_QR = 3, ORTHO_FINAL_QR = 4 };
+enum WarmRitz { RITZ_RAYLEIGH_CHOLESKY = 0, RITZ_DIAGONAL = 1, RITZ_PREVIOUS_SCALE = 2, RITZ_FULL = 3 };
 
 struct WarmSmem {
   __attribute__((aligned(16))) float m[MET_MAX_D * LDM];  // metric
@@ -193,6 +195,7 @@ struct WarmSmem {
   __attribute__((aligned(16))) float g[MET_MAX_R * LDB];  // Gram / Rayleigh matrix, its Cholesky factor (lower)
   __attribute__((aligned(16))) float lcol[MET_MAX_R];     // the Cholesky column in flight
   float colv[MET_MAX_R];      // per-column values (norms, diagonal Ritz values, scales)
+  float tau[MET_MAX_R];       // Householder scalars
   float scal[4];
   int32_t fail;
 };
@@ -391,14 +394,106 @@ __device__ __forceinline__ bool wf_cholesky_qr(WarmSmem& s, const float* src, in
   return !ok;
 }
 
+// Householder QR of a (n x r, rows of LDB floats) into q (n x r), as LAPACK geqrf + orgqr
+// (torch.linalg.qr, mode "reduced"): reflector k is H_k = I - tau_k v v^T with v[k] = 1,
+// v[i > k] = x[i] / (alpha - beta), beta = -sign(alpha) sqrt(alpha^2 + |x below|^2)
+// (alpha = x[k]; sign(+-0) = +), tau_k = (beta - alpha) / beta, and tau_k = 0 when x is zero
+// below the pivot; Q = H_0 ... H_{r-1} [I; 0].  Column j belongs to wave j % 16 and stays in
+// its registers (lane l: rows l and l + 64); the owner of column k + 1 forms reflector k + 1
+// as soon as H_k has been applied to it, so each reflector costs one barrier.  The
+// reflectors overwrite a (column k below the diagonal), tau goes to tau; Q is formed
+// backwards from them without barriers, each wave on its own columns.
+constexpr int QR_WAVES = WF_THREADS / 64;
+constexpr int QR_COLS = MET_MAX_R / QR_WAVES;
+__device__ __forceinline__ void qr_reflector(float x0, float x1, int k, int n, lds_f32* a, lds_f32* tau) {
+  const int lane = threadIdx.x & 63, i0 = lane, i1 = lane + 64;
+  const float below = (i0 > k && i0 < n ? x0 * x0 : 0.0f) + (i1 > k && i1 < n ? x1 * x1 : 0.0f);
+  const float sigma = wave_sum(below);
+  const float alpha = lane_read(k < 64 ? x0 : x1, k & 63);
+  float tk = 0.0f, sk = 0.0f;
+  if (sigma != 0.0f) {
+    const float nrm = sqrtf(alpha * alpha + sigma);
+    const float beta = alpha >= 0.0f ? -nrm : nrm;
+    tk = (beta - alpha) / beta;
+    sk = 1.0f / (alpha - beta);
+  }
+  if (i0 > k && i0 < n) a[i0 * LDB + k] = x0 * sk;
+  if (i1 > k && i1 < n) a[i1 * LDB + k] = x1 * sk;
+  if (lane == 0) tau[k] = tk;
+}
+__device__ __noinline__ void wf_householder_qr(lds_f32* a, lds_f32* q, lds_f32* tau, int n, int r) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, i0 = lane, i1 = lane + 64;
+  float col[QR_COLS][2];
+#pragma unroll
+  for (int c = 0; c < QR_COLS; ++c) {
+    const int j = wv + QR_WAVES * c;
+    col[c][0] = j < r && i0 < n ? a[i0 * LDB + j] : 0.0f;
+    col[c][1] = j < r && i1 < n ? a[i1 * LDB + j] : 0.0f;
+  }
+  if (wv == 0) qr_reflector(col[0][0], col[0][1], 0, n, a, tau);
+  __syncthreads();
+  for (int k = 0; k < r; ++k) {
+    const float v0 = i0 == k ? 1.0f : (i0 > k && i0 < n ? a[i0 * LDB + k] : 0.0f);
+    const float v1 = i1 == k ? 1.0f : (i1 > k && i1 < n ? a[i1 * LDB + k] : 0.0f);
+    const float tk = tau[k];
+#pragma unroll
+    for (int c = 0; c < QR_COLS; ++c) {
+      const int j = wv + QR_WAVES * c;
+      if (j > k && j < r) {
+        const float dot = wave_sum(v0 * col[c][0] + v1 * col[c][1]);
+        col[c][0] = __builtin_fmaf(-tk * dot, v0, col[c][0]);
+        col[c][1] = __builtin_fmaf(-tk * dot, v1, col[c][1]);
+        if (j == k + 1) qr_reflector(col[c][0], col[c][1], k + 1, n, a, tau);
+      }
+    }
+    __syncthreads();
+  }
+  float qc[QR_COLS][2];
+#pragma unroll
+  for (int c = 0; c < QR_COLS; ++c) qc[c][0] = qc[c][1] = 0.0f;
+  for (int k = r - 1; k >= 0; --k) {
+    const float v0 = i0 == k ? 1.0f : (i0 > k && i0 < n ? a[i0 * LDB + k] : 0.0f);
+    const float v1 = i1 == k ? 1.0f : (i1 > k && i1 < n ? a[i1 * LDB + k] : 0.0f);
+    const float tk = tau[k];
+#pragma unroll
+    for (int c = 0; c < QR_COLS; ++c) {
+      const int j = wv + QR_WAVES * c;
+      if (j > k && j < r) {
+        const float dot = wave_sum(v0 * qc[c][0] + v1 * qc[c][1]);
+        qc[c][0] = __builtin_fmaf(-tk * dot, v0, qc[c][0]);
+        qc[c][1] = __builtin_fmaf(-tk * dot, v1, qc[c][1]);
+      } else if (j == k) {
+        qc[c][0] = (i0 == k ? 1.0f : 0.0f) - tk * v0;
+        qc[c][1] = (i1 == k ? 1.0f : 0.0f) - tk * v1;
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < QR_COLS; ++c) {
+    const int j = wv + QR_WAVES * c;
+    if (j < r) {
+      if (i0 < n) q[i0 * LDB + j] = qc[c][0];
+      if (i1 < n) q[i1 * LDB + j] = qc[c][1];
+    }
+  }
+  __syncthreads();
+}
+__device__ __forceinline__ void wf_qr(WarmSmem& s, int n, int r) {  // s.w -> s.b
+  wf_householder_qr((lds_f32*)s.w, (lds_f32*)s.b, (lds_f32*)s.tau, n, r);
+}
+
 // One head per workgroup.  metric [n][n]; prev_state [n][r] (the previous basis, or the cold
 // factor); prev_factor [n][r] (nullable: the previous factor); outputs factor, state [n][r]
 // and recovered[h] (1 = a Cholesky failed or a result is not finite; then, when prev_factor
-// is given, factor and state are the previous ones).
+// is given, factor and state are the previous ones).  The full finish instead writes the
+// basis [n][r], the Rayleigh matrix [r][r] (diag(1 .. r) when it is not finite, so the
+// eigensolver only sees finite input) and the Cholesky failure flag into the workspace
+// arrays full_basis / full_ray / full_flag, for warm_full_finish_kernel.
 __global__ __launch_bounds__(WF_THREADS, 1) void warm_factor_kernel(
     const float* __restrict__ metric, const float* __restrict__ prev_state, const float* __restrict__ prev_factor,
     int32_t n, int32_t r, int32_t power_iters, int32_t ortho, int32_t ritz, float rayleigh_ridge, float cqr_ridge,
-    float* __restrict__ factor, float* __restrict__ state, uint8_t* __restrict__ recovered) {
+    float* __restrict__ factor, float* __restrict__ state, uint8_t* __restrict__ recovered,
+    float* __restrict__ full_basis, float* __restrict__ full_ray, int32_t* __restrict__ full_flag) {
   __shared__ WarmSmem s;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int64_t h = blockIdx.x;
@@ -410,15 +505,20 @@ __global__ __launch_bounds__(WF_THREADS, 1) void warm_factor_kernel(
   __syncthreads();
   bool failed = false;
   // previous column scales (only the previous_scale finish uses them), then the
-  // column-normalised previous basis
+  // column-normalised previous basis, or (each_qr) the Householder QR of the previous one
   wf_colnorms(s, s.b, n, r);
   __shared__ float prev_scale[MET_MAX_R];
   if (t < r) prev_scale[t] = s.colv[t];
   for (int e = t; e < n * r; e += WF_THREADS) {
     const int i = e / r, c = e - i * r;
-    s.b[i * LDB + c] /= s.colv[c];
+    if (ortho == ORTHO_EACH_QR) {
+      s.w[i * LDB + c] = s.b[i * LDB + c];
+    } else {
+      s.b[i * LDB + c] /= s.colv[c];
+    }
   }
   __syncthreads();
+  if (ortho == ORTHO_EACH_QR) wf_qr(s, n, r);
   __shared__ float diag_vals[MET_MAX_R];
   for (int it = 0; it < power_iters; ++it) {
     wf_apply(s, n, r);  // w = m b
@@ -432,7 +532,9 @@ __global__ __launch_bounds__(WF_THREADS, 1) void warm_factor_kernel(
       }
       __syncthreads();
     }
-    if (ortho == ORTHO_FINAL_CQR) {
+    if (ortho == ORTHO_EACH_QR) {
+      wf_qr(s, n, r);
+    } else if (ortho == ORTHO_FINAL_CQR || ortho == ORTHO_FINAL_QR) {
       // unorthogonalised power step: columns rescaled to unit norm
       wf_colnorms(s, s.w, n, r);
       for (int e = t; e < n * r; e += WF_THREADS) {
@@ -453,13 +555,39 @@ __global__ __launch_bounds__(WF_THREADS, 1) void warm_factor_kernel(
       }
     }
   }
-  if (ortho == ORTHO_FINAL_CQR) {
+  if (ortho == ORTHO_FINAL_CQR || ortho == ORTHO_FINAL_QR) {
     for (int e = t; e < n * r; e += WF_THREADS) {
       const int i = e / r, c = e - i * r;
       s.w[i * LDB + c] = s.b[i * LDB + c];
     }
     __syncthreads();
-    failed |= wf_cholesky_qr(s, s.w, n, r, 1e-6f);
+    if (ortho == ORTHO_FINAL_QR) {
+      wf_qr(s, n, r);
+    } else {
+      failed |= wf_cholesky_qr(s, s.w, n, r, 1e-6f);
+    }
+  }
+  if (ritz == RITZ_FULL) {
+    // Rayleigh matrix R = b^T (m b), symmetrised, the basis and the failure flag to the
+    // workspace; the reduced eigh and the factor follow in their own launches
+    wf_apply(s, n, r);
+    wf_gram(s, s.b, s.w, n, r, true);
+    __shared__ int32_t ray_bad;
+    if (t == 0) ray_bad = 0;
+    __syncthreads();
+    for (int e = t; e < r * r; e += WF_THREADS) {
+      if (!(fabsf(s.g[(e / r) * LDB + (e % r)]) < __builtin_huge_valf())) ray_bad = 1;
+    }
+    __syncthreads();
+    float* bo = full_basis + h * n * r;
+    float* ro = full_ray + h * r * r;
+    for (int e = t; e < n * r; e += WF_THREADS) bo[e] = s.b[(e / r) * LDB + (e % r)];
+    for (int e = t; e < r * r; e += WF_THREADS) {
+      const int p = e / r, q = e - p * r;
+      ro[e] = ray_bad ? (p == q ? static_cast<float>(p + 1) : 0.0f) : s.g[p * LDB + q];
+    }
+    if (t == 0) full_flag[h] = failed ? 1 : 0;
+    return;
   }
   // finish: the factor goes to w, the basis stays in b
   if (ritz == RITZ_PREVIOUS_SCALE || ritz == RITZ_DIAGONAL) {
@@ -544,6 +672,50 @@ __global__ __launch_bounds__(WF_THREADS, 1) void warm_factor_kernel(
     const int i = e / r, c = e - i * r;
     fo[e] = keep_prev ? pf[e] : s.w[i * LDB + c];
     so[e] = keep_prev ? ps[e] : s.b[i * LDB + c];
+  }
+  if (t == 0 && recovered != nullptr) recovered[h] = rec ? 1 : 0;
+}
+
+// The full Rayleigh-Ritz finish (operator_kmeans.py:460-466) for one head per workgroup:
+// factor = basis . U . diag(sqrt(max(lambda, 0) / max(mean max(lambda, 0), 1e-12))) with U,
+// lambda the eigenpairs of the Rayleigh matrix in ascending order; then the recovery of
+// warm_factor_kernel (a failed Cholesky-QR, or a factor or basis that is not finite).
+__global__ __launch_bounds__(256) void warm_full_finish_kernel(
+    const float* __restrict__ basis, const float* __restrict__ vecs, const float* __restrict__ vals,
+    const int32_t* __restrict__ flag, const float* __restrict__ prev_state, const float* __restrict__ prev_factor,
+    int32_t n, int32_t r, float* __restrict__ factor, float* __restrict__ state, uint8_t* __restrict__ recovered) {
+  __shared__ float u[MET_MAX_R * (MET_MAX_R + 1)];
+  __shared__ float f[MET_MAX_D * MET_MAX_R];
+  __shared__ float scale[MET_MAX_R];
+  __shared__ int32_t nonfinite;
+  const int t = threadIdx.x;
+  const int64_t h = blockIdx.x;
+  const float* bh_ = basis + h * n * r;
+  const float* uh = vecs + h * r * r;
+  if (t == 0) {
+    const float* lh = vals + h * r;
+    float sum = 0.0f;
+    for (int c = 0; c < r; ++c) sum += fmaxf(lh[c], 0.0f);
+    const float norm = fmaxf(sum / static_cast<float>(r), 1e-12f);
+    for (int c = 0; c < r; ++c) scale[c] = sqrtf(fmaxf(lh[c], 0.0f) / norm);
+    nonfinite = 0;
+  }
+  for (int e = t; e < r * r; e += 256) u[(e / r) * (MET_MAX_R + 1) + (e % r)] = uh[e];
+  __syncthreads();
+  for (int e = t; e < n * r; e += 256) {
+    const int i = e / r, c = e - i * r;
+    float acc = 0.0f;
+    for (int k = 0; k < r; ++k) acc = __builtin_fmaf(bh_[i * r + k], u[k * (MET_MAX_R + 1) + c], acc);
+    const float fv = acc * scale[c];
+    f[e] = fv;
+    if (!(fabsf(fv) < __builtin_huge_valf()) || !(fabsf(bh_[e]) < __builtin_huge_valf())) nonfinite = 1;
+  }
+  __syncthreads();
+  const bool rec = flag[h] != 0 || nonfinite != 0;
+  const bool keep_prev = rec && prev_factor != nullptr;
+  for (int e = t; e < n * r; e += 256) {
+    factor[h * n * r + e] = keep_prev ? prev_factor[h * n * r + e] : f[e];
+    state[h * n * r + e] = keep_prev ? prev_state[h * n * r + e] : bh_[e];
   }
   if (t == 0 && recovered != nullptr) recovered[h] = rec ? 1 : 0;
 }
@@ -641,26 +813,71 @@ extern "C" int spr_metric_factor(const float* metric, int64_t bh, int32_t n, int
   return SPR_OK;
 }
 
+// Workspace of spr_warm_metric_factor_ex: the full finish (ritz 3) keeps, per head, the
+// basis [n][rank], the Rayleigh matrix and its eigenvectors [rank][rank], the eigenvalues
+// [rank] and a flag; the other finishes need none.
+extern "C" size_t spr_warm_metric_factor_workspace(int64_t bh, int32_t n, int32_t rank, int32_t ritz) {
+  if (ritz != RITZ_FULL || bh <= 0 || n <= 0 || rank <= 0) return 0;
+  const size_t per = static_cast<size_t>(n) * rank + 2 * static_cast<size_t>(rank) * rank + rank + 1;
+  return static_cast<size_t>(bh) * per * sizeof(float);
+}
+
 // warm_subspace_metric_factor + the per-head recovery of N8V6Core._updated_factor.
 // ortho: 0 each_cholesky_qr, 1 each_cholesky_qr2, 2 cholesky_qr (once, after the
-// normalised power steps); ritz: 0 rayleigh_cholesky, 1 diagonal, 2 previous_scale.
-extern "C" int spr_warm_metric_factor(const float* metric, const float* prev_state, const float* prev_factor,
-                                      int64_t bh, int32_t n, int32_t rank, int32_t power_iters, int32_t ortho,
-                                      int32_t ritz, float rayleigh_ridge, float cqr_ridge, float* factor, float* state,
-                                      uint8_t* recovered, hipStream_t stream) {
+// normalised power steps), 3 each_qr, 4 final_qr (Householder QR); ritz: 0 rayleigh_cholesky,
+// 1 diagonal, 2 previous_scale, 3 full (three launches: the subspace kernel, spr_sym_top_eig
+// on the Rayleigh matrices, the finish).
+extern "C" int spr_warm_metric_factor_ex(const float* metric, const float* prev_state, const float* prev_factor,
+                                         int64_t bh, int32_t n, int32_t rank, int32_t power_iters, int32_t ortho,
+                                         int32_t ritz, float rayleigh_ridge, float cqr_ridge, float* factor,
+                                         float* state, uint8_t* recovered, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && n >= 1 && n <= MET_MAX_D, "spr_warm_metric_factor: n=%d outside [1, %d]", n, MET_MAX_D);
   SPR_REQUIRE(rank >= 1 && rank <= MET_MAX_R && rank <= n, "spr_warm_metric_factor: rank %d outside [1, 64]", rank);
   SPR_REQUIRE(power_iters >= 1, "spr_warm_metric_factor: power_iters must be positive");
-  SPR_REQUIRE(ortho >= 0 && ortho <= 2 && ritz >= 0 && ritz <= 2, "spr_warm_metric_factor: bad mode");
+  SPR_REQUIRE(ortho >= 0 && ortho <= 4 && ritz >= 0 && ritz <= 3, "spr_warm_metric_factor: bad mode");
   SPR_REQUIRE(rayleigh_ridge > 0.0f && cqr_ridge > 0.0f, "spr_warm_metric_factor: ridges must be positive");
   SPR_REQUIRE(bh <= 65535, "spr_warm_metric_factor: too many heads");
   if (bh == 0) return SPR_OK;
   SPR_REQUIRE(metric && prev_state && factor && state, "spr_warm_metric_factor: null pointer");
+  const size_t need = spr_warm_metric_factor_workspace(bh, n, rank, ritz);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+    spr_set_error("spr_warm_metric_factor: the full finish needs a workspace of %zu bytes (got %zu)", need,
+                  workspace_bytes);
+    return SPR_EWORKSPACE;
+  }
+  float* fb = nullptr;
+  float* fr = nullptr;
+  float* fv = nullptr;
+  float* fl = nullptr;
+  int32_t* ff = nullptr;
+  if (ritz == RITZ_FULL) {
+    fb = static_cast<float*>(workspace);
+    fr = fb + bh * n * rank;
+    fv = fr + bh * rank * rank;
+    fl = fv + bh * rank * rank;
+    ff = reinterpret_cast<int32_t*>(fl + bh * rank);
+  }
   warm_factor_kernel<<<dim3(static_cast<uint32_t>(bh)), WF_THREADS, 0, stream>>>(
       metric, prev_state, prev_factor, n, rank, power_iters, ortho, ritz, rayleigh_ridge, cqr_ridge, factor, state,
-      recovered);
+      recovered, fb, fr, ff);
   SPR_LAUNCHED("warm_factor_kernel");
+  if (ritz == RITZ_FULL) {
+    const int st = spr_sym_top_eig(fr, bh, rank, rank, 1, fv, fl, stream);
+    if (st != SPR_OK) return st;
+    warm_full_finish_kernel<<<dim3(static_cast<uint32_t>(bh)), 256, 0, stream>>>(
+        fb, fv, fl, ff, prev_state, prev_factor, n, rank, factor, state, recovered);
+    SPR_LAUNCHED("warm_full_finish_kernel");
+  }
   return SPR_OK;
+}
+
+extern "C" int spr_warm_metric_factor(const float* metric, const float* prev_state, const float* prev_factor,
+                                      int64_t bh, int32_t n, int32_t rank, int32_t power_iters, int32_t ortho,
+                                      int32_t ritz, float rayleigh_ridge, float cqr_ridge, float* factor, float* state,
+                                      uint8_t* recovered, hipStream_t stream) {
+  return spr_warm_metric_factor_ex(metric, prev_state, prev_factor, bh, n, rank, power_iters, ortho, ritz,
+                                   rayleigh_ridge, cqr_ridge, factor, state, recovered, nullptr, 0, stream);
 }
 
 // out fp32 [bh, m, r] = (x [bh, m, d] . factor [bh, d, r]) / div[h] (div nullable), with

@@ -7,8 +7,8 @@ import torch
 
 from .. import _lib
 
-ORTHO = {"each_cholesky_qr": 0, "each_cholesky_qr2": 1, "cholesky_qr": 2}
-RITZ = {"rayleigh_cholesky": 0, "diagonal": 1, "previous_scale": 2}
+ORTHO = {"each_cholesky_qr": 0, "each_cholesky_qr2": 1, "cholesky_qr": 2, "each_qr": 3, "final_qr": 4}
+RITZ = {"rayleigh_cholesky": 0, "diagonal": 1, "previous_scale": 2, "full": 3}
 
 
 def role_metric(x: torch.Tensor, *, rows: torch.Tensor | None = None, sizes: torch.Tensor | None = None,
@@ -64,7 +64,8 @@ def warm_metric_factor(metric: torch.Tensor, prev_state: torch.Tensor, rank: int
                        orthogonalization: str = "each_cholesky_qr2", ritz_mode: str = "rayleigh_cholesky",
                        rayleigh_ridge: float = 1e-4, cholesky_qr_ridge: float = 1e-5):
     """One warm subspace update.  Returns (factor, state, recovered bool [BH]); with
-    prev_factor, recovered heads keep prev_factor / prev_state."""
+    prev_factor, recovered heads keep prev_factor / prev_state.  The full finish's columns
+    are in ascending eigenvalue order with the eigensolver's signs."""
     dev = _lib.require_gpu(metric, prev_state, prev_factor, what="warm metric factor")
     bh, n, _ = metric.shape
     m = metric.float().contiguous()
@@ -73,9 +74,12 @@ def warm_metric_factor(metric: torch.Tensor, prev_state: torch.Tensor, rank: int
     factor = torch.empty((bh, n, rank), dtype=torch.float32, device=dev)
     state = torch.empty((bh, n, rank), dtype=torch.float32, device=dev)
     rec = torch.empty((bh,), dtype=torch.uint8, device=dev)
-    _lib.call("spr_warm_metric_factor", _lib.ptr(m), _lib.ptr(ps), _lib.ptr(pf), bh, n, int(rank), int(power_iters),
-              ORTHO[orthogonalization], RITZ[ritz_mode], float(rayleigh_ridge), float(cholesky_qr_ridge),
-              _lib.ptr(factor), _lib.ptr(state), _lib.ptr(rec), _lib.stream(dev))
+    nbytes = int(_lib.query("spr_warm_metric_factor_workspace", bh, n, int(rank), RITZ[ritz_mode]))
+    ws = _lib.workspace(nbytes, dev) if nbytes > 0 else None
+    _lib.call("spr_warm_metric_factor_ex", _lib.ptr(m), _lib.ptr(ps), _lib.ptr(pf), bh, n, int(rank),
+              int(power_iters), ORTHO[orthogonalization], RITZ[ritz_mode], float(rayleigh_ridge),
+              float(cholesky_qr_ridge), _lib.ptr(factor), _lib.ptr(state), _lib.ptr(rec), _lib.ptr(ws), nbytes,
+              _lib.stream(dev))
     return factor, state, rec.bool()
 
 

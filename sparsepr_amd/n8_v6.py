@@ -231,11 +231,11 @@ class N8V6Core:
 
     def _check_route_config(self, dim: int) -> None:
         cfg = self.config
-        if cfg.factor_orthogonalization not in _rm.ORTHO or cfg.factor_ritz_mode not in _rm.RITZ:
-            raise NotImplementedError(
-                f"factor_orthogonalization={cfg.factor_orthogonalization!r} / factor_ritz_mode="
-                f"{cfg.factor_ritz_mode!r} are not built for the MI355X kernels (Cholesky-QR variants and the "
-                "rayleigh_cholesky, diagonal and previous_scale finishes are).")
+        # the names warm_subspace_metric_factor accepts (operator_kmeans.py:308-326)
+        if cfg.factor_orthogonalization not in _rm.ORTHO:
+            raise RuntimeError(f"Unknown subspace orthogonalization {cfg.factor_orthogonalization!r}.")
+        if cfg.factor_ritz_mode not in _rm.RITZ:
+            raise RuntimeError(f"Unknown Rayleigh--Ritz mode {cfg.factor_ritz_mode!r}.")
         ranks = (cfg.role_q_rank, cfg.role_k_rank) + ((cfg.role_v_rank,) if cfg.role_v_weight > 0.0 else ())
         k_feature_dim = cfg.role_k_rank + (cfg.role_v_rank if cfg.role_v_weight > 0.0 else 0)
         if max(ranks) > 64 or dim not in (64, 128) or k_feature_dim > 128:

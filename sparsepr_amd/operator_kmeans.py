@@ -95,7 +95,8 @@ def warm_subspace_metric_factor(metric, previous_factor, rank, *, power_iters=1,
                                 ritz_mode="full", rayleigh_ridge=1e-6, cholesky_qr_ridge=1e-4, return_basis=False,
                                 return_recovery_mask=False):
     """Subspace-iteration update of a previous top-r factor (:219-477), one fused kernel per
-    call.  Returns factor, or (factor, basis[, recovery_mask]) as the reference."""
+    call (three with the full finish: the subspace kernel, the reduced eigensolver, the
+    factor).  Returns factor, or (factor, basis[, recovery_mask]) as the reference."""
     if metric.ndim != 3 or metric.shape[1] != metric.shape[2]:
         raise RuntimeError(f"Expected batched square metrics, got {tuple(metric.shape)}.")
     if rank <= 0 or rank > metric.shape[-1]:
@@ -115,11 +116,6 @@ def warm_subspace_metric_factor(metric, previous_factor, rank, *, power_iters=1,
         raise RuntimeError(f"Unknown subspace orthogonalization {orthogonalization!r}.")
     if ritz_mode not in {"full", "rayleigh_cholesky", "diagonal", "previous_scale"}:
         raise RuntimeError(f"Unknown Rayleigh--Ritz mode {ritz_mode!r}.")
-    if orthogonalization not in _rm.ORTHO or ritz_mode not in _rm.RITZ:
-        raise NotImplementedError(
-            f"warm_subspace_metric_factor({orthogonalization!r}, {ritz_mode!r}) is not built for the MI355X "
-            "kernels: use a Cholesky-QR orthogonalization and the rayleigh_cholesky, diagonal or previous_scale "
-            "finish.")
     if rank > 64 or metric.shape[-1] > 128:
         raise NotImplementedError("warm_subspace_metric_factor on the MI355X kernels supports D <= 128, rank <= 64.")
     factor, basis, rec = _rm.warm_metric_factor(

@@ -47,7 +47,8 @@ def test_role_metric_sampled_and_masked(dev, oracle):
     assert _rel(got.cpu().numpy(), oracle.role_metric(v, center=True)) <= 1e-5
 
 
-@pytest.mark.parametrize("n,rank", [(128, 16), (128, 48), (128, 64), (64, 64), (100, 33), (128, 5)])
+@pytest.mark.parametrize("n,rank", [(128, 16), (128, 48), (128, 64), (64, 64), (100, 33), (128, 5), (48, 48),
+                                    (16, 16)])
 def test_sym_top_eig_matches_eigh(dev, oracle, n, rank):
     """Eigenvalues (Rayleigh quotients) within 1e-5 of the spectral norm of numpy's; the basis
     orthonormal to 1e-5; the projector on the top-`rank` subspace equal to numpy's to 1e-4
@@ -101,11 +102,19 @@ def test_metric_factor_cold(dev, oracle):
 
 @pytest.mark.parametrize("ortho,ritz", [("each_cholesky_qr2", "rayleigh_cholesky"),
                                         ("each_cholesky_qr", "diagonal"),
-                                        ("cholesky_qr", "previous_scale")])
+                                        ("cholesky_qr", "previous_scale"),
+                                        ("each_qr", "full"),
+                                        ("each_qr", "rayleigh_cholesky"),
+                                        ("final_qr", "diagonal"),
+                                        ("final_qr", "full"),
+                                        ("each_cholesky_qr2", "full")])
 def test_warm_subspace_factor(dev, oracle, ortho, ritz):
     """The warm update against the float64 restatement from the same previous basis: factor
-    within 2e-3 of its largest entry, basis within 1e-3; a NaN metric head is reported
-    recovered and, with prev_factor, keeps the previous factor and state."""
+    within 2e-3 of its largest entry, basis within 1e-3 (the Householder bases carry LAPACK's
+    signs, so they compare entry by entry too); the full finish's columns have the
+    eigensolver's signs, so its factor is compared through F F^T (1e-4 relative) and its
+    column norms (ascending eigenvalues).  A NaN metric head is reported recovered and, with
+    prev_factor, keeps the previous factor and state."""
     from sparsepr_amd import operator_kmeans as ok
     from sparsepr_amd.kernels.role_metric import warm_metric_factor
 
@@ -120,7 +129,11 @@ def test_warm_subspace_factor(dev, oracle, ortho, ritz):
     rf, rb, rrec = oracle.warm_subspace_metric_factor(m, prev, r, 2, ortho, ritz, 1e-4, 1e-5)
     assert not rec.any() and not rrec.any()
     fn, bn = f.cpu().numpy(), b.cpu().numpy()
-    assert np.abs(fn - rf).max() <= 2e-3 * np.abs(rf).max()
+    if ritz == "full":
+        assert _rel(np.einsum("bir,bjr->bij", fn, fn), np.einsum("bir,bjr->bij", rf, rf)) <= 1e-4
+        assert np.abs(np.linalg.norm(fn, axis=1) - np.linalg.norm(rf, axis=1)).max() <= 1e-4 * np.abs(rf).max()
+    else:
+        assert np.abs(fn - rf).max() <= 2e-3 * np.abs(rf).max()
     assert np.abs(bn - rb).max() <= 1e-3
     bad = m.copy()
     bad[2, 0, 5] = np.nan
@@ -129,7 +142,11 @@ def test_warm_subspace_factor(dev, oracle, ortho, ritz):
                                       power_iters=2, orthogonalization=ortho, ritz_mode=ritz)
     assert rec2.cpu().tolist() == [False, False, True]
     assert np.array_equal(f2[2].cpu().numpy(), prev_f[2]) and np.array_equal(s2[2].cpu().numpy(), prev[2])
-    assert np.abs(f2[:2].cpu().numpy() - rf[:2]).max() <= 2e-3 * np.abs(rf).max()
+    f2n = f2[:2].cpu().numpy()
+    if ritz == "full":
+        assert _rel(np.einsum("bir,bjr->bij", f2n, f2n), np.einsum("bir,bjr->bij", rf[:2], rf[:2])) <= 1e-4
+    else:
+        assert np.abs(f2n - rf[:2]).max() <= 2e-3 * np.abs(rf).max()
 
 
 def test_project_rows(dev, oracle):

@@ -1089,6 +1089,75 @@ def test_warm_subspace_factor_fixed_point(oracle):
     assert rec.tolist() == [False, True]
 
 
+def test_householder_qr_is_the_lapack_convention(oracle):
+    """The reference's torch.linalg.qr is LAPACK geqrf + orgqr: R's diagonal is
+    -sign(pivot) |column|, and a column already zero below its pivot takes tau = 0 (Q's
+    column is e_k).  Hand-worked: [[3], [4]] -> Q = [[-0.6], [-0.8]]; [[2, 1], [0, 3], [0, 4]]
+    -> Q = [[1, 0], [0, -0.6], [0, -0.8]] (H_0 = I, then v = [1, 1/2], tau = 1.6)."""
+    assert np.allclose(oracle.householder_qr(np.array([[3.0], [4.0]])), [[-0.6], [-0.8]], atol=1e-15)
+    got = oracle.householder_qr(np.array([[2.0, 1.0], [0.0, 3.0], [0.0, 4.0]]))
+    assert np.allclose(got, [[1.0, 0.0], [0.0, -0.6], [0.0, -0.8]], atol=1e-15)
+    rng = np.random.default_rng(55)
+    a = rng.standard_normal((9, 4))
+    q = oracle.householder_qr(a)
+    r = q.T @ a
+    assert np.allclose(q.T @ q, np.eye(4), atol=1e-12) and np.allclose(np.tril(r, -1), 0.0, atol=1e-12)
+    assert np.sign(r[0, 0]) == -np.sign(a[0, 0])
+
+
+def test_warm_subspace_factor_householder_and_full_ritz(oracle):
+    """each_qr / final_qr (operator_kmeans.py:366-371, :405-419) and the full Rayleigh-Ritz
+    finish (:460-466).  Started on the exact top-r eigenvectors: the full finish gives
+    F F^T = P M P / mean(top eigenvalues) exactly (no ridge), its columns are orthogonal with
+    squared norms the top eigenvalues / their mean in ascending order, and a negative
+    eigenvalue inside the subspace is clamped to a zero column (and out of the mean).  Each
+    basis is orthonormal; one each_qr step is the QR of M Q(prev) (B^T M Q(prev) upper
+    triangular); final_qr's basis spans M^p prev; from a random start many steps converge
+    to the top subspace."""
+    rng = np.random.default_rng(56)
+    d, r = 16, 6
+    eig = np.linspace(0.1, 1.0, d) ** 3
+    eig[-r:] = [2.0, 2.5, 3.0, 4.0, 5.0, 7.0]
+    m, qm = _spectrum_matrix(rng, 2, d, eig)
+    top = qm[:, :, -r:]
+    proj = np.einsum("bir,bjr->bij", top, top)
+    pmp = proj @ m @ proj
+    prev = top * rng.uniform(0.5, 2.0, (2, 1, r))
+    for ortho in ("each_qr", "final_qr", "each_cholesky_qr2"):
+        f, b, rec = oracle.warm_subspace_metric_factor(m, prev, r, orthogonalization=ortho, ritz_mode="full")
+        assert not rec.any()
+        assert np.allclose(np.einsum("bir,bjr->bij", f, f), pmp / eig[-r:].mean(), atol=1e-9)
+        assert np.allclose(np.einsum("bir,bis->brs", b, b), np.eye(r), atol=1e-9)
+        assert np.allclose(np.einsum("bir,bis->brs", f, f), np.stack([np.diag(eig[-r:] / eig[-r:].mean())] * 2),
+                           atol=1e-9)
+    # one each_qr step from a random start is the QR of M Q(prev); final_qr spans M^p prev
+    prev_r = rng.standard_normal((2, d, r))
+    _, b1, _ = oracle.warm_subspace_metric_factor(m, prev_r, r, power_iters=1, orthogonalization="each_qr",
+                                                  ritz_mode="previous_scale")
+    for h in range(2):
+        q0, _ = np.linalg.qr(prev_r[h])
+        tri = b1[h].T @ (m[h] @ q0)
+        assert np.allclose(np.tril(tri, -1), 0.0, atol=1e-10) and np.allclose(b1[h].T @ b1[h], np.eye(r), atol=1e-12)
+    _, b3, _ = oracle.warm_subspace_metric_factor(m, prev_r, r, power_iters=3, orthogonalization="final_qr",
+                                                  ritz_mode="previous_scale")
+    for h in range(2):
+        target = np.linalg.matrix_power(m[h], 3) @ prev_r[h]
+        resid = target - b3[h] @ (b3[h].T @ target)
+        assert np.linalg.norm(resid) <= 1e-10 * np.linalg.norm(target)
+    fc, _, _ = oracle.warm_subspace_metric_factor(m, prev_r, r, power_iters=60, orthogonalization="each_qr",
+                                                  ritz_mode="full")
+    assert np.allclose(np.einsum("bir,bjr->bij", fc, fc), pmp / eig[-r:].mean(), atol=1e-8)
+    # a negative eigenvalue inside the tracked subspace: that column is zero, the mean skips it
+    eig2 = eig.copy()
+    eig2[-r] = -1.5
+    m2, qm2 = _spectrum_matrix(rng, 1, d, eig2)
+    f2, _, _ = oracle.warm_subspace_metric_factor(m2, qm2[:, :, -r:], r, orthogonalization="each_qr",
+                                                  ritz_mode="full")
+    norms2 = (f2[0] ** 2).sum(0)
+    kept = np.sort(eig2[-r:])[1:]
+    assert np.allclose(norms2, np.concatenate(([0.0], kept / (kept.sum() / r))), atol=1e-9)
+
+
 def test_project_rows_loop(oracle):
     rng = np.random.default_rng(54)
     x = rng.standard_normal((1, 5, 8)).astype(np.float32)
