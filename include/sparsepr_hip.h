@@ -262,6 +262,22 @@ int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense,
 int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
                      const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
                      float alpha, float norm_cap, void* out, hipStream_t stream);
+/* residual_repair.py:737-797 n8_prepare_repair_fit_triton (repair_features "output_role"):
+ *   x_fit fp32 [bh, m, d + role_dim] = [base[rows], role[rows]] with role fp32
+ *   [bh, n, role_dim]; dense_f, y_fit as spr_repair_fit_prep (role_dim 0 is that call). */
+int spr_repair_fit_prep_role(const void* base, int32_t base_dtype, const float* role, int32_t role_dim,
+                             const void* dense, int32_t dense_dtype, const int32_t* rows, int64_t bh, int64_t n,
+                             int32_t m, int32_t d, float* x_fit, float* dense_f, float* y_fit, hipStream_t stream);
+/* residual_repair.py:388-475 n8_repair_apply_triton (kernel :10-92):
+ *   out = base + alpha * ((([base, role] - x_mean) / x_scale) . left . basis^T + y_mean), the
+ *   correction's row norm capped at norm_cap times the base row's norm when norm_cap > 0.
+ *   role fp32 [bh, n, role_dim], role_dim in {0, 16, 32, 48, 64} (0: spr_repair_apply);
+ *   x_mean, x_scale fp32 [bh, d + role_dim]; y_mean fp32 [bh, d]; left fp32
+ *   [bh, d + role_dim, rank]; basis fp32 [bh, d, rank]; d in {64, 128}, rank 16. */
+int spr_repair_apply_role(const void* base, const float* role, int32_t role_dim, const float* x_mean,
+                          const float* x_scale, const float* y_mean, const float* left, const float* basis,
+                          int64_t bh, int64_t n, int32_t d, int32_t rank, float alpha, float norm_cap, void* out,
+                          hipStream_t stream);
 /* ---- model-edge fusions (spr_qkv.hip) */
 /* n8_ops.cu:16-105 wan_qkv_norm_rope_layout_kernel (host :356-413): q, k, v [batch, tokens,
  * channels = heads * head_dim] of dtype (0 bf16, 1 fp16, 2 fp32); RMSNorm over all channels of
@@ -350,7 +366,9 @@ int spr_role_metric(const void* x, int32_t dtype, int64_t bh, int64_t n, int32_t
                     int32_t count, const int32_t* sizes, int32_t center, float post_scale, float* out,
                     hipStream_t stream);
 /* residual_repair.py:263-465 fit_reduced_rank_residual / _fit_reduced_rank_residual_fp32 for
- * every configuration it accepts with m, p, d <= 128 and rank <= 16:
+ * every configuration it accepts with m, d <= 128, p <= 128 (or, in the dual form, m < p <= 256
+ * with 64 ceil(p / 64) (m | 1) <= 16512: the role-feature fit's p = d + role rank) and
+ * rank <= 16:
  *   weighted standardisation (:364-384; weights == NULL: plain mean and unbiased std);
  *   primal ridge solve for m >= p (:424-434), dual for m < p (:386-423, both fit_backend
  *   forms); the top-rank eigenvectors of the weighted output gram of the raw residual
@@ -367,7 +385,7 @@ int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t
 /* The same fit with the "skinny" route and decomposition_backend "triton_top16"
  * (residual_repair.py:435-451,497-503; the reference's GPU N8 repair, n8_v6.py:1310-1320):
  * the basis is spr_rrr_top16_basis of the weighted raw residual (basis_source 0) or of the
- * weighted fitted values (1).  m = 64, d = 128, rank = 16; p <= 128. */
+ * weighted fitted values (1).  m = 64, d = 128, rank = 16; p <= 256. */
 int spr_rrr_fit_top16(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
                       int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean, float* x_scale,
                       float* y_mean, float* left, float* basis, void* workspace, size_t workspace_bytes,

@@ -727,11 +727,14 @@ def recover_nonfinite_rrr_state(state, previous):
     return sel, rec
 
 
-def repair_apply(base, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap):
-    """out = base + alpha * (((base - mu)/sigma) left basis^T + y_mean), optional
-    norm cap (residual_repair.py:95-155 kernel, :620-646 torch).  float64."""
+def repair_apply(base, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap, role=None):
+    """out = base + alpha * (((x - mu)/sigma) left basis^T + y_mean), optional norm cap with
+    x = base, or x = [base, role] with role features (repair_features "output_role";
+    residual_repair.py:95-155 and :10-92 kernels, :600-646 torch: the split prediction sums
+    the base and the role coordinates, the cap compares with the base norm).  float64."""
     b = base.astype(np.float64)
-    z = (b - x_mean) / x_scale
+    x = b if role is None else np.concatenate((b, np.asarray(role, np.float64)), axis=-1)
+    z = (x - x_mean) / x_scale
     corr = (z @ left) @ np.swapaxes(basis, 1, 2) + y_mean
     if norm_cap > 0.0:
         bn = np.linalg.norm(b, axis=2, keepdims=True)

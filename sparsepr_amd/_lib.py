@@ -75,6 +75,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                         _vp]),
     "spr_repair_fit_prep": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "spr_repair_apply": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _f32, _f32, _vp, _vp]),
+    "spr_repair_fit_prep_role": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp,
+                                                _vp, _vp, _vp]),
+    "spr_repair_apply_role": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _f32,
+                                             _f32, _vp, _vp]),
     "spr_probe_scatter": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     # qkv.hip
     "spr_wan_qkv_norm_rope_layout": (ctypes.c_int, [_vp] * 7 + [_i32, _i64, _i64, _i32, _i32, _f32] + [_vp] * 4),

@@ -5,7 +5,9 @@
 //   select_role_equal_probes(_vectorized), select_first_token_largest_groups
 //       (src/sparsepr/models/cosmos3/residual_repair.py:36-260)
 //   n8_prepare_output_repair_fit_triton    (kernels/triton/residual_repair.py:798-857, kernel :330-363)
+//   n8_prepare_repair_fit_triton           (kernels/triton/residual_repair.py:737-797, kernel :285-327)
 //   n8_repair_apply_output_triton          (kernels/triton/residual_repair.py:478-562, kernel :95-155)
+//   n8_repair_apply_triton                 (kernels/triton/residual_repair.py:388-475, kernel :10-92)
 //   n8_exact_probe_scatter_triton          (kernels/triton/residual_repair.py:656-700, kernel :257-282)
 //
 // Probe selection runs in two launches.  (1) distance: each token's squared
@@ -387,50 +389,59 @@ __global__ __launch_bounds__(256) void probe_select_kernel(const float* __restri
   for (int j = threadIdx.x; j < have; j += blockDim.x) out_w[j] = __fdiv_rn(out_w[j], mean);
 }
 
-// x_fit = float(base[rows]), dense_f = float(dense), y_fit = dense_f - x_fit.
+// x_fit = float(base[rows]) (then, with role, float(role[rows]) in columns d .. d + rr of
+// rows of d + rr), dense_f = float(dense), y_fit = dense_f - float(base[rows]).
 template <typename TB, typename TD>
 __global__ void fit_prep_kernel(const TB* __restrict__ base, const TD* __restrict__ dense,
-                                const int32_t* __restrict__ rows, int64_t n, int32_t m, int32_t d,
-                                float* __restrict__ x_fit, float* __restrict__ dense_f, float* __restrict__ y_fit) {
+                                const float* __restrict__ role, int32_t rr, const int32_t* __restrict__ rows,
+                                int64_t n, int32_t m, int32_t d, float* __restrict__ x_fit,
+                                float* __restrict__ dense_f, float* __restrict__ y_fit) {
   const int64_t bh = blockIdx.y;
-  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < m * d; e += gridDim.x * blockDim.x) {
-    const int j = e / d;
-    const int c = e - j * d;
+  const int64_t xp = d + rr;  // x_fit row length
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < m * (d + rr); e += gridDim.x * blockDim.x) {
+    const int j = e / (d + rr);
+    const int c = e - j * (d + rr);
     const int32_t r = rows[bh * m + j];
-    const float b = (r >= 0 && r < n) ? load_elem(base, (bh * n + r) * d + c) : 0.0f;
+    const bool ok = r >= 0 && r < n;
+    if (c >= d) {
+      x_fit[(bh * m + j) * xp + c] = ok ? role[(bh * n + r) * rr + (c - d)] : 0.0f;
+      continue;
+    }
+    const float b = ok ? load_elem(base, (bh * n + r) * d + c) : 0.0f;
     const float y = load_elem(dense, (bh * m + j) * static_cast<int64_t>(d) + c);
     const int64_t o = (bh * m + j) * static_cast<int64_t>(d) + c;
-    x_fit[o] = b;
+    x_fit[(bh * m + j) * xp + c] = b;
     dense_f[o] = y;
     y_fit[o] = __fsub_rn(y, b);
   }
 }
 
-// out = base + alpha * (((base - mu) / sigma) L B^T + mu_y), optional norm cap.
-// One lane per token row (64 rows per wave); L and B are read from LDS as
-// wave-uniform broadcasts.  Loops over the head dim are fully unrolled so the
+// out = base + alpha * (((base - mu) / sigma) L B^T + mu_y), optional norm cap; with RR
+// role features the standardised role row joins the features (L has D + RR rows) and the
+// cap stays on the base norm.  One lane per token row (64 rows per wave); L and B are read
+// from LDS as wave-uniform broadcasts.  Loops over the head dim are fully unrolled so the
 // row stays in registers.
-template <int D, int RK>
+template <int D, int RK, int RR>
 __global__ __launch_bounds__(256) void repair_apply_kernel(const uint16_t* __restrict__ base,
+                                                           const float* __restrict__ role,
                                                            const float* __restrict__ x_mean,
                                                            const float* __restrict__ x_scale,
                                                            const float* __restrict__ y_mean,
                                                            const float* __restrict__ left,
                                                            const float* __restrict__ basis, int64_t n, float alpha,
                                                            float norm_cap, uint16_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) float Ls[D][RK];
+  constexpr int P = D + RR;
+  __shared__ __attribute__((aligned(16))) float Ls[P][RK];
   __shared__ __attribute__((aligned(16))) float Bs[D][RK];
-  __shared__ float mu[D], inv_sd[D], my[D];
+  __shared__ float mu[P], inv_sd[P], my[D];
   const int64_t bh = blockIdx.y;
-  for (int e = threadIdx.x; e < D * RK; e += blockDim.x) {
-    Ls[e / RK][e % RK] = left[bh * D * RK + e];
-    Bs[e / RK][e % RK] = basis[bh * D * RK + e];
+  for (int e = threadIdx.x; e < P * RK; e += blockDim.x) Ls[e / RK][e % RK] = left[bh * P * RK + e];
+  for (int e = threadIdx.x; e < D * RK; e += blockDim.x) Bs[e / RK][e % RK] = basis[bh * D * RK + e];
+  for (int e = threadIdx.x; e < P; e += blockDim.x) {
+    mu[e] = x_mean[bh * P + e];
+    inv_sd[e] = 1.0f / x_scale[bh * P + e];
   }
-  for (int e = threadIdx.x; e < D; e += blockDim.x) {
-    mu[e] = x_mean[bh * D + e];
-    inv_sd[e] = 1.0f / x_scale[bh * D + e];
-    my[e] = y_mean[bh * D + e];
-  }
+  for (int e = threadIdx.x; e < D; e += blockDim.x) my[e] = y_mean[bh * D + e];
   __syncthreads();
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= n) return;
@@ -456,6 +467,15 @@ __global__ __launch_bounds__(256) void repair_apply_kernel(const uint16_t* __res
       const float z = (b - mu[dd]) * inv_sd[dd];
 #pragma unroll
       for (int r = 0; r < RK; ++r) coords[r] = __builtin_fmaf(z, Ls[dd][r], coords[r]);
+    }
+  }
+  if constexpr (RR > 0) {
+    const float* rrow = role + (bh * n + t) * RR;
+#pragma unroll
+    for (int c = 0; c < RR; ++c) {
+      const float z = (rrow[c] - mu[D + c]) * inv_sd[D + c];
+#pragma unroll
+      for (int r = 0; r < RK; ++r) coords[r] = __builtin_fmaf(z, Ls[D + c][r], coords[r]);
     }
   }
   float scale = alpha;
@@ -540,8 +560,28 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds
 #endif
 }
 
-template <bool CAP>
+// The A fragment of rank row col of a stored [16][2] block: zeros for col >= 16 (read
+// from row col % 16, then selected away, so the load is not divergent).
+__device__ __forceinline__ u32x4 lfrag_at(const u32x4 (&blk)[16][2], int col, int part) {
+  const u32x4 v = blk[col & 15][part];
+  const bool live = col < 16;
+  return u32x4{live ? v.x : 0u, live ? v.y : 0u, live ? v.z : 0u, live ? v.w : 0u};
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// With RR role features (fp32 [n][RR] per head), each row's standardised role values join
+// the coordinates as RR / 16 more k-steps: lane (row, h) loads dims 16s + 8h .. + 7 of its
+// role row with two 16-byte loads per step at the top of the batch, before the next batch's
+// DMA, so they land while the batch waits and runs its base steps; the explicit waits count
+// those loads.  L then has D + RR rows, the statistics D + RR entries.
+template <bool CAP, int RR>
 __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* __restrict__ base,
+                                                                const float* __restrict__ role,
                                                                 const float* __restrict__ x_mean,
                                                                 const float* __restrict__ x_scale,
                                                                 const float* __restrict__ y_mean,
@@ -551,11 +591,16 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
                                                                 uint16_t* __restrict__ out) {
   constexpr int D = 128;
   constexpr int RK = 16;
+  constexpr int P = D + RR;          // features
+  constexpr int RS = RR / 16;        // role k-steps
+  constexpr int NR = 2 * RS;         // role loads per lane and batch
   constexpr int ROWB = D * 2;        // bytes per row
   constexpr int TILE = 32 * ROWB;    // one wave's batch
-  __shared__ u32x4 lfrag[8][2][32][2];   // [k-step s][k-half h][rank] (hi, lo): L[16s + 8h + e][rank], 0 past RK
+  // [k-step s][k-half h][rank] (hi, lo): L[16s + 8h + e][rank]; the A operand's ranks 16 .. 31
+  // are zero and are not stored (lanes with col >= 16 select zeros)
+  __shared__ u32x4 lfrag[8 + RS][2][RK][2];
   __shared__ u32x4 bfrag[4][32][2][2];   // [N-tile][row a][k-half h] (hi, lo): basis[32 nt + pi(a)][rho(h, m)]
-  __shared__ __attribute__((aligned(16))) float mu[D], inv_sd[D], my[D];
+  __shared__ __attribute__((aligned(16))) float mu[P], inv_sd[P], my[D];
   __shared__ __attribute__((aligned(1024))) uint8_t rows_lds[8][2][TILE];  // [wave][buffer]
   auto lds8 = [](const float* p, float (&x)[8]) {  // 8 consecutive floats, 32-byte aligned
     const spr::f32x4 a = reinterpret_cast<const spr::f32x4*>(p)[0];
@@ -564,7 +609,7 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
     x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
   };
   const int64_t bh = blockIdx.y;
-  const float* lm = left + bh * D * RK;
+  const float* lm = left + bh * P * RK;
   const float* bm = basis + bh * D * RK;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -589,8 +634,8 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
   int64_t w0 = static_cast<int64_t>(blockIdx.x) * 256 + wave * 32;
   if (w0 < n) dma(w0, rows_lds[wave][0]);
 
-  for (int f = tid; f < 8 * 2 * 32; f += blockDim.x) {
-    const int st = f / 64, hh = (f / 32) % 2, rk = f % 32;
+  for (int f = tid; f < (8 + RS) * 2 * RK; f += blockDim.x) {
+    const int st = f / (2 * RK), hh = (f / RK) % 2, rk = f % RK;
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = rk < RK ? lm[(16 * st + 8 * hh + e) * RK + rk] : 0.0f;
@@ -604,11 +649,11 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
     for (int m = 0; m < 8; ++m) v[m] = bm[dim * RK + 8 * (m / 4) + 4 * hh + m % 4];
     split_bf16x8(v, bfrag[nt][a][hh][0], bfrag[nt][a][hh][1]);
   }
-  for (int e = tid; e < D; e += blockDim.x) {
-    mu[e] = x_mean[bh * D + e];
-    inv_sd[e] = 1.0f / x_scale[bh * D + e];
-    my[e] = y_mean[bh * D + e];
+  for (int e = tid; e < P; e += blockDim.x) {
+    mu[e] = x_mean[bh * P + e];
+    inv_sd[e] = 1.0f / x_scale[bh * P + e];
   }
+  for (int e = tid; e < D; e += blockDim.x) my[e] = y_mean[bh * D + e];
   __syncthreads();
 
   // Batch it is DMA'd into buffer it % 2 one batch ahead.  Once its rows are in
@@ -621,13 +666,23 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
   for (int it = 0; w0 < n; w0 += stride, ++it) {
     const int buf = it & 1;
     const bool more = w0 + stride < n;
+    spr::f32x4 rv[RS > 0 ? RS : 1][2];  // this lane's role values, dims 16 s + 8 h + 4 u ..
+    if constexpr (RS > 0) {
+      const int64_t row = w0 + col;
+      const float* rp = role + (bh * n + (row < n ? row : 0)) * RR + 8 * h;
+#pragma unroll
+      for (int st = 0; st < RS; ++st) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) rv[st][u] = *reinterpret_cast<const spr::f32x4*>(rp + 16 * st + 4 * u);
+      }
+    }
     if (more) dma(w0 + stride, rows_lds[wave][buf ^ 1]);
     if (it >= 1 && more) {
-      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      wait_vmcnt<16 + NR>();
     } else if (it >= 1 || more) {
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      wait_vmcnt<8 + NR>();
     } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      wait_vmcnt<NR>();
     }
     uint8_t* tile = rows_lds[wave][buf];
     u32x4 bv[8];  // dims 16s + 8h .. + 7 of row col
@@ -649,8 +704,23 @@ __global__ __launch_bounds__(512) void repair_apply_mfma_kernel(const uint16_t* 
       }
       u32x4 zh, zl;
       split_bf16x8(z, zh, zl);
-      const u32x4 ah = lfrag[st][h][col][0];
-      const u32x4 al = lfrag[st][h][col][1];
+      const u32x4 ah = lfrag_at(lfrag[st][h], col, 0);
+      const u32x4 al = lfrag_at(lfrag[st][h], col, 1);
+      cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zh), cacc, 0, 0, 0);
+      cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(al), spr::as_bf16x8(zh), cacc, 0, 0, 0);
+      cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zl), cacc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int st = 0; st < RS; ++st) {  // role k-steps (rows past n: their values are never stored)
+      float z[8], m8[8], s8[8];
+      lds8(mu + D + 16 * st + 8 * h, m8);
+      lds8(inv_sd + D + 16 * st + 8 * h, s8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[e] = (rv[st][e / 4][e % 4] - m8[e]) * s8[e];
+      u32x4 zh, zl;
+      split_bf16x8(z, zh, zl);
+      const u32x4 ah = lfrag_at(lfrag[8 + st][h], col, 0);
+      const u32x4 al = lfrag_at(lfrag[8 + st][h], col, 1);
       cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zh), cacc, 0, 0, 0);
       cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(al), spr::as_bf16x8(zh), cacc, 0, 0, 0);
       cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ah), spr::as_bf16x8(zl), cacc, 0, 0, 0);
@@ -819,19 +889,24 @@ extern "C" int spr_probe_select(const float* dist, const int32_t* labels, const 
   return SPR_OK;
 }
 
-// base [bh, n, d] (dtype 0 bf16 / 2 fp32), dense [bh, m, d] (dense_dtype 0/2), rows
-// int32 [bh, m] -> x_fit, dense_f, y_fit fp32 [bh, m, d].
-extern "C" int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense, int32_t dense_dtype,
-                                   const int32_t* rows, int64_t bh, int64_t n, int32_t m, int32_t d, float* x_fit,
-                                   float* dense_f, float* y_fit, hipStream_t stream) {
-  SPR_REQUIRE(bh >= 0 && n >= 0 && m >= 0 && d >= 1, "spr_repair_fit_prep: bad size");
+// base [bh, n, d] (dtype 0 bf16 / 2 fp32), dense [bh, m, d] (dense_dtype 0/2), rows int32
+// [bh, m], role fp32 [bh, n, role_dim] (nullable when role_dim is 0) -> x_fit fp32
+// [bh, m, d + role_dim] = [base[rows], role[rows]], dense_f, y_fit fp32 [bh, m, d]
+// (n8_prepare_repair_fit_triton; role_dim 0 is the output-only preparation).
+extern "C" int spr_repair_fit_prep_role(const void* base, int32_t base_dtype, const float* role, int32_t role_dim,
+                                        const void* dense, int32_t dense_dtype, const int32_t* rows, int64_t bh,
+                                        int64_t n, int32_t m, int32_t d, float* x_fit, float* dense_f, float* y_fit,
+                                        hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && n >= 0 && m >= 0 && d >= 1 && role_dim >= 0, "spr_repair_fit_prep: bad size");
   SPR_REQUIRE(bh <= 65535, "spr_repair_fit_prep: bh exceeds 65535");
   if (bh == 0 || m == 0) return SPR_OK;
-  SPR_REQUIRE(base && dense && rows && x_fit && dense_f && y_fit, "spr_repair_fit_prep: null pointer");
-  dim3 grid(static_cast<uint32_t>(spr::ceil_div(static_cast<int64_t>(m) * d, 256)), static_cast<uint32_t>(bh));
+  SPR_REQUIRE(base && dense && rows && x_fit && dense_f && y_fit && (role || role_dim == 0),
+              "spr_repair_fit_prep: null pointer");
+  dim3 grid(static_cast<uint32_t>(spr::ceil_div(static_cast<int64_t>(m) * (d + role_dim), 256)),
+            static_cast<uint32_t>(bh));
 #define SPR_FP(TB, TD)                                                                                          \
   fit_prep_kernel<TB, TD><<<grid, 256, 0, stream>>>(static_cast<const TB*>(base), static_cast<const TD*>(dense), \
-                                                    rows, n, m, d, x_fit, dense_f, y_fit)
+                                                    role, role_dim, rows, n, m, d, x_fit, dense_f, y_fit)
   if (base_dtype == 0 && dense_dtype == 0) SPR_FP(uint16_t, uint16_t);
   else if (base_dtype == 0 && dense_dtype == 2) SPR_FP(uint16_t, float);
   else if (base_dtype == 2 && dense_dtype == 0) SPR_FP(float, uint16_t);
@@ -842,41 +917,86 @@ extern "C" int spr_repair_fit_prep(const void* base, int32_t base_dtype, const v
   return SPR_OK;
 }
 
-// bf16 base/out [bh, n, d]; x_mean, x_scale, y_mean fp32 [bh, d]; left,
-// basis fp32 [bh, d, rank]; d in {64, 128}, rank 16.
-extern "C" int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
-                                const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
-                                float alpha, float norm_cap, void* out, hipStream_t stream) {
+// base [bh, n, d] (dtype 0 bf16 / 2 fp32), dense [bh, m, d] (dense_dtype 0/2), rows
+// int32 [bh, m] -> x_fit, dense_f, y_fit fp32 [bh, m, d].
+extern "C" int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense, int32_t dense_dtype,
+                                   const int32_t* rows, int64_t bh, int64_t n, int32_t m, int32_t d, float* x_fit,
+                                   float* dense_f, float* y_fit, hipStream_t stream) {
+  return spr_repair_fit_prep_role(base, base_dtype, nullptr, 0, dense, dense_dtype, rows, bh, n, m, d, x_fit, dense_f,
+                                  y_fit, stream);
+}
+
+// bf16 base/out [bh, n, d]; role fp32 [bh, n, role_dim] (nullable when role_dim is 0);
+// x_mean, x_scale fp32 [bh, d + role_dim]; y_mean fp32 [bh, d]; left fp32
+// [bh, d + role_dim, rank]; basis fp32 [bh, d, rank]; d in {64, 128}, rank 16, role_dim in
+// {0, 16, 32, 48, 64}.
+extern "C" int spr_repair_apply_role(const void* base, const float* role, int32_t role_dim, const float* x_mean,
+                                     const float* x_scale, const float* y_mean, const float* left, const float* basis,
+                                     int64_t bh, int64_t n, int32_t d, int32_t rank, float alpha, float norm_cap,
+                                     void* out, hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && n >= 0, "spr_repair_apply: bad size");
   SPR_REQUIRE((d == 128 || d == 64) && rank == 16, "spr_repair_apply: requires D in {64, 128}, rank=16 (got %d, %d)",
               d, rank);
+  SPR_REQUIRE(role_dim >= 0 && role_dim <= 64 && role_dim % 16 == 0,
+              "spr_repair_apply: role_dim must be 0, 16, 32, 48 or 64 (got %d)", role_dim);
   SPR_REQUIRE(bh <= 65535, "spr_repair_apply: bh exceeds 65535");
   if (bh == 0 || n == 0) return SPR_OK;
-  SPR_REQUIRE(base && x_mean && x_scale && y_mean && left && basis && out, "spr_repair_apply: null pointer");
-  SPR_REQUIRE(reinterpret_cast<uintptr_t>(base) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0,
-              "spr_repair_apply: base/out must be 16-byte aligned");
+  SPR_REQUIRE(base && x_mean && x_scale && y_mean && left && basis && out && (role || role_dim == 0),
+              "spr_repair_apply: null pointer");
+  SPR_REQUIRE(reinterpret_cast<uintptr_t>(base) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(role) % 16 == 0,
+              "spr_repair_apply: base/out/role must be 16-byte aligned");
+  const uint16_t* b16 = static_cast<const uint16_t*>(base);
+  uint16_t* o16 = static_cast<uint16_t*>(out);
   if (d == 128) {
     SPR_REQUIRE(n * 256 < (int64_t(1) << 31), "spr_repair_apply: a head's rows exceed 2 GiB");
     // one resident workgroup per CU (256 CUs), each walking 256-row batches of one head
     const int64_t per_head = std::max<int64_t>(1, std::min<int64_t>(spr::ceil_div(n, 256), 256 / bh));
     dim3 grid(static_cast<uint32_t>(per_head), static_cast<uint32_t>(bh));
-    if (norm_cap > 0.0f) {
-      repair_apply_mfma_kernel<true><<<grid, 512, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
-                                                               y_mean, left, basis, n, alpha, norm_cap,
-                                                               static_cast<uint16_t*>(out));
-    } else {
-      repair_apply_mfma_kernel<false><<<grid, 512, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
-                                                                y_mean, left, basis, n, alpha, norm_cap,
-                                                                static_cast<uint16_t*>(out));
+#define SPR_RA(CAP, RR)                                                                                           \
+  repair_apply_mfma_kernel<CAP, RR><<<grid, 512, 0, stream>>>(b16, role, x_mean, x_scale, y_mean, left, basis, n, \
+                                                              alpha, norm_cap, o16)
+#define SPR_RA_CAP(RR)          \
+  do {                          \
+    if (norm_cap > 0.0f)        \
+      SPR_RA(true, RR);         \
+    else                        \
+      SPR_RA(false, RR);        \
+  } while (0)
+    switch (role_dim) {
+      case 0: SPR_RA_CAP(0); break;
+      case 16: SPR_RA_CAP(16); break;
+      case 32: SPR_RA_CAP(32); break;
+      case 48: SPR_RA_CAP(48); break;
+      default: SPR_RA_CAP(64); break;
     }
+#undef SPR_RA_CAP
+#undef SPR_RA
   } else {
     dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
-    repair_apply_kernel<64, 16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(base), x_mean, x_scale,
-                                                          y_mean, left, basis, n, alpha, norm_cap,
-                                                          static_cast<uint16_t*>(out));
+#define SPR_RA64(RR)                                                                                                \
+  repair_apply_kernel<64, 16, RR><<<grid, 256, 0, stream>>>(b16, role, x_mean, x_scale, y_mean, left, basis, n, alpha, \
+                                                            norm_cap, o16)
+    switch (role_dim) {
+      case 0: SPR_RA64(0); break;
+      case 16: SPR_RA64(16); break;
+      case 32: SPR_RA64(32); break;
+      case 48: SPR_RA64(48); break;
+      default: SPR_RA64(64); break;
+    }
+#undef SPR_RA64
   }
   SPR_LAUNCHED("repair_apply_kernel");
   return SPR_OK;
+}
+
+// bf16 base/out [bh, n, d]; x_mean, x_scale, y_mean fp32 [bh, d]; left, basis fp32
+// [bh, d, rank]; d in {64, 128}, rank 16 (the output-only form of spr_repair_apply_role).
+extern "C" int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
+                                const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
+                                float alpha, float norm_cap, void* out, hipStream_t stream) {
+  return spr_repair_apply_role(base, nullptr, 0, x_mean, x_scale, y_mean, left, basis, bh, n, d, rank, alpha,
+                               norm_cap, out, stream);
 }
 
 // out bf16 [bh, n, d]; out[b, rows[b, j]] = dense[b, j] (dense_dtype 0 bf16 / 2 fp32).

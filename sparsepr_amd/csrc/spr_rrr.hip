@@ -1,7 +1,8 @@
 // Weighted ridge reduced-rank residual fit.
 //
 // Replaces _fit_reduced_rank_residual_fp32 (src/sparsepr/models/cosmos3/residual_repair.py:317-465)
-// for every configuration it accepts with M, P, D <= 128 and rank <= 16:
+// for every configuration it accepts with M, D <= 128, P <= 128 (or, in the dual form M < P,
+// up to 256 while 64 ceil(P / 64) (M | 1) <= 16512) and rank <= 16:
 //   weighted (or, without weights, plain mean and unbiased std) standardisation (:364-384);
 //   the ridge solve in primal form for M >= P (:424-434) and in dual form for M < P (:386-423);
 //   the output basis of the raw residual or of the fitted values (:435-462): the
@@ -114,25 +115,27 @@ __global__ __launch_bounds__(256) void rrr_stats_kernel(const float* __restrict_
     ws = fmaxf(ws, 1e-20f);
     var_div = ws;
   }
-  if (t < p) {
-    float s = 0.0f;
+  for (int col = t; col < p + d; col += 256) {  // features, then outputs
+    if (col < p) {
+      float s = 0.0f;
 #pragma unroll 8
-    for (int r = 0; r < m; ++r) s += (wh != nullptr ? wh[r] : 1.0f) * xh[r * p + t];
-    const float mean = s / ws;
-    float v = 0.0f;
+      for (int r = 0; r < m; ++r) s += (wh != nullptr ? wh[r] : 1.0f) * xh[r * p + col];
+      const float mean = s / ws;
+      float v = 0.0f;
 #pragma unroll 8
-    for (int r = 0; r < m; ++r) {
-      const float dv = xh[r * p + t] - mean;
-      v += (wh != nullptr ? wh[r] : 1.0f) * (dv * dv);
+      for (int r = 0; r < m; ++r) {
+        const float dv = xh[r * p + col] - mean;
+        v += (wh != nullptr ? wh[r] : 1.0f) * (dv * dv);
+      }
+      x_mean[h * p + col] = mean;
+      x_scale[h * p + col] = clamp_min_nan(sqrtf(v / var_div), 1e-5f);
+    } else {
+      const int c = col - p;
+      float s = 0.0f;
+#pragma unroll 8
+      for (int r = 0; r < m; ++r) s += (wh != nullptr ? wh[r] : 1.0f) * yh[r * d + c];
+      y_mean[h * d + c] = s / ws;
     }
-    x_mean[h * p + t] = mean;
-    x_scale[h * p + t] = clamp_min_nan(sqrtf(v / var_div), 1e-5f);
-  } else if (t >= RRR_MAX && t - RRR_MAX < d) {
-    const int c = t - RRR_MAX;
-    float s = 0.0f;
-#pragma unroll 8
-    for (int r = 0; r < m; ++r) s += (wh != nullptr ? wh[r] : 1.0f) * yh[r * d + c];
-    y_mean[h * d + c] = s / ws;
   }
 }
 
@@ -188,22 +191,26 @@ __global__ __launch_bounds__(256) void rrr_gram_kernel(const float* __restrict__
         return ah[static_cast<int64_t>(r) * a_ld + cc];
     }
   };
-  for (int e = t; e < RRR_MAX * 32; e += 256) {
-    const int r = e >> 5, cc = e & 31;
-    const int ci = 32 * ti + cc, cj = 32 * tj + cc;
-    pa[r][cc] = (r < rows && ci < cols) ? elem(r, ci) : 0.0f;
-    pb[r][cc] = (r < rows && cj < cols) ? elem(r, cj) : 0.0f;
-  }
-  __syncthreads();
   const int ta = t >> 4, tb = t & 15;
   float s00 = 0.0f, s01 = 0.0f, s10 = 0.0f, s11 = 0.0f;
-  for (int r = 0; r < rows; ++r) {
-    const float u0 = pa[r][2 * ta], u1 = pa[r][2 * ta + 1];
-    const float v0 = pb[r][2 * tb], v1 = pb[r][2 * tb + 1];
-    s00 += u0 * v0;
-    s01 += u0 * v1;
-    s10 += u1 * v0;
-    s11 += u1 * v1;
+  for (int r0 = 0; r0 < rows; r0 += RRR_MAX) {  // the summed rows, 128 at a time (dual: p <= 256)
+    if (r0 > 0) __syncthreads();
+    for (int e = t; e < RRR_MAX * 32; e += 256) {
+      const int r = e >> 5, cc = e & 31;
+      const int ci = 32 * ti + cc, cj = 32 * tj + cc;
+      pa[r][cc] = (r0 + r < rows && ci < cols) ? elem(r0 + r, ci) : 0.0f;
+      pb[r][cc] = (r0 + r < rows && cj < cols) ? elem(r0 + r, cj) : 0.0f;
+    }
+    __syncthreads();
+    const int nr = min(rows - r0, RRR_MAX);
+    for (int r = 0; r < nr; ++r) {
+      const float u0 = pa[r][2 * ta], u1 = pa[r][2 * ta + 1];
+      const float v0 = pb[r][2 * tb], v1 = pb[r][2 * tb + 1];
+      s00 += u0 * v0;
+      s01 += u0 * v1;
+      s10 += u1 * v0;
+      s11 += u1 * v1;
+    }
   }
   const bool is_g = kind == GRAM_PRIMAL || kind == GRAM_DUAL;
   float* out = ws_slot(ws, h, is_g ? 0 : 1);
@@ -809,21 +816,33 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void sym_top_eig_kernel(const float
                   vals != nullptr ? vals + h * rank : nullptr);
 }
 
-// L (ng x ng lower, slot 0) into LDS and x_w^T into LDS ([p][m], zero padded).
+// x_w^T in LDS, [xt_rows(p)][xt_stride(m, p)] in an array of RRR_MAX * RRR_LS floats: feature
+// a is row a (rows from p on are zero), token r column r (columns from m on are zero).  Up
+// to 128 features: 128 rows of 129.  More features (the dual form, m < p <= 256): 64 ceil(p /
+// 64) rows of m | 1 (odd, so that the rows lane + 64 q of one column fall in distinct banks),
+// which fits when that product is at most RRR_MAX * RRR_LS.
+__host__ __device__ inline int xt_stride(int m, int p) { return p <= RRR_MAX ? RRR_LS : (m | 1); }
+__host__ __device__ inline int xt_rows(int p) { return p <= RRR_MAX ? RRR_MAX : 64 * ((p + 63) / 64); }
+
+// L (ng x ng lower, slot 0) into LDS and x_w^T into LDS (the layout above).
 __device__ __forceinline__ void load_factor_and_xt(const float* __restrict__ lg, int ng, const float* __restrict__ xh,
                                                    const float* __restrict__ wh, const float* __restrict__ xm,
                                                    const float* __restrict__ xs, int m, int p, float* ls,
                                                    float* xt) {
-  const int t = threadIdx.x, i = t >> 3, c = t & 7;
+  const int t = threadIdx.x;
   for (int e = t; e < RRR_MAT; e += RRR_THREADS) {
     const int r = e >> 7, cc = e & 127;
     ls[r * RRR_LS + cc] = (r < ng && cc <= r) ? lg[e] : 0.0f;
   }
-  const float sw = i < m ? (wh != nullptr ? sqrtf(wh[i]) : 1.0f) : 0.0f;
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int j = c + 8 * q;
-    xt[j * RRR_LS + i] = (i < m && j < p) ? (xh[i * p + j] - xm[j]) / xs[j] * sw : 0.0f;
+  const int xst = xt_stride(m, p), xr = xt_rows(p);
+  for (int e = t; e < m * p; e += RRR_THREADS) {  // x in its own order (coalesced reads)
+    const int i = e / p, j = e - i * p;
+    const float sw = wh != nullptr ? sqrtf(wh[i]) : 1.0f;
+    xt[j * xst + i] = (xh[e] - xm[j]) / xs[j] * sw;
+  }
+  for (int e = t; e < xr * xst; e += RRR_THREADS) {  // the zero padding (disjoint from the above)
+    const int j = e / xst, i = e - j * xst;
+    if (i >= m || j >= p) xt[e] = 0.0f;
   }
 }
 
@@ -880,29 +899,32 @@ __device__ __forceinline__ void chol_solve_wave(const float* ls, int n, int lane
   }
 }
 
-// v = x_w^T u for u over the m rows (held as in chol_solve_wave): entry a (< p) in lane a % 64.
-__device__ __forceinline__ void xt_times(const float* xt, int m, int lane, float& b0, float& b1) {
-  float l0 = 0.0f, l1 = 0.0f;
+// o = x_w^T u for u over the m rows (held as in chol_solve_wave): feature a (< p) in lane
+// a % 64 of o[a / 64].
+__device__ __forceinline__ void xt_times(const float* xt, int m, int p, int lane, float b0, float b1,
+                                         float (&o)[4]) {
+  const int xst = xt_stride(m, p), nfq = xt_rows(p) / 64;
+  float l[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int r0 = 0; r0 < m; r0 += 8) {
-    float e0[8], e1[8];
+    float e[4][8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int r = min(r0 + u, RRR_MAX - 1);
-      e0[u] = xt[lane * RRR_LS + r];
-      e1[u] = xt[(lane + 64) * RRR_LS + r];
+      const int r = min(r0 + u, xst - 1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) e[q][u] = q < nfq ? xt[(lane + 64 * q) * xst + r] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int r = r0 + u;
       if (r < m) {
         const float uu = lane_read(r < 64 ? b0 : b1, r & 63);
-        l0 += e0[u] * uu;
-        l1 += e1[u] * uu;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) l[q] += e[q][u] * uu;
       }
     }
   }
-  b0 = l0;
-  b1 = l1;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) o[q] = l[q];
 }
 
 __device__ __forceinline__ double lane_read_d(double v, int lane) {
@@ -914,46 +936,87 @@ __device__ __forceinline__ double lane_read_d(double v, int lane) {
 
 // G u for the ridge system, in fp64 from x_w (exact fp32 values in xt) rather than from the
 // rounded G: dual (u over the m rows): x_w x_w^T u + ridge u; primal (u over the p
-// features): x_w^T x_w u + ridge u.  u and the result are held as in chol_solve_wave.
+// features): x_w^T x_w u + ridge u.  u and the result are held as in chol_solve_wave; the
+// middle vector x_w^T u of the dual form (p <= 256 entries) as the output of xt_times.
 __device__ __forceinline__ void ridge_apply_f64(const float* xt, bool dual, int m, int p, float ridge, int lane,
                                                 float u0, float u1, double& g0, double& g1) {
-  const int n_in = dual ? m : p, n_mid = dual ? p : m;
-  double v0 = 0.0, v1 = 0.0;  // the middle vector: x_w^T u (dual) or x_w u (primal)
-  for (int k0 = 0; k0 < n_in; k0 += 8) {
-    float e0[8], e1[8];
+  const int xst = xt_stride(m, p), nfq = xt_rows(p) / 64;
+  double w0 = 0.0, w1 = 0.0;
+  if (dual) {
+    double v[4] = {0.0, 0.0, 0.0, 0.0};  // v[a] = sum_r x_w[r][a] u[r] = sum_r xt[a][r] u[r]
+    for (int k0 = 0; k0 < m; k0 += 8) {
+      float e[4][8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = min(k0 + u, RRR_MAX - 1);
-      // dual: v[a] = sum_r x_w[r][a] u[r] = xt[a][r]; primal: v[r] = sum_a x_w[r][a] u[a] = xt[a][r]
-      e0[u] = dual ? xt[lane * RRR_LS + k] : xt[k * RRR_LS + lane];
-      e1[u] = dual ? xt[(lane + 64) * RRR_LS + k] : xt[k * RRR_LS + lane + 64];
-    }
+      for (int u = 0; u < 8; ++u) {
+        const int k = min(k0 + u, xst - 1);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = k0 + u;
-      if (k < n_in) {
-        const double uk = static_cast<double>(lane_read(k < 64 ? u0 : u1, k & 63));
-        v0 = fma(static_cast<double>(e0[u]), uk, v0);
-        v1 = fma(static_cast<double>(e1[u]), uk, v1);
+        for (int q = 0; q < 4; ++q) e[q][u] = q < nfq ? xt[(lane + 64 * q) * xst + k] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + u;
+        if (k < m) {
+          const double uk = static_cast<double>(lane_read(k < 64 ? u0 : u1, k & 63));
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = fma(static_cast<double>(e[q][u]), uk, v[q]);
+        }
       }
     }
-  }
-  double w0 = 0.0, w1 = 0.0;  // x_w v (dual) or x_w^T v (primal)
-  for (int k0 = 0; k0 < n_mid; k0 += 8) {
-    float e0[8], e1[8];
+    for (int k0 = 0; k0 < p; k0 += 8) {  // w[r] = sum_a xt[a][r] v[a], r = lane, lane + 64
+      float e0[8], e1[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = min(k0 + u, RRR_MAX - 1);
-      e0[u] = dual ? xt[k * RRR_LS + lane] : xt[lane * RRR_LS + k];
-      e1[u] = dual ? xt[k * RRR_LS + lane + 64] : xt[(lane + 64) * RRR_LS + k];
+      for (int u = 0; u < 8; ++u) {
+        const int k = min(k0 + u, 64 * nfq - 1);
+        e0[u] = lane < xst ? xt[k * xst + lane] : 0.0f;
+        e1[u] = lane + 64 < xst ? xt[k * xst + lane + 64] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + u;
+        if (k < p) {
+          const double vq = k < 64 ? v[0] : (k < 128 ? v[1] : (k < 192 ? v[2] : v[3]));
+          const double vk = lane_read_d(vq, k & 63);
+          w0 = fma(static_cast<double>(e0[u]), vk, w0);
+          w1 = fma(static_cast<double>(e1[u]), vk, w1);
+        }
+      }
     }
+  } else {  // p <= 128 < 129 = xst
+    double v0 = 0.0, v1 = 0.0;  // v[r] = sum_a x_w[r][a] u[a] = sum_a xt[a][r] u[a]
+    for (int k0 = 0; k0 < p; k0 += 8) {
+      float e0[8], e1[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int k = k0 + u;
-      if (k < n_mid) {
-        const double vk = lane_read_d(k < 64 ? v0 : v1, k & 63);
-        w0 = fma(static_cast<double>(e0[u]), vk, w0);
-        w1 = fma(static_cast<double>(e1[u]), vk, w1);
+      for (int u = 0; u < 8; ++u) {
+        const int k = min(k0 + u, RRR_MAX - 1);
+        e0[u] = xt[k * xst + lane];
+        e1[u] = xt[k * xst + lane + 64];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + u;
+        if (k < p) {
+          const double uk = static_cast<double>(lane_read(k < 64 ? u0 : u1, k & 63));
+          v0 = fma(static_cast<double>(e0[u]), uk, v0);
+          v1 = fma(static_cast<double>(e1[u]), uk, v1);
+        }
+      }
+    }
+    for (int k0 = 0; k0 < m; k0 += 8) {  // w[a] = sum_r xt[a][r] v[r]
+      float e0[8], e1[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = min(k0 + u, RRR_MAX - 1);
+        e0[u] = xt[lane * xst + k];
+        e1[u] = xt[(lane + 64) * xst + k];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int k = k0 + u;
+        if (k < m) {
+          const double vk = lane_read_d(k < 64 ? v0 : v1, k & 63);
+          w0 = fma(static_cast<double>(e0[u]), vk, w0);
+          w1 = fma(static_cast<double>(e1[u]), vk, w1);
+        }
       }
     }
   }
@@ -1018,9 +1081,10 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_fitted_kernel(const float*
       b0 = y0 - ridge * b0;
       b1 = y1 - ridge * b1;
     } else {
-      b0 = y0;
-      b1 = y1;
-      xt_times(xt, m, lane, b0, b1);  // x_w^T y_w[:, col]
+      float o[4];
+      xt_times(xt, m, p, lane, y0, y1, o);  // x_w^T y_w[:, col] (primal: p <= 128)
+      b0 = o[0];
+      b1 = o[1];
       ridge_solve_refined(ls, xt, false, m, p, ridge, lane, b0, b1);
       float f0 = 0.0f, f1 = 0.0f;  // F[r] = sum_a x_w[r][a] W[a]
       for (int r = 0; r < m; ++r) {
@@ -1099,15 +1163,18 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* 
   if (wv >= rank) return;
   const int j = wv;
   float b0 = zs[lane][j], b1 = zs[lane + 64][j];  // zero at rows >= m
+  float o[4];
   if (dual) {
     ridge_solve_refined(ls, xt, true, m, p, ridge, lane, b0, b1);
-    xt_times(xt, m, lane, b0, b1);
+    xt_times(xt, m, p, lane, b0, b1, o);
   } else {
-    xt_times(xt, m, lane, b0, b1);
-    ridge_solve_refined(ls, xt, false, m, p, ridge, lane, b0, b1);
+    xt_times(xt, m, p, lane, b0, b1, o);
+    ridge_solve_refined(ls, xt, false, m, p, ridge, lane, o[0], o[1]);
   }
-  if (lane < p) left[(h * p + lane) * rank + j] = b0;
-  if (lane + 64 < p) left[(h * p + lane + 64) * rank + j] = b1;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (lane + 64 * q < p) left[(h * p + lane + 64 * q) * rank + j] = o[q];
+  }
 }
 
 // Per head: recovered = any non-finite value in the five state tensors; the output takes the
@@ -1328,7 +1395,12 @@ int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t
                    float* y_mean, float* left, float* basis, void* workspace, size_t workspace_bytes,
                    hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && m >= 1 && p >= 1 && d >= 1, "spr_rrr_fit: bad size");
-  SPR_REQUIRE(m <= RRR_MAX && p <= RRR_MAX && d <= RRR_MAX, "spr_rrr_fit: m, p, d must be at most %d", RRR_MAX);
+  SPR_REQUIRE(m <= RRR_MAX && d <= RRR_MAX, "spr_rrr_fit: m and d must be at most %d (got m=%d, d=%d)", RRR_MAX, m,
+              d);
+  SPR_REQUIRE(p <= 2 * RRR_MAX, "spr_rrr_fit: p must be at most %d (got %d)", 2 * RRR_MAX, p);
+  SPR_REQUIRE(xt_rows(p) * xt_stride(m, p) <= RRR_MAX * RRR_LS,
+              "spr_rrr_fit: p=%d features with m=%d rows exceed the LDS-resident dual solve (64 ceil(p / 64) (m | 1) "
+              "must be at most %d)", p, m, RRR_MAX * RRR_LS);
   SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d && rank <= m,
               "spr_rrr_fit: rank %d outside [1, min(16, d, m)]", rank);
   SPR_REQUIRE(ridge >= 0.0f, "spr_rrr_fit: ridge must be non-negative");
@@ -1398,8 +1470,8 @@ int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t
 
 // x [bh, m, p], y [bh, m, d], weights [bh, m] fp32 (nullable: unit weights, unbiased std);
 // outputs x_mean [bh, p], x_scale [bh, p], y_mean [bh, d], left [bh, p, rank], basis
-// [bh, d, rank] (fp32).  basis_source 0: raw residual, 1: fitted values.  m, p, d <= 128,
-// 1 <= rank <= min(16, d, m).
+// [bh, d, rank] (fp32).  basis_source 0: raw residual, 1: fitted values.  m, d <= 128;
+// p <= 128, or m < p <= 256 with 64 ceil(p / 64) (m | 1) <= 16512; 1 <= rank <= min(16, d, m).
 extern "C" int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
                               int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean,
                               float* x_scale, float* y_mean, float* left, float* basis, void* workspace,

@@ -30,7 +30,8 @@ from .kernels.role_projection import (role_k_projection_normalize, role_kv_proje
 from .kernels.selection import MODE_N8_NATIVE, MODE_TRITON, select_budget, top_p_key_budgets
 from .kernels.svg_ear import (attention_mass_scores_triton, svg_ear_grouped_value_error_scores_triton,
                               svg_ear_value_error_scores_triton)
-from .kernels.residual_repair import n8_exact_probe_scatter_triton, n8_prepare_output_repair_fit_triton
+from .kernels.residual_repair import (n8_exact_probe_scatter_triton, n8_prepare_output_repair_fit_triton,
+                                      n8_prepare_repair_fit_triton)
 from .residual_repair import (
     MODE_FIRST_TOKEN,
     MODE_ROUNDS,
@@ -115,13 +116,11 @@ class N8V6Config:
             raise ValueError("repair_norm_cap must be non-negative.")
         if self.repair_features not in {"output", "output_role"}:
             raise ValueError(f"repair_features must be output or output_role; got {self.repair_features!r}.")
-        if self.repair_features == "output_role":
-            # residual_repair.py:388-475,737-797 (role features appended to the fit's
-            # features) has no HIP kernels here; refuse it instead of running the
-            # output-only repair under the other name.
+        if self.repair_features == "output_role" and (self.role_q_rank % 16 != 0 or self.role_q_rank > 64):
+            # the role-feature apply kernel takes 16, 32, 48 or 64 role features per row
             raise NotImplementedError(
-                "repair_features='output_role' is not supported by the MI355X build: the role-feature fit "
-                "preparation and apply kernels are not built; use repair_features='output'.")
+                f"repair_features='output_role' on the MI355X kernels needs role_q_rank in (16, 32, 48, 64); got "
+                f"{self.role_q_rank}.")
         if self.repair_basis_source not in {"raw_residual", "fitted_residual"}:
             raise ValueError(f"repair_basis_source must be raw_residual or fitted_residual; got "
                              f"{self.repair_basis_source!r}.")
@@ -542,9 +541,6 @@ class N8V6Core:
         batch, heads, tokens, dim = q_video.shape
         bh = batch * heads
         cfg = self.config
-        if cfg.repair_features != "output":
-            raise NotImplementedError(f"repair_features={cfg.repair_features!r} is not supported by the MI355X "
-                                      "build; only the output-feature repair is built.")
         if route.probe_rows is not None and route.probe_weights is not None:
             rows, weights = route.probe_rows, route.probe_weights
             cache_hit = True
@@ -580,13 +576,26 @@ class N8V6Core:
         rows, weights, dense_probe, cache_hit = probes
         base = base_video.contiguous().view(bh, tokens, dim)
         count = int(rows.shape[1])
-        shape = (bh, count, dim)
+        # output_role: the Q role features join the fit's features (n8_v6.py:1246-1290)
+        role = route.q_role_features.contiguous() if cfg.repair_features == "output_role" else None
+        role_dim = 0 if role is None else int(role.shape[2])
+        shape = (bh, count, dim + role_dim)
         if self._fit_feature_buffer is None or tuple(self._fit_feature_buffer.shape) != shape:
             self._fit_feature_buffer = torch.empty(shape, device=base.device, dtype=torch.float32)
-            self._dense_probe_buffer = torch.empty(shape, device=base.device, dtype=torch.float32)
-            self._fit_target_buffer = torch.empty(shape, device=base.device, dtype=torch.float32)
-        x_fit, dense_probe_f, y_fit = n8_prepare_output_repair_fit_triton(
-            base, dense_probe, rows, self._fit_feature_buffer, self._dense_probe_buffer, self._fit_target_buffer)
+            self._dense_probe_buffer = torch.empty((bh, count, dim), device=base.device, dtype=torch.float32)
+            self._fit_target_buffer = torch.empty((bh, count, dim), device=base.device, dtype=torch.float32)
+        if role is not None:
+            x_fit, dense_probe_f, y_fit = n8_prepare_repair_fit_triton(
+                base, role, dense_probe, rows, self._fit_feature_buffer, self._dense_probe_buffer,
+                self._fit_target_buffer)
+        else:
+            x_fit, dense_probe_f, y_fit = n8_prepare_output_repair_fit_triton(
+                base, dense_probe, rows, self._fit_feature_buffer, self._dense_probe_buffer, self._fit_target_buffer)
+        if self.diagnostic_callback is not None:
+            self._emit_diagnostic("probe_fit", tensors={"probe_rows": rows, "probe_weights": weights,
+                                                        "dense_probe": dense_probe_f, "fit_features": x_fit,
+                                                        "fit_targets": y_fit},
+                                  scalars={"phase": "inputs_before_solver", "probe_count": count})
         # The reference's GPU route (n8_v6.py:1310-1320): with fewer probes than D the basis is
         # the top-16 subspace iteration, whose kernel takes exactly 64 probes at D = 128 (the
         # N8 default) and rank 16.  Other counts below D, which the reference's kernel refuses,
@@ -607,7 +616,7 @@ class N8V6Core:
             state = previous
         self.repair_state_current = state
         x_mean, x_scale, y_mean, left, basis = state
-        corrected = apply_reduced_rank_residual(base, None, x_mean, x_scale, y_mean, left, basis, cfg.repair_alpha,
+        corrected = apply_reduced_rank_residual(base, role, x_mean, x_scale, y_mean, left, basis, cfg.repair_alpha,
                                                 cfg.repair_norm_cap)
         n8_exact_probe_scatter_triton(corrected, rows, dense_probe_f)
         info = {
@@ -615,7 +624,7 @@ class N8V6Core:
             "probe_selection_policy": cfg.probe_selection_policy,
             "probe_selection_cache_hit": cache_hit,
             "repair_rank": min(cfg.repair_rank, count, dim),
-            "repair_feature_dim": dim,
+            "repair_feature_dim": dim + role_dim,
             "repair_features": cfg.repair_features,
             "repair_basis_source": cfg.repair_basis_source,
             "repair_backend": "hip_mi355x",

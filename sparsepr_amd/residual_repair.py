@@ -162,6 +162,16 @@ def fit_reduced_rank_residual(x_fit, y_fit, *, rank, ridge, weights=None, output
                         1 if basis_source == "fitted_residual" else 0, top16)
 
 
+def rrr_fit_supported(m: int, p: int, d: int, rank: int) -> bool:
+    """The sizes the LDS-resident fit kernels take: x_w^T lives in 128 x 129 floats, as 128
+    rows of 129 (P <= 128) or, in the dual form, 64 ceil(P / 64) rows of M | 1."""
+    if m > 128 or d > 128 or rank > 16 or p > 256:
+        return False
+    if p <= 128:
+        return True
+    return m < p and 64 * ((p + 63) // 64) * (m | 1) <= 128 * 129
+
+
 def _rrr_fit_hip(x, y, weights, rank, ridge, basis_source=0, top16=False):
     """The fit in 4 launches (raw residual basis) or 7 (fitted values), fp32 whatever
     the input dtype; with top16 the basis comes from the top-16 subspace iteration.
@@ -169,10 +179,10 @@ def _rrr_fit_hip(x, y, weights, rank, ridge, basis_source=0, top16=False):
     dev = _lib.require_gpu(x, y, weights, what="reduced-rank residual fit")
     bh, m, p = (int(v) for v in x.shape)
     d = int(y.shape[2])
-    if max(m, p, d) > 128 or rank > 16:
+    if not rrr_fit_supported(m, p, d, rank):
         raise NotImplementedError(
-            f"The MI355X reduced-rank fit handles M, P, D <= 128 and rank <= 16; got M={m}, P={p}, D={d}, "
-            f"rank={rank}.")
+            f"The MI355X reduced-rank fit handles M, D <= 128, P <= 128 (or M < P <= 256 with "
+            f"64 ceil(P / 64) (M | 1) <= 16512) and rank <= 16; got M={m}, P={p}, D={d}, rank={rank}.")
     if weights is not None and tuple(weights.shape) != (bh, m):
         raise RuntimeError(f"RRR weights must have shape {(bh, m)}, got {tuple(weights.shape)}.")
     x = x.float().contiguous()
@@ -261,22 +271,26 @@ def recover_nonfinite_rrr_state(state, previous):
 
 
 def apply_reduced_rank_residual(base, role, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap):
-    """base + alpha * correction (optional norm cap), in base's dtype (reference :600-646), on
-    the HIP apply kernel: output-only states (role None), bf16 base, D in {64, 128},
-    rank <= 16 (a smaller rank is padded with zero columns, which add nothing)."""
-    if role is not None:
-        raise NotImplementedError("The MI355X repair apply takes output features only; role features "
-                                  "(repair_features='output_role') are not built.")
+    """base + alpha * correction (optional norm cap on the base norm), in base's dtype
+    (reference :600-646), on the HIP apply kernel: bf16 base, D in {64, 128}, role features
+    (role [BH, N, R], R in {16, 32, 48, 64}, the last R rows of left and entries of
+    x_mean / x_scale) or none, rank <= 16 (a smaller rank is padded with zero columns, which
+    add nothing)."""
     bh, tokens, dim = (int(v) for v in base.shape)
     rank = int(left.shape[2])
-    if base.dtype != torch.bfloat16 or dim not in (64, 128) or rank > 16 or int(left.shape[1]) != dim:
+    role_dim = 0 if role is None else int(role.shape[2])
+    if (base.dtype != torch.bfloat16 or dim not in (64, 128) or rank > 16 or int(left.shape[1]) != dim + role_dim
+            or role_dim not in (0, 16, 32, 48, 64)):
         raise NotImplementedError(
-            f"The MI355X repair apply needs a bf16 base with D in (64, 128) and rank <= 16; got {base.dtype}, "
-            f"D={dim}, rank={rank}, left={tuple(left.shape)}.")
-    from .kernels.residual_repair import repair_apply_output
+            f"The MI355X repair apply needs a bf16 base with D in (64, 128), 0, 16, 32, 48 or 64 role features and "
+            f"rank <= 16; got {base.dtype}, D={dim}, role={role_dim}, rank={rank}, left={tuple(left.shape)}.")
+    from .kernels.residual_repair import repair_apply_output, repair_apply_role
 
     if rank < 16:
         left = torch.nn.functional.pad(left.float(), (0, 16 - rank))
         basis = torch.nn.functional.pad(basis.float(), (0, 16 - rank))
+    if role is not None:
+        return repair_apply_role(base.contiguous(), role.contiguous(), x_mean.contiguous(), x_scale.contiguous(),
+                                 y_mean.contiguous(), left.contiguous(), basis.contiguous(), alpha, norm_cap)
     return repair_apply_output(base.contiguous(), x_mean.contiguous(), x_scale.contiguous(), y_mean.contiguous(),
                                left.contiguous(), basis.contiguous(), alpha, norm_cap)

@@ -250,6 +250,74 @@ def test_rrr_fit_top16_matches_oracle(dev, oracle, p, basis_source, weighted):
                                   output_basis_backend="skinny", decomposition_backend="triton_top16")
 
 
+@pytest.mark.parametrize("d,rr", [(128, 64), (128, 16), (64, 48), (64, 64)])
+def test_fit_prep_and_apply_with_role_features(dev, oracle, d, rr):
+    """repair_features "output_role": the fused fit preparation packs [base[rows], role[rows]]
+    exactly (n8_prepare_repair_fit_triton); the apply with role features against the float64
+    oracle on a state fitted to those features (2e-2, bf16 output), with and without the norm
+    cap; at D = 128 with 64 role features through the reference's specialised entry point
+    (n8_repair_apply_triton), whose shape check refuses other sizes."""
+    from sparsepr_amd.kernels.residual_repair import n8_prepare_repair_fit_triton, n8_repair_apply_triton
+    from sparsepr_amd.residual_repair import apply_reduced_rank_residual
+
+    rng = np.random.default_rng(d + rr)
+    bh, n, m = 3, 3000, 64
+    base = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    role = (rng.standard_normal((bh, n, rr)) * 0.7 + 0.2).astype(np.float32)
+    dense = oracle.to_bf16(rng.standard_normal((bh, m, d)).astype(np.float32))
+    rows = np.stack([rng.choice(n, m, replace=False) for _ in range(bh)])
+    bt, rt = to_dev(base, dev, torch.bfloat16), to_dev(role, dev)
+    bufs = [torch.empty((bh, m, d + rr), device=dev), torch.empty((bh, m, d), device=dev),
+            torch.empty((bh, m, d), device=dev)]
+    xf, df, yf = n8_prepare_repair_fit_triton(bt, rt, to_dev(dense, dev, torch.bfloat16), to_dev(rows, dev), *bufs)
+    ref_x = np.concatenate((np.take_along_axis(base, rows[..., None], 1), np.take_along_axis(role, rows[..., None], 1)),
+                           axis=2)
+    assert (xf.cpu().numpy() == ref_x).all() and (df.cpu().numpy() == dense).all()
+    assert (yf.cpu().numpy() == dense - ref_x[:, :, :d]).all()
+    w = rng.uniform(0.5, 2, (bh, m)).astype(np.float32)
+    state = [t.astype(np.float32) for t in oracle.fit_reduced_rank_residual(ref_x, dense - ref_x[:, :, :d], 16, 0.1, w)]
+    st = [to_dev(t, dev) for t in state]
+    for cap in (0.0, 0.05):
+        out = apply_reduced_rank_residual(bt, rt, *st, 0.7, cap)
+        ref = oracle.repair_apply(base, *state, 0.7, cap, role=role)
+        assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
+        if (d, rr) == (128, 64):
+            out2 = n8_repair_apply_triton(bt, rt, *st, 0.7, cap)
+            assert torch.equal(out, out2)
+    if (d, rr) != (128, 64):
+        with pytest.raises(RuntimeError, match="requires D=128, role=64, rank=16"):
+            n8_repair_apply_triton(bt, rt, *st, 0.7, 0.0)
+
+
+@pytest.mark.parametrize("m,p,d,backend", [(64, 192, 128, "triton_top16"), (64, 192, 128, "eigh"),
+                                           (40, 256, 128, "eigh"), (80, 160, 64, "eigh")])
+@pytest.mark.parametrize("basis_source", ["raw_residual", "fitted_residual"])
+def test_rrr_fit_beyond_128_features(dev, oracle, m, p, d, backend, basis_source):
+    """The dual fit with more than 128 features (the output_role fit: P = D + role rank)
+    against the float64 oracle on the same route: statistics to 1e-4, left . basis^T to 2e-3
+    of its maximum; sizes whose x_w^T does not fit the kernels' LDS are refused."""
+    from sparsepr_amd.residual_repair import fit_reduced_rank_residual
+
+    rng = np.random.default_rng(m + p + d + (backend == "eigh") + 2 * (basis_source == "raw_residual"))
+    x = rng.standard_normal((4, m, p)).astype(np.float32)
+    noise = _top16_values(rng, 4, 0.1) if (m, d) == (64, 128) else 0.05 * rng.standard_normal((4, m, d))
+    y = (x @ rng.standard_normal((4, p, d)).astype(np.float32) * 0.02 + noise).astype(np.float32)
+    w = rng.uniform(0.5, 2.0, (4, m)).astype(np.float32)
+    got = fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=16, ridge=0.1, weights=to_dev(w, dev),
+                                    output_basis_backend="skinny", cache_identity=True, fit_backend="dual_cholesky",
+                                    decomposition_backend=backend, basis_source=basis_source)
+    ref = oracle.fit_reduced_rank_residual(x, y, 16, 0.1, w, basis_source=basis_source,
+                                           output_basis_backend="skinny", decomposition_backend=backend)
+    for g, r in zip(got[:3], ref[:3]):
+        assert np.allclose(g.cpu().numpy(), r, rtol=1e-4, atol=1e-5)
+    gl = (got[3] @ got[4].transpose(1, 2)).cpu().numpy()
+    rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
+    assert np.abs(gl - rl).max() <= 2e-3 * np.abs(rl).max()
+    with pytest.raises(NotImplementedError, match="16512"):
+        fit_reduced_rank_residual(torch.zeros((1, 120, 192), device=dev), torch.zeros((1, 120, d), device=dev),
+                                  rank=16, ridge=0.1)
+
+
 def test_rrr_fit_unweighted_single_row_is_recovered(dev):
     """M = 1 without weights: the unbiased std is NaN (as torch.std), the state is non-finite
     and the recovery selects the zero correction."""
@@ -293,8 +361,8 @@ def test_apply_pads_small_rank(dev, oracle):
     out = apply_reduced_rank_residual(to_dev(base, dev, torch.bfloat16), None, *[to_dev(t, dev) for t in st], 0.8, 0.0)
     ref = oracle.repair_apply(base, *st, 0.8, 0.0)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
-    with pytest.raises(NotImplementedError, match="output features only"):
-        apply_reduced_rank_residual(to_dev(base, dev, torch.bfloat16), torch.zeros(1, device=dev),
+    with pytest.raises(NotImplementedError, match="role features"):
+        apply_reduced_rank_residual(to_dev(base, dev, torch.bfloat16), torch.zeros((bh, n, 8), device=dev),
                                     *[to_dev(t, dev) for t in st], 0.8, 0.0)
 
 

@@ -586,6 +586,48 @@ def test_repair_apply_hand_worked(oracle):
     assert np.allclose(capped, [[[4.5, 6.0]]], rtol=0, atol=1e-12)
 
 
+def test_repair_apply_role_features_hand_worked(oracle):
+    """repair_features "output_role": the role features extend the standardised row, and the
+    norm cap compares with the base norm only.  One token by hand: base (1, 2), role (5,);
+    z = ((1-1)/2, (2-1)/4, (5-3)/2) = (0, 1/4, 1); left (1, 2, -1) -> z.left = -1/2;
+    corr = -1/2 (3, -1) + (1/2, -1) = (-1, -1/2); alpha 2 -> (-1, 1).  With cap 0.1: |base| =
+    sqrt 5, |corr| = sqrt(5) / 2, factor 0.2 -> corr (-0.2, -0.1), alpha 2 -> (0.6, 1.8)."""
+    base = np.array([[[1.0, 2.0]]])
+    role = np.array([[[5.0]]])
+    x_mean = np.array([[[1.0, 1.0, 3.0]]])
+    x_scale = np.array([[[2.0, 4.0, 2.0]]])
+    y_mean = np.array([[[0.5, -1.0]]])
+    left = np.array([[[1.0], [2.0], [-1.0]]])
+    basis = np.array([[[3.0], [-1.0]]])
+    out = oracle.repair_apply(base, x_mean, x_scale, y_mean, left, basis, 2.0, 0.0, role=role)
+    assert (out == np.array([[[-1.0, 1.0]]])).all()
+    capped = oracle.repair_apply(base, x_mean, x_scale, y_mean, left, basis, 2.0, 0.1, role=role)
+    assert np.allclose(capped, [[[0.6, 1.8]]], rtol=0, atol=1e-12)
+
+
+def test_repair_apply_role_at_fit_rows_satisfies_normal_equations(oracle):
+    """A full-rank fit on [base, role] features (P = D + R > M: the dual solve) applied at its
+    fit rows with the role rows passed separately: the residual satisfies the ridge normal
+    equations sum w xn^T r = ridge W over all P standardised features."""
+    rng = np.random.default_rng(43)
+    bh, m, d, rr, ridge = 2, 10, 6, 8, 0.4
+    base = rng.standard_normal((bh, m, d)) * 2.0 + 1.0
+    role = rng.standard_normal((bh, m, rr))
+    x = np.concatenate((base, role), axis=2).astype(np.float32)
+    y = (rng.standard_normal((bh, m, d)) + 0.5).astype(np.float32)
+    w = rng.uniform(0.5, 2.0, (bh, m)).astype(np.float32)
+    state = oracle.fit_reduced_rank_residual(x, y, d, ridge, w)
+    pred = oracle.repair_apply(x[:, :, :d], *state, 1.0, 0.0, role=x[:, :, d:]) - x[:, :, :d].astype(np.float64)
+    r = y.astype(np.float64) - pred
+    for h in range(bh):
+        wh = w[h].astype(np.float64)
+        mu = np.average(x[h].astype(np.float64), axis=0, weights=wh)
+        xn = (x[h] - mu) / np.sqrt(np.average((x[h] - mu) ** 2, axis=0, weights=wh))
+        W = state[3][h] @ state[4][h].T
+        assert np.abs(wh @ r[h]).max() <= 1e-9 * np.abs(y[h]).sum()
+        assert np.allclose((xn * wh[:, None]).T @ r[h], ridge * W, atol=1e-8)
+
+
 @pytest.mark.parametrize("m", [40, 8])
 def test_rrr_fitted_basis_by_lstsq(oracle, m):
     """basis_source="fitted_residual": the fitted values from numpy's least squares on the
