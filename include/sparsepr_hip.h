@@ -201,6 +201,20 @@ int spr_block_sparse_attention(const void* q, const void* k, const void* v, cons
                                int32_t d, int32_t qn, int32_t kn, float scale, const int32_t* q_index,
                                const int32_t* k_index, void* out, float* lse, void* workspace, size_t workspace_bytes,
                                hipStream_t stream);
+/* spr_block_sparse_attention_run / spr_block_sparse_attention for every element type and
+ * head dim the reference's attention takes (kmeans_utils.py:1847-2161 Triton: d in
+ * {16, 32, 64, 128}; FlashInfer, kmeans_utils.py:2164-2350: bf16 or fp16): q, k, v and out of
+ * dtype 0 bf16 / 1 fp16 (the probabilities P are rounded to the same type); d in
+ * {16, 32, 64, 128}.  The calls above are dtype 0. */
+int spr_block_sparse_attention_run_ex(const void* q, const void* k, const void* v, const void* plan,
+                                      size_t plan_bytes, int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d, int32_t qn,
+                                      int32_t kn, float scale, int32_t dtype, const int32_t* q_index,
+                                      const int32_t* k_index, void* out, float* lse, hipStream_t stream);
+int spr_block_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* map,
+                                  const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q, int64_t bh_kv,
+                                  int64_t s, int32_t d, int32_t qn, int32_t kn, float scale, int32_t dtype,
+                                  const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
+                                  void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* No counterpart in the reference: spr_block_sparse_attention for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops that forbid
  * hipMalloc).  Same arguments and results, with the plan kept in a fixed 64 MiB device
@@ -229,6 +243,13 @@ int spr_dense_attention_strided(const void* q, const void* k, const void* v, int
                                 int64_t s_kv, int64_t kv_head_stride, int32_t d, float scale, int32_t nsplit,
                                 void* out, int32_t out_dtype, float* lse, void* workspace, size_t workspace_bytes,
                                 hipStream_t stream);
+/* spr_dense_attention_strided with q, k, v of dtype 0 bf16 / 1 fp16, d in {16, 32, 64, 128}
+ * and out_dtype 0 bf16, 1 fp16 or 2 fp32 (F.scaled_dot_product_attention takes either
+ * half type). */
+int spr_dense_attention_strided_ex(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv,
+                                   int64_t m, int64_t s_kv, int64_t kv_head_stride, int32_t d, float scale,
+                                   int32_t dtype, int32_t nsplit, void* out, int32_t out_dtype, float* lse,
+                                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---------------------------------------------------------------- N8 residual repair
  * residual_repair.py:36-118 select_role_equal_probes(_vectorized), group distances:

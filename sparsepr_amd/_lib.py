@@ -68,6 +68,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            _vp, _sz, _vp]),
     "spr_dense_attention_strided": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _vp,
                                                    _i32, _vp, _vp, _sz, _vp]),
+    "spr_block_sparse_attention_run_ex": (ctypes.c_int, [_vp, _vp, _vp, _vp, _sz, _i64, _i64, _i64, _i32, _i32, _i32,
+                                                         _f32, _i32, _vp, _vp, _vp, _vp, _vp]),
+    "spr_block_sparse_attention_ex": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,
+                                                     _f32, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "spr_dense_attention_strided_ex": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _i32,
+                                                      _i32, _vp, _i32, _vp, _vp, _sz, _vp]),
     # repair.hip
     "spr_probe_distances": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp]),
     "spr_probe_select_workspace": (_sz, [_i64, _i32]),

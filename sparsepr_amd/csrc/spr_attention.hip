@@ -35,6 +35,7 @@
 // double-buffered, the next chunk fetched while the current one computes).
 #include "spr_common.h"
 #include <mutex>
+#include <type_traits>
 
 namespace {
 
@@ -65,6 +66,46 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// The element type of Q, K, V, P and the output: bf16 (F16 false) or fp16 (F16 true).  The
+// MFMA, the packing of two fp32 values (round to nearest even) and the row sum of two
+// packed probabilities (v_dot2_f32_bf16 / v_dot2_f32_f16) follow it.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+template <bool F16>
+__device__ __forceinline__ spr::f32x16 mfma16(u32x4 a, u32x4 b, spr::f32x16 c) {
+  if constexpr (F16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(b), c, 0, 0, 0);
+  }
+}
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2t(float lo, float hi) {
+  if constexpr (F16) {
+    const f16x2_t v = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    return pack2(lo, hi);
+  }
+}
+// acc + lo + hi of a packed pair
+template <bool F16>
+__device__ __forceinline__ float dot2_ones(uint32_t pk, float acc) {
+  if constexpr (F16) {
+    const f16x2_t ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pk), ones, acc, false);
+  } else {
+    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, acc, false);
+  }
+}
+// two NaNs of the element type
+template <bool F16>
+constexpr uint32_t nan_pair() {
+  return F16 ? 0x7E007E00u : 0x7FC07FC0u;
+}
+
 // max / sum of x over lanes l and l ^ 32 (v_permlane32_swap exchanges the upper
 // half-wave of one operand with the lower half of the other, so the two results
 // hold x[l] and x[l ^ 32] in some order; max and + are symmetric in them).
@@ -92,18 +133,24 @@ __device__ __forceinline__ int v_col(int p) { return (p & ~12) | ((p & 4) << 1) 
 // output is rescaled; p = 2^(s - m) stays below 2^8 in between.
 constexpr float RESCALE_SLACK = 8.0f;
 
+// D = 16: one 32-dim block of O^T whose rows 16 .. 31 (V^T rows kept at zero) are not
+// stored.  With fewer K pieces or V pairs per chunk than threads, the threads past them
+// load and stash nothing.
 template <int D, int NTHREADS>
 struct Tile {
   static constexpr int KSTEPS = D / 16;
-  static constexpr int DBLK = D / 32;
+  static constexpr int DBLK = D >= 32 ? D / 32 : 1;
+  static constexpr int VD = 32 * DBLK;       // dim rows of the V^T tile
   static constexpr int K_ROW = D * 2 + 16;   // bytes per key row of the K tile (+16 pad)
   static constexpr int V_ROW = BN * 2 + 16;  // bytes per dim row of the V^T tile (+16 pad: 8 consecutive
                                              // rows cover all 32 banks, so 128-bit reads are conflict-free)
   static constexpr int K_BYTES = BN * K_ROW;
-  static constexpr int V_BYTES = D * V_ROW;
-  static constexpr int K_PIECES = BN * D / 8 / NTHREADS;       // 16-byte K pieces per thread
-  static constexpr int V_PAIRS = (BN / 2) * (D / 8) / NTHREADS;  // (2 rows x 16 bytes) per thread
-  static_assert(K_PIECES >= 1 && V_PAIRS >= 1, "unsupported head dim");
+  static constexpr int V_BYTES = VD * V_ROW;
+  static constexpr int K_ITEMS = BN * D / 8;         // 16-byte K pieces per chunk
+  static constexpr int V_ITEMS = (BN / 2) * (D / 8);  // (2 rows x 16 bytes) V pairs per chunk
+  static constexpr int K_PIECES = (K_ITEMS + NTHREADS - 1) / NTHREADS;  // per thread
+  static constexpr int V_PAIRS = (V_ITEMS + NTHREADS - 1) / NTHREADS;
+  static_assert(D % 16 == 0 && D <= 128, "unsupported head dim");
 };
 
 // ---------------------------------------------------------------------------- plan
@@ -153,11 +200,11 @@ __device__ inline bool plan_matches(const int32_t* base, int64_t bh_kv, int32_t 
 // A plan built for other sizes: the whole (1-D) grid writes NaN over the output [bh_q, s, d]
 // bf16 and the LSE [bh_q, s] (when given), each workgroup a strided share, so the caller sees
 // the mismatch instead of stale memory.  d is 64 or 128, so the output is whole 16-byte pieces.
-__device__ inline void fill_nan_output(uint16_t* out, float* lse, int64_t bh_q, int32_t s, int32_t d) {
+__device__ inline void fill_nan_output(uint16_t* out, float* lse, int64_t bh_q, int32_t s, int32_t d, uint32_t nan2) {
   const int64_t step = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t pieces = bh_q * s * (d / 8);
-  const spr::u32x4 nan8 = {0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u};
+  const spr::u32x4 nan8 = {nan2, nan2, nan2, nan2};
   for (int64_t i = first; i < pieces; i += step) reinterpret_cast<spr::u32x4*>(out)[i] = nan8;
   if (lse != nullptr) {
     for (int64_t i = first; i < bh_q * s; i += step) lse[i] = __builtin_nanf("");
@@ -312,7 +359,7 @@ __global__ __launch_bounds__(THREADS) void attn_plan_kernel(const uint8_t* __res
 // QB = 2 runs one wave per SIMD with the output accumulators in AGPRs: every K
 // and V fragment read from LDS then feeds two MFMAs, and each wave carries twice
 // as many independent MFMA chains.
-template <int D, int MODE, bool SEGL, int NW, int QB, bool KIDX>
+template <int D, int MODE, bool SEGL, int NW, int QB, bool KIDX, bool F16>
 __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     int32_t s_q, int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan,
@@ -347,7 +394,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     bhq = logical / tiles_per_head;
     const int32_t t = static_cast<int32_t>(logical - bhq * tiles_per_head);
     if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) {
-      fill_nan_output(out, lse, bh_q, s_q, D);
+      fill_nan_output(out, lse, bh_q, s_q, D, nan_pair<F16>());
       return;
     }
     if (bhq >= bh_q) return;
@@ -463,10 +510,15 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   };
   int32_t krow[T::K_PIECES];  // key rows of this thread's K pieces in the next chunk to fetch
   int32_t vrow[2];              // key rows of this thread's two V rows
+  // K piece i of this thread: item tid + i NT (valid below K_ITEMS) is row item / (D / 8),
+  // piece item % (D / 8); V pair i: item tid + i NT (valid below V_ITEMS) is rows 2 rp,
+  // 2 rp + 1 (rp = tid % 32, the same for every i) and piece item / 32
+  auto k_live = [&](int i) { return tid + i * NT < T::K_ITEMS; };
+  auto v_live = [&](int i) { return tid + i * NT < T::V_ITEMS; };
   auto load_rows = [&](int c) {  // plain copies, so nothing waits on these reads until fetch()
     const int32_t* kr = key_rows[c % 4];
 #pragma unroll
-    for (int i = 0; i < T::K_PIECES; ++i) krow[i] = kr[tid / (D / 8) + i * (NT / (D / 8))];
+    for (int i = 0; i < T::K_PIECES; ++i) krow[i] = k_live(i) ? kr[(tid + i * NT) / (D / 8)] : 0;
     const int rp = tid % (BN / 2);
     vrow[0] = kr[2 * rp];
     vrow[1] = kr[2 * rp + 1];
@@ -478,7 +530,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   auto fetch_v = [&]() {
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
-      const int pc = tid / (BN / 2) + i * (NT / (BN / 2));
+      const int pc = v_live(i) ? (tid + i * NT) / (BN / 2) : 0;
       vreg[i][0] = bload(v_rsrc, vrow[0] * (D * 2) + pc * 16);
       vreg[i][1] = bload(v_rsrc, vrow[1] * (D * 2) + pc * 16);
     }
@@ -486,7 +538,8 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
   auto stash_k = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < T::K_PIECES; ++i) {
-      const int r = tid / (D / 8) + i * (NT / (D / 8));
+      if (!k_live(i)) continue;
+      const int r = (tid + i * NT) / (D / 8);
       const int pc = tid % (D / 8);
       *reinterpret_cast<u32x4*>(&k_tile[buf][r * T::K_ROW + pc * 16]) = kreg[i];
     }
@@ -496,7 +549,8 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     const int vc = v_col(2 * rp);  // keys 2rp, 2rp + 1 land in columns vc, vc + 1
 #pragma unroll
     for (int i = 0; i < T::V_PAIRS; ++i) {
-      const int pc = tid / (BN / 2) + i * (NT / (BN / 2));
+      if (!v_live(i)) continue;
+      const int pc = (tid + i * NT) / (BN / 2);
       const uint32_t a[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
       const uint32_t b[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
 #pragma unroll
@@ -510,6 +564,12 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
     }
   };
 
+  if constexpr (T::VD > D) {  // V^T rows past the head dim stay zero in both buffers
+    for (int e = tid; e < 2 * (T::VD - D) * (T::V_ROW / 4); e += NT) {
+      const int b = e / ((T::VD - D) * (T::V_ROW / 4)), w = e % ((T::VD - D) * (T::V_ROW / 4));
+      reinterpret_cast<uint32_t*>(&v_tile[b][D * T::V_ROW])[w] = 0u;
+    }
+  }
   if (nch > 0) {
     if constexpr (MODE == 0 && SEGL) __syncthreads();  // staged segment list visible to wave 0
     plan_chunk(0);
@@ -533,7 +593,6 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
 #pragma unroll
     for (int s = 0; s < T::KSTEPS; ++s) asm volatile("" ::"v"(qf[j][s].x), "v"(qf[j][s].y), "v"(qf[j][s].z), "v"(qf[j][s].w));
   }
-  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
   // Per chunk: K of chunk c + 1 is fetched at the top and stashed after the
   // first 32-key half (its LDS buffer is free since the last barrier), then V of
   // chunk c + 1 is fetched and stashed at the end, so the two staging sets are
@@ -557,8 +616,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
           const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
 #pragma unroll
           for (int j = 0; j < QB; ++j) {
-            s_acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[j][s]), s_acc[j],
-                                                               0, 0, 0);
+            s_acc[j] = mfma16<F16>(a, qf[j][s], s_acc[j]);
           }
         }
       }
@@ -611,12 +669,12 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
         for (int e = 0; e < 16; e += 2) {
           const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[j][e], scale_log2, neg_m));
           const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_acc[j][e + 1], scale_log2, neg_m));
-          const uint32_t pk = pack2(p0, p1);
+          const uint32_t pk = pack2t<F16>(p0, p1);
           pf[j][e / 8][(e % 8) / 2] = pk;
           if (e % 4 == 0) {
-            lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+            lsum0 = dot2_ones<F16>(pk, lsum0);
           } else {
-            lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+            lsum1 = dot2_ones<F16>(pk, lsum1);
           }
         }
         l_run[j] += lsum0 + lsum1;
@@ -630,8 +688,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
 #pragma unroll
           for (int j = 0; j < QB; ++j) {
             const u32x4 bfrag = u32x4{pf[j][tt][0], pf[j][tt][1], pf[j][tt][2], pf[j][tt][3]};
-            o_acc[j][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(bfrag),
-                                                                  o_acc[j][b], 0, 0, 0);
+            o_acc[j][b] = mfma16<F16>(a, bfrag, o_acc[j][b]);
           }
         }
       }
@@ -658,9 +715,10 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int d0 = b * 32 + 8 * i + 4 * half;
+            if (d0 >= D) continue;  // D = 16: the block's upper 16 dims are padding
             uint2 w;
-            w.x = pack2(o_acc[j][b][4 * i] * inv, o_acc[j][b][4 * i + 1] * inv);
-            w.y = pack2(o_acc[j][b][4 * i + 2] * inv, o_acc[j][b][4 * i + 3] * inv);
+            w.x = pack2t<F16>(o_acc[j][b][4 * i] * inv, o_acc[j][b][4 * i + 1] * inv);
+            w.y = pack2t<F16>(o_acc[j][b][4 * i + 2] * inv, o_acc[j][b][4 * i + 3] * inv);
             *reinterpret_cast<uint2*>(orow + d0) = w;
           }
         }
@@ -680,6 +738,7 @@ __global__ __launch_bounds__(NW * 64, QB == 2 ? 1 : 2) void attn_fwd_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int d0 = b * 32 + 8 * i + 4 * half;
+            if (d0 >= D) continue;
             *reinterpret_cast<spr::f32x4*>(po + d0) =
                 spr::f32x4{o_acc[j][b][4 * i], o_acc[j][b][4 * i + 1], o_acc[j][b][4 * i + 2], o_acc[j][b][4 * i + 3]};
           }
@@ -750,7 +809,7 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint8_t* p) {
 // chunk x - 3 (its buffer's previous chunk, x - 4, was last read before it)
 // and waited for before the barrier of chunk x - 1, two chunks later; key rows
 // are planned four chunks ahead.
-template <bool SEGL, bool KIDX>
+template <bool SEGL, bool KIDX, bool F16>
 __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, int32_t s_q,
     int32_t s_kv, int32_t group, int32_t qn, int32_t kn, const int32_t* __restrict__ plan, int32_t bh_q,
@@ -789,7 +848,7 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int64_t slot = logical / tiles_per_head;
   const int32_t tile = static_cast<int32_t>(logical - slot * tiles_per_head);
   if (!plan_matches(plan, bh_q / group, qn, kn, s_q)) {
-    fill_nan_output(out, lse, bh_q, s_q, D);
+    fill_nan_output(out, lse, bh_q, s_q, D, nan_pair<F16>());
     return;
   }
   if (slot >= bh_q) return;
@@ -900,7 +959,6 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
   const int v_lane = (4 * half + tr_i) * DROW + (tr_a & 1) * 8;
   const int v_piece = 2 * tr_g + (tr_a >> 1);
   const int v_x = 4 * tr_i;
-  const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
   auto s_mma = [&](spr::f32x16& acc, const uint8_t* kt, int kbk) {
     acc = spr::f32x16{};
@@ -908,7 +966,7 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
       const u32x4 a = *reinterpret_cast<const u32x4*>(arow + (((2 * s) ^ k_x) << 4));
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(qf[s]), acc, 0, 0, 0);
+      acc = mfma16<F16>(a, qf[s], acc);
     }
   };
   // Row max of half kbk (masked past the end) and lazy rescale; returns -m.
@@ -962,17 +1020,16 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
 #pragma unroll
     for (int st = 0; st < KSTEPS; ++st) {
       if (st + 2 < KSTEPS) ka[(st + 2) % 3] = kfrag(st + 2);
-      acc_next = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(ka[st % 3]), spr::as_bf16x8(qf[st]), acc_next,
-                                                         0, 0, 0);
+      acc_next = mfma16<F16>(ka[st % 3], qf[st], acc_next);
       const int e = 2 * st;
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e], scale_log2, neg_m));
       const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e + 1], scale_log2, neg_m));
-      const uint32_t pk = pack2(p0, p1);
+      const uint32_t pk = pack2t<F16>(p0, p1);
       pf[e / 8][(e % 8) / 2] = pk;
       if (e % 4 == 0) {
-        lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+        lsum0 = dot2_ones<F16>(pk, lsum0);
       } else {
-        lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+        lsum1 = dot2_ones<F16>(pk, lsum1);
       }
     }
     l_run += lsum0 + lsum1;
@@ -990,8 +1047,7 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
       if (f + 2 < 2 * DBLK) va[(f + 2) % 3] = vfrag(f + 2);
       const int tt = f / DBLK;
       const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
-      o_acc[f % DBLK] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(va[f % 3]), spr::as_bf16x8(bfrag),
-                                                                o_acc[f % DBLK], 0, 0, 0);
+      o_acc[f % DBLK] = mfma16<F16>(va[f % 3], bfrag, o_acc[f % DBLK]);
     }
   };
 
@@ -1004,12 +1060,12 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
     for (int e = 0; e < 16; e += 2) {
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e], scale_log2, neg_m));
       const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[e + 1], scale_log2, neg_m));
-      const uint32_t pk = pack2(p0, p1);
+      const uint32_t pk = pack2t<F16>(p0, p1);
       pf[e / 8][(e % 8) / 2] = pk;
       if (e % 4 == 0) {
-        lsum0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum0, false);
+        lsum0 = dot2_ones<F16>(pk, lsum0);
       } else {
-        lsum1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk), ones, lsum1, false);
+        lsum1 = dot2_ones<F16>(pk, lsum1);
       }
     }
     l_run += lsum0 + lsum1;
@@ -1020,8 +1076,7 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
       const u32x2 r1 = lds_read_tr16(vrow + 8 * DROW);
       const int tt = f / DBLK;
       const u32x4 bfrag = u32x4{pf[tt][0], pf[tt][1], pf[tt][2], pf[tt][3]};
-      o_acc[f % DBLK] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(u32x4{r0.x, r0.y, r1.x, r1.y}),
-                                                                spr::as_bf16x8(bfrag), o_acc[f % DBLK], 0, 0, 0);
+      o_acc[f % DBLK] = mfma16<F16>(u32x4{r0.x, r0.y, r1.x, r1.y}, bfrag, o_acc[f % DBLK]);
     }
   };
 
@@ -1246,8 +1301,8 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
       for (int i = 0; i < 4; ++i) {
         const int d0 = b * 32 + 8 * i + 4 * half;
         uint2 w;
-        w.x = pack2(o_acc[b][4 * i] * inv, o_acc[b][4 * i + 1] * inv);
-        w.y = pack2(o_acc[b][4 * i + 2] * inv, o_acc[b][4 * i + 3] * inv);
+        w.x = pack2t<F16>(o_acc[b][4 * i] * inv, o_acc[b][4 * i + 1] * inv);
+        w.y = pack2t<F16>(o_acc[b][4 * i + 2] * inv, o_acc[b][4 * i + 3] * inv);
         *reinterpret_cast<uint2*>(orow + d0) = w;
       }
     }
@@ -1259,7 +1314,7 @@ __global__ __launch_bounds__(512, 1) void attn_pipe_kernel(
 }
 
 // Merge split-key partials: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
-// One thread per (bhq, row, 4 dims).  out_dtype 0 = bf16, 2 = fp32.
+// One thread per (bhq, row, 4 dims).  out_dtype 0 = bf16, 1 = fp16, 2 = fp32.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part_o,
                                                            const float* __restrict__ part_ml, int64_t rows_total,
@@ -1287,10 +1342,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
     acc[3] += w * o[3];
   }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  if (out_dtype == 0) {
+  if (out_dtype == 0 || out_dtype == 1) {
     uint2 w;
-    w.x = pack2(acc[0] * inv, acc[1] * inv);
-    w.y = pack2(acc[2] * inv, acc[3] * inv);
+    w.x = out_dtype == 0 ? pack2(acc[0] * inv, acc[1] * inv) : pack2t<true>(acc[0] * inv, acc[1] * inv);
+    w.y = out_dtype == 0 ? pack2(acc[2] * inv, acc[3] * inv) : pack2t<true>(acc[2] * inv, acc[3] * inv);
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + r * D + d0) = w;
   } else {
     *reinterpret_cast<spr::f32x4*>(static_cast<float*>(out) + r * D + d0) =
@@ -1473,22 +1528,26 @@ extern "C" int spr_block_sparse_attention_plan_schedule(const int32_t* ids, cons
   return block_sparse_plan(nullptr, ids, counts, q_sizes, k_sizes, bh_kv, s, qn, kn, plan, plan_bytes, stream);
 }
 
-// q [bh_q, s, d], k/v [bh_kv, s, d] bf16 (cluster-contiguous), plan from
-// spr_block_sparse_attention_plan; out bf16 [bh_q, s, d]; lse fp32 [bh_q, s]
-// (nullable, natural log).  bh_q must be a multiple of bh_kv (GQA groups).
-// q_index int32 [bh_q, s] (nullable): q, out and lse stay in token order and
-// cluster-sorted row r is token q_index[r] (the Q permutation and its inverse
-// fused into the attention).  k_index int32 [bh_kv, s] (nullable): k and v stay
-// in token order and cluster-sorted key position p is token k_index[p] (the K/V
-// permutation fused into the key gather).
-extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan,
-                                              size_t plan_bytes, int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d,
-                                              int32_t qn, int32_t kn, float scale, const int32_t* q_index,
-                                              const int32_t* k_index, void* out, float* lse, hipStream_t stream) {
+// q [bh_q, s, d], k/v [bh_kv, s, d] (cluster-contiguous) of dtype 0 bf16 / 1 fp16, plan from
+// spr_block_sparse_attention_plan; out [bh_q, s, d] of the same dtype; lse fp32 [bh_q, s]
+// (nullable, natural log).  d in {16, 32, 64, 128}.  bh_q must be a multiple of bh_kv (GQA
+// groups).  q_index int32 [bh_q, s] (nullable): q, out and lse stay in token order and
+// cluster-sorted row r is token q_index[r] (the Q permutation and its inverse fused into the
+// attention).  k_index int32 [bh_kv, s] (nullable): k and v stay in token order and
+// cluster-sorted key position p is token k_index[p] (the K/V permutation fused into the key
+// gather).
+extern "C" int spr_block_sparse_attention_run_ex(const void* q, const void* k, const void* v, const void* plan,
+                                                 size_t plan_bytes, int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d,
+                                                 int32_t qn, int32_t kn, float scale, int32_t dtype,
+                                                 const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
+                                                 hipStream_t stream) {
   SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && s >= 0 && qn >= 1 && kn >= 1, "spr_block_sparse_attention_run: bad size");
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_block_sparse_attention_run: bh_q=%lld not a multiple of bh_kv=%lld",
               (long long)bh_q, (long long)bh_kv);
-  SPR_REQUIRE(d == 64 || d == 128, "spr_block_sparse_attention_run: head dim %d not supported (64, 128)", d);
+  SPR_REQUIRE(d == 16 || d == 32 || d == 64 || d == 128,
+              "spr_block_sparse_attention_run: head dim %d not supported (16, 32, 64, 128)", d);
+  SPR_REQUIRE(dtype == 0 || dtype == 1, "spr_block_sparse_attention_run: dtype must be 0 (bf16) or 1 (fp16), got %d",
+              dtype);
   // the row maximum is taken on unscaled scores and then scaled, which needs scale > 0
   SPR_REQUIRE(scale > 0.0f && scale < __builtin_huge_valf(),
               "spr_block_sparse_attention_run: scale must be positive and finite (got %g)", double(scale));
@@ -1514,57 +1573,90 @@ extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, cons
   dim3 grid(static_cast<uint32_t>(blocks));
   const int32_t group = static_cast<int32_t>(bh_q / bh_kv);
   const float scale_log2 = scale * 1.4426950408889634f;
-#define SPR_ATTN2(DD, SL, KX)                                                                                 \
-  attn_fwd_kernel<DD, 0, SL, ATTN_NW, ATTN_QB, KX><<<grid, ATTN_NW * 64, 0, stream>>>(                      \
-      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
-      static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
-      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles), scale_log2, q_index, k_index,            \
-      static_cast<uint16_t*>(out), lse, 0, nullptr, nullptr, s * DD)
-#define SPR_ATTN(DD, SL)               \
-  do {                                 \
-    if (k_index != nullptr) {          \
-      SPR_ATTN2(DD, SL, true);         \
-    } else {                           \
-      SPR_ATTN2(DD, SL, false);        \
-    }                                  \
-  } while (0)
   const bool seg_lds = kn <= MAX_LDS_SEGS;
-  const int64_t max_tiles_pipe = spr::ceil_div(s, 2 * BM) + qn;
-  dim3 grid_pipe(static_cast<uint32_t>(spr::ceil_div(max_tiles_pipe * bh_q, 8) * 8));
-#define SPR_PIPE(SL, KX)                                                                                      \
-  attn_pipe_kernel<SL, KX><<<grid_pipe, 512, 0, stream>>>(                                                      \
-      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),     \
-      static_cast<int32_t>(s), static_cast<int32_t>(s), group, qn, kn, static_cast<const int32_t*>(plan),    \
-      static_cast<int32_t>(bh_q), static_cast<int32_t>(max_tiles_pipe), scale_log2, q_index, k_index,       \
-      static_cast<uint16_t*>(out), lse)
+  const bool kx = k_index != nullptr;
+  const bool f16 = dtype == 1;
+  const uint16_t* q16 = static_cast<const uint16_t*>(q);
+  const uint16_t* k16 = static_cast<const uint16_t*>(k);
+  const uint16_t* v16 = static_cast<const uint16_t*>(v);
+  const int32_t* pl = static_cast<const int32_t*>(plan);
+  uint16_t* o16 = static_cast<uint16_t*>(out);
+  const int32_t s32 = static_cast<int32_t>(s), bhq32 = static_cast<int32_t>(bh_q);
   if (d == 128) {
-    if (k_index != nullptr) {
-      if (seg_lds) SPR_PIPE(true, true); else SPR_PIPE(false, true);
+    const int64_t max_tiles_pipe = spr::ceil_div(s, 2 * BM) + qn;
+    dim3 grid_pipe(static_cast<uint32_t>(spr::ceil_div(max_tiles_pipe * bh_q, 8) * 8));
+    const int32_t tph = static_cast<int32_t>(max_tiles_pipe);
+    auto pipe = [&](auto sl, auto kxc, auto f) {
+      attn_pipe_kernel<decltype(sl)::value, decltype(kxc)::value, decltype(f)::value><<<grid_pipe, 512, 0, stream>>>(
+          q16, k16, v16, s32, s32, group, qn, kn, pl, bhq32, tph, scale_log2, q_index, k_index, o16, lse);
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    if (seg_lds) {
+      if (kx) { f16 ? pipe(T_{}, T_{}, T_{}) : pipe(T_{}, T_{}, F_{}); }
+      else    { f16 ? pipe(T_{}, F_{}, T_{}) : pipe(T_{}, F_{}, F_{}); }
     } else {
-      if (seg_lds) SPR_PIPE(true, false); else SPR_PIPE(false, false);
+      if (kx) { f16 ? pipe(F_{}, T_{}, T_{}) : pipe(F_{}, T_{}, F_{}); }
+      else    { f16 ? pipe(F_{}, F_{}, T_{}) : pipe(F_{}, F_{}, F_{}); }
     }
-  } else {
-    if (seg_lds) SPR_ATTN(64, true); else SPR_ATTN(64, false);
+    SPR_LAUNCHED("attn_pipe_kernel");
+    return SPR_OK;
   }
-#undef SPR_ATTN
-#undef SPR_ATTN2
-#undef SPR_PIPE
+  auto fwd = [&](auto dd, auto sl, auto kxc, auto f) {
+    attn_fwd_kernel<decltype(dd)::value, 0, decltype(sl)::value, ATTN_NW, ATTN_QB, decltype(kxc)::value,
+                    decltype(f)::value><<<grid, ATTN_NW * 64, 0, stream>>>(
+        q16, k16, v16, s32, s32, group, qn, kn, pl, bhq32, static_cast<int32_t>(max_tiles), scale_log2, q_index,
+        k_index, o16, lse, 0, nullptr, nullptr, s * decltype(dd)::value);
+  };
+  auto by_flags = [&](auto dd) {
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    if (seg_lds) {
+      if (kx) { f16 ? fwd(dd, T_{}, T_{}, T_{}) : fwd(dd, T_{}, T_{}, F_{}); }
+      else    { f16 ? fwd(dd, T_{}, F_{}, T_{}) : fwd(dd, T_{}, F_{}, F_{}); }
+    } else {
+      if (kx) { f16 ? fwd(dd, F_{}, T_{}, T_{}) : fwd(dd, F_{}, T_{}, F_{}); }
+      else    { f16 ? fwd(dd, F_{}, F_{}, T_{}) : fwd(dd, F_{}, F_{}, F_{}); }
+    }
+  };
+  if (d == 64) by_flags(std::integral_constant<int, 64>{});
+  else if (d == 32) by_flags(std::integral_constant<int, 32>{});
+  else by_flags(std::integral_constant<int, 16>{});
   SPR_LAUNCHED("attn_fwd_kernel");
   return SPR_OK;
 }
 
-// Plan + run in one call (workspace = plan buffer).
+extern "C" int spr_block_sparse_attention_run(const void* q, const void* k, const void* v, const void* plan,
+                                              size_t plan_bytes, int64_t bh_q, int64_t bh_kv, int64_t s, int32_t d,
+                                              int32_t qn, int32_t kn, float scale, const int32_t* q_index,
+                                              const int32_t* k_index, void* out, float* lse, hipStream_t stream) {
+  return spr_block_sparse_attention_run_ex(q, k, v, plan, plan_bytes, bh_q, bh_kv, s, d, qn, kn, scale, 0, q_index,
+                                           k_index, out, lse, stream);
+}
+
+// Plan + run in one call (workspace = plan buffer); dtype as spr_block_sparse_attention_run_ex.
+extern "C" int spr_block_sparse_attention_ex(const void* q, const void* k, const void* v, const uint8_t* map,
+                                             const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q,
+                                             int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
+                                             int32_t dtype, const int32_t* q_index, const int32_t* k_index, void* out,
+                                             float* lse, void* workspace, size_t workspace_bytes,
+                                             hipStream_t stream) {
+  if (bh_q == 0 || s == 0) return SPR_OK;
+  int st = spr_block_sparse_attention_plan(map, q_sizes, k_sizes, bh_kv, s, qn, kn, workspace, workspace_bytes,
+                                           stream);
+  if (st != SPR_OK) return st;
+  return spr_block_sparse_attention_run_ex(q, k, v, workspace, workspace_bytes, bh_q, bh_kv, s, d, qn, kn, scale,
+                                           dtype, q_index, k_index, out, lse, stream);
+}
+
+// Plan + run in one call (workspace = plan buffer), bf16.
 extern "C" int spr_block_sparse_attention(const void* q, const void* k, const void* v, const uint8_t* map,
                                           const int32_t* q_sizes, const int32_t* k_sizes, int64_t bh_q,
                                           int64_t bh_kv, int64_t s, int32_t d, int32_t qn, int32_t kn, float scale,
                                           const int32_t* q_index, const int32_t* k_index, void* out, float* lse,
                                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (bh_q == 0 || s == 0) return SPR_OK;
-  int st = spr_block_sparse_attention_plan(map, q_sizes, k_sizes, bh_kv, s, qn, kn, workspace, workspace_bytes,
-                                           stream);
-  if (st != SPR_OK) return st;
-  return spr_block_sparse_attention_run(q, k, v, workspace, workspace_bytes, bh_q, bh_kv, s, d, qn, kn, scale,
-                                        q_index, k_index, out, lse, stream);
+  return spr_block_sparse_attention_ex(q, k, v, map, q_sizes, k_sizes, bh_q, bh_kv, s, d, qn, kn, scale, 0, q_index,
+                                       k_index, out, lse, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t spr_dense_attention_workspace(int64_t bh_q, int64_t m, int32_t d, int32_t nsplit) {
@@ -1590,17 +1682,21 @@ extern "C" int spr_dense_attention(const void* q, const void* k, const void* v, 
 
 // The same with kv head h's rows starting kv_head_stride elements after head h - 1's
 // (rows of d contiguous elements, s_kv of them per head): a slice of the keys of a larger
-// packed tensor is read in place.
-extern "C" int spr_dense_attention_strided(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv,
-                                           int64_t m, int64_t s_kv, int64_t kv_head_stride, int32_t d, float scale,
-                                           int32_t nsplit, void* out, int32_t out_dtype, float* lse, void* workspace,
-                                           size_t workspace_bytes, hipStream_t stream) {
+// packed tensor is read in place.  q, k, v of dtype 0 bf16 / 1 fp16; d in {16, 32, 64, 128};
+// out_dtype 0 bf16, 1 fp16, 2 fp32.
+extern "C" int spr_dense_attention_strided_ex(const void* q, const void* k, const void* v, int64_t bh_q,
+                                              int64_t bh_kv, int64_t m, int64_t s_kv, int64_t kv_head_stride,
+                                              int32_t d, float scale, int32_t dtype, int32_t nsplit, void* out,
+                                              int32_t out_dtype, float* lse, void* workspace, size_t workspace_bytes,
+                                              hipStream_t stream) {
   SPR_REQUIRE(bh_q >= 0 && bh_kv >= 1 && m >= 0 && s_kv >= 0 && nsplit >= 1, "spr_dense_attention: bad size");
   SPR_REQUIRE(kv_head_stride >= s_kv * d, "spr_dense_attention: kv head stride %lld below s_kv * d",
               static_cast<long long>(kv_head_stride));
   SPR_REQUIRE(bh_q % bh_kv == 0, "spr_dense_attention: bh_q not a multiple of bh_kv");
-  SPR_REQUIRE(d == 64 || d == 128, "spr_dense_attention: head dim %d not supported (64, 128)", d);
-  SPR_REQUIRE(out_dtype == 0 || out_dtype == 2, "spr_dense_attention: out_dtype must be 0 or 2");
+  SPR_REQUIRE(d == 16 || d == 32 || d == 64 || d == 128, "spr_dense_attention: head dim %d not supported "
+              "(16, 32, 64, 128)", d);
+  SPR_REQUIRE(dtype == 0 || dtype == 1, "spr_dense_attention: dtype must be 0 (bf16) or 1 (fp16)");
+  SPR_REQUIRE(out_dtype >= 0 && out_dtype <= 2, "spr_dense_attention: out_dtype must be 0, 1 or 2");
   SPR_REQUIRE(scale > 0.0f && scale < __builtin_huge_valf(),
               "spr_dense_attention: scale must be positive and finite (got %g)", double(scale));
   SPR_REQUIRE(s_kv * d * 2 < (int64_t(1) << 31) && m < (int64_t(1) << 31), "spr_dense_attention: too long");
@@ -1621,25 +1717,33 @@ extern "C" int spr_dense_attention_strided(const void* q, const void* k, const v
   const float scale_log2 = scale * 1.4426950408889634f;
   const int64_t rows_total = bh_q * m;
   const uint32_t cblocks = static_cast<uint32_t>(spr::ceil_div(rows_total * (d / 4), 256));
-  if (d == 128) {
-    attn_fwd_kernel<128, 1, false, 4, 1, false><<<grid, THREADS, 0, stream>>>(
+  auto run = [&](auto dd, auto f) -> int {
+    constexpr int DD = decltype(dd)::value;
+    attn_fwd_kernel<DD, 1, false, 4, 1, false, decltype(f)::value><<<grid, THREADS, 0, stream>>>(
         static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
         static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
         scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml, kv_head_stride);
     SPR_LAUNCHED("attn_fwd_kernel(dense)");
-    attn_combine_kernel<128><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
-                                                          nsplit, out_dtype, out, lse);
-  } else {
-    attn_fwd_kernel<64, 1, false, 4, 1, false><<<grid, THREADS, 0, stream>>>(
-        static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v),
-        static_cast<int32_t>(m), static_cast<int32_t>(s_kv), group, 0, 0, nullptr, static_cast<int32_t>(bh_q), 0,
-        scale_log2, nullptr, nullptr, nullptr, nullptr, split_len, part_o, part_ml, kv_head_stride);
-    SPR_LAUNCHED("attn_fwd_kernel(dense)");
-    attn_combine_kernel<64><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m),
-                                                         nsplit, out_dtype, out, lse);
-  }
-  SPR_LAUNCHED("attn_combine_kernel");
-  return SPR_OK;
+    attn_combine_kernel<DD><<<cblocks, 256, 0, stream>>>(part_o, part_ml, rows_total, static_cast<int32_t>(m), nsplit,
+                                                         out_dtype, out, lse);
+    SPR_LAUNCHED("attn_combine_kernel");
+    return SPR_OK;
+  };
+  auto by_dim = [&](auto f) -> int {
+    if (d == 128) return run(std::integral_constant<int, 128>{}, f);
+    if (d == 64) return run(std::integral_constant<int, 64>{}, f);
+    if (d == 32) return run(std::integral_constant<int, 32>{}, f);
+    return run(std::integral_constant<int, 16>{}, f);
+  };
+  return dtype == 1 ? by_dim(std::true_type{}) : by_dim(std::false_type{});
+}
+
+extern "C" int spr_dense_attention_strided(const void* q, const void* k, const void* v, int64_t bh_q, int64_t bh_kv,
+                                           int64_t m, int64_t s_kv, int64_t kv_head_stride, int32_t d, float scale,
+                                           int32_t nsplit, void* out, int32_t out_dtype, float* lse, void* workspace,
+                                           size_t workspace_bytes, hipStream_t stream) {
+  return spr_dense_attention_strided_ex(q, k, v, bh_q, bh_kv, m, s_kv, kv_head_stride, d, scale, 0, nsplit, out,
+                                        out_dtype, lse, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------- allocation-free variant

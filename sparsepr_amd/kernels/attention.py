@@ -12,10 +12,17 @@ from .. import _lib
 _PLAN_CACHE: dict = {}
 
 
+HEAD_DIMS = (16, 32, 64, 128)
+
+
 def _check_qkv(q, k, v, what):
+    """Q/K/V on one GPU, all bfloat16 or all float16, head dim in HEAD_DIMS."""
     dev = _lib.require_gpu(q, k, v, what=what)
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-        raise RuntimeError(f"{what}: bfloat16 Q/K/V required, got {q.dtype}/{k.dtype}/{v.dtype}")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise RuntimeError(f"{what}: bfloat16 or float16 Q/K/V of one dtype required, got "
+                           f"{q.dtype}/{k.dtype}/{v.dtype}")
+    if q.shape[-1] not in HEAD_DIMS:
+        raise RuntimeError(f"{what}: head dim {q.shape[-1]} not supported {HEAD_DIMS}")
     return dev
 
 
@@ -64,8 +71,9 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
                            block_row_sz: torch.Tensor, block_col_sz: torch.Tensor, *, return_lse: bool = False,
                            plan: torch.Tensor | None = None, scale: float | None = None,
                            q_index: torch.Tensor | None = None, k_index: torch.Tensor | None = None):
-    """q [BHq, S, D], k/v [BHkv, S, D] bf16 cluster-contiguous; map [BHkv, Qc, Kc];
-    sizes [BHkv, Qc] / [BHkv, Kc].  Returns out [BHq, S, D] (and lse [BHq, S]).
+    """q [BHq, S, D], k/v [BHkv, S, D] bf16 or fp16 cluster-contiguous, D in (16, 32, 64,
+    128); map [BHkv, Qc, Kc]; sizes [BHkv, Qc] / [BHkv, Kc].  Returns out [BHq, S, D] in
+    the input dtype (and lse [BHq, S]).
 
     With q_index int32 [BHq, S] (the stable argsort of the query labels), q and
     the outputs stay in token order: cluster-sorted row r is token q_index[r].
@@ -105,9 +113,9 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bl
     out = torch.empty_like(qc)
     lse = torch.empty((bh_q, s), dtype=torch.float32, device=dev) if return_lse else None
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(d)
-    _lib.call("spr_block_sparse_attention_run", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(plan),
-              plan.numel(), bh_q, bh_kv, s, d, qn, kn, sc, _lib.ptr(qi), _lib.ptr(ki), _lib.ptr(out), _lib.ptr(lse),
-              _lib.stream(dev))
+    _lib.call("spr_block_sparse_attention_run_ex", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(plan),
+              plan.numel(), bh_q, bh_kv, s, d, qn, kn, sc, _lib.DTYPE_CODE[qc.dtype], _lib.ptr(qi), _lib.ptr(ki),
+              _lib.ptr(out), _lib.ptr(lse), _lib.stream(dev))
     return (out, lse) if return_lse else out
 
 
@@ -130,7 +138,7 @@ def clear_plan_cache():
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float | None = None,
                     out_dtype: torch.dtype = torch.float32, return_lse: bool = False, nsplit: int | None = None):
     """softmax(q k^T * scale) v for few query rows: q [BHq, M, D], k/v [BHkv, S, D]
-    bf16 -> [BHq, M, D] in out_dtype (fp32 or bf16)."""
+    bf16 or fp16 -> [BHq, M, D] in out_dtype (fp32, bf16 or fp16)."""
     dev = _check_qkv(q, k, v, "dense attention")
     bh_q, m, d = q.shape
     bh_kv, s_kv, _ = k.shape
@@ -138,8 +146,8 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale:
         raise RuntimeError("dense attention: K/V shape mismatch")
     if bh_q % bh_kv != 0:
         raise RuntimeError("dense attention: Q heads must be a multiple of KV heads")
-    if out_dtype not in (torch.float32, torch.bfloat16):
-        raise RuntimeError("dense attention: out_dtype must be float32 or bfloat16")
+    if out_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise RuntimeError("dense attention: out_dtype must be float32, bfloat16 or float16")
     if nsplit is None:
         # one round of workgroups, two per CU over the chip's 256 CUs (measured at the
         # C4 shape: 21 splits 0.31 ms, 42 splits 0.32 ms, 43 splits 0.36 ms, since a
@@ -156,7 +164,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale:
     lse = torch.empty((bh_q, m), dtype=torch.float32, device=dev) if return_lse else None
     ws = _lib.workspace(_lib.query("spr_dense_attention_workspace", bh_q, m, d, nsplit), dev)
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(d)
-    _lib.call("spr_dense_attention_strided", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), bh_q, bh_kv, m, s_kv,
-              kc.stride(0) if bh_kv > 1 else s_kv * d, d, sc, nsplit, _lib.ptr(out),
-              0 if out_dtype == torch.bfloat16 else 2, _lib.ptr(lse), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
+    _lib.call("spr_dense_attention_strided_ex", _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), bh_q, bh_kv, m, s_kv,
+              kc.stride(0) if bh_kv > 1 else s_kv * d, d, sc, _lib.DTYPE_CODE[qc.dtype], nsplit, _lib.ptr(out),
+              _lib.DTYPE_CODE[out_dtype], _lib.ptr(lse), _lib.ptr(ws), ws.numel(), _lib.stream(dev))
     return (out, lse) if return_lse else out

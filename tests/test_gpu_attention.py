@@ -87,6 +87,58 @@ def test_block_sparse_matches_closed_form(dev, oracle, B, Hq, Hkv, S, D, qn, kn)
                 assert (got[b, h, r0:r1] == 0).all()
 
 
+@pytest.mark.parametrize("D,f16,Hq,Hkv", [(16, False, 2, 2), (32, False, 4, 2), (16, True, 2, 2), (32, True, 2, 2),
+                                         (64, True, 4, 2), (128, True, 2, 2)])
+def test_block_sparse_head_dims_and_fp16(dev, oracle, D, f16, Hq, Hkv):
+    """The head dims the reference's Triton path takes besides 64 and 128 (16 and 32:
+    kmeans_utils.py:1847-2161) and fp16 Q/K/V (fp16 P and output, as a float16 call of the
+    reference computes), against the float64 closed form of the same rounded inputs:
+    max-abs 2e-2, cosine 0.999, LSE 1e-3; all-dropped rows exactly 0."""
+    from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_flashinfer
+
+    rng = np.random.default_rng(D + 7 * f16 + Hq)
+    S, qn, kn = 700, 6, 11
+    q, k, v, m, qs, ks = _problem(oracle, rng, 1, Hq, Hkv, S, D, qn, kn)
+    tdt = torch.float16 if f16 else torch.bfloat16
+    if f16:  # fresh values rounded to fp16 (the bf16 ones would not use fp16's mantissa)
+        q, k, v = (rng.standard_normal(a.shape).astype(np.float16).astype(np.float32) for a in (q, k, v))
+    out, lse = dynamic_block_sparse_fwd_flashinfer(
+        to_dev(q, dev, tdt), to_dev(k, dev, tdt), to_dev(v, dev, tdt), torch.from_numpy(m),
+        torch.from_numpy(qs).int(), torch.from_numpy(ks).int(), is_cpu=True,
+        num_kv_heads=Hkv if Hkv != Hq else None, return_lse=True)
+    assert out.dtype == tdt and out.shape == (1, Hq, S, D)
+    ref, ref_lse = _reference(oracle, q, k, v, m, qs, ks)
+    got = out.float().cpu().numpy()
+    assert np.abs(got - ref).max() <= ATOL
+    assert _cos(got, ref) >= COS
+    g = lse.cpu().numpy()
+    fin = np.isfinite(ref_lse)
+    assert np.allclose(g[fin], ref_lse[fin], atol=1e-3, rtol=1e-4)
+    assert np.isneginf(g[~fin]).all()
+    for h in range(Hq):
+        r0 = int(qs[0, h // (Hq // Hkv), :1].sum())
+        r1 = r0 + int(qs[0, h // (Hq // Hkv), 1])
+        assert (got[0, h, r0:r1] == 0).all()
+
+
+@pytest.mark.parametrize("D,f16,out", [(16, False, torch.float32), (32, True, torch.float16),
+                                       (128, True, torch.float32), (64, True, torch.bfloat16)])
+def test_dense_probe_attention_head_dims_and_fp16(dev, oracle, D, f16, out):
+    from sparsepr_amd.kernels.attention import dense_attention
+
+    rng = np.random.default_rng(D + f16)
+    tdt = torch.float16 if f16 else torch.bfloat16
+    rnd = (lambda a: a.astype(np.float16).astype(np.float32)) if f16 else oracle.to_bf16
+    q = rnd(rng.standard_normal((3, 100, D)).astype(np.float32))
+    k = rnd(rng.standard_normal((3, 1500, D)).astype(np.float32))
+    v = rnd(rng.standard_normal((3, 1500, D)).astype(np.float32))
+    got = dense_attention(to_dev(q, dev, tdt), to_dev(k, dev, tdt), to_dev(v, dev, tdt), nsplit=3, out_dtype=out)
+    assert got.dtype == out
+    ref = oracle.dense_attention(q, k, v)
+    g = got.float().cpu().numpy()
+    assert np.abs(g - ref).max() <= 1e-2 and _cos(g, ref) >= 0.9999
+
+
 def test_block_sparse_matches_reference_loop(dev, oracle):
     """Against the loop-faithful restatement of dynamic_block_sparse_fwd_torch."""
     from sparsepr_amd.kmeans_utils import dynamic_block_sparse_fwd_triton
