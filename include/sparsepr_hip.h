@@ -279,7 +279,7 @@ int spr_repair_fit_prep(const void* base, int32_t base_dtype, const void* dense,
  *   out = base + alpha * (((base - x_mean) / x_scale) . left . basis^T + y_mean), the
  *   correction's row norm capped at norm_cap when norm_cap > 0.  base/out bf16
  *   [bh, n, d]; x_mean, x_scale, y_mean fp32 [bh, d]; left, basis fp32 [bh, d, rank];
- *   d in {64, 128}, rank 16. */
+ *   d in {64, 128}, rank in {16, 32, 64}. */
 int spr_repair_apply(const void* base, const float* x_mean, const float* x_scale, const float* y_mean,
                      const float* left, const float* basis, int64_t bh, int64_t n, int32_t d, int32_t rank,
                      float alpha, float norm_cap, void* out, hipStream_t stream);
@@ -294,7 +294,7 @@ int spr_repair_fit_prep_role(const void* base, int32_t base_dtype, const float* 
  *   correction's row norm capped at norm_cap times the base row's norm when norm_cap > 0.
  *   role fp32 [bh, n, role_dim], role_dim in {0, 16, 32, 48, 64} (0: spr_repair_apply);
  *   x_mean, x_scale fp32 [bh, d + role_dim]; y_mean fp32 [bh, d]; left fp32
- *   [bh, d + role_dim, rank]; basis fp32 [bh, d, rank]; d in {64, 128}, rank 16. */
+ *   [bh, d + role_dim, rank]; basis fp32 [bh, d, rank]; d in {64, 128}, rank in {16, 32, 64}. */
 int spr_repair_apply_role(const void* base, const float* role, int32_t role_dim, const float* x_mean,
                           const float* x_scale, const float* y_mean, const float* left, const float* basis,
                           int64_t bh, int64_t n, int32_t d, int32_t rank, float alpha, float norm_cap, void* out,
@@ -389,7 +389,7 @@ int spr_role_metric(const void* x, int32_t dtype, int64_t bh, int64_t n, int32_t
 /* residual_repair.py:263-465 fit_reduced_rank_residual / _fit_reduced_rank_residual_fp32 for
  * every configuration it accepts with m, d <= 128, p <= 128 (or, in the dual form, m < p <= 256
  * with 64 ceil(p / 64) (m | 1) <= 16512: the role-feature fit's p = d + role rank) and
- * rank <= 16:
+ * rank <= 64:
  *   weighted standardisation (:364-384; weights == NULL: plain mean and unbiased std);
  *   primal ridge solve for m >= p (:424-434), dual for m < p (:386-423, both fit_backend
  *   forms); the top-rank eigenvectors of the weighted output gram of the raw residual
@@ -398,7 +398,7 @@ int spr_role_metric(const void* x, int32_t dtype, int64_t bh, int64_t n, int32_t
  *   (:463-464).
  *   x [bh, m, p], y [bh, m, d], weights [bh, m] fp32; outputs x_mean [bh, p], x_scale
  *   [bh, p], y_mean [bh, d], left [bh, p, rank], basis [bh, d, rank] (basis columns in
- *   ascending eigenvalue order).  1 <= rank <= min(16, d, m).
+ *   ascending eigenvalue order).  1 <= rank <= min(64, d, m).
  *   workspace: spr_rrr_fit_workspace(bh) bytes of device memory. */
 int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p, int32_t d,
                    int32_t rank, float ridge, int32_t basis_source, float* x_mean, float* x_scale, float* y_mean,
@@ -421,7 +421,7 @@ int spr_rrr_fit_top16(const float* x, const float* y, const float* weights, int6
 int spr_rrr_top16_basis(const float* values, int64_t bh, int32_t power_iters, int32_t inv_sqrt_iters, float* basis,
                         hipStream_t stream);
 /* residual_repair.py:468-506 reduced_rank_output_basis: the top-rank right singular basis of
- * a [bh, m, d] fp32 as the eigenvectors of a^T a (ascending), m, d <= 128, rank <= min(16, d).
+ * a [bh, m, d] fp32 as the eigenvectors of a^T a (ascending), m, d <= 128, rank <= min(64, d).
  * workspace: spr_rrr_fit_workspace(bh) bytes. */
 int spr_rrr_output_basis(const float* a, int64_t bh, int32_t m, int32_t d, int32_t rank, float* basis,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);

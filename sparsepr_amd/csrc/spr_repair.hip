@@ -22,6 +22,7 @@
 #include <algorithm>
 
 #include "spr_common.h"
+#include <type_traits>
 
 namespace {
 
@@ -446,27 +447,46 @@ __global__ __launch_bounds__(256) void repair_apply_kernel(const uint16_t* __res
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= n) return;
   const u32x4* brow = reinterpret_cast<const u32x4*>(base + (bh * n + t) * D);
-  uint32_t packed[D / 2];
+  // Up to rank 32 the row stays in registers; at rank 64 the coordinates take them, and each
+  // pass over the row reads it again (from the cache)
+  constexpr bool HOLD = RK <= 32;
+  uint32_t packed[HOLD ? D / 2 : 1];
+  if constexpr (HOLD) {
 #pragma unroll
-  for (int i = 0; i < D / 8; ++i) {
-    const u32x4 w = brow[i];
-    packed[4 * i] = w.x;
-    packed[4 * i + 1] = w.y;
-    packed[4 * i + 2] = w.z;
-    packed[4 * i + 3] = w.w;
+    for (int i = 0; i < D / 8; ++i) {
+      const u32x4 w = brow[i];
+      packed[4 * i] = w.x;
+      packed[4 * i + 1] = w.y;
+      packed[4 * i + 2] = w.z;
+      packed[4 * i + 3] = w.w;
+    }
   }
+  auto piece = [&](int i) -> u32x4 {  // dims 8 i .. 8 i + 7 as bf16 pairs
+    if constexpr (HOLD) {
+      return u32x4{packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]};
+    } else {
+      return brow[i];
+    }
+  };
   float coords[RK];
 #pragma unroll
   for (int r = 0; r < RK; ++r) coords[r] = 0.0f;
+  float bn = 0.0f;
 #pragma unroll
-  for (int i = 0; i < D / 2; ++i) {
+  for (int i = 0; i < D / 8; ++i) {
+    const u32x4 w = piece(i);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int dd = 2 * i + e;
-      const float b = e ? spr::bf16_hi(packed[i]) : spr::bf16_lo(packed[i]);
-      const float z = (b - mu[dd]) * inv_sd[dd];
+    for (int h = 0; h < 4; ++h) {
 #pragma unroll
-      for (int r = 0; r < RK; ++r) coords[r] = __builtin_fmaf(z, Ls[dd][r], coords[r]);
+      for (int e = 0; e < 2; ++e) {
+        const int dd = 8 * i + 2 * h + e;
+        const float b = e ? spr::bf16_hi(ws[h]) : spr::bf16_lo(ws[h]);
+        bn = __builtin_fmaf(b, b, bn);
+        const float z = (b - mu[dd]) * inv_sd[dd];
+#pragma unroll
+        for (int r = 0; r < RK; ++r) coords[r] = __builtin_fmaf(z, Ls[dd][r], coords[r]);
+      }
     }
   }
   if constexpr (RR > 0) {
@@ -480,34 +500,29 @@ __global__ __launch_bounds__(256) void repair_apply_kernel(const uint16_t* __res
   }
   float scale = alpha;
   if (norm_cap > 0.0f) {
-    float bn = 0.0f, cn = 0.0f;
+    float cn = 0.0f;
 #pragma unroll
-    for (int i = 0; i < D / 2; ++i) {
+    for (int dd = 0; dd < D; ++dd) {
+      float corr = my[dd];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int dd = 2 * i + e;
-        const float b = e ? spr::bf16_hi(packed[i]) : spr::bf16_lo(packed[i]);
-        float corr = my[dd];
-#pragma unroll
-        for (int r = 0; r < RK; ++r) corr = __builtin_fmaf(coords[r], Bs[dd][r], corr);
-        bn = __builtin_fmaf(b, b, bn);
-        cn = __builtin_fmaf(corr, corr, cn);
-      }
+      for (int r = 0; r < RK; ++r) corr = __builtin_fmaf(coords[r], Bs[dd][r], corr);
+      cn = __builtin_fmaf(corr, corr, cn);
     }
     scale = alpha * fminf(1.0f, norm_cap * sqrtf(bn) / fmaxf(sqrtf(cn), 1e-20f));
   }
   u32x4* orow = reinterpret_cast<u32x4*>(out + (bh * n + t) * D);
 #pragma unroll
   for (int i = 0; i < D / 8; ++i) {
+    const u32x4 w = piece(i);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
     uint32_t o[4];
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
-      const uint32_t w = packed[4 * i + h];
       float res[2];
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int dd = 8 * i + 2 * h + e;
-        const float b = e ? spr::bf16_hi(w) : spr::bf16_lo(w);
+        const float b = e ? spr::bf16_hi(ws[h]) : spr::bf16_lo(ws[h]);
         float corr = my[dd];
 #pragma unroll
         for (int r = 0; r < RK; ++r) corr = __builtin_fmaf(coords[r], Bs[dd][r], corr);
@@ -928,15 +943,16 @@ extern "C" int spr_repair_fit_prep(const void* base, int32_t base_dtype, const v
 
 // bf16 base/out [bh, n, d]; role fp32 [bh, n, role_dim] (nullable when role_dim is 0);
 // x_mean, x_scale fp32 [bh, d + role_dim]; y_mean fp32 [bh, d]; left fp32
-// [bh, d + role_dim, rank]; basis fp32 [bh, d, rank]; d in {64, 128}, rank 16, role_dim in
+// [bh, d + role_dim, rank]; basis fp32 [bh, d, rank]; d in {64, 128}, rank in {16, 32, 64}
+// (rank 16 at d = 128 on the MFMA kernel, the others one lane per row), role_dim in
 // {0, 16, 32, 48, 64}.
 extern "C" int spr_repair_apply_role(const void* base, const float* role, int32_t role_dim, const float* x_mean,
                                      const float* x_scale, const float* y_mean, const float* left, const float* basis,
                                      int64_t bh, int64_t n, int32_t d, int32_t rank, float alpha, float norm_cap,
                                      void* out, hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && n >= 0, "spr_repair_apply: bad size");
-  SPR_REQUIRE((d == 128 || d == 64) && rank == 16, "spr_repair_apply: requires D in {64, 128}, rank=16 (got %d, %d)",
-              d, rank);
+  SPR_REQUIRE((d == 128 || d == 64) && (rank == 16 || rank == 32 || rank == 64),
+              "spr_repair_apply: requires D in {64, 128}, rank in {16, 32, 64} (got %d, %d)", d, rank);
   SPR_REQUIRE(role_dim >= 0 && role_dim <= 64 && role_dim % 16 == 0,
               "spr_repair_apply: role_dim must be 0, 16, 32, 48 or 64 (got %d)", role_dim);
   SPR_REQUIRE(bh <= 65535, "spr_repair_apply: bh exceeds 65535");
@@ -948,7 +964,31 @@ extern "C" int spr_repair_apply_role(const void* base, const float* role, int32_
               "spr_repair_apply: base/out/role must be 16-byte aligned");
   const uint16_t* b16 = static_cast<const uint16_t*>(base);
   uint16_t* o16 = static_cast<uint16_t*>(out);
-  if (d == 128) {
+  if (rank != 16) {
+    dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, 256)), static_cast<uint32_t>(bh));
+    auto lane_rows = [&](auto dd, auto rk) {
+      constexpr int DD = decltype(dd)::value, RKK = decltype(rk)::value;
+      switch (role_dim) {
+        case 0: repair_apply_kernel<DD, RKK, 0><<<grid, 256, 0, stream>>>(b16, role, x_mean, x_scale, y_mean, left,
+                                                                            basis, n, alpha, norm_cap, o16); break;
+        case 16: repair_apply_kernel<DD, RKK, 16><<<grid, 256, 0, stream>>>(b16, role, x_mean, x_scale, y_mean, left,
+                                                                              basis, n, alpha, norm_cap, o16); break;
+        case 32: repair_apply_kernel<DD, RKK, 32><<<grid, 256, 0, stream>>>(b16, role, x_mean, x_scale, y_mean, left,
+                                                                              basis, n, alpha, norm_cap, o16); break;
+        case 48: repair_apply_kernel<DD, RKK, 48><<<grid, 256, 0, stream>>>(b16, role, x_mean, x_scale, y_mean, left,
+                                                                              basis, n, alpha, norm_cap, o16); break;
+        default: repair_apply_kernel<DD, RKK, 64><<<grid, 256, 0, stream>>>(b16, role, x_mean, x_scale, y_mean, left,
+                                                                              basis, n, alpha, norm_cap, o16); break;
+      }
+    };
+    using R32 = std::integral_constant<int, 32>;
+    using R64 = std::integral_constant<int, 64>;
+    if (d == 128) {
+      if (rank == 32) lane_rows(std::integral_constant<int, 128>{}, R32{}); else lane_rows(std::integral_constant<int, 128>{}, R64{});
+    } else {
+      if (rank == 32) lane_rows(std::integral_constant<int, 64>{}, R32{}); else lane_rows(std::integral_constant<int, 64>{}, R64{});
+    }
+  } else if (d == 128) {
     SPR_REQUIRE(n * 256 < (int64_t(1) << 31), "spr_repair_apply: a head's rows exceed 2 GiB");
     // one resident workgroup per CU (256 CUs), each walking 256-row batches of one head
     const int64_t per_head = std::max<int64_t>(1, std::min<int64_t>(spr::ceil_div(n, 256), 256 / bh));

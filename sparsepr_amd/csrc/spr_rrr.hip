@@ -2,7 +2,7 @@
 //
 // Replaces _fit_reduced_rank_residual_fp32 (src/sparsepr/models/cosmos3/residual_repair.py:317-465)
 // for every configuration it accepts with M, D <= 128, P <= 128 (or, in the dual form M < P,
-// up to 256 while 64 ceil(P / 64) (M | 1) <= 16512) and rank <= 16:
+// up to 256 while 64 ceil(P / 64) (M | 1) <= 16512) and rank <= 64:
 //   weighted (or, without weights, plain mean and unbiased std) standardisation (:364-384);
 //   the ridge solve in primal form for M >= P (:424-434) and in dual form for M < P (:386-423);
 //   the output basis of the raw residual or of the fitted values (:435-462): the
@@ -44,7 +44,8 @@
 namespace {
 
 constexpr int RRR_MAX = 128;  // M, P, D at most
-constexpr int RRR_MAX_RANK = 16;
+constexpr int RRR_MAX_RANK = 16;   // basis columns per solve block (and the top-16 route's rank)
+constexpr int RRR_MAX_FIT_RANK = 64;  // largest fitted rank
 constexpr int RRR_THREADS = 1024;
 constexpr int RRR_MAT = RRR_MAX * RRR_MAX;  // one workspace matrix (floats)
 constexpr int RRR_LS = RRR_MAX + 1;         // padded LDS row: rows i and i + 1 start one bank apart
@@ -791,16 +792,26 @@ __device__ __forceinline__ void rrr_cholesky(float* sm, float* __restrict__ gmat
 }
 
 // role = blockIdx.y + role0: 0 the eigenvectors of B (slot 1), 1 the Cholesky factor of the
-// ng x ng matrix G (slot 0).
+// ng x ng matrix G (slot 0).  MAXR: the eigen solver's largest rank (16 or 64).
+template <int MAXR>
 __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_factor_kernel(float* __restrict__ ws, int32_t ng, int32_t d,
                                                                     int32_t rank, int32_t role0,
                                                                     float* __restrict__ basis) {
-  __shared__ float sm[EigLayout<RRR_MAX_RANK>::FLOATS];
+  __shared__ float sm[EigLayout<MAXR>::FLOATS];
   const int64_t h = blockIdx.x;
   if (blockIdx.y + role0 == 1) {
     rrr_cholesky(sm, ws_slot(ws, h, 0), ng);
   } else {
-    rrr_eigen<RRR_MAX_RANK>(sm, ws_slot(ws, h, 1), RRR_MAX, d, rank, false, basis + h * d * rank, nullptr);
+    rrr_eigen<MAXR>(sm, ws_slot(ws, h, 1), RRR_MAX, d, rank, false, basis + h * d * rank, nullptr);
+  }
+}
+// the factor kernel for a rank (one template per eigen-solver size)
+inline void launch_rrr_factor(dim3 grid, hipStream_t stream, float* ws, int32_t ng, int32_t d, int32_t rank,
+                              int32_t role0, float* basis) {
+  if (rank <= RRR_MAX_RANK) {
+    rrr_factor_kernel<RRR_MAX_RANK><<<grid, RRR_THREADS, 0, stream>>>(ws, ng, d, rank, role0, basis);
+  } else {
+    rrr_factor_kernel<RRR_MAX_FIT_RANK><<<grid, RRR_THREADS, 0, stream>>>(ws, ng, d, rank, role0, basis);
   }
 }
 
@@ -1102,7 +1113,9 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_fitted_kernel(const float*
   }
 }
 
-// Z = y_w basis, then left = G^-1 x_w^T Z (primal) or x_w^T G^-1 Z (dual).
+// Z = y_w basis, then left = G^-1 x_w^T Z (primal) or x_w^T G^-1 Z (dual), in blocks of 16
+// basis columns (one wave per column of a block; MULTI: more than one block).
+template <bool MULTI>
 __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* __restrict__ x,
                                                                    const float* __restrict__ y,
                                                                    const float* __restrict__ w, int32_t m, int32_t p,
@@ -1123,18 +1136,22 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* 
   const int ng = dual ? m : p;
   const float* yh = y + h * m * d;
   const float* wh = w != nullptr ? w + h * m : nullptr;
-  for (int e = t; e < RRR_MAX * RRR_MAX_RANK; e += RRR_THREADS) {
-    const int r = e / RRR_MAX_RANK, j = e % RRR_MAX_RANK;
-    bs[r][j] = (r < d && j < rank) ? basis[(h * d + r) * rank + j] : 0.0f;
-  }
   load_factor_and_xt(ws_slot(ws, h, 0), ng, x + h * m * p, wh, x_mean + h * p, x_scale + h * p, m, p, ls, xt);
-  // thread (row i, columns c + 8 q): y_w in registers
   const float sw = i < m ? (wh != nullptr ? sqrtf(wh[i]) : 1.0f) : 0.0f;
+  for (int j0 = 0; j0 < (MULTI ? rank : 1); j0 += RRR_MAX_RANK) {
+  // thread (row i, columns c + 8 q): y_w in registers (loaded per block, so that it is not
+  // held through the solves)
   float yw[16];
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
     const int j = c + 8 * q;
     yw[q] = (i < m && j < d) ? (yh[i * d + j] - y_mean[h * d + j]) * sw : 0.0f;
+  }
+  // basis columns j0 .. j0 + 15 (zero past rank); the barrier also ends the previous
+  // block's reads of zs
+  for (int e = t; e < RRR_MAX * RRR_MAX_RANK; e += RRR_THREADS) {
+    const int r = e / RRR_MAX_RANK, j = e % RRR_MAX_RANK;
+    bs[r][j] = (r < d && j0 + j < rank) ? basis[(h * d + r) * rank + j0 + j] : 0.0f;
   }
   __syncthreads();
   // Z[i][*] = sum_k y_w[i][k] basis[k][*], reduced over the 8 lanes of the row
@@ -1160,20 +1177,22 @@ __global__ __launch_bounds__(RRR_THREADS, 1) void rrr_solve_kernel(const float* 
     zs[i][c + 8] = pick16(z, c + 8);
   }
   __syncthreads();
-  if (wv >= rank) return;
-  const int j = wv;
-  float b0 = zs[lane][j], b1 = zs[lane + 64][j];  // zero at rows >= m
-  float o[4];
-  if (dual) {
-    ridge_solve_refined(ls, xt, true, m, p, ridge, lane, b0, b1);
-    xt_times(xt, m, p, lane, b0, b1, o);
-  } else {
-    xt_times(xt, m, p, lane, b0, b1, o);
-    ridge_solve_refined(ls, xt, false, m, p, ridge, lane, o[0], o[1]);
-  }
+  if (j0 + wv < rank) {
+    const int j = j0 + wv;
+    float b0 = zs[lane][wv], b1 = zs[lane + 64][wv];  // zero at rows >= m
+    float o[4];
+    if (dual) {
+      ridge_solve_refined(ls, xt, true, m, p, ridge, lane, b0, b1);
+      xt_times(xt, m, p, lane, b0, b1, o);
+    } else {
+      xt_times(xt, m, p, lane, b0, b1, o);
+      ridge_solve_refined(ls, xt, false, m, p, ridge, lane, o[0], o[1]);
+    }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    if (lane + 64 * q < p) left[(h * p + lane + 64 * q) * rank + j] = o[q];
+    for (int q = 0; q < 4; ++q) {
+      if (lane + 64 * q < p) left[(h * p + lane + 64 * q) * rank + j] = o[q];
+    }
+  }
   }
 }
 
@@ -1401,8 +1420,8 @@ int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t
   SPR_REQUIRE(xt_rows(p) * xt_stride(m, p) <= RRR_MAX * RRR_LS,
               "spr_rrr_fit: p=%d features with m=%d rows exceed the LDS-resident dual solve (64 ceil(p / 64) (m | 1) "
               "must be at most %d)", p, m, RRR_MAX * RRR_LS);
-  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d && rank <= m,
-              "spr_rrr_fit: rank %d outside [1, min(16, d, m)]", rank);
+  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_FIT_RANK && rank <= d && rank <= m,
+              "spr_rrr_fit: rank %d outside [1, min(64, d, m)]", rank);
   SPR_REQUIRE(ridge >= 0.0f, "spr_rrr_fit: ridge must be non-negative");
   SPR_REQUIRE(basis_source == 0 || basis_source == 1, "spr_rrr_fit: basis_source must be 0 (raw) or 1 (fitted)");
   SPR_REQUIRE(!top16 || (m == T16_M && d == T16_D && rank == T16_R),
@@ -1425,7 +1444,7 @@ int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t
     rrr_gram_kernel<<<dim3(nb, 10), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, nullptr,
                                                       0, 0, gkind, gkind, ws);
     SPR_LAUNCHED("rrr_gram_kernel");
-    rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 1, basis);
+    launch_rrr_factor(dim3(nb, 1), stream, ws, ng, d, rank, 1, basis);
     SPR_LAUNCHED("rrr_factor_kernel");
     if (basis_source == 0) {
       rrr_top16_kernel<<<dim3(nb), 256, 0, stream>>>(y, weights, y_mean, nullptr, 0, 0, T16_POWER_ITERS,
@@ -1443,13 +1462,13 @@ int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t
     rrr_gram_kernel<<<dim3(nb, 20), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, nullptr,
                                                       0, 0, gkind, GRAM_RESIDUAL, ws);
     SPR_LAUNCHED("rrr_gram_kernel");
-    rrr_factor_kernel<<<dim3(nb, 2), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 0, basis);
+    launch_rrr_factor(dim3(nb, 2), stream, ws, ng, d, rank, 0, basis);
     SPR_LAUNCHED("rrr_factor_kernel");
   } else {
     rrr_gram_kernel<<<dim3(nb, 10), 256, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean, nullptr,
                                                       0, 0, gkind, gkind, ws);
     SPR_LAUNCHED("rrr_gram_kernel");
-    rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 1, basis);
+    launch_rrr_factor(dim3(nb, 1), stream, ws, ng, d, rank, 1, basis);
     SPR_LAUNCHED("rrr_factor_kernel");
     rrr_fitted_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, ridge, x_mean, x_scale, y_mean,
                                                             ws);
@@ -1458,11 +1477,16 @@ int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t
                                                       ws + 2 * RRR_MAT, int64_t(RRR_SLOTS) * RRR_MAT, RRR_MAX,
                                                       GRAM_PLAIN, GRAM_PLAIN, ws);
     SPR_LAUNCHED("rrr_gram_kernel");
-    rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, ng, d, rank, 0, basis);
+    launch_rrr_factor(dim3(nb, 1), stream, ws, ng, d, rank, 0, basis);
     SPR_LAUNCHED("rrr_factor_kernel");
   }
-  rrr_solve_kernel<<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, ridge, x_mean, x_scale,
+  if (rank > RRR_MAX_RANK) {
+    rrr_solve_kernel<true><<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, ridge, x_mean, x_scale,
                                                          y_mean, ws, basis, left);
+  } else {
+    rrr_solve_kernel<false><<<dim3(nb), RRR_THREADS, 0, stream>>>(x, y, weights, m, p, d, rank, ridge, x_mean, x_scale,
+                                                         y_mean, ws, basis, left);
+  }
   SPR_LAUNCHED("rrr_solve_kernel");
   return SPR_OK;
 }
@@ -1471,7 +1495,7 @@ int rrr_fit_launch(const float* x, const float* y, const float* weights, int64_t
 // x [bh, m, p], y [bh, m, d], weights [bh, m] fp32 (nullable: unit weights, unbiased std);
 // outputs x_mean [bh, p], x_scale [bh, p], y_mean [bh, d], left [bh, p, rank], basis
 // [bh, d, rank] (fp32).  basis_source 0: raw residual, 1: fitted values.  m, d <= 128;
-// p <= 128, or m < p <= 256 with 64 ceil(p / 64) (m | 1) <= 16512; 1 <= rank <= min(16, d, m).
+// p <= 128, or m < p <= 256 with 64 ceil(p / 64) (m | 1) <= 16512; 1 <= rank <= min(64, d, m).
 extern "C" int spr_rrr_fit_ex(const float* x, const float* y, const float* weights, int64_t bh, int32_t m, int32_t p,
                               int32_t d, int32_t rank, float ridge, int32_t basis_source, float* x_mean,
                               float* x_scale, float* y_mean, float* left, float* basis, void* workspace,
@@ -1514,12 +1538,12 @@ extern "C" int spr_rrr_fit(const float* x, const float* y, const float* weights,
 }
 
 // Top-`rank` right singular basis of a [bh, m, d] (fp32): the eigenvectors of a^T a,
-// ascending eigenvalue order.  m, d <= 128, 1 <= rank <= min(16, d).
+// ascending eigenvalue order.  m, d <= 128, 1 <= rank <= min(64, d).
 extern "C" int spr_rrr_output_basis(const float* a, int64_t bh, int32_t m, int32_t d, int32_t rank, float* basis,
                                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
   SPR_REQUIRE(bh >= 0 && m >= 1 && d >= 1 && m <= RRR_MAX && d <= RRR_MAX,
               "spr_rrr_output_basis: m, d must be in [1, %d]", RRR_MAX);
-  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_RANK && rank <= d, "spr_rrr_output_basis: rank %d outside [1, min(16, d)]",
+  SPR_REQUIRE(rank >= 1 && rank <= RRR_MAX_FIT_RANK && rank <= d, "spr_rrr_output_basis: rank %d outside [1, min(64, d)]",
               rank);
   SPR_REQUIRE(bh <= 65535, "spr_rrr_output_basis: too many heads");
   if (bh == 0) return SPR_OK;
@@ -1534,7 +1558,7 @@ extern "C" int spr_rrr_output_basis(const float* a, int64_t bh, int32_t m, int32
   rrr_gram_kernel<<<dim3(nb, 10), 256, 0, stream>>>(nullptr, nullptr, nullptr, m, 1, d, 0.0f, nullptr, nullptr,
                                                     nullptr, a, int64_t(m) * d, d, GRAM_PLAIN, GRAM_PLAIN, ws);
   SPR_LAUNCHED("rrr_gram_kernel");
-  rrr_factor_kernel<<<dim3(nb, 1), RRR_THREADS, 0, stream>>>(ws, 1, d, rank, 0, basis);
+  launch_rrr_factor(dim3(nb, 1), stream, ws, 1, d, rank, 0, basis);
   SPR_LAUNCHED("rrr_factor_kernel");
   return SPR_OK;
 }

@@ -117,12 +117,14 @@ def n8_repair_apply_triton(base, role, x_mean, x_scale, y_mean, left, basis, alp
 
 def repair_apply_role(base, role, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap, out=None):
     """The apply kernel with role features: bf16 base [BH, N, D], D in {64, 128}; role fp32
-    [BH, N, R], R in {16, 32, 48, 64}; rank 16; x_mean / x_scale hold D + R entries."""
+    [BH, N, R], R in {16, 32, 48, 64}; rank 16, 32 or 64; x_mean / x_scale hold D + R
+    entries."""
     bh, tokens, dim = base.shape
     role_dim = int(role.shape[2])
     rank = int(left.shape[2])
-    if dim not in (64, 128) or rank != 16 or base.dtype != torch.bfloat16 or role_dim not in (16, 32, 48, 64):
-        raise RuntimeError(f"repair apply kernel needs bf16 D in (64, 128), role in (16, 32, 48, 64) and rank 16; "
+    if dim not in (64, 128) or rank not in (16, 32, 64) or base.dtype != torch.bfloat16 or role_dim not in (16, 32, 48, 64):
+        raise RuntimeError(f"repair apply kernel needs bf16 D in (64, 128), role in (16, 32, 48, 64) and rank in "
+                           f"(16, 32, 64); "
                            f"got {base.dtype} D={dim} role={role_dim} r={rank}")
     if out is None:
         out = torch.empty_like(base)
@@ -174,11 +176,12 @@ def n8_repair_apply_output_triton(base, x_mean, x_scale, y_mean, left, basis, al
 
 
 def repair_apply_output(base, x_mean, x_scale, y_mean, left, basis, alpha, norm_cap, out=None):
-    """The apply kernel for bf16 base [BH, N, D], D in {64, 128}, rank 16."""
+    """The apply kernel for bf16 base [BH, N, D], D in {64, 128}, rank 16, 32 or 64."""
     bh, tokens, dim = base.shape
     rank = int(left.shape[2])
-    if dim not in (64, 128) or rank != 16 or base.dtype != torch.bfloat16:
-        raise RuntimeError(f"repair apply kernel needs bf16 D in (64, 128) and rank 16; got {base.dtype} D={dim} r={rank}")
+    if dim not in (64, 128) or rank not in (16, 32, 64) or base.dtype != torch.bfloat16:
+        raise RuntimeError(f"repair apply kernel needs bf16 D in (64, 128) and rank in (16, 32, 64); got {base.dtype} "
+                           f"D={dim} r={rank}")
     if out is None:
         out = torch.empty_like(base)
     f = [t.float().contiguous() for t in (x_mean, x_scale, y_mean, left, basis)]

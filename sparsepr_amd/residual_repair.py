@@ -4,8 +4,8 @@ src/sparsepr/models/cosmos3/residual_repair.py).
 Probe selection, the fit-input gathers, the reduced-rank fit (csrc/spr_rrr.hip: primal
 or dual ridge solve, raw or fitted output basis, with or without weights), the
 non-finite state recovery, the low-rank apply and the exact probe scatter are HIP
-kernels.  Configurations outside the kernels' limits (M, P, D > 128, rank > 16, role
-features in the apply) raise instead of falling back to another implementation.
+kernels.  Configurations outside the kernels' limits (M or D > 128, P > 128 outside the dual
+form's LDS bound, rank > 64) raise instead of falling back to another implementation.
 """
 
 from __future__ import annotations
@@ -165,7 +165,7 @@ def fit_reduced_rank_residual(x_fit, y_fit, *, rank, ridge, weights=None, output
 def rrr_fit_supported(m: int, p: int, d: int, rank: int) -> bool:
     """The sizes the LDS-resident fit kernels take: x_w^T lives in 128 x 129 floats, as 128
     rows of 129 (P <= 128) or, in the dual form, 64 ceil(P / 64) rows of M | 1."""
-    if m > 128 or d > 128 or rank > 16 or p > 256:
+    if m > 128 or d > 128 or rank > 64 or p > 256:
         return False
     if p <= 128:
         return True
@@ -182,7 +182,7 @@ def _rrr_fit_hip(x, y, weights, rank, ridge, basis_source=0, top16=False):
     if not rrr_fit_supported(m, p, d, rank):
         raise NotImplementedError(
             f"The MI355X reduced-rank fit handles M, D <= 128, P <= 128 (or M < P <= 256 with "
-            f"64 ceil(P / 64) (M | 1) <= 16512) and rank <= 16; got M={m}, P={p}, D={d}, rank={rank}.")
+            f"64 ceil(P / 64) (M | 1) <= 16512) and rank <= 64; got M={m}, P={p}, D={d}, rank={rank}.")
     if weights is not None and tuple(weights.shape) != (bh, m):
         raise RuntimeError(f"RRR weights must have shape {(bh, m)}, got {tuple(weights.shape)}.")
     x = x.float().contiguous()
@@ -221,8 +221,8 @@ def reduced_rank_output_basis(weighted_fitted, *, rank, backend):
         raise RuntimeError(f"Unknown exact decomposition backend {backend!r}.")
     dev = _lib.require_gpu(weighted_fitted, what="reduced-rank output basis")
     bh, m, d = (int(v) for v in weighted_fitted.shape)
-    if max(m, d) > 128 or rank > 16:
-        raise NotImplementedError(f"The MI355X output basis handles M, D <= 128 and rank <= 16; got M={m}, D={d}, "
+    if max(m, d) > 128 or rank > 64:
+        raise NotImplementedError(f"The MI355X output basis handles M, D <= 128 and rank <= 64; got M={m}, D={d}, "
                                   f"rank={rank}.")
     a = weighted_fitted.float().contiguous()
     basis = torch.empty((bh, d, int(rank)), device=dev, dtype=torch.float32)
@@ -274,21 +274,22 @@ def apply_reduced_rank_residual(base, role, x_mean, x_scale, y_mean, left, basis
     """base + alpha * correction (optional norm cap on the base norm), in base's dtype
     (reference :600-646), on the HIP apply kernel: bf16 base, D in {64, 128}, role features
     (role [BH, N, R], R in {16, 32, 48, 64}, the last R rows of left and entries of
-    x_mean / x_scale) or none, rank <= 16 (a smaller rank is padded with zero columns, which
-    add nothing)."""
+    x_mean / x_scale) or none, rank <= 64 (padded with zero columns, which add nothing, to 16,
+    32 or 64)."""
     bh, tokens, dim = (int(v) for v in base.shape)
     rank = int(left.shape[2])
     role_dim = 0 if role is None else int(role.shape[2])
-    if (base.dtype != torch.bfloat16 or dim not in (64, 128) or rank > 16 or int(left.shape[1]) != dim + role_dim
+    if (base.dtype != torch.bfloat16 or dim not in (64, 128) or rank > 64 or int(left.shape[1]) != dim + role_dim
             or role_dim not in (0, 16, 32, 48, 64)):
         raise NotImplementedError(
             f"The MI355X repair apply needs a bf16 base with D in (64, 128), 0, 16, 32, 48 or 64 role features and "
-            f"rank <= 16; got {base.dtype}, D={dim}, role={role_dim}, rank={rank}, left={tuple(left.shape)}.")
+            f"rank <= 64; got {base.dtype}, D={dim}, role={role_dim}, rank={rank}, left={tuple(left.shape)}.")
     from .kernels.residual_repair import repair_apply_output, repair_apply_role
 
-    if rank < 16:
-        left = torch.nn.functional.pad(left.float(), (0, 16 - rank))
-        basis = torch.nn.functional.pad(basis.float(), (0, 16 - rank))
+    padded = 16 if rank <= 16 else (32 if rank <= 32 else 64)
+    if rank < padded:
+        left = torch.nn.functional.pad(left.float(), (0, padded - rank))
+        basis = torch.nn.functional.pad(basis.float(), (0, padded - rank))
     if role is not None:
         return repair_apply_role(base.contiguous(), role.contiguous(), x_mean.contiguous(), x_scale.contiguous(),
                                  y_mean.contiguous(), left.contiguous(), basis.contiguous(), alpha, norm_cap)

@@ -258,17 +258,20 @@ def test_n8_route_joint_kv_features_and_precisions(dev, oracle, v_weight, precis
     _check_call(oracle, core, q2, k2, v2, cap2, route2, cfg, prev=prev)
 
 
-def test_n8_output_role_repair(dev, oracle):
+@pytest.mark.parametrize("features,rank", [("output_role", 16), ("output", 32), ("output_role", 64)])
+def test_n8_output_role_repair(dev, oracle, features, rank):
     """repair_features "output_role" (n8_v6.py:1246-1371): the fit's features are the base
     output's probe rows and the route's Q role features at those rows (exact), P = 128 + 64
-    features on 64 probes (the dual fit on the top-16 basis); the repaired output against the
-    float64 oracle's fit and apply of the same inputs, probe rows exact."""
+    features on 64 probes (the dual fit; the top-16 basis at rank 16, the exact one at other
+    ranks); and repair_rank 32 / 64.  The repaired output against the float64 oracle's fit
+    and apply of the same inputs, probe rows exact."""
     from sparsepr_amd.n8_v6 import N8V6Config, N8V6Core
 
     q, k, v = _inputs(dev, seed=17)
     B, H, N, D = q.shape
     cfg = N8V6Config(num_q_centroids=96, num_k_centroids=200, kmeans_iter_init=4, probe_rows=64,
-                     target_density=0.25, repair_features="output_role")
+                     target_density=0.25, repair_features=features, repair_rank=rank)
+    role_dim = cfg.role_q_rank if features == "output_role" else 0
     core = N8V6Core(cfg)
     route = core.route(q, k, v)
     g = torch.Generator(device=dev).manual_seed(3)
@@ -277,7 +280,7 @@ def test_n8_output_role_repair(dev, oracle):
     core.diagnostic_callback = cap
     repaired, info = core.repair(base, q, k, v, route)
     torch.cuda.synchronize()
-    assert info["repair_feature_dim"] == D + cfg.role_q_rank
+    assert info["repair_feature_dim"] == D + role_dim and info["repair_rank"] == rank
     rows = cap.get("probe_rows").cpu().numpy()
     w = cap.get("probe_weights").cpu().numpy()
     xfit = cap.get("fit_features").cpu().numpy()
@@ -285,13 +288,14 @@ def test_n8_output_role_repair(dev, oracle):
     dense = cap.get("dense_probe").cpu().numpy()
     bn = base.reshape(H, N, D).float().cpu().numpy()
     role = route.q_role_features.cpu().numpy()
-    want_x = np.concatenate((np.take_along_axis(bn, rows[..., None].astype(np.int64), 1),
-                             np.take_along_axis(role, rows[..., None].astype(np.int64), 1)), axis=2)
+    want_x = np.take_along_axis(bn, rows[..., None].astype(np.int64), 1)
+    if role_dim:
+        want_x = np.concatenate((want_x, np.take_along_axis(role, rows[..., None].astype(np.int64), 1)), axis=2)
     assert np.array_equal(xfit, want_x) and np.array_equal(yfit, dense - want_x[:, :, :D])
     state = oracle.fit_reduced_rank_residual(xfit, yfit, cfg.repair_rank, cfg.repair_ridge, w,
                                              basis_source=cfg.repair_basis_source, output_basis_backend="skinny",
-                                             decomposition_backend="triton_top16")
-    ref = oracle.repair_apply(bn, *state, cfg.repair_alpha, cfg.repair_norm_cap, role=role)
+                                             decomposition_backend="triton_top16" if rank == 16 else "eigh")
+    ref = oracle.repair_apply(bn, *state, cfg.repair_alpha, cfg.repair_norm_cap, role=role if role_dim else None)
     for h in range(H):
         ref[h, rows[h]] = dense[h]
     got = repaired.reshape(H, N, D).float().cpu().numpy()

@@ -318,6 +318,57 @@ def test_rrr_fit_beyond_128_features(dev, oracle, m, p, d, backend, basis_source
                                   rank=16, ridge=0.1)
 
 
+@pytest.mark.parametrize("m,p,d,rank,basis_source", [(128, 128, 128, 32, "raw_residual"),
+                                                      (96, 64, 128, 64, "fitted_residual"),
+                                                      (64, 192, 128, 48, "raw_residual"),
+                                                      (40, 96, 64, 40, "fitted_residual")])
+def test_rrr_fit_ranks_beyond_16(dev, oracle, m, p, d, rank, basis_source):
+    """Ranks above 16 (the solve in blocks of 16 basis columns, the 64-vector eigen solver)
+    against the float64 fit on targets with a gap at the rank: statistics to 1e-4,
+    left . basis^T to 2e-3 of its maximum."""
+    from sparsepr_amd.residual_repair import fit_reduced_rank_residual
+
+    rng = np.random.default_rng(m + p + rank)
+    x = rng.standard_normal((3, m, p)).astype(np.float32)
+    strong = rng.standard_normal((3, m, rank)) @ rng.standard_normal((3, rank, d))
+    y = (0.3 * strong + 0.01 * rng.standard_normal((3, m, d)) + 0.02 * (x[:, :, :1] @ np.ones((1, d)))).astype(
+        np.float32)
+    w = rng.uniform(0.5, 2.0, (3, m)).astype(np.float32)
+    got = fit_reduced_rank_residual(to_dev(x, dev), to_dev(y, dev), rank=rank, ridge=0.1, weights=to_dev(w, dev),
+                                    output_basis_backend="skinny", fit_backend="dual_cholesky",
+                                    decomposition_backend="eigh", basis_source=basis_source)
+    ref = oracle.fit_reduced_rank_residual(x, y, rank, 0.1, w, basis_source=basis_source)
+    for g, r in zip(got[:3], ref[:3]):
+        assert np.allclose(g.cpu().numpy(), r, rtol=1e-4, atol=1e-5)
+    assert tuple(got[3].shape) == (3, p, rank) and tuple(got[4].shape) == (3, d, rank)
+    gl = (got[3] @ got[4].transpose(1, 2)).cpu().numpy()
+    rl = ref[3] @ np.swapaxes(ref[4], 1, 2)
+    assert np.abs(gl - rl).max() <= 2e-3 * np.abs(rl).max()
+
+
+@pytest.mark.parametrize("d,rank,rr", [(128, 32, 0), (128, 64, 16), (64, 64, 0), (64, 24, 32)])
+def test_apply_ranks_beyond_16(dev, oracle, d, rank, rr):
+    """The apply at ranks 32 and 64 (and 24, padded to 32), with and without role features
+    and the norm cap, against the float64 oracle (2e-2, bf16 output)."""
+    from sparsepr_amd.residual_repair import apply_reduced_rank_residual
+
+    rng = np.random.default_rng(d + rank + rr)
+    bh, n = 2, 1500
+    base = oracle.to_bf16(rng.standard_normal((bh, n, d)).astype(np.float32))
+    role = rng.standard_normal((bh, n, rr)).astype(np.float32) if rr else None
+    pp = d + rr
+    st = [rng.standard_normal((bh, 1, pp)).astype(np.float32) * 0.1,
+          rng.uniform(0.5, 2, (bh, 1, pp)).astype(np.float32),
+          rng.standard_normal((bh, 1, d)).astype(np.float32) * 0.1,
+          rng.standard_normal((bh, pp, rank)).astype(np.float32) * 0.03,
+          rng.standard_normal((bh, d, rank)).astype(np.float32) * 0.2]
+    for cap in (0.0, 0.05):
+        out = apply_reduced_rank_residual(to_dev(base, dev, torch.bfloat16), None if role is None else to_dev(role, dev),
+                                          *[to_dev(t, dev) for t in st], 0.8, cap)
+        ref = oracle.repair_apply(base, *st, 0.8, cap, role=role)
+        assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
+
+
 def test_rrr_fit_unweighted_single_row_is_recovered(dev):
     """M = 1 without weights: the unbiased std is NaN (as torch.std), the state is non-finite
     and the recovery selects the zero correction."""
