@@ -374,6 +374,21 @@ int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_sorted, const
                        float jensen_var_cap, const int32_t* k_sizes, int64_t q_heads, int32_t qn, int32_t kn,
                        int64_t kv_heads, int64_t t_stored, int32_t d, int32_t group, int32_t mode, float* scores,
                        hipStream_t stream);
+/* svg_ear.py:289-369 (+ wrapper :603-678) svg_ear_compensation_triton: the sparse output
+ * (numerator sparse, denominator 1, running max lse) extended, in blocks of block_k (16 or 32)
+ * key clusters, by e^(l_c - M) times the V centroid of every valid (count > 0) cluster the
+ * map does not select (reformulation 0 "skipped"), or of every valid cluster minus the
+ * selected ones (1 "n3_residual"); l_c = (tf32(q) . tf32(kc_c)) / sqrt(128) + log(max(count_c,
+ * 1)), the weights TF32-rounded as the reference's dot products see them.
+ * q [bh, tokens, 128] (q_dtype 0 bf16 / 2 fp32), sparse [bh, tokens, 128] (sparse_dtype 0 / 2),
+ * lse fp32 [bh, tokens], qlabels int32 [bh, tokens], dmap uint8 [bh, qc1, kn + 1] (row qlabel
+ * + 1, column cluster + 1), kcentroids / vcentroids fp32 [bh, kn, 128], kcounts fp32 [bh, kn]
+ * -> out fp32 [bh, tokens, 128] = acc / max(denom, 1e-30). */
+int spr_svg_ear_compensation(const void* q, int32_t q_dtype, const void* sparse, int32_t sparse_dtype,
+                             const float* lse, const int32_t* qlabels, const uint8_t* dmap, int32_t qc1,
+                             const float* kcentroids, const float* kcounts, const float* vcentroids, int64_t bh,
+                             int64_t tokens, int32_t d, int32_t kn, int32_t reformulation, int32_t block_k,
+                             float* out, hipStream_t stream);
 
 /* ---------------------------------------------------------------- N8 role metrics and factors
  * operator_kmeans.py:62-92,491-498 covariance / key_metric_from_queries /

@@ -969,6 +969,58 @@ def svg_ear_value_error_scores(qc, k_sorted, v_sorted, kc, vc, sizes, group, var
     return out.astype(np.float32)
 
 
+def svg_ear_compensation(q, sparse, lse, qlabels, dmap, kc, counts, vc, reformulation="skipped", block_k=32):
+    """SVG-EAR compensation (svg_ear.py:289-369 kernel, :603-678 wrapper) in float64.
+
+    Starting from the sparse output (numerator sparse, denominator 1, running max lse), the
+    key clusters are walked in blocks of block_k: logits l_c = (tf32(q) . tf32(kc_c)) /
+    sqrt(D) + log(max(n_c, 1)); a cluster is valid when n_c > 0 and selected when
+    dmap[qlabel + 1, c + 1] != 0.  "skipped" adds e^(l_c - M) tf32-weighted V centroids of
+    the valid unselected clusters; "n3_residual" adds those of every valid cluster and
+    subtracts the selected ones.  Per block the running max M is updated and the state
+    rescaled by e^(M_old - M_new) (NaN where both are -inf, as the reference's exp gives).
+    out = acc / max(denom, 1e-30).  q [BH, T, D]; sparse [BH, T, D]; lse, qlabels [BH, T];
+    dmap [BH, Qc + 1, Kc + 1]; kc, vc [BH, Kc, D]; counts [BH, Kc] -> float32 [BH, T, D]."""
+    q = np.asarray(q, np.float32)
+    bh, t, d = q.shape
+    kn = kc.shape[1]
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    n3 = reformulation == "n3_residual"
+    out = np.empty((bh, t, d), np.float64)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        for h in range(bh):
+            qt = tf32_rna(q[h]).astype(np.float64)
+            acc = np.asarray(sparse[h], np.float64).copy()
+            denom = np.ones(t)
+            row_max = np.asarray(lse[h], np.float64).copy()
+            rows = np.asarray(qlabels[h], np.int64) + 1
+            for k0 in range(0, kn, block_k):
+                k1 = min(k0 + block_k, kn)
+                kct = tf32_rna(np.asarray(kc[h, k0:k1], np.float32)).astype(np.float64)
+                vct = tf32_rna(np.asarray(vc[h, k0:k1], np.float32)).astype(np.float64)
+                cnt = np.asarray(counts[h, k0:k1], np.float64)
+                logits = (qt @ kct.T) * scale + np.log(np.maximum(cnt, 1.0))[None, :]
+                valid = (cnt > 0.0)[None, :]
+                sel = np.asarray(dmap[h], bool)[rows][:, k0 + 1:k1 + 1]
+                take = valid if n3 else (~sel & valid)
+                block_max = np.where(take, logits, -np.inf).max(axis=1)
+                new_max = np.maximum(row_max, block_max)
+                old = np.exp(row_max - new_max)
+                w = np.where(take, np.exp(logits - new_max[:, None]), 0.0)
+                wt = tf32_rna(w.astype(np.float32)).astype(np.float64)
+                if n3:
+                    ws = np.where(sel & valid, w, 0.0)
+                    wst = tf32_rna(ws.astype(np.float32)).astype(np.float64)
+                    acc = acc * old[:, None] + wt @ vct - wst @ vct
+                    denom = denom * old + w.sum(axis=1) - ws.sum(axis=1)
+                else:
+                    acc = acc * old[:, None] + wt @ vct
+                    denom = denom * old + w.sum(axis=1)
+                row_max = new_max
+            out[h] = acc / np.maximum(denom, 1e-30)[:, None]
+    return out.astype(np.float32)
+
+
 def role_projection_rms(x, factor):
     """Role-coordinate projection with row RMS normalisation (role_projection.py:16-55
     kernel, :58-103 wrapper): p = x . tf32(F) (x bf16-representable, so exact in TF32),

@@ -121,6 +121,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                                 _vp, _sz, _vp]),
     # svg_ear.hip
     "spr_svg_ear_scores_flops": (_sz, [_i64, _i32, _i64]),
+    "spr_svg_ear_compensation": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64,
+                                                _i32, _i32, _i32, _i32, _vp, _vp]),
     "spr_svg_ear_scores": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _i32, _i32, _i64, _i64,
                                           _i32, _i32, _i32, _vp, _vp]),
 }

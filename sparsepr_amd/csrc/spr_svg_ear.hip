@@ -511,7 +511,179 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_score_kernel(
   }
 }
 
+// ---------------------------------------------------------------- compensation
+// svg_ear_compensation_triton (svg_ear.py:289-369 kernel, :603-678 wrapper): the sparse
+// output (numerator, denominator 1, running max = its LSE) extended by the centroid
+// approximation of the key clusters the map did not select.  One workgroup per (64 query
+// rows, head); thread t owns row t / 4 and dims 32 (t % 4) .. + 31.  Key clusters go in
+// blocks of BK (the reference's BLOCK_K), their TF32-rounded K and V centroids staged in
+// LDS: the logit of a cluster is the quad's partial TF32 dot products summed over the four
+// lanes (DPP) / sqrt(D) + log(max(count, 1)); per block the running max moves and the state
+// is rescaled, the weights (TF32-rounded, as the reference's tl.dot sees them) times the V
+// centroids are summed apart and then added (N3: all valid clusters added, the selected
+// ones subtracted, as the reference orders it).  fp32 throughout.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  return v;
+}
+constexpr int SC_BQ = 64;
+constexpr int SC_PART = SE_D / 4;
+__device__ __forceinline__ float ldf(const uint16_t* p) { return spr::bf16_to_f32(*p); }  // bf16
+__device__ __forceinline__ float ldf(const float* p) { return *p; }
+template <typename T>
+struct TypeTag {
+  using type = T;
+};
+template <int BK, bool N3, typename TQ, typename TS>
+__global__ __launch_bounds__(256) void svg_ear_compensation_kernel(
+    const TQ* __restrict__ q, const TS* __restrict__ sparse, const float* __restrict__ lse,
+    const int32_t* __restrict__ qlabels, const uint8_t* __restrict__ dmap, int32_t qc1,
+    const float* __restrict__ kc, const float* __restrict__ counts, const float* __restrict__ vc, int64_t tokens,
+    int32_t kn, float scale, float* __restrict__ out) {
+  constexpr int D = SE_D;
+  __shared__ __attribute__((aligned(16))) float kcs[BK][D];
+  __shared__ __attribute__((aligned(16))) float vcs[BK][D];
+  __shared__ float lcnt[BK];
+  __shared__ int32_t cvalid[BK];
+  const int t = threadIdx.x, qi = t >> 2, d0 = SC_PART * (t & 3);
+  const int64_t h = blockIdx.y;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * SC_BQ + qi;
+  const bool live = row < tokens;
+  const int64_t r = live ? row : tokens - 1;  // rows past the end read the last row, store nothing
+  float qv[SC_PART], acc[SC_PART];
+#pragma unroll
+  for (int j = 0; j < SC_PART; ++j) {
+    qv[j] = tf32_rna(ldf(q + (h * tokens + r) * D + d0 + j));
+    acc[j] = ldf(sparse + (h * tokens + r) * D + d0 + j);
+  }
+  float denom = 1.0f;
+  float row_max = lse[h * tokens + r];
+  const int32_t drow = min(max(qlabels[h * tokens + r] + 1, 0), qc1 - 1);
+  const uint8_t* dm = dmap + (h * qc1 + drow) * static_cast<int64_t>(kn + 1) + 1;
+  for (int k0 = 0; k0 < kn; k0 += BK) {
+    __syncthreads();  // the previous block's centroids are read
+    for (int e = t; e < BK * D; e += 256) {
+      const int k = e / D, dd = e - k * D, kk = k0 + k;
+      kcs[k][dd] = kk < kn ? tf32_rna(kc[(h * kn + kk) * D + dd]) : 0.0f;
+      vcs[k][dd] = kk < kn ? tf32_rna(vc[(h * kn + kk) * D + dd]) : 0.0f;
+    }
+    if (t < BK) {
+      const int kk = k0 + t;
+      const float c = kk < kn ? counts[h * kn + kk] : 0.0f;
+      lcnt[t] = logf(fmaxf(c, 1.0f));
+      cvalid[t] = (kk < kn && c > 0.0f) ? 1 : 0;
+    }
+    __syncthreads();
+    float lg[BK];
+    uint32_t take = 0, selm = 0;  // bit k: cluster k0 + k added / (N3) selected and added
+    float bmax = -__builtin_huge_valf();
+#pragma unroll
+    for (int k = 0; k < BK; ++k) {
+      float pdot = 0.0f;
+#pragma unroll
+      for (int j = 0; j < SC_PART; j += 4) {
+        const spr::f32x4 kv = *reinterpret_cast<const spr::f32x4*>(&kcs[k][d0 + j]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pdot = __builtin_fmaf(qv[j + u], kv[u], pdot);
+      }
+      lg[k] = quad_sum(pdot) * scale + lcnt[k];
+      const bool act = live && cvalid[k] != 0;
+      const bool sel = k0 + k < kn ? dm[k0 + k] != 0 : true;
+      const bool tk = N3 ? act : (act && !sel);
+      take |= static_cast<uint32_t>(tk) << k;
+      selm |= static_cast<uint32_t>(N3 && act && sel) << k;
+      if (tk) bmax = fmaxf(bmax, lg[k]);
+    }
+    const float new_max = fmaxf(row_max, bmax);
+    const float old = exp_fast(row_max - new_max);  // NaN when both are -inf, as the reference's
+    float wsum = 0.0f, ssum = 0.0f;
+    float dota[SC_PART], dots[SC_PART];
+#pragma unroll
+    for (int j = 0; j < SC_PART; ++j) dota[j] = dots[j] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < BK; ++k) {
+      const float w = (take >> k) & 1u ? exp_fast(lg[k] - new_max) : 0.0f;
+      const float ws = (selm >> k) & 1u ? w : 0.0f;
+      wsum += w;
+      ssum += ws;
+      const float wt = tf32_rna(w), wst = tf32_rna(ws);
+#pragma unroll
+      for (int j = 0; j < SC_PART; j += 4) {
+        const spr::f32x4 vv = *reinterpret_cast<const spr::f32x4*>(&vcs[k][d0 + j]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          dota[j + u] = __builtin_fmaf(wt, vv[u], dota[j + u]);
+          if constexpr (N3) dots[j + u] = __builtin_fmaf(wst, vv[u], dots[j + u]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < SC_PART; ++j) {
+      acc[j] = acc[j] * old + dota[j];
+      if constexpr (N3) acc[j] -= dots[j];
+    }
+    denom = N3 ? (denom * old + wsum) - ssum : denom * old + wsum;
+    row_max = new_max;
+  }
+  if (live) {
+    const float inv_den = 1.0f / fmaxf(denom, 1e-30f);
+    float* orow = out + (h * tokens + row) * D + d0;
+#pragma unroll
+    for (int j = 0; j < SC_PART; j += 4) {
+      *reinterpret_cast<spr::f32x4*>(orow + j) =
+          spr::f32x4{acc[j] * inv_den, acc[j + 1] * inv_den, acc[j + 2] * inv_den, acc[j + 3] * inv_den};
+    }
+  }
+}
+
 }  // namespace
+
+// q [bh, tokens, 128] (q_dtype 0 bf16 / 2 fp32), sparse [bh, tokens, 128] (sparse_dtype 0 / 2),
+// lse fp32 [bh, tokens], qlabels int32 [bh, tokens], dmap uint8 [bh, qc1, kn + 1] (row
+// qlabel + 1, column cluster + 1), kcentroids / vcentroids fp32 [bh, kn, 128], kcounts fp32
+// [bh, kn] -> out fp32 [bh, tokens, 128].  reformulation 0 "skipped", 1 "n3_residual";
+// block_k 16 or 32.
+extern "C" int spr_svg_ear_compensation(const void* q, int32_t q_dtype, const void* sparse, int32_t sparse_dtype,
+                                        const float* lse, const int32_t* qlabels, const uint8_t* dmap, int32_t qc1,
+                                        const float* kcentroids, const float* kcounts, const float* vcentroids,
+                                        int64_t bh, int64_t tokens, int32_t d, int32_t kn, int32_t reformulation,
+                                        int32_t block_k, float* out, hipStream_t stream) {
+  SPR_REQUIRE(bh >= 0 && tokens >= 0 && kn >= 0 && qc1 >= 1, "spr_svg_ear_compensation: bad size");
+  SPR_REQUIRE(d == SE_D, "spr_svg_ear_compensation: requires DIM=128, got %d", d);
+  SPR_REQUIRE(reformulation == 0 || reformulation == 1, "spr_svg_ear_compensation: reformulation must be 0 or 1");
+  SPR_REQUIRE(block_k == 16 || block_k == 32, "spr_svg_ear_compensation: block_k must be 16 or 32 (got %d)", block_k);
+  SPR_REQUIRE((q_dtype == 0 || q_dtype == 2) && (sparse_dtype == 0 || sparse_dtype == 2),
+              "spr_svg_ear_compensation: q and sparse must be bf16 (0) or fp32 (2)");
+  SPR_REQUIRE(bh <= 65535, "spr_svg_ear_compensation: too many heads");
+  if (bh == 0 || tokens == 0) return SPR_OK;
+  SPR_REQUIRE(q && sparse && lse && qlabels && dmap && out && (kn == 0 || (kcentroids && kcounts && vcentroids)),
+              "spr_svg_ear_compensation: null pointer");
+  const dim3 grid(static_cast<uint32_t>(spr::ceil_div(tokens, SC_BQ)), static_cast<uint32_t>(bh));
+  const float scale = 1.0f / sqrtf(static_cast<float>(d));
+  auto go = [&](auto bk, auto n3, auto tq, auto ts) {
+    using TQ = typename decltype(tq)::type;
+    using TS = typename decltype(ts)::type;
+    svg_ear_compensation_kernel<decltype(bk)::value, decltype(n3)::value, TQ, TS><<<grid, 256, 0, stream>>>(
+        static_cast<const TQ*>(q), static_cast<const TS*>(sparse), lse, qlabels, dmap, qc1, kcentroids, kcounts,
+        vcentroids, tokens, kn, scale, out);
+  };
+  auto by_types = [&](auto bk, auto n3) {
+    using BF = TypeTag<uint16_t>;
+    using F32 = TypeTag<float>;
+    if (q_dtype == 0) {
+      if (sparse_dtype == 0) go(bk, n3, BF{}, BF{}); else go(bk, n3, BF{}, F32{});
+    } else {
+      if (sparse_dtype == 0) go(bk, n3, F32{}, BF{}); else go(bk, n3, F32{}, F32{});
+    }
+  };
+  auto by_mode = [&](auto bk) {
+    if (reformulation == 1) by_types(bk, std::true_type{}); else by_types(bk, std::false_type{});
+  };
+  if (block_k == 16) by_mode(std::integral_constant<int, 16>{}); else by_mode(std::integral_constant<int, 32>{});
+  SPR_LAUNCHED("svg_ear_compensation_kernel");
+  return SPR_OK;
+}
 
 extern "C" size_t spr_svg_ear_scores_flops(int64_t q_heads, int32_t qn, int64_t tokens) {
   return static_cast<size_t>(2) * q_heads * qn * tokens * SE_D;

@@ -3,7 +3,8 @@
 Same names, keyword signatures, validation and error texts as the reference's
 src/sparsepr/kernels/triton/svg_ear.py (attention_mass_scores_triton :372-450,
 svg_ear_value_error_scores_triton :453-531,
-svg_ear_grouped_value_error_scores_triton :534-600).  The Triton tiling
+svg_ear_grouped_value_error_scores_triton :534-600, svg_ear_compensation_triton
+:603-678).  The Triton tiling
 parameters (block_q, block_n, num_warps, num_stages) are validated as the
 reference validates them and otherwise ignored: the HIP kernel has one tiling
 (four waves per (query head, key cluster), 32-token chunks).  K and V must be
@@ -192,3 +193,72 @@ def svg_ear_grouped_value_error_scores_triton(
         raise RuntimeError("Grouped SVG-EAR supports warps={4,8}, stages={1,2,3}.")
     return _launch(MODE_VALUE_ERROR, qcentroids, k_sorted, v_sorted, kcentroids, vcentroids, None, 0.0,
                    kcluster_sizes, gqa_group)
+
+
+def svg_ear_compensation_triton(*, q_flat: torch.Tensor, sparse_flat: torch.Tensor, lse_flat: torch.Tensor,
+                                qlabels_gen: torch.Tensor, dynamic_map_query: torch.Tensor,
+                                kcentroids: torch.Tensor, kcluster_sizes: torch.Tensor, vcentroids: torch.Tensor,
+                                reformulation: str = "skipped", block_q: int = 64, block_k: int = 32) -> torch.Tensor:
+    """The sparse output extended by the centroid approximation of the unselected key
+    clusters (svg_ear.py:289-369 kernel, :603-678 wrapper; the same checks and error texts).
+    Returns fp32 [BH, T, 128].  block_q is ignored (one tiling of 64 rows); block_k, the
+    cluster block of the running max, may be 16 or 32."""
+    del block_q
+    if not q_flat.is_cuda:
+        raise RuntimeError("svg_ear_compensation_triton requires CUDA tensors.")
+    if reformulation not in {"skipped", "n3_residual"}:
+        raise RuntimeError(
+            f"SVG-EAR compensation reformulation must be 'skipped' or 'n3_residual', got {reformulation!r}."
+        )
+    bh, tokens, dim = q_flat.shape
+    clusters = kcentroids.shape[1]
+    if dim != 128:
+        raise RuntimeError(f"SVG-EAR compensation requires DIM=128, got {dim}.")
+    if sparse_flat.shape != (bh, tokens, dim):
+        raise RuntimeError(
+            f"SVG-EAR sparse output shape mismatch: got {tuple(sparse_flat.shape)}, expected {(bh, tokens, dim)}."
+        )
+    if lse_flat.shape != (bh, tokens):
+        raise RuntimeError(f"SVG-EAR LSE shape mismatch: got {tuple(lse_flat.shape)}, expected {(bh, tokens)}.")
+    if qlabels_gen.shape != (bh, tokens):
+        raise RuntimeError(
+            f"SVG-EAR query-label shape mismatch: got {tuple(qlabels_gen.shape)}, expected {(bh, tokens)}."
+        )
+    if dynamic_map_query.ndim != 3 or dynamic_map_query.shape[0] != bh:
+        raise RuntimeError(
+            f"SVG-EAR dynamic-map shape mismatch: got {tuple(dynamic_map_query.shape)}, "
+            f"expected batch-head dimension {bh}."
+        )
+    if dynamic_map_query.shape[2] != clusters + 1:
+        raise RuntimeError(
+            f"SVG-EAR dynamic-map K-cluster mismatch: got {dynamic_map_query.shape[2]}, expected {clusters + 1}."
+        )
+    expected_stats = (bh, clusters, dim)
+    if kcentroids.shape != expected_stats or vcentroids.shape != expected_stats:
+        raise RuntimeError(
+            f"SVG-EAR centroid shape mismatch: K={tuple(kcentroids.shape)}, "
+            f"V={tuple(vcentroids.shape)}, expected={expected_stats}."
+        )
+    if kcluster_sizes.shape != (bh, clusters):
+        raise RuntimeError(
+            f"SVG-EAR cluster-size shape mismatch: got {tuple(kcluster_sizes.shape)}, expected {(bh, clusters)}."
+        )
+    if block_k not in {16, 32}:
+        raise NotImplementedError(f"SVG-EAR compensation on the MI355X kernel takes block_k 16 or 32, got {block_k}.")
+    dev = _lib.require_gpu(q_flat, sparse_flat, lse_flat, qlabels_gen, dynamic_map_query, kcentroids, kcluster_sizes,
+                           vcentroids, what="SVG-EAR compensation")
+    qc = q_flat.contiguous() if q_flat.dtype in (torch.bfloat16, torch.float32) else q_flat.float().contiguous()
+    sc = (sparse_flat.contiguous() if sparse_flat.dtype in (torch.bfloat16, torch.float32)
+          else sparse_flat.float().contiguous())
+    lse = lse_flat.float().contiguous()
+    labels = qlabels_gen.to(torch.int32).contiguous()
+    dmap = (dynamic_map_query != 0).to(torch.uint8).contiguous()
+    kc = kcentroids.float().contiguous()
+    vc = vcentroids.float().contiguous()
+    counts = kcluster_sizes.float().contiguous()
+    out = torch.empty((bh, tokens, dim), device=dev, dtype=torch.float32)
+    _lib.call("spr_svg_ear_compensation", _lib.ptr(qc), _lib.DTYPE_CODE[qc.dtype], _lib.ptr(sc),
+              _lib.DTYPE_CODE[sc.dtype], _lib.ptr(lse), _lib.ptr(labels), _lib.ptr(dmap), int(dmap.shape[1]),
+              _lib.ptr(kc), _lib.ptr(counts), _lib.ptr(vc), bh, tokens, dim, clusters,
+              1 if reformulation == "n3_residual" else 0, int(block_k), _lib.ptr(out), _lib.stream(dev))
+    return out

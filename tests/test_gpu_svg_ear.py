@@ -176,3 +176,50 @@ def test_full_size_value_error_sampled_clusters(dev, oracle):
         err = np.abs(scores[0, :, c].astype(np.float64) - ref[0, :, 0]).max()
         assert err < ATOL, (c, err)
     assert np.isneginf(scores[0][:, s == 0]).all()
+
+
+@pytest.mark.parametrize("reformulation,block_k,sparse_bf16", [("skipped", 32, True), ("n3_residual", 32, False),
+                                                               ("skipped", 16, False), ("n3_residual", 16, True)])
+def test_svg_ear_compensation(dev, oracle, reformulation, block_k, sparse_bf16):
+    """svg_ear_compensation_triton (svg_ear.py:289-369, :603-678) against the float64
+    restatement on the same inputs: 70 key clusters (a partial last block), empty clusters,
+    a random selection map, bf16 queries; max-abs within 2e-3 of the largest output (the
+    TF32 rounding of an fp32 weight can land one step from the float64 one's); the NaN of a
+    row with LSE -inf whose first block adds nothing is reproduced."""
+    from sparsepr_amd.kernels.svg_ear import svg_ear_compensation_triton
+
+    rng = np.random.default_rng(block_k + len(reformulation))
+    bh, t, d, kn, qn = 3, 700, 128, 70, 12
+    q = oracle.to_bf16(rng.standard_normal((bh, t, d)).astype(np.float32))
+    sparse = rng.standard_normal((bh, t, d)).astype(np.float32) * 0.3
+    if sparse_bf16:
+        sparse = oracle.to_bf16(sparse)
+    lse = (rng.standard_normal((bh, t)) * 2.0).astype(np.float32)
+    labels = rng.integers(0, qn, (bh, t)).astype(np.int64)
+    dmap = rng.random((bh, qn + 1, kn + 1)) < 0.35
+    kc = (rng.standard_normal((bh, kn, d)) * 0.5).astype(np.float32)
+    vc = rng.standard_normal((bh, kn, d)).astype(np.float32)
+    counts = rng.integers(0, 40, (bh, kn)).astype(np.float32)
+    counts[:, ::9] = 0.0
+    # a row with LSE -inf whose first block adds nothing (skipped: its label row selects the
+    # whole block; n3_residual: the block's clusters of that head are empty): NaN in both
+    lse[1, 7] = -np.inf
+    if reformulation == "skipped":
+        dmap[1, labels[1, 7] + 1, 1:block_k + 1] = True
+    else:
+        counts[1, :block_k] = 0.0
+    out = svg_ear_compensation_triton(
+        q_flat=to_dev(q, dev, torch.bfloat16), sparse_flat=to_dev(sparse, dev, torch.bfloat16 if sparse_bf16 else None),
+        lse_flat=to_dev(lse, dev), qlabels_gen=to_dev(labels, dev), dynamic_map_query=to_dev(dmap, dev),
+        kcentroids=to_dev(kc, dev), kcluster_sizes=to_dev(counts.astype(np.int64), dev), vcentroids=to_dev(vc, dev),
+        reformulation=reformulation, block_k=block_k)
+    ref = oracle.svg_ear_compensation(q, sparse, lse, labels, dmap, kc, counts, vc, reformulation, block_k)
+    got = out.cpu().numpy()
+    assert (np.isnan(got) == np.isnan(ref)).all() and np.isnan(ref[1, 7]).all()
+    fin = ~np.isnan(ref)
+    assert np.abs(got[fin] - ref[fin]).max() <= 2e-3 * np.abs(ref[fin]).max()
+    with pytest.raises(RuntimeError, match="reformulation"):
+        svg_ear_compensation_triton(q_flat=out, sparse_flat=out, lse_flat=to_dev(lse, dev),
+                                    qlabels_gen=to_dev(labels, dev), dynamic_map_query=to_dev(dmap, dev),
+                                    kcentroids=to_dev(kc, dev), kcluster_sizes=to_dev(counts, dev),
+                                    vcentroids=to_dev(vc, dev), reformulation="bogus")

@@ -1200,6 +1200,52 @@ def test_warm_subspace_factor_householder_and_full_ritz(oracle):
     assert np.allclose(norms2, np.concatenate(([0.0], kept / (kept.sum() / r))), atol=1e-9)
 
 
+def test_svg_ear_compensation_closed_forms(oracle):
+    """svg_ear.py:289-369.  Every cluster selected: the sparse output comes back exactly, in
+    both reformulations.  No cluster selected and one valid cluster (count 4, tf32-exact
+    values): out = (s e^lse + 4 e^(q.kc / sqrt D) vc) / (e^lse + 4 e^(q.kc / sqrt D)), worked
+    by hand.  An empty cluster (count 0) adds nothing.  n3_residual equals skipped on random
+    masks (the same sum in exact arithmetic, up to the TF32 rounding of the weights).  A row with lse = -inf whose first block has no
+    cluster to add stays NaN, as the reference's exp(-inf - -inf) makes it."""
+    d = 4
+    q = np.array([[[2.0, 0.0, 0.0, 0.0]]], np.float32)
+    sparse = np.array([[[1.0, 2.0, 3.0, 4.0]]], np.float32)
+    lse = np.array([[0.5]], np.float32)
+    kc = np.array([[[1.0, 0.0, 0.0, 0.0], [3.0, 1.0, 0.0, 0.0]]], np.float32)
+    vc = np.array([[[8.0, 0.0, -8.0, 0.0], [5.0, 5.0, 5.0, 5.0]]], np.float32)
+    counts = np.array([[4.0, 0.0]], np.float32)
+    labels = np.zeros((1, 1), np.int64)
+    none = np.zeros((1, 2, 3), bool)
+    allsel = np.ones((1, 2, 3), bool)
+    for ref in ("skipped", "n3_residual"):
+        same = oracle.svg_ear_compensation(q, sparse, lse, labels, allsel, kc, counts, vc, ref)
+        assert np.array_equal(same, sparse)
+        got = oracle.svg_ear_compensation(q, sparse, lse, labels, none, kc, counts, vc, ref)
+        l0 = 2.0 / 2.0 + np.log(4.0)  # q.kc / sqrt(4) + log(count)
+        want = (sparse[0, 0] * np.exp(0.5) + np.exp(l0) * vc[0, 0]) / (np.exp(0.5) + np.exp(l0))
+        assert np.allclose(got[0, 0], want, rtol=1e-6)
+    rng = np.random.default_rng(57)
+    bh, t, kn, d = 2, 20, 70, 16
+    qr = rng.standard_normal((bh, t, d)).astype(np.float32)
+    sp = rng.standard_normal((bh, t, d)).astype(np.float32)
+    ls = rng.standard_normal((bh, t)).astype(np.float32)
+    lab = rng.integers(0, 5, (bh, t))
+    dm = rng.random((bh, 6, kn + 1)) < 0.4
+    kcr = rng.standard_normal((bh, kn, d)).astype(np.float32)
+    vcr = rng.standard_normal((bh, kn, d)).astype(np.float32)
+    cnt = rng.integers(0, 9, (bh, kn)).astype(np.float32)
+    a = oracle.svg_ear_compensation(qr, sp, ls, lab, dm, kcr, cnt, vcr, "skipped")
+    b = oracle.svg_ear_compensation(qr, sp, ls, lab, dm, kcr, cnt, vcr, "n3_residual")
+    # equal up to the TF32 rounding of the weights (their scale follows each mode's running max)
+    assert np.abs(a - b).max() <= 2e-3 * np.abs(a).max()
+    ls2 = ls.copy()
+    ls2[0, 0] = -np.inf
+    dm2 = dm.copy()
+    dm2[0, lab[0, 0] + 1, 1:33] = True  # nothing to add in the first block
+    nan = oracle.svg_ear_compensation(qr, sp, ls2, lab, dm2, kcr, cnt, vcr, "skipped")
+    assert np.isnan(nan[0, 0]).all() and np.isfinite(nan[0, 1:]).all()
+
+
 def test_project_rows_loop(oracle):
     rng = np.random.default_rng(54)
     x = rng.standard_normal((1, 5, 8)).astype(np.float32)
