@@ -72,15 +72,22 @@ __device__ __forceinline__ float load_f32<float>(const float* p) {
 // ---------------------------------------------------------------- covariance
 // grid (bh, tiles^2): tile (ti, tj) of the d x d output; rows used: rows[0 .. count) when
 // rows is given (the same positions for every head), else all n rows, each only when
-// sizes[h, r] > 0 (sizes nullable).
+// sizes[h, r] > 0 (sizes nullable).  Rows go in stages of RB: the stage's row indices and
+// validity are loaded once into LDS, then every thread loads its 2 x RB / 8 elements of
+// the two column blocks (independent loads), the next stage's while the current one is
+// summed.  The column means (center) take one such pass first: thread t sums column t % 32
+// over the stage rows r = t / 32 (mod 8), and the eight partial sums are added in order.
 template <typename T>
 __global__ __launch_bounds__(256) void role_metric_kernel(const T* __restrict__ x, int64_t n, int32_t d,
                                                           const int32_t* __restrict__ rows, int32_t count,
                                                           const int32_t* __restrict__ sizes, int32_t center,
                                                           float post_scale, float* __restrict__ out) {
-  constexpr int RB = 64;  // rows per LDS stage
+  constexpr int RB = 64;           // rows per stage
+  constexpr int PER = RB * 32 / 256;  // elements per thread and column block per stage (8)
   __shared__ float ta[RB][33];
   __shared__ float tb[RB][33];
+  __shared__ int64_t ridx[2][RB];  // row of each stage row (-1: not used)
+  __shared__ float part[8][64];
   __shared__ float mean_a[32], mean_b[32];
   __shared__ int32_t used_s;
   const int t = threadIdx.x;
@@ -90,53 +97,89 @@ __global__ __launch_bounds__(256) void role_metric_kernel(const T* __restrict__ 
   const T* xh = x + h * n * d;
   const int32_t* sz = sizes != nullptr ? sizes + h * n : nullptr;
   const int64_t total = rows != nullptr ? count : n;
-  auto row_of = [&](int64_t r) -> int64_t { return rows != nullptr ? rows[r] : r; };
-  auto valid = [&](int64_t r) -> bool { return sz == nullptr || sz[r] > 0; };
-
-  // column means over the used rows (sequential per column), and the used-row count
-  if (!center && sz == nullptr) {
+  const int64_t nstage = (total + RB - 1) / RB;
+  const int cc = t & 31, rg = t >> 5;  // column in the block, row group (rows rg + 8 i)
+  const int ca = 32 * ti + cc, cb = 32 * tj + cc;
+  // the row indices of stage s into ridx[s & 1] (threads 0 .. RB - 1)
+  auto stage_rows = [&](int64_t st) {
+    if (t < RB) {
+      const int64_t r = st * RB + t;
+      int64_t row = -1;
+      if (r < total) {
+        row = rows != nullptr ? rows[r] : r;
+        if (sz != nullptr && !(sz[row] > 0)) row = -1;
+      }
+      ridx[st & 1][t] = row;
+    }
+  };
+  auto load_vals = [&](int64_t st, float (&va)[PER], float (&vb)[PER]) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t row = ridx[st & 1][rg + 8 * i];
+      va[i] = (row >= 0 && ca < d) ? load_f32(xh + row * d + ca) : 0.0f;
+      vb[i] = (row >= 0 && cb < d) ? load_f32(xh + row * d + cb) : 0.0f;
+    }
+  };
+  // ---- column means and the used-row count
+  if (t == 0) used_s = 0;
+  float sa = 0.0f, sb = 0.0f;
+  int32_t used = 0;
+  const bool need_means = center || sz != nullptr;
+  if (need_means) {
+    for (int64_t st = 0; st < nstage; ++st) {
+      stage_rows(st);
+      __syncthreads();
+      float va[PER], vb[PER];
+      load_vals(st, va, vb);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        sa += va[i];
+        sb += vb[i];
+      }
+      if (t < RB) used += ridx[st & 1][t] >= 0 ? 1 : 0;
+      __syncthreads();  // ridx[st & 1] is rewritten two stages on
+    }
+    part[rg][cc] = sa;
+    part[rg][32 + cc] = sb;
+    if (t < RB) atomicAdd(&used_s, used);  // integer: order-independent
+    __syncthreads();
+    if (t < 64) {
+      float m = 0.0f;
+      for (int g = 0; g < 8; ++g) m += part[g][t];
+      const float cnt = static_cast<float>(used_s > 0 ? used_s : 1);
+      m = center ? m / cnt : 0.0f;
+      if (t < 32) mean_a[t] = m; else mean_b[t - 32] = m;
+    }
+  } else {
     if (t < 32) {
       mean_a[t] = 0.0f;
       mean_b[t] = 0.0f;
     }
     if (t == 0) used_s = static_cast<int32_t>(total);
-  } else if (t < 64) {
-    const int cc = t & 31;
-    const int col = (t < 32 ? 32 * ti : 32 * tj) + cc;
-    float s = 0.0f;
-    int32_t used = 0;
-    for (int64_t r = 0; r < total; ++r) {
-      const int64_t row = row_of(r);
-      if (!valid(row)) continue;
-      ++used;
-      if (center && col < d) s += load_f32(xh + row * d + col);
-    }
-    const float cnt = static_cast<float>(used > 0 ? used : 1);
-    const float m = center && col < d ? s / cnt : 0.0f;
-    if (t < 32) mean_a[cc] = m; else mean_b[cc] = m;
-    if (t == 0) used_s = used;
   }
   __syncthreads();
+  // ---- (x - mean_a)^T (x - mean_b) over the used rows
   const int a = t >> 4, b = t & 15;  // outputs (2a, 2a + 1) x (2b, 2b + 1) of the tile
   float s00 = 0.0f, s01 = 0.0f, s10 = 0.0f, s11 = 0.0f;
-  for (int64_t r0 = 0; r0 < total; r0 += RB) {
-    for (int e = t; e < RB * 32; e += 256) {
-      const int rr = e >> 5, cc = e & 31;
-      const int64_t r = r0 + rr;
-      float va = 0.0f, vb = 0.0f;
-      if (r < total) {
-        const int64_t row = row_of(r);
-        if (valid(row)) {
-          const int ca = 32 * ti + cc, cb = 32 * tj + cc;
-          if (ca < d) va = load_f32(xh + row * d + ca) - mean_a[cc];
-          if (cb < d) vb = load_f32(xh + row * d + cb) - mean_b[cc];
-        }
-      }
-      ta[rr][cc] = va;
-      tb[rr][cc] = vb;
-    }
+  float va[PER], vb[PER];
+  if (nstage > 0) {
+    stage_rows(0);
     __syncthreads();
-    const int rows_here = static_cast<int>(total - r0 < RB ? total - r0 : RB);
+    load_vals(0, va, vb);
+  }
+  for (int64_t st = 0; st < nstage; ++st) {
+    // stage st's values (in registers) into the tiles; stage st + 1's rows into the other
+    // ridx slot, then its values into registers while the tiles are summed
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int64_t row = ridx[st & 1][rg + 8 * i];
+      ta[rg + 8 * i][cc] = row >= 0 ? va[i] - mean_a[cc] : 0.0f;
+      tb[rg + 8 * i][cc] = row >= 0 ? vb[i] - mean_b[cc] : 0.0f;
+    }
+    if (st + 1 < nstage) stage_rows(st + 1);
+    __syncthreads();
+    if (st + 1 < nstage) load_vals(st + 1, va, vb);
+    const int rows_here = static_cast<int>(total - st * RB < RB ? total - st * RB : RB);
     for (int rr = 0; rr < rows_here; ++rr) {
       const float u0 = ta[rr][2 * a], u1 = ta[rr][2 * a + 1];
       const float v0 = tb[rr][2 * b], v1 = tb[rr][2 * b + 1];
