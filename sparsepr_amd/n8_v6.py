@@ -7,8 +7,9 @@ and Q, original-space centroids, the K/V permutation, SVG-EAR / attention-mass s
 scores, fixed-density or top-p key budgets and the exact budget selector.
 `N8V6Core.repair` runs the probe selection, dense probe attention, fit preparation, the
 reduced-rank fit, the apply and the exact scatter.  Every compute step is a HIP kernel of
-libsparsepr_hip.so.  Configurations whose kernels are not built (Householder-QR factor
-updates, output_role repair) raise NotImplementedError.
+libsparsepr_hip.so.  Configurations outside the kernels' sizes (head dims other than 64 and
+128, role ranks above 64, more than 128 K role features, output_role with a Q role rank that
+is not a multiple of 16) raise NotImplementedError.
 """
 
 from __future__ import annotations
@@ -237,9 +238,12 @@ class N8V6Core:
             raise RuntimeError(f"Unknown Rayleigh--Ritz mode {cfg.factor_ritz_mode!r}.")
         ranks = (cfg.role_q_rank, cfg.role_k_rank) + ((cfg.role_v_rank,) if cfg.role_v_weight > 0.0 else ())
         k_feature_dim = cfg.role_k_rank + (cfg.role_v_rank if cfg.role_v_weight > 0.0 else 0)
-        if max(ranks) > 64 or dim not in (64, 128) or k_feature_dim > 128:
-            raise NotImplementedError("N8 routing on the MI355X kernels needs head_dim 64 or 128, ranks <= 64 and "
-                                      "K role features (role_k_rank, + role_v_rank when role_v_weight > 0) <= 128.")
+        # the role-space k-means takes feature dims that are multiples of 16 up to 128
+        if (max(ranks) > 64 or dim not in (64, 128) or k_feature_dim > 128 or k_feature_dim % 16
+                or cfg.role_q_rank % 16):
+            raise NotImplementedError("N8 routing on the MI355X kernels needs head_dim 64 or 128, ranks <= 64, a "
+                                      "Q role rank that is a multiple of 16 and K role features (role_k_rank, "
+                                      "+ role_v_rank when role_v_weight > 0) a multiple of 16 up to 128.")
 
     def _kv_precision(self) -> str:
         """The fp32 matmul precision of the K (and V) role projections (n8_v6.py:658-704): the
