@@ -590,6 +590,322 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
   }
 }
 
+
+// The TF32 assignment with a batch's centroids resident in LDS: one workgroup per CU
+// (512 threads, two waves per SIMD) stages the scaled fp16 images of the centroids'
+// TF32 roundings once (padded rows; zeros and c_sq = +inf past k; the per-64-centroid
+// tile exponents of kmeans_assign_tf32_kernel, so both kernels form the same exact
+// products) and its waves walk 64-point blocks against them with no further barriers
+// (v_mfma_f32_32x32x16_f16 on the scaled images).
+//
+// Per 32-centroid step each lane scans its 16 candidates (index c0 + 4 half + 8i + j,
+// ascending in (i, j)) for the step's smallest unclamped distance
+// r = (x_sq + c_sq) - 2 cross (one rounding per step; 2 cross is exact), strict <, so
+// the lowest index wins among equal minima; the step's result then meets the running
+// best once.  The clamp max(r, 0) changes the answer only when some r <= 0: all such
+// candidates tie at 0 and the lowest index among them wins, which a (rare,
+// wave-uniform) rescan of the step restores.  The MFMAs of step s + 1 are issued in the
+// same instruction stream as the argmin of step s (interleaved by sched_group_barrier),
+// so the matrix pipe and the VALU work at the same time within a wave.
+//
+// A workgroup walks a contiguous range of the (batch, block) space; where the range
+// crosses into the next batch, the workgroup stages that batch's centroids in turn.
+constexpr int PIPE_THREADS = 512;
+constexpr int PIPE_WAVES = PIPE_THREADS / 64;
+constexpr size_t PIPE_LDS_LIMIT = 160 * 1024;
+
+template <int D>
+constexpr size_t pipe_lds_bytes(int64_t kpad) {
+  return static_cast<size_t>(kpad) * (D * 2 + 16) + static_cast<size_t>(kpad) * 4 +
+         static_cast<size_t>(kpad / CCHUNK) * 4;
+}
+
+template <int D>
+__global__ __launch_bounds__(PIPE_THREADS, 1) void kmeans_assign_tf32_resident_kernel(
+    const float* __restrict__ x, const float* __restrict__ c, const float* __restrict__ c_sq,
+    const float* __restrict__ x_sq_in, float* __restrict__ x_sq_out, int64_t batch, int64_t n, int32_t k,
+    int32_t* __restrict__ labels) {
+  static_assert(D % 16 == 0 && D <= 128, "D must be a multiple of 16, at most 128");
+  constexpr int KSTEPS = D / 16;
+  constexpr int ROW_BYTES = D * 2 + 16;  // padded LDS row: conflict-free 16-byte reads
+  extern __shared__ __attribute__((aligned(16))) uint8_t assign_smem[];
+  const int kpad = (k + CCHUNK - 1) / CCHUNK * CCHUNK;  // a multiple of 64: an even number of steps
+  uint8_t* cent = assign_smem;
+  float* csq_l = reinterpret_cast<float*>(assign_smem + static_cast<int64_t>(kpad) * ROW_BYTES);
+  int* cexp_l = reinterpret_cast<int*>(csq_l + kpad);  // scale exponent per 64-centroid tile
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+
+  const int64_t nblk = (n + ASSIGN_POINTS_PER_WAVE - 1) / ASSIGN_POINTS_PER_WAVE;  // 64-point blocks per batch
+  const int64_t total = batch * nblk;
+  const int64_t g_begin = total * blockIdx.x / gridDim.x;
+  const int64_t g_end = total * (blockIdx.x + 1) / gridDim.x;
+
+  for (int64_t g0 = g_begin; g0 < g_end;) {
+    const int64_t b = g0 / nblk;
+    const int64_t seg_end = std::min(g_end, (b + 1) * nblk);
+    const float* csqb = c_sq + b * k;
+
+    // ---- stage batch b's centroids (every wave is past the previous batch's blocks)
+    __syncthreads();
+    const float* cb = c + b * k * D;
+    for (int t = wave; t < kpad / CCHUNK; t += PIPE_WAVES) {
+      float m = 0.0f;
+      for (int i = lane; i < CCHUNK * D / 4; i += 64) {
+        const int row = t * CCHUNK + i / (D / 4);
+        const spr::f32x4 v = row < k ? *reinterpret_cast<const spr::f32x4*>(cb + static_cast<int64_t>(row) * D +
+                                                                          (i % (D / 4)) * 4)
+                                     : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) m = fmaxf(m, tf32_abs(v[u]));
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      const int et = tf32_scale_exp(m);
+      if (lane == 0) cexp_l[t] = et;
+      for (int i = lane; i < CCHUNK * D / 4; i += 64) {
+        const int row = t * CCHUNK + i / (D / 4);
+        const int vec = i % (D / 4);
+        const spr::f32x4 v = row < k ? *reinterpret_cast<const spr::f32x4*>(cb + static_cast<int64_t>(row) * D +
+                                                                          vec * 4)
+                                     : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        uint32_t h[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) h[u] = tf32_f16_bits(v[u], et);
+        *reinterpret_cast<uint2*>(cent + row * ROW_BYTES + vec * 8) = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      }
+    }
+
+    for (int r = tid; r < kpad; r += PIPE_THREADS) csq_l[r] = r < k ? csqb[r] : __builtin_huge_valf();
+    __syncthreads();
+
+    for (int64_t g = g0 + wave; g < seg_end; g += PIPE_WAVES) {
+      const int64_t p0 = (g - b * nblk) * ASSIGN_POINTS_PER_WAVE + col;
+      u32x4 xf[2][KSTEPS];
+      float xsq[2];
+      int xexp[2] = {0, 0};
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const int64_t p = p0 + 32 * f;
+        const bool live = p < n;
+        const float* xb = x + b * n * D;
+        float part = 0.0f, amax = 0.0f;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          const spr::f32x4* src = reinterpret_cast<const spr::f32x4*>(xb + p * D + s * 16 + half * 8);
+          const spr::f32x4 v0 = live ? src[0] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          const spr::f32x4 v1 = live ? src[1] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          const float e[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            part = __fadd_rn(part, __fmul_rn(e[u], e[u]));
+            amax = fmaxf(amax, tf32_abs(e[u]));
+          }
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        xexp[f] = tf32_scale_exp(amax);
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {  // the row again (cached), now as scaled fp16
+          const spr::f32x4* src = reinterpret_cast<const spr::f32x4*>(xb + p * D + s * 16 + half * 8);
+          const spr::f32x4 v0 = live ? src[0] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          const spr::f32x4 v1 = live ? src[1] : spr::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          const float e[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          uint32_t h[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) h[u] = tf32_f16_bits(e[u], xexp[f]);
+          xf[f][s] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+        }
+        const float other = __shfl_xor(part, 32, 64);
+        float tot = part + other;
+        if (x_sq_in != nullptr) {
+          tot = live ? x_sq_in[b * n + p] : 0.0f;
+        } else if (x_sq_out != nullptr && live && half == 0) {
+          x_sq_out[b * n + p] = tot;
+        }
+        xsq[f] = tot;
+      }
+
+      float best[2] = {3.4e38f, 3.4e38f};
+      int32_t best_idx[2] = {0, 0};
+
+      // MFMAs of the 32 centroids from c0 into acc (both point fragments)
+      auto mfma_step = [&](spr::f32x16 (&acc)[2], int c0) {
+        const uint8_t* arow = cent + (c0 + col) * ROW_BYTES + half * 16;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            acc[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                            __builtin_bit_cast(f16x8_t, xf[f][s]),
+                                                            s == 0 ? spr::f32x16{} : acc[f], 0, 0, 0);
+          }
+        }
+      };
+      // -2 x.c = acc * kf, kf = -2 2^-(point exponent + tile exponent) (exact)
+      auto factors = [&](int c0, float (&kf)[2]) {
+        const int et = cexp_l[c0 / CCHUNK];
+        kf[0] = __builtin_ldexpf(-2.0f, -(xexp[0] + et));
+        kf[1] = __builtin_ldexpf(-2.0f, -(xexp[1] + et));
+      };
+      // step-local (min, argmin) of the unclamped distances of acc (centroids c0 ..)
+      auto scan = [&](const spr::f32x16 (&acc)[2], int c0, const float (&kf)[2], float (&lb)[2],
+                      int32_t (&lo)[2]) {
+        const float* cs = csq_l + c0 + 4 * half;
+        spr::f32x4 c4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c4[i] = *reinterpret_cast<const spr::f32x4*>(cs + 8 * i);
+        // eight independent chains (fragment f, row group i: offsets 8i .. 8i + 3), then a
+        // merge in ascending offset order that takes a later chain only when strictly
+        // smaller, so the lowest offset still wins among equal minima
+        float cb[2][4];
+        int32_t co[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float r = __builtin_fmaf(kf[f], acc[f][4 * i + j], __fadd_rn(xsq[f], c4[i][j]));
+              if (j == 0) {
+                cb[f][i] = r;
+                co[f][i] = 8 * i;
+              } else {
+                const bool t = r < cb[f][i];
+                co[f][i] = t ? 8 * i + j : co[f][i];
+                cb[f][i] = fminf(r, cb[f][i]);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {  // (0, 1) and (2, 3)
+            const bool t = cb[f][2 * h + 1] < cb[f][2 * h];
+            co[f][2 * h] = t ? co[f][2 * h + 1] : co[f][2 * h];
+            cb[f][2 * h] = fminf(cb[f][2 * h + 1], cb[f][2 * h]);
+          }
+          const bool t = cb[f][2] < cb[f][0];
+          lo[f] = t ? co[f][2] : co[f][0];
+          lb[f] = fminf(cb[f][2], cb[f][0]);
+        }
+      };
+      // clamp rule and merge into the running best
+      auto finish = [&](const spr::f32x16 (&acc)[2], int c0, const float (&kf)[2], float (&lb)[2],
+                        int32_t (&lo)[2]) {
+        if (__ballot(lb[0] <= 0.0f || lb[1] <= 0.0f) != 0ull) {
+          // first candidate with r <= 0, in index order, at distance 0
+          const float* cs = csq_l + c0 + 4 * half;
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            bool found = false;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int off = 8 * i + j;
+                const float r = __builtin_fmaf(kf[f], acc[f][4 * i + j], __fadd_rn(xsq[f], cs[off]));
+                if (lb[f] <= 0.0f && !found && r <= 0.0f) {
+                  lo[f] = off;
+                  found = true;
+                }
+              }
+            }
+            lb[f] = fmaxf(lb[f], 0.0f);
+          }
+        }
+        const int32_t base = c0 + 4 * half;
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const bool t = lb[f] < best[f];
+          best[f] = t ? lb[f] : best[f];
+          best_idx[f] = t ? base + lo[f] : best_idx[f];
+        }
+      };
+      // the argmin of step cc (acc_c) with the MFMAs of step cn (acc_n) interleaved
+      auto fused = [&](spr::f32x16 (&acc_n)[2], int cn, const spr::f32x16 (&acc_c)[2], int cc) {
+        float kf[2], lb[2];
+        int32_t lo[2];
+        factors(cc, kf);
+        mfma_step(acc_n, cn);
+        scan(acc_c, cc, kf, lb, lo);
+        // KSTEPS fragment reads and 4 c_sq reads first, then one MFMA per VALU group
+        __builtin_amdgcn_sched_group_barrier(0x100, KSTEPS + 4, 0);
+#pragma unroll
+        for (int m = 0; m < 2 * KSTEPS; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 150 / (2 * KSTEPS), 0);
+        }
+        finish(acc_c, cc, kf, lb, lo);
+      };
+
+      spr::f32x16 acc_a[2], acc_b[2];
+      mfma_step(acc_a, 0);
+      int c0 = 0;
+      for (; c0 + 64 < kpad; c0 += 64) {
+        fused(acc_b, c0 + 32, acc_a, c0);
+        fused(acc_a, c0 + 64, acc_b, c0 + 32);
+      }
+      fused(acc_b, c0 + 32, acc_a, c0);
+      {
+        float kf[2], lb[2];
+        int32_t lo[2];
+        factors(c0 + 32, kf);
+        scan(acc_b, c0 + 32, kf, lb, lo);
+        finish(acc_b, c0 + 32, kf, lb, lo);
+      }
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const float od = __shfl_xor(best[f], 32, 64);
+        const int32_t oi = __shfl_xor(best_idx[f], 32, 64);
+        if (od < best[f] || (od == best[f] && oi < best_idx[f])) {
+          best[f] = od;
+          best_idx[f] = oi;
+        }
+        const int64_t p = p0 + 32 * f;
+        if (half == 0 && p < n) labels[b * n + p] = best_idx[f];
+      }
+    }
+    g0 = seg_end;
+  }
+}
+
+// Launches kmeans_assign_tf32_resident_kernel<D> when its LDS holds the padded
+// centroids (*used = true); otherwise launches nothing (*used = false) and the caller
+// takes the streamed kmeans_assign_tf32_kernel.  A grid of at most 256 workgroups (one
+// per CU) splits the (batch, 64-point block) space evenly.
+template <int D>
+int launch_tf32_resident(const float* x, const float* c, const float* c_sq, const float* x_sq, float* x_sq_out,
+                         int64_t batch, int64_t n, int32_t k, int32_t* labels, hipStream_t stream, bool* used) {
+  *used = false;
+  const int64_t kpad = spr::ceil_div(k, CCHUNK) * CCHUNK;
+  const size_t lds = pipe_lds_bytes<D>(kpad);
+  if (lds > PIPE_LDS_LIMIT) return SPR_OK;
+  static bool lds_raised = false;  // dynamic LDS beyond 64 KB must be allowed once per process
+  if (!lds_raised) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&kmeans_assign_tf32_resident_kernel<D>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(PIPE_LDS_LIMIT));
+    if (e != hipSuccess) {
+      spr_set_error("spr_kmeans_assign_tf32: hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+      return SPR_ELAUNCH;
+    }
+    lds_raised = true;
+  }
+  const int64_t blocks = batch * spr::ceil_div(n, ASSIGN_POINTS_PER_WAVE);
+  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(256, spr::ceil_div(blocks, PIPE_WAVES)));
+  kmeans_assign_tf32_resident_kernel<D><<<static_cast<uint32_t>(grid), PIPE_THREADS, lds, stream>>>(
+      x, c, c_sq, x_sq, x_sq_out, batch, n, k, labels);
+  SPR_LAUNCHED("kmeans_assign_tf32_resident_kernel");
+  *used = true;
+  return SPR_OK;
+}
+
 // ---------------------------------------------------------------- segmented mean
 // Mean of one cluster from its fp64 sum: mean32 = float(sum / count) (empty ->
 // previous centroid), out = mean32 in the centroid dtype, optional running
@@ -1047,9 +1363,15 @@ extern "C" int spr_kmeans_assign_tf32(const float* x, const float* centroids, co
   SPR_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(centroids) % 16 == 0,
               "spr_kmeans_assign_tf32: x and centroids must be 16-byte aligned");
   dim3 grid(static_cast<uint32_t>(spr::ceil_div(n, ASSIGN_POINTS)), static_cast<uint32_t>(batch));
-#define SPR_TF32_ASSIGN(DD)                                                                                    \
-  kmeans_assign_tf32_kernel<DD><<<grid, ASSIGN_THREADS, 0, stream>>>(x, centroids, c_sq, x_sq, x_sq_out, n, k, \
-                                                                     labels)
+#define SPR_TF32_ASSIGN(DD)                                                                                      \
+  do {                                                                                                           \
+    bool used = false;                                                                                           \
+    const int st = launch_tf32_resident<DD>(x, centroids, c_sq, x_sq, x_sq_out, batch, n, k, labels, stream,    \
+                                            &used);                                                             \
+    if (st != SPR_OK || used) return st;                                                                         \
+    kmeans_assign_tf32_kernel<DD><<<grid, ASSIGN_THREADS, 0, stream>>>(x, centroids, c_sq, x_sq, x_sq_out, n, k, \
+                                                                       labels);                                  \
+  } while (0)
   switch (d) {
     case 16: SPR_TF32_ASSIGN(16); break;
     case 32: SPR_TF32_ASSIGN(32); break;
