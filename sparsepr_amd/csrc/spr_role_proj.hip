@@ -24,6 +24,8 @@
 // from LDS, B = X^T fragments straight from HBM (lane = token, 16 contiguous bytes per
 // 16-dim step, the next block's prefetched), so each lane ends up with R / 2 values of
 // one token and the row's sum of squares needs one exchange between the two half-waves.
+#include <algorithm>
+
 #include "spr_common.h"
 
 namespace {
@@ -33,7 +35,7 @@ using spr::u32x4;
 
 constexpr int RP_THREADS = 256;
 constexpr int RP_WAVES = RP_THREADS / 64;
-constexpr int RP_TOKENS = 2048;  // tokens per workgroup
+constexpr int RP_TOKENS = 512;  // tokens per block (a workgroup takes several blocks of its head)
 constexpr int RP_MAX_R = 128;
 
 __device__ __forceinline__ float tf32_rna(float x) {
@@ -100,16 +102,18 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
   if (MODE == 2) {
     // the head's scale: fp64 sum of the partials in block order, then as the reference
     // rounds it: fp32 mean, sqrt, clamp at 1e-8
+    const int64_t nparts = (n + RP_TOKENS - 1) / RP_TOKENS;
     double tot = 0.0;
-    for (uint32_t i = 0; i < gridDim.x; ++i) tot += partial[b * gridDim.x + i];
+    for (int64_t i = 0; i < nparts; ++i) tot += partial[b * nparts + i];
     div = fmaxf(sqrtf(static_cast<float>(tot / (static_cast<double>(n) * rank))), 1.0e-8f);
     if (blockIdx.x == 0 && tid == 0) head_scale[b] = div;
   }
-  double wsum = 0.0;  // MODE 1: this lane's sum of p^2
-  const int64_t t_begin = static_cast<int64_t>(blockIdx.x) * RP_TOKENS;
-  const int64_t t_end = min(t_begin + RP_TOKENS, n);
+  // Token blocks of RP_TOKENS: this workgroup takes blocks blockIdx.x, + gridDim.x, ... of its
+  // head (the grid holds as many workgroups per head as stay resident at once, so no second
+  // round of workgroups trails the first).  MODE 1 writes one partial per block.
+  const int64_t nvb = (n + RP_TOKENS - 1) / RP_TOKENS;
   // X^T fragments of a 32-token block: lane = token, 16 bytes per 16-dim step (zero past the end)
-  auto load_x = [&](u32x4 (&xf)[KSTEPS], int64_t t0) {
+  auto load_x = [&](u32x4 (&xf)[KSTEPS], int64_t t0, int64_t t_end) {
     const int64_t t = t0 + col;
     const bool live = t < t_end;
     const uint16_t* xr = xb + (live ? t : t0) * D + 8 * half;
@@ -119,89 +123,151 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
       if (!live) xf[s] = u32x4{0, 0, 0, 0};
     }
   };
+  // this wave's next 32-token block after (vb, t0): the next one of the block, else the
+  // first of the workgroup's next block; vb = nvb when there is none
+  auto skip_empty = [&](int64_t& vb, int64_t& t0) {  // a short last block may hold none of this wave's rows
+    while (vb < nvb && t0 >= min((vb + 1) * RP_TOKENS, n)) {
+      vb += gridDim.x;
+      t0 = vb * RP_TOKENS + 32 * wave;
+    }
+  };
+  auto advance = [&](int64_t& vb, int64_t& t0) {
+    t0 += 32 * RP_WAVES;
+    skip_empty(vb, t0);
+  };
+  int64_t vb = blockIdx.x, t0 = vb * RP_TOKENS + 32 * wave;
+  skip_empty(vb, t0);
   u32x4 xn[KSTEPS];
-  if (t_begin + 32 * wave < t_end) load_x(xn, t_begin + 32 * wave);
-  for (int64_t t0 = t_begin + 32 * wave; t0 < t_end; t0 += 32 * RP_WAVES) {
-    const int64_t t = t0 + col;
-    const bool live = t < t_end;
-    u32x4 xf[KSTEPS];
+  if (vb < nvb) load_x(xn, t0, min((vb + 1) * RP_TOKENS, n));
+  double wsum = 0.0;  // MODE 1: this lane's sum of p^2 over the current block
+  for (int64_t cur = blockIdx.x; cur < nvb; cur += gridDim.x) {
+    const int64_t t_end = min((cur + 1) * RP_TOKENS, n);
+    while (vb == cur) {
+      const int64_t t = t0 + col;
+      const bool live = t < t_end;
+      u32x4 xf[KSTEPS];
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) xf[s] = xn[s];
-    // the next block's loads are in flight during this block's MFMAs and stores
-    if (t0 + 32 * RP_WAVES < t_end) load_x(xn, t0 + 32 * RP_WAVES);
-    f32x16 acc[RB];
+      for (int s = 0; s < KSTEPS; ++s) xf[s] = xn[s];
+      const int64_t t_row = t0;
+      // the next block's loads are in flight during this block's MFMAs and stores
+      advance(vb, t0);
+      if (vb < nvb) load_x(xn, t0, min((vb + 1) * RP_TOKENS, n));
+      f32x16 acc[RB];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      acc[rb] = f32x16{};
-      const int r = 32 * rb + col;
+      for (int rb = 0; rb < RB; ++rb) {
+        acc[rb] = f32x16{};
+        const int r = 32 * rb + col;
 #pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
-        const int off = r * ROWB + (((2 * s + half) ^ (r % (D / 8))) << 4);
+        for (int s = 0; s < KSTEPS; ++s) {
+          const int off = r * ROWB + (((2 * s + half) ^ (r % (D / 8))) << 4);
 #pragma unroll
-        for (int pc = 0; pc < NP; ++pc) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(fpc[pc] + off);
-          acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[s]), acc[rb], 0, 0, 0);
+          for (int pc = 0; pc < NP; ++pc) {
+            const u32x4 a = *reinterpret_cast<const u32x4*>(fpc[pc] + off);
+            acc[rb] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[s]), acc[rb], 0, 0, 0);
+          }
         }
       }
-    }
-    // lane (token col, half) holds p_r for r = 32 rb + 8 (e / 4) + 4 half + e % 4 (zero past rank)
-    float ss = 0.0f;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) ss = __builtin_fmaf(acc[rb][e], acc[rb][e], ss);
-    }
-    if (MODE == 1) {
-      wsum += live ? static_cast<double>(ss) : 0.0;
-      continue;
-    }
-    ss = sum_xor32(ss);
-    const float inv = 1.0f / sqrtf(fmaxf(ss / static_cast<float>(rank), 1.0e-12f));
-    auto nrm = [&](float v) { return MODE == 0 ? v * inv : (weight * v) / div; };
-    if (live) {
-      float* orow = MODE == 2 ? ob + t * out_ld + out_col : ob + t * rank;
+      // lane (token col, half) holds p_r for r = 32 rb + 8 (e / 4) + 4 half + e % 4 (zero past rank)
+      float ss = 0.0f;
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int r0 = 32 * rb + 8 * g + 4 * half;
-          if (r0 + 3 < rank && (rank & 3) == 0 && (MODE != 2 || ((out_ld | out_col) & 3) == 0)) {
-            *reinterpret_cast<float4*>(orow + r0) = make_float4(nrm(acc[rb][4 * g]), nrm(acc[rb][4 * g + 1]),
-                                                                nrm(acc[rb][4 * g + 2]), nrm(acc[rb][4 * g + 3]));
-          } else {
+        for (int e = 0; e < 16; ++e) ss = __builtin_fmaf(acc[rb][e], acc[rb][e], ss);
+      }
+      if (MODE == 1) {
+        wsum += live ? static_cast<double>(ss) : 0.0;
+        continue;
+      }
+      ss = sum_xor32(ss);
+      const float inv = 1.0f / sqrtf(fmaxf(ss / static_cast<float>(rank), 1.0e-12f));
+      auto nrm = [&](float v) { return MODE == 0 ? v * inv : (weight * v) / div; };
+      if (live) {
+        const int64_t tt = t_row + col;
+        float* orow = MODE == 2 ? ob + tt * out_ld + out_col : ob + tt * rank;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              if (r0 + i < rank) orow[r0 + i] = nrm(acc[rb][4 * g + i]);
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int r0 = 32 * rb + 8 * g + 4 * half;
+            if (r0 + 3 < rank && (rank & 3) == 0 && (MODE != 2 || ((out_ld | out_col) & 3) == 0)) {
+              *reinterpret_cast<float4*>(orow + r0) = make_float4(nrm(acc[rb][4 * g]), nrm(acc[rb][4 * g + 1]),
+                                                                  nrm(acc[rb][4 * g + 2]), nrm(acc[rb][4 * g + 3]));
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                if (r0 + i < rank) orow[r0 + i] = nrm(acc[rb][4 * g + i]);
+              }
             }
           }
         }
       }
     }
-  }
-  if (MODE == 1) {
-    // lanes in order, then waves in order: the same fp64 sum on every run
-    for (int o = 1; o < 64; o <<= 1) wsum += __shfl_xor(wsum, o, 64);
-    if (lane == 0) red_l[wave] = wsum;
-    __syncthreads();
-    if (tid == 0) {
-      double t = 0.0;
-      for (int w = 0; w < RP_WAVES; ++w) t += red_l[w];
-      partial[b * gridDim.x + blockIdx.x] = t;
+    if (MODE == 1) {
+      // lanes in order, then waves in order: the same fp64 sum on every run
+      for (int o = 1; o < 64; o <<= 1) wsum += __shfl_xor(wsum, o, 64);
+      if (lane == 0) red_l[wave] = wsum;
+      __syncthreads();
+      if (tid == 0) {
+        double tsum = 0.0;
+        for (int w = 0; w < RP_WAVES; ++w) tsum += red_l[w];
+        partial[b * nvb + cur] = tsum;
+      }
+      __syncthreads();
+      wsum = 0.0;
     }
   }
 }
 
 }  // namespace
 
+// Compute units of the calling thread's current device (queried once per device).
+static int rp_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Workgroups per head: as many as stay resident together (per_cu per CU, from the
+// occupancy calculator), shared evenly by the heads, at most one per token block.
+static uint32_t rp_groups_per_head(int64_t bh, int64_t n, int per_cu) {
+  const int64_t resident = static_cast<int64_t>(std::max(per_cu, 1)) * rp_cu_count();
+  const int64_t nvb = (n + RP_TOKENS - 1) / RP_TOKENS;
+  return static_cast<uint32_t>(std::max<int64_t>(1, std::min<int64_t>(nvb, resident / std::max<int64_t>(bh, 1))));
+}
+
+// Resident workgroups per CU of role_projection_kernel<D, RB, MODE, PREC> (queried once per
+// instantiation; 1 if the query fails).
+template <int D, int RB, int MODE, int PREC>
+static int rp_occupancy() {
+  static int cached = 0;
+  if (cached == 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, role_projection_kernel<D, RB, MODE, PREC>, RP_THREADS, 0) !=
+            hipSuccess ||
+        nb <= 0)
+      nb = 1;
+    cached = nb;
+  }
+  return cached;
+}
+
 template <int MODE, int PREC>
-static void launch_role_projection(dim3 grid, hipStream_t stream, const uint16_t* xp, const float* factor, int64_t n,
-                                   int32_t d, int32_t rank, float* out, int32_t out_ld, int32_t out_col, float weight,
-                                   double* partial, float* head_scale) {
+static void launch_role_projection(int64_t bh, hipStream_t stream, const uint16_t* xp, const float* factor,
+                                   int64_t n, int32_t d, int32_t rank, float* out, int32_t out_ld, int32_t out_col,
+                                   float weight, double* partial, float* head_scale) {
   const int rb = (rank + 31) / 32;
-#define SPR_RP(DD, RBB)                                                                                     \
-  role_projection_kernel<DD, RBB, MODE, PREC><<<grid, RP_THREADS, 0, stream>>>(xp, factor, n, rank, out,  \
-                                                                              out_ld, out_col, weight,    \
-                                                                              partial, head_scale)
+#define SPR_RP(DD, RBB)                                                                                      \
+  role_projection_kernel<DD, RBB, MODE, PREC>                                                                \
+      <<<dim3(rp_groups_per_head(bh, n, (rp_occupancy<DD, RBB, MODE, PREC>())),          \
+              static_cast<uint32_t>(bh)),                                                                    \
+         RP_THREADS, 0, stream>>>(xp, factor, n, rank, out, out_ld, out_col, weight, partial, head_scale)
   if (d == 128) {
     if (rb == 1) SPR_RP(128, 1); else if (rb == 2) SPR_RP(128, 2); else if (rb == 3) SPR_RP(128, 3); else SPR_RP(128, 4);
   } else {
@@ -219,8 +285,7 @@ extern "C" int spr_role_projection_rms(const void* x, const float* factor, int64
   if (bh == 0 || n == 0) return SPR_OK;
   SPR_REQUIRE(x && factor && out, "spr_role_projection_rms: null pointer");
   SPR_REQUIRE(bh <= 65535, "spr_role_projection_rms: too many heads");
-  const dim3 grid(static_cast<uint32_t>((n + RP_TOKENS - 1) / RP_TOKENS), static_cast<uint32_t>(bh));
-  launch_role_projection<0, 0>(grid, stream, static_cast<const uint16_t*>(x), factor, n, d, rank, out, rank, 0, 1.0f,
+  launch_role_projection<0, 0>(bh, stream, static_cast<const uint16_t*>(x), factor, n, d, rank, out, rank, 0, 1.0f,
                                nullptr, nullptr);
   SPR_LAUNCHED("role_projection_kernel");
   return SPR_OK;
@@ -250,14 +315,13 @@ extern "C" int spr_role_k_projection_ex(const void* x, const float* factor, int6
     spr_set_error("spr_role_k_projection: workspace of %zu bytes needed", spr_role_k_projection_workspace(bh, n));
     return SPR_EWORKSPACE;
   }
-  const dim3 grid(static_cast<uint32_t>((n + RP_TOKENS - 1) / RP_TOKENS), static_cast<uint32_t>(bh));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   double* part = static_cast<double*>(workspace);
 #define SPR_KP(PP)                                                                                             \
   do {                                                                                                         \
-    launch_role_projection<1, PP>(grid, stream, xp, factor, n, d, rank, nullptr, 0, 0, 1.0f, part, nullptr);   \
+    launch_role_projection<1, PP>(bh, stream, xp, factor, n, d, rank, nullptr, 0, 0, 1.0f, part, nullptr);   \
     SPR_LAUNCHED("role_projection_kernel<sum of squares>");                                                    \
-    launch_role_projection<2, PP>(grid, stream, xp, factor, n, d, rank, out, out_ld, out_col, weight, part,     \
+    launch_role_projection<2, PP>(bh, stream, xp, factor, n, d, rank, out, out_ld, out_col, weight, part,     \
                                   key_scale);                                                                  \
     SPR_LAUNCHED("role_projection_kernel<head scale>");                                                        \
   } while (0)

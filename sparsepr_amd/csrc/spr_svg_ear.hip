@@ -102,61 +102,65 @@ __device__ __forceinline__ float sum_xor32(float x) {
 
 constexpr int SE_ROW = SE_D * 2;  // bytes per bf16 token row
 constexpr int SE_CPW = 8;         // key clusters per workgroup
-constexpr int CL_CLUSTERS = 64;   // clusters per centroid-logit workgroup
+constexpr int CL_CLUSTERS = 32;   // clusters per centroid-logit workgroup
+constexpr int CL_ROWS = SE_THREADS / 4;  // query rows per centroid-logit workgroup
 
-// l_c = (q . kc) / sqrt(D) (+ 0.5 min(sum_d q_d^2 var_d / D, cap)) for 128 query rows x
-// 64 clusters per workgroup: thread -> query row tid / 2, clusters 32 (tid % 2) .. + 31;
-// fp32 fma chains over d in order.  Written to out [qh, qn, kn].
+// l_c = (q . kc) / sqrt(D) (+ 0.5 min(sum_d q_d^2 var_d / D, cap)) for CL_ROWS query rows x
+// CL_CLUSTERS clusters per workgroup: thread -> query row tid / 4, clusters
+// 8 (tid % 4) .. + 7; fp32 fma chains over d in order.  Written to out [qh, qn, kn].
 __global__ __launch_bounds__(SE_THREADS) void svg_ear_centroid_logit_kernel(
     const float* __restrict__ qc, const float* __restrict__ kcent, const float* __restrict__ var_k, float cap,
     int32_t qn, int32_t kn, int32_t group, float* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) float kc_l[CL_CLUSTERS][SE_D];
   __shared__ __attribute__((aligned(16))) float var_l[CL_CLUSTERS][SE_D];
-  const int64_t qh = blockIdx.y;
+  const int64_t qh = blockIdx.z;
   const int64_t kh = qh / group;
   const int cb = blockIdx.x * CL_CLUSTERS;
   const int ncl = min(CL_CLUSTERS, kn - cb);
   const int tid = threadIdx.x;
   const float scale = 1.0f / 11.313708498984761f;
-  for (int i = tid; i < CL_CLUSTERS * SE_D; i += SE_THREADS) {
-    const int c = i / SE_D, d = i % SE_D;
+  for (int i = tid; i < CL_CLUSTERS * SE_D / 4; i += SE_THREADS) {
+    const int c = i / (SE_D / 4), d = 4 * (i % (SE_D / 4));
     const bool live = c < ncl;
-    kc_l[c][d] = live ? kcent[(kh * kn + cb + c) * SE_D + d] : 0.0f;
-    var_l[c][d] = (live && var_k != nullptr) ? var_k[(kh * kn + cb + c) * SE_D + d] : 0.0f;
+    const int64_t o = (kh * kn + cb + c) * SE_D + d;
+    *reinterpret_cast<float4*>(&kc_l[c][d]) =
+        live ? *reinterpret_cast<const float4*>(kcent + o) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    *reinterpret_cast<float4*>(&var_l[c][d]) =
+        (live && var_k != nullptr) ? *reinterpret_cast<const float4*>(var_k + o) : float4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   __syncthreads();
-  const int h = tid & 1;
-  for (int r = tid >> 1; r < qn; r += SE_THREADS / 2) {
-    const float* qrow = qc + (qh * qn + r) * SE_D;
-    float dot[32], s2[32];
+  const int r = blockIdx.y * CL_ROWS + tid / 4;
+  const int c0 = 8 * (tid % 4);
+  if (r >= qn) return;
+  const float* qrow = qc + (qh * qn + r) * SE_D;
+  float dot[8], s2[8];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) dot[j] = s2[j] = 0.0f;
-    for (int d0 = 0; d0 < SE_D; d0 += 4) {
-      const float4 qv = *reinterpret_cast<const float4*>(qrow + d0);
+  for (int j = 0; j < 8; ++j) dot[j] = s2[j] = 0.0f;
+  for (int d0 = 0; d0 < SE_D; d0 += 4) {
+    const float4 qv = *reinterpret_cast<const float4*>(qrow + d0);
 #pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        const float4 kv = *reinterpret_cast<const float4*>(&kc_l[32 * h + j][d0]);
-        dot[j] = __builtin_fmaf(qv.x, kv.x, dot[j]);
-        dot[j] = __builtin_fmaf(qv.y, kv.y, dot[j]);
-        dot[j] = __builtin_fmaf(qv.z, kv.z, dot[j]);
-        dot[j] = __builtin_fmaf(qv.w, kv.w, dot[j]);
-        if (var_k != nullptr) {
-          const float4 vv = *reinterpret_cast<const float4*>(&var_l[32 * h + j][d0]);
-          s2[j] = __builtin_fmaf(qv.x * qv.x, vv.x, s2[j]);
-          s2[j] = __builtin_fmaf(qv.y * qv.y, vv.y, s2[j]);
-          s2[j] = __builtin_fmaf(qv.z * qv.z, vv.z, s2[j]);
-          s2[j] = __builtin_fmaf(qv.w * qv.w, vv.w, s2[j]);
-        }
+    for (int j = 0; j < 8; ++j) {
+      const float4 kv = *reinterpret_cast<const float4*>(&kc_l[c0 + j][d0]);
+      dot[j] = __builtin_fmaf(qv.x, kv.x, dot[j]);
+      dot[j] = __builtin_fmaf(qv.y, kv.y, dot[j]);
+      dot[j] = __builtin_fmaf(qv.z, kv.z, dot[j]);
+      dot[j] = __builtin_fmaf(qv.w, kv.w, dot[j]);
+      if (var_k != nullptr) {
+        const float4 vv = *reinterpret_cast<const float4*>(&var_l[c0 + j][d0]);
+        s2[j] = __builtin_fmaf(qv.x * qv.x, vv.x, s2[j]);
+        s2[j] = __builtin_fmaf(qv.y * qv.y, vv.y, s2[j]);
+        s2[j] = __builtin_fmaf(qv.z * qv.z, vv.z, s2[j]);
+        s2[j] = __builtin_fmaf(qv.w * qv.w, vv.w, s2[j]);
       }
     }
-    float* orow = out + (qh * qn + r) * kn + cb + 32 * h;
+  }
+  float* orow = out + (qh * qn + r) * kn + cb + c0;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) {
-      if (32 * h + j < ncl) {
-        float l = dot[j] * scale;
-        if (var_k != nullptr) l += 0.5f * fminf(s2[j] / static_cast<float>(SE_D), cap);
-        orow[j] = l;
-      }
+  for (int j = 0; j < 8; ++j) {
+    if (c0 + j < ncl) {
+      float l = dot[j] * scale;
+      if (var_k != nullptr) l += 0.5f * fminf(s2[j] / static_cast<float>(SE_D), cap);
+      orow[j] = l;
     }
   }
 }
@@ -700,7 +704,7 @@ extern "C" int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_so
               "spr_svg_ear_scores: bad size");
   SPR_REQUIRE(q_heads == kv_heads * group, "spr_svg_ear_scores: q_heads %lld != kv_heads %lld * group %d",
               static_cast<long long>(q_heads), static_cast<long long>(kv_heads), group);
-  SPR_REQUIRE(q_heads <= 65535 && kn <= (1 << 30), "spr_svg_ear_scores: grid too large");
+  SPR_REQUIRE(q_heads <= 65535 && kn <= (1 << 30) && qn <= (1 << 22), "spr_svg_ear_scores: grid too large");
   SPR_REQUIRE(t_stored < (int64_t(1) << 31) / (2 * SE_D) - SE_CHUNK,
               "spr_svg_ear_scores: at most %lld stored tokens per head",
               static_cast<long long>((int64_t(1) << 31) / (2 * SE_D) - SE_CHUNK - 1));
@@ -714,6 +718,7 @@ extern "C" int spr_svg_ear_scores(const float* q_centroids, const uint16_t* k_so
   if (mode == 0) {
     const bool jensen = jensen_var_cap > 0.0f;
     svg_ear_centroid_logit_kernel<<<dim3(static_cast<uint32_t>((kn + CL_CLUSTERS - 1) / CL_CLUSTERS),
+                                         static_cast<uint32_t>((qn + CL_ROWS - 1) / CL_ROWS),
                                          static_cast<uint32_t>(q_heads)),
                                     SE_THREADS, 0, stream>>>(q_centroids, k_centroids, jensen ? var_k_diag : nullptr,
                                                              jensen ? jensen_var_cap : 0.0f, qn, kn, group, scores);
