@@ -340,19 +340,20 @@ __device__ __forceinline__ void wf_gram(WarmSmem& s, const float* a, const float
 // its LDS pointers carry their address space, so the accesses stay LDS instructions.
 typedef __attribute__((address_space(3))) float lds_f32;
 typedef __attribute__((address_space(3))) int32_t lds_i32;
+template <int RMAX>
 __device__ __noinline__ void wf_cholesky_wave(const lds_f32* src, lds_f32* g, lds_f32* lcol, lds_i32* fail, int r,
                                               float shift) {
   const int lane = threadIdx.x & 63;
-  float row[MET_MAX_R];
+  float row[RMAX];
 #pragma unroll
-  for (int j = 0; j < MET_MAX_R; ++j) {
+  for (int j = 0; j < RMAX; ++j) {
     row[j] = (lane < r && j <= lane && j < r) ? src[lane * LDB + j] + (j == lane ? shift : 0.0f) : 0.0f;
   }
   bool ok = true;
 #pragma unroll
-  for (int k = 0; k < MET_MAX_R; ++k) {
+  for (int k = 0; k < RMAX; ++k) {
     if (k < r) {
-      const float piv = __shfl(row[k], k, 64);
+      const float piv = lane_read(row[k], k);
       ok = ok && (piv > 0.0f) && (piv < __builtin_huge_valf());
       const float lkk = sqrtf(fmaxf(piv, 1e-30f));
       const float lik = lane > k ? row[k] / lkk : 0.0f;
@@ -360,20 +361,33 @@ __device__ __noinline__ void wf_cholesky_wave(const lds_f32* src, lds_f32* g, ld
       lcol[lane] = lik;
       wave_sync();
 #pragma unroll
-      for (int j = k + 1; j < MET_MAX_R; ++j) row[j] -= lik * lcol[j];  // entries past the lane are unused
+      for (int j = k + 1; j < RMAX; ++j) row[j] -= lik * lcol[j];  // entries past the lane are unused
       wave_sync();
     }
   }
 #pragma unroll
-  for (int j = 0; j < MET_MAX_R; ++j) {
+  for (int j = 0; j < RMAX; ++j) {
     if (lane < r && j <= lane) g[lane * LDB + j] = row[j];
   }
   if (lane == 0) *fail = ok ? 0 : 1;
 }
 __device__ __forceinline__ bool wf_cholesky(WarmSmem& s, const float* src, int r, float shift) {
   if (threadIdx.x < 64) {
-    // generic to LDS address space (the pointers point into the workgroup's LDS)
-    wf_cholesky_wave((const lds_f32*)src, (lds_f32*)s.g, (lds_f32*)s.lcol, (lds_i32*)&s.fail, r, shift);
+    // generic to LDS address space (the pointers point into the workgroup's LDS); the
+    // unrolled loops stop at r rounded up to 16
+    const lds_f32* a = (const lds_f32*)src;
+    lds_f32* g = (lds_f32*)s.g;
+    lds_f32* lc = (lds_f32*)s.lcol;
+    lds_i32* f = (lds_i32*)&s.fail;
+    if (r <= 16) {
+      wf_cholesky_wave<16>(a, g, lc, f, r, shift);
+    } else if (r <= 32) {
+      wf_cholesky_wave<32>(a, g, lc, f, r, shift);
+    } else if (r <= 48) {
+      wf_cholesky_wave<48>(a, g, lc, f, r, shift);
+    } else {
+      wf_cholesky_wave<MET_MAX_R>(a, g, lc, f, r, shift);
+    }
   }
   __syncthreads();
   return s.fail == 0;
@@ -383,17 +397,18 @@ __device__ __forceinline__ bool wf_cholesky(WarmSmem& s, const float* src, int r
 // Threads 8 i .. 8 i + 7 share the row; thread 8 i + u keeps y[c] for c = u mod 8 in
 // registers, and each step sums the eight partial dot products (DPP) before the division.
 // Out of line for the same reason as the Cholesky.
+template <int RMAX>
 __device__ __noinline__ void wf_solve_rows(const lds_f32* g, const lds_f32* w, lds_f32* b, int n, int r, bool ok) {
   const int t = threadIdx.x, i = t >> 3, u = t & 7;
-  float y[MET_MAX_R / 8];
+  float y[RMAX / 8];
 #pragma unroll
-  for (int q = 0; q < MET_MAX_R / 8; ++q) y[q] = 0.0f;
+  for (int q = 0; q < RMAX / 8; ++q) y[q] = 0.0f;
 #pragma unroll
-  for (int c = 0; c < MET_MAX_R; ++c) {
+  for (int c = 0; c < RMAX; ++c) {
     if (c < r) {
       float part = 0.0f;
 #pragma unroll
-      for (int q = 0; q < MET_MAX_R / 8; ++q) {
+      for (int q = 0; q < RMAX / 8; ++q) {
         if (8 * q < c) {
           const int k = 8 * q + u;
           part = k < c ? __builtin_fmaf(g[c * LDB + k], y[q], part) : part;
@@ -407,7 +422,7 @@ __device__ __noinline__ void wf_solve_rows(const lds_f32* g, const lds_f32* w, l
   }
   if (i < n) {
 #pragma unroll
-    for (int q = 0; q < MET_MAX_R / 8; ++q) {
+    for (int q = 0; q < RMAX / 8; ++q) {
       if (8 * q + u < r) b[i * LDB + 8 * q + u] = y[q];
     }
   }
@@ -424,7 +439,9 @@ __device__ __forceinline__ bool wf_cholesky_qr(WarmSmem& s, const float* src, in
     s.w[i * LDB + c] = src[i * LDB + c] / s.colv[c];
   }
   __syncthreads();
-  wf_gram(s, s.w, s.w, n, r, true);
+  // w^T w is symmetric as computed (each tile pair sums the same products in the same
+  // order), so symmetrising would return it unchanged
+  wf_gram(s, s.w, s.w, n, r, false);
   if (threadIdx.x == 0) {
     float tr = 0.0f;
     for (int c = 0; c < r; ++c) tr += s.g[c * LDB + c];
@@ -432,7 +449,18 @@ __device__ __forceinline__ bool wf_cholesky_qr(WarmSmem& s, const float* src, in
   }
   __syncthreads();
   const bool ok = wf_cholesky(s, s.g, r, s.scal[0]);  // in place
-  wf_solve_rows((const lds_f32*)s.g, (const lds_f32*)s.w, (lds_f32*)s.b, n, r, ok);
+  const lds_f32* gl = (const lds_f32*)s.g;
+  const lds_f32* wl = (const lds_f32*)s.w;
+  lds_f32* bl = (lds_f32*)s.b;
+  if (r <= 16) {
+    wf_solve_rows<16>(gl, wl, bl, n, r, ok);
+  } else if (r <= 32) {
+    wf_solve_rows<32>(gl, wl, bl, n, r, ok);
+  } else if (r <= 48) {
+    wf_solve_rows<48>(gl, wl, bl, n, r, ok);
+  } else {
+    wf_solve_rows<MET_MAX_R>(gl, wl, bl, n, r, ok);
+  }
   __syncthreads();
   return !ok;
 }
