@@ -61,8 +61,10 @@ def test_role_projection_full_size(dev, oracle):
     assert np.abs(out[:, rows].cpu().numpy().astype(np.float64) - ref).max() < ATOL
 
 
-@pytest.mark.parametrize("bh,n,d,r", [(2, 1000, 128, 64), (3, 4500, 128, 48), (1, 77, 64, 32)])
+@pytest.mark.parametrize("bh,n,d,r", [(2, 1000, 128, 64), (3, 4500, 128, 48), (1, 77, 64, 32), (24, 30001, 128, 48)])
 def test_role_k_projection_matches_oracle(dev, oracle, bh, n, d, r):
+    """(24, 30001, 128, 48): 59 blocks of 512 tokens per head against about 1,000 resident
+    workgroups, so workgroups walk several blocks of their head (and a short last one)."""
     from sparsepr_amd.kernels.role_projection import role_k_projection_normalize
 
     rng = np.random.default_rng(7 * n + r)
