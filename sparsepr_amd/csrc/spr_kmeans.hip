@@ -418,12 +418,14 @@ __global__ void centroid_sq_kernel(const T* __restrict__ c, int64_t rows, int32_
   out[r] = s;
 }
 
-// Same assignment with the batch's centroids resident in LDS: a 1024-thread
-// workgroup (four waves per SIMD) stages all k centroids once (padded rows;
-// zeros and c_sq = +inf past k), then each wave walks 64-point blocks of the
-// batch against them with no further barriers, centroid reloads or staging
-// work.  Used while the padded centroids fit in LDS (k <= ASSIGN_RESIDENT_K at
-// D = 128).
+// The assignment with the batch's centroids resident in LDS: a 1024-thread
+// workgroup (four waves per SIMD) stages all k centroids once (padded rows, and
+// -c_sq / 2 per centroid: zeros and -inf past k), then each wave walks 64-point
+// blocks of the batch against them with no further barriers, centroid reloads or
+// staging work.  The MFMA accumulator starts at -c_sq / 2, so it ends at
+// x.c - c_sq / 2 and the nearest centroid of a step is its largest entry; the
+// distance x_sq + c_sq - 2 x.c is formed once per step for its best candidate.
+// Used while the padded centroids fit in LDS (k <= ASSIGN_RESIDENT_K at D = 128).
 constexpr int ASSIGN_RESIDENT_K = 512;
 
 constexpr int ASSIGN_RESIDENT_THREADS = 1024;
@@ -457,7 +459,7 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
                             : u32x4{0, 0, 0, 0};
     *reinterpret_cast<u32x4*>(cent + row * ROW_BYTES + vec * 16) = v;
   }
-  for (int r = tid; r < kpad; r += blockDim.x) csq_l[r] = r < k ? csqb[r] : __builtin_huge_valf();
+  for (int r = tid; r < kpad; r += blockDim.x) csq_l[r] = r < k ? -0.5f * csqb[r] : -__builtin_huge_valf();
   __syncthreads();
 
   const int64_t blocks = (n + ASSIGN_POINTS_PER_WAVE - 1) / ASSIGN_POINTS_PER_WAVE;
@@ -503,78 +505,92 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
     }
 
     // Per 32-centroid step each lane scans its 16 candidates (index c0 + 4 half +
-    // 8i + j, ascending in (i, j)) for the step's smallest unclamped distance
-    // r = (x_sq + c_sq) - 2 cross (one rounding per step; 2 cross is exact),
-    // strict <, so the lowest index wins among equal minima; the step's result
-    // then meets the running best once.  The clamp max(r, 0) changes the answer
-    // only when some r <= 0: all such candidates tie at 0 and the lowest index
-    // among them wins, which a (rare, wave-uniform) rescan of the step restores.
+    // 8i + j, ascending in (i, j)) for the step's largest accumulator entry
+    // x.c - c_sq / 2 (the smallest unclamped distance), strict >, so the lowest
+    // index wins among equal entries; the step's distance x_sq - 2 max (one
+    // rounding) then meets the running best once.  The clamp max(r, 0) changes the
+    // answer only when some distance is <= 0: all such candidates tie at 0 and the
+    // lowest index among them wins, which a (rare, wave-uniform) rescan restores.
     float best[2] = {3.4e38f, 3.4e38f};
     int32_t best_idx[2] = {0, 0};
     for (int c0 = 0; c0 < kpad; c0 += 32) {
-      spr::f32x16 acc0 = {}, acc1 = {};
+      // accumulator = -c_sq / 2 + x . c (row 8i + 4 half + j of the step: centroid c0 + that)
+      const float* cs = csq_l + c0 + 4 * half;
+      spr::f32x16 cinit;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const spr::f32x4 c4 = *reinterpret_cast<const spr::f32x4*>(cs + 8 * i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cinit[4 * i + j] = c4[j];
+      }
+      spr::f32x16 acc0, acc1;
       const uint8_t* arow = cent + (c0 + col) * ROW_BYTES + half * 16;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[0][s]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[1][s]), acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[0][s]),
+                                                       s == 0 ? cinit : acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(spr::as_bf16x8(a), spr::as_bf16x8(xf[1][s]),
+                                                       s == 0 ? cinit : acc1, 0, 0, 0);
       }
-      const float* csq_step = csq_l + c0 + 4 * half;
-      float lb0 = 0.0f, lb1 = 0.0f;
-      int32_t lo0 = 0, lo1 = 0;
+      // step-local argmax of the accumulator (the smallest c_sq - 2 x.c): four chains per
+      // fragment, merged in ascending offset order, strict >, so the lowest offset wins ties
+      float lb[2];
+      int32_t lo[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int off = 8 * i + j;
-          const float csq = csq_step[off];
-          const float r0 = __builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq));
-          const float r1 = __builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq));
-          if (off == 0) {
-            lb0 = r0;
-            lb1 = r1;
-          } else {
-            const bool t0 = r0 < lb0;
-            const bool t1 = r1 < lb1;
-            lb0 = t0 ? r0 : lb0;
-            lo0 = t0 ? off : lo0;
-            lb1 = t1 ? r1 : lb1;
-            lo1 = t1 ? off : lo1;
-          }
-        }
-      }
-      if (__ballot(lb0 <= 0.0f || lb1 <= 0.0f) != 0ull) {
-        // first candidate with r <= 0, in index order, at distance 0
-        bool found0 = false, found1 = false;
+      for (int f = 0; f < 2; ++f) {
+        const spr::f32x16& acc = f == 0 ? acc0 : acc1;
+        float cb[4];
+        int32_t co[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+          cb[i] = acc[4 * i];
+          co[i] = 8 * i;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int off = 8 * i + j;
-            const float csq = csq_step[off];
-            const float r0 = __builtin_fmaf(-2.0f, acc0[4 * i + j], __fadd_rn(xsq[0], csq));
-            const float r1 = __builtin_fmaf(-2.0f, acc1[4 * i + j], __fadd_rn(xsq[1], csq));
-            if (lb0 <= 0.0f && !found0 && r0 <= 0.0f) {
-              lo0 = off;
-              found0 = true;
-            }
-            if (lb1 <= 0.0f && !found1 && r1 <= 0.0f) {
-              lo1 = off;
-              found1 = true;
-            }
+          for (int j = 1; j < 4; ++j) {
+            const bool t = acc[4 * i + j] > cb[i];
+            co[i] = t ? 8 * i + j : co[i];
+            cb[i] = fmaxf(acc[4 * i + j], cb[i]);
           }
         }
-        lb0 = fmaxf(lb0, 0.0f);
-        lb1 = fmaxf(lb1, 0.0f);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bool t = cb[2 * h + 1] > cb[2 * h];
+          co[2 * h] = t ? co[2 * h + 1] : co[2 * h];
+          cb[2 * h] = fmaxf(cb[2 * h + 1], cb[2 * h]);
+        }
+        const bool t = cb[2] > cb[0];
+        lo[f] = t ? co[2] : co[0];
+        // the distance x_sq + c_sq - 2 x.c of the step's best, one rounding
+        lb[f] = __builtin_fmaf(-2.0f, fmaxf(cb[2], cb[0]), xsq[f]);
+      }
+      if (__ballot(lb[0] <= 0.0f || lb[1] <= 0.0f) != 0ull) {
+        // the clamp at 0: the first candidate whose distance is <= 0, in index order
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+          const spr::f32x16& acc = f == 0 ? acc0 : acc1;
+          bool found = false;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float r = __builtin_fmaf(-2.0f, acc[4 * i + j], xsq[f]);
+              if (lb[f] <= 0.0f && !found && r <= 0.0f) {
+                lo[f] = 8 * i + j;
+                found = true;
+              }
+            }
+          }
+          lb[f] = fmaxf(lb[f], 0.0f);
+        }
       }
       const int32_t base = c0 + 4 * half;
-      const bool t0 = lb0 < best[0];
-      const bool t1 = lb1 < best[1];
-      best[0] = t0 ? lb0 : best[0];
-      best_idx[0] = t0 ? base + lo0 : best_idx[0];
-      best[1] = t1 ? lb1 : best[1];
-      best_idx[1] = t1 ? base + lo1 : best_idx[1];
+#pragma unroll
+      for (int f = 0; f < 2; ++f) {
+        const bool t = lb[f] < best[f];
+        best[f] = t ? lb[f] : best[f];
+        best_idx[f] = t ? base + lo[f] : best_idx[f];
+      }
     }
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
