@@ -615,14 +615,16 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
 // (v_mfma_f32_32x32x16_f16 on the scaled images).
 //
 // Per 32-centroid step each lane scans its 16 candidates (index c0 + 4 half + 8i + j,
-// ascending in (i, j)) for the step's smallest unclamped distance
-// r = (x_sq + c_sq) - 2 cross (one rounding per step; 2 cross is exact), strict <, so
-// the lowest index wins among equal minima; the step's result then meets the running
-// best once.  The clamp max(r, 0) changes the answer only when some r <= 0: all such
-// candidates tie at 0 and the lowest index among them wins, which a (rare,
-// wave-uniform) rescan of the step restores.  The MFMAs of step s + 1 are issued in the
-// same instruction stream as the argmin of step s (interleaved by sched_group_barrier),
-// so the matrix pipe and the VALU work at the same time within a wave.
+// ascending in (i, j)) for the step's smallest c_sq - 2 cross (one fused multiply-add;
+// 2 cross is exact), strict <, so the lowest index wins among equal minima; x_sq is
+// added to the step's best only, and the result meets the running best once.  (The
+// streamed kernel forms (x_sq + c_sq) - 2 cross per candidate: the two can differ only
+// between candidates within a few fp32 ulp of x_sq + c_sq of each other.)  The clamp
+// max(r, 0) changes the answer only when some r <= 0: all such candidates tie at 0 and
+// the lowest index among them wins, which a (rare, wave-uniform) rescan of the step
+// restores.  The MFMAs of step s + 1 are issued in the same instruction stream as the
+// argmin of step s (interleaved by sched_group_barrier), so the matrix pipe and the VALU
+// work at the same time within a wave.
 //
 // A workgroup walks a contiguous range of the (batch, block) space; where the range
 // crosses into the next batch, the workgroup stages that batch's centroids in turn.
@@ -768,7 +770,8 @@ __global__ __launch_bounds__(PIPE_THREADS, 1) void kmeans_assign_tf32_resident_k
         kf[0] = __builtin_ldexpf(-2.0f, -(xexp[0] + et));
         kf[1] = __builtin_ldexpf(-2.0f, -(xexp[1] + et));
       };
-      // step-local (min, argmin) of the unclamped distances of acc (centroids c0 ..)
+      // step-local (min, argmin) of c_sq - 2 x.c over acc (centroids c0 ..), then the best's
+      // unclamped distance x_sq + (c_sq - 2 x.c)
       auto scan = [&](const spr::f32x16 (&acc)[2], int c0, const float (&kf)[2], float (&lb)[2],
                       int32_t (&lo)[2]) {
         const float* cs = csq_l + c0 + 4 * half;
@@ -786,7 +789,7 @@ __global__ __launch_bounds__(PIPE_THREADS, 1) void kmeans_assign_tf32_resident_k
           for (int f = 0; f < 2; ++f) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const float r = __builtin_fmaf(kf[f], acc[f][4 * i + j], __fadd_rn(xsq[f], c4[i][j]));
+              const float r = __builtin_fmaf(kf[f], acc[f][4 * i + j], c4[i][j]);  // c_sq - 2 x.c
               if (j == 0) {
                 cb[f][i] = r;
                 co[f][i] = 8 * i;
@@ -808,7 +811,7 @@ __global__ __launch_bounds__(PIPE_THREADS, 1) void kmeans_assign_tf32_resident_k
           }
           const bool t = cb[f][2] < cb[f][0];
           lo[f] = t ? co[f][2] : co[f][0];
-          lb[f] = fminf(cb[f][2], cb[f][0]);
+          lb[f] = __fadd_rn(xsq[f], fminf(cb[f][2], cb[f][0]));  // the step best's distance
         }
       };
       // clamp rule and merge into the running best
@@ -825,7 +828,7 @@ __global__ __launch_bounds__(PIPE_THREADS, 1) void kmeans_assign_tf32_resident_k
 #pragma unroll
               for (int j = 0; j < 4; ++j) {
                 const int off = 8 * i + j;
-                const float r = __builtin_fmaf(kf[f], acc[f][4 * i + j], __fadd_rn(xsq[f], cs[off]));
+                const float r = __fadd_rn(xsq[f], __builtin_fmaf(kf[f], acc[f][4 * i + j], cs[off]));
                 if (lb[f] <= 0.0f && !found && r <= 0.0f) {
                   lo[f] = off;
                   found = true;
