@@ -23,6 +23,8 @@
 // and the threshold (a python float compared against a bf16 tensor is cast to bf16).
 #pragma clang fp contract(off)
 
+#include <type_traits>
+
 #include "spr_common.h"
 
 namespace {
@@ -76,30 +78,111 @@ __device__ __forceinline__ float row_dot(const float* q_row, const float* kr, in
   return acc;
 }
 
-// Sorts n2 (a power of two) (value, index) pairs in LDS so that ranks_before holds along
-// the array (a bitonic network; the order is total, so the result equals a rank sort's).
-// Every thread of the block calls it.
-__device__ void bitonic_rank_sort(float* v, int32_t* idx, int n2) {
-  for (int size = 2; size <= n2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < n2; i += blockDim.x) {
-        const int l = i ^ stride;
-        if (l > i) {
-          const float vi = v[i], vl = v[l];
-          const int32_t ii = idx[i], il = idx[l];
-          const bool first = (i & size) == 0;  // this run ends up in ranks_before order
-          const bool swap = first ? ranks_before(vl, il, vi, ii) : ranks_before(vi, ii, vl, il);
-          if (swap) {
-            v[i] = vl;
-            v[l] = vi;
-            idx[i] = il;
-            idx[l] = ii;
-          }
-        }
+// Sort key of (value, index) under ranks_before: ascending keys are descending values,
+// ties by ascending index.  The high word is the value's order-preserving unsigned image
+// (-0 taken as +0, so that equal values tie as under ==), complemented; the low word is
+// the index.  (NaN values, which ranks_before leaves unordered, get a fixed place.)
+__device__ __forceinline__ uint64_t rank_key(float v, int32_t i) {
+  uint32_t b = __float_as_uint(v);
+  if ((b << 1) == 0u) b = 0u;
+  const uint32_t up = (b & 0x80000000u) ? ~b : (b | 0x80000000u);  // ascending in v
+  return (static_cast<uint64_t>(~up) << 32) | static_cast<uint32_t>(i);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
+  const int lo = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v)), mask, 64);
+  const int hi = __shfl_xor(static_cast<int>(static_cast<uint32_t>(v >> 32)), mask, 64);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+
+// One exchange stage (run length SIZE, partner distance STRIDE) of a bitonic network over
+// 64 E keys, lane l holding positions l E .. l E + E - 1; keys end up ascending.  Strides
+// below E exchange inside the lane, the others with lane ^ (STRIDE / E) by shuffles (then
+// SIZE > STRIDE >= E, so a run's direction, position & SIZE, comes from the lane bits).
+template <int E, int SIZE, int STRIDE>
+__device__ __forceinline__ void bitonic_stage(uint64_t (&k)[E], int lane) {
+  if constexpr (STRIDE >= E) {
+    constexpr int LX = STRIDE / E;
+    const bool take_min = ((lane & LX) == 0) == (((lane * E) & SIZE) == 0);
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const uint64_t o = shfl_xor_u64(k[r], LX);
+      k[r] = (take_min ? o < k[r] : o > k[r]) ? o : k[r];
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      if ((r & STRIDE) == 0) {
+        constexpr bool IN_LANE = SIZE < E;
+        const bool ascending = IN_LANE ? (r & SIZE) == 0 : ((lane * E) & SIZE) == 0;
+        const uint64_t a = k[r], b = k[r | STRIDE];
+        const bool sw = ascending ? b < a : a < b;
+        k[r] = sw ? b : a;
+        k[r | STRIDE] = sw ? a : b;
       }
-      __syncthreads();
     }
   }
+}
+
+// The whole network from stage (SIZE, STRIDE) on, every index a compile-time constant.
+template <int E, int SIZE, int STRIDE>
+__device__ __forceinline__ void bitonic_from(uint64_t (&k)[E], int lane) {
+  bitonic_stage<E, SIZE, STRIDE>(k, lane);
+  if constexpr (STRIDE > 1) {
+    bitonic_from<E, SIZE, STRIDE / 2>(k, lane);
+  } else if constexpr (SIZE < 64 * E) {
+    bitonic_from<E, 2 * SIZE, SIZE>(k, lane);
+  }
+}
+
+// Sorts 64 E keys held E per lane (lane l: positions l E .. l E + E - 1), ascending.
+template <int E>
+__device__ __forceinline__ void wave_sort_keys(uint64_t (&k)[E], int lane) {
+  bitonic_from<E, 2, 1>(k, lane);
+}
+
+// Sorts the n2 (a power of two, n2 <= 64 E) (value, index) pairs in LDS so that
+// ranks_before holds along the array.  One wave, in registers (wave_sort_keys; positions
+// past n2 hold the largest key); then the values (bit for bit, read back through the
+// sorted indices) and indices are stored in rank order.  The order is total, so the
+// result equals a rank sort's.  Only the calling wave touches the arrays.
+template <int E>
+__device__ void wave_rank_sort(float* v, int32_t* idx, int n2) {
+  const int lane = threadIdx.x & 63;
+  uint64_t k[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int pos = lane * E + r;
+    k[r] = pos < n2 ? rank_key(v[pos], idx[pos]) : ~0ull;
+  }
+  wave_sort_keys<E>(k, lane);
+  float val[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int pos = lane * E + r;
+    val[r] = pos < n2 ? v[static_cast<uint32_t>(k[r])] : 0.0f;
+  }
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int pos = lane * E + r;
+    if (pos < n2) {
+      v[pos] = val[r];
+      idx[pos] = static_cast<int32_t>(static_cast<uint32_t>(k[r]));
+    }
+  }
+}
+
+// Calls f(std::integral_constant<int, E>) with E = n2 / 64 (at least 1), the register
+// count per lane of wave_rank_sort, for n2 a power of two up to 4096.
+template <typename F>
+void by_sort_width(int n2, F&& f) {
+  if (n2 <= 64) f(std::integral_constant<int, 1>{});
+  else if (n2 <= 128) f(std::integral_constant<int, 2>{});
+  else if (n2 <= 256) f(std::integral_constant<int, 4>{});
+  else if (n2 <= 512) f(std::integral_constant<int, 8>{});
+  else if (n2 <= 1024) f(std::integral_constant<int, 16>{});
+  else if (n2 <= 2048) f(std::integral_constant<int, 32>{});
+  else f(std::integral_constant<int, 64>{});
 }
 
 __device__ __forceinline__ int pow2_at_least(int n) {
@@ -111,13 +194,14 @@ __device__ __forceinline__ int pow2_at_least(int n) {
 // One workgroup per (bh, q-cluster) row.
 //   scores, max, weighted exp, sum (index order, one wave reading 64 values per step
 //   into registers), probabilities;
-//   sort by (probability desc, index asc) with a bitonic network (the order is
-//   total, so the result equals a rank sort's);
+//   sort by (probability desc, index asc): one wave's bitonic network in registers
+//   (the order is total, so the result equals a rank sort's);
 //   the shown cumsum of the sorted probabilities never decreases (terms >= 0,
 //   bf16 rounding monotone), so "remove rank r when r > 0 and the cumsum through
 //   r - 1 exceeds p" keeps exactly the ranks below cut = max(first such r,
 //   preserve): one wave walks the chain up to the crossing only, 64 values at a time.
 // Dynamic LDS: 2 x n2 floats/ints (n2 = kn rounded up to a power of two).
+template <int E>  // n2 <= 64 E
 __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __restrict__ qc,
                                                                const float* __restrict__ kc,
                                                                const int32_t* __restrict__ k_sizes,
@@ -180,7 +264,8 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
     sorted_idx[j] = j;
   }
   __syncthreads();
-  bitonic_rank_sort(sorted_val, sorted_idx, n2);
+  if (wave0) wave_rank_sort<E>(sorted_val, sorted_idx, n2);
+  __syncthreads();
 
   if (wave0) {
     const float thr = score_bf16 ? bf16r(p) : p;
@@ -224,7 +309,7 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
   }
 }
 
-// One workgroup per (bh, q) row of scores [bh, qn, kn].
+// One wave per (bh, q) row of scores [bh, qn, kn].
 // mode 0: n8_ops.cu semantics, mode 1: selector_budget.py / CPU-fallback semantics.
 // Both walk the clusters in (score desc, index asc) order, skip empty ones, and keep a
 // cluster while the running cost of the non-empty clusters so far stays within the
@@ -232,67 +317,62 @@ __global__ __launch_bounds__(SEL_THREADS) void topp_map_kernel(const float* __re
 // with cum the inclusive prefix sum of the non-empty costs in sorted order.  They differ
 // in the one extra cluster taken when the budget is not met: mode 0 the first non-empty
 // cluster past it (the crossing), mode 1 the cluster at sorted position `count`.
-// Dynamic LDS: n2 floats + n2 ints + kn bytes (n2 = kn rounded up to a power of two).
-__global__ __launch_bounds__(SEL_THREADS) void select_budget_kernel(
+// The row's keys are sorted in registers (wave_sort_keys: lane l holds ranks
+// l E .. l E + E - 1), the prefix sum runs over those ranks where they lie (lane totals
+// scanned across the wave), and the kept flags go through an LDS byte row to the map row
+// and the ascending schedule.
+// Dynamic LDS: kn bytes rounded up to 16.
+template <int E>  // kn <= 64 E
+__global__ __launch_bounds__(64) void select_budget_kernel(
     const float* __restrict__ scores, const int32_t* __restrict__ sizes, const int32_t* __restrict__ budgets,
     int32_t qn, int32_t kn, int32_t mode, uint8_t* __restrict__ out, int32_t* __restrict__ ids,
     int32_t* __restrict__ counts) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t sel_dyn[];
-  __shared__ long long wave_tot[SEL_THREADS / 64];
-  __shared__ long long red_sel[SEL_THREADS / 64];
-  __shared__ int32_t red_cnt[SEL_THREADS / 64], red_valid[SEL_THREADS / 64], red_cross[SEL_THREADS / 64];
-  const int n2 = pow2_at_least(kn);
-  float* val = reinterpret_cast<float*>(sel_dyn);
-  int32_t* order = reinterpret_cast<int32_t*>(val + n2);
-  uint8_t* keep = reinterpret_cast<uint8_t*>(order + n2);
+  extern __shared__ __attribute__((aligned(16))) uint8_t keep[];
   const int64_t row = blockIdx.x;
   const int64_t bh = row / qn;
   const int32_t q = static_cast<int32_t>(row - bh * qn);
   const float* srow = scores + row * kn;
   const int32_t* sz = sizes + bh * kn;
-  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int lane = threadIdx.x;
   const int32_t budget = budgets[row];
-  for (int j = t; j < n2; j += blockDim.x) {
-    val[j] = j < kn ? srow[j] : -__builtin_huge_valf();  // padding sorts last
-    order[j] = j;
-    if (j < kn) keep[j] = 0;
+  for (int j = 4 * lane; j < kn; j += 256) *reinterpret_cast<uint32_t*>(keep + j) = 0u;
+  uint64_t k[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int pos = lane * E + r;
+    k[r] = pos < kn ? rank_key(srow[pos], pos) : ~0ull;  // padding sorts last
   }
-  __syncthreads();
-  bitonic_rank_sort(val, order, n2);
-  // inclusive prefix sum of the non-empty costs in sorted order: thread t owns ranks
-  // [t E, t E + E)
-  const int per = (n2 + SEL_THREADS - 1) / SEL_THREADS;
-  const int r0 = t * per;
-  long long local = 0;
-  for (int u = 0; u < per; ++u) {
-    const int r = r0 + u;
-    if (r < kn) local += max(sz[order[r]], 0);
+  wave_sort_keys<E>(k, lane);
+  // costs in rank order; the exclusive prefix of the non-empty costs before this lane's ranks
+  int32_t cost[E];
+  long long tot = 0;
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    cost[r] = lane * E + r < kn ? sz[static_cast<uint32_t>(k[r])] : 0;
+    tot += max(cost[r], 0);
   }
-  long long incl = local;  // wave inclusive scan of the thread totals
+  long long incl = tot;
   for (int o = 1; o < 64; o <<= 1) {
     const long long up = __shfl_up(incl, o, 64);
     if (lane >= o) incl += up;
   }
-  if (lane == 63) wave_tot[wv] = incl;
-  __syncthreads();
-  long long cum = incl - local;
-  for (int w = 0; w < wv; ++w) cum += wave_tot[w];
+  long long cum = incl - tot;
   long long sel = 0;
   int32_t cnt = 0, valid = 0, cross = 0x7FFFFFFF;
-  for (int u = 0; u < per; ++u) {
-    const int r = r0 + u;
-    if (r >= kn) break;
-    const int32_t c = order[r];
-    const int32_t cost = sz[c];
-    if (cost <= 0) continue;
-    cum += cost;
-    ++valid;
-    if (cum <= budget) {
-      keep[c] = 1;
-      sel += cost;
-      ++cnt;
-    } else {
-      cross = min(cross, r);
+  __syncthreads();  // the cleared flags are stored before any is set
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int rank = lane * E + r;
+    if (rank < kn && cost[r] > 0) {
+      cum += cost[r];
+      ++valid;
+      if (cum <= budget) {
+        keep[static_cast<uint32_t>(k[r])] = 1;
+        sel += cost[r];
+        ++cnt;
+      } else {
+        cross = min(cross, rank);
+      }
     }
   }
   for (int o = 32; o > 0; o >>= 1) {
@@ -301,47 +381,37 @@ __global__ __launch_bounds__(SEL_THREADS) void select_budget_kernel(
     valid += __shfl_xor(valid, o, 64);
     cross = min(cross, __shfl_xor(cross, o, 64));
   }
-  if (lane == 0) {
-    red_sel[wv] = sel;
-    red_cnt[wv] = cnt;
-    red_valid[wv] = valid;
-    red_cross[wv] = cross;
+  // the one extra cluster, at rank `crossing` (mode 0) or `count` (mode 1), set by its lane
+  int32_t extra = -1;
+  if (mode == 0) {
+    if (budget > 0 && sel < budget && cross != 0x7FFFFFFF) extra = cross;
+  } else {
+    if (budget > 0 && sel < budget && cnt < valid && cnt < kn) extra = cnt;
   }
-  __syncthreads();
-  if (t == 0) {
-    long long selected = 0;
-    int32_t count = 0, n_valid = 0, crossing = 0x7FFFFFFF;
-    for (int w = 0; w < SEL_THREADS / 64; ++w) {
-      selected += red_sel[w];
-      count += red_cnt[w];
-      n_valid += red_valid[w];
-      crossing = min(crossing, red_cross[w]);
-    }
-    if (mode == 0) {
-      if (budget > 0 && selected < budget && crossing != 0x7FFFFFFF) keep[order[crossing]] = 1;
-    } else {
-      if (budget > 0 && selected < budget && count < n_valid && count < kn) keep[order[count]] = 1;
+  if (extra >= 0 && extra / E == lane) {
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      if (r == extra % E) keep[static_cast<uint32_t>(k[r])] = 1;
     }
   }
   __syncthreads();
   const int64_t stride = static_cast<int64_t>(kn) + 1;
   uint8_t* orow = out + (bh * (qn + 1) + q + 1) * stride;
-  for (int j = threadIdx.x; j <= kn; j += blockDim.x) orow[j] = (j == 0) ? 1 : keep[j - 1];
+  for (int j = lane; j <= kn; j += 64) orow[j] = (j == 0) ? 1 : keep[j - 1];
   if (q == 0) {
     uint8_t* head = out + bh * (qn + 1) * stride;
-    for (int j = threadIdx.x; j <= kn; j += blockDim.x) head[j] = (j == 0) ? 1 : 0;
+    for (int j = lane; j <= kn; j += 64) head[j] = (j == 0) ? 1 : 0;
   }
-  if (ids != nullptr && counts != nullptr && threadIdx.x < 64) {
-    // ascending compaction of the kept flags by wave 0
-    const int lane = threadIdx.x;
+  if (ids != nullptr && counts != nullptr) {
+    // ascending compaction of the kept flags
     int32_t* irow = ids + row * kn;
     int32_t base = 0;
     for (int c0 = 0; c0 < kn; c0 += 64) {
       const int c = c0 + lane;
-      const bool k = c < kn && keep[c];
-      const uint64_t bits = __ballot(k);
+      const bool kc = c < kn && keep[c];
+      const uint64_t bits = __ballot(kc);
       const int pos = __popcll(bits & ((1ull << lane) - 1ull));
-      if (k) irow[base + pos] = c;
+      if (kc) irow[base + pos] = c;
       base += __popcll(bits);
     }
     if (lane == 0) counts[row] = base;
@@ -454,8 +524,10 @@ extern "C" int spr_topp_map(const float* qc, const float* kc, const int32_t* k_s
   int n2 = 1;
   while (n2 < kn) n2 <<= 1;
   const size_t lds = static_cast<size_t>(n2) * 8;  // at most 32 KB (kn <= 4096)
-  topp_map_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, lds, stream>>>(
-      qc, kc, k_sizes, qn, kn, d, sqrt_d, p, preserve, score_bf16, map, budgets);
+  by_sort_width(n2, [&](auto e) {
+    topp_map_kernel<decltype(e)::value><<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, lds, stream>>>(
+        qc, kc, k_sizes, qn, kn, d, sqrt_d, p, preserve, score_bf16, map, budgets);
+  });
   SPR_LAUNCHED("topp_map_kernel");
   return SPR_OK;
 }
@@ -474,9 +546,11 @@ extern "C" int spr_select_budget(const float* scores, const int32_t* sizes, cons
   if (qn == 0) return SPR_OK;
   int n2 = 1;
   while (n2 < kn) n2 <<= 1;
-  const size_t lds = static_cast<size_t>(n2) * 8 + ((static_cast<size_t>(kn) + 15) & ~size_t(15));  // <= 36 KB
-  select_budget_kernel<<<dim3(static_cast<uint32_t>(bh * qn)), SEL_THREADS, lds, stream>>>(
-      scores, sizes, budgets, qn, kn, mode, out, ids, counts);
+  const size_t lds = (static_cast<size_t>(kn) + 15) & ~size_t(15);  // the kept flags
+  by_sort_width(n2, [&](auto e) {
+    select_budget_kernel<decltype(e)::value><<<dim3(static_cast<uint32_t>(bh * qn)), 64, lds, stream>>>(
+        scores, sizes, budgets, qn, kn, mode, out, ids, counts);
+  });
   SPR_LAUNCHED("select_budget_kernel");
   return SPR_OK;
 }
