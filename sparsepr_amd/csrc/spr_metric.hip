@@ -810,16 +810,31 @@ __global__ __launch_bounds__(256) void project_rows_kernel(const float* __restri
   const float* fh = f + h * d * r;
   float acc = 0.0f;
   if (lane < r) {
-    for (int j = 0; j < d; ++j) {
-      float xv = xr[j], fv = fh[j * r + lane];
-      if (precision == 1) {
-        xv = tf32_rna(xv);
-        fv = tf32_rna(fv);
-      } else if (precision == 2) {
-        xv = spr::bf16_to_f32(spr::f32_to_bf16(xv));
-        fv = spr::bf16_to_f32(spr::f32_to_bf16(fv));
+    // the loads of 16 steps are issued before their multiply-adds, so the chain waits on
+    // one memory latency per 16 steps instead of one per step
+    constexpr int JB = 16;
+    for (int j0 = 0; j0 < d; j0 += JB) {
+      float xv[JB], fv[JB];
+#pragma unroll
+      for (int u = 0; u < JB; ++u) {
+        const int j = min(j0 + u, d - 1);
+        xv[u] = xr[j];
+        fv[u] = fh[j * r + lane];
       }
-      acc = __builtin_fmaf(xv, fv, acc);
+#pragma unroll
+      for (int u = 0; u < JB; ++u) {
+        if (j0 + u < d) {
+          float a = xv[u], b = fv[u];
+          if (precision == 1) {
+            a = tf32_rna(a);
+            b = tf32_rna(b);
+          } else if (precision == 2) {
+            a = spr::bf16_to_f32(spr::f32_to_bf16(a));
+            b = spr::bf16_to_f32(spr::f32_to_bf16(b));
+          }
+          acc = __builtin_fmaf(a, b, acc);
+        }
+      }
     }
     if (div != nullptr) acc = acc / div[h];
   }
