@@ -82,8 +82,10 @@ __global__ __launch_bounds__(256) void role_metric_kernel(const T* __restrict__ 
                                                           const int32_t* __restrict__ rows, int32_t count,
                                                           const int32_t* __restrict__ sizes, int32_t center,
                                                           float post_scale, float* __restrict__ out) {
-  constexpr int RB = 64;           // rows per stage
-  constexpr int PER = RB * 32 / 256;  // elements per thread and column block per stage (8)
+  // rows per stage: each stage waits on a row-index load and then a value load, so larger
+  // stages mean fewer waits; the sums run over the rows in the same order for any RB
+  constexpr int RB = 192;
+  constexpr int PER = RB * 32 / 256;  // elements per thread and column block per stage (24)
   __shared__ float ta[RB][33];
   __shared__ float tb[RB][33];
   __shared__ int64_t ridx[2][RB];  // row of each stage row (-1: not used)
