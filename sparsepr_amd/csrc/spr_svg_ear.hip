@@ -19,7 +19,7 @@
 // (E *= alpha^2, w_c *= alpha; the mass sum *= alpha).
 //
 // Layout.  A first kernel writes the centroid logits l_c [query head, centroid,
-// cluster] (fp32 dot products over d, sequential, 64 clusters per workgroup)
+// cluster] (fp32 dot products over d, sequential, 128 rows x 32 clusters per workgroup)
 // into the score buffer; the score kernel overwrites each entry with its score.
 // The score kernel runs one workgroup of four waves per (query head, 8
 // consecutive key clusters); wave w scores query rows 32 w .. 32 w + 31 of each
@@ -103,11 +103,12 @@ __device__ __forceinline__ float sum_xor32(float x) {
 constexpr int SE_ROW = SE_D * 2;  // bytes per bf16 token row
 constexpr int SE_CPW = 8;         // key clusters per workgroup
 constexpr int CL_CLUSTERS = 32;   // clusters per centroid-logit workgroup
-constexpr int CL_ROWS = SE_THREADS / 4;  // query rows per centroid-logit workgroup
+constexpr int CL_ROWS = 2 * (SE_THREADS / 4);  // query rows per centroid-logit workgroup
 
 // l_c = (q . kc) / sqrt(D) (+ 0.5 min(sum_d q_d^2 var_d / D, cap)) for CL_ROWS query rows x
-// CL_CLUSTERS clusters per workgroup: thread -> query row tid / 4, clusters
-// 8 (tid % 4) .. + 7; fp32 fma chains over d in order.  Written to out [qh, qn, kn].
+// CL_CLUSTERS clusters per workgroup: thread -> query rows tid / 4 and tid / 4 + CL_ROWS / 2,
+// clusters 8 (tid % 4) .. + 7 (each centroid read from LDS serves two rows); fp32 fma chains
+// over d in order.  Written to out [qh, qn, kn].
 __global__ __launch_bounds__(SE_THREADS) void svg_ear_centroid_logit_kernel(
     const float* __restrict__ qc, const float* __restrict__ kcent, const float* __restrict__ var_k, float cap,
     int32_t qn, int32_t kn, int32_t group, float* __restrict__ out) {
@@ -129,40 +130,55 @@ __global__ __launch_bounds__(SE_THREADS) void svg_ear_centroid_logit_kernel(
         (live && var_k != nullptr) ? *reinterpret_cast<const float4*>(var_k + o) : float4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   __syncthreads();
-  const int r = blockIdx.y * CL_ROWS + tid / 4;
+  const int r0 = blockIdx.y * CL_ROWS + tid / 4;
+  const int r1 = r0 + CL_ROWS / 2;
   const int c0 = 8 * (tid % 4);
-  if (r >= qn) return;
-  const float* qrow = qc + (qh * qn + r) * SE_D;
-  float dot[8], s2[8];
+  if (r0 >= qn) return;
+  const float* qrow0 = qc + (qh * qn + r0) * SE_D;
+  const float* qrow1 = qc + (qh * qn + min(r1, qn - 1)) * SE_D;  // a row past qn computes, stores nothing
+  float dot0[8], s20[8], dot1[8], s21[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) dot[j] = s2[j] = 0.0f;
+  for (int j = 0; j < 8; ++j) dot0[j] = s20[j] = dot1[j] = s21[j] = 0.0f;
   for (int d0 = 0; d0 < SE_D; d0 += 4) {
-    const float4 qv = *reinterpret_cast<const float4*>(qrow + d0);
+    const float4 qa = *reinterpret_cast<const float4*>(qrow0 + d0);
+    const float4 qb = *reinterpret_cast<const float4*>(qrow1 + d0);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float4 kv = *reinterpret_cast<const float4*>(&kc_l[c0 + j][d0]);
-      dot[j] = __builtin_fmaf(qv.x, kv.x, dot[j]);
-      dot[j] = __builtin_fmaf(qv.y, kv.y, dot[j]);
-      dot[j] = __builtin_fmaf(qv.z, kv.z, dot[j]);
-      dot[j] = __builtin_fmaf(qv.w, kv.w, dot[j]);
+      dot0[j] = __builtin_fmaf(qa.x, kv.x, dot0[j]);
+      dot0[j] = __builtin_fmaf(qa.y, kv.y, dot0[j]);
+      dot0[j] = __builtin_fmaf(qa.z, kv.z, dot0[j]);
+      dot0[j] = __builtin_fmaf(qa.w, kv.w, dot0[j]);
+      dot1[j] = __builtin_fmaf(qb.x, kv.x, dot1[j]);
+      dot1[j] = __builtin_fmaf(qb.y, kv.y, dot1[j]);
+      dot1[j] = __builtin_fmaf(qb.z, kv.z, dot1[j]);
+      dot1[j] = __builtin_fmaf(qb.w, kv.w, dot1[j]);
       if (var_k != nullptr) {
         const float4 vv = *reinterpret_cast<const float4*>(&var_l[c0 + j][d0]);
-        s2[j] = __builtin_fmaf(qv.x * qv.x, vv.x, s2[j]);
-        s2[j] = __builtin_fmaf(qv.y * qv.y, vv.y, s2[j]);
-        s2[j] = __builtin_fmaf(qv.z * qv.z, vv.z, s2[j]);
-        s2[j] = __builtin_fmaf(qv.w * qv.w, vv.w, s2[j]);
+        s20[j] = __builtin_fmaf(qa.x * qa.x, vv.x, s20[j]);
+        s20[j] = __builtin_fmaf(qa.y * qa.y, vv.y, s20[j]);
+        s20[j] = __builtin_fmaf(qa.z * qa.z, vv.z, s20[j]);
+        s20[j] = __builtin_fmaf(qa.w * qa.w, vv.w, s20[j]);
+        s21[j] = __builtin_fmaf(qb.x * qb.x, vv.x, s21[j]);
+        s21[j] = __builtin_fmaf(qb.y * qb.y, vv.y, s21[j]);
+        s21[j] = __builtin_fmaf(qb.z * qb.z, vv.z, s21[j]);
+        s21[j] = __builtin_fmaf(qb.w * qb.w, vv.w, s21[j]);
       }
     }
   }
-  float* orow = out + (qh * qn + r) * kn + cb + c0;
+  auto store = [&](int r, const float (&dot)[8], const float (&s2)[8]) {
+    float* orow = out + (qh * qn + r) * kn + cb + c0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    if (c0 + j < ncl) {
-      float l = dot[j] * scale;
-      if (var_k != nullptr) l += 0.5f * fminf(s2[j] / static_cast<float>(SE_D), cap);
-      orow[j] = l;
+    for (int j = 0; j < 8; ++j) {
+      if (c0 + j < ncl) {
+        float l = dot[j] * scale;
+        if (var_k != nullptr) l += 0.5f * fminf(s2[j] / static_cast<float>(SE_D), cap);
+        orow[j] = l;
+      }
     }
-  }
+  };
+  store(r0, dot0, s20);
+  if (r1 < qn) store(r1, dot1, s21);
 }
 
 template <int MODE>  // 0: value error (scores holds l_c on entry), 1: attention mass
