@@ -22,7 +22,10 @@ def _centroids(rng, bh, qn, kn, d, scale=1.0):
     return qc, kc, ks
 
 
-@pytest.mark.parametrize("bh,qn,kn,d", [(4, 32, 64, 64), (2, 128, 512, 128), (1, 5, 300, 128),
+# key-cluster counts that reach every register width of the one-wave sort (1 .. 64 keys per
+# lane: kn up to 64, 128, 256, 512, 1024, 2048, 4096)
+@pytest.mark.parametrize("bh,qn,kn,d", [(4, 32, 64, 64), (2, 9, 100, 64), (2, 17, 256, 64), (2, 128, 512, 128),
+                                        (1, 5, 300, 128), (1, 11, 1000, 128), (1, 3, 2000, 64),
                                         (1, 3, 4096, 64), (3, 100, 500, 128)])
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("p,ratio", [(0.9, 0.0), (0.7, 0.0), (0.95, 0.1)])
@@ -129,13 +132,18 @@ def test_selector_known_answer_gpu(dev):
 
 
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("bh,qn,kn", [(2, 7, 9), (3, 100, 1000), (1, 4, 4096)])
+@pytest.mark.parametrize("bh,qn,kn", [(2, 7, 9), (1, 3, 64), (1, 3, 65), (2, 9, 100), (2, 17, 200), (3, 50, 512),
+                                     (3, 100, 1000), (1, 6, 2000), (1, 4, 4096)])
 def test_selector_random_vs_oracle(dev, oracle, mode, bh, qn, kn):
+    """Rows of every register width of the one-wave sort (kn up to 64 E for E = 1 .. 64), with
+    many tied scores (the index breaks them) and empty clusters."""
     from sparsepr_amd.kernels.selection import select_budget
 
     rng = np.random.default_rng(mode * 7 + kn)
     scores = rng.integers(-5, 6, (bh, qn, kn)).astype(np.float32)  # many ties
     scores[..., ::3] = rng.standard_normal(scores[..., ::3].shape)
+    scores[..., 1::11] = -0.0  # ties with the +0.0 entries: compared as equal, so the index decides
+    scores[..., 2::13] = -np.inf  # empty-cluster scores
     sizes = rng.integers(0, 50, (bh, kn)).astype(np.int32)
     budgets = rng.integers(0, 25 * kn, (bh, qn)).astype(np.int32)
     out, ids, counts = select_budget(to_dev(scores, dev), to_dev(sizes, dev), to_dev(budgets, dev), mode,
