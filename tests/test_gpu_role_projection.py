@@ -14,8 +14,10 @@ ATOL = 2e-5
 
 
 @pytest.mark.parametrize("bh,n,d,r", [(2, 1000, 128, 64), (1, 777, 128, 48), (3, 65, 64, 32), (1, 300, 128, 100),
-                                      (1, 513, 128, 128), (2, 40, 64, 16)])
+                                      (1, 513, 128, 128), (2, 40, 64, 16), (24, 30001, 128, 64)])
 def test_role_projection_matches_oracle(dev, oracle, bh, n, d, r):
+    """(24, 30001, 128, 64): 118 blocks of 256 tokens per head against about 1,000 resident
+    workgroups, so workgroups walk several blocks of their head (and a short last one)."""
     from sparsepr_amd.kernels.role_projection import role_projection_rms_triton
 
     rng = np.random.default_rng(n + r)
@@ -61,9 +63,9 @@ def test_role_projection_full_size(dev, oracle):
     assert np.abs(out[:, rows].cpu().numpy().astype(np.float64) - ref).max() < ATOL
 
 
-@pytest.mark.parametrize("bh,n,d,r", [(2, 1000, 128, 64), (3, 4500, 128, 48), (1, 77, 64, 32), (24, 30001, 128, 48)])
+@pytest.mark.parametrize("bh,n,d,r", [(2, 1000, 128, 64), (3, 4500, 128, 48), (1, 77, 64, 32), (24, 60001, 128, 48)])
 def test_role_k_projection_matches_oracle(dev, oracle, bh, n, d, r):
-    """(24, 30001, 128, 48): 59 blocks of 512 tokens per head against about 1,000 resident
+    """(24, 60001, 128, 48): 59 blocks of 1024 tokens per head against about 1,000 resident
     workgroups, so workgroups walk several blocks of their head (and a short last one)."""
     from sparsepr_amd.kernels.role_projection import role_k_projection_normalize
 
