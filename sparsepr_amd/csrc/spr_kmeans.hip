@@ -608,7 +608,7 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
 
 
 // The TF32 assignment with a batch's centroids resident in LDS: one workgroup per CU
-// (512 threads, two waves per SIMD) stages the scaled fp16 images of the centroids'
+// (768 or 512 threads, pipe_threads) stages the scaled fp16 images of the centroids'
 // TF32 roundings once (padded rows; zeros and c_sq = +inf past k; the per-64-centroid
 // tile exponents of kmeans_assign_tf32_kernel, so both kernels form the same exact
 // products) and its waves walk 64-point blocks against them with no further barriers
@@ -628,8 +628,12 @@ __global__ __launch_bounds__(ASSIGN_RESIDENT_THREADS, 1) void kmeans_assign_resi
 //
 // A workgroup walks a contiguous range of the (batch, block) space; where the range
 // crosses into the next batch, the workgroup stages that batch's centroids in turn.
-constexpr int PIPE_THREADS = 512;
-constexpr int PIPE_WAVES = PIPE_THREADS / 64;
+// Threads per workgroup: three waves per SIMD where the registers allow it (D <= 64: 165 and
+// 168 VGPRs, the latter with 12 bytes of spill), two above.  At the N8 shapes 768 threads took
+// the K assign (Kc 1000, D 48) from 658 to 590 us and the Q assign (Qc 300, D 64) from 358
+// to 323 us against 512, with the same labels.
+template <int D>
+constexpr int pipe_threads() { return D <= 64 ? 768 : 512; }
 constexpr size_t PIPE_LDS_LIMIT = 160 * 1024;
 
 template <int D>
@@ -639,13 +643,15 @@ constexpr size_t pipe_lds_bytes(int64_t kpad) {
 }
 
 template <int D>
-__global__ __launch_bounds__(PIPE_THREADS, 1) void kmeans_assign_tf32_resident_kernel(
+__global__ __launch_bounds__(pipe_threads<D>(), 1) void kmeans_assign_tf32_resident_kernel(
     const float* __restrict__ x, const float* __restrict__ c, const float* __restrict__ c_sq,
     const float* __restrict__ x_sq_in, float* __restrict__ x_sq_out, int64_t batch, int64_t n, int32_t k,
     int32_t* __restrict__ labels) {
   static_assert(D % 16 == 0 && D <= 128, "D must be a multiple of 16, at most 128");
   constexpr int KSTEPS = D / 16;
   constexpr int ROW_BYTES = D * 2 + 16;  // padded LDS row: conflict-free 16-byte reads
+  constexpr int PIPE_THREADS = pipe_threads<D>();
+  constexpr int PIPE_WAVES = PIPE_THREADS / 64;
   extern __shared__ __attribute__((aligned(16))) uint8_t assign_smem[];
   const int kpad = (k + CCHUNK - 1) / CCHUNK * CCHUNK;  // a multiple of 64: an even number of steps
   uint8_t* cent = assign_smem;
@@ -917,7 +923,8 @@ int launch_tf32_resident(const float* x, const float* c, const float* c_sq, cons
     lds_raised = true;
   }
   const int64_t blocks = batch * spr::ceil_div(n, ASSIGN_POINTS_PER_WAVE);
-  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(256, spr::ceil_div(blocks, PIPE_WAVES)));
+  constexpr int PIPE_THREADS = pipe_threads<D>();
+  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(256, spr::ceil_div(blocks, PIPE_THREADS / 64)));
   kmeans_assign_tf32_resident_kernel<D><<<static_cast<uint32_t>(grid), PIPE_THREADS, lds, stream>>>(
       x, c, c_sq, x_sq, x_sq_out, batch, n, k, labels);
   SPR_LAUNCHED("kmeans_assign_tf32_resident_kernel");

@@ -254,13 +254,15 @@ def test_kmeans_full_size_properties(dev):
 
 
 @pytest.mark.parametrize("b,n,k,d", [(2, 3000, 300, 64), (2, 2500, 1000, 48), (1, 777, 37, 16), (1, 1000, 64, 32),
-                                     (1, 600, 70, 128), (3, 2100, 77, 48), (2, 1500, 600, 128)])
+                                     (1, 600, 70, 128), (3, 2100, 77, 48), (3, 1900, 77, 48), (3, 1900, 120, 64),
+                                     (2, 1500, 600, 128)])
 def test_assign_tf32_matches_oracle_up_to_ties(dev, oracle, b, n, k, d):
     """fp32 role-space features (the N8 route's shapes: rank 64 / 300 Q clusters, rank 48 /
-    1000 K clusters): TF32 products, fp32 norms, lowest index on ties.  (3, 2100, 77, 48)
-    gives the resident kernel a workgroup whose share of 64-point blocks crosses from one
-    batch into the next (33 blocks per batch, 13 workgroups); (2, 1500, 600, 128) does not
-    fit its LDS and runs the streamed kernel."""
+    1000 K clusters): TF32 products, fp32 norms, lowest index on ties.  (3, 1900, 77, 48)
+    and (3, 1900, 120, 64) give the resident kernel (12 waves per workgroup at these D)
+    workgroups whose shares of 64-point blocks cross from one batch into the next (30 blocks
+    per batch, 8 workgroups of 11.25 blocks); (2, 1500, 600, 128) does not fit its LDS and
+    runs the streamed kernel."""
     from sparsepr_amd.flash_kmeans.kmeans_impl import euclid_assign
 
     rng = np.random.default_rng(n + k + d)
