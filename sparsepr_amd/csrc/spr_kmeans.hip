@@ -1007,7 +1007,9 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
   constexpr int VPR = D / E;         // vectors per row
   static_assert(D % E == 0 && VPR <= 256, "unsupported D");
   constexpr int R = 256 / VPR;       // row groups (threads past R * VPR idle)
-  constexpr int RPT = 8;             // rows per thread per pass
+  // rows per thread per pass: 8 for bf16 rows; 4 for fp32 (fewer registers, more waves: the
+  // N8 means 142 -> 117 us at D 48 and 168 -> 140 us at D 64 against 8; 2 and 16 slower)
+  constexpr int RPT = sizeof(T) == 4 ? 4 : 8;
   __shared__ double red[R][D + 1];
   __shared__ float sq[D], cv[D];
 
