@@ -21,7 +21,7 @@
 // Layout.  A first kernel writes the centroid logits l_c [query head, centroid,
 // cluster] (fp32 dot products over d, sequential, 128 rows x 32 clusters per workgroup)
 // into the score buffer; the score kernel overwrites each entry with its score.
-// The score kernel runs one workgroup of four waves per (query head, 4
+// The score kernel runs one workgroup of four waves per (query head, 8
 // consecutive key clusters); wave w scores query rows 32 w .. 32 w + 31 of each
 // group of 128 (a loop covers more centroids).  The clusters' tokens are one
 // contiguous run, walked in 32-token chunks (a chunk never spans two clusters).
@@ -101,9 +101,9 @@ __device__ __forceinline__ float sum_xor32(float x) {
 }
 
 constexpr int SE_ROW = SE_D * 2;  // bytes per bf16 token row
-// key clusters per workgroup: 4 against 8 took 10 % off at 512 clusters x 128 centroids and
-// 2-7 % at 1000 x 300 (more, smaller workgroups balance better); 2 and 16 were slower
-constexpr int SE_CPW = 4;
+// key clusters per workgroup (4 was faster on synthetic cluster sizes but 2 % slower on the
+// routed clusters of the C4 bench, and within noise in the N8 step; 2 and 16 were slower)
+constexpr int SE_CPW = 8;
 constexpr int CL_CLUSTERS = 32;   // clusters per centroid-logit workgroup
 constexpr int CL_ROWS = 2 * (SE_THREADS / 4);  // query rows per centroid-logit workgroup
 
