@@ -37,10 +37,10 @@ using spr::u32x4;
 constexpr int RP_THREADS = 256;
 constexpr int RP_WAVES = RP_THREADS / 64;
 // Tokens per block (a workgroup takes several blocks of its head): 256 for the row-normalised
-// projection, 1024 for the two passes of the per-head scale (which must agree, since the
-// second sums the first's per-block partials in block order).  Measured in the N8 step
-// against 512 for both: Q projection 0.39 -> 0.36 ms, K projection 0.64 -> 0.63 ms.
-constexpr int rp_tokens(int mode) { return mode == 0 ? 256 : 1024; }
+// projection (MODE 0) and the K projection's scaling pass (MODE 2), 1024 for its sum pass
+// (MODE 1: one fp64 partial per block, which MODE 2 sums in block order).  Measured in the N8
+// step against 512 for all: Q projection 0.39 -> 0.36 ms, K projection 0.64 -> 0.61 ms.
+constexpr int rp_tokens(int mode) { return mode == 1 ? 1024 : 256; }
 constexpr int RP_MAX_R = 128;
 
 __device__ __forceinline__ float tf32_rna(float x) {
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(RP_THREADS) void role_projection_kernel(const uint1
   if (MODE == 2) {
     // the head's scale: fp64 sum of the partials in block order, then as the reference
     // rounds it: fp32 mean, sqrt, clamp at 1e-8
-    const int64_t nparts = (n + RP_TOKENS - 1) / RP_TOKENS;
+    const int64_t nparts = (n + rp_tokens(1) - 1) / rp_tokens(1);  // the first pass's blocks
     double tot = 0.0;
     for (int64_t i = 0; i < nparts; ++i) tot += partial[b * nparts + i];
     div = fmaxf(sqrtf(static_cast<float>(tot / (static_cast<double>(n) * rank))), 1.0e-8f);
