@@ -24,7 +24,8 @@ def _centroids(rng, bh, qn, kn, d, scale=1.0):
 
 # key-cluster counts that reach every register width of the one-wave sort (1 .. 64 keys per
 # lane: kn up to 64, 128, 256, 512, 1024, 2048, 4096)
-@pytest.mark.parametrize("bh,qn,kn,d", [(4, 32, 64, 64), (2, 9, 100, 64), (2, 17, 256, 64), (2, 128, 512, 128),
+@pytest.mark.parametrize("bh,qn,kn,d", [(2, 3, 1, 64), (2, 5, 2, 64), (4, 32, 64, 64), (2, 9, 100, 64), (2, 17, 256, 64),
+                                        (2, 128, 512, 128),
                                         (1, 5, 300, 128), (1, 11, 1000, 128), (1, 3, 2000, 64),
                                         (1, 3, 4096, 64), (3, 100, 500, 128)])
 @pytest.mark.parametrize("bf16", [False, True])
@@ -132,7 +133,7 @@ def test_selector_known_answer_gpu(dev):
 
 
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("bh,qn,kn", [(2, 7, 9), (1, 3, 64), (1, 3, 65), (2, 9, 100), (2, 17, 200), (3, 50, 512),
+@pytest.mark.parametrize("bh,qn,kn", [(2, 3, 1), (2, 5, 2), (2, 7, 9), (1, 3, 64), (1, 3, 65), (2, 9, 100), (2, 17, 200), (3, 50, 512),
                                      (3, 100, 1000), (1, 6, 2000), (1, 4, 4096)])
 def test_selector_random_vs_oracle(dev, oracle, mode, bh, qn, kn):
     """Rows of every register width of the one-wave sort (kn up to 64 E for E = 1 .. 64), with
