@@ -97,9 +97,10 @@ int spr_kmeans_assign_tf32(const float* x, const float* centroids, const float* 
  *   d a multiple of 16 up to 128).  Nullable outputs: mean32 fp32 [batch,k,d], out dtype [batch,k,d],
  *   shift_max fp32 scalar (pre-zeroed; max_k ||out-old||), sums_accum fp32 += sums,
  *   counts_accum int32 += counts, c_sq_out fp32 [batch,k] = squared norms of `out` (as
- *   spr_centroid_sq computes them, for the next assignment).  Large clusters are split into row slices whose fp64 partial
- *   sums go to the workspace (spr_centroid_mean_workspace bytes, 0 when no split is needed)
- *   and are added in slice order. */
+ *   spr_centroid_sq computes them, for the next assignment).  Each cluster's rows are split
+ *   into slices of 512 (a plan made on the device from the offsets); their fp64 partial sums
+ *   go to the workspace (spr_centroid_mean_workspace bytes, with the plan) and are added in
+ *   slice order. */
 size_t spr_centroid_mean_workspace(int64_t batch, int64_t n, int32_t k, int32_t d);
 int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, const int32_t* offsets,
                       const void* old, int64_t batch, int64_t n, int32_t k, int32_t d, float* mean32, void* out,

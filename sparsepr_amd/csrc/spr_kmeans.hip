@@ -992,17 +992,78 @@ __device__ void finalize_mean(double s, int32_t count, int64_t b, int32_t cl, in
   }
 }
 
-// T: uint16_t (bf16) or float.  Workgroup (cl * nsplit + sp, b) sums slice sp of
-// the `nsplit` equal slices of cluster cl's rows (sorted order) in fp64.  With
-// nsplit == 1 it also finalizes; otherwise it writes the slice sums to
-// partial[b][cl][sp][D] for centroid_mean_finalize_kernel, which adds the
-// slices in order (the result does not depend on the split).
+// Slices of a cluster's rows (sorted order): every cluster with rows gets ceil(rows / MEAN_SLICE)
+// slices of its own, so a large cluster is spread over many workgroups whatever the other
+// clusters' sizes (on the C4 route's Q labels, the largest of 128 clusters holds 17,805 of
+// 118,800 rows; slices sized from the average left it to two workgroups: 204 us per update
+// against 134 us on uniform labels).
+constexpr int MEAN_SLICE = 512;
+
+// One workgroup per batch: slice_base[b][c] = the first slice of cluster c (exclusive scan of
+// ceil(rows_c / MEAN_SLICE), c = 0 .. k; capped at maxs, the slices the workspace holds, so
+// a malformed offsets table cannot index past it) and slice_rows[b][s] = {x, y, c, m}: rows
+// [x, y) of cluster c, which has m slices (an empty range with m = 0 past the last slice).
+// Offsets are clamped as the mean kernels clamp them.
+__global__ __launch_bounds__(256) void mean_slice_plan_kernel(const int32_t* __restrict__ offsets, int64_t n,
+                                                              int32_t k, int32_t maxs, int32_t* __restrict__ slice_base,
+                                                              int4* __restrict__ slice_rows) {
+  __shared__ int32_t wave_tot[4];
+  const int64_t b = blockIdx.x;
+  const int32_t* off = offsets + b * (k + 1);
+  int32_t* sb = slice_base + b * (k + 1);
+  int4* sr = slice_rows + b * static_cast<int64_t>(maxs);
+  const int32_t n32 = static_cast<int32_t>(n);
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int per = (k + 255) / 256;
+  const int c0 = min(t * per, k), c1 = min(c0 + per, k);
+  auto slices_of = [&](int c, int32_t& start, int32_t& end) {
+    start = min(max(off[c], 0), n32);
+    end = min(max(off[c + 1], start), n32);
+    return (end - start + MEAN_SLICE - 1) / MEAN_SLICE;
+  };
+  int64_t local = 0;
+  for (int c = c0; c < c1; ++c) {
+    int32_t a, e;
+    local += slices_of(c, a, e);
+  }
+  int64_t incl = local;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t up = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += up;
+  }
+  if (lane == 63) wave_tot[wv] = static_cast<int32_t>(min(incl, static_cast<int64_t>(maxs)));
+  __syncthreads();
+  int64_t base = incl - local;
+  for (int w = 0; w < wv; ++w) base += wave_tot[w];
+  for (int c = c0; c < c1; ++c) {
+    int32_t a, e;
+    const int ns = slices_of(c, a, e);
+    sb[c] = static_cast<int32_t>(min(base, static_cast<int64_t>(maxs)));
+    for (int j = 0; j < ns; ++j) {
+      const int64_t si = base + j;
+      if (si < maxs) sr[si] = int4{a + j * MEAN_SLICE, min(a + (j + 1) * MEAN_SLICE, e), c, ns};
+    }
+    base += ns;
+  }
+  __syncthreads();
+  int64_t total = 0;
+  for (int w = 0; w < 4; ++w) total += wave_tot[w];
+  total = min(total, static_cast<int64_t>(maxs));
+  if (t == 0) sb[k] = static_cast<int32_t>(total);
+  for (int64_t si = total + t; si < maxs; si += 256) sr[si] = int4{0, 0, 0, 0};
+}
+
+// T: uint16_t (bf16) or float.  Workgroup (s, b) sums slice s of batch b (rows
+// slice_rows[b][s] of the sorted order) in fp64.  The one slice of a cluster finalizes its
+// mean directly; otherwise the sum goes to partial[b][s][D], and
+// centroid_mean_finalize_kernel adds the cluster's slices in order (the result does not
+// depend on the split).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void centroid_mean_kernel(
-    const T* __restrict__ x, const int32_t* __restrict__ sorted_idx, const int32_t* __restrict__ offsets,
-    const T* __restrict__ old, int64_t n, int32_t k, int32_t nsplit, double* __restrict__ partial,
-    float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max, float* __restrict__ sums_accum,
-    int32_t* __restrict__ counts_accum, float* __restrict__ c_sq_out) {
+    const T* __restrict__ x, const int32_t* __restrict__ sorted_idx, const int4* __restrict__ slice_rows, int64_t n,
+    int32_t maxs, double* __restrict__ partial, const int32_t* __restrict__ offsets, const T* __restrict__ old,
+    int32_t k, float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max,
+    float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum, float* __restrict__ c_sq_out) {
   constexpr int E = 16 / sizeof(T);  // elements per 16-byte vector
   constexpr int VPR = D / E;         // vectors per row
   static_assert(D % E == 0 && VPR <= 256, "unsupported D");
@@ -1017,20 +1078,14 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
   const int v = tid % VPR;
   const int rg = tid / VPR;
   const int64_t b = blockIdx.y;
-  const int32_t cl = blockIdx.x / nsplit;
-  const int32_t sp = blockIdx.x - cl * nsplit;
-  const int32_t* off = offsets + b * (k + 1);
-  // offsets come from spr_argsort_labels; clamp anyway so a bad table cannot
-  // index outside [0, n).
   const int32_t n32 = static_cast<int32_t>(n);
-  const int32_t c_start = min(max(off[cl], 0), n32);
-  const int32_t c_end = min(max(off[cl + 1], c_start), n32);
-  const int32_t slice = (c_end - c_start + nsplit - 1) / nsplit;
-  const int32_t start = min(c_start + sp * slice, c_end);
-  const int32_t end = min(start + slice, c_end);
+  const int4 rr = slice_rows[b * maxs + blockIdx.x];
+  if (rr.w == 0) return;  // past the last slice
+  // the plan's ranges lie in [0, n); clamp anyway
+  const int32_t start = min(max(rr.x, 0), n32);
+  const int32_t end = min(max(rr.y, start), n32);
   const int32_t* idx = sorted_idx + b * n;
   const T* xb = x + b * n * D;
-
   double acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.0;
@@ -1087,30 +1142,38 @@ __global__ __launch_bounds__(256) void centroid_mean_kernel(
   if (tid < D) {
     for (int g = 0; g < R; ++g) s += red[g][tid];
   }
-  if (nsplit > 1) {
-    if (tid < D) partial[((b * k + cl) * nsplit + sp) * D + tid] = s;
+  if (rr.w > 1) {
+    if (tid < D) partial[(b * maxs + blockIdx.x) * D + tid] = s;
     return;
   }
-  finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, c_sq_out,
+  // the cluster's only slice: its rows are the whole cluster
+  const int32_t cl = min(max(rr.z, 0), k - 1);
+  finalize_mean<T, D>(s, end - start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, c_sq_out,
                       sq, cv);
 }
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void centroid_mean_finalize_kernel(
-    const double* __restrict__ partial, const int32_t* __restrict__ offsets, const T* __restrict__ old, int64_t n,
-    int32_t k, int32_t nsplit, float* __restrict__ mean32, T* __restrict__ out, float* __restrict__ shift_max,
-    float* __restrict__ sums_accum, int32_t* __restrict__ counts_accum, float* __restrict__ c_sq_out) {
+    const double* __restrict__ partial, const int32_t* __restrict__ slice_base, int32_t maxs,
+    const int32_t* __restrict__ offsets, const T* __restrict__ old, int64_t n, int32_t k, float* __restrict__ mean32,
+    T* __restrict__ out, float* __restrict__ shift_max, float* __restrict__ sums_accum,
+    int32_t* __restrict__ counts_accum, float* __restrict__ c_sq_out) {
   __shared__ float sq[D], cv[D];
   const int64_t b = blockIdx.y;
   const int32_t cl = blockIdx.x;
   const int32_t* off = offsets + b * (k + 1);
+  const int32_t* sb = slice_base + b * (k + 1);
   const int32_t n32 = static_cast<int32_t>(n);
   const int32_t c_start = min(max(off[cl], 0), n32);
   const int32_t c_end = min(max(off[cl + 1], c_start), n32);
+  const int32_t s0 = min(max(sb[cl], 0), maxs);
+  const int32_t s1 = min(max(sb[cl + 1], s0), maxs);
+  // a cluster of one slice (the plan's rule) was finalized by that slice's workgroup
+  if ((c_end - c_start + MEAN_SLICE - 1) / MEAN_SLICE == 1) return;
   double s = 0.0;
   if (threadIdx.x < D) {
-    const double* p = partial + (b * k + cl) * nsplit * D + threadIdx.x;
-    for (int sp = 0; sp < nsplit; ++sp) s += p[sp * D];
+    const double* p = partial + b * static_cast<int64_t>(maxs) * D + threadIdx.x;
+    for (int32_t sp = s0; sp < s1; ++sp) s += p[static_cast<int64_t>(sp) * D];
   }
   finalize_mean<T, D>(s, c_end - c_start, b, cl, k, old, mean32, out, shift_max, sums_accum, counts_accum, c_sq_out,
                       sq, cv);
@@ -1490,17 +1553,27 @@ extern "C" int spr_original_centroids(const void* x, const void* y, int32_t dtyp
 // Outputs (each nullable): mean32 fp32 [b,k,d]; out (dtype) [b,k,d];
 // shift_max (fp32 scalar, must start at 0; receives max_k ||out - old||);
 // sums_accum fp32 [b,k,d] += sums; counts_accum int32 [b,k] += counts.
-// Slices per cluster: about 512 rows each on average, at most 16.  (Per 1,000-row clusters
-// of 64-dimension fp32 rows, 256-row slices and their finalize launch took 182 us against
-// 169 us with one workgroup per cluster; 128-row slices were slower still.)
+// Slices per cluster for the original-space means: about 512 rows each on average, at most
+// 16.  (Per 1,000-row clusters of 64-dimension fp32 rows, 256-row slices and their finalize
+// launch took 182 us against 169 us with one workgroup per cluster; 128-row slices were
+// slower still.)
 static int32_t mean_splits(int64_t n, int32_t k) {
   const int64_t avg = n / (k > 0 ? k : 1);
   return static_cast<int32_t>(std::min<int64_t>(16, std::max<int64_t>(1, (avg + 511) / 512)));
 }
 
+// Slices the per-cluster plan can hold: sum_c ceil(rows_c / MEAN_SLICE) <= n / MEAN_SLICE + k.
+static int64_t mean_max_slices(int64_t n, int32_t k) { return (n + MEAN_SLICE - 1) / MEAN_SLICE + k; }
+static size_t align16(size_t v) { return (v + 15) & ~static_cast<size_t>(15); }
+
+// Workspace of spr_centroid_mean: fp64 slice sums [batch][maxs][d], the slice plan's cluster
+// bases [batch][k + 1] and slices [batch][maxs] (rows, cluster, the cluster's slice count).
 extern "C" size_t spr_centroid_mean_workspace(int64_t batch, int64_t n, int32_t k, int32_t d) {
-  const int32_t ns = mean_splits(n, k);
-  return ns > 1 ? static_cast<size_t>(batch * k * ns * static_cast<int64_t>(d) * sizeof(double)) : 0;
+  if (batch <= 0 || k < 1 || d < 1 || n < 0) return 0;
+  const int64_t maxs = mean_max_slices(n, k);
+  return align16(static_cast<size_t>(batch * maxs * d) * sizeof(double)) +
+         align16(static_cast<size_t>(batch * (k + 1)) * sizeof(int32_t)) +
+         align16(static_cast<size_t>(batch * maxs) * sizeof(int4));
 }
 
 extern "C" int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* sorted_idx, const int32_t* offsets,
@@ -1512,25 +1585,34 @@ extern "C" int spr_centroid_mean(const void* x, int32_t dtype, const int32_t* so
   if (batch == 0) return SPR_OK;
   SPR_REQUIRE(sorted_idx && offsets && old, "spr_centroid_mean: null pointer");
   SPR_REQUIRE(n == 0 || x, "spr_centroid_mean: null x");
-  const int32_t ns = mean_splits(n, k);
+  SPR_REQUIRE(n < (int64_t(1) << 31), "spr_centroid_mean: n too large");
+  const int64_t maxs = mean_max_slices(n, k);
+  SPR_REQUIRE(maxs < (int64_t(1) << 31), "spr_centroid_mean: too many clusters");
   const size_t need = spr_centroid_mean_workspace(batch, n, k, d);
-  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+  if (workspace_bytes < need || workspace == nullptr) {
     spr_set_error("spr_centroid_mean: workspace %zu < %zu bytes", workspace_bytes, need);
     return SPR_EWORKSPACE;
   }
-  SPR_REQUIRE(static_cast<int64_t>(k) * ns < (int64_t(1) << 31), "spr_centroid_mean: too many clusters");
-  double* partial = static_cast<double*>(workspace);
-  dim3 grid(static_cast<uint32_t>(k * ns), static_cast<uint32_t>(batch));
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  double* partial = reinterpret_cast<double*>(ws);
+  ws += align16(static_cast<size_t>(batch * maxs * d) * sizeof(double));
+  int32_t* slice_base = reinterpret_cast<int32_t*>(ws);
+  ws += align16(static_cast<size_t>(batch * (k + 1)) * sizeof(int32_t));
+  int4* slice_rows = reinterpret_cast<int4*>(ws);
+  const int32_t ms = static_cast<int32_t>(maxs);
+  mean_slice_plan_kernel<<<dim3(static_cast<uint32_t>(batch)), 256, 0, stream>>>(offsets, n, k, ms, slice_base,
+                                                                                 slice_rows);
+  SPR_LAUNCHED("mean_slice_plan_kernel");
+  dim3 grid(static_cast<uint32_t>(maxs), static_cast<uint32_t>(batch));
   dim3 fgrid(static_cast<uint32_t>(k), static_cast<uint32_t>(batch));
 #define SPR_MEAN_CASE(T, DD)                                                                                 \
   do {                                                                                                       \
     centroid_mean_kernel<T, DD><<<grid, 256, 0, stream>>>(                                                   \
-        static_cast<const T*>(x), sorted_idx, offsets, static_cast<const T*>(old), n, k, ns, partial, mean32, \
-        static_cast<T*>(out), shift_max, sums_accum, counts_accum, c_sq_out);                                \
-    if (ns > 1)                                                                                              \
-      centroid_mean_finalize_kernel<T, DD><<<fgrid, 256, 0, stream>>>(                                       \
-          partial, offsets, static_cast<const T*>(old), n, k, ns, mean32, static_cast<T*>(out), shift_max,   \
-          sums_accum, counts_accum, c_sq_out);                                                               \
+        static_cast<const T*>(x), sorted_idx, slice_rows, n, ms, partial, offsets, static_cast<const T*>(old), k, \
+        mean32, static_cast<T*>(out), shift_max, sums_accum, counts_accum, c_sq_out);                         \
+    centroid_mean_finalize_kernel<T, DD><<<fgrid, 256, 0, stream>>>(                                         \
+        partial, slice_base, ms, offsets, static_cast<const T*>(old), n, k, mean32, static_cast<T*>(out),    \
+        shift_max, sums_accum, counts_accum, c_sq_out);                                                      \
   } while (0)
   if (dtype == 0) {
     switch (d) {
