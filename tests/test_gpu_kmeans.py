@@ -87,6 +87,35 @@ def test_centroid_mean_bit_exact(dev, oracle, k, d):
     assert abs(float(res.shift.item()) - shift) <= 1e-5 * max(shift, 1.0)
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 48)])
+def test_centroid_mean_skewed_clusters(dev, oracle, dtype, d):
+    """Each cluster's rows are cut into 512-row slices planned on the device: one cluster holds
+    about 80 % of the rows (dozens of slices, summed by the finalize kernel), one about 5 %
+    (a few slices), the rest one slice each (finalized by that slice's workgroup), two none
+    (the previous centroid): every mean bit-exact to the float64 one."""
+    from sparsepr_amd.flash_kmeans.kmeans_impl import centroid_update_sorted
+
+    rng = np.random.default_rng(41 + d)
+    b, n, k = 2, 30000, 40
+    x = _gmm(oracle, rng, b, n, d, 20)
+    if dtype == torch.float32:
+        x = (x + 1e-3 * rng.standard_normal(x.shape)).astype(np.float32)  # not bf16 values
+    labels = rng.integers(8, k, (b, n)).astype(np.int32)
+    u = rng.random((b, n))
+    labels[u < 0.8] = 0
+    labels[(u >= 0.8) & (u < 0.85)] = 7
+    old = rng.standard_normal((b, k, d)).astype(np.float32)
+    if dtype == torch.bfloat16:
+        old = oracle.to_bf16(old)
+    res = centroid_update_sorted(to_dev(x, dev, dtype), to_dev(labels, dev), to_dev(old, dev, dtype),
+                                 want_mean32=True, want_shift=True)
+    cent, mean32, counts = oracle.centroid_update(x, labels, old, out_bf16=dtype == torch.bfloat16)
+    assert counts[0, 0] > 40 * 512 and counts[0, 5] == 0 and counts[0, 6] == 0
+    assert (res.mean32.cpu().numpy() == mean32).all()
+    assert (res.centroids.float().cpu().numpy() == cent).all()
+    assert (res.sizes.cpu().numpy() == counts).all()
+
+
 def test_centroid_update_accumulates_into_buffers(dev, oracle):
     from sparsepr_amd.flash_kmeans import triton_centroid_update_sorted_euclid
 
