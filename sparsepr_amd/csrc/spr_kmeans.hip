@@ -1019,7 +1019,7 @@ __global__ __launch_bounds__(256) void mean_slice_plan_kernel(const int32_t* __r
   auto slices_of = [&](int c, int32_t& start, int32_t& end) {
     start = min(max(off[c], 0), n32);
     end = min(max(off[c + 1], start), n32);
-    return (end - start + MEAN_SLICE - 1) / MEAN_SLICE;
+    return static_cast<int32_t>((static_cast<int64_t>(end) - start + MEAN_SLICE - 1) / MEAN_SLICE);
   };
   int64_t local = 0;
   for (int c = c0; c < c1; ++c) {
@@ -1041,7 +1041,10 @@ __global__ __launch_bounds__(256) void mean_slice_plan_kernel(const int32_t* __r
     sb[c] = static_cast<int32_t>(min(base, static_cast<int64_t>(maxs)));
     for (int j = 0; j < ns; ++j) {
       const int64_t si = base + j;
-      if (si < maxs) sr[si] = int4{a + j * MEAN_SLICE, min(a + (j + 1) * MEAN_SLICE, e), c, ns};
+      if (si < maxs) {
+        const int64_t lo = a + static_cast<int64_t>(j) * MEAN_SLICE;  // 64-bit: no overflow near n = 2^31
+        sr[si] = int4{static_cast<int32_t>(lo), static_cast<int32_t>(min<int64_t>(lo + MEAN_SLICE, e)), c, ns};
+      }
     }
     base += ns;
   }
@@ -1169,7 +1172,7 @@ __global__ __launch_bounds__(256) void centroid_mean_finalize_kernel(
   const int32_t s0 = min(max(sb[cl], 0), maxs);
   const int32_t s1 = min(max(sb[cl + 1], s0), maxs);
   // a cluster of one slice (the plan's rule) was finalized by that slice's workgroup
-  if ((c_end - c_start + MEAN_SLICE - 1) / MEAN_SLICE == 1) return;
+  if ((static_cast<int64_t>(c_end) - c_start + MEAN_SLICE - 1) / MEAN_SLICE == 1) return;
   double s = 0.0;
   if (threadIdx.x < D) {
     const double* p = partial + b * static_cast<int64_t>(maxs) * D + threadIdx.x;
