@@ -166,7 +166,7 @@ def test_project_rows(dev, oracle):
     assert np.abs(got - ref).max() <= 1e-5
 
 
-@pytest.mark.parametrize("k,joint", [(300, True), (4, True), (100, False)])  # k = 4: split clusters
+@pytest.mark.parametrize("k,joint", [(300, True), (4, True), (100, False), (50, True)])  # k = 4: split clusters
 def test_original_centroids_exact(dev, oracle, k, joint):
     """fp32 means of bf16 K (and V) under labels, empty clusters from the fp32 fallback or
     zeros: bit-exact against the float64 sums (exact for bf16 rows) rounded to fp32."""
@@ -178,6 +178,8 @@ def test_original_centroids_exact(dev, oracle, k, joint):
     x = oracle.to_bf16(rng.standard_normal((2, n, d)).astype(np.float32))
     y = oracle.to_bf16(rng.standard_normal((2, n, d)).astype(np.float32))
     labels = rng.integers(0, k, (2, n)).astype(np.int32)
+    if k == 50:
+        labels[rng.random((2, n)) < 0.7] = 2  # one cluster of several 512-row slices, the rest one each
     labels[labels == 1] = 0  # cluster 1 empty
     sizes = np.stack([np.bincount(r, minlength=k) for r in labels])
     fb = rng.standard_normal((2, k, d)).astype(np.float32)
